@@ -1,0 +1,120 @@
+/*
+ * od_mi355x.h — C ABI of the MI355X (gfx950) kernels for OpenDecider's quantized scoring forward path.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are DEVICE pointers of the current HIP device; bf16 tensors are passed as uint16_t bit patterns.
+ *   - Sizes and strides are in ELEMENTS, int64_t; the last dimension of every tensor is contiguous.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream). Work is enqueued on it and
+ *     the call returns without synchronizing.
+ *   - Nothing allocates device or host memory and nothing synchronizes, so every call may be captured in a
+ *     HIP graph. Calls are reentrant (no mutable global state).
+ *   - Return value: OD_OK (0) or a negative OD_ERR_* code; no exception crosses the ABI. od_strerror() gives
+ *     the text. (The reference's own C ABI uses the same int-rc convention: deploy/llamacpp/od_llama.cpp:13-22,
+ *     mapped to RuntimeError by src/opendecider/llamacpp.py:57-58.)
+ */
+#ifndef OD_MI355X_H
+#define OD_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* od_stream_t;
+
+#define OD_OK 0
+#define OD_ERR_NULL (-1)        /* a required pointer is NULL */
+#define OD_ERR_SHAPE (-2)       /* a size or stride is out of range or inconsistent */
+#define OD_ERR_ALIGN (-3)       /* a pointer or leading dimension breaks the 16-byte alignment the kernel needs */
+#define OD_ERR_UNSUPPORTED (-4) /* head dim / GQA ratio / row length outside what the kernels are built for */
+#define OD_ERR_LAUNCH (-5)      /* the kernel launch failed (hipGetLastError) */
+
+/* Text for an OD_* code. */
+const char* od_strerror(int code);
+
+/* ABI version of this library (bumped when a signature changes). */
+int od_abi_version(void);
+
+/*
+ * od_act_quant — per-row dynamic int8 quantization, with optional SmoothQuant input scaling.
+ * Replaces: Int8Tensor.quantize (src/opendecider/quant.py:36-41) applied per token to activations, the
+ * SmoothedLinear input scaling x * inv_s (quant.py:325,328-329), and the dynamic activation quantizer inside
+ * GemLite A8W8_int8_dynamic (called at quant.py:305-311, :336-347). Also used for Int8Linear's per-output-channel
+ * weight quantization (quant.py:124-126), which is the same formula over weight rows.
+ *   x      bf16 [M, K], row stride ldx
+ *   inv_s  bf16 [K] or NULL; when given, each element is first rounded to bf16(x * inv_s)
+ *   xq     int8 [M, K], row stride ldq (out)
+ *   sx     fp32 [M] (out): scale = max(max_k |x|, 1e-8) / 127 (IEEE fp32 division)
+ *   q = round_half_even(x / scale) (IEEE fp32 division), clamped to [-127, 127].
+ * Bit-exact with the torch formula. Any M >= 0, K >= 1.
+ */
+int od_act_quant(const uint16_t* x, int64_t ldx, const uint16_t* inv_s, int8_t* xq, int64_t ldq, float* sx,
+                 int64_t M, int64_t K, od_stream_t stream);
+
+/*
+ * od_w8a8_gemm — int8 x int8 -> int32 GEMM on CDNA4 int8 MFMA with a bf16 dequant epilogue.
+ * Replaces: the GEMM of GemLite A8W8_int8_dynamic behind gemlite_a8w8_ / smooth_a8w8_
+ * (src/opendecider/quant.py:302-314, :332-350), and Int8Linear.forward's dequantize + F.linear
+ * (quant.py:149-157) when attached through its `_fused` slot (quant.py:150-152, 398-409).
+ *   a        int8 [M, K], row stride lda          sa  fp32 [M]  per-token activation scales
+ *   w        int8 [N, K] (nn.Linear layout), ldw  sw  fp32 [N]  per-output-channel weight scales
+ *   bias     bf16 [N] or NULL
+ *   residual bf16 [M, N] (row stride ldr) or NULL, added in fp32 before the single rounding
+ *   out      bf16 [M, N], row stride ldo, or NULL (then only acc is written)
+ *   acc      int32 [M, N], row stride ldacc, or NULL (debug / parity: the exact accumulators)
+ *   out = bf16( ((float(acc) * sa[m]) * sw[n]) + float(bias[n]) + float(residual[m, n]) )
+ * Requires K % 16 == 0, lda/ldw % 16 == 0 and 16-byte aligned a/w (int8 rows are read in 16-byte chunks).
+ */
+int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const int8_t* w, int64_t ldw, const float* sw,
+                 const uint16_t* bias, const uint16_t* residual, int64_t ldr, uint16_t* out, int64_t ldo,
+                 int32_t* acc, int64_t ldacc, int64_t M, int64_t N, int64_t K, od_stream_t stream);
+
+/*
+ * od_kv_quant_append — quantize new K or V rows (one scale per token per head) and append them to an int8 cache.
+ * Replaces: maybe_quantize / Int8Tensor.quantize on cache tensors (quant.py:36-41,105-109) as called by
+ * PackedCache.pack (src/opendecider/backbone.py:446) and by PrefixCache._take, which quantizes only the new
+ * tokens' slice (src/opendecider/state_cache.py:79).
+ *   x  bf16, logical shape [B, H, n_new, D], element strides (sxb, sxh, sxt), last dim contiguous
+ *   q  int8 [B, H, cap, D] contiguous (out): rows n0 .. n0+n_new-1 are written
+ *   s  fp32 [B, H, cap] contiguous (out): the matching scales
+ * Same formula and bytes as od_act_quant per row; requires n0 + n_new <= cap.
+ */
+int od_kv_quant_append(const uint16_t* x, int64_t B, int64_t H, int64_t n_new, int64_t D, int64_t sxb, int64_t sxh,
+                       int64_t sxt, int8_t* q, float* s, int64_t cap, int64_t n0, od_stream_t stream);
+
+/*
+ * od_branched_attn — branched (Hydragen) option-row attention over an int8 shared state, one launch.
+ * Replaces: _split_attention (src/opendecider/prefix_attn.py:43-76) with its two wide_attention launches
+ * (src/opendecider/wide_attention.py:70-91) and the torch LSE merge (prefix_attn.py:74-76), the per-state loop
+ * of _forward (prefix_attn.py:118-128), and the per-layer dequantized copy of the state K/V
+ * (prefix_attn.py:145-149): the int8 state is read directly and its scales are folded into the scores.
+ *   q         bf16 [R, Hq, t, D], element strides (sqr, sqh, sqt)        R option rows of t tokens
+ *   k_own     bf16 [R, Hkv, t, D], strides (skr, skh, skt)                each row's own keys (causal)
+ *   v_own     bf16 [R, Hkv, t, D], strides (svr, svh, svt)
+ *   kq, vq    int8 [Ns, Hkv, cap, D] contiguous                          the states' K/V (first T tokens used)
+ *   ks, vs    fp32 [Ns, Hkv, cap] contiguous                             per-(token, head) scales
+ *   kvalid    uint8 [Ns, T] (nonzero = real key) or NULL                  prefix key mask (pads / holes)
+ *   row_start int32 [Ns + 1] device array: the rows of state s are rows row_start[s] .. row_start[s+1]-1
+ *             (rows grouped by state; NULL means Ns == 1 and every row reads state 0)
+ *   max_rows  the largest row_start[s+1] - row_start[s] (sizes the grid; must be exact or an upper bound)
+ *   out       bf16 [R, Hq, t, D], strides (sor, soh, sot) (out)
+ *   lse       fp32 [R, Hq, t] contiguous or NULL (out): natural-log LSE of the merged scaled scores
+ * Query head h reads KV head h / (Hq / Hkv). Every query sees every valid prefix key and its own row's keys
+ * 0..i (causal). A query with no visible key would return 0 (never happens: its own key is visible).
+ * Supports D in {64, 128}, Hq % Hkv == 0, 1 <= t <= 256, T <= cap.
+ */
+int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                     const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                     const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                     const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
+                     const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
+                     uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
+                     int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, int64_t cap,
+                     float scale, od_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OD_MI355X_H */

@@ -1,0 +1,77 @@
+"""ctypes binding of libod_mi355x.so (include/od_mi355x.h) and the torch-side plumbing around it.
+
+The library must have been built in-tree (python -m opendecider_amd.build). There is no fallback: every op of this
+package fails loudly when the library is missing or a tensor is not on the GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libod_mi355x.so")
+ABI_VERSION = 1
+
+_c_ptr = ctypes.c_void_p
+_i64 = ctypes.c_int64
+
+# name -> argtypes, matching include/od_mi355x.h
+SIGNATURES = {
+    "od_strerror": [ctypes.c_int],
+    "od_abi_version": [],
+    "od_act_quant": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr],
+    "od_w8a8_gemm": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _c_ptr, _i64,
+                     _i64, _i64, _i64, _c_ptr],
+    "od_kv_quant_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _i64, _i64, _c_ptr],
+    "od_branched_attn": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
+                         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr,
+                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _c_ptr],
+}
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded once). Raises RuntimeError if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m opendecider_amd.build` "
+                               "(there is no CPU fallback for these kernels)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_char_p if name == "od_strerror" else ctypes.c_int
+        if L.od_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH}: ABI version {L.od_abi_version()} != {ABI_VERSION}; rebuild it")
+        _LIB = L
+    return _LIB
+
+
+def check(rc: int, name: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{name} failed: {lib().od_strerror(rc).decode()} (code {rc})")
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_gpu(*tensors, name: str) -> None:
+    """The ops run only on the GPU through the HIP library; anything else is an error, never a fallback."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{name}: tensors must be on the MI355X (got device {t.device}); "
+                               "opendecider_amd has no CPU path")
+
+
+def bf16_bits(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"expected bfloat16, got {t.dtype}")
+    return t

@@ -1,0 +1,526 @@
+// Branched (Hydragen) option-row attention over an int8 shared state, for gfx950.
+//
+// Math (src/opendecider/prefix_attn.py:43-76, src/opendecider/wide_attention.py:13-67): every query of every
+// option row attends (a) all valid keys of its state's prefix and (b) its own row's keys 0..i (causal); the two
+// softmax parts are merged by log-sum-exp. Here both parts run through ONE online softmax (FlashAttention-2
+// style): the prefix key blocks first, then the row's own keys as extra masked blocks. Merging partials by LSE and
+// continuing the online softmax over the own keys are the same computation.
+//
+// Work decomposition. A "slot" is one query (option row, token, GQA head of the KV group). Grid =
+// (slot tiles, Hkv, states); a workgroup of 4 waves owns 128 consecutive slots of one (state, KV head) and streams
+// that state's int8 K/V once for all of them; a wave owns 32 slots.
+//
+// Layout trick. Scores are computed transposed, S^T = K Q^T, on V_MFMA_F32_32X32X16_F16 with the 32 keys of a key
+// tile as rows and the wave's 32 slots as columns. In the MFMA result layout lane l holds slot l % 32, so the
+// running max / sum / rescale of the online softmax are lane-local (plus one exchange with lane l ^ 32), and the
+// probabilities already sit where the second MFMA, O^T += V^T P^T, wants its B operand: k-step m of the P.V
+// product takes registers 8 (m % 2) .. +7 of key tile m / 2. The V tile is written to LDS transposed (V^T, d-major)
+// with the key order inside every 16-key group permuted to match (bits 2 and 3 of the key index swapped).
+//
+// Numerics (all exact except the fp32 accumulation and the two fp16 roundings noted):
+//  * int8 K/V values are converted to fp16 exactly (|q| <= 127) with the 0x6400 magic-number trick;
+//  * the per-(token, head) fp32 K scale is folded into the scores: s = raw * ks[j] (+ -inf for masked keys);
+//  * queries are bf16; each slot's query is multiplied by a power of two 2^e (exact) so that its absmax lies in
+//    [2^14, 2^15) and converted to fp16 (exact: fp16 has more mantissa bits than bf16); the factor 2^-e is folded
+//    with the softmax scale and log2(e) into one per-slot multiplier;
+//  * the row's own bf16 K/V get one power-of-two factor per 32-key block in the same way;
+//  * the per-key V scale is folded into the probabilities, P' = p * vs[j] / 2^E_b, rounded to fp16 (relative
+//    error 2^-11), with E_b the exponent of the block's largest V scale so that P' lies in [0, 1]; the power of two
+//    is carried in the rescale of the accumulator. P and V are therefore never rounded to bf16.
+// Masked keys get a -inf score; a block with no visible key is an exact no-op for a slot; every row's arithmetic is
+// independent of its position among the rows (fixed key order, no cross-slot reduction), so option order cannot
+// change a result.
+#include "od_common.h"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kSlotsPerTile = kWaves * 32;
+constexpr int kBlockKeys = 64;  // prefix keys per block (2 key tiles of 32)
+constexpr int kOwnKeys = 32;    // own keys per block (1 key tile)
+constexpr float kLn2 = 0.693147180559945309f;
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k_own;
+  const uint16_t* v_own;
+  const int8_t* kq;
+  const float* ks;
+  const int8_t* vq;
+  const float* vs;
+  const uint8_t* kvalid;
+  const int32_t* row_start;
+  uint16_t* out;
+  float* lse;
+  int64_t sqr, sqh, sqt, skr, skh, skt, svr, svh, svt, sor, soh, sot;
+  int R, Hq, Hkv, t, Ns, T, cap, rep;
+  float scale_log2;
+};
+
+template <int D>
+struct Smem {
+  _Float16 k[2][kBlockKeys * D];   // [key][d], 16-byte chunks swizzled by key & 7
+  _Float16 vt[2][D * kBlockKeys];  // [d][permuted key], 16-byte chunks swizzled by d & 7
+  float gk[2][kBlockKeys];         // score multiplier of key j (its K scale)
+  float kb[2][kBlockKeys];         // 0, or -inf for a masked key
+  float fv[2][kBlockKeys];         // V scale of key j divided by 2^E_b
+  int eb[2];                       // E_b
+  float red[2][kWaves];
+};
+
+template <int D>
+__device__ __forceinline__ int k_off(int key, int chunk) { return key * D + ((chunk ^ (key & 7)) << 3); }
+__device__ __forceinline__ int vt_off(int d, int chunk) { return d * kBlockKeys + ((chunk ^ (d & 7)) << 3); }
+// position of key j (0..63) inside its V^T row: bits 2 and 3 swapped
+__device__ __forceinline__ int jj_of(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
+
+__device__ __forceinline__ half2v h2_bits(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+__device__ __forceinline__ uint32_t bits_h2(half2v h) { return __builtin_bit_cast(uint32_t, h); }
+
+// 4 int8 (one dword) -> 4 exact fp16 (two dwords): byte u = q + 128 goes into the low mantissa of 1024 + u
+// (fp16 0x6400 | u), then 1152 is subtracted (exact).
+__device__ __forceinline__ void i8x4_to_h(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+  lo = bits_h2(h2_bits(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
+  hi = bits_h2(h2_bits(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  half2v h = {(_Float16)a, (_Float16)b};
+  return bits_h2(h);
+}
+
+// exponent e with |x| < 2^e (x != 0); 0 for x == 0
+__device__ __forceinline__ int exp_above(float amax) {
+  int e = 0;
+  if (amax > 0.0f) frexpf(amax, &e);
+  return e;
+}
+
+// ---------------------------------------------------------------------------------------------- block loaders
+// Prefix block (int8 state, keys j0 .. j0+63): registers first (issued before the previous block's compute), then
+// converted into LDS buffer `buf`.
+template <int D>
+struct PrefixRegs {
+  uint4 k[(kBlockKeys * D / 16 + kThreads - 1) / kThreads];
+  uint2 v[4];
+  float sc;   // thread < 64: K scale of key tid; 64 <= thread < 128: V scale of key tid - 64
+  int ok;     // key valid (thread < 64)
+};
+
+template <int D>
+__device__ __forceinline__ void prefix_load(const AttnArgs& p, int s, int g, int j0, PrefixRegs<D>& r) {
+  const int tid = threadIdx.x;
+  const int64_t head_base = ((int64_t)s * p.Hkv + g) * p.cap;
+  constexpr int kChunks = kBlockKeys * D / 16;  // 16-byte int8 chunks per K block
+  constexpr int kCpk = D / 16;                  // chunks per key
+#pragma unroll
+  for (int i = 0; i < (kChunks + kThreads - 1) / kThreads; ++i) {
+    const int cid = i * kThreads + tid;
+    const int key = cid / kCpk, c = cid % kCpk;
+    r.k[i] = make_uint4(0, 0, 0, 0);
+    if (cid < kChunks && j0 + key < p.T)
+      r.k[i] = *reinterpret_cast<const uint4*>(p.kq + (head_base + j0 + key) * D + c * 16);
+  }
+  constexpr int kDg = D / 8;
+  const int dg = tid % kDg, kg = tid / kDg;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int key = 4 * kg + a;
+    r.v[a] = make_uint2(0, 0);
+    if (kg < kBlockKeys / 4 && j0 + key < p.T)
+      r.v[a] = *reinterpret_cast<const uint2*>(p.vq + (head_base + j0 + key) * D + 8 * dg);
+  }
+  r.sc = 0.0f;
+  r.ok = 0;
+  if (tid < 2 * kBlockKeys) {
+    const int key = tid % kBlockKeys, j = j0 + key;
+    if (j < p.T) {
+      r.sc = tid < kBlockKeys ? p.ks[head_base + j] : p.vs[head_base + j];
+      r.ok = p.kvalid ? (p.kvalid[(int64_t)s * p.T + j] != 0) : 1;
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void prefix_store(Smem<D>& sm, int buf, const PrefixRegs<D>& r) {
+  const int tid = threadIdx.x;
+  constexpr int kChunks = kBlockKeys * D / 16;
+  constexpr int kCpk = D / 16;
+#pragma unroll
+  for (int i = 0; i < (kChunks + kThreads - 1) / kThreads; ++i) {
+    const int cid = i * kThreads + tid;
+    if (cid < kChunks) {
+      const int key = cid / kCpk, c = cid % kCpk;
+      uint4 h0, h1;
+      i8x4_to_h(r.k[i].x, h0.x, h0.y);
+      i8x4_to_h(r.k[i].y, h0.z, h0.w);
+      i8x4_to_h(r.k[i].z, h1.x, h1.y);
+      i8x4_to_h(r.k[i].w, h1.z, h1.w);
+      *reinterpret_cast<uint4*>(&sm.k[buf][k_off<D>(key, 2 * c)]) = h0;
+      *reinterpret_cast<uint4*>(&sm.k[buf][k_off<D>(key, 2 * c + 1)]) = h1;
+    }
+  }
+  constexpr int kDg = D / 8;
+  const int dg = tid % kDg, kg = tid / kDg;
+  if (kg < kBlockKeys / 4) {
+    // 4 keys x 8 bytes -> for each of the 8 d: the 4 keys' bytes (a 4x4 byte transpose per dword half)
+    uint32_t cols[8];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const uint32_t L0 = half ? r.v[0].y : r.v[0].x, L1 = half ? r.v[1].y : r.v[1].x;
+      const uint32_t L2 = half ? r.v[2].y : r.v[2].x, L3 = half ? r.v[3].y : r.v[3].x;
+      const uint32_t t0 = __builtin_amdgcn_perm(L1, L0, 0x05010400u);  // L0b0 L1b0 L0b1 L1b1
+      const uint32_t t1 = __builtin_amdgcn_perm(L3, L2, 0x05010400u);  // L2b0 L3b0 L2b1 L3b1
+      const uint32_t t2 = __builtin_amdgcn_perm(L1, L0, 0x07030602u);  // L0b2 L1b2 L0b3 L1b3
+      const uint32_t t3 = __builtin_amdgcn_perm(L3, L2, 0x07030602u);
+      cols[half * 4 + 0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+      cols[half * 4 + 1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+      cols[half * 4 + 2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+      cols[half * 4 + 3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+    }
+    const int jj0 = jj_of(4 * kg);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = 8 * dg + e;
+      uint2 hv;
+      i8x4_to_h(cols[e], hv.x, hv.y);
+      *reinterpret_cast<uint2*>(&sm.vt[buf][vt_off(d, jj0 >> 3) + (jj0 & 7)]) = hv;
+    }
+  }
+  // scales: wave 0 -> K scales and masks, wave 1 -> V scales with the block's power-of-two normalisation
+  if (tid < kBlockKeys) {
+    sm.gk[buf][tid] = r.ok ? r.sc : 0.0f;
+    sm.kb[buf][tid] = r.ok ? 0.0f : -INFINITY;
+  } else if (tid < 2 * kBlockKeys) {
+    const int e = exp_above(od_wave_max(r.sc));
+    sm.fv[buf][tid - kBlockKeys] = ldexpf(r.sc, -e);
+    if (tid == kBlockKeys) sm.eb[buf] = e;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------- compute
+template <int D, int KT, bool OWN>
+__device__ __forceinline__ void attend_block(const Smem<D>& sm, int buf, const half8 (&qf)[D / 16], float c_i,
+                                             float& m_run, float& l_run, int& e_run, v16f (&o)[D / 32], int own_row,
+                                             int own_j0, int slot_row, int slot_tok) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  v16f s[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    s[kt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const half8 a = *reinterpret_cast<const half8*>(&sm.k[buf][k_off<D>(kt * 32 + col, ks * 2 + h)]);
+      s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s[kt], 0, 0, 0);
+    }
+  }
+  // scores of this lane's slot: key = kt*32 + 8*(r/4) + 4*h + r%4
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int key0 = kt * 32 + 8 * r4 + 4 * h;
+      const float4 g4 = *reinterpret_cast<const float4*>(&sm.gk[buf][key0]);
+      const float4 b4 = *reinterpret_cast<const float4*>(&sm.kb[buf][key0]);
+      const float gg[4] = {g4.x, g4.y, g4.z, g4.w}, bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float y = fmaf(s[kt][4 * r4 + e], gg[e], bb[e]);
+        if (OWN && !(slot_row == own_row && own_j0 + key0 + e <= slot_tok)) y = -INFINITY;
+        s[kt][4 * r4 + e] = y;
+        mloc = fmaxf(mloc, y);
+      }
+    }
+  }
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  const float m_new = fmaxf(m_run, mloc * c_i);
+  const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_safe);
+  float psum = 0.0f;
+  half8 pb[2 * KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int key0 = kt * 32 + 8 * r4 + 4 * h;
+      const float4 f4 = *reinterpret_cast<const float4*>(&sm.fv[buf][key0]);
+      const float ff[4] = {f4.x, f4.y, f4.z, f4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * r4 + e;
+        const float pr = __builtin_amdgcn_exp2f(fmaf(s[kt][r], c_i, -m_safe));
+        psum += pr;
+        pb[kt * 2 + (r >> 3)][r & 7] = (_Float16)(pr * ff[e]);
+      }
+    }
+  }
+  psum += __shfl_xor(psum, 32, 64);
+  l_run = l_run * alpha + psum;
+  m_run = m_new;
+  const int eb = sm.eb[buf];
+  const float rs = ldexpf(alpha, e_run - eb);
+  e_run = eb;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[dt][r] *= rs;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+    for (int m = 0; m < 2 * KT; ++m) {
+      const half8 a = *reinterpret_cast<const half8*>(&sm.vt[buf][vt_off(dt * 32 + col, 2 * m + h)]);
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[m], o[dt], 0, 0, 0);
+    }
+  }
+}
+
+// Workgroup max of two values (every thread gets both).
+__device__ __forceinline__ void wg_max2(float (&red)[2][kWaves], float& a, float& b) {
+  a = od_wave_max(a);
+  b = od_wave_max(b);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][w] = a;
+    red[1][w] = b;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    a = fmaxf(a, red[0][i]);
+    b = fmaxf(b, red[1][i]);
+  }
+}
+
+// Own keys j0 .. j0+31 of option row `row` (bf16) into LDS buffer 0, scaled by powers of two into fp16.
+template <int D>
+__device__ __forceinline__ void own_stage(const AttnArgs& p, Smem<D>& sm, int row, int g, int j0) {
+  const int tid = threadIdx.x;
+  const int n_keys = min(kOwnKeys, p.t - j0);
+  const uint16_t* kb = p.k_own + (int64_t)row * p.skr + (int64_t)g * p.skh;
+  const uint16_t* vb = p.v_own + (int64_t)row * p.svr + (int64_t)g * p.svh;
+  constexpr int kCpk = D / 8;                 // 8-value chunks per key
+  constexpr int kChunks = kOwnKeys * kCpk;    // K chunks of the block
+  constexpr int kKIt = (kChunks + kThreads - 1) / kThreads;
+  uint4 kr[kKIt];
+  float ka = 0.0f, va = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kKIt; ++i) {
+    const int cid = i * kThreads + tid;
+    const int key = cid / kCpk, c = cid % kCpk;
+    kr[i] = make_uint4(0, 0, 0, 0);
+    if (cid < kChunks && key < n_keys) kr[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)(j0 + key) * p.skt + 8 * c);
+    const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      ka = fmaxf(ka, fmaxf(fabsf(__uint_as_float(w4[e] << 16)), fabsf(__uint_as_float(w4[e] & 0xffff0000u))));
+  }
+  // V: a thread takes 4 keys x 8 d (kOwnKeys / 4 key groups x D / 8 d groups <= 256 threads)
+  const int dg = tid % kCpk, kg = tid / kCpk;
+  const bool vact = kg < kOwnKeys / 4;
+  uint4 vr[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int key = 4 * kg + a;
+    vr[a] = make_uint4(0, 0, 0, 0);
+    if (vact && key < n_keys) vr[a] = *reinterpret_cast<const uint4*>(vb + (int64_t)(j0 + key) * p.svt + 8 * dg);
+    const uint32_t w4[4] = {vr[a].x, vr[a].y, vr[a].z, vr[a].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      va = fmaxf(va, fmaxf(fabsf(__uint_as_float(w4[e] << 16)), fabsf(__uint_as_float(w4[e] & 0xffff0000u))));
+  }
+  wg_max2(sm.red, ka, va);
+  const int ek = 15 - exp_above(ka), ev = 15 - exp_above(va);  // |x| 2^e < 2^15
+#pragma unroll
+  for (int i = 0; i < kKIt; ++i) {
+    const int cid = i * kThreads + tid;
+    if (cid < kChunks) {
+      const int key = cid / kCpk, c = cid % kCpk;
+      const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+      uint4 hk;
+      uint32_t* ho = &hk.x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ho[e] = pack_h2(ldexpf(__uint_as_float(w4[e] << 16), ek), ldexpf(__uint_as_float(w4[e] & 0xffff0000u), ek));
+      *reinterpret_cast<uint4*>(&sm.k[0][k_off<D>(key, c)]) = hk;
+    }
+  }
+  if (vact) {
+    const int jj0 = jj_of(4 * kg);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float vals[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const uint32_t w4[4] = {vr[a].x, vr[a].y, vr[a].z, vr[a].w};
+        const uint32_t wd = w4[e >> 1];
+        vals[a] = ldexpf(__uint_as_float((e & 1) ? (wd & 0xffff0000u) : (wd << 16)), ev);
+      }
+      uint2 hv = make_uint2(pack_h2(vals[0], vals[1]), pack_h2(vals[2], vals[3]));
+      *reinterpret_cast<uint2*>(&sm.vt[0][vt_off(8 * dg + e, jj0 >> 3) + (jj0 & 7)]) = hv;
+    }
+  }
+  if (tid < kOwnKeys) {
+    const bool ok = tid < n_keys;
+    sm.gk[0][tid] = ok ? ldexpf(1.0f, -ek) : 0.0f;
+    sm.kb[0][tid] = ok ? 0.0f : -INFINITY;
+    sm.fv[0][tid] = 1.0f;
+    if (tid == 0) sm.eb[0] = -ev;
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) {
+  __shared__ Smem<D> sm;
+  const int s = blockIdx.z, g = blockIdx.y;
+  const int row0 = p.row_start ? p.row_start[s] : 0;
+  const int nrows = p.row_start ? p.row_start[s + 1] - row0 : p.R;
+  const int per_row = p.t * p.rep;
+  const int nslots = nrows * per_row;
+  const int slot_base = blockIdx.x * kSlotsPerTile;
+  if (slot_base >= nslots) return;  // uniform over the workgroup
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  const int z = slot_base + wave * 32 + col;
+  const bool slot_ok = z < nslots;
+  int slot_row = -1, slot_tok = 0, slot_head = 0;
+  if (slot_ok) {
+    const int rl = z / per_row, rem = z - rl * per_row;
+    slot_row = row0 + rl;
+    slot_tok = rem / p.rep;
+    slot_head = g * p.rep + rem % p.rep;
+  }
+
+  // query fragments: lane holds Q[slot][ks*16 + 8h .. +8] for ks = 0 .. D/16-1, scaled by 2^eq into fp16
+  half8 qf[D / 16];
+  float c_i;  // per-slot multiplier: softmax scale * log2(e) * 2^-eq
+  {
+    uint4 raw[D / 16];
+    float qa = 0.0f;
+    const uint16_t* qp = p.q + (int64_t)slot_row * p.sqr + (int64_t)slot_head * p.sqh + (int64_t)slot_tok * p.sqt;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      raw[ks] = slot_ok ? *reinterpret_cast<const uint4*>(qp + ks * 16 + 8 * h) : make_uint4(0, 0, 0, 0);
+      const uint32_t w4[4] = {raw[ks].x, raw[ks].y, raw[ks].z, raw[ks].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        qa = fmaxf(qa, fmaxf(fabsf(__uint_as_float(w4[e] << 16)), fabsf(__uint_as_float(w4[e] & 0xffff0000u))));
+    }
+    qa = fmaxf(qa, __shfl_xor(qa, 32, 64));
+    const int eq = 15 - exp_above(qa);
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const uint32_t w4[4] = {raw[ks].x, raw[ks].y, raw[ks].z, raw[ks].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qf[ks][2 * e] = (_Float16)ldexpf(__uint_as_float(w4[e] << 16), eq);
+        qf[ks][2 * e + 1] = (_Float16)ldexpf(__uint_as_float(w4[e] & 0xffff0000u), eq);
+      }
+    }
+    c_i = ldexpf(p.scale_log2, -eq);
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  int e_run = 0;
+  v16f o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) o[dt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+  // ---- prefix: the state's int8 K/V, 64 keys per block, double buffered
+  const int nb = (p.T + kBlockKeys - 1) / kBlockKeys;
+  if (nb > 0) {
+    PrefixRegs<D> pr;
+    prefix_load<D>(p, s, g, 0, pr);
+    prefix_store<D>(sm, 0, pr);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+      const int cur = b & 1;
+      if (b + 1 < nb) prefix_load<D>(p, s, g, (b + 1) * kBlockKeys, pr);
+      attend_block<D, 2, false>(sm, cur, qf, c_i, m_run, l_run, e_run, o, 0, 0, slot_row, slot_tok);
+      if (b + 1 < nb) prefix_store<D>(sm, cur ^ 1, pr);
+      __syncthreads();
+    }
+  }
+
+  // ---- own keys: every option row that has a slot in this tile, 32 keys per block
+  const int last = min(slot_base + kSlotsPerTile, nslots) - 1;
+  const int r_lo = row0 + slot_base / per_row, r_hi = row0 + last / per_row;
+  for (int row = r_lo; row <= r_hi; ++row) {
+    for (int j0 = 0; j0 < p.t; j0 += kOwnKeys) {
+      __syncthreads();  // LDS buffer 0 free
+      own_stage<D>(p, sm, row, g, j0);
+      __syncthreads();
+      attend_block<D, 1, true>(sm, 0, qf, c_i, m_run, l_run, e_run, o, row, j0, slot_row, slot_tok);
+    }
+  }
+
+  if (!slot_ok) return;
+  // ---- epilogue: out = O 2^E / l (bf16), lse = (m + log2 l) ln 2
+  const float inv = l_run > 0.0f ? ldexpf(1.0f / l_run, e_run) : 0.0f;
+  uint16_t* op = p.out + (int64_t)slot_row * p.sor + (int64_t)slot_head * p.soh + (int64_t)slot_tok * p.sot;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int d0 = dt * 32 + 8 * r4 + 4 * h;
+      const uint32_t lo = (uint32_t)od_f32_to_bf16(o[dt][4 * r4] * inv) |
+                          ((uint32_t)od_f32_to_bf16(o[dt][4 * r4 + 1] * inv) << 16);
+      const uint32_t hi = (uint32_t)od_f32_to_bf16(o[dt][4 * r4 + 2] * inv) |
+                          ((uint32_t)od_f32_to_bf16(o[dt][4 * r4 + 3] * inv) << 16);
+      *reinterpret_cast<uint2*>(op + d0) = make_uint2(lo, hi);
+    }
+  }
+  if (p.lse && h == 0) {
+    p.lse[((int64_t)slot_row * p.Hq + slot_head) * p.t + slot_tok] =
+        l_run > 0.0f ? (m_run + __log2f(l_run)) * kLn2 : -INFINITY;
+  }
+}
+
+}  // namespace
+
+extern "C" int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, const uint16_t* k_own,
+                                int64_t skr, int64_t skh, int64_t skt, const uint16_t* v_own, int64_t svr,
+                                int64_t svh, int64_t svt, const int8_t* kq, const float* ks, const int8_t* vq,
+                                const float* vs, const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
+                                uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t R,
+                                int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, int64_t cap,
+                                float scale, od_stream_t stream) {
+  if (R < 0 || Hq < 1 || Hkv < 1 || t < 1 || Ns < 1 || T < 0 || cap < T || max_rows < 0) return OD_ERR_SHAPE;
+  if (Hq % Hkv) return OD_ERR_UNSUPPORTED;
+  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (t > 256) return OD_ERR_UNSUPPORTED;
+  if (!row_start && Ns != 1) return OD_ERR_SHAPE;
+  if (!row_start) max_rows = R;
+  if (R == 0 || max_rows == 0) return OD_OK;
+  if (!q || !k_own || !v_own || !out || (T > 0 && (!kq || !ks || !vq || !vs))) return OD_ERR_NULL;
+  const int64_t strides[] = {sqr, sqh, sqt, skr, skh, skt, svr, svh, svt};
+  for (int64_t st : strides)
+    if (st < 0 || st % 8) return OD_ERR_ALIGN;
+  if (sor < 0 || soh < 0 || sot < 0 || sor % 4 || soh % 4 || sot % 4) return OD_ERR_ALIGN;
+  if (!od_aligned16(q) || !od_aligned16(k_own) || !od_aligned16(v_own) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
+  if (T > 0 && (!od_aligned16(kq) || !od_aligned16(vq))) return OD_ERR_ALIGN;
+  const int64_t rep = Hq / Hkv;
+  const int64_t tiles = (max_rows * t * rep + kSlotsPerTile - 1) / kSlotsPerTile;
+  if (tiles > 0x7fffffff || Hkv > 65535 || Ns > 65535 || R * t * rep > 0x7fffffff || cap * Hkv * Ns * D > (1ll << 40))
+    return OD_ERR_SHAPE;
+  AttnArgs a{q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, lse, sqr, sqh, sqt, skr, skh, skt, svr, svh,
+             svt, sor, soh, sot, (int)R, (int)Hq, (int)Hkv, (int)t, (int)Ns, (int)T, (int)cap, (int)rep,
+             scale * 1.4426950408889634f};
+  dim3 grid((unsigned)tiles, (unsigned)Hkv, (unsigned)Ns), block(kThreads);
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 128) {
+    branched_attn_kernel<128><<<grid, block, 0, st>>>(a);
+  } else {
+    branched_attn_kernel<64><<<grid, block, 0, st>>>(a);
+  }
+  return od_launch_status();
+}

@@ -1,0 +1,156 @@
+"""Thin torch wrappers of the C ABI (include/od_mi355x.h): shape checks, output allocation on the current device,
+and the current HIP stream. Every function requires CUDA (ROCm) tensors and raises otherwise."""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import check, lib, ptr, require_gpu, stream_of
+
+
+def act_quant(x: torch.Tensor, inv_s: torch.Tensor | None = None, ld: int | None = None):
+    """Per-row int8 quantization of x (..., K) bf16 (Int8Tensor.quantize, quant.py:36-41), with the optional
+    SmoothQuant input scale inv_s (K,) bf16 applied first (quant.py:329). Returns (xq int8 (rows, ld), sx fp32
+    (rows,)) with rows = x.numel() // K; columns K..ld-1 of xq are zero (ld >= K pads rows for the GEMM)."""
+    require_gpu(x, inv_s, name="act_quant")
+    _lib.bf16_bits(x)
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    ld = K if ld is None else ld
+    xq = (torch.zeros if ld > K else torch.empty)(M, ld, dtype=torch.int8, device=x.device)
+    sx = torch.empty(M, dtype=torch.float32, device=x.device)
+    if inv_s is not None:
+        _lib.bf16_bits(inv_s)
+        inv_s = inv_s.contiguous()
+        if inv_s.numel() != K:
+            raise ValueError(f"inv_s has {inv_s.numel()} elements, expected {K}")
+    check(lib().od_act_quant(ptr(x2), x2.stride(0) if M > 1 else K, ptr(inv_s), ptr(xq), ld, ptr(sx), M, K,
+                             stream_of(x)), "od_act_quant")
+    return xq, sx
+
+
+def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, bias=None, residual=None,
+              out: torch.Tensor | None = None, want_out: bool = True, want_acc: bool = False):
+    """int8 a (M, Kp) x int8 w (N, Kp)^T -> bf16 (M, N) = bf16(float(acc) sa[m] sw[n] + bias + residual); Kp is
+    the padded row length (multiple of 16; padding columns are zero in both operands). Returns out, or (out, acc int32 (M, N)) with want_acc."""
+    require_gpu(a, sa, w, sw, bias, residual, out, name="w8a8_gemm")
+    if a.dtype != torch.int8 or w.dtype != torch.int8:
+        raise TypeError("w8a8_gemm: a and w must be int8")
+    M, Kp = a.shape
+    N = w.shape[0]
+    if w.shape[1] != Kp:
+        raise ValueError(f"w8a8_gemm: a has {Kp} columns, w has {w.shape[1]}")
+    if sa.numel() != M or sw.numel() != N:
+        raise ValueError("w8a8_gemm: scale sizes do not match (M, N)")
+    if want_out and out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    acc = torch.empty(M, N, dtype=torch.int32, device=a.device) if want_acc else None
+    if residual is not None:
+        _lib.bf16_bits(residual)
+        if residual.shape != (M, N) or residual.stride(-1) != 1:
+            raise ValueError("w8a8_gemm: residual must be (M, N) with contiguous rows")
+    if bias is not None:
+        _lib.bf16_bits(bias)
+        bias = bias.contiguous()
+    o = out if want_out else None
+    check(lib().od_w8a8_gemm(ptr(a), a.stride(0), ptr(sa.contiguous()), ptr(w), w.stride(0), ptr(sw.contiguous()),
+                             ptr(bias), ptr(residual), residual.stride(0) if residual is not None else 0, ptr(o),
+                             o.stride(0) if o is not None else 0, ptr(acc), N if acc is not None else 0, M, N, Kp,
+                             stream_of(a)), "od_w8a8_gemm")
+    if want_acc:
+        return o, acc
+    return o
+
+
+def kv_quant_append(x: torch.Tensor, q_cache: torch.Tensor, s_cache: torch.Tensor, n0: int) -> None:
+    """Quantize x (B, H, n, D) bf16 per (token, head) and write it at positions n0..n0+n-1 of the int8 cache
+    q_cache (B, H, cap, D) and its fp32 scales s_cache (B, H, cap) (Int8Tensor.quantize on the new tokens only,
+    state_cache.py:79)."""
+    require_gpu(x, q_cache, s_cache, name="kv_quant_append")
+    _lib.bf16_bits(x)
+    B, H, n, D = x.shape
+    if q_cache.dtype != torch.int8 or s_cache.dtype != torch.float32:
+        raise TypeError("kv_quant_append: cache must be int8 with fp32 scales")
+    if q_cache.shape[:2] != (B, H) or q_cache.shape[3] != D or s_cache.shape != q_cache.shape[:3]:
+        raise ValueError("kv_quant_append: cache shape does not match the new rows")
+    if not (q_cache.is_contiguous() and s_cache.is_contiguous()):
+        raise ValueError("kv_quant_append: cache buffers must be contiguous")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    cap = q_cache.shape[2]
+    check(lib().od_kv_quant_append(ptr(x), B, H, n, D, x.stride(0), x.stride(1), x.stride(2), ptr(q_cache),
+                                   ptr(s_cache), cap, n0, stream_of(x)), "od_kv_quant_append")
+
+
+def _rows_aligned(t: torch.Tensor) -> torch.Tensor:
+    """Last dim contiguous, 16-byte aligned base and strides that are multiples of 8 elements (16-byte loads)."""
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]):
+        t = t.contiguous()
+    return t
+
+
+def row_start_of(row_counts, device) -> tuple[torch.Tensor, int]:
+    """Device int32 offsets (Ns + 1,) of option rows grouped by state, and the largest group, from host counts.
+    Validated here on the host, so the kernel never reads an offset past the rows it was given."""
+    counts = [int(c) for c in row_counts]
+    if not counts or min(counts) < 0:
+        raise ValueError("row_counts must be a non-empty list of non-negative ints")
+    starts = [0]
+    for c in counts:
+        starts.append(starts[-1] + c)
+    return torch.tensor(starts, dtype=torch.int32).to(device, non_blocking=True), max(counts)
+
+
+def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, row_counts=None, length=None,
+                  out=None, return_lse: bool = False, row_start=None, max_rows=None):
+    """Branched option-row attention over int8 states (od_branched_attn). q (R, Hq, t, D) bf16; k_own/v_own
+    (R, Hkv, t, D) bf16; kq/vq (Ns, Hkv, cap, D) int8 of which the first T tokens are used (T = `length`, else
+    kvalid.shape[1], else cap); ks/vs (Ns, Hkv, cap) fp32; kvalid (Ns, T) bool/uint8 or None.
+    Rows are grouped by state: row_counts (host ints, one per state) or a prebuilt (row_start, max_rows) pair from
+    row_start_of(); neither means Ns == 1. Returns out (R, Hq, t, D) bf16 [, lse (R, Hq, t) fp32]."""
+    require_gpu(q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, name="branched_attn")
+    for x in (q, k_own, v_own):
+        _lib.bf16_bits(x)
+    R, Hq, t, D = q.shape
+    Hkv = k_own.shape[1]
+    Ns, _, cap, _ = kq.shape
+    if kq.dtype != torch.int8 or vq.dtype != torch.int8 or ks.dtype != torch.float32 or vs.dtype != torch.float32:
+        raise TypeError("branched_attn: state must be int8 with fp32 scales")
+    if k_own.shape != (R, Hkv, t, D) or v_own.shape != (R, Hkv, t, D):
+        raise ValueError("branched_attn: own k/v must be (R, Hkv, t, D)")
+    if kq.shape != (Ns, Hkv, cap, D) or vq.shape != kq.shape or ks.shape != (Ns, Hkv, cap) or vs.shape != ks.shape:
+        raise ValueError("branched_attn: state K/V must be (Ns, Hkv, cap, D) with scales (Ns, Hkv, cap)")
+    if not (kq.is_contiguous() and vq.is_contiguous() and ks.is_contiguous() and vs.is_contiguous()):
+        raise ValueError("branched_attn: state buffers must be contiguous")
+    T = int(length) if length is not None else (cap if kvalid is None else kvalid.shape[1])
+    if T < 0 or T > cap:
+        raise ValueError(f"branched_attn: length {T} outside [0, {cap}]")
+    if kvalid is not None:
+        if kvalid.shape != (Ns, T) or T > cap:
+            raise ValueError("branched_attn: kvalid must be (Ns, T) with T <= cap")
+        kvalid = kvalid.to(torch.uint8).contiguous()
+    if row_counts is not None:
+        if len(row_counts) != Ns or sum(int(c) for c in row_counts) != R:
+            raise ValueError("branched_attn: row_counts must have one entry per state and sum to R")
+        row_start, max_rows = row_start_of(row_counts, q.device)
+    if row_start is None:
+        if Ns != 1:
+            raise ValueError("branched_attn: row_start is required with several states")
+        max_rows = R
+    else:
+        if row_start.dtype != torch.int32 or row_start.numel() != Ns + 1:
+            raise ValueError("branched_attn: row_start must be int32 (Ns + 1,)")
+        if max_rows is None:
+            raise ValueError("branched_attn: max_rows is required with row_start")
+    q, k_own, v_own = _rows_aligned(q), _rows_aligned(k_own), _rows_aligned(v_own)
+    if out is None:
+        out = torch.empty(R, Hq, t, D, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(R, Hq, t, dtype=torch.float32, device=q.device) if return_lse else None
+    check(lib().od_branched_attn(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
+                                 *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
+                                 ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv, t,
+                                 D, Ns, T, cap, float(scale), stream_of(q)), "od_branched_attn")
+    return (out, lse) if return_lse else out

@@ -1,0 +1,52 @@
+"""Shared-prefix (Hydragen) attention for branched option rows on the MI355X.
+
+Drop-in for the op at the centre of src/opendecider/prefix_attn.py: `_split_attention` (prefix_attn.py:43-76), its
+per-state loop in `_forward` (prefix_attn.py:118-128) and the per-layer dequantized copy of the state's K/V made by
+`shared_prefix_attention` (prefix_attn.py:145-149). Here the int8 state goes to the kernel as it is stored, with
+its per-(token, head) scales, and one launch covers every row of every state: prefix partial, own causal partial
+and their log-sum-exp merge.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import kernels
+from .quant import Int8Tensor
+
+
+def _state_parts(K, V):
+    """(kq, ks, vq, vs) from Int8Tensor states (Hkv, T, D) or (Ns, Hkv, T, D) with fp32 scales (..., 1)."""
+    if not (isinstance(K, Int8Tensor) and isinstance(V, Int8Tensor)):
+        raise TypeError("the MI355X shared-prefix attention reads the int8 state: pass Int8Tensor K/V "
+                        "(as stored by the packed cache) instead of dequantized tensors")
+    kq, vq = K.q, V.q
+    ks, vs = K.scale.float(), V.scale.float()
+    if kq.dim() == 3:
+        kq, vq, ks, vs = kq[None], vq[None], ks[None], vs[None]
+    return kq.contiguous(), ks.reshape(kq.shape[:3]).contiguous(), vq.contiguous(), vs.reshape(vq.shape[:3]).contiguous()
+
+
+def _split_attention(q, k, v, Kp, Vp, pm, scale):
+    """Hydragen split for rows continuing ONE shared prefix (prefix_attn.py:43-76): q (n, Hq, t, D) attends the
+    prefix Kp/Vp (Int8Tensor, (Hkv, T, D); pm (T,) real keys or None) and its own row's k/v (n, Hkv, t, D)
+    causally; the two softmax parts are merged by their log-sum-exp. Returns (n, Hq, t, D) in v.dtype."""
+    kq, ks, vq, vs = _state_parts(Kp, Vp)
+    kvalid = None if pm is None else pm.reshape(1, -1)
+    out = kernels.branched_attn(q, k, v, kq, ks, vq, vs, scale, kvalid=kvalid, length=kq.shape[2])
+    return out.to(v.dtype)
+
+
+split_attention = _split_attention
+
+
+def split_attention_int8(q, k, v, Kq, Ks, Vq, Vs, pm, scale, row_counts=None, return_lse: bool = False):
+    """The batched form: rows of several states in one launch. q (R, Hq, t, D); k/v (R, Hkv, t, D); Kq/Vq int8
+    (Ns, Hkv, T, D) or (Hkv, T, D); Ks/Vs fp32 (Ns, Hkv, T[, 1]); pm (Ns, T) bool or None; row_counts: how many
+    consecutive rows belong to each state (rows grouped by state; None for one state)."""
+    if Kq.dim() == 3:
+        Kq, Vq, Ks, Vs = Kq[None], Vq[None], Ks[None], Vs[None]
+    Ks = Ks.float().reshape(Kq.shape[:3]).contiguous()
+    Vs = Vs.float().reshape(Vq.shape[:3]).contiguous()
+    return kernels.branched_attn(q, k, v, Kq.contiguous(), Ks, Vq.contiguous(), Vs, scale, kvalid=pm,
+                                 row_counts=row_counts, length=Kq.shape[2] if pm is None else None,
+                                 return_lse=return_lse)

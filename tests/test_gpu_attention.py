@@ -1,0 +1,123 @@
+"""GPU parity of the branched option-row attention (od_branched_attn) against the oracle.
+
+Bar: outputs within 2e-3 relative of the oracle's fp32 result (tests/helpers.py), natural-log LSE within 1e-4
+absolute, and option-row order invariance (outputs of permuted rows are the permuted outputs; required <= 1e-6,
+checked bitwise). The oracle dequantizes the int8 state in fp32 (q * s); the reference's own bf16 materialize
+(q.to(bf16) * s.to(bf16), quant.py:45) is checked against at the same 2e-3 bar on the config-1 shape.
+"""
+import math
+
+import pytest
+import torch
+
+from helpers import assert_close_rel
+from oracle import attention as oa
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def make_case(seed, Ns, row_counts, Hq, Hkv, t, D, T, cap=None, holes=False):
+    g = torch.Generator().manual_seed(seed)
+    R = sum(row_counts)
+    cap = T if cap is None else cap
+    kv_src = torch.randn(2, Ns, Hkv, T, D, generator=g).to(torch.bfloat16)
+    kq, ks = oq.quantize_rows(kv_src[0])
+    vq, vs = oq.quantize_rows(kv_src[1])
+    ks, vs = ks[..., 0], vs[..., 0]
+    if cap > T:  # capacity beyond the filled length: garbage that must not be read
+        pad = lambda x, v: torch.cat([x, torch.full((*x.shape[:2], cap - T, *x.shape[3:]), v, dtype=x.dtype)], 2)
+        kq, vq, ks, vs = pad(kq, 99), pad(vq, -99), pad(ks, 1e3), pad(vs, 1e3)
+    q = torch.randn(R, Hq, t, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(R, Hkv, t, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(R, Hkv, t, D, generator=g).to(torch.bfloat16)
+    kvalid = None
+    if holes:
+        kvalid = torch.ones(Ns, T, dtype=torch.bool)
+        kvalid[-1, : T // 3] = False
+        kvalid[0, T // 2: T // 2 + 5] = False
+    row_state = torch.repeat_interleave(torch.arange(Ns), torch.tensor(row_counts))
+    return dict(q=q, k=k, v=v, kq=kq, ks=ks, vq=vq, vs=vs, kvalid=kvalid, row_counts=row_counts,
+                row_state=row_state, T=T, scale=D ** -0.5)
+
+
+def run_gpu(c, return_lse=True, q=None):
+    from opendecider_amd import kernels
+    Ns = c["kq"].shape[0]
+    return kernels.branched_attn(
+        c["q"].to(DEV) if q is None else q, c["k"].to(DEV), c["v"].to(DEV), c["kq"].to(DEV), c["ks"].to(DEV),
+        c["vq"].to(DEV), c["vs"].to(DEV), c["scale"],
+        kvalid=None if c["kvalid"] is None else c["kvalid"].to(DEV),
+        row_counts=c["row_counts"] if Ns > 1 else None, length=c["T"], return_lse=return_lse)
+
+
+def run_oracle(c, dequant="fp32"):
+    T = c["T"]
+    return oa.branched_attention_int8(c["q"], c["k"], c["v"], c["kq"][:, :, :T], c["ks"][:, :, :T],
+                                      c["vq"][:, :, :T], c["vs"][:, :, :T], c["scale"], c["kvalid"], c["row_state"],
+                                      dequant=dequant)
+
+
+CASES = {
+    "two_states_holes": dict(seed=1, Ns=2, row_counts=[3, 2], Hq=8, Hkv=2, t=5, D=128, T=100, holes=True),
+    "own_two_chunks_d64": dict(seed=2, Ns=1, row_counts=[3], Hq=4, Hkv=4, t=40, D=64, T=64),
+    "own_only_T0": dict(seed=3, Ns=1, row_counts=[2], Hq=4, Hkv=2, t=7, D=128, T=0),
+    "gqa8_T130_cap200": dict(seed=4, Ns=1, row_counts=[5], Hq=32, Hkv=4, t=3, D=128, T=130, cap=200),
+    "empty_state_group": dict(seed=5, Ns=3, row_counts=[2, 0, 3], Hq=8, Hkv=2, t=9, D=128, T=70),
+    "t1_single_token_rows": dict(seed=6, Ns=2, row_counts=[4, 3], Hq=8, Hkv=8, t=1, D=64, T=257),
+    "config4_like_t12": dict(seed=7, Ns=1, row_counts=[11], Hq=32, Hkv=8, t=12, D=128, T=300),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_branched_attention_matches_oracle(gpu_lib, name):
+    c = make_case(**CASES[name])
+    out, lse = run_gpu(c)
+    ref, ref_lse = run_oracle(c)
+    assert_close_rel(out.float().cpu(), ref, what=name)
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+
+
+def test_all_prefix_keys_masked_gives_own_part(gpu_lib):
+    """A state whose keys are all masked: the rows see only their own keys (wide_attention.py:62 rule)."""
+    c = make_case(seed=8, Ns=1, row_counts=[3], Hq=4, Hkv=2, t=6, D=128, T=80)
+    c["kvalid"] = torch.zeros(1, 80, dtype=torch.bool)
+    out, _ = run_gpu(c)
+    own, _ = oa.attention(c["q"], c["k"], c["v"], c["scale"], None, causal=True)
+    assert_close_rel(out.float().cpu(), own, what="masked prefix")
+
+
+def test_strided_query_view(gpu_lib):
+    """q as the (R, t, Hq, D) projection viewed (R, Hq, t, D), the layout a fused QKV GEMM produces."""
+    c = make_case(seed=9, Ns=1, row_counts=[4], Hq=8, Hkv=2, t=6, D=128, T=90)
+    qv = c["q"].transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    assert not qv.is_contiguous()
+    out_s, _ = run_gpu(c, q=qv)
+    out_c, _ = run_gpu(c)
+    assert torch.equal(out_s, out_c)
+
+
+def test_option_order_invariance_bitwise(gpu_lib):
+    """Shuffling the option rows of each request permutes the outputs and changes nothing else (bitwise)."""
+    c = make_case(seed=10, Ns=4, row_counts=[8, 8, 8, 8], Hq=32, Hkv=8, t=16, D=128, T=256)
+    g = torch.Generator().manual_seed(11)
+    perm = torch.cat([torch.randperm(8, generator=g) + 8 * i for i in range(4)])
+    out, lse = run_gpu(c)
+    cp = dict(c, q=c["q"][perm], k=c["k"][perm], v=c["v"][perm])
+    out_p, lse_p = run_gpu(cp)
+    assert torch.equal(out_p, out[perm.to(DEV)])
+    assert torch.equal(lse_p, lse[perm.to(DEV)])
+
+
+def test_config1_branched_attention_full_shape(gpu_lib):
+    """8 requests; state S=2048 int8 K/V with per-token-per-head fp32 scales (source bf16 N(0,1)); 32 option rows of
+    16 tokens per request; GQA 32 query / 8 KV heads; head_dim 128; no prefix mask; own tokens causal; LSE merge."""
+    c = make_case(seed=1, Ns=8, row_counts=[32] * 8, Hq=32, Hkv=8, t=16, D=128, T=2048)
+    out, lse = run_gpu(c)
+    ref, ref_lse = run_oracle(c)
+    e = assert_close_rel(out.float().cpu(), ref, what="config1 vs fp32 dequant")
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+    ref_b, _ = run_oracle(c, dequant="bf16")
+    assert_close_rel(out.float().cpu(), ref_b, what="config1 vs reference bf16 materialize")
+    print(f"config1 norm-relative error vs fp32-dequant oracle: {e:.2e}")

@@ -1,0 +1,194 @@
+"""GPU parity of the quantizers and the W8A8 GEMM against the oracle (bit-exact bytes, scales and int32 accumulators;
+bit-exact bf16 epilogue, which runs the oracle's fp32 operations in the same order)."""
+import pytest
+import torch
+
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _x(g, M, K, outliers=0.01, scale=1.0):
+    x = torch.randn(M, K, generator=g) * scale
+    n_out = max(1, int(round(outliers * K))) if outliers else 0
+    if n_out:
+        x[:, torch.randperm(K, generator=g)[:n_out]] *= 20
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,K", [(1, 8), (5, 64), (33, 128), (17, 200), (7, 37), (64, 4096), (3, 12288), (300, 520)])
+@pytest.mark.parametrize("smooth", [False, True])
+def test_act_quant_bit_exact(gpu_lib, M, K, smooth):
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(M * 1000 + K)
+    x = _x(g, M, K)
+    if M > 2:
+        x[1] = 0                                          # all-zero row: clamp_min(1e-8)
+    inv = (1.0 / (torch.rand(K, generator=g) * 1.5 + 0.5)).to(torch.bfloat16) if smooth else None
+    xq, sx = kernels.act_quant(x.to(DEV), None if inv is None else inv.to(DEV))
+    rq, rs = oq.act_quant(x, inv)
+    assert torch.equal(xq.cpu(), rq)
+    assert torch.equal(sx.cpu(), rs)
+
+
+def test_act_quant_strided_rows_and_padding(gpu_lib):
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(1)
+    big = _x(g, 40, 96)
+    x = big[:, 16:80]                                     # row stride 96, K = 64
+    xd = big.to(DEV)[:, 16:80]
+    assert xd.stride(0) == 96
+    xq, sx = kernels.act_quant(xd, None, ld=80)
+    rq, rs = oq.act_quant(x)
+    assert torch.equal(xq[:, :64].cpu(), rq) and torch.equal(sx.cpu(), rs)
+    assert (xq[:, 64:] == 0).all()
+
+
+@pytest.mark.parametrize("B,H,n,D,n0,cap", [(1, 8, 256, 128, 0, 256), (2, 8, 37, 128, 100, 200), (3, 2, 5, 64, 7, 12),
+                                            (1, 4, 9, 256, 0, 9), (2, 3, 4, 40, 1, 6)])
+def test_kv_quant_append_bytes(gpu_lib, B, H, n, D, n0, cap):
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(B + H + n + D)
+    x = torch.randn(B, H, n, D, generator=g).to(torch.bfloat16)
+    qc = torch.zeros(B, H, cap, D, dtype=torch.int8, device=DEV)
+    sc = torch.zeros(B, H, cap, dtype=torch.float32, device=DEV)
+    kernels.kv_quant_append(x.to(DEV), qc, sc, n0)
+    rq, rs = oq.quantize_rows(x)
+    assert torch.equal(qc[:, :, n0:n0 + n].cpu(), rq)
+    assert torch.equal(sc[:, :, n0:n0 + n].cpu(), rs[..., 0])
+    assert (qc[:, :, :n0] == 0).all() and (qc[:, :, n0 + n:] == 0).all() and (sc[:, :, n0 + n:] == 0).all()
+
+
+def test_kv_append_strided_input_equals_whole(gpu_lib):
+    """(B, T, H, D) projections viewed as (B, H, T, D): two appends == quantizing the whole tensor."""
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(2, 50, 4, 128, generator=g).to(torch.bfloat16)      # (B, T, H, D)
+    xv = x.to(DEV).transpose(1, 2)                                       # (B, H, T, D) view
+    qc = torch.zeros(2, 4, 64, 128, dtype=torch.int8, device=DEV)
+    sc = torch.zeros(2, 4, 64, dtype=torch.float32, device=DEV)
+    kernels.kv_quant_append(xv[:, :, :30], qc, sc, 0)
+    kernels.kv_quant_append(xv[:, :, 30:], qc, sc, 30)
+    rq, rs = oq.quantize_rows(x.transpose(1, 2))
+    assert torch.equal(qc[:, :, :50].cpu(), rq) and torch.equal(sc[:, :, :50].cpu(), rs[..., 0])
+
+
+def _gemm_case(g, M, N, K):
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sa = torch.rand(M, generator=g) * 0.05 + 1e-3
+    sw = torch.rand(N, generator=g) * 1.5e-3 + 0.5e-3
+    return a, w, sa, sw
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 16), (7, 33, 48), (256, 256, 128), (300, 200, 208), (64, 6144, 512),
+                                   (513, 4097, 1040), (256, 4096, 4096)])
+def test_gemm_int32_accumulators_bit_exact(gpu_lib, M, N, K):
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(M + N + K)
+    a, w, sa, sw = _gemm_case(g, M, N, K)
+    out, acc = kernels.w8a8_gemm(a.to(DEV), sa.to(DEV), w.to(DEV), sw.to(DEV), want_acc=True)
+    ref_acc = oq.int_gemm(a, w)
+    assert torch.equal(acc.cpu(), ref_acc)
+    assert torch.equal(out.cpu(), oq.w8a8_epilogue(ref_acc, sa, sw))
+
+
+def test_gemm_extreme_accumulators(gpu_lib):
+    """+-127 everywhere at K = 12288: the largest |acc| the 9B shapes reach (1.98e8) stays exact."""
+    from opendecider_amd import kernels
+    M, N, K = 64, 64, 12288
+    a = torch.full((M, K), 127, dtype=torch.int8)
+    a[1::2] = -127
+    w = torch.full((N, K), 127, dtype=torch.int8)
+    _, acc = kernels.w8a8_gemm(a.to(DEV), torch.ones(M, device=DEV), w.to(DEV), torch.ones(N, device=DEV),
+                               want_acc=True)
+    assert torch.equal(acc.cpu(), oq.int_gemm(a, w))
+    assert acc[0, 0].item() == 127 * 127 * K and acc[1, 0].item() == -127 * 127 * K
+
+
+def test_gemm_bias_residual_epilogue(gpu_lib):
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(3)
+    M, N, K = 130, 96, 256
+    a, w, sa, sw = _gemm_case(g, M, N, K)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    out = kernels.w8a8_gemm(a.to(DEV), sa.to(DEV), w.to(DEV), sw.to(DEV), bias.to(DEV), res.to(DEV))
+    assert torch.equal(out.cpu(), oq.w8a8_epilogue(oq.int_gemm(a, w), sa, sw, bias, res))
+
+
+def test_config0_single_w8a8_linear(gpu_lib):
+    """X bf16 [256,4096] N(0,1) with 1% outlier channels x20, per-token int8; W int8 [4096,4096] uniform in
+    [-127,127]; per-channel fp32 scales U(0.5e-3, 2e-3); int32 accumulators compared exactly."""
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(0)
+    x = _x(g, 256, 4096)
+    w = torch.randint(-127, 128, (4096, 4096), generator=g, dtype=torch.int8)
+    sw = torch.rand(4096, generator=g) * 1.5e-3 + 0.5e-3
+    xq, sx = kernels.act_quant(x.to(DEV))
+    out, acc = kernels.w8a8_gemm(xq, sx, w.to(DEV), sw.to(DEV), want_acc=True)
+    rout, racc, rxq, rsx = oq.w8a8_linear(x, w, sw)
+    assert torch.equal(xq.cpu(), rxq) and torch.equal(sx.cpu(), rsx)
+    assert torch.equal(acc.cpu(), racc)
+    assert torch.equal(out.cpu(), rout)
+
+
+def test_w8a8_linear_module_smoothquant(gpu_lib):
+    """W8A8Linear.from_linear with a SmoothQuant fold == the oracle's W8A8 linear on the same weights."""
+    from opendecider_amd.quant import SmoothedLinear, W8A8Linear, smooth_a8w8_
+    g = torch.Generator().manual_seed(4)
+    K, N = 512, 384
+    lin = torch.nn.Linear(K, N, bias=True).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_((torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16))
+    s = torch.rand(K, generator=g) * 1.5 + 0.5
+    x = _x(g, 3 * 41, K).view(3, 41, K)
+    net = torch.nn.Sequential(lin).to(DEV)
+    smooth_a8w8_(net, {"0": s})
+    assert isinstance(net[0], SmoothedLinear) and isinstance(net[0].inner, W8A8Linear)
+    y = net(x.to(DEV))
+    wq, sw = oq.quantize_weight(oq.smooth_fold(lin.weight.data.cpu(), s))
+    inv = net[0].inner.inv_s.cpu()
+    # bf16(1/s): the GPU reciprocal may differ from the CPU one by one bf16 step on rare ties
+    assert ((inv.float() - oq.smooth_inv(s).float()).abs() <= inv.float().abs() * 2.0 ** -7).all()
+    ref, _, _, _ = oq.w8a8_linear(x.reshape(-1, K), wq, sw, lin.bias.data.cpu(), inv)
+    assert torch.equal(net[0].inner.qweight.cpu(), wq)
+    assert torch.equal(net[0].inner.w_scale.cpu(), sw)
+    assert torch.equal(y.reshape(-1, N).cpu(), ref)
+
+
+def test_fused_kernels_keep_module_objects_and_hooks(gpu_lib):
+    """Restates the reference's test_fused_kernels_keep_module_objects_and_hooks (test_int8_gemm.py:52-67) and
+    test_dense_path_reads_the_packed_weights_exactly (:33-49) for the W8A8 slot."""
+    from opendecider_amd.quant import Int8Linear, fast_int8_kernels_
+    torch.manual_seed(0)
+    lin = Int8Linear(torch.nn.Linear(256, 128, bias=False).to(DEV).to(torch.bfloat16))
+    w_ref = lin.weight.clone()
+
+    class BB:
+        device = torch.device(DEV)
+        lm = torch.nn.Module()
+    BB.lm.layers = torch.nn.Sequential(lin)
+    lin.register_forward_hook(lambda mod, args, out: out + 100.0)
+    x = torch.randn(8, 256, device=DEV, dtype=torch.bfloat16)
+    y0 = BB.lm.layers(x).float()
+    assert fast_int8_kernels_(BB) == 1
+    assert BB.lm.layers[0] is lin and lin.qweight.numel() == 0
+    assert torch.equal(lin.weight, w_ref)
+    y1 = BB.lm.layers(x).float()
+    assert (y1 - 100.0).abs().mean() < 50 and ((y1 - y0).norm() / y0.norm()).item() < 1e-2
+
+
+def test_int8_tensor_quantize_matches_reference_formula(gpu_lib):
+    from opendecider_amd.quant import Int8Tensor
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 5, 64, generator=g).to(torch.bfloat16)
+    t = Int8Tensor.quantize(x.to(DEV))
+    rq, rs = oq.quantize_rows(x)
+    assert torch.equal(t.q.cpu(), rq)
+    assert t.scale.dtype == torch.bfloat16 and torch.equal(t.scale.cpu(), rs.to(torch.bfloat16))
+    t32 = Int8Tensor.quantize(x.to(DEV), scale_dtype=torch.float32)
+    assert torch.equal(t32.scale.cpu(), rs)
+    err = (t.dequantize().float().cpu() - x.float()).abs().max()
+    assert err <= x.float().abs().amax() / 127 + 1e-2

@@ -1,0 +1,126 @@
+"""Pins the attention oracle (oracle/attention.py): float64 brute-force softmax loops on tiny shapes, the LSE merge
+against ONE softmax over the concatenated keys (the reference's math note, docs/branched_shared_prefix_math.md
+:39-48), torch.logsumexp, permutation equivariance over option rows, and the empty-key-set rules of
+wide_attention.py:62,65-67."""
+import pytest
+import torch
+
+from oracle import attention as oa
+
+
+def _rand(g, *shape):
+    return torch.randn(*shape, generator=g)
+
+
+@pytest.mark.parametrize("B,H,G,T,S,causal", [(1, 4, 2, 5, 5, True), (2, 4, 1, 3, 9, True), (1, 2, 2, 4, 7, False),
+                                              (2, 6, 3, 1, 4, True)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_attention_matches_brute_force(B, H, G, T, S, causal, masked):
+    g = torch.Generator().manual_seed(B * 100 + T * 10 + S)
+    D, Dv = 8, 6
+    q, k, v = _rand(g, B, H, T, D), _rand(g, B, G, S, D), _rand(g, B, G, S, Dv)
+    kvalid = None
+    if masked:
+        kvalid = torch.ones(B, S, dtype=torch.bool)
+        kvalid[-1, : S // 2] = False
+    o, lse = oa.attention(q, k, v, 0.37, kvalid, causal, dtype=torch.float64)
+    rep = H // G
+    for b in range(B):
+        for h in range(H):
+            allowed = [[(not causal or j <= i + S - T) and (kvalid is None or bool(kvalid[b, j])) for j in range(S)]
+                       for i in range(T)]
+            ob, lb = oa.brute_force_attention(q[b, h], k[b, h // rep], v[b, h // rep], 0.37, allowed)
+            assert torch.allclose(o[b, h], ob, atol=1e-12)
+            fin = torch.isfinite(lb)
+            assert torch.equal(fin, torch.isfinite(lse[b, h]))
+            assert torch.allclose(lse[b, h][fin], lb[fin], atol=1e-12)
+
+
+def test_empty_rows_give_zero_and_neg_inf():
+    g = torch.Generator().manual_seed(1)
+    q, k, v = _rand(g, 1, 2, 3, 4), _rand(g, 1, 1, 5, 4), _rand(g, 1, 1, 5, 4)
+    kvalid = torch.zeros(1, 5, dtype=torch.bool)
+    o, lse = oa.attention(q, k, v, 0.5, kvalid, causal=False)
+    assert torch.equal(o, torch.zeros_like(o)) and torch.isneginf(lse).all()
+
+
+def test_lse_is_logsumexp_of_scaled_scores():
+    g = torch.Generator().manual_seed(2)
+    q, k, v = _rand(g, 2, 4, 6, 16), _rand(g, 2, 2, 11, 16), _rand(g, 2, 2, 11, 16)
+    o, lse = oa.attention(q, k, v, 16 ** -0.5, causal=False, dtype=torch.float64)
+    s = torch.einsum("bhtd,bhsd->bhts", q.double(), k.double().repeat_interleave(2, 1)) * 16 ** -0.5
+    assert torch.allclose(lse, torch.logsumexp(s, -1), atol=1e-12)
+    assert torch.allclose(o, torch.softmax(s, -1) @ v.double().repeat_interleave(2, 1), atol=1e-12)
+
+
+def _one_softmax_split(q, k, v, Kp, Vp, pm, scale):
+    """One softmax per query over [prefix keys ; own keys] with the split's mask, float64 brute force."""
+    n, Hq, t, D = q.shape
+    Hkv, T = Kp.shape[0], Kp.shape[1]
+    rep = Hq // Hkv
+    out = torch.zeros(n, Hq, t, Vp.shape[-1], dtype=torch.float64)
+    lse = torch.zeros(n, Hq, t, dtype=torch.float64)
+    for r in range(n):
+        for h in range(Hq):
+            kk = torch.cat([Kp[h // rep], k[r, h // rep]], 0)
+            vv = torch.cat([Vp[h // rep], v[r, h // rep]], 0)
+            allowed = [[(j < T and (pm is None or bool(pm[j]))) or (j >= T and j - T <= i) for j in range(T + t)]
+                       for i in range(t)]
+            out[r, h], lse[r, h] = oa.brute_force_attention(q[r, h], kk, vv, scale, allowed)
+    return out, lse
+
+
+@pytest.mark.parametrize("pm_kind", ["none", "holes", "all_masked"])
+def test_split_merge_equals_one_softmax(pm_kind):
+    g = torch.Generator().manual_seed(4)
+    n, Hq, Hkv, t, T, D = 3, 4, 2, 4, 9, 8
+    q, k, v = _rand(g, n, Hq, t, D), _rand(g, n, Hkv, t, D), _rand(g, n, Hkv, t, D)
+    Kp, Vp = _rand(g, Hkv, T, D), _rand(g, Hkv, T, D)
+    pm = None
+    if pm_kind == "holes":
+        pm = torch.ones(T, dtype=torch.bool)
+        pm[[0, 1, 5]] = False
+    elif pm_kind == "all_masked":
+        pm = torch.zeros(T, dtype=torch.bool)
+    out, lse = oa.split_attention(q, k, v, Kp, Vp, pm, 0.3, dtype=torch.float64)
+    ref, ref_lse = _one_softmax_split(q, k, v, Kp, Vp, pm, 0.3)
+    assert torch.allclose(out, ref, atol=1e-12) and torch.allclose(lse, ref_lse, atol=1e-12)
+
+
+def test_split_rows_are_permutation_equivariant():
+    g = torch.Generator().manual_seed(6)
+    n, Hq, Hkv, t, T, D = 6, 4, 1, 3, 10, 8
+    q, k, v = _rand(g, n, Hq, t, D), _rand(g, n, Hkv, t, D), _rand(g, n, Hkv, t, D)
+    Kp, Vp = _rand(g, Hkv, T, D), _rand(g, Hkv, T, D)
+    perm = torch.randperm(n, generator=g)
+    out, _ = oa.split_attention(q, k, v, Kp, Vp, None, 0.3)
+    out_p, _ = oa.split_attention(q[perm], k[perm], v[perm], Kp, Vp, None, 0.3)
+    assert (out_p - out[perm]).abs().max().item() <= 1e-6
+
+
+def test_branched_int8_rows_read_their_state():
+    """row_state routes each row to its state: equal to running split_attention per state on dequantized K/V."""
+    g = torch.Generator().manual_seed(7)
+    Ns, R, Hq, Hkv, t, T, D = 2, 5, 4, 2, 3, 6, 8
+    kq = torch.randint(-127, 128, (Ns, Hkv, T, D), generator=g, dtype=torch.int8)
+    vq = torch.randint(-127, 128, (Ns, Hkv, T, D), generator=g, dtype=torch.int8)
+    ks, vs = torch.rand(Ns, Hkv, T, generator=g) * 0.02, torch.rand(Ns, Hkv, T, generator=g) * 0.02
+    q, k, v = _rand(g, R, Hq, t, D), _rand(g, R, Hkv, t, D), _rand(g, R, Hkv, t, D)
+    rs = torch.tensor([1, 0, 1, 1, 0])
+    out, lse = oa.branched_attention_int8(q, k, v, kq, ks, vq, vs, 0.3, row_state=rs)
+    for r in range(R):
+        s = int(rs[r])
+        Kp = kq[s].float() * ks[s][..., None]
+        Vp = vq[s].float() * vs[s][..., None]
+        o1, l1 = oa.split_attention(q[r:r + 1], k[r:r + 1], v[r:r + 1], Kp, Vp, None, 0.3)
+        assert torch.allclose(out[r], o1[0], atol=1e-6) and torch.allclose(lse[r], l1[0], atol=1e-6)
+
+
+def test_bf16_dequant_is_the_reference_materialize():
+    g = torch.Generator().manual_seed(8)
+    kq = torch.randint(-127, 128, (2, 5, 8), generator=g, dtype=torch.int8)
+    ks = torch.rand(2, 5, generator=g) * 0.03
+    got = oa.dequant_state(kq, ks, "bf16")
+    exp = (kq.to(torch.bfloat16) * ks[..., None].to(torch.bfloat16)).float()
+    assert torch.equal(got, exp)
+    assert torch.equal(oa.dequant_state(kq, ks, "fp32"), kq.float() * ks[..., None])
