@@ -1,30 +1,49 @@
 """Tolerances shared by the parity tests.
 
-Floating-point outputs are held to the path's stated bar, 2e-3 relative, in two forms:
-  * norm-relative:  ||out - ref||_2 <= 2e-3 ||ref||_2
-  * elementwise:    |out - ref| <= 2e-3 (|ref| + rms(ref))
-`ref` is the oracle's fp32 value (before any bf16 rounding), so a bf16 output's own rounding (<= 2^-9 relative)
-is inside the budget. Probabilities are held to 1e-4 absolute. Integer and byte outputs are compared exactly.
+The path's bar for floating-point outputs is 2e-3 relative against the oracle's fp32 result. A bf16 output cannot
+agree elementwise with an fp32 value to better than its own rounding (up to 2^-9 relative, and two candidate
+roundings differ by 2^-8), so the bar is checked in three forms:
+  * norm-relative, whole tensor:     ||out - ref||_2 <= 2e-3 ||ref||_2
+  * norm-relative, every slice along dim 0 (one option row, one token row, ...)
+  * elementwise:                     |out - ref| <= 2^-8 |ref| + 2e-3 rms(ref)
+    (one bf16 step at the element's own magnitude, plus 2e-3 of the tensor's rms for the kernel's own error)
+Probabilities are held to 1e-4 absolute. Integer and byte outputs are compared exactly.
 """
 import torch
 
 REL = 2e-3
 PROB_ABS = 1e-4
+BF16_STEP = 2.0 ** -8
 
 
 def rel_err(out: torch.Tensor, ref: torch.Tensor) -> float:
     out, ref = out.detach().double().cpu(), ref.detach().double().cpu()
-    return ((out - ref).norm() / ref.norm().clamp_min(1e-30)).item()
+    return ((out - ref).norm() / ref.norm().clamp_min(1e-300)).item()
 
 
-def assert_close_rel(out: torch.Tensor, ref: torch.Tensor, rel: float = REL, what: str = ""):
+def error_stats(out: torch.Tensor, ref: torch.Tensor) -> dict:
+    out, ref = out.detach().double().cpu(), ref.detach().double().cpu()
+    d = (out - ref).abs()
+    rms = ref.pow(2).mean().sqrt().clamp_min(1e-300)
+    return {
+        "norm_rel": ((out - ref).norm() / ref.norm().clamp_min(1e-300)).item(),
+        "max_abs_over_rms": (d.max() / rms).item(),
+        "elem_ratio": (d / (BF16_STEP * ref.abs() + REL * rms)).max().item(),  # <= 1 passes
+    }
+
+
+def assert_close_rel(out: torch.Tensor, ref: torch.Tensor, rel: float = REL, what: str = "") -> dict:
     out, ref = out.detach().double().cpu(), ref.detach().double().cpu()
     assert out.shape == ref.shape, (what, out.shape, ref.shape)
     assert torch.isfinite(out).all(), f"{what}: non-finite values"
-    e = rel_err(out, ref)
-    assert e <= rel, f"{what}: norm-relative error {e:.3e} > {rel}"
+    st = error_stats(out, ref)
+    assert st["norm_rel"] <= rel, f"{what}: norm-relative error {st}"
+    if out.dim() > 1 and out.shape[0] > 1:
+        o2, r2 = out.reshape(out.shape[0], -1), ref.reshape(ref.shape[0], -1)
+        per = ((o2 - r2).norm(dim=1) / r2.norm(dim=1).clamp_min(1e-300))
+        st["worst_slice_norm_rel"] = per.max().item()
+        assert st["worst_slice_norm_rel"] <= rel, f"{what}: a slice along dim 0 is beyond {rel}: {st}"
     rms = ref.pow(2).mean().sqrt()
-    bad = (out - ref).abs() > rel * (ref.abs() + rms)
-    assert not bad.any(), (f"{what}: {int(bad.sum())} elements beyond {rel} (|ref| + rms); worst "
-                           f"{((out - ref).abs() / (ref.abs() + rms)).max().item():.3e}")
-    return e
+    bad = (out - ref).abs() > BF16_STEP * ref.abs() + rel * rms
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond 2^-8|ref| + {rel} rms: {st}"
+    return st
