@@ -113,6 +113,35 @@ int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
                      int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, int64_t cap,
                      float scale, od_stream_t stream);
 
+/*
+ * Row kernels of the dense decoder layer that carries the path in the decision-forward harness (not reference
+ * functions: the reference runs these steps inside HF Qwen3.5 modules; they are fused here around the W8A8 GEMMs).
+ *
+ * od_rmsnorm_quant: y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), optionally y = bf16(y * inv_s), then the
+ *   od_act_quant formula per row. x bf16 [M, K] (row stride ldx), w / inv_s bf16 [K], xq int8 [M, ldq], sx fp32 [M].
+ */
+int od_rmsnorm_quant(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* inv_s, float eps, int8_t* xq,
+                     int64_t ldq, float* sx, int64_t M, int64_t K, od_stream_t stream);
+
+/*
+ * od_silu_mul_quant: y = bf16(bf16(silu(g)) * u) with g = gu[:, :F], u = gu[:, F:2F] (fused gate+up GEMM output,
+ *   row stride ldg), optionally y = bf16(y * inv_s), then the od_act_quant formula per row -> aq int8 [M, ldq],
+ *   sa fp32 [M].
+ */
+int od_silu_mul_quant(const uint16_t* gu, int64_t ldg, int64_t F, const uint16_t* inv_s, int8_t* aq, int64_t ldq,
+                      float* sa, int64_t M, od_stream_t stream);
+
+/*
+ * od_qk_norm_rope: in place on the QKV GEMM output qkv bf16 [M, ld] whose row holds n_heads_q query heads then
+ *   n_heads_k key heads of D values: per head n = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))) (w = q_w or k_w,
+ *   bf16 [D]), then rotary embedding out = bf16(bf16(n * cos) + bf16(rotate_half(n) * sin)) with cos/sin bf16
+ *   tables [n_pos, D/2] indexed by pos[row] (int32 [M]; a position outside [0, n_pos) yields NaN). Same convention
+ *   as the reference's apply_rotary_pos_emb call (src/opendecider/prefix_attn.py:81,90). D in {64, 128}.
+ */
+int od_qk_norm_rope(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int64_t n_heads_k, int64_t D,
+                    const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t, const uint16_t* sin_t,
+                    int64_t n_pos, const int32_t* pos, float eps, od_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

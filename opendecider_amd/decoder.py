@@ -1,0 +1,203 @@
+"""Decision-forward harness on the MI355X: a dense 9B-class decoder whose linears are W8A8 (int8 MFMA), whose
+option-row attention is the branched kernel over int8 state K/V, with the option readout on top.
+
+This is the backbone stand-in that carries the path (the reference runs the same per-layer steps inside HF Qwen3.5
+modules: the W8A8 linears in every nn.Linear slot, src/opendecider/prefix_attn.py:79-131 for the attention layer,
+option logits + 'none' in src/opendecider/v3.py:639-643,701-709 and the softmax in src/opendecider/decider.py:255-257).
+Per layer, for the M = rows x tokens option-row tokens:
+    od_rmsnorm_quant -> od_w8a8_gemm (QKV) -> od_qk_norm_rope -> od_branched_attn -> od_act_quant
+    -> od_w8a8_gemm (O, + residual) -> od_rmsnorm_quant -> od_w8a8_gemm (gate+up) -> od_silu_mul_quant
+    -> od_w8a8_gemm (down, + residual)
+All activations live in preallocated HBM buffers; nothing allocates or synchronizes inside a forward, so the whole
+forward can be captured in one HIP graph.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import kernels
+from .kv_cache import Int8KVCache
+
+
+@dataclass
+class DecoderConfig:
+    hidden: int = 4096
+    ffn: int = 12288
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    n_layers: int = 36
+    vocab: int = 151936
+    eps: float = 1e-6
+    theta: float = 1e6
+
+    @property
+    def qkv_out(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+def rope_tables(cfg: DecoderConfig, n_pos: int):
+    """cos/sin bf16 tables [n_pos, D/2]: inv_freq = 1 / theta^(2i/D), angle = pos * inv_freq in fp32 (computed on
+    the host, as the rotary-embedding module of the backbone does)."""
+    D = cfg.head_dim
+    inv_freq = 1.0 / (cfg.theta ** (torch.arange(0, D, 2, dtype=torch.int64).float() / D))
+    ang = torch.arange(n_pos, dtype=torch.float32)[:, None] * inv_freq[None, :]
+    return ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+
+
+class QLinear:
+    """One W8A8 linear's device tensors: int8 weight (out, in), fp32 per-output-channel scale, bf16 1/s."""
+
+    def __init__(self, w: torch.Tensor, s: torch.Tensor | None, device):
+        w = w.to(device)
+        inv = None
+        if s is not None:
+            # fold W * s per input channel in fp32, round to bf16 (quant.py:343-344); bf16(1/s) (quant.py:325)
+            w = (w.float() * s.to(device, torch.float32)[None, :]).to(torch.bfloat16)
+            inv = (1.0 / s.float().cpu()).to(torch.bfloat16).to(device)
+        q, sc = kernels.act_quant(w.to(torch.bfloat16))
+        self.q, self.scale, self.inv_s = q, sc, inv
+        self.out_features, self.in_features = q.shape
+
+
+def random_layer_weights(cfg: DecoderConfig, g: torch.Generator, device, smooth: bool = True) -> dict:
+    """One layer of random-init bf16 weights (linears N(0, 0.02), norms near 1) and SmoothQuant factors
+    s ~ U(0.5, 2) per linear input, generated on `device`."""
+    bf = torch.bfloat16
+    H, F, D = cfg.hidden, cfg.ffn, cfg.head_dim
+
+    def lin(n, k):
+        return (torch.randn(n, k, generator=g, device=device) * 0.02).to(bf)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
+
+    def sm(n):
+        return (torch.rand(n, generator=g, device=device) * 1.5 + 0.5) if smooth else None
+
+    return {"ln1": norm(H), "ln2": norm(H), "q_norm": norm(D), "k_norm": norm(D),
+            "wqkv": lin(cfg.qkv_out, H), "wo": lin(H, cfg.n_heads * D), "wgu": lin(2 * F, H), "wdown": lin(H, F),
+            "s_qkv": sm(H), "s_o": sm(cfg.n_heads * D), "s_gu": sm(H), "s_down": sm(F)}
+
+
+def random_decoder(cfg: DecoderConfig, seed: int = 0, device="cuda", max_pos: int = 65536) -> "DenseDecoder":
+    """A random-init decoder of `cfg` built layer by layer on the GPU (bf16 weights are quantized and dropped one
+    layer at a time). The embedding is random bf16 (vocab x hidden)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    H = cfg.hidden
+    head = {"final_norm": (1.0 + 0.1 * torch.randn(H, generator=g, device=device)).to(torch.bfloat16),
+            "head": torch.randn(H, generator=g, device=device) / H ** 0.5,
+            "none_logit": torch.zeros((), device=device), "layers": []}
+    dec = DenseDecoder(cfg, head, None, device, max_pos)
+    for _ in range(cfg.n_layers):
+        dec.add_layer(random_layer_weights(cfg, g, device))
+    dec.embed = torch.randn(cfg.vocab, H, generator=g, device=device).to(torch.bfloat16)
+    return dec
+
+
+class DenseDecoder:
+    """Weights from a dict (oracle.decoder.make_weights layout) on any device; quantized on the GPU."""
+
+    def __init__(self, cfg: DecoderConfig, weights: dict, embed: torch.Tensor | None, device="cuda",
+                 max_pos: int = 65536):
+        self.cfg, self.dev = cfg, torch.device(device)
+        self.layers = []
+        for lw in weights["layers"]:
+            self.add_layer(lw)
+        self.final_norm = weights["final_norm"].to(self.dev)
+        self.head = weights["head"].to(self.dev).float()
+        self.none_logit = weights["none_logit"].to(self.dev).float()
+        self.embed = None if embed is None else embed.to(self.dev)
+        cos, sin = rope_tables(cfg, max_pos)
+        self.cos, self.sin = cos.to(self.dev), sin.to(self.dev)
+        self._ws = None
+
+    def add_layer(self, lw: dict) -> None:
+        L = {k: lw[k].to(self.dev) for k in ("ln1", "ln2", "q_norm", "k_norm")}
+        for name in ("qkv", "o", "gu", "down"):
+            L[name] = QLinear(lw["w" + name], lw.get("s_" + name), self.dev)
+        self.layers.append(L)
+
+    # ---------------------------------------------------------------- buffers
+    def workspace(self, M: int):
+        if self._ws is not None and self._ws["M"] == M:
+            return self._ws
+        cfg, d = self.cfg, self.dev
+        bf = torch.bfloat16
+        kmax = max(cfg.hidden, cfg.ffn, cfg.n_heads * cfg.head_dim)
+        self._ws = {
+            "M": M,
+            "h": [torch.empty(M, cfg.hidden, dtype=bf, device=d) for _ in range(2)],
+            "xq": torch.empty(M, (kmax + 15) // 16 * 16, dtype=torch.int8, device=d),
+            "sx": torch.empty(M, dtype=torch.float32, device=d),
+            "qkv": torch.empty(M, cfg.qkv_out, dtype=bf, device=d),
+            "attn": torch.empty(M, cfg.n_heads * cfg.head_dim, dtype=bf, device=d),
+            "gu": torch.empty(M, 2 * cfg.ffn, dtype=bf, device=d),
+        }
+        return self._ws
+
+    # ---------------------------------------------------------------- forward
+    def layer(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict, state_k: Int8KVCache,
+              state_v: Int8KVCache, R: int, t: int, pos: torch.Tensor, row_start, max_rows: int, kvalid=None):
+        cfg, L = self.cfg, self.layers[li]
+        D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+        M = h.shape[0]
+        xq, sx = ws["xq"], ws["sx"]
+        # attention block
+        kernels.rmsnorm_quant(h, L["ln1"], cfg.eps, L["qkv"].inv_s, xq[:, :cfg.hidden], sx)
+        qkv = kernels.w8a8_gemm(xq[:, :cfg.hidden], sx, L["qkv"].q, L["qkv"].scale, out=ws["qkv"])
+        kernels.qk_norm_rope(qkv, Hq, Hk, D, L["q_norm"], L["k_norm"], self.cos, self.sin, pos, cfg.eps)
+        q = qkv[:, :Hq * D].view(R, t, Hq, D).transpose(1, 2)
+        k = qkv[:, Hq * D:(Hq + Hk) * D].view(R, t, Hk, D).transpose(1, 2)
+        v = qkv[:, (Hq + Hk) * D:].view(R, t, Hk, D).transpose(1, 2)
+        attn = ws["attn"].view(R, t, Hq, D).transpose(1, 2)
+        T = state_k.length
+        kernels.branched_attn(q, k, v, state_k.q, state_k.scale, state_v.q, state_v.scale, D ** -0.5, kvalid=kvalid,
+                              length=T, out=attn, row_start=row_start, max_rows=max_rows)
+        kernels.act_quant(ws["attn"], L["o"].inv_s, xq=xq[:, :Hq * D], sx=sx)
+        kernels.w8a8_gemm(xq[:, :Hq * D], sx, L["o"].q, L["o"].scale, residual=h, out=h_out)
+        # MLP block
+        kernels.rmsnorm_quant(h_out, L["ln2"], cfg.eps, L["gu"].inv_s, xq[:, :cfg.hidden], sx)
+        gu = kernels.w8a8_gemm(xq[:, :cfg.hidden], sx, L["gu"].q, L["gu"].scale, out=ws["gu"])
+        kernels.silu_mul_quant(gu, cfg.ffn, L["down"].inv_s, xq=xq[:, :cfg.ffn], sx=sx)
+        kernels.w8a8_gemm(xq[:, :cfg.ffn], sx, L["down"].q, L["down"].scale, residual=h_out, out=h)
+        return h  # the layer's output is written back into h (h_out held the mid-layer residual)
+
+    def rows_forward(self, h0: torch.Tensor, states: list, R: int, t: int, pos: torch.Tensor, row_start, max_rows,
+                     kvalid=None) -> torch.Tensor:
+        """Option-row tokens h0 (M = R t, hidden) bf16 through every layer; states[l] = (K cache, V cache)."""
+        ws = self.workspace(h0.shape[0])
+        h, mid = ws["h"]
+        h.copy_(h0)
+        for li in range(len(self.layers)):
+            self.layer(li, h, mid, ws, states[li][0], states[li][1], R, t, pos, row_start, max_rows, kvalid)
+        return h
+
+    def readout(self, h: torch.Tensor, B: int, n_opt: int, t: int) -> torch.Tensor:
+        """Mean-pool each option row's final-normed hidden states, one logit per row, the 'none' logit appended,
+        log-softmax per request: (B, n_opt + 1) fp32."""
+        hf = h.float()
+        r = torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + self.cfg.eps)
+        hn = (self.final_norm * (hf * r).to(torch.bfloat16)).float()
+        pooled = hn.view(B, n_opt, t, -1).mean(2)
+        logits = torch.cat([pooled @ self.head, self.none_logit.expand(B, 1)], 1)
+        return torch.log_softmax(logits, -1)
+
+    def positions(self, T: int, R: int, t: int) -> torch.Tensor:
+        if T + t > self.cos.shape[0]:
+            raise ValueError(f"positions up to {T + t} exceed the rotary tables ({self.cos.shape[0]})")
+        return (T + torch.arange(t, dtype=torch.int32)).repeat(R).to(self.dev)
+
+    def score(self, ids: torch.Tensor, states: list, kvalid=None) -> torch.Tensor:
+        """ids (B, n_opt, t) option-row token ids on the GPU; states[l] = (K, V) Int8KVCache of the B cached
+        states. Returns (B, n_opt + 1) log-probabilities over the options and 'none'."""
+        B, n_opt, t = ids.shape
+        R = B * n_opt
+        T = states[0][0].length
+        h0 = self.embed.index_select(0, ids.reshape(-1))
+        pos = self.positions(T, R, t)
+        row_start, max_rows = kernels.row_start_of([n_opt] * B, self.dev)
+        h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
+        return self.readout(h, B, n_opt, t)

@@ -8,28 +8,96 @@ from . import _lib
 from ._lib import check, lib, ptr, require_gpu, stream_of
 
 
-def act_quant(x: torch.Tensor, inv_s: torch.Tensor | None = None, ld: int | None = None):
+def _quant_outputs(M, K, ld, device, xq, sx):
+    if xq is None:
+        ld = K if ld is None else ld
+        xq = (torch.zeros if ld > K else torch.empty)(M, ld, dtype=torch.int8, device=device)
+    elif xq.dtype != torch.int8 or xq.shape[0] != M or xq.shape[1] < K or xq.stride(1) != 1:
+        raise ValueError("quantized output must be int8 (M, >= K) with contiguous rows")
+    if sx is None:
+        sx = torch.empty(M, dtype=torch.float32, device=device)
+    elif sx.dtype != torch.float32 or sx.numel() != M or not sx.is_contiguous():
+        raise ValueError("scale output must be fp32 (M,) contiguous")
+    return xq, sx
+
+
+def _vec(v, n, name):
+    if v is None:
+        return None
+    _lib.bf16_bits(v)
+    v = v.contiguous()
+    if v.numel() != n:
+        raise ValueError(f"{name} has {v.numel()} elements, expected {n}")
+    return v
+
+
+def act_quant(x: torch.Tensor, inv_s: torch.Tensor | None = None, ld: int | None = None, xq=None, sx=None):
     """Per-row int8 quantization of x (..., K) bf16 (Int8Tensor.quantize, quant.py:36-41), with the optional
     SmoothQuant input scale inv_s (K,) bf16 applied first (quant.py:329). Returns (xq int8 (rows, ld), sx fp32
-    (rows,)) with rows = x.numel() // K; columns K..ld-1 of xq are zero (ld >= K pads rows for the GEMM)."""
-    require_gpu(x, inv_s, name="act_quant")
+    (rows,)) with rows = x.numel() // K; columns K..ld-1 of a freshly allocated xq are zero (ld >= K pads rows for
+    the GEMM). xq / sx may be given (preallocated; xq may be a column slice of a wider buffer)."""
+    require_gpu(x, inv_s, xq, sx, name="act_quant")
     _lib.bf16_bits(x)
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     M = x2.shape[0]
-    ld = K if ld is None else ld
-    xq = (torch.zeros if ld > K else torch.empty)(M, ld, dtype=torch.int8, device=x.device)
-    sx = torch.empty(M, dtype=torch.float32, device=x.device)
-    if inv_s is not None:
-        _lib.bf16_bits(inv_s)
-        inv_s = inv_s.contiguous()
-        if inv_s.numel() != K:
-            raise ValueError(f"inv_s has {inv_s.numel()} elements, expected {K}")
-    check(lib().od_act_quant(ptr(x2), x2.stride(0) if M > 1 else K, ptr(inv_s), ptr(xq), ld, ptr(sx), M, K,
+    xq, sx = _quant_outputs(M, K, ld, x.device, xq, sx)
+    inv_s = _vec(inv_s, K, "inv_s")
+    check(lib().od_act_quant(ptr(x2), x2.stride(0) if M > 1 else K, ptr(inv_s), ptr(xq), xq.stride(0), ptr(sx), M, K,
                              stream_of(x)), "od_act_quant")
     return xq, sx
+
+
+def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float, inv_s=None, xq=None, sx=None):
+    """RMSNorm (bf16(w * bf16(x * rsqrt(mean x^2 + eps)))) -> optional SmoothQuant scale -> per-row int8.
+    x (M, K) bf16 with contiguous rows. Returns (xq, sx)."""
+    require_gpu(x, w, inv_s, xq, sx, name="rmsnorm_quant")
+    _lib.bf16_bits(x)
+    M, K = x.shape
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    xq, sx = _quant_outputs(M, K, None, x.device, xq, sx)
+    w, inv_s = _vec(w, K, "w"), _vec(inv_s, K, "inv_s")
+    check(lib().od_rmsnorm_quant(ptr(x), x.stride(0), ptr(w), ptr(inv_s), float(eps), ptr(xq), xq.stride(0), ptr(sx),
+                                 M, K, stream_of(x)), "od_rmsnorm_quant")
+    return xq, sx
+
+
+def silu_mul_quant(gu: torch.Tensor, F: int, inv_s=None, xq=None, sx=None):
+    """bf16(bf16(silu(g)) * u) of the fused gate+up output gu (M, >= 2F) -> optional SmoothQuant scale -> per-row
+    int8. Returns (xq (M, F), sx)."""
+    require_gpu(gu, inv_s, xq, sx, name="silu_mul_quant")
+    _lib.bf16_bits(gu)
+    M = gu.shape[0]
+    if gu.stride(1) != 1 or gu.shape[1] < 2 * F:
+        raise ValueError("silu_mul_quant: gu must be (M, >= 2F) with contiguous rows")
+    xq, sx = _quant_outputs(M, F, None, gu.device, xq, sx)
+    inv_s = _vec(inv_s, F, "inv_s")
+    check(lib().od_silu_mul_quant(ptr(gu), gu.stride(0), F, ptr(inv_s), ptr(xq), xq.stride(0), ptr(sx), M,
+                                  stream_of(gu)), "od_silu_mul_quant")
+    return xq, sx
+
+
+def qk_norm_rope(qkv: torch.Tensor, n_heads_q: int, n_heads_k: int, D: int, q_w, k_w, cos_t, sin_t, pos,
+                 eps: float) -> None:
+    """In place on qkv (M, >= (Hq + Hk) D): per-head RMSNorm of the q and k heads, then rotary embedding with the
+    bf16 cos/sin tables [positions, D/2] at positions pos (M,) int32."""
+    require_gpu(qkv, q_w, k_w, cos_t, sin_t, pos, name="qk_norm_rope")
+    _lib.bf16_bits(qkv)
+    M = qkv.shape[0]
+    if qkv.stride(1) != 1:
+        raise ValueError("qk_norm_rope: qkv must have contiguous rows")
+    q_w, k_w = _vec(q_w, D, "q_w"), _vec(k_w, D, "k_w")
+    if cos_t.shape != sin_t.shape or cos_t.shape[1] != D // 2 or not (cos_t.is_contiguous() and sin_t.is_contiguous()):
+        raise ValueError("qk_norm_rope: cos/sin tables must be contiguous [positions, D/2]")
+    if pos.dtype != torch.int32 or pos.numel() != M:
+        raise ValueError("qk_norm_rope: pos must be int32 (M,)")
+    check(lib().od_qk_norm_rope(ptr(qkv), qkv.stride(0), M, n_heads_q, n_heads_k, D, ptr(q_w), ptr(k_w),
+                                ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos.contiguous()), float(eps),
+                                stream_of(qkv)),
+          "od_qk_norm_rope")
 
 
 def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, bias=None, residual=None,

@@ -1,0 +1,182 @@
+"""CPU oracle of the decision-forward harness: a dense 9B-class decoder (Qwen3-style layer: RMSNorm, fused QKV,
+per-head q/k RMSNorm, rotary embedding, GQA attention, output projection, SwiGLU MLP) whose linears are W8A8 and
+whose attention is the branched option-row attention over int8 state K/V, followed by the option readout (mean-pool
+each option row, one logit per row, a learned 'none' logit, log-softmax per request).
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+This layer is the harness that carries the path, not a reference function: the reference runs the same steps inside
+HF Qwen3.5 modules (src/opendecider/prefix_attn.py:79-131 for the attention layer, the W8A8 linears in every
+nn.Linear slot, decision logits + 'none' at src/opendecider/v3.py:639-643,701-709 and softmax at
+src/opendecider/decider.py:255-257). Rounding follows torch bf16 module arithmetic: every elementwise product of
+bf16 tensors rounds to bf16 once.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import attention as oa
+from . import quant as oq
+
+
+@dataclass
+class DecoderConfig:
+    hidden: int = 4096
+    ffn: int = 12288
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    n_layers: int = 36
+    vocab: int = 151936
+    eps: float = 1e-6
+    theta: float = 1e6
+
+    @property
+    def qkv_out(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+def make_weights(cfg: DecoderConfig, seed: int = 0, device="cpu", layers: int | None = None, smooth: bool = True):
+    """Random-init weights of the decoder (bf16, N(0, 0.02) linears, norms near 1) and SmoothQuant factors
+    s ~ U(0.5, 2) per linear input. Deterministic for a seed and device. Returns a dict."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    bf = torch.bfloat16
+    H, F, D = cfg.hidden, cfg.ffn, cfg.head_dim
+
+    def lin(n, k):
+        return (torch.randn(n, k, generator=g, device=device) * 0.02).to(bf)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
+
+    def sm(n):
+        return (torch.rand(n, generator=g, device=device) * 1.5 + 0.5) if smooth else None
+
+    out = {"layers": []}
+    for _ in range(cfg.n_layers if layers is None else layers):
+        out["layers"].append({
+            "ln1": norm(H), "ln2": norm(H), "q_norm": norm(D), "k_norm": norm(D),
+            "wqkv": lin(cfg.qkv_out, H), "wo": lin(H, cfg.n_heads * D), "wgu": lin(2 * F, H), "wdown": lin(H, F),
+            "s_qkv": sm(H), "s_o": sm(cfg.n_heads * D), "s_gu": sm(H), "s_down": sm(F),
+        })
+    out["final_norm"] = norm(H)
+    out["head"] = (torch.randn(H, generator=g, device=device) / H ** 0.5).float()
+    out["none_logit"] = torch.zeros((), device=device)
+    return out
+
+
+def make_embedding(cfg: DecoderConfig, seed: int = 0, device="cpu"):
+    g = torch.Generator(device=device).manual_seed(seed + 7919)
+    return torch.randn(cfg.vocab, cfg.hidden, generator=g, device=device).to(torch.bfloat16)
+
+
+def quantize_linear(w: torch.Tensor, s: torch.Tensor | None):
+    """SmoothQuant fold W * s (quant.py:343-344), per-channel int8 (quant.py:124-126), bf16(1/s) (quant.py:325)."""
+    if s is not None:
+        w = oq.smooth_fold(w, s)
+    q, sw = oq.quantize_weight(w)
+    return q, sw, None if s is None else oq.smooth_inv(s)
+
+
+def rope_tables(cfg: DecoderConfig, n_pos: int):
+    """cos/sin bf16 tables [n_pos, D/2]: inv_freq = 1 / theta^(2i/D), angle = pos * inv_freq in fp32."""
+    D = cfg.head_dim
+    inv_freq = 1.0 / (cfg.theta ** (torch.arange(0, D, 2, dtype=torch.int64).float() / D))
+    ang = torch.arange(n_pos, dtype=torch.float32)[:, None] * inv_freq[None, :]
+    return ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """w * bf16(x * rsqrt(mean(x^2) + eps)) in bf16 (the HF RMSNorm arithmetic)."""
+    xf = x.float()
+    r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w * (xf * r).to(torch.bfloat16)
+
+
+def qk_norm_rope(qkv: torch.Tensor, cfg: DecoderConfig, q_w, k_w, cos, sin, pos) -> torch.Tensor:
+    """Per-head RMSNorm of the q and k heads of qkv (M, qkv_out), then rotate_half RoPE; v untouched."""
+    M = qkv.shape[0]
+    D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    L = D // 2
+    out = qkv.clone()
+    c = cos[pos].repeat(1, 2)[:, None, :]            # (M, 1, D), halves shared
+    s = sin[pos].repeat(1, 2)[:, None, :]
+    for lo, nh, w in ((0, Hq, q_w), (Hq * D, Hk, k_w)):
+        x = qkv[:, lo:lo + nh * D].reshape(M, nh, D)
+        n = rmsnorm(x, w, cfg.eps)
+        rot = torch.cat([-n[..., L:], n[..., :L]], -1)
+        out[:, lo:lo + nh * D] = ((n * c) + (rot * s)).reshape(M, nh * D)
+    return out
+
+
+def swiglu(gu: torch.Tensor, F: int) -> torch.Tensor:
+    """bf16(bf16(silu(g)) * u) with g = gu[:, :F], u = gu[:, F:]."""
+    return torch.nn.functional.silu(gu[:, :F]) * gu[:, F:]
+
+
+def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: int, pos, cos, sin,
+                  row_state=None, kvalid=None, attn_hook=None):
+    """One decoder layer over the option-row tokens h (M = R * t, hidden) bf16. qlin: {name: (q, sw, inv_s)}.
+    state_k/state_v: (kq int8 (Ns, Hkv, T, D), ks fp32 (Ns, Hkv, T)) of this layer. attn_hook, if given, maps the
+    bf16 attention output (M, Hq D) to the tensor used downstream (sensitivity studies). Returns the new h."""
+    D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    x = rmsnorm(h, lw["ln1"], cfg.eps)
+    q, sw, inv = qlin["wqkv"]
+    qkv, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
+    qkv = qk_norm_rope(qkv, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
+    qh = qkv[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
+    kh = qkv[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
+    vh = qkv[:, (Hq + Hk) * D:].reshape(R, t, Hk, D).transpose(1, 2)
+    o, _ = oa.branched_attention_int8(qh, kh, vh, state_k[0], state_k[1], state_v[0], state_v[1], D ** -0.5,
+                                      kvalid, row_state)
+    attn = o.to(torch.bfloat16).transpose(1, 2).reshape(R * t, Hq * D)
+    if attn_hook is not None:
+        attn = attn_hook(attn)
+    q, sw, inv = qlin["wo"]
+    h, _, _, _ = oq.w8a8_linear(attn, q, sw, inv_s=inv, residual=h)
+    x = rmsnorm(h, lw["ln2"], cfg.eps)
+    q, sw, inv = qlin["wgu"]
+    gu, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
+    a = swiglu(gu, cfg.ffn)
+    q, sw, inv = qlin["wdown"]
+    h, _, _, _ = oq.w8a8_linear(a, q, sw, inv_s=inv, residual=h)
+    return h
+
+
+def quantize_layer(lw):
+    return {k: quantize_linear(lw[k], lw["s_" + k[1:]]) for k in ("wqkv", "wo", "wgu", "wdown")}
+
+
+def readout(h, final_norm, head, none_logit, cfg: DecoderConfig, B: int, n_opt: int, t: int):
+    """Mean-pool each option row's final-normed hidden states, one logit per row (pooled . head), append the
+    'none' logit, log-softmax per request. Returns (B, n_opt + 1) fp32 log-probabilities."""
+    hf = rmsnorm(h, final_norm, cfg.eps).float().reshape(B, n_opt, t, -1).mean(2)
+    logits = hf @ head.float()
+    logits = torch.cat([logits, none_logit.float().expand(B, 1)], 1)
+    return torch.log_softmax(logits, -1)
+
+
+def nudge_bf16(x: torch.Tensor, frac: float, seed: int) -> torch.Tensor:
+    """x (bf16) with a seeded `frac` of its elements moved by one bf16 step up or down: a perturbation the size of
+    one rounding difference, used to measure how strongly the forward amplifies rounding noise."""
+    g = torch.Generator().manual_seed(seed)
+    bits = x.contiguous().view(torch.int16)
+    flip = ((torch.rand(bits.shape, generator=g) < frac) & (x.contiguous() != 0)).to(torch.int16)  # zeros stay
+    sign = (torch.randint(0, 2, bits.shape, generator=g) * 2 - 1).to(torch.int16)
+    return (bits + flip * sign).view(torch.bfloat16)
+
+
+def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, kvalid=None, attn_hook=None):
+    """Option-row scoring pass: ids (B, n_opt, t) token ids; state_kv[l] = ((kq, ks), (vq, vs)) per layer for the
+    B cached states of length T. Returns (B, n_opt + 1) log-probabilities."""
+    B, n_opt, t = ids.shape
+    R = B * n_opt
+    h = embed[ids.reshape(-1)]
+    pos = (T + torch.arange(t)).repeat(R)
+    cos, sin = rope_tables(cfg, T + t)
+    row_state = torch.arange(B).repeat_interleave(n_opt)
+    for li, lw in enumerate(weights["layers"]):
+        h = layer_forward(h, lw, quantize_layer(lw), cfg, state_kv[li][0], state_kv[li][1], R, t, pos, cos, sin,
+                          row_state, kvalid, attn_hook)
+    return readout(h, weights["final_norm"], weights["head"], weights["none_logit"], cfg, B, n_opt, t)

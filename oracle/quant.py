@@ -54,12 +54,14 @@ def act_quant(x: torch.Tensor, inv_s: torch.Tensor | None = None) -> tuple[torch
 
 
 def int_gemm(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """int8 A (M, K) x int8 W (N, K) (nn.Linear layout) -> exact int32 accumulators (M, N). |acc| <= 127^2 K, which
-    stays below 2^31 for K < 133,144, so int64 arithmetic narrowed to int32 is exact."""
+    """int8 A (M, K) x int8 W (N, K) (nn.Linear layout) -> exact int32 accumulators (M, N), with torch's CPU
+    int8 x int8 -> int32 matmul. |acc| <= 127^2 K stays below 2^31 for K < 133,144, so int32 accumulation is exact
+    (pinned against an int64 matmul and scalar loops in tests/test_oracle_quant.py)."""
     assert a.dtype == torch.int8 and w.dtype == torch.int8 and a.shape[-1] == w.shape[-1]
     assert a.shape[-1] < 133_144
-    acc = a.reshape(-1, a.shape[-1]).to(torch.int64) @ w.to(torch.int64).t()
-    return acc.to(torch.int32).reshape(*a.shape[:-1], w.shape[0])
+    a2 = a.detach().to("cpu").reshape(-1, a.shape[-1]).contiguous()
+    acc = torch._int_mm(a2, w.detach().to("cpu").t().contiguous())
+    return acc.reshape(*a.shape[:-1], w.shape[0])
 
 
 def w8a8_epilogue(acc: torch.Tensor, sx: torch.Tensor, sw: torch.Tensor, bias: torch.Tensor | None = None,

@@ -1,0 +1,190 @@
+"""GPU parity of the decoder-layer row kernels and of the whole decision forward against the oracle.
+
+Row kernels: int8 bytes and fp32 scales are exact where the device and the oracle compute the same fp32 value; the
+RMSNorm / SwiGLU pre-quantization values can differ in the last fp32 bits (reduction order, device rsqrt and exp),
+which may move a bf16 rounding and then one int8 step, so those are held to: scales within 2^-7 relative, bytes
+within one step, and at most 0.5% of bytes off. RoPE outputs within one bf16 step.
+Decision forward: every stage of every layer against the oracle fed the GPU's input to that stage (bit-exact except
+the attention, which is held to its 2e-3 bar), end-to-end probabilities within the oracle's own sensitivity to
+rounding-size perturbations of the attention output, and option-order invariance (<= 1e-6).
+"""
+import pytest
+import torch
+
+from helpers import PROB_ABS, assert_close_rel
+from oracle import attention as oa
+from oracle import decoder as od
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _close_quant(xq, sx, rq, rs):
+    xq, sx = xq.cpu(), sx.cpu()
+    assert ((sx - rs).abs() <= rs.abs() * 2.0 ** -7).all()
+    d = (xq.int() - rq.int()).abs()
+    assert d.max().item() <= 1 and (d > 0).float().mean().item() <= 5e-3, (d.max().item(), (d > 0).float().mean())
+
+
+@pytest.mark.parametrize("M,K,smooth", [(7, 4096, False), (33, 4096, True), (5, 200, True)])
+def test_rmsnorm_quant(gpu_lib, M, K, smooth):
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(M + K)
+    x = (torch.randn(M, K, generator=g) * 2).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    inv = (1 / (torch.rand(K, generator=g) * 1.5 + 0.5)).to(torch.bfloat16) if smooth else None
+    xq, sx = kernels.rmsnorm_quant(x.to(DEV), w.to(DEV), 1e-6, None if inv is None else inv.to(DEV))
+    rq, rs = oq.act_quant(od.rmsnorm(x, w, 1e-6), inv)
+    _close_quant(xq, sx, rq, rs)
+
+
+@pytest.mark.parametrize("M,F,smooth", [(9, 12288, True), (4, 96, False)])
+def test_silu_mul_quant(gpu_lib, M, F, smooth):
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(M + F)
+    gu = (torch.randn(M, 2 * F, generator=g) * 3).to(torch.bfloat16)
+    inv = (1 / (torch.rand(F, generator=g) * 1.5 + 0.5)).to(torch.bfloat16) if smooth else None
+    xq, sx = kernels.silu_mul_quant(gu.to(DEV), F, None if inv is None else inv.to(DEV))
+    rq, rs = oq.act_quant(od.swiglu(gu, F), inv)
+    _close_quant(xq, sx, rq, rs)
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_qk_norm_rope(gpu_lib, D):
+    from opendecider_amd import kernels
+    cfg = od.DecoderConfig(hidden=8 * D, n_heads=8, n_kv_heads=2, head_dim=D)
+    g = torch.Generator().manual_seed(D)
+    M = 37
+    qkv = (torch.randn(M, cfg.qkv_out, generator=g) * 2).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    pos = torch.randint(0, 40000, (M,), generator=g)
+    cos, sin = od.rope_tables(cfg, 40000)
+    ref = od.qk_norm_rope(qkv, cfg, qw, kw, cos, sin, pos)
+    x = qkv.to(DEV)
+    kernels.qk_norm_rope(x, 8, 2, D, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV), pos.to(DEV, torch.int32),
+                         cfg.eps)
+    got = x.cpu().float()
+    assert ((got - ref.float()).abs() <= ref.float().abs() * 2.0 ** -7 + 2.0 ** -14).all()
+    assert torch.equal(x.cpu()[:, 10 * D:], qkv[:, 10 * D:])
+
+
+def _states(cfg, B, T, layers, seed):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(layers):
+        kv = torch.randn(2, B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).to(torch.bfloat16)
+        kq, ks = oq.quantize_rows(kv[0])
+        vq, vs = oq.quantize_rows(kv[1])
+        out.append(((kq, ks[..., 0]), (vq, vs[..., 0])))
+    return out
+
+
+def _gpu_states(states, cap):
+    from opendecider_amd.kv_cache import Int8KVCache
+    res = []
+    for (kq, ks), (vq, vs) in states:
+        B, H, T, D = kq.shape
+        pair = []
+        for q, s in ((kq, ks), (vq, vs)):
+            c = Int8KVCache(B, H, D, cap, DEV)
+            c.q[:, :, :T].copy_(q.to(DEV))
+            c.scale[:, :, :T].copy_(s.to(DEV))
+            c.length = T
+            pair.append(c)
+        res.append(tuple(pair))
+    return res
+
+
+CASES = [
+    ("tiny_d64", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500), 2, 5, 4, 70),
+    ("9b_dims_2_layers", dict(n_layers=2, vocab=1000), 2, 6, 16, 256),
+]
+
+
+def _setup(cfg_kw, B, n_opt, t, T):
+    from opendecider_amd.decoder import DecoderConfig, DenseDecoder
+    cfg = od.DecoderConfig(**cfg_kw)
+    w = od.make_weights(cfg, seed=3)
+    emb = od.make_embedding(cfg, seed=3)
+    states = _states(cfg, B, T, cfg.n_layers, 4)
+    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=torch.Generator().manual_seed(5))
+    dec = DenseDecoder(DecoderConfig(**cfg_kw), w, emb, DEV, max_pos=T + t + 8)
+    return cfg, w, emb, states, ids, dec, _gpu_states(states, T + 32)
+
+
+@pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
+def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
+    """Every stage of every layer against the oracle fed the GPU's own input to that stage. The RMSNorm / SwiGLU
+    quantizers are held to the row-kernel bar (their fp32 sums and rsqrt / exp may differ in the last bit); the
+    GEMMs (+residual) and q/k norm + RoPE downstream of the GPU's own int8 bytes are bit-exact; the attention is
+    held to its 2e-3 bar. The kernels are deterministic, so re-running a quantizer reproduces the layer's bytes."""
+    from opendecider_amd import kernels
+    cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
+    R, M = B * n_opt, B * n_opt * t
+    D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    pos = (T + torch.arange(t)).repeat(R)
+    cos, sin = od.rope_tables(cfg, T + t + 8)
+    row_state = torch.arange(B).repeat_interleave(n_opt)
+    ws = dec.workspace(M)
+    h, mid = ws["h"]
+    h.copy_(emb[ids.reshape(-1)].to(DEV))
+    rs, mr = kernels.row_start_of([n_opt] * B, DEV)
+    for li in range(cfg.n_layers):
+        lw, ql, L = w["layers"][li], od.quantize_layer(w["layers"][li]), dec.layers[li]
+        h_in_g = h.clone()
+        h_in = h_in_g.cpu()
+        dec.layer(li, h, mid, ws, gs[li][0], gs[li][1], R, t, pos.to(DEV, torch.int32), rs, mr)
+        qkv_g, attn_g, mid_g, gu_g, out_g = (ws["qkv"].cpu(), ws["attn"].cpu(), mid.cpu(), ws["gu"].cpu(), h.cpu())
+        # RMSNorm 1 + quantize, then QKV GEMM + q/k norm + RoPE from the GPU's bytes
+        xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["qkv"].inv_s)
+        _close_quant(xq, sx, *oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps), ql["wqkv"][2]))
+        qkv_lin = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wqkv"][0]), sx.cpu(), ql["wqkv"][1])
+        assert torch.equal(qkv_g[:, (Hq + Hk) * D:], qkv_lin[:, (Hq + Hk) * D:]), f"layer {li}: QKV GEMM (v part)"
+        qkv = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
+        # per-head RMSNorm sums D squares in another order than the oracle, so a normed value may differ by one
+        # bf16 step; RoPE mixes each pair (i, i + D/2), so the bound is one step of the pair's norm
+        gq = qkv_g[:, :(Hq + Hk) * D].float().reshape(M, Hq + Hk, 2, D // 2)
+        rq = qkv[:, :(Hq + Hk) * D].float().reshape(M, Hq + Hk, 2, D // 2)
+        pair = rq.pow(2).sum(2, keepdim=True).sqrt()
+        assert ((gq - rq).abs() <= pair * 2.0 ** -6 + 2.0 ** -14).all(), f"layer {li}: q/k norm + RoPE"
+        # attention
+        qh = qkv_g[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
+        kh = qkv_g[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
+        vh = qkv_g[:, (Hq + Hk) * D:].reshape(R, t, Hk, D).transpose(1, 2)
+        (kq, ks), (vq, vs) = states[li]
+        o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, None, row_state)
+        assert_close_rel(attn_g.float(), o.transpose(1, 2).reshape(M, Hq * D), what=f"layer {li}: attention")
+        # O projection + residual (the attention output's quantizer is bit-exact)
+        h_mid = oq.w8a8_linear(attn_g, *ql["wo"][:2], inv_s=ql["wo"][2], residual=h_in)[0]
+        assert torch.equal(mid_g, h_mid), f"layer {li}: O projection + residual"
+        # RMSNorm 2 + quantize, gate+up GEMM from the GPU's bytes
+        xq, sx = kernels.rmsnorm_quant(mid.clone(), L["ln2"], cfg.eps, L["gu"].inv_s)
+        _close_quant(xq, sx, *oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps), ql["wgu"][2]))
+        gu = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wgu"][0]), sx.cpu(), ql["wgu"][1])
+        assert torch.equal(gu_g, gu), f"layer {li}: gate+up GEMM"
+        # SwiGLU + quantize, down GEMM + residual from the GPU's bytes
+        xq, sx = kernels.silu_mul_quant(ws["gu"], cfg.ffn, L["down"].inv_s)
+        _close_quant(xq, sx, *oq.act_quant(od.swiglu(gu_g, cfg.ffn), ql["wdown"][2]))
+        h_out = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wdown"][0]), sx.cpu(), ql["wdown"][1], residual=mid_g)
+        assert torch.equal(out_g, h_out), f"layer {li}: down GEMM + residual"
+
+
+@pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
+def test_decision_forward_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, T):
+    """End to end the GPU forward and the oracle differ only through the attention output's bf16 rounding, which
+    dynamic int8 activation quantization amplifies (one step on a token's absmax element rescales the token). The
+    bar: the probability difference is within the oracle's own response to a perturbation of that size (one bf16
+    step in 10% of its attention outputs, every layer), and never above 1e-2; option order invariance <= 1e-6."""
+    cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
+    ref = od.decision_forward(ids, w, emb, cfg, states, T)
+    nudged = od.decision_forward(ids, w, emb, cfg, states, T, attn_hook=lambda a: od.nudge_bf16(a, 0.10, 17))
+    lp = dec.score(ids.to(DEV), gs)
+    dp = (lp.exp().cpu() - ref.exp()).abs().max().item()
+    dp_nudge = (nudged.exp() - ref.exp()).abs().max().item()
+    print(f"{name}: max |dp| GPU vs oracle {dp:.2e}; oracle vs nudged oracle {dp_nudge:.2e}")
+    assert dp <= max(3 * dp_nudge, PROB_ABS) and dp <= 1e-2
+    perm = torch.randperm(n_opt, generator=torch.Generator().manual_seed(6))
+    lp_p = dec.score(ids[:, perm].to(DEV), gs)
+    assert (lp_p[:, :n_opt].exp() - lp[:, perm.to(DEV)].exp()).abs().max().item() <= 1e-6

@@ -1,0 +1,112 @@
+"""Pins the decision-forward oracle (oracle/decoder.py) step by step against independent float64 math: RMSNorm's
+closed form, RoPE as a complex rotation (norm preservation, relative-position property), SwiGLU, the readout's
+normalisation, and option-order invariance of the whole forward."""
+import math
+
+import torch
+
+from oracle import decoder as od
+
+
+def test_rmsnorm_matches_float64_within_bf16_rounding():
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(6, 64, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(64, generator=g)).to(torch.bfloat16)
+    y = od.rmsnorm(x, w, 1e-6).double()
+    xd = x.double()
+    ref = w.double() * xd / torch.sqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
+    assert ((y - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-12).all()
+    # closed form: a constant row normalises to sign * w
+    c = torch.full((1, 64), -2.5, dtype=torch.bfloat16)
+    assert torch.equal(od.rmsnorm(c, w, 0.0), (-w.float()).to(torch.bfloat16)[None])
+
+
+def _rope64(x, pos, cfg):
+    """Independent float64 RoPE: pairs (x_i, x_{i+D/2}) rotated by pos * theta^(-2i/D) as complex numbers."""
+    D = x.shape[-1]
+    L = D // 2
+    i = torch.arange(L, dtype=torch.float64)
+    ang = pos[:, None].double() * cfg.theta ** (-2 * i / D)
+    z = torch.complex(x[..., :L].double(), x[..., L:].double()) * torch.exp(1j * ang)[:, None, :]
+    return torch.cat([z.real, z.imag], -1)
+
+
+def test_qk_norm_rope_is_a_rotation_of_the_normed_heads():
+    cfg = od.DecoderConfig(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64)
+    g = torch.Generator().manual_seed(1)
+    M = 10
+    qkv = torch.randn(M, cfg.qkv_out, generator=g).to(torch.bfloat16)
+    qw, kw = torch.ones(64, dtype=torch.bfloat16), (1 + 0.1 * torch.randn(64, generator=g)).to(torch.bfloat16)
+    pos = torch.tensor([0, 1, 2, 5, 77, 1000, 4095, 4096, 20000, 32767])
+    cos, sin = od.rope_tables(cfg, 32768)
+    out = od.qk_norm_rope(qkv, cfg, qw, kw, cos, sin, pos)
+    D = 64
+    qn = od.rmsnorm(qkv[:, :4 * D].reshape(M, 4, D), qw, cfg.eps)
+    ref = _rope64(qn, pos, cfg)
+    got = out[:, :4 * D].reshape(M, 4, D).double()
+    assert (got - ref).abs().max().item() < 0.05                      # bf16 tables and products
+    # a rotation keeps each pair's norm (within bf16 rounding) and leaves v untouched
+    nr = lambda t: (t[..., :32] ** 2 + t[..., 32:] ** 2).sqrt()
+    assert ((nr(got) - nr(qn.double())).abs() <= nr(qn.double()) * 0.02 + 1e-3).all()
+    assert torch.equal(out[:, 6 * D:], qkv[:, 6 * D:])
+
+
+def test_rope_scores_depend_on_relative_position_only():
+    """q_m . k_n after RoPE equals q_{m+d} . k_{n+d} (float64 restatement of the same rotation)."""
+    cfg = od.DecoderConfig(head_dim=128)
+    g = torch.Generator().manual_seed(2)
+    q, k = torch.randn(1, 1, 128, generator=g), torch.randn(1, 1, 128, generator=g)
+    s1 = (_rope64(q, torch.tensor([10]), cfg) * _rope64(k, torch.tensor([3]), cfg)).sum()
+    s2 = (_rope64(q, torch.tensor([5010]), cfg) * _rope64(k, torch.tensor([5003]), cfg)).sum()
+    assert abs(s1.item() - s2.item()) < 1e-9
+
+
+def test_swiglu_matches_float64():
+    g = torch.Generator().manual_seed(3)
+    gu = (torch.randn(5, 2 * 48, generator=g) * 4).to(torch.bfloat16)
+    y = od.swiglu(gu, 48).double()
+    gd, ud = gu[:, :48].double(), gu[:, 48:].double()
+    ref = gd / (1 + torch.exp(-gd)) * ud
+    assert ((y - ref).abs() <= ref.abs() * 2.0 ** -7 + 1e-6).all()
+
+
+def test_readout_normalises_and_appends_none():
+    cfg = od.DecoderConfig(hidden=32)
+    g = torch.Generator().manual_seed(4)
+    h = torch.randn(2 * 3 * 4, 32, generator=g).to(torch.bfloat16)
+    head = torch.randn(32, generator=g)
+    lp = od.readout(h, torch.ones(32, dtype=torch.bfloat16), head, torch.tensor(0.3), cfg, 2, 3, 4)
+    assert lp.shape == (2, 4)
+    assert torch.allclose(lp.exp().sum(-1), torch.ones(2), atol=1e-6)
+    # the none logit is the last entry: its log-prob is 0.3 - logsumexp(all logits)
+    hf = od.rmsnorm(h, torch.ones(32, dtype=torch.bfloat16), cfg.eps).double().reshape(2, 3, 4, 32).mean(2)
+    logits = torch.cat([hf @ head.double(), torch.full((2, 1), 0.3, dtype=torch.float64)], 1)
+    assert torch.allclose(lp[:, 3].double(), 0.3 - torch.logsumexp(logits, 1), atol=1e-5)
+    assert torch.allclose(lp.double(), torch.log_softmax(logits, 1), atol=1e-5)
+
+
+def _tiny_states(cfg, B, T, layers, seed):
+    from oracle import quant as oq
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(layers):
+        kv = torch.randn(2, B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).to(torch.bfloat16)
+        kq, ks = oq.quantize_rows(kv[0])
+        vq, vs = oq.quantize_rows(kv[1])
+        out.append(((kq, ks[..., 0]), (vq, vs[..., 0])))
+    return out
+
+
+def test_decision_forward_is_option_order_invariant():
+    cfg = od.DecoderConfig(hidden=128, ffn=256, n_heads=4, n_kv_heads=2, head_dim=32, n_layers=2, vocab=97)
+    w = od.make_weights(cfg, seed=5)
+    emb = od.make_embedding(cfg, seed=5)
+    B, n_opt, t, T = 2, 5, 3, 20
+    states = _tiny_states(cfg, B, T, cfg.n_layers, 6)
+    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=torch.Generator().manual_seed(7))
+    lp = od.decision_forward(ids, w, emb, cfg, states, T)
+    perm = torch.tensor([3, 0, 4, 1, 2])
+    lp_p = od.decision_forward(ids[:, perm], w, emb, cfg, states, T)
+    assert (lp_p[:, :n_opt] - lp[:, perm]).abs().max().item() <= 1e-6
+    assert (lp_p[:, n_opt] - lp[:, n_opt]).abs().max().item() <= 1e-6
+    assert torch.allclose(lp.exp().sum(-1), torch.ones(B), atol=1e-5)

@@ -112,11 +112,13 @@ def test_int_gemm_brute_force_and_closed_form():
     assert oq.int_gemm(big, -big)[0, 0].item() == -127 * 127 * 12288
 
 
-def test_int_gemm_matches_torch_int_mm():
+@pytest.mark.parametrize("M,N,K", [(32, 64, 256), (1, 3, 16), (300, 70, 1040)])
+def test_int_gemm_matches_int64_matmul(M, N, K):
     g = torch.Generator().manual_seed(8)
-    a = torch.randint(-127, 128, (32, 256), generator=g, dtype=torch.int8)
-    w = torch.randint(-127, 128, (64, 256), generator=g, dtype=torch.int8)
-    assert torch.equal(oq.int_gemm(a, w), torch._int_mm(a, w.t().contiguous()))
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    ref = (a.to(torch.int64) @ w.to(torch.int64).t())
+    assert torch.equal(oq.int_gemm(a, w).to(torch.int64), ref)
 
 
 def test_epilogue_within_one_bf16_rounding_of_float64():
