@@ -2,23 +2,27 @@
 // cores (V_MFMA_I32_32X32X32_I8), then the dequant epilogue out = bf16(float(acc) * sa[m] * sw[n] (+ bias)
 // (+ residual)).
 //
-// Tiling (MFMA-bound at the 9B shapes; one workgroup of 4 waves per CU):
-//   * workgroup tile BM x BN = 256 x {256 | 192}; K is staged through LDS in 128-byte slabs, double buffered
-//     (2 x (32 KB + BN * 128 B) <= 128 KB of the 160 KB LDS);
-//   * global -> LDS with direct-to-LDS buffer loads (16 B per lane, no staging registers); rows past M/N and bytes
-//     past K come back as zeros from the buffer range check;
-//   * 2 x 2 waves, each owning a 128 x BN/2 sub-tile = 4 x (BN/64) MFMA tiles of 32 x 32 (up to 256 int32
-//     accumulators per lane, held in the accumulation registers);
-//   * LDS rows are 128 B; the 16-byte chunk c of row r lives at chunk c ^ (r & 7), so the 8 lanes the LDS serves
-//     together (rows r..r+7, one logical chunk) hit 8 different bank groups; the swizzle is applied on the global
-//     side of the DMA (lane i fetches the chunk that belongs in slot i);
-//   * blockIdx -> tile is XCD-aware: the hardware deals workgroups round-robin over the 8 XCDs, so each XCD gets a
-//     contiguous range of tiles in a grouped (kGroupM tile-rows) order, and the tiles one XCD runs together share
-//     A/W panels in that XCD's L2;
-//   * epilogue: fp32 dequantized values staged through the (now idle) LDS in two 128-row halves, then the
-//     residual is added, the value rounded once to bf16 and stored 4 columns per lane, a wave per row segment;
-//   * the exact int32 accumulators (parity / debug) come from a separate instantiation that only writes them.
+// Tiling (MFMA-bound at the 9B shapes; one workgroup of 8 waves per CU):
+//   * workgroup tile BM x BN = 256 x {256 | 192}; K streams through LDS in 64-byte slabs, 4 stages deep
+//     (4 x (16 KB + BN * 64 B) <= 128 KB of the 160 KB LDS). Global -> LDS uses direct-to-LDS buffer loads (16 B
+//     per lane, no staging registers) issued 3 stages ahead; a stage is waited for with a vmcnt that leaves the
+//     newer stages in flight, then one barrier. Rows past M/N and bytes past K read as zeros (buffer range check).
+//   * every stage (A slab + W slab) is its own __shared__ array: the compiler can then tell that an LDS read of
+//     stage s does not alias the DMA filling stage s + 3 and does not serialize them.
+//   * 4 x 2 waves (2 per SIMD, so one wave's MFMAs cover the other's LDS latency), each owning a 64 x BN/2
+//     sub-tile = 2 x (BN/64) MFMA tiles of 32 x 32 (up to 128 int32 accumulators per lane).
+//   * LDS rows are 64 B (4 chunks of 16 B); chunk c of row r is stored at chunk c ^ ((r >> 1) & 3), so the 8 lanes
+//     the LDS serves together (rows r..r+7, one logical chunk) hit 8 different bank groups; the swizzle is applied
+//     on the global side of the DMA (lane i fetches the chunk that belongs in slot i).
+//   * blockIdx -> tile is XCD-aware: workgroups are dealt round-robin over the 8 XCDs, so each XCD gets a contiguous
+//     range of tiles in a grouped (kGroupM tile-rows) order, and the tiles one XCD runs together share A/W panels
+//     in its L2.
+//   * epilogue: each wave stages its accumulators 32 rows at a time through a private LDS band and writes 4
+//     columns per lane, a wave covering whole row segments; scales, bias and residual are applied in fp32 in the
+//     oracle's order and rounded once to bf16. No workgroup barrier after the one that ends the main loop.
 // int32 accumulation is exact for K < 133,144 (|acc| <= 127^2 K < 2^31), so any correct GEMM is bit-exact.
+#include <type_traits>
+
 #include "od_common.h"
 
 namespace {
@@ -27,11 +31,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kThreads = 256;
+constexpr int kWM = 4, kWN = 2;            // wave grid of a workgroup
+constexpr int kThreads = 64 * kWM * kWN;   // 512
 constexpr int BM = 256;
-constexpr int BK = 128;
+constexpr int BK = 64;       // bytes of K per stage
+constexpr int kStages = 4;
 constexpr int kGroupM = 4;
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any range: the load returns zeros
+
+template <int N>
+using IC = std::integral_constant<int, N>;
 
 struct GemmArgs {
   const int8_t* a;
@@ -47,24 +56,85 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 4); }
+// byte offset of logical 16-byte chunk c (0..3) of row r inside a stage buffer
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 3)) << 4); }
 
-// DMA of a ROWS x 128 B slab (rows row0.., bytes k0..k0+127) into LDS. Per wave instruction, lane l writes LDS
-// bytes [base + 16 l, base + 16 l + 16): LDS chunk index cid = i * 256 + wave * 64 + lane, row = cid / 8,
-// physical chunk = cid % 8, which holds logical chunk (cid % 8) ^ (row & 7).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without a memory fence: the stage waits are explicit vmcnt waits (a fenced __syncthreads would
+// wait for every DMA in flight, including the stages being prefetched). The "memory" clobber keeps the compiler
+// from moving LDS accesses across it.
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// DMA of a ROWS x 64 B slab into LDS. Per wave instruction, lane l writes LDS bytes [base + 16 l, +16): LDS chunk
+// index cid = i * 256 + wave * 64 + lane, row = cid / 4, physical chunk = cid % 4, which holds logical chunk
+// (cid % 4) ^ ((row >> 1) & 3). The per-lane part of the global offset (row * ld + 16 * logical chunk) is fixed
+// for the whole K loop (voff[i]); the k0 of the slab goes in the instruction's scalar offset. With KTAIL (K not a
+// multiple of the slab) chunks past K are sent out of the buffer's range and read as zeros.
+// A slab of ROWS x 64 B is ROWS / 16 wave-instructions of 64 lanes x 16 B, dealt round-robin to the waves: wave w
+// issues instruction i * kWaves + w for i = 0, 1, ... while it is below ROWS / 16.
+constexpr int kWaves = kWM * kWN;
+
 template <int ROWS>
-__device__ __forceinline__ void dma_slab(__amdgpu_buffer_rsrc_t rsrc, int64_t ld, int64_t k0, int64_t K,
-                                         int8_t* lds) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__device__ __forceinline__ constexpr int slab_iters() { return (ROWS / 16 + kWaves - 1) / kWaves; }
+
+// DMA instructions wave w issues for one ROWS-row slab
+template <int ROWS>
+__device__ __forceinline__ int slab_loads(int wave) {
+  constexpr int n = ROWS / 16;
+  return n / kWaves + (wave < n % kWaves ? 1 : 0);
+}
+
+template <int ROWS>
+struct SlabOffsets {
+  int v[slab_iters<ROWS>()];
+  int col[slab_iters<ROWS>()];  // byte column of the chunk inside the slab
+  __device__ __forceinline__ void init(int64_t ld) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < ROWS * 8 / kThreads; ++i) {
-    const int cid = i * kThreads + wave * 64 + lane;
-    const int row = cid >> 3;
-    const int lchunk = (cid & 7) ^ (row & 7);
-    const int64_t gk = k0 + (lchunk << 4);
-    const int off = gk < K ? (int)(row * ld + gk) : kOOB;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(lds + (i * kThreads + wave * 64) * 16), 16, off, 0, 0,
-                                             0);
+    for (int i = 0; i < slab_iters<ROWS>(); ++i) {
+      const int cid = (i * kWaves + wave) * 64 + lane;
+      const int row = cid >> 2;
+      col[i] = ((cid & 3) ^ ((row >> 1) & 3)) << 4;
+      v[i] = (int)(row * ld) + col[i];
+    }
+  }
+};
+
+// One direct-to-LDS 16-byte load per lane: LDS[m0 + 16 lane] = buffer[voff + soff]. Written as inline assembly so
+// that the compiler's wait-count pass does not see it: the compiler would otherwise wait for every DMA in flight
+// before the next LDS read (it cannot always tell the stage buffers apart), collapsing the pipeline. The waits for
+// these loads are the explicit vmcnt waits of the pipeline. m0 is not used by anything else in this kernel.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const int8_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)p;
+}
+
+// DMA of a ROWS x 64 B slab into LDS. Lane l of wave-instruction q writes LDS bytes [16 (64 q + l), +16): chunk
+// index cid = 64 q + l, row = cid / 4, physical chunk = cid % 4, holding logical chunk (cid % 4) ^ ((row >> 1) & 3).
+// The per-lane part of the global offset (row * ld + 16 * logical chunk) is fixed for the whole K loop (so.v); the
+// k0 of the slab goes in the instruction's scalar offset. With KTAIL (K not a multiple of the slab) chunks past K
+// are sent out of the buffer's range and read as zeros.
+template <int ROWS, bool KTAIL>
+__device__ __forceinline__ void dma_slab(__amdgpu_buffer_rsrc_t rsrc, const SlabOffsets<ROWS>& so, int k0, int K,
+                                         int8_t* lds) {
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < slab_iters<ROWS>(); ++i) {
+    const int q = i * kWaves + wave;
+    if ((ROWS / 16) % kWaves != 0 && q >= ROWS / 16) break;  // wave-uniform
+    int voff = so.v[i];
+    if constexpr (KTAIL) voff = (k0 + so.col[i] < K) ? voff : kOOB;
+    dma16(rsrc, __builtin_amdgcn_readfirstlane(lds_addr(lds + q * 64 * 16)), voff, k0);
   }
 }
 
@@ -81,19 +151,24 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
   tn = in_group / gsz;
 }
 
-template <int BN, bool ACC_ONLY>
+template <int BN, bool ACC_ONLY, bool KTAIL>
 __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
-  constexpr int TM = 4;              // 32-row MFMA tiles per wave (128 rows)
-  constexpr int TN = BN / 64;        // 32-col MFMA tiles per wave (BN / 2 cols)
+  constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile
+  constexpr int TM = kRowsW / 32;    // 32-row MFMA tiles per wave
+  constexpr int TN = kColsW / 32;    // 32-col MFMA tiles per wave
   constexpr int kSlabA = BM * BK, kSlabB = BN * BK;
-  __shared__ __attribute__((aligned(16))) int8_t lds[2 * (kSlabA + kSlabB)];
+  // DMA instructions this wave issues per stage (the W slab of BN = 192 does not split evenly over the waves)
+  constexpr int kLoadsHi = BM / 16 / kWaves + (BN / 16 + kWaves - 1) / kWaves;
+  constexpr int kLoadsLo = BM / 16 / kWaves + (BN / 16) / kWaves;
+  // stage buffers: A slab at offset 0, W slab at offset kSlabA (four LDS objects: the compiler tracks DMA into each)
+  __shared__ __attribute__((aligned(16))) int8_t s0[kSlabA + kSlabB], s1[kSlabA + kSlabB], s2[kSlabA + kSlabB],
+      s3[kSlabA + kSlabB];
 
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const bool vec8 = (p.ldo % 4 == 0) && ((((uintptr_t)p.out) & 7u) == 0);
+  const int wm = wave / kWN, wn = wave % kWN;
 
   const int64_t rows_a = min((int64_t)BM, p.M - m0), rows_b = min((int64_t)BN, p.N - n0);
   const __amdgpu_buffer_rsrc_t ra =
@@ -103,6 +178,23 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
       __builtin_amdgcn_make_buffer_rsrc((void*)(p.w + n0 * p.ldw), (short)0, (int)((rows_b - 1) * p.ldw + p.K),
                                         0x00020000);
 
+  auto abuf = [&](auto I) -> int8_t* {
+    if constexpr (decltype(I)::value == 0) return s0;
+    else if constexpr (decltype(I)::value == 1) return s1;
+    else if constexpr (decltype(I)::value == 2) return s2;
+    else return s3;
+  };
+  auto bbuf = [&](auto I) -> int8_t* { return abuf(I) + kSlabA; };
+  SlabOffsets<BM> soa;
+  SlabOffsets<BN> sob;
+  soa.init(p.lda);
+  sob.init(p.ldw);
+  const int K = (int)p.K;
+  auto issue = [&](auto I, int kt) {
+    dma_slab<BM, KTAIL>(ra, soa, kt * BK, K, abuf(I));
+    dma_slab<BN, KTAIL>(rb, sob, kt * BK, K, bbuf(I));
+  };
+
   v16i acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -110,31 +202,39 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
   const int nk = (int)((p.K + BK - 1) / BK);
-  dma_slab<BM>(ra, p.lda, 0, p.K, lds);
-  dma_slab<BN>(rb, p.ldw, 0, p.K, lds + 2 * kSlabA);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  issue(IC<0>{}, 0);
+  if (nk > 1) issue(IC<1>{}, 1);
+  if (nk > 2) issue(IC<2>{}, 2);
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      dma_slab<BM>(ra, p.lda, (int64_t)(kt + 1) * BK, p.K, lds + (cur ^ 1) * kSlabA);
-      dma_slab<BN>(rb, p.ldw, (int64_t)(kt + 1) * BK, p.K, lds + 2 * kSlabA + (cur ^ 1) * kSlabB);
+  // one pipeline step: wait for stage I (k-tile kt), refill stage I+3 with k-tile kt+3, compute stage I
+  auto step = [&](auto I, int kt) {
+    if (kt >= nk) return;
+    const int newer = min(2, nk - 1 - kt);  // stages issued after this one and still allowed in flight
+    const bool hi = slab_loads<BM>(wave) + slab_loads<BN>(wave) == kLoadsHi;  // wave-uniform
+    if (newer == 2) {
+      if (hi) wait_vm<2 * kLoadsHi>(); else wait_vm<2 * kLoadsLo>();
+    } else if (newer == 1) {
+      if (hi) wait_vm<kLoadsHi>(); else wait_vm<kLoadsLo>();
+    } else {
+      wait_vm<0>();
     }
-    const int8_t* la = lds + cur * kSlabA;
-    const int8_t* lb = lds + 2 * kSlabA + cur * kSlabB;
+    barrier();
+    constexpr int kNext = (decltype(I)::value + 3) % kStages;
+    if (kt + 3 < nk) issue(IC<kNext>{}, kt + 3);
+    const int8_t* la = abuf(I);
+    const int8_t* lb = bbuf(I);
 #pragma unroll
     for (int s = 0; s < BK / 32; ++s) {
       const int chunk = s * 2 + (lane >> 5);
       v4i fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int row = wm * 128 + i * 32 + (lane & 31);
+        const int row = wm * kRowsW + i * 32 + (lane & 31);
         fa[i] = *reinterpret_cast<const v4i*>(la + swz(row, chunk));
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const int row = wn * (BN / 2) + j * 32 + (lane & 31);
+        const int row = wn * kColsW + j * 32 + (lane & 31);
         fb[j] = *reinterpret_cast<const v4i*>(lb + swz(row, chunk));
       }
 #pragma unroll
@@ -142,79 +242,68 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+  };
+
+  for (int kt = 0; kt < nk; kt += kStages) {
+    step(IC<0>{}, kt);
+    step(IC<1>{}, kt + 1);
+    step(IC<2>{}, kt + 2);
+    step(IC<3>{}, kt + 3);
   }
+  __syncthreads();  // every wave is done reading the stage buffers; each now reuses one as its private band
 
   // Epilogue. C layout of a 32x32 MFMA tile: lane l holds column l % 32 and rows 8*(r/4) + 4*(l/32) + r%4.
-  if constexpr (ACC_ONLY) {
+  // A wave handles its kRowsW x kColsW sub-tile in bands of 32 rows: accumulators -> a private LDS band
+  // (32 x kColsW int32; wave w uses half w % 2 of stage buffer w / 2), then each lane takes 4
+  // consecutive columns of a row (a wave covers whole rows).
+  int8_t* stage_of_wave = (wave >> 1) == 0 ? s0 : (wave >> 1) == 1 ? s1 : (wave >> 1) == 2 ? s2 : s3;
+  constexpr int kCols = kColsW;           // columns of the wave's sub-tile
+  constexpr int kC4 = kCols / 4;          // 4-column chunks per row
+  constexpr int kBand = 32 * kCols * 4;   // bytes of one band
+  static_assert(2 * kBand <= kSlabA + kSlabB, "epilogue bands do not fit");
+  int32_t* band = reinterpret_cast<int32_t*>(stage_of_wave + (wave & 1) * kBand);
+  const int64_t n_w = n0 + wn * kCols;
+  const bool vec_out = (p.ldo % 4 == 0) && ((((uintptr_t)p.out) & 7u) == 0);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int64_t n = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (m < p.M && n < p.N) p.acc[m * p.ldacc + n] = acc[i][j][r];
-        }
-    }
-    return;
-  }
-  // Scales into LDS (the main loop ended with a barrier, so the LDS is free).
-  __shared__ float s_sa[BM], s_sw[BN], s_bias[BN];
-  for (int i = threadIdx.x; i < BM; i += kThreads) s_sa[i] = (m0 + i < p.M) ? p.sa[m0 + i] : 0.0f;
-  for (int i = threadIdx.x; i < BN; i += kThreads) {
-    const bool ok = n0 + i < p.N;
-    s_sw[i] = ok ? p.sw[n0 + i] : 0.0f;
-    s_bias[i] = (ok && p.bias) ? od_bf16_to_f32(p.bias[n0 + i]) : 0.0f;
-  }
-  // Two halves of 128 rows: the waves of half h write their fp32 values ((acc * sa) * sw + bias) into an LDS
-  // tile [128][BN] (16-byte chunks swizzled by row & 7); then every thread adds the residual, rounds once to
-  // bf16 and stores 4 columns (8 B) per step, a wave covering 256 contiguous columns of a row.
-  float* ft = reinterpret_cast<float*>(lds);
-  constexpr int kC4 = BN / 4;  // 16-byte chunks per fp32 row
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    __syncthreads();
-    if (wm == half) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int nl = wn * (BN / 2) + j * 32 + (lane & 31);
-        const float swn = s_sw[nl], bn = s_bias[nl];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int ml = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);  // row within the half
-            float y = (float)acc[i][j][r] * s_sa[half * 128 + ml];
-            y = y * swn;
-            y = y + bn;
-            ft[ml * BN + (((nl >> 2) ^ (ml & 7)) << 2) + (nl & 3)] = y;
-          }
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        band[row * kCols + j * 32 + (lane & 31)] = acc[i][j][r];
       }
     }
-    __syncthreads();
-    for (int id = threadIdx.x; id < 128 * kC4; id += kThreads) {
-      const int ml = id / kC4, c = id % kC4;
-      const int64_t m = m0 + half * 128 + ml, n = n0 + c * 4;
+    const int64_t m_band = m0 + wm * kRowsW + i * 32;
+#pragma unroll 4
+    for (int id = lane; id < 32 * kC4; id += 64) {
+      const int row = id / kC4, c = id % kC4;
+      const int64_t m = m_band + row, n = n_w + c * 4;
+      const int4 v = *reinterpret_cast<const int4*>(band + row * kCols + c * 4);
       if (m >= p.M || n >= p.N) continue;
-      const float4 v = *reinterpret_cast<const float4*>(ft + ml * BN + ((c ^ (ml & 7)) << 2));
-      float y[4] = {v.x, v.y, v.z, v.w};
-      if (p.residual) {
-        const uint16_t* rr = p.residual + m * p.ldr + n;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < p.N) y[e] = y[e] + od_bf16_to_f32(rr[e]);
-      }
-      uint16_t* dst = p.out + m * p.ldo + n;
-      if (vec8 && n + 4 <= p.N) {
-        const uint32_t lo = (uint32_t)od_f32_to_bf16(y[0]) | ((uint32_t)od_f32_to_bf16(y[1]) << 16);
-        const uint32_t hi = (uint32_t)od_f32_to_bf16(y[2]) | ((uint32_t)od_f32_to_bf16(y[3]) << 16);
-        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+      const int vv[4] = {v.x, v.y, v.z, v.w};
+      if constexpr (ACC_ONLY) {
+        int32_t* dst = p.acc + m * p.ldacc + n;
+        for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = vv[e];
       } else {
-        for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = od_f32_to_bf16(y[e]);
+        const float sam = p.sa[m];
+        float y[4];
+        uint16_t* dst = p.out + m * p.ldo + n;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t ne = n + e < p.N ? n + e : p.N - 1;
+          y[e] = (float)vv[e] * sam;
+          y[e] = y[e] * p.sw[ne];
+          if (p.bias) y[e] = y[e] + od_bf16_to_f32(p.bias[ne]);
+          if (p.residual) y[e] = y[e] + od_bf16_to_f32(p.residual[m * p.ldr + ne]);
+        }
+        if (vec_out && n + 4 <= p.N) {
+          const uint32_t lo = (uint32_t)od_f32_to_bf16(y[0]) | ((uint32_t)od_f32_to_bf16(y[1]) << 16);
+          const uint32_t hi = (uint32_t)od_f32_to_bf16(y[2]) | ((uint32_t)od_f32_to_bf16(y[3]) << 16);
+          *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+        } else {
+          for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = od_f32_to_bf16(y[e]);
+        }
       }
     }
   }
@@ -247,21 +336,22 @@ extern "C" int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const
   p.tiles_n = (int)tiles_n;
   dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
-  if (acc) {
+  const bool ktail = (K % BK) != 0;
+  auto launch = [&](auto BNc, auto ACCc, auto TAILc) {
+    w8a8_gemm_kernel<decltype(BNc)::value, decltype(ACCc)::value, decltype(TAILc)::value><<<grid, block, 0, st>>>(p);
+  };
+  auto launch2 = [&](auto ACCc) {
     if (use192) {
-      w8a8_gemm_kernel<192, true><<<grid, block, 0, st>>>(p);
+      ktail ? launch(IC<192>{}, ACCc, std::true_type{}) : launch(IC<192>{}, ACCc, std::false_type{});
     } else {
-      w8a8_gemm_kernel<256, true><<<grid, block, 0, st>>>(p);
+      ktail ? launch(IC<256>{}, ACCc, std::true_type{}) : launch(IC<256>{}, ACCc, std::false_type{});
     }
+  };
+  if (acc) {
+    launch2(std::true_type{});
     const int rc = od_launch_status();
     if (rc != OD_OK) return rc;
   }
-  if (out) {
-    if (use192) {
-      w8a8_gemm_kernel<192, false><<<grid, block, 0, st>>>(p);
-    } else {
-      w8a8_gemm_kernel<256, false><<<grid, block, 0, st>>>(p);
-    }
-  }
+  if (out) launch2(std::false_type{});
   return od_launch_status();
 }
