@@ -141,6 +141,185 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(uint16_t* __rest
   hp[i + L] = od_f32_to_bf16(bfr(nb * c) + bfr(na * s));
 }
 
+// ---------------------------------------------------------------------------- register-resident fast paths
+// A row of 256 * 8 * NV elements is held in registers (NV 16-byte vectors of 8 bf16 per thread, vector v of thread
+// t covering elements (v * 256 + t) * 8 .. +7), so the row is read from HBM once and written once.
+__device__ __forceinline__ void unpack8(const uint4 u, float (&f)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[2 * j] = __uint_as_float(w[j] << 16);
+    f[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ uint2 pack_q8(const float (&y)[8], float scale) {
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lo |= ((uint32_t)(uint8_t)q8(y[j], scale)) << (8 * j);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) hi |= ((uint32_t)(uint8_t)q8(y[4 + j], scale)) << (8 * j);
+  return make_uint2(lo, hi);
+}
+
+template <int NV>
+__global__ __launch_bounds__(kThreads) void rmsnorm_quant_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                     const uint16_t* __restrict__ w,
+                                                                     const uint16_t* __restrict__ inv_s, float eps,
+                                                                     int8_t* __restrict__ xq, int64_t ldq,
+                                                                     float* __restrict__ sx) {
+  constexpr int K = kThreads * 8 * NV;
+  __shared__ float red[kThreads / OD_WAVE];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * ldx;
+  float y[NV][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int k = (v * kThreads + threadIdx.x) * 8;
+    unpack8(*reinterpret_cast<const uint4*>(xr + k), y[v]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(y[v][e], y[v][e], ss);
+  }
+  ss = block_sum(ss, red);
+  const float r = 1.0f / sqrtf(ss / (float)K + eps);
+  float amax = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int k = (v * kThreads + threadIdx.x) * 8;
+    float wv[8], iv[8];
+    unpack8(*reinterpret_cast<const uint4*>(w + k), wv);
+    if (inv_s) unpack8(*reinterpret_cast<const uint4*>(inv_s + k), iv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float t = bfr(wv[e] * bfr(y[v][e] * r));
+      if (inv_s) t = bfr(t * iv[e]);
+      y[v][e] = t;
+      amax = fmaxf(amax, fabsf(t));
+    }
+  }
+  amax = block_max(amax, red);
+  const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+  int8_t* qr = xq + row * ldq;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int k = (v * kThreads + threadIdx.x) * 8;
+    *reinterpret_cast<uint2*>(qr + k) = pack_q8(y[v], scale);
+  }
+  if (threadIdx.x == 0) sx[row] = scale;
+}
+
+// silu(g) = g / (1 + exp(-g)) with the device exp and reciprocal (a few fp32 ulps; the value is then rounded to
+// bf16, which hides the difference except at rare rounding ties).
+__device__ __forceinline__ float silu_fast(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+
+template <int NV>
+__global__ __launch_bounds__(kThreads) void silu_mul_quant_vec_kernel(const uint16_t* __restrict__ gu, int64_t ldg,
+                                                                      const uint16_t* __restrict__ inv_s,
+                                                                      int8_t* __restrict__ aq, int64_t ldq,
+                                                                      float* __restrict__ sa) {
+  constexpr int F = kThreads * 8 * NV;
+  __shared__ float red[kThreads / OD_WAVE];
+  const int64_t row = blockIdx.x;
+  const uint16_t* gr = gu + row * ldg;
+  float y[NV][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int k = (v * kThreads + threadIdx.x) * 8;
+    float g[8], u[8], iv[8];
+    unpack8(*reinterpret_cast<const uint4*>(gr + k), g);
+    unpack8(*reinterpret_cast<const uint4*>(gr + F + k), u);
+    if (inv_s) unpack8(*reinterpret_cast<const uint4*>(inv_s + k), iv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float t = bfr(bfr(silu_fast(g[e])) * u[e]);
+      if (inv_s) t = bfr(t * iv[e]);
+      y[v][e] = t;
+      amax = fmaxf(amax, fabsf(t));
+    }
+  }
+  amax = block_max(amax, red);
+  const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+  int8_t* qr = aq + row * ldq;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int k = (v * kThreads + threadIdx.x) * 8;
+    *reinterpret_cast<uint2*>(qr + k) = pack_q8(y[v], scale);
+  }
+  if (threadIdx.x == 0) sa[row] = scale;
+}
+
+// q/k RMSNorm + RoPE for head_dim 128 with 16 lanes per head: lane j holds d = 4j..4j+3 and the rotary partners
+// 64 + 4j..64 + 4j + 3, so every load and store is 8 bytes and no lane exchange is needed for the rotation.
+__global__ __launch_bounds__(kThreads) void qk_norm_rope128_kernel(uint16_t* __restrict__ qkv, int64_t ld, int64_t M,
+                                                                   int n_heads_q, int n_heads_k,
+                                                                   const uint16_t* __restrict__ qw,
+                                                                   const uint16_t* __restrict__ kw,
+                                                                   const uint16_t* __restrict__ cos_t,
+                                                                   const uint16_t* __restrict__ sin_t, int64_t n_pos,
+                                                                   const int32_t* __restrict__ pos, float eps) {
+  constexpr int D = 128, L = 64;
+  const int heads = n_heads_q + n_heads_k;
+  const int64_t gh = (int64_t)blockIdx.x * (kThreads / 16) + threadIdx.x / 16;
+  if (gh >= M * heads) return;  // whole 16-lane groups exit together
+  const int64_t row = gh / heads;
+  const int head = (int)(gh % heads);
+  const int j = threadIdx.x % 16;
+  uint16_t* hp = qkv + row * ld + (int64_t)head * D;
+  const uint16_t* w = head < n_heads_q ? qw : kw;
+  const uint2 ra = *reinterpret_cast<const uint2*>(hp + 4 * j), rb = *reinterpret_cast<const uint2*>(hp + L + 4 * j);
+  const uint2 wa = *reinterpret_cast<const uint2*>(w + 4 * j), wb = *reinterpret_cast<const uint2*>(w + L + 4 * j);
+  float a[4], b[4], fa[4], fb[4];
+  const uint32_t ua[2] = {ra.x, ra.y}, ub[2] = {rb.x, rb.y}, uwa[2] = {wa.x, wa.y}, uwb[2] = {wb.x, wb.y};
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    a[2 * e] = __uint_as_float(ua[e] << 16);
+    a[2 * e + 1] = __uint_as_float(ua[e] & 0xffff0000u);
+    b[2 * e] = __uint_as_float(ub[e] << 16);
+    b[2 * e + 1] = __uint_as_float(ub[e] & 0xffff0000u);
+    fa[2 * e] = __uint_as_float(uwa[e] << 16);
+    fa[2 * e + 1] = __uint_as_float(uwa[e] & 0xffff0000u);
+    fb[2 * e] = __uint_as_float(uwb[e] << 16);
+    fb[2 * e + 1] = __uint_as_float(uwb[e] & 0xffff0000u);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ss = fmaf(b[e], b[e], fmaf(a[e], a[e], ss));
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, OD_WAVE);
+  const float r = 1.0f / sqrtf(ss / (float)D + eps);
+  const int64_t p = pos[row];
+  const bool in_table = p >= 0 && p < n_pos;  // a position past the tables yields NaN, never an out-of-bounds read
+  float c[4], sn[4];
+  if (in_table) {
+    const uint2 rc = *reinterpret_cast<const uint2*>(cos_t + p * L + 4 * j);
+    const uint2 rs = *reinterpret_cast<const uint2*>(sin_t + p * L + 4 * j);
+    const uint32_t uc[2] = {rc.x, rc.y}, us[2] = {rs.x, rs.y};
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      c[2 * e] = __uint_as_float(uc[e] << 16);
+      c[2 * e + 1] = __uint_as_float(uc[e] & 0xffff0000u);
+      sn[2 * e] = __uint_as_float(us[e] << 16);
+      sn[2 * e + 1] = __uint_as_float(us[e] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c[e] = sn[e] = __builtin_nanf("");
+  }
+  uint16_t oa[4], ob[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float na = bfr(fa[e] * bfr(a[e] * r)), nb = bfr(fb[e] * bfr(b[e] * r));
+    oa[e] = od_f32_to_bf16(bfr(na * c[e]) + bfr(-nb * sn[e]));
+    ob[e] = od_f32_to_bf16(bfr(nb * c[e]) + bfr(na * sn[e]));
+  }
+  *reinterpret_cast<uint2*>(hp + 4 * j) =
+      make_uint2((uint32_t)oa[0] | ((uint32_t)oa[1] << 16), (uint32_t)oa[2] | ((uint32_t)oa[3] << 16));
+  *reinterpret_cast<uint2*>(hp + L + 4 * j) =
+      make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
+}
+
 }  // namespace
 
 extern "C" int od_rmsnorm_quant(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* inv_s, float eps,
@@ -149,8 +328,19 @@ extern "C" int od_rmsnorm_quant(const uint16_t* x, int64_t ldx, const uint16_t* 
   if (M == 0) return OD_OK;
   if (!x || !w || !xq || !sx) return OD_ERR_NULL;
   if (M > 0x7fffffff) return OD_ERR_SHAPE;
-  rmsnorm_quant_kernel<<<dim3((unsigned)M), dim3(kThreads), 0, (hipStream_t)stream>>>(x, ldx, w, inv_s, eps, xq, ldq,
-                                                                                      sx, (int)K);
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = (ldx % 8 == 0) && (ldq % 8 == 0) && od_aligned16(x) && od_aligned16(w) &&
+                   (!inv_s || od_aligned16(inv_s)) && ((((uintptr_t)xq) & 7u) == 0);
+  const dim3 grid((unsigned)M), block(kThreads);
+  if (vec && K == 2048) {
+    rmsnorm_quant_vec_kernel<1><<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+  } else if (vec && K == 4096) {
+    rmsnorm_quant_vec_kernel<2><<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+  } else if (vec && K == 8192) {
+    rmsnorm_quant_vec_kernel<4><<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+  } else {
+    rmsnorm_quant_kernel<<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx, (int)K);
+  }
   return od_launch_status();
 }
 
@@ -160,8 +350,19 @@ extern "C" int od_silu_mul_quant(const uint16_t* gu, int64_t ldg, int64_t F, con
   if (M == 0) return OD_OK;
   if (!gu || !aq || !sa) return OD_ERR_NULL;
   if (M > 0x7fffffff) return OD_ERR_SHAPE;
-  silu_mul_quant_kernel<<<dim3((unsigned)M), dim3(kThreads), 0, (hipStream_t)stream>>>(gu, ldg, F, inv_s, aq, ldq,
-                                                                                       sa);
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = (ldg % 8 == 0) && (F % 8 == 0) && (ldq % 8 == 0) && od_aligned16(gu) &&
+                   (!inv_s || od_aligned16(inv_s)) && ((((uintptr_t)aq) & 7u) == 0);
+  const dim3 grid((unsigned)M), block(kThreads);
+  if (vec && F == 2048 * 6) {
+    silu_mul_quant_vec_kernel<6><<<grid, block, 0, st>>>(gu, ldg, inv_s, aq, ldq, sa);
+  } else if (vec && F == 2048 * 4) {
+    silu_mul_quant_vec_kernel<4><<<grid, block, 0, st>>>(gu, ldg, inv_s, aq, ldq, sa);
+  } else if (vec && F == 2048 * 3) {
+    silu_mul_quant_vec_kernel<3><<<grid, block, 0, st>>>(gu, ldg, inv_s, aq, ldq, sa);
+  } else {
+    silu_mul_quant_kernel<<<grid, block, 0, st>>>(gu, ldg, F, inv_s, aq, ldq, sa);
+  }
   return od_launch_status();
 }
 
@@ -178,7 +379,15 @@ extern "C" int od_qk_norm_rope(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_h
   const int64_t blocks = (M * heads + per_block - 1) / per_block;
   if (blocks > 0x7fffffff || heads > 0x7fffffff) return OD_ERR_SHAPE;
   hipStream_t st = (hipStream_t)stream;
-  if (D == 128) {
+  const bool vec128 = D == 128 && (ld % 4 == 0) && ((((uintptr_t)qkv) & 7u) == 0) && ((((uintptr_t)q_w) & 7u) == 0) &&
+                      ((((uintptr_t)k_w) & 7u) == 0) && ((((uintptr_t)cos_t) & 7u) == 0) &&
+                      ((((uintptr_t)sin_t) & 7u) == 0);
+  if (vec128) {
+    const int64_t b16 = (M * heads + kThreads / 16 - 1) / (kThreads / 16);
+    if (b16 > 0x7fffffff) return OD_ERR_SHAPE;
+    qk_norm_rope128_kernel<<<dim3((unsigned)b16), dim3(kThreads), 0, st>>>(qkv, ld, M, (int)n_heads_q, (int)n_heads_k,
+                                                                           q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
+  } else if (D == 128) {
     qk_norm_rope_kernel<128><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
         qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
   } else {
