@@ -62,20 +62,52 @@ struct AttnArgs {
   float scale_log2;
 };
 
+// Every array is 16-byte aligned so that fragment and scale accesses compile to single ds_read_b128 /
+// ds_write_b128 instructions (without the alignment the compiler splits them into 4-byte pairs).
 template <int D>
-struct Smem {
-  _Float16 k[2][kBlockKeys * D];   // [key][d], 16-byte chunks swizzled by key & 7
-  _Float16 vt[2][D * kBlockKeys];  // [d][permuted key], 16-byte chunks swizzled by d & 7
-  float gk[2][kBlockKeys];         // score multiplier of key j (its K scale)
-  float kb[2][kBlockKeys];         // 0, or -inf for a masked key
-  float fv[2][kBlockKeys];         // V scale of key j divided by 2^E_b
-  int eb[2];                       // E_b
+struct alignas(16) Smem {
+  alignas(16) _Float16 k[2][kBlockKeys * D];   // [key][d], 16-byte chunks swizzled (k_off)
+  alignas(16) _Float16 vt[2][D * kBlockKeys];  // [d][permuted key], 16-byte chunks swizzled (vt_off)
+  alignas(16) float gk[2][kBlockKeys];         // score multiplier of key j (its K scale)
+  alignas(16) float kb[2][kBlockKeys];         // 0, or -inf for a masked key
+  alignas(16) float fv[2][kBlockKeys];         // V scale of key j divided by 2^E_b
+  int eb[2];                                   // E_b
   float red[2][kWaves];
 };
 
+// LDS swizzles. gfx950 LDS: reads see 64 4-byte banks (a 256-byte period) and serve 16 lanes of a ds_read_b128
+// per cycle; writes go 128 bytes per cycle with a 128-byte bank period (8 lanes of a ds_write_b128, 16 lanes of a
+// ds_write_b64). A fragment read has lanes 16g .. 16g+15 take 16 consecutive rows (keys of K, d of V^T) at one
+// logical 16-byte chunk, so the chunk is XORed with a function of the row that gives those 16 rows 16 distinct
+// bank quads:
+//  * K, rows of 2D bytes (D/8 chunks): 128/D rows share a 256-byte period, XOR with (key / (128/D)) mod D/8;
+//  * V^T, rows of 128 bytes (8 chunks), two rows per period: XOR with ((d >> 1) ^ (d >> 3)) & 7, which is a
+//    bijection on any 8 consecutive even (or odd) d and also on {8 dg + e : dg = 8 consecutive values} for a
+//    fixed e, which the transposing store needs (see vmap).
 template <int D>
-__device__ __forceinline__ int k_off(int key, int chunk) { return key * D + ((chunk ^ (key & 7)) << 3); }
-__device__ __forceinline__ int vt_off(int d, int chunk) { return d * kBlockKeys + ((chunk ^ (d & 7)) << 3); }
+__device__ __forceinline__ int k_off(int key, int chunk) {
+  return key * D + ((chunk ^ ((key / (128 / D)) & (D / 8 - 1))) << 3);
+}
+__device__ __forceinline__ int vt_off(int d, int chunk) {
+  return d * kBlockKeys + ((chunk ^ (((d >> 1) ^ (d >> 3)) & 7)) << 3);
+}
+
+// Thread -> (d group dg of 8 d, key group kg of 4 keys) of the transposing V store. A thread writes 8 bytes (its
+// 4 keys) into each of the V^T rows 8 dg .. 8 dg + 7. Lanes 16i .. 16i+15 form one ds_write_b64 bank cycle: bits
+// 0..2 of the lane pick 8 consecutive dg (8 distinct chunks after the V^T swizzle) and bit 3 flips bit 1 of kg,
+// which is the half of the 16-byte chunk the 4 keys occupy, so the 16 lanes write 16 distinct 8-byte slots.
+// D = 128: 16 dg x 16 kg = 256 threads; D = 64: 8 dg x 16 kg = threads 0..127. kg < 8 <=> thread < D.
+template <int D>
+__device__ __forceinline__ void vmap(int tid, int& dg, int& kg) {
+  const int lo = tid & 7, t3 = (tid >> 3) & 1, hi = tid >> 4;
+  if constexpr (D == 128) {
+    dg = lo | ((hi & 1) << 3);
+    kg = (t3 << 1) | ((hi >> 1) & 1) | ((hi >> 2) << 2);
+  } else {
+    dg = lo;
+    kg = (t3 << 1) | (hi & 1) | ((hi >> 1) << 2);
+  }
+}
 // position of key j (0..63) inside its V^T row: bits 2 and 3 swapped
 __device__ __forceinline__ int jj_of(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
 
@@ -128,13 +160,13 @@ __device__ __forceinline__ void prefix_load(const AttnArgs& p, int s, int g, int
     if (cid < kChunks && j0 + key < p.T)
       r.k[i] = *reinterpret_cast<const uint4*>(p.kq + (head_base + j0 + key) * D + c * 16);
   }
-  constexpr int kDg = D / 8;
-  const int dg = tid % kDg, kg = tid / kDg;
+  int dg, kg;
+  vmap<D>(tid, dg, kg);
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const int key = 4 * kg + a;
     r.v[a] = make_uint2(0, 0);
-    if (kg < kBlockKeys / 4 && j0 + key < p.T)
+    if (tid < 2 * D && j0 + key < p.T)
       r.v[a] = *reinterpret_cast<const uint2*>(p.vq + (head_base + j0 + key) * D + 8 * dg);
   }
   r.sc = 0.0f;
@@ -158,18 +190,23 @@ __device__ __forceinline__ void prefix_store(Smem<D>& sm, int buf, const PrefixR
     const int cid = i * kThreads + tid;
     if (cid < kChunks) {
       const int key = cid / kCpk, c = cid % kCpk;
+      // the 16 int8 values become two fp16 chunks, 2c and 2c + 1; lanes with bit 2 set store 2c + 1 first, so
+      // that the 8 lanes of a ds_write_b128 bank cycle hit 8 distinct chunks of the 128-byte period
+      const int flip = (tid >> 2) & 1;
+      const uint32_t a0 = flip ? r.k[i].z : r.k[i].x, a1 = flip ? r.k[i].w : r.k[i].y;
+      const uint32_t b0 = flip ? r.k[i].x : r.k[i].z, b1 = flip ? r.k[i].y : r.k[i].w;
       uint4 h0, h1;
-      i8x4_to_h(r.k[i].x, h0.x, h0.y);
-      i8x4_to_h(r.k[i].y, h0.z, h0.w);
-      i8x4_to_h(r.k[i].z, h1.x, h1.y);
-      i8x4_to_h(r.k[i].w, h1.z, h1.w);
-      *reinterpret_cast<uint4*>(&sm.k[buf][k_off<D>(key, 2 * c)]) = h0;
-      *reinterpret_cast<uint4*>(&sm.k[buf][k_off<D>(key, 2 * c + 1)]) = h1;
+      i8x4_to_h(a0, h0.x, h0.y);
+      i8x4_to_h(a1, h0.z, h0.w);
+      i8x4_to_h(b0, h1.x, h1.y);
+      i8x4_to_h(b1, h1.z, h1.w);
+      *reinterpret_cast<uint4*>(&sm.k[buf][k_off<D>(key, 2 * c + flip)]) = h0;
+      *reinterpret_cast<uint4*>(&sm.k[buf][k_off<D>(key, 2 * c + 1 - flip)]) = h1;
     }
   }
-  constexpr int kDg = D / 8;
-  const int dg = tid % kDg, kg = tid / kDg;
-  if (kg < kBlockKeys / 4) {
+  int dg, kg;
+  vmap<D>(tid, dg, kg);
+  if (tid < 2 * D) {
     // 4 keys x 8 bytes -> for each of the 8 d: the 4 keys' bytes (a 4x4 byte transpose per dword half)
     uint32_t cols[8];
 #pragma unroll
@@ -323,9 +360,10 @@ __device__ __forceinline__ void own_stage(const AttnArgs& p, Smem<D>& sm, int ro
     for (int e = 0; e < 4; ++e)
       ka = fmaxf(ka, fmaxf(fabsf(__uint_as_float(w4[e] << 16)), fabsf(__uint_as_float(w4[e] & 0xffff0000u))));
   }
-  // V: a thread takes 4 keys x 8 d (kOwnKeys / 4 key groups x D / 8 d groups <= 256 threads)
-  const int dg = tid % kCpk, kg = tid / kCpk;
-  const bool vact = kg < kOwnKeys / 4;
+  // V: a thread takes 4 keys x 8 d (kOwnKeys / 4 key groups x D / 8 d groups, threads 0 .. D - 1)
+  int dg, kg;
+  vmap<D>(tid, dg, kg);
+  const bool vact = tid < D;
   uint4 vr[4];
 #pragma unroll
   for (int a = 0; a < 4; ++a) {

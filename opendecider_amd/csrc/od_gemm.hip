@@ -56,8 +56,14 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
+// Chunk swizzle of the 64-byte LDS rows. An operand read is a ds_read_b128 in which lanes 16g..16g+15 take 16
+// consecutive rows at one logical chunk, and gfx950 serves 16 lanes of a ds_read_b128 per cycle from 64 4-byte
+// banks (a 256-byte period): rows r and r + 4 share their bank set unless their chunks differ, so the chunk is
+// XORed with bits 2..3 of the row, which makes the 16 reads of a group land on 16 distinct 16-byte bank quads.
+__device__ __forceinline__ int chunk_xor(int row) { return (row >> 2) & 3; }
+
 // byte offset of logical 16-byte chunk c (0..3) of row r inside a stage buffer
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 3)) << 4); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ chunk_xor(row)) << 4); }
 
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -71,7 +77,7 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 
 // DMA of a ROWS x 64 B slab into LDS. Per wave instruction, lane l writes LDS bytes [base + 16 l, +16): LDS chunk
 // index cid = i * 256 + wave * 64 + lane, row = cid / 4, physical chunk = cid % 4, which holds logical chunk
-// (cid % 4) ^ ((row >> 1) & 3). The per-lane part of the global offset (row * ld + 16 * logical chunk) is fixed
+// (cid % 4) ^ chunk_xor(row). The per-lane part of the global offset (row * ld + 16 * logical chunk) is fixed
 // for the whole K loop (voff[i]); the k0 of the slab goes in the instruction's scalar offset. With KTAIL (K not a
 // multiple of the slab) chunks past K are sent out of the buffer's range and read as zeros.
 // A slab of ROWS x 64 B is ROWS / 16 wave-instructions of 64 lanes x 16 B, dealt round-robin to the waves: wave w
@@ -98,7 +104,7 @@ struct SlabOffsets {
     for (int i = 0; i < slab_iters<ROWS>(); ++i) {
       const int cid = (i * kWaves + wave) * 64 + lane;
       const int row = cid >> 2;
-      col[i] = ((cid & 3) ^ ((row >> 1) & 3)) << 4;
+      col[i] = ((cid & 3) ^ chunk_xor(row)) << 4;
       v[i] = (int)(row * ld) + col[i];
     }
   }
@@ -120,7 +126,7 @@ __device__ __forceinline__ uint32_t lds_addr(const int8_t* p) {
 }
 
 // DMA of a ROWS x 64 B slab into LDS. Lane l of wave-instruction q writes LDS bytes [16 (64 q + l), +16): chunk
-// index cid = 64 q + l, row = cid / 4, physical chunk = cid % 4, holding logical chunk (cid % 4) ^ ((row >> 1) & 3).
+// index cid = 64 q + l, row = cid / 4, physical chunk = cid % 4, holding logical chunk (cid % 4) ^ chunk_xor(row).
 // The per-lane part of the global offset (row * ld + 16 * logical chunk) is fixed for the whole K loop (so.v); the
 // k0 of the slab goes in the instruction's scalar offset. With KTAIL (K not a multiple of the slab) chunks past K
 // are sent out of the buffer's range and read as zeros.
