@@ -144,6 +144,17 @@ __device__ __forceinline__ void dma_slab(__amdgpu_buffer_rsrc_t rsrc, const Slab
   }
 }
 
+// Instruction i (0 .. slab_iters - 1) of this wave's share of dma_slab, if the wave has one (wave-uniform).
+template <int ROWS, bool KTAIL>
+__device__ __forceinline__ void dma_one(__amdgpu_buffer_rsrc_t rsrc, const SlabOffsets<ROWS>& so, int i, int k0, int K,
+                                        int8_t* lds) {
+  const int q = i * kWaves + (threadIdx.x >> 6);
+  if ((ROWS / 16) % kWaves != 0 && q >= ROWS / 16) return;
+  int voff = so.v[i];
+  if constexpr (KTAIL) voff = (k0 + so.col[i] < K) ? voff : kOOB;
+  dma16(rsrc, __builtin_amdgcn_readfirstlane(lds_addr(lds + q * 64 * 16)), voff, k0);
+}
+
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int ntiles = tiles_m * tiles_n;
   const int xcd = bid & 7, local = bid >> 3;
@@ -157,7 +168,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
   tn = in_group / gsz;
 }
 
-template <int BN, bool ACC_ONLY, bool KTAIL>
+template <int BN, bool ACC_ONLY, bool GENERAL>
 __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile
   constexpr int TM = kRowsW / 32;    // 32-row MFMA tiles per wave
@@ -197,8 +208,14 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   sob.init(p.ldw);
   const int K = (int)p.K;
   auto issue = [&](auto I, int kt) {
-    dma_slab<BM, KTAIL>(ra, soa, kt * BK, K, abuf(I));
-    dma_slab<BN, KTAIL>(rb, sob, kt * BK, K, bbuf(I));
+    dma_slab<BM, GENERAL>(ra, soa, kt * BK, K, abuf(I));
+    dma_slab<BN, GENERAL>(rb, sob, kt * BK, K, bbuf(I));
+  };
+  // the same DMA one instruction at a time: j < slab_iters<BM> is A instruction j, then the W instructions
+  constexpr int kDmaA = slab_iters<BM>(), kDma = kDmaA + slab_iters<BN>();
+  auto issue_one = [&](auto I, int kt, int j) {
+    if (j < kDmaA) dma_one<BM, GENERAL>(ra, soa, j, kt * BK, K, abuf(I));
+    else dma_one<BN, GENERAL>(rb, sob, j - kDmaA, kt * BK, K, bbuf(I));
   };
 
   v16i acc[TM][TN];
@@ -208,46 +225,74 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
   const int nk = (int)((p.K + BK - 1) / BK);
-  issue(IC<0>{}, 0);
-  if (nk > 1) issue(IC<1>{}, 1);
-  if (nk > 2) issue(IC<2>{}, 2);
-
-  // one pipeline step: wait for stage I (k-tile kt), refill stage I+3 with k-tile kt+3, compute stage I
-  auto step = [&](auto I, int kt) {
-    if (kt >= nk) return;
-    const int newer = min(2, nk - 1 - kt);  // stages issued after this one and still allowed in flight
-    const bool hi = slab_loads<BM>(wave) + slab_loads<BN>(wave) == kLoadsHi;  // wave-uniform
-    if (newer == 2) {
+  const bool hi = slab_loads<BM>(wave) + slab_loads<BN>(wave) == kLoadsHi;  // wave-uniform
+  // wait until at most `newer` stages issued after the awaited one are still in flight (this wave's DMAs)
+  auto wait_stage = [&](int newer) {
+    if (newer >= 2) {
       if (hi) wait_vm<2 * kLoadsHi>(); else wait_vm<2 * kLoadsLo>();
     } else if (newer == 1) {
       if (hi) wait_vm<kLoadsHi>(); else wait_vm<kLoadsLo>();
     } else {
       wait_vm<0>();
     }
-    barrier();
-    constexpr int kNext = (decltype(I)::value + 3) % kStages;
-    if (kt + 3 < nk) issue(IC<kNext>{}, kt + 3);
-    const int8_t* la = abuf(I);
-    const int8_t* lb = bbuf(I);
+  };
+  // operand fragments of k-step s (32 of the stage's 64 k) of one stage buffer
+  auto frags = [&](const int8_t* la, const int8_t* lb, int s, v4i (&fa)[TM], v4i (&fb)[TN]) {
+    const int chunk = s * 2 + (lane >> 5);
 #pragma unroll
-    for (int s = 0; s < BK / 32; ++s) {
-      const int chunk = s * 2 + (lane >> 5);
-      v4i fa[TM], fb[TN];
+    for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(la + swz(wm * kRowsW + i * 32 + (lane & 31), chunk));
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = wm * kRowsW + i * 32 + (lane & 31);
-        fa[i] = *reinterpret_cast<const v4i*>(la + swz(row, chunk));
-      }
+    for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const v4i*>(lb + swz(wn * kColsW + j * 32 + (lane & 31), chunk));
+  };
+  auto mma = [&](const v4i (&fa)[TM], const v4i (&fb)[TN]) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int row = wn * kColsW + j * 32 + (lane & 31);
-        fb[j] = *reinterpret_cast<const v4i*>(lb + swz(row, chunk));
-      }
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+  };
+  // The MFMAs of one k-step with the refill DMA of stage I (k-tile kt) spread between them, one instruction after
+  // every TM*TN/kDma MFMAs: issued as one burst right after the barrier, the DMAs of all 8 waves fill the
+  // texture-address queue and the waves stall at issue instead of running their MFMAs.
+  auto mma_dma = [&](const v4i (&fa)[TM], const v4i (&fb)[TN], auto I, int kt, bool refill) {
+    constexpr int kMf = TM * TN;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    for (int x = 0; x < kMf; ++x) {
+      acc[x / TN][x % TN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[x / TN], fb[x % TN], acc[x / TN][x % TN], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < kDma; ++j)
+        if (j * kMf / kDma == x && refill) issue_one(I, kt, j);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+
+  // Pipeline. Stage buffer I % 4 holds k-tile I; three k-tiles are in flight ahead of the one being computed.
+  // Fragments are register double-buffered across k-steps and across stages: step kt loads k-step 1 of its
+  // stage, runs k-step 0, then (once stage kt+1 has landed for every wave: own vmcnt wait + barrier) loads k-step 0
+  // of stage kt+1 and runs k-step 1 while refilling the buffer of k-tile kt-1 with k-tile kt+3 (every wave is past
+  // its last read of kt-1: those reads fed MFMAs issued before the barrier). LDS latency is thus always
+  // covered by 8 MFMAs of the same wave.
+  v4i f0a[TM], f0b[TN], f1a[TM], f1b[TN];
+  issue(IC<0>{}, 0);
+  if (nk > 1) issue(IC<1>{}, 1);
+  if (nk > 2) issue(IC<2>{}, 2);
+  wait_stage(min(2, nk - 1));
+  barrier();
+  frags(abuf(IC<0>{}), bbuf(IC<0>{}), 0, f0a, f0b);
+
+  auto step = [&](auto I, int kt) {
+    if (kt >= nk) return;
+    constexpr int kI = decltype(I)::value, kN = (kI + 1) % kStages, kR = (kI + 3) % kStages;
+    frags(abuf(I), bbuf(I), 1, f1a, f1b);
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs they overlap
+    mma(f0a, f0b);
+    // Unconditional also on the last k-tile (then it reads an idle, in-bounds stage buffer whose values are
+    // never used): a branch here would merge two paths with different numbers of LDS reads in flight, and the
+    // compiler's lgkmcnt wait before k-step 1 would then also wait for the reads of the next stage.
+    wait_stage(min(1, nk - 2 - kt));
+    barrier();
+    frags(abuf(IC<kN>{}), bbuf(IC<kN>{}), 0, f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_dma(f1a, f1b, IC<kR>{}, kt + 3, kt + 3 < nk);
   };
 
   for (int kt = 0; kt < nk; kt += kStages) {
@@ -258,57 +303,119 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   }
   __syncthreads();  // every wave is done reading the stage buffers; each now reuses one as its private band
 
-  // Epilogue. C layout of a 32x32 MFMA tile: lane l holds column l % 32 and rows 8*(r/4) + 4*(l/32) + r%4.
-  // A wave handles its kRowsW x kColsW sub-tile in bands of 32 rows: accumulators -> a private LDS band
-  // (32 x kColsW int32; wave w uses half w % 2 of stage buffer w / 2), then each lane takes 4
-  // consecutive columns of a row (a wave covers whole rows).
+  // Epilogue, in two passes per band of 32 rows of the wave's kRowsW x kColsW sub-tile.
+  //  1. In the MFMA result layout (lane l holds column l % 32 of each 32x32 tile and rows
+  //     8*(r/4) + 4*(l/32) + r%4), t = (float(acc) * sa[m]) * sw[n] (the raw int32 with ACC_ONLY) goes to a private
+  //     LDS band (32 x kColsW 4-byte words; wave w uses half w % 2 of stage buffer w / 2). A lane needs one sw per
+  //     column tile and 16 sa per band, loaded up front.
+  //  2. Row-major: lane l takes the 4 columns 4 (l % kC4) .. +3 of rows l / kC4 + kRowsPass * it, so its bias
+  //     values are fixed for the tile; y = bf16((t + bias) + residual), the same fp32 operation order as the
+  //     unfused product, with one rounding. Rows go in groups of 4 whose residual loads issue together.
+  // The epilogue runs once per tile, so its code is kept small (it is fetched anew for every tile): only the
+  // GENERAL variant carries the scalar paths for unaligned rows and a ragged last column group.
   int8_t* stage_of_wave = (wave >> 1) == 0 ? s0 : (wave >> 1) == 1 ? s1 : (wave >> 1) == 2 ? s2 : s3;
-  constexpr int kCols = kColsW;           // columns of the wave's sub-tile
-  constexpr int kC4 = kCols / 4;          // 4-column chunks per row
-  constexpr int kBand = 32 * kCols * 4;   // bytes of one band
+  constexpr int kCols = kColsW;               // columns of the wave's sub-tile
+  constexpr int kC4 = kCols / 4;              // 4-column chunks per row
+  constexpr int kRowsPass = 64 / kC4;         // rows one pass of the wave covers
+  constexpr int kPasses = (32 + kRowsPass - 1) / kRowsPass;
+  static_assert(kPasses % 4 == 0, "row groups of 4");
+  constexpr int kBand = 32 * kCols * 4;       // bytes of one band
   static_assert(2 * kBand <= kSlabA + kSlabB, "epilogue bands do not fit");
-  int32_t* band = reinterpret_cast<int32_t*>(stage_of_wave + (wave & 1) * kBand);
+  uint32_t* band = reinterpret_cast<uint32_t*>(stage_of_wave + (wave & 1) * kBand);
   const int64_t n_w = n0 + wn * kCols;
-  const bool vec_out = (p.ldo % 4 == 0) && ((((uintptr_t)p.out) & 7u) == 0);
+  const int col = lane & 31, h = lane >> 5;
+  float swv[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) swv[j] = ACC_ONLY ? 0.0f : p.sw[min(n_w + j * 32 + col, p.N - 1)];
+  // row pass: this lane's 4 columns and their bias
+  const int c4 = lane % kC4, rr = lane / kC4;
+  const int64_t n = n_w + 4 * c4;
+  const bool lane_on = rr < kRowsPass && n < p.N;
+  float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (!ACC_ONLY && p.bias) {
+    if constexpr (GENERAL) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bias4[e] = od_bf16_to_f32(p.bias[min(n + e, p.N - 1)]);
+    } else if (lane_on) {
+      const uint2 b = *reinterpret_cast<const uint2*>(p.bias + n);
+      bias4[0] = __uint_as_float(b.x << 16);
+      bias4[1] = __uint_as_float(b.x & 0xffff0000u);
+      bias4[2] = __uint_as_float(b.y << 16);
+      bias4[3] = __uint_as_float(b.y & 0xffff0000u);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    const int64_t m_band = m0 + wm * kRowsW + i * 32;
+    float sav[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      sav[r] = ACC_ONLY ? 0.0f : p.sa[min(m_band + 8 * (r >> 2) + 4 * h + (r & 3), p.M - 1)];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        band[row * kCols + j * 32 + (lane & 31)] = acc[i][j][r];
+        const int row = 8 * (r >> 2) + 4 * h + (r & 3);
+        uint32_t word;
+        if constexpr (ACC_ONLY) {
+          word = (uint32_t)acc[i][j][r];
+        } else {
+          float t = (float)acc[i][j][r] * sav[r];
+          t = t * swv[j];
+          word = __float_as_uint(t);
+        }
+        band[row * kCols + j * 32 + col] = word;
       }
     }
-    const int64_t m_band = m0 + wm * kRowsW + i * 32;
-#pragma unroll 4
-    for (int id = lane; id < 32 * kC4; id += 64) {
-      const int row = id / kC4, c = id % kC4;
-      const int64_t m = m_band + row, n = n_w + c * 4;
-      const int4 v = *reinterpret_cast<const int4*>(band + row * kCols + c * 4);
-      if (m >= p.M || n >= p.N) continue;
-      const int vv[4] = {v.x, v.y, v.z, v.w};
-      if constexpr (ACC_ONLY) {
-        int32_t* dst = p.acc + m * p.ldacc + n;
-        for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = vv[e];
-      } else {
-        const float sam = p.sa[m];
-        float y[4];
-        uint16_t* dst = p.out + m * p.ldo + n;
+    if (!lane_on) continue;
+#pragma unroll 1
+    for (int it0 = 0; it0 < kPasses; it0 += 4) {
+      uint2 res[4];
+      if (!ACC_ONLY && p.residual) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t ne = n + e < p.N ? n + e : p.N - 1;
-          y[e] = (float)vv[e] * sam;
-          y[e] = y[e] * p.sw[ne];
-          if (p.bias) y[e] = y[e] + od_bf16_to_f32(p.bias[ne]);
-          if (p.residual) y[e] = y[e] + od_bf16_to_f32(p.residual[m * p.ldr + ne]);
+        for (int u = 0; u < 4; ++u) {
+          const uint16_t* rp = p.residual + min(m_band + kRowsPass * (it0 + u) + rr, p.M - 1) * p.ldr;
+          if constexpr (GENERAL) {
+            uint32_t e4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) e4[e] = rp[min(n + e, p.N - 1)];
+            res[u] = make_uint2(e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16));
+          } else {
+            res[u] = *reinterpret_cast<const uint2*>(rp + n);
+          }
         }
-        if (vec_out && n + 4 <= p.N) {
-          const uint32_t lo = (uint32_t)od_f32_to_bf16(y[0]) | ((uint32_t)od_f32_to_bf16(y[1]) << 16);
-          const uint32_t hi = (uint32_t)od_f32_to_bf16(y[2]) | ((uint32_t)od_f32_to_bf16(y[3]) << 16);
-          *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int row = kRowsPass * (it0 + u) + rr;
+        const int64_t m = m_band + row;
+        if (row >= 32 || m >= p.M) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(band + row * kCols + 4 * c4);
+        if constexpr (ACC_ONLY) {
+          int32_t* dst = p.acc + m * p.ldacc + n;
+          if constexpr (GENERAL) {
+            const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+            for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = (int32_t)vv[e];
+          } else {
+            *reinterpret_cast<uint4*>(dst) = v;
+          }
         } else {
-          for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = od_f32_to_bf16(y[e]);
+          const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+          const uint32_t rw[4] = {res[u].x << 16, res[u].x & 0xffff0000u, res[u].y << 16, res[u].y & 0xffff0000u};
+          uint32_t o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float y = __uint_as_float(vv[e]);
+            if (p.bias) y = y + bias4[e];
+            if (p.residual) y = y + __uint_as_float(rw[e]);
+            o[e] = od_f32_to_bf16(y);
+          }
+          uint16_t* dst = p.out + m * p.ldo + n;
+          if constexpr (GENERAL) {
+            for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = (uint16_t)o[e];
+          } else {
+            *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+          }
         }
       }
     }
@@ -342,22 +449,27 @@ extern "C" int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const
   p.tiles_n = (int)tiles_n;
   dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
-  const bool ktail = (K % BK) != 0;
-  auto launch = [&](auto BNc, auto ACCc, auto TAILc) {
-    w8a8_gemm_kernel<decltype(BNc)::value, decltype(ACCc)::value, decltype(TAILc)::value><<<grid, block, 0, st>>>(p);
+  // The fast variant needs whole k-tiles and 4-column output groups that are 8-byte (bf16) / 16-byte (int32)
+  // aligned; anything else takes the GENERAL variant.
+  auto al = [](const void* q, unsigned a) { return (((uintptr_t)q) & (a - 1)) == 0; };
+  const bool fast_k = K % BK == 0 && N % 4 == 0;
+  const bool fast_out = fast_k && ldo % 4 == 0 && al(out, 8) && al(bias, 8) && ldr % 4 == 0 && al(residual, 8);
+  const bool fast_acc = fast_k && ldacc % 4 == 0 && al(acc, 16);
+  auto launch = [&](auto BNc, auto ACCc, auto GENc) {
+    w8a8_gemm_kernel<decltype(BNc)::value, decltype(ACCc)::value, decltype(GENc)::value><<<grid, block, 0, st>>>(p);
   };
-  auto launch2 = [&](auto ACCc) {
+  auto launch2 = [&](auto ACCc, bool general) {
     if (use192) {
-      ktail ? launch(IC<192>{}, ACCc, std::true_type{}) : launch(IC<192>{}, ACCc, std::false_type{});
+      general ? launch(IC<192>{}, ACCc, std::true_type{}) : launch(IC<192>{}, ACCc, std::false_type{});
     } else {
-      ktail ? launch(IC<256>{}, ACCc, std::true_type{}) : launch(IC<256>{}, ACCc, std::false_type{});
+      general ? launch(IC<256>{}, ACCc, std::true_type{}) : launch(IC<256>{}, ACCc, std::false_type{});
     }
   };
   if (acc) {
-    launch2(std::true_type{});
+    launch2(std::true_type{}, !fast_acc);
     const int rc = od_launch_status();
     if (rc != OD_OK) return rc;
   }
-  if (out) launch2(std::false_type{});
+  if (out) launch2(std::false_type{}, !fast_out);
   return od_launch_status();
 }
