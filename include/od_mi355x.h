@@ -114,6 +114,27 @@ int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
                      float scale, od_stream_t stream);
 
 /*
+ * od_wide_attn — flash attention over bf16 K/V.
+ * Replaces: wide_attention / _wide_fwd (src/opendecider/wide_attention.py:13-91).
+ *   q      bf16 [B, H, T, DK], element strides (sqb, sqh, sqt)
+ *   k      bf16 [B, G, S, DK], strides (skb, skg, sks)
+ *   v      bf16 [B, G, S, DV], strides (svb, svg, svs)
+ *   kvalid uint8 [B, S] with row stride smb (nonzero = real key) or NULL
+ *   out    bf16 [B, H, T, DV], strides (sob, soh, sot) (out)
+ *   lse    fp32 [B, H, T] contiguous or NULL (out): natural-log log-sum-exp of the scaled scores, -inf where a
+ *          query sees no key
+ * Query head h reads KV group h / (H / G); queries are the last T of the S key positions (query t sits at t + S - T
+ * and, with causal != 0, sees keys 0 .. t + S - T). A query with no visible key returns 0. P is rounded to bf16
+ * before the P.V product, as in the reference. Supports H % G == 0, DK <= 512 with DK % 8 == 0, DV in
+ * {64, 128, 256}; element strides multiples of 8 (q, k, v) and 4 (out); q, k, v 16-byte aligned, out 8-byte.
+ */
+int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* k, int64_t skb,
+                 int64_t skg, int64_t sks, const uint16_t* v, int64_t svb, int64_t svg, int64_t svs,
+                 const uint8_t* kvalid, int64_t smb, uint16_t* out, int64_t sob, int64_t soh, int64_t sot, float* lse,
+                 int64_t B, int64_t H, int64_t G, int64_t T, int64_t S, int64_t DK, int64_t DV, int causal,
+                 float scale, od_stream_t stream);
+
+/*
  * Row kernels of the dense decoder layer that carries the path in the decision-forward harness (not reference
  * functions: the reference runs these steps inside HF Qwen3.5 modules; they are fused here around the W8A8 GEMMs).
  *

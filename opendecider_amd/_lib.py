@@ -27,6 +27,9 @@ SIGNATURES = {
     "od_branched_attn": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
                          _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr,
                          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _c_ptr],
+    "od_wide_attn": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64,
+                     _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int,
+                     ctypes.c_float, _c_ptr],
     "od_rmsnorm_quant": [_c_ptr, _i64, _c_ptr, _c_ptr, ctypes.c_float, _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr],
     "od_silu_mul_quant": [_c_ptr, _i64, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _c_ptr],
     "od_qk_norm_rope": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr,

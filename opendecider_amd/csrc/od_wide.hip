@@ -1,0 +1,367 @@
+// Flash attention over bf16 K/V (the wide_attention contract), for gfx950.
+//
+// Math (src/opendecider/wide_attention.py:13-67): queries are the last T of S key positions (query t sits at
+// position t + S - T); with causal it sees keys 0 .. t + S - T, kvalid (B, S) masks keys, GQA head h reads KV group
+// h / (H / G). Online softmax in the exp2 domain: s = (q.k) * scale * log2(e), m, l, acc as FlashAttention-2; P is
+// rounded to bf16 before the P.V product (the reference's p.to(v.dtype)); out = acc / l, 0 for a query with no
+// visible key; LSE = (m + log2 l) ln 2, -inf for such a query.
+//
+// Work decomposition. A "slot" is one (token, head of the KV group) pair, slot z -> token z / rep, head
+// g * rep + z % rep (the reference's row order). Grid = (slot tiles of 128, B * G); a workgroup of 4 waves owns 128
+// consecutive slots of one (batch, KV group) and streams that group's K/V once for all of them; a wave owns 32.
+//
+// Layout trick (as in the branched kernel): scores are computed transposed, S^T = K Q^T, on
+// V_MFMA_F32_32X32X16_BF16 with the 32 keys of a key tile as rows and the wave's 32 slots as columns, so the online
+// softmax is lane-local, and the probabilities sit where O^T += V^T P^T wants its B operand. V is stored in LDS
+// transposed (V^T, d-major), with bits 2 and 3 of the key index swapped inside each 16-key group to match the MFMA
+// result layout. Q is held in registers (the reduction dimension DK is padded with zeros to DKP).
+#include "od_common.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int kSlotsPerTile = 128;
+constexpr int kBK = 64;  // keys per block (2 key tiles of 32)
+constexpr float kLn2 = 0.693147180559945309f;
+
+struct WideArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint8_t* kvalid;
+  uint16_t* out;
+  float* lse;
+  int64_t sqb, sqh, sqt, skb, skg, sks, svb, svg, svs, sob, soh, sot, smb;
+  int H, G, T, S, DK, rep, causal;
+  float scale_log2;
+};
+
+template <int DKP, int DV, int NBUF>
+struct alignas(16) WSmem {
+  alignas(16) uint16_t k[NBUF][kBK * DKP];   // [key][d], 16-byte chunks swizzled (wk_off)
+  alignas(16) uint16_t vt[NBUF][DV * kBK];   // [d][permuted key], 16-byte chunks swizzled (wvt_off)
+  alignas(16) float kb[NBUF][kBK];           // 0, or -inf for a key out of range or masked by kvalid
+};
+
+// LDS swizzles for gfx950's banking (reads: 64 4-byte banks, 16 lanes of a ds_read_b128 per cycle; writes: a
+// 128-byte period, 8 lanes of a ds_write_b128 or 16 of a ds_write_b64 per cycle). A fragment read has lanes
+// 16i .. 16i+15 take 16 consecutive rows at one logical chunk:
+//  * K rows are 2 DKP bytes (DKP/8 chunks): for DKP >= 128 every row starts a 256-byte period and the chunk is XORed
+//    with key & 15; for DKP = 64 two rows share a period and it is XORed with (key >> 1) & 7;
+//  * V^T rows are 128 bytes (8 chunks of 8 keys): XOR with ((d >> 1) ^ (d >> 3)) & 7, a bijection on 8
+//    consecutive even (or odd) d and on {8 dg + e} for 8 consecutive dg, which the transposing store uses (wvmap).
+template <int DKP>
+__device__ __forceinline__ int wk_off(int key, int chunk) {
+  const int x = DKP == 64 ? ((key >> 1) & 7) : (key & 15);
+  return key * DKP + ((chunk ^ x) << 3);
+}
+__device__ __forceinline__ int wvt_off(int d, int chunk) {
+  return d * kBK + ((chunk ^ (((d >> 1) ^ (d >> 3)) & 7)) << 3);
+}
+// position of key j (0..63) inside its V^T row: bits 2 and 3 swapped
+__device__ __forceinline__ int wjj_of(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
+
+// Thread -> (d group dg of 8 d, key group kg of 4 keys) for the transposing V store, for 128 d (16 dg x 16 kg over
+// 256 threads). Lanes 16i .. 16i+15 form one ds_write_b64 bank cycle: lane bits 0..2 pick 8 consecutive dg (8
+// distinct chunks after the V^T swizzle) and bit 3 flips bit 1 of kg, the half of the 16-byte chunk its 4 keys
+// occupy, so the 16 lanes write 16 distinct 8-byte slots. DV = 64 uses threads 0..127 (dg < 8), DV = 256 runs the
+// map twice with dg + 16 (d + 128 leaves the swizzle's low bits unchanged).
+__device__ __forceinline__ void wvmap(int tid, int& dg, int& kg) {
+  const int lo = tid & 7, t3 = (tid >> 3) & 1, hi = tid >> 4;
+  dg = lo | ((hi & 1) << 3);
+  kg = (t3 << 1) | ((hi >> 1) & 1) | ((hi >> 2) << 2);
+}
+
+template <int DV>
+__device__ __forceinline__ void wvmap_dv(int tid, int& dg, int& kg, bool& on) {
+  if constexpr (DV == 64) {
+    // 8 dg x 16 kg over threads 0..127 (same lane pattern with bit 3 of dg taken from bit 4 of the thread)
+    const int lo = tid & 7, t3 = (tid >> 3) & 1, hi = tid >> 4;
+    dg = lo;
+    kg = (t3 << 1) | (hi & 1) | ((hi >> 1) << 2);
+    on = tid < 128;
+  } else {
+    wvmap(tid, dg, kg);
+    on = true;
+  }
+}
+
+constexpr int kVPairs(int DV) { return DV == 256 ? 2 : 1; }
+
+template <int DKP, int DV>
+struct BlockRegs {
+  uint4 k[(kBK * DKP / 8 + kThreads - 1) / kThreads];
+  uint4 v[kVPairs(DV)][4];
+  int ok;  // thread < 64: key tid valid
+};
+
+template <int DKP, int DV>
+__device__ __forceinline__ void block_load(const WideArgs& p, int b, int g, int j0, BlockRegs<DKP, DV>& r) {
+  const int tid = threadIdx.x;
+  const uint16_t* kbase = p.k + (int64_t)b * p.skb + (int64_t)g * p.skg;
+  const uint16_t* vbase = p.v + (int64_t)b * p.svb + (int64_t)g * p.svg;
+  constexpr int kCpk = DKP / 8;                 // 16-byte chunks per key
+  constexpr int kChunks = kBK * kCpk;
+#pragma unroll
+  for (int i = 0; i < (kChunks + kThreads - 1) / kThreads; ++i) {
+    const int cid = i * kThreads + tid;
+    const int key = cid / kCpk, c = cid % kCpk;
+    r.k[i] = make_uint4(0, 0, 0, 0);
+    if (cid < kChunks && j0 + key < p.S && 8 * c < p.DK)
+      r.k[i] = *reinterpret_cast<const uint4*>(kbase + (int64_t)(j0 + key) * p.sks + 8 * c);
+  }
+  int dg, kg;
+  bool on;
+  wvmap_dv<DV>(tid, dg, kg, on);
+#pragma unroll
+  for (int hp = 0; hp < kVPairs(DV); ++hp) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int key = 4 * kg + a;
+      r.v[hp][a] = make_uint4(0, 0, 0, 0);
+      if (on && j0 + key < p.S)
+        r.v[hp][a] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(j0 + key) * p.svs + 8 * (dg + 16 * hp));
+    }
+  }
+  r.ok = 0;
+  if (tid < kBK) {
+    const int j = j0 + tid;
+    r.ok = j < p.S && (!p.kvalid || p.kvalid[(int64_t)b * p.smb + j] != 0);
+  }
+}
+
+template <int DKP, int DV, int NBUF>
+__device__ __forceinline__ void block_store(WSmem<DKP, DV, NBUF>& sm, int buf, const BlockRegs<DKP, DV>& r) {
+  const int tid = threadIdx.x;
+  constexpr int kCpk = DKP / 8;
+  constexpr int kChunks = kBK * kCpk;
+#pragma unroll
+  for (int i = 0; i < (kChunks + kThreads - 1) / kThreads; ++i) {
+    const int cid = i * kThreads + tid;
+    if (cid < kChunks) *reinterpret_cast<uint4*>(&sm.k[buf][wk_off<DKP>(cid / kCpk, cid % kCpk)]) = r.k[i];
+  }
+  int dg, kg;
+  bool on;
+  wvmap_dv<DV>(tid, dg, kg, on);
+  if (on) {
+    const int jj0 = wjj_of(4 * kg);
+#pragma unroll
+    for (int hp = 0; hp < kVPairs(DV); ++hp) {
+      const uint32_t w[4][4] = {{r.v[hp][0].x, r.v[hp][0].y, r.v[hp][0].z, r.v[hp][0].w},
+                                {r.v[hp][1].x, r.v[hp][1].y, r.v[hp][1].z, r.v[hp][1].w},
+                                {r.v[hp][2].x, r.v[hp][2].y, r.v[hp][2].z, r.v[hp][2].w},
+                                {r.v[hp][3].x, r.v[hp][3].y, r.v[hp][3].z, r.v[hp][3].w}};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // element e of the 4 keys: bf16 halves of dword e / 2
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        uint2 hv;
+        hv.x = __builtin_amdgcn_perm(w[1][e >> 1], w[0][e >> 1], sel);
+        hv.y = __builtin_amdgcn_perm(w[3][e >> 1], w[2][e >> 1], sel);
+        const int d = 8 * (dg + 16 * hp) + e;
+        *reinterpret_cast<uint2*>(&sm.vt[buf][wvt_off(d, jj0 >> 3) + (jj0 & 7)]) = hv;
+      }
+    }
+  }
+  if (tid < kBK) sm.kb[buf][tid] = r.ok ? 0.0f : -INFINITY;
+}
+
+template <int DKP, int DV, int NBUF>
+__device__ __forceinline__ void wide_block(const WSmem<DKP, DV, NBUF>& sm, int buf, const bf16x8 (&qf)[DKP / 16],
+                                           float scale_log2, float& m_run, float& l_run, v16f (&o)[DV / 32],
+                                           bool check_causal, int j0, int qpos) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  constexpr int KT = kBK / 32;
+  v16f s[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    s[kt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < DKP / 16; ++ks) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sm.k[buf][wk_off<DKP>(kt * 32 + col, ks * 2 + h)]);
+      s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[kt], 0, 0, 0);
+    }
+  }
+  // scores of this lane's slot: key = kt*32 + 8*(r/4) + 4*h + r%4
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int key0 = kt * 32 + 8 * r4 + 4 * h;
+      const float4 b4 = *reinterpret_cast<const float4*>(&sm.kb[buf][key0]);
+      const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float y = fmaf(s[kt][4 * r4 + e], scale_log2, bb[e]);
+        if (check_causal && j0 + key0 + e > qpos) y = -INFINITY;
+        s[kt][4 * r4 + e] = y;
+        mloc = fmaxf(mloc, y);
+      }
+    }
+  }
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  const float m_new = fmaxf(m_run, mloc);
+  const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_safe);
+  float psum = 0.0f;
+  bf16x8 pb[2 * KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pr = __builtin_amdgcn_exp2f(s[kt][r] - m_safe);
+      psum += pr;
+      pb[kt * 2 + (r >> 3)][r & 7] = __builtin_bit_cast(__bf16, od_f32_to_bf16(pr));
+    }
+  }
+  psum += __shfl_xor(psum, 32, 64);
+  l_run = l_run * alpha + psum;
+  m_run = m_new;
+#pragma unroll
+  for (int dt = 0; dt < DV / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+#pragma unroll
+  for (int dt = 0; dt < DV / 32; ++dt) {
+#pragma unroll
+    for (int m = 0; m < 2 * KT; ++m) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sm.vt[buf][wvt_off(dt * 32 + col, 2 * m + h)]);
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[m], o[dt], 0, 0, 0);
+    }
+  }
+}
+
+template <int DKP, int DV, int NBUF, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void wide_attn_kernel(WideArgs p) {
+  __shared__ WSmem<DKP, DV, NBUF> sm;
+  const int bg = blockIdx.y;
+  const int b = bg / p.G, g = bg % p.G;
+  const int nslots = p.T * p.rep;
+  const int slot_base = blockIdx.x * kSlotsPerTile;
+  if (slot_base >= nslots) return;  // uniform over the workgroup
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  const int z = slot_base + wave * 32 + col;
+  const bool slot_ok = z < nslots;
+  const int tok = slot_ok ? z / p.rep : p.T - 1;
+  const int head = g * p.rep + (slot_ok ? z % p.rep : 0);
+  const int shift = p.S - p.T;
+  const int qpos = tok + shift;
+
+  // query fragments: lane holds Q[slot][ks*16 + 8h .. +8], zero past DK
+  bf16x8 qf[DKP / 16];
+  {
+    const uint16_t* qp = p.q + (int64_t)b * p.sqb + (int64_t)head * p.sqh + (int64_t)tok * p.sqt;
+#pragma unroll
+    for (int ks = 0; ks < DKP / 16; ++ks) {
+      uint4 raw = make_uint4(0, 0, 0, 0);
+      if (slot_ok && ks * 16 + 8 * h < p.DK) raw = *reinterpret_cast<const uint4*>(qp + ks * 16 + 8 * h);
+      qf[ks] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  v16f o[DV / 32];
+#pragma unroll
+  for (int dt = 0; dt < DV / 32; ++dt) o[dt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+  // keys this tile can see: causal stops after the last token's position
+  const int last = min(slot_base + kSlotsPerTile, nslots) - 1;
+  const int tok_lo = slot_base / p.rep, tok_hi = last / p.rep;
+  const int kend = p.causal ? min(p.S, tok_hi + shift + 1) : p.S;
+  const int nb = (kend + kBK - 1) / kBK;
+  // a block whose last key is at or below the first token's position needs no causal check
+  const int free_until = tok_lo + shift;
+  if (nb > 0) {
+    BlockRegs<DKP, DV> br;
+    block_load<DKP, DV>(p, b, g, 0, br);
+    block_store<DKP, DV, NBUF>(sm, 0, br);
+    __syncthreads();
+    for (int blk = 0; blk < nb; ++blk) {
+      const int cur = NBUF == 2 ? (blk & 1) : 0;
+      const int j0 = blk * kBK;
+      if (blk + 1 < nb) block_load<DKP, DV>(p, b, g, j0 + kBK, br);
+      wide_block<DKP, DV, NBUF>(sm, cur, qf, p.scale_log2, m_run, l_run, o, p.causal && j0 + kBK - 1 > free_until, j0,
+                                qpos);
+      if (blk + 1 < nb) {
+        if constexpr (NBUF == 1) __syncthreads();  // every wave is done with the single buffer
+        block_store<DKP, DV, NBUF>(sm, NBUF == 2 ? (cur ^ 1) : 0, br);
+      }
+      __syncthreads();
+    }
+  }
+
+  if (!slot_ok) return;
+  // epilogue: out = acc / l (0 where l = 0), lse = (m + log2 l) ln 2
+  uint16_t* op = p.out + (int64_t)b * p.sob + (int64_t)head * p.soh + (int64_t)tok * p.sot;
+  const float den = l_run == 0.0f ? 1.0f : l_run;
+#pragma unroll
+  for (int dt = 0; dt < DV / 32; ++dt) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int d0 = dt * 32 + 8 * r4 + 4 * h;
+      const uint32_t lo = (uint32_t)od_f32_to_bf16(o[dt][4 * r4] / den) |
+                          ((uint32_t)od_f32_to_bf16(o[dt][4 * r4 + 1] / den) << 16);
+      const uint32_t hi = (uint32_t)od_f32_to_bf16(o[dt][4 * r4 + 2] / den) |
+                          ((uint32_t)od_f32_to_bf16(o[dt][4 * r4 + 3] / den) << 16);
+      *reinterpret_cast<uint2*>(op + d0) = make_uint2(lo, hi);
+    }
+  }
+  if (p.lse && h == 0)
+    p.lse[((int64_t)b * p.H + head) * p.T + tok] = (m_run + __log2f(l_run)) * kLn2;
+}
+
+template <int DKP, int DV>
+void launch_wide(const WideArgs& a, dim3 grid, hipStream_t st) {
+  // LDS: double-buffered K + V^T up to DKP = 256; DKP = 512 is single-buffered (its K block alone is 64 KB).
+  // Two workgroups per CU where the registers allow it (Q and O fragments grow with DKP and DV).
+  constexpr int NBUF = DKP <= 256 ? 2 : 1;
+  constexpr int OCC = (DKP <= 128 && DV <= 128) ? 2 : 1;
+  wide_attn_kernel<DKP, DV, NBUF, OCC><<<grid, dim3(kThreads), 0, st>>>(a);
+}
+
+}  // namespace
+
+extern "C" int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* k, int64_t skb,
+                            int64_t skg, int64_t sks, const uint16_t* v, int64_t svb, int64_t svg, int64_t svs,
+                            const uint8_t* kvalid, int64_t smb, uint16_t* out, int64_t sob, int64_t soh, int64_t sot,
+                            float* lse, int64_t B, int64_t H, int64_t G, int64_t T, int64_t S, int64_t DK, int64_t DV,
+                            int causal, float scale, od_stream_t stream) {
+  if (B < 0 || H < 1 || G < 1 || T < 0 || S < 0 || DK < 1) return OD_ERR_SHAPE;
+  if (H % G) return OD_ERR_SHAPE;
+  if (DV != 64 && DV != 128 && DV != 256) return OD_ERR_UNSUPPORTED;
+  if (DK > 512) return OD_ERR_UNSUPPORTED;
+  if (B == 0 || T == 0) return OD_OK;
+  if (!q || !k || !v || !out) return OD_ERR_NULL;
+  if (DK % 8) return OD_ERR_ALIGN;
+  const int64_t strides[] = {sqb, sqh, sqt, skb, skg, sks, svb, svg, svs};
+  for (int64_t s : strides)
+    if (s < 0 || s % 8) return OD_ERR_ALIGN;
+  if (sob < 0 || soh < 0 || sot < 0 || sob % 4 || soh % 4 || sot % 4 || smb < 0) return OD_ERR_ALIGN;
+  if (!od_aligned16(q) || !od_aligned16(k) || !od_aligned16(v) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
+  const int64_t rep = H / G;
+  const int64_t tiles = (T * rep + kSlotsPerTile - 1) / kSlotsPerTile;
+  if (tiles > 0x7fffffff || B * G > 65535 || T * rep > 0x7fffffff || S > 0x7fffffff - kBK) return OD_ERR_SHAPE;
+  WideArgs a{q, k, v, kvalid, out, lse, sqb, sqh, sqt, skb, skg, sks, svb, svg, svs, sob, soh, sot, smb,
+             (int)H, (int)G, (int)T, (int)S, (int)DK, (int)rep, causal ? 1 : 0, scale * 1.4426950408889634f};
+  dim3 grid((unsigned)tiles, (unsigned)(B * G));
+  hipStream_t st = (hipStream_t)stream;
+  const int dkp = DK <= 64 ? 64 : DK <= 128 ? 128 : DK <= 256 ? 256 : 512;
+  auto by_dv = [&](auto DKc) {
+    constexpr int DKP = decltype(DKc)::value;
+    if (DV == 64) launch_wide<DKP, 64>(a, grid, st);
+    else if (DV == 128) launch_wide<DKP, 128>(a, grid, st);
+    else launch_wide<DKP, 256>(a, grid, st);
+  };
+  if (dkp == 64) by_dv(std::integral_constant<int, 64>{});
+  else if (dkp == 128) by_dv(std::integral_constant<int, 128>{});
+  else if (dkp == 256) by_dv(std::integral_constant<int, 256>{});
+  else by_dv(std::integral_constant<int, 512>{});
+  return od_launch_status();
+}

@@ -222,3 +222,28 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
                                  ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv, t,
                                  D, Ns, T, cap, float(scale), stream_of(q)), "od_branched_attn")
     return (out, lse) if return_lse else out
+
+
+def wide_attn(q, k, v, scale: float, kvalid=None, causal: bool = True, return_lse: bool = False, out=None):
+    """Flash attention over bf16 K/V (od_wide_attn). q (B, H, T, DK), k (B, G, S, DK), v (B, G, S, DV) bf16 with
+    DK % 8 == 0 and DK <= 512, DV in {64, 128, 256}; kvalid (B, S) bool/uint8 or None. Queries are the last T of the
+    S positions. Returns out (B, H, T, DV) bf16 [, lse (B, H, T) fp32]."""
+    require_gpu(q, k, v, kvalid, out, name="wide_attn")
+    for x in (q, k, v):
+        _lib.bf16_bits(x)
+    B, H, T, DK = q.shape
+    G, S, DV = k.shape[1], k.shape[2], v.shape[-1]
+    if k.shape != (B, G, S, DK) or v.shape[:3] != (B, G, S):
+        raise ValueError("wide_attn: k must be (B, G, S, DK) and v (B, G, S, DV)")
+    if kvalid is not None:
+        if kvalid.shape != (B, S):
+            raise ValueError("wide_attn: kvalid must be (B, S)")
+        kvalid = kvalid.to(torch.uint8).contiguous()
+    q, k, v = _rows_aligned(q), _rows_aligned(k), _rows_aligned(v)
+    if out is None:
+        out = torch.empty(B, H, T, DV, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=q.device) if return_lse else None
+    check(lib().od_wide_attn(ptr(q), *q.stride()[:3], ptr(k), *k.stride()[:3], ptr(v), *v.stride()[:3], ptr(kvalid),
+                             kvalid.stride(0) if kvalid is not None else 0, ptr(out), *out.stride()[:3], ptr(lse), B, H,
+                             G, T, S, DK, DV, 1 if causal else 0, float(scale), stream_of(q)), "od_wide_attn")
+    return (out, lse) if return_lse else out

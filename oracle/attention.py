@@ -58,6 +58,57 @@ def attention(q, k, v, scale: float, kvalid=None, causal: bool = True, dtype=tor
     return o, lse
 
 
+def wide_attention_blocked(q, k, v, scale: float, kvalid=None, causal: bool = True, block: int = 64,
+                           with_bound: bool = False):
+    """_wide_fwd (wide_attention.py:13-67) step by step in fp32, one key block of `block` keys at a time:
+    s = (q.k) * scale * log2(e) with masked keys at -inf (:46-53), m_new = max(m, rowmax s) (:54), m_safe = 0 where
+    m_new = -inf (:55), p = exp2(s - m_safe) (:56), alpha = exp2(m - m_safe) (:57), l = l alpha + sum p (:58),
+    acc = acc alpha + bf16(p) @ v (:60, p.to(v.dtype) with bf16 v), out = acc / (l or 1) (:62), lse =
+    (m + log2 l) ln 2 (:66). The kernel under test runs the same blocking (64 keys), so the bf16 rounding of p
+    happens against the same running max. Returns (o (B,H,T,Dv) fp32, lse (B,H,T) fp32) and, with with_bound,
+    the per-element bound 2^-7 (sum_j p_j |v_j|) / l on how far an implementation of the same algorithm can move
+    when each bf16(p_j) lands on the neighbouring bf16 value (one ulp, at most 2^-7 p_j), e.g. because its exp2
+    differs in the last bit."""
+    B, H, T, _ = q.shape
+    G, S, Dv = k.shape[1], k.shape[2], v.shape[-1]
+    rep = H // G
+    assert H % G == 0 and v.shape[2] == S
+    qf = _f(q, torch.float32)
+    kf = _f(k, torch.float32).repeat_interleave(rep, 1)
+    vb = _f(v, torch.float32).repeat_interleave(rep, 1)
+    c = scale * 1.4426950408889634
+    pos = torch.arange(T)[:, None] + (S - T)
+    m = torch.full((B, H, T), NEG_INF)
+    l_ = torch.zeros(B, H, T)
+    acc = torch.zeros(B, H, T, Dv)
+    acc_abs = torch.zeros(B, H, T, Dv)
+    for n0 in range(0, S, block):
+        n1 = min(S, n0 + block)
+        s = torch.einsum("bhtd,bhsd->bhts", qf, kf[:, :, n0:n1]) * c
+        ok = torch.ones(T, n1 - n0, dtype=torch.bool)
+        if causal:
+            ok = torch.arange(n0, n1)[None, :] <= pos
+        okb = ok[None, None].expand(B, H, T, n1 - n0)
+        if kvalid is not None:
+            okb = okb & _f(kvalid[:, n0:n1], torch.bool)[:, None, None, :]
+        s = torch.where(okb, s, torch.full_like(s, NEG_INF))
+        m_new = torch.maximum(m, s.amax(-1))
+        m_safe = torch.where(m_new == NEG_INF, torch.zeros_like(m_new), m_new)
+        p = torch.exp2(s - m_safe[..., None])
+        alpha = torch.exp2(m - m_safe)
+        l_ = l_ * alpha + p.sum(-1)
+        acc = acc * alpha[..., None] + p.to(torch.bfloat16).float() @ vb[:, :, n0:n1]
+        if with_bound:
+            acc_abs = acc_abs * alpha[..., None] + p @ vb[:, :, n0:n1].abs()
+        m = m_new
+    den = torch.where(l_ == 0, torch.ones_like(l_), l_)[..., None]
+    out = acc / den
+    lse = (m + torch.log2(l_)) * 0.6931471805599453
+    if with_bound:
+        return out, lse, 2.0 ** -7 * acc_abs / den
+    return out, lse
+
+
 def lse_merge(o_p, l_p, o_o, l_o):
     """The exact merge of two softmax partials (prefix_attn.py:74-76): m = max(l_p, l_o), w = exp(l - m),
     out = (o_p w_p + o_o w_o) / (w_p + w_o). Both parts empty -> 0 output. Returns (out, merged lse)."""

@@ -32,7 +32,9 @@ def error_stats(out: torch.Tensor, ref: torch.Tensor) -> dict:
     }
 
 
-def assert_close_rel(out: torch.Tensor, ref: torch.Tensor, rel: float = REL, what: str = "") -> dict:
+def assert_close_rel(out: torch.Tensor, ref: torch.Tensor, rel: float = REL, what: str = "", elem_steps: int = 1) -> dict:
+    """The three forms above; elem_steps widens the elementwise form to that many bf16 steps of |ref| (used where
+    the algorithm itself rounds an intermediate to bf16, so a last-bit difference upstream can flip that rounding)."""
     out, ref = out.detach().double().cpu(), ref.detach().double().cpu()
     assert out.shape == ref.shape, (what, out.shape, ref.shape)
     assert torch.isfinite(out).all(), f"{what}: non-finite values"
@@ -44,6 +46,6 @@ def assert_close_rel(out: torch.Tensor, ref: torch.Tensor, rel: float = REL, wha
         st["worst_slice_norm_rel"] = per.max().item()
         assert st["worst_slice_norm_rel"] <= rel, f"{what}: a slice along dim 0 is beyond {rel}: {st}"
     rms = ref.pow(2).mean().sqrt()
-    bad = (out - ref).abs() > BF16_STEP * ref.abs() + rel * rms
-    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond 2^-8|ref| + {rel} rms: {st}"
+    bad = (out - ref).abs() > elem_steps * BF16_STEP * ref.abs() + rel * rms
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond {elem_steps} x 2^-8|ref| + {rel} rms: {st}"
     return st

@@ -124,3 +124,51 @@ def test_bf16_dequant_is_the_reference_materialize():
     exp = (kq.to(torch.bfloat16) * ks[..., None].to(torch.bfloat16)).float()
     assert torch.equal(got, exp)
     assert torch.equal(oa.dequant_state(kq, ks, "fp32"), kq.float() * ks[..., None])
+
+
+# ---- wide_attention_blocked (the reference kernel's arithmetic, step by step)
+
+def test_wide_blocked_pinned_by_exact_attention():
+    """The blocked restatement differs from exact attention only by p's bf16 rounding: its LSE (a sum of unrounded
+    p) matches the exact LSE to fp32 accuracy, and its output is within the bf16 rounding of p. A dropped rescale,
+    a wrong causal offset or a missed mask moves either far beyond these bounds."""
+    g = torch.Generator().manual_seed(0)
+    B, H, G, T, S, DK, DV = 2, 4, 2, 37, 150, 40, 24
+    q = torch.randn(B, H, T, DK, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, G, S, DK, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, G, S, DV, generator=g).to(torch.bfloat16)
+    kv = torch.ones(B, S, dtype=torch.bool)
+    kv[1, :50] = False
+    for causal in (True, False):
+        ob, lb, bound = oa.wide_attention_blocked(q, k, v, DK ** -0.5, kv, causal=causal, block=64, with_bound=True)
+        oe, le = oa.attention(q, k, v, DK ** -0.5, kv, causal=causal)
+        # rounding p to bf16 moves it by at most half an ulp, i.e. half the one-ulp flip bound
+        assert ((ob - oe).abs() <= bound / 2 + 1e-6).all()
+        fin = torch.isfinite(le)
+        assert torch.equal(torch.isfinite(lb), fin)
+        assert (lb[fin] - le[fin]).abs().max().item() < 1e-5
+        assert ((ob - oe).norm() / oe.norm()).item() < 2e-3
+        assert (ob - oe).abs().max().item() < 2e-2
+
+
+def test_wide_blocked_matches_brute_force_on_tiny_case():
+    g = torch.Generator().manual_seed(1)
+    T, S, D = 3, 7, 8
+    q = torch.randn(1, 1, T, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 1, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, 1, S, D, generator=g).to(torch.bfloat16)
+    kv = torch.tensor([[True, False, True, True, True, True, False]])
+    allowed = [[kv[0, j].item() and j <= i + S - T for j in range(S)] for i in range(T)]
+    ref, lref = oa.brute_force_attention(q[0, 0], k[0, 0], v[0, 0], D ** -0.5, allowed)
+    ob, lb = oa.wide_attention_blocked(q, k, v, D ** -0.5, kv, causal=True, block=2)
+    assert (lb[0, 0].double() - lref).abs().max().item() < 1e-5
+    assert (ob[0, 0].double() - ref).abs().max().item() < 1e-2 * ref.abs().max().item()
+
+
+def test_wide_blocked_empty_rows():
+    q = torch.randn(1, 2, 4, 8).to(torch.bfloat16)
+    k = torch.randn(1, 1, 5, 8).to(torch.bfloat16)
+    v = torch.randn(1, 1, 5, 8).to(torch.bfloat16)
+    kv = torch.zeros(1, 5, dtype=torch.bool)
+    ob, lb = oa.wide_attention_blocked(q, k, v, 0.3, kv, causal=False)
+    assert torch.count_nonzero(ob).item() == 0 and torch.isneginf(lb).all()
