@@ -4,7 +4,10 @@ option-row attention is the branched kernel over int8 state K/V, with the option
 This is the backbone stand-in that carries the path (the reference runs the same per-layer steps inside HF Qwen3.5
 modules: the W8A8 linears in every nn.Linear slot, src/opendecider/prefix_attn.py:79-131 for the attention layer,
 option logits + 'none' in src/opendecider/v3.py:639-643,701-709 and the softmax in src/opendecider/decider.py:255-257).
-Per layer, for the M = rows x tokens option-row tokens:
+State prefill (prefill): the same layer with causal wide_attention over the new tokens' bf16 K/V (or, for a record
+appended to a cached state, the branched kernel over the int8 cache + the record's own tokens), the new K/V quantized
+into per-layer int8 caches by od_kv_quant_append. Scoring (score), per layer, for the M = rows x tokens option-row
+tokens:
     od_rmsnorm_quant -> od_w8a8_gemm (QKV) -> od_qk_norm_rope -> od_branched_attn -> od_act_quant
     -> od_w8a8_gemm (O, + residual) -> od_rmsnorm_quant -> od_w8a8_gemm (gate+up) -> od_silu_mul_quant
     -> od_w8a8_gemm (down, + residual)
@@ -112,7 +115,7 @@ class DenseDecoder:
         self.embed = None if embed is None else embed.to(self.dev)
         cos, sin = rope_tables(cfg, max_pos)
         self.cos, self.sin = cos.to(self.dev), sin.to(self.dev)
-        self._ws = None
+        self._ws = {}
 
     def add_layer(self, lw: dict) -> None:
         L = {k: lw[k].to(self.dev) for k in ("ln1", "ln2", "q_norm", "k_norm")}
@@ -122,12 +125,13 @@ class DenseDecoder:
 
     # ---------------------------------------------------------------- buffers
     def workspace(self, M: int):
-        if self._ws is not None and self._ws["M"] == M:
-            return self._ws
+        """Activation buffers for M tokens (kept per M: a decision runs a state prefill and the option rows)."""
+        if M in self._ws:
+            return self._ws[M]
         cfg, d = self.cfg, self.dev
         bf = torch.bfloat16
         kmax = max(cfg.hidden, cfg.ffn, cfg.n_heads * cfg.head_dim)
-        self._ws = {
+        self._ws[M] = {
             "M": M,
             "h": [torch.empty(M, cfg.hidden, dtype=bf, device=d) for _ in range(2)],
             "xq": torch.empty(M, (kmax + 15) // 16 * 16, dtype=torch.int8, device=d),
@@ -136,34 +140,97 @@ class DenseDecoder:
             "attn": torch.empty(M, cfg.n_heads * cfg.head_dim, dtype=bf, device=d),
             "gu": torch.empty(M, 2 * cfg.ffn, dtype=bf, device=d),
         }
-        return self._ws
+        return self._ws[M]
+
+    def new_state_caches(self, batch: int, capacity: int) -> list:
+        """Empty per-layer (K, V) int8 caches for `batch` states of up to `capacity` tokens."""
+        cfg = self.cfg
+        return [(Int8KVCache(batch, cfg.n_kv_heads, cfg.head_dim, capacity, self.dev),
+                 Int8KVCache(batch, cfg.n_kv_heads, cfg.head_dim, capacity, self.dev)) for _ in self.layers]
 
     # ---------------------------------------------------------------- forward
-    def layer(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict, state_k: Int8KVCache,
-              state_v: Int8KVCache, R: int, t: int, pos: torch.Tensor, row_start, max_rows: int, kvalid=None):
+    def _attn_in(self, li: int, h: torch.Tensor, ws: dict, pos: torch.Tensor) -> torch.Tensor:
+        """RMSNorm + quantize, W8A8 QKV GEMM, q/k norm + RoPE (in place): the layer's qkv (M, qkv_out) bf16."""
         cfg, L = self.cfg, self.layers[li]
+        kernels.rmsnorm_quant(h, L["ln1"], cfg.eps, L["qkv"].inv_s, ws["xq"][:, :cfg.hidden], ws["sx"])
+        qkv = kernels.w8a8_gemm(ws["xq"][:, :cfg.hidden], ws["sx"], L["qkv"].q, L["qkv"].scale, out=ws["qkv"])
+        kernels.qk_norm_rope(qkv, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, L["q_norm"], L["k_norm"], self.cos,
+                             self.sin, pos, cfg.eps)
+        return qkv
+
+    def _heads(self, qkv: torch.Tensor, ws: dict, R: int, t: int):
+        """(R, heads, t, D) views of q, k, v in the qkv buffer and of the attention output buffer."""
+        cfg = self.cfg
         D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
-        M = h.shape[0]
-        xq, sx = ws["xq"], ws["sx"]
-        # attention block
-        kernels.rmsnorm_quant(h, L["ln1"], cfg.eps, L["qkv"].inv_s, xq[:, :cfg.hidden], sx)
-        qkv = kernels.w8a8_gemm(xq[:, :cfg.hidden], sx, L["qkv"].q, L["qkv"].scale, out=ws["qkv"])
-        kernels.qk_norm_rope(qkv, Hq, Hk, D, L["q_norm"], L["k_norm"], self.cos, self.sin, pos, cfg.eps)
         q = qkv[:, :Hq * D].view(R, t, Hq, D).transpose(1, 2)
         k = qkv[:, Hq * D:(Hq + Hk) * D].view(R, t, Hk, D).transpose(1, 2)
         v = qkv[:, (Hq + Hk) * D:].view(R, t, Hk, D).transpose(1, 2)
         attn = ws["attn"].view(R, t, Hq, D).transpose(1, 2)
-        T = state_k.length
-        kernels.branched_attn(q, k, v, state_k.q, state_k.scale, state_v.q, state_v.scale, D ** -0.5, kvalid=kvalid,
-                              length=T, out=attn, row_start=row_start, max_rows=max_rows)
-        kernels.act_quant(ws["attn"], L["o"].inv_s, xq=xq[:, :Hq * D], sx=sx)
-        kernels.w8a8_gemm(xq[:, :Hq * D], sx, L["o"].q, L["o"].scale, residual=h, out=h_out)
-        # MLP block
+        return q, k, v, attn
+
+    def _attn_out_mlp(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict) -> torch.Tensor:
+        """Quantize the attention output, W8A8 O GEMM + residual (into h_out), RMSNorm + quantize, gate+up GEMM,
+        SwiGLU + quantize, down GEMM + residual (back into h)."""
+        cfg, L = self.cfg, self.layers[li]
+        xq, sx = ws["xq"], ws["sx"]
+        hd = cfg.n_heads * cfg.head_dim
+        kernels.act_quant(ws["attn"], L["o"].inv_s, xq=xq[:, :hd], sx=sx)
+        kernels.w8a8_gemm(xq[:, :hd], sx, L["o"].q, L["o"].scale, residual=h, out=h_out)
         kernels.rmsnorm_quant(h_out, L["ln2"], cfg.eps, L["gu"].inv_s, xq[:, :cfg.hidden], sx)
         gu = kernels.w8a8_gemm(xq[:, :cfg.hidden], sx, L["gu"].q, L["gu"].scale, out=ws["gu"])
         kernels.silu_mul_quant(gu, cfg.ffn, L["down"].inv_s, xq=xq[:, :cfg.ffn], sx=sx)
         kernels.w8a8_gemm(xq[:, :cfg.ffn], sx, L["down"].q, L["down"].scale, residual=h_out, out=h)
-        return h  # the layer's output is written back into h (h_out held the mid-layer residual)
+        return h
+
+    def layer(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict, state_k: Int8KVCache,
+              state_v: Int8KVCache, R: int, t: int, pos: torch.Tensor, row_start, max_rows: int, kvalid=None):
+        """One layer over R option rows of t tokens that attend their state's int8 K/V and themselves."""
+        D = self.cfg.head_dim
+        qkv = self._attn_in(li, h, ws, pos)
+        q, k, v, attn = self._heads(qkv, ws, R, t)
+        kernels.branched_attn(q, k, v, state_k.q, state_k.scale, state_v.q, state_v.scale, D ** -0.5, kvalid=kvalid,
+                              length=state_k.length, out=attn, row_start=row_start, max_rows=max_rows)
+        return self._attn_out_mlp(li, h, h_out, ws)  # the output goes back into h (h_out held the mid residual)
+
+    def prefill_layer(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict, cache_k: Int8KVCache,
+                      cache_v: Int8KVCache, B: int, S: int, pos: torch.Tensor, kvalid=None, row_start=None):
+        """One layer over S new state tokens of each of B states, appended after the cache's current n0 tokens.
+        n0 = 0: causal attention among the new tokens on bf16 K/V (wide_attention), as the backbone's state pass.
+        n0 > 0 (an appended record, S <= 256): the new tokens attend the cached int8 state and themselves causally
+        (the branched kernel with one row per state). Then only the new tokens' K/V are quantized and appended
+        (state_cache.py:79)."""
+        D = self.cfg.head_dim
+        qkv = self._attn_in(li, h, ws, pos)
+        q, k, v, attn = self._heads(qkv, ws, B, S)
+        n0 = cache_k.length
+        if n0 == 0:
+            kernels.wide_attn(q, k, v, D ** -0.5, kvalid=kvalid, causal=True, out=attn)
+        else:
+            if S > 256:
+                raise ValueError(f"prefill: an appended record of {S} tokens exceeds 256 (append it in pieces)")
+            rs, mr = (None, B) if B == 1 else (row_start, B)
+            kernels.branched_attn(q, k, v, cache_k.q, cache_k.scale, cache_v.q, cache_v.scale, D ** -0.5,
+                                  kvalid=kvalid, length=n0, out=attn, row_start=rs, max_rows=mr)
+        cache_k.append(k)
+        cache_v.append(v)
+        return self._attn_out_mlp(li, h, h_out, ws)
+
+    def prefill(self, ids: torch.Tensor, caches: list, kvalid=None) -> torch.Tensor:
+        """ids (B, S) state token ids on the GPU, appended to the B states held in caches[l] = (K, V) (all layers at
+        the same length n0). kvalid: (B, S) key mask of the new tokens (first prefill) or (B, n0) of the cached
+        ones (an appended record). Returns the new tokens' final hidden states (B S, hidden)."""
+        B, S = ids.shape
+        n0 = caches[0][0].length
+        if n0 + S > self.cos.shape[0]:
+            raise ValueError(f"positions up to {n0 + S} exceed the rotary tables ({self.cos.shape[0]})")
+        ws = self.workspace(B * S)
+        h, mid = ws["h"]
+        h.copy_(self.embed.index_select(0, ids.reshape(-1)))
+        pos = (n0 + torch.arange(S, dtype=torch.int32)).repeat(B).to(self.dev)
+        row_start = kernels.row_start_of([1] * B, self.dev)[0] if (n0 > 0 and B > 1) else None
+        for li in range(len(self.layers)):
+            self.prefill_layer(li, h, mid, ws, caches[li][0], caches[li][1], B, S, pos, kvalid, row_start)
+        return h
 
     def rows_forward(self, h0: torch.Tensor, states: list, R: int, t: int, pos: torch.Tensor, row_start, max_rows,
                      kvalid=None) -> torch.Tensor:

@@ -115,6 +115,20 @@ def swiglu(gu: torch.Tensor, F: int) -> torch.Tensor:
     return torch.nn.functional.silu(gu[:, :F]) * gu[:, F:]
 
 
+def _layer_tail(h, attn, qlin, lw, cfg: DecoderConfig):
+    """O projection + residual, RMSNorm, gate+up, SwiGLU, down + residual (each linear W8A8 with its fused
+    activation quantizer)."""
+    q, sw, inv = qlin["wo"]
+    h, _, _, _ = oq.w8a8_linear(attn, q, sw, inv_s=inv, residual=h)
+    x = rmsnorm(h, lw["ln2"], cfg.eps)
+    q, sw, inv = qlin["wgu"]
+    gu, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
+    a = swiglu(gu, cfg.ffn)
+    q, sw, inv = qlin["wdown"]
+    h, _, _, _ = oq.w8a8_linear(a, q, sw, inv_s=inv, residual=h)
+    return h
+
+
 def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: int, pos, cos, sin,
                   row_state=None, kvalid=None, attn_hook=None):
     """One decoder layer over the option-row tokens h (M = R * t, hidden) bf16. qlin: {name: (q, sw, inv_s)}.
@@ -133,15 +147,50 @@ def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: 
     attn = o.to(torch.bfloat16).transpose(1, 2).reshape(R * t, Hq * D)
     if attn_hook is not None:
         attn = attn_hook(attn)
-    q, sw, inv = qlin["wo"]
-    h, _, _, _ = oq.w8a8_linear(attn, q, sw, inv_s=inv, residual=h)
-    x = rmsnorm(h, lw["ln2"], cfg.eps)
-    q, sw, inv = qlin["wgu"]
-    gu, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
-    a = swiglu(gu, cfg.ffn)
-    q, sw, inv = qlin["wdown"]
-    h, _, _, _ = oq.w8a8_linear(a, q, sw, inv_s=inv, residual=h)
-    return h
+    return _layer_tail(h, attn, qlin, lw, cfg)
+
+
+def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: int = 0, kvalid=None,
+                    attn_hook=None):
+    """State pass over S new tokens of each of B states (ids (B, S)) appended after n0 cached tokens.
+    n0 = 0: causal attention among the new tokens on their bf16 K/V (exact softmax attention, the contract of the
+    backbone's attention on the state, wide_attention.py:70-91). n0 > 0: the new tokens attend the cached int8 state
+    (state_kv[l] = ((kq, ks), (vq, vs)) of length n0) and themselves causally, merged by LSE (one row per state,
+    prefix_attn.py:43-76). Then only the new tokens' K/V are quantized per (token, head) and appended
+    (state_cache.py:79, quant.py:36-41). Returns (h (B S, hidden) bf16, the per-layer state K/V of length n0 + S)."""
+    B, S = ids.shape
+    D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    h = embed[ids.reshape(-1)]
+    pos = (n0 + torch.arange(S)).repeat(B)
+    cos, sin = rope_tables(cfg, n0 + S)
+    out_kv = []
+    for li, lw in enumerate(weights["layers"]):
+        qlin = quantize_layer(lw)
+        x = rmsnorm(h, lw["ln1"], cfg.eps)
+        q, sw, inv = qlin["wqkv"]
+        qkv, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
+        qkv = qk_norm_rope(qkv, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
+        qh = qkv[:, :Hq * D].reshape(B, S, Hq, D).transpose(1, 2)
+        kh = qkv[:, Hq * D:(Hq + Hk) * D].reshape(B, S, Hk, D).transpose(1, 2)
+        vh = qkv[:, (Hq + Hk) * D:].reshape(B, S, Hk, D).transpose(1, 2)
+        if n0 == 0:
+            o, _ = oa.attention(qh, kh, vh, D ** -0.5, kvalid, causal=True)
+        else:
+            (kq, ks), (vq, vs) = state_kv[li]
+            o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, kvalid, torch.arange(B))
+        attn = o.to(torch.bfloat16).transpose(1, 2).reshape(B * S, Hq * D)
+        if attn_hook is not None:
+            attn = attn_hook(attn)
+        kq_new, ks_new = oq.quantize_rows(kh.contiguous())
+        vq_new, vs_new = oq.quantize_rows(vh.contiguous())
+        ks_new, vs_new = ks_new[..., 0], vs_new[..., 0]
+        if n0 > 0:
+            (kq, ks), (vq, vs) = state_kv[li]
+            kq_new, ks_new = torch.cat([kq, kq_new], 2), torch.cat([ks, ks_new], 2)
+            vq_new, vs_new = torch.cat([vq, vq_new], 2), torch.cat([vs, vs_new], 2)
+        out_kv.append(((kq_new, ks_new), (vq_new, vs_new)))
+        h = _layer_tail(h, attn, qlin, lw, cfg)
+    return h, out_kv
 
 
 def quantize_layer(lw):

@@ -188,3 +188,66 @@ def test_decision_forward_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, T):
     perm = torch.randperm(n_opt, generator=torch.Generator().manual_seed(6))
     lp_p = dec.score(ids[:, perm].to(DEV), gs)
     assert (lp_p[:, :n_opt].exp() - lp[:, perm.to(DEV)].exp()).abs().max().item() <= 1e-6
+
+
+PREFILL_CASES = [
+    ("tiny_d64", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500), 2, 5, 4, 70,
+     [24, 7]),
+    ("9b_dims_2_layers", dict(n_layers=2, vocab=1000), 2, 6, 16, 256, [256]),
+]
+
+
+def _prefill_setup(cfg_kw, B, S, cap):
+    from opendecider_amd.decoder import DecoderConfig, DenseDecoder
+    cfg = od.DecoderConfig(**cfg_kw)
+    w = od.make_weights(cfg, seed=7)
+    emb = od.make_embedding(cfg, seed=7)
+    dec = DenseDecoder(DecoderConfig(**cfg_kw), w, emb, DEV, max_pos=cap + 64)
+    return cfg, w, emb, dec
+
+
+@pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,S,records", PREFILL_CASES)
+def test_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, S, records):
+    """The decision forward from token ids: the states are prefilled through every layer (causal wide_attention on
+    the new tokens' bf16 K/V, K/V quantized into per-layer int8 caches), then records are appended (each attends
+    the int8 cache + itself, and only its K/V are quantized and appended), then the option rows are scored.
+    Layer-0 cache bytes are held to the row-kernel bar (one int8 step, few bytes off); the probabilities to the
+    oracle's own sensitivity to rounding-size perturbations of every attention output (prefill and rows), never
+    above 1e-2."""
+    cap = S + sum(records)
+    cfg, w, emb, dec = _prefill_setup(cfg_kw, B, S, cap)
+    g = torch.Generator().manual_seed(8)
+    ids_state = torch.randint(0, cfg.vocab, (B, S), generator=g)
+    recs = [torch.randint(0, cfg.vocab, (B, n), generator=g) for n in records]
+    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g)
+    print(f"{name}: prefill B={B} S={S} records={records}", flush=True)
+
+    caches = dec.new_state_caches(B, cap)
+    dec.prefill(ids_state.to(DEV), caches)
+    torch.cuda.synchronize()
+    _, kv_ref = od.prefill_forward(ids_state, w, emb, cfg)
+    for (kc, vc), ((kq, ks), (vq, vs)) in zip(caches[:1], kv_ref[:1]):
+        _close_quant(kc.q[:, :, :S].reshape(-1, cfg.head_dim), kc.scale[:, :, :S].reshape(-1),
+                     kq.reshape(-1, cfg.head_dim), ks.reshape(-1))
+        _close_quant(vc.q[:, :, :S].reshape(-1, cfg.head_dim), vc.scale[:, :, :S].reshape(-1),
+                     vq.reshape(-1, cfg.head_dim), vs.reshape(-1))
+    n0 = S
+    for r in recs:
+        dec.prefill(r.to(DEV), caches)
+        _, kv_ref = od.prefill_forward(r, w, emb, cfg, state_kv=kv_ref, n0=n0)
+        n0 += r.shape[1]
+    assert all(kc.length == n0 and vc.length == n0 for kc, vc in caches)
+    lp = dec.score(ids.to(DEV), caches)
+    ref = od.decision_forward(ids, w, emb, cfg, kv_ref, n0)
+
+    hook = lambda a: od.nudge_bf16(a, 0.10, 17)
+    _, kv_n = od.prefill_forward(ids_state, w, emb, cfg, attn_hook=hook)
+    m = S
+    for r in recs:
+        _, kv_n = od.prefill_forward(r, w, emb, cfg, state_kv=kv_n, n0=m, attn_hook=hook)
+        m += r.shape[1]
+    nudged = od.decision_forward(ids, w, emb, cfg, kv_n, n0, attn_hook=hook)
+    dp = (lp.exp().cpu() - ref.exp()).abs().max().item()
+    dp_nudge = (nudged.exp() - ref.exp()).abs().max().item()
+    print(f"{name}: max |dp| GPU vs oracle {dp:.2e}; oracle vs nudged oracle {dp_nudge:.2e}")
+    assert dp <= max(3 * dp_nudge, PROB_ABS) and dp <= 1e-2

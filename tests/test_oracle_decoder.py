@@ -6,6 +6,7 @@ import math
 import torch
 
 from oracle import decoder as od
+from oracle import quant as oq
 
 
 def test_rmsnorm_matches_float64_within_bf16_rounding():
@@ -110,3 +111,55 @@ def test_decision_forward_is_option_order_invariant():
     assert (lp_p[:, :n_opt] - lp[:, perm]).abs().max().item() <= 1e-6
     assert (lp_p[:, n_opt] - lp[:, n_opt]).abs().max().item() <= 1e-6
     assert torch.allclose(lp.exp().sum(-1), torch.ones(B), atol=1e-5)
+
+
+# ---- state prefill (prefill_forward)
+
+def _tiny():
+    cfg = od.DecoderConfig(hidden=64, ffn=128, n_heads=4, n_kv_heads=2, head_dim=16, n_layers=2, vocab=97)
+    return cfg, od.make_weights(cfg, seed=11), od.make_embedding(cfg, seed=11)
+
+
+def test_prefill_is_causal():
+    """A state token's hidden state depends only on the tokens before it: prefilling a prefix of the ids gives the
+    same hidden states for that prefix as prefilling all of them."""
+    cfg, w, emb = _tiny()
+    ids = torch.randint(0, cfg.vocab, (2, 20), generator=torch.Generator().manual_seed(1))
+    h_all, kv_all = od.prefill_forward(ids, w, emb, cfg)
+    h_pre, kv_pre = od.prefill_forward(ids[:, :13], w, emb, cfg)
+    hs = h_all.reshape(2, 20, -1)[:, :13].reshape(26, -1)
+    assert ((hs.float() - h_pre.float()).abs() <= 1e-2 * h_pre.float().abs().max()).all()
+    for (k1, _), (k2, _) in zip(kv_all, kv_pre):
+        d = (k1[0][:, :, :13].int() - k2[0].int()).abs()
+        assert d.max().item() <= 1 and (d > 0).float().mean().item() < 0.01
+
+
+def test_prefill_append_keeps_cache_and_positions():
+    """An appended record leaves the cached tokens' bytes untouched, grows every layer's cache by the record's
+    length, and its layer-0 keys are the ones computed at positions n0 .. n0 + S - 1 (RoPE continues the state)."""
+    cfg, w, emb = _tiny()
+    g = torch.Generator().manual_seed(2)
+    ids0 = torch.randint(0, cfg.vocab, (2, 17), generator=g)
+    rec = torch.randint(0, cfg.vocab, (2, 9), generator=g)
+    _, kv0 = od.prefill_forward(ids0, w, emb, cfg)
+    _, kv1 = od.prefill_forward(rec, w, emb, cfg, state_kv=kv0, n0=17)
+    for ((kq0, ks0), (vq0, vs0)), ((kq1, ks1), (vq1, vs1)) in zip(kv0, kv1):
+        assert kq1.shape[2] == 26 and vs1.shape[2] == 26
+        assert torch.equal(kq1[:, :, :17], kq0) and torch.equal(vq1[:, :, :17], vq0)
+        assert torch.equal(ks1[:, :, :17], ks0) and torch.equal(vs1[:, :, :17], vs0)
+    # layer 0 keys of the record, recomputed directly at positions 17 .. 25
+    lw = w["layers"][0]
+    ql = od.quantize_layer(lw)
+    x = od.rmsnorm(emb[rec.reshape(-1)], lw["ln1"], cfg.eps)
+    qkv, _, _, _ = oq.w8a8_linear(x, ql["wqkv"][0], ql["wqkv"][1], inv_s=ql["wqkv"][2])
+    cos, sin = od.rope_tables(cfg, 26)
+    qkv = od.qk_norm_rope(qkv, cfg, lw["q_norm"], lw["k_norm"], cos, sin, (17 + torch.arange(9)).repeat(2))
+    D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    k = qkv[:, Hq * D:(Hq + Hk) * D].reshape(2, 9, Hk, D).transpose(1, 2).contiguous()
+    kq, ks = oq.quantize_rows(k)
+    assert torch.equal(kv1[0][0][0][:, :, 17:], kq)
+    # and they differ from keys rotated as if the record started at position 0
+    qkv0 = od.qk_norm_rope(oq.w8a8_linear(x, ql["wqkv"][0], ql["wqkv"][1], inv_s=ql["wqkv"][2])[0], cfg,
+                           lw["q_norm"], lw["k_norm"], cos, sin, torch.arange(9).repeat(2))
+    k0 = qkv0[:, Hq * D:(Hq + Hk) * D].reshape(2, 9, Hk, D).transpose(1, 2).contiguous()
+    assert not torch.equal(oq.quantize_rows(k0)[0], kq)
