@@ -8,7 +8,7 @@ q/k norm + RoPE, branched attention over the int8 state + own tokens, W8A8 O GEM
 W8A8 gate+up GEMM, SwiGLU+quantize, W8A8 down GEMM (+residual). The states' K/V are synthetic (bf16 N(0,1)
 quantized by the append kernel) and resident in HBM before timing; so are the option token ids.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--workload scoring|decision|wide_choice]
 
 Prints ONE JSON line: metric / value (decisions/s) / timing, the roofline of the dominant kernel (the W8A8 GEMM,
 int8 MFMA), the branched attention's figures, and a CPU baseline (the oracle, on this host's cores, on a bounded
@@ -41,6 +41,11 @@ def parse():
     ap.add_argument("--options", type=int, default=32)
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--state", type=int, default=2048)
+    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice"], default="scoring",
+                    help="scoring (default): the metric's option-row scoring pass over cached 2048-token states; "
+                         "decision: full decision forward from token ids (4 requests, 4096-token states prefilled, "
+                         "64 options x 24 tokens); wide_choice: a 32768-token int8 state growing by 256-token "
+                         "records, 2 requests x 255 options x 12 tokens scored after each record")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-repeats", type=int, default=3)
     return ap.parse_args()
@@ -132,6 +137,163 @@ def cpu_baseline(args):
                        f"scaled x{args.layers} layers")}
 
 
+def wide_work(q, k, v, scale, kvalid=None, causal=True, return_lse=False, out=None):
+    B, H, T, DK = q.shape
+    G, S, DV = k.shape[1], k.shape[2], v.shape[-1]
+    pairs = B * H * (T * S - (T * (T - 1) // 2 if causal and T == S else 0))
+    return (2 * pairs * (DK + DV), 2 * (q.numel() + k.numel() + v.numel() + B * H * T * DV))
+
+
+def append_work(x, q_cache, s_cache, n0):
+    return (x.numel(), x.numel() * 2 + x.numel() + x.shape[0] * x.shape[1] * x.shape[2] * 4)
+
+
+def _gemm_roofline(gemm_t):
+    n_g, ms_g, (ops_g, _) = gemm_t.summary()
+    tops = ops_g / (ms_g * 1e-3) / 1e12 if n_g else 0.0
+    return {"kernel": "od_w8a8_gemm", "bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+            "frac": tops / INT8_PEAK_TOPS, "traffic": None, "launches": n_g,
+            "avg_launch_us": ms_g / max(n_g, 1) * 1e3}, ms_g
+
+
+def run_decision(args):
+    """Full decision forward from token ids: 4 requests, each a 4096-token state prefilled through the 36 layers
+    (causal wide_attention, K/V quantized into int8 caches) and 64 options x 24 tokens scored against it."""
+    import torch
+
+    from opendecider_amd import decoder as dmod
+    from opendecider_amd import kernels
+    dev = "cuda:0"
+    cfg = dmod.DecoderConfig(n_layers=args.layers)
+    B, S, n_opt, t = 4, 4096, 64, 24
+    dec = dmod.random_decoder(cfg, seed=0, device=dev, max_pos=S + t + 16)
+    g = torch.Generator(device=dev).manual_seed(3)
+    ids_state = torch.randint(0, cfg.vocab, (B, S), generator=g, device=dev)
+    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g, device=dev)
+    caches = dec.new_state_caches(B, S)
+    gemm_t = KernelTimer(kernels.w8a8_gemm, gemm_work)
+    wide_t = KernelTimer(kernels.wide_attn, wide_work)
+    attn_t = KernelTimer(kernels.branched_attn, attn_work)
+    kernels.w8a8_gemm, kernels.wide_attn, kernels.branched_attn = gemm_t, wide_t, attn_t
+
+    def decide():
+        for kc, vc in caches:
+            kc.length = vc.length = 0
+        dec.prefill(ids_state, caches)
+        return dec.score(ids, caches)
+
+    for _ in range(args.warmup):
+        out = decide()
+    torch.cuda.synchronize()
+    gemm_t.active = wide_t.active = attn_t.active = True
+    lat = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        out = decide()
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t0)
+    gemm_t.active = wide_t.active = attn_t.active = False
+    assert torch.isfinite(out).all(), "non-finite log-probabilities"
+    lat_sorted = sorted(lat)
+    p50 = lat_sorted[len(lat) // 2]
+    roof, ms_g = _gemm_roofline(gemm_t)
+    n_w, ms_w, (fl_w, _) = wide_t.summary()
+    n_a, ms_a, (fl_a, by_a) = attn_t.summary()
+    tot_ms = sum(lat) * 1e3
+    return {
+        "metric": "decisions/sec (config 3: 4096-token states prefilled from ids, 64 options x 24 tokens, 9B dims)",
+        "value": B / p50, "unit": "decisions/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": sum(lat) / len(lat) * 1e3, "p50_latency_ms": p50 * 1e3,
+        "p90_latency_ms": lat_sorted[min(len(lat) - 1, int(0.9 * len(lat)))] * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": (f"full decision forward: {B} requests, {S}-token states of random ids prefilled "
+                                f"through {cfg.n_layers} layers, {n_opt} options x {t} tokens scored, 'none' "
+                                "appended; 9B dims, random init"),
+                   "requests": B, "state_tokens": S, "options": n_opt, "tokens_per_option": t,
+                   "layers": cfg.n_layers},
+        "roofline": roof,
+        "state_attention": {"kernel": "od_wide_attn (causal)", "tflops": fl_w / (ms_w * 1e-3) / 1e12 if n_w else 0,
+                            "frac_of_bf16_mfma": fl_w / (ms_w * 1e-3) / 1e12 / BF16_PEAK_TFLOPS if n_w else 0,
+                            "launches": n_w, "avg_launch_us": ms_w / max(n_w, 1) * 1e3},
+        "row_attention": {"kernel": "od_branched_attn", "tflops": fl_a / (ms_a * 1e-3) / 1e12 if n_a else 0,
+                          "algorithmic_gbs": by_a / (ms_a * 1e-3) / 1e9 if n_a else 0, "launches": n_a},
+        "time_share": {"gemm": ms_g / tot_ms, "state_attention": ms_w / tot_ms, "row_attention": ms_a / tot_ms},
+    }
+
+
+def run_wide_choice(args):
+    """A 32768-token shared state cached as int8 K/V (36 layers; synthetic bf16 N(0,1) K/V quantized by the append
+    kernel), grown by 8 records of 256 tokens (each prefilled through the decoder on top of the cache, only the new
+    K/V quantized and appended); after each record 2 requests x 255 options x 12 tokens are scored against it."""
+    import torch
+
+    from opendecider_amd import decoder as dmod
+    from opendecider_amd import kernels
+    dev = "cuda:0"
+    cfg = dmod.DecoderConfig(n_layers=args.layers)
+    S0, n_rec, rec, n_req, n_opt, t = 32768, 8, 256, 2, 255, 12
+    cap = S0 + n_rec * rec
+    dec = dmod.random_decoder(cfg, seed=0, device=dev, max_pos=cap + t + 16)
+    g = torch.Generator(device=dev).manual_seed(4)
+    caches = dec.new_state_caches(1, cap)
+    for kc, vc in caches:
+        for c in (kc, vc):
+            for j in range(0, S0, 8192):  # synthetic state K/V, quantized by the append kernel in pieces
+                c.append(torch.randn(1, cfg.n_kv_heads, 8192, cfg.head_dim, generator=g, device=dev)
+                         .to(torch.bfloat16))
+    records = [torch.randint(0, cfg.vocab, (1, rec), generator=g, device=dev) for _ in range(n_rec + args.warmup)]
+    ids = torch.randint(0, cfg.vocab, (1, n_req * n_opt, t), generator=g, device=dev)
+    app_t = KernelTimer(kernels.kv_quant_append, append_work)
+    attn_t = KernelTimer(kernels.branched_attn, attn_work)
+    kernels.kv_quant_append, kernels.branched_attn = app_t, attn_t
+    # warm-up: one record + one scoring pass, then rewind the caches
+    for i in range(args.warmup):
+        dec.prefill(records[n_rec + i], caches)
+        dec.score(ids, caches)
+        for kc, vc in caches:
+            kc.length = vc.length = S0
+    torch.cuda.synchronize()
+    rec_ms, score_ms = [], []
+    app_ms = []
+    for r in range(n_rec):
+        app_t.active = True
+        t0 = time.perf_counter()
+        dec.prefill(records[r], caches)
+        torch.cuda.synchronize()
+        rec_ms.append((time.perf_counter() - t0) * 1e3)
+        app_t.active = False
+        n_ap, ms_ap, _ = app_t.summary()
+        app_ms.append(ms_ap)
+        app_t.events, app_t.units = [], []
+        attn_t.active = True
+        t0 = time.perf_counter()
+        out = dec.score(ids, caches)
+        torch.cuda.synchronize()
+        score_ms.append((time.perf_counter() - t0) * 1e3)
+        attn_t.active = False
+    assert torch.isfinite(out).all(), "non-finite log-probabilities"
+    n_a, ms_a, (fl_a, by_a) = attn_t.summary()
+    gbs = by_a / (ms_a * 1e-3) / 1e9
+    return {
+        "metric": "attention HBM GB/s and append cost per record (config 4: 32k int8 state + 8 x 256-token records, "
+                  "2 x 255 options x 12 tokens)",
+        "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": n_rec, "warmup": args.warmup,
+        "ms_per_step": sum(rec_ms) / n_rec + sum(score_ms) / n_rec, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": (f"{S0}-token shared int8 state (36 layers) + {n_rec} records x {rec} tokens, "
+                                f"{n_req} requests x {n_opt} options x {t} tokens after each record; 9B dims"),
+                   "state_tokens": S0, "records": n_rec, "record_tokens": rec, "requests": n_req,
+                   "options": n_opt, "tokens_per_option": t, "layers": cfg.n_layers},
+        "attention": {"kernel": "od_branched_attn", "algorithmic_gbs": gbs, "frac_of_hbm": gbs / HBM_PEAK_GBS,
+                      "tflops": fl_a / (ms_a * 1e-3) / 1e12, "launches": n_a,
+                      "avg_launch_us": ms_a / max(n_a, 1) * 1e3},
+        "append_per_record": {"full_prefill_ms": sum(rec_ms) / n_rec,
+                              "kernel_only_us": sum(app_ms) / n_rec * 1e3,
+                              "kernel": "od_kv_quant_append (K and V, 36 layers)"},
+        "scoring_ms": sum(score_ms) / n_rec,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -139,6 +301,11 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     import torch
+    if args.workload != "scoring":
+        torch.cuda.set_device(0)
+        fn = run_decision if args.workload == "decision" else run_wide_choice
+        print(json.dumps(fn(args)))
+        return
 
     from opendecider_amd import decoder as dmod
     from opendecider_amd import kernels
