@@ -2,24 +2,29 @@
 // cores (V_MFMA_I32_32X32X32_I8), then the dequant epilogue out = bf16(float(acc) * sa[m] * sw[n] (+ bias)
 // (+ residual)).
 //
-// Tiling (MFMA-bound at the 9B shapes; one workgroup of 8 waves per CU):
-//   * workgroup tile BM x BN = 256 x {256 | 192}; K streams through LDS in 64-byte slabs, 4 stages deep
-//     (4 x (16 KB + BN * 64 B) <= 128 KB of the 160 KB LDS). Global -> LDS uses direct-to-LDS buffer loads (16 B
-//     per lane, no staging registers) issued 3 stages ahead; a stage is waited for with a vmcnt that leaves the
-//     newer stages in flight, then one barrier. Rows past M/N and bytes past K read as zeros (buffer range check).
-//   * every stage (A slab + W slab) is its own __shared__ array: the compiler can then tell that an LDS read of
-//     stage s does not alias the DMA filling stage s + 3 and does not serialize them.
-//   * 4 x 2 waves (2 per SIMD, so one wave's MFMAs cover the other's LDS latency), each owning a 64 x BN/2
-//     sub-tile = 2 x (BN/64) MFMA tiles of 32 x 32 (up to 128 int32 accumulators per lane).
-//   * LDS rows are 64 B (4 chunks of 16 B); chunk c of row r is stored at chunk c ^ ((r >> 1) & 3), so the 8 lanes
-//     the LDS serves together (rows r..r+7, one logical chunk) hit 8 different bank groups; the swizzle is applied
-//     on the global side of the DMA (lane i fetches the chunk that belongs in slot i).
+// Tiling (MFMA-bound at the 9B shapes; one workgroup of 8 waves per CU, two per SIMD so that one wave's MFMAs
+// cover the other's LDS latency and barrier waits):
+//   * workgroup tile BM x BN = 256 x {256 | 192}; K advances 128 bytes per stage, so every row segment a stage
+//     loads is one whole 128-byte line (64-byte segments measured at about 60% of the L2 -> CU rate).
+//   * global -> registers -> LDS: each thread holds the next stage of its share of the A and W slabs in registers
+//     (buffer loads issued a stage before they are needed) and writes it into the LDS buffer that is not being
+//     read; the LDS holds two stages (2 x (256 + BN) x 128 B <= 128 KB). Rows past M/N and bytes past K read as
+//     zeros (buffer range check).
+//   * 4 x 2 waves, each owning a 64 x BN/2 sub-tile = 2 x (BN/64) MFMA tiles of 32 x 32 (up to 128 int32
+//     accumulators per lane). Per 32 k a wave reads 2 + BN/64 fragments (ds_read_b128) for 2 x BN/64 MFMAs.
+//   * software pipeline: fragments are double-buffered in registers across k-steps and across stages; the LDS
+//     writes and buffer loads of the next stages are spread between the MFMAs of one k-step; one barrier per
+//     stage, preceded by an lgkmcnt wait only (a fenced barrier would also wait for the loads in flight).
+//   * LDS rows are 128 B (8 chunks of 16 B); chunk c of row r is stored at c ^ ((r >> 1) & 7). gfx950 serves 16
+//     lanes of a ds_read_b128 per cycle from 64 banks (256-byte period): a fragment read (16 consecutive rows,
+//     one chunk) then hits 16 distinct 16-byte bank quads; the 8 lanes of a ds_write_b128 cycle write the 8
+//     chunks of one row, also distinct.
 //   * blockIdx -> tile is XCD-aware: workgroups are dealt round-robin over the 8 XCDs, so each XCD gets a contiguous
 //     range of tiles in a grouped (kGroupM tile-rows) order, and the tiles one XCD runs together share A/W panels
 //     in its L2.
 //   * epilogue: each wave stages its accumulators 32 rows at a time through a private LDS band and writes 4
 //     columns per lane, a wave covering whole row segments; scales, bias and residual are applied in fp32 in the
-//     oracle's order and rounded once to bf16. No workgroup barrier after the one that ends the main loop.
+//     oracle's order and rounded once to bf16.
 // int32 accumulation is exact for K < 133,144 (|acc| <= 127^2 K < 2^31), so any correct GEMM is bit-exact.
 #include <type_traits>
 
@@ -29,18 +34,14 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kWM = 4, kWN = 2;            // wave grid of a workgroup
 constexpr int kThreads = 64 * kWM * kWN;   // 512
 constexpr int BM = 256;
-constexpr int BK = 64;       // bytes of K per stage
-constexpr int kStages = 4;
+constexpr int BK = 128;      // bytes of K per stage
+constexpr int kCpr = BK / 16;  // 16-byte chunks per row per stage
 constexpr int kGroupM = 4;
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any range: the load returns zeros
-
-template <int N>
-using IC = std::integral_constant<int, N>;
 
 struct GemmArgs {
   const int8_t* a;
@@ -56,103 +57,12 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
-// Chunk swizzle of the 64-byte LDS rows. An operand read is a ds_read_b128 in which lanes 16g..16g+15 take 16
-// consecutive rows at one logical chunk, and gfx950 serves 16 lanes of a ds_read_b128 per cycle from 64 4-byte
-// banks (a 256-byte period): rows r and r + 4 share their bank set unless their chunks differ, so the chunk is
-// XORed with bits 2..3 of the row, which makes the 16 reads of a group land on 16 distinct 16-byte bank quads.
-__device__ __forceinline__ int chunk_xor(int row) { return (row >> 2) & 3; }
+// byte offset of logical chunk c (0..7) of row r inside a slab
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-// byte offset of logical 16-byte chunk c (0..3) of row r inside a stage buffer
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ chunk_xor(row)) << 4); }
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Workgroup barrier without a memory fence: the stage waits are explicit vmcnt waits (a fenced __syncthreads would
-// wait for every DMA in flight, including the stages being prefetched). The "memory" clobber keeps the compiler
-// from moving LDS accesses across it.
-__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// DMA of a ROWS x 64 B slab into LDS. Per wave instruction, lane l writes LDS bytes [base + 16 l, +16): LDS chunk
-// index cid = i * 256 + wave * 64 + lane, row = cid / 4, physical chunk = cid % 4, which holds logical chunk
-// (cid % 4) ^ chunk_xor(row). The per-lane part of the global offset (row * ld + 16 * logical chunk) is fixed
-// for the whole K loop (voff[i]); the k0 of the slab goes in the instruction's scalar offset. With KTAIL (K not a
-// multiple of the slab) chunks past K are sent out of the buffer's range and read as zeros.
-// A slab of ROWS x 64 B is ROWS / 16 wave-instructions of 64 lanes x 16 B, dealt round-robin to the waves: wave w
-// issues instruction i * kWaves + w for i = 0, 1, ... while it is below ROWS / 16.
-constexpr int kWaves = kWM * kWN;
-
-template <int ROWS>
-__device__ __forceinline__ constexpr int slab_iters() { return (ROWS / 16 + kWaves - 1) / kWaves; }
-
-// DMA instructions wave w issues for one ROWS-row slab
-template <int ROWS>
-__device__ __forceinline__ int slab_loads(int wave) {
-  constexpr int n = ROWS / 16;
-  return n / kWaves + (wave < n % kWaves ? 1 : 0);
-}
-
-template <int ROWS>
-struct SlabOffsets {
-  int v[slab_iters<ROWS>()];
-  int col[slab_iters<ROWS>()];  // byte column of the chunk inside the slab
-  __device__ __forceinline__ void init(int64_t ld) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < slab_iters<ROWS>(); ++i) {
-      const int cid = (i * kWaves + wave) * 64 + lane;
-      const int row = cid >> 2;
-      col[i] = ((cid & 3) ^ chunk_xor(row)) << 4;
-      v[i] = (int)(row * ld) + col[i];
-    }
-  }
-};
-
-// One direct-to-LDS 16-byte load per lane: LDS[m0 + 16 lane] = buffer[voff + soff]. Written as inline assembly so
-// that the compiler's wait-count pass does not see it: the compiler would otherwise wait for every DMA in flight
-// before the next LDS read (it cannot always tell the stage buffers apart), collapsing the pipeline. The waits for
-// these loads are the explicit vmcnt waits of the pipeline. m0 is not used by anything else in this kernel.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds_base, int voff, int soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
-               : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const int8_t* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)p;
-}
-
-// DMA of a ROWS x 64 B slab into LDS. Lane l of wave-instruction q writes LDS bytes [16 (64 q + l), +16): chunk
-// index cid = 64 q + l, row = cid / 4, physical chunk = cid % 4, holding logical chunk (cid % 4) ^ chunk_xor(row).
-// The per-lane part of the global offset (row * ld + 16 * logical chunk) is fixed for the whole K loop (so.v); the
-// k0 of the slab goes in the instruction's scalar offset. With KTAIL (K not a multiple of the slab) chunks past K
-// are sent out of the buffer's range and read as zeros.
-template <int ROWS, bool KTAIL>
-__device__ __forceinline__ void dma_slab(__amdgpu_buffer_rsrc_t rsrc, const SlabOffsets<ROWS>& so, int k0, int K,
-                                         int8_t* lds) {
-  const int wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int i = 0; i < slab_iters<ROWS>(); ++i) {
-    const int q = i * kWaves + wave;
-    if ((ROWS / 16) % kWaves != 0 && q >= ROWS / 16) break;  // wave-uniform
-    int voff = so.v[i];
-    if constexpr (KTAIL) voff = (k0 + so.col[i] < K) ? voff : kOOB;
-    dma16(rsrc, __builtin_amdgcn_readfirstlane(lds_addr(lds + q * 64 * 16)), voff, k0);
-  }
-}
-
-// Instruction i (0 .. slab_iters - 1) of this wave's share of dma_slab, if the wave has one (wave-uniform).
-template <int ROWS, bool KTAIL>
-__device__ __forceinline__ void dma_one(__amdgpu_buffer_rsrc_t rsrc, const SlabOffsets<ROWS>& so, int i, int k0, int K,
-                                        int8_t* lds) {
-  const int q = i * kWaves + (threadIdx.x >> 6);
-  if ((ROWS / 16) % kWaves != 0 && q >= ROWS / 16) return;
-  int voff = so.v[i];
-  if constexpr (KTAIL) voff = (k0 + so.col[i] < K) ? voff : kOOB;
-  dma16(rsrc, __builtin_amdgcn_readfirstlane(lds_addr(lds + q * 64 * 16)), voff, k0);
+__device__ __forceinline__ void barrier_lds() {
+  // LDS traffic of this wave complete, then the workgroup barrier (no fence: buffer loads stay in flight)
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -168,18 +78,33 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
   tn = in_group / gsz;
 }
 
+// One thread's share of a ROWS x 128-byte slab: load i covers row i * (kThreads / kCpr) + tid / kCpr, chunk
+// tid % kCpr (8 consecutive lanes read one whole 128-byte row segment). The per-thread byte offset in the matrix
+// (vo) and in the slab (lo) are those of load 0; load i adds i * 64 rows (ld * 64 * i bytes in the matrix,
+// 64 * 128 * i bytes in LDS, an immediate).
+template <int ROWS>
+struct Slab {
+  static constexpr int kLoads = ROWS * kCpr / kThreads;  // 4 for 256 rows, 3 for 192
+  static constexpr int kRowsPerLoad = kThreads / kCpr;   // 64
+  int vo, lo, col;
+  __device__ __forceinline__ void init(int64_t ld) {
+    const int tid = threadIdx.x;
+    const int row = tid / kCpr, c = tid % kCpr;
+    col = c * 16;
+    vo = (int)(row * ld) + col;  // < 32 ld + 128: the host keeps 256 ld below 2^31
+    lo = swz(row, c);  // rows i * 64 + row keep the same (row >> 1) & 7, so the swizzle is load-independent
+  }
+};
+
 template <int BN, bool ACC_ONLY, bool GENERAL>
 __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
-  constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile
-  constexpr int TM = kRowsW / 32;    // 32-row MFMA tiles per wave
-  constexpr int TN = kColsW / 32;    // 32-col MFMA tiles per wave
-  constexpr int kSlabA = BM * BK, kSlabB = BN * BK;
-  // DMA instructions this wave issues per stage (the W slab of BN = 192 does not split evenly over the waves)
-  constexpr int kLoadsHi = BM / 16 / kWaves + (BN / 16 + kWaves - 1) / kWaves;
-  constexpr int kLoadsLo = BM / 16 / kWaves + (BN / 16) / kWaves;
-  // stage buffers: A slab at offset 0, W slab at offset kSlabA (four LDS objects: the compiler tracks DMA into each)
-  __shared__ __attribute__((aligned(16))) int8_t s0[kSlabA + kSlabB], s1[kSlabA + kSlabB], s2[kSlabA + kSlabB],
-      s3[kSlabA + kSlabB];
+  constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile: 64 x BN/2
+  constexpr int TM = kRowsW / 32;    // 2
+  constexpr int TN = kColsW / 32;    // 4 or 3
+  constexpr int kSlabA = BM * BK, kSlabB = BN * BK, kStage = kSlabA + kSlabB;
+  using SA = Slab<BM>;
+  using SB = Slab<BN>;
+  __shared__ __attribute__((aligned(16))) int8_t smem[2 * kStage];
 
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -194,28 +119,51 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   const __amdgpu_buffer_rsrc_t rb =
       __builtin_amdgcn_make_buffer_rsrc((void*)(p.w + n0 * p.ldw), (short)0, (int)((rows_b - 1) * p.ldw + p.K),
                                         0x00020000);
-
-  auto abuf = [&](auto I) -> int8_t* {
-    if constexpr (decltype(I)::value == 0) return s0;
-    else if constexpr (decltype(I)::value == 1) return s1;
-    else if constexpr (decltype(I)::value == 2) return s2;
-    else return s3;
-  };
-  auto bbuf = [&](auto I) -> int8_t* { return abuf(I) + kSlabA; };
-  SlabOffsets<BM> soa;
-  SlabOffsets<BN> sob;
-  soa.init(p.lda);
-  sob.init(p.ldw);
+  SA sa_;
+  SB sb_;
+  sa_.init(p.lda);
+  sb_.init(p.ldw);
   const int K = (int)p.K;
-  auto issue = [&](auto I, int kt) {
-    dma_slab<BM, GENERAL>(ra, soa, kt * BK, K, abuf(I));
-    dma_slab<BN, GENERAL>(rb, sob, kt * BK, K, bbuf(I));
+  const int nk = (K + BK - 1) / BK;
+  const int lda_step = (int)(p.lda * SA::kRowsPerLoad), ldw_step = (int)(p.ldw * SB::kRowsPerLoad);
+
+  // zero-length descriptors: a k-tile past the end reads through these and gets zeros
+  const __amdgpu_buffer_rsrc_t ra0 = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb0 = __builtin_amdgcn_make_buffer_rsrc((void*)p.w, (short)0, 0, 0x00020000);
+
+  // register stage of the slabs
+  v4i ga[SA::kLoads], gb[SB::kLoads];
+  // global -> registers, k-tile kt. One vector offset per matrix (the thread's row and chunk); the load's row step
+  // (i * 64 rows) and the tile's k0 are the scalar offset, so no per-load offsets stay live across the loop. In
+  // the GENERAL variant a chunk past K gets the vector offset kOOB - soffset: the sum is kOOB, past the range.
+  auto gload_a = [&](int kt, int i) {
+    const int soff = kt * BK + i * lda_step;
+    int vo = sa_.vo;
+    if (GENERAL && kt * BK + sa_.col >= K) vo = kOOB - soff;
+    ga[i] = __builtin_amdgcn_raw_buffer_load_b128(kt < nk ? ra : ra0, vo, soff, 0);
   };
-  // the same DMA one instruction at a time: j < slab_iters<BM> is A instruction j, then the W instructions
-  constexpr int kDmaA = slab_iters<BM>(), kDma = kDmaA + slab_iters<BN>();
-  auto issue_one = [&](auto I, int kt, int j) {
-    if (j < kDmaA) dma_one<BM, GENERAL>(ra, soa, j, kt * BK, K, abuf(I));
-    else dma_one<BN, GENERAL>(rb, sob, j - kDmaA, kt * BK, K, bbuf(I));
+  auto gload_b = [&](int kt, int i) {
+    const int soff = kt * BK + i * ldw_step;
+    int vo = sb_.vo;
+    if (GENERAL && kt * BK + sb_.col >= K) vo = kOOB - soff;
+    gb[i] = __builtin_amdgcn_raw_buffer_load_b128(kt < nk ? rb : rb0, vo, soff, 0);
+  };
+  // registers -> LDS stage buffer
+  auto swrite_a = [&](int buf, int i) {
+    *reinterpret_cast<v4i*>(smem + buf * kStage + sa_.lo + i * SA::kRowsPerLoad * BK) = ga[i];
+  };
+  auto swrite_b = [&](int buf, int i) {
+    *reinterpret_cast<v4i*>(smem + buf * kStage + kSlabA + sb_.lo + i * SB::kRowsPerLoad * BK) = gb[i];
+  };
+  // operand fragments of k-step s (32 of the stage's 128 k) of stage buffer buf
+  auto frags = [&](int buf, int s, v4i (&fa)[TM], v4i (&fb)[TN]) {
+    const int chunk = s * 2 + (lane >> 5);
+    const int8_t* la = smem + buf * kStage;
+    const int8_t* lb = la + kSlabA;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(la + swz(wm * kRowsW + i * 32 + (lane & 31), chunk));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const v4i*>(lb + swz(wn * kColsW + j * 32 + (lane & 31), chunk));
   };
 
   v16i acc[TM][TN];
@@ -224,104 +172,98 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  const int nk = (int)((p.K + BK - 1) / BK);
-  const bool hi = slab_loads<BM>(wave) + slab_loads<BN>(wave) == kLoadsHi;  // wave-uniform
-  // wait until at most `newer` stages issued after the awaited one are still in flight (this wave's DMAs)
-  auto wait_stage = [&](int newer) {
-    if (newer >= 2) {
-      if (hi) wait_vm<2 * kLoadsHi>(); else wait_vm<2 * kLoadsLo>();
-    } else if (newer == 1) {
-      if (hi) wait_vm<kLoadsHi>(); else wait_vm<kLoadsLo>();
-    } else {
-      wait_vm<0>();
-    }
-  };
-  // operand fragments of k-step s (32 of the stage's 64 k) of one stage buffer
-  auto frags = [&](const int8_t* la, const int8_t* lb, int s, v4i (&fa)[TM], v4i (&fb)[TN]) {
-    const int chunk = s * 2 + (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(la + swz(wm * kRowsW + i * 32 + (lane & 31), chunk));
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const v4i*>(lb + swz(wn * kColsW + j * 32 + (lane & 31), chunk));
-  };
-  auto mma = [&](const v4i (&fa)[TM], const v4i (&fb)[TN]) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-  };
-  // The MFMAs of one k-step with the refill DMA of stage I (k-tile kt) spread between them, one instruction after
-  // every TM*TN/kDma MFMAs: issued as one burst right after the barrier, the DMAs of all 8 waves fill the
-  // texture-address queue and the waves stall at issue instead of running their MFMAs.
-  auto mma_dma = [&](const v4i (&fa)[TM], const v4i (&fb)[TN], auto I, int kt, bool refill) {
-    constexpr int kMf = TM * TN;
+  // The MFMAs of one k-step; `fill` issues the o-th of this k-step's kOps memory operations after MFMA
+  // o * kMf / kOps (spreading them so that no wave stalls on a full queue while its MFMA pipe idles).
+  constexpr int kMf = TM * TN;
+  auto mma = [&](const v4i (&fa)[TM], const v4i (&fb)[TN], auto fill, auto OPS) {
+    constexpr int kOps = decltype(OPS)::value;
 #pragma unroll
     for (int x = 0; x < kMf; ++x) {
       acc[x / TN][x % TN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[x / TN], fb[x % TN], acc[x / TN][x % TN], 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < kDma; ++j)
-        if (j * kMf / kDma == x && refill) issue_one(I, kt, j);
+      for (int o = 0; o < kOps; ++o)
+        if (o * kMf / kOps == x) fill(o);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
+  auto nofill = [](int) {};
+  using Zero = std::integral_constant<int, 0>;
 
-  // Pipeline. Stage buffer I % 4 holds k-tile I; three k-tiles are in flight ahead of the one being computed.
-  // Fragments are register double-buffered across k-steps and across stages: step kt loads k-step 1 of its
-  // stage, runs k-step 0, then (once stage kt+1 has landed for every wave: own vmcnt wait + barrier) loads k-step 0
-  // of stage kt+1 and runs k-step 1 while refilling the buffer of k-tile kt-1 with k-tile kt+3 (every wave is past
-  // its last read of kt-1: those reads fed MFMAs issued before the barrier). LDS latency is thus always
-  // covered by 8 MFMAs of the same wave.
+  // Pipeline. LDS buffer kt % 2 holds k-tile kt while it is computed; the register stage holds the next k-tile
+  // from its buffer loads until it is written to LDS. Stage kt:
+  //   k-step 0: read k-step 1's fragments; MFMAs of k-step 0 interleaved with the LDS writes of k-tile kt + 1
+  //             (registers -> LDS buffer (kt+1) % 2, free since the barrier that ended stage kt-1), then the buffer
+  //             loads of k-tile kt + 2 into the freed registers (a whole stage to land)
+  //   k-steps 1, 2: read the next k-step's fragments, MFMAs
+  //   k-step 3: lgkmcnt wait + barrier (k-tile kt+1 is in LDS for every wave, every wave is done reading kt),
+  //             read k-step 0 of k-tile kt+1, MFMAs of k-step 3
   v4i f0a[TM], f0b[TN], f1a[TM], f1b[TN];
-  issue(IC<0>{}, 0);
-  if (nk > 1) issue(IC<1>{}, 1);
-  if (nk > 2) issue(IC<2>{}, 2);
-  wait_stage(min(2, nk - 1));
-  barrier();
-  frags(abuf(IC<0>{}), bbuf(IC<0>{}), 0, f0a, f0b);
+  constexpr int kOpsA = SA::kLoads, kOpsB = SB::kLoads;
+  constexpr int kOps0 = 2 * (kOpsA + kOpsB);  // LDS writes and buffer loads in k-step 0
 
-  auto step = [&](auto I, int kt) {
-    if (kt >= nk) return;
-    constexpr int kI = decltype(I)::value, kN = (kI + 1) % kStages, kR = (kI + 3) % kStages;
-    frags(abuf(I), bbuf(I), 1, f1a, f1b);
-    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs they overlap
-    mma(f0a, f0b);
-    // Unconditional also on the last k-tile (then it reads an idle, in-bounds stage buffer whose values are
-    // never used): a branch here would merge two paths with different numbers of LDS reads in flight, and the
-    // compiler's lgkmcnt wait before k-step 1 would then also wait for the reads of the next stage.
-    wait_stage(min(1, nk - 2 - kt));
-    barrier();
-    frags(abuf(IC<kN>{}), bbuf(IC<kN>{}), 0, f0a, f0b);
+#pragma unroll
+  for (int i = 0; i < kOpsA; ++i) gload_a(0, i);
+#pragma unroll
+  for (int i = 0; i < kOpsB; ++i) gload_b(0, i);
+#pragma unroll
+  for (int i = 0; i < kOpsA; ++i) swrite_a(0, i);
+#pragma unroll
+  for (int i = 0; i < kOpsB; ++i) swrite_b(0, i);
+#pragma unroll
+  for (int i = 0; i < kOpsA; ++i) gload_a(1, i);
+#pragma unroll
+  for (int i = 0; i < kOpsB; ++i) gload_b(1, i);
+  barrier_lds();
+  frags(0, 0, f0a, f0b);
+
+  // one stage; CUR = kt % 2 (LDS buffer of k-tile kt), NXT = 1 - CUR
+  auto stage = [&](int CUR, int kt) {
+    const int NXT = 1 - CUR;
+    frags(CUR, 1, f1a, f1b);
     __builtin_amdgcn_sched_barrier(0);
-    mma_dma(f1a, f1b, IC<kR>{}, kt + 3, kt + 3 < nk);
+    auto fill0 = [&](int o) {
+      if (o < kOpsA) swrite_a(NXT, o);
+      else if (o < kOpsA + kOpsB) swrite_b(NXT, o - kOpsA);
+      else if (o < 2 * kOpsA + kOpsB) gload_a(kt + 2, o - kOpsA - kOpsB);
+      else gload_b(kt + 2, o - 2 * kOpsA - kOpsB);
+    };
+    mma(f0a, f0b, fill0, std::integral_constant<int, kOps0>{});
+    frags(CUR, 2, f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(f1a, f1b, nofill, Zero{});
+    frags(CUR, 3, f1a, f1b);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(f0a, f0b, nofill, Zero{});
+    barrier_lds();
+    frags(NXT, 0, f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(f1a, f1b, nofill, Zero{});
   };
 
-  for (int kt = 0; kt < nk; kt += kStages) {
-    step(IC<0>{}, kt);
-    step(IC<1>{}, kt + 1);
-    step(IC<2>{}, kt + 2);
-    step(IC<3>{}, kt + 3);
-  }
-  __syncthreads();  // every wave is done reading the stage buffers; each now reuses one as its private band
+  // (the stage index is a run-time value: unrolling two stages with compile-time buffer indices lengthens the
+  // live ranges enough to spill the staged loads)
+  for (int kt = 0; kt < nk; ++kt) stage(kt & 1, kt);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the loads past the end (zeros) land before LDS is reused
+  __syncthreads();
 
   // Epilogue, in two passes per band of 32 rows of the wave's kRowsW x kColsW sub-tile.
   //  1. In the MFMA result layout (lane l holds column l % 32 of each 32x32 tile and rows
   //     8*(r/4) + 4*(l/32) + r%4), t = (float(acc) * sa[m]) * sw[n] (the raw int32 with ACC_ONLY) goes to a private
-  //     LDS band (32 x kColsW 4-byte words; wave w uses half w % 2 of stage buffer w / 2). A lane needs one sw per
-  //     column tile and 16 sa per band, loaded up front.
+  //     LDS band (32 x kColsW 4-byte words). A lane needs one sw per column tile and 16 sa per band, loaded up
+  //     front.
   //  2. Row-major: lane l takes the 4 columns 4 (l % kC4) .. +3 of rows l / kC4 + kRowsPass * it, so its bias
   //     values are fixed for the tile; y = bf16((t + bias) + residual), the same fp32 operation order as the
   //     unfused product, with one rounding. Rows go in groups of 4 whose residual loads issue together.
   // The epilogue runs once per tile, so its code is kept small (it is fetched anew for every tile): only the
   // GENERAL variant carries the scalar paths for unaligned rows and a ragged last column group.
-  int8_t* stage_of_wave = (wave >> 1) == 0 ? s0 : (wave >> 1) == 1 ? s1 : (wave >> 1) == 2 ? s2 : s3;
   constexpr int kCols = kColsW;               // columns of the wave's sub-tile
   constexpr int kC4 = kCols / 4;              // 4-column chunks per row
   constexpr int kRowsPass = 64 / kC4;         // rows one pass of the wave covers
   constexpr int kPasses = (32 + kRowsPass - 1) / kRowsPass;
   static_assert(kPasses % 4 == 0, "row groups of 4");
   constexpr int kBand = 32 * kCols * 4;       // bytes of one band
-  static_assert(2 * kBand <= kSlabA + kSlabB, "epilogue bands do not fit");
-  uint32_t* band = reinterpret_cast<uint32_t*>(stage_of_wave + (wave & 1) * kBand);
+  static_assert(kWM * kWN * kBand <= 2 * kStage, "epilogue bands do not fit");
+  uint32_t* band = reinterpret_cast<uint32_t*>(smem + wave * kBand);
   const int64_t n_w = n0 + wn * kCols;
   const int col = lane & 31, h = lane >> 5;
   float swv[TN];
@@ -346,6 +288,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    __builtin_amdgcn_sched_barrier(0);  // one band at a time (hoisting the next band's loads spills)
     const int64_t m_band = m0 + wm * kRowsW + i * 32;
     float sav[16];
 #pragma unroll
@@ -367,54 +310,55 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
         band[row * kCols + j * 32 + col] = word;
       }
     }
-    if (!lane_on) continue;
+    if (lane_on) {
 #pragma unroll 1
-    for (int it0 = 0; it0 < kPasses; it0 += 4) {
-      uint2 res[4];
-      if (!ACC_ONLY && p.residual) {
+      for (int it0 = 0; it0 < kPasses; it0 += 4) {
+        uint2 res[4];
+        if (!ACC_ONLY && p.residual) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint16_t* rp = p.residual + min(m_band + kRowsPass * (it0 + u) + rr, p.M - 1) * p.ldr;
-          if constexpr (GENERAL) {
-            uint32_t e4[4];
+          for (int u = 0; u < 4; ++u) {
+            const uint16_t* rp = p.residual + min(m_band + kRowsPass * (it0 + u) + rr, p.M - 1) * p.ldr;
+            if constexpr (GENERAL) {
+              uint32_t e4[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) e4[e] = rp[min(n + e, p.N - 1)];
-            res[u] = make_uint2(e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16));
-          } else {
-            res[u] = *reinterpret_cast<const uint2*>(rp + n);
+              for (int e = 0; e < 4; ++e) e4[e] = rp[min(n + e, p.N - 1)];
+              res[u] = make_uint2(e4[0] | (e4[1] << 16), e4[2] | (e4[3] << 16));
+            } else {
+              res[u] = *reinterpret_cast<const uint2*>(rp + n);
+            }
           }
         }
-      }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int row = kRowsPass * (it0 + u) + rr;
-        const int64_t m = m_band + row;
-        if (row >= 32 || m >= p.M) continue;
-        const uint4 v = *reinterpret_cast<const uint4*>(band + row * kCols + 4 * c4);
-        if constexpr (ACC_ONLY) {
-          int32_t* dst = p.acc + m * p.ldacc + n;
-          if constexpr (GENERAL) {
+        for (int u = 0; u < 4; ++u) {
+          const int row = kRowsPass * (it0 + u) + rr;
+          const int64_t m = m_band + row;
+          if (row >= 32 || m >= p.M) continue;
+          const uint4 v = *reinterpret_cast<const uint4*>(band + row * kCols + 4 * c4);
+          if constexpr (ACC_ONLY) {
+            int32_t* dst = p.acc + m * p.ldacc + n;
+            if constexpr (GENERAL) {
+              const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+              for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = (int32_t)vv[e];
+            } else {
+              *reinterpret_cast<uint4*>(dst) = v;
+            }
+          } else {
             const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-            for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = (int32_t)vv[e];
-          } else {
-            *reinterpret_cast<uint4*>(dst) = v;
-          }
-        } else {
-          const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-          const uint32_t rw[4] = {res[u].x << 16, res[u].x & 0xffff0000u, res[u].y << 16, res[u].y & 0xffff0000u};
-          uint32_t o[4];
+            const uint32_t rw[4] = {res[u].x << 16, res[u].x & 0xffff0000u, res[u].y << 16, res[u].y & 0xffff0000u};
+            uint32_t o[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float y = __uint_as_float(vv[e]);
-            if (p.bias) y = y + bias4[e];
-            if (p.residual) y = y + __uint_as_float(rw[e]);
-            o[e] = od_f32_to_bf16(y);
-          }
-          uint16_t* dst = p.out + m * p.ldo + n;
-          if constexpr (GENERAL) {
-            for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = (uint16_t)o[e];
-          } else {
-            *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+            for (int e = 0; e < 4; ++e) {
+              float y = __uint_as_float(vv[e]);
+              if (p.bias) y = y + bias4[e];
+              if (p.residual) y = y + __uint_as_float(rw[e]);
+              o[e] = od_f32_to_bf16(y);
+            }
+            uint16_t* dst = p.out + m * p.ldo + n;
+            if constexpr (GENERAL) {
+              for (int e = 0; e < 4 && n + e < p.N; ++e) dst[e] = (uint16_t)o[e];
+            } else {
+              *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+            }
           }
         }
       }
@@ -460,9 +404,11 @@ extern "C" int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const
   };
   auto launch2 = [&](auto ACCc, bool general) {
     if (use192) {
-      general ? launch(IC<192>{}, ACCc, std::true_type{}) : launch(IC<192>{}, ACCc, std::false_type{});
+      general ? launch(std::integral_constant<int, 192>{}, ACCc, std::true_type{})
+              : launch(std::integral_constant<int, 192>{}, ACCc, std::false_type{});
     } else {
-      general ? launch(IC<256>{}, ACCc, std::true_type{}) : launch(IC<256>{}, ACCc, std::false_type{});
+      general ? launch(std::integral_constant<int, 256>{}, ACCc, std::true_type{})
+              : launch(std::integral_constant<int, 256>{}, ACCc, std::false_type{});
     }
   };
   if (acc) {
