@@ -114,6 +114,26 @@ int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
                      float scale, od_stream_t stream);
 
 /*
+ * od_branched_attn_split — od_branched_attn with the state's keys split into nsplit contiguous ranges processed by
+ * separate workgroups (for shapes with few slot tiles: few rows over a long state), merged by log-sum-exp.
+ * Replaces: the same reference code as od_branched_attn; the split is an exact regrouping of the LSE merge of
+ * prefix_attn.py:74-76 over more parts.
+ *   nsplit     1 .. 256 (1 behaves as od_branched_attn and ignores ws)
+ *   ws         fp32 workspace of at least ws_floats >= nsplit * R * Hq * t * (D + 1) floats, 16-byte aligned: each
+ *              split's normalized partial output and LSE (caller-owned; contents undefined after the call)
+ * Other arguments and the result as od_branched_attn. Two launches on `stream` (splits, then the merge).
+ */
+int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                           const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                           const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                           const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
+                           const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
+                           uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
+                           int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
+                           int64_t cap, float scale, int64_t nsplit, float* ws, int64_t ws_floats,
+                           od_stream_t stream);
+
+/*
  * od_wide_attn — flash attention over bf16 K/V.
  * Replaces: wide_attention / _wide_fwd (src/opendecider/wide_attention.py:13-91).
  *   q      bf16 [B, H, T, DK], element strides (sqb, sqh, sqt)

@@ -27,6 +27,10 @@ SIGNATURES = {
     "od_branched_attn": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
                          _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr,
                          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _c_ptr],
+    "od_branched_attn_split": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
+                               _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64,
+                               _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _c_ptr,
+                               _i64, _c_ptr],
     "od_wide_attn": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64,
                      _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int,
                      ctypes.c_float, _c_ptr],

@@ -60,6 +60,8 @@ struct AttnArgs {
   int64_t sqr, sqh, sqt, skr, skh, skt, svr, svh, svt, sor, soh, sot;
   int R, Hq, Hkv, t, Ns, T, cap, rep;
   float scale_log2;
+  int nsplit;   // key-range splits (1: one pass writes out/lse)
+  float* part;  // nsplit > 1: fp32 partials, o [nsplit][R][Hq][t][D] then lse [nsplit][R][Hq][t]
 };
 
 // Every array is 16-byte aligned so that fragment and scale accesses compile to single ds_read_b128 /
@@ -418,7 +420,7 @@ __device__ __forceinline__ void own_stage(const AttnArgs& p, Smem<D>& sm, int ro
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) {
   __shared__ Smem<D> sm;
-  const int s = blockIdx.z, g = blockIdx.y;
+  const int s = blockIdx.z / p.nsplit, sp = blockIdx.z % p.nsplit, g = blockIdx.y;
   const int row0 = p.row_start ? p.row_start[s] : 0;
   const int nrows = p.row_start ? p.row_start[s + 1] - row0 : p.R;
   const int per_row = p.t * p.rep;
@@ -473,25 +475,28 @@ __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) 
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) o[dt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  // ---- prefix: the state's int8 K/V, 64 keys per block, double buffered
-  const int nb = (p.T + kBlockKeys - 1) / kBlockKeys;
-  if (nb > 0) {
+  // ---- prefix: the state's int8 K/V, 64 keys per block, double buffered; split sp of nsplit takes the blocks
+  // [sp * bps, (sp + 1) * bps)
+  const int nb_all = (p.T + kBlockKeys - 1) / kBlockKeys;
+  const int bps = (nb_all + p.nsplit - 1) / p.nsplit;
+  const int b_lo = min(nb_all, sp * bps), b_hi = min(nb_all, b_lo + bps);
+  if (b_hi > b_lo) {
     PrefixRegs<D> pr;
-    prefix_load<D>(p, s, g, 0, pr);
+    prefix_load<D>(p, s, g, b_lo * kBlockKeys, pr);
     prefix_store<D>(sm, 0, pr);
     __syncthreads();
-    for (int b = 0; b < nb; ++b) {
-      const int cur = b & 1;
-      if (b + 1 < nb) prefix_load<D>(p, s, g, (b + 1) * kBlockKeys, pr);
+    for (int b = b_lo; b < b_hi; ++b) {
+      const int cur = (b - b_lo) & 1;
+      if (b + 1 < b_hi) prefix_load<D>(p, s, g, (b + 1) * kBlockKeys, pr);
       attend_block<D, 2, false>(sm, cur, qf, c_i, m_run, l_run, e_run, o, 0, 0, slot_row, slot_tok);
-      if (b + 1 < nb) prefix_store<D>(sm, cur ^ 1, pr);
+      if (b + 1 < b_hi) prefix_store<D>(sm, cur ^ 1, pr);
       __syncthreads();
     }
   }
 
-  // ---- own keys: every option row that has a slot in this tile, 32 keys per block
+  // ---- own keys (the last split): every option row that has a slot in this tile, 32 keys per block
   const int last = min(slot_base + kSlotsPerTile, nslots) - 1;
-  const int r_lo = row0 + slot_base / per_row, r_hi = row0 + last / per_row;
+  const int r_lo = row0 + slot_base / per_row, r_hi = sp == p.nsplit - 1 ? row0 + last / per_row : r_lo - 1;
   for (int row = r_lo; row <= r_hi; ++row) {
     for (int j0 = 0; j0 < p.t; j0 += kOwnKeys) {
       __syncthreads();  // LDS buffer 0 free
@@ -504,6 +509,22 @@ __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) 
   if (!slot_ok) return;
   // ---- epilogue: out = O 2^E / l (bf16), lse = (m + log2 l) ln 2
   const float inv = l_run > 0.0f ? ldexpf(1.0f / l_run, e_run) : 0.0f;
+  const float lse_v = l_run > 0.0f ? (m_run + __log2f(l_run)) * kLn2 : -INFINITY;
+  const int64_t slot_idx = ((int64_t)slot_row * p.Hq + slot_head) * p.t + slot_tok;
+  if (p.nsplit > 1) {
+    // this split's normalized fp32 partial and its LSE, merged by od_attn_combine
+    const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
+    float* po = p.part + ((int64_t)sp * nsl + slot_idx) * D;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        *reinterpret_cast<float4*>(po + dt * 32 + 8 * r4 + 4 * h) =
+            make_float4(o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
+                        o[dt][4 * r4 + 3] * inv);
+    if (h == 0) p.part[(int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx] = lse_v;
+    return;
+  }
   uint16_t* op = p.out + (int64_t)slot_row * p.sor + (int64_t)slot_head * p.soh + (int64_t)slot_tok * p.sot;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) {
@@ -517,10 +538,106 @@ __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) 
       *reinterpret_cast<uint2*>(op + d0) = make_uint2(lo, hi);
     }
   }
-  if (p.lse && h == 0) {
-    p.lse[((int64_t)slot_row * p.Hq + slot_head) * p.t + slot_tok] =
-        l_run > 0.0f ? (m_run + __log2f(l_run)) * kLn2 : -INFINITY;
+  if (p.lse && h == 0) p.lse[slot_idx] = lse_v;
+}
+
+// LSE merge of the key-range splits (prefix_attn.py:74-76 generalised to n parts): M = max_s lse_s,
+// w_s = exp(lse_s - M), out = sum_s w_s o_s / sum_s w_s (bf16), lse = M + log(sum_s w_s); no visible key in any
+// split -> 0 and -inf. One thread per (slot, 8 values of d).
+template <int D>
+__global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
+  const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t slot = gid / (D / 8);
+  const int d0 = (int)(gid % (D / 8)) * 8;
+  if (slot >= nsl) return;
+  const float* lse_p = p.part + (int64_t)p.nsplit * nsl * D;
+  float M = -INFINITY;
+  for (int sp = 0; sp < p.nsplit; ++sp) M = fmaxf(M, lse_p[sp * nsl + slot]);
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float wsum = 0.0f;
+  if (M != -INFINITY) {
+    for (int sp = 0; sp < p.nsplit; ++sp) {
+      const float l = lse_p[sp * nsl + slot];
+      if (l == -INFINITY) continue;
+      const float w = __expf(l - M);
+      wsum += w;
+      const float4* po = reinterpret_cast<const float4*>(p.part + (sp * nsl + slot) * D + d0);
+      const float4 a = po[0], b = po[1];
+      acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
+      acc[4] += w * b.x; acc[5] += w * b.y; acc[6] += w * b.z; acc[7] += w * b.w;
+    }
   }
+  const int row = (int)(slot / ((int64_t)p.Hq * p.t)), rem = (int)(slot % ((int64_t)p.Hq * p.t));
+  const int head = rem / p.t, tok = rem % p.t;
+  const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+  uint32_t w4[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    w4[e] = (uint32_t)od_f32_to_bf16(acc[2 * e] * inv) | ((uint32_t)od_f32_to_bf16(acc[2 * e + 1] * inv) << 16);
+  uint16_t* op = p.out + (int64_t)row * p.sor + (int64_t)head * p.soh + (int64_t)tok * p.sot + d0;
+  *reinterpret_cast<uint2*>(op) = make_uint2(w4[0], w4[1]);
+  *reinterpret_cast<uint2*>(op + 4) = make_uint2(w4[2], w4[3]);
+  if (p.lse && d0 == 0) p.lse[slot] = wsum > 0.0f ? M + __logf(wsum) : -INFINITY;
+}
+
+}  // namespace
+
+namespace {
+
+int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, const uint16_t* k_own, int64_t skr,
+                    int64_t skh, int64_t skt, const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                    const int8_t* kq, const float* ks, const int8_t* vq, const float* vs, const uint8_t* kvalid,
+                    const int32_t* row_start, int64_t max_rows, uint16_t* out, int64_t sor, int64_t soh, int64_t sot,
+                    float* lse, int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
+                    int64_t cap, float scale, int64_t nsplit, float* ws, int64_t ws_floats, od_stream_t stream) {
+  if (R < 0 || Hq < 1 || Hkv < 1 || t < 1 || Ns < 1 || T < 0 || cap < T || max_rows < 0) return OD_ERR_SHAPE;
+  if (Hq % Hkv) return OD_ERR_UNSUPPORTED;
+  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (t > 256) return OD_ERR_UNSUPPORTED;
+  if (!row_start && Ns != 1) return OD_ERR_SHAPE;
+  if (nsplit < 1 || nsplit > 256) return OD_ERR_SHAPE;
+  if (!row_start) max_rows = R;
+  if (R == 0 || max_rows == 0) return OD_OK;
+  if (!q || !k_own || !v_own || !out || (T > 0 && (!kq || !ks || !vq || !vs))) return OD_ERR_NULL;
+  if (nsplit > 1) {
+    if (!ws) return OD_ERR_NULL;
+    if (ws_floats < nsplit * R * Hq * t * (D + 1)) return OD_ERR_SHAPE;
+    if (!od_aligned16(ws)) return OD_ERR_ALIGN;
+  }
+  const int64_t strides[] = {sqr, sqh, sqt, skr, skh, skt, svr, svh, svt};
+  for (int64_t st : strides)
+    if (st < 0 || st % 8) return OD_ERR_ALIGN;
+  if (sor < 0 || soh < 0 || sot < 0 || sor % 4 || soh % 4 || sot % 4) return OD_ERR_ALIGN;
+  if (!od_aligned16(q) || !od_aligned16(k_own) || !od_aligned16(v_own) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
+  if (T > 0 && (!od_aligned16(kq) || !od_aligned16(vq))) return OD_ERR_ALIGN;
+  const int64_t rep = Hq / Hkv;
+  const int64_t tiles = (max_rows * t * rep + kSlotsPerTile - 1) / kSlotsPerTile;
+  if (tiles > 0x7fffffff || Hkv > 65535 || Ns * nsplit > 65535 || R * t * rep > 0x7fffffff ||
+      cap * Hkv * Ns * D > (1ll << 40) || nsplit * R * Hq * t * (D + 1) > (1ll << 40))
+    return OD_ERR_SHAPE;
+  AttnArgs a{q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, lse, sqr, sqh, sqt, skr, skh, skt, svr, svh,
+             svt, sor, soh, sot, (int)R, (int)Hq, (int)Hkv, (int)t, (int)Ns, (int)T, (int)cap, (int)rep,
+             scale * 1.4426950408889634f, (int)nsplit, nsplit > 1 ? ws : nullptr};
+  dim3 grid((unsigned)tiles, (unsigned)Hkv, (unsigned)(Ns * nsplit)), block(kThreads);
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 128) {
+    branched_attn_kernel<128><<<grid, block, 0, st>>>(a);
+  } else {
+    branched_attn_kernel<64><<<grid, block, 0, st>>>(a);
+  }
+  if (nsplit > 1) {
+    const int rc = od_launch_status();
+    if (rc != OD_OK) return rc;
+    const int64_t threads = R * Hq * t * (D / 8);
+    const unsigned blocks = (unsigned)((threads + 255) / 256);
+    if (D == 128) {
+      combine_kernel<128><<<blocks, 256, 0, st>>>(a);
+    } else {
+      combine_kernel<64><<<blocks, 256, 0, st>>>(a);
+    }
+  }
+  return od_launch_status();
 }
 
 }  // namespace
@@ -532,33 +649,20 @@ extern "C" int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int
                                 uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t R,
                                 int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, int64_t cap,
                                 float scale, od_stream_t stream) {
-  if (R < 0 || Hq < 1 || Hkv < 1 || t < 1 || Ns < 1 || T < 0 || cap < T || max_rows < 0) return OD_ERR_SHAPE;
-  if (Hq % Hkv) return OD_ERR_UNSUPPORTED;
-  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
-  if (t > 256) return OD_ERR_UNSUPPORTED;
-  if (!row_start && Ns != 1) return OD_ERR_SHAPE;
-  if (!row_start) max_rows = R;
-  if (R == 0 || max_rows == 0) return OD_OK;
-  if (!q || !k_own || !v_own || !out || (T > 0 && (!kq || !ks || !vq || !vs))) return OD_ERR_NULL;
-  const int64_t strides[] = {sqr, sqh, sqt, skr, skh, skt, svr, svh, svt};
-  for (int64_t st : strides)
-    if (st < 0 || st % 8) return OD_ERR_ALIGN;
-  if (sor < 0 || soh < 0 || sot < 0 || sor % 4 || soh % 4 || sot % 4) return OD_ERR_ALIGN;
-  if (!od_aligned16(q) || !od_aligned16(k_own) || !od_aligned16(v_own) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
-  if (T > 0 && (!od_aligned16(kq) || !od_aligned16(vq))) return OD_ERR_ALIGN;
-  const int64_t rep = Hq / Hkv;
-  const int64_t tiles = (max_rows * t * rep + kSlotsPerTile - 1) / kSlotsPerTile;
-  if (tiles > 0x7fffffff || Hkv > 65535 || Ns > 65535 || R * t * rep > 0x7fffffff || cap * Hkv * Ns * D > (1ll << 40))
-    return OD_ERR_SHAPE;
-  AttnArgs a{q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, lse, sqr, sqh, sqt, skr, skh, skt, svr, svh,
-             svt, sor, soh, sot, (int)R, (int)Hq, (int)Hkv, (int)t, (int)Ns, (int)T, (int)cap, (int)rep,
-             scale * 1.4426950408889634f};
-  dim3 grid((unsigned)tiles, (unsigned)Hkv, (unsigned)Ns), block(kThreads);
-  hipStream_t st = (hipStream_t)stream;
-  if (D == 128) {
-    branched_attn_kernel<128><<<grid, block, 0, st>>>(a);
-  } else {
-    branched_attn_kernel<64><<<grid, block, 0, st>>>(a);
-  }
-  return od_launch_status();
+  return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, kq, ks, vq, vs, kvalid,
+                         row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale, 1, nullptr,
+                         0, stream);
+}
+
+extern "C" int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, const uint16_t* k_own,
+                                      int64_t skr, int64_t skh, int64_t skt, const uint16_t* v_own, int64_t svr,
+                                      int64_t svh, int64_t svt, const int8_t* kq, const float* ks, const int8_t* vq,
+                                      const float* vs, const uint8_t* kvalid, const int32_t* row_start,
+                                      int64_t max_rows, uint16_t* out, int64_t sor, int64_t soh, int64_t sot,
+                                      float* lse, int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns,
+                                      int64_t T, int64_t cap, float scale, int64_t nsplit, float* ws,
+                                      int64_t ws_floats, od_stream_t stream) {
+  return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, kq, ks, vq, vs, kvalid,
+                         row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale, nsplit, ws,
+                         ws_floats, stream);
 }

@@ -172,13 +172,23 @@ def row_start_of(row_counts, device) -> tuple[torch.Tensor, int]:
     return torch.tensor(starts, dtype=torch.int32).to(device, non_blocking=True), max(counts)
 
 
+def split_count(slot_tiles: int, T: int, target_workgroups: int = 1024, min_blocks: int = 4) -> int:
+    """Key-range splits for od_branched_attn_split: enough workgroups to fill the GPU when the slot tiles alone do
+    not (few option rows over a long state), keeping at least `min_blocks` 64-key blocks per split."""
+    if slot_tiles >= target_workgroups // 2:
+        return 1
+    blocks = (T + 63) // 64
+    return max(1, min(-(-target_workgroups // max(slot_tiles, 1)), blocks // min_blocks, 256))
+
+
 def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, row_counts=None, length=None,
-                  out=None, return_lse: bool = False, row_start=None, max_rows=None):
+                  out=None, return_lse: bool = False, row_start=None, max_rows=None, n_split=None):
     """Branched option-row attention over int8 states (od_branched_attn). q (R, Hq, t, D) bf16; k_own/v_own
     (R, Hkv, t, D) bf16; kq/vq (Ns, Hkv, cap, D) int8 of which the first T tokens are used (T = `length`, else
     kvalid.shape[1], else cap); ks/vs (Ns, Hkv, cap) fp32; kvalid (Ns, T) bool/uint8 or None.
     Rows are grouped by state: row_counts (host ints, one per state) or a prebuilt (row_start, max_rows) pair from
-    row_start_of(); neither means Ns == 1. Returns out (R, Hq, t, D) bf16 [, lse (R, Hq, t) fp32]."""
+    row_start_of(); neither means Ns == 1. n_split: key-range splits (od_branched_attn_split); None picks them from
+    the grid size (split_count). Returns out (R, Hq, t, D) bf16 [, lse (R, Hq, t) fp32]."""
     require_gpu(q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, name="branched_attn")
     for x in (q, k_own, v_own):
         _lib.bf16_bits(x)
@@ -217,10 +227,21 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
     if out is None:
         out = torch.empty(R, Hq, t, D, dtype=torch.bfloat16, device=q.device)
     lse = torch.empty(R, Hq, t, dtype=torch.float32, device=q.device) if return_lse else None
-    check(lib().od_branched_attn(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
-                                 *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
-                                 ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv, t,
-                                 D, Ns, T, cap, float(scale), stream_of(q)), "od_branched_attn")
+    if n_split is None:
+        tiles = -(-(int(max_rows) * t * (Hq // Hkv)) // 128)
+        n_split = split_count(tiles * Hkv * Ns, T)
+    if n_split > 1:
+        ws = torch.empty(n_split * R * Hq * t * (D + 1), dtype=torch.float32, device=q.device)
+        check(lib().od_branched_attn_split(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
+                                           *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
+                                           ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R,
+                                           Hq, Hkv, t, D, Ns, T, cap, float(scale), int(n_split), ptr(ws), ws.numel(),
+                                           stream_of(q)), "od_branched_attn_split")
+    else:
+        check(lib().od_branched_attn(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
+                                     *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
+                                     ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv,
+                                     t, D, Ns, T, cap, float(scale), stream_of(q)), "od_branched_attn")
     return (out, lse) if return_lse else out
 
 

@@ -41,14 +41,14 @@ def make_case(seed, Ns, row_counts, Hq, Hkv, t, D, T, cap=None, holes=False):
                 row_state=row_state, T=T, scale=D ** -0.5)
 
 
-def run_gpu(c, return_lse=True, q=None):
+def run_gpu(c, return_lse=True, q=None, n_split=None):
     from opendecider_amd import kernels
     Ns = c["kq"].shape[0]
     return kernels.branched_attn(
         c["q"].to(DEV) if q is None else q, c["k"].to(DEV), c["v"].to(DEV), c["kq"].to(DEV), c["ks"].to(DEV),
         c["vq"].to(DEV), c["vs"].to(DEV), c["scale"],
         kvalid=None if c["kvalid"] is None else c["kvalid"].to(DEV),
-        row_counts=c["row_counts"] if Ns > 1 else None, length=c["T"], return_lse=return_lse)
+        row_counts=c["row_counts"] if Ns > 1 else None, length=c["T"], return_lse=return_lse, n_split=n_split)
 
 
 def run_oracle(c, dequant="fp32"):
@@ -129,3 +129,38 @@ def test_config1_branched_attention_full_shape(gpu_lib):
     d_kernel, d_oracles = rel_err(out.float().cpu(), ref_b), rel_err(ref, ref_b)
     print(f"config1: kernel vs bf16-materialize {d_kernel:.2e}; fp32 vs bf16-materialize oracles {d_oracles:.2e}")
     assert abs(d_kernel - d_oracles) <= 2e-3
+
+
+# ---- key-range splits (od_branched_attn_split): the same result, merged by LSE
+
+SPLIT_CASES = [("two_states_holes", 2), ("two_states_holes", 7), ("own_two_chunks_d64", 3), ("own_only_T0", 4),
+               ("empty_state_group", 3), ("t1_single_token_rows", 5), ("config4_like_t12", 64)]
+
+
+@pytest.mark.parametrize("name,n_split", SPLIT_CASES)
+def test_split_matches_oracle(gpu_lib, name, n_split):
+    """The state's 64-key blocks dealt to n_split workgroups (more splits than blocks leaves some empty; the own
+    keys go to the last split), each split's normalized fp32 partial merged by LSE: the same bar as one pass."""
+    c = make_case(**CASES[name])
+    print(f"split {name} n_split={n_split}", flush=True)
+    out, lse = run_gpu(c, n_split=n_split)
+    ref, ref_lse = run_oracle(c)
+    assert_close_rel(out.float().cpu(), ref, what=f"{name} split {n_split}")
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+
+
+def test_split_long_state_auto(gpu_lib):
+    """Few rows over a long state: the wrapper splits the keys by itself; result within the bar and order
+    invariant (bitwise) under a shuffle of the rows."""
+    from opendecider_amd import kernels
+    c = make_case(seed=12, Ns=2, row_counts=[2, 2], Hq=32, Hkv=8, t=16, D=128, T=4096)
+    tiles = -(-(2 * 16 * 4) // 128) * 8 * 2
+    assert kernels.split_count(tiles, 4096) > 1
+    out, lse = run_gpu(c)
+    ref, ref_lse = run_oracle(c)
+    assert_close_rel(out.float().cpu(), ref, what="long state auto split")
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+    perm = torch.tensor([1, 0, 3, 2])
+    cp = dict(c, q=c["q"][perm], k=c["k"][perm], v=c["v"][perm])
+    out_p, lse_p = run_gpu(cp)
+    assert torch.equal(out_p, out[perm.to(DEV)]) and torch.equal(lse_p, lse[perm.to(DEV)])
