@@ -44,6 +44,13 @@ constexpr int kSlotsPerTile = kWaves * 32;
 constexpr int kBlockKeys = 64;  // prefix keys per block (2 key tiles of 32)
 constexpr int kOwnKeys = 32;    // own keys per block (1 key tile)
 constexpr float kLn2 = 0.693147180559945309f;
+// Lazy rescaling. The running max of a slot only moves when a block raises its scaled scores by more than kSlack
+// (log2 units), so p = exp2(s - m) <= 2^kSlack; the power-of-two frame E of the V scales (fv = vs / 2^E) only
+// moves when a block's largest V scale leaves [2^(E - kFrame), 2^(E + kFrame)), so fv < 2^kFrame and
+// P' = p fv < 2^15 stays inside fp16. The accumulator is rescaled only when either moves.
+constexpr float kSlack = 8.0f;
+constexpr int kFrame = 7;
+constexpr int kNoFrame = -1000000;
 
 struct AttnArgs {
   const uint16_t* q;
@@ -74,6 +81,7 @@ struct alignas(16) Smem {
   alignas(16) float kb[2][kBlockKeys];         // 0, or -inf for a masked key
   alignas(16) float fv[2][kBlockKeys];         // V scale of key j divided by 2^E_b
   int eb[2];                                   // E_b
+  int ef;                                      // the frame prefix_store gives the next block (kNoFrame: none yet)
   float red[2][kWaves];
 };
 
@@ -173,11 +181,15 @@ __device__ __forceinline__ void prefix_load(const AttnArgs& p, int s, int g, int
   }
   r.sc = 0.0f;
   r.ok = 0;
-  if (tid < 2 * kBlockKeys) {
-    const int key = tid % kBlockKeys, j = j0 + key;
+  // wave 0 reads the K scales and the key mask, wave 1 the V scales (the choice is wave-uniform, so the base
+  // pointers stay scalar)
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (wv < 2) {
+    const int j = j0 + (tid & 63);
+    const float* sc = (wv == 0 ? p.ks : p.vs) + head_base;
     if (j < p.T) {
-      r.sc = tid < kBlockKeys ? p.ks[head_base + j] : p.vs[head_base + j];
-      r.ok = p.kvalid ? (p.kvalid[(int64_t)s * p.T + j] != 0) : 1;
+      r.sc = sc[j];
+      r.ok = (wv == 0 && p.kvalid) ? (p.kvalid[(int64_t)s * p.T + j] != 0) : 1;
     }
   }
 }
@@ -238,9 +250,20 @@ __device__ __forceinline__ void prefix_store(Smem<D>& sm, int buf, const PrefixR
     sm.gk[buf][tid] = r.ok ? r.sc : 0.0f;
     sm.kb[buf][tid] = r.ok ? 0.0f : -INFINITY;
   } else if (tid < 2 * kBlockKeys) {
-    const int e = exp_above(od_wave_max(r.sc));
-    sm.fv[buf][tid - kBlockKeys] = ldexpf(r.sc, -e);
-    if (tid == kBlockKeys) sm.eb[buf] = e;
+    // the block's V scales in the current power-of-two frame (kept in LDS; only wave 1 reads and writes it, and
+    // the workgroup barrier between two blocks orders its accesses)
+    // common case, two ballots: every scale below 2^(frame + kFrame) and one at least 2^(frame - kFrame - 1);
+    // otherwise (rare, and the first block) the frame moves to the exponent of the block's largest scale
+    int e_frame = sm.ef;
+    const bool keep = e_frame != kNoFrame &&
+                      __builtin_amdgcn_ballot_w64(r.sc >= ldexpf(1.0f, e_frame + kFrame)) == 0 &&
+                      __builtin_amdgcn_ballot_w64(r.sc >= ldexpf(1.0f, e_frame - kFrame - 1)) != 0;
+    if (!keep) e_frame = exp_above(od_wave_max(r.sc));
+    sm.fv[buf][tid - kBlockKeys] = ldexpf(r.sc, -e_frame);
+    if (tid == kBlockKeys) {
+      sm.eb[buf] = e_frame;
+      sm.ef = e_frame;
+    }
   }
 }
 
@@ -281,9 +304,25 @@ __device__ __forceinline__ void attend_block(const Smem<D>& sm, int buf, const h
     }
   }
   mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-  const float m_new = fmaxf(m_run, mloc * c_i);
-  const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
-  const float alpha = __builtin_amdgcn_exp2f(m_run - m_safe);
+  const float mc = mloc * c_i;
+  const int eb = sm.eb[buf];
+  // rescale (wave-uniform branch) only if some slot's max grows by more than kSlack or the V frame moved. Each slot
+  // moves its own max only on its own condition (the others get alpha = exp2(0) = 1), so a slot's arithmetic does
+  // not depend on which slots share its wave and option order cannot change a result.
+  const bool grow = mc > m_run + kSlack;
+  if (__builtin_amdgcn_ballot_w64(grow) != 0 || eb != e_run) {
+    const float m_new = grow ? mc : m_run;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+    const float rs = ldexpf(alpha, e_run - eb);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] *= rs;
+    l_run *= alpha;
+    m_run = m_new;
+    e_run = eb;
+  }
+  const float m_safe = m_run == -INFINITY ? 0.0f : m_run;
   float psum = 0.0f;
   half8 pb[2 * KT];
 #pragma unroll
@@ -303,15 +342,7 @@ __device__ __forceinline__ void attend_block(const Smem<D>& sm, int buf, const h
     }
   }
   psum += __shfl_xor(psum, 32, 64);
-  l_run = l_run * alpha + psum;
-  m_run = m_new;
-  const int eb = sm.eb[buf];
-  const float rs = ldexpf(alpha, e_run - eb);
-  e_run = eb;
-#pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[dt][r] *= rs;
+  l_run += psum;
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) {
 #pragma unroll
@@ -412,6 +443,9 @@ __device__ __forceinline__ void own_stage(const AttnArgs& p, Smem<D>& sm, int ro
     const bool ok = tid < n_keys;
     sm.gk[0][tid] = ok ? ldexpf(1.0f, -ek) : 0.0f;
     sm.kb[0][tid] = ok ? 0.0f : -INFINITY;
+    // V' = V 2^ev, so the block's frame is -ev with fv = 1. (Not the running frame: which frame the accumulator
+    // is in when a row's own block comes depends on the rows before it in the tile, and a P' that is an fp16
+    // subnormal in one frame and normal in another would round differently, breaking option-order invariance.)
     sm.fv[0][tid] = 1.0f;
     if (tid == 0) sm.eb[0] = -ev;
   }
@@ -470,7 +504,8 @@ __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) 
   }
 
   float m_run = -INFINITY, l_run = 0.0f;
-  int e_run = 0;
+  int e_run = 0;  // the V-scale frame the accumulator is in (follows the blocks' frames)
+  if (threadIdx.x == kBlockKeys) sm.ef = kNoFrame;  // read and written by this wave only (prefix_store)
   v16f o[D / 32];
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) o[dt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
