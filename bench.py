@@ -51,51 +51,71 @@ def parse():
     return ap.parse_args()
 
 
-class KernelTimer:
-    """Wraps a kernels.* entry point and brackets every call with HIP events on the current stream (the stream the
-    kernel is launched on), accumulating its algorithmic work."""
+class AbiTimer:
+    """Brackets every call of one C-ABI entry point with HIP events on the current stream (the stream its kernels
+    are launched on) and accumulates the call's algorithmic work, computed from the ABI arguments. It replaces the
+    entry point on the loaded library, so the events enclose the launch only (not the Python argument checks
+    around it)."""
 
-    def __init__(self, fn, work):
+    def __init__(self, name, work):
         import torch
-        self.fn, self.work, self.torch = fn, work, torch
-        self.events, self.units, self.active = [], [], False
 
-    def __call__(self, *a, **k):
+        from opendecider_amd import _lib
+        self.L = _lib.lib()
+        self.name, self.fn, self.work, self.torch = name, getattr(self.L, name), work, torch
+        self.events, self.units, self.active = [], [], False
+        setattr(self.L, name, self)
+
+    def __call__(self, *a):
         if not self.active:
-            return self.fn(*a, **k)
+            return self.fn(*a)
         e0, e1 = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
         e0.record()
-        r = self.fn(*a, **k)
+        r = self.fn(*a)
         e1.record()
         self.events.append((e0, e1))
-        self.units.append(self.work(*a, **k))
+        self.units.append(self.work(*a))
         return r
 
     def summary(self):
         ms = [e0.elapsed_time(e1) for e0, e1 in self.events]
         n = len(ms)
-        tot_ms = sum(ms)
-        tot_units = [sum(u[i] for u in self.units) for i in range(len(self.units[0]))] if n else []
-        return n, tot_ms, tot_units
+        tot = [sum(u[i] for u in self.units) for i in range(len(self.units[0]))] if n else [0, 0]
+        return n, sum(ms), tot
+
+    def reset(self):
+        self.events, self.units = [], []
 
 
-def gemm_work(a, sa, w, sw, bias=None, residual=None, out=None, want_out=True, want_acc=False):
-    M, K = a.shape
-    N = w.shape[0]
-    return (2 * M * N * K, M * K + N * K + 2 * M * N + (2 * M * N if residual is not None else 0))
+# (work units from the raw arguments of each entry point, in include/od_mi355x.h order)
+def gemm_work(a, lda, sa, w, ldw, sw, bias, residual, ldr, out, ldo, acc, ldacc, M, N, K, stream):
+    return (2 * M * N * K, M * K + N * K + 2 * M * N + (2 * M * N if residual else 0))
 
 
-def attn_work(q, k_own, v_own, kq, ks, vq, vs, scale, kvalid=None, row_counts=None, length=None, out=None,
-              return_lse=False, row_start=None, max_rows=None):
-    R, Hq, t, D = q.shape
-    Ns, Hkv, cap, _ = kq.shape
-    T = length
+def attn_work(*a):
+    R, Hq, Hkv, t, D, Ns, T = a[24:31]
     rows_per_state = R // Ns
     flops_prefix = 4 * Ns * Hq * rows_per_state * t * T * D
     flops_own = 4 * R * Hq * t * (t + 1) // 2 * D
     # algorithmic HBM bytes: int8 state K/V + fp32 scales once, q / own k,v / out once
     bytes_ = 2 * Ns * Hkv * T * D + 2 * Ns * Hkv * T * 4 + 2 * R * Hq * t * D * 2 + 2 * R * Hkv * t * D * 2
     return (flops_prefix + flops_own, bytes_)
+
+
+def wide_work(*a):
+    B, H, G, T, S, DK, DV, causal = a[19:27]
+    pairs = B * H * (T * S - (T * (T - 1) // 2 if causal and T == S else 0))
+    return (2 * pairs * (DK + DV), 2 * (B * H * T * DK + 2 * B * G * S * DK + B * H * T * DV))
+
+
+def append_work(x, B, H, n, D, *rest):
+    return (B * H * n * D, B * H * n * D * 3 + B * H * n * 4)
+
+
+# HBM-side traffic of od_w8a8_gemm per launch at M = 4096 (bytes), from two rocprofv3 --pmc passes (FETCH_SIZE,
+# then WRITE_SIZE) over the four layer GEMMs, each counter scaled by its reading for a plain 256 MiB device copy
+# (fetch x2.000, write x1.000); the summary is profiles/w8a8_gemm_traffic_M4096.md.
+GEMM_TRAFFIC_M4096 = {(6144, 4096): 218.6e6, (4096, 4096): 168.0e6, (24576, 4096): 806.3e6, (4096, 12288): 369.3e6}
 
 
 def cpu_baseline(args):
@@ -171,10 +191,9 @@ def run_decision(args):
     ids_state = torch.randint(0, cfg.vocab, (B, S), generator=g, device=dev)
     ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g, device=dev)
     caches = dec.new_state_caches(B, S)
-    gemm_t = KernelTimer(kernels.w8a8_gemm, gemm_work)
-    wide_t = KernelTimer(kernels.wide_attn, wide_work)
-    attn_t = KernelTimer(kernels.branched_attn, attn_work)
-    kernels.w8a8_gemm, kernels.wide_attn, kernels.branched_attn = gemm_t, wide_t, attn_t
+    gemm_t = AbiTimer("od_w8a8_gemm", gemm_work)
+    wide_t = AbiTimer("od_wide_attn", wide_work)
+    attn_t = AbiTimer("od_branched_attn", attn_work)
 
     def decide():
         for kc, vc in caches:
@@ -243,9 +262,8 @@ def run_wide_choice(args):
                          .to(torch.bfloat16))
     records = [torch.randint(0, cfg.vocab, (1, rec), generator=g, device=dev) for _ in range(n_rec + args.warmup)]
     ids = torch.randint(0, cfg.vocab, (1, n_req * n_opt, t), generator=g, device=dev)
-    app_t = KernelTimer(kernels.kv_quant_append, append_work)
-    attn_t = KernelTimer(kernels.branched_attn, attn_work)
-    kernels.kv_quant_append, kernels.branched_attn = app_t, attn_t
+    app_t = AbiTimer("od_kv_quant_append", append_work)
+    attn_t = AbiTimer("od_branched_attn", attn_work)
     # warm-up: one record + one scoring pass, then rewind the caches
     for i in range(args.warmup):
         dec.prefill(records[n_rec + i], caches)
@@ -264,7 +282,7 @@ def run_wide_choice(args):
         app_t.active = False
         n_ap, ms_ap, _ = app_t.summary()
         app_ms.append(ms_ap)
-        app_t.events, app_t.units = [], []
+        app_t.reset()
         attn_t.active = True
         t0 = time.perf_counter()
         out = dec.score(ids, caches)
@@ -328,9 +346,11 @@ def main():
     ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g, device=dev)
     torch.cuda.synchronize()
 
-    gemm_t = KernelTimer(kernels.w8a8_gemm, gemm_work)
-    attn_t = KernelTimer(kernels.branched_attn, attn_work)
-    kernels.w8a8_gemm, kernels.branched_attn = gemm_t, attn_t
+    gemm_t = AbiTimer("od_w8a8_gemm", gemm_work)
+    attn_t = AbiTimer("od_branched_attn", attn_work)
+    gemm_shapes = []
+    orig_work = gemm_t.work
+    gemm_t.work = lambda *a: (gemm_shapes.append((a[14], a[15])), orig_work(*a))[1]
 
     for _ in range(args.warmup):
         out = dec.score(ids, states)
@@ -346,6 +366,8 @@ def main():
 
     ms_per_step = dt / args.steps * 1e3
     n_g, ms_g, (ops_g, bytes_g) = gemm_t.summary()
+    known = [GEMM_TRAFFIC_M4096.get(sh) for sh in gemm_shapes]
+    traffic = sum(known) / len(known) if known and None not in known and args.tokens * args.options * args.requests == 4096 else None
     n_a, ms_a, (fl_a, by_a) = attn_t.summary()
     gemm_tops = ops_g / (ms_g * 1e-3) / 1e12
     attn_tflops = fl_a / (ms_a * 1e-3) / 1e12
@@ -370,7 +392,9 @@ def main():
                    "layers": cfg.n_layers, "tokens_per_layer": B * n_opt * t},
         "roofline": {"kernel": "od_w8a8_gemm (all 4 layer GEMMs)", "bound": "mfma",
                      "achieved": gemm_tops, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": gemm_tops / INT8_PEAK_TOPS, "traffic": None,
+                     "frac": gemm_tops / INT8_PEAK_TOPS, "traffic": traffic,
+                     "traffic_unit": "bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE)",
+                     "algorithmic_bytes": bytes_g / max(n_g, 1),
                      "note": "int8 ops (TOPS) per launch over launch duration (HIP events, timed region)",
                      "launches": n_g, "avg_launch_us": ms_g / max(n_g, 1) * 1e3},
         "attention": {"kernel": "od_branched_attn", "tflops": attn_tflops, "frac_of_bf16_mfma": attn_tflops /
