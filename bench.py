@@ -41,11 +41,13 @@ def parse():
     ap.add_argument("--options", type=int, default=32)
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--state", type=int, default=2048)
-    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice"], default="scoring",
+    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm_traffic"], default="scoring",
                     help="scoring (default): the metric's option-row scoring pass over cached 2048-token states; "
                          "decision: full decision forward from token ids (4 requests, 4096-token states prefilled, "
                          "64 options x 24 tokens); wide_choice: a 32768-token int8 state growing by 256-token "
-                         "records, 2 requests x 255 options x 12 tokens scored after each record")
+                         "records, 2 requests x 255 options x 12 tokens scored after each record; gemm_traffic: "
+                         "the run the GEMM traffic counters are read on (a 256 MiB device copy to calibrate them, "
+                         "then two scoring passes through 2 layers, i.e. each M = 4096 GEMM shape twice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-repeats", type=int, default=3)
     return ap.parse_args()
@@ -312,6 +314,38 @@ def run_wide_choice(args):
     }
 
 
+def run_gemm_traffic(args):
+    """The run profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE for roofline.traffic: a 256 MiB device copy
+    (known bytes, to calibrate the counters), then two scoring passes through 2 layers (M = 4096: QKV, O, gate+up,
+    down each twice)."""
+    import torch
+
+    from opendecider_amd import decoder as dmod
+    from opendecider_amd.kv_cache import Int8KVCache
+    dev = "cuda:0"
+    x = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    cfg = dmod.DecoderConfig(n_layers=2)
+    dec = dmod.random_decoder(cfg, seed=0, device=dev, max_pos=2048 + 32)
+    g = torch.Generator(device=dev).manual_seed(1)
+    states = []
+    for _ in range(cfg.n_layers):
+        pair = []
+        for _ in range(2):
+            c = Int8KVCache(8, cfg.n_kv_heads, cfg.head_dim, 2048, dev)
+            c.append(torch.randn(8, cfg.n_kv_heads, 2048, cfg.head_dim, generator=g, device=dev).to(torch.bfloat16))
+            pair.append(c)
+        states.append(tuple(pair))
+    ids = torch.randint(0, cfg.vocab, (8, 32, 16), generator=g, device=dev)
+    for _ in range(2):
+        dec.score(ids, states)
+    torch.cuda.synchronize()
+    return {"workload": "gemm_traffic", "copy_bytes": 256 << 20, "layers": 2, "passes": 2, "tokens_per_layer": 4096}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -321,7 +355,7 @@ def main():
     import torch
     if args.workload != "scoring":
         torch.cuda.set_device(0)
-        fn = run_decision if args.workload == "decision" else run_wide_choice
+        fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm_traffic": run_gemm_traffic}[args.workload]
         print(json.dumps(fn(args)))
         return
 
