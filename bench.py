@@ -104,6 +104,52 @@ def attn_work(*a):
     return (flops_prefix + flops_own, bytes_)
 
 
+def staged_work(*a):
+    # od_branched_attn_staged: the same work as od_branched_attn (its arguments sit three places earlier)
+    R, Hq, Hkv, t, D, Ns, T = a[21:28]
+    return attn_work(*([None] * 24 + [R, Hq, Hkv, t, D, Ns, T]))
+
+
+def stage_work(*a):
+    # od_attn_stage: part of the same attention (its work is counted once, on the attention call)
+    return (0, 0)
+
+
+ATTN_KERNELS = "od_attn_stage + od_branched_attn_staged (or od_branched_attn)"
+
+
+class AttnTimers:
+    """The branched attention's entry points timed together: od_branched_attn (int8 path), od_attn_stage and
+    od_branched_attn_staged (staged path)."""
+
+    def __init__(self):
+        self.timers = [AbiTimer("od_branched_attn", attn_work), AbiTimer("od_attn_stage", stage_work),
+                       AbiTimer("od_branched_attn_staged", staged_work)]
+
+    @property
+    def active(self):
+        return self.timers[0].active
+
+    @active.setter
+    def active(self, v):
+        for t in self.timers:
+            t.active = v
+
+    def summary(self):
+        n, ms, tot = 0, 0.0, [0, 0]
+        for t in self.timers:
+            tn, tms, ttot = t.summary()
+            if t.name != "od_attn_stage":
+                n += tn
+            ms += tms
+            tot = [tot[0] + ttot[0], tot[1] + ttot[1]]
+        return n, ms, tot
+
+    def reset(self):
+        for t in self.timers:
+            t.reset()
+
+
 def wide_work(*a):
     B, H, G, T, S, DK, DV, causal = a[19:27]
     pairs = B * H * (T * S - (T * (T - 1) // 2 if causal and T == S else 0))
@@ -195,7 +241,7 @@ def run_decision(args):
     caches = dec.new_state_caches(B, S)
     gemm_t = AbiTimer("od_w8a8_gemm", gemm_work)
     wide_t = AbiTimer("od_wide_attn", wide_work)
-    attn_t = AbiTimer("od_branched_attn", attn_work)
+    attn_t = AttnTimers()
 
     def decide():
         for kc, vc in caches:
@@ -236,7 +282,7 @@ def run_decision(args):
         "state_attention": {"kernel": "od_wide_attn (causal)", "tflops": fl_w / (ms_w * 1e-3) / 1e12 if n_w else 0,
                             "frac_of_bf16_mfma": fl_w / (ms_w * 1e-3) / 1e12 / BF16_PEAK_TFLOPS if n_w else 0,
                             "launches": n_w, "avg_launch_us": ms_w / max(n_w, 1) * 1e3},
-        "row_attention": {"kernel": "od_branched_attn", "tflops": fl_a / (ms_a * 1e-3) / 1e12 if n_a else 0,
+        "row_attention": {"kernel": ATTN_KERNELS, "tflops": fl_a / (ms_a * 1e-3) / 1e12 if n_a else 0,
                           "algorithmic_gbs": by_a / (ms_a * 1e-3) / 1e9 if n_a else 0, "launches": n_a},
         "time_share": {"gemm": ms_g / tot_ms, "state_attention": ms_w / tot_ms, "row_attention": ms_a / tot_ms},
     }
@@ -265,7 +311,7 @@ def run_wide_choice(args):
     records = [torch.randint(0, cfg.vocab, (1, rec), generator=g, device=dev) for _ in range(n_rec + args.warmup)]
     ids = torch.randint(0, cfg.vocab, (1, n_req * n_opt, t), generator=g, device=dev)
     app_t = AbiTimer("od_kv_quant_append", append_work)
-    attn_t = AbiTimer("od_branched_attn", attn_work)
+    attn_t = AttnTimers()
     # warm-up: one record + one scoring pass, then rewind the caches
     for i in range(args.warmup):
         dec.prefill(records[n_rec + i], caches)
@@ -304,7 +350,7 @@ def run_wide_choice(args):
                                 f"{n_req} requests x {n_opt} options x {t} tokens after each record; 9B dims"),
                    "state_tokens": S0, "records": n_rec, "record_tokens": rec, "requests": n_req,
                    "options": n_opt, "tokens_per_option": t, "layers": cfg.n_layers},
-        "attention": {"kernel": "od_branched_attn", "algorithmic_gbs": gbs, "frac_of_hbm": gbs / HBM_PEAK_GBS,
+        "attention": {"kernel": ATTN_KERNELS, "algorithmic_gbs": gbs, "frac_of_hbm": gbs / HBM_PEAK_GBS,
                       "tflops": fl_a / (ms_a * 1e-3) / 1e12, "launches": n_a,
                       "avg_launch_us": ms_a / max(n_a, 1) * 1e3},
         "append_per_record": {"full_prefill_ms": sum(rec_ms) / n_rec,
@@ -381,7 +427,7 @@ def main():
     torch.cuda.synchronize()
 
     gemm_t = AbiTimer("od_w8a8_gemm", gemm_work)
-    attn_t = AbiTimer("od_branched_attn", attn_work)
+    attn_t = AttnTimers()
     gemm_shapes = []
     orig_work = gemm_t.work
     gemm_t.work = lambda *a: (gemm_shapes.append((a[14], a[15])), orig_work(*a))[1]
@@ -431,7 +477,7 @@ def main():
                      "algorithmic_bytes": bytes_g / max(n_g, 1),
                      "note": "int8 ops (TOPS) per launch over launch duration (HIP events, timed region)",
                      "launches": n_g, "avg_launch_us": ms_g / max(n_g, 1) * 1e3},
-        "attention": {"kernel": "od_branched_attn", "tflops": attn_tflops, "frac_of_bf16_mfma": attn_tflops /
+        "attention": {"kernel": ATTN_KERNELS, "tflops": attn_tflops, "frac_of_bf16_mfma": attn_tflops /
                       BF16_PEAK_TFLOPS, "algorithmic_gbs": attn_gbs, "frac_of_hbm": attn_gbs / HBM_PEAK_GBS,
                       "launches": n_a, "avg_launch_us": ms_a / max(n_a, 1) * 1e3},
         "time_share": {"gemm": ms_g / (ms_per_step * args.steps), "attention": ms_a / (ms_per_step * args.steps)},

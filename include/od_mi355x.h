@@ -88,7 +88,8 @@ int od_kv_quant_append(const uint16_t* x, int64_t B, int64_t H, int64_t n_new, i
  * Replaces: _split_attention (src/opendecider/prefix_attn.py:43-76) with its two wide_attention launches
  * (src/opendecider/wide_attention.py:70-91) and the torch LSE merge (prefix_attn.py:74-76), the per-state loop
  * of _forward (prefix_attn.py:118-128), and the per-layer dequantized copy of the state K/V
- * (prefix_attn.py:145-149): the int8 state is read directly and its scales are folded into the scores.
+ * (prefix_attn.py:145-149): the int8 state is read directly; every workgroup converts each 64-key block in its own
+ * LDS (keys to exact bf16 with their scales applied to the scores, values to fp16 with the scales folded in).
  *   q         bf16 [R, Hq, t, D], element strides (sqr, sqh, sqt)        R option rows of t tokens
  *   k_own     bf16 [R, Hkv, t, D], strides (skr, skh, skt)                each row's own keys (causal)
  *   v_own     bf16 [R, Hkv, t, D], strides (svr, svh, svt)
@@ -132,6 +133,46 @@ int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t 
                            int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
                            int64_t cap, float scale, int64_t nsplit, float* ws, int64_t ws_floats,
                            od_stream_t stream);
+
+/*
+ * od_attn_stage_size — bytes of the block images od_attn_stage writes for a state of Ns x Hkv heads and T keys:
+ * Ns * Hkv * ceil(T / 64) images of 4 * 64 * D + 528 bytes. No GPU work.
+ * Has no counterpart in the reference (a size query for od_attn_stage's output buffer).
+ */
+int od_attn_stage_size(int64_t Ns, int64_t Hkv, int64_t T, int64_t D, int64_t* img_bytes);
+
+/*
+ * od_attn_stage — converts an int8 state into attention block images, once for all the workgroups that read it.
+ * Replaces: the per-layer dequantized copy of the state K/V (prefix_attn.py:145-149, quant.py:40-47
+ * materialize), in the form od_branched_attn_staged consumes: per (state, head, 64-key block) the keys as exact
+ * bf16 integers with their fp32 score multipliers (K scale times the softmax scale), the values in fp16 with the
+ * per-key scales folded in (one rounding per value), both swizzled for the LDS fragment reads, a -inf row for masked
+ * keys and the block's V exponent.
+ *   kq, vq, ks, vs, kvalid, Ns, Hkv, T, cap, D   as od_branched_attn
+ *   scale      the softmax scale of the attention calls that will read the images
+ *   img        device buffer of at least od_attn_stage_size bytes, 16-byte aligned (out)
+ * One launch on `stream`. The images equal what od_branched_attn builds in LDS, so od_branched_attn_staged over
+ * them returns the same bits as od_branched_attn.
+ */
+int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq, const float* vs, const uint8_t* kvalid,
+                  int64_t Ns, int64_t Hkv, int64_t T, int64_t cap, int64_t D, float scale, void* img,
+                  int64_t img_bytes, od_stream_t stream);
+
+/*
+ * od_branched_attn_staged — od_branched_attn_split over block images from od_attn_stage: each workgroup copies the
+ * images straight into LDS (global_load_lds) instead of converting the int8 state itself.
+ * Replaces: the same reference code as od_branched_attn.
+ *   img, img_bytes   the images of the state (Ns, Hkv, T, D and scale as passed to od_attn_stage)
+ *   nsplit, ws, ws_floats   as od_branched_attn_split (nsplit = 1 ignores ws)
+ * Other arguments and the result as od_branched_attn.
+ */
+int od_branched_attn_staged(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                            const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                            const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                            const void* img, int64_t img_bytes, const int32_t* row_start, int64_t max_rows,
+                            uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
+                            int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
+                            float scale, int64_t nsplit, float* ws, int64_t ws_floats, od_stream_t stream);
 
 /*
  * od_wide_attn — flash attention over bf16 K/V.

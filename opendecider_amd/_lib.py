@@ -31,6 +31,12 @@ SIGNATURES = {
                                _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64,
                                _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _c_ptr,
                                _i64, _c_ptr],
+    "od_attn_stage_size": [_i64, _i64, _i64, _i64, _c_ptr],
+    "od_attn_stage": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _c_ptr,
+                      _i64, _c_ptr],
+    "od_branched_attn_staged": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
+                                _c_ptr, _i64, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64,
+                                _i64, _i64, _i64, ctypes.c_float, _i64, _c_ptr, _i64, _c_ptr],
     "od_wide_attn": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64,
                      _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int,
                      ctypes.c_float, _c_ptr],

@@ -8,25 +8,33 @@
 //
 // Work decomposition. A "slot" is one query (option row, token, GQA head of the KV group). Grid =
 // (slot tiles, Hkv, states); a workgroup of 4 waves owns 128 consecutive slots of one (state, KV head) and streams
-// that state's int8 K/V once for all of them; a wave owns 32 slots.
+// that state's K/V once for all of them; a wave owns 32 slots.
+//
+// State blocks. The state's keys go in blocks of 64. A block is consumed from LDS as a "block image": its keys as
+// exact fp16 integers with their fp32 scales beside them, its values in fp16 with the per-key scales folded in, both
+// in the swizzled layout the fragment reads want, a -inf bias row for masked keys and two block constants (V
+// exponent, has-a-masked-key). Two paths build
+// it: od_attn_stage writes every block's image to memory once per state (then each workgroup copies images straight
+// into LDS with global_load_lds, and no workgroup converts anything), and od_branched_attn converts the int8 blocks
+// itself in every workgroup. Both produce the same bytes, so both give bit-identical results.
 //
 // Layout trick. Scores are computed transposed, S^T = K Q^T, on V_MFMA_F32_32X32X16_F16 with the 32 keys of a key
 // tile as rows and the wave's 32 slots as columns. In the MFMA result layout lane l holds slot l % 32, so the
 // running max / sum / rescale of the online softmax are lane-local (plus one exchange with lane l ^ 32), and the
 // probabilities already sit where the second MFMA, O^T += V^T P^T, wants its B operand: k-step m of the P.V
-// product takes registers 8 (m % 2) .. +7 of key tile m / 2. The V tile is written to LDS transposed (V^T, d-major)
-// with the key order inside every 16-key group permuted to match (bits 2 and 3 of the key index swapped).
+// product takes registers 8 (m % 2) .. +7 of key tile m / 2. The V tile is stored transposed (V^T, d-major) with
+// the key order inside every 16-key group permuted to match (bits 2 and 3 of the key index swapped).
 //
-// Numerics (all exact except the fp32 accumulation and the two fp16 roundings noted):
-//  * int8 K/V values are converted to fp16 exactly (|q| <= 127) with the 0x6400 magic-number trick;
-//  * the per-(token, head) fp32 K scale is folded into the scores: s = raw * ks[j] (+ -inf for masked keys);
+// Numerics (fp32 accumulation; the fp16 roundings noted are the only others):
+//  * a state key's int8 values are converted to fp16 exactly (|q| <= 127) and its fp32 K scale multiplies the
+//    score: s = raw * ks[j] (+ -inf for a masked key), so the scores see the exact dequantized keys;
+//  * a state value becomes V' = fp16(q vs 2^-eb), one rounding, with the block's V exponent eb; the accumulator
+//    carries one power-of-two frame and is rescaled when a block's frame differs;
 //  * queries are bf16; each slot's query is multiplied by a power of two 2^e (exact) so that its absmax lies in
 //    [2^14, 2^15) and converted to fp16 (exact: fp16 has more mantissa bits than bf16); the factor 2^-e is folded
 //    with the softmax scale and log2(e) into one per-slot multiplier;
-//  * the row's own bf16 K/V get one power-of-two factor per 32-key block in the same way;
-//  * the per-key V scale is folded into the probabilities, P' = p * vs[j] / 2^E_b, rounded to fp16 (relative
-//    error 2^-11), with E_b the exponent of the block's largest V scale so that P' lies in [0, 1]; the power of two
-//    is carried in the rescale of the accumulator. P and V are therefore never rounded to bf16.
+//  * the row's own bf16 K/V get one power-of-two factor per 32-key block in the same way (exact);
+//  * probabilities p = exp2(y) <= 2^8 are rounded to fp16 for the P.V product; their sum is taken unrounded.
 // Masked keys get a -inf score; a block with no visible key is an exact no-op for a slot; every row's arithmetic is
 // independent of its position among the rows (fixed key order, no cross-slot reduction), so option order cannot
 // change a result.
@@ -35,6 +43,7 @@
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -44,13 +53,10 @@ constexpr int kSlotsPerTile = kWaves * 32;
 constexpr int kBlockKeys = 64;  // prefix keys per block (2 key tiles of 32)
 constexpr int kOwnKeys = 32;    // own keys per block (1 key tile)
 constexpr float kLn2 = 0.693147180559945309f;
-// Lazy rescaling. The running max of a slot only moves when a block raises its scaled scores by more than kSlack
-// (log2 units), so p = exp2(s - m) <= 2^kSlack; the power-of-two frame E of the V scales (fv = vs / 2^E) only
-// moves when a block's largest V scale leaves [2^(E - kFrame), 2^(E + kFrame)), so fv < 2^kFrame and
-// P' = p fv < 2^15 stays inside fp16. The accumulator is rescaled only when either moves.
+// Lazy rescaling: the running max of a slot only moves when a block raises its scaled scores by more than kSlack
+// (log2 units), so p = exp2(s - m) <= 2^kSlack; the accumulator is rescaled only when the max or the V frame moves.
 constexpr float kSlack = 8.0f;
-constexpr int kFrame = 7;
-constexpr int kNoFrame = -1000000;
+constexpr int kNoFrame = -1000000;  // a block without a visible key leaves the accumulator's frame alone
 
 struct AttnArgs {
   const uint16_t* q;
@@ -69,20 +75,34 @@ struct AttnArgs {
   float scale_log2;
   int nsplit;   // key-range splits (1: one pass writes out/lse)
   float* part;  // nsplit > 1: fp32 partials, o [nsplit][R][Hq][t][D] then lse [nsplit][R][Hq][t]
+  const uint8_t* img;  // staged block images [Ns][Hkv][nb] (null: convert the int8 state in the kernel)
 };
 
-// Every array is 16-byte aligned so that fragment and scale accesses compile to single ds_read_b128 /
-// ds_write_b128 instructions (without the alignment the compiler splits them into 4-byte pairs).
+// One block of 64 state keys as the attention reads it from LDS (and as od_attn_stage stores it, byte for byte).
+// Every array is 16-byte aligned so that fragment accesses compile to single ds_read_b128 / ds_write_b128
+// instructions (without the alignment the compiler splits them into 4-byte pairs).
 template <int D>
-struct alignas(16) Smem {
-  alignas(16) _Float16 k[2][kBlockKeys * D];   // [key][d], 16-byte chunks swizzled (k_off)
-  alignas(16) _Float16 vt[2][D * kBlockKeys];  // [d][permuted key], 16-byte chunks swizzled (vt_off)
-  alignas(16) float gk[2][kBlockKeys];         // score multiplier of key j (its K scale)
-  alignas(16) float kb[2][kBlockKeys];         // 0, or -inf for a masked key
-  alignas(16) float fv[2][kBlockKeys];         // V scale of key j divided by 2^E_b
-  int eb[2];                                   // E_b
-  int ef;                                      // the frame prefix_store gives the next block (kNoFrame: none yet)
+struct alignas(16) BlockImg {
+  alignas(16) uint16_t k[kBlockKeys * D];   // [key][d] int8 keys as exact bf16, 16-byte chunks swizzled (k_off)
+  alignas(16) _Float16 vt[D * kBlockKeys];  // [d][permuted key] V', swizzled (vt_off)
+  alignas(16) float gk[kBlockKeys];         // the score multiplier of key j: ks_j scale log2(e) (0 if masked)
+  alignas(16) float kb[kBlockKeys];         // 0, or -inf for a masked key
+  alignas(16) int info[4];                  // the block constants: 0, eb, masked, 0
+};
+static_assert(sizeof(BlockImg<128>) == 4 * kBlockKeys * 128 + 8 * kBlockKeys + 16, "block image layout");
+static_assert(sizeof(BlockImg<64>) == 4 * kBlockKeys * 64 + 8 * kBlockKeys + 16, "block image layout");
+
+template <int D>
+struct alignas(16) Smem {  // double-buffered block images
+  BlockImg<D> b[2];
   float red[2][kWaves];
+};
+
+// The block constants (wave-uniform).
+struct BlockInfo {
+  int ek;      // the block's scores carry 2^-ek (own blocks; 0 for state blocks)
+  int eb;      // the block's values carry 2^-eb (kNoFrame: no visible key)
+  int masked;  // some key of the block is masked (its kb row must be added)
 };
 
 // LDS swizzles. gfx950 LDS: reads see 64 4-byte banks (a 256-byte period) and serve 16 lanes of a ds_read_b128
@@ -132,6 +152,21 @@ __device__ __forceinline__ void i8x4_to_h(uint32_t w, uint32_t& lo, uint32_t& hi
   lo = bits_h2(h2_bits(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
   hi = bits_h2(h2_bits(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
 }
+// 4 int8 (one dword) -> 4 exact bf16 (two dwords): |q| <= 127 has at most 7 significant bits, so the fp32 value's
+// top half is the exact bf16
+__device__ __forceinline__ void i8x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t f0 = __float_as_uint((float)(int8_t)(w & 0xffu)), f1 = __float_as_uint((float)(int8_t)((w >> 8) & 0xffu));
+  const uint32_t f2 = __float_as_uint((float)(int8_t)((w >> 16) & 0xffu)), f3 = __float_as_uint((float)(int8_t)(w >> 24));
+  lo = __builtin_amdgcn_perm(f1, f0, 0x07060302u);
+  hi = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
+}
+
+// an exact fp16 pair times two fp32 factors, each product rounded once to fp16 (v_fma_mixlo/mixhi_f16)
+__device__ __forceinline__ uint32_t h2_times(uint32_t h, float f0, float f1) {
+  const half2v a = h2_bits(h);
+  const half2v r = {(_Float16)__builtin_fmaf((float)a.x, f0, 0.0f), (_Float16)__builtin_fmaf((float)a.y, f1, 0.0f)};
+  return bits_h2(r);
+}
 
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   half2v h = {(_Float16)a, (_Float16)b};
@@ -145,58 +180,84 @@ __device__ __forceinline__ int exp_above(float amax) {
   return e;
 }
 
-// ---------------------------------------------------------------------------------------------- block loaders
-// Prefix block (int8 state, keys j0 .. j0+63): registers first (issued before the previous block's compute), then
-// converted into LDS buffer `buf`.
+// ----------------------------------------------------------------------------------------- state block images
+// Loads of one int8 state block (keys j0 .. j0+63 of one (state, KV head)) go through buffer descriptors over the
+// head's slab: the range check returns zeros for keys at or past the state's length, so no load is predicated, and
+// every per-thread offset is a 32-bit constant (the block's position is the scalar offset).
+struct PrefixSrc {
+  __amdgpu_buffer_rsrc_t k, v, ks, vs, valid;
+  bool has_valid;
+};
+
+template <int D>
+__device__ __forceinline__ PrefixSrc prefix_src(const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
+                                                const uint8_t* kvalid, int Hkv, int T, int cap, int s, int g) {
+  const int64_t head_base = ((int64_t)s * Hkv + g) * cap;
+  PrefixSrc src;
+  src.k = __builtin_amdgcn_make_buffer_rsrc((void*)(kq + head_base * D), (short)0, T * D, 0x00020000);
+  src.v = __builtin_amdgcn_make_buffer_rsrc((void*)(vq + head_base * D), (short)0, T * D, 0x00020000);
+  src.ks = __builtin_amdgcn_make_buffer_rsrc((void*)(ks + head_base), (short)0, T * 4, 0x00020000);
+  src.vs = __builtin_amdgcn_make_buffer_rsrc((void*)(vs + head_base), (short)0, T * 4, 0x00020000);
+  src.has_valid = kvalid != nullptr;
+  src.valid = __builtin_amdgcn_make_buffer_rsrc((void*)(kvalid ? kvalid + (int64_t)s * T : nullptr), (short)0,
+                                                kvalid ? T : 0, 0x00020000);
+  return src;
+}
+
 template <int D>
 struct PrefixRegs {
   uint4 k[(kBlockKeys * D / 16 + kThreads - 1) / kThreads];
   uint2 v[4];
-  float sc;   // thread < 64: K scale of key tid; 64 <= thread < 128: V scale of key tid - 64
-  int ok;     // key valid (thread < 64)
+  float ks, vs;  // lane l of every wave: the K and V scale of key j0 + l (0 past the state's length)
+  int in_range;  // lane l: key j0 + l exists
+  int valid;     // lane l: its kvalid byte (1 without a mask); only read when converting, so the load is not waited
 };
 
 template <int D>
-__device__ __forceinline__ void prefix_load(const AttnArgs& p, int s, int g, int j0, PrefixRegs<D>& r) {
+__device__ __forceinline__ void prefix_load(const PrefixSrc& src, int T, int j0, PrefixRegs<D>& r) {
   const int tid = threadIdx.x;
-  const int64_t head_base = ((int64_t)s * p.Hkv + g) * p.cap;
-  constexpr int kChunks = kBlockKeys * D / 16;  // 16-byte int8 chunks per K block
-  constexpr int kCpk = D / 16;                  // chunks per key
+  constexpr int kChunks = kBlockKeys * D / 16;  // 16-byte int8 chunks per K block; chunk cid = bytes 16 cid ..
 #pragma unroll
   for (int i = 0; i < (kChunks + kThreads - 1) / kThreads; ++i) {
     const int cid = i * kThreads + tid;
-    const int key = cid / kCpk, c = cid % kCpk;
     r.k[i] = make_uint4(0, 0, 0, 0);
-    if (cid < kChunks && j0 + key < p.T)
-      r.k[i] = *reinterpret_cast<const uint4*>(p.kq + (head_base + j0 + key) * D + c * 16);
+    if (cid < kChunks)
+      r.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.k, cid * 16, j0 * D, 0));
   }
   int dg, kg;
   vmap<D>(tid, dg, kg);
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
-    const int key = 4 * kg + a;
     r.v[a] = make_uint2(0, 0);
-    if (tid < 2 * D && j0 + key < p.T)
-      r.v[a] = *reinterpret_cast<const uint2*>(p.vq + (head_base + j0 + key) * D + 8 * dg);
+    if (tid < 2 * D)
+      r.v[a] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.v, (4 * kg + a) * D + 8 * dg, j0 * D, 0));
   }
-  r.sc = 0.0f;
-  r.ok = 0;
-  // wave 0 reads the K scales and the key mask, wave 1 the V scales (the choice is wave-uniform, so the base
-  // pointers stay scalar)
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (wv < 2) {
-    const int j = j0 + (tid & 63);
-    const float* sc = (wv == 0 ? p.ks : p.vs) + head_base;
-    if (j < p.T) {
-      r.sc = sc[j];
-      r.ok = (wv == 0 && p.kvalid) ? (p.kvalid[(int64_t)s * p.T + j] != 0) : 1;
-    }
-  }
+  const int l = tid & 63;
+  r.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.ks, l * 4, j0 * 4, 0));
+  r.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.vs, l * 4, j0 * 4, 0));
+  r.in_range = j0 + l < T;
+  r.valid = src.has_valid ? (int)__builtin_amdgcn_raw_buffer_load_b8(src.valid, l, j0, 0) : 1;
 }
 
+// Converts a loaded int8 block into its image `dst` (LDS, or memory for od_attn_stage) and returns the block
+// constants. K: the int8 values as exact bf16 and beside them the score multipliers gk_j = ks_j scale_log2 (the
+// K scale times the softmax scale in log2 units, one fp32 rounding). V' = fp16(q fv_j), one rounding
+// (v_fma_mix), with the fp32 factor fv_j = vs_j 2^-eb (exact); 2^eb lies above the block's largest V scale, so
+// |V'| < 128. (Rounding fv_j to fp16 first would shift all of key j's values the same way, which under cancellation
+// is visible in the output.) A masked key gets a zero V factor (P V' must stay finite), a zero K scale and a -inf
+// bias. Every wave derives the constants from the same 64 scales, so the waves agree without exchanging them.
 template <int D>
-__device__ __forceinline__ void prefix_store(Smem<D>& sm, int buf, const PrefixRegs<D>& r) {
+__device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, BlockImg<D>& dst, float scale_log2) {
   const int tid = threadIdx.x;
+  const bool ok = r.in_range && r.valid != 0;
+  const float vs_ok = ok ? r.vs : 0.0f;
+  BlockInfo bi;
+  bi.masked = __builtin_amdgcn_ballot_w64(!ok) != 0;
+  bi.ek = 0;
+  const float vmax = od_wave_max_dpp(vs_ok);
+  bi.eb = __builtin_amdgcn_ballot_w64(ok) != 0 ? exp_above(vmax) : kNoFrame;
+  const float fv = ok ? ldexpf(vs_ok, -bi.eb) : 0.0f;  // lane l: key l's V factor
+
   constexpr int kChunks = kBlockKeys * D / 16;
   constexpr int kCpk = D / 16;
 #pragma unroll
@@ -204,18 +265,18 @@ __device__ __forceinline__ void prefix_store(Smem<D>& sm, int buf, const PrefixR
     const int cid = i * kThreads + tid;
     if (cid < kChunks) {
       const int key = cid / kCpk, c = cid % kCpk;
-      // the 16 int8 values become two fp16 chunks, 2c and 2c + 1; lanes with bit 2 set store 2c + 1 first, so
+      // the 16 int8 values become two bf16 chunks, 2c and 2c + 1; lanes with bit 2 set store 2c + 1 first, so
       // that the 8 lanes of a ds_write_b128 bank cycle hit 8 distinct chunks of the 128-byte period
       const int flip = (tid >> 2) & 1;
       const uint32_t a0 = flip ? r.k[i].z : r.k[i].x, a1 = flip ? r.k[i].w : r.k[i].y;
       const uint32_t b0 = flip ? r.k[i].x : r.k[i].z, b1 = flip ? r.k[i].y : r.k[i].w;
       uint4 h0, h1;
-      i8x4_to_h(a0, h0.x, h0.y);
-      i8x4_to_h(a1, h0.z, h0.w);
-      i8x4_to_h(b0, h1.x, h1.y);
-      i8x4_to_h(b1, h1.z, h1.w);
-      *reinterpret_cast<uint4*>(&sm.k[buf][k_off<D>(key, 2 * c + flip)]) = h0;
-      *reinterpret_cast<uint4*>(&sm.k[buf][k_off<D>(key, 2 * c + 1 - flip)]) = h1;
+      i8x4_to_bf16(a0, h0.x, h0.y);
+      i8x4_to_bf16(a1, h0.z, h0.w);
+      i8x4_to_bf16(b0, h1.x, h1.y);
+      i8x4_to_bf16(b1, h1.z, h1.w);
+      *reinterpret_cast<uint4*>(&dst.k[k_off<D>(key, 2 * c + flip)]) = h0;
+      *reinterpret_cast<uint4*>(&dst.k[k_off<D>(key, 2 * c + 1 - flip)]) = h1;
     }
   }
   int dg, kg;
@@ -236,127 +297,251 @@ __device__ __forceinline__ void prefix_store(Smem<D>& sm, int buf, const PrefixR
       cols[half * 4 + 2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
       cols[half * 4 + 3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
     }
+    // the factors of the thread's 4 keys (a V^T dword holds keys 0,1 or keys 2,3 of the group)
+    const float f0 = __shfl(fv, 4 * kg, 64), f1 = __shfl(fv, 4 * kg + 1, 64);
+    const float f2 = __shfl(fv, 4 * kg + 2, 64), f3 = __shfl(fv, 4 * kg + 3, 64);
     const int jj0 = jj_of(4 * kg);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int d = 8 * dg + e;
       uint2 hv;
       i8x4_to_h(cols[e], hv.x, hv.y);
-      *reinterpret_cast<uint2*>(&sm.vt[buf][vt_off(d, jj0 >> 3) + (jj0 & 7)]) = hv;
+      hv.x = h2_times(hv.x, f0, f1);
+      hv.y = h2_times(hv.y, f2, f3);
+      *reinterpret_cast<uint2*>(&dst.vt[vt_off(d, jj0 >> 3) + (jj0 & 7)]) = hv;
     }
   }
-  // scales: wave 0 -> K scales and masks, wave 1 -> V scales with the block's power-of-two normalisation
   if (tid < kBlockKeys) {
-    sm.gk[buf][tid] = r.ok ? r.sc : 0.0f;
-    sm.kb[buf][tid] = r.ok ? 0.0f : -INFINITY;
-  } else if (tid < 2 * kBlockKeys) {
-    // the block's V scales in the current power-of-two frame (kept in LDS; only wave 1 reads and writes it, and
-    // the workgroup barrier between two blocks orders its accesses)
-    // common case, two ballots: every scale below 2^(frame + kFrame) and one at least 2^(frame - kFrame - 1);
-    // otherwise (rare, and the first block) the frame moves to the exponent of the block's largest scale
-    int e_frame = sm.ef;
-    const bool keep = e_frame != kNoFrame &&
-                      __builtin_amdgcn_ballot_w64(r.sc >= ldexpf(1.0f, e_frame + kFrame)) == 0 &&
-                      __builtin_amdgcn_ballot_w64(r.sc >= ldexpf(1.0f, e_frame - kFrame - 1)) != 0;
-    if (!keep) e_frame = exp_above(od_wave_max(r.sc));
-    sm.fv[buf][tid - kBlockKeys] = ldexpf(r.sc, -e_frame);
-    if (tid == kBlockKeys) {
-      sm.eb[buf] = e_frame;
-      sm.ef = e_frame;
-    }
+    dst.gk[tid] = ok ? r.ks * scale_log2 : 0.0f;
+    dst.kb[tid] = ok ? 0.0f : -INFINITY;
   }
+  if (tid == 0) *reinterpret_cast<int4*>(dst.info) = make_int4(bi.ek, bi.eb, bi.masked, 0);
+  return bi;
+}
+
+// The block constants of an image in LDS, as wave-uniform values.
+__device__ __forceinline__ BlockInfo read_info(const int* info) {
+  const int4 v = *reinterpret_cast<const int4*>(info);
+  BlockInfo bi;
+  bi.ek = __builtin_amdgcn_readfirstlane(v.x);
+  bi.eb = __builtin_amdgcn_readfirstlane(v.y);
+  bi.masked = __builtin_amdgcn_readfirstlane(v.z);
+  return bi;
+}
+
+// One global_load_lds_dwordx4: lane l copies 16 bytes from its `src` to LDS byte lds_base + 16 l (lds_base is
+// wave-uniform, passed in M0). Written as inline asm so that the compiler does not track it: the caller waits for it
+// (vmcnt) and orders it with barriers, whereas the compiler would wait for it before every LDS read that it cannot
+// prove disjoint from the copy, which is every read of the other image buffer. The compiler keeps nothing in M0 in
+// these kernels (no LDS DMA, movrel or sendmsg of its own), so setting it here disturbs no live value.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
+               : "memory", "m0");
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(p);
+}
+
+// Copies NBYTES (a multiple of 16) of a staged image into LDS, 16 bytes per lane and no registers: round i moves
+// bytes [4096 i, 4096 (i + 1)), wave w the 1 KiB at 1024 w of it, and lanes of the first wave take the tail.
+// Completion is a vmcnt wait by every thread that issued a part, then a barrier.
+template <int NBYTES>
+__device__ __forceinline__ void copy_bytes(const void* src, void* dst) {
+  constexpr int kRound = kThreads * 16;
+  constexpr int kFull = NBYTES / kRound;
+  constexpr int kTailLanes = (NBYTES - kFull * kRound) / 16;
+  static_assert(NBYTES % 16 == 0 && kTailLanes <= 64, "copy shape");
+  const int tid = threadIdx.x;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const char* s = reinterpret_cast<const char*>(src);
+  const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(dst));
+#pragma unroll
+  for (int i = 0; i < kFull; ++i) dma16(s + i * kRound + tid * 16, d + i * kRound + wave * 1024);
+  if (kTailLanes > 0 && tid < kTailLanes) dma16(s + kFull * kRound + tid * 16, d + kFull * kRound);
 }
 
 // ------------------------------------------------------------------------------------------------- compute
-template <int D, int KT, bool OWN>
-__device__ __forceinline__ void attend_block(const Smem<D>& sm, int buf, const half8 (&qf)[D / 16], float c_i,
-                                             float& m_run, float& l_run, int& e_run, v16f (&o)[D / 32], int own_row,
-                                             int own_j0, int slot_row, int slot_tok) {
+// One block of the online softmax for the wave's 32 slots, in three pieces:
+//  * qk_scores: S^T = K Q^T on V_MFMA_F32_32X32X16_BF16 (exact products; fragment reads KA k-steps ahead);
+//  * softmax_block: y = S gk + kb - m (log2 units; gk the per-key K scale times the softmax scale, kb the mask; own
+//    blocks: y = S c - m with the causal mask), the block max, the running max m moved only when the block raises it
+//    by more than kSlack, p = exp2(y), P to fp16, l = l alpha + sum p; it returns whether the accumulator needs
+//    rescaling (some slot's max moved, or the V frame differs);
+//  * pv_block: O^T += V'^T P^T (fragment reads VA steps ahead).
+// Each slot moves its own max only on its own condition (the others get alpha = exp2(0) = 1), so a slot's arithmetic
+// does not depend on which slots share its wave and option order cannot change a result.
+template <int D, int KT, int KA>
+__device__ __forceinline__ void qk_scores(const uint16_t* kimg, const bf16x8 (&qf)[D / 16], v16f (&s)[KT]) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
-  v16f s[KT];
+  constexpr int KS = D / 16;
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
-    s[kt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int kt = 0; kt < KT; ++kt) s[kt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  bf16x8 kf[KA + 1][KT];
+  auto kread = [&](int ks) {
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      const half8 a = *reinterpret_cast<const half8*>(&sm.k[buf][k_off<D>(kt * 32 + col, ks * 2 + h)]);
-      s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s[kt], 0, 0, 0);
-    }
+    for (int kt = 0; kt < KT; ++kt)
+      kf[ks % (KA + 1)][kt] = *reinterpret_cast<const bf16x8*>(&kimg[k_off<D>(kt * 32 + col, ks * 2 + h)]);
+  };
+#pragma unroll
+  for (int ks = 0; ks < KA; ++ks) kread(ks);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks + KA < KS) kread(ks + KA);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+      s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % (KA + 1)][kt], qf[ks], s[kt], 0, 0, 0);
   }
-  // scores of this lane's slot: key = kt*32 + 8*(r/4) + 4*h + r%4
-  float mloc = -INFINITY;
+  // keep the reads KA k-steps ahead of the MFMAs (left alone, the scheduler sinks each read to its MFMA)
+  __builtin_amdgcn_sched_group_barrier(0x100, KA * KT, 0);
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks + KA < KS) __builtin_amdgcn_sched_group_barrier(0x100, KT, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, KT, 0);
+  }
+}
+
+// masked: some key of the block is masked (only then is the bias row read); c: own blocks' score multiplier
+template <int D, int KT, bool OWN>
+__device__ __forceinline__ bool softmax_block(const float* gk, const float* kb, bool masked, v16f (&s)[KT], float c,
+                                              int eb, float& m_run, float& l_run, int e_run, float& alpha,
+                                              half8 (&pb)[2 * KT], int own_row, int own_j0, int slot_row,
+                                              int slot_tok) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5;
+  const float m_safe = m_run == -INFINITY ? 0.0f : m_run;
+  // this lane's slot sees keys kt*32 + 8*(r/4) + 4*h + r%4
+  if constexpr (OWN) {
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int key0 = kt * 32 + 8 * r4 + 4 * h;
-      const float4 g4 = *reinterpret_cast<const float4*>(&sm.gk[buf][key0]);
-      const float4 b4 = *reinterpret_cast<const float4*>(&sm.kb[buf][key0]);
-      const float gg[4] = {g4.x, g4.y, g4.z, g4.w}, bb[4] = {b4.x, b4.y, b4.z, b4.w};
+    for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float y = fmaf(s[kt][4 * r4 + e], gg[e], bb[e]);
-        if (OWN && !(slot_row == own_row && own_j0 + key0 + e <= slot_tok)) y = -INFINITY;
-        s[kt][4 * r4 + e] = y;
-        mloc = fmaxf(mloc, y);
+      for (int r = 0; r < 16; ++r) {
+        const int key = own_j0 + kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        s[kt][r] = (slot_row == own_row && key <= slot_tok) ? fmaf(s[kt][r], c, -m_safe) : -INFINITY;
       }
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const float4 g4 = *reinterpret_cast<const float4*>(&gk[kt * 32 + 8 * r4 + 4 * h]);
+        s[kt][4 * r4] = fmaf(s[kt][4 * r4], g4.x, -m_safe);
+        s[kt][4 * r4 + 1] = fmaf(s[kt][4 * r4 + 1], g4.y, -m_safe);
+        s[kt][4 * r4 + 2] = fmaf(s[kt][4 * r4 + 2], g4.z, -m_safe);
+        s[kt][4 * r4 + 3] = fmaf(s[kt][4 * r4 + 3], g4.w, -m_safe);
+      }
+    if (masked) {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const float4 b4 = *reinterpret_cast<const float4*>(&kb[kt * 32 + 8 * r4 + 4 * h]);
+          s[kt][4 * r4] += b4.x;
+          s[kt][4 * r4 + 1] += b4.y;
+          s[kt][4 * r4 + 2] += b4.z;
+          s[kt][4 * r4 + 3] += b4.w;
+        }
     }
   }
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-  const float mc = mloc * c_i;
-  const int eb = sm.eb[buf];
-  // rescale (wave-uniform branch) only if some slot's max grows by more than kSlack or the V frame moved. Each slot
-  // moves its own max only on its own condition (the others get alpha = exp2(0) = 1), so a slot's arithmetic does
-  // not depend on which slots share its wave and option order cannot change a result.
-  const bool grow = mc > m_run + kSlack;
-  if (__builtin_amdgcn_ballot_w64(grow) != 0 || eb != e_run) {
-    const float m_new = grow ? mc : m_run;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.0f : m_new));
-    const float rs = ldexpf(alpha, e_run - eb);
+  float amax = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) amax = fmaxf(amax, s[kt][r]);
+  amax = od_xor32_max(amax);
+  // y is relative to the old max; a slot whose block max exceeds it by more than kSlack (or that sees its first key)
+  // moves its max to the block max and shifts its y (wave-uniform branch, rare)
+  const bool grow = m_run == -INFINITY ? amax > -INFINITY : amax > kSlack;
+  alpha = 1.0f;
+  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    const float shift = grow ? amax : 0.0f;
+    const float m_new = m_safe + shift;
+    alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 for a slot's first visible block, 1 if it did not grow
+    if (grow) m_run = m_new;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kt][r] -= shift;
+  }
+  float psum = 0.0f;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pr = __builtin_amdgcn_exp2f(s[kt][r]);
+      psum += pr;
+      pb[kt * 2 + (r >> 3)][r & 7] = (_Float16)pr;
+    }
+  l_run = fmaf(l_run, alpha, od_xor32_sum(psum));
+  const int e_blk = eb == kNoFrame ? e_run : eb;
+  return __builtin_amdgcn_ballot_w64(grow) != 0 || e_blk != e_run;
+}
+
+// the accumulator into the block's frame (and each slot's new max): O *= alpha 2^(e_run - e_blk)
+template <int D>
+__device__ __forceinline__ void rescale(v16f (&o)[D / 32], float alpha, int eb, int& e_run) {
+  const int e_blk = eb == kNoFrame ? e_run : eb;
+  const float rs = ldexpf(alpha, e_run - e_blk);
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[dt][r] *= rs;
+  e_run = e_blk;
+}
+
+template <int D, int KT, int VA>
+__device__ __forceinline__ void pv_block(const _Float16* vtimg, const half8 (&pb)[2 * KT], v16f (&o)[D / 32]) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  constexpr int kVA = VA < 2 * KT ? VA : 2 * KT - 1;
+  half8 vf[kVA + 1][D / 32];
+  auto vread = [&](int m) {
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
+      vf[m % (kVA + 1)][dt] = *reinterpret_cast<const half8*>(&vtimg[vt_off(dt * 32 + col, 2 * m + h)]);
+  };
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] *= rs;
-    l_run *= alpha;
-    m_run = m_new;
-    e_run = eb;
+  for (int m = 0; m < kVA; ++m) vread(m);
+#pragma unroll
+  for (int m = 0; m < 2 * KT; ++m) {
+    if (m + kVA < 2 * KT) vread(m + kVA);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[m % (kVA + 1)][dt], pb[m], o[dt], 0, 0, 0);
   }
-  const float m_safe = m_run == -INFINITY ? 0.0f : m_run;
-  float psum = 0.0f;
+  __builtin_amdgcn_sched_group_barrier(0x100, kVA * (D / 32), 0);
+#pragma unroll
+  for (int m = 0; m < 2 * KT; ++m) {
+    if (m + kVA < 2 * KT) __builtin_amdgcn_sched_group_barrier(0x100, D / 32, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, D / 32, 0);
+  }
+}
+
+// The three pieces in sequence. `mid` runs between the softmax and the P V product (the int8 path issues the next
+// block's global loads there, so that their registers are not held through the score and softmax phases).
+template <int D, int KT, bool OWN, typename Mid>
+__device__ __forceinline__ void attend_block(const uint16_t* kimg, const _Float16* vtimg, const float* gk,
+                                             const float* kb, const bf16x8 (&qf)[D / 16], float c, int eb,
+                                             bool masked, float& m_run, float& l_run, int& e_run, v16f (&o)[D / 32],
+                                             int own_row, int own_j0, int slot_row, int slot_tok, Mid&& mid) {
+  constexpr int KA = 2;
+  v16f s[KT];
+  qk_scores<D, KT, KA>(kimg, qf, s);
+  float alpha;
   half8 pb[2 * KT];
-#pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int key0 = kt * 32 + 8 * r4 + 4 * h;
-      const float4 f4 = *reinterpret_cast<const float4*>(&sm.fv[buf][key0]);
-      const float ff[4] = {f4.x, f4.y, f4.z, f4.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * r4 + e;
-        const float pr = __builtin_amdgcn_exp2f(fmaf(s[kt][r], c_i, -m_safe));
-        psum += pr;
-        pb[kt * 2 + (r >> 3)][r & 7] = (_Float16)(pr * ff[e]);
-      }
-    }
-  }
-  psum += __shfl_xor(psum, 32, 64);
-  l_run += psum;
-#pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) {
-#pragma unroll
-    for (int m = 0; m < 2 * KT; ++m) {
-      const half8 a = *reinterpret_cast<const half8*>(&sm.vt[buf][vt_off(dt * 32 + col, 2 * m + h)]);
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[m], o[dt], 0, 0, 0);
-    }
-  }
+  const bool rs = softmax_block<D, KT, OWN>(gk, kb, masked, s, c, eb, m_run, l_run, e_run, alpha, pb, own_row,
+                                            own_j0, slot_row, slot_tok);
+  mid();
+  if (rs) rescale<D>(o, alpha, eb, e_run);
+  pv_block<D, KT, 1>(vtimg, pb, o);
 }
 
 // Workgroup max of two values (every thread gets both).
 __device__ __forceinline__ void wg_max2(float (&red)[2][kWaves], float& a, float& b) {
-  a = od_wave_max(a);
-  b = od_wave_max(b);
+  a = od_wave_max_dpp(a);
+  b = od_wave_max_dpp(b);
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     red[0][w] = a;
@@ -370,9 +555,14 @@ __device__ __forceinline__ void wg_max2(float (&red)[2][kWaves], float& a, float
   }
 }
 
-// Own keys j0 .. j0+31 of option row `row` (bf16) into LDS buffer 0, scaled by powers of two into fp16.
+// Own keys j0 .. j0+31 of option row `row` into a block image's K and V arrays: the bf16 keys as they are (the
+// score MFMAs take bf16), the bf16 values scaled by one power of two into fp16, V' = V 2^ev (exact), whose frame
+// bi.eb = -ev is the block's own (not the running frame: which frame the accumulator is in when a row's own block
+// comes depends on the rows before it in the tile, and a P V' product that rounds differently in another frame would
+// break option-order invariance).
 template <int D>
-__device__ __forceinline__ void own_stage(const AttnArgs& p, Smem<D>& sm, int row, int g, int j0) {
+__device__ __forceinline__ void own_stage(const AttnArgs& p, float (&red)[2][kWaves], uint16_t* kdst,
+                                          _Float16* vtdst, int row, int g, int j0, BlockInfo& bi) {
   const int tid = threadIdx.x;
   const int n_keys = min(kOwnKeys, p.t - j0);
   const uint16_t* kb = p.k_own + (int64_t)row * p.skr + (int64_t)g * p.skh;
@@ -380,24 +570,22 @@ __device__ __forceinline__ void own_stage(const AttnArgs& p, Smem<D>& sm, int ro
   constexpr int kCpk = D / 8;                 // 8-value chunks per key
   constexpr int kChunks = kOwnKeys * kCpk;    // K chunks of the block
   constexpr int kKIt = (kChunks + kThreads - 1) / kThreads;
-  uint4 kr[kKIt];
-  float ka = 0.0f, va = 0.0f;
 #pragma unroll
   for (int i = 0; i < kKIt; ++i) {
     const int cid = i * kThreads + tid;
     const int key = cid / kCpk, c = cid % kCpk;
-    kr[i] = make_uint4(0, 0, 0, 0);
-    if (cid < kChunks && key < n_keys) kr[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)(j0 + key) * p.skt + 8 * c);
-    const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      ka = fmaxf(ka, fmaxf(fabsf(__uint_as_float(w4[e] << 16)), fabsf(__uint_as_float(w4[e] & 0xffff0000u))));
+    if (cid < kChunks) {
+      uint4 kr = make_uint4(0, 0, 0, 0);
+      if (key < n_keys) kr = *reinterpret_cast<const uint4*>(kb + (int64_t)(j0 + key) * p.skt + 8 * c);
+      *reinterpret_cast<uint4*>(&kdst[k_off<D>(key, c)]) = kr;
+    }
   }
   // V: a thread takes 4 keys x 8 d (kOwnKeys / 4 key groups x D / 8 d groups, threads 0 .. D - 1)
   int dg, kg;
   vmap<D>(tid, dg, kg);
   const bool vact = tid < D;
   uint4 vr[4];
+  float va = 0.0f, unused = 0.0f;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const int key = 4 * kg + a;
@@ -408,22 +596,8 @@ __device__ __forceinline__ void own_stage(const AttnArgs& p, Smem<D>& sm, int ro
     for (int e = 0; e < 4; ++e)
       va = fmaxf(va, fmaxf(fabsf(__uint_as_float(w4[e] << 16)), fabsf(__uint_as_float(w4[e] & 0xffff0000u))));
   }
-  wg_max2(sm.red, ka, va);
-  const int ek = 15 - exp_above(ka), ev = 15 - exp_above(va);  // |x| 2^e < 2^15
-#pragma unroll
-  for (int i = 0; i < kKIt; ++i) {
-    const int cid = i * kThreads + tid;
-    if (cid < kChunks) {
-      const int key = cid / kCpk, c = cid % kCpk;
-      const uint32_t w4[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
-      uint4 hk;
-      uint32_t* ho = &hk.x;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        ho[e] = pack_h2(ldexpf(__uint_as_float(w4[e] << 16), ek), ldexpf(__uint_as_float(w4[e] & 0xffff0000u), ek));
-      *reinterpret_cast<uint4*>(&sm.k[0][k_off<D>(key, c)]) = hk;
-    }
-  }
+  wg_max2(red, va, unused);
+  const int ev = 15 - exp_above(va);  // |x| 2^ev < 2^15
   if (vact) {
     const int jj0 = jj_of(4 * kg);
 #pragma unroll
@@ -436,30 +610,32 @@ __device__ __forceinline__ void own_stage(const AttnArgs& p, Smem<D>& sm, int ro
         vals[a] = ldexpf(__uint_as_float((e & 1) ? (wd & 0xffff0000u) : (wd << 16)), ev);
       }
       uint2 hv = make_uint2(pack_h2(vals[0], vals[1]), pack_h2(vals[2], vals[3]));
-      *reinterpret_cast<uint2*>(&sm.vt[0][vt_off(8 * dg + e, jj0 >> 3) + (jj0 & 7)]) = hv;
+      *reinterpret_cast<uint2*>(&vtdst[vt_off(8 * dg + e, jj0 >> 3) + (jj0 & 7)]) = hv;
     }
   }
-  if (tid < kOwnKeys) {
-    const bool ok = tid < n_keys;
-    sm.gk[0][tid] = ok ? ldexpf(1.0f, -ek) : 0.0f;
-    sm.kb[0][tid] = ok ? 0.0f : -INFINITY;
-    // V' = V 2^ev, so the block's frame is -ev with fv = 1. (Not the running frame: which frame the accumulator
-    // is in when a row's own block comes depends on the rows before it in the tile, and a P' that is an fp16
-    // subnormal in one frame and normal in another would round differently, breaking option-order invariance.)
-    sm.fv[0][tid] = 1.0f;
-    if (tid == 0) sm.eb[0] = -ev;
-  }
+  bi.ek = 0;
+  bi.eb = -ev;
+  bi.masked = 0;  // the causal mask is applied per score
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) {
-  __shared__ Smem<D> sm;
-  const int s = blockIdx.z / p.nsplit, sp = blockIdx.z % p.nsplit, g = blockIdx.y;
+template <int D, bool STAGED>
+__device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& sm) {
+  // XCD-aware work order: workgroups are dealt round-robin over the 8 XCDs, so flat id f runs on XCD f % 8. Work item
+  // w = (state split, KV head, slot tile) with the tile fastest is given to XCD (w's range), so that the tiles of
+  // one (state, head) share one XCD's L2 for the state blocks they all stream.
+  const int tiles = gridDim.x;
+  const int n_items = tiles * gridDim.y * gridDim.z;
+  const int f = blockIdx.x + tiles * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int xcd = f & 7, local = f >> 3, per = n_items >> 3, rem = n_items & 7;
+  const int w = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int tile = w % tiles, zy = w / tiles;
+  const int g = zy % gridDim.y, zz = zy / gridDim.y;
+  const int s = zz / p.nsplit, sp = zz % p.nsplit;
   const int row0 = p.row_start ? p.row_start[s] : 0;
   const int nrows = p.row_start ? p.row_start[s + 1] - row0 : p.R;
   const int per_row = p.t * p.rep;
   const int nslots = nrows * per_row;
-  const int slot_base = blockIdx.x * kSlotsPerTile;
+  const int slot_base = tile * kSlotsPerTile;
   if (slot_base >= nslots) return;  // uniform over the workgroup
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -474,58 +650,66 @@ __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) 
     slot_head = g * p.rep + rem % p.rep;
   }
 
-  // query fragments: lane holds Q[slot][ks*16 + 8h .. +8] for ks = 0 .. D/16-1, scaled by 2^eq into fp16
-  half8 qf[D / 16];
-  float c_i;  // per-slot multiplier: softmax scale * log2(e) * 2^-eq
+  // ---- prefix: the state's blocks; split sp of nsplit takes the blocks [sp * bps, (sp + 1) * bps)
+  const int nb_all = (p.T + kBlockKeys - 1) / kBlockKeys;
+  const int bps = (nb_all + p.nsplit - 1) / p.nsplit;
+  const int b_lo = min(nb_all, sp * bps), b_hi = min(nb_all, b_lo + bps);
+  // the first block's copy (staged path) goes out before the queries are read
+  const BlockImg<D>* img = STAGED ? reinterpret_cast<const BlockImg<D>*>(p.img) + ((int64_t)s * p.Hkv + g) * nb_all
+                                  : nullptr;
+  if (STAGED && b_hi > b_lo) copy_bytes<(int)sizeof(BlockImg<D>)>(img + b_lo, &sm.b[0]);
+
+  // query fragments: lane holds Q[slot][ks*16 + 8h .. +8] for ks = 0 .. D/16-1, bf16 as given
+  bf16x8 qf[D / 16];
   {
-    uint4 raw[D / 16];
-    float qa = 0.0f;
     const uint16_t* qp = p.q + (int64_t)slot_row * p.sqr + (int64_t)slot_head * p.sqh + (int64_t)slot_tok * p.sqt;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      raw[ks] = slot_ok ? *reinterpret_cast<const uint4*>(qp + ks * 16 + 8 * h) : make_uint4(0, 0, 0, 0);
-      const uint32_t w4[4] = {raw[ks].x, raw[ks].y, raw[ks].z, raw[ks].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        qa = fmaxf(qa, fmaxf(fabsf(__uint_as_float(w4[e] << 16)), fabsf(__uint_as_float(w4[e] & 0xffff0000u))));
-    }
-    qa = fmaxf(qa, __shfl_xor(qa, 32, 64));
-    const int eq = 15 - exp_above(qa);
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      const uint32_t w4[4] = {raw[ks].x, raw[ks].y, raw[ks].z, raw[ks].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        qf[ks][2 * e] = (_Float16)ldexpf(__uint_as_float(w4[e] << 16), eq);
-        qf[ks][2 * e + 1] = (_Float16)ldexpf(__uint_as_float(w4[e] & 0xffff0000u), eq);
-      }
-    }
-    c_i = ldexpf(p.scale_log2, -eq);
+    for (int ks = 0; ks < D / 16; ++ks)
+      qf[ks] = __builtin_bit_cast(bf16x8, slot_ok ? *reinterpret_cast<const uint4*>(qp + ks * 16 + 8 * h)
+                                                  : make_uint4(0, 0, 0, 0));
   }
 
   float m_run = -INFINITY, l_run = 0.0f;
-  int e_run = 0;  // the V-scale frame the accumulator is in (follows the blocks' frames)
-  if (threadIdx.x == kBlockKeys) sm.ef = kNoFrame;  // read and written by this wave only (prefix_store)
+  int e_run = 0;  // the power-of-two frame the accumulator is in (follows the blocks' V exponents)
   v16f o[D / 32];
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) o[dt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  // ---- prefix: the state's int8 K/V, 64 keys per block, double buffered; split sp of nsplit takes the blocks
-  // [sp * bps, (sp + 1) * bps)
-  const int nb_all = (p.T + kBlockKeys - 1) / kBlockKeys;
-  const int bps = (nb_all + p.nsplit - 1) / p.nsplit;
-  const int b_lo = min(nb_all, sp * bps), b_hi = min(nb_all, b_lo + bps);
   if (b_hi > b_lo) {
-    PrefixRegs<D> pr;
-    prefix_load<D>(p, s, g, b_lo * kBlockKeys, pr);
-    prefix_store<D>(sm, 0, pr);
-    __syncthreads();
-    for (int b = b_lo; b < b_hi; ++b) {
-      const int cur = (b - b_lo) & 1;
-      if (b + 1 < b_hi) prefix_load<D>(p, s, g, (b + 1) * kBlockKeys, pr);
-      attend_block<D, 2, false>(sm, cur, qf, c_i, m_run, l_run, e_run, o, 0, 0, slot_row, slot_tok);
-      if (b + 1 < b_hi) prefix_store<D>(sm, cur ^ 1, pr);
+    if constexpr (STAGED) {
+      // block images straight from memory into the double-buffered LDS images
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      for (int b = b_lo; b < b_hi; ++b) {
+        const int buf = (b - b_lo) & 1;
+        const BlockImg<D>& bk = sm.b[buf];
+        const BlockInfo ci = read_info(bk.info);
+        // the other buffer was last read before the previous barrier
+        if (b + 1 < b_hi) copy_bytes<(int)sizeof(BlockImg<D>)>(img + b + 1, &sm.b[buf ^ 1]);
+        attend_block<D, 2, false>(bk.k, bk.vt, bk.gk, bk.kb, qf, 0.0f, ci.eb, ci.masked != 0, m_run, l_run, e_run, o,
+                                  0, 0, slot_row, slot_tok, [] {});
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      }
+    } else {
+      // the int8 state, converted here: registers first (loads issued during the previous block), then LDS
+      const PrefixSrc src = prefix_src<D>(p.kq, p.ks, p.vq, p.vs, p.kvalid, p.Hkv, p.T, p.cap, s, g);
+      PrefixRegs<D> pr;
+      prefix_load<D>(src, p.T, b_lo * kBlockKeys, pr);
+      BlockInfo cur = convert_block<D>(pr, sm.b[0], p.scale_log2);
+      __syncthreads();
+      for (int b = b_lo; b < b_hi; ++b) {
+        const int buf = (b - b_lo) & 1;
+        const BlockImg<D>& bk = sm.b[buf];
+        attend_block<D, 2, false>(bk.k, bk.vt, bk.gk, bk.kb, qf, 0.0f, cur.eb, cur.masked != 0, m_run, l_run, e_run, o,
+                                  0, 0, slot_row, slot_tok, [&] {
+                                    if (b + 1 < b_hi) prefix_load<D>(src, p.T, (b + 1) * kBlockKeys, pr);
+                                  });
+        BlockInfo nxt = cur;
+        if (b + 1 < b_hi) nxt = convert_block<D>(pr, sm.b[buf ^ 1], p.scale_log2);
+        __syncthreads();
+        cur = nxt;
+      }
     }
   }
 
@@ -534,10 +718,12 @@ __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) 
   const int r_lo = row0 + slot_base / per_row, r_hi = sp == p.nsplit - 1 ? row0 + last / per_row : r_lo - 1;
   for (int row = r_lo; row <= r_hi; ++row) {
     for (int j0 = 0; j0 < p.t; j0 += kOwnKeys) {
-      __syncthreads();  // LDS buffer 0 free
-      own_stage<D>(p, sm, row, g, j0);
+      __syncthreads();  // LDS image 0 free
+      BlockInfo bi;
+      own_stage<D>(p, sm.red, sm.b[0].k, sm.b[0].vt, row, g, j0, bi);
       __syncthreads();
-      attend_block<D, 1, true>(sm, 0, qf, c_i, m_run, l_run, e_run, o, row, j0, slot_row, slot_tok);
+      attend_block<D, 1, true>(sm.b[0].k, sm.b[0].vt, nullptr, nullptr, qf, p.scale_log2, bi.eb, false, m_run, l_run,
+                               e_run, o, row, j0, slot_row, slot_tok, [] {});
     }
   }
 
@@ -547,7 +733,7 @@ __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) 
   const float lse_v = l_run > 0.0f ? (m_run + __log2f(l_run)) * kLn2 : -INFINITY;
   const int64_t slot_idx = ((int64_t)slot_row * p.Hq + slot_head) * p.t + slot_tok;
   if (p.nsplit > 1) {
-    // this split's normalized fp32 partial and its LSE, merged by od_attn_combine
+    // this split's normalized fp32 partial and its LSE, merged by combine_kernel
     const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
     float* po = p.part + ((int64_t)sp * nsl + slot_idx) * D;
 #pragma unroll
@@ -574,6 +760,42 @@ __global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) 
     }
   }
   if (p.lse && h == 0) p.lse[slot_idx] = lse_v;
+}
+
+// The int8 path: two workgroups per CU (two waves per SIMD hide each other's phases).
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) {
+  __shared__ Smem<D> sm;
+  branched_attn_body<D, false>(p, sm);
+}
+
+// The staged path: the same, each workgroup copying block images into LDS.
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void branched_staged_kernel(AttnArgs p) {
+  __shared__ Smem<D> sm;
+  branched_attn_body<D, true>(p, sm);
+}
+
+// od_attn_stage: one workgroup per (block, KV head, state) converts an int8 block into its image.
+struct StageArgs {
+  const int8_t* kq;
+  const float* ks;
+  const int8_t* vq;
+  const float* vs;
+  const uint8_t* kvalid;
+  uint8_t* img;
+  int Hkv, T, cap, nb;
+  float scale_log2;
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void stage_kernel(StageArgs p) {
+  const int b = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+  const PrefixSrc src = prefix_src<D>(p.kq, p.ks, p.vq, p.vs, p.kvalid, p.Hkv, p.T, p.cap, s, g);
+  PrefixRegs<D> pr;
+  prefix_load<D>(src, p.T, b * kBlockKeys, pr);
+  const int64_t blk = ((int64_t)s * p.Hkv + g) * p.nb + b;
+  convert_block<D>(pr, reinterpret_cast<BlockImg<D>*>(p.img)[blk], p.scale_log2);
 }
 
 // LSE merge of the key-range splits (prefix_attn.py:74-76 generalised to n parts): M = max_s lse_s,
@@ -623,9 +845,11 @@ namespace {
 int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, const uint16_t* k_own, int64_t skr,
                     int64_t skh, int64_t skt, const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
                     const int8_t* kq, const float* ks, const int8_t* vq, const float* vs, const uint8_t* kvalid,
-                    const int32_t* row_start, int64_t max_rows, uint16_t* out, int64_t sor, int64_t soh, int64_t sot,
-                    float* lse, int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
-                    int64_t cap, float scale, int64_t nsplit, float* ws, int64_t ws_floats, od_stream_t stream) {
+                    const void* img, const int32_t* row_start, int64_t max_rows, uint16_t* out,
+                    int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t R, int64_t Hq, int64_t Hkv, int64_t t,
+                    int64_t D, int64_t Ns, int64_t T, int64_t cap, float scale, int64_t nsplit, float* ws,
+                    int64_t ws_floats, od_stream_t stream) {
+  const bool staged = img != nullptr;
   if (R < 0 || Hq < 1 || Hkv < 1 || t < 1 || Ns < 1 || T < 0 || cap < T || max_rows < 0) return OD_ERR_SHAPE;
   if (Hq % Hkv) return OD_ERR_UNSUPPORTED;
   if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
@@ -634,7 +858,8 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
   if (nsplit < 1 || nsplit > 256) return OD_ERR_SHAPE;
   if (!row_start) max_rows = R;
   if (R == 0 || max_rows == 0) return OD_OK;
-  if (!q || !k_own || !v_own || !out || (T > 0 && (!kq || !ks || !vq || !vs))) return OD_ERR_NULL;
+  if (!q || !k_own || !v_own || !out) return OD_ERR_NULL;
+  if (T > 0 && !staged && (!kq || !ks || !vq || !vs)) return OD_ERR_NULL;
   if (nsplit > 1) {
     if (!ws) return OD_ERR_NULL;
     if (ws_floats < nsplit * R * Hq * t * (D + 1)) return OD_ERR_SHAPE;
@@ -645,21 +870,23 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
     if (st < 0 || st % 8) return OD_ERR_ALIGN;
   if (sor < 0 || soh < 0 || sot < 0 || sor % 4 || soh % 4 || sot % 4) return OD_ERR_ALIGN;
   if (!od_aligned16(q) || !od_aligned16(k_own) || !od_aligned16(v_own) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
-  if (T > 0 && (!od_aligned16(kq) || !od_aligned16(vq))) return OD_ERR_ALIGN;
+  if (T > 0 && !staged && (!od_aligned16(kq) || !od_aligned16(vq))) return OD_ERR_ALIGN;
+  if (T > 0 && staged && !od_aligned16(img)) return OD_ERR_ALIGN;
   const int64_t rep = Hq / Hkv;
   const int64_t tiles = (max_rows * t * rep + kSlotsPerTile - 1) / kSlotsPerTile;
   if (tiles > 0x7fffffff || Hkv > 65535 || Ns * nsplit > 65535 || R * t * rep > 0x7fffffff ||
-      cap * Hkv * Ns * D > (1ll << 40) || nsplit * R * Hq * t * (D + 1) > (1ll << 40))
+      cap * Hkv * Ns * D > (1ll << 40) || nsplit * R * Hq * t * (D + 1) > (1ll << 40) ||
+      T * D >= (1ll << 31))  // one (state, head) slab is addressed with 32-bit buffer offsets
     return OD_ERR_SHAPE;
   AttnArgs a{q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, lse, sqr, sqh, sqt, skr, skh, skt, svr, svh,
              svt, sor, soh, sot, (int)R, (int)Hq, (int)Hkv, (int)t, (int)Ns, (int)T, (int)cap, (int)rep,
-             scale * 1.4426950408889634f, (int)nsplit, nsplit > 1 ? ws : nullptr};
+             scale * 1.4426950408889634f, (int)nsplit, nsplit > 1 ? ws : nullptr, static_cast<const uint8_t*>(img)};
   dim3 grid((unsigned)tiles, (unsigned)Hkv, (unsigned)(Ns * nsplit)), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
   if (D == 128) {
-    branched_attn_kernel<128><<<grid, block, 0, st>>>(a);
+    staged ? branched_staged_kernel<128><<<grid, block, 0, st>>>(a) : branched_attn_kernel<128><<<grid, block, 0, st>>>(a);
   } else {
-    branched_attn_kernel<64><<<grid, block, 0, st>>>(a);
+    staged ? branched_staged_kernel<64><<<grid, block, 0, st>>>(a) : branched_attn_kernel<64><<<grid, block, 0, st>>>(a);
   }
   if (nsplit > 1) {
     const int rc = od_launch_status();
@@ -675,6 +902,9 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
   return od_launch_status();
 }
 
+int64_t stage_blocks(int64_t Ns, int64_t Hkv, int64_t T) { return Ns * Hkv * ((T + kBlockKeys - 1) / kBlockKeys); }
+int64_t stage_block_bytes(int64_t D) { return D == 128 ? (int64_t)sizeof(BlockImg<128>) : (int64_t)sizeof(BlockImg<64>); }
+
 }  // namespace
 
 extern "C" int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, const uint16_t* k_own,
@@ -685,8 +915,8 @@ extern "C" int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int
                                 int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, int64_t cap,
                                 float scale, od_stream_t stream) {
   return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, kq, ks, vq, vs, kvalid,
-                         row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale, 1, nullptr,
-                         0, stream);
+                         nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale,
+                         1, nullptr, 0, stream);
 }
 
 extern "C" int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, const uint16_t* k_own,
@@ -698,6 +928,53 @@ extern "C" int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sq
                                       int64_t T, int64_t cap, float scale, int64_t nsplit, float* ws,
                                       int64_t ws_floats, od_stream_t stream) {
   return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, kq, ks, vq, vs, kvalid,
-                         row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale, nsplit, ws,
-                         ws_floats, stream);
+                         nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale,
+                         nsplit, ws, ws_floats, stream);
+}
+
+extern "C" int od_attn_stage_size(int64_t Ns, int64_t Hkv, int64_t T, int64_t D, int64_t* img_bytes) {
+  if (Ns < 1 || Hkv < 1 || T < 0) return OD_ERR_SHAPE;
+  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (!img_bytes) return OD_ERR_NULL;
+  *img_bytes = stage_blocks(Ns, Hkv, T) * stage_block_bytes(D);
+  return OD_OK;
+}
+
+extern "C" int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
+                             const uint8_t* kvalid, int64_t Ns, int64_t Hkv, int64_t T, int64_t cap, int64_t D,
+                             float scale, void* img, int64_t img_bytes, od_stream_t stream) {
+  if (Ns < 1 || Hkv < 1 || T < 0 || cap < T) return OD_ERR_SHAPE;
+  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (T == 0) return OD_OK;
+  if (!kq || !ks || !vq || !vs || !img) return OD_ERR_NULL;
+  if (!od_aligned16(kq) || !od_aligned16(vq) || !od_aligned16(img)) return OD_ERR_ALIGN;
+  const int64_t nb = (T + kBlockKeys - 1) / kBlockKeys;
+  if (img_bytes < stage_blocks(Ns, Hkv, T) * stage_block_bytes(D)) return OD_ERR_SHAPE;
+  if (nb > 0x7fffffff || Hkv > 65535 || Ns > 65535 || T * D >= (1ll << 31) || cap * Hkv * Ns * D > (1ll << 40))
+    return OD_ERR_SHAPE;
+  StageArgs a{kq, ks, vq, vs, kvalid, static_cast<uint8_t*>(img), (int)Hkv, (int)T, (int)cap, (int)nb,
+              scale * 1.4426950408889634f};
+  dim3 grid((unsigned)nb, (unsigned)Hkv, (unsigned)Ns), block(kThreads);
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 128) {
+    stage_kernel<128><<<grid, block, 0, st>>>(a);
+  } else {
+    stage_kernel<64><<<grid, block, 0, st>>>(a);
+  }
+  return od_launch_status();
+}
+
+extern "C" int od_branched_attn_staged(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                                       const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                                       const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt, const void* img,
+                                       int64_t img_bytes, const int32_t* row_start, int64_t max_rows, uint16_t* out,
+                                       int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t R, int64_t Hq,
+                                       int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, float scale,
+                                       int64_t nsplit, float* ws, int64_t ws_floats, od_stream_t stream) {
+  if (T > 0 && !img) return OD_ERR_NULL;
+  if ((D == 64 || D == 128) && Ns >= 1 && Hkv >= 1 && T > 0 && img_bytes < stage_blocks(Ns, Hkv, T) * stage_block_bytes(D))
+    return OD_ERR_SHAPE;
+  return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, nullptr, nullptr, nullptr,
+                         nullptr, nullptr, T > 0 ? img : nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq,
+                         Hkv, t, D, Ns, T, T, scale, nsplit, ws, ws_floats, stream);
 }

@@ -37,3 +37,40 @@ static inline int od_launch_status() {
 }
 
 static inline bool od_aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
+
+// One DPP step of a max reduction: x = max(x, x moved by CTRL); lanes of rows outside ROW_MASK compare with
+// themselves (update_dpp keeps `old` there).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float od_dpp_max_step(float x) {
+  const int y = __builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, ROW_MASK, 0xf, false);
+  return fmaxf(x, __int_as_float(y));
+}
+
+// Max over the 64 lanes of a wave with DPP row operations (no LDS round trips), returned wave-uniform.
+__device__ __forceinline__ float od_wave_max_dpp(float v) {
+  v = od_dpp_max_step<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = od_dpp_max_step<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = od_dpp_max_step<0x124, 0xf>(v);  // row_ror:4
+  v = od_dpp_max_step<0x128, 0xf>(v);  // row_ror:8   -> every lane holds its row's max
+  v = od_dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v = od_dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3 -> lane 63 holds the wave max
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Lane l and lane l ^ 32 exchange through v_permlane32_swap: swap(u, u) returns {u[l mod 32], u[32 + l mod 32]}
+// in every lane, so the low-half value comes first in both lanes of a pair.
+__device__ __forceinline__ void od_xor32_pair(float v, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float od_xor32_max(float v) {
+  float lo, hi;
+  od_xor32_pair(v, lo, hi);
+  return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float od_xor32_sum(float v) {
+  float lo, hi;
+  od_xor32_pair(v, lo, hi);
+  return lo + hi;
+}

@@ -2,6 +2,8 @@
 and the current HIP stream. Every function requires CUDA (ROCm) tensors and raises otherwise."""
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -181,14 +183,39 @@ def split_count(slot_tiles: int, T: int, target_workgroups: int = 1024, min_bloc
     return max(1, min(-(-target_workgroups // max(slot_tiles, 1)), blocks // min_blocks, 256))
 
 
+# The staged path writes each state block's image (twice the int8 bytes) once and lets every slot tile copy it
+# instead of converting it; it pays off when several tiles read each (state, head).
+STAGE_MIN_TILES = 4
+
+
+def stage_state(kq, ks, vq, vs, length: int, scale: float, kvalid=None, out=None):
+    """Block images of an int8 state for od_branched_attn_staged (od_attn_stage): kq/vq (Ns, Hkv, cap, D) int8,
+    ks/vs (Ns, Hkv, cap) fp32, the first `length` tokens, the softmax scale of the attention that reads them,
+    kvalid (Ns, length) uint8 or None. Returns a uint8 device buffer of od_attn_stage_size bytes (`out` is reused
+    when it is large enough)."""
+    Ns, Hkv, cap, D = kq.shape
+    nbytes = ctypes.c_int64(0)
+    check(lib().od_attn_stage_size(Ns, Hkv, int(length), D, ctypes.byref(nbytes)), "od_attn_stage_size")
+    if out is None or out.numel() < nbytes.value:
+        out = torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=kq.device)
+    check(lib().od_attn_stage(ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid), Ns, Hkv, int(length), cap, D,
+                              float(scale), ptr(out), out.numel(), stream_of(kq)), "od_attn_stage")
+    return out
+
+
 def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, row_counts=None, length=None,
-                  out=None, return_lse: bool = False, row_start=None, max_rows=None, n_split=None):
-    """Branched option-row attention over int8 states (od_branched_attn). q (R, Hq, t, D) bf16; k_own/v_own
-    (R, Hkv, t, D) bf16; kq/vq (Ns, Hkv, cap, D) int8 of which the first T tokens are used (T = `length`, else
-    kvalid.shape[1], else cap); ks/vs (Ns, Hkv, cap) fp32; kvalid (Ns, T) bool/uint8 or None.
+                  out=None, return_lse: bool = False, row_start=None, max_rows=None, n_split=None, staged=None,
+                  stage_buf=None):
+    """Branched option-row attention over int8 states. q (R, Hq, t, D) bf16; k_own/v_own (R, Hkv, t, D) bf16;
+    kq/vq (Ns, Hkv, cap, D) int8 of which the first T tokens are used (T = `length`, else kvalid.shape[1], else
+    cap); ks/vs (Ns, Hkv, cap) fp32; kvalid (Ns, T) bool/uint8 or None.
     Rows are grouped by state: row_counts (host ints, one per state) or a prebuilt (row_start, max_rows) pair from
-    row_start_of(); neither means Ns == 1. n_split: key-range splits (od_branched_attn_split); None picks them from
-    the grid size (split_count). Returns out (R, Hq, t, D) bf16 [, lse (R, Hq, t) fp32]."""
+    row_start_of(); neither means Ns == 1. n_split: key-range splits; None picks them from the grid size
+    (split_count). staged: convert the state once into block images (od_attn_stage, into `stage_buf` when given and
+    large enough) and run od_branched_attn_staged over them; False runs od_branched_attn / od_branched_attn_split,
+    which convert in every workgroup (same results, bit for bit); None stages when at least STAGE_MIN_TILES slot
+    tiles read each (state, head), so that the conversion is shared. Returns out (R, Hq, t, D) bf16
+    [, lse (R, Hq, t) fp32]."""
     require_gpu(q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, name="branched_attn")
     for x in (q, k_own, v_own):
         _lib.bf16_bits(x)
@@ -227,11 +254,23 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
     if out is None:
         out = torch.empty(R, Hq, t, D, dtype=torch.bfloat16, device=q.device)
     lse = torch.empty(R, Hq, t, dtype=torch.float32, device=q.device) if return_lse else None
+    tiles = -(-(int(max_rows) * t * (Hq // Hkv)) // 128)  # slot tiles per (state, head)
     if n_split is None:
-        tiles = -(-(int(max_rows) * t * (Hq // Hkv)) // 128)
         n_split = split_count(tiles * Hkv * Ns, T)
+    if staged is None:
+        staged = tiles >= STAGE_MIN_TILES
+    ws = None
     if n_split > 1:
         ws = torch.empty(n_split * R * Hq * t * (D + 1), dtype=torch.float32, device=q.device)
+    if staged and T > 0:
+        img = stage_state(kq, ks, vq, vs, T, scale, kvalid, out=stage_buf)
+        check(lib().od_branched_attn_staged(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
+                                            *v_own.stride()[:3], ptr(img), img.numel(), ptr(row_start),
+                                            int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv, t, D,
+                                            Ns, T, float(scale), int(n_split), ptr(ws),
+                                            0 if ws is None else ws.numel(), stream_of(q)),
+              "od_branched_attn_staged")
+    elif n_split > 1:
         check(lib().od_branched_attn_split(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
                                            *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
                                            ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R,

@@ -2,7 +2,8 @@
 
 Bar: outputs within 2e-3 relative of the oracle's fp32 result (the three forms in tests/helpers.py), natural-log LSE
 within 1e-4 absolute, and option-row order invariance (outputs of permuted rows are the permuted outputs; required
-<= 1e-6, checked bitwise). The oracle dequantizes the int8 state exactly in fp32 (q * s). The reference's own bf16
+<= 1e-6, checked bitwise). The staged path (od_attn_stage + od_branched_attn_staged, the default) and the direct path
+(od_branched_attn, converting in every workgroup) must agree bit for bit. The oracle dequantizes the int8 state exactly in fp32 (q * s). The reference's own bf16
 materialize (q.to(bf16) * s.to(bf16), quant.py:45) is further from that exact value than this kernel is; on the
 config-1 shape the test reports both distances.
 """
@@ -41,14 +42,15 @@ def make_case(seed, Ns, row_counts, Hq, Hkv, t, D, T, cap=None, holes=False):
                 row_state=row_state, T=T, scale=D ** -0.5)
 
 
-def run_gpu(c, return_lse=True, q=None, n_split=None):
+def run_gpu(c, return_lse=True, q=None, n_split=None, staged=True):
     from opendecider_amd import kernels
     Ns = c["kq"].shape[0]
     return kernels.branched_attn(
         c["q"].to(DEV) if q is None else q, c["k"].to(DEV), c["v"].to(DEV), c["kq"].to(DEV), c["ks"].to(DEV),
         c["vq"].to(DEV), c["vs"].to(DEV), c["scale"],
         kvalid=None if c["kvalid"] is None else c["kvalid"].to(DEV),
-        row_counts=c["row_counts"] if Ns > 1 else None, length=c["T"], return_lse=return_lse, n_split=n_split)
+        row_counts=c["row_counts"] if Ns > 1 else None, length=c["T"], return_lse=return_lse, n_split=n_split,
+        staged=staged)
 
 
 def run_oracle(c, dequant="fp32"):
@@ -164,3 +166,36 @@ def test_split_long_state_auto(gpu_lib):
     cp = dict(c, q=c["q"][perm], k=c["k"][perm], v=c["v"][perm])
     out_p, lse_p = run_gpu(cp)
     assert torch.equal(out_p, out[perm.to(DEV)]) and torch.equal(lse_p, lse[perm.to(DEV)])
+
+
+# ---- staged block images (od_attn_stage + od_branched_attn_staged) against the direct path: the same bits
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_staged_equals_direct_bitwise(gpu_lib, name):
+    """Both paths build the same block images (one in memory, one in each workgroup's LDS), so outputs and LSE
+    agree bit for bit, with and without a key-range split."""
+    c = make_case(**CASES[name])
+    print(f"staged vs direct {name}", flush=True)
+    for n_split in (1, 3):
+        out_s, lse_s = run_gpu(c, n_split=n_split, staged=True)
+        out_d, lse_d = run_gpu(c, n_split=n_split, staged=False)
+        assert torch.equal(out_s.view(torch.int16), out_d.view(torch.int16)), (name, n_split)
+        assert torch.equal(lse_s, lse_d), (name, n_split)
+
+
+def test_stage_size_and_errors(gpu_lib):
+    """od_attn_stage_size follows Ns * Hkv * ceil(T / 64) * (4 * 64 * D + 528); a too-small image is refused."""
+    import ctypes
+    from opendecider_amd._lib import lib, check
+    n = ctypes.c_int64(0)
+    assert lib().od_attn_stage_size(3, 2, 130, 128, ctypes.byref(n)) == 0
+    assert n.value == 3 * 2 * 3 * (4 * 64 * 128 + 528)
+    assert lib().od_attn_stage_size(1, 1, 64, 64, ctypes.byref(n)) == 0 and n.value == 4 * 64 * 64 + 528
+    assert lib().od_attn_stage_size(1, 1, 64, 96, ctypes.byref(n)) != 0
+    kq = torch.zeros(1, 1, 64, 128, dtype=torch.int8, device=DEV)
+    ks = torch.ones(1, 1, 64, device=DEV)
+    img = torch.empty(100, dtype=torch.uint8, device=DEV)
+    rc = lib().od_attn_stage(kq.data_ptr(), ks.data_ptr(), kq.data_ptr(), ks.data_ptr(), None, 1, 1, 64, 64, 128,
+                             0.125, img.data_ptr(), img.numel(), torch.cuda.current_stream().cuda_stream)
+    with pytest.raises(RuntimeError):
+        check(rc, "od_attn_stage")
