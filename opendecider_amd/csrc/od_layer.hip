@@ -26,6 +26,30 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
+// Max over the workgroup of non-negative fp32 values compared as bit patterns (a NaN dominates).
+__device__ __forceinline__ float block_max_bits(float f, float* red) {
+  const uint32_t v = od_wave_umax_dpp(__float_as_uint(f));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = __uint_as_float(v);
+  __syncthreads();
+  uint32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < kThreads / OD_WAVE; ++i) s = max(s, __float_as_uint(red[i]));
+  return __uint_as_float(s);
+}
+
+// Workgroup sum with DPP wave sums, in a fixed order.
+__device__ __forceinline__ float block_sum_dpp(float v, float* red) {
+  v = od_wave_sum_dpp(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kThreads / OD_WAVE; ++i) s += red[i];
+  return s;
+}
+
 __device__ __forceinline__ float block_max(float v, float* red) {
   v = od_wave_max(v);
   __syncthreads();
@@ -35,12 +59,6 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 #pragma unroll
   for (int i = 0; i < kThreads / OD_WAVE; ++i) s = fmaxf(s, red[i]);
   return s;
-}
-
-__device__ __forceinline__ int8_t q8(float v, float scale) {
-  float qf = rintf(v / scale);
-  qf = fminf(fmaxf(qf, -127.0f), 127.0f);
-  return (int8_t)(int)qf;
 }
 
 // ---------------------------------------------------------------------------- RMSNorm + quantize
@@ -70,9 +88,9 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_kernel(const uint16_t*
   float amax = 0.0f;
   for (int k = threadIdx.x; k < K; k += kThreads) amax = fmaxf(amax, fabsf(rms_val(xr, w, inv_s, k, r)));
   amax = block_max(amax, red);
-  const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+  const float scale = od_q8_scale(amax), inv = 1.0f / scale;
   int8_t* qr = xq + row * ldq;
-  for (int k = threadIdx.x; k < K; k += kThreads) qr[k] = q8(rms_val(xr, w, inv_s, k, r), scale);
+  for (int k = threadIdx.x; k < K; k += kThreads) qr[k] = od_q8_one(rms_val(xr, w, inv_s, k, r), scale, inv);
   if (threadIdx.x == 0) sx[row] = scale;
 }
 
@@ -96,9 +114,9 @@ __global__ __launch_bounds__(kThreads) void silu_mul_quant_kernel(const uint16_t
   float amax = 0.0f;
   for (int64_t k = threadIdx.x; k < F; k += kThreads) amax = fmaxf(amax, fabsf(swiglu_val(gr, F, inv_s, k)));
   amax = block_max(amax, red);
-  const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+  const float scale = od_q8_scale(amax), inv = 1.0f / scale;
   int8_t* qr = aq + row * ldq;
-  for (int64_t k = threadIdx.x; k < F; k += kThreads) qr[k] = q8(swiglu_val(gr, F, inv_s, k), scale);
+  for (int64_t k = threadIdx.x; k < F; k += kThreads) qr[k] = od_q8_one(swiglu_val(gr, F, inv_s, k), scale, inv);
   if (threadIdx.x == 0) sa[row] = scale;
 }
 
@@ -143,26 +161,24 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(uint16_t* __rest
 
 // ---------------------------------------------------------------------------- register-resident fast paths
 // A row of 256 * 8 * NV elements is held in registers (NV 16-byte vectors of 8 bf16 per thread, vector v of thread
-// t covering elements (v * 256 + t) * 8 .. +7), so the row is read from HBM once and written once.
-__device__ __forceinline__ void unpack8(const uint4 u, float (&f)[8]) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f[2 * j] = __uint_as_float(w[j] << 16);
-    f[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-  }
+// t covering elements (v * 256 + t) * 8 .. +7), so the row is read from HBM once and written once. Every load of a
+// row (x, the norm weight, the smoothing scale) is issued before the first reduction. These kernels are bound by
+// VALU issue rather than HBM at 4096 x 4096: the bf16 round trips go two values per v_cvt_pk_bf16_f32 and the
+// quantizer multiplies by 1 / scale (exact, see od_q8_words).
+__device__ __forceinline__ void unpack2(uint32_t w, float& lo, float& hi) {
+  lo = __uint_as_float(w << 16);
+  hi = __uint_as_float(w & 0xffff0000u);
 }
 
-__device__ __forceinline__ uint2 pack_q8(const float (&y)[8], float scale) {
-  uint32_t lo = 0, hi = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) lo |= ((uint32_t)(uint8_t)q8(y[j], scale)) << (8 * j);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) hi |= ((uint32_t)(uint8_t)q8(y[4 + j], scale)) << (8 * j);
-  return make_uint2(lo, hi);
+__device__ __forceinline__ uint32_t word(const uint4& u, int j) { return j == 0 ? u.x : j == 1 ? u.y : j == 2 ? u.z : u.w; }
+
+__device__ __forceinline__ void store_q8(int8_t* dst, const float (&y)[8], float scale, float inv) {
+  uint32_t w[2];
+  od_q8_words<8>(y, scale, inv, w);
+  *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
 }
 
-template <int NV>
+template <int NV, bool INV>
 __global__ __launch_bounds__(kThreads) void rmsnorm_quant_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                      const uint16_t* __restrict__ w,
                                                                      const uint16_t* __restrict__ inv_s, float eps,
@@ -172,40 +188,53 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_vec_kernel(const uint1
   __shared__ float red[kThreads / OD_WAVE];
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * ldx;
+  uint4 xv[NV], wv[NV], iv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int k = (v * kThreads + threadIdx.x) * 8;
+    xv[v] = *reinterpret_cast<const uint4*>(xr + k);
+    wv[v] = *reinterpret_cast<const uint4*>(w + k);
+    if (INV) iv[v] = *reinterpret_cast<const uint4*>(inv_s + k);
+  }
   float y[NV][8];
   float ss = 0.0f;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int k = (v * kThreads + threadIdx.x) * 8;
-    unpack8(*reinterpret_cast<const uint4*>(xr + k), y[v]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) unpack2(word(xv[v], j), y[v][2 * j], y[v][2 * j + 1]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss = fmaf(y[v][e], y[v][e], ss);
   }
-  ss = block_sum(ss, red);
+  ss = block_sum_dpp(ss, red);
   const float r = 1.0f / sqrtf(ss / (float)K + eps);
-  float amax = 0.0f;
+  uint32_t am = 0;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    const int k = (v * kThreads + threadIdx.x) * 8;
-    float wv[8], iv[8];
-    unpack8(*reinterpret_cast<const uint4*>(w + k), wv);
-    if (inv_s) unpack8(*reinterpret_cast<const uint4*>(inv_s + k), iv);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float t = bfr(wv[e] * bfr(y[v][e] * r));
-      if (inv_s) t = bfr(t * iv[e]);
-      y[v][e] = t;
-      amax = fmaxf(amax, fabsf(t));
+    for (int j = 0; j < 4; ++j) {
+      float a = y[v][2 * j] * r, b = y[v][2 * j + 1] * r, wa, wb;
+      od_bfr2(a, b);
+      unpack2(word(wv[v], j), wa, wb);
+      a *= wa;
+      b *= wb;
+      uint32_t p = od_bfr2(a, b);
+      if (INV) {
+        float ia, ib;
+        unpack2(word(iv[v], j), ia, ib);
+        a *= ia;
+        b *= ib;
+        p = od_bfr2(a, b);
+      }
+      y[v][2 * j] = a;
+      y[v][2 * j + 1] = b;
+      am = od_absmax_bf16x2(am, p);
     }
   }
-  amax = block_max(amax, red);
-  const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+  const float amax = block_max_bits(od_absmax_bf16x2_value(am), red);
+  const float scale = od_q8_scale(amax), inv = 1.0f / scale;
   int8_t* qr = xq + row * ldq;
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int k = (v * kThreads + threadIdx.x) * 8;
-    *reinterpret_cast<uint2*>(qr + k) = pack_q8(y[v], scale);
-  }
+  for (int v = 0; v < NV; ++v) store_q8(qr + (v * kThreads + threadIdx.x) * 8, y[v], scale, inv);
   if (threadIdx.x == 0) sx[row] = scale;
 }
 
@@ -213,7 +242,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_vec_kernel(const uint1
 // bf16, which hides the difference except at rare rounding ties).
 __device__ __forceinline__ float silu_fast(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
-template <int NV>
+template <int NV, bool INV>
 __global__ __launch_bounds__(kThreads) void silu_mul_quant_vec_kernel(const uint16_t* __restrict__ gu, int64_t ldg,
                                                                       const uint16_t* __restrict__ inv_s,
                                                                       int8_t* __restrict__ aq, int64_t ldq,
@@ -223,30 +252,41 @@ __global__ __launch_bounds__(kThreads) void silu_mul_quant_vec_kernel(const uint
   const int64_t row = blockIdx.x;
   const uint16_t* gr = gu + row * ldg;
   float y[NV][8];
-  float amax = 0.0f;
+  uint32_t am = 0;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int k = (v * kThreads + threadIdx.x) * 8;
-    float g[8], u[8], iv[8];
-    unpack8(*reinterpret_cast<const uint4*>(gr + k), g);
-    unpack8(*reinterpret_cast<const uint4*>(gr + F + k), u);
-    if (inv_s) unpack8(*reinterpret_cast<const uint4*>(inv_s + k), iv);
+    const uint4 g8 = *reinterpret_cast<const uint4*>(gr + k);
+    const uint4 u8 = *reinterpret_cast<const uint4*>(gr + F + k);
+    uint4 i8;
+    if (INV) i8 = *reinterpret_cast<const uint4*>(inv_s + k);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float t = bfr(bfr(silu_fast(g[e])) * u[e]);
-      if (inv_s) t = bfr(t * iv[e]);
-      y[v][e] = t;
-      amax = fmaxf(amax, fabsf(t));
+    for (int j = 0; j < 4; ++j) {
+      float ga, gb, ua, ub;
+      unpack2(word(g8, j), ga, gb);
+      unpack2(word(u8, j), ua, ub);
+      float a = silu_fast(ga), b = silu_fast(gb);
+      od_bfr2(a, b);
+      a *= ua;
+      b *= ub;
+      uint32_t p = od_bfr2(a, b);
+      if (INV) {
+        float ia, ib;
+        unpack2(word(i8, j), ia, ib);
+        a *= ia;
+        b *= ib;
+        p = od_bfr2(a, b);
+      }
+      y[v][2 * j] = a;
+      y[v][2 * j + 1] = b;
+      am = od_absmax_bf16x2(am, p);
     }
   }
-  amax = block_max(amax, red);
-  const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+  const float amax = block_max_bits(od_absmax_bf16x2_value(am), red);
+  const float scale = od_q8_scale(amax), inv = 1.0f / scale;
   int8_t* qr = aq + row * ldq;
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int k = (v * kThreads + threadIdx.x) * 8;
-    *reinterpret_cast<uint2*>(qr + k) = pack_q8(y[v], scale);
-  }
+  for (int v = 0; v < NV; ++v) store_q8(qr + (v * kThreads + threadIdx.x) * 8, y[v], scale, inv);
   if (threadIdx.x == 0) sa[row] = scale;
 }
 
@@ -320,6 +360,26 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope128_kernel(uint16_t* __r
       make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
 }
 
+template <int NV>
+void launch_rmsnorm_vec(dim3 grid, hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                        const uint16_t* inv_s, float eps, int8_t* xq, int64_t ldq, float* sx) {
+  if (inv_s) {
+    rmsnorm_quant_vec_kernel<NV, true><<<grid, dim3(kThreads), 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+  } else {
+    rmsnorm_quant_vec_kernel<NV, false><<<grid, dim3(kThreads), 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+  }
+}
+
+template <int NV>
+void launch_silu_vec(dim3 grid, hipStream_t st, const uint16_t* gu, int64_t ldg, const uint16_t* inv_s, int8_t* aq,
+                     int64_t ldq, float* sa) {
+  if (inv_s) {
+    silu_mul_quant_vec_kernel<NV, true><<<grid, dim3(kThreads), 0, st>>>(gu, ldg, inv_s, aq, ldq, sa);
+  } else {
+    silu_mul_quant_vec_kernel<NV, false><<<grid, dim3(kThreads), 0, st>>>(gu, ldg, inv_s, aq, ldq, sa);
+  }
+}
+
 }  // namespace
 
 extern "C" int od_rmsnorm_quant(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* inv_s, float eps,
@@ -333,11 +393,11 @@ extern "C" int od_rmsnorm_quant(const uint16_t* x, int64_t ldx, const uint16_t* 
                    (!inv_s || od_aligned16(inv_s)) && ((((uintptr_t)xq) & 7u) == 0);
   const dim3 grid((unsigned)M), block(kThreads);
   if (vec && K == 2048) {
-    rmsnorm_quant_vec_kernel<1><<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+    launch_rmsnorm_vec<1>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx);
   } else if (vec && K == 4096) {
-    rmsnorm_quant_vec_kernel<2><<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+    launch_rmsnorm_vec<2>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx);
   } else if (vec && K == 8192) {
-    rmsnorm_quant_vec_kernel<4><<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+    launch_rmsnorm_vec<4>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx);
   } else {
     rmsnorm_quant_kernel<<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx, (int)K);
   }
@@ -355,11 +415,11 @@ extern "C" int od_silu_mul_quant(const uint16_t* gu, int64_t ldg, int64_t F, con
                    (!inv_s || od_aligned16(inv_s)) && ((((uintptr_t)aq) & 7u) == 0);
   const dim3 grid((unsigned)M), block(kThreads);
   if (vec && F == 2048 * 6) {
-    silu_mul_quant_vec_kernel<6><<<grid, block, 0, st>>>(gu, ldg, inv_s, aq, ldq, sa);
+    launch_silu_vec<6>(grid, st, gu, ldg, inv_s, aq, ldq, sa);
   } else if (vec && F == 2048 * 4) {
-    silu_mul_quant_vec_kernel<4><<<grid, block, 0, st>>>(gu, ldg, inv_s, aq, ldq, sa);
+    launch_silu_vec<4>(grid, st, gu, ldg, inv_s, aq, ldq, sa);
   } else if (vec && F == 2048 * 3) {
-    silu_mul_quant_vec_kernel<3><<<grid, block, 0, st>>>(gu, ldg, inv_s, aq, ldq, sa);
+    launch_silu_vec<3>(grid, st, gu, ldg, inv_s, aq, ldq, sa);
   } else {
     silu_mul_quant_kernel<<<grid, block, 0, st>>>(gu, ldg, F, inv_s, aq, ldq, sa);
   }

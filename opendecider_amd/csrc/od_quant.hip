@@ -6,10 +6,15 @@
 // where v_k = float(x_k), or float(bf16(float(x_k) * float(inv_s_k))) with a SmoothQuant input scale
 // (quant.py:329: the product is rounded to bf16 before it is quantized).
 //
-// HBM-bound: every element is read from HBM once (the second pass over a row hits L1/L2: a row is at most a few
-// tens of KB and is owned by one workgroup) and written once as int8. A group of LANES threads owns a row; rows
-// of 64..512 elements (KV heads, small linears) use 8..64 lanes so that a wave covers several rows, wider rows
-// use a whole 256-thread workgroup. Loads are 16 B (8 bf16) per lane when the row layout allows it.
+// The division by scale is a multiplication by 1 / scale with an exact fallback (od_q8_words), which gives the
+// quotient's result bit for bit. The row max runs on bf16 bit patterns, so a NaN in a row makes its scale NaN and
+// its bytes 0, as torch's amax (which propagates NaN) and float -> int8 conversion on x86 do.
+//
+// Every element is read from HBM once and written once as int8: rows up to 4 * 256 * 8 elements stay in registers
+// between the max and the quantization; longer rows are read twice (the second pass hits L1/L2). A group of LANES
+// threads owns a row; rows of 64..512 elements (KV heads, small linears) use 8..64 lanes so that a wave covers
+// several rows, wider rows use a whole 256-thread workgroup. Loads are 16 B (8 bf16) per lane when the row layout
+// allows it.
 #include "od_common.h"
 
 namespace {
@@ -53,34 +58,58 @@ __device__ __forceinline__ float load_val(const uint16_t* xin, const uint16_t* i
   return v;
 }
 
+// 8 consecutive values of a row from one 16-byte load, times the smoothing scale and rounded to bf16 when there is
+// one; returns the packed |bf16| max of the 8 (see od_absmax_bf16x2).
 template <bool HAS_INV>
-__device__ __forceinline__ void load8(const uint16_t* xin, const uint16_t* inv_s, int64_t k, float (&v)[8]) {
+__device__ __forceinline__ uint32_t load8(const uint16_t* xin, const uint16_t* inv_s, int64_t k, float (&v)[8]) {
   const uint4 raw = *reinterpret_cast<const uint4*>(xin + k);
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint4 rs{};
+  if (HAS_INV) rs = *reinterpret_cast<const uint4*>(inv_s + k);
+  const uint32_t ws[4] = {rs.x, rs.y, rs.z, rs.w};
+  uint32_t am = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    v[2 * j] = __uint_as_float(w[j] << 16);
-    v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-  }
-  if (HAS_INV) {
-    const uint4 rs = *reinterpret_cast<const uint4*>(inv_s + k);
-    const uint32_t ws[4] = {rs.x, rs.y, rs.z, rs.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[2 * j] = od_bf16_to_f32(od_f32_to_bf16(v[2 * j] * __uint_as_float(ws[j] << 16)));
-      v[2 * j + 1] = od_bf16_to_f32(od_f32_to_bf16(v[2 * j + 1] * __uint_as_float(ws[j] & 0xffff0000u)));
+    float a = __uint_as_float(w[j] << 16), b = __uint_as_float(w[j] & 0xffff0000u);
+    uint32_t p = w[j];
+    if (HAS_INV) {
+      a *= __uint_as_float(ws[j] << 16);
+      b *= __uint_as_float(ws[j] & 0xffff0000u);
+      p = od_bfr2(a, b);
     }
+    v[2 * j] = a;
+    v[2 * j + 1] = b;
+    am = od_absmax_bf16x2(am, p);
+  }
+  return am;
+}
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Max of the row's bit patterns over the LANES threads that own it (LANES = 256: the whole workgroup).
+template <int LANES>
+__device__ __forceinline__ uint32_t row_umax(uint32_t v) {
+  if constexpr (LANES == OD_WAVE) {
+    return od_wave_umax_dpp(v);
+  } else if constexpr (LANES < OD_WAVE) {
+#pragma unroll
+    for (int o = LANES / 2; o > 0; o >>= 1) v = umax(v, (uint32_t)__shfl_xor((int)v, o, OD_WAVE));
+    return v;
+  } else {
+    __shared__ uint32_t red[kThreads / OD_WAVE];
+    v = od_wave_umax_dpp(v);
+    if (threadIdx.x % OD_WAVE == 0) red[threadIdx.x / OD_WAVE] = v;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kThreads / OD_WAVE; ++i) v = umax(v, red[i]);
+    return v;
   }
 }
 
-__device__ __forceinline__ int8_t quant1(float v, float scale) {
-  float qf = rintf(v / scale);
-  qf = fminf(fmaxf(qf, -127.0f), 127.0f);
-  return (int8_t)(int)qf;
-}
-
-// LANES threads per row; VEC = 8 (16-byte loads) or 1.
-template <int LANES, int VEC, int MODE, bool HAS_INV>
+// LANES threads per row; VEC = 8 (16-byte loads) or 1. With VEC = 8 and NIT > 0 a lane holds its NIT groups of 8
+// values in registers (K <= NIT * LANES * 8), so the row is read once; NIT = 0 reads it twice (the second pass
+// hits L1/L2).
+template <int LANES, int VEC, int MODE, bool HAS_INV, int NIT>
 __global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowMap m, const uint16_t* __restrict__ inv_s,
                                                               int64_t n_rows, int64_t K) {
   constexpr int kRowsPerBlock = kThreads / LANES;
@@ -92,47 +121,71 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowMap m, const ui
   float* sout = nullptr;
   if (live) map_row<MODE>(m, r, xin, qout, sout);
 
-  float amax = 0.0f;
-  if (live) {
-    if constexpr (VEC == 8) {
+  if constexpr (VEC == 8 && NIT > 0) {
+    float v[NIT][8];
+    uint32_t am = 0;
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      const int64_t k = ((int64_t)i * LANES + lane) * 8;
+      if (live && k < K) am = od_absmax_bf16x2(am, load8<HAS_INV>(xin, inv_s, k, v[i]));
+    }
+    const float amax = __uint_as_float(row_umax<LANES>(__float_as_uint(od_absmax_bf16x2_value(am))));
+    if (!live) return;
+    const float scale = od_q8_scale(amax), inv = 1.0f / scale;
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      const int64_t k = ((int64_t)i * LANES + lane) * 8;
+      if (k < K) {
+        uint32_t w[2];
+        od_q8_words<8>(v[i], scale, inv, w);
+        *reinterpret_cast<uint2*>(qout + k) = make_uint2(w[0], w[1]);
+      }
+    }
+    if (lane == 0) *sout = scale;
+  } else if constexpr (VEC == 8) {
+    uint32_t am = 0;
+    if (live) {
       for (int64_t k = (int64_t)lane * 8; k < K; k += LANES * 8) {
         float v[8];
-        load8<HAS_INV>(xin, inv_s, k, v);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+        am = od_absmax_bf16x2(am, load8<HAS_INV>(xin, inv_s, k, v));
       }
-    } else {
-      for (int64_t k = lane; k < K; k += LANES) amax = fmaxf(amax, fabsf(load_val<HAS_INV>(xin, inv_s, k)));
     }
-  }
-  if constexpr (LANES <= OD_WAVE) {
-    amax = od_group_max<LANES <= OD_WAVE ? LANES : OD_WAVE>(amax);
-  } else {
-    __shared__ float red[kThreads / OD_WAVE];
-    amax = od_wave_max(amax);
-    if (threadIdx.x % OD_WAVE == 0) red[threadIdx.x / OD_WAVE] = amax;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kThreads / OD_WAVE; ++i) amax = fmaxf(amax, red[i]);
-  }
-  if (!live) return;
-  const float scale = fmaxf(amax, 1e-8f) / 127.0f;
-
-  if constexpr (VEC == 8) {
+    const float amax = __uint_as_float(row_umax<LANES>(__float_as_uint(od_absmax_bf16x2_value(am))));
+    if (!live) return;
+    const float scale = od_q8_scale(amax), inv = 1.0f / scale;
     for (int64_t k = (int64_t)lane * 8; k < K; k += LANES * 8) {
       float v[8];
-      load8<HAS_INV>(xin, inv_s, k, v);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= ((uint32_t)(uint8_t)quant1(v[j], scale)) << (8 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) hi |= ((uint32_t)(uint8_t)quant1(v[4 + j], scale)) << (8 * j);
-      *reinterpret_cast<uint2*>(qout + k) = make_uint2(lo, hi);
+      (void)load8<HAS_INV>(xin, inv_s, k, v);
+      uint32_t w[2];
+      od_q8_words<8>(v, scale, inv, w);
+      *reinterpret_cast<uint2*>(qout + k) = make_uint2(w[0], w[1]);
     }
+    if (lane == 0) *sout = scale;
   } else {
-    for (int64_t k = lane; k < K; k += LANES) qout[k] = quant1(load_val<HAS_INV>(xin, inv_s, k), scale);
+    uint32_t am = 0;
+    if (live) {
+      for (int64_t k = lane; k < K; k += LANES) am = umax(am, __float_as_uint(fabsf(load_val<HAS_INV>(xin, inv_s, k))));
+    }
+    const float amax = __uint_as_float(row_umax<LANES>(am));
+    if (!live) return;
+    const float scale = od_q8_scale(amax), inv = 1.0f / scale;
+    for (int64_t k = lane; k < K; k += LANES) qout[k] = od_q8_one(load_val<HAS_INV>(xin, inv_s, k), scale, inv);
+    if (lane == 0) *sout = scale;
   }
-  if (lane == 0) *sout = scale;
+}
+
+template <int LANES, int VEC, int MODE, bool HAS_INV>
+void launch_nit(dim3 grid, hipStream_t st, const RowMap& m, const uint16_t* inv_s, int64_t n_rows, int64_t K) {
+  const int64_t groups = (K + VEC * LANES - 1) / (VEC * LANES);  // groups of VEC values per lane
+  if (VEC == 8 && groups <= 1) {
+    quant_rows_kernel<LANES, VEC, MODE, HAS_INV, 1><<<grid, dim3(kThreads), 0, st>>>(m, inv_s, n_rows, K);
+  } else if (VEC == 8 && groups <= 2) {
+    quant_rows_kernel<LANES, VEC, MODE, HAS_INV, 2><<<grid, dim3(kThreads), 0, st>>>(m, inv_s, n_rows, K);
+  } else if (VEC == 8 && groups <= 4) {
+    quant_rows_kernel<LANES, VEC, MODE, HAS_INV, 4><<<grid, dim3(kThreads), 0, st>>>(m, inv_s, n_rows, K);
+  } else {
+    quant_rows_kernel<LANES, VEC, MODE, HAS_INV, 0><<<grid, dim3(kThreads), 0, st>>>(m, inv_s, n_rows, K);
+  }
 }
 
 template <int MODE, bool HAS_INV, int VEC>
@@ -142,13 +195,13 @@ int launch_lanes(const RowMap& m, const uint16_t* inv_s, int64_t n_rows, int64_t
   const int64_t rows_per_block = kThreads / lanes;
   const int64_t blocks = (n_rows + rows_per_block - 1) / rows_per_block;
   if (blocks > 0x7fffffff) return OD_ERR_SHAPE;
-  dim3 grid((unsigned)blocks), block(kThreads);
+  dim3 grid((unsigned)blocks);
   switch (lanes) {
-    case 8: quant_rows_kernel<8, VEC, MODE, HAS_INV><<<grid, block, 0, st>>>(m, inv_s, n_rows, K); break;
-    case 16: quant_rows_kernel<16, VEC, MODE, HAS_INV><<<grid, block, 0, st>>>(m, inv_s, n_rows, K); break;
-    case 32: quant_rows_kernel<32, VEC, MODE, HAS_INV><<<grid, block, 0, st>>>(m, inv_s, n_rows, K); break;
-    case 64: quant_rows_kernel<64, VEC, MODE, HAS_INV><<<grid, block, 0, st>>>(m, inv_s, n_rows, K); break;
-    default: quant_rows_kernel<256, VEC, MODE, HAS_INV><<<grid, block, 0, st>>>(m, inv_s, n_rows, K); break;
+    case 8: launch_nit<8, VEC, MODE, HAS_INV>(grid, st, m, inv_s, n_rows, K); break;
+    case 16: launch_nit<16, VEC, MODE, HAS_INV>(grid, st, m, inv_s, n_rows, K); break;
+    case 32: launch_nit<32, VEC, MODE, HAS_INV>(grid, st, m, inv_s, n_rows, K); break;
+    case 64: launch_nit<64, VEC, MODE, HAS_INV>(grid, st, m, inv_s, n_rows, K); break;
+    default: launch_nit<256, VEC, MODE, HAS_INV>(grid, st, m, inv_s, n_rows, K); break;
   }
   return od_launch_status();
 }

@@ -116,6 +116,7 @@ class DenseDecoder:
         cos, sin = rope_tables(cfg, max_pos)
         self.cos, self.sin = cos.to(self.dev), sin.to(self.dev)
         self._ws = {}
+        self._rows = {}
 
     def add_layer(self, lw: dict) -> None:
         L = {k: lw[k].to(self.dev) for k in ("ln1", "ln2", "q_norm", "k_norm")}
@@ -264,7 +265,16 @@ class DenseDecoder:
         R = B * n_opt
         T = states[0][0].length
         h0 = self.embed.index_select(0, ids.reshape(-1))
-        pos = self.positions(T, R, t)
-        row_start, max_rows = kernels.row_start_of([n_opt] * B, self.dev)
+        pos, row_start, max_rows = self.row_layout(T, B, n_opt, t)
         h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
         return self.readout(h, B, n_opt, t)
+
+    def row_layout(self, T: int, B: int, n_opt: int, t: int):
+        """Device positions and per-state row offsets of a scoring pass, built once per shape: a host-to-device
+        copy per pass would wait for the previous pass to drain the stream."""
+        key = (T, B, n_opt, t)
+        if key not in self._rows:
+            pos = self.positions(T, B * n_opt, t)
+            row_start, max_rows = kernels.row_start_of([n_opt] * B, self.dev)
+            self._rows[key] = (pos, row_start, max_rows)
+        return self._rows[key]
