@@ -210,17 +210,6 @@ def cpu_baseline(args):
                        f"scaled x{args.layers} layers")}
 
 
-def wide_work(q, k, v, scale, kvalid=None, causal=True, return_lse=False, out=None):
-    B, H, T, DK = q.shape
-    G, S, DV = k.shape[1], k.shape[2], v.shape[-1]
-    pairs = B * H * (T * S - (T * (T - 1) // 2 if causal and T == S else 0))
-    return (2 * pairs * (DK + DV), 2 * (q.numel() + k.numel() + v.numel() + B * H * T * DV))
-
-
-def append_work(x, q_cache, s_cache, n0):
-    return (x.numel(), x.numel() * 2 + x.numel() + x.shape[0] * x.shape[1] * x.shape[2] * 4)
-
-
 def _gemm_roofline(gemm_t):
     n_g, ms_g, (ops_g, _) = gemm_t.summary()
     tops = ops_g / (ms_g * 1e-3) / 1e12 if n_g else 0.0

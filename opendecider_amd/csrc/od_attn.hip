@@ -11,29 +11,30 @@
 // that state's K/V once for all of them; a wave owns 32 slots.
 //
 // State blocks. The state's keys go in blocks of 64. A block is consumed from LDS as a "block image": its keys as
-// exact fp16 integers with their fp32 scales beside them, its values in fp16 with the per-key scales folded in, both
-// in the swizzled layout the fragment reads want, a -inf bias row for masked keys and two block constants (V
-// exponent, has-a-masked-key). Two paths build
-// it: od_attn_stage writes every block's image to memory once per state (then each workgroup copies images straight
-// into LDS with global_load_lds, and no workgroup converts anything), and od_branched_attn converts the int8 blocks
-// itself in every workgroup. Both produce the same bytes, so both give bit-identical results.
+// exact bf16 integers with their score multipliers beside them, its values in fp16 with the per-key scales folded in,
+// both in the swizzled layout the fragment reads want, a -inf bias row for masked keys and the block constants (V
+// exponent, has-a-masked-key). Two paths build it: od_attn_stage writes every block's image to memory once per
+// state (then each workgroup copies images straight into LDS with global_load_lds and converts nothing), and
+// od_branched_attn converts the int8 blocks itself in every workgroup. Both produce the same bytes, so both give
+// bit-identical results; the host takes the staged path when a (state, KV head) has enough slot tiles to share the
+// images.
 //
-// Layout trick. Scores are computed transposed, S^T = K Q^T, on V_MFMA_F32_32X32X16_F16 with the 32 keys of a key
+// Layout trick. Scores are computed transposed, S^T = K Q^T, on V_MFMA_F32_32X32X16_BF16 with the 32 keys of a key
 // tile as rows and the wave's 32 slots as columns. In the MFMA result layout lane l holds slot l % 32, so the
 // running max / sum / rescale of the online softmax are lane-local (plus one exchange with lane l ^ 32), and the
-// probabilities already sit where the second MFMA, O^T += V^T P^T, wants its B operand: k-step m of the P.V
-// product takes registers 8 (m % 2) .. +7 of key tile m / 2. The V tile is stored transposed (V^T, d-major) with
-// the key order inside every 16-key group permuted to match (bits 2 and 3 of the key index swapped).
+// probabilities already sit where the second MFMA, O^T += V^T P^T on V_MFMA_F32_32X32X16_F16, wants its B operand:
+// k-step m of the P.V product takes registers 8 (m % 2) .. +7 of key tile m / 2. The V tile is stored transposed
+// (V^T, d-major) with the key order inside every 16-key group permuted to match (bits 2 and 3 of the key index
+// swapped).
 //
-// Numerics (fp32 accumulation; the fp16 roundings noted are the only others):
-//  * a state key's int8 values are converted to fp16 exactly (|q| <= 127) and its fp32 K scale multiplies the
-//    score: s = raw * ks[j] (+ -inf for a masked key), so the scores see the exact dequantized keys;
-//  * a state value becomes V' = fp16(q vs 2^-eb), one rounding, with the block's V exponent eb; the accumulator
+// Numerics (fp32 accumulation; the roundings noted are the only others):
+//  * queries are used as they are (bf16); a state key's int8 values are exact bf16 integers, so the MFMA products
+//    are exact, and the score of key j is raw_j * gk_j with gk_j = ks_j scale log2(e) (one rounding in gk_j, one in
+//    the product): the scores see the exact dequantized keys;
+//  * the row's own bf16 keys are used as they are, with the multiplier scale log2(e);
+//  * a state value becomes V' = fp16(q vs_j 2^-eb), one rounding, with the block's V exponent eb; the accumulator
 //    carries one power-of-two frame and is rescaled when a block's frame differs;
-//  * queries are bf16; each slot's query is multiplied by a power of two 2^e (exact) so that its absmax lies in
-//    [2^14, 2^15) and converted to fp16 (exact: fp16 has more mantissa bits than bf16); the factor 2^-e is folded
-//    with the softmax scale and log2(e) into one per-slot multiplier;
-//  * the row's own bf16 K/V get one power-of-two factor per 32-key block in the same way (exact);
+//  * the row's own bf16 values get one power-of-two factor per 32-key block and are converted to fp16;
 //  * probabilities p = exp2(y) <= 2^8 are rounded to fp16 for the P.V product; their sum is taken unrounded.
 // Masked keys get a -inf score; a block with no visible key is an exact no-op for a slot; every row's arithmetic is
 // independent of its position among the rows (fixed key order, no cross-slot reduction), so option order cannot

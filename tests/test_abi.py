@@ -57,3 +57,18 @@ def test_host_only_entry_points(library):
     assert L.od_strerror(0) == b"ok" or b"ok" in L.od_strerror(0).lower()
     for code in (-1, -2, -3, -4, -5):
         assert isinstance(L.od_strerror(code), bytes) and L.od_strerror(code)
+
+
+def test_bench_work_counters_take_the_abi_arguments():
+    """bench.py's timers replace entry points on the loaded library and count each call's work from the raw ABI
+    arguments, so every work function must accept exactly that entry point's argument list."""
+    import sys
+    sys.path.insert(0, ROOT)
+    import bench
+    from opendecider_amd import _lib
+    for name, fn in [("od_w8a8_gemm", bench.gemm_work), ("od_branched_attn", bench.attn_work),
+                     ("od_branched_attn_staged", bench.staged_work), ("od_attn_stage", bench.stage_work),
+                     ("od_wide_attn", bench.wide_work), ("od_kv_quant_append", bench.append_work)]:
+        n = len(_lib.SIGNATURES[name])
+        work = fn(*([1] * n))
+        assert len(work) == 2 and all(isinstance(w, (int, float)) for w in work), name
