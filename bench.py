@@ -165,6 +165,12 @@ def append_work(x, B, H, n, D, *rest):
     return (B * H * n * D, B * H * n * D * 3 + B * H * n * 4)
 
 
+def rope_append_work(qkv, ld, B, S, Hq, Hk, D, *rest):
+    # od_qk_norm_rope_kv_append: q/k/v heads read, q/k heads written back, int8 K/V + scales written
+    tok = B * S
+    return (tok * (Hq + 2 * Hk) * D, tok * ((Hq + 2 * Hk) * D * 2 + (Hq + Hk) * D * 2 + 2 * Hk * (D + 4)))
+
+
 # HBM-side traffic of od_w8a8_gemm per launch at M = 4096 (bytes), from two rocprofv3 --pmc passes (FETCH_SIZE,
 # then WRITE_SIZE) over the four layer GEMMs, each counter scaled by its reading for a plain 256 MiB device copy
 # (fetch x2.000, write x1.000); the summary is profiles/w8a8_gemm_traffic_M4096.md.
@@ -304,7 +310,7 @@ def run_wide_choice(args):
                          .to(torch.bfloat16))
     records = [torch.randint(0, cfg.vocab, (1, rec), generator=g, device=dev) for _ in range(n_rec + args.warmup)]
     ids = torch.randint(0, cfg.vocab, (1, n_req * n_opt, t), generator=g, device=dev)
-    app_t = AbiTimer("od_kv_quant_append", append_work)
+    app_t = AbiTimer("od_qk_norm_rope_kv_append", rope_append_work)
     attn_t = AttnTimers()
     # warm-up: one record + one scoring pass, then rewind the caches
     for i in range(args.warmup):
@@ -349,7 +355,8 @@ def run_wide_choice(args):
                       "avg_launch_us": ms_a / max(n_a, 1) * 1e3},
         "append_per_record": {"full_prefill_ms": sum(rec_ms) / n_rec,
                               "kernel_only_us": sum(app_ms) / n_rec * 1e3,
-                              "kernel": "od_kv_quant_append (K and V, 36 layers)"},
+                              "kernel": ("od_qk_norm_rope_kv_append (q/k norm + RoPE and the K/V quantize-append "
+                                         "in one pass, 36 layers)")},
         "scoring_ms": sum(score_ms) / n_rec,
     }
 

@@ -224,6 +224,23 @@ int od_qk_norm_rope(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int
                     const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t, const uint16_t* sin_t,
                     int64_t n_pos, const int32_t* pos, float eps, od_stream_t stream);
 
+/*
+ * od_qk_norm_rope_kv_append: od_qk_norm_rope plus the int8 K/V append of the same tokens, in one pass over the QKV
+ *   GEMM output. Replaces, for a state prefill: the q/k norm + RoPE of the attention layer (prefix_attn.py:81-90)
+ *   followed by the quantization of the new tokens' K/V slice that PrefixCache._take (state_cache.py:79) and
+ *   PackedCache.pack (backbone.py:446) run through Int8Tensor.quantize (quant.py:36-41).
+ *   qkv bf16 [B * S, ld], row b * S + i = token i of state b, holding n_heads_q query heads, n_heads_k key heads
+ *   and n_heads_k value heads of D values. Query and key heads are normalized and rotated in place as in
+ *   od_qk_norm_rope (pos int32 [B * S]); then every key head (after RoPE) and value head is quantized per (token,
+ *   head) into kq / vq int8 [B, n_heads_k, cap, D] rows n0 .. n0 + S - 1 with scales ks / vs fp32 [B, n_heads_k, cap]:
+ *   the bytes od_kv_quant_append writes for the same bf16 values. Requires n0 + S <= cap, D in {64, 128},
+ *   ld % 4 == 0, 8-byte aligned qkv / weights / tables and 4-byte aligned kq / vq (else OD_ERR_ALIGN).
+ */
+int od_qk_norm_rope_kv_append(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, int64_t n_heads_q, int64_t n_heads_k,
+                              int64_t D, const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
+                              const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps, int8_t* kq,
+                              float* ks, int8_t* vq, float* vs, int64_t cap, int64_t n0, od_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -290,59 +290,102 @@ __global__ __launch_bounds__(kThreads) void silu_mul_quant_vec_kernel(const uint
   if (threadIdx.x == 0) sa[row] = scale;
 }
 
-// q/k RMSNorm + RoPE for head_dim 128 with 16 lanes per head: lane j holds d = 4j..4j+3 and the rotary partners
-// 64 + 4j..64 + 4j + 3, so every load and store is 8 bytes and no lane exchange is needed for the rotation.
-__global__ __launch_bounds__(kThreads) void qk_norm_rope128_kernel(uint16_t* __restrict__ qkv, int64_t ld, int64_t M,
-                                                                   int n_heads_q, int n_heads_k,
-                                                                   const uint16_t* __restrict__ qw,
-                                                                   const uint16_t* __restrict__ kw,
-                                                                   const uint16_t* __restrict__ cos_t,
-                                                                   const uint16_t* __restrict__ sin_t, int64_t n_pos,
-                                                                   const int32_t* __restrict__ pos, float eps) {
-  constexpr int D = 128, L = 64;
-  const int heads = n_heads_q + n_heads_k;
-  const int64_t gh = (int64_t)blockIdx.x * (kThreads / 16) + threadIdx.x / 16;
-  if (gh >= M * heads) return;  // whole 16-lane groups exit together
+// q/k RMSNorm + RoPE with G = D / 8 lanes per head: lane j holds d = 4j..4j+3 and the rotary partners
+// D/2 + 4j..D/2 + 4j + 3, so every load and store is 8 bytes and no lane exchange is needed for the rotation.
+// APPEND: the launch also covers the n_heads_k value heads of every row, and the key heads (after RoPE) and value
+// heads are quantized per (token, head) into int8 caches, with the bytes od_kv_quant_append writes for the same
+// bf16 values (row m = b * S + i of qkv goes to cache row (b * n_heads_k + h) * cap + n0 + i).
+struct KvAppend {
+  int8_t* kq;
+  float* ks;
+  int8_t* vq;
+  float* vs;
+  int64_t S, cap, n0;
+};
+
+__device__ __forceinline__ void unpack4(uint2 u, float (&f)[4]) {
+  f[0] = __uint_as_float(u.x << 16);
+  f[1] = __uint_as_float(u.x & 0xffff0000u);
+  f[2] = __uint_as_float(u.y << 16);
+  f[3] = __uint_as_float(u.y & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint2 pack4(const uint16_t (&h)[4]) {
+  return make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+}
+
+// Quantizes a head's D bf16 values held 8 per lane (oa: d = 4j.., ob: D/2 + 4j..) over the G lanes of its group and
+// writes the int8 row and its scale.
+template <int D>
+__device__ __forceinline__ void quant_head(const uint16_t (&oa)[4], const uint16_t (&ob)[4], int j, int8_t* qrow,
+                                           float* srow) {
+  constexpr int G = D / 8;
+  float y[8];
+  uint32_t bits = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[e] = od_bf16_to_f32(oa[e]);
+    y[4 + e] = od_bf16_to_f32(ob[e]);
+    bits = max(bits, (uint32_t)(oa[e] & 0x7fffu));
+    bits = max(bits, (uint32_t)(ob[e] & 0x7fffu));
+  }
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) bits = max(bits, (uint32_t)__shfl_xor((int)bits, o, OD_WAVE));
+  const float scale = od_q8_scale(__uint_as_float(bits << 16)), inv = 1.0f / scale;
+  uint32_t w[2];
+  od_q8_words<8>(y, scale, inv, w);
+  *reinterpret_cast<uint32_t*>(qrow + 4 * j) = w[0];
+  *reinterpret_cast<uint32_t*>(qrow + D / 2 + 4 * j) = w[1];
+  if (j == 0) *srow = scale;
+}
+
+template <int D, bool APPEND>
+__global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restrict__ qkv, int64_t ld, int64_t M,
+                                                               int n_heads_q, int n_heads_k,
+                                                               const uint16_t* __restrict__ qw,
+                                                               const uint16_t* __restrict__ kw,
+                                                               const uint16_t* __restrict__ cos_t,
+                                                               const uint16_t* __restrict__ sin_t, int64_t n_pos,
+                                                               const int32_t* __restrict__ pos, float eps,
+                                                               KvAppend kv) {
+  constexpr int G = D / 8, L = D / 2;
+  const int heads = n_heads_q + n_heads_k * (APPEND ? 2 : 1);
+  const int64_t gh = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
+  if (gh >= M * heads) return;  // whole G-lane groups exit together
   const int64_t row = gh / heads;
   const int head = (int)(gh % heads);
-  const int j = threadIdx.x % 16;
+  const int j = threadIdx.x % G;
   uint16_t* hp = qkv + row * ld + (int64_t)head * D;
-  const uint16_t* w = head < n_heads_q ? qw : kw;
   const uint2 ra = *reinterpret_cast<const uint2*>(hp + 4 * j), rb = *reinterpret_cast<const uint2*>(hp + L + 4 * j);
-  const uint2 wa = *reinterpret_cast<const uint2*>(w + 4 * j), wb = *reinterpret_cast<const uint2*>(w + L + 4 * j);
-  float a[4], b[4], fa[4], fb[4];
-  const uint32_t ua[2] = {ra.x, ra.y}, ub[2] = {rb.x, rb.y}, uwa[2] = {wa.x, wa.y}, uwb[2] = {wb.x, wb.y};
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    a[2 * e] = __uint_as_float(ua[e] << 16);
-    a[2 * e + 1] = __uint_as_float(ua[e] & 0xffff0000u);
-    b[2 * e] = __uint_as_float(ub[e] << 16);
-    b[2 * e + 1] = __uint_as_float(ub[e] & 0xffff0000u);
-    fa[2 * e] = __uint_as_float(uwa[e] << 16);
-    fa[2 * e + 1] = __uint_as_float(uwa[e] & 0xffff0000u);
-    fb[2 * e] = __uint_as_float(uwb[e] << 16);
-    fb[2 * e + 1] = __uint_as_float(uwb[e] & 0xffff0000u);
+  int64_t crow = 0;
+  if (APPEND) {
+    const int64_t b = row / kv.S, i = row % kv.S;
+    crow = (b * n_heads_k + (head - n_heads_q) % n_heads_k) * kv.cap + kv.n0 + i;
   }
+  if (APPEND && head >= n_heads_q + n_heads_k) {  // a value head: quantize only
+    const uint16_t va[4] = {(uint16_t)ra.x, (uint16_t)(ra.x >> 16), (uint16_t)ra.y, (uint16_t)(ra.y >> 16)};
+    const uint16_t vb[4] = {(uint16_t)rb.x, (uint16_t)(rb.x >> 16), (uint16_t)rb.y, (uint16_t)(rb.y >> 16)};
+    quant_head<D>(va, vb, j, kv.vq + crow * D, kv.vs + crow);
+    return;
+  }
+  const uint16_t* w = head < n_heads_q ? qw : kw;
+  float a[4], b[4], fa[4], fb[4];
+  unpack4(ra, a);
+  unpack4(rb, b);
+  unpack4(*reinterpret_cast<const uint2*>(w + 4 * j), fa);
+  unpack4(*reinterpret_cast<const uint2*>(w + L + 4 * j), fb);
   float ss = 0.0f;
 #pragma unroll
   for (int e = 0; e < 4; ++e) ss = fmaf(b[e], b[e], fmaf(a[e], a[e], ss));
 #pragma unroll
-  for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, OD_WAVE);
+  for (int o = G / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, OD_WAVE);
   const float r = 1.0f / sqrtf(ss / (float)D + eps);
   const int64_t p = pos[row];
   const bool in_table = p >= 0 && p < n_pos;  // a position past the tables yields NaN, never an out-of-bounds read
   float c[4], sn[4];
   if (in_table) {
-    const uint2 rc = *reinterpret_cast<const uint2*>(cos_t + p * L + 4 * j);
-    const uint2 rs = *reinterpret_cast<const uint2*>(sin_t + p * L + 4 * j);
-    const uint32_t uc[2] = {rc.x, rc.y}, us[2] = {rs.x, rs.y};
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      c[2 * e] = __uint_as_float(uc[e] << 16);
-      c[2 * e + 1] = __uint_as_float(uc[e] & 0xffff0000u);
-      sn[2 * e] = __uint_as_float(us[e] << 16);
-      sn[2 * e + 1] = __uint_as_float(us[e] & 0xffff0000u);
-    }
+    unpack4(*reinterpret_cast<const uint2*>(cos_t + p * L + 4 * j), c);
+    unpack4(*reinterpret_cast<const uint2*>(sin_t + p * L + 4 * j), sn);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e) c[e] = sn[e] = __builtin_nanf("");
@@ -354,10 +397,9 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope128_kernel(uint16_t* __r
     oa[e] = od_f32_to_bf16(bfr(na * c[e]) + bfr(-nb * sn[e]));
     ob[e] = od_f32_to_bf16(bfr(nb * c[e]) + bfr(na * sn[e]));
   }
-  *reinterpret_cast<uint2*>(hp + 4 * j) =
-      make_uint2((uint32_t)oa[0] | ((uint32_t)oa[1] << 16), (uint32_t)oa[2] | ((uint32_t)oa[3] << 16));
-  *reinterpret_cast<uint2*>(hp + L + 4 * j) =
-      make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
+  *reinterpret_cast<uint2*>(hp + 4 * j) = pack4(oa);
+  *reinterpret_cast<uint2*>(hp + L + 4 * j) = pack4(ob);
+  if (APPEND && head >= n_heads_q) quant_head<D>(oa, ob, j, kv.kq + crow * D, kv.ks + crow);
 }
 
 template <int NV>
@@ -426,6 +468,30 @@ extern "C" int od_silu_mul_quant(const uint16_t* gu, int64_t ldg, int64_t F, con
   return od_launch_status();
 }
 
+namespace {
+
+bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; }
+
+template <bool APPEND>
+int launch_rope_vec(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int64_t n_heads_k, int64_t D,
+                    const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t, const uint16_t* sin_t,
+                    int64_t n_pos, const int32_t* pos, float eps, const KvAppend& kv, hipStream_t st) {
+  const int64_t heads = n_heads_q + n_heads_k * (APPEND ? 2 : 1);
+  const int64_t per_block = kThreads / (D / 8);
+  const int64_t blocks = (M * heads + per_block - 1) / per_block;
+  if (blocks > 0x7fffffff || heads > 0x7fffffff) return OD_ERR_SHAPE;
+  if (D == 128) {
+    qk_rope_vec_kernel<128, APPEND><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
+        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+  } else {
+    qk_rope_vec_kernel<64, APPEND><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
+        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+  }
+  return od_launch_status();
+}
+
+}  // namespace
+
 extern "C" int od_qk_norm_rope(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int64_t n_heads_k,
                                int64_t D, const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
                                const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps,
@@ -439,14 +505,11 @@ extern "C" int od_qk_norm_rope(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_h
   const int64_t blocks = (M * heads + per_block - 1) / per_block;
   if (blocks > 0x7fffffff || heads > 0x7fffffff) return OD_ERR_SHAPE;
   hipStream_t st = (hipStream_t)stream;
-  const bool vec128 = D == 128 && (ld % 4 == 0) && ((((uintptr_t)qkv) & 7u) == 0) && ((((uintptr_t)q_w) & 7u) == 0) &&
-                      ((((uintptr_t)k_w) & 7u) == 0) && ((((uintptr_t)cos_t) & 7u) == 0) &&
-                      ((((uintptr_t)sin_t) & 7u) == 0);
-  if (vec128) {
-    const int64_t b16 = (M * heads + kThreads / 16 - 1) / (kThreads / 16);
-    if (b16 > 0x7fffffff) return OD_ERR_SHAPE;
-    qk_norm_rope128_kernel<<<dim3((unsigned)b16), dim3(kThreads), 0, st>>>(qkv, ld, M, (int)n_heads_q, (int)n_heads_k,
-                                                                           q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
+  const bool vec = (ld % 4 == 0) && aligned8(qkv) && aligned8(q_w) && aligned8(k_w) && aligned8(cos_t) &&
+                   aligned8(sin_t);
+  if (vec) {
+    return launch_rope_vec<false>(qkv, ld, M, n_heads_q, n_heads_k, D, q_w, k_w, cos_t, sin_t, n_pos, pos, eps,
+                                  KvAppend{}, st);
   } else if (D == 128) {
     qk_norm_rope_kernel<128><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
         qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
@@ -455,4 +518,25 @@ extern "C" int od_qk_norm_rope(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_h
         qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
   }
   return od_launch_status();
+}
+
+extern "C" int od_qk_norm_rope_kv_append(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, int64_t n_heads_q,
+                                         int64_t n_heads_k, int64_t D, const uint16_t* q_w, const uint16_t* k_w,
+                                         const uint16_t* cos_t, const uint16_t* sin_t, int64_t n_pos,
+                                         const int32_t* pos, float eps, int8_t* kq, float* ks, int8_t* vq, float* vs,
+                                         int64_t cap, int64_t n0, od_stream_t stream) {
+  if (B < 0 || S < 0 || n_heads_q < 0 || n_heads_k < 0 || ld < (n_heads_q + 2 * n_heads_k) * D) return OD_ERR_SHAPE;
+  if (n0 < 0 || cap < 0 || n0 + S > cap) return OD_ERR_SHAPE;
+  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  const int64_t M = B * S;
+  if (M == 0 || n_heads_q + n_heads_k == 0) return OD_OK;
+  if (!qkv || !q_w || !k_w || !cos_t || !sin_t || !pos) return OD_ERR_NULL;
+  if (n_heads_k > 0 && (!kq || !ks || !vq || !vs)) return OD_ERR_NULL;
+  if (B * n_heads_k * cap > (int64_t)1 << 40) return OD_ERR_SHAPE;
+  if ((ld % 4) || !aligned8(qkv) || !aligned8(q_w) || !aligned8(k_w) || !aligned8(cos_t) || !aligned8(sin_t) ||
+      (((uintptr_t)kq) & 3u) || (((uintptr_t)vq) & 3u))
+    return OD_ERR_ALIGN;
+  KvAppend kv{kq, ks, vq, vs, S, cap, n0};
+  return launch_rope_vec<true>(qkv, ld, M, n_heads_q, n_heads_k, D, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv,
+                               (hipStream_t)stream);
 }

@@ -150,13 +150,19 @@ class DenseDecoder:
                  Int8KVCache(batch, cfg.n_kv_heads, cfg.head_dim, capacity, self.dev)) for _ in self.layers]
 
     # ---------------------------------------------------------------- forward
-    def _attn_in(self, li: int, h: torch.Tensor, ws: dict, pos: torch.Tensor) -> torch.Tensor:
-        """RMSNorm + quantize, W8A8 QKV GEMM, q/k norm + RoPE (in place): the layer's qkv (M, qkv_out) bf16."""
+    def _attn_in(self, li: int, h: torch.Tensor, ws: dict, pos: torch.Tensor, append=None) -> torch.Tensor:
+        """RMSNorm + quantize, W8A8 QKV GEMM, q/k norm + RoPE (in place): the layer's qkv (M, qkv_out) bf16.
+        append = (B, S, K cache, V cache): the same pass also appends the tokens' int8 K/V to the caches."""
         cfg, L = self.cfg, self.layers[li]
         kernels.rmsnorm_quant(h, L["ln1"], cfg.eps, L["qkv"].inv_s, ws["xq"][:, :cfg.hidden], ws["sx"])
         qkv = kernels.w8a8_gemm(ws["xq"][:, :cfg.hidden], ws["sx"], L["qkv"].q, L["qkv"].scale, out=ws["qkv"])
-        kernels.qk_norm_rope(qkv, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, L["q_norm"], L["k_norm"], self.cos,
-                             self.sin, pos, cfg.eps)
+        if append is None:
+            kernels.qk_norm_rope(qkv, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, L["q_norm"], L["k_norm"], self.cos,
+                                 self.sin, pos, cfg.eps)
+        else:
+            B, S, cache_k, cache_v = append
+            kernels.qk_norm_rope_kv_append(qkv, B, S, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, L["q_norm"],
+                                           L["k_norm"], self.cos, self.sin, pos, cfg.eps, cache_k, cache_v)
         return qkv
 
     def _heads(self, qkv: torch.Tensor, ws: dict, R: int, t: int):
@@ -198,22 +204,21 @@ class DenseDecoder:
         """One layer over S new state tokens of each of B states, appended after the cache's current n0 tokens.
         n0 = 0: causal attention among the new tokens on bf16 K/V (wide_attention), as the backbone's state pass.
         n0 > 0 (an appended record, S <= 256): the new tokens attend the cached int8 state and themselves causally
-        (the branched kernel with one row per state). Then only the new tokens' K/V are quantized and appended
-        (state_cache.py:79)."""
+        (the branched kernel with one row per state). Only the new tokens' K/V are quantized and appended
+        (state_cache.py:79), in the same pass as the q/k norm + RoPE; the attention reads the cache's first n0 tokens
+        only."""
         D = self.cfg.head_dim
-        qkv = self._attn_in(li, h, ws, pos)
-        q, k, v, attn = self._heads(qkv, ws, B, S)
         n0 = cache_k.length
+        if S > 256 and n0 > 0:
+            raise ValueError(f"prefill: an appended record of {S} tokens exceeds 256 (append it in pieces)")
+        qkv = self._attn_in(li, h, ws, pos, append=(B, S, cache_k, cache_v))
+        q, k, v, attn = self._heads(qkv, ws, B, S)
         if n0 == 0:
             kernels.wide_attn(q, k, v, D ** -0.5, kvalid=kvalid, causal=True, out=attn)
         else:
-            if S > 256:
-                raise ValueError(f"prefill: an appended record of {S} tokens exceeds 256 (append it in pieces)")
             rs, mr = (None, B) if B == 1 else (row_start, B)
             kernels.branched_attn(q, k, v, cache_k.q, cache_k.scale, cache_v.q, cache_v.scale, D ** -0.5,
                                   kvalid=kvalid, length=n0, out=attn, row_start=rs, max_rows=mr)
-        cache_k.append(k)
-        cache_v.append(v)
         return self._attn_out_mlp(li, h, h_out, ws)
 
     def prefill(self, ids: torch.Tensor, caches: list, kvalid=None) -> torch.Tensor:

@@ -102,6 +102,35 @@ def qk_norm_rope(qkv: torch.Tensor, n_heads_q: int, n_heads_k: int, D: int, q_w,
           "od_qk_norm_rope")
 
 
+def qk_norm_rope_kv_append(qkv: torch.Tensor, B: int, S: int, n_heads_q: int, n_heads_k: int, D: int, q_w, k_w,
+                           cos_t, sin_t, pos, eps: float, k_cache, v_cache) -> None:
+    """qk_norm_rope on qkv (B S, >= (Hq + 2 Hk) D), then the new tokens' key heads (after RoPE) and value heads
+    quantized per (token, head) and written at positions length .. length + S - 1 of the Int8KVCache pair, in one
+    pass (the bytes kv_quant_append writes for the same bf16 K/V). The caches' lengths are advanced."""
+    require_gpu(qkv, q_w, k_w, cos_t, sin_t, pos, k_cache.q, v_cache.q, name="qk_norm_rope_kv_append")
+    _lib.bf16_bits(qkv)
+    if qkv.stride(1) != 1 or qkv.shape[0] != B * S:
+        raise ValueError("qk_norm_rope_kv_append: qkv must be (B S, ...) with contiguous rows")
+    q_w, k_w = _vec(q_w, D, "q_w"), _vec(k_w, D, "k_w")
+    if cos_t.shape != sin_t.shape or cos_t.shape[1] != D // 2 or not (cos_t.is_contiguous() and sin_t.is_contiguous()):
+        raise ValueError("qk_norm_rope_kv_append: cos/sin tables must be contiguous [positions, D/2]")
+    if pos.dtype != torch.int32 or pos.numel() != B * S:
+        raise ValueError("qk_norm_rope_kv_append: pos must be int32 (B S,)")
+    n0 = k_cache.length
+    if v_cache.length != n0 or k_cache.q.shape != (B, n_heads_k, k_cache.capacity, D) or \
+            v_cache.q.shape != k_cache.q.shape:
+        raise ValueError("qk_norm_rope_kv_append: K/V caches must match (B, Hkv, cap, D) at the same length")
+    if n0 + S > k_cache.capacity:
+        raise ValueError(f"qk_norm_rope_kv_append: {n0} + {S} tokens exceed the capacity {k_cache.capacity}")
+    check(lib().od_qk_norm_rope_kv_append(ptr(qkv), qkv.stride(0), B, S, n_heads_q, n_heads_k, D, ptr(q_w), ptr(k_w),
+                                          ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos.contiguous()), float(eps),
+                                          ptr(k_cache.q), ptr(k_cache.scale), ptr(v_cache.q), ptr(v_cache.scale),
+                                          k_cache.capacity, n0, stream_of(qkv)),
+          "od_qk_norm_rope_kv_append")
+    k_cache.length += S
+    v_cache.length += S
+
+
 def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, bias=None, residual=None,
               out: torch.Tensor | None = None, want_out: bool = True, want_acc: bool = False):
     """int8 a (M, Kp) x int8 w (N, Kp)^T -> bf16 (M, N) = bf16(float(acc) sa[m] sw[n] + bias + residual); Kp is

@@ -70,6 +70,56 @@ def test_qk_norm_rope(gpu_lib, D):
     assert torch.equal(x.cpu()[:, 10 * D:], qkv[:, 10 * D:])
 
 
+@pytest.mark.parametrize("D,B,S,n0", [(128, 2, 37, 0), (128, 3, 16, 21), (64, 2, 9, 5)])
+def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0):
+    """The fused q/k norm + RoPE + int8 K/V append writes exactly what qk_norm_rope followed by two kv_quant_append
+    calls write: the same qkv bits, cache bytes and scales, and leaves the cache rows before n0 and after n0 + S
+    alone. Then the fused result against the oracle: RoPE within one bf16 step, K/V bytes = the oracle's
+    quantizer applied to the GPU's rotated K and to V."""
+    from opendecider_amd import kernels
+    from opendecider_amd.kv_cache import Int8KVCache
+    Hq, Hk, cap = 8, 2, n0 + S + 7
+    cfg = od.DecoderConfig(hidden=Hq * D, n_heads=Hq, n_kv_heads=Hk, head_dim=D)
+    g = torch.Generator().manual_seed(D + S + n0)
+    qkv = (torch.randn(B * S, cfg.qkv_out, generator=g) * 2).to(torch.bfloat16)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    pos = (n0 + torch.arange(S, dtype=torch.int32)).repeat(B).to(DEV)
+    cos, sin = (t.to(DEV) for t in od.rope_tables(cfg, n0 + S + 8))
+    caches = []
+    for _ in range(2):
+        pair = [Int8KVCache(B, Hk, D, cap, DEV) for _ in range(2)]
+        for c in pair:                                   # sentinel bytes around the appended rows
+            c.q.fill_(77)
+            c.scale.fill_(-1.0)
+            c.length = n0
+        caches.append(pair)
+    x1, x2 = qkv.to(DEV), qkv.to(DEV)
+    print(f"fused rope+append D={D} B={B} S={S} n0={n0}", flush=True)
+    kernels.qk_norm_rope_kv_append(x1, B, S, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, *caches[0])
+    kernels.qk_norm_rope(x2, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps)
+    k = x2[:, Hq * D:(Hq + Hk) * D].view(B, S, Hk, D).transpose(1, 2)
+    v = x2[:, (Hq + Hk) * D:].view(B, S, Hk, D).transpose(1, 2)
+    caches[1][0].append(k)
+    caches[1][1].append(v)
+    torch.cuda.synchronize()
+    assert torch.equal(x1.view(torch.int16), x2.view(torch.int16))
+    for a, b in zip(caches[0], caches[1]):
+        assert a.length == b.length == n0 + S
+        assert torch.equal(a.q, b.q) and torch.equal(a.scale.view(torch.int32), b.scale.view(torch.int32))
+        assert (a.q[:, :, :n0] == 77).all() and (a.q[:, :, n0 + S:] == 77).all()
+    ref = od.qk_norm_rope(qkv, cfg, qw.cpu(), kw.cpu(), cos.cpu(), sin.cpu(), pos.cpu().long())
+    got = x1.cpu().float()
+    assert ((got - ref.float()).abs() <= ref.float().abs() * 2.0 ** -7 + 2.0 ** -14).all()
+    for c, cols in ((caches[0][0], slice(Hq * D, (Hq + Hk) * D)), (caches[0][1], slice((Hq + Hk) * D, None))):
+        src = x1.cpu()[:, cols].view(B, S, Hk, D).transpose(1, 2)
+        rq, rs = oq.quantize_rows(src.reshape(-1, D))
+        assert torch.equal(c.q[:, :, n0:n0 + S].cpu().reshape(-1, D), rq)
+        assert torch.equal(c.scale[:, :, n0:n0 + S].cpu().reshape(-1), rs.reshape(-1))
+    with pytest.raises(ValueError):                      # past the capacity: refused before any write
+        kernels.qk_norm_rope_kv_append(x1, B, S, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, *caches[0])
+
+
 def _states(cfg, B, T, layers, seed):
     g = torch.Generator().manual_seed(seed)
     out = []
