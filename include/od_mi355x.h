@@ -84,6 +84,20 @@ int od_kv_quant_append(const uint16_t* x, int64_t B, int64_t H, int64_t n_new, i
                        int64_t sxt, int8_t* q, float* s, int64_t cap, int64_t n0, od_stream_t stream);
 
 /*
+ * od_kv_copy_rows — copy runs of int8 cache rows (with their fp32 scales) between two K/V buffers, every matrix and
+ * head in one launch, bytes unchanged. Replaces: PrefixCache._take's copy of a snapshot's own tokens and
+ * PrefixCache._restore's concatenation of the path's deltas followed by a re-pack (state_cache.py:68-93,106-124,
+ * which dequantizes and quantizes again); here a restore writes the stored bytes back.
+ *   src_q int8 / src_s fp32: n_mats matrices (a layer's K or V of one state) at element strides src_mat_q /
+ *   src_mat_s, each [H][src_cap][D] / [H][src_cap]; dst likewise with dst_cap. seg: HOST array of n_seg runs
+ *   (src_row, dst_row, n_rows), every run copied for every matrix and head. Requires D % 16 == 0, 16-byte aligned
+ *   src_q / dst_q and matrix strides, each run inside both capacities (checked), n_mats * H <= 65535.
+ */
+int od_kv_copy_rows(const int8_t* src_q, const float* src_s, int64_t src_mat_q, int64_t src_mat_s, int64_t src_cap,
+                    int8_t* dst_q, float* dst_s, int64_t dst_mat_q, int64_t dst_mat_s, int64_t dst_cap,
+                    int64_t n_mats, int64_t H, int64_t D, const int64_t* seg, int64_t n_seg, od_stream_t stream);
+
+/*
  * od_branched_attn — branched (Hydragen) option-row attention over an int8 shared state, one launch.
  * Replaces: _split_attention (src/opendecider/prefix_attn.py:43-76) with its two wide_attention launches
  * (src/opendecider/wide_attention.py:70-91) and the torch LSE merge (prefix_attn.py:74-76), the per-state loop

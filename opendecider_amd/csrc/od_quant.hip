@@ -260,6 +260,89 @@ extern "C" int od_kv_quant_append(const uint16_t* x, int64_t B, int64_t H, int64
   return launch_quant<kKv>(m, nullptr, n_rows, D, vec_ok, (hipStream_t)stream);
 }
 
+namespace {
+
+// ---------------------------------------------------------------------------- int8 K/V row copies
+// Copies runs of cache rows (int8 [rows, D] + fp32 scale per row) between two buffers laid out as
+// [n_mats][H][cap][D] (a matrix is one layer's K or V of one state). A launch takes up to kMaxSegs runs by value; a
+// workgroup copies one 64-row chunk of one run for one (matrix, head): 16-byte loads and stores, HBM-bound.
+constexpr int kMaxSegs = 32;
+constexpr int kCopyRows = 64;
+
+struct CopySegs {
+  int64_t src_row[kMaxSegs], dst_row[kMaxSegs], n_rows[kMaxSegs];
+  int first_chunk[kMaxSegs + 1];
+  int n_seg;
+};
+
+struct CopyArgs {
+  const int8_t* src_q;
+  const float* src_s;
+  int8_t* dst_q;
+  float* dst_s;
+  int64_t src_mat_q, src_mat_s, src_cap, dst_mat_q, dst_mat_s, dst_cap;
+  int H, D;
+};
+
+__global__ __launch_bounds__(kThreads) void kv_copy_rows_kernel(CopyArgs a, CopySegs sg) {
+  const int chunk = blockIdx.x;
+  int s = 0;
+  while (s + 1 < sg.n_seg && sg.first_chunk[s + 1] <= chunk) ++s;  // wave-uniform
+  const int64_t r0 = (int64_t)(chunk - sg.first_chunk[s]) * kCopyRows;
+  const int64_t n = min((int64_t)kCopyRows, sg.n_rows[s] - r0);
+  const int mat = blockIdx.y / a.H, h = blockIdx.y % a.H;
+  const int64_t src_row = (int64_t)h * a.src_cap + sg.src_row[s] + r0;
+  const int64_t dst_row = (int64_t)h * a.dst_cap + sg.dst_row[s] + r0;
+  const int8_t* sq = a.src_q + mat * a.src_mat_q + src_row * a.D;
+  int8_t* dq = a.dst_q + mat * a.dst_mat_q + dst_row * a.D;
+  const int64_t vecs = n * a.D / 16;  // D % 16 == 0
+  for (int64_t i = threadIdx.x; i < vecs; i += kThreads)
+    reinterpret_cast<uint4*>(dq)[i] = reinterpret_cast<const uint4*>(sq)[i];
+  if (threadIdx.x < n) a.dst_s[mat * a.dst_mat_s + dst_row + threadIdx.x] = a.src_s[mat * a.src_mat_s + src_row + threadIdx.x];
+}
+
+}  // namespace
+
+extern "C" int od_kv_copy_rows(const int8_t* src_q, const float* src_s, int64_t src_mat_q, int64_t src_mat_s,
+                               int64_t src_cap, int8_t* dst_q, float* dst_s, int64_t dst_mat_q, int64_t dst_mat_s,
+                               int64_t dst_cap, int64_t n_mats, int64_t H, int64_t D, const int64_t* seg,
+                               int64_t n_seg, od_stream_t stream) {
+  if (n_mats < 0 || H < 0 || D < 16 || D % 16 || n_seg < 0 || src_cap < 0 || dst_cap < 0) return OD_ERR_SHAPE;
+  if (n_mats == 0 || H == 0 || n_seg == 0) return OD_OK;
+  if (!src_q || !src_s || !dst_q || !dst_s || !seg) return OD_ERR_NULL;
+  if (n_mats * H > 65535) return OD_ERR_SHAPE;
+  if (src_mat_q < H * src_cap * D || dst_mat_q < H * dst_cap * D || src_mat_s < H * src_cap || dst_mat_s < H * dst_cap)
+    return OD_ERR_SHAPE;
+  if (!od_aligned16(src_q) || !od_aligned16(dst_q) || (src_mat_q % 16) || (dst_mat_q % 16)) return OD_ERR_ALIGN;
+  for (int64_t i = 0; i < n_seg; ++i) {  // every run inside both buffers (the kernel trusts the table)
+    const int64_t s0 = seg[3 * i], d0 = seg[3 * i + 1], n = seg[3 * i + 2];
+    if (n < 0 || s0 < 0 || d0 < 0 || s0 + n > src_cap || d0 + n > dst_cap) return OD_ERR_SHAPE;
+  }
+  CopyArgs a{src_q, src_s, dst_q, dst_s, src_mat_q, src_mat_s, src_cap, dst_mat_q, dst_mat_s, dst_cap, (int)H, (int)D};
+  for (int64_t base = 0; base < n_seg; base += kMaxSegs) {
+    CopySegs sg{};
+    int chunks = 0;
+    for (int64_t i = base; i < n_seg && sg.n_seg < kMaxSegs; ++i) {
+      const int64_t n = seg[3 * i + 2];
+      if (n == 0) continue;
+      const int k = sg.n_seg++;
+      sg.src_row[k] = seg[3 * i];
+      sg.dst_row[k] = seg[3 * i + 1];
+      sg.n_rows[k] = n;
+      sg.first_chunk[k] = chunks;
+      const int64_t c = (n + kCopyRows - 1) / kCopyRows;
+      if (chunks + c > 0x7fffffff) return OD_ERR_SHAPE;
+      chunks += (int)c;
+    }
+    if (sg.n_seg == 0) continue;
+    sg.first_chunk[sg.n_seg] = chunks;
+    kv_copy_rows_kernel<<<dim3((unsigned)chunks, (unsigned)(n_mats * H)), dim3(kThreads), 0, (hipStream_t)stream>>>(a, sg);
+    const int rc = od_launch_status();
+    if (rc != OD_OK) return rc;
+  }
+  return OD_OK;
+}
+
 extern "C" const char* od_strerror(int code) {
   switch (code) {
     case OD_OK: return "ok";

@@ -21,7 +21,7 @@ from dataclasses import dataclass
 import torch
 
 from . import kernels
-from .kv_cache import Int8KVCache
+from .kv_cache import Int8KVCache, StateKV
 
 
 @dataclass
@@ -143,11 +143,10 @@ class DenseDecoder:
         }
         return self._ws[M]
 
-    def new_state_caches(self, batch: int, capacity: int) -> list:
-        """Empty per-layer (K, V) int8 caches for `batch` states of up to `capacity` tokens."""
+    def new_state_caches(self, batch: int, capacity: int) -> StateKV:
+        """Empty per-layer (K, V) int8 caches for `batch` states of up to `capacity` tokens, in one allocation."""
         cfg = self.cfg
-        return [(Int8KVCache(batch, cfg.n_kv_heads, cfg.head_dim, capacity, self.dev),
-                 Int8KVCache(batch, cfg.n_kv_heads, cfg.head_dim, capacity, self.dev)) for _ in self.layers]
+        return StateKV(len(self.layers), batch, cfg.n_kv_heads, cfg.head_dim, capacity, self.dev)
 
     # ---------------------------------------------------------------- forward
     def _attn_in(self, li: int, h: torch.Tensor, ws: dict, pos: torch.Tensor, append=None) -> torch.Tensor:

@@ -184,6 +184,34 @@ def kv_quant_append(x: torch.Tensor, q_cache: torch.Tensor, s_cache: torch.Tenso
                                    ptr(s_cache), cap, n0, stream_of(x)), "od_kv_quant_append")
 
 
+def kv_copy_rows(src_q: torch.Tensor, src_s: torch.Tensor, dst_q: torch.Tensor, dst_s: torch.Tensor, segs) -> None:
+    """Copy runs of int8 cache rows and their fp32 scales, bytes unchanged, in one launch (per 32 runs).
+    src_q (n_mats, H, src_cap, D) int8 and src_s (n_mats, H, src_cap) fp32, each matrix [H, cap, D] contiguous (any
+    stride between matrices); dst_q / dst_s likewise with their own capacity. segs: (src_row, dst_row, n_rows) runs,
+    each copied for every matrix and head."""
+    require_gpu(src_q, src_s, dst_q, dst_s, name="kv_copy_rows")
+    n_mats, H, src_cap, D = src_q.shape
+    dst_cap = dst_q.shape[2]
+    if src_q.dtype != torch.int8 or dst_q.dtype != torch.int8 or src_s.dtype != torch.float32 or \
+            dst_s.dtype != torch.float32:
+        raise TypeError("kv_copy_rows: int8 rows with fp32 scales")
+    if dst_q.shape != (n_mats, H, dst_cap, D) or src_s.shape != (n_mats, H, src_cap) or \
+            dst_s.shape != (n_mats, H, dst_cap):
+        raise ValueError("kv_copy_rows: source and destination shapes do not match")
+    for q, s in ((src_q, src_s), (dst_q, dst_s)):
+        cap = q.shape[2]
+        if q.stride()[1:] != (cap * D, D, 1) or s.stride()[1:] != (cap, 1):
+            raise ValueError("kv_copy_rows: every matrix must be a contiguous [H, cap, D] block")
+    flat = [int(v) for seg in segs for v in seg]
+    if len(flat) % 3:
+        raise ValueError("kv_copy_rows: segments are (src_row, dst_row, n_rows) triples")
+    arr = (ctypes.c_int64 * max(len(flat), 1))(*flat)
+    check(lib().od_kv_copy_rows(ptr(src_q), ptr(src_s), src_q.stride(0), src_s.stride(0), src_cap, ptr(dst_q),
+                                ptr(dst_s), dst_q.stride(0), dst_s.stride(0), dst_cap, n_mats, H, D,
+                                ctypes.cast(arr, ctypes.c_void_p), len(flat) // 3, stream_of(src_q)),
+          "od_kv_copy_rows")
+
+
 def _rows_aligned(t: torch.Tensor) -> torch.Tensor:
     """Last dim contiguous, 16-byte aligned base and strides that are multiples of 8 elements (16-byte loads)."""
     if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]):

@@ -25,6 +25,17 @@ class Int8KVCache:
         self.length = 0
         self.dtype = dtype
 
+    @classmethod
+    def from_tensors(cls, q: torch.Tensor, scale: torch.Tensor, dtype=torch.bfloat16) -> "Int8KVCache":
+        """A cache over existing buffers q int8 (B, Hkv, cap, D) and scale fp32 (B, Hkv, cap), both contiguous."""
+        if q.dtype != torch.int8 or scale.dtype != torch.float32 or scale.shape != q.shape[:3]:
+            raise TypeError("Int8KVCache.from_tensors: q int8 (B, H, cap, D) with fp32 scales (B, H, cap)")
+        if not (q.is_contiguous() and scale.is_contiguous()):
+            raise ValueError("Int8KVCache.from_tensors: buffers must be contiguous")
+        c = cls.__new__(cls)
+        c.q, c.scale, c.length, c.dtype = q, scale, 0, dtype
+        return c
+
     @property
     def capacity(self) -> int:
         return self.q.shape[2]
@@ -41,6 +52,56 @@ class Int8KVCache:
         """The filled part as an Int8Tensor (views, no copy): q (B, Hkv, T, D), scale (B, Hkv, T, 1) fp32."""
         T = self.length
         return Int8Tensor(self.q[:, :, :T], self.scale[:, :, :T, None], self.dtype)
+
+    def nbytes(self) -> int:
+        return self.q.numel() + self.scale.numel() * 4
+
+
+class StateKV:
+    """Every layer's K and V caches of `batch` states in one allocation: q int8 (2 L, B, Hkv, cap, D) and scale fp32
+    (2 L, B, Hkv, cap), matrix 2 l being layer l's K and 2 l + 1 its V. Indexing and iteration give the per-layer
+    (K, V) Int8KVCache pairs (views), so it stands wherever the decoder takes a list of cache pairs; one state's rows
+    of every layer are then reachable at one matrix stride, which lets one launch copy them all
+    (kernels.kv_copy_rows)."""
+
+    def __init__(self, n_layers: int, batch: int, n_heads: int, head_dim: int, capacity: int, device,
+                 dtype=torch.bfloat16):
+        self.q = torch.zeros(2 * n_layers, batch, n_heads, capacity, head_dim, dtype=torch.int8, device=device)
+        self.scale = torch.zeros(2 * n_layers, batch, n_heads, capacity, dtype=torch.float32, device=device)
+        self.pairs = [(Int8KVCache.from_tensors(self.q[2 * li], self.scale[2 * li], dtype),
+                       Int8KVCache.from_tensors(self.q[2 * li + 1], self.scale[2 * li + 1], dtype))
+                      for li in range(n_layers)]
+
+    def __len__(self) -> int:
+        return len(self.pairs)
+
+    def __getitem__(self, li):
+        return self.pairs[li]
+
+    def __iter__(self):
+        return iter(self.pairs)
+
+    @property
+    def capacity(self) -> int:
+        return self.q.shape[3]
+
+    @property
+    def length(self) -> int:
+        n = {c.length for pair in self.pairs for c in pair}
+        if len(n) != 1:
+            raise RuntimeError(f"StateKV: layers hold different lengths {sorted(n)}")
+        return n.pop()
+
+    def set_length(self, n: int) -> None:
+        if not 0 <= n <= self.capacity:
+            raise ValueError(f"StateKV: length {n} outside [0, {self.capacity}]")
+        for pair in self.pairs:
+            for c in pair:
+                c.length = n
+
+    def state(self, b: int):
+        """State b of every layer: q (2 L, Hkv, cap, D) and scale (2 L, Hkv, cap) views."""
+        return self.q[:, b], self.scale[:, b]
 
     def nbytes(self) -> int:
         return self.q.numel() + self.scale.numel() * 4
