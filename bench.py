@@ -98,6 +98,40 @@ def gemm_work(a, lda, sa, w, ldw, sw, bias, residual, ldr, out, ldo, acc, ldacc,
     return (2 * M * N * K, M * K + N * K + 2 * M * N + (2 * M * N if residual else 0))
 
 
+def swiglu_work(a, lda, sa, w, ldw, sw, out, ldo, M, N, K, stream):
+    # od_w8a8_gemm_swiglu: the gate+up GEMM (N = 2F weight rows), output bf16 [M, F]
+    return (2 * M * N * K, M * K + N * K + M * N)
+
+
+class GemmTimers:
+    """The W8A8 GEMM entry points timed together (od_w8a8_gemm for QKV / O / down, od_w8a8_gemm_swiglu for
+    gate+up); `shapes` records the shape key of every timed launch."""
+
+    def __init__(self, every=1):
+        self.shapes = []
+        self.timers = [AbiTimer("od_w8a8_gemm", gemm_work, every), AbiTimer("od_w8a8_gemm_swiglu", swiglu_work, every)]
+        plain, fused = (t.work for t in self.timers)
+        self.timers[0].work = lambda *a: (self.shapes.append((a[14], a[15])), plain(*a))[1]
+        self.timers[1].work = lambda *a: (self.shapes.append(("swiglu", a[9], a[10])), fused(*a))[1]
+        self.every = every
+
+    @property
+    def active(self):
+        return self.timers[0].active
+
+    @active.setter
+    def active(self, v):
+        for t in self.timers:
+            t.active = v
+
+    def summary(self):
+        n, ms, tot = 0, 0.0, [0, 0]
+        for t in self.timers:
+            tn, tms, ttot = t.summary()
+            n, ms, tot = n + tn, ms + tms, [tot[0] + ttot[0], tot[1] + ttot[1]]
+        return n, ms, tot
+
+
 def attn_work(*a):
     R, Hq, Hkv, t, D, Ns, T = a[24:31]
     rows_per_state = R // Ns
@@ -171,10 +205,12 @@ def rope_append_work(qkv, ld, B, S, Hq, Hk, D, *rest):
     return (tok * (Hq + 2 * Hk) * D, tok * ((Hq + 2 * Hk) * D * 2 + (Hq + Hk) * D * 2 + 2 * Hk * (D + 4)))
 
 
-# HBM-side traffic of od_w8a8_gemm per launch at M = 4096 (bytes), from two rocprofv3 --pmc passes (FETCH_SIZE,
-# then WRITE_SIZE) over the four layer GEMMs, each counter scaled by its reading for a plain 256 MiB device copy
-# (fetch x2.000, write x1.000); the summary is profiles/w8a8_gemm_traffic_M4096.md.
-GEMM_TRAFFIC_M4096 = {(6144, 4096): 218.6e6, (4096, 4096): 168.0e6, (24576, 4096): 806.3e6, (4096, 12288): 369.3e6}
+# HBM-side traffic of the layer GEMMs per launch at M = 4096 (bytes), from two rocprofv3 --pmc passes (FETCH_SIZE,
+# then WRITE_SIZE) over the four layer GEMMs (gate+up through od_w8a8_gemm_swiglu), each counter scaled by its
+# reading for a plain 256 MiB device copy (fetch x2.000, write x1.000); the summary is
+# profiles/w8a8_gemm_traffic_M4096.md.
+GEMM_TRAFFIC_M4096 = {(6144, 4096): 218.5e6, (4096, 4096): 168.0e6, ("swiglu", 24576, 4096): 705.5e6,
+                      (4096, 12288): 369.3e6}
 
 
 def cpu_baseline(args):
@@ -219,7 +255,8 @@ def cpu_baseline(args):
 def _gemm_roofline(gemm_t):
     n_g, ms_g, (ops_g, _) = gemm_t.summary()
     tops = ops_g / (ms_g * 1e-3) / 1e12 if n_g else 0.0
-    return {"kernel": "od_w8a8_gemm", "bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+    return {"kernel": "od_w8a8_gemm + od_w8a8_gemm_swiglu", "bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS,
+            "unit": "TFLOP/s",
             "frac": tops / INT8_PEAK_TOPS, "traffic": None, "launches": n_g,
             "avg_launch_us": ms_g / max(n_g, 1) * 1e3}, ms_g
 
@@ -239,7 +276,7 @@ def run_decision(args):
     ids_state = torch.randint(0, cfg.vocab, (B, S), generator=g, device=dev)
     ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g, device=dev)
     caches = dec.new_state_caches(B, S)
-    gemm_t = AbiTimer("od_w8a8_gemm", gemm_work)
+    gemm_t = GemmTimers()
     wide_t = AbiTimer("od_wide_attn", wide_work)
     attn_t = AttnTimers()
 
@@ -427,13 +464,10 @@ def main():
     ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g, device=dev)
     torch.cuda.synchronize()
 
-    # every 5th GEMM call (5 is prime to the 4 GEMMs of a layer, so the timed calls cycle through the 4 shapes
-    # evenly) and every 3rd layer's attention carry timing events
-    gemm_t = AbiTimer("od_w8a8_gemm", gemm_work, every=5)
+    # every 5th call of each GEMM entry point (5 is prime to the 3 od_w8a8_gemm calls of a layer, so the timed
+    # calls cycle through the shapes evenly) and every 3rd layer's attention carry timing events
+    gemm_t = GemmTimers(every=5)
     attn_t = AttnTimers(every=3)
-    gemm_shapes = []
-    orig_work = gemm_t.work
-    gemm_t.work = lambda *a: (gemm_shapes.append((a[14], a[15])), orig_work(*a))[1]
 
     for _ in range(args.warmup):
         out = dec.score(ids, states)
@@ -449,7 +483,7 @@ def main():
 
     ms_per_step = dt / args.steps * 1e3
     n_g, ms_g, (ops_g, bytes_g) = gemm_t.summary()
-    known = [GEMM_TRAFFIC_M4096.get(sh) for sh in gemm_shapes]
+    known = [GEMM_TRAFFIC_M4096.get(sh) for sh in gemm_t.shapes]
     traffic = sum(known) / len(known) if known and None not in known and args.tokens * args.options * args.requests == 4096 else None
     n_a, ms_a, (fl_a, by_a) = attn_t.summary()
     gemm_tops = ops_g / (ms_g * 1e-3) / 1e12
@@ -473,7 +507,7 @@ def main():
                                 f"FFN 12288, 32/8 heads, head_dim 128), W8A8 linears, random init"),
                    "requests": B, "options": n_opt, "tokens_per_option": t, "state_tokens": T,
                    "layers": cfg.n_layers, "tokens_per_layer": B * n_opt * t},
-        "roofline": {"kernel": "od_w8a8_gemm (all 4 layer GEMMs)", "bound": "mfma",
+        "roofline": {"kernel": "od_w8a8_gemm + od_w8a8_gemm_swiglu (all 4 layer GEMMs)", "bound": "mfma",
                      "achieved": gemm_tops, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": gemm_tops / INT8_PEAK_TOPS, "traffic": traffic,
                      "traffic_unit": "bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE)",

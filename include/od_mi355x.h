@@ -71,6 +71,18 @@ int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const int8_t* w,
                  int32_t* acc, int64_t ldacc, int64_t M, int64_t N, int64_t K, od_stream_t stream);
 
 /*
+ * od_w8a8_gemm_swiglu — the gate+up projection of the decoder MLP with SwiGLU in its epilogue (no reference
+ * counterpart as one function: the reference runs the two projections and silu(gate) * up as separate modules).
+ *   w int8 [N, K] with N = 2F rows interleaved: row 2f is gate channel f, row 2f + 1 up channel f; sw fp32 [N].
+ *   g = bf16(float(acc[m, 2f]) * sa[m] * sw[2f]), u likewise from row 2f + 1 (the od_w8a8_gemm output without bias
+ *   or residual), out[m, f] = bf16(bf16(silu(g)) * u), out bf16 [M, F] with row stride ldo >= F: the values
+ *   od_w8a8_gemm followed by od_silu_mul_quant's SwiGLU produce, without the [M, 2F] round trip through HBM.
+ * Same requirements as od_w8a8_gemm; N must be even.
+ */
+int od_w8a8_gemm_swiglu(const int8_t* a, int64_t lda, const float* sa, const int8_t* w, int64_t ldw, const float* sw,
+                        uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, od_stream_t stream);
+
+/*
  * od_kv_quant_append — quantize new K or V rows (one scale per token per head) and append them to an int8 cache.
  * Replaces: maybe_quantize / Int8Tensor.quantize on cache tensors (quant.py:36-41,105-109) as called by
  * PackedCache.pack (src/opendecider/backbone.py:446) and by PrefixCache._take, which quantizes only the new

@@ -44,6 +44,7 @@ SIGNATURES = {
     "od_silu_mul_quant": [_c_ptr, _i64, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _c_ptr],
     "od_qk_norm_rope": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr,
                         ctypes.c_float, _c_ptr],
+    "od_w8a8_gemm_swiglu": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _c_ptr],
     "od_kv_copy_rows": [_c_ptr, _c_ptr, _i64, _i64, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr,
                         _i64, _c_ptr],
     "od_qk_norm_rope_kv_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64,

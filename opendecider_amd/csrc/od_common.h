@@ -43,6 +43,11 @@ __device__ __forceinline__ float od_absmax_bf16x2_value(uint32_t acc) {
   return __uint_as_float((lo > hi ? lo : hi) << 16);
 }
 
+// silu(g) = g / (1 + exp(-g)) with the device exp and reciprocal (a few fp32 ulps; the value is then rounded to
+// bf16, which hides the difference except at rare rounding ties). Every SwiGLU kernel uses this one function, so
+// fused and unfused paths agree bit for bit.
+__device__ __forceinline__ float od_silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+
 // Max over the 64 lanes of a wave (every lane gets the result).
 __device__ __forceinline__ float od_wave_max(float v) {
 #pragma unroll

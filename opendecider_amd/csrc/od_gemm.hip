@@ -57,6 +57,8 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
+__device__ __forceinline__ float bfr(float v) { return od_bf16_to_f32(od_f32_to_bf16(v)); }
+
 // byte offset of logical chunk c (0..7) of row r inside a slab
 __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
@@ -96,7 +98,7 @@ struct Slab {
   }
 };
 
-template <int BN, bool ACC_ONLY, bool GENERAL>
+template <int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU>
 __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile: 64 x BN/2
   constexpr int TM = kRowsW / 32;    // 2
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
       acc[x / TN][x % TN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[x / TN], fb[x % TN], acc[x / TN][x % TN], 0, 0, 0);
 #pragma unroll
       for (int o = 0; o < kOps; ++o)
-        if (o * kMf / kOps == x) fill(o);
+        if (o * kMf / (kOps > 0 ? kOps : 1) == x) fill(o);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -342,6 +344,19 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
             } else {
               *reinterpret_cast<uint4*>(dst) = v;
             }
+          } else if constexpr (SWIGLU) {
+            // columns n .. n+3 are (gate f, up f, gate f+1, up f+1) with f = n / 2: out[m, f] =
+            // bf16(bf16(silu(g)) * u), g and u being the bf16 gate and up outputs (no bias, no residual)
+            const float g0 = bfr(__uint_as_float(v.x)), u0 = bfr(__uint_as_float(v.y));
+            const float g1 = bfr(__uint_as_float(v.z)), u1 = bfr(__uint_as_float(v.w));
+            const uint32_t h0 = od_f32_to_bf16(bfr(od_silu(g0)) * u0), h1 = od_f32_to_bf16(bfr(od_silu(g1)) * u1);
+            uint16_t* dst = p.out + m * p.ldo + n / 2;
+            if constexpr (GENERAL) {
+              if (n < p.N) dst[0] = (uint16_t)h0;
+              if (n + 2 < p.N) dst[1] = (uint16_t)h1;
+            } else {
+              *reinterpret_cast<uint32_t*>(dst) = h0 | (h1 << 16);
+            }
           } else {
             const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
             const uint32_t rw[4] = {res[u].x << 16, res[u].x & 0xffff0000u, res[u].y << 16, res[u].y & 0xffff0000u};
@@ -368,20 +383,11 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
 
 }  // namespace
 
-extern "C" int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const int8_t* w, int64_t ldw,
-                            const float* sw, const uint16_t* bias, const uint16_t* residual, int64_t ldr,
-                            uint16_t* out, int64_t ldo, int32_t* acc, int64_t ldacc, int64_t M, int64_t N, int64_t K,
-                            od_stream_t stream) {
-  if (M < 0 || N < 0 || K < 1) return OD_ERR_SHAPE;
-  if (M == 0 || N == 0) return OD_OK;
-  if (!a || !w || (!out && !acc)) return OD_ERR_NULL;
-  if (out && (!sa || !sw)) return OD_ERR_NULL;
-  if (lda < K || ldw < K || (out && ldo < N) || (acc && ldacc < N) || (residual && ldr < N)) return OD_ERR_SHAPE;
-  if (K % 16 || lda % 16 || ldw % 16 || !od_aligned16(a) || !od_aligned16(w)) return OD_ERR_ALIGN;
-  if (K >= 133144) return OD_ERR_UNSUPPORTED;  // int32 accumulators could overflow
-  // buffer offsets are 32-bit: one tile's A panel (256 rows) and W panel must stay below 2 GiB
-  if ((int64_t)BM * lda >= (1ll << 31) || (int64_t)256 * ldw >= (1ll << 31)) return OD_ERR_UNSUPPORTED;
-  GemmArgs p{a, sa, w, sw, bias, residual, out, acc, lda, ldw, ldr, ldo, ldacc, M, N, K, 0, 0};
+namespace {
+
+int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st) {
+  GemmArgs p = p0;
+  const int64_t M = p.M, N = p.N, K = p.K;
   const int64_t tiles_m = (M + BM - 1) / BM;
   // BN: 256, or 192 when that takes fewer tile-widths of work at 256 workgroups per wave (e.g. N = 6144).
   const int64_t t256 = tiles_m * ((N + 255) / 256), t192 = tiles_m * ((N + 191) / 192);
@@ -392,30 +398,76 @@ extern "C" int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const
   p.tiles_m = (int)tiles_m;
   p.tiles_n = (int)tiles_n;
   dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
-  hipStream_t st = (hipStream_t)stream;
   // The fast variant needs whole k-tiles and 4-column output groups that are 8-byte (bf16) / 16-byte (int32)
-  // aligned; anything else takes the GENERAL variant.
+  // aligned (with SwiGLU, 2-column output groups 4-byte aligned); anything else takes the GENERAL variant.
   auto al = [](const void* q, unsigned a) { return (((uintptr_t)q) & (a - 1)) == 0; };
   const bool fast_k = K % BK == 0 && N % 4 == 0;
-  const bool fast_out = fast_k && ldo % 4 == 0 && al(out, 8) && al(bias, 8) && ldr % 4 == 0 && al(residual, 8);
-  const bool fast_acc = fast_k && ldacc % 4 == 0 && al(acc, 16);
-  auto launch = [&](auto BNc, auto ACCc, auto GENc) {
-    w8a8_gemm_kernel<decltype(BNc)::value, decltype(ACCc)::value, decltype(GENc)::value><<<grid, block, 0, st>>>(p);
+  const bool fast_out = fast_k && (swiglu ? (p.ldo % 2 == 0 && al(p.out, 4))
+                                          : (p.ldo % 4 == 0 && al(p.out, 8) && al(p.bias, 8) && p.ldr % 4 == 0 &&
+                                             al(p.residual, 8)));
+  const bool fast_acc = fast_k && p.ldacc % 4 == 0 && al(p.acc, 16);
+  auto launch = [&](auto BNc, auto ACCc, auto GENc, auto SWc) {
+    w8a8_gemm_kernel<decltype(BNc)::value, decltype(ACCc)::value, decltype(GENc)::value, decltype(SWc)::value>
+        <<<grid, block, 0, st>>>(p);
   };
-  auto launch2 = [&](auto ACCc, bool general) {
+  auto launch2 = [&](auto ACCc, auto SWc, bool general) {
     if (use192) {
-      general ? launch(std::integral_constant<int, 192>{}, ACCc, std::true_type{})
-              : launch(std::integral_constant<int, 192>{}, ACCc, std::false_type{});
+      general ? launch(std::integral_constant<int, 192>{}, ACCc, std::true_type{}, SWc)
+              : launch(std::integral_constant<int, 192>{}, ACCc, std::false_type{}, SWc);
     } else {
-      general ? launch(std::integral_constant<int, 256>{}, ACCc, std::true_type{})
-              : launch(std::integral_constant<int, 256>{}, ACCc, std::false_type{});
+      general ? launch(std::integral_constant<int, 256>{}, ACCc, std::true_type{}, SWc)
+              : launch(std::integral_constant<int, 256>{}, ACCc, std::false_type{}, SWc);
     }
   };
-  if (acc) {
-    launch2(std::true_type{}, !fast_acc);
+  if (p.acc) {
+    launch2(std::true_type{}, std::false_type{}, !fast_acc);
     const int rc = od_launch_status();
     if (rc != OD_OK) return rc;
   }
-  if (out) launch2(std::false_type{}, !fast_out);
+  if (p.out) {
+    if (swiglu) {
+      launch2(std::false_type{}, std::true_type{}, !fast_out);
+    } else {
+      launch2(std::false_type{}, std::false_type{}, !fast_out);
+    }
+  }
   return od_launch_status();
+}
+
+int gemm_check(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t K) {
+  if (K % 16 || lda % 16 || ldw % 16 || !od_aligned16(a) || !od_aligned16(w)) return OD_ERR_ALIGN;
+  if (K >= 133144) return OD_ERR_UNSUPPORTED;  // int32 accumulators could overflow
+  // buffer offsets are 32-bit: one tile's A panel (256 rows) and W panel must stay below 2 GiB
+  if ((int64_t)BM * lda >= (1ll << 31) || (int64_t)256 * ldw >= (1ll << 31)) return OD_ERR_UNSUPPORTED;
+  return OD_OK;
+}
+
+}  // namespace
+
+extern "C" int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const int8_t* w, int64_t ldw,
+                            const float* sw, const uint16_t* bias, const uint16_t* residual, int64_t ldr,
+                            uint16_t* out, int64_t ldo, int32_t* acc, int64_t ldacc, int64_t M, int64_t N, int64_t K,
+                            od_stream_t stream) {
+  if (M < 0 || N < 0 || K < 1) return OD_ERR_SHAPE;
+  if (M == 0 || N == 0) return OD_OK;
+  if (!a || !w || (!out && !acc)) return OD_ERR_NULL;
+  if (out && (!sa || !sw)) return OD_ERR_NULL;
+  if (lda < K || ldw < K || (out && ldo < N) || (acc && ldacc < N) || (residual && ldr < N)) return OD_ERR_SHAPE;
+  const int rc = gemm_check(a, lda, w, ldw, K);
+  if (rc != OD_OK) return rc;
+  GemmArgs p{a, sa, w, sw, bias, residual, out, acc, lda, ldw, ldr, ldo, ldacc, M, N, K, 0, 0};
+  return gemm_launch(p, false, (hipStream_t)stream);
+}
+
+extern "C" int od_w8a8_gemm_swiglu(const int8_t* a, int64_t lda, const float* sa, const int8_t* w, int64_t ldw,
+                                   const float* sw, uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                   od_stream_t stream) {
+  if (M < 0 || N < 0 || K < 1 || N % 2) return OD_ERR_SHAPE;
+  if (M == 0 || N == 0) return OD_OK;
+  if (!a || !w || !out || !sa || !sw) return OD_ERR_NULL;
+  if (lda < K || ldw < K || ldo < N / 2) return OD_ERR_SHAPE;
+  const int rc = gemm_check(a, lda, w, ldw, K);
+  if (rc != OD_OK) return rc;
+  GemmArgs p{a, sa, w, sw, nullptr, nullptr, out, nullptr, lda, ldw, 0, ldo, 0, M, N, K, 0, 0};
+  return gemm_launch(p, true, (hipStream_t)stream);
 }

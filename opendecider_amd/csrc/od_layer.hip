@@ -238,9 +238,6 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_vec_kernel(const uint1
   if (threadIdx.x == 0) sx[row] = scale;
 }
 
-// silu(g) = g / (1 + exp(-g)) with the device exp and reciprocal (a few fp32 ulps; the value is then rounded to
-// bf16, which hides the difference except at rare rounding ties).
-__device__ __forceinline__ float silu_fast(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 template <int NV, bool INV>
 __global__ __launch_bounds__(kThreads) void silu_mul_quant_vec_kernel(const uint16_t* __restrict__ gu, int64_t ldg,
@@ -265,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_quant_vec_kernel(const uint
       float ga, gb, ua, ub;
       unpack2(word(g8, j), ga, gb);
       unpack2(word(u8, j), ua, ub);
-      float a = silu_fast(ga), b = silu_fast(gb);
+      float a = od_silu(ga), b = od_silu(gb);
       od_bfr2(a, b);
       a *= ua;
       b *= ub;

@@ -10,7 +10,7 @@
 // quotient's result bit for bit. The row max runs on bf16 bit patterns, so a NaN in a row makes its scale NaN and
 // its bytes 0, as torch's amax (which propagates NaN) and float -> int8 conversion on x86 do.
 //
-// Every element is read from HBM once and written once as int8: rows up to 4 * 256 * 8 elements stay in registers
+// Every element is read from HBM once and written once as int8: rows up to 6 * 256 * 8 elements stay in registers
 // between the max and the quantization; longer rows are read twice (the second pass hits L1/L2). A group of LANES
 // threads owns a row; rows of 64..512 elements (KV heads, small linears) use 8..64 lanes so that a wave covers
 // several rows, wider rows use a whole 256-thread workgroup. Loads are 16 B (8 bf16) per lane when the row layout
@@ -183,6 +183,8 @@ void launch_nit(dim3 grid, hipStream_t st, const RowMap& m, const uint16_t* inv_
     quant_rows_kernel<LANES, VEC, MODE, HAS_INV, 2><<<grid, dim3(kThreads), 0, st>>>(m, inv_s, n_rows, K);
   } else if (VEC == 8 && groups <= 4) {
     quant_rows_kernel<LANES, VEC, MODE, HAS_INV, 4><<<grid, dim3(kThreads), 0, st>>>(m, inv_s, n_rows, K);
+  } else if (VEC == 8 && LANES == 256 && groups <= 6) {
+    quant_rows_kernel<LANES, VEC, MODE, HAS_INV, 6><<<grid, dim3(kThreads), 0, st>>>(m, inv_s, n_rows, K);
   } else {
     quant_rows_kernel<LANES, VEC, MODE, HAS_INV, 0><<<grid, dim3(kThreads), 0, st>>>(m, inv_s, n_rows, K);
   }

@@ -9,8 +9,8 @@ appended to a cached state, the branched kernel over the int8 cache + the record
 into per-layer int8 caches by od_kv_quant_append. Scoring (score), per layer, for the M = rows x tokens option-row
 tokens:
     od_rmsnorm_quant -> od_w8a8_gemm (QKV) -> od_qk_norm_rope -> od_branched_attn -> od_act_quant
-    -> od_w8a8_gemm (O, + residual) -> od_rmsnorm_quant -> od_w8a8_gemm (gate+up) -> od_silu_mul_quant
-    -> od_w8a8_gemm (down, + residual)
+    -> od_w8a8_gemm (O, + residual) -> od_rmsnorm_quant -> od_w8a8_gemm_swiglu (gate+up with SwiGLU in the
+    epilogue; gate and up weight rows interleaved) -> od_act_quant -> od_w8a8_gemm (down, + residual)
 All activations live in preallocated HBM buffers; nothing allocates or synchronizes inside a forward, so the whole
 forward can be captured in one HIP graph.
 """
@@ -120,8 +120,10 @@ class DenseDecoder:
 
     def add_layer(self, lw: dict) -> None:
         L = {k: lw[k].to(self.dev) for k in ("ln1", "ln2", "q_norm", "k_norm")}
-        for name in ("qkv", "o", "gu", "down"):
+        for name in ("qkv", "o", "down"):
             L[name] = QLinear(lw["w" + name], lw.get("s_" + name), self.dev)
+        # gate and up rows interleaved for the SwiGLU GEMM (a row permutation: per-row quantization is unchanged)
+        L["gu"] = QLinear(kernels.interleave_gate_up(lw["wgu"]), lw.get("s_gu"), self.dev)
         self.layers.append(L)
 
     # ---------------------------------------------------------------- buffers
@@ -139,7 +141,7 @@ class DenseDecoder:
             "sx": torch.empty(M, dtype=torch.float32, device=d),
             "qkv": torch.empty(M, cfg.qkv_out, dtype=bf, device=d),
             "attn": torch.empty(M, cfg.n_heads * cfg.head_dim, dtype=bf, device=d),
-            "gu": torch.empty(M, 2 * cfg.ffn, dtype=bf, device=d),
+            "hmlp": torch.empty(M, cfg.ffn, dtype=bf, device=d),
         }
         return self._ws[M]
 
@@ -175,16 +177,16 @@ class DenseDecoder:
         return q, k, v, attn
 
     def _attn_out_mlp(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict) -> torch.Tensor:
-        """Quantize the attention output, W8A8 O GEMM + residual (into h_out), RMSNorm + quantize, gate+up GEMM,
-        SwiGLU + quantize, down GEMM + residual (back into h)."""
+        """Quantize the attention output, W8A8 O GEMM + residual (into h_out), RMSNorm + quantize, gate+up GEMM with
+        SwiGLU in its epilogue, quantize, down GEMM + residual (back into h)."""
         cfg, L = self.cfg, self.layers[li]
         xq, sx = ws["xq"], ws["sx"]
         hd = cfg.n_heads * cfg.head_dim
         kernels.act_quant(ws["attn"], L["o"].inv_s, xq=xq[:, :hd], sx=sx)
         kernels.w8a8_gemm(xq[:, :hd], sx, L["o"].q, L["o"].scale, residual=h, out=h_out)
         kernels.rmsnorm_quant(h_out, L["ln2"], cfg.eps, L["gu"].inv_s, xq[:, :cfg.hidden], sx)
-        gu = kernels.w8a8_gemm(xq[:, :cfg.hidden], sx, L["gu"].q, L["gu"].scale, out=ws["gu"])
-        kernels.silu_mul_quant(gu, cfg.ffn, L["down"].inv_s, xq=xq[:, :cfg.ffn], sx=sx)
+        hm = kernels.w8a8_gemm_swiglu(xq[:, :cfg.hidden], sx, L["gu"].q, L["gu"].scale, out=ws["hmlp"])
+        kernels.act_quant(hm, L["down"].inv_s, xq=xq[:, :cfg.ffn], sx=sx)
         kernels.w8a8_gemm(xq[:, :cfg.ffn], sx, L["down"].q, L["down"].scale, residual=h_out, out=h)
         return h
 

@@ -164,6 +164,37 @@ def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tens
     return o
 
 
+def interleave_gate_up(w: torch.Tensor) -> torch.Tensor:
+    """Rows [gate (F); up (F)] -> [gate 0, up 0, gate 1, up 1, ...], the layout w8a8_gemm_swiglu takes (works on
+    weights or per-row scales)."""
+    F = w.shape[0] // 2
+    return torch.stack([w[:F], w[F:]], 1).reshape(w.shape)
+
+
+def w8a8_gemm_swiglu(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tensor,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """int8 a (M, Kp) x interleaved gate/up int8 w (2F, Kp)^T -> bf16 (M, F) = bf16(bf16(silu(g)) * u) with g, u
+    the bf16 gate and up outputs of w8a8_gemm (rows 2f and 2f + 1 of w)."""
+    require_gpu(a, sa, w, sw, out, name="w8a8_gemm_swiglu")
+    if a.dtype != torch.int8 or w.dtype != torch.int8:
+        raise TypeError("w8a8_gemm_swiglu: a and w must be int8")
+    M, Kp = a.shape
+    N = w.shape[0]
+    if w.shape[1] != Kp or N % 2:
+        raise ValueError("w8a8_gemm_swiglu: w must be (2F, Kp) with a's Kp")
+    if sa.numel() != M or sw.numel() != N:
+        raise ValueError("w8a8_gemm_swiglu: scale sizes do not match (M, 2F)")
+    if out is None:
+        out = torch.empty(M, N // 2, dtype=torch.bfloat16, device=a.device)
+    if out.shape != (M, N // 2) or out.stride(-1) != 1:
+        raise ValueError("w8a8_gemm_swiglu: out must be (M, F) with contiguous rows")
+    _lib.bf16_bits(out)
+    check(lib().od_w8a8_gemm_swiglu(ptr(a), a.stride(0), ptr(sa.contiguous()), ptr(w), w.stride(0),
+                                    ptr(sw.contiguous()), ptr(out), out.stride(0), M, N, Kp, stream_of(a)),
+          "od_w8a8_gemm_swiglu")
+    return out
+
+
 def kv_quant_append(x: torch.Tensor, q_cache: torch.Tensor, s_cache: torch.Tensor, n0: int) -> None:
     """Quantize x (B, H, n, D) bf16 per (token, head) and write it at positions n0..n0+n-1 of the int8 cache
     q_cache (B, H, cap, D) and its fp32 scales s_cache (B, H, cap) (Int8Tensor.quantize on the new tokens only,

@@ -66,7 +66,8 @@ def test_bench_work_counters_take_the_abi_arguments():
     sys.path.insert(0, ROOT)
     import bench
     from opendecider_amd import _lib
-    for name, fn in [("od_w8a8_gemm", bench.gemm_work), ("od_branched_attn", bench.attn_work),
+    for name, fn in [("od_w8a8_gemm", bench.gemm_work), ("od_w8a8_gemm_swiglu", bench.swiglu_work),
+                     ("od_branched_attn", bench.attn_work),
                      ("od_branched_attn_staged", bench.staged_work), ("od_attn_stage", bench.stage_work),
                      ("od_wide_attn", bench.wide_work), ("od_kv_quant_append", bench.append_work),
                      ("od_qk_norm_rope_kv_append", bench.rope_append_work)]:

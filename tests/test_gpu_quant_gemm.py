@@ -3,6 +3,7 @@ bit-exact bf16 epilogue, which runs the oracle's fp32 operations in the same ord
 import pytest
 import torch
 
+from oracle import decoder as od
 from oracle import quant as oq
 
 pytestmark = pytest.mark.gpu
@@ -192,3 +193,31 @@ def test_int8_tensor_quantize_matches_reference_formula(gpu_lib):
     assert torch.equal(t32.scale.cpu(), rs)
     err = (t.dequantize().float().cpu() - x.float()).abs().max()
     assert err <= x.float().abs().amax() / 127 + 1e-2
+
+
+@pytest.mark.parametrize("M,K,F", [(4096, 4096, 12288), (300, 272, 520), (77, 4096, 98)])
+def test_w8a8_gemm_swiglu_equals_gemm_then_swiglu(gpu_lib, M, K, F):
+    """The SwiGLU epilogue gives the bytes of the plain GEMM followed by the SwiGLU kernel (shared device silu):
+    quantizing its h equals od_silu_mul_quant on the plain GEMM's [gate | up] output, bit for bit; and h differs
+    from the oracle's SwiGLU of the oracle's (bit-exact) GEMM output on <= 0.5% of elements, by at most two bf16
+    steps (the device and host exp may round silu(g) to neighbouring bf16 values, which the product with u keeps).
+    Odd shapes take the GENERAL variant (K tail, ragged tiles)."""
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(M + K + F)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (2 * F, K), generator=g, dtype=torch.int8)
+    sa = torch.rand(M, generator=g) * 1e-2
+    sw = torch.rand(2 * F, generator=g) * 1e-3
+    print(f"w8a8_gemm_swiglu M={M} K={K} F={F}", flush=True)
+    h = kernels.w8a8_gemm_swiglu(a.to(DEV), sa.to(DEV), kernels.interleave_gate_up(w).to(DEV),
+                                 kernels.interleave_gate_up(sw).to(DEV))
+    gu = kernels.w8a8_gemm(a.to(DEV), sa.to(DEV), w.to(DEV), sw.to(DEV))
+    inv = (1 / (torch.rand(F, generator=g) + 0.5)).to(torch.bfloat16).to(DEV)
+    xq1, sx1 = kernels.act_quant(h, inv)
+    xq2, sx2 = kernels.silu_mul_quant(gu, F, inv)
+    assert torch.equal(xq1, xq2) and torch.equal(sx1, sx2)
+    ref_gu = oq.w8a8_epilogue(oq.int_gemm(a, w), sa, sw)
+    assert torch.equal(gu.cpu(), ref_gu)
+    ref = od.swiglu(ref_gu, F).float()
+    d = (h.cpu().float() - ref).abs()
+    assert (d <= ref.abs() * 2.0 ** -6 + 2.0 ** -120).all() and (d > 0).float().mean().item() <= 5e-3
