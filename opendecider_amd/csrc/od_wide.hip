@@ -44,6 +44,7 @@ struct alignas(16) WSmem {
   alignas(16) uint16_t k[NBUF][kBK * DKP];   // [key][d], 16-byte chunks swizzled (wk_off)
   alignas(16) uint16_t vt[NBUF][DV * kBK];   // [d][permuted key], 16-byte chunks swizzled (wvt_off)
   alignas(16) float kb[NBUF][kBK];           // 0, or -inf for a key out of range or masked by kvalid
+  int mk[NBUF];                              // the block has a key out of range or masked (its kb row is needed)
 };
 
 // LDS swizzles for gfx950's banking (reads: 64 4-byte banks, 16 lanes of a ds_read_b128 per cycle; writes: a
@@ -98,11 +99,21 @@ struct BlockRegs {
   int ok;  // thread < 64: key tid valid
 };
 
+// One block's K / V rows through buffer descriptors based at the block's first key and bounded by the keys that
+// exist (S - j0 rows): rows past S read as zeros without a per-lane check, and the per-lane offsets (key * stride +
+// chunk) are the same for every block, so no 64-bit address stays live across the loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const uint16_t* base, int64_t stride, int64_t rows) {
+  const int64_t bytes = rows * stride * 2;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                           0x00020000);
+}
+
 template <int DKP, int DV>
 __device__ __forceinline__ void block_load(const WideArgs& p, int b, int g, int j0, BlockRegs<DKP, DV>& r) {
   const int tid = threadIdx.x;
-  const uint16_t* kbase = p.k + (int64_t)b * p.skb + (int64_t)g * p.skg;
-  const uint16_t* vbase = p.v + (int64_t)b * p.svb + (int64_t)g * p.svg;
+  const uint16_t* kbase = p.k + (int64_t)b * p.skb + (int64_t)g * p.skg + (int64_t)j0 * p.sks;
+  const uint16_t* vbase = p.v + (int64_t)b * p.svb + (int64_t)g * p.svg + (int64_t)j0 * p.svs;
+  const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kbase, p.sks, p.S - j0), rv = rows_rsrc(vbase, p.svs, p.S - j0);
   constexpr int kCpk = DKP / 8;                 // 16-byte chunks per key
   constexpr int kChunks = kBK * kCpk;
 #pragma unroll
@@ -110,8 +121,8 @@ __device__ __forceinline__ void block_load(const WideArgs& p, int b, int g, int 
     const int cid = i * kThreads + tid;
     const int key = cid / kCpk, c = cid % kCpk;
     r.k[i] = make_uint4(0, 0, 0, 0);
-    if (cid < kChunks && j0 + key < p.S && 8 * c < p.DK)
-      r.k[i] = *reinterpret_cast<const uint4*>(kbase + (int64_t)(j0 + key) * p.sks + 8 * c);
+    if (cid < kChunks && 8 * c < p.DK)
+      r.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, (int)(key * p.sks * 2 + 16 * c), 0, 0));
   }
   int dg, kg;
   bool on;
@@ -122,8 +133,9 @@ __device__ __forceinline__ void block_load(const WideArgs& p, int b, int g, int 
     for (int a = 0; a < 4; ++a) {
       const int key = 4 * kg + a;
       r.v[hp][a] = make_uint4(0, 0, 0, 0);
-      if (on && j0 + key < p.S)
-        r.v[hp][a] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(j0 + key) * p.svs + 8 * (dg + 16 * hp));
+      if (on)
+        r.v[hp][a] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, (int)(key * p.svs * 2 + 16 * (dg + 16 * hp)), 0, 0));
     }
   }
   r.ok = 0;
@@ -166,72 +178,129 @@ __device__ __forceinline__ void block_store(WSmem<DKP, DV, NBUF>& sm, int buf, c
       }
     }
   }
-  if (tid < kBK) sm.kb[buf][tid] = r.ok ? 0.0f : -INFINITY;
+  if (tid < kBK) {
+    sm.kb[buf][tid] = r.ok ? 0.0f : -INFINITY;
+    const bool all_ok = __builtin_amdgcn_ballot_w64(r.ok != 0) == ~0ull;  // wave 0 holds the block's 64 keys
+    if (tid == 0) sm.mk[buf] = all_ok ? 0 : 1;
+  }
 }
 
-template <int DKP, int DV, int NBUF>
+// `mid` runs between the softmax and the P.V product: the caller issues the next block's global loads there, so
+// that their registers are not held through the score and softmax phases.
+template <int DKP, int DV, int NBUF, typename Mid>
 __device__ __forceinline__ void wide_block(const WSmem<DKP, DV, NBUF>& sm, int buf, const bf16x8 (&qf)[DKP / 16],
                                            float scale_log2, float& m_run, float& l_run, v16f (&o)[DV / 32],
-                                           bool check_causal, int j0, int qpos) {
+                                           bool check_causal, int j0, int qpos, Mid&& mid) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
   constexpr int KT = kBK / 32;
+  constexpr int KS = DKP / 16;
+  // fragment reads run RA fragments ahead of the MFMAs that consume them (one fragment = one MFMA operand),
+  // through a ring of RA + 1 fragments
+  constexpr int RA = DKP + DV <= 192 ? 2 : 1;
   v16f s[KT];
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
-    s[kt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int kt = 0; kt < KT; ++kt) s[kt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  {
+    constexpr int NQ = KS * KT;  // MFMA i: k-step i / KT, key tile i % KT
+    bf16x8 kf[RA + 1];
+    auto kread = [&](int i) {
+      kf[i % (RA + 1)] =
+          *reinterpret_cast<const bf16x8*>(&sm.k[buf][wk_off<DKP>((i % KT) * 32 + col, (i / KT) * 2 + h)]);
+    };
 #pragma unroll
-    for (int ks = 0; ks < DKP / 16; ++ks) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sm.k[buf][wk_off<DKP>(kt * 32 + col, ks * 2 + h)]);
-      s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[kt], 0, 0, 0);
+    for (int i = 0; i < RA; ++i) kread(i);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      if (i + RA < NQ) kread(i + RA);
+      s[i % KT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i % (RA + 1)], qf[i / KT], s[i % KT], 0, 0, 0);
+    }
+    // keep the reads RA MFMAs ahead (left alone, the scheduler sinks each read to its MFMA)
+    __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      if (i + RA < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
   }
-  // scores of this lane's slot: key = kt*32 + 8*(r/4) + 4*h + r%4
+  // y = s scale log2(e) (+ the block's key bias), -inf past a query's causal limit; this lane's slot sees keys
+  // kt*32 + 8*(r/4) + 4*h + r%4. Then FlashAttention-2's update with the block max, as the reference's kernel:
+  // m' = max(m, max y), p = exp2(y - m') rounded to bf16 for P.V, l' = l exp2(m - m') + sum p, O' = O exp2(m - m').
+  // O is only multiplied when some slot of the wave moved its max (otherwise the factor is exactly 1).
+  if (sm.mk[buf]) {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const float4 b4 = *reinterpret_cast<const float4*>(&sm.kb[buf][kt * 32 + 8 * r4 + 4 * h]);
+        s[kt][4 * r4] = fmaf(s[kt][4 * r4], scale_log2, b4.x);
+        s[kt][4 * r4 + 1] = fmaf(s[kt][4 * r4 + 1], scale_log2, b4.y);
+        s[kt][4 * r4 + 2] = fmaf(s[kt][4 * r4 + 2], scale_log2, b4.z);
+        s[kt][4 * r4 + 3] = fmaf(s[kt][4 * r4 + 3], scale_log2, b4.w);
+      }
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kt][r] = fmaf(s[kt][r], scale_log2, 0.0f);
+  }
+  if (check_causal) {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (j0 + kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3) > qpos) s[kt][r] = -INFINITY;
+  }
   float mloc = -INFINITY;
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
+  for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int key0 = kt * 32 + 8 * r4 + 4 * h;
-      const float4 b4 = *reinterpret_cast<const float4*>(&sm.kb[buf][key0]);
-      const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float y = fmaf(s[kt][4 * r4 + e], scale_log2, bb[e]);
-        if (check_causal && j0 + key0 + e > qpos) y = -INFINITY;
-        s[kt][4 * r4 + e] = y;
-        mloc = fmaxf(mloc, y);
-      }
-    }
-  }
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-  const float m_new = fmaxf(m_run, mloc);
+    for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kt][r]);
+  mloc = od_xor32_max(mloc);
+  const bool moved = mloc > m_run;
+  const float m_new = moved ? mloc : m_run;
   const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
-  const float alpha = __builtin_amdgcn_exp2f(m_run - m_safe);
+  const bool any_moved = __builtin_amdgcn_ballot_w64(moved) != 0;
+  const float alpha = moved ? __builtin_amdgcn_exp2f(m_run - m_safe) : 1.0f;
   float psum = 0.0f;
   bf16x8 pb[2 * KT];
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
+  for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float pr = __builtin_amdgcn_exp2f(s[kt][r] - m_safe);
       psum += pr;
-      pb[kt * 2 + (r >> 3)][r & 7] = __builtin_bit_cast(__bf16, od_f32_to_bf16(pr));
+      pb[kt * 2 + (r >> 3)][r & 7] = (__bf16)pr;
     }
-  }
-  psum += __shfl_xor(psum, 32, 64);
-  l_run = l_run * alpha + psum;
+  l_run = l_run * alpha + od_xor32_sum(psum);
   m_run = m_new;
+  mid();
+  if (any_moved) {
 #pragma unroll
-  for (int dt = 0; dt < DV / 32; ++dt)
+    for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+  }
+  {
+    constexpr int NV = 2 * KT * (DV / 32);  // MFMA i: k-step i / (DV / 32), d tile i % (DV / 32)
+    bf16x8 vf[RA + 1];
+    auto vread = [&](int i) {
+      vf[i % (RA + 1)] = *reinterpret_cast<const bf16x8*>(
+          &sm.vt[buf][wvt_off((i % (DV / 32)) * 32 + col, 2 * (i / (DV / 32)) + h)]);
+    };
 #pragma unroll
-  for (int dt = 0; dt < DV / 32; ++dt) {
+    for (int i = 0; i < RA; ++i) vread(i);
 #pragma unroll
-    for (int m = 0; m < 2 * KT; ++m) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(&sm.vt[buf][wvt_off(dt * 32 + col, 2 * m + h)]);
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[m], o[dt], 0, 0, 0);
+    for (int i = 0; i < NV; ++i) {
+      if (i + RA < NV) vread(i + RA);
+      o[i % (DV / 32)] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[i % (RA + 1)], pb[i / (DV / 32)], o[i % (DV / 32)], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (i + RA < NV) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
   }
 }
@@ -239,10 +308,17 @@ __device__ __forceinline__ void wide_block(const WSmem<DKP, DV, NBUF>& sm, int b
 template <int DKP, int DV, int NBUF, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void wide_attn_kernel(WideArgs p) {
   __shared__ WSmem<DKP, DV, NBUF> sm;
-  const int bg = blockIdx.y;
+  // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs (flat id f runs on XCD f % 8); work item
+  // w = bg * tiles + tile goes to XCD (w's range), so the slot tiles of one (batch, KV group) share an L2 for the
+  // K/V they all stream. A bijection of [0, tiles * B G).
+  const int tiles = gridDim.x, total = gridDim.x * gridDim.y;
+  const int f = blockIdx.x + blockIdx.y * tiles;
+  const int per = total >> 3, rem = total & 7, xcd = f & 7, local = f >> 3;
+  const int w = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int bg = w / tiles;
   const int b = bg / p.G, g = bg % p.G;
   const int nslots = p.T * p.rep;
-  const int slot_base = blockIdx.x * kSlotsPerTile;
+  const int slot_base = (w % tiles) * kSlotsPerTile;
   if (slot_base >= nslots) return;  // uniform over the workgroup
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -286,9 +362,10 @@ __global__ __launch_bounds__(kThreads, OCC) void wide_attn_kernel(WideArgs p) {
     for (int blk = 0; blk < nb; ++blk) {
       const int cur = NBUF == 2 ? (blk & 1) : 0;
       const int j0 = blk * kBK;
-      if (blk + 1 < nb) block_load<DKP, DV>(p, b, g, j0 + kBK, br);
       wide_block<DKP, DV, NBUF>(sm, cur, qf, p.scale_log2, m_run, l_run, o, p.causal && j0 + kBK - 1 > free_until, j0,
-                                qpos);
+                                qpos, [&] {
+                                  if (blk + 1 < nb) block_load<DKP, DV>(p, b, g, j0 + kBK, br);
+                                });
       if (blk + 1 < nb) {
         if constexpr (NBUF == 1) __syncthreads();  // every wave is done with the single buffer
         block_store<DKP, DV, NBUF>(sm, NBUF == 2 ? (cur ^ 1) : 0, br);
