@@ -221,3 +221,40 @@ def test_w8a8_gemm_swiglu_equals_gemm_then_swiglu(gpu_lib, M, K, F):
     ref = od.swiglu(ref_gu, F).float()
     d = (h.cpu().float() - ref).abs()
     assert (d <= ref.abs() * 2.0 ** -6 + 2.0 ** -120).all() and (d > 0).float().mean().item() <= 5e-3
+
+
+def test_quantizer_near_half_integer_quotients(gpu_lib):
+    """The device quantizer multiplies by 1 / scale and redoes the IEEE division only for quotients within 2^-15
+    of a half-integer. Rows are built so that many of their values land there (found by searching all bf16 values
+    below each row's absmax): act_quant's bytes and scales must equal the oracle's, with and without the smoothing
+    scale (here 1, so the values are unchanged)."""
+    import numpy as np
+    rng = np.random.default_rng(9)
+    allv = torch.arange(1, 0x7F80, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float().numpy()
+    K, rows, n_near = 1024, [], 0
+    while len(rows) < 192:
+        amax = np.float32(torch.tensor(float(np.exp(rng.uniform(-7, 5)))).bfloat16().float().item())
+        scale = np.float32(max(amax, np.float32(1e-8)) / np.float32(127))
+        v = allv[allv <= amax]
+        q = (v / scale).astype(np.float32)
+        near = v[np.abs(np.abs(q - np.rint(q)) - 0.5) <= 2.0 ** -15]
+        if near.size == 0:
+            continue
+        row = rng.choice(v, K).astype(np.float32) * rng.choice([-1.0, 1.0], K).astype(np.float32)
+        row[0] = amax
+        k = min(near.size, K // 4)
+        row[1:1 + 2 * k:2], row[2:2 + 2 * k:2] = near[:k], -near[:k]
+        rows.append(row)
+        n_near += 2 * k
+    from opendecider_amd import kernels
+    x = torch.from_numpy(np.stack(rows)).to(torch.bfloat16)
+    rq, rs = oq.quantize_rows(x)
+    # the multiplication alone (no fallback), restated on the CPU, gets some of these bytes wrong
+    xf, sf = x.float().numpy(), rs.numpy().astype(np.float32)
+    fast = np.clip(np.rint((xf * (np.float32(1) / sf)).astype(np.float32)), -127, 127).astype(np.int8)
+    assert n_near >= 192 and (fast != rq.numpy()).any()
+    xq, sx = kernels.act_quant(x.to(DEV))
+    assert torch.equal(xq.cpu()[:, :K], rq) and torch.equal(sx.cpu(), rs[:, 0])
+    ones = torch.ones(K, dtype=torch.bfloat16, device=DEV)
+    xq1, sx1 = kernels.act_quant(x.to(DEV), ones)
+    assert torch.equal(xq1.cpu()[:, :K], rq) and torch.equal(sx1.cpu(), rs[:, 0])
