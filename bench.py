@@ -41,13 +41,16 @@ def parse():
     ap.add_argument("--options", type=int, default=32)
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--state", type=int, default=2048)
-    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm_traffic"], default="scoring",
+    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm_traffic", "attention"],
+                    default="scoring",
                     help="scoring (default): the metric's option-row scoring pass over cached 2048-token states; "
                          "decision: full decision forward from token ids (4 requests, 4096-token states prefilled, "
                          "64 options x 24 tokens); wide_choice: a 32768-token int8 state growing by 256-token "
                          "records, 2 requests x 255 options x 12 tokens scored after each record; gemm_traffic: "
                          "the run the GEMM traffic counters are read on (a 256 MiB device copy to calibrate them, "
-                         "then two scoring passes through 2 layers, i.e. each M = 4096 GEMM shape twice)")
+                         "then two scoring passes through 2 layers, i.e. each M = 4096 GEMM shape twice); "
+                         "attention: the branched attention alone on the config-1 shape and on the KV-bound probe "
+                         "(32768-token states, 2 options x 16 tokens per state)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-repeats", type=int, default=3)
     return ap.parse_args()
@@ -153,17 +156,18 @@ def stage_work(*a):
     return (0, 0)
 
 
-ATTN_KERNELS = "od_attn_stage + od_branched_attn_staged (or od_branched_attn)"
+ATTN_KERNELS = "od_attn_stage + od_branched_attn_staged (or od_branched_attn / od_branched_attn_split)"
 
 
 class AttnTimers:
-    """The branched attention's entry points timed together: od_branched_attn (int8 path), od_attn_stage and
-    od_branched_attn_staged (staged path)."""
+    """The branched attention's entry points timed together: od_branched_attn and od_branched_attn_split (direct
+    path), od_attn_stage and od_branched_attn_staged (staged path)."""
 
     def __init__(self, every=1):
         # one stage and one attention call per layer: the same `every` times both on the same layers
         self.timers = [AbiTimer("od_branched_attn", attn_work, every), AbiTimer("od_attn_stage", stage_work, every),
-                       AbiTimer("od_branched_attn_staged", staged_work, every)]
+                       AbiTimer("od_branched_attn_staged", staged_work, every),
+                       AbiTimer("od_branched_attn_split", attn_work, every)]  # same leading arguments
 
     @property
     def active(self):
@@ -430,6 +434,58 @@ def run_gemm_traffic(args):
     return {"workload": "gemm_traffic", "copy_bytes": 256 << 20, "layers": 2, "passes": 2, "tokens_per_layer": 4096}
 
 
+def run_attention(args):
+    """The branched attention alone on the two shapes its roofline is quoted on: the config-1 shape (8 states of
+    2048 int8 K/V tokens, 32 options x 16 tokens each, 32/8 heads, head_dim 128: bf16-MFMA-bound) and the KV-bound
+    probe (the same dims with 32768-token states and 2 options x 16 tokens each: about 250 FLOP per K/V byte). K/V
+    int8 uniform in [-127, 127] with fp32 scales, queries and own K/V bf16 N(0, 1); HIP events around every call."""
+    import torch
+
+    from opendecider_amd import kernels
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(5)
+    Hq, Hkv, t, D = 32, 8, 16, 128
+    res = {}
+    for name, Ns, rows, T in (("config1", 8, 32, 2048), ("kv_probe", 8, 2, 32768)):
+        R = Ns * rows
+        q = torch.randn(R, Hq, t, D, device=dev, generator=g).to(torch.bfloat16)
+        k = torch.randn(R, Hkv, t, D, device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn(R, Hkv, t, D, device=dev, generator=g).to(torch.bfloat16)
+        kq = torch.randint(-127, 128, (Ns, Hkv, T, D), device=dev, dtype=torch.int8, generator=g)
+        vq = torch.randint(-127, 128, (Ns, Hkv, T, D), device=dev, dtype=torch.int8, generator=g)
+        ks = torch.rand(Ns, Hkv, T, device=dev, generator=g) * 0.02
+        vs = torch.rand(Ns, Hkv, T, device=dev, generator=g) * 0.02
+        rs, mr = kernels.row_start_of([rows] * Ns, dev)
+        out = torch.empty_like(q)
+        timers = AttnTimers()
+
+        def call():
+            kernels.branched_attn(q, k, v, kq, ks, vq, vs, D ** -0.5, out=out, row_start=rs, max_rows=mr, length=T)
+
+        for _ in range(args.warmup):
+            call()
+        torch.cuda.synchronize()
+        timers.active = True
+        for _ in range(args.steps):
+            call()
+        torch.cuda.synchronize()
+        timers.active = False
+        n, ms, (fl, by) = timers.summary()
+        kv_bytes = 2 * Ns * Hkv * T * (D + 4)
+        res[name] = {"states": Ns, "state_tokens": T, "options_per_state": rows, "tokens_per_option": t,
+                     "avg_launch_us": ms / n * 1e3, "tflops": fl / (ms * 1e-3) / 1e12,
+                     "frac_of_bf16_mfma": fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                     "kv_gbs": kv_bytes / (ms / n * 1e-3) / 1e9,
+                     "kv_frac_of_hbm": kv_bytes / (ms / n * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "algorithmic_gbs": by / (ms * 1e-3) / 1e9, "launches": n,
+                     "path": "staged" if kernels.uses_staging(rows, t, Hq, Hkv) else "direct"}
+    return {"metric": "branched attention: KV GB/s on the KV-bound probe (TFLOP/s on the config-1 shape beside it)",
+            "value": res["kv_probe"]["kv_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": res["kv_probe"]["avg_launch_us"] / 1e3, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "int8 K/V, bf16 MFMA", "data": "synthetic",
+            "config": {"workload": "branched attention alone: config-1 shape and KV-bound probe"}, "shapes": res}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -439,7 +495,8 @@ def main():
     import torch
     if args.workload != "scoring":
         torch.cuda.set_device(0)
-        fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm_traffic": run_gemm_traffic}[args.workload]
+        fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm_traffic": run_gemm_traffic,
+              "attention": run_attention}[args.workload]
         print(json.dumps(fn(args)))
         return
 

@@ -291,6 +291,12 @@ def stage_state(kq, ks, vq, vs, length: int, scale: float, kvalid=None, out=None
     return out
 
 
+def uses_staging(max_rows: int, t: int, n_heads_q: int, n_heads_k: int) -> bool:
+    """Whether branched_attn takes the staged path by itself for this row layout (at least STAGE_MIN_TILES slot
+    tiles of 128 per (state, head))."""
+    return -(-(int(max_rows) * t * (n_heads_q // n_heads_k)) // 128) >= STAGE_MIN_TILES
+
+
 def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, row_counts=None, length=None,
                   out=None, return_lse: bool = False, row_start=None, max_rows=None, n_split=None, staged=None,
                   stage_buf=None):

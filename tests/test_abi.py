@@ -67,7 +67,7 @@ def test_bench_work_counters_take_the_abi_arguments():
     import bench
     from opendecider_amd import _lib
     for name, fn in [("od_w8a8_gemm", bench.gemm_work), ("od_w8a8_gemm_swiglu", bench.swiglu_work),
-                     ("od_branched_attn", bench.attn_work),
+                     ("od_branched_attn", bench.attn_work), ("od_branched_attn_split", bench.attn_work),
                      ("od_branched_attn_staged", bench.staged_work), ("od_attn_stage", bench.stage_work),
                      ("od_wide_attn", bench.wide_work), ("od_kv_quant_append", bench.append_work),
                      ("od_qk_norm_rope_kv_append", bench.rope_append_work)]:
