@@ -810,11 +810,15 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
   const int d0 = (int)(gid % (D / 8)) * 8;
   if (slot >= nsl) return;
   const float* lse_p = p.part + (int64_t)p.nsplit * nsl * D;
+  // the loops are unrolled so that the loads of several splits are in flight together (a rolled loop waits for
+  // one split's partial at a time)
   float M = -INFINITY;
+#pragma unroll 8
   for (int sp = 0; sp < p.nsplit; ++sp) M = fmaxf(M, lse_p[sp * nsl + slot]);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   float wsum = 0.0f;
   if (M != -INFINITY) {
+#pragma unroll 8
     for (int sp = 0; sp < p.nsplit; ++sp) {
       const float l = lse_p[sp * nsl + slot];
       if (l == -INFINITY) continue;
