@@ -529,14 +529,18 @@ __device__ __forceinline__ void attend_block(const uint16_t* kimg, const _Float1
                                              int own_row, int own_j0, int slot_row, int slot_tok, Mid&& mid) {
   constexpr int KA = 2;
   v16f s[KT];
+  __builtin_amdgcn_s_setprio(1);  // a wave issuing MFMAs goes first, the other wave's softmax fills the gaps
   qk_scores<D, KT, KA>(kimg, qf, s);
+  __builtin_amdgcn_s_setprio(0);
   float alpha;
   half8 pb[2 * KT];
   const bool rs = softmax_block<D, KT, OWN>(gk, kb, masked, s, c, eb, m_run, l_run, e_run, alpha, pb, own_row,
                                             own_j0, slot_row, slot_tok);
   mid();
   if (rs) rescale<D>(o, alpha, eb, e_run);
+  __builtin_amdgcn_s_setprio(1);
   pv_block<D, KT, 1>(vtimg, pb, o);
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // Workgroup max of two values (every thread gets both).
