@@ -33,7 +33,8 @@
 //    the product): the scores see the exact dequantized keys;
 //  * the row's own bf16 keys are used as they are, with the multiplier scale log2(e);
 //  * a state value becomes V' = fp16(q vs_j 2^-eb), one rounding, with the block's V exponent eb; the accumulator
-//    carries one power-of-two frame and is rescaled when a block's frame differs;
+//    carries one power-of-two frame, moved lazily (a state block in a frame up to kFrameSlack below it enters with
+//    its probabilities times 2^(eb - frame), exact while those stay normal fp16);
 //  * the row's own bf16 values get one power-of-two factor per 32-key block and are converted to fp16;
 //  * probabilities p = exp2(y) <= 2^8 are rounded to fp16 for the P.V product; their sum is taken unrounded.
 // Masked keys get a -inf score; a block with no visible key is an exact no-op for a slot; every row's arithmetic is
@@ -55,9 +56,12 @@ constexpr int kBlockKeys = 64;  // prefix keys per block (2 key tiles of 32)
 constexpr int kOwnKeys = 32;    // own keys per block (1 key tile)
 constexpr float kLn2 = 0.693147180559945309f;
 // Lazy rescaling: the running max of a slot only moves when a block raises its scaled scores by more than kSlack
-// (log2 units), so p = exp2(s - m) <= 2^kSlack; the accumulator is rescaled only when the max or the V frame moves.
+// (log2 units), so p = exp2(s - m) <= 2^kSlack; the accumulator is rescaled only when the max or its frame moves.
 constexpr float kSlack = 8.0f;
 constexpr int kNoFrame = -1000000;  // a block without a visible key leaves the accumulator's frame alone
+// The accumulator's power-of-two frame moves down to a block's V frame only when that lies more than kFrameSlack
+// below it; such a block's probabilities carry 2^(eb - frame) >= 2^-kFrameSlack instead.
+constexpr int kFrameSlack = 3;
 
 struct AttnArgs {
   const uint16_t* q;
@@ -86,7 +90,7 @@ template <int D>
 struct alignas(16) BlockImg {
   alignas(16) uint16_t k[kBlockKeys * D];   // [key][d] int8 keys as exact bf16, 16-byte chunks swizzled (k_off)
   alignas(16) _Float16 vt[D * kBlockKeys];  // [d][permuted key] V', swizzled (vt_off)
-  alignas(16) float gk[kBlockKeys];         // the score multiplier of key j: ks_j scale log2(e) (0 if masked)
+  alignas(16) float gk[kBlockKeys];         // the score multiplier of key j: ks_j scale log2(e) (1 if masked)
   alignas(16) float kb[kBlockKeys];         // 0, or -inf for a masked key
   alignas(16) int info[4];                  // the block constants: 0, eb, masked, 0
 };
@@ -245,8 +249,9 @@ __device__ __forceinline__ void prefix_load(const PrefixSrc& src, int T, int j0,
 // K scale times the softmax scale in log2 units, one fp32 rounding). V' = fp16(q fv_j), one rounding
 // (v_fma_mix), with the fp32 factor fv_j = vs_j 2^-eb (exact); 2^eb lies above the block's largest V scale, so
 // |V'| < 128. (Rounding fv_j to fp16 first would shift all of key j's values the same way, which under cancellation
-// is visible in the output.) A masked key gets a zero V factor (P V' must stay finite), a zero K scale and a -inf
-// bias. Every wave derives the constants from the same 64 scales, so the waves agree without exchanging them.
+// is visible in the output.) A masked key gets a zero V factor (P V' must stay finite), a -inf bias (added to its
+// raw score) and the multiplier 1 (so the score stays -inf). Every wave derives the constants from the same 64
+// scales, so the waves agree without exchanging them.
 template <int D>
 __device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, BlockImg<D>& dst, float scale_log2) {
   const int tid = threadIdx.x;
@@ -313,7 +318,7 @@ __device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, Block
     }
   }
   if (tid < kBlockKeys) {
-    dst.gk[tid] = ok ? r.ks * scale_log2 : 0.0f;
+    dst.gk[tid] = ok ? r.ks * scale_log2 : 1.0f;
     dst.kb[tid] = ok ? 0.0f : -INFINITY;
   }
   if (tid == 0) *reinterpret_cast<int4*>(dst.info) = make_int4(bi.ek, bi.eb, bi.masked, 0);
@@ -349,18 +354,32 @@ __device__ __forceinline__ uint32_t lds_addr(T* p) {
 // bytes [4096 i, 4096 (i + 1)), wave w the 1 KiB at 1024 w of it, and lanes of the first wave take the tail.
 // Completion is a vmcnt wait by every thread that issued a part, then a barrier.
 template <int NBYTES>
-__device__ __forceinline__ void copy_bytes(const void* src, void* dst) {
-  constexpr int kRound = kThreads * 16;
-  constexpr int kFull = NBYTES / kRound;
-  constexpr int kTailLanes = (NBYTES - kFull * kRound) / 16;
+struct CopyShape {
+  static constexpr int kRound = kThreads * 16;
+  static constexpr int kFull = NBYTES / kRound;
+  static constexpr int kTailLanes = (NBYTES - kFull * kRound) / 16;
+  static constexpr int kRounds = kFull + (kTailLanes > 0 ? 1 : 0);
   static_assert(NBYTES % 16 == 0 && kTailLanes <= 64, "copy shape");
+};
+
+// Round i of such a copy (so that a caller can spread the rounds over its work).
+template <int NBYTES>
+__device__ __forceinline__ void copy_round(const void* src, void* dst, int i) {
+  using C = CopyShape<NBYTES>;
   const int tid = threadIdx.x;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const char* s = reinterpret_cast<const char*>(src);
   const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(dst));
+  if (i < C::kFull)
+    dma16(s + i * C::kRound + tid * 16, d + i * C::kRound + wave * 1024);
+  else if (tid < C::kTailLanes)
+    dma16(s + C::kFull * C::kRound + tid * 16, d + C::kFull * C::kRound);
+}
+
+template <int NBYTES>
+__device__ __forceinline__ void copy_bytes(const void* src, void* dst) {
 #pragma unroll
-  for (int i = 0; i < kFull; ++i) dma16(s + i * kRound + tid * 16, d + i * kRound + wave * 1024);
-  if (kTailLanes > 0 && tid < kTailLanes) dma16(s + kFull * kRound + tid * 16, d + kFull * kRound);
+  for (int i = 0; i < CopyShape<NBYTES>::kRounds; ++i) copy_round<NBYTES>(src, dst, i);
 }
 
 // ------------------------------------------------------------------------------------------------- compute
@@ -368,12 +387,28 @@ __device__ __forceinline__ void copy_bytes(const void* src, void* dst) {
 //  * qk_scores: S^T = K Q^T on V_MFMA_F32_32X32X16_BF16 (exact products; fragment reads KA k-steps ahead);
 //  * softmax_block: y = S gk + kb - m (log2 units; gk the per-key K scale times the softmax scale, kb the mask; own
 //    blocks: y = S c - m with the causal mask), the block max, the running max m moved only when the block raises it
-//    by more than kSlack, p = exp2(y), P to fp16, l = l alpha + sum p; it returns whether the accumulator needs
-//    rescaling (some slot's max moved, or the V frame differs);
+//    by more than kSlack, p = exp2(y), P to fp16, l = l alpha + sum p; it returns whether some slot's max moved
+//    (the accumulator is rescaled then, or when its frame moves);
 //  * pv_block: O^T += V'^T P^T (fragment reads VA steps ahead).
 // Each slot moves its own max only on its own condition (the others get alpha = exp2(0) = 1), so a slot's arithmetic
 // does not depend on which slots share its wave and option order cannot change a result.
-template <int D, int KT, int KA>
+// The schedule of qk_scores' reads and MFMAs: the reads KA k-steps ahead of the MFMAs (left alone, the scheduler sinks
+// each read to its MFMA). With NV > 0, NV VALU instructions go after each k-step's MFMAs, so that they issue while
+// the MFMAs run: these are taken from the code between the qk_scores call (with SCHED false) and this call, which
+// must be independent of the scores.
+template <int D, int KT, int KA, int NV>
+__device__ __forceinline__ void qk_sched() {
+  constexpr int KS = D / 16;
+  __builtin_amdgcn_sched_group_barrier(0x100, KA * KT, 0);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks + KA < KS) __builtin_amdgcn_sched_group_barrier(0x100, KT, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, KT, 0);
+    if (NV > 0) __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+  }
+}
+
+template <int D, int KT, int KA, bool SCHED = true>
 __device__ __forceinline__ void qk_scores(const uint16_t* kimg, const bf16x8 (&qf)[D / 16], v16f (&s)[KT]) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
@@ -395,24 +430,40 @@ __device__ __forceinline__ void qk_scores(const uint16_t* kimg, const bf16x8 (&q
     for (int kt = 0; kt < KT; ++kt)
       s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % (KA + 1)][kt], qf[ks], s[kt], 0, 0, 0);
   }
-  // keep the reads KA k-steps ahead of the MFMAs (left alone, the scheduler sinks each read to its MFMA)
-  __builtin_amdgcn_sched_group_barrier(0x100, KA * KT, 0);
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    if (ks + KA < KS) __builtin_amdgcn_sched_group_barrier(0x100, KT, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, KT, 0);
-  }
+  if (SCHED) qk_sched<D, KT, KA, 0>();
 }
 
-// masked: some key of the block is masked (only then is the bias row read); c: own blocks' score multiplier
-template <int D, int KT, bool OWN>
-__device__ __forceinline__ bool softmax_block(const float* gk, const float* kb, bool masked, v16f (&s)[KT], float c,
-                                              int eb, float& m_run, float& l_run, int e_run, float& alpha,
-                                              half8 (&pb)[2 * KT], int own_row, int own_j0, int slot_row,
-                                              int slot_tok) {
+// Adds a state block's bias row (0, or -inf for a masked key) to the raw scores: a masked key's score is then -inf
+// whatever its multiplier (which is 1 for a masked key, so the product stays -inf).
+template <int KT>
+__device__ __forceinline__ void apply_mask(const float* kb, v16f (&s)[KT]) {
+  const int h = (threadIdx.x & 63) >> 5;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const float4 b4 = *reinterpret_cast<const float4*>(&kb[kt * 32 + 8 * r4 + 4 * h]);
+      s[kt][4 * r4] += b4.x;
+      s[kt][4 * r4 + 1] += b4.y;
+      s[kt][4 * r4 + 2] += b4.z;
+      s[kt][4 * r4 + 3] += b4.w;
+    }
+}
+
+// c: own blocks' score multiplier.
+// dlt = eb - e_new <= 0: the block's values are in frame eb and the accumulator in frame e_new, so the block's
+// probabilities enter the P.V product as p 2^dlt (folded into the exponent, exact while p 2^dlt is a normal fp16).
+// A state block with masked keys has had its bias row added to the raw scores (apply_mask). sched() runs at the end
+// of the common path, which is straight-line code (the caller's scheduling directives for that region).
+template <int D, int KT, bool OWN, typename Sched>
+__device__ __forceinline__ bool softmax_block(const float* gk, v16f (&s)[KT], float c, int dlt,
+                                              float& m_run, float& l_run, float& alpha, half8 (&pb)[2 * KT],
+                                              int own_row, int own_j0, int slot_row, int slot_tok, Sched&& sched) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5;
   const float m_safe = m_run == -INFINITY ? 0.0f : m_run;
+  const float fdlt = (float)dlt;
+  const float bias = fdlt - m_safe;
   // this lane's slot sees keys kt*32 + 8*(r/4) + 4*h + r%4
   if constexpr (OWN) {
 #pragma unroll
@@ -420,7 +471,7 @@ __device__ __forceinline__ bool softmax_block(const float* gk, const float* kb, 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = own_j0 + kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        s[kt][r] = (slot_row == own_row && key <= slot_tok) ? fmaf(s[kt][r], c, -m_safe) : -INFINITY;
+        s[kt][r] = (slot_row == own_row && key <= slot_tok) ? fmaf(s[kt][r], c, bias) : -INFINITY;
       }
   } else {
 #pragma unroll
@@ -428,68 +479,65 @@ __device__ __forceinline__ bool softmax_block(const float* gk, const float* kb, 
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const float4 g4 = *reinterpret_cast<const float4*>(&gk[kt * 32 + 8 * r4 + 4 * h]);
-        s[kt][4 * r4] = fmaf(s[kt][4 * r4], g4.x, -m_safe);
-        s[kt][4 * r4 + 1] = fmaf(s[kt][4 * r4 + 1], g4.y, -m_safe);
-        s[kt][4 * r4 + 2] = fmaf(s[kt][4 * r4 + 2], g4.z, -m_safe);
-        s[kt][4 * r4 + 3] = fmaf(s[kt][4 * r4 + 3], g4.w, -m_safe);
+        s[kt][4 * r4] = fmaf(s[kt][4 * r4], g4.x, bias);
+        s[kt][4 * r4 + 1] = fmaf(s[kt][4 * r4 + 1], g4.y, bias);
+        s[kt][4 * r4 + 2] = fmaf(s[kt][4 * r4 + 2], g4.z, bias);
+        s[kt][4 * r4 + 3] = fmaf(s[kt][4 * r4 + 3], g4.w, bias);
       }
-    if (masked) {
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const float4 b4 = *reinterpret_cast<const float4*>(&kb[kt * 32 + 8 * r4 + 4 * h]);
-          s[kt][4 * r4] += b4.x;
-          s[kt][4 * r4 + 1] += b4.y;
-          s[kt][4 * r4 + 2] += b4.z;
-          s[kt][4 * r4 + 3] += b4.w;
-        }
-    }
   }
   float amax = -INFINITY;
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) amax = fmaxf(amax, s[kt][r]);
-  amax = od_xor32_max(amax);
-  // y is relative to the old max; a slot whose block max exceeds it by more than kSlack (or that sees its first key)
-  // moves its max to the block max and shifts its y (wave-uniform branch, rare)
+  amax = od_xor32_max(amax) - fdlt;  // the block max relative to the running max
+  // a slot whose block max exceeds its running max by more than kSlack (or that sees its first key) moves its max
+  // to the block max and shifts its y (wave-uniform branch, rare)
   const bool grow = m_run == -INFINITY ? amax > -INFINITY : amax > kSlack;
   alpha = 1.0f;
-  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+  float psum = 0.0f;
+  // p = exp2(y - shift) into fp16 P, psum = sum p
+  auto probs = [&](float shift) {
+    psum = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = __builtin_amdgcn_exp2f(s[kt][r] - shift);
+        psum += pr;
+        pb[kt * 2 + (r >> 3)][r & 7] = (_Float16)pr;
+      }
+  };
+  // The common case (no slot grows, shift 0) runs straight through, so that the whole softmax is one scheduling
+  // region that a caller can interleave with MFMAs; a block where some slot grows redoes the probabilities.
+  const bool any_grow = __builtin_amdgcn_ballot_w64(grow) != 0;
+  probs(0.0f);
+  sched();
+  // pins the common path's results here: without it the compiler sinks them into the no-growth side of the branch
+  if constexpr (KT == 2)
+    asm volatile("" : "+v"(pb[0]), "+v"(pb[1]), "+v"(pb[2]), "+v"(pb[3]), "+v"(psum));
+  else
+    asm volatile("" : "+v"(pb[0]), "+v"(pb[1]), "+v"(psum));
+  if (any_grow) {
     const float shift = grow ? amax : 0.0f;
     const float m_new = m_safe + shift;
     alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 for a slot's first visible block, 1 if it did not grow
     if (grow) m_run = m_new;
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kt][r] -= shift;
+    probs(shift);
   }
-  float psum = 0.0f;
-#pragma unroll
-  for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float pr = __builtin_amdgcn_exp2f(s[kt][r]);
-      psum += pr;
-      pb[kt * 2 + (r >> 3)][r & 7] = (_Float16)pr;
-    }
-  l_run = fmaf(l_run, alpha, od_xor32_sum(psum));
-  const int e_blk = eb == kNoFrame ? e_run : eb;
-  return __builtin_amdgcn_ballot_w64(grow) != 0 || e_blk != e_run;
+  l_run = fmaf(l_run, alpha, ldexpf(od_xor32_sum(psum), -dlt));
+  return any_grow;
 }
 
-// the accumulator into the block's frame (and each slot's new max): O *= alpha 2^(e_run - e_blk)
+// The accumulator into frame e_new (and each slot's new max): O *= alpha 2^(e_run - e_new).
 template <int D>
-__device__ __forceinline__ void rescale(v16f (&o)[D / 32], float alpha, int eb, int& e_run) {
-  const int e_blk = eb == kNoFrame ? e_run : eb;
-  const float rs = ldexpf(alpha, e_run - e_blk);
+__device__ __forceinline__ void rescale(v16f (&o)[D / 32], float alpha, int e_new, int& e_run) {
+  const float rs = ldexpf(alpha, e_run - e_new);
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dt][r] *= rs;
-  e_run = e_blk;
+  e_run = e_new;
 }
 
 template <int D, int KT, int VA>
@@ -520,6 +568,18 @@ __device__ __forceinline__ void pv_block(const _Float16* vtimg, const half8 (&pb
   }
 }
 
+// The frame the accumulator takes for a block whose values are in frame eb. Over the state blocks it follows the
+// blocks' V exponents lazily: it moves up to a block's frame (P 2^dlt must not exceed the fp16 range) and down only
+// by more than kFrameSlack (to keep small P 2^dlt normal); in between the block's probabilities carry
+// 2^dlt = 2^(eb - frame). Every slot sees the same state blocks in the same order, so the frames do not depend on
+// the option rows. An own block always takes its own frame: the frame the accumulator is in when it comes depends
+// on the rows before it in the tile, and P 2^dlt can round differently (subnormal fp16) from P. Wave-uniform, like
+// the frames.
+template <bool OWN>
+__device__ __forceinline__ int frame_for(int e_blk, int e_run) {
+  return (OWN || e_run == kNoFrame || e_blk > e_run || e_blk < e_run - kFrameSlack) ? e_blk : e_run;
+}
+
 // The three pieces in sequence. `mid` runs between the softmax and the P V product (the int8 path issues the next
 // block's global loads there, so that their registers are not held through the score and softmax phases).
 template <int D, int KT, bool OWN, typename Mid>
@@ -532,14 +592,108 @@ __device__ __forceinline__ void attend_block(const uint16_t* kimg, const _Float1
   __builtin_amdgcn_s_setprio(1);  // a wave issuing MFMAs goes first, the other wave's softmax fills the gaps
   qk_scores<D, KT, KA>(kimg, qf, s);
   __builtin_amdgcn_s_setprio(0);
+  const int e_blk = eb == kNoFrame ? e_run : eb;
+  const int e_new = frame_for<OWN>(e_blk, e_run);
   float alpha;
   half8 pb[2 * KT];
-  const bool rs = softmax_block<D, KT, OWN>(gk, kb, masked, s, c, eb, m_run, l_run, e_run, alpha, pb, own_row,
-                                            own_j0, slot_row, slot_tok);
+  if (!OWN && masked) apply_mask<KT>(kb, s);
+  const bool grow = softmax_block<D, KT, OWN>(gk, s, c, e_blk - e_new, m_run, l_run, alpha, pb, own_row, own_j0,
+                                              slot_row, slot_tok, [] {});
   mid();
-  if (rs) rescale<D>(o, alpha, eb, e_run);
+  if (grow || e_new != e_run) rescale<D>(o, alpha, e_new, e_run);
   __builtin_amdgcn_s_setprio(1);
   pv_block<D, KT, 1>(vtimg, pb, o);
+  __builtin_amdgcn_s_setprio(0);
+}
+
+// One state block of the staged path, software-pipelined over the blocks: the NEXT block's scores (keys at knext)
+// are computed while this block's softmax runs, then this block's P.V product. s holds this block's scores on entry;
+// sn receives the next block's. The score MFMAs go one k-step at a time, each followed by a share of the softmax's
+// common path (a group of 4 scores: multiplier, max, exp2, sum, fp16) that the scheduler may not move across the
+// k-steps, so the wave issues VALU work while its MFMAs run; dma(ks) issues the k-step's share of the copies of
+// later blocks. The arithmetic per block is that of attend_block (the same operations on the same values in the
+// same order), so both paths give the same bits.
+template <int D, typename Dma>
+__device__ __forceinline__ void staged_step(const BlockImg<D>& cur, const uint16_t* knext, const bf16x8 (&qf)[D / 16],
+                                            v16f (&s)[2], v16f (&sn)[2], float& m_run, float& l_run, int& e_run,
+                                            v16f (&o)[D / 32], Dma&& dma) {
+  constexpr int KT = 2, KA = 1, KS = D / 16;
+  constexpr int kGroups = KT * 4;          // groups of 4 scores: (key tile kt, register quad r4)
+  constexpr int kPerStep = kGroups / KS;   // D = 128: one group per k-step; D = 64: two
+  static_assert(kGroups % KS == 0, "score groups per k-step");
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  const BlockInfo ci = read_info(cur.info);
+  const int e_blk = ci.eb == kNoFrame ? e_run : ci.eb;
+  const int e_new = frame_for<false>(e_blk, e_run);
+  const int dlt = e_blk - e_new;
+  if (ci.masked) apply_mask<KT>(cur.kb, s);  // rare: a state's last block, or a key mask
+  const float m_safe = m_run == -INFINITY ? 0.0f : m_run;
+  const float fdlt = (float)dlt;
+  const float bias = fdlt - m_safe;
+  float amax = -INFINITY, psum = 0.0f;
+  half8 pb[2 * KT];
+
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) sn[kt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  bf16x8 kf[KA + 1][KT];
+  auto kread = [&](int ks) {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+      kf[ks % (KA + 1)][kt] = *reinterpret_cast<const bf16x8*>(&knext[k_off<D>(kt * 32 + col, ks * 2 + h)]);
+  };
+#pragma unroll
+  for (int ks = 0; ks < KA; ++ks) kread(ks);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks + KA < KS) kread(ks + KA);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+      sn[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % (KA + 1)][kt], qf[ks], sn[kt], 0, 0, 0);
+    dma(ks);
+#pragma unroll
+    for (int c = 0; c < kPerStep; ++c) {
+      const int grp = ks * kPerStep + c, kt = grp / 4, r4 = grp % 4;
+      const float4 g4 = *reinterpret_cast<const float4*>(&cur.gk[kt * 32 + 8 * r4 + 4 * h]);
+      const float gg[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * r4 + e;
+        s[kt][r] = fmaf(s[kt][r], gg[e], bias);
+        amax = fmaxf(amax, s[kt][r]);
+        const float pr = __builtin_amdgcn_exp2f(s[kt][r]);
+        psum += pr;
+        pb[kt * 2 + (r >> 3)][r & 7] = (_Float16)pr;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // pins the common path's results here: without it the compiler sinks them into the no-growth side of the branch
+  asm volatile("" : "+v"(pb[0]), "+v"(pb[1]), "+v"(pb[2]), "+v"(pb[3]), "+v"(psum));
+  // the rest of softmax_block: growth (rare), the running sum, the rescale
+  amax = od_xor32_max(amax) - fdlt;
+  const bool grow = m_run == -INFINITY ? amax > -INFINITY : amax > kSlack;
+  float alpha = 1.0f;
+  const bool any_grow = __builtin_amdgcn_ballot_w64(grow) != 0;
+  if (any_grow) {
+    const float shift = grow ? amax : 0.0f;
+    const float m_new = m_safe + shift;
+    alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    if (grow) m_run = m_new;
+    psum = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = __builtin_amdgcn_exp2f(s[kt][r] - shift);
+        psum += pr;
+        pb[kt * 2 + (r >> 3)][r & 7] = (_Float16)pr;
+      }
+  }
+  l_run = fmaf(l_run, alpha, ldexpf(od_xor32_sum(psum), -dlt));
+  if (any_grow || e_new != e_run) rescale<D>(o, alpha, e_new, e_run);
+  __builtin_amdgcn_s_setprio(1);
+  pv_block<D, KT, 1>(cur.vt, pb, o);
   __builtin_amdgcn_s_setprio(0);
 }
 
@@ -675,26 +829,52 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
   }
 
   float m_run = -INFINITY, l_run = 0.0f;
-  int e_run = 0;  // the power-of-two frame the accumulator is in (follows the blocks' V exponents)
+  int e_run = kNoFrame;  // the power-of-two frame the accumulator is in (follows the blocks' V exponents)
   v16f o[D / 32];
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) o[dt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
   if (b_hi > b_lo) {
     if constexpr (STAGED) {
-      // block images straight from memory into the double-buffered LDS images
+      // Block images straight from memory into the double-buffered LDS images, the keys one block ahead of the rest:
+      // block j lives in buffer (j - b_lo) & 1; during block b's step, whose score MFMAs read block b + 1's keys,
+      // block b + 2's keys go into buffer b (its keys were read in the previous step) and block b + 1's values,
+      // multipliers and constants into the other buffer (block b - 1's, read in the previous step).
+      constexpr int kKeyBytes = (int)offsetof(BlockImg<D>, vt);
+      constexpr int kRestBytes = (int)sizeof(BlockImg<D>) - kKeyBytes;
+      auto rest = [](const BlockImg<D>* bi) { return reinterpret_cast<const char*>(bi) + kKeyBytes; };
+      if (b_lo + 1 < b_hi) copy_bytes<kKeyBytes>(img + b_lo + 1, sm.b[1].k);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      for (int b = b_lo; b < b_hi; ++b) {
+      v16f s0[2], s1[2];
+      qk_scores<D, 2, 2>(sm.b[0].k, qf, s0);
+      __syncthreads();  // block b_lo's keys are read: block b_lo + 2's may go into buffer 0
+      // the copies' rounds (global_load_lds instructions) are spread over the step's k-steps: issued all at once, the
+      // eight waves of a CU queue behind each other at the texture unit
+      constexpr int kKR = CopyShape<kKeyBytes>::kRounds, kNR = kKR + CopyShape<kRestBytes>::kRounds;
+      auto step = [&](int b, v16f (&sc)[2], v16f (&sn)[2]) {
         const int buf = (b - b_lo) & 1;
-        const BlockImg<D>& bk = sm.b[buf];
-        const BlockInfo ci = read_info(bk.info);
-        // the other buffer was last read before the previous barrier
-        if (b + 1 < b_hi) copy_bytes<(int)sizeof(BlockImg<D>)>(img + b + 1, &sm.b[buf ^ 1]);
-        attend_block<D, 2, false>(bk.k, bk.vt, bk.gk, bk.kb, qf, 0.0f, ci.eb, ci.masked != 0, m_run, l_run, e_run, o,
-                                  0, 0, slot_row, slot_tok, [] {});
+        BlockImg<D>& cur = sm.b[buf];
+        BlockImg<D>& nxt = sm.b[buf ^ 1];
+        auto dma = [&](int ks) {
+#pragma unroll
+          for (int r = ks * kNR / (D / 16); r < (ks + 1) * kNR / (D / 16); ++r) {
+            if (r < kKR) {
+              if (b + 2 < b_hi) copy_round<kKeyBytes>(img + b + 2, cur.k, r);
+            } else if (b + 1 < b_hi) {
+              copy_round<kRestBytes>(rest(img + b + 1), reinterpret_cast<char*>(&nxt) + kKeyBytes, r - kKR);
+            }
+          }
+        };
+        // the last block's step scores its own keys again (in place of a next block), and the result is not used
+        staged_step<D>(cur, b + 1 < b_hi ? nxt.k : cur.k, qf, sc, sn, m_run, l_run, e_run, o, dma);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+      };
+      // two blocks per trip, so that the scores alternate between s0 and s1 without register copies
+      for (int b = b_lo; b < b_hi; b += 2) {
+        step(b, s0, s1);
+        if (b + 1 < b_hi) step(b + 1, s1, s0);
       }
     } else {
       // the int8 state, converted here: registers first (loads issued during the previous block), then LDS
@@ -727,8 +907,10 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
       BlockInfo bi;
       own_stage<D>(p, sm.red, sm.b[0].k, sm.b[0].vt, row, g, j0, bi);
       __syncthreads();
-      attend_block<D, 1, true>(sm.b[0].k, sm.b[0].vt, nullptr, nullptr, qf, p.scale_log2, bi.eb, false, m_run, l_run,
-                               e_run, o, row, j0, slot_row, slot_tok, [] {});
+      // a wave with no slot in this row skips its block (all its scores would be masked)
+      if (__builtin_amdgcn_ballot_w64(slot_row == row) != 0)
+        attend_block<D, 1, true>(sm.b[0].k, sm.b[0].vt, nullptr, nullptr, qf, p.scale_log2, bi.eb, false, m_run,
+                                 l_run, e_run, o, row, j0, slot_row, slot_tok, [] {});
     }
   }
 
