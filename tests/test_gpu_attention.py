@@ -18,11 +18,16 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def make_case(seed, Ns, row_counts, Hq, Hkv, t, D, T, cap=None, holes=False):
+def make_case(seed, Ns, row_counts, Hq, Hkv, t, D, T, cap=None, holes=False, vspread=False):
     g = torch.Generator().manual_seed(seed)
     R = sum(row_counts)
     cap = T if cap is None else cap
-    kv_src = torch.randn(2, Ns, Hkv, T, D, generator=g).to(torch.bfloat16)
+    kv_src = torch.randn(2, Ns, Hkv, T, D, generator=g)
+    if vspread:  # the values of every 64-token block of the state times 2^u, u uniform in -10..6: the blocks' V frames
+        # (the kernel's unit) spread over 17 binades, so consecutive blocks often differ by more than 3 binades
+        u = torch.randint(-10, 7, (Ns, Hkv, -(-T // 64), 1, 1), generator=g).float()
+        kv_src[1] *= torch.exp2(u).expand(-1, -1, -1, 64, 1).reshape(Ns, Hkv, -1, 1)[:, :, :T]
+    kv_src = kv_src.to(torch.bfloat16)
     kq, ks = oq.quantize_rows(kv_src[0])
     vq, vs = oq.quantize_rows(kv_src[1])
     ks, vs = ks[..., 0], vs[..., 0]
@@ -68,6 +73,9 @@ CASES = {
     "empty_state_group": dict(seed=5, Ns=3, row_counts=[2, 0, 3], Hq=8, Hkv=2, t=9, D=128, T=70),
     "t1_single_token_rows": dict(seed=6, Ns=2, row_counts=[4, 3], Hq=8, Hkv=8, t=1, D=64, T=257),
     "config4_like_t12": dict(seed=7, Ns=1, row_counts=[11], Hq=32, Hkv=8, t=12, D=128, T=300),
+    # V scales over 17 binades: the accumulator's power-of-two frame moves up and down across the state blocks and
+    # many blocks enter with their probabilities scaled by 2^-1..2^-3
+    "v_frames_spread": dict(seed=8, Ns=2, row_counts=[3, 4], Hq=8, Hkv=2, t=6, D=128, T=700, vspread=True),
 }
 
 
@@ -101,16 +109,22 @@ def test_strided_query_view(gpu_lib):
     assert torch.equal(out_s, out_c)
 
 
-def test_option_order_invariance_bitwise(gpu_lib):
-    """Shuffling the option rows of each request permutes the outputs and changes nothing else (bitwise)."""
-    c = make_case(seed=10, Ns=4, row_counts=[8, 8, 8, 8], Hq=32, Hkv=8, t=16, D=128, T=256)
+@pytest.mark.parametrize("vspread", [False, True])
+def test_option_order_invariance_bitwise(gpu_lib, vspread):
+    """Shuffling the option rows of each request permutes the outputs and changes nothing else (bitwise), also when
+    the state's V frames spread over many binades (the accumulator's frame then moves between blocks)."""
+    c = make_case(seed=10, Ns=4, row_counts=[8, 8, 8, 8], Hq=32, Hkv=8, t=16, D=128, T=256, vspread=vspread)
+    if vspread:  # own values over a few binades too, so that the rows' own blocks take different frames
+        g0 = torch.Generator().manual_seed(12)
+        c["v"] = (c["v"].float() * torch.exp2(torch.randint(-6, 7, (32, 1, 1, 1), generator=g0).float())).bfloat16()
     g = torch.Generator().manual_seed(11)
     perm = torch.cat([torch.randperm(8, generator=g) + 8 * i for i in range(4)])
-    out, lse = run_gpu(c)
-    cp = dict(c, q=c["q"][perm], k=c["k"][perm], v=c["v"][perm])
-    out_p, lse_p = run_gpu(cp)
-    assert torch.equal(out_p, out[perm.to(DEV)])
-    assert torch.equal(lse_p, lse[perm.to(DEV)])
+    for staged in (True, False):
+        out, lse = run_gpu(c, staged=staged)
+        cp = dict(c, q=c["q"][perm], k=c["k"][perm], v=c["v"][perm])
+        out_p, lse_p = run_gpu(cp, staged=staged)
+        assert torch.equal(out_p, out[perm.to(DEV)]), staged
+        assert torch.equal(lse_p, lse[perm.to(DEV)]), staged
 
 
 def test_config1_branched_attention_full_shape(gpu_lib):
@@ -136,7 +150,8 @@ def test_config1_branched_attention_full_shape(gpu_lib):
 # ---- key-range splits (od_branched_attn_split): the same result, merged by LSE
 
 SPLIT_CASES = [("two_states_holes", 2), ("two_states_holes", 7), ("own_two_chunks_d64", 3), ("own_only_T0", 4),
-               ("empty_state_group", 3), ("t1_single_token_rows", 5), ("config4_like_t12", 64)]
+               ("empty_state_group", 3), ("t1_single_token_rows", 5), ("config4_like_t12", 64),
+               ("v_frames_spread", 5)]
 
 
 @pytest.mark.parametrize("name,n_split", SPLIT_CASES)
