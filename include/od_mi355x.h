@@ -110,6 +110,26 @@ int od_kv_copy_rows(const int8_t* src_q, const float* src_s, int64_t src_mat_q, 
                     int64_t n_mats, int64_t H, int64_t D, const int64_t* seg, int64_t n_seg, od_stream_t stream);
 
 /*
+ * od_lm_head_logprob — log-prob of one token per row under an LM head whose rows are an int8 table, with the
+ * normaliser over the whole vocabulary and no rows x vocabulary logits in memory. Replaces: Backbone.token_logprob
+ * (src/opendecider/backbone.py:164-178) over Int8Embedding / Int8Linear rows (src/opendecider/quant.py:122-132,
+ * 159-161,183-203), i.e. its chunk loop of dequant_rows + bf16 matmul + logsumexp + logaddexp and the fp32 target
+ * term. Feeds the option-token LM feature (src/opendecider/v3.py:438-442,527-538).
+ *   hb     bf16 [M, ldh]: bf16(h), the matmul operand
+ *   hn     [M, ldhn], fp32 (hn_fp32 != 0) or bf16: h as the target term reads it (may alias hb when h is bf16)
+ *   w      int8 [V, ldw] table rows; scale bf16 [V] (the per-row scale in the table's dtype)
+ *   tok    int32 [M] device array: the token of each row (a token outside [0, V) gives NaN)
+ *   out    fp32 [M] (out): sum_k float(h[m,k]) * float(w[tok,k] * scale[tok]) - logsumexp_v bf16(hb[m] . bf16(w[v] * scale[v]))
+ *   ws     fp32 workspace of at least od_lm_head_logprob_ws(M, V) floats (per-row partial max / sum)
+ * Requires K % 64 == 0, ldh % 8 == 0, ldw % 16 == 0, hb and w 16-byte aligned, 256 * ldh * 2 and 256 * ldw below
+ * 2^31. Two launches (logit tiles with the partial log-sum-exp in their epilogue, then a per-row combine).
+ */
+int od_lm_head_logprob_ws(int64_t M, int64_t V, int64_t* ws_floats);
+int od_lm_head_logprob(const uint16_t* hb, int64_t ldh, const void* hn, int64_t ldhn, int hn_fp32, const int8_t* w,
+                       int64_t ldw, const uint16_t* scale, const int32_t* tok, int64_t M, int64_t V, int64_t K,
+                       float* out, float* ws, int64_t ws_floats, od_stream_t stream);
+
+/*
  * od_branched_attn — branched (Hydragen) option-row attention over an int8 shared state, one launch.
  * Replaces: _split_attention (src/opendecider/prefix_attn.py:43-76) with its two wide_attention launches
  * (src/opendecider/wide_attention.py:70-91) and the torch LSE merge (prefix_attn.py:74-76), the per-state loop

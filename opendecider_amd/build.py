@@ -22,7 +22,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libod_mi355x.so")
-SOURCES = ["od_quant.hip", "od_gemm.hip", "od_attn.hip", "od_wide.hip", "od_layer.hip"]
+SOURCES = ["od_quant.hip", "od_gemm.hip", "od_attn.hip", "od_wide.hip", "od_layer.hip", "od_lmhead.hip"]
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-inline-asm"]

@@ -401,3 +401,47 @@ def wide_attn(q, k, v, scale: float, kvalid=None, causal: bool = True, return_ls
                              kvalid.stride(0) if kvalid is not None else 0, ptr(out), *out.stride()[:3], ptr(lse), B, H,
                              G, T, S, DK, DV, 1 if causal else 0, float(scale), stream_of(q)), "od_wide_attn")
     return (out, lse) if return_lse else out
+
+
+def lm_head_logprob(h: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, tok: torch.Tensor,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """log softmax(h @ W^T)[tok] for the int8 table W = qweight (V, K) with per-row scales `scale` (V,) or (V, 1)
+    bf16 (Backbone.token_logprob, backbone.py:164-178, over Int8Embedding / Int8Linear rows): the normaliser from the
+    bf16 logits of bf16(h) against the bf16-dequantized rows, the target term in fp32. h (..., K) bf16 or fp32,
+    tok (...) integer. Returns fp32 (...). One pass over the table; no (rows, V) logits are allocated."""
+    require_gpu(h, qweight, scale, tok, out, name="lm_head_logprob")
+    if qweight.dtype != torch.int8 or qweight.dim() != 2:
+        raise TypeError("qweight must be an int8 (V, K) table")
+    V, K = qweight.shape
+    sc = _lib.bf16_bits(scale).reshape(-1).contiguous()
+    if sc.numel() != V:
+        raise ValueError(f"scale has {sc.numel()} elements, expected {V}")
+    if h.shape[-1] != K:
+        raise ValueError(f"h has {h.shape[-1]} features, the table {K}")
+    lead = h.shape[:-1]
+    h2 = h.reshape(-1, K)
+    M = h2.shape[0]
+    if tok.shape != lead:
+        raise ValueError(f"tok shape {tuple(tok.shape)} != h's leading shape {tuple(lead)}")
+    if h2.dtype == torch.bfloat16:
+        hb = _rows_aligned(h2)
+        hn, hn_fp32 = hb, 0
+    elif h2.dtype == torch.float32:
+        hn, hn_fp32 = (h2 if h2.stride(-1) == 1 else h2.contiguous()), 1
+        hb = h2.to(torch.bfloat16).contiguous()  # the matmul operand, bf16(h) as the reference's h.to(bfloat16)
+    else:
+        raise TypeError(f"h must be bfloat16 or float32, got {h2.dtype}")
+    w = qweight if qweight.stride(-1) == 1 and qweight.stride(0) % 16 == 0 and qweight.data_ptr() % 16 == 0 \
+        else qweight.contiguous()
+    t32 = tok.reshape(-1).to(torch.int32).contiguous()
+    if out is None:
+        out = torch.empty(M, dtype=torch.float32, device=h.device)
+    elif out.dtype != torch.float32 or out.numel() != M or not out.is_contiguous():
+        raise ValueError("out must be fp32 contiguous with one element per row")
+    n = ctypes.c_int64()
+    check(lib().od_lm_head_logprob_ws(M, V, ctypes.byref(n)), "od_lm_head_logprob_ws")
+    ws = torch.empty(max(n.value, 1), dtype=torch.float32, device=h.device)
+    check(lib().od_lm_head_logprob(ptr(hb), hb.stride(0), ptr(hn), hn.stride(0), hn_fp32, ptr(w), w.stride(0),
+                                   ptr(sc), ptr(t32), M, V, K, ptr(out), ptr(ws), ws.numel(), stream_of(h)),
+          "od_lm_head_logprob")
+    return out.view(lead)
