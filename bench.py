@@ -8,7 +8,8 @@ q/k norm + RoPE, branched attention over the int8 state + own tokens, W8A8 O GEM
 W8A8 gate+up GEMM, SwiGLU+quantize, W8A8 down GEMM (+residual). The states' K/V are synthetic (bf16 N(0,1)
 quantized by the append kernel) and resident in HBM before timing; so are the option token ids.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--workload scoring|decision|wide_choice]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                    [--workload scoring|decision|wide_choice|gemm_traffic|attention|lm_logprob]
 
 Prints ONE JSON line: metric / value (decisions/s) / timing, the roofline of the dominant kernel (the W8A8 GEMM,
 int8 MFMA), the branched attention's figures, and a CPU baseline (the oracle, on this host's cores, on a bounded
@@ -41,7 +42,8 @@ def parse():
     ap.add_argument("--options", type=int, default=32)
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--state", type=int, default=2048)
-    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm_traffic", "attention"],
+    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm_traffic", "attention",
+                                           "lm_logprob"],
                     default="scoring",
                     help="scoring (default): the metric's option-row scoring pass over cached 2048-token states; "
                          "decision: full decision forward from token ids (4 requests, 4096-token states prefilled, "
@@ -50,7 +52,8 @@ def parse():
                          "the run the GEMM traffic counters are read on (a 256 MiB device copy to calibrate them, "
                          "then two scoring passes through 2 layers, i.e. each M = 4096 GEMM shape twice); "
                          "attention: the branched attention alone on the config-1 shape and on the KV-bound probe "
-                         "(32768-token states, 2 options x 16 tokens per state)")
+                         "(32768-token states, 2 options x 16 tokens per state); lm_logprob: the LM head's token "
+                         "log-prob of 1024 rows over a 151936 x 4096 int8 table")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-repeats", type=int, default=3)
     return ap.parse_args()
@@ -486,6 +489,66 @@ def run_attention(args):
             "config": {"workload": "branched attention alone: config-1 shape and KV-bound probe"}, "shapes": res}
 
 
+def run_lm_logprob(args):
+    """The LM head's token log-prob (the option-token LM feature, backbone.py:164-178) over a Qwen-size int8
+    vocabulary table: 151936 rows x 4096 (Int8Table of random N(0, 0.03) rows, bf16 scales), 1024 rows of bf16 h
+    N(0, 2) (16 options x 64 tokens) with random target tokens. One call = od_lm_head_logprob (the bf16-MFMA logit
+    tiles with the table dequantized on the fly and the log-sum-exp in their epilogue, then the per-row combine);
+    HIP events around the timed calls. CPU baseline: the oracle on 2 rows over the whole vocabulary."""
+    import torch
+
+    from opendecider_amd import Int8Table, token_logprob
+    dev = "cuda:0"
+    V, K, M = 151936, 4096, 1024
+    g = torch.Generator(device=dev).manual_seed(7)
+    w = (torch.randn(V, K, device=dev, generator=g) * 0.03).to(torch.bfloat16)
+    table = Int8Table(w)
+    del w
+    h = (torch.randn(M, K, device=dev, generator=g) * 2.0).to(torch.bfloat16)
+    tok = torch.randint(0, V, (M,), device=dev, generator=g)
+    out = None
+    for _ in range(args.warmup):
+        out = token_logprob(table, h, tok)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        out = token_logprob(table, h, tok)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / args.steps
+    assert torch.isfinite(out).all()
+    flops = 2.0 * M * V * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    table_bytes = V * K + V * 2
+    res = {"metric": "LM-head token log-probs/s over an int8 151936 x 4096 table (bf16 MFMA TFLOP/s beside it)",
+           "value": M / (ms * 1e-3), "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "int8 table, bf16 MFMA", "data": "synthetic",
+           "config": {"workload": f"token_logprob: {M} rows of h (bf16, hidden {K}) against a {V}-row int8 LM-head "
+                                  "table, one target token per row"},
+           "roofline": {"kernel": "od_lm_head_logprob (lm_logits_kernel + lm_combine_kernel)", "bound": "mfma",
+                        "achieved": tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": tflops / BF16_PEAK_TFLOPS, "traffic": None,
+                        "algorithmic_bytes": table_bytes + M * K * 2 + M * 8,
+                        "note": "2 x rows x vocabulary x hidden FLOP per call over the call's duration (HIP events)",
+                        "avg_launch_us": ms * 1e3}}
+    if not args.no_cpu_baseline:
+        from oracle import lm_head as ol
+        torch.set_num_threads(os.cpu_count() or 1)
+        q, sc = table.qweight.cpu(), table.scale.cpu().reshape(-1)
+        hs, ts = h[:2].cpu(), tok[:2].cpu()
+        rows = lambda idx, dt: ol.int8_rows(q, sc, idx, dt)
+        ol.token_logprob(hs[:1], rows, V, ts[:1])
+        t0 = time.perf_counter()
+        ol.token_logprob(hs, rows, V, ts)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": 2 / dt, "unit": "rows/s", "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"the oracle (float64 logits of the bf16 operands, chunked logaddexp) on 2 "
+                                         f"rows over the whole {V}-row table, {dt:.1f} s, after a 1-row warm-up"}
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -496,7 +559,7 @@ def main():
     if args.workload != "scoring":
         torch.cuda.set_device(0)
         fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm_traffic": run_gemm_traffic,
-              "attention": run_attention}[args.workload]
+              "attention": run_attention, "lm_logprob": run_lm_logprob}[args.workload]
         print(json.dumps(fn(args)))
         return
 

@@ -121,8 +121,9 @@ int od_kv_copy_rows(const int8_t* src_q, const float* src_s, int64_t src_mat_q, 
  *   tok    int32 [M] device array: the token of each row (a token outside [0, V) gives NaN)
  *   out    fp32 [M] (out): sum_k float(h[m,k]) * float(w[tok,k] * scale[tok]) - logsumexp_v bf16(hb[m] . bf16(w[v] * scale[v]))
  *   ws     fp32 workspace of at least od_lm_head_logprob_ws(M, V) floats (per-row partial max / sum)
- * Requires K % 64 == 0, ldh % 8 == 0, ldw % 16 == 0, hb and w 16-byte aligned, 256 * ldh * 2 and 256 * ldw below
- * 2^31. Two launches (logit tiles with the partial log-sum-exp in their epilogue, then a per-row combine).
+ * Requires K % 64 == 0, ldh % 8 == 0, ldw % 16 == 0, ldhn % 4 (fp32) or % 8 (bf16) == 0, hb, hn and w 16-byte
+ * aligned, 256 * ldh * 2 and 256 * ldw below 2^31. Two launches (logit tiles with the partial log-sum-exp in
+ * their epilogue, then a per-row combine).
  */
 int od_lm_head_logprob_ws(int64_t M, int64_t V, int64_t* ws_floats);
 int od_lm_head_logprob(const uint16_t* hb, int64_t ldh, const void* hn, int64_t ldhn, int hn_fp32, const int8_t* w,

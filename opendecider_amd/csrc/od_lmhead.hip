@@ -243,7 +243,8 @@ __global__ __launch_bounds__(kThreads, 1) void lm_logits_kernel(LmArgs p) {
 
 // One wave per row: lse = M + log sum_p s_p exp(m_p - M) over the partials (M = max_p m_p), and the target term
 // sum_k float(h[m,k]) * (q[t,k] * s[t]) (each product rounded to fp32, then summed, as the reference's
-// (h.float() * row).sum(-1)); out = target - lse, NaN for a token id outside [0, V).
+// (h.float() * row).sum(-1); here each lane sums 8 consecutive k at a time, then the wave); out = target - lse, NaN
+// for a token id outside [0, V). Loads are 8 int8 / 8 bf16 / 2 x 4 fp32 per lane (K % 8 == 0, aligned rows).
 template <bool HF32>
 __global__ __launch_bounds__(256) void lm_combine_kernel(const float* __restrict__ part, int n_parts,
                                                          const void* __restrict__ hn, int64_t ldhn,
@@ -254,14 +255,16 @@ __global__ __launch_bounds__(256) void lm_combine_kernel(const float* __restrict
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (m >= M) return;  // wave-uniform
-  const float* pr = part + m * n_parts * 2;
+  const float2* pr = reinterpret_cast<const float2*>(part + m * n_parts * 2);
   float mx = -INFINITY;
-  for (int q = lane; q < n_parts; q += 64) mx = fmaxf(mx, pr[2 * q]);
+#pragma unroll 4
+  for (int q = lane; q < n_parts; q += 64) mx = fmaxf(mx, pr[q].x);
   mx = od_wave_max_dpp(mx);
   float sm = 0.0f;
+#pragma unroll 4
   for (int q = lane; q < n_parts; q += 64) {
-    const float pm = pr[2 * q];
-    if (pm != -INFINITY) sm += pr[2 * q + 1] * __builtin_amdgcn_exp2f((pm - mx) * kLog2e);
+    const float2 v = pr[q];
+    if (v.x != -INFINITY) sm += v.y * __builtin_amdgcn_exp2f((v.x - mx) * kLog2e);
   }
   sm = od_wave_sum_dpp(sm);
   const float lse = mx + __logf(sm);
@@ -271,11 +274,29 @@ __global__ __launch_bounds__(256) void lm_combine_kernel(const float* __restrict
   if (valid) {
     const int8_t* row = w + (int64_t)t * ldw;
     const float s = od_bf16_to_f32(scale[t]);
-    for (int64_t k = lane; k < K; k += 64) {
-      const float hv = HF32 ? reinterpret_cast<const float*>(hn)[m * ldhn + k]
-                            : od_bf16_to_f32(reinterpret_cast<const uint16_t*>(hn)[m * ldhn + k]);
-      const float wv = (float)row[k] * s;
-      dot += hv * wv;
+#pragma unroll 2
+    for (int64_t k = (int64_t)lane * 8; k < K; k += 64 * 8) {
+      const uint2 qw = *reinterpret_cast<const uint2*>(row + k);
+      float hv[8];
+      if constexpr (HF32) {
+        const float4* hp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(hn) + m * ldhn + k);
+        const float4 a = hp[0], b = hp[1];
+        hv[0] = a.x; hv[1] = a.y; hv[2] = a.z; hv[3] = a.w; hv[4] = b.x; hv[5] = b.y; hv[6] = b.z; hv[7] = b.w;
+      } else {
+        const uint4 hb = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(hn) + m * ldhn + k);
+        const uint32_t hw[4] = {hb.x, hb.y, hb.z, hb.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hv[2 * e] = __uint_as_float(hw[e] << 16);
+          hv[2 * e + 1] = __uint_as_float(hw[e] & 0xffff0000u);
+        }
+      }
+      const uint32_t qq[2] = {qw.x, qw.y};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float wv = (float)(int8_t)((qq[e >> 2] >> (8 * (e & 3))) & 0xffu) * s;
+        dot += hv[e] * wv;
+      }
     }
   }
   dot = od_wave_sum_dpp(dot);
@@ -301,6 +322,7 @@ extern "C" int od_lm_head_logprob(const uint16_t* hb, int64_t ldh, const void* h
   if (ldh < K || ldhn < K || ldw < K) return OD_ERR_SHAPE;
   // whole 64-k stages and 16-byte rows; buffer offsets are 32-bit: a tile's panels stay below 2 GiB
   if (K % BK || ldh % 8 || ldw % 16 || !od_aligned16(hb) || !od_aligned16(w)) return OD_ERR_ALIGN;
+  if (!od_aligned16(hn) || ldhn % (hn_fp32 ? 4 : 8)) return OD_ERR_ALIGN;
   if ((int64_t)BM * ldh * 2 >= (1ll << 31) || (int64_t)BN * ldw >= (1ll << 31)) return OD_ERR_UNSUPPORTED;
   int64_t need = 0;
   od_lm_head_logprob_ws(M, V, &need);

@@ -427,7 +427,8 @@ def lm_head_logprob(h: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
         hb = _rows_aligned(h2)
         hn, hn_fp32 = hb, 0
     elif h2.dtype == torch.float32:
-        hn, hn_fp32 = (h2 if h2.stride(-1) == 1 else h2.contiguous()), 1
+        ok = h2.stride(-1) == 1 and h2.stride(0) % 4 == 0 and h2.data_ptr() % 16 == 0
+        hn, hn_fp32 = (h2 if ok else h2.contiguous()), 1
         hb = h2.to(torch.bfloat16).contiguous()  # the matmul operand, bf16(h) as the reference's h.to(bfloat16)
     else:
         raise TypeError(f"h must be bfloat16 or float32, got {h2.dtype}")
