@@ -131,6 +131,19 @@ int od_lm_head_logprob(const uint16_t* hb, int64_t ldh, const void* hn, int64_t 
                        float* out, float* ws, int64_t ws_floats, od_stream_t stream);
 
 /*
+ * od_lm_head_logprob_q4 — od_lm_head_logprob over a Q4_0 table (Q4Table, src/opendecider/quant.py:206-246): rows of
+ * K / 32 blocks, each 16 bytes of nibbles (block positions 0-15 in the low nibbles, 16-31 in the high ones) and an
+ * fp16 scale d; a value is (q - 8) * d. The logits use the reference's bf16 dequant_rows ((q - 8) in bf16 times
+ * d.to(bf16), rounded to bf16); the target term uses (q - 8) * d in fp32.
+ *   qs  uint8 [V, ldq >= K / 2] (ldq % 16 == 0, 16-byte aligned);  d  fp16 bits [V, ldd >= K / 32]
+ * Other arguments, workspace and requirements as od_lm_head_logprob.
+ */
+int od_lm_head_logprob_q4(const uint16_t* hb, int64_t ldh, const void* hn, int64_t ldhn, int hn_fp32,
+                          const uint8_t* qs, int64_t ldq, const uint16_t* d, int64_t ldd, const int32_t* tok,
+                          int64_t M, int64_t V, int64_t K, float* out, float* ws, int64_t ws_floats,
+                          od_stream_t stream);
+
+/*
  * od_branched_attn — branched (Hydragen) option-row attention over an int8 shared state, one launch.
  * Replaces: _split_attention (src/opendecider/prefix_attn.py:43-76) with its two wide_attention launches
  * (src/opendecider/wide_attention.py:70-91) and the torch LSE merge (prefix_attn.py:74-76), the per-state loop

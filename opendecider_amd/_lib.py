@@ -52,6 +52,8 @@ SIGNATURES = {
     "od_lm_head_logprob_ws": [_i64, _i64, _c_ptr],
     "od_lm_head_logprob": [_c_ptr, _i64, _c_ptr, _i64, ctypes.c_int, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64,
                            _c_ptr, _c_ptr, _i64, _c_ptr],
+    "od_lm_head_logprob_q4": [_c_ptr, _i64, _c_ptr, _i64, ctypes.c_int, _c_ptr, _i64, _c_ptr, _i64, _c_ptr, _i64,
+                              _i64, _i64, _c_ptr, _c_ptr, _i64, _c_ptr],
 }
 
 _LIB = None

@@ -403,6 +403,40 @@ def wide_attn(q, k, v, scale: float, kvalid=None, causal: bool = True, return_ls
     return (out, lse) if return_lse else out
 
 
+def _lm_h_operands(h: torch.Tensor, K: int):
+    """(hb bf16 rows for the matmul, hn rows for the target term, hn_fp32 flag, M, leading shape)."""
+    if h.shape[-1] != K:
+        raise ValueError(f"h has {h.shape[-1]} features, the table {K}")
+    lead = h.shape[:-1]
+    h2 = h.reshape(-1, K)
+    if h2.dtype == torch.bfloat16:
+        hb = _rows_aligned(h2)
+        return hb, hb, 0, h2.shape[0], lead
+    if h2.dtype == torch.float32:
+        ok = h2.stride(-1) == 1 and h2.stride(0) % 4 == 0 and h2.data_ptr() % 16 == 0
+        hb = h2.to(torch.bfloat16).contiguous()  # the matmul operand, bf16(h) as the reference's h.to(bfloat16)
+        return hb, (h2 if ok else h2.contiguous()), 1, h2.shape[0], lead
+    raise TypeError(f"h must be bfloat16 or float32, got {h2.dtype}")
+
+
+def _lm_common(h, tok, out, M, lead, V):
+    if tok.shape != lead:
+        raise ValueError(f"tok shape {tuple(tok.shape)} != h's leading shape {tuple(lead)}")
+    t32 = tok.reshape(-1).to(torch.int32).contiguous()
+    if out is None:
+        out = torch.empty(M, dtype=torch.float32, device=h.device)
+    elif out.dtype != torch.float32 or out.numel() != M or not out.is_contiguous():
+        raise ValueError("out must be fp32 contiguous with one element per row")
+    n = ctypes.c_int64()
+    check(lib().od_lm_head_logprob_ws(M, V, ctypes.byref(n)), "od_lm_head_logprob_ws")
+    ws = torch.empty(max(n.value, 1), dtype=torch.float32, device=h.device)
+    return t32, out, ws
+
+
+def _table_rows(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 and t.stride(0) % 16 == 0 and t.data_ptr() % 16 == 0 else t.contiguous()
+
+
 def lm_head_logprob(h: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor, tok: torch.Tensor,
                     out: torch.Tensor | None = None) -> torch.Tensor:
     """log softmax(h @ W^T)[tok] for the int8 table W = qweight (V, K) with per-row scales `scale` (V,) or (V, 1)
@@ -416,33 +450,31 @@ def lm_head_logprob(h: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
     sc = _lib.bf16_bits(scale).reshape(-1).contiguous()
     if sc.numel() != V:
         raise ValueError(f"scale has {sc.numel()} elements, expected {V}")
-    if h.shape[-1] != K:
-        raise ValueError(f"h has {h.shape[-1]} features, the table {K}")
-    lead = h.shape[:-1]
-    h2 = h.reshape(-1, K)
-    M = h2.shape[0]
-    if tok.shape != lead:
-        raise ValueError(f"tok shape {tuple(tok.shape)} != h's leading shape {tuple(lead)}")
-    if h2.dtype == torch.bfloat16:
-        hb = _rows_aligned(h2)
-        hn, hn_fp32 = hb, 0
-    elif h2.dtype == torch.float32:
-        ok = h2.stride(-1) == 1 and h2.stride(0) % 4 == 0 and h2.data_ptr() % 16 == 0
-        hn, hn_fp32 = (h2 if ok else h2.contiguous()), 1
-        hb = h2.to(torch.bfloat16).contiguous()  # the matmul operand, bf16(h) as the reference's h.to(bfloat16)
-    else:
-        raise TypeError(f"h must be bfloat16 or float32, got {h2.dtype}")
-    w = qweight if qweight.stride(-1) == 1 and qweight.stride(0) % 16 == 0 and qweight.data_ptr() % 16 == 0 \
-        else qweight.contiguous()
-    t32 = tok.reshape(-1).to(torch.int32).contiguous()
-    if out is None:
-        out = torch.empty(M, dtype=torch.float32, device=h.device)
-    elif out.dtype != torch.float32 or out.numel() != M or not out.is_contiguous():
-        raise ValueError("out must be fp32 contiguous with one element per row")
-    n = ctypes.c_int64()
-    check(lib().od_lm_head_logprob_ws(M, V, ctypes.byref(n)), "od_lm_head_logprob_ws")
-    ws = torch.empty(max(n.value, 1), dtype=torch.float32, device=h.device)
+    hb, hn, hn_fp32, M, lead = _lm_h_operands(h, K)
+    t32, out, ws = _lm_common(h, tok, out, M, lead, V)
+    w = _table_rows(qweight)
     check(lib().od_lm_head_logprob(ptr(hb), hb.stride(0), ptr(hn), hn.stride(0), hn_fp32, ptr(w), w.stride(0),
                                    ptr(sc), ptr(t32), M, V, K, ptr(out), ptr(ws), ws.numel(), stream_of(h)),
           "od_lm_head_logprob")
+    return out.view(lead)
+
+
+def lm_head_logprob_q4(h: torch.Tensor, qs: torch.Tensor, d: torch.Tensor, tok: torch.Tensor,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """lm_head_logprob over a Q4_0 table (Q4Table, quant.py:206-246): qs uint8 (V, K / 2) packed nibbles, d fp16
+    (V, K / 32) block scales."""
+    require_gpu(h, qs, d, tok, out, name="lm_head_logprob_q4")
+    if qs.dtype != torch.uint8 or qs.dim() != 2 or d.dtype != torch.float16 or d.dim() != 2:
+        raise TypeError("a Q4 table is qs uint8 (V, K/2) and d float16 (V, K/32)")
+    V, K = qs.shape[0], qs.shape[1] * 2
+    if d.shape != (V, K // 32):
+        raise ValueError(f"d has shape {tuple(d.shape)}, expected {(V, K // 32)}")
+    hb, hn, hn_fp32, M, lead = _lm_h_operands(h, K)
+    t32, out, ws = _lm_common(h, tok, out, M, lead, V)
+    q = _table_rows(qs)
+    dd = d if d.stride(-1) == 1 else d.contiguous()
+    check(lib().od_lm_head_logprob_q4(ptr(hb), hb.stride(0), ptr(hn), hn.stride(0), hn_fp32, ptr(q), q.stride(0),
+                                      ptr(dd), dd.stride(0), ptr(t32), M, V, K, ptr(out), ptr(ws), ws.numel(),
+                                      stream_of(h)),
+          "od_lm_head_logprob_q4")
     return out.view(lead)

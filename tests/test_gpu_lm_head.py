@@ -98,3 +98,67 @@ def test_module_api_and_full_vocab_rows(gpu_lib):
     q, s = table.qweight.cpu(), table.scale.cpu().reshape(-1)
     want = _oracle(h.cpu(), q, s, tok.cpu())
     assert (got - want).abs().max().item() <= 1e-3, (got, want)
+
+
+# ---- Q4_0 tables (od_lm_head_logprob_q4)
+
+def _q4_case(M, V, K, seed, h_dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(V, K, generator=g) * 0.05
+    qs, d = ol.q4_table(w)
+    h = (torch.randn(M, K, generator=g) * 2.0).to(h_dtype)
+    tok = torch.randint(0, V, (M,), generator=g)
+    return h, qs, d, tok
+
+
+def _q4_gpu(h, qs, d, tok):
+    from opendecider_amd import kernels
+    return kernels.lm_head_logprob_q4(h.to(DEV), qs.to(DEV), d.to(DEV), tok.to(DEV)).cpu()
+
+
+def _q4_oracle(h, qs, d, tok):
+    return ol.token_logprob(h, lambda idx, dt: ol.q4_rows(qs, d, idx, dt), qs.shape[0], tok)
+
+
+@pytest.mark.parametrize("M,V,K,h_dtype", [(37, 10007, 256, torch.bfloat16), (300, 4429, 128, torch.float32),
+                                           (513, 2304, 192, torch.bfloat16)])
+def test_q4_logprob_matches_oracle(gpu_lib, M, V, K, h_dtype):
+    print(f"lm head q4 M={M} V={V} K={K} {h_dtype}", flush=True)
+    h, qs, d, tok = _q4_case(M, V, K, M + V + 1, h_dtype)
+    got, want = _q4_gpu(h, qs, d, tok), _q4_oracle(h, qs, d, tok)
+    assert (got - want).abs().max().item() <= 1e-3
+    pg, pw = got.double().exp(), want.double().exp()
+    assert ((pg - pw).abs() <= torch.maximum(2e-3 * pw, torch.full_like(pw, 1e-4))).all()
+
+
+def test_q4_one_hot_closed_form(gpu_lib):
+    """One-hot h over a Q4 table whose block scales are powers of two (entries exact in bf16 and fp16): the float64
+    log_softmax of a table column, at both nibble halves of a block."""
+    g = torch.Generator().manual_seed(8)
+    V, K = 900, 64
+    qv = torch.randint(0, 16, (V, K // 32, 32), generator=g)
+    qv[..., 3] = 0
+    dd = torch.exp2(torch.randint(-10, -3, (V, K // 32, 1), generator=g).float())
+    w = ((qv - 8).float() * dd).view(V, K)
+    qs, d = ol.q4_table(w)
+    ks = [0, 15, 16, 31, 40, 63]
+    h = torch.zeros(len(ks), K, dtype=torch.bfloat16)
+    for i, k in enumerate(ks):
+        h[i, k] = 1.0
+    tok = torch.tensor([0, 450, 899, 1, 2, 3])
+    got = _q4_gpu(h, qs, d, tok).double()
+    want = torch.stack([torch.log_softmax(w[:, k].double(), 0)[t] for k, t in zip(ks, tok.tolist())])
+    assert torch.allclose(got, want, atol=5e-6), (got - want).abs().max()
+
+
+def test_q4_module_api(gpu_lib):
+    """Q4Table + token_logprob equals the kernel wrapper, and Q4Table's bytes are the oracle's."""
+    from opendecider_amd import Q4Table, token_logprob
+    g = torch.Generator().manual_seed(12)
+    w = torch.randn(3000, 256, generator=g) * 0.05
+    t = Q4Table(w.to(DEV))
+    qs, d = ol.q4_table(w)
+    assert torch.equal(t.qs.cpu(), qs) and torch.equal(t.d.cpu(), d)
+    h = torch.randn(20, 256, generator=g).to(torch.bfloat16)
+    tok = torch.randint(0, 3000, (20,), generator=g)
+    assert torch.equal(token_logprob(t, h.to(DEV), tok.to(DEV)).cpu(), _q4_gpu(h, qs, d, tok))
