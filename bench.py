@@ -494,7 +494,8 @@ def run_lm_logprob(args):
     vocabulary table: 151936 rows x 4096 (Int8Table of random N(0, 0.03) rows, bf16 scales), 1024 rows of bf16 h
     N(0, 2) (16 options x 64 tokens) with random target tokens. One call = od_lm_head_logprob (the bf16-MFMA logit
     tiles with the table dequantized on the fly and the log-sum-exp in their epilogue, then the per-row combine);
-    HIP events around the timed calls. CPU baseline: the oracle on 2 rows over the whole vocabulary."""
+    HIP events around the timed calls. The same rows against the table re-quantized as Q4_0 are reported beside
+    (od_lm_head_logprob_q4). CPU baseline: the oracle on 2 rows over the whole vocabulary."""
     import torch
 
     from opendecider_amd import Int8Table, token_logprob
@@ -533,6 +534,22 @@ def run_lm_logprob(args):
                         "algorithmic_bytes": table_bytes + M * K * 2 + M * 8,
                         "note": "2 x rows x vocabulary x hidden FLOP per call over the call's duration (HIP events)",
                         "avg_launch_us": ms * 1e3}}
+    # the same rows against the same table held as Q4_0 (4.5 bits per value)
+    from opendecider_amd import Q4Table
+    t4 = Q4Table(table.weight)
+    for _ in range(args.warmup):
+        token_logprob(t4, h, tok)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(args.steps):
+        out4 = token_logprob(t4, h, tok)
+    e.record()
+    torch.cuda.synchronize()
+    ms4 = s.elapsed_time(e) / args.steps
+    assert torch.isfinite(out4).all()
+    res["q4_table"] = {"ms_per_call": ms4, "rows_per_s": M / (ms4 * 1e-3), "tflops": flops / (ms4 * 1e-3) / 1e12,
+                       "frac_of_bf16_mfma": flops / (ms4 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+    del t4
     if not args.no_cpu_baseline:
         from oracle import lm_head as ol
         torch.set_num_threads(os.cpu_count() or 1)
