@@ -162,3 +162,20 @@ def test_q4_module_api(gpu_lib):
     h = torch.randn(20, 256, generator=g).to(torch.bfloat16)
     tok = torch.randint(0, 3000, (20,), generator=g)
     assert torch.equal(token_logprob(t, h.to(DEV), tok.to(DEV)).cpu(), _q4_gpu(h, qs, d, tok))
+
+
+def test_leading_dims_and_empty_rows(gpu_lib):
+    """h (..., K) and tok (...) give log-probs of shape (...), the rows of a flattened call; zero rows give an empty
+    result without a launch (both table formats)."""
+    from opendecider_amd import kernels
+    h, q, s, tok = _case(12, 3000, 128, 21)
+    flat = _gpu(h, q, s, tok)
+    got = kernels.lm_head_logprob(h.view(3, 4, 128).to(DEV), q.to(DEV), s.to(DEV), tok.view(3, 4).to(DEV)).cpu()
+    assert got.shape == (3, 4) and torch.equal(got.reshape(-1), flat)
+    e = kernels.lm_head_logprob(h[:0].to(DEV), q.to(DEV), s.to(DEV), tok[:0].to(DEV))
+    assert e.shape == (0,)
+    qs, d = ol.q4_table(q.float() * s.float()[:, None])
+    e4 = kernels.lm_head_logprob_q4(h[:0].to(DEV), qs.to(DEV), d.to(DEV), tok[:0].to(DEV))
+    assert e4.shape == (0,)
+    g4 = kernels.lm_head_logprob_q4(h.view(2, 6, 128).to(DEV), qs.to(DEV), d.to(DEV), tok.view(2, 6).to(DEV)).cpu()
+    assert torch.equal(g4.reshape(-1), _q4_gpu(h, qs, d, tok))
