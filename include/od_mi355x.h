@@ -30,6 +30,10 @@ typedef void* od_stream_t;
 #define OD_ERR_UNSUPPORTED (-4) /* head dim / GQA ratio / row length outside what the kernels are built for */
 #define OD_ERR_LAUNCH (-5)      /* the kernel launch failed (hipGetLastError) */
 
+/* How the branched attention turns the int8 state into K/V (the `dequant` argument). */
+#define OD_DEQUANT_BF16 0 /* the reference's materialize: q.to(bf16) * s.to(bf16), one bf16 rounding per value */
+#define OD_DEQUANT_FP32 1 /* the exact q * s (the K scale folded into the scores, V' rounded once to fp16) */
+
 /* Text for an OD_* code. */
 const char* od_strerror(int code);
 
@@ -149,7 +153,8 @@ int od_lm_head_logprob_q4(const uint16_t* hb, int64_t ldh, const void* hn, int64
  * (src/opendecider/wide_attention.py:70-91) and the torch LSE merge (prefix_attn.py:74-76), the per-state loop
  * of _forward (prefix_attn.py:118-128), and the per-layer dequantized copy of the state K/V
  * (prefix_attn.py:145-149): the int8 state is read directly; every workgroup converts each 64-key block in its own
- * LDS (keys to exact bf16 with their scales applied to the scores, values to fp16 with the scales folded in).
+ * LDS, dequantized as `dequant` says: OD_DEQUANT_BF16, the reference's materialize (quant.py:45; keys and values
+ * bf16(q * bf16(s)), one rounding each), or OD_DEQUANT_FP32, the exact q * s.
  *   q         bf16 [R, Hq, t, D], element strides (sqr, sqh, sqt)        R option rows of t tokens
  *   k_own     bf16 [R, Hkv, t, D], strides (skr, skh, skt)                each row's own keys (causal)
  *   v_own     bf16 [R, Hkv, t, D], strides (svr, svh, svt)
@@ -161,6 +166,7 @@ int od_lm_head_logprob_q4(const uint16_t* hb, int64_t ldh, const void* hn, int64
  *   max_rows  the largest row_start[s+1] - row_start[s] (sizes the grid; must be exact or an upper bound)
  *   out       bf16 [R, Hq, t, D], strides (sor, soh, sot) (out)
  *   lse       fp32 [R, Hq, t] contiguous or NULL (out): natural-log LSE of the merged scaled scores
+ *   dequant   OD_DEQUANT_BF16 or OD_DEQUANT_FP32 (else OD_ERR_UNSUPPORTED)
  * Query head h reads KV head h / (Hq / Hkv). Every query sees every valid prefix key and its own row's keys
  * 0..i (causal). A query with no visible key would return 0 (never happens: its own key is visible).
  * Supports D in {64, 128}, Hq % Hkv == 0, 1 <= t <= 256, T <= cap.
@@ -172,7 +178,7 @@ int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
                      const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
                      uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
                      int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, int64_t cap,
-                     float scale, od_stream_t stream);
+                     float scale, int dequant, od_stream_t stream);
 
 /*
  * od_branched_attn_split — od_branched_attn with the state's keys split into nsplit contiguous ranges processed by
@@ -191,7 +197,7 @@ int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t 
                            const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
                            uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
                            int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
-                           int64_t cap, float scale, int64_t nsplit, float* ws, int64_t ws_floats,
+                           int64_t cap, float scale, int dequant, int64_t nsplit, float* ws, int64_t ws_floats,
                            od_stream_t stream);
 
 /*
@@ -204,25 +210,27 @@ int od_attn_stage_size(int64_t Ns, int64_t Hkv, int64_t T, int64_t D, int64_t* i
 /*
  * od_attn_stage — converts an int8 state into attention block images, once for all the workgroups that read it.
  * Replaces: the per-layer dequantized copy of the state K/V (prefix_attn.py:145-149, quant.py:40-47
- * materialize), in the form od_branched_attn_staged consumes: per (state, head, 64-key block) the keys as exact
- * bf16 integers with their fp32 score multipliers (K scale times the softmax scale), the values in fp16 with the
- * per-key scales folded in (one rounding per value), both swizzled for the LDS fragment reads, a -inf row for masked
- * keys and the block's V exponent.
- *   kq, vq, ks, vs, kvalid, Ns, Hkv, T, cap, D   as od_branched_attn
+ * materialize), in the form od_branched_attn_staged consumes: per (state, head, 64-key block) the keys in bf16
+ * with their fp32 score multipliers, the values in fp16 times a power of two, both swizzled for the LDS fragment
+ * reads, a -inf row for masked keys and the block's V exponent. With OD_DEQUANT_BF16 the keys and values are the
+ * reference's materialized bf16(q * bf16(s)) and the multiplier is the softmax scale; with OD_DEQUANT_FP32 the keys
+ * are the int8 values, the multiplier is the K scale times the softmax scale, and the values are fp16(q * s).
+ *   kq, vq, ks, vs, kvalid, Ns, Hkv, T, cap, D, dequant   as od_branched_attn
  *   scale      the softmax scale of the attention calls that will read the images
  *   img        device buffer of at least od_attn_stage_size bytes, 16-byte aligned (out)
  * One launch on `stream`. The images equal what od_branched_attn builds in LDS, so od_branched_attn_staged over
  * them returns the same bits as od_branched_attn.
  */
 int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq, const float* vs, const uint8_t* kvalid,
-                  int64_t Ns, int64_t Hkv, int64_t T, int64_t cap, int64_t D, float scale, void* img,
-                  int64_t img_bytes, od_stream_t stream);
+                  int64_t Ns, int64_t Hkv, int64_t T, int64_t cap, int64_t D, float scale, int dequant,
+                  void* img, int64_t img_bytes, od_stream_t stream);
 
 /*
  * od_branched_attn_staged — od_branched_attn_split over block images from od_attn_stage: each workgroup copies the
  * images straight into LDS (global_load_lds) instead of converting the int8 state itself.
  * Replaces: the same reference code as od_branched_attn.
- *   img, img_bytes   the images of the state (Ns, Hkv, T, D and scale as passed to od_attn_stage)
+ *   img, img_bytes   the images of the state (Ns, Hkv, T, D and scale as passed to od_attn_stage; the images carry
+ *                    the dequantization)
  *   nsplit, ws, ws_floats   as od_branched_attn_split (nsplit = 1 ignores ws)
  * Other arguments and the result as od_branched_attn.
  */
@@ -254,6 +262,23 @@ int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const
                  const uint8_t* kvalid, int64_t smb, uint16_t* out, int64_t sob, int64_t soh, int64_t sot, float* lse,
                  int64_t B, int64_t H, int64_t G, int64_t T, int64_t S, int64_t DK, int64_t DV, int causal,
                  float scale, od_stream_t stream);
+
+/*
+ * od_lse_merge — merge two attention partials by their log-sum-exp.
+ * Replaces: the merge of _split_attention's prefix and own parts (src/opendecider/prefix_attn.py:74-76), used when
+ * the prefix arrives as dense bf16 K/V (the reference's _forward passes materialized K/V, prefix_attn.py:127,145-149)
+ * and the two parts come from od_wide_attn.
+ *   o1, o2  bf16 [n, H, t, D] at element strides (s1r, s1h, s1t) / (s2r, s2h, s2t), last dim contiguous
+ *   l1, l2  fp32 [n, H, t] at element strides (t1r, t1h, t1t) / (t2r, t2h, t2t): natural-log LSE of each part
+ *   out     bf16 [n, H, t, D], strides (sor, soh, sot) (out); lse fp32 [n, H, t] contiguous or NULL (out)
+ *   m = max(l1, l2), w_i = exp(l_i - m), out = bf16((float(o1) w1 + float(o2) w2) / (w1 + w2)), lse = m + log(w1 + w2);
+ *   a slot with both parts empty (-inf) gets 0 and -inf. Requires D % 8 == 0, bf16 strides multiples of 8 and
+ *   16-byte aligned o1 / o2 / out.
+ */
+int od_lse_merge(const uint16_t* o1, int64_t s1r, int64_t s1h, int64_t s1t, const float* l1, int64_t t1r, int64_t t1h,
+                 int64_t t1t, const uint16_t* o2, int64_t s2r, int64_t s2h, int64_t s2t, const float* l2, int64_t t2r,
+                 int64_t t2h, int64_t t2t, uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t n,
+                 int64_t H, int64_t t, int64_t D, od_stream_t stream);
 
 /*
  * Row kernels of the dense decoder layer that carries the path in the decision-forward harness (not reference

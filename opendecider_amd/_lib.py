@@ -11,7 +11,7 @@ import os
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libod_mi355x.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_ptr = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -26,14 +26,14 @@ SIGNATURES = {
     "od_kv_quant_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _i64, _i64, _c_ptr],
     "od_branched_attn": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
                          _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr,
-                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _c_ptr],
+                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _c_ptr],
     "od_branched_attn_split": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
                                _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64,
-                               _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _c_ptr,
-                               _i64, _c_ptr],
+                               _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _i64,
+                               _c_ptr, _i64, _c_ptr],
     "od_attn_stage_size": [_i64, _i64, _i64, _i64, _c_ptr],
-    "od_attn_stage": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _c_ptr,
-                      _i64, _c_ptr],
+    "od_attn_stage": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
+                      ctypes.c_int, _c_ptr, _i64, _c_ptr],
     "od_branched_attn_staged": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
                                 _c_ptr, _i64, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64,
                                 _i64, _i64, _i64, ctypes.c_float, _i64, _c_ptr, _i64, _c_ptr],
@@ -49,6 +49,8 @@ SIGNATURES = {
                         _i64, _c_ptr],
     "od_qk_norm_rope_kv_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64,
                                   _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _c_ptr],
+    "od_lse_merge": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64,
+                     _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64, _c_ptr],
     "od_lm_head_logprob_ws": [_i64, _i64, _c_ptr],
     "od_lm_head_logprob": [_c_ptr, _i64, _c_ptr, _i64, ctypes.c_int, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64,
                            _c_ptr, _c_ptr, _i64, _c_ptr],
@@ -75,6 +77,16 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(f"{LIB_PATH}: ABI version {L.od_abi_version()} != {ABI_VERSION}; rebuild it")
         _LIB = L
     return _LIB
+
+
+# od_branched_attn / od_attn_stage dequantization of the int8 state (include/od_mi355x.h)
+DEQUANT = {"bf16": 0, "fp32": 1}
+
+
+def dequant_code(mode: str) -> int:
+    if mode not in DEQUANT:
+        raise ValueError(f"dequant must be one of {sorted(DEQUANT)}, got {mode!r}")
+    return DEQUANT[mode]
 
 
 def check(rc: int, name: str) -> None:

@@ -28,13 +28,18 @@
 // swapped).
 //
 // Numerics (fp32 accumulation; the roundings noted are the only others):
-//  * queries are used as they are (bf16); a state key's int8 values are exact bf16 integers, so the MFMA products
-//    are exact, and the score of key j is raw_j * gk_j with gk_j = ks_j scale log2(e) (one rounding in gk_j, one in
-//    the product): the scores see the exact dequantized keys;
-//  * the row's own bf16 keys are used as they are, with the multiplier scale log2(e);
-//  * a state value becomes V' = fp16(q vs_j 2^-eb), one rounding, with the block's V exponent eb; the accumulator
-//    carries one power-of-two frame, moved lazily (a state block in a frame up to kFrameSlack below it enters with
-//    its probabilities times 2^(eb - frame), exact while those stay normal fp16);
+//  * the state's int8 K/V are dequantized in one of two ways (the `dq` argument):
+//    - OD_DEQUANT_BF16, the reference's materialize (quant.py:45, prefix_attn.py:145-149): K' = bf16(q bf16(ks_j))
+//      and V' = bf16(q bf16(vs_j)), each product rounded once to bf16. K' goes to the score MFMAs as it is (the
+//      bf16 products with the queries are exact) and the score of key j is raw_j * scale log2(e); V' (8 significant
+//      bits) is stored as fp16 V' 2^-eb, exact;
+//    - OD_DEQUANT_FP32, the exact q * s: a state key's int8 values are exact bf16 integers and the score of key j
+//      is raw_j * gk_j with gk_j = ks_j scale log2(e) (one rounding in gk_j, one in the product); a state value
+//      becomes fp16(q vs_j 2^-eb), one rounding;
+//    eb is the block's V exponent; the accumulator carries one power-of-two frame, moved lazily (a state block in
+//    a frame up to kFrameSlack below it enters with its probabilities times 2^(eb - frame), exact while those stay
+//    normal fp16);
+//  * queries are used as they are (bf16), and so are the row's own bf16 keys, with the multiplier scale log2(e);
 //  * the row's own bf16 values get one power-of-two factor per 32-key block and are converted to fp16;
 //  * probabilities p = exp2(y) <= 2^8 are rounded to fp16 for the P.V product; their sum is taken unrounded.
 // Masked keys get a -inf score; a block with no visible key is an exact no-op for a slot; every row's arithmetic is
@@ -78,6 +83,7 @@ struct AttnArgs {
   int64_t sqr, sqh, sqt, skr, skh, skt, svr, svh, svt, sor, soh, sot;
   int R, Hq, Hkv, t, Ns, T, cap, rep;
   float scale_log2;
+  int dq;       // OD_DEQUANT_BF16 or OD_DEQUANT_FP32 (the int8 path; staged images carry their own)
   int nsplit;   // key-range splits (1: one pass writes out/lse)
   float* part;  // nsplit > 1: fp32 partials, o [nsplit][R][Hq][t][D] then lse [nsplit][R][Hq][t]
   const uint8_t* img;  // staged block images [Ns][Hkv][nb] (null: convert the int8 state in the kernel)
@@ -88,9 +94,9 @@ struct AttnArgs {
 // instructions (without the alignment the compiler splits them into 4-byte pairs).
 template <int D>
 struct alignas(16) BlockImg {
-  alignas(16) uint16_t k[kBlockKeys * D];   // [key][d] int8 keys as exact bf16, 16-byte chunks swizzled (k_off)
+  alignas(16) uint16_t k[kBlockKeys * D];   // [key][d] bf16 keys (K', or the int8 values), chunks swizzled (k_off)
   alignas(16) _Float16 vt[D * kBlockKeys];  // [d][permuted key] V', swizzled (vt_off)
-  alignas(16) float gk[kBlockKeys];         // the score multiplier of key j: ks_j scale log2(e) (1 if masked)
+  alignas(16) float gk[kBlockKeys];         // score multiplier of key j: scale log2(e) [* ks_j] (1 if masked)
   alignas(16) float kb[kBlockKeys];         // 0, or -inf for a masked key
   alignas(16) int info[4];                  // the block constants: 0, eb, masked, 0
 };
@@ -173,6 +179,28 @@ __device__ __forceinline__ uint32_t h2_times(uint32_t h, float f0, float f1) {
   return bits_h2(r);
 }
 
+// bf16 materialize of 4 int8 key values (one dword) with the key's bf16 scale sb: bf16(q * sb) per value (the
+// fp32 product of a 7-bit integer and an 8-bit significand is exact; one rounding to bf16)
+__device__ __forceinline__ void i8x4_times_bf16(uint32_t w, float sb, uint32_t& lo, uint32_t& hi) {
+  const float f0 = (float)(int8_t)(w & 0xffu) * sb, f1 = (float)(int8_t)((w >> 8) & 0xffu) * sb;
+  const float f2 = (float)(int8_t)((w >> 16) & 0xffu) * sb, f3 = (float)(int8_t)(w >> 24) * sb;
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((od_f32x2){f0, f1}, od_bf16x2));
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((od_f32x2){f2, f3}, od_bf16x2));
+}
+
+// an exact fp16 pair of int8 values times two fp32 factors f = bf16(vs) 2^-eb (exact), each product rounded once to
+// bf16 precision (the reference's bf16 product; the power of two does not change the rounding) and stored as fp16,
+// which holds the 8 significant bits exactly (v_cvt_pkrtz_f16_f32 on an exactly representable value is exact)
+__device__ __forceinline__ uint32_t h2_times_bf16(uint32_t h, float f0, float f1) {
+  const half2v a = h2_bits(h);
+  const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                                      (od_f32x2){(float)a.x * f0, (float)a.y * f1}, od_bf16x2));
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(p << 16), __uint_as_float(p & 0xffff0000u)));
+}
+
+// bf16 rounding of an fp32 scale, as an fp32 value
+__device__ __forceinline__ float bf16_round(float f) { return od_bf16_to_f32(od_f32_to_bf16(f)); }
+
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   half2v h = {(_Float16)a, (_Float16)b};
   return bits_h2(h);
@@ -245,15 +273,20 @@ __device__ __forceinline__ void prefix_load(const PrefixSrc& src, int T, int j0,
 }
 
 // Converts a loaded int8 block into its image `dst` (LDS, or memory for od_attn_stage) and returns the block
-// constants. K: the int8 values as exact bf16 and beside them the score multipliers gk_j = ks_j scale_log2 (the
-// K scale times the softmax scale in log2 units, one fp32 rounding). V' = fp16(q fv_j), one rounding
-// (v_fma_mix), with the fp32 factor fv_j = vs_j 2^-eb (exact); 2^eb lies above the block's largest V scale, so
-// |V'| < 128. (Rounding fv_j to fp16 first would shift all of key j's values the same way, which under cancellation
-// is visible in the output.) A masked key gets a zero V factor (P V' must stay finite), a -inf bias (added to its
-// raw score) and the multiplier 1 (so the score stays -inf). Every wave derives the constants from the same 64
-// scales, so the waves agree without exchanging them.
+// constants.
+//  * dq = OD_DEQUANT_BF16: K' = bf16(q bf16(ks_j)) beside the multiplier scale_log2 (the softmax scale in log2
+//    units); V' = bf16(q bf16(vs_j)) 2^-eb in fp16 (exact: 8 significant bits, |V'| < 128).
+//  * dq = OD_DEQUANT_FP32: the int8 values as exact bf16 beside the multipliers gk_j = ks_j scale_log2 (one fp32
+//    rounding); V' = fp16(q fv_j), one rounding (v_fma_mix), with the fp32 factor fv_j = vs_j 2^-eb (exact).
+//    (Rounding fv_j to fp16 first would shift all of key j's values the same way, which under cancellation is
+//    visible in the output.)
+// 2^eb lies above the block's largest V scale. A masked key gets a zero V factor (P V' must stay finite), a -inf
+// bias (added to its raw score) and the multiplier 1 (so the score stays -inf). Every wave derives the constants
+// from the same 64 scales, so the waves agree without exchanging them.
 template <int D>
-__device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, BlockImg<D>& dst, float scale_log2) {
+__device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, BlockImg<D>& dst, float scale_log2,
+                                                   int dq) {
+  const bool mat = dq == OD_DEQUANT_BF16;
   const int tid = threadIdx.x;
   const bool ok = r.in_range && r.valid != 0;
   const float vs_ok = ok ? r.vs : 0.0f;
@@ -262,7 +295,8 @@ __device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, Block
   bi.ek = 0;
   const float vmax = od_wave_max_dpp(vs_ok);
   bi.eb = __builtin_amdgcn_ballot_w64(ok) != 0 ? exp_above(vmax) : kNoFrame;
-  const float fv = ok ? ldexpf(vs_ok, -bi.eb) : 0.0f;  // lane l: key l's V factor
+  const float fv = ok ? ldexpf(mat ? bf16_round(vs_ok) : vs_ok, -bi.eb) : 0.0f;  // lane l: key l's V factor
+  const float ksb = bf16_round(r.ks);  // lane l: key l's bf16 K scale (materialize)
 
   constexpr int kChunks = kBlockKeys * D / 16;
   constexpr int kCpk = D / 16;
@@ -277,10 +311,18 @@ __device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, Block
       const uint32_t a0 = flip ? r.k[i].z : r.k[i].x, a1 = flip ? r.k[i].w : r.k[i].y;
       const uint32_t b0 = flip ? r.k[i].x : r.k[i].z, b1 = flip ? r.k[i].y : r.k[i].w;
       uint4 h0, h1;
-      i8x4_to_bf16(a0, h0.x, h0.y);
-      i8x4_to_bf16(a1, h0.z, h0.w);
-      i8x4_to_bf16(b0, h1.x, h1.y);
-      i8x4_to_bf16(b1, h1.z, h1.w);
+      if (mat) {
+        const float sb = __shfl(ksb, key, 64);
+        i8x4_times_bf16(a0, sb, h0.x, h0.y);
+        i8x4_times_bf16(a1, sb, h0.z, h0.w);
+        i8x4_times_bf16(b0, sb, h1.x, h1.y);
+        i8x4_times_bf16(b1, sb, h1.z, h1.w);
+      } else {
+        i8x4_to_bf16(a0, h0.x, h0.y);
+        i8x4_to_bf16(a1, h0.z, h0.w);
+        i8x4_to_bf16(b0, h1.x, h1.y);
+        i8x4_to_bf16(b1, h1.z, h1.w);
+      }
       *reinterpret_cast<uint4*>(&dst.k[k_off<D>(key, 2 * c + flip)]) = h0;
       *reinterpret_cast<uint4*>(&dst.k[k_off<D>(key, 2 * c + 1 - flip)]) = h1;
     }
@@ -312,13 +354,18 @@ __device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, Block
       const int d = 8 * dg + e;
       uint2 hv;
       i8x4_to_h(cols[e], hv.x, hv.y);
-      hv.x = h2_times(hv.x, f0, f1);
-      hv.y = h2_times(hv.y, f2, f3);
+      if (mat) {
+        hv.x = h2_times_bf16(hv.x, f0, f1);
+        hv.y = h2_times_bf16(hv.y, f2, f3);
+      } else {
+        hv.x = h2_times(hv.x, f0, f1);
+        hv.y = h2_times(hv.y, f2, f3);
+      }
       *reinterpret_cast<uint2*>(&dst.vt[vt_off(d, jj0 >> 3) + (jj0 & 7)]) = hv;
     }
   }
   if (tid < kBlockKeys) {
-    dst.gk[tid] = ok ? r.ks * scale_log2 : 1.0f;
+    dst.gk[tid] = ok ? (mat ? scale_log2 : r.ks * scale_log2) : 1.0f;
     dst.kb[tid] = ok ? 0.0f : -INFINITY;
   }
   if (tid == 0) *reinterpret_cast<int4*>(dst.info) = make_int4(bi.ek, bi.eb, bi.masked, 0);
@@ -881,7 +928,7 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
       const PrefixSrc src = prefix_src<D>(p.kq, p.ks, p.vq, p.vs, p.kvalid, p.Hkv, p.T, p.cap, s, g);
       PrefixRegs<D> pr;
       prefix_load<D>(src, p.T, b_lo * kBlockKeys, pr);
-      BlockInfo cur = convert_block<D>(pr, sm.b[0], p.scale_log2);
+      BlockInfo cur = convert_block<D>(pr, sm.b[0], p.scale_log2, p.dq);
       __syncthreads();
       for (int b = b_lo; b < b_hi; ++b) {
         const int buf = (b - b_lo) & 1;
@@ -891,7 +938,7 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
                                     if (b + 1 < b_hi) prefix_load<D>(src, p.T, (b + 1) * kBlockKeys, pr);
                                   });
         BlockInfo nxt = cur;
-        if (b + 1 < b_hi) nxt = convert_block<D>(pr, sm.b[buf ^ 1], p.scale_log2);
+        if (b + 1 < b_hi) nxt = convert_block<D>(pr, sm.b[buf ^ 1], p.scale_log2, p.dq);
         __syncthreads();
         cur = nxt;
       }
@@ -973,6 +1020,7 @@ struct StageArgs {
   uint8_t* img;
   int Hkv, T, cap, nb;
   float scale_log2;
+  int dq;
 };
 
 template <int D>
@@ -982,7 +1030,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(StageArgs p) {
   PrefixRegs<D> pr;
   prefix_load<D>(src, p.T, b * kBlockKeys, pr);
   const int64_t blk = ((int64_t)s * p.Hkv + g) * p.nb + b;
-  convert_block<D>(pr, reinterpret_cast<BlockImg<D>*>(p.img)[blk], p.scale_log2);
+  convert_block<D>(pr, reinterpret_cast<BlockImg<D>*>(p.img)[blk], p.scale_log2, p.dq);
 }
 
 // LSE merge of the key-range splits (prefix_attn.py:74-76 generalised to n parts): M = max_s lse_s,
@@ -1029,6 +1077,54 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
   if (p.lse && d0 == 0) p.lse[slot] = wsum > 0.0f ? M + __logf(wsum) : -INFINITY;
 }
 
+// Merge of two attention partials by their log-sum-exp (prefix_attn.py:74-76): m = max(l1, l2),
+// w_i = exp(l_i - m), out = bf16((o1 w1 + o2 w2) / (w1 + w2)) from the bf16 partials read as fp32, lse = m +
+// log(w1 + w2); both parts empty (m = -inf) -> 0 and -inf. One thread per (slot, 8 values of d).
+struct MergeArgs {
+  const uint16_t* o1;
+  const float* l1;
+  const uint16_t* o2;
+  const float* l2;
+  uint16_t* out;
+  float* lse;
+  int64_t s1r, s1h, s1t, t1r, t1h, t1t, s2r, s2h, s2t, t2r, t2h, t2t, sor, soh, sot;
+  int64_t n, H, t, D;
+};
+
+__global__ __launch_bounds__(256) void lse_merge_kernel(MergeArgs p) {
+  const int64_t groups = p.D / 8;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t slot = gid / groups;
+  if (slot >= p.n * p.H * p.t) return;
+  const int64_t d0 = (gid % groups) * 8;
+  const int64_t r = slot / (p.H * p.t), h = (slot / p.t) % p.H, i = slot % p.t;
+  const float l1 = p.l1[r * p.t1r + h * p.t1h + i * p.t1t], l2 = p.l2[r * p.t2r + h * p.t2h + i * p.t2t];
+  const float m = fmaxf(l1, l2);
+  float w1 = 0.0f, w2 = 0.0f;
+  if (m != -INFINITY) {
+    w1 = expf(l1 - m);
+    w2 = expf(l2 - m);
+  }
+  const float den = w1 + w2;
+  const uint4 a = *reinterpret_cast<const uint4*>(p.o1 + r * p.s1r + h * p.s1h + i * p.s1t + d0);
+  const uint4 b = *reinterpret_cast<const uint4*>(p.o2 + r * p.s2r + h * p.s2h + i * p.s2t + d0);
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
+  uint32_t res[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float y[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float x1 = __uint_as_float(k ? (aw[e] & 0xffff0000u) : (aw[e] << 16));
+      const float x2 = __uint_as_float(k ? (bw[e] & 0xffff0000u) : (bw[e] << 16));
+      y[k] = den > 0.0f ? (x1 * w1 + x2 * w2) / den : 0.0f;
+    }
+    res[e] = (uint32_t)od_f32_to_bf16(y[0]) | ((uint32_t)od_f32_to_bf16(y[1]) << 16);
+  }
+  *reinterpret_cast<uint4*>(p.out + r * p.sor + h * p.soh + i * p.sot + d0) = make_uint4(res[0], res[1], res[2], res[3]);
+  if (p.lse && d0 == 0) p.lse[slot] = den > 0.0f ? m + logf(den) : -INFINITY;
+}
+
 }  // namespace
 
 namespace {
@@ -1038,9 +1134,10 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
                     const int8_t* kq, const float* ks, const int8_t* vq, const float* vs, const uint8_t* kvalid,
                     const void* img, const int32_t* row_start, int64_t max_rows, uint16_t* out,
                     int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t R, int64_t Hq, int64_t Hkv, int64_t t,
-                    int64_t D, int64_t Ns, int64_t T, int64_t cap, float scale, int64_t nsplit, float* ws,
+                    int64_t D, int64_t Ns, int64_t T, int64_t cap, float scale, int dq, int64_t nsplit, float* ws,
                     int64_t ws_floats, od_stream_t stream) {
   const bool staged = img != nullptr;
+  if (dq != OD_DEQUANT_BF16 && dq != OD_DEQUANT_FP32) return OD_ERR_UNSUPPORTED;
   if (R < 0 || Hq < 1 || Hkv < 1 || t < 1 || Ns < 1 || T < 0 || cap < T || max_rows < 0) return OD_ERR_SHAPE;
   if (Hq % Hkv) return OD_ERR_UNSUPPORTED;
   if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
@@ -1071,7 +1168,8 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
     return OD_ERR_SHAPE;
   AttnArgs a{q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, lse, sqr, sqh, sqt, skr, skh, skt, svr, svh,
              svt, sor, soh, sot, (int)R, (int)Hq, (int)Hkv, (int)t, (int)Ns, (int)T, (int)cap, (int)rep,
-             scale * 1.4426950408889634f, (int)nsplit, nsplit > 1 ? ws : nullptr, static_cast<const uint8_t*>(img)};
+             scale * 1.4426950408889634f, dq, (int)nsplit, nsplit > 1 ? ws : nullptr,
+             static_cast<const uint8_t*>(img)};
   dim3 grid((unsigned)tiles, (unsigned)Hkv, (unsigned)(Ns * nsplit)), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
   if (D == 128) {
@@ -1104,10 +1202,10 @@ extern "C" int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int
                                 const float* vs, const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
                                 uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t R,
                                 int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, int64_t cap,
-                                float scale, od_stream_t stream) {
+                                float scale, int dequant, od_stream_t stream) {
   return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, kq, ks, vq, vs, kvalid,
                          nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale,
-                         1, nullptr, 0, stream);
+                         dequant, 1, nullptr, 0, stream);
 }
 
 extern "C" int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, const uint16_t* k_own,
@@ -1116,11 +1214,11 @@ extern "C" int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sq
                                       const float* vs, const uint8_t* kvalid, const int32_t* row_start,
                                       int64_t max_rows, uint16_t* out, int64_t sor, int64_t soh, int64_t sot,
                                       float* lse, int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns,
-                                      int64_t T, int64_t cap, float scale, int64_t nsplit, float* ws,
+                                      int64_t T, int64_t cap, float scale, int dequant, int64_t nsplit, float* ws,
                                       int64_t ws_floats, od_stream_t stream) {
   return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, kq, ks, vq, vs, kvalid,
                          nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale,
-                         nsplit, ws, ws_floats, stream);
+                         dequant, nsplit, ws, ws_floats, stream);
 }
 
 extern "C" int od_attn_stage_size(int64_t Ns, int64_t Hkv, int64_t T, int64_t D, int64_t* img_bytes) {
@@ -1133,8 +1231,9 @@ extern "C" int od_attn_stage_size(int64_t Ns, int64_t Hkv, int64_t T, int64_t D,
 
 extern "C" int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
                              const uint8_t* kvalid, int64_t Ns, int64_t Hkv, int64_t T, int64_t cap, int64_t D,
-                             float scale, void* img, int64_t img_bytes, od_stream_t stream) {
+                             float scale, int dequant, void* img, int64_t img_bytes, od_stream_t stream) {
   if (Ns < 1 || Hkv < 1 || T < 0 || cap < T) return OD_ERR_SHAPE;
+  if (dequant != OD_DEQUANT_BF16 && dequant != OD_DEQUANT_FP32) return OD_ERR_UNSUPPORTED;
   if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
   if (T == 0) return OD_OK;
   if (!kq || !ks || !vq || !vs || !img) return OD_ERR_NULL;
@@ -1144,7 +1243,7 @@ extern "C" int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq
   if (nb > 0x7fffffff || Hkv > 65535 || Ns > 65535 || T * D >= (1ll << 31) || cap * Hkv * Ns * D > (1ll << 40))
     return OD_ERR_SHAPE;
   StageArgs a{kq, ks, vq, vs, kvalid, static_cast<uint8_t*>(img), (int)Hkv, (int)T, (int)cap, (int)nb,
-              scale * 1.4426950408889634f};
+              scale * 1.4426950408889634f, dequant};
   dim3 grid((unsigned)nb, (unsigned)Hkv, (unsigned)Ns), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
   if (D == 128) {
@@ -1167,5 +1266,30 @@ extern "C" int od_branched_attn_staged(const uint16_t* q, int64_t sqr, int64_t s
     return OD_ERR_SHAPE;
   return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, nullptr, nullptr, nullptr,
                          nullptr, nullptr, T > 0 ? img : nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq,
-                         Hkv, t, D, Ns, T, T, scale, nsplit, ws, ws_floats, stream);
+                         Hkv, t, D, Ns, T, T, scale, OD_DEQUANT_BF16, nsplit, ws, ws_floats, stream);
+}
+
+extern "C" int od_lse_merge(const uint16_t* o1, int64_t s1r, int64_t s1h, int64_t s1t, const float* l1, int64_t t1r,
+                            int64_t t1h, int64_t t1t, const uint16_t* o2, int64_t s2r, int64_t s2h, int64_t s2t,
+                            const float* l2, int64_t t2r, int64_t t2h, int64_t t2t, uint16_t* out, int64_t sor,
+                            int64_t soh, int64_t sot, float* lse, int64_t n, int64_t H, int64_t t, int64_t D,
+                            od_stream_t stream) {
+  if (n < 0 || H < 0 || t < 0 || D < 8 || D % 8) return OD_ERR_SHAPE;
+  if (n == 0 || H == 0 || t == 0) return OD_OK;
+  if (!o1 || !l1 || !o2 || !l2 || !out) return OD_ERR_NULL;
+  const int64_t bstr[] = {s1r, s1h, s1t, s2r, s2h, s2t, sor, soh, sot};
+  for (int64_t v : bstr)
+    if (v < 0 || v % 8) return OD_ERR_ALIGN;
+  const int64_t lstr[] = {t1r, t1h, t1t, t2r, t2h, t2t};
+  for (int64_t v : lstr)
+    if (v < 0) return OD_ERR_SHAPE;
+  if (!od_aligned16(o1) || !od_aligned16(o2) || !od_aligned16(out)) return OD_ERR_ALIGN;
+  const int64_t threads = n * H * t * (D / 8);
+  if (threads > ((int64_t)1 << 40)) return OD_ERR_SHAPE;
+  MergeArgs a{o1, l1, o2, l2, out, lse, s1r, s1h, s1t, t1r, t1h, t1t, s2r, s2h, s2t, t2r, t2h, t2t, sor, soh, sot,
+              n, H, t, D};
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks > 0x7fffffff) return OD_ERR_SHAPE;
+  lse_merge_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(a);
+  return od_launch_status();
 }

@@ -43,10 +43,37 @@ __device__ __forceinline__ float od_absmax_bf16x2_value(uint32_t acc) {
   return __uint_as_float((lo > hi ? lo : hi) << 16);
 }
 
-// silu(g) = g / (1 + exp(-g)) with the device exp and reciprocal (a few fp32 ulps; the value is then rounded to
-// bf16, which hides the difference except at rare rounding ties). Every SwiGLU kernel uses this one function, so
-// fused and unfused paths agree bit for bit.
-__device__ __forceinline__ float od_silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+// bf16(RN32(silu(g))), silu(g) = g / (1 + exp(-g)): the fp32 value of silu correctly rounded, then rounded to
+// bf16 (the SwiGLU of a bf16 module computes silu in fp32 and rounds to bf16). The fast step uses the device expf
+// (about 1 ulp) and a reciprocal (1 ulp), so it lies within 4 fp32 ulps of silu(g); its bf16 rounding is then the
+// bf16 rounding of the correctly rounded value unless its low 16 bits lie within 16 ulps of the bf16 midpoint
+// 0x8000. Those values (about 1 in 2000), and |g| >= 64 (where exp(-g) or the result leaves the normal fp32 range),
+// are recomputed in float64 and rounded once to fp32. Every SwiGLU kernel uses this one function, so fused and
+// unfused paths agree bit for bit, and g has 65536 values, so it is checked against the oracle exhaustively.
+__device__ __forceinline__ float od_silu_bf16(float g) {
+  float s = g * __builtin_amdgcn_rcpf(1.0f + expf(-g));
+  const uint32_t lo = __float_as_uint(s) & 0xffffu;
+  if (__builtin_expect((lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 64.0f), 0)) {
+    const double gd = (double)g;
+    s = (float)(gd / (1.0 + exp(-gd)));
+  }
+  return od_bf16_to_f32(od_f32_to_bf16(s));
+}
+
+// The RMSNorm factor r = RN32(1 / sqrt(ss / K + eps)) from a float64 sum of squares ss: every square of a bf16 value
+// is exact in float64 and so is their sum unless the row spans more than ~25 binades, so r does not depend on the
+// order of the sum; division and square root are the IEEE float64 operations, rounded once to fp32 at the end.
+__device__ __forceinline__ float od_rms_factor(double ss, int64_t K, float eps) {
+  return (float)(1.0 / sqrt(ss / (double)K + (double)eps));
+}
+
+// Sum of a double over aligned groups of G lanes (G a power of two <= 64), every lane of the group gets it.
+template <int G>
+__device__ __forceinline__ double od_group_sum_f64(double v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, OD_WAVE);
+  return v;
+}
 
 // Max over the 64 lanes of a wave (every lane gets the result).
 __device__ __forceinline__ float od_wave_max(float v) {
@@ -150,7 +177,12 @@ __device__ __forceinline__ float od_xor32_sum(float v) {
 // pattern is then the int8 value in two's complement. NaN inputs give 0.
 constexpr float kOdRoundMagic = 12582912.0f;  // 1.5 * 2^23
 
-__device__ __forceinline__ float od_q8_scale(float amax) { return fmaxf(amax, 1e-8f) / 127.0f; }
+// scale = max(amax, 1e-8) / 127 with torch's NaN rule (amax and clamp_min propagate NaN): a row holding a NaN gets a
+// NaN scale, and its bytes then come out 0 (1 / NaN is NaN, and the quantizer's NaN values carry a zero low byte).
+// A row holding an infinity gets an infinite scale and zero bytes, as in torch (x / inf = 0, inf / inf = NaN -> 0).
+__device__ __forceinline__ float od_q8_scale(float amax) {
+  return (amax != amax ? amax : fmaxf(amax, 1e-8f)) / 127.0f;
+}
 
 // Returns 1.5 * 2^23 + rint(v * inv); dmax collects |v * inv - rint(v * inv)| (<= 0.5), and a lane needs the
 // division when it reaches 0.5 - 2^-15.

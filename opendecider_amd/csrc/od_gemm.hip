@@ -349,7 +349,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
             // bf16(bf16(silu(g)) * u), g and u being the bf16 gate and up outputs (no bias, no residual)
             const float g0 = bfr(__uint_as_float(v.x)), u0 = bfr(__uint_as_float(v.y));
             const float g1 = bfr(__uint_as_float(v.z)), u1 = bfr(__uint_as_float(v.w));
-            const uint32_t h0 = od_f32_to_bf16(bfr(od_silu(g0)) * u0), h1 = od_f32_to_bf16(bfr(od_silu(g1)) * u1);
+            const uint32_t h0 = od_f32_to_bf16(od_silu_bf16(g0) * u0), h1 = od_f32_to_bf16(od_silu_bf16(g1) * u1);
             uint16_t* dst = p.out + m * p.ldo + n / 2;
             if constexpr (GENERAL) {
               if (n < p.N) dst[0] = (uint16_t)h0;

@@ -4,8 +4,9 @@
 //   od_silu_mul_quant  SwiGLU (silu(gate) * up) -> (SmoothQuant input scale) -> per-token int8
 // All are HBM-bound (a few bytes per element); each fuses what would otherwise be separate bf16 round trips.
 // Rounding follows the bf16 module arithmetic of the decoder they serve (every elementwise product of two bf16
-// tensors is rounded to bf16 once), so the CPU oracle reproduces them up to the fp32 reduction order and the
-// rsqrt / exp of the device.
+// tensors is rounded to bf16 once). The two values that a plain fp32 evaluation would leave dependent on the device
+// (the order of a sum, the last bit of exp / rsqrt) are correctly rounded instead: the RMSNorm factor comes from a
+// float64 sum of squares (od_rms_factor) and silu from od_silu_bf16, so the outputs equal the oracle's bit for bit.
 #include "od_common.h"
 
 namespace {
@@ -14,13 +15,13 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ float bfr(float v) { return od_bf16_to_f32(od_f32_to_bf16(v)); }
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, OD_WAVE);
+// Workgroup sum of doubles (wave shuffles, then the per-wave sums in a fixed order).
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+  v = od_group_sum_f64<OD_WAVE>(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  float s = 0.0f;
+  double s = 0.0;
 #pragma unroll
   for (int i = 0; i < kThreads / OD_WAVE; ++i) s += red[i];
   return s;
@@ -38,18 +39,6 @@ __device__ __forceinline__ float block_max_bits(float f, float* red) {
   return __uint_as_float(s);
 }
 
-// Workgroup sum with DPP wave sums, in a fixed order.
-__device__ __forceinline__ float block_sum_dpp(float v, float* red) {
-  v = od_wave_sum_dpp(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kThreads / OD_WAVE; ++i) s += red[i];
-  return s;
-}
-
 __device__ __forceinline__ float block_max(float v, float* red) {
   v = od_wave_max(v);
   __syncthreads();
@@ -62,7 +51,8 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 // ---------------------------------------------------------------------------- RMSNorm + quantize
-// y_k = bf16(w_k * bf16(x_k * r)), r = 1 / sqrt(mean(x^2) + eps); then optionally y_k = bf16(y_k * inv_s_k);
+// y_k = bf16(w_k * bf16(x_k * r)), r = 1 / sqrt(mean(x^2) + eps) (od_rms_factor); then optionally
+// y_k = bf16(y_k * inv_s_k);
 // then the per-row int8 quantizer. One workgroup per row; the row is read three times (L1/L2 after the first).
 __device__ __forceinline__ float rms_val(const uint16_t* xr, const uint16_t* w, const uint16_t* inv_s, int k, float r) {
   float y = bfr(od_bf16_to_f32(w[k]) * bfr(od_bf16_to_f32(xr[k]) * r));
@@ -76,15 +66,16 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_kernel(const uint16_t*
                                                                  int8_t* __restrict__ xq, int64_t ldq,
                                                                  float* __restrict__ sx, int K) {
   __shared__ float red[kThreads / OD_WAVE];
+  __shared__ double red64[kThreads / OD_WAVE];
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * ldx;
-  float ss = 0.0f;
+  double ss = 0.0;
   for (int k = threadIdx.x; k < K; k += kThreads) {
-    const float v = od_bf16_to_f32(xr[k]);
-    ss = fmaf(v, v, ss);
+    const double v = (double)od_bf16_to_f32(xr[k]);
+    ss = fma(v, v, ss);
   }
-  ss = block_sum(ss, red);
-  const float r = 1.0f / sqrtf(ss / (float)K + eps);
+  ss = block_sum_f64(ss, red64);
+  const float r = od_rms_factor(ss, K, eps);
   float amax = 0.0f;
   for (int k = threadIdx.x; k < K; k += kThreads) amax = fmaxf(amax, fabsf(rms_val(xr, w, inv_s, k, r)));
   amax = block_max(amax, red);
@@ -95,11 +86,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_kernel(const uint16_t*
 }
 
 // ---------------------------------------------------------------------------- SwiGLU + quantize
-// y_k = bf16(bf16(silu(g_k)) * u_k), silu(g) = g / (1 + exp(-g)) in fp32, g = gu[row, k], u = gu[row, F + k].
+// y_k = bf16(bf16(silu(g_k)) * u_k) with bf16(silu(g)) from od_silu_bf16, g = gu[row, k], u = gu[row, F + k].
 __device__ __forceinline__ float swiglu_val(const uint16_t* gr, int64_t F, const uint16_t* inv_s, int64_t k) {
   const float g = od_bf16_to_f32(gr[k]);
   const float u = od_bf16_to_f32(gr[F + k]);
-  float y = bfr(bfr(g / (1.0f + expf(-g))) * u);
+  float y = bfr(od_silu_bf16(g) * u);
   if (inv_s) y = bfr(y * od_bf16_to_f32(inv_s[k]));
   return y;
 }
@@ -122,7 +113,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_quant_kernel(const uint16_t
 
 // ---------------------------------------------------------------------------- q/k RMSNorm + RoPE
 // For every token row and every q head then k head (D values at qkv[row, head * D ...]):
-//   n_d = bf16(w_d * bf16(x_d * r)),  r = 1 / sqrt(mean(x^2) + eps)
+//   n_d = bf16(w_d * bf16(x_d * r)),  r = 1 / sqrt(mean(x^2) + eps) (od_rms_factor)
 //   out_d = bf16(bf16(n_d * cos_d) + bf16(rot_d * sin_d)),  rot = (-n[D/2:], n[:D/2]) (rotate_half)
 // cos/sin: bf16 tables [n_pos, D/2] (the two halves of a head share them), row index = pos[token].
 // A group of D/2 lanes owns one head; lane i holds the pair (i, i + D/2).
@@ -145,10 +136,8 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(uint16_t* __rest
   uint16_t* hp = qkv + row * ld + (int64_t)head * D;
   const uint16_t* w = head < n_heads_q ? qw : kw;
   const float a = od_bf16_to_f32(hp[i]), b = od_bf16_to_f32(hp[i + L]);
-  float ss = fmaf(a, a, b * b);
-#pragma unroll
-  for (int o = L / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, OD_WAVE);
-  const float r = 1.0f / sqrtf(ss / (float)D + eps);
+  const double ss = od_group_sum_f64<L>(fma((double)a, (double)a, (double)b * (double)b));
+  const float r = od_rms_factor(ss, D, eps);
   const float na = bfr(od_bf16_to_f32(w[i]) * bfr(a * r));
   const float nb = bfr(od_bf16_to_f32(w[i + L]) * bfr(b * r));
   const int64_t p = pos[row];
@@ -196,17 +185,18 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_vec_kernel(const uint1
     wv[v] = *reinterpret_cast<const uint4*>(w + k);
     if (INV) iv[v] = *reinterpret_cast<const uint4*>(inv_s + k);
   }
+  __shared__ double red64[kThreads / OD_WAVE];
   float y[NV][8];
-  float ss = 0.0f;
+  double ss = 0.0;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) unpack2(word(xv[v], j), y[v][2 * j], y[v][2 * j + 1]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(y[v][e], y[v][e], ss);
+    for (int e = 0; e < 8; ++e) ss = fma((double)y[v][e], (double)y[v][e], ss);
   }
-  ss = block_sum_dpp(ss, red);
-  const float r = 1.0f / sqrtf(ss / (float)K + eps);
+  ss = block_sum_f64(ss, red64);
+  const float r = od_rms_factor(ss, K, eps);
   uint32_t am = 0;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -262,8 +252,7 @@ __global__ __launch_bounds__(kThreads) void silu_mul_quant_vec_kernel(const uint
       float ga, gb, ua, ub;
       unpack2(word(g8, j), ga, gb);
       unpack2(word(u8, j), ua, ub);
-      float a = od_silu(ga), b = od_silu(gb);
-      od_bfr2(a, b);
+      float a = od_silu_bf16(ga), b = od_silu_bf16(gb);
       a *= ua;
       b *= ub;
       uint32_t p = od_bfr2(a, b);
@@ -371,12 +360,11 @@ __global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restr
   unpack4(rb, b);
   unpack4(*reinterpret_cast<const uint2*>(w + 4 * j), fa);
   unpack4(*reinterpret_cast<const uint2*>(w + L + 4 * j), fb);
-  float ss = 0.0f;
+  double ss = 0.0;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) ss = fmaf(b[e], b[e], fmaf(a[e], a[e], ss));
-#pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, OD_WAVE);
-  const float r = 1.0f / sqrtf(ss / (float)D + eps);
+  for (int e = 0; e < 4; ++e) ss = fma((double)b[e], (double)b[e], fma((double)a[e], (double)a[e], ss));
+  ss = od_group_sum_f64<G>(ss);
+  const float r = od_rms_factor(ss, D, eps);
   const int64_t p = pos[row];
   const bool in_table = p >= 0 && p < n_pos;  // a position past the tables yields NaN, never an out-of-bounds read
   float c[4], sn[4];

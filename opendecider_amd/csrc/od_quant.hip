@@ -357,4 +357,4 @@ extern "C" const char* od_strerror(int code) {
   }
 }
 
-extern "C" int od_abi_version(void) { return 1; }
+extern "C" int od_abi_version(void) { return 2; }

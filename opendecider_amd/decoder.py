@@ -115,6 +115,8 @@ class DenseDecoder:
         self.embed = None if embed is None else embed.to(self.dev)
         cos, sin = rope_tables(cfg, max_pos)
         self.cos, self.sin = cos.to(self.dev), sin.to(self.dev)
+        self.temperature = float(weights.get("temperature", 1.0))
+        self._eps32 = float(torch.tensor(cfg.eps, dtype=torch.float32))
         self._ws = {}
         self._rows = {}
 
@@ -217,7 +219,7 @@ class DenseDecoder:
         if n0 == 0:
             kernels.wide_attn(q, k, v, D ** -0.5, kvalid=kvalid, causal=True, out=attn)
         else:
-            rs, mr = (None, B) if B == 1 else (row_start, B)
+            rs, mr = (None, 1) if B == 1 else (row_start, 1)  # one row (the record) per state
             kernels.branched_attn(q, k, v, cache_k.q, cache_k.scale, cache_v.q, cache_v.scale, D ** -0.5,
                                   kvalid=kvalid, length=n0, out=attn, row_start=rs, max_rows=mr)
         return self._attn_out_mlp(li, h, h_out, ws)
@@ -233,8 +235,7 @@ class DenseDecoder:
         ws = self.workspace(B * S)
         h, mid = ws["h"]
         h.copy_(self.embed.index_select(0, ids.reshape(-1)))
-        pos = (n0 + torch.arange(S, dtype=torch.int32)).repeat(B).to(self.dev)
-        row_start = kernels.row_start_of([1] * B, self.dev)[0] if (n0 > 0 and B > 1) else None
+        pos, row_start = self.prefill_layout(n0, B, S)
         for li in range(len(self.layers)):
             self.prefill_layer(li, h, mid, ws, caches[li][0], caches[li][1], B, S, pos, kvalid, row_start)
         return h
@@ -251,13 +252,16 @@ class DenseDecoder:
 
     def readout(self, h: torch.Tensor, B: int, n_opt: int, t: int) -> torch.Tensor:
         """Mean-pool each option row's final-normed hidden states, one logit per row, the 'none' logit appended,
-        log-softmax per request: (B, n_opt + 1) fp32."""
+        divided by the decision temperature (softmax(logits / T), decider.py:255-257), log-softmax per request:
+        (B, n_opt + 1) fp32. The RMSNorm factor is the correctly rounded one (a float64 mean of squares, as
+        od_rmsnorm_quant computes it)."""
         hf = h.float()
-        r = torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + self.cfg.eps)
+        hd = hf.double()
+        r = (1.0 / torch.sqrt((hd * hd).sum(-1, keepdim=True) / hd.shape[-1] + self._eps32)).float()
         hn = (self.final_norm * (hf * r).to(torch.bfloat16)).float()
         pooled = hn.view(B, n_opt, t, -1).mean(2)
         logits = torch.cat([pooled @ self.head, self.none_logit.expand(B, 1)], 1)
-        return torch.log_softmax(logits, -1)
+        return torch.log_softmax(logits / self.temperature, -1)
 
     def positions(self, T: int, R: int, t: int) -> torch.Tensor:
         if T + t > self.cos.shape[0]:
@@ -274,6 +278,17 @@ class DenseDecoder:
         pos, row_start, max_rows = self.row_layout(T, B, n_opt, t)
         h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
         return self.readout(h, B, n_opt, t)
+
+    def prefill_layout(self, n0: int, B: int, S: int):
+        """Device positions of a state pass appending S tokens at n0 to B states, and the one-row-per-state offsets
+        (None for a first prefill or one state), built once per shape so that a prefill makes no host-to-device
+        copy."""
+        key = ("prefill", n0, B, S)
+        if key not in self._rows:
+            pos = (n0 + torch.arange(S, dtype=torch.int32)).repeat(B).to(self.dev)
+            row_start = kernels.row_start_of([1] * B, self.dev)[0] if (n0 > 0 and B > 1) else None
+            self._rows[key] = (pos, row_start)
+        return self._rows[key]
 
     def row_layout(self, T: int, B: int, n_opt: int, t: int):
         """Device positions and per-state row offsets of a scoring pass, built once per shape: a host-to-device

@@ -23,6 +23,28 @@ def _quant_outputs(M, K, ld, device, xq, sx):
     return xq, sx
 
 
+def _check_out(out, shape, device, name):
+    """A caller-given bf16 output must have the exact shape and contiguous rows (the kernels write shape-many
+    elements through its strides); None allocates one."""
+    if out is None:
+        return torch.empty(*shape, dtype=torch.bfloat16, device=device)
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != tuple(shape) or out.stride(-1) != 1:
+        raise ValueError(f"{name}: out must be bf16 {tuple(shape)} with a contiguous last dim, got "
+                         f"{out.dtype} {tuple(out.shape)} strides {out.stride()}")
+    if not out.is_cuda:
+        raise RuntimeError(f"{name}: out must be on the GPU")
+    return out
+
+
+def _scales(t, n, name):
+    """fp32 per-row / per-channel scales, contiguous (the kernels read n floats)."""
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32, got {t.dtype}")
+    if t.numel() != n:
+        raise ValueError(f"{name} has {t.numel()} elements, expected {n}")
+    return t.contiguous()
+
+
 def _vec(v, n, name):
     if v is None:
         return None
@@ -142,10 +164,9 @@ def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tens
     N = w.shape[0]
     if w.shape[1] != Kp:
         raise ValueError(f"w8a8_gemm: a has {Kp} columns, w has {w.shape[1]}")
-    if sa.numel() != M or sw.numel() != N:
-        raise ValueError("w8a8_gemm: scale sizes do not match (M, N)")
-    if want_out and out is None:
-        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    sa, sw = _scales(sa, M, "w8a8_gemm: sa"), _scales(sw, N, "w8a8_gemm: sw")  # kept alive across the launch
+    if want_out:
+        out = _check_out(out, (M, N), a.device, "w8a8_gemm")
     acc = torch.empty(M, N, dtype=torch.int32, device=a.device) if want_acc else None
     if residual is not None:
         _lib.bf16_bits(residual)
@@ -155,7 +176,7 @@ def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tens
         _lib.bf16_bits(bias)
         bias = bias.contiguous()
     o = out if want_out else None
-    check(lib().od_w8a8_gemm(ptr(a), a.stride(0), ptr(sa.contiguous()), ptr(w), w.stride(0), ptr(sw.contiguous()),
+    check(lib().od_w8a8_gemm(ptr(a), a.stride(0), ptr(sa), ptr(w), w.stride(0), ptr(sw),
                              ptr(bias), ptr(residual), residual.stride(0) if residual is not None else 0, ptr(o),
                              o.stride(0) if o is not None else 0, ptr(acc), N if acc is not None else 0, M, N, Kp,
                              stream_of(a)), "od_w8a8_gemm")
@@ -182,15 +203,10 @@ def w8a8_gemm_swiglu(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: tor
     N = w.shape[0]
     if w.shape[1] != Kp or N % 2:
         raise ValueError("w8a8_gemm_swiglu: w must be (2F, Kp) with a's Kp")
-    if sa.numel() != M or sw.numel() != N:
-        raise ValueError("w8a8_gemm_swiglu: scale sizes do not match (M, 2F)")
-    if out is None:
-        out = torch.empty(M, N // 2, dtype=torch.bfloat16, device=a.device)
-    if out.shape != (M, N // 2) or out.stride(-1) != 1:
-        raise ValueError("w8a8_gemm_swiglu: out must be (M, F) with contiguous rows")
-    _lib.bf16_bits(out)
-    check(lib().od_w8a8_gemm_swiglu(ptr(a), a.stride(0), ptr(sa.contiguous()), ptr(w), w.stride(0),
-                                    ptr(sw.contiguous()), ptr(out), out.stride(0), M, N, Kp, stream_of(a)),
+    sa, sw = _scales(sa, M, "w8a8_gemm_swiglu: sa"), _scales(sw, N, "w8a8_gemm_swiglu: sw")
+    out = _check_out(out, (M, N // 2), a.device, "w8a8_gemm_swiglu")
+    check(lib().od_w8a8_gemm_swiglu(ptr(a), a.stride(0), ptr(sa), ptr(w), w.stride(0),
+                                    ptr(sw), ptr(out), out.stride(0), M, N, Kp, stream_of(a)),
           "od_w8a8_gemm_swiglu")
     return out
 
@@ -276,18 +292,29 @@ def split_count(slot_tiles: int, T: int, target_workgroups: int = 1024, min_bloc
 STAGE_MIN_TILES = 4
 
 
-def stage_state(kq, ks, vq, vs, length: int, scale: float, kvalid=None, out=None):
+def stage_size(Ns: int, Hkv: int, length: int, D: int) -> int:
+    """Bytes of the block images of Ns x Hkv heads of `length` keys (od_attn_stage_size)."""
+    nbytes = ctypes.c_int64(0)
+    check(lib().od_attn_stage_size(int(Ns), int(Hkv), int(length), int(D), ctypes.byref(nbytes)),
+          "od_attn_stage_size")
+    return nbytes.value
+
+
+def stage_state(kq, ks, vq, vs, length: int, scale: float, kvalid=None, out=None, dequant: str = "bf16"):
     """Block images of an int8 state for od_branched_attn_staged (od_attn_stage): kq/vq (Ns, Hkv, cap, D) int8,
     ks/vs (Ns, Hkv, cap) fp32, the first `length` tokens, the softmax scale of the attention that reads them,
-    kvalid (Ns, length) uint8 or None. Returns a uint8 device buffer of od_attn_stage_size bytes (`out` is reused
-    when it is large enough)."""
+    kvalid (Ns, length) uint8 or None, dequant "bf16" (the reference's materialize) or "fp32" (exact q * s).
+    Returns a uint8 device buffer of od_attn_stage_size bytes (`out` is reused when it is large enough)."""
+    require_gpu(kq, ks, vq, vs, kvalid, out, name="stage_state")
     Ns, Hkv, cap, D = kq.shape
-    nbytes = ctypes.c_int64(0)
-    check(lib().od_attn_stage_size(Ns, Hkv, int(length), D, ctypes.byref(nbytes)), "od_attn_stage_size")
-    if out is None or out.numel() < nbytes.value:
-        out = torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=kq.device)
+    nbytes = stage_size(Ns, Hkv, length, D)
+    if out is None or out.numel() < nbytes:
+        out = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=kq.device)
+    elif out.dtype != torch.uint8 or not out.is_contiguous():
+        raise ValueError("stage_state: out must be a contiguous uint8 buffer")
     check(lib().od_attn_stage(ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid), Ns, Hkv, int(length), cap, D,
-                              float(scale), ptr(out), out.numel(), stream_of(kq)), "od_attn_stage")
+                              float(scale), _lib.dequant_code(dequant), ptr(out), out.numel(), stream_of(kq)),
+          "od_attn_stage")
     return out
 
 
@@ -299,7 +326,7 @@ def uses_staging(max_rows: int, t: int, n_heads_q: int, n_heads_k: int) -> bool:
 
 def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, row_counts=None, length=None,
                   out=None, return_lse: bool = False, row_start=None, max_rows=None, n_split=None, staged=None,
-                  stage_buf=None):
+                  stage_buf=None, dequant: str = "bf16", images=None):
     """Branched option-row attention over int8 states. q (R, Hq, t, D) bf16; k_own/v_own (R, Hkv, t, D) bf16;
     kq/vq (Ns, Hkv, cap, D) int8 of which the first T tokens are used (T = `length`, else kvalid.shape[1], else
     cap); ks/vs (Ns, Hkv, cap) fp32; kvalid (Ns, T) bool/uint8 or None.
@@ -308,8 +335,10 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
     (split_count). staged: convert the state once into block images (od_attn_stage, into `stage_buf` when given and
     large enough) and run od_branched_attn_staged over them; False runs od_branched_attn / od_branched_attn_split,
     which convert in every workgroup (same results, bit for bit); None stages when at least STAGE_MIN_TILES slot
-    tiles read each (state, head), so that the conversion is shared. Returns out (R, Hq, t, D) bf16
-    [, lse (R, Hq, t) fp32]."""
+    tiles read each (state, head), so that the conversion is shared. images: block images already built by
+    stage_state for this state, length, scale, mask and dequant (the staged path then skips od_attn_stage; the
+    caller keeps them valid). dequant: "bf16", the reference's materialize bf16(q * bf16(s)) (quant.py:45,
+    prefix_attn.py:145-149), or "fp32", the exact q * s. Returns out (R, Hq, t, D) bf16 [, lse (R, Hq, t) fp32]."""
     require_gpu(q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, name="branched_attn")
     for x in (q, k_own, v_own):
         _lib.bf16_bits(x)
@@ -344,20 +373,23 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
             raise ValueError("branched_attn: row_start must be int32 (Ns + 1,)")
         if max_rows is None:
             raise ValueError("branched_attn: max_rows is required with row_start")
+    dq = _lib.dequant_code(dequant)
     q, k_own, v_own = _rows_aligned(q), _rows_aligned(k_own), _rows_aligned(v_own)
-    if out is None:
-        out = torch.empty(R, Hq, t, D, dtype=torch.bfloat16, device=q.device)
+    out = _check_out(out, (R, Hq, t, D), q.device, "branched_attn")
     lse = torch.empty(R, Hq, t, dtype=torch.float32, device=q.device) if return_lse else None
     tiles = -(-(int(max_rows) * t * (Hq // Hkv)) // 128)  # slot tiles per (state, head)
     if n_split is None:
         n_split = split_count(tiles * Hkv * Ns, T)
     if staged is None:
-        staged = tiles >= STAGE_MIN_TILES
+        staged = images is not None or tiles >= STAGE_MIN_TILES
     ws = None
     if n_split > 1:
         ws = torch.empty(n_split * R * Hq * t * (D + 1), dtype=torch.float32, device=q.device)
     if staged and T > 0:
-        img = stage_state(kq, ks, vq, vs, T, scale, kvalid, out=stage_buf)
+        img = images if images is not None else stage_state(kq, ks, vq, vs, T, scale, kvalid, out=stage_buf,
+                                                            dequant=dequant)
+        if img.numel() < stage_size(Ns, Hkv, T, D):
+            raise ValueError("branched_attn: the block images are smaller than the state needs")
         check(lib().od_branched_attn_staged(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
                                             *v_own.stride()[:3], ptr(img), img.numel(), ptr(row_start),
                                             int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv, t, D,
@@ -368,13 +400,13 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
         check(lib().od_branched_attn_split(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
                                            *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
                                            ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R,
-                                           Hq, Hkv, t, D, Ns, T, cap, float(scale), int(n_split), ptr(ws), ws.numel(),
-                                           stream_of(q)), "od_branched_attn_split")
+                                           Hq, Hkv, t, D, Ns, T, cap, float(scale), dq, int(n_split), ptr(ws),
+                                           ws.numel(), stream_of(q)), "od_branched_attn_split")
     else:
         check(lib().od_branched_attn(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
                                      *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
                                      ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv,
-                                     t, D, Ns, T, cap, float(scale), stream_of(q)), "od_branched_attn")
+                                     t, D, Ns, T, cap, float(scale), dq, stream_of(q)), "od_branched_attn")
     return (out, lse) if return_lse else out
 
 
@@ -394,12 +426,33 @@ def wide_attn(q, k, v, scale: float, kvalid=None, causal: bool = True, return_ls
             raise ValueError("wide_attn: kvalid must be (B, S)")
         kvalid = kvalid.to(torch.uint8).contiguous()
     q, k, v = _rows_aligned(q), _rows_aligned(k), _rows_aligned(v)
-    if out is None:
-        out = torch.empty(B, H, T, DV, dtype=torch.bfloat16, device=q.device)
+    out = _check_out(out, (B, H, T, DV), q.device, "wide_attn")
     lse = torch.empty(B, H, T, dtype=torch.float32, device=q.device) if return_lse else None
     check(lib().od_wide_attn(ptr(q), *q.stride()[:3], ptr(k), *k.stride()[:3], ptr(v), *v.stride()[:3], ptr(kvalid),
                              kvalid.stride(0) if kvalid is not None else 0, ptr(out), *out.stride()[:3], ptr(lse), B, H,
                              G, T, S, DK, DV, 1 if causal else 0, float(scale), stream_of(q)), "od_wide_attn")
+    return (out, lse) if return_lse else out
+
+
+def lse_merge(o1: torch.Tensor, l1: torch.Tensor, o2: torch.Tensor, l2: torch.Tensor, out=None,
+              return_lse: bool = False):
+    """Merge two attention partials by their log-sum-exp (prefix_attn.py:74-76) with od_lse_merge: o1/o2 (n, H, t, D)
+    bf16 views (any strides, last dim contiguous), l1/l2 (n, H, t) fp32 views. Returns out (n, H, t, D) bf16
+    [, lse (n, H, t) fp32]."""
+    require_gpu(o1, l1, o2, l2, out, name="lse_merge")
+    for x in (o1, o2):
+        _lib.bf16_bits(x)
+    n, H, t, D = o1.shape
+    if o2.shape != o1.shape or l1.shape != (n, H, t) or l2.shape != (n, H, t):
+        raise ValueError("lse_merge: partials must be (n, H, t, D) with LSEs (n, H, t)")
+    if l1.dtype != torch.float32 or l2.dtype != torch.float32:
+        raise TypeError("lse_merge: LSEs must be float32")
+    o1, o2 = _rows_aligned(o1), _rows_aligned(o2)
+    out = _check_out(out, (n, H, t, D), o1.device, "lse_merge")
+    lse = torch.empty(n, H, t, dtype=torch.float32, device=o1.device) if return_lse else None
+    check(lib().od_lse_merge(ptr(o1), *o1.stride()[:3], ptr(l1), *l1.stride(), ptr(o2), *o2.stride()[:3], ptr(l2),
+                             *l2.stride(), ptr(out), *out.stride()[:3], ptr(lse), n, H, t, D, stream_of(o1)),
+          "od_lse_merge")
     return (out, lse) if return_lse else out
 
 

@@ -2,9 +2,11 @@
 
 Drop-in for the op at the centre of src/opendecider/prefix_attn.py: `_split_attention` (prefix_attn.py:43-76), its
 per-state loop in `_forward` (prefix_attn.py:118-128) and the per-layer dequantized copy of the state's K/V made by
-`shared_prefix_attention` (prefix_attn.py:145-149). Here the int8 state goes to the kernel as it is stored, with
-its per-(token, head) scales, and one launch covers every row of every state: prefix partial, own causal partial
-and their log-sum-exp merge.
+`shared_prefix_attention` (prefix_attn.py:145-149). An int8 state (Int8Tensor) goes to the branched kernel as it is
+stored, with its per-(token, head) scales, and one launch covers every row: prefix partial, own causal partial and
+their log-sum-exp merge, the state dequantized in registers as the reference materializes it (bf16(q * bf16(s))).
+A dense bf16 prefix, as the reference's _forward passes it (prefix_attn.py:127), takes the reference's own GPU
+route: od_wide_attn over the prefix and over the own keys, each with its LSE, then od_lse_merge.
 """
 from __future__ import annotations
 
@@ -15,10 +17,8 @@ from .quant import Int8Tensor
 
 
 def _state_parts(K, V):
-    """(kq, ks, vq, vs) from Int8Tensor states (Hkv, T, D) or (Ns, Hkv, T, D) with fp32 scales (..., 1)."""
-    if not (isinstance(K, Int8Tensor) and isinstance(V, Int8Tensor)):
-        raise TypeError("the MI355X shared-prefix attention reads the int8 state: pass Int8Tensor K/V "
-                        "(as stored by the packed cache) instead of dequantized tensors")
+    """(kq, ks, vq, vs) from Int8Tensor states (Hkv, T, D) or (Ns, Hkv, T, D) with scales (..., 1) (fp32, or the
+    reference's bf16 stored scale, whose value is exact in fp32)."""
     kq, vq = K.q, V.q
     ks, vs = K.scale.float(), V.scale.float()
     if kq.dim() == 3:
@@ -26,27 +26,44 @@ def _state_parts(K, V):
     return kq.contiguous(), ks.reshape(kq.shape[:3]).contiguous(), vq.contiguous(), vs.reshape(vq.shape[:3]).contiguous()
 
 
-def _split_attention(q, k, v, Kp, Vp, pm, scale):
+def _split_attention(q, k, v, Kp, Vp, pm, scale, dequant: str = "bf16"):
     """Hydragen split for rows continuing ONE shared prefix (prefix_attn.py:43-76): q (n, Hq, t, D) attends the
-    prefix Kp/Vp (Int8Tensor, (Hkv, T, D); pm (T,) real keys or None) and its own row's k/v (n, Hkv, t, D)
-    causally; the two softmax parts are merged by their log-sum-exp. Returns (n, Hq, t, D) in v.dtype."""
-    kq, ks, vq, vs = _state_parts(Kp, Vp)
-    kvalid = None if pm is None else pm.reshape(1, -1)
-    out = kernels.branched_attn(q, k, v, kq, ks, vq, vs, scale, kvalid=kvalid, length=kq.shape[2])
-    return out.to(v.dtype)
+    prefix Kp/Vp ((Hkv, T, D); pm (T,) real keys or None) and its own row's k/v (n, Hkv, t, D) causally; the two
+    softmax parts are merged by their log-sum-exp. Kp/Vp are either Int8Tensor (the int8 state read directly,
+    dequantized as `dequant` says: "bf16" is the reference's materialize, "fp32" the exact q * s) or dense bf16
+    tensors as the reference's caller passes them (prefix_attn.py:127). Returns (n, Hq, t, D) in v.dtype."""
+    if isinstance(Kp, Int8Tensor) and isinstance(Vp, Int8Tensor):
+        kq, ks, vq, vs = _state_parts(Kp, Vp)
+        kvalid = None if pm is None else pm.reshape(1, -1)
+        out = kernels.branched_attn(q, k, v, kq, ks, vq, vs, scale, kvalid=kvalid, length=kq.shape[2],
+                                    dequant=dequant)
+        return out.to(v.dtype)
+    if isinstance(Kp, Int8Tensor) or isinstance(Vp, Int8Tensor):
+        raise TypeError("_split_attention: Kp and Vp must both be Int8Tensor or both dense tensors")
+    n, Hq, t, D = q.shape
+    T = Kp.shape[1]
+    qs = q.transpose(0, 1).reshape(1, Hq, n * t, D)  # all rows' queries against the prefix keys only
+    kvalid = None if pm is None else pm.reshape(1, T)
+    o_p, l_p = kernels.wide_attn(qs, Kp[None], Vp[None], scale, kvalid=kvalid, causal=False, return_lse=True)
+    o_o, l_o = kernels.wide_attn(q, k, v, scale, causal=True, return_lse=True)
+    o_p = o_p.view(Hq, n, t, -1).transpose(0, 1)
+    l_p = l_p.view(Hq, n, t).transpose(0, 1)
+    return kernels.lse_merge(o_p, l_p, o_o, l_o).to(v.dtype)
 
 
 split_attention = _split_attention
 
 
-def split_attention_int8(q, k, v, Kq, Ks, Vq, Vs, pm, scale, row_counts=None, return_lse: bool = False):
+def split_attention_int8(q, k, v, Kq, Ks, Vq, Vs, pm, scale, row_counts=None, return_lse: bool = False,
+                         dequant: str = "bf16"):
     """The batched form: rows of several states in one launch. q (R, Hq, t, D); k/v (R, Hkv, t, D); Kq/Vq int8
     (Ns, Hkv, T, D) or (Hkv, T, D); Ks/Vs fp32 (Ns, Hkv, T[, 1]); pm (Ns, T) bool or None; row_counts: how many
-    consecutive rows belong to each state (rows grouped by state; None for one state)."""
+    consecutive rows belong to each state (rows grouped by state; None for one state); dequant as
+    _split_attention."""
     if Kq.dim() == 3:
         Kq, Vq, Ks, Vs = Kq[None], Vq[None], Ks[None], Vs[None]
     Ks = Ks.float().reshape(Kq.shape[:3]).contiguous()
     Vs = Vs.float().reshape(Vq.shape[:3]).contiguous()
     return kernels.branched_attn(q, k, v, Kq.contiguous(), Ks, Vq.contiguous(), Vs, scale, kvalid=pm,
                                  row_counts=row_counts, length=Kq.shape[2] if pm is None else None,
-                                 return_lse=return_lse)
+                                 return_lse=return_lse, dequant=dequant)

@@ -169,9 +169,10 @@ def branched_attention(q, k_own, v_own, Kp, Vp, scale: float, kvalid=None, row_s
 
 
 def branched_attention_int8(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, row_state=None,
-                            dequant: str = "fp32", dtype=torch.float32):
-    """The int8-state branched attention: the state K/V are dequantized (dequant_state) and passed to
-    branched_attention. kq/vq (Ns,Hkv,T,D) int8; ks/vs (Ns,Hkv,T) fp32."""
+                            dequant: str = "bf16", dtype=torch.float32):
+    """The int8-state branched attention: the state K/V are dequantized (dequant_state; "bf16" is the reference's
+    materialize, prefix_attn.py:145-149, and the default) and passed to branched_attention. kq/vq (Ns,Hkv,T,D) int8;
+    ks/vs (Ns,Hkv,T) fp32."""
     Kp = dequant_state(kq, ks, dequant).to(dtype)
     Vp = dequant_state(vq, vs, dequant).to(dtype)
     return branched_attention(q, k_own, v_own, Kp, Vp, scale, kvalid, row_state, dtype)

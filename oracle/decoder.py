@@ -87,11 +87,23 @@ def rope_tables(cfg: DecoderConfig, n_pos: int):
     return ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
 
 
+def rms_factor(x: torch.Tensor, eps: float) -> torch.Tensor:
+    """r = 1 / sqrt(mean(x^2) + eps) over the last dim, the HF RMSNorm factor (fp32 in the reference:
+    torch.rsqrt(x.float().pow(2).mean(-1) + eps)), evaluated in float64 and rounded once to fp32: the correctly
+    rounded value of that expression (the reference's fp32 evaluation lands within a few fp32 ulps of it). The
+    squares of bf16 / fp32 inputs are exact in float64 and their sum is exact unless the row spans more than ~25
+    binades, so the result does not depend on the summation order; eps enters as the fp32 value the reference adds."""
+    xd = x.detach().to("cpu").double()
+    ms = (xd * xd).sum(-1, keepdim=True) / xd.shape[-1]
+    eps32 = float(torch.tensor(eps, dtype=torch.float32))
+    return (1.0 / torch.sqrt(ms + eps32)).float()
+
+
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    """w * bf16(x * rsqrt(mean(x^2) + eps)) in bf16 (the HF RMSNorm arithmetic)."""
+    """w * bf16(x * r) in bf16 (the HF RMSNorm arithmetic: x * r in fp32, rounded to bf16, times the bf16 weight,
+    rounded again), r = rms_factor(x)."""
     xf = x.float()
-    r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return w * (xf * r).to(torch.bfloat16)
+    return w * (xf * rms_factor(xf, eps)).to(torch.bfloat16)
 
 
 def qk_norm_rope(qkv: torch.Tensor, cfg: DecoderConfig, q_w, k_w, cos, sin, pos) -> torch.Tensor:
@@ -110,9 +122,19 @@ def qk_norm_rope(qkv: torch.Tensor, cfg: DecoderConfig, q_w, k_w, cos, sin, pos)
     return out
 
 
+def silu_bf16(g: torch.Tensor) -> torch.Tensor:
+    """bf16(silu(g)) for bf16 g, with silu(g) = g / (1 + exp(-g)) evaluated in float64 and rounded once to fp32
+    before the bf16 rounding: the reference's F.silu on a bf16 tensor computes g / (1 + exp(-g)) in fp32 and rounds
+    to bf16; this is that fp32 value correctly rounded. g has 65536 possible values, so the function is a table
+    that a kernel can be checked against exhaustively."""
+    gd = g.double()
+    return (gd / (1.0 + torch.exp(-gd))).float().to(torch.bfloat16)
+
+
 def swiglu(gu: torch.Tensor, F: int) -> torch.Tensor:
-    """bf16(bf16(silu(g)) * u) with g = gu[:, :F], u = gu[:, F:]."""
-    return torch.nn.functional.silu(gu[:, :F]) * gu[:, F:]
+    """bf16(bf16(silu(g)) * u) with g = gu[:, :F], u = gu[:, F:] (torch's bf16 product: fp32 product, one
+    rounding)."""
+    return silu_bf16(gu[:, :F]) * gu[:, F:]
 
 
 def _layer_tail(h, attn, qlin, lw, cfg: DecoderConfig):
@@ -130,10 +152,13 @@ def _layer_tail(h, attn, qlin, lw, cfg: DecoderConfig):
 
 
 def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: int, pos, cos, sin,
-                  row_state=None, kvalid=None, attn_hook=None):
+                  row_state=None, kvalid=None, attn_hook=None, dequant: str = "bf16", attn_dtype=torch.float32):
     """One decoder layer over the option-row tokens h (M = R * t, hidden) bf16. qlin: {name: (q, sw, inv_s)}.
     state_k/state_v: (kq int8 (Ns, Hkv, T, D), ks fp32 (Ns, Hkv, T)) of this layer. attn_hook, if given, maps the
-    bf16 attention output (M, Hq D) to the tensor used downstream (sensitivity studies). Returns the new h."""
+    bf16 attention output (M, Hq D) to the tensor used downstream (sensitivity studies). dequant: how the int8 state
+    becomes K/V ("bf16": the reference's materialize, q.to(bf16) * s.to(bf16), prefix_attn.py:145-149; "fp32": q * s
+    exact); attn_dtype: the attention's arithmetic (fp32 as the reference's CPU branch, or float64 to measure how
+    much the result depends on the accumulation). Returns the new h."""
     D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     x = rmsnorm(h, lw["ln1"], cfg.eps)
     q, sw, inv = qlin["wqkv"]
@@ -143,7 +168,7 @@ def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: 
     kh = qkv[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
     vh = qkv[:, (Hq + Hk) * D:].reshape(R, t, Hk, D).transpose(1, 2)
     o, _ = oa.branched_attention_int8(qh, kh, vh, state_k[0], state_k[1], state_v[0], state_v[1], D ** -0.5,
-                                      kvalid, row_state)
+                                      kvalid, row_state, dequant=dequant, dtype=attn_dtype)
     attn = o.to(torch.bfloat16).transpose(1, 2).reshape(R * t, Hq * D)
     if attn_hook is not None:
         attn = attn_hook(attn)
@@ -151,13 +176,14 @@ def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: 
 
 
 def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: int = 0, kvalid=None,
-                    attn_hook=None):
+                    attn_hook=None, dequant: str = "bf16", attn_dtype=torch.float32):
     """State pass over S new tokens of each of B states (ids (B, S)) appended after n0 cached tokens.
     n0 = 0: causal attention among the new tokens on their bf16 K/V (exact softmax attention, the contract of the
     backbone's attention on the state, wide_attention.py:70-91). n0 > 0: the new tokens attend the cached int8 state
     (state_kv[l] = ((kq, ks), (vq, vs)) of length n0) and themselves causally, merged by LSE (one row per state,
     prefix_attn.py:43-76). Then only the new tokens' K/V are quantized per (token, head) and appended
-    (state_cache.py:79, quant.py:36-41). Returns (h (B S, hidden) bf16, the per-layer state K/V of length n0 + S)."""
+    (state_cache.py:79, quant.py:36-41). dequant / attn_dtype as layer_forward. Returns (h (B S, hidden) bf16, the
+    per-layer state K/V of length n0 + S)."""
     B, S = ids.shape
     D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     h = embed[ids.reshape(-1)]
@@ -174,10 +200,11 @@ def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: 
         kh = qkv[:, Hq * D:(Hq + Hk) * D].reshape(B, S, Hk, D).transpose(1, 2)
         vh = qkv[:, (Hq + Hk) * D:].reshape(B, S, Hk, D).transpose(1, 2)
         if n0 == 0:
-            o, _ = oa.attention(qh, kh, vh, D ** -0.5, kvalid, causal=True)
+            o, _ = oa.attention(qh, kh, vh, D ** -0.5, kvalid, causal=True, dtype=attn_dtype)
         else:
             (kq, ks), (vq, vs) = state_kv[li]
-            o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, kvalid, torch.arange(B))
+            o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, kvalid, torch.arange(B),
+                                              dequant=dequant, dtype=attn_dtype)
         attn = o.to(torch.bfloat16).transpose(1, 2).reshape(B * S, Hq * D)
         if attn_hook is not None:
             attn = attn_hook(attn)
@@ -197,13 +224,15 @@ def quantize_layer(lw):
     return {k: quantize_linear(lw[k], lw["s_" + k[1:]]) for k in ("wqkv", "wo", "wgu", "wdown")}
 
 
-def readout(h, final_norm, head, none_logit, cfg: DecoderConfig, B: int, n_opt: int, t: int):
+def readout(h, final_norm, head, none_logit, cfg: DecoderConfig, B: int, n_opt: int, t: int,
+            temperature: float = 1.0):
     """Mean-pool each option row's final-normed hidden states, one logit per row (pooled . head), append the
-    'none' logit, log-softmax per request. Returns (B, n_opt + 1) fp32 log-probabilities."""
+    'none' logit, divide by the decision temperature (the reference's softmax(logits / T), decider.py:255-257) and
+    log-softmax per request. Returns (B, n_opt + 1) fp32 log-probabilities."""
     hf = rmsnorm(h, final_norm, cfg.eps).float().reshape(B, n_opt, t, -1).mean(2)
     logits = hf @ head.float()
     logits = torch.cat([logits, none_logit.float().expand(B, 1)], 1)
-    return torch.log_softmax(logits, -1)
+    return torch.log_softmax(logits / temperature, -1)
 
 
 def nudge_bf16(x: torch.Tensor, frac: float, seed: int) -> torch.Tensor:
@@ -216,9 +245,13 @@ def nudge_bf16(x: torch.Tensor, frac: float, seed: int) -> torch.Tensor:
     return (bits + flip * sign).view(torch.bfloat16)
 
 
-def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, kvalid=None, attn_hook=None):
+def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, kvalid=None, attn_hook=None,
+                     dequant: str = "bf16", attn_dtype=torch.float32, temperature: float | None = None):
     """Option-row scoring pass: ids (B, n_opt, t) token ids; state_kv[l] = ((kq, ks), (vq, vs)) per layer for the
-    B cached states of length T. Returns (B, n_opt + 1) log-probabilities."""
+    B cached states of length T. dequant / attn_dtype as layer_forward, temperature as readout (None: the weights'
+    "temperature", 1 if absent). Returns (B, n_opt + 1) log-probabilities."""
+    if temperature is None:
+        temperature = float(weights.get("temperature", 1.0))
     B, n_opt, t = ids.shape
     R = B * n_opt
     h = embed[ids.reshape(-1)]
@@ -227,5 +260,5 @@ def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, 
     row_state = torch.arange(B).repeat_interleave(n_opt)
     for li, lw in enumerate(weights["layers"]):
         h = layer_forward(h, lw, quantize_layer(lw), cfg, state_kv[li][0], state_kv[li][1], R, t, pos, cos, sin,
-                          row_state, kvalid, attn_hook)
-    return readout(h, weights["final_norm"], weights["head"], weights["none_logit"], cfg, B, n_opt, t)
+                          row_state, kvalid, attn_hook, dequant, attn_dtype)
+    return readout(h, weights["final_norm"], weights["head"], weights["none_logit"], cfg, B, n_opt, t, temperature)

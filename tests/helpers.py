@@ -49,3 +49,24 @@ def assert_close_rel(out: torch.Tensor, ref: torch.Tensor, rel: float = REL, wha
     bad = (out - ref).abs() > elem_steps * BF16_STEP * ref.abs() + rel * rms
     assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond {elem_steps} x 2^-8|ref| + {rel} rms: {st}"
     return st
+
+
+def decoder_case(cfg_kw: dict, B: int, n_opt: int, t: int, T: int, temperature: float = 1.0):
+    """The seeded decision-forward case shared by the GPU end-to-end tests and the CPU tests of their bar: random-init
+    weights (seed 3) with the decision temperature, embedding (seed 3), per-layer int8 states of T tokens (source bf16
+    N(0,1), seed 4) and option token ids (seed 5). Returns (cfg, weights, embedding, states, ids)."""
+    from oracle import decoder as od
+    from oracle import quant as oq
+    cfg = od.DecoderConfig(**cfg_kw)
+    w = od.make_weights(cfg, seed=3)
+    w["temperature"] = temperature
+    emb = od.make_embedding(cfg, seed=3)
+    g = torch.Generator().manual_seed(4)
+    states = []
+    for _ in range(cfg.n_layers):
+        kv = torch.randn(2, B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).to(torch.bfloat16)
+        kq, ks = oq.quantize_rows(kv[0])
+        vq, vs = oq.quantize_rows(kv[1])
+        states.append(((kq, ks[..., 0]), (vq, vs[..., 0])))
+    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=torch.Generator().manual_seed(5))
+    return cfg, w, emb, states, ids

@@ -1,30 +1,36 @@
 """GPU parity of the decoder-layer row kernels and of the whole decision forward against the oracle.
 
-Row kernels: int8 bytes and fp32 scales are exact where the device and the oracle compute the same fp32 value; the
-RMSNorm / SwiGLU pre-quantization values can differ in the last fp32 bits (reduction order, device rsqrt and exp),
-which may move a bf16 rounding and then one int8 step, so those are held to: scales within 2^-7 relative, bytes
-within one step, and at most 0.5% of bytes off. RoPE outputs within one bf16 step.
+Row kernels: bit-exact. The RMSNorm factor is the correctly rounded fp32 value of 1 / sqrt(mean(x^2) + eps) (a float64
+sum of squares on both sides) and bf16(silu(g)) the bf16 rounding of the correctly rounded fp32 silu, so int8 bytes,
+fp32 scales and the RoPE outputs equal the oracle's; silu is checked on all 65536 bf16 inputs.
 Decision forward: every stage of every layer against the oracle fed the GPU's input to that stage (bit-exact except
-the attention, which is held to its 2e-3 bar), end-to-end probabilities within the oracle's own sensitivity to
-rounding-size perturbations of the attention output, and option-order invariance (<= 1e-6).
+the attention, which is held to its 2e-3 bar against the reference's bf16-materialized state), and the readout of the
+GPU's final hidden states within 1e-6. End to end (GPU and oracle each run on their own): option probabilities within
+1e-4 absolute, log-probabilities within 2e-3 relative and option-order invariance <= 1e-6, at the harness's decision
+temperature T_E2E (the reference's softmax(logits / T), decider.py:255-257). The random-init W8A8 network re-rolls
+its quantization noise wherever one attention output lands on the neighbouring bf16 value, so at T = 1 the oracle
+disagrees with itself (fp32 against float64 attention accumulation) by 2.8e-4 on these shapes; at T_E2E = 16 that
+floor is 2.2e-5, and tests/test_oracle_decoder.py shows that planted kernel mistakes still move the probabilities
+past 1e-4 there. The T = 1 difference is printed as a diagnostic.
 """
 import pytest
 import torch
 
-from helpers import PROB_ABS, assert_close_rel
+from helpers import PROB_ABS, REL, assert_close_rel, decoder_case
 from oracle import attention as oa
 from oracle import decoder as od
 from oracle import quant as oq
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
+T_E2E = 16.0
 
 
-def _close_quant(xq, sx, rq, rs):
+def _exact_quant(xq, sx, rq, rs, what=""):
     xq, sx = xq.cpu(), sx.cpu()
-    assert ((sx - rs).abs() <= rs.abs() * 2.0 ** -7).all()
+    assert torch.equal(sx.view(torch.int32), rs.reshape(sx.shape).contiguous().view(torch.int32)), f"{what}: scales"
     d = (xq.int() - rq.int()).abs()
-    assert d.max().item() <= 1 and (d > 0).float().mean().item() <= 5e-3, (d.max().item(), (d > 0).float().mean())
+    assert d.max().item() == 0, (what, d.max().item(), (d > 0).float().mean().item())
 
 
 @pytest.mark.parametrize("M,K,smooth", [(7, 4096, False), (33, 4096, True), (5, 200, True)])
@@ -36,7 +42,7 @@ def test_rmsnorm_quant(gpu_lib, M, K, smooth):
     inv = (1 / (torch.rand(K, generator=g) * 1.5 + 0.5)).to(torch.bfloat16) if smooth else None
     xq, sx = kernels.rmsnorm_quant(x.to(DEV), w.to(DEV), 1e-6, None if inv is None else inv.to(DEV))
     rq, rs = oq.act_quant(od.rmsnorm(x, w, 1e-6), inv)
-    _close_quant(xq, sx, rq, rs)
+    _exact_quant(xq, sx, rq, rs, "rmsnorm_quant")
 
 
 @pytest.mark.parametrize("M,F,smooth", [(9, 12288, True), (4, 96, False)])
@@ -47,7 +53,34 @@ def test_silu_mul_quant(gpu_lib, M, F, smooth):
     inv = (1 / (torch.rand(F, generator=g) * 1.5 + 0.5)).to(torch.bfloat16) if smooth else None
     xq, sx = kernels.silu_mul_quant(gu.to(DEV), F, None if inv is None else inv.to(DEV))
     rq, rs = oq.act_quant(od.swiglu(gu, F), inv)
-    _close_quant(xq, sx, rq, rs)
+    _exact_quant(xq, sx, rq, rs, "silu_mul_quant")
+
+
+def test_silu_all_bf16_inputs(gpu_lib):
+    """bf16(silu(g)) of the SwiGLU GEMM epilogue on every bf16 bit pattern of g (normal numbers, zeros, infinities,
+    NaNs; the 2 x 127 x 128 subnormal patterns are left out: the epilogue forms g from an fp32 product, where the
+    device may flush them) against the oracle's correctly rounded table. One row, K = 16: a = e_0, gate row 2f =
+    e_0 with scale g_f, up row 2f + 1 = e_0 with scale 1, so g = g_f and u = 1 exactly."""
+    from opendecider_amd import kernels
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    gv = bits.view(torch.bfloat16)
+    expo = (bits.int() >> 7) & 0xFF
+    keep = (expo != 0) | ((bits.int() & 0x7F) == 0)
+    gv = gv[keep]
+    F = gv.numel()
+    a = torch.zeros(1, 16, dtype=torch.int8)
+    a[0, 0] = 1
+    w = torch.zeros(2 * F, 16, dtype=torch.int8)
+    w[:, 0] = 1
+    sw = torch.ones(2 * F)
+    sw[0::2] = gv.float()
+    out = kernels.w8a8_gemm_swiglu(a.to(DEV), torch.ones(1, device=DEV), w.to(DEV), sw.to(DEV))
+    got = out.cpu()[0]
+    ref = od.silu_bf16(gv)
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(got), nan)
+    bad = (got.view(torch.int16) != ref.view(torch.int16)) & ~nan
+    assert not bad.any(), (gv[bad][:8], got[bad][:8], ref[bad][:8])
 
 
 @pytest.mark.parametrize("D", [128, 64])
@@ -65,8 +98,7 @@ def test_qk_norm_rope(gpu_lib, D):
     x = qkv.to(DEV)
     kernels.qk_norm_rope(x, 8, 2, D, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV), pos.to(DEV, torch.int32),
                          cfg.eps)
-    got = x.cpu().float()
-    assert ((got - ref.float()).abs() <= ref.float().abs() * 2.0 ** -7 + 2.0 ** -14).all()
+    assert torch.equal(x.cpu().view(torch.int16), ref.view(torch.int16))
     assert torch.equal(x.cpu()[:, 10 * D:], qkv[:, 10 * D:])
 
 
@@ -109,8 +141,7 @@ def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0):
         assert torch.equal(a.q, b.q) and torch.equal(a.scale.view(torch.int32), b.scale.view(torch.int32))
         assert (a.q[:, :, :n0] == 77).all() and (a.q[:, :, n0 + S:] == 77).all()
     ref = od.qk_norm_rope(qkv, cfg, qw.cpu(), kw.cpu(), cos.cpu(), sin.cpu(), pos.cpu().long())
-    got = x1.cpu().float()
-    assert ((got - ref.float()).abs() <= ref.float().abs() * 2.0 ** -7 + 2.0 ** -14).all()
+    assert torch.equal(x1.cpu().view(torch.int16), ref.view(torch.int16))
     for c, cols in ((caches[0][0], slice(Hq * D, (Hq + Hk) * D)), (caches[0][1], slice((Hq + Hk) * D, None))):
         src = x1.cpu()[:, cols].view(B, S, Hk, D).transpose(1, 2)
         rq, rs = oq.quantize_rows(src.reshape(-1, D))
@@ -118,17 +149,6 @@ def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0):
         assert torch.equal(c.scale[:, :, n0:n0 + S].cpu().reshape(-1), rs.reshape(-1))
     with pytest.raises(ValueError):                      # past the capacity: refused before any write
         kernels.qk_norm_rope_kv_append(x1, B, S, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, *caches[0])
-
-
-def _states(cfg, B, T, layers, seed):
-    g = torch.Generator().manual_seed(seed)
-    out = []
-    for _ in range(layers):
-        kv = torch.randn(2, B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).to(torch.bfloat16)
-        kq, ks = oq.quantize_rows(kv[0])
-        vq, vs = oq.quantize_rows(kv[1])
-        out.append(((kq, ks[..., 0]), (vq, vs[..., 0])))
-    return out
 
 
 def _gpu_states(states, cap):
@@ -149,27 +169,23 @@ def _gpu_states(states, cap):
 
 CASES = [
     ("tiny_d64", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500), 2, 5, 4, 70),
-    ("9b_dims_2_layers", dict(n_layers=2, vocab=1000), 2, 6, 16, 256),
+    ("9b_dims_2_layers", dict(n_layers=2, vocab=1000), 2, 32, 16, 256),
 ]
 
 
 def _setup(cfg_kw, B, n_opt, t, T):
     from opendecider_amd.decoder import DecoderConfig, DenseDecoder
-    cfg = od.DecoderConfig(**cfg_kw)
-    w = od.make_weights(cfg, seed=3)
-    emb = od.make_embedding(cfg, seed=3)
-    states = _states(cfg, B, T, cfg.n_layers, 4)
-    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=torch.Generator().manual_seed(5))
+    cfg, w, emb, states, ids = decoder_case(cfg_kw, B, n_opt, t, T, T_E2E)
     dec = DenseDecoder(DecoderConfig(**cfg_kw), w, emb, DEV, max_pos=T + t + 8)
     return cfg, w, emb, states, ids, dec, _gpu_states(states, T + 32)
 
 
 @pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
 def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
-    """Every stage of every layer against the oracle fed the GPU's own input to that stage. The RMSNorm / SwiGLU
-    quantizers are held to the row-kernel bar (their fp32 sums and rsqrt / exp may differ in the last bit); the
-    GEMMs (+residual) and q/k norm + RoPE downstream of the GPU's own int8 bytes are bit-exact; the attention is
-    held to its 2e-3 bar. The kernels are deterministic, so re-running a quantizer reproduces the layer's bytes."""
+    """Every stage of every layer against the oracle fed the GPU's own input to that stage: the quantizers, GEMMs
+    (+ residual), q/k norm + RoPE and SwiGLU are bit-exact; the attention is held to its 2e-3 bar against the
+    reference's bf16-materialized state. The kernels are deterministic, so re-running a quantizer reproduces the
+    layer's bytes. Finally the oracle's readout of the GPU's final hidden states equals the GPU's within 1e-6."""
     from opendecider_amd import kernels
     cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
     R, M = B * n_opt, B * n_opt * t
@@ -189,22 +205,16 @@ def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
         qkv_g, attn_g, mid_g, hm_g, out_g = (ws["qkv"].cpu(), ws["attn"].cpu(), mid.cpu(), ws["hmlp"].cpu(), h.cpu())
         # RMSNorm 1 + quantize, then QKV GEMM + q/k norm + RoPE from the GPU's bytes
         xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["qkv"].inv_s)
-        _close_quant(xq, sx, *oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps), ql["wqkv"][2]))
+        _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps), ql["wqkv"][2]), f"layer {li}: ln1")
         qkv_lin = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wqkv"][0]), sx.cpu(), ql["wqkv"][1])
-        assert torch.equal(qkv_g[:, (Hq + Hk) * D:], qkv_lin[:, (Hq + Hk) * D:]), f"layer {li}: QKV GEMM (v part)"
         qkv = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
-        # per-head RMSNorm sums D squares in another order than the oracle, so a normed value may differ by one
-        # bf16 step; RoPE mixes each pair (i, i + D/2), so the bound is one step of the pair's norm
-        gq = qkv_g[:, :(Hq + Hk) * D].float().reshape(M, Hq + Hk, 2, D // 2)
-        rq = qkv[:, :(Hq + Hk) * D].float().reshape(M, Hq + Hk, 2, D // 2)
-        pair = rq.pow(2).sum(2, keepdim=True).sqrt()
-        assert ((gq - rq).abs() <= pair * 2.0 ** -6 + 2.0 ** -14).all(), f"layer {li}: q/k norm + RoPE"
+        assert torch.equal(qkv_g.view(torch.int16), qkv.view(torch.int16)), f"layer {li}: QKV GEMM + q/k norm + RoPE"
         # attention
         qh = qkv_g[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
         kh = qkv_g[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
         vh = qkv_g[:, (Hq + Hk) * D:].reshape(R, t, Hk, D).transpose(1, 2)
         (kq, ks), (vq, vs) = states[li]
-        o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, None, row_state)
+        o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, None, row_state, dequant="bf16")
         assert_close_rel(attn_g.float(), o.transpose(1, 2).reshape(M, Hq * D), what=f"layer {li}: attention")
         # O projection + residual (the attention output's quantizer is bit-exact)
         h_mid = oq.w8a8_linear(attn_g, *ql["wo"][:2], inv_s=ql["wo"][2], residual=h_in)[0]
@@ -213,12 +223,10 @@ def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
         # is bit-exact to the GEMM epilogue, its SwiGLU uses the host exp (one step on bf16(silu(g)) can become two on
         # h after the product with u), so h is held to two bf16 steps on <= 0.5%
         xq, sx = kernels.rmsnorm_quant(mid.clone(), L["ln2"], cfg.eps, L["gu"].inv_s)
-        _close_quant(xq, sx, *oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps), ql["wgu"][2]))
+        _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps), ql["wgu"][2]), f"layer {li}: ln2")
         gu = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wgu"][0]), sx.cpu(), ql["wgu"][1])
         hm = od.swiglu(gu, cfg.ffn)
-        d = (hm_g.float() - hm.float()).abs()
-        assert (d <= hm.float().abs() * 2.0 ** -6 + 2.0 ** -120).all() and (d > 0).float().mean() <= 5e-3, \
-            f"layer {li}: gate+up GEMM + SwiGLU"
+        assert torch.equal(hm_g.view(torch.int16), hm.view(torch.int16)), f"layer {li}: gate+up GEMM + SwiGLU"
         # the same h through the unfused GPU path (gate+up GEMM in the original row order, then SwiGLU + quantize)
         # gives the same bytes as quantizing the fused GEMM's h
         gu_plain = kernels.w8a8_gemm(xq, sx, L["gu"].q.view(cfg.ffn, 2, -1).transpose(0, 1).reshape(2 * cfg.ffn, -1),
@@ -227,25 +235,35 @@ def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
         xq, sx = kernels.act_quant(ws["hmlp"], L["down"].inv_s)
         assert torch.equal(xq, xq2) and torch.equal(sx, sx2), f"layer {li}: fused SwiGLU vs unfused"
         # quantize, down GEMM + residual from the GPU's bytes
-        _close_quant(xq, sx, *oq.act_quant(hm_g, ql["wdown"][2]))
+        _exact_quant(xq, sx, *oq.act_quant(hm_g, ql["wdown"][2]), f"layer {li}: SwiGLU output quantizer")
         h_out = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wdown"][0]), sx.cpu(), ql["wdown"][1], residual=mid_g)
         assert torch.equal(out_g, h_out), f"layer {li}: down GEMM + residual"
+    lp = dec.readout(h, B, n_opt, t)
+    ref = od.readout(h.cpu(), w["final_norm"], w["head"], w["none_logit"], cfg, B, n_opt, t, T_E2E)
+    assert (lp.cpu() - ref).abs().max().item() <= 1e-6, "readout"
+
+
+def _assert_e2e(lp, ref, what):
+    """The path's end-to-end bar: probabilities within 1e-4 absolute, log-probabilities within 2e-3 relative; the
+    T = 1 difference (log-probs at T = 1 are log_softmax(T_E2E * lp), the same logits) is printed."""
+    lp = lp.cpu()
+    dp = (lp.exp() - ref.exp()).abs().max().item()
+    dl = ((lp - ref).abs() / ref.abs()).max().item()
+    one = lambda x: torch.log_softmax(x * T_E2E, -1).exp()
+    dp1 = (one(lp) - one(ref)).abs().max().item()
+    print(f"{what}: T={T_E2E:g}: max |dp| {dp:.2e}, max log-prob rel {dl:.2e}; at T=1 (diagnostic) max |dp| {dp1:.2e}")
+    assert dp <= PROB_ABS and dl <= REL, (dp, dl)
 
 
 @pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
 def test_decision_forward_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, T):
-    """End to end the GPU forward and the oracle differ only through the attention output's bf16 rounding, which
-    dynamic int8 activation quantization amplifies (one step on a token's absmax element rescales the token). The
-    bar: the probability difference is within the oracle's own response to a perturbation of that size (one bf16
-    step in 10% of its attention outputs, every layer), and never above 1e-2; option order invariance <= 1e-6."""
+    """The GPU forward and the oracle (the reference's arithmetic, state materialized in bf16) each run on their own:
+    the end-to-end bar at T_E2E, and option-order invariance <= 1e-6."""
     cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
+    print(f"{name}: e2e B={B} options={n_opt} t={t} T={T}", flush=True)
     ref = od.decision_forward(ids, w, emb, cfg, states, T)
-    nudged = od.decision_forward(ids, w, emb, cfg, states, T, attn_hook=lambda a: od.nudge_bf16(a, 0.10, 17))
     lp = dec.score(ids.to(DEV), gs)
-    dp = (lp.exp().cpu() - ref.exp()).abs().max().item()
-    dp_nudge = (nudged.exp() - ref.exp()).abs().max().item()
-    print(f"{name}: max |dp| GPU vs oracle {dp:.2e}; oracle vs nudged oracle {dp_nudge:.2e}")
-    assert dp <= max(3 * dp_nudge, PROB_ABS) and dp <= 1e-2
+    _assert_e2e(lp, ref, name)
     perm = torch.randperm(n_opt, generator=torch.Generator().manual_seed(6))
     lp_p = dec.score(ids[:, perm].to(DEV), gs)
     assert (lp_p[:, :n_opt].exp() - lp[:, perm.to(DEV)].exp()).abs().max().item() <= 1e-6
@@ -254,7 +272,7 @@ def test_decision_forward_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, T):
 PREFILL_CASES = [
     ("tiny_d64", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500), 2, 5, 4, 70,
      [24, 7]),
-    ("9b_dims_2_layers", dict(n_layers=2, vocab=1000), 2, 6, 16, 256, [256]),
+    ("9b_dims_2_layers", dict(n_layers=2, vocab=1000), 2, 32, 16, 256, [256]),
 ]
 
 
@@ -262,6 +280,7 @@ def _prefill_setup(cfg_kw, B, S, cap):
     from opendecider_amd.decoder import DecoderConfig, DenseDecoder
     cfg = od.DecoderConfig(**cfg_kw)
     w = od.make_weights(cfg, seed=7)
+    w["temperature"] = T_E2E
     emb = od.make_embedding(cfg, seed=7)
     dec = DenseDecoder(DecoderConfig(**cfg_kw), w, emb, DEV, max_pos=cap + 64)
     return cfg, w, emb, dec
@@ -272,9 +291,8 @@ def test_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, S, rec
     """The decision forward from token ids: the states are prefilled through every layer (causal wide_attention on
     the new tokens' bf16 K/V, K/V quantized into per-layer int8 caches), then records are appended (each attends
     the int8 cache + itself, and only its K/V are quantized and appended), then the option rows are scored.
-    Layer-0 cache bytes are held to the row-kernel bar (one int8 step, few bytes off); the probabilities to the
-    oracle's own sensitivity to rounding-size perturbations of every attention output (prefill and rows), never
-    above 1e-2."""
+    Layer-0 cache bytes are bit-exact (layer 0's K/V depend on no attention); the probabilities are held to the
+    end-to-end bar at T_E2E."""
     cap = S + sum(records)
     cfg, w, emb, dec = _prefill_setup(cfg_kw, B, S, cap)
     g = torch.Generator().manual_seed(8)
@@ -288,10 +306,10 @@ def test_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, S, rec
     torch.cuda.synchronize()
     _, kv_ref = od.prefill_forward(ids_state, w, emb, cfg)
     for (kc, vc), ((kq, ks), (vq, vs)) in zip(caches[:1], kv_ref[:1]):
-        _close_quant(kc.q[:, :, :S].reshape(-1, cfg.head_dim), kc.scale[:, :, :S].reshape(-1),
-                     kq.reshape(-1, cfg.head_dim), ks.reshape(-1))
-        _close_quant(vc.q[:, :, :S].reshape(-1, cfg.head_dim), vc.scale[:, :, :S].reshape(-1),
-                     vq.reshape(-1, cfg.head_dim), vs.reshape(-1))
+        _exact_quant(kc.q[:, :, :S].reshape(-1, cfg.head_dim), kc.scale[:, :, :S].reshape(-1),
+                     kq.reshape(-1, cfg.head_dim), ks.reshape(-1), "layer 0 K cache")
+        _exact_quant(vc.q[:, :, :S].reshape(-1, cfg.head_dim), vc.scale[:, :, :S].reshape(-1),
+                     vq.reshape(-1, cfg.head_dim), vs.reshape(-1), "layer 0 V cache")
     n0 = S
     for r in recs:
         dec.prefill(r.to(DEV), caches)
@@ -301,14 +319,4 @@ def test_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, S, rec
     lp = dec.score(ids.to(DEV), caches)
     ref = od.decision_forward(ids, w, emb, cfg, kv_ref, n0)
 
-    hook = lambda a: od.nudge_bf16(a, 0.10, 17)
-    _, kv_n = od.prefill_forward(ids_state, w, emb, cfg, attn_hook=hook)
-    m = S
-    for r in recs:
-        _, kv_n = od.prefill_forward(r, w, emb, cfg, state_kv=kv_n, n0=m, attn_hook=hook)
-        m += r.shape[1]
-    nudged = od.decision_forward(ids, w, emb, cfg, kv_n, n0, attn_hook=hook)
-    dp = (lp.exp().cpu() - ref.exp()).abs().max().item()
-    dp_nudge = (nudged.exp() - ref.exp()).abs().max().item()
-    print(f"{name}: max |dp| GPU vs oracle {dp:.2e}; oracle vs nudged oracle {dp_nudge:.2e}")
-    assert dp <= max(3 * dp_nudge, PROB_ABS) and dp <= 1e-2
+    _assert_e2e(lp, ref, f"{name} (prefilled)")

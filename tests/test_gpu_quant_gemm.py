@@ -258,3 +258,30 @@ def test_quantizer_near_half_integer_quotients(gpu_lib):
     ones = torch.ones(K, dtype=torch.bfloat16, device=DEV)
     xq1, sx1 = kernels.act_quant(x.to(DEV), ones)
     assert torch.equal(xq1.cpu()[:, :K], rq) and torch.equal(sx1.cpu(), rs[:, 0])
+
+
+@pytest.mark.parametrize("K", [4096, 200, 128])
+def test_quantizers_nan_and_inf_rows(gpu_lib, K):
+    """torch's rule for non-finite rows (quant.py:38-40 on CPU): a row holding a NaN gets a NaN scale (amax and
+    clamp_min propagate it) and zero bytes; a row holding an infinity gets an infinite scale and zero bytes (x / inf
+    = 0, inf / inf = NaN -> 0). Both quantizers (per-token activations, per-(token, head) K/V append) follow it, on
+    the vector and the scalar paths."""
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(K)
+    x = torch.randn(6, K, generator=g).to(torch.bfloat16)
+    x[1, 7] = float("nan")
+    x[3, K - 1] = float("inf")
+    x[4, 0] = float("-inf")
+    x[5, 2] = float("nan")
+    x[5, 3] = float("inf")
+    rq, rs = oq.quantize_rows(x)
+    xq, sx = kernels.act_quant(x.to(DEV))
+    assert torch.equal(xq.cpu(), rq)
+    assert torch.equal(sx.cpu().view(torch.int32)[[0, 2]], rs[[0, 2], 0].view(torch.int32))
+    assert torch.isnan(sx.cpu()[[1, 5]]).all() and torch.isinf(sx.cpu()[[3, 4]]).all()
+    if K % 16 == 0 and K <= 256:
+        q = torch.full((1, 6, 4, K), 55, dtype=torch.int8, device=DEV)
+        s = torch.full((1, 6, 4), -1.0, device=DEV)
+        kernels.kv_quant_append(x.view(1, 6, 1, K).to(DEV), q, s, 1)
+        assert torch.equal(q[0, :, 1].cpu(), rq) and (q[0, :, 0] == 55).all() and (q[0, :, 2:] == 55).all()
+        assert torch.isnan(s[0, [1, 5], 1].cpu()).all() and torch.isinf(s[0, [3, 4], 1].cpu()).all()

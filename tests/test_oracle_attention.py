@@ -107,9 +107,14 @@ def test_branched_int8_rows_read_their_state():
     ks, vs = torch.rand(Ns, Hkv, T, generator=g) * 0.02, torch.rand(Ns, Hkv, T, generator=g) * 0.02
     q, k, v = _rand(g, R, Hq, t, D), _rand(g, R, Hkv, t, D), _rand(g, R, Hkv, t, D)
     rs = torch.tensor([1, 0, 1, 1, 0])
-    out, lse = oa.branched_attention_int8(q, k, v, kq, ks, vq, vs, 0.3, row_state=rs)
+    out, lse = oa.branched_attention_int8(q, k, v, kq, ks, vq, vs, 0.3, row_state=rs, dequant="fp32")
+    outb, _ = oa.branched_attention_int8(q, k, v, kq, ks, vq, vs, 0.3, row_state=rs)  # default: bf16 materialize
     for r in range(R):
         s = int(rs[r])
+        Kb = (kq[s].to(torch.bfloat16) * ks[s][..., None].to(torch.bfloat16)).float()
+        Vb = (vq[s].to(torch.bfloat16) * vs[s][..., None].to(torch.bfloat16)).float()
+        ob, _ = oa.split_attention(q[r:r + 1], k[r:r + 1], v[r:r + 1], Kb, Vb, None, 0.3)
+        assert torch.allclose(outb[r], ob[0], atol=1e-6)
         Kp = kq[s].float() * ks[s][..., None]
         Vp = vq[s].float() * vs[s][..., None]
         o1, l1 = oa.split_attention(q[r:r + 1], k[r:r + 1], v[r:r + 1], Kp, Vp, None, 0.3)

@@ -163,3 +163,122 @@ def test_prefill_append_keeps_cache_and_positions():
                            lw["q_norm"], lw["k_norm"], cos, sin, torch.arange(9).repeat(2))
     k0 = qkv0[:, Hq * D:(Hq + Hk) * D].reshape(2, 9, Hk, D).transpose(1, 2).contiguous()
     assert not torch.equal(oq.quantize_rows(k0)[0], kq)
+
+
+# ---- the correctly rounded RMSNorm factor and SiLU that the row kernels reproduce bit for bit
+
+def _nearest_f32(d):
+    """The fp32 value nearest to the Decimal d (ties to even), by comparing the neighbours of a float64 guess."""
+    import decimal
+    import numpy as np
+    f = np.float32(float(d))
+    best = None
+    for c in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
+        err = abs(decimal.Decimal(float(c)) - d)
+        key = (err, int(np.array(c).view(np.int32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, c)
+    return float(best[1])
+
+
+def test_rms_factor_is_the_correctly_rounded_value():
+    """rms_factor = RN32(1 / sqrt(sum(x^2) / K + eps32)), checked against 60-digit decimal arithmetic on rows that
+    span many binades, and within 2 fp32 ulps of the reference's fp32 expression torch.rsqrt(x.pow(2).mean() + eps)."""
+    import decimal
+    decimal.getcontext().prec = 60
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(24, 300, generator=g) * torch.exp2(torch.randint(-12, 12, (24, 300), generator=g).float()))
+    x = x.to(torch.bfloat16)
+    x[3] = 0
+    r = od.rms_factor(x, 1e-6)
+    eps = decimal.Decimal(float(torch.tensor(1e-6, dtype=torch.float32)))
+    for i in range(x.shape[0]):
+        ss = sum(decimal.Decimal(float(v)) ** 2 for v in x[i].float().tolist())
+        exact = 1 / (ss / x.shape[1] + eps).sqrt()
+        assert r[i, 0].item() == _nearest_f32(exact), i
+    ref32 = torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6)
+    ulp = (r.view(torch.int32) - ref32.view(torch.int32)).abs()
+    assert ulp.max().item() <= 2
+
+
+def test_silu_bf16_is_the_correctly_rounded_value_on_all_bf16_inputs():
+    """silu_bf16(g) = bf16(RN32(g / (1 + exp(-g)))) on all 65536 bf16 inputs: checked against 40-digit decimal
+    arithmetic on a spread sample of the finite nonzero inputs with |g| <= 200 (beyond that the result is g or a tiny
+    negative, checked directly), and equal bit for bit to torch's own bf16 F.silu (the reference's arithmetic) on every
+    input except g < -88, where torch's fp32 exp(-g) overflows and it returns -0 instead of the tiny exact value."""
+    import decimal
+    decimal.getcontext().prec = 40
+    g = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    s = od.silu_bf16(g)
+    gf = g.float()
+    fin = torch.isfinite(gf) & (gf != 0) & (gf.abs() <= 200)
+    idx = fin.nonzero().squeeze(1).tolist()
+    for i in idx[::7] + idx[1::97]:  # a seventh of the inputs plus a spread sample (the full set takes ~10 s more)
+        d = decimal.Decimal(float(gf[i]))
+        exact = d / (1 + (-d).exp())
+        want = torch.tensor(_nearest_f32(exact), dtype=torch.float32).to(torch.bfloat16)
+        assert s[i].view(torch.int16) == want.view(torch.int16), (gf[i].item(), s[i].item(), want.item())
+    big = (gf.abs() > 200) & torch.isfinite(gf)
+    assert torch.equal(s[big & (gf > 0)], g[big & (gf > 0)])
+    assert (s[big & (gf < 0)].float().abs() <= 2.0 ** -120).all()
+    assert s[gf == 0].float().eq(0).all() and torch.isnan(s[torch.isnan(gf)]).all()
+    assert s[gf == float("inf")].float().eq(float("inf")).all() and torch.isnan(s[gf == float("-inf")]).all()
+    ref = torch.nn.functional.silu(g)
+    ok = torch.isfinite(ref) & ~(gf < -88)  # below -88 torch's fp32 exp(-g) overflows and it returns -0
+    assert torch.equal(s[ok].view(torch.int16), ref[ok].view(torch.int16))
+
+
+# ---- the end-to-end bar of the GPU tests: what it can see at the harness's decision temperature
+
+E2E_SCORING = (dict(n_layers=2, vocab=1000), 2, 32, 16, 256)   # tests/test_gpu_decoder.py CASES["9b_dims_2_layers"]
+T_E2E = 16.0
+
+
+def test_end_to_end_bar_separates_kernel_mistakes_from_the_oracles_own_noise():
+    """At the GPU end-to-end test's configuration and temperature: the oracle with float64 attention accumulation
+    moves the option probabilities by well under 1e-4 (its own rounding floor, 2.2e-5), while planted mistakes of the
+    kind a kernel can make move them past the 1e-4 bar: a wrong GQA head mapping (3.9e-4), the keys of another state
+    (2.9e-4), the SmoothQuant scale dropped before the O projection (2.5e-4). Smaller planted mistakes (one position
+    off in RoPE, a non-causal own block, the V scale of the neighbouring token) land near 1e-4 (0.9-1.3e-4); the
+    stage-by-stage GPU test, bit-exact outside the attention, is what pins those."""
+    from helpers import decoder_case
+    from oracle import attention as oa
+    cfg_kw, B, n_opt, t, T = E2E_SCORING
+    cfg, w, emb, states, ids = decoder_case(cfg_kw, B, n_opt, t, T, T_E2E)
+    ref = od.decision_forward(ids, w, emb, cfg, states, T)
+
+    def dp(x):
+        return (x.exp() - ref.exp()).abs().max().item()
+
+    floor = dp(od.decision_forward(ids, w, emb, cfg, states, T, attn_dtype=torch.float64))
+    orig = oa.branched_attention_int8
+    Hq, Hkv = cfg.n_heads, cfg.n_kv_heads
+    src = (torch.arange(Hq) % Hkv) * (Hq // Hkv) + torch.arange(Hq) // Hkv
+    inv = torch.argsort(src)
+
+    def gqa(q, *a, **k):  # query head h reads KV head h % Hkv instead of h // (Hq / Hkv)
+        o, lse = orig(q[:, src], *a, **k)
+        return o[:, inv], lse[:, inv]
+
+    oa.branched_attention_int8 = gqa
+    try:
+        wrong_gqa = dp(od.decision_forward(ids, w, emb, cfg, states, T))
+    finally:
+        oa.branched_attention_int8 = orig
+    other = [((kq.flip(0), ks.flip(0)), v) for (kq, ks), v in states]
+    wrong_state = dp(od.decision_forward(ids, w, emb, cfg, other, T))
+    orig_q = od.quantize_layer
+
+    def no_smooth_o(lw):
+        d = orig_q(lw)
+        d["wo"] = (d["wo"][0], d["wo"][1], None)
+        return d
+
+    od.quantize_layer = no_smooth_o
+    try:
+        dropped = dp(od.decision_forward(ids, w, emb, cfg, states, T))
+    finally:
+        od.quantize_layer = orig_q
+    print(f"floor {floor:.2e}; GQA {wrong_gqa:.2e}, other state {wrong_state:.2e}, no 1/s {dropped:.2e}")
+    assert floor <= 3e-5
+    assert min(wrong_gqa, wrong_state, dropped) >= 2e-4
