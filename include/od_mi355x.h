@@ -226,7 +226,25 @@ int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq, const flo
                   void* img, int64_t img_bytes, od_stream_t stream);
 
 /*
- * od_branched_attn_staged — od_branched_attn_split over block images from od_attn_stage: each workgroup copies the
+ * od_attn_stage_bf16 — block images of a DENSE bf16 state, for od_branched_attn_staged.
+ * Replaces: the prefix part of _split_attention when its caller passes materialized bf16 K/V
+ * (src/opendecider/prefix_attn.py:43-57, called at :127 with K/V from :145-149), i.e. the reference's
+ * wide_attention prefix call (wide_attention.py:70-91) and its LSE merge with the own part (prefix_attn.py:74-76):
+ * the images feed the same one-softmax attention as the int8 state's.
+ *   k, v      bf16 [Ns, Hkv, T, D] at element strides (skb, skh, skt) / (svb, svh, svt) (multiples of 8), last dim
+ *             contiguous, 16-byte aligned
+ *   kvalid    uint8 [Ns, T] or NULL (as od_branched_attn)
+ *   scale     the softmax scale of the attention calls that will read the images
+ *   img       device buffer of at least od_attn_stage_size bytes, 16-byte aligned (out)
+ * Keys are used as they are; values become fp16(v 2^-eb) with 2^eb above the block's largest |v| (exact down to
+ * 2^(eb - 14)). D in {64, 128}. One launch on `stream`.
+ */
+int od_attn_stage_bf16(const uint16_t* k, int64_t skb, int64_t skh, int64_t skt, const uint16_t* v, int64_t svb,
+                       int64_t svh, int64_t svt, const uint8_t* kvalid, int64_t Ns, int64_t Hkv, int64_t T, int64_t D,
+                       float scale, void* img, int64_t img_bytes, od_stream_t stream);
+
+/*
+ * od_branched_attn_staged — od_branched_attn_split over block images from od_attn_stage / od_attn_stage_bf16: each workgroup copies the
  * images straight into LDS (global_load_lds) instead of converting the int8 state itself.
  * Replaces: the same reference code as od_branched_attn.
  *   img, img_bytes   the images of the state (Ns, Hkv, T, D and scale as passed to od_attn_stage; the images carry
@@ -262,23 +280,6 @@ int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const
                  const uint8_t* kvalid, int64_t smb, uint16_t* out, int64_t sob, int64_t soh, int64_t sot, float* lse,
                  int64_t B, int64_t H, int64_t G, int64_t T, int64_t S, int64_t DK, int64_t DV, int causal,
                  float scale, od_stream_t stream);
-
-/*
- * od_lse_merge — merge two attention partials by their log-sum-exp.
- * Replaces: the merge of _split_attention's prefix and own parts (src/opendecider/prefix_attn.py:74-76), used when
- * the prefix arrives as dense bf16 K/V (the reference's _forward passes materialized K/V, prefix_attn.py:127,145-149)
- * and the two parts come from od_wide_attn.
- *   o1, o2  bf16 [n, H, t, D] at element strides (s1r, s1h, s1t) / (s2r, s2h, s2t), last dim contiguous
- *   l1, l2  fp32 [n, H, t] at element strides (t1r, t1h, t1t) / (t2r, t2h, t2t): natural-log LSE of each part
- *   out     bf16 [n, H, t, D], strides (sor, soh, sot) (out); lse fp32 [n, H, t] contiguous or NULL (out)
- *   m = max(l1, l2), w_i = exp(l_i - m), out = bf16((float(o1) w1 + float(o2) w2) / (w1 + w2)), lse = m + log(w1 + w2);
- *   a slot with both parts empty (-inf) gets 0 and -inf. Requires D % 8 == 0, bf16 strides multiples of 8 and
- *   16-byte aligned o1 / o2 / out.
- */
-int od_lse_merge(const uint16_t* o1, int64_t s1r, int64_t s1h, int64_t s1t, const float* l1, int64_t t1r, int64_t t1h,
-                 int64_t t1t, const uint16_t* o2, int64_t s2r, int64_t s2h, int64_t s2t, const float* l2, int64_t t2r,
-                 int64_t t2h, int64_t t2t, uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t n,
-                 int64_t H, int64_t t, int64_t D, od_stream_t stream);
 
 /*
  * Row kernels of the dense decoder layer that carries the path in the decision-forward harness (not reference

@@ -49,8 +49,8 @@ SIGNATURES = {
                         _i64, _c_ptr],
     "od_qk_norm_rope_kv_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64,
                                   _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _c_ptr],
-    "od_lse_merge": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64,
-                     _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64, _c_ptr],
+    "od_attn_stage_bf16": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64,
+                           ctypes.c_float, _c_ptr, _i64, _c_ptr],
     "od_lm_head_logprob_ws": [_i64, _i64, _c_ptr],
     "od_lm_head_logprob": [_c_ptr, _i64, _c_ptr, _i64, ctypes.c_int, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64,
                            _c_ptr, _c_ptr, _i64, _c_ptr],

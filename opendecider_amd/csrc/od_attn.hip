@@ -1033,6 +1033,83 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(StageArgs p) {
   convert_block<D>(pr, reinterpret_cast<BlockImg<D>*>(p.img)[blk], p.scale_log2, p.dq);
 }
 
+// od_attn_stage_bf16: one workgroup per (block, KV head, state) writes the image of 64 keys of a dense bf16 state
+// (the reference's materialized K/V): the keys as they are beside the multiplier scale_log2, the values as
+// V' = fp16(v 2^-eb) with 2^eb above the block's largest |v| (exact while |v| >= 2^(eb - 14); smaller values become
+// fp16 subnormals, within 2^(eb - 25) of v), a masked key (past T or kvalid 0) with zero K and V, multiplier 1 and a
+// -inf bias, as convert_block writes them.
+struct StageBf16Args {
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint8_t* kvalid;
+  uint8_t* img;
+  int64_t skb, skh, skt, svb, svh, svt;
+  int Hkv, T, nb;
+  float scale_log2;
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void stage_bf16_kernel(StageBf16Args p) {
+  __shared__ float red[kWaves];
+  const int b = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int j0 = b * kBlockKeys;
+  BlockImg<D>& dst = reinterpret_cast<BlockImg<D>*>(p.img)[((int64_t)s * p.Hkv + g) * p.nb + b];
+  const uint16_t* kbase = p.k + (int64_t)s * p.skb + (int64_t)g * p.skh;
+  const uint16_t* vbase = p.v + (int64_t)s * p.svb + (int64_t)g * p.svh;
+  auto valid = [&](int key) {
+    return j0 + key < p.T && (!p.kvalid || p.kvalid[(int64_t)s * p.T + j0 + key] != 0);
+  };
+  constexpr int kChunks = kBlockKeys * D / 8;  // 16-byte chunks of 8 bf16
+  for (int cid = tid; cid < kChunks; cid += kThreads) {
+    const int key = cid / (D / 8), c = cid % (D / 8);
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (valid(key)) val = *reinterpret_cast<const uint4*>(kbase + (int64_t)(j0 + key) * p.skt + 8 * c);
+    *reinterpret_cast<uint4*>(&dst.k[k_off<D>(key, c)]) = val;
+  }
+  int dg, kg;
+  vmap<D>(tid, dg, kg);
+  uint4 vv[4];
+  float vmax = 0.0f;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    vv[a] = make_uint4(0, 0, 0, 0);
+    if (tid < 2 * D && valid(4 * kg + a))
+      vv[a] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(j0 + 4 * kg + a) * p.svt + 8 * dg);
+    const uint32_t w[4] = {vv[a].x, vv[a].y, vv[a].z, vv[a].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      vmax = fmaxf(vmax, fmaxf(fabsf(__uint_as_float(w[e] << 16)), fabsf(__uint_as_float(w[e] & 0xffff0000u))));
+  }
+  vmax = od_wave_max_dpp(vmax);
+  if ((tid & 63) == 0) red[tid >> 6] = vmax;
+  __syncthreads();
+  vmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const bool ok = valid(tid & 63);
+  const bool any = __builtin_amdgcn_ballot_w64(ok) != 0;
+  const int eb = any ? exp_above(vmax) : kNoFrame;
+  if (tid < 2 * D) {
+    const float f = any ? ldexpf(1.0f, -eb) : 0.0f;
+    const int jj0 = jj_of(4 * kg);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {  // d = 8 dg + e: the 4 keys' values
+      float x[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const uint32_t w = e < 2 ? vv[a].x : e < 4 ? vv[a].y : e < 6 ? vv[a].z : vv[a].w;
+        x[a] = __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16)) * f;
+      }
+      const uint2 hv = make_uint2(pack_h2(x[0], x[1]), pack_h2(x[2], x[3]));
+      *reinterpret_cast<uint2*>(&dst.vt[vt_off(8 * dg + e, jj0 >> 3) + (jj0 & 7)]) = hv;
+    }
+  }
+  if (tid < kBlockKeys) {
+    dst.gk[tid] = ok ? p.scale_log2 : 1.0f;
+    dst.kb[tid] = ok ? 0.0f : -INFINITY;
+  }
+  if (tid == 0) *reinterpret_cast<int4*>(dst.info) = make_int4(0, eb, __builtin_amdgcn_ballot_w64(!ok) != 0, 0);
+}
+
 // LSE merge of the key-range splits (prefix_attn.py:74-76 generalised to n parts): M = max_s lse_s,
 // w_s = exp(lse_s - M), out = sum_s w_s o_s / sum_s w_s (bf16), lse = M + log(sum_s w_s); no visible key in any
 // split -> 0 and -inf. One thread per (slot, 8 values of d).
@@ -1075,54 +1152,6 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
   *reinterpret_cast<uint2*>(op) = make_uint2(w4[0], w4[1]);
   *reinterpret_cast<uint2*>(op + 4) = make_uint2(w4[2], w4[3]);
   if (p.lse && d0 == 0) p.lse[slot] = wsum > 0.0f ? M + __logf(wsum) : -INFINITY;
-}
-
-// Merge of two attention partials by their log-sum-exp (prefix_attn.py:74-76): m = max(l1, l2),
-// w_i = exp(l_i - m), out = bf16((o1 w1 + o2 w2) / (w1 + w2)) from the bf16 partials read as fp32, lse = m +
-// log(w1 + w2); both parts empty (m = -inf) -> 0 and -inf. One thread per (slot, 8 values of d).
-struct MergeArgs {
-  const uint16_t* o1;
-  const float* l1;
-  const uint16_t* o2;
-  const float* l2;
-  uint16_t* out;
-  float* lse;
-  int64_t s1r, s1h, s1t, t1r, t1h, t1t, s2r, s2h, s2t, t2r, t2h, t2t, sor, soh, sot;
-  int64_t n, H, t, D;
-};
-
-__global__ __launch_bounds__(256) void lse_merge_kernel(MergeArgs p) {
-  const int64_t groups = p.D / 8;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t slot = gid / groups;
-  if (slot >= p.n * p.H * p.t) return;
-  const int64_t d0 = (gid % groups) * 8;
-  const int64_t r = slot / (p.H * p.t), h = (slot / p.t) % p.H, i = slot % p.t;
-  const float l1 = p.l1[r * p.t1r + h * p.t1h + i * p.t1t], l2 = p.l2[r * p.t2r + h * p.t2h + i * p.t2t];
-  const float m = fmaxf(l1, l2);
-  float w1 = 0.0f, w2 = 0.0f;
-  if (m != -INFINITY) {
-    w1 = expf(l1 - m);
-    w2 = expf(l2 - m);
-  }
-  const float den = w1 + w2;
-  const uint4 a = *reinterpret_cast<const uint4*>(p.o1 + r * p.s1r + h * p.s1h + i * p.s1t + d0);
-  const uint4 b = *reinterpret_cast<const uint4*>(p.o2 + r * p.s2r + h * p.s2h + i * p.s2t + d0);
-  const uint32_t aw[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-  uint32_t res[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float y[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const float x1 = __uint_as_float(k ? (aw[e] & 0xffff0000u) : (aw[e] << 16));
-      const float x2 = __uint_as_float(k ? (bw[e] & 0xffff0000u) : (bw[e] << 16));
-      y[k] = den > 0.0f ? (x1 * w1 + x2 * w2) / den : 0.0f;
-    }
-    res[e] = (uint32_t)od_f32_to_bf16(y[0]) | ((uint32_t)od_f32_to_bf16(y[1]) << 16);
-  }
-  *reinterpret_cast<uint4*>(p.out + r * p.sor + h * p.soh + i * p.sot + d0) = make_uint4(res[0], res[1], res[2], res[3]);
-  if (p.lse && d0 == 0) p.lse[slot] = den > 0.0f ? m + logf(den) : -INFINITY;
 }
 
 }  // namespace
@@ -1269,27 +1298,30 @@ extern "C" int od_branched_attn_staged(const uint16_t* q, int64_t sqr, int64_t s
                          Hkv, t, D, Ns, T, T, scale, OD_DEQUANT_BF16, nsplit, ws, ws_floats, stream);
 }
 
-extern "C" int od_lse_merge(const uint16_t* o1, int64_t s1r, int64_t s1h, int64_t s1t, const float* l1, int64_t t1r,
-                            int64_t t1h, int64_t t1t, const uint16_t* o2, int64_t s2r, int64_t s2h, int64_t s2t,
-                            const float* l2, int64_t t2r, int64_t t2h, int64_t t2t, uint16_t* out, int64_t sor,
-                            int64_t soh, int64_t sot, float* lse, int64_t n, int64_t H, int64_t t, int64_t D,
-                            od_stream_t stream) {
-  if (n < 0 || H < 0 || t < 0 || D < 8 || D % 8) return OD_ERR_SHAPE;
-  if (n == 0 || H == 0 || t == 0) return OD_OK;
-  if (!o1 || !l1 || !o2 || !l2 || !out) return OD_ERR_NULL;
-  const int64_t bstr[] = {s1r, s1h, s1t, s2r, s2h, s2t, sor, soh, sot};
-  for (int64_t v : bstr)
-    if (v < 0 || v % 8) return OD_ERR_ALIGN;
-  const int64_t lstr[] = {t1r, t1h, t1t, t2r, t2h, t2t};
-  for (int64_t v : lstr)
-    if (v < 0) return OD_ERR_SHAPE;
-  if (!od_aligned16(o1) || !od_aligned16(o2) || !od_aligned16(out)) return OD_ERR_ALIGN;
-  const int64_t threads = n * H * t * (D / 8);
-  if (threads > ((int64_t)1 << 40)) return OD_ERR_SHAPE;
-  MergeArgs a{o1, l1, o2, l2, out, lse, s1r, s1h, s1t, t1r, t1h, t1t, s2r, s2h, s2t, t2r, t2h, t2t, sor, soh, sot,
-              n, H, t, D};
-  const int64_t blocks = (threads + 255) / 256;
-  if (blocks > 0x7fffffff) return OD_ERR_SHAPE;
-  lse_merge_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(a);
+
+extern "C" int od_attn_stage_bf16(const uint16_t* k, int64_t skb, int64_t skh, int64_t skt, const uint16_t* v,
+                                  int64_t svb, int64_t svh, int64_t svt, const uint8_t* kvalid, int64_t Ns,
+                                  int64_t Hkv, int64_t T, int64_t D, float scale, void* img, int64_t img_bytes,
+                                  od_stream_t stream) {
+  if (Ns < 1 || Hkv < 1 || T < 0) return OD_ERR_SHAPE;
+  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (T == 0) return OD_OK;
+  if (!k || !v || !img) return OD_ERR_NULL;
+  const int64_t strides[] = {skb, skh, skt, svb, svh, svt};
+  for (int64_t st : strides)
+    if (st < 0 || st % 8) return OD_ERR_ALIGN;
+  if (!od_aligned16(k) || !od_aligned16(v) || !od_aligned16(img)) return OD_ERR_ALIGN;
+  const int64_t nb = (T + kBlockKeys - 1) / kBlockKeys;
+  if (img_bytes < stage_blocks(Ns, Hkv, T) * stage_block_bytes(D)) return OD_ERR_SHAPE;
+  if (nb > 0x7fffffff || Hkv > 65535 || Ns > 65535 || T > 0x7fffffff) return OD_ERR_SHAPE;
+  StageBf16Args a{k, v, kvalid, static_cast<uint8_t*>(img), skb, skh, skt, svb, svh, svt, (int)Hkv, (int)T, (int)nb,
+                  scale * 1.4426950408889634f};
+  dim3 grid((unsigned)nb, (unsigned)Hkv, (unsigned)Ns), block(kThreads);
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 128) {
+    stage_bf16_kernel<128><<<grid, block, 0, st>>>(a);
+  } else {
+    stage_bf16_kernel<64><<<grid, block, 0, st>>>(a);
+  }
   return od_launch_status();
 }

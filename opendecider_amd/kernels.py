@@ -318,6 +318,61 @@ def stage_state(kq, ks, vq, vs, length: int, scale: float, kvalid=None, out=None
     return out
 
 
+def stage_state_bf16(k, v, length: int, scale: float, kvalid=None, out=None):
+    """Block images of a DENSE bf16 state (od_attn_stage_bf16): k/v (Ns, Hkv, >= length, D) bf16 (any strides that
+    are multiples of 8 elements, last dim contiguous), the first `length` tokens, kvalid (Ns, length) uint8 or None.
+    Returns a uint8 device buffer for branched_attn_images."""
+    require_gpu(k, v, kvalid, out, name="stage_state_bf16")
+    _lib.bf16_bits(k)
+    _lib.bf16_bits(v)
+    Ns, Hkv, _, D = k.shape
+    if v.shape[:2] != (Ns, Hkv) or v.shape[3] != D or min(k.shape[2], v.shape[2]) < length:
+        raise ValueError("stage_state_bf16: k and v must be (Ns, Hkv, >= length, D)")
+    k, v = _rows_aligned(k), _rows_aligned(v)
+    nbytes = stage_size(Ns, Hkv, length, D)
+    if out is None or out.numel() < nbytes:
+        out = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=k.device)
+    check(lib().od_attn_stage_bf16(ptr(k), *k.stride()[:3], ptr(v), *v.stride()[:3], ptr(kvalid), Ns, Hkv,
+                                   int(length), D, float(scale), ptr(out), out.numel(), stream_of(k)),
+          "od_attn_stage_bf16")
+    return out
+
+
+def branched_attn_images(q, k_own, v_own, img, Ns: int, T: int, scale: float, row_start=None, max_rows=None,
+                         out=None, return_lse: bool = False, n_split=None):
+    """The branched attention over block images already built (stage_state / stage_state_bf16) for Ns states of T
+    keys: od_branched_attn_staged. q (R, Hq, t, D), k_own/v_own (R, Hkv, t, D) bf16; rows grouped by state through
+    row_start/max_rows (None: one state). Returns out [, lse] as branched_attn."""
+    require_gpu(q, k_own, v_own, img, row_start, out, name="branched_attn_images")
+    for x in (q, k_own, v_own):
+        _lib.bf16_bits(x)
+    R, Hq, t, D = q.shape
+    Hkv = k_own.shape[1]
+    if k_own.shape != (R, Hkv, t, D) or v_own.shape != (R, Hkv, t, D):
+        raise ValueError("branched_attn_images: own k/v must be (R, Hkv, t, D)")
+    if T > 0 and (img.dtype != torch.uint8 or img.numel() < stage_size(Ns, Hkv, T, D)):
+        raise ValueError("branched_attn_images: the block images are smaller than the state needs")
+    if row_start is None:
+        if Ns != 1:
+            raise ValueError("branched_attn_images: row_start is required with several states")
+        max_rows = R
+    elif row_start.dtype != torch.int32 or row_start.numel() != Ns + 1 or max_rows is None:
+        raise ValueError("branched_attn_images: row_start must be int32 (Ns + 1,) with max_rows")
+    q, k_own, v_own = _rows_aligned(q), _rows_aligned(k_own), _rows_aligned(v_own)
+    out = _check_out(out, (R, Hq, t, D), q.device, "branched_attn_images")
+    lse = torch.empty(R, Hq, t, dtype=torch.float32, device=q.device) if return_lse else None
+    tiles = -(-(int(max_rows) * t * (Hq // Hkv)) // 128)
+    if n_split is None:
+        n_split = split_count(tiles * Hkv * Ns, T)
+    ws = torch.empty(n_split * R * Hq * t * (D + 1), dtype=torch.float32, device=q.device) if n_split > 1 else None
+    check(lib().od_branched_attn_staged(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
+                                        *v_own.stride()[:3], ptr(img), img.numel(), ptr(row_start), int(max_rows),
+                                        ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv, t, D, Ns, T, float(scale),
+                                        int(n_split), ptr(ws), 0 if ws is None else ws.numel(), stream_of(q)),
+          "od_branched_attn_staged")
+    return (out, lse) if return_lse else out
+
+
 def uses_staging(max_rows: int, t: int, n_heads_q: int, n_heads_k: int) -> bool:
     """Whether branched_attn takes the staged path by itself for this row layout (at least STAGE_MIN_TILES slot
     tiles of 128 per (state, head))."""
@@ -431,28 +486,6 @@ def wide_attn(q, k, v, scale: float, kvalid=None, causal: bool = True, return_ls
     check(lib().od_wide_attn(ptr(q), *q.stride()[:3], ptr(k), *k.stride()[:3], ptr(v), *v.stride()[:3], ptr(kvalid),
                              kvalid.stride(0) if kvalid is not None else 0, ptr(out), *out.stride()[:3], ptr(lse), B, H,
                              G, T, S, DK, DV, 1 if causal else 0, float(scale), stream_of(q)), "od_wide_attn")
-    return (out, lse) if return_lse else out
-
-
-def lse_merge(o1: torch.Tensor, l1: torch.Tensor, o2: torch.Tensor, l2: torch.Tensor, out=None,
-              return_lse: bool = False):
-    """Merge two attention partials by their log-sum-exp (prefix_attn.py:74-76) with od_lse_merge: o1/o2 (n, H, t, D)
-    bf16 views (any strides, last dim contiguous), l1/l2 (n, H, t) fp32 views. Returns out (n, H, t, D) bf16
-    [, lse (n, H, t) fp32]."""
-    require_gpu(o1, l1, o2, l2, out, name="lse_merge")
-    for x in (o1, o2):
-        _lib.bf16_bits(x)
-    n, H, t, D = o1.shape
-    if o2.shape != o1.shape or l1.shape != (n, H, t) or l2.shape != (n, H, t):
-        raise ValueError("lse_merge: partials must be (n, H, t, D) with LSEs (n, H, t)")
-    if l1.dtype != torch.float32 or l2.dtype != torch.float32:
-        raise TypeError("lse_merge: LSEs must be float32")
-    o1, o2 = _rows_aligned(o1), _rows_aligned(o2)
-    out = _check_out(out, (n, H, t, D), o1.device, "lse_merge")
-    lse = torch.empty(n, H, t, dtype=torch.float32, device=o1.device) if return_lse else None
-    check(lib().od_lse_merge(ptr(o1), *o1.stride()[:3], ptr(l1), *l1.stride(), ptr(o2), *o2.stride()[:3], ptr(l2),
-                             *l2.stride(), ptr(out), *out.stride()[:3], ptr(lse), n, H, t, D, stream_of(o1)),
-          "od_lse_merge")
     return (out, lse) if return_lse else out
 
 

@@ -5,8 +5,8 @@ per-state loop in `_forward` (prefix_attn.py:118-128) and the per-layer dequanti
 `shared_prefix_attention` (prefix_attn.py:145-149). An int8 state (Int8Tensor) goes to the branched kernel as it is
 stored, with its per-(token, head) scales, and one launch covers every row: prefix partial, own causal partial and
 their log-sum-exp merge, the state dequantized in registers as the reference materializes it (bf16(q * bf16(s))).
-A dense bf16 prefix, as the reference's _forward passes it (prefix_attn.py:127), takes the reference's own GPU
-route: od_wide_attn over the prefix and over the own keys, each with its LSE, then od_lse_merge.
+A dense bf16 prefix, as the reference's _forward passes it (prefix_attn.py:127), is written into the same block
+images (od_attn_stage_bf16) and attended by the same one-softmax kernel.
 """
 from __future__ import annotations
 
@@ -40,15 +40,10 @@ def _split_attention(q, k, v, Kp, Vp, pm, scale, dequant: str = "bf16"):
         return out.to(v.dtype)
     if isinstance(Kp, Int8Tensor) or isinstance(Vp, Int8Tensor):
         raise TypeError("_split_attention: Kp and Vp must both be Int8Tensor or both dense tensors")
-    n, Hq, t, D = q.shape
     T = Kp.shape[1]
-    qs = q.transpose(0, 1).reshape(1, Hq, n * t, D)  # all rows' queries against the prefix keys only
-    kvalid = None if pm is None else pm.reshape(1, T)
-    o_p, l_p = kernels.wide_attn(qs, Kp[None], Vp[None], scale, kvalid=kvalid, causal=False, return_lse=True)
-    o_o, l_o = kernels.wide_attn(q, k, v, scale, causal=True, return_lse=True)
-    o_p = o_p.view(Hq, n, t, -1).transpose(0, 1)
-    l_p = l_p.view(Hq, n, t).transpose(0, 1)
-    return kernels.lse_merge(o_p, l_p, o_o, l_o).to(v.dtype)
+    kvalid = None if pm is None else pm.reshape(1, T).to(torch.uint8).contiguous()
+    img = kernels.stage_state_bf16(Kp[None], Vp[None], T, scale, kvalid)
+    return kernels.branched_attn_images(q, k, v, img, 1, T, scale).to(v.dtype)
 
 
 split_attention = _split_attention

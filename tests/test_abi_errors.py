@@ -64,10 +64,10 @@ def test_attention_checks(L):
     w = (1024, 128, 128)
     assert L.od_wide_attn(P, *w, P, *w, P, *w, None, 0, P, *w, None, 1, 2, 2, 4, 4, 128, 96, 1, 0.1, None) == UNSUP
     assert L.od_wide_attn(P, *w, P, *w, P, *w, None, 0, P, *w, None, 1, 3, 2, 4, 4, 128, 128, 1, 0.1, None) == SHAPE
-    assert L.od_lse_merge(P, 8, 8, 8, P, 1, 1, 1, P, 8, 8, 8, P, 1, 1, 1, P, 8, 8, 8, None, 1, 1, 1, 12,
-                          None) == SHAPE  # D % 8 != 0
-    assert L.od_lse_merge(P, 12, 8, 8, P, 1, 1, 1, P, 8, 8, 8, P, 1, 1, 1, P, 8, 8, 8, None, 1, 1, 1, 16,
-                          None) == ALIGN  # a stride that is not a multiple of 8
+    bf = (1024, 128, 128)
+    assert L.od_attn_stage_bf16(P, *bf, P, *bf, None, 1, 1, 64, 96, 0.1, P, 1 << 20, None) == UNSUP  # D = 96
+    assert L.od_attn_stage_bf16(P, 1028, 128, 128, P, *bf, None, 1, 1, 64, 128, 0.1, P, 1 << 20, None) == ALIGN
+    assert L.od_attn_stage_bf16(P, *bf, P, *bf, None, 1, 1, 64, 128, 0.1, P, 100, None) == SHAPE  # image too small
 
 
 def test_row_kernel_checks(L):

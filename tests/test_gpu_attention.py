@@ -243,21 +243,3 @@ def test_split_attention_dense_prefix(gpu_lib, n, Hq, Hkv, t, D, T, mask):
     out_i = _split_attention(c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV), Ki, Vi,
                              None if pm is None else pm.to(DEV), c["scale"])
     assert_close_rel(out_i.float().cpu(), ref, what="int8 prefix")
-
-
-def test_lse_merge_matches_oracle(gpu_lib):
-    """od_lse_merge on strided partials (the prefix part in the (H, n, t) order the wide kernel returns it) against
-    the oracle's merge, including slots whose first part is empty (-inf)."""
-    from opendecider_amd import kernels
-    g = torch.Generator().manual_seed(77)
-    n, H, t, D = 3, 4, 5, 64
-    o1 = torch.randn(H, n, t, D, generator=g).to(torch.bfloat16)
-    l1 = torch.randn(H, n, t, generator=g) * 3
-    l1[0, 1, 2] = float("-inf")
-    o2 = torch.randn(n, H, t, D, generator=g).to(torch.bfloat16)
-    l2 = torch.randn(n, H, t, generator=g) * 3
-    out, lse = kernels.lse_merge(o1.to(DEV).transpose(0, 1), l1.to(DEV).transpose(0, 1), o2.to(DEV), l2.to(DEV),
-                                 return_lse=True)
-    ref, ref_lse = oa.lse_merge(o1.transpose(0, 1).float(), l1.transpose(0, 1), o2.float(), l2)
-    assert_close_rel(out.float().cpu(), ref, what="lse merge")
-    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-5
