@@ -1087,6 +1087,7 @@ __global__ __launch_bounds__(kThreads) void stage_bf16_kernel(StageBf16Args p) {
   vmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const bool ok = valid(tid & 63);
   const bool any = __builtin_amdgcn_ballot_w64(ok) != 0;
+  const int masked = __builtin_amdgcn_ballot_w64(!ok) != 0;  // taken with the whole wave active
   const int eb = any ? exp_above(vmax) : kNoFrame;
   if (tid < 2 * D) {
     const float f = any ? ldexpf(1.0f, -eb) : 0.0f;
@@ -1107,7 +1108,7 @@ __global__ __launch_bounds__(kThreads) void stage_bf16_kernel(StageBf16Args p) {
     dst.gk[tid] = ok ? p.scale_log2 : 1.0f;
     dst.kb[tid] = ok ? 0.0f : -INFINITY;
   }
-  if (tid == 0) *reinterpret_cast<int4*>(dst.info) = make_int4(0, eb, __builtin_amdgcn_ballot_w64(!ok) != 0, 0);
+  if (tid == 0) *reinterpret_cast<int4*>(dst.info) = make_int4(0, eb, masked, 0);
 }
 
 // LSE merge of the key-range splits (prefix_attn.py:74-76 generalised to n parts): M = max_s lse_s,
