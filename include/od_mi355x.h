@@ -29,6 +29,7 @@ typedef void* od_stream_t;
 #define OD_ERR_ALIGN (-3)       /* a pointer or leading dimension breaks the 16-byte alignment the kernel needs */
 #define OD_ERR_UNSUPPORTED (-4) /* head dim / GQA ratio / row length outside what the kernels are built for */
 #define OD_ERR_LAUNCH (-5)      /* the kernel launch failed (hipGetLastError) */
+#define OD_ERR_SCRATCH (-6)     /* the work needs more than the library's static scratch (od_*_noalloc) */
 
 /* How the branched attention turns the int8 state into K/V (the `dequant` argument). */
 #define OD_DEQUANT_BF16 0 /* the reference's materialize: q.to(bf16) * s.to(bf16), one bf16 rounding per value */
@@ -199,6 +200,28 @@ int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t 
                            int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
                            int64_t cap, float scale, int dequant, int64_t nsplit, float* ws, int64_t ws_floats,
                            od_stream_t stream);
+
+/*
+ * od_branched_attn_split_noalloc — od_branched_attn_split without a workspace argument and without any allocation:
+ * the per-split partials go to a static device array inside the library (OD_SPLIT_SCRATCH_FLOATS floats = 64 MiB per
+ * GPU, held from the first call until the process ends). No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ *   arguments, result and launches as od_branched_attn_split (without ws / ws_floats)
+ *   nsplit * R * Hq * t * (D + 1) must not exceed OD_SPLIT_SCRATCH_FLOATS (else OD_ERR_SCRATCH, nothing launched);
+ *   nsplit = 1 uses no scratch.
+ * Every call on one GPU shares that GPU's array, which keeps the last call's partials (every partial a call's merge
+ * reads is written by the same call, so nothing needs clearing): calls that overlap on one GPU (two streams, two
+ * threads) race and must be serialized by the caller.
+ */
+#define OD_SPLIT_SCRATCH_FLOATS (16ll * 1024 * 1024)
+int od_branched_attn_split_noalloc(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                                   const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                                   const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                                   const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
+                                   const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
+                                   uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
+                                   int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
+                                   int64_t cap, float scale, int dequant, int64_t nsplit, od_stream_t stream);
 
 /*
  * od_attn_stage_size — bytes of the block images od_attn_stage writes for a state of Ns x Hkv heads and T keys:

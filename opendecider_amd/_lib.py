@@ -31,6 +31,10 @@ SIGNATURES = {
                                _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64,
                                _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _i64,
                                _c_ptr, _i64, _c_ptr],
+    "od_branched_attn_split_noalloc": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
+                                       _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64,
+                                       _i64, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                       ctypes.c_float, ctypes.c_int, _i64, _c_ptr],
     "od_attn_stage_size": [_i64, _i64, _i64, _i64, _c_ptr],
     "od_attn_stage": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
                       ctypes.c_int, _c_ptr, _i64, _c_ptr],
@@ -78,6 +82,9 @@ def lib() -> ctypes.CDLL:
         _LIB = L
     return _LIB
 
+
+# the static scratch of od_branched_attn_split_noalloc (include/od_mi355x.h), in floats
+SPLIT_SCRATCH_FLOATS = 16 * 1024 * 1024
 
 # od_branched_attn / od_attn_stage dequantization of the int8 state (include/od_mi355x.h)
 DEQUANT = {"bf16": 0, "fp32": 1}

@@ -45,7 +45,15 @@
 // Masked keys get a -inf score; a block with no visible key is an exact no-op for a slot; every row's arithmetic is
 // independent of its position among the rows (fixed key order, no cross-slot reduction), so option order cannot
 // change a result.
+#include <mutex>
+
 #include "od_common.h"
+
+// The split workspace of od_branched_attn_split_noalloc: a static device array (one copy per GPU, alive until the
+// process ends). Host code never passes this name to a kernel or a copy (on the host it is a stand-in, not a device
+// address): scratch_ptr() resolves each device's copy with hipGetSymbolAddress once and the kernels take that
+// pointer.
+static __device__ __align__(256) float scratch[OD_SPLIT_SCRATCH_FLOATS];
 
 namespace {
 
@@ -1325,4 +1333,49 @@ extern "C" int od_attn_stage_bf16(const uint16_t* k, int64_t skb, int64_t skh, i
     stage_bf16_kernel<64><<<grid, block, 0, st>>>(a);
   }
   return od_launch_status();
+}
+
+namespace {
+
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+float* g_scratch[kMaxDevices] = {};
+
+// This device's copy of `scratch` (resolved on the first call made with the device current).
+int scratch_ptr(float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return OD_ERR_LAUNCH;
+  if (dev < 0 || dev >= kMaxDevices) return OD_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return OD_ERR_LAUNCH;
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch[dev];
+  return OD_OK;
+}
+
+}  // namespace
+
+extern "C" int od_branched_attn_split_noalloc(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                                              const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                                              const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                                              const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
+                                              const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
+                                              uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
+                                              int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns,
+                                              int64_t T, int64_t cap, float scale, int dequant, int64_t nsplit,
+                                              od_stream_t stream) {
+  if (R < 0 || Hq < 1 || t < 1 || D < 1 || nsplit < 1 || nsplit > 256) return OD_ERR_SHAPE;
+  const int64_t need = nsplit > 1 ? nsplit * R * Hq * t * (D + 1) : 0;
+  if (need > OD_SPLIT_SCRATCH_FLOATS) return OD_ERR_SCRATCH;
+  float* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_ptr(&ws);
+    if (rc != OD_OK) return rc;
+  }
+  return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, kq, ks, vq, vs, kvalid,
+                         nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale,
+                         dequant, nsplit, ws, need, stream);
 }

@@ -353,6 +353,7 @@ extern "C" const char* od_strerror(int code) {
     case OD_ERR_ALIGN: return "a pointer or leading dimension breaks the 16-byte alignment the kernel needs";
     case OD_ERR_UNSUPPORTED: return "head dim / GQA ratio / row length outside what the kernels are built for";
     case OD_ERR_LAUNCH: return "kernel launch failed";
+    case OD_ERR_SCRATCH: return "the work needs more than the library's static scratch (od_*_noalloc)";
     default: return "unknown error";
   }
 }

@@ -381,7 +381,7 @@ def uses_staging(max_rows: int, t: int, n_heads_q: int, n_heads_k: int) -> bool:
 
 def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, row_counts=None, length=None,
                   out=None, return_lse: bool = False, row_start=None, max_rows=None, n_split=None, staged=None,
-                  stage_buf=None, dequant: str = "bf16", images=None):
+                  stage_buf=None, dequant: str = "bf16", images=None, static_workspace: bool = False):
     """Branched option-row attention over int8 states. q (R, Hq, t, D) bf16; k_own/v_own (R, Hkv, t, D) bf16;
     kq/vq (Ns, Hkv, cap, D) int8 of which the first T tokens are used (T = `length`, else kvalid.shape[1], else
     cap); ks/vs (Ns, Hkv, cap) fp32; kvalid (Ns, T) bool/uint8 or None.
@@ -393,7 +393,9 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
     tiles read each (state, head), so that the conversion is shared. images: block images already built by
     stage_state for this state, length, scale, mask and dequant (the staged path then skips od_attn_stage; the
     caller keeps them valid). dequant: "bf16", the reference's materialize bf16(q * bf16(s)) (quant.py:45,
-    prefix_attn.py:145-149), or "fp32", the exact q * s. Returns out (R, Hq, t, D) bf16 [, lse (R, Hq, t) fp32]."""
+    prefix_attn.py:145-149), or "fp32", the exact q * s. static_workspace: the direct path's split partials go to
+    the library's static scratch (od_branched_attn_split_noalloc: nothing is allocated for them; calls on one GPU
+    must not overlap). Returns out (R, Hq, t, D) bf16 [, lse (R, Hq, t) fp32]."""
     require_gpu(q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, name="branched_attn")
     for x in (q, k_own, v_own):
         _lib.bf16_bits(x)
@@ -437,8 +439,10 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
         n_split = split_count(tiles * Hkv * Ns, T)
     if staged is None:
         staged = images is not None or tiles >= STAGE_MIN_TILES
+    if static_workspace:
+        staged = False
     ws = None
-    if n_split > 1:
+    if n_split > 1 and not static_workspace:
         ws = torch.empty(n_split * R * Hq * t * (D + 1), dtype=torch.float32, device=q.device)
     if staged and T > 0:
         img = images if images is not None else stage_state(kq, ks, vq, vs, T, scale, kvalid, out=stage_buf,
@@ -451,6 +455,13 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
                                             Ns, T, float(scale), int(n_split), ptr(ws),
                                             0 if ws is None else ws.numel(), stream_of(q)),
               "od_branched_attn_staged")
+    elif static_workspace:
+        check(lib().od_branched_attn_split_noalloc(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3],
+                                                   ptr(v_own), *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq),
+                                                   ptr(vs), ptr(kvalid), ptr(row_start), int(max_rows), ptr(out),
+                                                   *out.stride()[:3], ptr(lse), R, Hq, Hkv, t, D, Ns, T, cap,
+                                                   float(scale), dq, int(n_split), stream_of(q)),
+              "od_branched_attn_split_noalloc")
     elif n_split > 1:
         check(lib().od_branched_attn_split(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
                                            *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
