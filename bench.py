@@ -288,8 +288,7 @@ def run_decision(args):
     attn_t = AttnTimers()
 
     def decide():
-        for kc, vc in caches:
-            kc.length = vc.length = 0
+        caches.set_length(0)
         dec.prefill(ids_state, caches)
         return dec.score(ids, caches)
 
@@ -360,8 +359,7 @@ def run_wide_choice(args):
     for i in range(args.warmup):
         dec.prefill(records[n_rec + i], caches)
         dec.score(ids, caches)
-        for kc, vc in caches:
-            kc.length = vc.length = S0
+        caches.set_length(S0)
     torch.cuda.synchronize()
     rec_ms, score_ms = [], []
     app_ms = []

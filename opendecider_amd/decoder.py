@@ -119,6 +119,7 @@ class DenseDecoder:
         self._eps32 = float(torch.tensor(cfg.eps, dtype=torch.float32))
         self._ws = {}
         self._rows = {}
+        self._images = {}  # layer -> (key, block images of that layer's state K/V)
 
     def add_layer(self, lw: dict) -> None:
         L = {k: lw[k].to(self.dev) for k in ("ln1", "ln2", "q_norm", "k_norm")}
@@ -192,14 +193,33 @@ class DenseDecoder:
         kernels.w8a8_gemm(xq[:, :cfg.ffn], sx, L["down"].q, L["down"].scale, residual=h_out, out=h)
         return h
 
+    def state_images(self, li: int, state_k: Int8KVCache, state_v: Int8KVCache):
+        """Layer li's block images of the cached states (od_attn_stage), built once and reused by every scoring pass
+        until the caches change (their generation counters or length move). Only for an unmasked state."""
+        cfg = self.cfg
+        key = (id(state_k), id(state_v), state_k.generation, state_v.generation, state_k.length)
+        hit = self._images.get(li)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        img = kernels.stage_state(state_k.q, state_k.scale, state_v.q, state_v.scale, state_k.length,
+                                  cfg.head_dim ** -0.5, out=None if hit is None else hit[1])
+        self._images[li] = (key, img)
+        return img
+
     def layer(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict, state_k: Int8KVCache,
               state_v: Int8KVCache, R: int, t: int, pos: torch.Tensor, row_start, max_rows: int, kvalid=None):
-        """One layer over R option rows of t tokens that attend their state's int8 K/V and themselves."""
-        D = self.cfg.head_dim
+        """One layer over R option rows of t tokens that attend their state's int8 K/V and themselves. When the
+        staged path applies (enough slot tiles per (state, head)) and the state is unmasked, the state's block images
+        come from state_images (built once per state version, not per pass)."""
+        cfg = self.cfg
+        D = cfg.head_dim
         qkv = self._attn_in(li, h, ws, pos)
         q, k, v, attn = self._heads(qkv, ws, R, t)
+        img = None
+        if kvalid is None and state_k.length > 0 and kernels.uses_staging(max_rows, t, cfg.n_heads, cfg.n_kv_heads):
+            img = self.state_images(li, state_k, state_v)
         kernels.branched_attn(q, k, v, state_k.q, state_k.scale, state_v.q, state_v.scale, D ** -0.5, kvalid=kvalid,
-                              length=state_k.length, out=attn, row_start=row_start, max_rows=max_rows)
+                              length=state_k.length, out=attn, row_start=row_start, max_rows=max_rows, images=img)
         return self._attn_out_mlp(li, h, h_out, ws)  # the output goes back into h (h_out held the mid residual)
 
     def prefill_layer(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict, cache_k: Int8KVCache,
@@ -289,6 +309,36 @@ class DenseDecoder:
             row_start = kernels.row_start_of([1] * B, self.dev)[0] if (n0 > 0 and B > 1) else None
             self._rows[key] = (pos, row_start)
         return self._rows[key]
+
+    def capture_scoring(self, states, B: int, n_opt: int, t: int, kvalid=None):
+        """A HIP graph of every layer of a scoring pass over `states` for B requests x n_opt options x t tokens
+        (every kernel launch of the pass recorded once, deploy.py:1-14's static mode). Returns run(ids) -> (B,
+        n_opt + 1) log-probabilities: it copies the rows' embeddings into the graph's input buffer, replays the graph
+        and reads out. The graph holds the addresses of the states' K/V, their block images, the row layout and the
+        activation buffers: re-capture after the states change (append, restore)."""
+        cfg = self.cfg
+        R = B * n_opt
+        T = states[0][0].length
+        pos, row_start, max_rows = self.row_layout(T, B, n_opt, t)
+        h0 = torch.zeros(R * t, cfg.hidden, dtype=torch.bfloat16, device=self.dev)
+        side = torch.cuda.Stream(self.dev)  # warm-up off the capture: block images, module loads
+        side.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(side):
+            self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
+        torch.cuda.current_stream(self.dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
+
+        def run(ids: torch.Tensor) -> torch.Tensor:
+            if tuple(ids.shape) != (B, n_opt, t):
+                raise ValueError(f"captured for ids of shape {(B, n_opt, t)}, got {tuple(ids.shape)}")
+            h0.copy_(self.embed.index_select(0, ids.reshape(-1)))
+            graph.replay()
+            return self.readout(h, B, n_opt, t)
+
+        run.graph = graph
+        return run
 
     def row_layout(self, T: int, B: int, n_opt: int, t: int):
         """Device positions and per-state row offsets of a scoring pass, built once per shape: a host-to-device

@@ -151,6 +151,9 @@ def qk_norm_rope_kv_append(qkv: torch.Tensor, B: int, S: int, n_heads_q: int, n_
           "od_qk_norm_rope_kv_append")
     k_cache.length += S
     v_cache.length += S
+    for c in (k_cache, v_cache):
+        if hasattr(c, "touch"):
+            c.touch()
 
 
 def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, bias=None, residual=None,

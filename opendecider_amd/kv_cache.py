@@ -24,6 +24,7 @@ class Int8KVCache:
         self.scale = torch.zeros(batch, n_heads, capacity, dtype=torch.float32, device=device)
         self.length = 0
         self.dtype = dtype
+        self.generation = 0  # bumped by every write through this package (derived data, e.g. block images, keys on it)
 
     @classmethod
     def from_tensors(cls, q: torch.Tensor, scale: torch.Tensor, dtype=torch.bfloat16) -> "Int8KVCache":
@@ -33,8 +34,12 @@ class Int8KVCache:
         if not (q.is_contiguous() and scale.is_contiguous()):
             raise ValueError("Int8KVCache.from_tensors: buffers must be contiguous")
         c = cls.__new__(cls)
-        c.q, c.scale, c.length, c.dtype = q, scale, 0, dtype
+        c.q, c.scale, c.length, c.dtype, c.generation = q, scale, 0, dtype, 0
         return c
+
+    def touch(self) -> None:
+        """Mark the bytes as changed (call after writing q / scale directly)."""
+        self.generation += 1
 
     @property
     def capacity(self) -> int:
@@ -47,6 +52,7 @@ class Int8KVCache:
             raise ValueError(f"Int8KVCache: {self.length} + {n} tokens exceed the capacity {self.capacity}")
         kernels.kv_quant_append(x, self.q, self.scale, self.length)
         self.length += n
+        self.touch()
 
     def as_int8_tensor(self) -> Int8Tensor:
         """The filled part as an Int8Tensor (views, no copy): q (B, Hkv, T, D), scale (B, Hkv, T, 1) fp32."""
@@ -98,6 +104,7 @@ class StateKV:
         for pair in self.pairs:
             for c in pair:
                 c.length = n
+                c.touch()
 
     def state(self, b: int):
         """State b of every layer: q (2 L, Hkv, cap, D) and scale (2 L, Hkv, cap) views."""

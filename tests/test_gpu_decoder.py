@@ -320,3 +320,24 @@ def test_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, S, rec
     ref = od.decision_forward(ids, w, emb, cfg, kv_ref, n0)
 
     _assert_e2e(lp, ref, f"{name} (prefilled)")
+
+
+@pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
+def test_scoring_pass_graph_replays_equal_eager(gpu_lib, name, cfg_kw, B, n_opt, t, T):
+    """The whole scoring pass captured in one HIP graph (deploy.py:1-14's static mode): three replays, with eager
+    passes on other option ids between them, each equal bit for bit to the eager pass on the same ids; then new ids
+    through the same graph equal their eager pass."""
+    cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
+    ids2 = torch.randint(0, cfg.vocab, ids.shape, generator=torch.Generator().manual_seed(9))
+    print(f"{name}: graph capture B={B} options={n_opt} t={t} T={T}", flush=True)
+    eager = dec.score(ids.to(DEV), gs)
+    eager2 = dec.score(ids2.to(DEV), gs)
+    run = dec.capture_scoring(gs, B, n_opt, t)
+    for i in range(3):
+        lp = run(ids.to(DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(lp, eager), f"replay {i}"
+        other = dec.score(ids2.to(DEV), gs)
+        torch.cuda.synchronize()
+        assert torch.equal(other, eager2), f"eager pass after replay {i}"
+    assert torch.equal(run(ids2.to(DEV)), eager2)
