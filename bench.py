@@ -8,12 +8,15 @@ q/k norm + RoPE, branched attention over the int8 state + own tokens, W8A8 O GEM
 W8A8 gate+up GEMM, SwiGLU+quantize, W8A8 down GEMM (+residual). The states' K/V are synthetic (bf16 N(0,1)
 quantized by the append kernel) and resident in HBM before timing; so are the option token ids.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--workload scoring|decision|wide_choice|gemm_traffic|attention|lm_logprob]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--scoring-only]
+                    [--workload scoring|decision|wide_choice|gemm|gemm_traffic|attention|lm_logprob]
 
 Prints ONE JSON line: metric / value (decisions/s) / timing, the roofline of the dominant kernel (the W8A8 GEMM,
 int8 MFMA), the branched attention's figures, and a CPU baseline (the oracle, on this host's cores, on a bounded
-sample of the same workload, scaled).
+sample of the same workload, scaled). The default line also carries the full decision forward from token ids
+("decision": 4096-token states prefilled, 64 options x 24 tokens) and the wide-choice growing state ("wide_choice":
+a 32768-token int8 state + 256-token records, 2 x 255 options x 12 tokens), each with its own CPU baseline
+(--scoring-only leaves them out).
 """
 from __future__ import annotations
 
@@ -42,8 +45,8 @@ def parse():
     ap.add_argument("--options", type=int, default=32)
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--state", type=int, default=2048)
-    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm_traffic", "attention",
-                                           "lm_logprob"],
+    ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm", "gemm_traffic",
+                                           "attention", "lm_logprob"],
                     default="scoring",
                     help="scoring (default): the metric's option-row scoring pass over cached 2048-token states; "
                          "decision: full decision forward from token ids (4 requests, 4096-token states prefilled, "
@@ -53,8 +56,11 @@ def parse():
                          "then two scoring passes through 2 layers, i.e. each M = 4096 GEMM shape twice); "
                          "attention: the branched attention alone on the config-1 shape and on the KV-bound probe "
                          "(32768-token states, 2 options x 16 tokens per state); lm_logprob: the LM head's token "
-                         "log-prob of 1024 rows over a 151936 x 4096 int8 table")
+                         "log-prob of 1024 rows over a 151936 x 4096 int8 table; gemm: the W8A8 linear alone over "
+                         "the reference's (K, N) x M sweep (scripts/bench_gemm.py) and the 9B layer shapes at M = 4096")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--scoring-only", action="store_true",
+                    help="the default line without its decision / wide_choice sub-objects")
     ap.add_argument("--cpu-sample-repeats", type=int, default=3)
     return ap.parse_args()
 
@@ -259,6 +265,58 @@ def cpu_baseline(args):
                        f"scaled x{args.layers} layers")}
 
 
+def cpu_baseline_decision(args):
+    """The oracle on a bounded sample of the decision forward: ONE request (a 4096-token state of random ids
+    prefilled, then 64 options x 24 tokens scored) through ONE 9B-dims layer, timed once, scaled x36 layers."""
+    import torch
+
+    from oracle import decoder as od
+    torch.set_num_threads(os.cpu_count() or 1)
+    cfg = od.DecoderConfig(n_layers=1)
+    w = od.make_weights(cfg, seed=1)
+    emb = torch.randn(4096, cfg.hidden, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(2)
+    S, n_opt, t = 4096, 64, 24
+    ids_s = torch.randint(0, 4096, (1, S), generator=g)
+    ids_o = torch.randint(0, 4096, (1, n_opt, t), generator=g)
+    t0 = time.perf_counter()
+    _, kv = od.prefill_forward(ids_s, w, emb, cfg)
+    od.decision_forward(ids_o, w, emb, cfg, kv, S)
+    per_layer = time.perf_counter() - t0
+    per_request = per_layer * args.layers
+    return {"value": 1.0 / per_request, "unit": "decisions/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"1 request ({S}-token state prefilled + {n_opt} options x {t} tokens) x 1 of {args.layers} "
+                       f"layers, one run, {per_layer:.1f} s per layer, scaled x{args.layers} layers")}
+
+
+def cpu_baseline_wide(args):
+    """The oracle on a bounded sample of the wide-choice workload: ONE 256-token record appended to a 32768-token
+    int8 state through ONE 9B-dims layer (attention over the cached state + itself, only the new K/V quantized),
+    timed once, scaled x36 layers: the full-record append cost."""
+    import torch
+
+    from oracle import decoder as od
+    from oracle import quant as oq
+    torch.set_num_threads(os.cpu_count() or 1)
+    cfg = od.DecoderConfig(n_layers=1)
+    w = od.make_weights(cfg, seed=1)
+    emb = torch.randn(4096, cfg.hidden, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(4)
+    S0, rec = 32768, 256
+    kv = torch.randn(2, 1, cfg.n_kv_heads, S0, cfg.head_dim, generator=g).to(torch.bfloat16)
+    kq, ks = oq.quantize_rows(kv[0])
+    vq, vs = oq.quantize_rows(kv[1])
+    state = [((kq, ks[..., 0]), (vq, vs[..., 0]))]
+    ids = torch.randint(0, 4096, (1, rec), generator=g)
+    t0 = time.perf_counter()
+    od.prefill_forward(ids, w, emb, cfg, state_kv=state, n0=S0)
+    per_layer = time.perf_counter() - t0
+    return {"value": per_layer * args.layers * 1e3, "unit": "ms per appended record (full prefill)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"1 record of {rec} tokens onto a {S0}-token int8 state x 1 of {args.layers} layers, one run, "
+                       f"{per_layer:.2f} s per layer, scaled x{args.layers} layers")}
+
+
 def _gemm_roofline(gemm_t):
     n_g, ms_g, (ops_g, _) = gemm_t.summary()
     tops = ops_g / (ms_g * 1e-3) / 1e12 if n_g else 0.0
@@ -401,6 +459,118 @@ def run_wide_choice(args):
                                          "in one pass, 36 layers)")},
         "scoring_ms": sum(score_ms) / n_rec,
     }
+
+
+def run_gemm(args):
+    """The W8A8 linear alone: od_act_quant + od_w8a8_gemm on the reference's sweep (scripts/bench_gemm.py:22-23:
+    (K, N) in {(2048, 6144), (6144, 2048), (2048, 2048)} x M in {64, 512, 2048, 8192}) and on the 9B layer shapes at
+    M = 4096 (QKV 4096 -> 6144, O 4096 -> 4096, gate+up 4096 -> 24576 also with SwiGLU in the epilogue, down
+    12288 -> 4096). Inputs as config 2: X bf16 N(0, 1) with 1% outlier channels x20, W N(0, 0.02) with SmoothQuant
+    factors U(0.5, 2) folded in, per-channel int8; 1/s fused into the activation quantizer. HIP events over 20 calls
+    of each kernel after 3 warm-up calls; the vendor int8 GEMM (torch._int_mm, hipBLASLt, int32 output, no
+    epilogue) beside it. Each timing is a replay of a HIP graph of the 20 calls (GPU time, no host launch gaps).
+    CPU baselines on config 0 (M = 256, 4096 x 4096): the reference's CPU linear path
+    (Int8Linear.forward: dequantize + F.linear in bf16, quant.py:156-157) and the W8A8 oracle."""
+    import torch
+
+    from opendecider_amd import kernels
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(6)
+    reps = 20
+
+    def timed(fn):
+        # the reps calls captured in one HIP graph and replayed: GPU time only (at small M the host's launch
+        # overhead would otherwise be what is measured)
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        graph.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3  # us
+
+    def operands(M, K, N):
+        x = torch.randn(M, K, device=dev, generator=g)
+        idx = torch.randperm(K, device=dev, generator=g)[: (K + 99) // 100]
+        x[:, idx] *= 20
+        x = x.to(torch.bfloat16)
+        s = torch.rand(K, device=dev, generator=g) * 1.5 + 0.5
+        wt = (torch.randn(N, K, device=dev, generator=g) * 0.02 * s[None, :]).to(torch.bfloat16)
+        wq, sw = kernels.act_quant(wt)
+        inv = (1.0 / s).to(torch.bfloat16)
+        return x, inv, wq, sw
+
+    rows = []
+    shapes = [("bench_gemm", K, N, M) for K, N in ((2048, 6144), (6144, 2048), (2048, 2048))
+              for M in (64, 512, 2048, 8192)]
+    shapes += [("9b_qkv", 4096, 6144, 4096), ("9b_o", 4096, 4096, 4096), ("9b_gate_up", 4096, 24576, 4096),
+               ("9b_down", 12288, 4096, 4096)]
+    for name, K, N, M in shapes:
+        x, inv, wq, sw = operands(M, K, N)
+        xq, sx = kernels.act_quant(x, inv)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        us_q = timed(lambda: kernels.act_quant(x, inv, xq=xq, sx=sx))
+        us_g = timed(lambda: kernels.w8a8_gemm(xq, sx, wq, sw, out=out))
+        us_v = timed(lambda: torch._int_mm(xq, wq.t()))
+        ops = 2 * M * N * K
+        row = {"shape": name, "M": M, "K": K, "N": N, "act_quant_us": us_q, "gemm_us": us_g,
+               "gemm_tops": ops / us_g / 1e6, "frac": ops / us_g / 1e6 / INT8_PEAK_TOPS,
+               "linear_tops": ops / (us_q + us_g) / 1e6, "vendor_int_mm_us": us_v}
+        if name == "9b_gate_up":
+            hm = torch.empty(M, N // 2, dtype=torch.bfloat16, device=dev)
+            wi = kernels.interleave_gate_up(wq)
+            si = kernels.interleave_gate_up(sw)
+            us_s = timed(lambda: kernels.w8a8_gemm_swiglu(xq, sx, wi, si, out=hm))
+            row["swiglu_gemm_us"] = us_s
+            row["swiglu_gemm_tops"] = ops / us_s / 1e6
+        rows.append(row)
+        del x, xq, wq, out
+    nine = [r for r in rows if r["shape"].startswith("9b_")]
+    ops9 = sum(2 * r["M"] * r["N"] * r["K"] for r in nine)
+    us9 = sum(r.get("swiglu_gemm_us", r["gemm_us"]) for r in nine)
+    res = {"metric": "int8 GEMM TOPS (W8A8 linear, per shape)", "value": ops9 / us9 / 1e6, "unit": "TOPS",
+           "n_gpus": 1, "steps": reps, "warmup": 3, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+           "config": {"workload": "W8A8 linear sweep: scripts/bench_gemm.py shapes and the 9B layer GEMMs at M = 4096"},
+           "roofline": {"kernel": "od_w8a8_gemm (gate+up: od_w8a8_gemm_swiglu)", "bound": "mfma",
+                        "achieved": ops9 / us9 / 1e6, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                        "frac": ops9 / us9 / 1e6 / INT8_PEAK_TOPS, "traffic": None,
+                        "note": "the four 9B layer GEMMs at M = 4096 together"},
+           "shapes": rows}
+    if not args.no_cpu_baseline:
+        import torch as _t
+        from oracle import quant as oq
+        _t.set_num_threads(os.cpu_count() or 1)
+        cg = _t.Generator().manual_seed(0)
+        M, K, N = 256, 4096, 4096
+        x = _t.randn(M, K, generator=cg).to(_t.bfloat16)
+        wq = _t.randint(-127, 128, (N, K), generator=cg, dtype=_t.int8)
+        sw = _t.rand(N, generator=cg) * 1.5e-3 + 0.5e-3
+        ops = 2 * M * N * K
+        tims = {}
+        for label, fn in (("dequant + F.linear (Int8Linear.forward)", lambda: oq.int8_linear_dequant(x, wq, sw)),
+                          ("W8A8 port (act-quant, int32 GEMM, epilogue)", lambda: oq.w8a8_linear(x, wq, sw))):
+            fn()
+            ts = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            tims[label] = sorted(ts)[2]
+        ref = tims["dequant + F.linear (Int8Linear.forward)"]
+        res["cpu_baseline"] = {"value": ops / ref / 1e12, "unit": "TOPS", "cores": _t.get_num_threads(),
+                               "kind": "port",
+                               "sample": (f"config 0 (M={M}, K={K}, N={N}), median of 5: the reference's CPU linear "
+                                          f"path {ref * 1e3:.1f} ms; the W8A8 oracle "
+                                          f"{tims['W8A8 port (act-quant, int32 GEMM, epilogue)'] * 1e3:.1f} ms")}
+    return res
 
 
 def run_gemm_traffic(args):
@@ -573,8 +743,9 @@ def main():
     import torch
     if args.workload != "scoring":
         torch.cuda.set_device(0)
-        fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm_traffic": run_gemm_traffic,
-              "attention": run_attention, "lm_logprob": run_lm_logprob}[args.workload]
+        fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm": run_gemm,
+              "gemm_traffic": run_gemm_traffic, "attention": run_attention,
+              "lm_logprob": run_lm_logprob}[args.workload]
         print(json.dumps(fn(args)))
         return
 
@@ -658,7 +829,31 @@ def main():
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args)
+    if not args.scoring_only:
+        del states, dec
+        torch.cuda.empty_cache()
+        res["decision"] = _sub(run_decision(_sub_args(args, steps=10, warmup=2)),
+                               ("value", "unit", "p50_latency_ms", "p90_latency_ms", "config", "roofline",
+                                "state_attention", "row_attention", "time_share"))
+        if not args.no_cpu_baseline:
+            res["decision"]["cpu_baseline"] = cpu_baseline_decision(args)
+        torch.cuda.empty_cache()
+        res["wide_choice"] = _sub(run_wide_choice(_sub_args(args, warmup=1)),
+                                  ("value", "unit", "config", "attention", "append_per_record", "scoring_ms"))
+        if not args.no_cpu_baseline:
+            res["wide_choice"]["cpu_baseline"] = cpu_baseline_wide(args)
     print(json.dumps(res))
+
+
+def _sub_args(args, **kw):
+    a = argparse.Namespace(**vars(args))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _sub(d, keys):
+    return {k: d[k] for k in keys if k in d}
 
 
 if __name__ == "__main__":
