@@ -58,6 +58,17 @@ int od_act_quant(const uint16_t* x, int64_t ldx, const uint16_t* inv_s, int8_t* 
                  int64_t M, int64_t K, od_stream_t stream);
 
 /*
+ * od_gate_act_quant — od_act_quant of the attention output times the output gate.
+ * Replaces: `o * torch.sigmoid(gate)` ahead of o_proj in the Qwen3.5 attention layer (src/opendecider/prefix_attn.py:
+ * 84-85,130) fused with o_proj's input scaling and dynamic activation quantization (as od_act_quant).
+ *   x     bf16 [M, K] (row stride ldx): the attention output;  gate  bf16 [M, K] (row stride ldg)
+ *   each element first becomes bf16(x * bf16(sigmoid(g))) (sigmoid correctly rounded in fp32, then to bf16, as
+ *   torch's bf16 sigmoid), then the od_act_quant formula (with inv_s when given). Other arguments as od_act_quant.
+ */
+int od_gate_act_quant(const uint16_t* x, int64_t ldx, const uint16_t* gate, int64_t ldg, const uint16_t* inv_s,
+                      int8_t* xq, int64_t ldq, float* sx, int64_t M, int64_t K, od_stream_t stream);
+
+/*
  * od_w8a8_gemm — int8 x int8 -> int32 GEMM on CDNA4 int8 MFMA with a bf16 dequant epilogue.
  * Replaces: the GEMM of GemLite A8W8_int8_dynamic behind gemlite_a8w8_ / smooth_a8w8_
  * (src/opendecider/quant.py:302-314, :332-350), and Int8Linear.forward's dequantize + F.linear
@@ -282,6 +293,29 @@ int od_branched_attn_staged(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t
                             uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
                             int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
                             float scale, int64_t nsplit, float* ws, int64_t ws_floats, od_stream_t stream);
+
+/*
+ * od_branched_attn_staged2 — the branched attention over a TWO-LEVEL shared prefix: every row group (a question)
+ * attends the blocks of its state, then the blocks of its own question K/V, then each row's own tokens causally, in
+ * one online softmax. Replaces: the question-cache path of the attention layer, which joins the state K/V and each
+ * question's own K/V along the keys before the split attention (src/opendecider/prefix_attn.py:94-99, driven by
+ * v3.py:446-534 _branched_feats_qcache) and the per-question LSE merge with the own part (prefix_attn.py:74-76).
+ *   img, img_bytes   level 1: block images of n_states states x Hkv heads x T keys (od_attn_stage, int8 state)
+ *   group_state      int32 [n_groups] device array: the state of each row group (NULL: group g reads state g); a
+ *                    value outside [0, n_states) reads no level-1 keys
+ *   img2, img2_bytes level 2: block images of n_groups x Hkv heads x T2 keys (od_attn_stage_bf16 of the questions'
+ *                    dense bf16 K/V, pads masked with its kvalid); T2 = 0: no second level
+ *   row_start        int32 [n_groups + 1]: the rows of group g (NULL: n_groups == 1)
+ *   other arguments, workspace and result as od_branched_attn_staged
+ */
+int od_branched_attn_staged2(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                             const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                             const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                             const void* img, int64_t img_bytes, const int32_t* group_state, int64_t n_states,
+                             int64_t T, const void* img2, int64_t img2_bytes, int64_t T2, const int32_t* row_start,
+                             int64_t max_rows, uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
+                             int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t n_groups, float scale,
+                             int64_t nsplit, float* ws, int64_t ws_floats, od_stream_t stream);
 
 /*
  * od_wide_attn — flash attention over bf16 K/V.

@@ -21,6 +21,7 @@ SIGNATURES = {
     "od_strerror": [ctypes.c_int],
     "od_abi_version": [],
     "od_act_quant": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr],
+    "od_gate_act_quant": [_c_ptr, _i64, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr],
     "od_w8a8_gemm": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _c_ptr, _i64,
                      _i64, _i64, _i64, _c_ptr],
     "od_kv_quant_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _i64, _i64, _c_ptr],
@@ -41,6 +42,10 @@ SIGNATURES = {
     "od_branched_attn_staged": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
                                 _c_ptr, _i64, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64,
                                 _i64, _i64, _i64, ctypes.c_float, _i64, _c_ptr, _i64, _c_ptr],
+    "od_branched_attn_staged2": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
+                                 _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr, _i64, _i64, _c_ptr, _i64, _c_ptr, _i64,
+                                 _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i64,
+                                 _c_ptr, _i64, _c_ptr],
     "od_wide_attn": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64,
                      _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int,
                      ctypes.c_float, _c_ptr],

@@ -95,6 +95,11 @@ struct AttnArgs {
   int nsplit;   // key-range splits (1: one pass writes out/lse)
   float* part;  // nsplit > 1: fp32 partials, o [nsplit][R][Hq][t][D] then lse [nsplit][R][Hq][t]
   const uint8_t* img;  // staged block images [Ns][Hkv][nb] (null: convert the int8 state in the kernel)
+  // Two-level prefix (staged only): row group s reads the first level of state group_state[s] (its `img` images)
+  // and then its own second-level images img2 [groups][Hkv][nb2] of T2 keys (a question's K/V).
+  const uint8_t* img2;
+  const int32_t* group_state;
+  int T2, n_states;
 };
 
 // One block of 64 state keys as the attention reads it from LDS (and as od_attn_stage stores it, byte for byte).
@@ -864,14 +869,25 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
     slot_head = g * p.rep + rem % p.rep;
   }
 
-  // ---- prefix: the state's blocks; split sp of nsplit takes the blocks [sp * bps, (sp + 1) * bps)
-  const int nb_all = (p.T + kBlockKeys - 1) / kBlockKeys;
+  // ---- prefix: the state's blocks (then, two-level, the group's own second-level blocks); split sp of nsplit takes
+  // the blocks [sp * bps, (sp + 1) * bps)
+  const int nb1_all = (p.T + kBlockKeys - 1) / kBlockKeys;
+  int st = s;  // the state whose (first-level) blocks this row group reads
+  if (p.group_state) st = p.group_state[s];
+  const bool st_ok = st >= 0 && st < p.n_states;  // a group naming no valid state reads no first-level keys
+  if (!st_ok) st = 0;
+  const int nb1 = st_ok ? nb1_all : 0;
+  const int nb2 = p.img2 ? (p.T2 + kBlockKeys - 1) / kBlockKeys : 0;
+  const int nb_all = nb1 + nb2;
   const int bps = (nb_all + p.nsplit - 1) / p.nsplit;
   const int b_lo = min(nb_all, sp * bps), b_hi = min(nb_all, b_lo + bps);
   // the first block's copy (staged path) goes out before the queries are read
-  const BlockImg<D>* img = STAGED ? reinterpret_cast<const BlockImg<D>*>(p.img) + ((int64_t)s * p.Hkv + g) * nb_all
-                                  : nullptr;
-  if (STAGED && b_hi > b_lo) copy_bytes<(int)sizeof(BlockImg<D>)>(img + b_lo, &sm.b[0]);
+  const BlockImg<D>* img1 =
+      STAGED ? reinterpret_cast<const BlockImg<D>*>(p.img) + ((int64_t)st * p.Hkv + g) * nb1_all : nullptr;
+  const BlockImg<D>* img2 =
+      STAGED && p.img2 ? reinterpret_cast<const BlockImg<D>*>(p.img2) + ((int64_t)s * p.Hkv + g) * nb2 : nullptr;
+  auto blk = [&](int b) { return b < nb1 ? img1 + b : img2 + (b - nb1); };
+  if (STAGED && b_hi > b_lo) copy_bytes<(int)sizeof(BlockImg<D>)>(blk(b_lo), &sm.b[0]);
 
   // query fragments: lane holds Q[slot][ks*16 + 8h .. +8] for ks = 0 .. D/16-1, bf16 as given
   bf16x8 qf[D / 16];
@@ -898,7 +914,7 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
       constexpr int kKeyBytes = (int)offsetof(BlockImg<D>, vt);
       constexpr int kRestBytes = (int)sizeof(BlockImg<D>) - kKeyBytes;
       auto rest = [](const BlockImg<D>* bi) { return reinterpret_cast<const char*>(bi) + kKeyBytes; };
-      if (b_lo + 1 < b_hi) copy_bytes<kKeyBytes>(img + b_lo + 1, sm.b[1].k);
+      if (b_lo + 1 < b_hi) copy_bytes<kKeyBytes>(blk(b_lo + 1), sm.b[1].k);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       v16f s0[2], s1[2];
@@ -915,9 +931,9 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
 #pragma unroll
           for (int r = ks * kNR / (D / 16); r < (ks + 1) * kNR / (D / 16); ++r) {
             if (r < kKR) {
-              if (b + 2 < b_hi) copy_round<kKeyBytes>(img + b + 2, cur.k, r);
+              if (b + 2 < b_hi) copy_round<kKeyBytes>(blk(b + 2), cur.k, r);
             } else if (b + 1 < b_hi) {
-              copy_round<kRestBytes>(rest(img + b + 1), reinterpret_cast<char*>(&nxt) + kKeyBytes, r - kKR);
+              copy_round<kRestBytes>(rest(blk(b + 1)), reinterpret_cast<char*>(&nxt) + kKeyBytes, r - kKR);
             }
           }
         };
@@ -1167,14 +1183,25 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
 
 namespace {
 
+int64_t stage_blocks(int64_t Ns, int64_t Hkv, int64_t T) { return Ns * Hkv * ((T + kBlockKeys - 1) / kBlockKeys); }
+int64_t stage_block_bytes(int64_t D) { return D == 128 ? (int64_t)sizeof(BlockImg<128>) : (int64_t)sizeof(BlockImg<64>); }
+
+// The second prefix level of od_branched_attn_staged2 (absent for the other entry points).
+struct Level2 {
+  const void* img2;
+  int64_t img2_bytes;
+  const int32_t* group_state;
+  int64_t T2, n_states;
+};
+
 int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, const uint16_t* k_own, int64_t skr,
                     int64_t skh, int64_t skt, const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
                     const int8_t* kq, const float* ks, const int8_t* vq, const float* vs, const uint8_t* kvalid,
                     const void* img, const int32_t* row_start, int64_t max_rows, uint16_t* out,
                     int64_t sor, int64_t soh, int64_t sot, float* lse, int64_t R, int64_t Hq, int64_t Hkv, int64_t t,
                     int64_t D, int64_t Ns, int64_t T, int64_t cap, float scale, int dq, int64_t nsplit, float* ws,
-                    int64_t ws_floats, od_stream_t stream) {
-  const bool staged = img != nullptr;
+                    int64_t ws_floats, od_stream_t stream, const Level2* l2 = nullptr) {
+  const bool staged = img != nullptr || l2 != nullptr;
   if (dq != OD_DEQUANT_BF16 && dq != OD_DEQUANT_FP32) return OD_ERR_UNSUPPORTED;
   if (R < 0 || Hq < 1 || Hkv < 1 || t < 1 || Ns < 1 || T < 0 || cap < T || max_rows < 0) return OD_ERR_SHAPE;
   if (Hq % Hkv) return OD_ERR_UNSUPPORTED;
@@ -1197,17 +1224,25 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
   if (sor < 0 || soh < 0 || sot < 0 || sor % 4 || soh % 4 || sot % 4) return OD_ERR_ALIGN;
   if (!od_aligned16(q) || !od_aligned16(k_own) || !od_aligned16(v_own) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
   if (T > 0 && !staged && (!od_aligned16(kq) || !od_aligned16(vq))) return OD_ERR_ALIGN;
-  if (T > 0 && staged && !od_aligned16(img)) return OD_ERR_ALIGN;
+  if (T > 0 && staged && (!img || !od_aligned16(img))) return img ? OD_ERR_ALIGN : OD_ERR_NULL;
   const int64_t rep = Hq / Hkv;
   const int64_t tiles = (max_rows * t * rep + kSlotsPerTile - 1) / kSlotsPerTile;
   if (tiles > 0x7fffffff || Hkv > 65535 || Ns * nsplit > 65535 || R * t * rep > 0x7fffffff ||
       cap * Hkv * Ns * D > (1ll << 40) || nsplit * R * Hq * t * (D + 1) > (1ll << 40) ||
       T * D >= (1ll << 31))  // one (state, head) slab is addressed with 32-bit buffer offsets
     return OD_ERR_SHAPE;
+  if (l2) {
+    if (l2->T2 < 0 || l2->n_states < 1 || l2->n_states > 65535 || l2->T2 * D >= (1ll << 31)) return OD_ERR_SHAPE;
+    if (l2->T2 > 0 && !l2->img2) return OD_ERR_NULL;
+    if (l2->T2 > 0 && !od_aligned16(l2->img2)) return OD_ERR_ALIGN;
+    if (l2->T2 > 0 && l2->img2_bytes < stage_blocks(Ns, Hkv, l2->T2) * stage_block_bytes(D)) return OD_ERR_SHAPE;
+  }
   AttnArgs a{q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, lse, sqr, sqh, sqt, skr, skh, skt, svr, svh,
              svt, sor, soh, sot, (int)R, (int)Hq, (int)Hkv, (int)t, (int)Ns, (int)T, (int)cap, (int)rep,
              scale * 1.4426950408889634f, dq, (int)nsplit, nsplit > 1 ? ws : nullptr,
-             static_cast<const uint8_t*>(img)};
+             static_cast<const uint8_t*>(img),
+             l2 && l2->T2 > 0 ? static_cast<const uint8_t*>(l2->img2) : nullptr, l2 ? l2->group_state : nullptr,
+             l2 ? (int)l2->T2 : 0, l2 ? (int)l2->n_states : (int)Ns};
   dim3 grid((unsigned)tiles, (unsigned)Hkv, (unsigned)(Ns * nsplit)), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
   if (D == 128) {
@@ -1229,8 +1264,6 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
   return od_launch_status();
 }
 
-int64_t stage_blocks(int64_t Ns, int64_t Hkv, int64_t T) { return Ns * Hkv * ((T + kBlockKeys - 1) / kBlockKeys); }
-int64_t stage_block_bytes(int64_t D) { return D == 128 ? (int64_t)sizeof(BlockImg<128>) : (int64_t)sizeof(BlockImg<64>); }
 
 }  // namespace
 
@@ -1378,4 +1411,25 @@ extern "C" int od_branched_attn_split_noalloc(const uint16_t* q, int64_t sqr, in
   return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, kq, ks, vq, vs, kvalid,
                          nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq, Hkv, t, D, Ns, T, cap, scale,
                          dequant, nsplit, ws, need, stream);
+}
+
+extern "C" int od_branched_attn_staged2(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                                        const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                                        const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                                        const void* img, int64_t img_bytes, const int32_t* group_state,
+                                        int64_t n_states, int64_t T, const void* img2, int64_t img2_bytes, int64_t T2,
+                                        const int32_t* row_start, int64_t max_rows, uint16_t* out, int64_t sor,
+                                        int64_t soh, int64_t sot, float* lse, int64_t R, int64_t Hq, int64_t Hkv,
+                                        int64_t t, int64_t D, int64_t n_groups, float scale, int64_t nsplit,
+                                        float* ws, int64_t ws_floats, od_stream_t stream) {
+  if (n_groups < 1 || n_states < 1 || T < 0) return OD_ERR_SHAPE;
+  if (T > 0 && !img) return OD_ERR_NULL;
+  if (!group_state && n_groups > n_states) return OD_ERR_SHAPE;
+  if ((D == 64 || D == 128) && T > 0 && img_bytes < stage_blocks(n_states, Hkv, T) * stage_block_bytes(D))
+    return OD_ERR_SHAPE;
+  const Level2 l2{img2, img2_bytes, group_state, T2, n_states};
+  // with T = 0 the level-1 images may be absent: the staged path then reads only the second level
+  return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, nullptr, nullptr, nullptr,
+                         nullptr, nullptr, T > 0 ? img : nullptr, row_start, max_rows, out, sor, soh, sot, lse, R,
+                         Hq, Hkv, t, D, n_groups, T, T, scale, OD_DEQUANT_BF16, nsplit, ws, ws_floats, stream, &l2);
 }

@@ -67,6 +67,21 @@ __device__ __forceinline__ float od_silu_bf16(float g) {
   return od_bf16_to_f32(od_f32_to_bf16(s));
 }
 
+// bf16(RN32(sigmoid(g))), sigmoid(g) = 1 / (1 + exp(-g)), for the output gate (torch.sigmoid on a bf16 tensor
+// computes in fp32 and rounds to bf16): the same exp(-g) as od_silu_bf16, then the sum and a reciprocal, within
+// 4 fp32 ulps; values within 16 ulps of a bf16 midpoint, and |g| >= 64, are recomputed in float64.
+__device__ __forceinline__ float od_sigmoid_bf16(float g) {
+  const float t = -g * kOdLog2eLoLn2;
+  const float e = __builtin_amdgcn_exp2f(-g * kOdLog2eHi) * __builtin_fmaf(t, __builtin_fmaf(t, 0.5f, 1.0f), 1.0f);
+  float s = __builtin_amdgcn_rcpf(1.0f + e);
+  const uint32_t lo = __float_as_uint(s) & 0xffffu;
+  if (__builtin_expect((lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 64.0f), 0)) {
+    const double gd = (double)g;
+    s = (float)(1.0 / (1.0 + exp(-gd)));
+  }
+  return od_bf16_to_f32(od_f32_to_bf16(s));
+}
+
 // The RMSNorm factor r = RN32(1 / sqrt(ss / K + eps)) from a float64 sum of squares ss: every square of a bf16 value
 // is exact in float64 and so is their sum unless the row spans more than ~25 binades, so r does not depend on the
 // order of the sum; division and square root are the IEEE float64 operations, rounded once to fp32 at the end.

@@ -4,7 +4,8 @@
 //   scale = max(max_k |v_k|, 1e-8) / 127          (IEEE fp32 division)
 //   q_k   = clamp(rint(v_k / scale), -127, 127)     (IEEE fp32 division, round half to even)
 // where v_k = float(x_k), or float(bf16(float(x_k) * float(inv_s_k))) with a SmoothQuant input scale
-// (quant.py:329: the product is rounded to bf16 before it is quantized).
+// (quant.py:329: the product is rounded to bf16 before it is quantized). The gated mode (od_gate_act_quant) first
+// forms x_k = bf16(x_k * bf16(sigmoid(g_k))), the attention output times the output gate (prefix_attn.py:130).
 //
 // The division by scale is a multiplication by 1 / scale with an exact fallback (od_q8_words), which gives the
 // quotient's result bit for bit. The row max runs on bf16 bit patterns, so a NaN in a row makes its scale NaN and
@@ -21,22 +22,26 @@ namespace {
 
 constexpr int kThreads = 256;
 
-enum Mode { kAct = 0, kKv = 1 };
+enum Mode { kAct = 0, kKv = 1, kGate = 2 };
 
 struct RowMap {
   // kAct: row r of x (stride ldx) -> row r of q (stride ldq), scale s[r].
   // kKv : row r = ((b * H + h) * n_new + i) of x (strides sxb, sxh, sxt) -> cache row (b * H + h) * cap + n0 + i.
+  // kGate: as kAct, with the gate row r of `gate` (stride ldg) beside x.
   const uint16_t* x;
   int8_t* q;
   float* s;
   int64_t ldx, ldq;
   int64_t H, n_new, sxb, sxh, sxt, cap, n0;
+  const uint16_t* gate;
+  int64_t ldg;
 };
 
 template <int MODE>
 __device__ __forceinline__ void map_row(const RowMap& m, int64_t r, const uint16_t*& xin, int8_t*& qout,
-                                        float*& sout) {
-  if (MODE == kAct) {
+                                        float*& sout, const uint16_t*& gin) {
+  gin = MODE == kGate ? m.gate + r * m.ldg : nullptr;
+  if (MODE != kKv) {
     xin = m.x + r * m.ldx;
     qout = m.q + r * m.ldq;
     sout = m.s + r;
@@ -51,27 +56,36 @@ __device__ __forceinline__ void map_row(const RowMap& m, int64_t r, const uint16
   }
 }
 
-template <bool HAS_INV>
-__device__ __forceinline__ float load_val(const uint16_t* xin, const uint16_t* inv_s, int64_t k) {
+template <bool HAS_INV, bool GATE>
+__device__ __forceinline__ float load_val(const uint16_t* xin, const uint16_t* gin, const uint16_t* inv_s, int64_t k) {
   float v = od_bf16_to_f32(xin[k]);
+  if (GATE) v = od_bf16_to_f32(od_f32_to_bf16(v * od_sigmoid_bf16(od_bf16_to_f32(gin[k]))));
   if (HAS_INV) v = od_bf16_to_f32(od_f32_to_bf16(v * od_bf16_to_f32(inv_s[k])));
   return v;
 }
 
 // 8 consecutive values of a row from one 16-byte load, times the smoothing scale and rounded to bf16 when there is
 // one; returns the packed |bf16| max of the 8 (see od_absmax_bf16x2).
-template <bool HAS_INV>
-__device__ __forceinline__ uint32_t load8(const uint16_t* xin, const uint16_t* inv_s, int64_t k, float (&v)[8]) {
+template <bool HAS_INV, bool GATE>
+__device__ __forceinline__ uint32_t load8(const uint16_t* xin, const uint16_t* gin, const uint16_t* inv_s, int64_t k,
+                                          float (&v)[8]) {
   const uint4 raw = *reinterpret_cast<const uint4*>(xin + k);
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-  uint4 rs{};
+  uint4 rs{}, rg{};
   if (HAS_INV) rs = *reinterpret_cast<const uint4*>(inv_s + k);
+  if (GATE) rg = *reinterpret_cast<const uint4*>(gin + k);
   const uint32_t ws[4] = {rs.x, rs.y, rs.z, rs.w};
+  const uint32_t wg[4] = {rg.x, rg.y, rg.z, rg.w};
   uint32_t am = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float a = __uint_as_float(w[j] << 16), b = __uint_as_float(w[j] & 0xffff0000u);
     uint32_t p = w[j];
+    if (GATE) {
+      a *= od_sigmoid_bf16(__uint_as_float(wg[j] << 16));
+      b *= od_sigmoid_bf16(__uint_as_float(wg[j] & 0xffff0000u));
+      p = od_bfr2(a, b);
+    }
     if (HAS_INV) {
       a *= __uint_as_float(ws[j] << 16);
       b *= __uint_as_float(ws[j] & 0xffff0000u);
@@ -116,10 +130,12 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowMap m, const ui
   const int lane = threadIdx.x % LANES;
   const int64_t r = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / LANES;
   const bool live = r < n_rows;  // no early return: the 256-lane variant has a barrier below
+  constexpr bool GATE = MODE == kGate;
   const uint16_t* xin = nullptr;
+  const uint16_t* gin = nullptr;
   int8_t* qout = nullptr;
   float* sout = nullptr;
-  if (live) map_row<MODE>(m, r, xin, qout, sout);
+  if (live) map_row<MODE>(m, r, xin, qout, sout, gin);
 
   if constexpr (VEC == 8 && NIT > 0) {
     float v[NIT][8];
@@ -127,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowMap m, const ui
 #pragma unroll
     for (int i = 0; i < NIT; ++i) {
       const int64_t k = ((int64_t)i * LANES + lane) * 8;
-      if (live && k < K) am = od_absmax_bf16x2(am, load8<HAS_INV>(xin, inv_s, k, v[i]));
+      if (live && k < K) am = od_absmax_bf16x2(am, load8<HAS_INV, GATE>(xin, gin, inv_s, k, v[i]));
     }
     const float amax = __uint_as_float(row_umax<LANES>(__float_as_uint(od_absmax_bf16x2_value(am))));
     if (!live) return;
@@ -147,7 +163,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowMap m, const ui
     if (live) {
       for (int64_t k = (int64_t)lane * 8; k < K; k += LANES * 8) {
         float v[8];
-        am = od_absmax_bf16x2(am, load8<HAS_INV>(xin, inv_s, k, v));
+        am = od_absmax_bf16x2(am, load8<HAS_INV, GATE>(xin, gin, inv_s, k, v));
       }
     }
     const float amax = __uint_as_float(row_umax<LANES>(__float_as_uint(od_absmax_bf16x2_value(am))));
@@ -155,7 +171,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowMap m, const ui
     const float scale = od_q8_scale(amax), inv = 1.0f / scale;
     for (int64_t k = (int64_t)lane * 8; k < K; k += LANES * 8) {
       float v[8];
-      (void)load8<HAS_INV>(xin, inv_s, k, v);
+      (void)load8<HAS_INV, GATE>(xin, gin, inv_s, k, v);
       uint32_t w[2];
       od_q8_words<8>(v, scale, inv, w);
       *reinterpret_cast<uint2*>(qout + k) = make_uint2(w[0], w[1]);
@@ -164,12 +180,14 @@ __global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowMap m, const ui
   } else {
     uint32_t am = 0;
     if (live) {
-      for (int64_t k = lane; k < K; k += LANES) am = umax(am, __float_as_uint(fabsf(load_val<HAS_INV>(xin, inv_s, k))));
+      for (int64_t k = lane; k < K; k += LANES)
+        am = umax(am, __float_as_uint(fabsf(load_val<HAS_INV, GATE>(xin, gin, inv_s, k))));
     }
     const float amax = __uint_as_float(row_umax<LANES>(am));
     if (!live) return;
     const float scale = od_q8_scale(amax), inv = 1.0f / scale;
-    for (int64_t k = lane; k < K; k += LANES) qout[k] = od_q8_one(load_val<HAS_INV>(xin, inv_s, k), scale, inv);
+    for (int64_t k = lane; k < K; k += LANES)
+      qout[k] = od_q8_one(load_val<HAS_INV, GATE>(xin, gin, inv_s, k), scale, inv);
     if (lane == 0) *sout = scale;
   }
 }
@@ -235,6 +253,25 @@ extern "C" int od_act_quant(const uint16_t* x, int64_t ldx, const uint16_t* inv_
   const bool vec_ok = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && od_aligned16(x) &&
                       ((((uintptr_t)xq) & 7u) == 0) && (!inv_s || od_aligned16(inv_s));
   return launch_quant<kAct>(m, inv_s, M, K, vec_ok, (hipStream_t)stream);
+}
+
+extern "C" int od_gate_act_quant(const uint16_t* x, int64_t ldx, const uint16_t* gate, int64_t ldg,
+                                 const uint16_t* inv_s, int8_t* xq, int64_t ldq, float* sx, int64_t M, int64_t K,
+                                 od_stream_t stream) {
+  if (M < 0 || K < 1 || ldx < K || ldq < K || ldg < K) return OD_ERR_SHAPE;
+  if (M == 0) return OD_OK;
+  if (!x || !gate || !xq || !sx) return OD_ERR_NULL;
+  RowMap m{};
+  m.x = x;
+  m.q = xq;
+  m.s = sx;
+  m.ldx = ldx;
+  m.ldq = ldq;
+  m.gate = gate;
+  m.ldg = ldg;
+  const bool vec_ok = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && (ldg % 8 == 0) && od_aligned16(x) &&
+                      od_aligned16(gate) && ((((uintptr_t)xq) & 7u) == 0) && (!inv_s || od_aligned16(inv_s));
+  return launch_quant<kGate>(m, inv_s, M, K, vec_ok, (hipStream_t)stream);
 }
 
 extern "C" int od_kv_quant_append(const uint16_t* x, int64_t B, int64_t H, int64_t n_new, int64_t D, int64_t sxb,

@@ -35,10 +35,11 @@ class DecoderConfig:
     vocab: int = 151936
     eps: float = 1e-6
     theta: float = 1e6
+    gated: bool = False  # Qwen3.5's output gate: q_proj gives each head's q and gate (prefix_attn.py:84-85,130)
 
     @property
     def qkv_out(self) -> int:
-        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+        return (self.n_heads * (2 if self.gated else 1) + 2 * self.n_kv_heads) * self.head_dim
 
 
 def rope_tables(cfg: DecoderConfig, n_pos: int):
@@ -121,9 +122,27 @@ class DenseDecoder:
         self._rows = {}
         self._images = {}  # layer -> (key, block images of that layer's state K/V)
 
+    def qkv_rows(self) -> torch.Tensor | None:
+        """Gated: the row order that takes the fused projection from the reference's layout (q_proj's per-head
+        [q_h; gate_h], then k_proj, v_proj) to [q (Hq D); k; v; gate (Hq D)], so that q and k keep their places for
+        the q/k norm + RoPE kernels and the gate is one contiguous block (a row permutation: per-row quantization
+        is unchanged). None when not gated."""
+        cfg = self.cfg
+        if not cfg.gated:
+            return None
+        D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+        heads = torch.arange(Hq)[:, None] * 2 * D
+        q_rows = (heads + torch.arange(D)[None, :]).reshape(-1)
+        g_rows = (heads + D + torch.arange(D)[None, :]).reshape(-1)
+        kv_rows = 2 * Hq * D + torch.arange(2 * Hk * D)
+        return torch.cat([q_rows, kv_rows, g_rows])
+
     def add_layer(self, lw: dict) -> None:
         L = {k: lw[k].to(self.dev) for k in ("ln1", "ln2", "q_norm", "k_norm")}
-        for name in ("qkv", "o", "down"):
+        rows = self.qkv_rows()
+        wqkv = lw["wqkv"] if rows is None else lw["wqkv"][rows.to(lw["wqkv"].device)]
+        L["qkv"] = QLinear(wqkv, lw.get("s_qkv"), self.dev)
+        for name in ("o", "down"):
             L[name] = QLinear(lw["w" + name], lw.get("s_" + name), self.dev)
         # gate and up rows interleaved for the SwiGLU GEMM (a row permutation: per-row quantization is unchanged)
         L["gu"] = QLinear(kernels.interleave_gate_up(lw["wgu"]), lw.get("s_gu"), self.dev)
@@ -175,7 +194,7 @@ class DenseDecoder:
         D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
         q = qkv[:, :Hq * D].view(R, t, Hq, D).transpose(1, 2)
         k = qkv[:, Hq * D:(Hq + Hk) * D].view(R, t, Hk, D).transpose(1, 2)
-        v = qkv[:, (Hq + Hk) * D:].view(R, t, Hk, D).transpose(1, 2)
+        v = qkv[:, (Hq + Hk) * D:(Hq + 2 * Hk) * D].view(R, t, Hk, D).transpose(1, 2)
         attn = ws["attn"].view(R, t, Hq, D).transpose(1, 2)
         return q, k, v, attn
 
@@ -185,7 +204,11 @@ class DenseDecoder:
         cfg, L = self.cfg, self.layers[li]
         xq, sx = ws["xq"], ws["sx"]
         hd = cfg.n_heads * cfg.head_dim
-        kernels.act_quant(ws["attn"], L["o"].inv_s, xq=xq[:, :hd], sx=sx)
+        if cfg.gated:  # o * sigmoid(gate) fused into o_proj's input quantizer (prefix_attn.py:130)
+            gate = ws["qkv"][:, (cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim:]
+            kernels.gate_act_quant(ws["attn"], gate, L["o"].inv_s, xq=xq[:, :hd], sx=sx)
+        else:
+            kernels.act_quant(ws["attn"], L["o"].inv_s, xq=xq[:, :hd], sx=sx)
         kernels.w8a8_gemm(xq[:, :hd], sx, L["o"].q, L["o"].scale, residual=h, out=h_out)
         kernels.rmsnorm_quant(h_out, L["ln2"], cfg.eps, L["gu"].inv_s, xq[:, :cfg.hidden], sx)
         hm = kernels.w8a8_gemm_swiglu(xq[:, :cfg.hidden], sx, L["gu"].q, L["gu"].scale, out=ws["hmlp"])

@@ -74,6 +74,28 @@ def act_quant(x: torch.Tensor, inv_s: torch.Tensor | None = None, ld: int | None
     return xq, sx
 
 
+def gate_act_quant(x: torch.Tensor, gate: torch.Tensor, inv_s: torch.Tensor | None = None, xq=None, sx=None):
+    """Per-row int8 quantization of bf16(x * bf16(sigmoid(gate))) (the attention output times the output gate,
+    prefix_attn.py:130), with the optional SmoothQuant input scale inv_s applied after the gate. x, gate (M, K) bf16
+    with contiguous rows (any row strides). Returns (xq int8 (M, K), sx fp32 (M,))."""
+    require_gpu(x, gate, inv_s, xq, sx, name="gate_act_quant")
+    _lib.bf16_bits(x)
+    _lib.bf16_bits(gate)
+    M, K = x.shape
+    if gate.shape != (M, K):
+        raise ValueError("gate_act_quant: gate must have x's shape")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    if gate.stride(1) != 1:
+        gate = gate.contiguous()
+    xq, sx = _quant_outputs(M, K, None, x.device, xq, sx)
+    inv_s = _vec(inv_s, K, "inv_s")
+    check(lib().od_gate_act_quant(ptr(x), x.stride(0) if M > 1 else K, ptr(gate), gate.stride(0) if M > 1 else K,
+                                  ptr(inv_s), ptr(xq), xq.stride(0), ptr(sx), M, K, stream_of(x)),
+          "od_gate_act_quant")
+    return xq, sx
+
+
 def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float, inv_s=None, xq=None, sx=None):
     """RMSNorm (bf16(w * bf16(x * rsqrt(mean x^2 + eps)))) -> optional SmoothQuant scale -> per-row int8.
     x (M, K) bf16 with contiguous rows. Returns (xq, sx)."""
@@ -373,6 +395,50 @@ def branched_attn_images(q, k_own, v_own, img, Ns: int, T: int, scale: float, ro
                                         ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv, t, D, Ns, T, float(scale),
                                         int(n_split), ptr(ws), 0 if ws is None else ws.numel(), stream_of(q)),
           "od_branched_attn_staged")
+    return (out, lse) if return_lse else out
+
+
+def branched_attn_two_level(q, k_own, v_own, img, n_states: int, T: int, img2, T2: int, scale: float,
+                            group_state=None, row_start=None, max_rows=None, out=None, return_lse: bool = False,
+                            n_split=None):
+    """The branched attention over a two-level prefix (od_branched_attn_staged2): the rows of group g attend the
+    block images of state group_state[g] (img: stage_state of n_states states of T keys), then group g's own
+    second-level images (img2: stage_state_bf16 of the groups' dense K/V, T2 keys), then their own tokens causally.
+    q (R, Hq, t, D), k_own/v_own (R, Hkv, t, D) bf16; rows grouped by group through row_start (int32 (G + 1,)) and
+    max_rows; group_state int32 (G,) device tensor or None (group g reads state g). Returns out [, lse]."""
+    require_gpu(q, k_own, v_own, img, img2, group_state, row_start, out, name="branched_attn_two_level")
+    for x in (q, k_own, v_own):
+        _lib.bf16_bits(x)
+    R, Hq, t, D = q.shape
+    Hkv = k_own.shape[1]
+    if k_own.shape != (R, Hkv, t, D) or v_own.shape != (R, Hkv, t, D):
+        raise ValueError("branched_attn_two_level: own k/v must be (R, Hkv, t, D)")
+    if row_start is None:
+        G, max_rows = 1, R
+    else:
+        if row_start.dtype != torch.int32 or max_rows is None:
+            raise ValueError("branched_attn_two_level: row_start must be int32 (G + 1,) with max_rows")
+        G = row_start.numel() - 1
+    if group_state is not None and (group_state.dtype != torch.int32 or group_state.numel() != G):
+        raise ValueError("branched_attn_two_level: group_state must be int32 (G,)")
+    if T > 0 and (img is None or img.numel() < stage_size(n_states, Hkv, T, D)):
+        raise ValueError("branched_attn_two_level: the level-1 images are smaller than the states need")
+    if T2 > 0 and (img2 is None or img2.numel() < stage_size(G, Hkv, T2, D)):
+        raise ValueError("branched_attn_two_level: the level-2 images are smaller than the groups need")
+    q, k_own, v_own = _rows_aligned(q), _rows_aligned(k_own), _rows_aligned(v_own)
+    out = _check_out(out, (R, Hq, t, D), q.device, "branched_attn_two_level")
+    lse = torch.empty(R, Hq, t, dtype=torch.float32, device=q.device) if return_lse else None
+    tiles = -(-(int(max_rows) * t * (Hq // Hkv)) // 128)
+    if n_split is None:
+        n_split = split_count(tiles * Hkv * G, T + T2)
+    ws = torch.empty(n_split * R * Hq * t * (D + 1), dtype=torch.float32, device=q.device) if n_split > 1 else None
+    check(lib().od_branched_attn_staged2(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
+                                         *v_own.stride()[:3], ptr(img), 0 if img is None else img.numel(),
+                                         ptr(group_state), int(n_states), int(T), ptr(img2),
+                                         0 if img2 is None else img2.numel(), int(T2), ptr(row_start), int(max_rows),
+                                         ptr(out), *out.stride()[:3], ptr(lse), R, Hq, Hkv, t, D, G, float(scale),
+                                         int(n_split), ptr(ws), 0 if ws is None else ws.numel(), stream_of(q)),
+          "od_branched_attn_staged2")
     return (out, lse) if return_lse else out
 
 

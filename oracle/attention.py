@@ -178,6 +178,31 @@ def branched_attention_int8(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvali
     return branched_attention(q, k_own, v_own, Kp, Vp, scale, kvalid, row_state, dtype)
 
 
+def two_level_attention(q, k_own, v_own, kq, ks, vq, vs, Kq2, Vq2, qmask, scale: float, row_group, group_state,
+                        dequant: str = "bf16", dtype=torch.float32):
+    """The question-cache attention (prefix_attn.py:94-99 then _split_attention): the rows of question g attend the
+    prefix [its state's K/V ; question g's own K/V] (state_of_group = group_state[g]; the int8 state dequantized as
+    dequant_state; the question K/V dense, pads masked by qmask (G, T2)) and their own tokens causally, merged by
+    LSE. q (R,Hq,t,D); k_own/v_own (R,Hkv,t,D); kq/vq (Ns,Hkv,T,D) int8, ks/vs (Ns,Hkv,T); Kq2/Vq2 (G,Hkv,T2,D);
+    row_group (R,) int. Returns (out (R,Hq,t,D), lse (R,Hq,t))."""
+    Kp = dequant_state(kq, ks, dequant)
+    Vp = dequant_state(vq, vs, dequant)
+    R, Hq, t, D = q.shape
+    rg = row_group.detach().to("cpu").long()
+    out = torch.zeros(R, Hq, t, Vp.shape[-1], dtype=dtype)
+    lse = torch.zeros(R, Hq, t, dtype=dtype)
+    T = Kp.shape[2]
+    for gi in torch.unique(rg).tolist():
+        r = (rg == gi).nonzero().squeeze(1)
+        s = int(group_state[gi])
+        K = torch.cat([Kp[s], _f(Kq2[gi], torch.float32)], 1).to(dtype)
+        V = torch.cat([Vp[s], _f(Vq2[gi], torch.float32)], 1).to(dtype)
+        pm = torch.cat([torch.ones(T, dtype=torch.bool), _f(qmask[gi], torch.bool)])
+        o, l_ = split_attention(q[r], k_own[r], v_own[r], K, V, pm, scale, dtype)
+        out[r], lse[r] = o, l_
+    return out, lse
+
+
 def brute_force_attention(q, k, v, scale: float, allowed):
     """Scalar float64 softmax attention for tiny shapes: q (Tq, D), k (Tk, D), v (Tk, Dv), allowed[i][j] bool.
     Returns (out (Tq, Dv) float64, lse (Tq,) float64). Used only to pin the vectorised oracle."""

@@ -31,10 +31,11 @@ class DecoderConfig:
     vocab: int = 151936
     eps: float = 1e-6
     theta: float = 1e6
+    gated: bool = False  # Qwen3.5's output gate: q_proj gives each head's q and gate (prefix_attn.py:84-85,130)
 
     @property
     def qkv_out(self) -> int:
-        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+        return (self.n_heads * (2 if self.gated else 1) + 2 * self.n_kv_heads) * self.head_dim
 
 
 def make_weights(cfg: DecoderConfig, seed: int = 0, device="cpu", layers: int | None = None, smooth: bool = True):
@@ -131,6 +132,31 @@ def silu_bf16(g: torch.Tensor) -> torch.Tensor:
     return (gd / (1.0 + torch.exp(-gd))).float().to(torch.bfloat16)
 
 
+def sigmoid_bf16(g: torch.Tensor) -> torch.Tensor:
+    """bf16(sigmoid(g)) for bf16 g, sigmoid(g) = 1 / (1 + exp(-g)) evaluated in float64 and rounded once to fp32
+    before the bf16 rounding (torch's sigmoid on a bf16 tensor computes in fp32 and rounds to bf16)."""
+    gd = g.double()
+    return (1.0 / (1.0 + torch.exp(-gd))).float().to(torch.bfloat16)
+
+
+def split_qkv(qkv: torch.Tensor, cfg: DecoderConfig):
+    """The fused projection's output in the reference's layout -> (q|k|v (M, (Hq + 2 Hkv) D), gate (M, Hq D) or
+    None). Gated: q_proj's rows hold each head's q then its gate, (Hq, 2D) per token (prefix_attn.py:84-85), then
+    k_proj's and v_proj's rows."""
+    if not cfg.gated:
+        return qkv, None
+    M = qkv.shape[0]
+    D, Hq = cfg.head_dim, cfg.n_heads
+    qg = qkv[:, :2 * Hq * D].reshape(M, Hq, 2 * D)
+    q, gate = qg[..., :D].reshape(M, Hq * D), qg[..., D:].reshape(M, Hq * D)
+    return torch.cat([q, qkv[:, 2 * Hq * D:]], 1), gate
+
+
+def output_gate(attn: torch.Tensor, gate: torch.Tensor | None) -> torch.Tensor:
+    """o * sigmoid(gate) (prefix_attn.py:130): the bf16 product of the attention output and bf16(sigmoid(gate))."""
+    return attn if gate is None else attn * sigmoid_bf16(gate)
+
+
 def swiglu(gu: torch.Tensor, F: int) -> torch.Tensor:
     """bf16(bf16(silu(g)) * u) with g = gu[:, :F], u = gu[:, F:] (torch's bf16 product: fp32 product, one
     rounding)."""
@@ -163,6 +189,7 @@ def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: 
     x = rmsnorm(h, lw["ln1"], cfg.eps)
     q, sw, inv = qlin["wqkv"]
     qkv, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
+    qkv, gate = split_qkv(qkv, cfg)
     qkv = qk_norm_rope(qkv, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
     qh = qkv[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
     kh = qkv[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
@@ -172,7 +199,7 @@ def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: 
     attn = o.to(torch.bfloat16).transpose(1, 2).reshape(R * t, Hq * D)
     if attn_hook is not None:
         attn = attn_hook(attn)
-    return _layer_tail(h, attn, qlin, lw, cfg)
+    return _layer_tail(h, output_gate(attn, gate), qlin, lw, cfg)
 
 
 def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: int = 0, kvalid=None,
@@ -195,6 +222,7 @@ def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: 
         x = rmsnorm(h, lw["ln1"], cfg.eps)
         q, sw, inv = qlin["wqkv"]
         qkv, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
+        qkv, gate = split_qkv(qkv, cfg)
         qkv = qk_norm_rope(qkv, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
         qh = qkv[:, :Hq * D].reshape(B, S, Hq, D).transpose(1, 2)
         kh = qkv[:, Hq * D:(Hq + Hk) * D].reshape(B, S, Hk, D).transpose(1, 2)
@@ -216,7 +244,7 @@ def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: 
             kq_new, ks_new = torch.cat([kq, kq_new], 2), torch.cat([ks, ks_new], 2)
             vq_new, vs_new = torch.cat([vq, vq_new], 2), torch.cat([vs, vs_new], 2)
         out_kv.append(((kq_new, ks_new), (vq_new, vs_new)))
-        h = _layer_tail(h, attn, qlin, lw, cfg)
+        h = _layer_tail(h, output_gate(attn, gate), qlin, lw, cfg)
     return h, out_kv
 
 

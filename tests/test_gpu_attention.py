@@ -243,3 +243,74 @@ def test_split_attention_dense_prefix(gpu_lib, n, Hq, Hkv, t, D, T, mask):
     out_i = _split_attention(c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV), Ki, Vi,
                              None if pm is None else pm.to(DEV), c["scale"])
     assert_close_rel(out_i.float().cpu(), ref, what="int8 prefix")
+
+
+# ---- two-level prefix (the question cache): state blocks, then the question's own K/V, then the row's tokens
+
+TWO_LEVEL = [
+    dict(seed=61, Ns=2, counts=[2, 0, 3], Hq=8, Hkv=2, t=5, D=128, T=200, T2=70),
+    dict(seed=62, Ns=1, counts=[4, 3], Hq=32, Hkv=8, t=16, D=128, T=2048, T2=130),
+    dict(seed=63, Ns=3, counts=[1, 2, 1, 3], Hq=4, Hkv=4, t=9, D=64, T=0, T2=40),
+    dict(seed=64, Ns=2, counts=[3, 5], Hq=16, Hkv=4, t=12, D=128, T=300, T2=256),
+]
+
+
+def _two_level_case(seed, Ns, counts, Hq, Hkv, t, D, T, T2):
+    g = torch.Generator().manual_seed(seed)
+    G, R = len(counts), sum(counts)
+    c = make_case(seed=seed, Ns=Ns, row_counts=[R] + [0] * (Ns - 1), Hq=Hq, Hkv=Hkv, t=t, D=D, T=T)
+    kq2 = torch.randn(G, Hkv, T2, D, generator=g).to(torch.bfloat16)
+    vq2 = torch.randn(G, Hkv, T2, D, generator=g).to(torch.bfloat16)
+    lens = torch.randint(1, T2 + 1, (G,), generator=g) if T2 > 0 else torch.zeros(G, dtype=torch.long)
+    qmask = torch.arange(T2)[None, :] < lens[:, None]  # each question's K/V right-padded to T2
+    group_state = torch.randint(0, Ns, (G,), generator=g, dtype=torch.int32)
+    row_group = torch.repeat_interleave(torch.arange(G), torch.tensor(counts))
+    return c, kq2, vq2, qmask, group_state, row_group
+
+
+def _run_two_level(c, kq2, vq2, qmask, group_state, counts, T, T2, n_split=None, q=None):
+    from opendecider_amd import kernels
+    img = kernels.stage_state(c["kq"].to(DEV), c["ks"].to(DEV), c["vq"].to(DEV), c["vs"].to(DEV), T, c["scale"]) \
+        if T > 0 else None
+    img2 = kernels.stage_state_bf16(kq2.to(DEV), vq2.to(DEV), T2, c["scale"], qmask.to(torch.uint8).to(DEV)) \
+        if T2 > 0 else None
+    rs, mr = kernels.row_start_of(counts, DEV)
+    return kernels.branched_attn_two_level(c["q"].to(DEV) if q is None else q, c["k"].to(DEV), c["v"].to(DEV), img,
+                                           c["kq"].shape[0], T, img2, T2, c["scale"],
+                                           group_state=group_state.to(DEV), row_start=rs, max_rows=mr,
+                                           return_lse=True, n_split=n_split)
+
+
+@pytest.mark.parametrize("case", TWO_LEVEL, ids=lambda c: f"Ns{c['Ns']}-G{len(c['counts'])}-T{c['T']}-T2{c['T2']}")
+def test_two_level_prefix_matches_oracle(gpu_lib, case):
+    """Rows of question g attend [state group_state[g] (int8, bf16-materialized) ; question g's dense K/V (right
+    pads masked)] and their own tokens causally (prefix_attn.py:94-99 + _split_attention): against the oracle at the
+    2e-3 bar, one pass and split; option order inside a group is bitwise invariant."""
+    c, kq2, vq2, qmask, gs, rg = _two_level_case(**case)
+    T, T2, counts = case["T"], case["T2"], case["counts"]
+    print(f"two-level {case}", flush=True)
+    ref, ref_lse = oa.two_level_attention(c["q"], c["k"], c["v"], c["kq"], c["ks"], c["vq"], c["vs"], kq2, vq2,
+                                          qmask, c["scale"], rg, gs)
+    for n_split in (1, 3):
+        out, lse = _run_two_level(c, kq2, vq2, qmask, gs, counts, T, T2, n_split=n_split)
+        assert_close_rel(out.float().cpu(), ref, what=f"two-level split {n_split}")
+        assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+    # shuffle the rows inside every group: outputs permute bitwise
+    g = torch.Generator().manual_seed(case["seed"] + 1)
+    starts = [0]
+    for n in counts:
+        starts.append(starts[-1] + n)
+    perm = torch.cat([torch.randperm(n, generator=g) + s for n, s in zip(counts, starts)])
+    cp = dict(c, q=c["q"][perm], k=c["k"][perm], v=c["v"][perm])
+    out_p, _ = _run_two_level(cp, kq2, vq2, qmask, gs, counts, T, T2, n_split=1)
+    out1, _ = _run_two_level(c, kq2, vq2, qmask, gs, counts, T, T2, n_split=1)
+    assert torch.equal(out_p, out1[perm.to(DEV)])
+
+
+def test_two_level_without_questions_equals_one_level(gpu_lib):
+    """T2 = 0 and group g reading state g: the same bits as od_branched_attn_staged over the same images."""
+    from opendecider_amd import kernels
+    c = make_case(seed=66, Ns=2, row_counts=[3, 4], Hq=8, Hkv=2, t=6, D=128, T=260)
+    ref, ref_lse = run_gpu(c, staged=True, n_split=1)
+    out, lse = _run_two_level(c, None, None, None, torch.arange(2, dtype=torch.int32), [3, 4], 260, 0, n_split=1)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)) and torch.equal(lse, ref_lse)

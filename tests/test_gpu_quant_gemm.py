@@ -285,3 +285,40 @@ def test_quantizers_nan_and_inf_rows(gpu_lib, K):
         kernels.kv_quant_append(x.view(1, 6, 1, K).to(DEV), q, s, 1)
         assert torch.equal(q[0, :, 1].cpu(), rq) and (q[0, :, 0] == 55).all() and (q[0, :, 2:] == 55).all()
         assert torch.isnan(s[0, [1, 5], 1].cpu()).all() and torch.isinf(s[0, [3, 4], 1].cpu()).all()
+
+
+@pytest.mark.parametrize("M,K,smooth", [(5, 4096, True), (33, 4096, False), (7, 200, True), (64, 128, True)])
+def test_gate_act_quant_bit_exact(gpu_lib, M, K, smooth):
+    """od_gate_act_quant = the oracle's act_quant of bf16(x * bf16(sigmoid(g))) (prefix_attn.py:130 then o_proj's
+    input quantization), bytes and scales, on the vector and scalar paths and with a gate that is a strided view."""
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    big = (torch.randn(M, 2 * K, generator=g) * 6).to(torch.bfloat16)
+    gate = big[:, K:]
+    inv = (1 / (torch.rand(K, generator=g) * 1.5 + 0.5)).to(torch.bfloat16) if smooth else None
+    xq, sx = kernels.gate_act_quant(x.to(DEV), big.to(DEV)[:, K:], None if inv is None else inv.to(DEV))
+    rq, rs = oq.act_quant(od.output_gate(x, gate), inv)
+    assert torch.equal(xq.cpu(), rq) and torch.equal(sx.cpu().view(torch.int32), rs.view(torch.int32))
+
+
+@pytest.mark.parametrize("K", [1, 8])
+def test_gate_sigmoid_on_all_bf16_inputs(gpu_lib, K):
+    """bf16(sigmoid(g)) inside od_gate_act_quant on every bf16 bit pattern of g: row r holds x = (1, 0, ...) and the
+    gate g_r, so its scale max(bf16(sigmoid(g_r)), 1e-8) / 127 carries the gate value (bit-exact against the
+    oracle's correctly rounded table wherever sigmoid(g) >= 1e-8); K = 1 runs the scalar path, K = 8 the vector one."""
+    from opendecider_amd import kernels
+    gv = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    keep = ((gv.view(torch.int16).int() >> 7) & 0xFF) != 0  # normal numbers, infinities and NaNs
+    gv = gv[keep]
+    M = gv.numel()
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    x[:, 0] = 1.0
+    gate = torch.zeros(M, K, dtype=torch.bfloat16)
+    gate[:, 0] = gv
+    _, sx = kernels.gate_act_quant(x.to(DEV), gate.to(DEV))
+    ref = od.sigmoid_bf16(gv).float().clamp_min(1e-8) / 127.0
+    got = sx.cpu()
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got[~nan].view(torch.int32), ref[~nan].view(torch.int32))

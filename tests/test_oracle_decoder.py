@@ -228,18 +228,37 @@ def test_silu_bf16_is_the_correctly_rounded_value_on_all_bf16_inputs():
     assert torch.equal(s[ok].view(torch.int16), ref[ok].view(torch.int16))
 
 
+def test_sigmoid_bf16_is_torch_bf16_sigmoid():
+    """sigmoid_bf16 (the output gate's bf16(sigmoid(g)), correctly rounded in fp32 first) equals torch's bf16 sigmoid
+    bit for bit on every bf16 input except g < -88 (where torch's fp32 exp(-g) overflows and it returns 0), and the
+    60-digit decimal value on a sample."""
+    import decimal
+    decimal.getcontext().prec = 40
+    g = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    s = od.sigmoid_bf16(g)
+    gf = g.float()
+    ref = torch.sigmoid(g)
+    ok = torch.isfinite(ref) & ~(gf < -88)
+    assert torch.equal(s[ok].view(torch.int16), ref[ok].view(torch.int16))
+    fin = (torch.isfinite(gf) & (gf.abs() <= 80)).nonzero().squeeze(1).tolist()
+    for i in fin[::53]:
+        d = decimal.Decimal(float(gf[i]))
+        want = torch.tensor(_nearest_f32(1 / (1 + (-d).exp())), dtype=torch.float32).to(torch.bfloat16)
+        assert s[i].view(torch.int16) == want.view(torch.int16), gf[i].item()
+
+
 # ---- the end-to-end bar of the GPU tests: what it can see at the harness's decision temperature
 
 E2E_SCORING = (dict(n_layers=2, vocab=1000), 2, 32, 16, 256)   # tests/test_gpu_decoder.py CASES["9b_dims_2_layers"]
-T_E2E = 16.0
+T_E2E = 24.0
 
 
 def test_end_to_end_bar_separates_kernel_mistakes_from_the_oracles_own_noise():
     """At the GPU end-to-end test's configuration and temperature: the oracle with float64 attention accumulation
-    moves the option probabilities by well under 1e-4 (its own rounding floor, 2.2e-5), while planted mistakes of the
-    kind a kernel can make move them past the 1e-4 bar: a wrong GQA head mapping (3.9e-4), the keys of another state
-    (2.9e-4), the SmoothQuant scale dropped before the O projection (2.5e-4). Smaller planted mistakes (one position
-    off in RoPE, a non-causal own block, the V scale of the neighbouring token) land near 1e-4 (0.9-1.3e-4); the
+    moves the option probabilities by well under 1e-4 (its own rounding floor, 1.4e-5), while planted mistakes of the
+    kind a kernel can make move them past the 1e-4 bar: a wrong GQA head mapping (2.6e-4), the keys of another state
+    (1.9e-4), the SmoothQuant scale dropped before the O projection (1.6e-4). Smaller planted mistakes (one position
+    off in RoPE, a non-causal own block, the V scale of the neighbouring token) land below 1e-4 (0.6-0.8e-4); the
     stage-by-stage GPU test, bit-exact outside the attention, is what pins those."""
     from helpers import decoder_case
     from oracle import attention as oa
@@ -280,5 +299,5 @@ def test_end_to_end_bar_separates_kernel_mistakes_from_the_oracles_own_noise():
     finally:
         od.quantize_layer = orig_q
     print(f"floor {floor:.2e}; GQA {wrong_gqa:.2e}, other state {wrong_state:.2e}, no 1/s {dropped:.2e}")
-    assert floor <= 3e-5
-    assert min(wrong_gqa, wrong_state, dropped) >= 2e-4
+    assert floor <= 2e-5
+    assert min(wrong_gqa, wrong_state, dropped) >= 1.3e-4
