@@ -293,8 +293,88 @@ class DenseDecoder:
             self.layer(li, h, mid, ws, states[li][0], states[li][1], R, t, pos, row_start, max_rows, kvalid)
         return h
 
-    def readout(self, h: torch.Tensor, B: int, n_opt: int, t: int) -> torch.Tensor:
-        """Mean-pool each option row's final-normed hidden states, one logit per row, the 'none' logit appended,
+    def question_pass(self, ids_q: torch.Tensor, qlen, states, group_state) -> "QuestionCache":
+        """The question pass of the question cache (v3.py:446-534): question g's tokens (ids_q (G, Lq) on the GPU,
+        right-padded; qlen its real lengths) at positions T .. T + Lq - 1 after its state group_state[g] attend that
+        state's int8 K/V and themselves causally through every layer (the branched kernel, one row per question), and
+        each layer's question K/V (bf16, after q/k norm + RoPE; prefix_attn.py:92-93's capture) are written straight
+        into block images (od_attn_stage_bf16, keys past qlen[g] masked): the second prefix level the option rows
+        read. Questions must be grouped by state (group_state non-decreasing)."""
+        cfg = self.cfg
+        G, Lq = ids_q.shape
+        gs = [int(s) for s in group_state]
+        qlen = [int(n) for n in qlen]
+        if len(gs) != G or len(qlen) != G or any(b < a for a, b in zip(gs, gs[1:])):
+            raise ValueError("question_pass: one state per question, questions grouped by state")
+        if any(not 1 <= n <= Lq for n in qlen) or Lq > 256:
+            raise ValueError("question_pass: 1 <= qlen <= Lq <= 256")
+        T = states[0][0].length
+        Ns = states[0][0].q.shape[0]
+        if T + Lq > self.cos.shape[0]:
+            raise ValueError(f"question_pass: positions up to {T + Lq} exceed the rotary tables ({self.cos.shape[0]})")
+        if min(gs) < 0 or max(gs) >= Ns:
+            raise ValueError(f"question_pass: group_state outside [0, {Ns})")
+        ws = self.workspace(G * Lq)
+        h, mid = ws["h"]
+        h.copy_(self.embed.index_select(0, ids_q.reshape(-1)))
+        pos = (T + torch.arange(Lq, dtype=torch.int32)).repeat(G).to(self.dev)
+        row_start, max_rows = kernels.row_start_of([gs.count(s) for s in range(Ns)], self.dev)
+        qmask = (torch.arange(Lq)[None, :] < torch.tensor(qlen)[:, None]).to(torch.uint8).to(self.dev)
+        D = cfg.head_dim
+        images = []
+        for li in range(len(self.layers)):
+            state_k, state_v = states[li]
+            qkv = self._attn_in(li, h, ws, pos)
+            q, k, v, attn = self._heads(qkv, ws, G, Lq)
+            img = None
+            if state_k.length > 0 and kernels.uses_staging(max_rows, Lq, cfg.n_heads, cfg.n_kv_heads):
+                img = self.state_images(li, state_k, state_v)
+            kernels.branched_attn(q, k, v, state_k.q, state_k.scale, state_v.q, state_v.scale, D ** -0.5,
+                                  length=state_k.length, out=attn, row_start=row_start, max_rows=max_rows,
+                                  images=img)
+            images.append(kernels.stage_state_bf16(k, v, Lq, D ** -0.5, qmask))
+            self._attn_out_mlp(li, h, mid, ws)
+        return QuestionCache(images, Lq, qlen, gs, torch.tensor(gs, dtype=torch.int32).to(self.dev), T)
+
+    def score_qcache(self, ids_o: torch.Tensor, qc: "QuestionCache", states) -> torch.Tensor:
+        """Option rows over the question cache: ids_o (G, n_opt, t) on the GPU; the rows of question g start right
+        after its last real token (position T + qlen[g], v3.py:520) and attend [state group_state[g] ; question g's
+        K/V] and their own tokens (od_branched_attn_staged2). Returns (G, n_opt + 1) log-probabilities."""
+        cfg = self.cfg
+        G, n_opt, t = ids_o.shape
+        if G != len(qc.qlen):
+            raise ValueError("score_qcache: one group of option rows per question")
+        T = states[0][0].length
+        if T != qc.T:
+            raise ValueError("score_qcache: the states changed since the question pass")
+        R = G * n_opt
+        if T + max(qc.qlen) + t > self.cos.shape[0]:
+            raise ValueError(f"score_qcache: positions up to {T + max(qc.qlen) + t} exceed the rotary tables")
+        key = ("qcache", T, tuple(qc.qlen), n_opt, t)
+        if key not in self._rows:
+            pos = torch.cat([T + n + torch.arange(t, dtype=torch.int32) for n in qc.qlen for _ in range(n_opt)])
+            self._rows[key] = (pos.to(self.dev), *kernels.row_start_of([n_opt] * G, self.dev))
+        pos, row_start, max_rows = self._rows[key]
+        ws = self.workspace(R * t)
+        h, mid = ws["h"]
+        h.copy_(self.embed.index_select(0, ids_o.reshape(-1)))
+        Ns = states[0][0].q.shape[0]
+        D = cfg.head_dim
+        for li in range(len(self.layers)):
+            state_k, state_v = states[li]
+            qkv = self._attn_in(li, h, ws, pos)
+            q, k, v, attn = self._heads(qkv, ws, R, t)
+            img = self.state_images(li, state_k, state_v) if T > 0 else None
+            kernels.branched_attn_two_level(q, k, v, img, Ns, T, qc.images[li], qc.Lq, D ** -0.5,
+                                            group_state=qc.group_state, row_start=row_start, max_rows=max_rows,
+                                            out=attn)
+            self._attn_out_mlp(li, h, mid, ws)
+        return self.readout(h, G, n_opt, t)
+
+    def readout(self, h: torch.Tensor, B: int, n_opt: int, t: int, pool_last: int | None = None) -> torch.Tensor:
+        """Mean-pool each option row's final-normed hidden states (the last pool_last tokens of each row when
+        given: the option's own tokens of a row that carries its question too), one logit per row, the 'none' logit
+        appended,
         divided by the decision temperature (softmax(logits / T), decider.py:255-257), log-softmax per request:
         (B, n_opt + 1) fp32. The RMSNorm factor is the correctly rounded one (a float64 mean of squares, as
         od_rmsnorm_quant computes it)."""
@@ -302,7 +382,8 @@ class DenseDecoder:
         hd = hf.double()
         r = (1.0 / torch.sqrt((hd * hd).sum(-1, keepdim=True) / hd.shape[-1] + self._eps32)).float()
         hn = (self.final_norm * (hf * r).to(torch.bfloat16)).float()
-        pooled = hn.view(B, n_opt, t, -1).mean(2)
+        hn = hn.view(B, n_opt, t, -1)
+        pooled = (hn if pool_last is None else hn[:, :, t - pool_last:]).mean(2)
         logits = torch.cat([pooled @ self.head, self.none_logit.expand(B, 1)], 1)
         return torch.log_softmax(logits / self.temperature, -1)
 
@@ -311,7 +392,7 @@ class DenseDecoder:
             raise ValueError(f"positions up to {T + t} exceed the rotary tables ({self.cos.shape[0]})")
         return (T + torch.arange(t, dtype=torch.int32)).repeat(R).to(self.dev)
 
-    def score(self, ids: torch.Tensor, states: list, kvalid=None) -> torch.Tensor:
+    def score(self, ids: torch.Tensor, states: list, kvalid=None, pool_last: int | None = None) -> torch.Tensor:
         """ids (B, n_opt, t) option-row token ids on the GPU; states[l] = (K, V) Int8KVCache of the B cached
         states. Returns (B, n_opt + 1) log-probabilities over the options and 'none'."""
         B, n_opt, t = ids.shape
@@ -320,7 +401,7 @@ class DenseDecoder:
         h0 = self.embed.index_select(0, ids.reshape(-1))
         pos, row_start, max_rows = self.row_layout(T, B, n_opt, t)
         h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
-        return self.readout(h, B, n_opt, t)
+        return self.readout(h, B, n_opt, t, pool_last)
 
     def prefill_layout(self, n0: int, B: int, S: int):
         """Device positions of a state pass appending S tokens at n0 to B states, and the one-row-per-state offsets
@@ -372,3 +453,15 @@ class DenseDecoder:
             row_start, max_rows = kernels.row_start_of([n_opt] * B, self.dev)
             self._rows[key] = (pos, row_start, max_rows)
         return self._rows[key]
+
+
+@dataclass
+class QuestionCache:
+    """The question cache of a question pass: per layer, the block images of every question's K/V (the second prefix
+    level), the padded length Lq, the real lengths, each question's state, and the state length it was built on."""
+    images: list
+    Lq: int
+    qlen: list
+    gs: list
+    group_state: torch.Tensor
+    T: int

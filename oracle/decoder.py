@@ -178,13 +178,16 @@ def _layer_tail(h, attn, qlin, lw, cfg: DecoderConfig):
 
 
 def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: int, pos, cos, sin,
-                  row_state=None, kvalid=None, attn_hook=None, dequant: str = "bf16", attn_dtype=torch.float32):
+                  row_state=None, kvalid=None, attn_hook=None, dequant: str = "bf16", attn_dtype=torch.float32,
+                  capture=None, two_level=None):
     """One decoder layer over the option-row tokens h (M = R * t, hidden) bf16. qlin: {name: (q, sw, inv_s)}.
     state_k/state_v: (kq int8 (Ns, Hkv, T, D), ks fp32 (Ns, Hkv, T)) of this layer. attn_hook, if given, maps the
     bf16 attention output (M, Hq D) to the tensor used downstream (sensitivity studies). dequant: how the int8 state
     becomes K/V ("bf16": the reference's materialize, q.to(bf16) * s.to(bf16), prefix_attn.py:145-149; "fp32": q * s
     exact); attn_dtype: the attention's arithmetic (fp32 as the reference's CPU branch, or float64 to measure how
-    much the result depends on the accumulation). Returns the new h."""
+    much the result depends on the accumulation). capture: a list that receives this layer's (k, v) (R, Hkv, t, D)
+    bf16 after q/k norm + RoPE (the question pass's capture, prefix_attn.py:92-93). two_level: (Kq2, Vq2, qmask,
+    row_group, group_state) to attend the two-level prefix instead (prefix_attn.py:94-99). Returns the new h."""
     D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     x = rmsnorm(h, lw["ln1"], cfg.eps)
     q, sw, inv = qlin["wqkv"]
@@ -194,8 +197,15 @@ def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: 
     qh = qkv[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
     kh = qkv[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
     vh = qkv[:, (Hq + Hk) * D:].reshape(R, t, Hk, D).transpose(1, 2)
-    o, _ = oa.branched_attention_int8(qh, kh, vh, state_k[0], state_k[1], state_v[0], state_v[1], D ** -0.5,
-                                      kvalid, row_state, dequant=dequant, dtype=attn_dtype)
+    if capture is not None:
+        capture.append((kh.contiguous(), vh.contiguous()))
+    if two_level is not None:
+        Kq2, Vq2, qmask, row_group, group_state = two_level
+        o, _ = oa.two_level_attention(qh, kh, vh, state_k[0], state_k[1], state_v[0], state_v[1], Kq2, Vq2, qmask,
+                                      D ** -0.5, row_group, group_state, dequant=dequant, dtype=attn_dtype)
+    else:
+        o, _ = oa.branched_attention_int8(qh, kh, vh, state_k[0], state_k[1], state_v[0], state_v[1], D ** -0.5,
+                                          kvalid, row_state, dequant=dequant, dtype=attn_dtype)
     attn = o.to(torch.bfloat16).transpose(1, 2).reshape(R * t, Hq * D)
     if attn_hook is not None:
         attn = attn_hook(attn)
@@ -253,11 +263,13 @@ def quantize_layer(lw):
 
 
 def readout(h, final_norm, head, none_logit, cfg: DecoderConfig, B: int, n_opt: int, t: int,
-            temperature: float = 1.0):
-    """Mean-pool each option row's final-normed hidden states, one logit per row (pooled . head), append the
-    'none' logit, divide by the decision temperature (the reference's softmax(logits / T), decider.py:255-257) and
-    log-softmax per request. Returns (B, n_opt + 1) fp32 log-probabilities."""
-    hf = rmsnorm(h, final_norm, cfg.eps).float().reshape(B, n_opt, t, -1).mean(2)
+            temperature: float = 1.0, pool_last: int | None = None):
+    """Mean-pool each option row's final-normed hidden states (its last pool_last tokens when given: the option's
+    own tokens of a row that also carries its question), one logit per row (pooled . head), append the 'none' logit,
+    divide by the decision temperature (the reference's softmax(logits / T), decider.py:255-257) and log-softmax per
+    request. Returns (B, n_opt + 1) fp32 log-probabilities."""
+    hf = rmsnorm(h, final_norm, cfg.eps).float().reshape(B, n_opt, t, -1)
+    hf = (hf if pool_last is None else hf[:, :, t - pool_last:]).mean(2)
     logits = hf @ head.float()
     logits = torch.cat([logits, none_logit.float().expand(B, 1)], 1)
     return torch.log_softmax(logits / temperature, -1)
@@ -274,7 +286,8 @@ def nudge_bf16(x: torch.Tensor, frac: float, seed: int) -> torch.Tensor:
 
 
 def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, kvalid=None, attn_hook=None,
-                     dequant: str = "bf16", attn_dtype=torch.float32, temperature: float | None = None):
+                     dequant: str = "bf16", attn_dtype=torch.float32, temperature: float | None = None,
+                     pool_last: int | None = None):
     """Option-row scoring pass: ids (B, n_opt, t) token ids; state_kv[l] = ((kq, ks), (vq, vs)) per layer for the
     B cached states of length T. dequant / attn_dtype as layer_forward, temperature as readout (None: the weights'
     "temperature", 1 if absent). Returns (B, n_opt + 1) log-probabilities."""
@@ -289,4 +302,47 @@ def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, 
     for li, lw in enumerate(weights["layers"]):
         h = layer_forward(h, lw, quantize_layer(lw), cfg, state_kv[li][0], state_kv[li][1], R, t, pos, cos, sin,
                           row_state, kvalid, attn_hook, dequant, attn_dtype)
-    return readout(h, weights["final_norm"], weights["head"], weights["none_logit"], cfg, B, n_opt, t, temperature)
+    return readout(h, weights["final_norm"], weights["head"], weights["none_logit"], cfg, B, n_opt, t, temperature,
+                   pool_last)
+
+
+def question_forward(ids_q, weights, embed, cfg: DecoderConfig, state_kv, T: int, group_state, attn_dtype=torch.float32):
+    """The question pass of the question cache (v3.py:446-534, the capture of prefix_attn.py:92-93): question g's
+    Lq tokens (ids_q (G, Lq), right-padded), at positions T .. T + Lq - 1 after its state group_state[g], attend that
+    state's int8 K/V and themselves causally through every layer. Pads come after the real tokens, so no real token
+    sees them; they are masked as keys by the rows. Returns [(K, V) (G, Hkv, Lq, D) bf16] per layer."""
+    G, Lq = ids_q.shape
+    h = embed[ids_q.reshape(-1)]
+    pos = (T + torch.arange(Lq)).repeat(G)
+    cos, sin = rope_tables(cfg, T + Lq)
+    gs = torch.as_tensor(group_state).long()
+    out = []
+    for li, lw in enumerate(weights["layers"]):
+        h = layer_forward(h, lw, quantize_layer(lw), cfg, state_kv[li][0], state_kv[li][1], G, Lq, pos, cos, sin,
+                          gs, attn_dtype=attn_dtype, capture=out)
+    return out
+
+
+def qcache_decision_forward(ids_o, weights, embed, cfg: DecoderConfig, state_kv, T: int, q_kv, qlen, group_state,
+                            attn_dtype=torch.float32, temperature: float | None = None):
+    """Option rows over the question cache: ids_o (G, n_opt, t); the rows of question g start right after their
+    question's last real token (position T + qlen[g], v3.py:520) and attend [state group_state[g] ; question g's K/V
+    from question_forward, keys past qlen[g] masked] + their own tokens causally (prefix_attn.py:94-99). Returns
+    (G, n_opt + 1) log-probabilities."""
+    if temperature is None:
+        temperature = float(weights.get("temperature", 1.0))
+    G, n_opt, t = ids_o.shape
+    R = G * n_opt
+    qlen = torch.as_tensor(qlen).long()
+    Lq = q_kv[0][0].shape[2]
+    row_group = torch.arange(G).repeat_interleave(n_opt)
+    pos = (T + qlen[row_group][:, None] + torch.arange(t)[None, :]).reshape(-1)
+    qmask = torch.arange(Lq)[None, :] < qlen[:, None]
+    cos, sin = rope_tables(cfg, T + Lq + t)
+    gs = torch.as_tensor(group_state).long()
+    h = embed[ids_o.reshape(-1)]
+    for li, lw in enumerate(weights["layers"]):
+        Kq2, Vq2 = q_kv[li]
+        h = layer_forward(h, lw, quantize_layer(lw), cfg, state_kv[li][0], state_kv[li][1], R, t, pos, cos, sin,
+                          attn_dtype=attn_dtype, two_level=(Kq2, Vq2, qmask, row_group, gs))
+    return readout(h, weights["final_norm"], weights["head"], weights["none_logit"], cfg, G, n_opt, t, temperature)

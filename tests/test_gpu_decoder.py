@@ -352,3 +352,41 @@ def test_scoring_pass_graph_replays_equal_eager(gpu_lib, name, cfg_kw, B, n_opt,
         torch.cuda.synchronize()
         assert torch.equal(other, eager2), f"eager pass after replay {i}"
     assert torch.equal(run(ids2.to(DEV)), eager2)
+
+
+QCACHE_CASES = [
+    # name, cfg, states, state tokens, questions (their states), question width, real lengths, options, tokens
+    ("tiny_d64", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500), 2, 70,
+     [0, 0, 1], 12, [12, 7, 10], 4, 5),
+    ("9b_dims_2_layers", dict(n_layers=2, vocab=1000), 2, 256, [0, 1], 48, [48, 33], 32, 8),
+    # one unpadded question per state: also compared with rows that carry the question
+    ("tiny_d64_full", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500), 2, 70,
+     [0, 1], 12, [12, 12], 4, 5),
+    ("9b_dims_2_layers_full", dict(n_layers=2, vocab=1000), 2, 256, [0, 1], 48, [48, 48], 32, 8),
+]
+
+
+@pytest.mark.parametrize("name,cfg_kw,B,T,gs,Lq,qlen,n_opt,t", QCACHE_CASES)
+def test_question_cache_end_to_end(gpu_lib, name, cfg_kw, B, T, gs, Lq, qlen, n_opt, t):
+    """The question cache (v3.py:446-534): a question pass (each question's tokens over its state, every layer's
+    question K/V kept as block images, pads masked), then option rows over [state ; question K/V] + their own tokens
+    (od_branched_attn_staged2), against the oracle's question_forward + qcache_decision_forward at the end-to-end
+    bar; and against rows that carry [question ; option] over the state alone (same features, v3.py:447-450) at the
+    same bar, for the questions without pads."""
+    cfg, w, emb, states, _, dec, gstates = _setup(cfg_kw, B, 1, Lq + t, T)  # rotary tables past T + Lq + t
+    g = torch.Generator().manual_seed(11)
+    ids_q = torch.randint(0, cfg.vocab, (len(gs), Lq), generator=g)
+    ids_o = torch.randint(0, cfg.vocab, (len(gs), n_opt, t), generator=g)
+    print(f"{name}: question cache questions={len(gs)} Lq={Lq} qlen={qlen} options={n_opt} t={t}", flush=True)
+    qc = dec.question_pass(ids_q.to(DEV), qlen, gstates, gs)
+    lp = dec.score_qcache(ids_o.to(DEV), qc, gstates)
+    q_kv = od.question_forward(ids_q, w, emb, cfg, states, T, gs)
+    ref = od.qcache_decision_forward(ids_o, w, emb, cfg, states, T, q_kv, qlen, gs)
+    _assert_e2e(lp, ref, f"{name} (question cache)")
+    full = [i for i, n in enumerate(qlen) if n == Lq and gs.count(gs[i]) == 1]
+    if len(full) == B:  # one unpadded question per state: rows that carry the question, scored by `score`
+        rows = torch.cat([ids_q[full][:, None, :].expand(B, n_opt, Lq), ids_o[full]], 2)
+        lp_rows = dec.score(rows.to(DEV), gstates, pool_last=t)
+        dp = (lp_rows.exp() - lp[full].exp()).abs().max().item()
+        print(f"{name}: question cache vs rows carrying the question: max |dp| {dp:.2e}")
+        assert dp <= PROB_ABS

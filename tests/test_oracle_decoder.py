@@ -301,3 +301,23 @@ def test_end_to_end_bar_separates_kernel_mistakes_from_the_oracles_own_noise():
     print(f"floor {floor:.2e}; GQA {wrong_gqa:.2e}, other state {wrong_state:.2e}, no 1/s {dropped:.2e}")
     assert floor <= 2e-5
     assert min(wrong_gqa, wrong_state, dropped) >= 1.3e-4
+
+
+def test_question_cache_equals_rows_that_carry_the_question():
+    """The question cache's claim (v3.py:447-450: same features as repeating the question in each row): with float64
+    attention, a question pass + option rows over [state ; question K/V] give the same log-probabilities as rows that
+    carry [question ; option] tokens over the state alone, pooled over the option tokens only (one question per
+    state, no pads): every bf16 attention output agrees, so everything downstream is identical."""
+    from helpers import decoder_case
+    cfg, w, emb, states, _ = decoder_case(dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64,
+                                               n_layers=2, vocab=500), 2, 1, 1, 70, 24.0)
+    g = torch.Generator().manual_seed(12)
+    Lq, n_opt, t = 9, 4, 5
+    ids_q = torch.randint(0, 500, (2, Lq), generator=g)
+    ids_o = torch.randint(0, 500, (2, n_opt, t), generator=g)
+    q_kv = od.question_forward(ids_q, w, emb, cfg, states, 70, [0, 1], attn_dtype=torch.float64)
+    lp_qc = od.qcache_decision_forward(ids_o, w, emb, cfg, states, 70, q_kv, [Lq, Lq], [0, 1],
+                                       attn_dtype=torch.float64)
+    rows = torch.cat([ids_q[:, None, :].expand(2, n_opt, Lq), ids_o], 2)  # (2, n_opt, Lq + t)
+    lp_rows = od.decision_forward(rows, w, emb, cfg, states, 70, attn_dtype=torch.float64, pool_last=t)
+    assert (lp_qc - lp_rows).abs().max().item() <= 1e-6
