@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--state", type=int, default=2048)
     ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm", "gemm_traffic",
-                                           "attention", "lm_logprob"],
+                                           "attention", "lm_logprob", "qcache_rows"],
                     default="scoring",
                     help="scoring (default): the metric's option-row scoring pass over cached 2048-token states; "
                          "decision: full decision forward from token ids (4 requests, 4096-token states prefilled, "
@@ -57,7 +57,9 @@ def parse():
                          "attention: the branched attention alone on the config-1 shape and on the KV-bound probe "
                          "(32768-token states, 2 options x 16 tokens per state); lm_logprob: the LM head's token "
                          "log-prob of 1024 rows over a 151936 x 4096 int8 table; gemm: the W8A8 linear alone over "
-                         "the reference's (K, N) x M sweep (scripts/bench_gemm.py) and the 9B layer shapes at M = 4096")
+                         "the reference's (K, N) x M sweep (scripts/bench_gemm.py) and the 9B layer shapes at M = 4096; "
+                         "qcache_rows: decide latency with and without the question cache over the reference's "
+                         "(questions, options) shapes (scripts/bench_qcache_rows.py)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--scoring-only", action="store_true",
                     help="the default line without its decision / wide_choice sub-objects")
@@ -573,6 +575,70 @@ def run_gemm(args):
     return res
 
 
+def run_qcache_rows(args):
+    """Where the question cache pays off (scripts/bench_qcache_rows.py): the latency of one decision with and
+    without it, over the reference's (questions, options) shapes, on a 36-layer 9B-dims decoder with one cached
+    900-token int8 state (synthetic K/V). A question is its prompt plus the listing of its options: 24 + 4 k tokens
+    for k options (capped at 256); an option is 6 tokens. With the cache: one question pass (each question's tokens
+    over the state; every layer's question K/V kept as second-level block images) and then the option rows over
+    [state ; question]. Without: every option row carries its question's tokens followed by its own, over the state
+    alone, pooled over the option tokens. Median of 3 after a warm-up, each call synchronized."""
+    import torch
+
+    from opendecider_amd import decoder as dmod
+    dev = "cuda:0"
+    cfg = dmod.DecoderConfig(n_layers=args.layers)
+    S, t = 900, 6
+    shapes = [(1, 4), (3, 4), (2, 16), (4, 16), (2, 32), (8, 16), (4, 32), (16, 8), (8, 32), (16, 16), (16, 32)]
+    dec = dmod.random_decoder(cfg, seed=0, device=dev, max_pos=S + 256 + t + 16)
+    g = torch.Generator(device=dev).manual_seed(7)
+    states = dec.new_state_caches(1, S)
+    for kc, vc in states:
+        for c in (kc, vc):
+            c.append(torch.randn(1, cfg.n_kv_heads, S, cfg.head_dim, generator=g, device=dev).to(torch.bfloat16))
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[1] * 1e3
+
+    rows = []
+    for n, k in shapes:
+        Lq = min(256 - t, 24 + 4 * k)
+        ids_q = torch.randint(0, cfg.vocab, (n, Lq), generator=g, device=dev)
+        ids_o = torch.randint(0, cfg.vocab, (n, k, t), generator=g, device=dev)
+        gs = [0] * n
+
+        def with_cache():
+            qc = dec.question_pass(ids_q, [Lq] * n, states, gs)
+            return dec.score_qcache(ids_o, qc, states)
+
+        rows_ids = torch.cat([ids_q[:, None, :].expand(n, k, Lq), ids_o], 2).reshape(1, n * k, Lq + t)
+
+        def without_cache():
+            return dec.score(rows_ids, states, pool_last=t)
+
+        w_ms, wo_ms = timed(with_cache), timed(without_cache)
+        rows.append({"questions": n, "options": k, "rows": n * k, "question_tokens": Lq, "option_tokens": t,
+                     "with_qcache_ms": w_ms, "without_qcache_ms": wo_ms, "speedup": wo_ms / w_ms})
+        dec._ws.clear()
+        torch.cuda.empty_cache()
+    last = rows[-1]
+    return {"metric": "decide latency with / without the question cache (speedup at 16 questions x 32 options)",
+            "value": last["speedup"], "unit": "x", "n_gpus": 1, "steps": 3, "warmup": 1, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+            "config": {"workload": (f"one {S}-token int8 state, {cfg.n_layers}-layer 9B-dims decoder; questions of "
+                                    f"24 + 4 k tokens, options of {t} tokens; scripts/bench_qcache_rows.py shapes"),
+                       "state_tokens": S, "layers": cfg.n_layers},
+            "shapes": rows}
+
+
 def run_gemm_traffic(args):
     """The run profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE for roofline.traffic: a 256 MiB device copy
     (known bytes, to calibrate the counters), then two scoring passes through 2 layers (M = 4096: QKV, O, gate+up,
@@ -745,7 +811,7 @@ def main():
         torch.cuda.set_device(0)
         fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm": run_gemm,
               "gemm_traffic": run_gemm_traffic, "attention": run_attention,
-              "lm_logprob": run_lm_logprob}[args.workload]
+              "lm_logprob": run_lm_logprob, "qcache_rows": run_qcache_rows}[args.workload]
         print(json.dumps(fn(args)))
         return
 
