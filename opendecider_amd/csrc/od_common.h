@@ -44,23 +44,18 @@ __device__ __forceinline__ float od_absmax_bf16x2_value(uint32_t acc) {
 }
 
 // bf16(RN32(silu(g))), silu(g) = g / (1 + exp(-g)): the fp32 value of silu correctly rounded, then rounded to
-// bf16 (the SwiGLU of a bf16 module computes silu in fp32 and rounds to bf16). The fast step for a bf16 value g
-// splits -g log2(e) = y_hi + y_lo exactly enough: y_hi = -g L_hi is exact (g has 8 significant bits, L_hi = log2(e)
-// to 16 bits), and exp2(y_lo) = 1 + t + t^2 / 2 with t = -g (log2(e) - L_hi) ln 2, |t| < 2^-10; so
-// exp(-g) = v_exp_f32(y_hi) (1 + t + t^2 / 2) is within about 2 ulps, and with the sum, the reciprocal and the
-// product the fast value lies within 4 fp32 ulps of silu(g). Its bf16 rounding is then the bf16 rounding of the
-// correctly rounded value unless its low 16 bits lie within 16 ulps of the bf16 midpoint 0x8000. Those values
-// (about 1 in 2000), and |g| >= 64 (where exp(-g) or the result leaves the normal fp32 range), are recomputed in
-// float64 and rounded once to fp32. Every SwiGLU kernel uses this one function, so fused and unfused paths agree bit
-// for bit, and g has 65536 values, so it is checked against the oracle exhaustively.
-constexpr float kOdLog2eHi = 1.44268798828125f;      // 47274 / 2^15
-constexpr float kOdLog2eLoLn2 = 4.888495368504664e-06f;  // (log2(e) - kOdLog2eHi) ln 2
+// bf16 (the SwiGLU of a bf16 module computes silu in fp32 and rounds to bf16). Fast step for |g| < 16:
+// exp(-g) = v_exp_f32(RN(-g L)) with L = log2(e) in fp32; the argument (|arg| < 23.1) is off by at most 2^-20 from
+// the product's rounding plus 16 |L - log2(e)| < 3.1e-7 from the constant, i.e. 1.3e-6, which costs 7.5 fp32 ulps
+// in exp; v_exp_f32 adds one more, and the sum, the reciprocal and the product keep the fast value within 11 ulps of
+// silu(g). Its bf16 rounding is then the bf16 rounding of the correctly rounded value unless
+// its low 16 bits lie within 16 ulps of the bf16 midpoint 0x8000. Those values (about 1 in 2000), and |g| >= 16, are
+// recomputed in float64 and rounded once to fp32. Every SwiGLU kernel uses this one function, so fused and unfused
+// paths agree bit for bit, and g has 65536 values, so it is checked against the oracle exhaustively.
 __device__ __forceinline__ float od_silu_bf16(float g) {
-  const float t = -g * kOdLog2eLoLn2;
-  const float e = __builtin_amdgcn_exp2f(-g * kOdLog2eHi) * __builtin_fmaf(t, __builtin_fmaf(t, 0.5f, 1.0f), 1.0f);
-  float s = g * __builtin_amdgcn_rcpf(1.0f + e);
+  float s = g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
   const uint32_t lo = __float_as_uint(s) & 0xffffu;
-  if (__builtin_expect((lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 64.0f), 0)) {
+  if (__builtin_expect((lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 16.0f), 0)) {
     const double gd = (double)g;
     s = (float)(gd / (1.0 + exp(-gd)));
   }
@@ -69,13 +64,11 @@ __device__ __forceinline__ float od_silu_bf16(float g) {
 
 // bf16(RN32(sigmoid(g))), sigmoid(g) = 1 / (1 + exp(-g)), for the output gate (torch.sigmoid on a bf16 tensor
 // computes in fp32 and rounds to bf16): the same exp(-g) as od_silu_bf16, then the sum and a reciprocal, within
-// 4 fp32 ulps; values within 16 ulps of a bf16 midpoint, and |g| >= 64, are recomputed in float64.
+// 10 fp32 ulps; values within 16 ulps of a bf16 midpoint, and |g| >= 16, are recomputed in float64.
 __device__ __forceinline__ float od_sigmoid_bf16(float g) {
-  const float t = -g * kOdLog2eLoLn2;
-  const float e = __builtin_amdgcn_exp2f(-g * kOdLog2eHi) * __builtin_fmaf(t, __builtin_fmaf(t, 0.5f, 1.0f), 1.0f);
-  float s = __builtin_amdgcn_rcpf(1.0f + e);
+  float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
   const uint32_t lo = __float_as_uint(s) & 0xffffu;
-  if (__builtin_expect((lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 64.0f), 0)) {
+  if (__builtin_expect((lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 16.0f), 0)) {
     const double gd = (double)g;
     s = (float)(1.0 / (1.0 + exp(-gd)));
   }
