@@ -6,26 +6,31 @@
 // cover the other's LDS latency and barrier waits):
 //   * workgroup tile BM x BN = 256 x {256 | 192}; K advances 128 bytes per stage, so every row segment a stage
 //     loads is one whole 128-byte line (64-byte segments measured at about 60% of the L2 -> CU rate).
-//   * global -> registers -> LDS: each thread holds the next stage of its share of the A and W slabs in registers
-//     (buffer loads issued a stage before they are needed) and writes it into the LDS buffer that is not being
-//     read; the LDS holds two stages (2 x (256 + BN) x 128 B <= 128 KB). Rows past M/N and bytes past K read as
-//     zeros (buffer range check).
+//   * persistent workgroups, one per CU: workgroup b computes tiles b, b + G, b + 2G, ... (G = grid size), as one
+//     pipeline over its (tile, k-tile) stages, so the next tile's first stage loads during the last stage of the
+//     current one and the epilogue's stores drain while the next tile computes (launched one tile per workgroup,
+//     every CU stalled on its epilogue at the same time: about 10-15 us per wave of tiles).
+//   * global -> LDS by LDS DMA (buffer_load_dwordx4 ... lds): no register staging and no LDS write instructions;
+//     the LDS holds two stages (2 x (256 + BN) x 128 B <= 128 KB) and the loads of the next stage are issued at
+//     the start of the current one. Rows past M/N and bytes past K read as zeros (buffer range check).
 //   * 4 x 2 waves, each owning a 64 x BN/2 sub-tile = 2 x (BN/64) MFMA tiles of 32 x 32 (up to 128 int32
 //     accumulators per lane). Per 32 k a wave reads 2 + BN/64 fragments (ds_read_b128) for 2 x BN/64 MFMAs.
-//   * software pipeline: fragments are double-buffered in registers across k-steps and across stages; the LDS
-//     writes and buffer loads of the next stages are spread between the MFMAs of one k-step; one barrier per
-//     stage, preceded by an lgkmcnt wait only (a fenced barrier would also wait for the loads in flight).
+//   * software pipeline: fragments are double-buffered in registers across k-steps and across stages; the DMA
+//     loads of the next stage are spread between the MFMAs of one k-step; one barrier per stage.
 //   * LDS rows are 128 B (8 chunks of 16 B); chunk c of row r is stored at c ^ ((r >> 1) & 7). gfx950 serves 16
 //     lanes of a ds_read_b128 per cycle from 64 banks (256-byte period): a fragment read (16 consecutive rows,
-//     one chunk) then hits 16 distinct 16-byte bank quads; the 8 lanes of a ds_write_b128 cycle write the 8
-//     chunks of one row, also distinct.
+//     one chunk) then hits 16 distinct 16-byte bank quads.
 //   * blockIdx -> tile is XCD-aware: workgroups are dealt round-robin over the 8 XCDs, so each XCD gets a contiguous
 //     range of tiles in a grouped (kGroupM tile-rows) order, and the tiles one XCD runs together share A/W panels
-//     in its L2.
-//   * epilogue: each wave stages its accumulators 32 rows at a time through a private LDS band and writes 4
+//     in its L2 (G is a multiple of 8, so a workgroup's later tiles stay on its XCD's range).
+//   * epilogue: each wave stages its accumulators 16 rows at a time through a private LDS band and writes 4
 //     columns per lane, a wave covering whole row segments; scales, bias and residual are applied in fp32 in the
 //     oracle's order and rounded once to bf16.
+// Measured ceiling on MI355X: int8 MFMAs on changing operands, fed by LDS fragment reads and no global traffic,
+// sustain about 3.0-3.1 of the 5.0 POP/s peak (the clock drops to about 1.9-2.1 GHz under that load; with constant
+// operands the same loop reaches 4.9 POP/s at 2.38 GHz).
 // int32 accumulation is exact for K < 133,144 (|acc| <= 127^2 K < 2^31), so any correct GEMM is bit-exact.
+#include <atomic>
 #include <type_traits>
 
 #include "od_common.h"
@@ -62,11 +67,6 @@ __device__ __forceinline__ float bfr(float v) { return od_bf16_to_f32(od_f32_to_
 // byte offset of logical chunk c (0..7) of row r inside a slab
 __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-__device__ __forceinline__ void barrier_lds() {
-  // LDS traffic of this wave complete, then the workgroup barrier (no fence: buffer loads stay in flight)
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int ntiles = tiles_m * tiles_n;
   const int xcd = bid & 7, local = bid >> 3;
@@ -80,193 +80,31 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
   tn = in_group / gsz;
 }
 
-// One thread's share of a ROWS x 128-byte slab: load i covers row i * (kThreads / kCpr) + tid / kCpr, chunk
-// tid % kCpr (8 consecutive lanes read one whole 128-byte row segment). The per-thread byte offset in the matrix
-// (vo) and in the slab (lo) are those of load 0; load i adds i * 64 rows (ld * 64 * i bytes in the matrix,
-// 64 * 128 * i bytes in LDS, an immediate).
-template <int ROWS>
-struct Slab {
-  static constexpr int kLoads = ROWS * kCpr / kThreads;  // 4 for 256 rows, 3 for 192
-  static constexpr int kRowsPerLoad = kThreads / kCpr;   // 64
-  int vo, lo, col;
-  __device__ __forceinline__ void init(int64_t ld) {
-    const int tid = threadIdx.x;
-    const int row = tid / kCpr, c = tid % kCpr;
-    col = c * 16;
-    vo = (int)(row * ld) + col;  // < 32 ld + 128: the host keeps 256 ld below 2^31
-    lo = swz(row, c);  // rows i * 64 + row keep the same (row >> 1) & 7, so the swizzle is load-independent
-  }
-};
-
-template <int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU>
-__global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
-  constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile: 64 x BN/2
-  constexpr int TM = kRowsW / 32;    // 2
-  constexpr int TN = kColsW / 32;    // 4 or 3
-  constexpr int kSlabA = BM * BK, kSlabB = BN * BK, kStage = kSlabA + kSlabB;
-  using SA = Slab<BM>;
-  using SB = Slab<BN>;
-  __shared__ __attribute__((aligned(16))) int8_t smem[2 * kStage];
-
-  int tm, tn;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / kWN, wn = wave % kWN;
-
-  const int64_t rows_a = min((int64_t)BM, p.M - m0), rows_b = min((int64_t)BN, p.N - n0);
-  const __amdgpu_buffer_rsrc_t ra =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(p.a + m0 * p.lda), (short)0, (int)((rows_a - 1) * p.lda + p.K),
-                                        0x00020000);
-  const __amdgpu_buffer_rsrc_t rb =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(p.w + n0 * p.ldw), (short)0, (int)((rows_b - 1) * p.ldw + p.K),
-                                        0x00020000);
-  SA sa_;
-  SB sb_;
-  sa_.init(p.lda);
-  sb_.init(p.ldw);
-  const int K = (int)p.K;
-  const int nk = (K + BK - 1) / BK;
-  const int lda_step = (int)(p.lda * SA::kRowsPerLoad), ldw_step = (int)(p.ldw * SB::kRowsPerLoad);
-
-  // zero-length descriptors: a k-tile past the end reads through these and gets zeros
-  const __amdgpu_buffer_rsrc_t ra0 = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, 0, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rb0 = __builtin_amdgcn_make_buffer_rsrc((void*)p.w, (short)0, 0, 0x00020000);
-
-  // register stage of the slabs
-  v4i ga[SA::kLoads], gb[SB::kLoads];
-  // global -> registers, k-tile kt. One vector offset per matrix (the thread's row and chunk); the load's row step
-  // (i * 64 rows) and the tile's k0 are the scalar offset, so no per-load offsets stay live across the loop. In
-  // the GENERAL variant a chunk past K gets the vector offset kOOB - soffset: the sum is kOOB, past the range.
-  auto gload_a = [&](int kt, int i) {
-    const int soff = kt * BK + i * lda_step;
-    int vo = sa_.vo;
-    if (GENERAL && kt * BK + sa_.col >= K) vo = kOOB - soff;
-    ga[i] = __builtin_amdgcn_raw_buffer_load_b128(kt < nk ? ra : ra0, vo, soff, 0);
-  };
-  auto gload_b = [&](int kt, int i) {
-    const int soff = kt * BK + i * ldw_step;
-    int vo = sb_.vo;
-    if (GENERAL && kt * BK + sb_.col >= K) vo = kOOB - soff;
-    gb[i] = __builtin_amdgcn_raw_buffer_load_b128(kt < nk ? rb : rb0, vo, soff, 0);
-  };
-  // registers -> LDS stage buffer
-  auto swrite_a = [&](int buf, int i) {
-    *reinterpret_cast<v4i*>(smem + buf * kStage + sa_.lo + i * SA::kRowsPerLoad * BK) = ga[i];
-  };
-  auto swrite_b = [&](int buf, int i) {
-    *reinterpret_cast<v4i*>(smem + buf * kStage + kSlabA + sb_.lo + i * SB::kRowsPerLoad * BK) = gb[i];
-  };
-  // operand fragments of k-step s (32 of the stage's 128 k) of stage buffer buf
-  auto frags = [&](int buf, int s, v4i (&fa)[TM], v4i (&fb)[TN]) {
-    const int chunk = s * 2 + (lane >> 5);
-    const int8_t* la = smem + buf * kStage;
-    const int8_t* lb = la + kSlabA;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(la + swz(wm * kRowsW + i * 32 + (lane & 31), chunk));
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const v4i*>(lb + swz(wn * kColsW + j * 32 + (lane & 31), chunk));
-  };
-
-  v16i acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-
-  // The MFMAs of one k-step; `fill` issues the o-th of this k-step's kOps memory operations after MFMA
-  // o * kMf / kOps (spreading them so that no wave stalls on a full queue while its MFMA pipe idles).
-  constexpr int kMf = TM * TN;
-  auto mma = [&](const v4i (&fa)[TM], const v4i (&fb)[TN], auto fill, auto OPS) {
-    constexpr int kOps = decltype(OPS)::value;
-#pragma unroll
-    for (int x = 0; x < kMf; ++x) {
-      acc[x / TN][x % TN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[x / TN], fb[x % TN], acc[x / TN][x % TN], 0, 0, 0);
-#pragma unroll
-      for (int o = 0; o < kOps; ++o)
-        if (o * kMf / (kOps > 0 ? kOps : 1) == x) fill(o);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  auto nofill = [](int) {};
-  using Zero = std::integral_constant<int, 0>;
-
-  // Pipeline. LDS buffer kt % 2 holds k-tile kt while it is computed; the register stage holds the next k-tile
-  // from its buffer loads until it is written to LDS. Stage kt:
-  //   k-step 0: read k-step 1's fragments; MFMAs of k-step 0 interleaved with the LDS writes of k-tile kt + 1
-  //             (registers -> LDS buffer (kt+1) % 2, free since the barrier that ended stage kt-1), then the buffer
-  //             loads of k-tile kt + 2 into the freed registers (a whole stage to land)
-  //   k-steps 1, 2: read the next k-step's fragments, MFMAs
-  //   k-step 3: lgkmcnt wait + barrier (k-tile kt+1 is in LDS for every wave, every wave is done reading kt),
-  //             read k-step 0 of k-tile kt+1, MFMAs of k-step 3
-  v4i f0a[TM], f0b[TN], f1a[TM], f1b[TN];
-  constexpr int kOpsA = SA::kLoads, kOpsB = SB::kLoads;
-  constexpr int kOps0 = 2 * (kOpsA + kOpsB);  // LDS writes and buffer loads in k-step 0
-
-#pragma unroll
-  for (int i = 0; i < kOpsA; ++i) gload_a(0, i);
-#pragma unroll
-  for (int i = 0; i < kOpsB; ++i) gload_b(0, i);
-#pragma unroll
-  for (int i = 0; i < kOpsA; ++i) swrite_a(0, i);
-#pragma unroll
-  for (int i = 0; i < kOpsB; ++i) swrite_b(0, i);
-#pragma unroll
-  for (int i = 0; i < kOpsA; ++i) gload_a(1, i);
-#pragma unroll
-  for (int i = 0; i < kOpsB; ++i) gload_b(1, i);
-  barrier_lds();
-  frags(0, 0, f0a, f0b);
-
-  // one stage; CUR = kt % 2 (LDS buffer of k-tile kt), NXT = 1 - CUR
-  auto stage = [&](int CUR, int kt) {
-    const int NXT = 1 - CUR;
-    frags(CUR, 1, f1a, f1b);
-    __builtin_amdgcn_sched_barrier(0);
-    auto fill0 = [&](int o) {
-      if (o < kOpsA) swrite_a(NXT, o);
-      else if (o < kOpsA + kOpsB) swrite_b(NXT, o - kOpsA);
-      else if (o < 2 * kOpsA + kOpsB) gload_a(kt + 2, o - kOpsA - kOpsB);
-      else gload_b(kt + 2, o - 2 * kOpsA - kOpsB);
-    };
-    mma(f0a, f0b, fill0, std::integral_constant<int, kOps0>{});
-    frags(CUR, 2, f0a, f0b);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(f1a, f1b, nofill, Zero{});
-    frags(CUR, 3, f1a, f1b);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(f0a, f0b, nofill, Zero{});
-    barrier_lds();
-    frags(NXT, 0, f0a, f0b);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(f1a, f1b, nofill, Zero{});
-  };
-
-  // (the stage index is a run-time value: unrolling two stages with compile-time buffer indices lengthens the
-  // live ranges enough to spill the staged loads)
-  for (int kt = 0; kt < nk; ++kt) stage(kt & 1, kt);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the loads past the end (zeros) land before LDS is reused
-  __syncthreads();
-
-  // Epilogue, in two passes per band of 32 rows of the wave's kRowsW x kColsW sub-tile.
-  //  1. In the MFMA result layout (lane l holds column l % 32 of each 32x32 tile and rows
-  //     8*(r/4) + 4*(l/32) + r%4), t = (float(acc) * sa[m]) * sw[n] (the raw int32 with ACC_ONLY) goes to a private
-  //     LDS band (32 x kColsW 4-byte words). A lane needs one sw per column tile and 16 sa per band, loaded up
-  //     front.
-  //  2. Row-major: lane l takes the 4 columns 4 (l % kC4) .. +3 of rows l / kC4 + kRowsPass * it, so its bias
-  //     values are fixed for the tile; y = bf16((t + bias) + residual), the same fp32 operation order as the
-  //     unfused product, with one rounding. Rows go in groups of 4 whose residual loads issue together.
-  // The epilogue runs once per tile, so its code is kept small (it is fetched anew for every tile): only the
-  // GENERAL variant carries the scalar paths for unaligned rows and a ragged last column group.
-  constexpr int kCols = kColsW;               // columns of the wave's sub-tile
+// Epilogue of one tile, per wave, in passes of 16 rows of the wave's kRowsW x kCols sub-tile (two per 32-row
+// MFMA band):
+//  1. In the MFMA result layout (lane l holds column l % 32 of each 32x32 tile and rows 8*(r/4) + 4*(l/32) + r%4),
+//     t = (float(acc) * sa[m]) * sw[n] (the raw int32 with ACC_ONLY) goes to a private LDS band (16 x kCols 4-byte
+//     words; the eight bands fill at most one stage buffer). A lane needs one sw per column tile and 16 sa per
+//     32-row band, loaded up front.
+//  2. Row-major: lane l takes the 4 columns 4 (l % kC4) .. +3 of rows l / kC4 + kRowsPass * it, so its bias
+//     values are fixed for the tile; y = bf16((t + bias) + residual), the same fp32 operation order as the
+//     unfused product, with one rounding. Rows go in groups of 4 whose residual loads issue together.
+// Only the GENERAL variant carries the scalar paths for unaligned rows and a ragged last column group.
+template <int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU, int TM, int TN>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, const v16i (&acc)[TM][TN], int8_t* stage_buf, int tm,
+                                         int tn, int wm, int wn, int wave, int lane) {
+  constexpr int kRowsW = BM / kWM;
+  constexpr int kCols = BN / kWN;             // columns of the wave's sub-tile
   constexpr int kC4 = kCols / 4;              // 4-column chunks per row
   constexpr int kRowsPass = 64 / kC4;         // rows one pass of the wave covers
-  constexpr int kPasses = (32 + kRowsPass - 1) / kRowsPass;
+  constexpr int kHalf = 16;                   // rows per band
+  constexpr int kPasses = (kHalf + kRowsPass - 1) / kRowsPass;
   static_assert(kPasses % 4 == 0, "row groups of 4");
-  constexpr int kBand = 32 * kCols * 4;       // bytes of one band
-  static_assert(kWM * kWN * kBand <= 2 * kStage, "epilogue bands do not fit");
-  uint32_t* band = reinterpret_cast<uint32_t*>(smem + wave * kBand);
-  const int64_t n_w = n0 + wn * kCols;
+  constexpr int kBand = kHalf * kCols * 4;    // bytes of one band
+  static_assert(kWM * kWN * kBand <= (BM + BN) * BK, "epilogue bands do not fit in a stage buffer");
+  uint32_t* band = reinterpret_cast<uint32_t*>(stage_buf + wave * kBand);
+  const int64_t m_w = (int64_t)tm * BM + wm * kRowsW;
+  const int64_t n_w = (int64_t)tn * BN + wn * kCols;
   const int col = lane & 31, h = lane >> 5;
   float swv[TN];
 #pragma unroll
@@ -290,36 +128,40 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    __builtin_amdgcn_sched_barrier(0);  // one band at a time (hoisting the next band's loads spills)
-    const int64_t m_band = m0 + wm * kRowsW + i * 32;
+    const int64_t m_band = m_w + i * 32;
     float sav[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       sav[r] = ACC_ONLY ? 0.0f : p.sa[min(m_band + 8 * (r >> 2) + 4 * h + (r & 3), p.M - 1)];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+    for (int q = 0; q < 2; ++q) {
+      __builtin_amdgcn_sched_barrier(0);  // one band at a time (hoisting the next band's loads spills)
+      // rows 16 q .. 16 q + 15 of the 32-row band: r = 8 q .. 8 q + 7
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 8 * (r >> 2) + 4 * h + (r & 3);
-        uint32_t word;
-        if constexpr (ACC_ONLY) {
-          word = (uint32_t)acc[i][j][r];
-        } else {
-          float t = (float)acc[i][j][r] * sav[r];
-          t = t * swv[j];
-          word = __float_as_uint(t);
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int r = 8 * q; r < 8 * q + 8; ++r) {
+          const int row = 8 * ((r >> 2) & 1) + 4 * h + (r & 3);
+          uint32_t word;
+          if constexpr (ACC_ONLY) {
+            word = (uint32_t)acc[i][j][r];
+          } else {
+            float t = (float)acc[i][j][r] * sav[r];
+            t = t * swv[j];
+            word = __float_as_uint(t);
+          }
+          band[row * kCols + j * 32 + col] = word;
         }
-        band[row * kCols + j * 32 + col] = word;
       }
-    }
-    if (lane_on) {
+      if (!lane_on) continue;
+      const int64_t m_half = m_band + 16 * q;
 #pragma unroll 1
       for (int it0 = 0; it0 < kPasses; it0 += 4) {
         uint2 res[4];
         if (!ACC_ONLY && p.residual) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const uint16_t* rp = p.residual + min(m_band + kRowsPass * (it0 + u) + rr, p.M - 1) * p.ldr;
+            const uint16_t* rp = p.residual + min(m_half + kRowsPass * (it0 + u) + rr, p.M - 1) * p.ldr;
             if constexpr (GENERAL) {
               uint32_t e4[4];
 #pragma unroll
@@ -333,8 +175,8 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int row = kRowsPass * (it0 + u) + rr;
-          const int64_t m = m_band + row;
-          if (row >= 32 || m >= p.M) continue;
+          const int64_t m = m_half + row;
+          if (row >= kHalf || m >= p.M) continue;
           const uint4 v = *reinterpret_cast<const uint4*>(band + row * kCols + 4 * c4);
           if constexpr (ACC_ONLY) {
             int32_t* dst = p.acc + m * p.ldacc + n;
@@ -381,9 +223,192 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   }
 }
 
+// One LDS-DMA load (buffer_load_dwordx4 ... lds): lane l copies the 16 bytes at byte vo + soff of buffer r to LDS
+// byte lds_base + 16 l (lds_base is wave-uniform, passed in M0); bytes past the buffer's range arrive as zeros.
+// Inline asm, so that the compiler does not track it: the kernel waits for it (vmcnt) and orders it with barriers
+// itself, where the compiler would wait for it before every LDS read it cannot prove disjoint from the copy (every
+// read of the other stage buffer). M0 is declared clobbered.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int vo, int soff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(vo), "s"(r), "s"(soff),
+               "s"(lds_base)
+               : "memory", "m0");
+}
+
+// buffer descriptors of one tile's A panel (BM rows) and W panel (BN rows); a zero range reads zeros
+struct Panels {
+  __amdgpu_buffer_rsrc_t a, w;
+};
+
+template <int BN>
+__device__ __forceinline__ Panels panels_of(const GemmArgs& p, int v, int ntiles) {
+  if (v >= ntiles) {
+    return {__builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, 0, 0x00020000),
+            __builtin_amdgcn_make_buffer_rsrc((void*)p.w, (short)0, 0, 0x00020000)};
+  }
+  int tm, tn;
+  tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t rows_a = min((int64_t)BM, p.M - m0), rows_w = min((int64_t)BN, p.N - n0);
+  return {__builtin_amdgcn_make_buffer_rsrc((void*)(p.a + m0 * p.lda), (short)0,
+                                            (int)((rows_a - 1) * p.lda + p.K), 0x00020000),
+          __builtin_amdgcn_make_buffer_rsrc((void*)(p.w + n0 * p.ldw), (short)0,
+                                            (int)((rows_w - 1) * p.ldw + p.K), 0x00020000)};
+}
+
+template <int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU>
+__global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
+  constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile: 64 x BN/2
+  constexpr int TM = kRowsW / 32;    // 2
+  constexpr int TN = kColsW / 32;    // 4 or 3
+  constexpr int kSlabA = BM * BK, kSlabB = BN * BK, kStage = kSlabA + kSlabB;
+  constexpr int kOpsA = BM / 64, kOpsB = BN / 64;  // DMA loads per wave per stage (8 waves x 8 rows each)
+  __shared__ __attribute__((aligned(16))) int8_t smem[2 * kStage];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / kWN, wn = wave % kWN;
+  const int K = (int)p.K;
+  const int nk = (K + BK - 1) / BK;
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int lda_step = (int)(p.lda * 64), ldw_step = (int)(p.ldw * 64);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)(smem);
+
+  // DMA load o of a stage: wave w moves slab rows 8 (w + 8 o') .. +7 (o' = o, or o - kOpsA for the W slab); lane
+  // l takes row l / 8 of those and physical chunk l % 8 of the row, which holds logical chunk (l % 8) ^ ((row >> 1)
+  // & 7): the LDS row is then already in the swizzled layout frags() reads. (row >> 1) & 7 depends only on the
+  // wave's parity and l / 16, so each lane's vector offset is the same for every load; the load's rows and the
+  // k-tile go in the scalar offset. In the GENERAL variant a chunk past K gets the vector offset kOOB - soffset:
+  // the sum is kOOB, past the range (zeros).
+  const int dc = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
+  const int dvo_a = (int)((8 * wave + (lane >> 3)) * p.lda) + dc * 16;
+  const int dvo_w = (int)((8 * wave + (lane >> 3)) * p.ldw) + dc * 16;
+  auto dma = [&](int buf, const Panels& pn, int kt, int o) {
+    if (o < kOpsA) {
+      const int soff = kt * BK + o * lda_step;
+      int vo = dvo_a;
+      if (GENERAL && kt * BK + dc * 16 >= K) vo = kOOB - soff;
+      dma16(pn.a, vo, soff, lds0 + buf * kStage + wave * 1024 + o * 8192);
+    } else {
+      const int soff = kt * BK + (o - kOpsA) * ldw_step;
+      int vo = dvo_w;
+      if (GENERAL && kt * BK + dc * 16 >= K) vo = kOOB - soff;
+      dma16(pn.w, vo, soff, lds0 + buf * kStage + kSlabA + wave * 1024 + (o - kOpsA) * 8192);
+    }
+  };
+  // operand fragments of k-step s (32 of the stage's 128 k) of stage buffer buf
+  auto frags = [&](int buf, int s, v4i (&fa)[TM], v4i (&fb)[TN]) {
+    const int chunk = s * 2 + (lane >> 5);
+    const int8_t* la = smem + buf * kStage;
+    const int8_t* lb = la + kSlabA;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(la + swz(wm * kRowsW + i * 32 + (lane & 31), chunk));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const v4i*>(lb + swz(wn * kColsW + j * 32 + (lane & 31), chunk));
+  };
+
+  v16i acc[TM][TN];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  };
+
+  // The MFMAs of one k-step; `fill` issues the o-th of this k-step's kOps memory operations after MFMA
+  // o * kMf / kOps (spreading them so that no wave stalls on a full queue while its MFMA pipe idles).
+  constexpr int kMf = TM * TN;
+  auto mma = [&](const v4i (&fa)[TM], const v4i (&fb)[TN], auto fill, auto OPS) {
+    constexpr int kOps = decltype(OPS)::value;
+#pragma unroll
+    for (int x = 0; x < kMf; ++x) {
+      acc[x / TN][x % TN] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[x / TN], fb[x % TN], acc[x / TN][x % TN], 0, 0, 0);
+#pragma unroll
+      for (int o = 0; o < kOps; ++o)
+        if (o * kMf / (kOps > 0 ? kOps : 1) == x) fill(o);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto nofill = [](int) {};
+  using Zero = std::integral_constant<int, 0>;
+
+  // Pipeline over the sequence of (tile, k-tile) stages of this workgroup: tiles v = blockIdx.x + i * gridDim.x
+  // (gridDim.x is a multiple of 8 or covers every tile, so all of a workgroup's tiles come from its XCD's range).
+  // LDS buffer CUR holds the stage being computed; stage s:
+  //   k-step 0: read k-step 1's fragments; MFMAs of k-step 0 interleaved with the DMA loads of the next stage of
+  //             the sequence (k-tile kt + 1 of this tile, or k-tile 0 of the next tile) into buffer NXT, free since
+  //             the barrier that ended the previous stage
+  //   k-steps 1, 2: read the next k-step's fragments, MFMAs
+  //   k-step 3: vmcnt + lgkmcnt wait and barrier (the next stage is in LDS for every wave, every wave is done
+  //             reading CUR), read k-step 0 of the next stage, MFMAs of k-step 3
+  // After a tile's last stage its accumulators go out through the epilogue, which stages them in buffer CUR of
+  // that stage (read by no one any more) while NXT already holds the next tile's first stage; the epilogue's
+  // global stores drain while the next tile computes.
+  v4i f0a[TM], f0b[TN], f1a[TM], f1b[TN];
+  constexpr int kOps0 = kOpsA + kOpsB;
+  int v = blockIdx.x;
+  Panels cur = panels_of<BN>(p, v, ntiles);
+#pragma unroll
+  for (int o = 0; o < kOps0; ++o) dma(0, cur, 0, o);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  frags(0, 0, f0a, f0b);
+  zero_acc();
+
+  auto stage = [&](int CUR, const Panels& src, int kt_src) {
+    const int NXT = 1 - CUR;
+    frags(CUR, 1, f1a, f1b);
+    __builtin_amdgcn_sched_barrier(0);
+    auto fill0 = [&](int o) { dma(NXT, src, kt_src, o); };
+    mma(f0a, f0b, fill0, std::integral_constant<int, kOps0>{});
+    frags(CUR, 2, f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(f1a, f1b, nofill, Zero{});
+    frags(CUR, 3, f1a, f1b);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(f0a, f0b, nofill, Zero{});
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    frags(NXT, 0, f0a, f0b);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(f1a, f1b, nofill, Zero{});
+  };
+
+  int buf = 0;
+  // (the stage buffer is a run-time value: unrolling two stages with compile-time buffer indices lengthens the
+  // live ranges)
+  for (; v < ntiles; v += gridDim.x) {
+    const Panels nxt = panels_of<BN>(p, v + (int)gridDim.x, ntiles);
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      stage(buf, cur, kt + 1);
+      buf ^= 1;
+    }
+    stage(buf, nxt, 0);
+    buf ^= 1;
+    int tm, tn;
+    tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
+    epilogue<BN, ACC_ONLY, GENERAL, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, tm, tn, wm, wn, wave, lane);
+    // every wave is done with its band (in the buffer the next stage's DMA loads overwrite) before that stage
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    zero_acc();
+    cur = nxt;
+  }
+}
+
 }  // namespace
 
 namespace {
+
+// compute units of the current device, rounded down to a multiple of 8 (whole XCDs), cached per device
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+    n -= n % 8;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st) {
   GemmArgs p = p0;
@@ -397,7 +422,10 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st) {
   if (tiles_m * tiles_n > 0x7fffffff) return OD_ERR_SHAPE;
   p.tiles_m = (int)tiles_m;
   p.tiles_n = (int)tiles_n;
-  dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
+  // persistent workgroups: one per CU (the kernel's LDS admits one), each looping over tiles bid + i * grid
+  const int64_t ntiles = tiles_m * tiles_n;
+  const int64_t cus = cu_count();
+  dim3 grid((unsigned)(ntiles <= cus ? ntiles : cus)), block(kThreads);
   // The fast variant needs whole k-tiles and 4-column output groups that are 8-byte (bf16) / 16-byte (int32)
   // aligned (with SwiGLU, 2-column output groups 4-byte aligned); anything else takes the GENERAL variant.
   auto al = [](const void* q, unsigned a) { return (((uintptr_t)q) & (a - 1)) == 0; };
