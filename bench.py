@@ -34,6 +34,39 @@ INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 / fp16 MFMA
 HBM_PEAK_GBS = 8000.0
 
+PROBE_MODES = {0: ("int8", "constant operands"), 1: ("int8", "operands changing every round"),
+               2: ("int8", "operands read from LDS (6 fragment reads per 8 MFMAs)"),
+               3: ("bf16", "operands changing every round"), 4: ("bf16", "operands read from LDS")}
+
+
+def mfma_ceiling(modes=(0, 1, 2, 3, 4), iters=100000):
+    """Matrix-core throughput the chip sustains (od_probe_mfma in libod_probe.so): per mode, dense TOPS (int8) or
+    TFLOP/s (bf16) and the mean core clock in MHz under that load (s_memtime over s_memrealtime)."""
+    import ctypes
+
+    from opendecider_amd import build as _b
+    L = ctypes.CDLL(_b.PROBE_LIB)
+    L.od_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                ctypes.POINTER(ctypes.c_double)]
+    L.od_probe_mfma.restype = ctypes.c_int
+    out = {}
+    for m in modes:
+        tops, mhz = ctypes.c_double(), ctypes.c_double()
+        rc = L.od_probe_mfma(m, iters, ctypes.byref(tops), ctypes.byref(mhz))
+        if rc != 0:
+            raise RuntimeError(f"od_probe_mfma({m}) failed: {rc}")
+        dt, what = PROBE_MODES[m]
+        peak = INT8_PEAK_TOPS if dt == "int8" else BF16_PEAK_TFLOPS
+        out[f"mode{m}"] = {"dtype": dt, "operands": what, "value": tops.value, "frac_of_peak": tops.value / peak,
+                           "clock_mhz": mhz.value}
+    return out
+
+
+def _sustained(ceil, mode):
+    c = ceil[f"mode{mode}"]
+    return {"value": c["value"], "clock_mhz": c["clock_mhz"], "frac_of_peak": c["frac_of_peak"],
+            "probe": f"od_probe_mfma mode {mode}: {c['dtype']} MFMAs, {c['operands']}, 8 waves per CU"}
+
 
 def parse():
     ap = argparse.ArgumentParser()
@@ -46,7 +79,7 @@ def parse():
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--state", type=int, default=2048)
     ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm", "gemm_traffic",
-                                           "attention", "lm_logprob", "qcache_rows"],
+                                           "attention", "lm_logprob", "qcache_rows", "mfma_ceiling"],
                     default="scoring",
                     help="scoring (default): the metric's option-row scoring pass over cached 2048-token states; "
                          "decision: full decision forward from token ids (4 requests, 4096-token states prefilled, "
@@ -59,7 +92,9 @@ def parse():
                          "log-prob of 1024 rows over a 151936 x 4096 int8 table; gemm: the W8A8 linear alone over "
                          "the reference's (K, N) x M sweep (scripts/bench_gemm.py) and the 9B layer shapes at M = 4096; "
                          "qcache_rows: decide latency with and without the question cache over the reference's "
-                         "(questions, options) shapes (scripts/bench_qcache_rows.py)")
+                         "(questions, options) shapes (scripts/bench_qcache_rows.py); mfma_ceiling: what the "
+                         "matrix cores sustain (int8 and bf16 MFMAs on constant, changing and LDS-fed operands, one "
+                         "8-wave workgroup per CU) with the core clock under that load")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--scoring-only", action="store_true",
                     help="the default line without its decision / wide_choice sub-objects")
@@ -546,6 +581,9 @@ def run_gemm(args):
                         "frac": ops9 / us9 / 1e6 / INT8_PEAK_TOPS, "traffic": None,
                         "note": "the four 9B layer GEMMs at M = 4096 together"},
            "shapes": rows}
+    ceil = mfma_ceiling(modes=(1, 2))
+    res["roofline"]["sustained"] = _sustained(ceil, 2)
+    res["roofline"]["frac_of_sustained"] = res["roofline"]["achieved"] / ceil["mode2"]["value"]
     if not args.no_cpu_baseline:
         import torch as _t
         from oracle import quant as oq
@@ -573,6 +611,22 @@ def run_gemm(args):
                                           f"path {ref * 1e3:.1f} ms; the W8A8 oracle "
                                           f"{tims['W8A8 port (act-quant, int32 GEMM, epilogue)'] * 1e3:.1f} ms")}
     return res
+
+
+def run_mfma_ceiling(args):
+    """What the matrix cores sustain on this chip: od_probe_mfma's five modes (int8 on constant / changing /
+    LDS-fed operands, bf16 on changing / LDS-fed operands), one 8-wave workgroup per CU, 100000 rounds of 8 MFMAs
+    per wave, with the core clock under that load. `value` is the int8 LDS-fed rate, the ceiling the W8A8 GEMM's
+    inner loop has without any global traffic."""
+    ceil = mfma_ceiling()
+    return {"metric": "int8 MFMA sustained TOPS (LDS-fed operands)", "value": ceil["mode2"]["value"], "unit": "TOPS",
+            "n_gpus": 1, "steps": 1, "warmup": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8", "data": "synthetic",
+            "config": {"workload": "matrix-core ceiling probe: one 8-wave workgroup per CU, 100000 rounds of 8 "
+                                   "independent 32x32 MFMAs per wave"},
+            "roofline": {"bound": "mfma", "achieved": ceil["mode2"]["value"], "peak": INT8_PEAK_TOPS,
+                         "unit": "TFLOP/s", "frac": ceil["mode2"]["frac_of_peak"], "traffic": None},
+            "modes": ceil}
 
 
 def run_qcache_rows(args):
@@ -811,7 +865,8 @@ def main():
         torch.cuda.set_device(0)
         fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm": run_gemm,
               "gemm_traffic": run_gemm_traffic, "attention": run_attention,
-              "lm_logprob": run_lm_logprob, "qcache_rows": run_qcache_rows}[args.workload]
+              "lm_logprob": run_lm_logprob, "qcache_rows": run_qcache_rows,
+              "mfma_ceiling": run_mfma_ceiling}[args.workload]
         print(json.dumps(fn(args)))
         return
 
@@ -893,6 +948,11 @@ def main():
         "time_share": {"gemm": ms_g * gemm_t.every / (ms_per_step * args.steps),
                        "attention": ms_a * attn_t.timers[0].every / (ms_per_step * args.steps)},
     }
+    ceil = mfma_ceiling(modes=(2, 4))
+    res["roofline"]["sustained"] = _sustained(ceil, 2)
+    res["roofline"]["frac_of_sustained"] = gemm_tops / ceil["mode2"]["value"]
+    res["attention"]["sustained_bf16"] = _sustained(ceil, 4)
+    res["attention"]["frac_of_sustained_bf16"] = attn_tflops / ceil["mode4"]["value"]
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args)
     if not args.scoring_only:

@@ -23,6 +23,9 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libod_mi355x.so")
 SOURCES = ["od_quant.hip", "od_gemm.hip", "od_attn.hip", "od_wide.hip", "od_layer.hip", "od_lmhead.hip"]
+# the matrix-core ceiling probe bench.py reports beside the rooflines, in a library of its own
+PROBE_SOURCE = "od_probe.hip"
+PROBE_LIB = os.path.join(PKG, "libod_probe.so")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-inline-asm"]
@@ -38,15 +41,19 @@ def _run(cmd):
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every kernel source for gfx950 and link libod_mi355x.so. Returns the library path."""
+    """Compile every kernel source for gfx950 and link libod_mi355x.so (and libod_probe.so). Returns the path of
+    libod_mi355x.so."""
     os.makedirs(BUILD, exist_ok=True)
     objs = [os.path.join(BUILD, s.replace(".hip", ".o")) for s in SOURCES]
     cmds = [[HIPCC, *FLAGS, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    probe_obj = os.path.join(BUILD, PROBE_SOURCE.replace(".hip", ".o"))
+    cmds.append([HIPCC, *FLAGS, "-c", os.path.join(CSRC, PROBE_SOURCE), "-o", probe_obj])
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         outs = list(ex.map(_run, cmds))
-    tmp = LIB + ".tmp"
-    outs.append(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]))
-    os.replace(tmp, LIB)
+    for lib, lib_objs in ((LIB, objs), (PROBE_LIB, [probe_obj])):
+        tmp = lib + ".tmp"
+        outs.append(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *lib_objs, "-o", tmp]))
+        os.replace(tmp, lib)
     if verbose:
         for o in outs:
             if o.strip():
