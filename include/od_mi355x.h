@@ -99,6 +99,21 @@ int od_w8a8_gemm_swiglu(const int8_t* a, int64_t lda, const float* sa, const int
                         uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, od_stream_t stream);
 
 /*
+ * od_w8a8_gemm_ws — od_w8a8_gemm's out (swiglu = 0) or od_w8a8_gemm_swiglu's (swiglu = 1: bias and residual NULL,
+ * out bf16 [M, N/2]) with a caller workspace for split-K. Replaces the same reference calls as those two; the
+ * workspace has no reference counterpart (GemLite picks its own split-K, quant.py:302-314).
+ * Shapes with too few 256-row tiles to fill the chip (small M: the row and question passes) split K over several
+ * workgroups per tile, each writing exact int32 partial sums to its plane of ws; a second pass adds the planes and
+ * applies the same epilogue, so out is bit-identical to the unsplit call. ws: int32, 16-byte aligned, ws_ints
+ * elements; od_w8a8_gemm_ws_size gives the size the current device's plan uses for (M, N, K) (0: no split). With
+ * ws NULL or smaller than that, the call runs unsplit. Other requirements as od_w8a8_gemm.
+ */
+int od_w8a8_gemm_ws_size(int64_t M, int64_t N, int64_t K, int64_t* ws_ints);
+int od_w8a8_gemm_ws(const int8_t* a, int64_t lda, const float* sa, const int8_t* w, int64_t ldw, const float* sw,
+                    const uint16_t* bias, const uint16_t* residual, int64_t ldr, uint16_t* out, int64_t ldo, int64_t M,
+                    int64_t N, int64_t K, int swiglu, int32_t* ws, int64_t ws_ints, od_stream_t stream);
+
+/*
  * od_kv_quant_append — quantize new K or V rows (one scale per token per head) and append them to an int8 cache.
  * Replaces: maybe_quantize / Int8Tensor.quantize on cache tensors (quant.py:36-41,105-109) as called by
  * PackedCache.pack (src/opendecider/backbone.py:446) and by PrefixCache._take, which quantizes only the new

@@ -54,6 +54,9 @@ SIGNATURES = {
     "od_qk_norm_rope": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr,
                         ctypes.c_float, _c_ptr],
     "od_w8a8_gemm_swiglu": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _c_ptr],
+    "od_w8a8_gemm_ws_size": [_i64, _i64, _i64, _c_ptr],
+    "od_w8a8_gemm_ws": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64,
+                        _i64, ctypes.c_int, _c_ptr, _i64, _c_ptr],
     "od_kv_copy_rows": [_c_ptr, _c_ptr, _i64, _i64, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr,
                         _i64, _c_ptr],
     "od_qk_norm_rope_kv_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64,

@@ -60,6 +60,8 @@ struct GemmArgs {
   int64_t lda, ldw, ldr, ldo, ldacc;
   int64_t M, N, K;
   int tiles_m, tiles_n;
+  int kt_per;            // k-tiles per split (blockIdx.y = split); nk without split-K
+  int64_t split_stride;  // int32 elements between the partial-sum planes of two splits (ACC_ONLY)
 };
 
 __device__ __forceinline__ float bfr(float v) { return od_bf16_to_f32(od_f32_to_bf16(v)); }
@@ -270,6 +272,10 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   const int K = (int)p.K;
   const int nk = (K + BK - 1) / BK;
   const int ntiles = p.tiles_m * p.tiles_n;
+  // split-K: this workgroup sums k-tiles kb .. ke-1 (all of them without split) and, with ACC_ONLY, writes its
+  // partial sums to plane blockIdx.y of p.acc
+  const int kb = blockIdx.y * p.kt_per, ke = min(nk, kb + p.kt_per);
+  if constexpr (ACC_ONLY) p.acc += blockIdx.y * p.split_stride;
   const int lda_step = (int)(p.lda * 64), ldw_step = (int)(p.ldw * 64);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)(smem);
 
@@ -348,7 +354,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   int v = blockIdx.x;
   Panels cur = panels_of<BN>(p, v, ntiles);
 #pragma unroll
-  for (int o = 0; o < kOps0; ++o) dma(0, cur, 0, o);
+  for (int o = 0; o < kOps0; ++o) dma(0, cur, kb, o);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   frags(0, 0, f0a, f0b);
   zero_acc();
@@ -376,11 +382,11 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   // live ranges)
   for (; v < ntiles; v += gridDim.x) {
     const Panels nxt = panels_of<BN>(p, v + (int)gridDim.x, ntiles);
-    for (int kt = 0; kt + 1 < nk; ++kt) {
+    for (int kt = kb; kt + 1 < ke; ++kt) {
       stage(buf, cur, kt + 1);
       buf ^= 1;
     }
-    stage(buf, nxt, 0);
+    stage(buf, nxt, kb);
     buf ^= 1;
     int tm, tn;
     tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
@@ -410,18 +416,111 @@ int cu_count() {
   return n;
 }
 
-int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st) {
-  GemmArgs p = p0;
-  const int64_t M = p.M, N = p.N, K = p.K;
+struct Tiling {
+  bool use192;
+  int64_t tiles_m, tiles_n;
+};
+
+Tiling tiling_of(int64_t M, int64_t N) {
   const int64_t tiles_m = (M + BM - 1) / BM;
   // BN: 256, or 192 when that takes fewer tile-widths of work at 256 workgroups per wave (e.g. N = 6144).
   const int64_t t256 = tiles_m * ((N + 255) / 256), t192 = tiles_m * ((N + 191) / 192);
   const int64_t cost256 = ((t256 + 255) / 256) * 256, cost192 = ((t192 + 255) / 256) * 192;
   const bool use192 = cost192 < cost256;
-  const int64_t tiles_n = use192 ? (N + 191) / 192 : (N + 255) / 256;
+  return {use192, tiles_m, use192 ? (N + 191) / 192 : (N + 255) / 256};
+}
+
+// Split-K for shapes with too few tiles to fill the chip (small M): `splits` workgroups per tile each sum
+// kt_per k-tiles into their own int32 plane of a workspace [splits][M][ldws], and splitk_finalize_kernel adds the
+// planes (integer sums: exact) and applies the same epilogue. Chosen when a simple cost model (about 1 us per
+// k-tile stage of a 256 x 192 tile, the partial planes written and read once at ~3 TB/s, ~2.5 us for the extra
+// launch) predicts at least 15% less time than one pass.
+struct SplitPlan {
+  int splits, kt_per;
+  int64_t ldws, ws_ints;
+};
+
+SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
+  const int nk = (int)((K + BK - 1) / BK);
+  const SplitPlan none{1, nk, 0, 0};
+  const Tiling t = tiling_of(M, N);
+  const int64_t ntiles = t.tiles_m * t.tiles_n, cus = cu_count();
+  if (ntiles * 2 > cus || nk < 4) return none;
+  const double t_stage = (t.use192 ? 192.0 : 256.0) / 192.0;  // us per stage
+  const double base = nk * t_stage;
+  double best = 0.85 * base;
+  SplitPlan bp = none;
+  for (int s = 2; s <= 16 && ntiles * s <= cus; ++s) {
+    const int per = (nk + s - 1) / s;
+    const int used = (nk + per - 1) / per;  // splits that get k-tiles
+    if (used != s) continue;
+    const double est = per * t_stage + 2.0 * s * (double)M * (double)N * 4.0 / 3.0e6 + 2.5;
+    if (est < best) {
+      best = est;
+      const int64_t ldws = (N + 3) / 4 * 4;
+      bp = {s, per, ldws, (int64_t)s * M * ldws};
+    }
+  }
+  return bp;
+}
+
+// out from the split-K partial planes: one thread per 4 columns of a row; the sum of the planes is the exact int32
+// accumulator, then the epilogue's fp32 operations in its order (SwiGLU pairs columns as the GEMM's epilogue does).
+template <bool SWIGLU>
+__global__ __launch_bounds__(256) void splitk_finalize_kernel(GemmArgs p, const int32_t* ws, int splits,
+                                                              int64_t stride) {
+  const int64_t n4 = (p.N + 3) / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= p.M * n4) return;
+  const int64_t m = idx / n4, n = (idx - m * n4) * 4;
+  const int32_t* src = ws + m * p.ldacc + n;
+  int32_t a4[4] = {0, 0, 0, 0};
+  if (n + 4 <= p.N) {
+    for (int sp = 0; sp < splits; ++sp) {
+      const int4 v = *reinterpret_cast<const int4*>(src + sp * stride);
+      a4[0] += v.x;
+      a4[1] += v.y;
+      a4[2] += v.z;
+      a4[3] += v.w;
+    }
+  } else {
+    for (int sp = 0; sp < splits; ++sp)
+      for (int e = 0; n + e < p.N; ++e) a4[e] += src[sp * stride + e];
+  }
+  const float sam = p.sa[m];
+  float t[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x = (float)a4[e] * sam;
+    t[e] = x * p.sw[min(n + e, p.N - 1)];
+  }
+  if constexpr (SWIGLU) {
+    // columns n .. n+3 are (gate f, up f, gate f+1, up f+1) with f = n / 2 (N even)
+    uint16_t* dst = p.out + m * p.ldo + n / 2;
+    dst[0] = (uint16_t)od_f32_to_bf16(od_silu_bf16(bfr(t[0])) * bfr(t[1]));
+    if (n + 2 < p.N) dst[1] = (uint16_t)od_f32_to_bf16(od_silu_bf16(bfr(t[2])) * bfr(t[3]));
+  } else {
+    for (int e = 0; e < 4 && n + e < p.N; ++e) {
+      float y = t[e];
+      if (p.bias) y = y + od_bf16_to_f32(p.bias[n + e]);
+      if (p.residual) y = y + od_bf16_to_f32(p.residual[m * p.ldr + n + e]);
+      p.out[m * p.ldo + n + e] = (uint16_t)od_f32_to_bf16(y);
+    }
+  }
+}
+
+int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan* sp = nullptr,
+                int32_t* ws = nullptr) {
+  GemmArgs p = p0;
+  const int64_t M = p.M, N = p.N, K = p.K;
+  const Tiling t = tiling_of(M, N);
+  const bool use192 = t.use192;
+  const int64_t tiles_m = t.tiles_m, tiles_n = t.tiles_n;
   if (tiles_m * tiles_n > 0x7fffffff) return OD_ERR_SHAPE;
   p.tiles_m = (int)tiles_m;
   p.tiles_n = (int)tiles_n;
+  p.kt_per = (int)((K + BK - 1) / BK);
+  p.split_stride = 0;
   // persistent workgroups: one per CU (the kernel's LDS admits one), each looping over tiles bid + i * grid
   const int64_t ntiles = tiles_m * tiles_n;
   const int64_t cus = cu_count();
@@ -430,10 +529,6 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st) {
   // aligned (with SwiGLU, 2-column output groups 4-byte aligned); anything else takes the GENERAL variant.
   auto al = [](const void* q, unsigned a) { return (((uintptr_t)q) & (a - 1)) == 0; };
   const bool fast_k = K % BK == 0 && N % 4 == 0;
-  const bool fast_out = fast_k && (swiglu ? (p.ldo % 2 == 0 && al(p.out, 4))
-                                          : (p.ldo % 4 == 0 && al(p.out, 8) && al(p.bias, 8) && p.ldr % 4 == 0 &&
-                                             al(p.residual, 8)));
-  const bool fast_acc = fast_k && p.ldacc % 4 == 0 && al(p.acc, 16);
   auto launch = [&](auto BNc, auto ACCc, auto GENc, auto SWc) {
     w8a8_gemm_kernel<decltype(BNc)::value, decltype(ACCc)::value, decltype(GENc)::value, decltype(SWc)::value>
         <<<grid, block, 0, st>>>(p);
@@ -447,6 +542,32 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st) {
               : launch(std::integral_constant<int, 256>{}, ACCc, std::false_type{}, SWc);
     }
   };
+  if (sp && sp->splits > 1) {
+    // partial planes into the workspace, then the finalize pass writes out
+    GemmArgs q = p;
+    p.out = nullptr;
+    p.acc = ws;
+    p.ldacc = sp->ldws;
+    p.kt_per = sp->kt_per;
+    p.split_stride = M * sp->ldws;
+    grid.y = (unsigned)sp->splits;
+    launch2(std::true_type{}, std::false_type{}, !(fast_k && al(ws, 16)));
+    const int rc = od_launch_status();
+    if (rc != OD_OK) return rc;
+    q.ldacc = sp->ldws;
+    const int64_t threads = M * ((N + 3) / 4);
+    const dim3 fgrid((unsigned)((threads + 255) / 256));
+    if (swiglu) {
+      splitk_finalize_kernel<true><<<fgrid, 256, 0, st>>>(q, ws, sp->splits, M * sp->ldws);
+    } else {
+      splitk_finalize_kernel<false><<<fgrid, 256, 0, st>>>(q, ws, sp->splits, M * sp->ldws);
+    }
+    return od_launch_status();
+  }
+  const bool fast_out = fast_k && (swiglu ? (p.ldo % 2 == 0 && al(p.out, 4))
+                                          : (p.ldo % 4 == 0 && al(p.out, 8) && al(p.bias, 8) && p.ldr % 4 == 0 &&
+                                             al(p.residual, 8)));
+  const bool fast_acc = fast_k && p.ldacc % 4 == 0 && al(p.acc, 16);
   if (p.acc) {
     launch2(std::true_type{}, std::false_type{}, !fast_acc);
     const int rc = od_launch_status();
@@ -483,7 +604,7 @@ extern "C" int od_w8a8_gemm(const int8_t* a, int64_t lda, const float* sa, const
   if (lda < K || ldw < K || (out && ldo < N) || (acc && ldacc < N) || (residual && ldr < N)) return OD_ERR_SHAPE;
   const int rc = gemm_check(a, lda, w, ldw, K);
   if (rc != OD_OK) return rc;
-  GemmArgs p{a, sa, w, sw, bias, residual, out, acc, lda, ldw, ldr, ldo, ldacc, M, N, K, 0, 0};
+  GemmArgs p{a, sa, w, sw, bias, residual, out, acc, lda, ldw, ldr, ldo, ldacc, M, N, K, 0, 0, 0, 0};
   return gemm_launch(p, false, (hipStream_t)stream);
 }
 
@@ -496,6 +617,30 @@ extern "C" int od_w8a8_gemm_swiglu(const int8_t* a, int64_t lda, const float* sa
   if (lda < K || ldw < K || ldo < N / 2) return OD_ERR_SHAPE;
   const int rc = gemm_check(a, lda, w, ldw, K);
   if (rc != OD_OK) return rc;
-  GemmArgs p{a, sa, w, sw, nullptr, nullptr, out, nullptr, lda, ldw, 0, ldo, 0, M, N, K, 0, 0};
+  GemmArgs p{a, sa, w, sw, nullptr, nullptr, out, nullptr, lda, ldw, 0, ldo, 0, M, N, K, 0, 0, 0, 0};
   return gemm_launch(p, true, (hipStream_t)stream);
+}
+
+extern "C" int od_w8a8_gemm_ws_size(int64_t M, int64_t N, int64_t K, int64_t* ws_ints) {
+  if (!ws_ints) return OD_ERR_NULL;
+  if (M < 0 || N < 0 || K < 1) return OD_ERR_SHAPE;
+  *ws_ints = (M == 0 || N == 0) ? 0 : split_plan(M, N, K).ws_ints;
+  return OD_OK;
+}
+
+extern "C" int od_w8a8_gemm_ws(const int8_t* a, int64_t lda, const float* sa, const int8_t* w, int64_t ldw,
+                               const float* sw, const uint16_t* bias, const uint16_t* residual, int64_t ldr,
+                               uint16_t* out, int64_t ldo, int64_t M, int64_t N, int64_t K, int swiglu, int32_t* ws,
+                               int64_t ws_ints, od_stream_t stream) {
+  if (M < 0 || N < 0 || K < 1 || ws_ints < 0 || (swiglu && N % 2)) return OD_ERR_SHAPE;
+  if (M == 0 || N == 0) return OD_OK;
+  if (!a || !w || !out || !sa || !sw) return OD_ERR_NULL;
+  if (swiglu && (bias || residual)) return OD_ERR_UNSUPPORTED;
+  if (lda < K || ldw < K || ldo < (swiglu ? N / 2 : N) || (residual && ldr < N)) return OD_ERR_SHAPE;
+  const int rc = gemm_check(a, lda, w, ldw, K);
+  if (rc != OD_OK) return rc;
+  GemmArgs p{a, sa, w, sw, bias, residual, out, nullptr, lda, ldw, ldr, ldo, 0, M, N, K, 0, 0, 0, 0};
+  const SplitPlan sp = split_plan(M, N, K);
+  const bool split = sp.splits > 1 && ws && ws_ints >= sp.ws_ints && od_aligned16(ws);
+  return gemm_launch(p, swiglu != 0, (hipStream_t)stream, split ? &sp : nullptr, split ? ws : nullptr);
 }

@@ -178,6 +178,24 @@ def qk_norm_rope_kv_append(qkv: torch.Tensor, B: int, S: int, n_heads_q: int, n_
             c.touch()
 
 
+_SPLITK_WS: dict = {}
+
+
+def splitk_workspace(M: int, N: int, Kp: int, device) -> torch.Tensor | None:
+    """The int32 workspace od_w8a8_gemm_ws splits K with for this shape on `device` (None when its plan does not
+    split: enough 256-row tiles to fill the chip). The plan depends only on the shape and the device's CU count, so
+    the size is cached."""
+    device = torch.device(device)
+    key = (device.index, M, N, Kp)
+    n = _SPLITK_WS.get(key)
+    if n is None:
+        v = ctypes.c_int64(0)
+        with torch.cuda.device(device):
+            check(lib().od_w8a8_gemm_ws_size(M, N, Kp, ctypes.byref(v)), "od_w8a8_gemm_ws_size")
+        n = _SPLITK_WS[key] = v.value
+    return torch.empty(n, dtype=torch.int32, device=device) if n else None
+
+
 def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, bias=None, residual=None,
               out: torch.Tensor | None = None, want_out: bool = True, want_acc: bool = False):
     """int8 a (M, Kp) x int8 w (N, Kp)^T -> bf16 (M, N) = bf16(float(acc) sa[m] sw[n] + bias + residual); Kp is
@@ -201,6 +219,13 @@ def w8a8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tens
         _lib.bf16_bits(bias)
         bias = bias.contiguous()
     o = out if want_out else None
+    ws = splitk_workspace(M, N, Kp, a.device) if want_out and not want_acc else None
+    if ws is not None:
+        # small M: split-K through the workspace (bit-identical to the one-pass GEMM)
+        check(lib().od_w8a8_gemm_ws(ptr(a), a.stride(0), ptr(sa), ptr(w), w.stride(0), ptr(sw), ptr(bias),
+                                    ptr(residual), residual.stride(0) if residual is not None else 0, ptr(o),
+                                    o.stride(0), M, N, Kp, 0, ptr(ws), ws.numel(), stream_of(a)), "od_w8a8_gemm_ws")
+        return o
     check(lib().od_w8a8_gemm(ptr(a), a.stride(0), ptr(sa), ptr(w), w.stride(0), ptr(sw),
                              ptr(bias), ptr(residual), residual.stride(0) if residual is not None else 0, ptr(o),
                              o.stride(0) if o is not None else 0, ptr(acc), N if acc is not None else 0, M, N, Kp,
@@ -230,6 +255,12 @@ def w8a8_gemm_swiglu(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: tor
         raise ValueError("w8a8_gemm_swiglu: w must be (2F, Kp) with a's Kp")
     sa, sw = _scales(sa, M, "w8a8_gemm_swiglu: sa"), _scales(sw, N, "w8a8_gemm_swiglu: sw")
     out = _check_out(out, (M, N // 2), a.device, "w8a8_gemm_swiglu")
+    ws = splitk_workspace(M, N, Kp, a.device)
+    if ws is not None:
+        check(lib().od_w8a8_gemm_ws(ptr(a), a.stride(0), ptr(sa), ptr(w), w.stride(0), ptr(sw), None, None, 0,
+                                    ptr(out), out.stride(0), M, N, Kp, 1, ptr(ws), ws.numel(), stream_of(a)),
+              "od_w8a8_gemm_ws")
+        return out
     check(lib().od_w8a8_gemm_swiglu(ptr(a), a.stride(0), ptr(sa), ptr(w), w.stride(0),
                                     ptr(sw), ptr(out), out.stride(0), M, N, Kp, stream_of(a)),
           "od_w8a8_gemm_swiglu")

@@ -322,3 +322,60 @@ def test_gate_sigmoid_on_all_bf16_inputs(gpu_lib, K):
     nan = torch.isnan(ref)
     assert torch.equal(torch.isnan(got), nan)
     assert torch.equal(got[~nan].view(torch.int32), ref[~nan].view(torch.int32))
+
+
+def _one_pass(a, sa, w, sw, bias, res, swiglu):
+    """The GEMM without split-K: od_w8a8_gemm / od_w8a8_gemm_swiglu called directly."""
+    from opendecider_amd import _lib
+    from opendecider_amd._lib import ptr, stream_of
+    M, K = a.shape
+    N = w.shape[0]
+    out = torch.empty(M, N // 2 if swiglu else N, dtype=torch.bfloat16, device=DEV)
+    L = _lib.lib()
+    if swiglu:
+        rc = L.od_w8a8_gemm_swiglu(ptr(a), K, ptr(sa), ptr(w), K, ptr(sw), ptr(out), out.stride(0), M, N, K,
+                                   stream_of(a))
+    else:
+        rc = L.od_w8a8_gemm(ptr(a), K, ptr(sa), ptr(w), K, ptr(sw), ptr(bias), ptr(res), N if res is not None else 0,
+                            ptr(out), N, None, 0, M, N, K, stream_of(a))
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(64, 6144, 2048, "plain"), (1, 2048, 6144, "bias_res"), (7, 3000, 4000, "res"),
+                                       (64, 2048, 2048, "bias"), (64, 24576, 4096, "swiglu"), (5, 1030, 6144, "swiglu"),
+                                       (33, 20, 2064, "bias_res"), (64, 4096, 12288, "res"), (200, 2048, 6144, "plain")])
+def test_splitk_bit_identical_to_one_pass(gpu_lib, M, N, K, epi):
+    """Small-M shapes take split-K (int32 partial planes in a workspace, summed exactly, then the same epilogue):
+    the output equals the one-pass GEMM's bit for bit, also when the workspace is one element short (the call then
+    runs one pass), and on the small cases the oracle's."""
+    from opendecider_amd import _lib, kernels
+    from opendecider_amd._lib import ptr, stream_of
+    g = torch.Generator().manual_seed(M + N + K)
+    a, w, sa, sw = _gemm_case(g, M, N, K)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16).to(DEV) if "bias" in epi else None
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV) if "res" in epi else None
+    ad, wd, sad, swd = a.to(DEV), w.to(DEV), sa.to(DEV), sw.to(DEV)
+    swiglu = epi == "swiglu"
+    print(f"splitk M={M} N={N} K={K} {epi}", flush=True)
+    ws = kernels.splitk_workspace(M, N, K, DEV)
+    if (M, N, K) in ((64, 6144, 2048), (1, 2048, 6144), (64, 24576, 4096), (64, 4096, 12288), (64, 2048, 2048)):
+        assert ws is not None, "the plan should split this shape"
+    if swiglu:
+        got = kernels.w8a8_gemm_swiglu(ad, sad, wd, swd)
+    else:
+        got = kernels.w8a8_gemm(ad, sad, wd, swd, bias, res)
+    ref = _one_pass(ad, sad, wd, swd, bias, res, swiglu)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    if ws is not None:
+        short = torch.empty(ws.numel() - 1, dtype=torch.int32, device=DEV)
+        out = torch.empty_like(ref)
+        rc = _lib.lib().od_w8a8_gemm_ws(ptr(ad), K, ptr(sad), ptr(wd), K, ptr(swd), ptr(bias), ptr(res),
+                                        N if res is not None else 0, ptr(out), out.stride(0), M, N, K, int(swiglu),
+                                        ptr(short), short.numel(), stream_of(ad))
+        assert rc == 0
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    if M * N * K <= 64 * 6144 * 2048 and not swiglu:
+        refo = oq.w8a8_epilogue(oq.int_gemm(a, w), sa, sw, None if bias is None else bias.cpu(),
+                                None if res is None else res.cpu())
+        assert torch.equal(got.cpu(), refo)
