@@ -4,7 +4,8 @@
 //
 // Tiling (MFMA-bound at the 9B shapes; one workgroup of 8 waves per CU, two per SIMD so that one wave's MFMAs
 // cover the other's LDS latency and barrier waits):
-//   * workgroup tile BM x BN = 256 x {256 | 192}; K advances 128 bytes per stage, so every row segment a stage
+//   * workgroup tile BM x BN = 256 x 256, 256 x 192 or 128 x 256 (chosen per shape: 128-row tiles when M is too
+//     small to fill the chip with 256-row ones); K advances 128 bytes per stage, so every row segment a stage
 //     loads is one whole 128-byte line (64-byte segments measured at about 60% of the L2 -> CU rate).
 //   * persistent workgroups, one per CU: workgroup b computes tiles b, b + G, b + 2G, ... (G = grid size), as one
 //     pipeline over its (tile, k-tile) stages, so the next tile's first stage loads during the last stage of the
@@ -13,8 +14,9 @@
 //   * global -> LDS by LDS DMA (buffer_load_dwordx4 ... lds): no register staging and no LDS write instructions;
 //     the LDS holds two stages (2 x (256 + BN) x 128 B <= 128 KB) and the loads of the next stage are issued at
 //     the start of the current one. Rows past M/N and bytes past K read as zeros (buffer range check).
-//   * 4 x 2 waves, each owning a 64 x BN/2 sub-tile = 2 x (BN/64) MFMA tiles of 32 x 32 (up to 128 int32
-//     accumulators per lane). Per 32 k a wave reads 2 + BN/64 fragments (ds_read_b128) for 2 x BN/64 MFMAs.
+//   * BM/64 x 8/(BM/64) waves (4 x 2 or 2 x 4), each owning a 64 x BN/(8/(BM/64)) sub-tile = 2 x TN MFMA tiles of
+//     32 x 32 (up to 128 int32 accumulators per lane). Per 32 k a wave reads 2 + TN fragments (ds_read_b128) for
+//     2 x TN MFMAs.
 //   * software pipeline: fragments are double-buffered in registers across k-steps and across stages; the DMA
 //     loads of the next stage are spread between the MFMAs of one k-step; one barrier per stage.
 //   * LDS rows are 128 B (8 chunks of 16 B); chunk c of row r is stored at c ^ ((r >> 1) & 7). gfx950 serves 16
@@ -40,9 +42,13 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kWM = 4, kWN = 2;            // wave grid of a workgroup
-constexpr int kThreads = 64 * kWM * kWN;   // 512
-constexpr int BM = 256;
+constexpr int kThreads = 512;  // 8 waves
+// wave grid of a workgroup with BM rows: BM / 64 x 8 / (BM / 64) waves, each owning 64 rows
+template <int BM>
+struct WaveGrid {
+  static constexpr int kWM = BM / 64, kWN = 8 / kWM;
+};
+constexpr int kMaxBM = 256;
 constexpr int BK = 128;      // bytes of K per stage
 constexpr int kCpr = BK / 16;  // 16-byte chunks per row per stage
 constexpr int kGroupM = 4;
@@ -92,9 +98,10 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 //     values are fixed for the tile; y = bf16((t + bias) + residual), the same fp32 operation order as the
 //     unfused product, with one rounding. Rows go in groups of 4 whose residual loads issue together.
 // Only the GENERAL variant carries the scalar paths for unaligned rows and a ragged last column group.
-template <int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU, int TM, int TN>
+template <int BM, int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU, int TM, int TN>
 __device__ __forceinline__ void epilogue(const GemmArgs& p, const v16i (&acc)[TM][TN], int8_t* stage_buf, int tm,
                                          int tn, int wm, int wn, int wave, int lane) {
+  constexpr int kWM = WaveGrid<BM>::kWM, kWN = WaveGrid<BM>::kWN;
   constexpr int kRowsW = BM / kWM;
   constexpr int kCols = BN / kWN;             // columns of the wave's sub-tile
   constexpr int kC4 = kCols / 4;              // 4-column chunks per row
@@ -241,7 +248,7 @@ struct Panels {
   __amdgpu_buffer_rsrc_t a, w;
 };
 
-template <int BN>
+template <int BM, int BN>
 __device__ __forceinline__ Panels panels_of(const GemmArgs& p, int v, int ntiles) {
   if (v >= ntiles) {
     return {__builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, 0, 0x00020000),
@@ -257,11 +264,13 @@ __device__ __forceinline__ Panels panels_of(const GemmArgs& p, int v, int ntiles
                                             (int)((rows_w - 1) * p.ldw + p.K), 0x00020000)};
 }
 
-template <int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU>
+template <int BM, int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU>
 __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
-  constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile: 64 x BN/2
+  constexpr int kWM = WaveGrid<BM>::kWM, kWN = WaveGrid<BM>::kWN;
+  constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile: 64 x BN/kWN
   constexpr int TM = kRowsW / 32;    // 2
-  constexpr int TN = kColsW / 32;    // 4 or 3
+  constexpr int TN = kColsW / 32;    // 4 or 3 (BM = 256), 2 (BM = 128)
+  static_assert(kColsW % 32 == 0, "a wave's columns are whole 32-column MFMA tiles");
   constexpr int kSlabA = BM * BK, kSlabB = BN * BK, kStage = kSlabA + kSlabB;
   constexpr int kOpsA = BM / 64, kOpsB = BN / 64;  // DMA loads per wave per stage (8 waves x 8 rows each)
   __shared__ __attribute__((aligned(16))) int8_t smem[2 * kStage];
@@ -352,7 +361,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   v4i f0a[TM], f0b[TN], f1a[TM], f1b[TN];
   constexpr int kOps0 = kOpsA + kOpsB;
   int v = blockIdx.x;
-  Panels cur = panels_of<BN>(p, v, ntiles);
+  Panels cur = panels_of<BM, BN>(p, v, ntiles);
 #pragma unroll
   for (int o = 0; o < kOps0; ++o) dma(0, cur, kb, o);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
@@ -381,7 +390,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   // (the stage buffer is a run-time value: unrolling two stages with compile-time buffer indices lengthens the
   // live ranges)
   for (; v < ntiles; v += gridDim.x) {
-    const Panels nxt = panels_of<BN>(p, v + (int)gridDim.x, ntiles);
+    const Panels nxt = panels_of<BM, BN>(p, v + (int)gridDim.x, ntiles);
     for (int kt = kb; kt + 1 < ke; ++kt) {
       stage(buf, cur, kt + 1);
       buf ^= 1;
@@ -390,7 +399,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
     buf ^= 1;
     int tm, tn;
     tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
-    epilogue<BN, ACC_ONLY, GENERAL, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, tm, tn, wm, wn, wave, lane);
+    epilogue<BM, BN, ACC_ONLY, GENERAL, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, tm, tn, wm, wn, wave, lane);
     // every wave is done with its band (in the buffer the next stage's DMA loads overwrite) before that stage
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     zero_acc();
@@ -417,17 +426,27 @@ int cu_count() {
 }
 
 struct Tiling {
-  bool use192;
+  int bm, bn;
   int64_t tiles_m, tiles_n;
 };
 
+// Tile shape: 256 x 256, 256 x 192 or 128 x 256, whichever takes the least time by the count of 256-workgroup
+// waves of tiles times the work of one tile (a 128-row tile runs its stage in about 0.575 of a 256 x 256 one: half
+// the MFMAs, a higher fragment-read ratio). Large M keeps 256-row tiles; M <= ~2048 gets 128-row ones.
 Tiling tiling_of(int64_t M, int64_t N) {
-  const int64_t tiles_m = (M + BM - 1) / BM;
-  // BN: 256, or 192 when that takes fewer tile-widths of work at 256 workgroups per wave (e.g. N = 6144).
-  const int64_t t256 = tiles_m * ((N + 255) / 256), t192 = tiles_m * ((N + 191) / 192);
-  const int64_t cost256 = ((t256 + 255) / 256) * 256, cost192 = ((t192 + 255) / 256) * 192;
-  const bool use192 = cost192 < cost256;
-  return {use192, tiles_m, use192 ? (N + 191) / 192 : (N + 255) / 256};
+  const struct { int bm, bn; double cost; } cand[3] = {{256, 256, 1.0}, {256, 192, 0.75}, {128, 256, 0.575}};
+  const int64_t cus = cu_count();
+  Tiling best{256, 256, 0, 0};
+  double best_cost = 0.0;
+  for (const auto& c : cand) {
+    const int64_t tm = (M + c.bm - 1) / c.bm, tn = (N + c.bn - 1) / c.bn;
+    const double cost = (double)((tm * tn + cus - 1) / cus) * c.cost;
+    if (best.tiles_m == 0 || cost < best_cost) {
+      best = {c.bm, c.bn, tm, tn};
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 // Split-K for shapes with too few tiles to fill the chip (small M): `splits` workgroups per tile each sum
@@ -446,7 +465,7 @@ SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
   const Tiling t = tiling_of(M, N);
   const int64_t ntiles = t.tiles_m * t.tiles_n, cus = cu_count();
   if (ntiles * 2 > cus || nk < 4) return none;
-  const double t_stage = (t.use192 ? 192.0 : 256.0) / 192.0;  // us per stage
+  const double t_stage = (double)t.bm * t.bn / (256.0 * 192.0);  // us per stage
   const double base = nk * t_stage;
   double best = 0.85 * base;
   SplitPlan bp = none;
@@ -514,7 +533,6 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
   GemmArgs p = p0;
   const int64_t M = p.M, N = p.N, K = p.K;
   const Tiling t = tiling_of(M, N);
-  const bool use192 = t.use192;
   const int64_t tiles_m = t.tiles_m, tiles_n = t.tiles_n;
   if (tiles_m * tiles_n > 0x7fffffff) return OD_ERR_SHAPE;
   p.tiles_m = (int)tiles_m;
@@ -529,17 +547,21 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
   // aligned (with SwiGLU, 2-column output groups 4-byte aligned); anything else takes the GENERAL variant.
   auto al = [](const void* q, unsigned a) { return (((uintptr_t)q) & (a - 1)) == 0; };
   const bool fast_k = K % BK == 0 && N % 4 == 0;
-  auto launch = [&](auto BNc, auto ACCc, auto GENc, auto SWc) {
-    w8a8_gemm_kernel<decltype(BNc)::value, decltype(ACCc)::value, decltype(GENc)::value, decltype(SWc)::value>
-        <<<grid, block, 0, st>>>(p);
+  auto launch = [&](auto BMc, auto BNc, auto ACCc, auto GENc, auto SWc) {
+    w8a8_gemm_kernel<decltype(BMc)::value, decltype(BNc)::value, decltype(ACCc)::value, decltype(GENc)::value,
+                     decltype(SWc)::value><<<grid, block, 0, st>>>(p);
+  };
+  auto launch1 = [&](auto BMc, auto BNc, auto ACCc, auto SWc, bool general) {
+    general ? launch(BMc, BNc, ACCc, std::true_type{}, SWc) : launch(BMc, BNc, ACCc, std::false_type{}, SWc);
   };
   auto launch2 = [&](auto ACCc, auto SWc, bool general) {
-    if (use192) {
-      general ? launch(std::integral_constant<int, 192>{}, ACCc, std::true_type{}, SWc)
-              : launch(std::integral_constant<int, 192>{}, ACCc, std::false_type{}, SWc);
+    using I = std::integral_constant<int, 256>;
+    if (t.bm == 128) {
+      launch1(std::integral_constant<int, 128>{}, I{}, ACCc, SWc, general);
+    } else if (t.bn == 192) {
+      launch1(I{}, std::integral_constant<int, 192>{}, ACCc, SWc, general);
     } else {
-      general ? launch(std::integral_constant<int, 256>{}, ACCc, std::true_type{}, SWc)
-              : launch(std::integral_constant<int, 256>{}, ACCc, std::false_type{}, SWc);
+      launch1(I{}, I{}, ACCc, SWc, general);
     }
   };
   if (sp && sp->splits > 1) {
@@ -587,7 +609,7 @@ int gemm_check(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64
   if (K % 16 || lda % 16 || ldw % 16 || !od_aligned16(a) || !od_aligned16(w)) return OD_ERR_ALIGN;
   if (K >= 133144) return OD_ERR_UNSUPPORTED;  // int32 accumulators could overflow
   // buffer offsets are 32-bit: one tile's A panel (256 rows) and W panel must stay below 2 GiB
-  if ((int64_t)BM * lda >= (1ll << 31) || (int64_t)256 * ldw >= (1ll << 31)) return OD_ERR_UNSUPPORTED;
+  if ((int64_t)kMaxBM * lda >= (1ll << 31) || (int64_t)256 * ldw >= (1ll << 31)) return OD_ERR_UNSUPPORTED;
   return OD_OK;
 }
 

@@ -359,7 +359,7 @@ def test_splitk_bit_identical_to_one_pass(gpu_lib, M, N, K, epi):
     swiglu = epi == "swiglu"
     print(f"splitk M={M} N={N} K={K} {epi}", flush=True)
     ws = kernels.splitk_workspace(M, N, K, DEV)
-    if (M, N, K) in ((64, 6144, 2048), (1, 2048, 6144), (64, 24576, 4096), (64, 4096, 12288), (64, 2048, 2048)):
+    if (M, N, K) in ((1, 2048, 6144), (64, 4096, 12288), (64, 2048, 2048), (5, 1030, 6144), (200, 2048, 6144)):
         assert ws is not None, "the plan should split this shape"
     if swiglu:
         got = kernels.w8a8_gemm_swiglu(ad, sad, wd, swd)
