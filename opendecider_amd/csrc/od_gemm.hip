@@ -428,21 +428,23 @@ int cu_count() {
 struct Tiling {
   int bm, bn;
   int64_t tiles_m, tiles_n;
+  double rel;  // time of one tile relative to a 256 x 256 one
 };
 
-// Tile shape: 256 x 256, 256 x 192 or 128 x 256, whichever takes the least time by the count of 256-workgroup
-// waves of tiles times the work of one tile (a 128-row tile runs its stage in about 0.575 of a 256 x 256 one: half
-// the MFMAs, a higher fragment-read ratio). Large M keeps 256-row tiles; M <= ~2048 gets 128-row ones.
+// Tile shape: 256 x 256, 256 x 192 or 128 x 256, whichever takes the least time by the number of tiles each
+// persistent workgroup runs times the time of one tile. Measured per-tile times relative to 256 x 256 (K = 4096 and
+// 12288, N = 4096 to 24576, M = 512 to 16384): 0.79-0.88 for 256 x 192, 0.61-0.69 for 128 x 256 (a smaller tile
+// reads more LDS fragments per MFMA); 0.84 and 0.68 pick the fastest of the three at every measured shape.
 Tiling tiling_of(int64_t M, int64_t N) {
-  const struct { int bm, bn; double cost; } cand[3] = {{256, 256, 1.0}, {256, 192, 0.75}, {128, 256, 0.575}};
+  const struct { int bm, bn; double cost; } cand[3] = {{256, 256, 1.0}, {256, 192, 0.84}, {128, 256, 0.68}};
   const int64_t cus = cu_count();
-  Tiling best{256, 256, 0, 0};
+  Tiling best{256, 256, 0, 0, 1.0};
   double best_cost = 0.0;
   for (const auto& c : cand) {
     const int64_t tm = (M + c.bm - 1) / c.bm, tn = (N + c.bn - 1) / c.bn;
     const double cost = (double)((tm * tn + cus - 1) / cus) * c.cost;
     if (best.tiles_m == 0 || cost < best_cost) {
-      best = {c.bm, c.bn, tm, tn};
+      best = {c.bm, c.bn, tm, tn, c.cost};
       best_cost = cost;
     }
   }
@@ -451,9 +453,9 @@ Tiling tiling_of(int64_t M, int64_t N) {
 
 // Split-K for shapes with too few tiles to fill the chip (small M): `splits` workgroups per tile each sum
 // kt_per k-tiles into their own int32 plane of a workspace [splits][M][ldws], and splitk_finalize_kernel adds the
-// planes (integer sums: exact) and applies the same epilogue. Chosen when a simple cost model (about 1 us per
-// k-tile stage of a 256 x 192 tile, the partial planes written and read once at ~3 TB/s, ~2.5 us for the extra
-// launch) predicts at least 15% less time than one pass.
+// planes (integer sums: exact) and applies the same epilogue. Chosen when a simple cost model (about 1.2 us per
+// k-tile stage of a 256 x 256 tile, scaled by the tile's relative time; the partial planes written and read once
+// at ~3 TB/s; ~2.5 us for the extra launch) predicts at least 15% less time than one pass.
 struct SplitPlan {
   int splits, kt_per;
   int64_t ldws, ws_ints;
@@ -465,7 +467,7 @@ SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
   const Tiling t = tiling_of(M, N);
   const int64_t ntiles = t.tiles_m * t.tiles_n, cus = cu_count();
   if (ntiles * 2 > cus || nk < 4) return none;
-  const double t_stage = (double)t.bm * t.bn / (256.0 * 192.0);  // us per stage
+  const double t_stage = 1.2 * t.rel;  // us per k-tile stage of one tile
   const double base = nk * t_stage;
   double best = 0.85 * base;
   SplitPlan bp = none;
