@@ -131,6 +131,40 @@ def test_bf16_dequant_is_the_reference_materialize():
     assert torch.equal(oa.dequant_state(kq, ks, "fp32"), kq.float() * ks[..., None])
 
 
+def test_two_level_attention_matches_brute_force():
+    """The question-cache attention (two_level_attention) against scalar float64 softmax loops: every query of a row
+    of question g sees all keys of its state, the unmasked keys of question g, and its own row's keys 0..i; GQA
+    head h reads KV head h // (Hq / Hkv). Pads of a question are excluded; rows of two questions on one state."""
+    g = torch.Generator().manual_seed(17)
+    Ns, Hq, Hkv, T, T2, t, D = 2, 4, 2, 5, 4, 3, 8
+    kq = torch.randint(-127, 128, (Ns, Hkv, T, D), generator=g, dtype=torch.int8)
+    vq = torch.randint(-127, 128, (Ns, Hkv, T, D), generator=g, dtype=torch.int8)
+    ks, vs = torch.rand(Ns, Hkv, T, generator=g) * 0.02, torch.rand(Ns, Hkv, T, generator=g) * 0.02
+    group_state = [1, 1, 0]
+    Kq2, Vq2 = _rand(g, 3, Hkv, T2, D), _rand(g, 3, Hkv, T2, D)
+    qmask = torch.tensor([[1, 1, 1, 0], [1, 1, 1, 1], [1, 0, 0, 0]], dtype=torch.bool)
+    row_group = torch.tensor([0, 0, 1, 2, 2])
+    R = len(row_group)
+    q, k, v = _rand(g, R, Hq, t, D), _rand(g, R, Hkv, t, D), _rand(g, R, Hkv, t, D)
+    out, lse = oa.two_level_attention(q, k, v, kq, ks, vq, vs, Kq2, Vq2, qmask, 0.4, row_group, group_state,
+                                      dequant="fp32", dtype=torch.float64)
+    for r in range(R):
+        gi = int(row_group[r])
+        s = group_state[gi]
+        for h in range(Hq):
+            kv = h // (Hq // Hkv)
+            Ks = kq[s, kv].double() * ks[s, kv][:, None].double()
+            Vs = vq[s, kv].double() * vs[s, kv][:, None].double()
+            keep = qmask[gi].nonzero().squeeze(1)
+            K = torch.cat([Ks, Kq2[gi, kv][keep].double(), k[r, kv].double()])
+            V = torch.cat([Vs, Vq2[gi, kv][keep].double(), v[r, kv].double()])
+            n_pre = T + len(keep)
+            allowed = [[j < n_pre or j - n_pre <= i for j in range(len(K))] for i in range(t)]
+            o_bf, l_bf = oa.brute_force_attention(q[r, h], K, V, 0.4, allowed)
+            assert torch.allclose(out[r, h], o_bf, atol=1e-9), (r, h)
+            assert torch.allclose(lse[r, h], l_bf, atol=1e-9), (r, h)
+
+
 # ---- wide_attention_blocked (the reference kernel's arithmetic, step by step)
 
 def test_wide_blocked_pinned_by_exact_attention():
