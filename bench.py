@@ -502,7 +502,7 @@ def run_gemm(args):
     """The W8A8 linear alone: od_act_quant + od_w8a8_gemm on the reference's sweep (scripts/bench_gemm.py:22-23:
     (K, N) in {(2048, 6144), (6144, 2048), (2048, 2048)} x M in {64, 512, 2048, 8192}) and on the 9B layer shapes at
     M = 4096 (QKV 4096 -> 6144, O 4096 -> 4096, gate+up 4096 -> 24576 also with SwiGLU in the epilogue, down
-    12288 -> 4096). Inputs as config 2: X bf16 N(0, 1) with 1% outlier channels x20, W N(0, 0.02) with SmoothQuant
+    12288 -> 4096), and the single 256 x 4096 x 4096 linear of config 0. Inputs as config 2: X bf16 N(0, 1) with 1% outlier channels x20, W N(0, 0.02) with SmoothQuant
     factors U(0.5, 2) folded in, per-channel int8; 1/s fused into the activation quantizer. HIP events over 20 calls
     of each kernel after 3 warm-up calls; the vendor int8 GEMM (torch._int_mm, hipBLASLt, int32 output, no
     epilogue) beside it. Each timing is a replay of a HIP graph of the 20 calls (GPU time, no host launch gaps).
@@ -547,6 +547,7 @@ def run_gemm(args):
     rows = []
     shapes = [("bench_gemm", K, N, M) for K, N in ((2048, 6144), (6144, 2048), (2048, 2048))
               for M in (64, 512, 2048, 8192)]
+    shapes += [("config0", 4096, 4096, 256)]
     shapes += [("9b_qkv", 4096, 6144, 4096), ("9b_o", 4096, 4096, 4096), ("9b_gate_up", 4096, 24576, 4096),
                ("9b_down", 12288, 4096, 4096)]
     for name, K, N, M in shapes:
