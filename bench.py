@@ -771,11 +771,39 @@ def run_attention(args):
                      "kv_frac_of_hbm": kv_bytes / (ms / n * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "algorithmic_gbs": by / (ms * 1e-3) / 1e9, "launches": n,
                      "path": "staged" if kernels.uses_staging(rows, t, Hq, Hkv) else "direct"}
-    return {"metric": "branched attention: KV GB/s on the KV-bound probe (TFLOP/s on the config-1 shape beside it)",
-            "value": res["kv_probe"]["kv_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": res["kv_probe"]["avg_launch_us"] / 1e3, "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "int8 K/V, bf16 MFMA", "data": "synthetic",
-            "config": {"workload": "branched attention alone: config-1 shape and KV-bound probe"}, "shapes": res}
+    out = {"metric": "branched attention: KV GB/s on the KV-bound probe (TFLOP/s on the config-1 shape beside it)",
+           "value": res["kv_probe"]["kv_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": res["kv_probe"]["avg_launch_us"] / 1e3, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "int8 K/V, bf16 MFMA", "data": "synthetic",
+           "config": {"workload": "branched attention alone: config-1 shape and KV-bound probe"}, "shapes": res}
+    if not args.no_cpu_baseline:
+        # the reference's CPU branch of _split_attention (prefix_attn.py:58-76) on K/V materialized in bf16, as the
+        # oracle restates it, for 1 of the 8 config-1 states (32 options x 16 tokens over 2048 keys), scaled x8
+        from oracle import attention as oa
+        torch.set_num_threads(os.cpu_count() or 1)
+        cg = torch.Generator().manual_seed(5)
+        T, rows = 2048, 32
+        q = torch.randn(rows, Hq, t, D, generator=cg).to(torch.bfloat16)
+        k = torch.randn(rows, Hkv, t, D, generator=cg).to(torch.bfloat16)
+        v = torch.randn(rows, Hkv, t, D, generator=cg).to(torch.bfloat16)
+        kq = torch.randint(-127, 128, (1, Hkv, T, D), generator=cg, dtype=torch.int8)
+        vq = torch.randint(-127, 128, (1, Hkv, T, D), generator=cg, dtype=torch.int8)
+        ks, vs = torch.rand(1, Hkv, T, generator=cg) * 0.02, torch.rand(1, Hkv, T, generator=cg) * 0.02
+        fn = lambda: oa.branched_attention_int8(q, k, v, kq, ks, vq, vs, D ** -0.5)
+        fn()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        per_state = sorted(ts)[1]
+        out["cpu_baseline"] = {"value": 1e3 * per_state * 8, "unit": "ms per config-1 call", "cores": torch.get_num_threads(),
+                               "kind": "port",
+                               "sample": (f"1 of the 8 states (32 options x 16 tokens over 2048 int8 keys, K/V "
+                                          f"materialized in bf16), median of 3 after a warm-up: {per_state * 1e3:.0f} ms, "
+                                          f"scaled x8"),
+                               "gpu_speedup": per_state * 8 / (res["config1"]["avg_launch_us"] * 1e-6)}
+    return out
 
 
 def run_lm_logprob(args):
