@@ -14,6 +14,9 @@ Modules
              Reference: src/opendecider/wide_attention.py, src/opendecider/prefix_attn.py.
   decoder    A dense 9B-class decoder layer stack used as the decision-forward harness around the path, and the
              option pooling + 'none' logit + log-softmax readout.
+  gdn        The Gated DeltaNet (linear-attention) layer of the Qwen3.5 hybrid backbone: conv + SiLU, l2norm,
+             gates, the gated delta rule, the gated RMSNorm. Reference: transformers' Qwen3.5 modules, which the
+             reference runs (src/opendecider/backbone.py:256-289, skipkv.py:208-231).
 
 Pinning (how each function is checked, in tests/test_oracle_*.py)
   quant.quantize_rows      brute-force per-element IEEE float32 arithmetic with numpy and round-half-even, hand
@@ -24,6 +27,9 @@ Pinning (how each function is checked, in tests/test_oracle_*.py)
   quant.smooth_*           the reference test test_int8_gemm.py:70-88 restated (float64 exactness, formula).
   attention.*              float64 brute-force softmax loops on tiny shapes; merge == one softmax over the
                            concatenated keys; permutation equivariance; empty key set; torch.logsumexp.
+  gdn.*                    transformers' own functions (causal_conv1d_fn / _update, l2norm, the recurrent and
+                           chunked gated delta rule, Qwen3_5RMSNormGated), a pure-decay closed form, continuation ==
+                           whole sequence, decimal rsqrt.
   decoder.*                the layer is the build's own harness (not a reference function): each sub-step is
                            pinned separately (RMSNorm closed form, RoPE rotation norm preservation and the
                            position-difference invariance of q.k, SwiGLU) and the whole forward is checked for

@@ -1,0 +1,140 @@
+"""Pins the Gated DeltaNet oracle (oracle/gdn.py) on the CPU: against transformers' own Qwen3.5 functions (the
+third-party code the reference runs these layers through; transformers 5.15.0 here, the reference requires >=5.2),
+against closed forms that hold whatever the implementation (no write: pure decay; continuation of a sequence equals
+the whole sequence), and against decimal arithmetic where the oracle claims correct rounding."""
+import decimal
+
+import pytest
+import torch
+
+from oracle import gdn as og
+
+mq = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+
+
+def _bf(g, *shape, scale=1.0):
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def test_conv_silu_matches_causal_conv1d_fresh_and_continued():
+    g = torch.Generator().manual_seed(0)
+    S, L, C = 3, 29, 40
+    x, w = _bf(g, S, L, C), _bf(g, C, 4, scale=0.3)
+    state = _bf(g, S, 3, C)
+    y, new = og.conv_silu(x, w, None)
+    ref = mq.causal_conv1d_fn(x.transpose(1, 2), w, None, activation="silu").transpose(1, 2)
+    assert torch.equal(y, ref)
+    assert torch.equal(new, x[:, -3:])
+    cs = state.transpose(1, 2).contiguous().clone()
+    y2, new2 = og.conv_silu(x, w, state)
+    ref2 = mq.causal_conv1d_update(x.transpose(1, 2).contiguous(), cs, w, None, activation="silu").transpose(1, 2)
+    assert torch.equal(y2, ref2)
+    assert torch.equal(new2, cs.transpose(1, 2))          # the reference's updated conv state
+    # a 1- and a 2-token continuation keep the right tail of the previous state
+    for L2 in (1, 2):
+        _, n = og.conv_silu(x[:, :L2], w, state)
+        assert torch.equal(n, torch.cat([state, x[:, :L2]], 1)[:, -3:])
+
+
+def test_gates_match_the_reference_formula():
+    g = torch.Generator().manual_seed(1)
+    a, b = _bf(g, 50, 32, scale=3.0), _bf(g, 50, 32, scale=3.0)
+    a[0, :4] = torch.tensor([25.0, -30.0, 19.875, 20.125])   # both sides of softplus' threshold
+    A_log = torch.log(torch.rand(32, generator=g) * 15.5 + 0.5).to(torch.bfloat16)
+    dt = (1 + 0.1 * torch.randn(32, generator=g)).to(torch.bfloat16)
+    gg, beta = og.gates(a, b, A_log, dt)
+    ref = -A_log.float().exp() * torch.nn.functional.softplus(a.float() + dt)
+    assert ((gg - ref).abs() <= 2 * ref.abs() * 2.0 ** -23).all()       # within torch's fp32 exp / log1p ulps
+    assert torch.equal(beta.to(torch.bfloat16), b.sigmoid())
+
+
+def test_l2norm_bf16_is_the_reference_arithmetic_with_a_correctly_rounded_rsqrt():
+    """Squares, sum, + eps and the product as torch's bf16 ops give them; the rsqrt correctly rounded (torch's CPU
+    bf16 rsqrt is an approximation: where the two differ, the oracle's is the nearest bf16 to the exact value)."""
+    g = torch.Generator().manual_seed(2)
+    x = _bf(g, 4000, 16)
+    got = og.l2norm_bf16(x)
+    ref = mq.l2norm(x, dim=-1, eps=1e-6)
+    diff = (got != ref).any(-1)
+    assert diff.float().mean().item() < 0.01
+    den = ((x.float() * x.float()).to(torch.bfloat16).double().sum(-1).float().to(torch.bfloat16).float()
+           + torch.tensor(1e-6)).to(torch.bfloat16)
+    decimal.getcontext().prec = 30
+    for i in diff.nonzero().squeeze(1).tolist()[:40]:
+        exact = 1 / decimal.Decimal(float(den[i])).sqrt()
+        want = torch.tensor(float(exact)).to(torch.bfloat16)
+        inv = (got[i].float() / x[i].float())[x[i] != 0]
+        # every element's product used the same inv: recover it from the element with the largest |x|
+        j = x[i].float().abs().argmax()
+        assert torch.equal((x[i, j].float() * want.float()).to(torch.bfloat16), got[i, j]), (i, inv)
+
+
+def test_recurrence_matches_transformers_recurrent_and_chunked():
+    g = torch.Generator().manual_seed(3)
+    S, L, H, dk, dv = 2, 70, 4, 32, 16
+    q = og.l2norm_bf16(_bf(g, S, L, H, dk))
+    k = og.l2norm_bf16(_bf(g, S, L, H, dk))
+    v = _bf(g, S, L, H, dv)
+    a, b = _bf(g, S, L, H), _bf(g, S, L, H)
+    A_log = torch.log(torch.rand(H, generator=g) * 15.5 + 0.5).to(torch.bfloat16)
+    dt = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    gg, beta = og.gates(a, b, A_log, dt)
+    init = torch.randn(S, H, dk, dv, generator=g)
+    o, st = og.recurrence(q, k, v, gg, beta, init, torch.float64)
+    o32, st32 = og.recurrence(q, k, v, gg, beta, init, torch.float32)
+    ref_o, ref_st = mq.torch_recurrent_gated_delta_rule(q, k, v, gg, beta.to(torch.bfloat16), init, True)
+    chk_o, chk_st = mq.torch_chunk_gated_delta_rule(q, k, v, gg, beta.to(torch.bfloat16), initial_state=init,
+                                                    output_final_state=True)
+    step = lambda t: t.float().abs() * 2.0 ** -7 + 1e-6
+    for other in (ref_o, chk_o, o32):
+        assert ((o.float() - other.float()).abs() <= step(o)).all()      # within one bf16 step
+    assert torch.allclose(st.float(), ref_st, atol=1e-5) and torch.allclose(st.float(), chk_st, atol=1e-5)
+    assert torch.equal(o32, ref_o)                                          # fp32 mode: the reference's own ops
+
+
+def test_pure_decay_closed_form():
+    """beta = 0 (no writes): S_t = exp(sum g) S_0 and o_t = exp(sum_{<=t} g) S_0^T q_t / sqrt(dk)."""
+    g = torch.Generator().manual_seed(4)
+    S, L, H, dk, dv = 1, 9, 2, 8, 4
+    q = og.l2norm_bf16(_bf(g, S, L, H, dk))
+    k = og.l2norm_bf16(_bf(g, S, L, H, dk))
+    v = _bf(g, S, L, H, dv)
+    gg = -torch.rand(S, L, H, generator=g)
+    init = torch.randn(S, H, dk, dv, generator=g).double()
+    o, st = og.recurrence(q, k, v, gg, torch.zeros(S, L, H), init.float(), torch.float64)
+    cum = torch.cumsum(gg.double(), 1)
+    assert torch.allclose(st, torch.exp(cum[:, -1])[..., None, None] * init.float().double(), rtol=1e-12)
+    qs = (q.float() * torch.tensor(1 / dk ** 0.5)).double()
+    want = torch.einsum("slh,shkv,slhk->slhv", torch.exp(cum), init.float().double(), qs)
+    assert torch.allclose(o.float(), want.float().to(torch.bfloat16).float())
+
+
+def test_continuation_equals_the_whole_sequence():
+    """The branch-row identity behind a shared prefix state: a sequence run as [prefix] then [row] continuing the
+    prefix's conv and recurrent states equals the whole [prefix ; row] run (float64 recurrence)."""
+    cfg = og.GDNConfig(hidden=64, n_k_heads=2, n_v_heads=4, dk=16, dv=8)
+    g = torch.Generator().manual_seed(5)
+    lw = og.make_gdn_weights(cfg, g)
+    qlin = og.quantize_gdn(lw)
+    P, L = 11, 6
+    x = _bf(g, P + L, cfg.hidden)
+    whole, _, st_whole = og.gdn_mixer(x, lw, qlin, cfg, 1, P + L)
+    pre, conv_s, rec_s = og.gdn_mixer(x[:P], lw, qlin, cfg, 1, P)
+    row, _, st_row = og.gdn_mixer(x[P:], lw, qlin, cfg, 1, L, conv_state=conv_s, rec_state=rec_s)
+    # the W8A8 projection quantizes per token, so token rows are independent of the split
+    assert torch.equal(torch.cat([pre, row]), whole)
+    assert torch.allclose(st_row, st_whole)
+
+
+def test_gated_norm_matches_qwen3_5_rmsnorm_gated():
+    g = torch.Generator().manual_seed(6)
+    o, z = _bf(g, 300, 4, 64), _bf(g, 300, 4, 64, scale=2.0)
+    w = (1 + 0.1 * torch.randn(64, generator=g)).to(torch.bfloat16)
+    m = mq.Qwen3_5RMSNormGated(64, eps=1e-6)
+    m.weight.data = w.clone()
+    m = m.to(torch.bfloat16)
+    ref = m(o.reshape(-1, 64), z.reshape(-1, 64)).reshape(o.shape)
+    got = og.gated_norm(o, z, w, 1e-6)
+    # the reference's fp32 rsqrt and silu are within a few ulps of the correctly rounded values the oracle uses
+    d = (got.float() - ref.float()).abs()
+    assert (d <= got.float().abs() * 2.0 ** -7 + 1e-30).all() and (got != ref).float().mean().item() < 0.01
