@@ -399,6 +399,42 @@ int od_qk_norm_rope_kv_append(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, i
                               const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps, int8_t* kq,
                               float* ks, int8_t* vq, float* vs, int64_t cap, int64_t n0, od_stream_t stream);
 
+/*
+ * Gated DeltaNet (linear-attention) layers of the Qwen3.5 hybrid backbone: the passes between the layer's input
+ * projection (one W8A8 GEMM giving [qkv | z | b | a]) and its out_proj. Replaces the body of transformers'
+ * Qwen3_5GatedDeltaNet.forward that the reference runs (src/opendecider/backbone.py:256-289 padded continuations,
+ * src/opendecider/skipkv.py:208-231): causal_conv1d_fn / causal_conv1d_update + SiLU, l2norm, the gates, the
+ * chunked / recurrent gated delta rule and Qwen3_5RMSNormGated; for option rows continuing a shared state, the
+ * per-row state copies of the reference (backbone.py:529-571 row_states) become reads of the one shared state
+ * (docs/branched_shared_prefix_math.md:16-37).
+ * Token layout: M = S * L tokens, sequence s = tokens s L .. s L + L - 1. Dims: n_k key heads of dk, n_v value heads
+ * of dv (n_v % n_k == 0, value head h reads key head h / (n_v / n_k)), C = 2 n_k dk + n_v dv conv channels.
+ *
+ * od_gdn_prep: proj bf16 [M, ldp] ([qkv C | z n_v dv | b n_v | a n_v], ldp % 8 == 0, 16-byte aligned); conv_w bf16
+ *   [C, 4]; conv_in bf16 [n_states, 3, C] (the previous 3 pre-conv inputs of each state) or NULL (zeros); seq_state
+ *   int32 [S] (the state sequence s continues; NULL: state s; an index outside [0, n_states) reads zeros); A_log,
+ *   dt_bias bf16 [n_v]. Writes qk bf16 [M, 2 n_k dk] (l2-normed q heads then k heads), v bf16 [M, n_v dv], g fp32
+ *   [M, n_v] = -exp(A_log) softplus(a + dt_bias), beta fp32 [M, n_v] = bf16(sigmoid(b)), and, if conv_out is not NULL,
+ *   bf16 [S, 3, C]: the last 3 pre-conv inputs of each [state ; sequence] (conv_out must not overlap conv_in).
+ *   dk, dv multiples of 16 with dk / 16 a power of two <= 64, C <= 16384, n_v <= C / 16.
+ * od_gdn_recurrence: qk, v, g, beta as od_gdn_prep writes them; init fp32 [n_states, n_v, dk, dv] or NULL (zeros),
+ *   read through seq_state as above; writes o bf16 [M, n_v dv] and, if final_state is not NULL, fp32 [S, n_v, dk,
+ *   dv] (final_state may alias init only when seq_state is NULL). dk == 128, dv % 32 == 0; L >= 1.
+ * od_gdn_norm_quant: o bf16 [M, ldo], z bf16 [M, ldz] (the z columns of proj), w bf16 [dv], inv_s bf16 [n_v dv] or
+ *   NULL: y = bf16(bf16(w * bf16(o * r)) * silu(z)) per value head (r = 1 / sqrt(mean(o^2) + eps)), then
+ *   od_act_quant's bytes and scale of y (times inv_s): xq int8 [M, ldq] (ldq % 16 == 0), sx fp32 [M].
+ */
+int od_gdn_prep(const uint16_t* proj, int64_t ldp, const uint16_t* conv_w, const uint16_t* conv_in,
+                const int32_t* seq_state, int64_t n_states, const uint16_t* A_log, const uint16_t* dt_bias, int64_t S,
+                int64_t L, int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, uint16_t* qk, uint16_t* v, float* g,
+                float* beta, uint16_t* conv_out, od_stream_t stream);
+int od_gdn_recurrence(const uint16_t* qk, const uint16_t* v, const float* g, const float* beta, const float* init,
+                      const int32_t* seq_state, int64_t n_states, int64_t S, int64_t L, int64_t n_k, int64_t n_v,
+                      int64_t dk, int64_t dv, uint16_t* o, float* final_state, od_stream_t stream);
+int od_gdn_norm_quant(const uint16_t* o, int64_t ldo, const uint16_t* z, int64_t ldz, const uint16_t* w,
+                      const uint16_t* inv_s, float eps, int64_t M, int64_t n_v, int64_t dv, int8_t* xq, int64_t ldq,
+                      float* sx, od_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

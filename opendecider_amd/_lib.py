@@ -63,6 +63,12 @@ SIGNATURES = {
                                   _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _c_ptr],
     "od_attn_stage_bf16": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64,
                            ctypes.c_float, _c_ptr, _i64, _c_ptr],
+    "od_gdn_prep": [_c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64,
+                    _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
+    "od_gdn_recurrence": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                          _c_ptr, _c_ptr, _c_ptr],
+    "od_gdn_norm_quant": [_c_ptr, _i64, _c_ptr, _i64, _c_ptr, _c_ptr, ctypes.c_float, _i64, _i64, _i64, _c_ptr, _i64,
+                          _c_ptr, _c_ptr],
     "od_lm_head_logprob_ws": [_i64, _i64, _c_ptr],
     "od_lm_head_logprob": [_c_ptr, _i64, _c_ptr, _i64, ctypes.c_int, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64,
                            _c_ptr, _c_ptr, _i64, _c_ptr],

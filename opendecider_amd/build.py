@@ -22,7 +22,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libod_mi355x.so")
-SOURCES = ["od_quant.hip", "od_gemm.hip", "od_attn.hip", "od_wide.hip", "od_layer.hip", "od_lmhead.hip"]
+SOURCES = ["od_quant.hip", "od_gemm.hip", "od_attn.hip", "od_wide.hip", "od_layer.hip", "od_lmhead.hip", "od_gdn.hip"]
 # the matrix-core ceiling probe bench.py reports beside the rooflines, in a library of its own
 PROBE_SOURCE = "od_probe.hip"
 PROBE_LIB = os.path.join(PKG, "libod_probe.so")

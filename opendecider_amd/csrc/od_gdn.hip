@@ -1,0 +1,462 @@
+// Gated DeltaNet (linear-attention) layer of the Qwen3.5 hybrid backbone, for gfx950: the three passes between the
+// layer's two W8A8 linears (in_proj, out_proj).
+//
+// Math (transformers' Qwen3_5GatedDeltaNet, which the reference runs: src/opendecider/backbone.py:256-289,
+// src/opendecider/skipkv.py:208-231; branch rows reading the shared prefix state instead of copying it,
+// docs/branched_shared_prefix_math.md:16-37). Per token of a sequence and per value head, state S in R^{dk x dv}:
+//   od_gdn_prep        y = bf16(silu(bf16(sum_j w[c, j] x[t - 3 + j, c]))) over [previous 3 inputs ; the sequence]
+//                      (depthwise causal conv, kernel 4); q, k = l2norm(y) per head in bf16 arithmetic; v = y;
+//                      beta = bf16(sigmoid(b)), g = -exp(A_log) softplus(a + dt_bias) in fp32; the sequence's last
+//                      3 inputs become its new conv state
+//   od_gdn_recurrence  S <- S e^g ; kv = S^T k ; delta = (v - kv) beta ; S <- S + k delta^T ; o = S^T (q / sqrt(dk))
+//                      (fp32), S starting from the state the sequence continues (none: zeros)
+//   od_gdn_norm_quant  bf16(bf16(w * bf16(o * rms(o))) * silu(z)) per value head (the gated RMSNorm), then the
+//                      out_proj input quantizer (optional SmoothQuant factors), per token
+// Every sum whose order torch leaves open (the conv taps, the squares of the l2norm and of the RMSNorm) is taken
+// exactly in float64 and rounded once, and the transcendental functions of the gates are evaluated in float64, so
+// od_gdn_prep and od_gdn_norm_quant give the oracle's bytes; the recurrence keeps fp32 with reductions in hardware
+// order.
+//
+// Layouts: proj bf16 [M, ldp] = [qkv (C = 2 n_k dk + n_v dv) | z (n_v dv) | b (n_v) | a (n_v)] with M = S L tokens,
+// sequence s holding tokens s L .. s L + L - 1; conv states bf16 [., 3, C]; q|k bf16 [M, 2 n_k dk]; v bf16
+// [M, n_v dv]; g, beta fp32 [M, n_v]; recurrent states fp32 [., n_v, dk, dv]; o bf16 [M, n_v dv].
+#include "od_common.h"
+
+namespace {
+
+constexpr int kConvTaps = 4;
+constexpr int kChan = 16;  // channels per thread in the row passes
+
+// ------------------------------------------------------------------------------------------------ od_gdn_prep
+struct PrepArgs {
+  const uint16_t* proj;
+  const uint16_t* conv_w;
+  const uint16_t* conv_in;
+  const int32_t* seq_state;
+  const uint16_t* A_log;
+  const uint16_t* dt_bias;
+  uint16_t* qk;
+  uint16_t* v;
+  float* g;
+  float* beta;
+  uint16_t* conv_out;
+  int64_t ldp, S, L, n_states;
+  int n_k, n_v, dk, dv, C;
+};
+
+__device__ __forceinline__ void load16(const uint16_t* p, float (&f)[kChan]) {
+  const uint4 a = *reinterpret_cast<const uint4*>(p);
+  const uint4 b = *reinterpret_cast<const uint4*>(p + 8);
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ void store16(uint16_t* p, const float (&f)[kChan]) {
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[i] = (uint32_t)od_f32_to_bf16(f[2 * i]) | ((uint32_t)od_f32_to_bf16(f[2 * i + 1]) << 16);
+  *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint4*>(p + 8) = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+__device__ __forceinline__ float bf(float x) { return od_bf16_to_f32(od_f32_to_bf16(x)); }
+
+// One workgroup per token; thread i handles channels 16 i .. 16 i + 15 (a q / k head is dk / 16 consecutive
+// threads, all in one wave).
+__global__ __launch_bounds__(1024) void gdn_prep_kernel(PrepArgs p) {
+  const int64_t m = blockIdx.x;
+  const int64_t s = m / p.L, t = m - s * p.L;
+  const int tid = threadIdx.x;
+  const int c0 = tid * kChan;
+  const bool on = c0 < p.C;
+  int64_t st = p.seq_state ? (int64_t)p.seq_state[s] : s;
+  const bool st_ok = p.conv_in != nullptr && st >= 0 && st < p.n_states;
+  const int kd = p.n_k * p.dk;
+
+  // conv inputs x[t - 3 + j] = full[t + j] over full = [state (3 rows) ; the sequence's tokens]
+  float y[kChan];
+  if (on) {
+    double acc[kChan];
+#pragma unroll
+    for (int i = 0; i < kChan; ++i) acc[i] = 0.0;
+    uint16_t wt[kChan * kConvTaps];
+#pragma unroll
+    for (int i = 0; i < kChan * kConvTaps / 8; ++i)
+      *reinterpret_cast<uint4*>(&wt[8 * i]) = *reinterpret_cast<const uint4*>(p.conv_w + (int64_t)c0 * kConvTaps + 8 * i);
+#pragma unroll
+    for (int j = 0; j < kConvTaps; ++j) {
+      const int64_t r = t + j;  // row of full
+      float x[kChan];
+      if (r >= kConvTaps - 1) {
+        load16(p.proj + (s * p.L + r - (kConvTaps - 1)) * p.ldp + c0, x);
+      } else if (st_ok) {
+        load16(p.conv_in + (st * (kConvTaps - 1) + r) * p.C + c0, x);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kChan; ++i) x[i] = 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kChan; ++i) acc[i] += (double)od_bf16_to_f32(wt[i * kConvTaps + j]) * (double)x[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kChan; ++i) y[i] = od_silu_bf16(bf((float)acc[i]));
+  } else {
+#pragma unroll
+    for (int i = 0; i < kChan; ++i) y[i] = 0.0f;
+  }
+
+  // l2norm of the q and k heads: squares rounded to bf16, their exact sum rounded to bf16, + eps, rsqrt and the
+  // product each rounded to bf16 (torch's bf16 arithmetic, with a correctly rounded rsqrt)
+  const bool qk_chan = on && c0 < 2 * kd;
+  double ss = 0.0;
+  if (qk_chan) {
+#pragma unroll
+    for (int i = 0; i < kChan; ++i) ss += (double)bf(y[i] * y[i]);
+  }
+  const int G = p.dk / kChan;  // lanes per head (a power of two <= 64)
+  for (int o = G / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, OD_WAVE);
+  if (qk_chan) {
+    const float sb = bf((float)ss);
+    const float den = bf(sb + 1e-6f);
+    const float inv = bf((float)(1.0 / sqrt((double)den)));
+#pragma unroll
+    for (int i = 0; i < kChan; ++i) y[i] = bf(y[i] * inv);
+    store16(p.qk + m * (int64_t)(2 * kd) + c0, y);
+  } else if (on) {
+    store16(p.v + m * (int64_t)(p.n_v * p.dv) + (c0 - 2 * kd), y);
+  }
+
+  // gates of the value heads
+  if (tid < p.n_v) {
+    const uint16_t* row = p.proj + m * p.ldp + p.C + (int64_t)p.n_v * p.dv;
+    const float b = od_bf16_to_f32(row[tid]), a = od_bf16_to_f32(row[p.n_v + tid]);
+    p.beta[m * p.n_v + tid] = od_sigmoid_bf16(b);
+    const float e = (float)exp((double)od_bf16_to_f32(p.A_log[tid]));
+    const float x = (float)((double)a + (double)od_bf16_to_f32(p.dt_bias[tid]));
+    const float sp = x > 20.0f ? x : (float)log1p(exp((double)x));
+    p.g[m * p.n_v + tid] = (float)(-((double)e * (double)sp));
+  }
+
+  // the new conv state: the last 3 rows of [state ; tokens]
+  if (p.conv_out && on) {
+    const int64_t keep = kConvTaps - 1;
+    if (t >= p.L - keep) {
+      float x[kChan];
+      load16(p.proj + m * p.ldp + c0, x);
+      store16(p.conv_out + (s * keep + (t - (p.L - keep))) * p.C + c0, x);
+    }
+    if (t == 0) {
+      for (int64_t j = p.L; j < keep; ++j) {  // sequences shorter than 3 keep part of the old state
+        float x[kChan];
+        if (st_ok) {
+          load16(p.conv_in + (st * keep + j) * p.C + c0, x);
+        } else {
+#pragma unroll
+          for (int i = 0; i < kChan; ++i) x[i] = 0.0f;
+        }
+        store16(p.conv_out + (s * keep + (j - p.L)) * p.C + c0, x);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ recurrence
+// One workgroup of 4 waves per (sequence, value head, 32 columns of the state); wave w owns columns 8 w .. 8 w + 7
+// of those, lane l column l / 8 and rows 16 (l % 8) .. + 15 (dk = 128), 16 fp32 state values in registers. The
+// columns of S evolve independently (column j only needs k, q, v_j, g, beta), so the waves never exchange anything;
+// the 8 lanes of a column reduce their partial dot products with DPP. The token inputs go through LDS in chunks of
+// 32 tokens, the next chunk loaded into registers while the current one is computed.
+constexpr int kRecThreads = 256;
+constexpr int kRecCols = 32;   // state columns per workgroup
+constexpr int kChunk = 32;     // tokens per staged chunk
+constexpr int kDk = 128;
+
+struct RecArgs {
+  const uint16_t* qk;
+  const uint16_t* v;
+  const float* g;
+  const float* beta;
+  const float* init;
+  const int32_t* seq_state;
+  uint16_t* o;
+  float* final_state;
+  int64_t S, L, n_states;
+  int n_k, n_v, dv;
+};
+
+struct RecSmem {
+  uint16_t q[kChunk][kDk];
+  uint16_t k[kChunk][kDk];
+  uint16_t v[kChunk][kRecCols];
+  float g[kChunk];
+  float beta[kChunk];
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+// sum over the 8 lanes of an aligned group: quads, then the two quads of a half-row (row_half_mirror)
+__device__ __forceinline__ float sum8(float x) {
+  x = dpp_add<0xB1>(x);   // quad_perm [1,0,3,2]
+  x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]
+  return dpp_add<0x141>(x);  // row_half_mirror: lane i of 8 adds lane 7 - i (the other quad's sum)
+}
+
+__global__ __launch_bounds__(kRecThreads) void gdn_recurrence_kernel(RecArgs p) {
+  __shared__ __attribute__((aligned(16))) RecSmem sm[2];
+  const int nblk = p.dv / kRecCols;
+  const int64_t bid = blockIdx.x;
+  const int cb = (int)(bid % nblk);
+  const int h = (int)((bid / nblk) % p.n_v);
+  const int64_t s = bid / ((int64_t)nblk * p.n_v);
+  const int hk = h / (p.n_v / p.n_k);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rg = lane & 7;                        // rows 16 rg .. 16 rg + 15
+  const int cl = wave * 8 + (lane >> 3);          // column within the workgroup's 32
+  const int col = cb * kRecCols + cl;             // column of the head's state
+  const int64_t kd = (int64_t)p.n_k * kDk;
+  const int64_t m0 = s * p.L;
+
+  float S[16];
+  const int64_t st = p.seq_state ? (int64_t)p.seq_state[s] : s;
+  if (p.init && st >= 0 && st < p.n_states) {
+    const float* src = p.init + ((st * p.n_v + h) * kDk + 16 * rg) * p.dv + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) S[r] = src[(int64_t)r * p.dv];
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) S[r] = 0.0f;
+  }
+  const float qscale = (float)0.08838834764831845;  // fp32(1 / sqrt(128)), as the reference scales the fp32 query
+
+  // chunk loads: thread i takes 16-byte pieces i, i + 256, ... of [q rows | k rows] (2 x 32 x 256 B), thread i < 128
+  // piece i of the v block (32 tokens x 64 B), threads 128..191 g and beta
+  uint4 rq[4];
+  uint4 rv;
+  float rgb;
+  auto gload = [&](int64_t t0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int piece = tid + i * kRecThreads;   // 0 .. 1023
+      const int isk = piece >> 9, tok = (piece >> 4) & 31, part = piece & 15;
+      const int64_t tt = t0 + tok;
+      rq[i] = tt < p.L ? *reinterpret_cast<const uint4*>(p.qk + (m0 + tt) * 2 * kd + isk * kd + (int64_t)hk * kDk +
+                                                          part * 8)
+                       : make_uint4(0, 0, 0, 0);
+    }
+    if (tid < 128) {
+      const int tok = tid >> 2, part = tid & 3;
+      const int64_t tt = t0 + tok;
+      rv = tt < p.L ? *reinterpret_cast<const uint4*>(p.v + (m0 + tt) * (int64_t)p.n_v * p.dv + (int64_t)h * p.dv +
+                                                      cb * kRecCols + part * 8)
+                    : make_uint4(0, 0, 0, 0);
+    } else if (tid < 192) {
+      const int tok = (tid - 128) & 31;
+      const int64_t tt = t0 + tok;
+      const float* src = tid < 160 ? p.g : p.beta;
+      rgb = tt < p.L ? src[(m0 + tt) * p.n_v + h] : 0.0f;
+    }
+  };
+  auto swrite = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int piece = tid + i * kRecThreads;
+      const int isk = piece >> 9, tok = (piece >> 4) & 31, part = piece & 15;
+      uint16_t* dst = isk ? &sm[buf].k[tok][part * 8] : &sm[buf].q[tok][part * 8];
+      *reinterpret_cast<uint4*>(dst) = rq[i];
+    }
+    if (tid < 128) {
+      *reinterpret_cast<uint4*>(&sm[buf].v[tid >> 2][(tid & 3) * 8]) = rv;
+    } else if (tid < 192) {
+      const int tok = (tid - 128) & 31;
+      (tid < 160 ? sm[buf].g : sm[buf].beta)[tok] = rgb;
+    }
+  };
+
+  const int64_t nchunk = (p.L + kChunk - 1) / kChunk;
+  gload(0);
+  swrite(0);
+  __syncthreads();
+  for (int64_t c = 0; c < nchunk; ++c) {
+    const int buf = (int)(c & 1);
+    const int64_t t0 = c * kChunk;
+    if (c + 1 < nchunk) gload(t0 + kChunk);
+    const int ntok = (int)min((int64_t)kChunk, p.L - t0);
+    for (int tt = 0; tt < ntok; ++tt) {
+      float kf[16], qf[16];
+      load16(&sm[buf].k[tt][16 * rg], kf);
+      load16(&sm[buf].q[tt][16 * rg], qf);
+      const float vv = od_bf16_to_f32(sm[buf].v[tt][cl]);
+      const float eg = expf(sm[buf].g[tt]);
+      const float bb = sm[buf].beta[tt];
+      float kv = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        S[r] = S[r] * eg;
+        kv = fmaf(S[r], kf[r], kv);
+      }
+      kv = sum8(kv);
+      const float delta = (vv - kv) * bb;
+      float os = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        S[r] = fmaf(kf[r], delta, S[r]);
+        os = fmaf(S[r], qf[r] * qscale, os);
+      }
+      os = sum8(os);
+      if (rg == 0) p.o[(m0 + t0 + tt) * (int64_t)p.n_v * p.dv + (int64_t)h * p.dv + col] = od_f32_to_bf16(os);
+    }
+    if (c + 1 < nchunk) {
+      __syncthreads();  // every wave is done with buffer buf ^ 1 (read in chunk c - 1)
+      swrite(buf ^ 1);
+      __syncthreads();
+    }
+  }
+  if (p.final_state) {
+    float* dst = p.final_state + ((s * p.n_v + h) * kDk + 16 * rg) * p.dv + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dst[(int64_t)r * p.dv] = S[r];
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ norm + quant
+struct NormArgs {
+  const uint16_t* o;
+  const uint16_t* z;
+  const uint16_t* w;
+  const uint16_t* inv_s;
+  int8_t* xq;
+  float* sx;
+  int64_t ldo, ldz, ldq;
+  int n_v, dv;
+  float eps;
+};
+
+// One workgroup per token; thread i handles values 16 i .. 16 i + 15 of the n_v dv outputs (a head is dv / 16
+// consecutive threads in one wave).
+__global__ __launch_bounds__(1024) void gdn_norm_quant_kernel(NormArgs p) {
+  __shared__ uint32_t red[16];
+  const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int V = p.n_v * p.dv;
+  const int c0 = tid * kChan;
+  const bool on = c0 < V;
+  float o[kChan], z[kChan];
+  if (on) {
+    load16(p.o + m * p.ldo + c0, o);
+    load16(p.z + m * p.ldz + c0, z);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kChan; ++i) o[i] = z[i] = 0.0f;
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < kChan; ++i) ss += (double)o[i] * (double)o[i];
+  const int G = p.dv / kChan;
+  for (int d = G / 2; d > 0; d >>= 1) ss += __shfl_xor(ss, d, OD_WAVE);
+  const float r = od_rms_factor(ss, p.dv, p.eps);
+  float y[kChan];
+  uint32_t amax = 0;
+#pragma unroll
+  for (int i = 0; i < kChan; ++i) {
+    const int c = c0 + i;
+    const float hn = bf(o[i] * r);
+    const float hw = bf(od_bf16_to_f32(p.w[c % p.dv]) * hn);
+    const double zd = (double)z[i];
+    const float sl = (float)(zd / (1.0 + exp(-zd)));
+    float v = bf(hw * sl);
+    if (p.inv_s) v = bf(v * od_bf16_to_f32(p.inv_s[c]));
+    y[i] = on ? v : 0.0f;
+    const uint32_t a = (__float_as_uint(y[i]) >> 16) & 0x7fffu;  // |bf16| bits: NaN patterns exceed every number
+    amax = a > amax ? a : amax;
+  }
+  amax = od_wave_umax_dpp(amax);
+  if (lane == 0) red[wave] = amax;
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t mx = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) mx = red[w] > mx ? red[w] : mx;
+    red[0] = mx;
+  }
+  __syncthreads();
+  const float scale = od_q8_scale(__uint_as_float(red[0] << 16));
+  const float inv = 1.0f / scale;
+  uint32_t wq[kChan / 4];
+  od_q8_words<kChan>(y, scale, inv, wq);
+  if (on) *reinterpret_cast<uint4*>(p.xq + m * p.ldq + c0) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+  if (tid == 0) p.sx[m] = scale;
+}
+
+int threads_for(int64_t channels) {
+  const int64_t t = (channels / kChan + 63) / 64 * 64;
+  return (int)t;
+}
+
+bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+}  // namespace
+
+extern "C" int od_gdn_prep(const uint16_t* proj, int64_t ldp, const uint16_t* conv_w, const uint16_t* conv_in,
+                           const int32_t* seq_state, int64_t n_states, const uint16_t* A_log, const uint16_t* dt_bias,
+                           int64_t S, int64_t L, int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, uint16_t* qk,
+                           uint16_t* v, float* g, float* beta, uint16_t* conv_out, od_stream_t stream) {
+  if (S < 0 || L < 0 || n_k < 1 || n_v < 1 || dk < 1 || dv < 1 || n_states < 0) return OD_ERR_SHAPE;
+  if (S == 0 || L == 0) return OD_OK;
+  if (!proj || !conv_w || !A_log || !dt_bias || !qk || !v || !g || !beta) return OD_ERR_NULL;
+  const int64_t C = 2 * n_k * dk + n_v * dv;
+  if (n_v % n_k || dk % kChan || dv % kChan || !pow2(dk / kChan) || dk / kChan > 64 || C / kChan > 1024 ||
+      n_v > C / kChan)
+    return OD_ERR_UNSUPPORTED;
+  if (ldp < C + n_v * dv + 2 * n_v) return OD_ERR_SHAPE;
+  if (ldp % 8 || !od_aligned16(proj) || !od_aligned16(conv_w) || (conv_in && !od_aligned16(conv_in)) ||
+      !od_aligned16(qk) || !od_aligned16(v) || (conv_out && !od_aligned16(conv_out)))
+    return OD_ERR_ALIGN;
+  if (S * L > 0x7fffffffll) return OD_ERR_SHAPE;
+  PrepArgs p{proj, conv_w, conv_in, seq_state, A_log, dt_bias, qk, v, g, beta, conv_out, ldp, S, L, n_states,
+             (int)n_k, (int)n_v, (int)dk, (int)dv, (int)C};
+  gdn_prep_kernel<<<dim3((unsigned)(S * L)), dim3(threads_for(C)), 0, (hipStream_t)stream>>>(p);
+  return od_launch_status();
+}
+
+extern "C" int od_gdn_recurrence(const uint16_t* qk, const uint16_t* v, const float* g, const float* beta,
+                                 const float* init, const int32_t* seq_state, int64_t n_states, int64_t S, int64_t L,
+                                 int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, uint16_t* o, float* final_state,
+                                 od_stream_t stream) {
+  if (S < 0 || L < 0 || n_k < 1 || n_v < 1 || n_states < 0) return OD_ERR_SHAPE;
+  if (S == 0 || L == 0) {
+    if (S > 0 && final_state) {
+      // an empty continuation: the final state is the initial one (zeros without init) -- not supported here
+      return OD_ERR_SHAPE;
+    }
+    return OD_OK;
+  }
+  if (!qk || !v || !g || !beta || !o) return OD_ERR_NULL;
+  if (dk != kDk || dv % kRecCols || n_v % n_k) return OD_ERR_UNSUPPORTED;
+  if (!od_aligned16(qk) || !od_aligned16(v)) return OD_ERR_ALIGN;
+  const int64_t blocks = S * n_v * (dv / kRecCols);
+  if (blocks > 0x7fffffffll) return OD_ERR_SHAPE;
+  RecArgs p{qk, v, g, beta, init, seq_state, o, final_state, S, L, n_states, (int)n_k, (int)n_v, (int)dv};
+  gdn_recurrence_kernel<<<dim3((unsigned)blocks), dim3(kRecThreads), 0, (hipStream_t)stream>>>(p);
+  return od_launch_status();
+}
+
+extern "C" int od_gdn_norm_quant(const uint16_t* o, int64_t ldo, const uint16_t* z, int64_t ldz, const uint16_t* w,
+                                 const uint16_t* inv_s, float eps, int64_t M, int64_t n_v, int64_t dv, int8_t* xq,
+                                 int64_t ldq, float* sx, od_stream_t stream) {
+  if (M < 0 || n_v < 1 || dv < 1) return OD_ERR_SHAPE;
+  if (M == 0) return OD_OK;
+  if (!o || !z || !w || !xq || !sx) return OD_ERR_NULL;
+  const int64_t V = n_v * dv;
+  if (dv % kChan || !pow2(dv / kChan) || dv / kChan > 64 || V / kChan > 1024) return OD_ERR_UNSUPPORTED;
+  if (ldo < V || ldz < V || ldq < V) return OD_ERR_SHAPE;
+  if (ldo % 8 || ldz % 8 || ldq % 16 || !od_aligned16(o) || !od_aligned16(z) || !od_aligned16(xq)) return OD_ERR_ALIGN;
+  if (M > 0x7fffffffll) return OD_ERR_SHAPE;
+  NormArgs p{o, z, w, inv_s, xq, sx, ldo, ldz, ldq, (int)n_v, (int)dv, eps};
+  gdn_norm_quant_kernel<<<dim3((unsigned)M), dim3(threads_for(V)), 0, (hipStream_t)stream>>>(p);
+  return od_launch_status();
+}

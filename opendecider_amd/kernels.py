@@ -675,3 +675,106 @@ def lm_head_logprob_q4(h: torch.Tensor, qs: torch.Tensor, d: torch.Tensor, tok: 
                                       stream_of(h)),
           "od_lm_head_logprob_q4")
     return out.view(lead)
+
+
+# ------------------------------------------------------------------------------------------- Gated DeltaNet layers
+def gdn_prep(proj: torch.Tensor, conv_w: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor, S: int, L: int,
+             n_k: int, n_v: int, dk: int, dv: int, conv_in=None, seq_state=None, conv_out: bool = False):
+    """od_gdn_prep: the conv + SiLU, l2norm and gates of a GDN layer. proj (S L, >= proj_out) bf16 with contiguous
+    rows ([qkv | z | b | a]); conv_w (C, 4) bf16; A_log, dt_bias (n_v,) bf16; conv_in (n_states, 3, C) bf16 or
+    None; seq_state int32 (S,) or None. Returns (qk (S L, 2 n_k dk), v (S L, n_v dv), g, beta (S L, n_v) fp32,
+    new conv states (S, 3, C) or None)."""
+    require_gpu(proj, conv_w, A_log, dt_bias, conv_in, seq_state, name="gdn_prep")
+    for t in (proj, conv_w, A_log, dt_bias):
+        _lib.bf16_bits(t)
+    C = 2 * n_k * dk + n_v * dv
+    M = S * L
+    if proj.shape[0] != M or proj.shape[1] < C + n_v * dv + 2 * n_v or proj.stride(1) != 1:
+        raise ValueError("gdn_prep: proj must be (S L, >= 2 n_k dk + 2 n_v dv + 2 n_v) with contiguous rows")
+    conv_w = conv_w.contiguous()
+    if conv_w.shape != (C, 4):
+        raise ValueError(f"gdn_prep: conv_w must be ({C}, 4)")
+    A_log, dt_bias = A_log.contiguous(), dt_bias.contiguous()
+    n_states = 0
+    if conv_in is not None:
+        _lib.bf16_bits(conv_in)
+        conv_in = conv_in.contiguous()
+        if conv_in.dim() != 3 or conv_in.shape[1:] != (3, C):
+            raise ValueError("gdn_prep: conv_in must be (n_states, 3, C)")
+        n_states = conv_in.shape[0]
+    if seq_state is not None:
+        if seq_state.dtype != torch.int32 or seq_state.numel() != S:
+            raise ValueError("gdn_prep: seq_state must be int32 (S,)")
+        seq_state = seq_state.contiguous()
+    dev = proj.device
+    qk = torch.empty(M, 2 * n_k * dk, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(M, n_v * dv, dtype=torch.bfloat16, device=dev)
+    g = torch.empty(M, n_v, dtype=torch.float32, device=dev)
+    beta = torch.empty(M, n_v, dtype=torch.float32, device=dev)
+    co = torch.empty(S, 3, C, dtype=torch.bfloat16, device=dev) if conv_out else None
+    check(lib().od_gdn_prep(ptr(proj), proj.stride(0) if M > 1 else proj.shape[1], ptr(conv_w), ptr(conv_in),
+                            ptr(seq_state), n_states, ptr(A_log), ptr(dt_bias), S, L, n_k, n_v, dk, dv, ptr(qk),
+                            ptr(v), ptr(g), ptr(beta), ptr(co), stream_of(proj)), "od_gdn_prep")
+    return qk, v, g, beta, co
+
+
+def gdn_recurrence(qk: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor, S: int, L: int, n_k: int,
+                   n_v: int, dk: int, dv: int, init=None, seq_state=None, final: bool | torch.Tensor = False,
+                   out=None):
+    """od_gdn_recurrence: the gated delta rule over S sequences of L tokens (inputs as gdn_prep returns them),
+    starting from init (n_states, n_v, dk, dv) fp32 through seq_state, or zeros. final: True for a new fp32 state
+    tensor (S, n_v, dk, dv), or a tensor to write it into (may be init when seq_state is None). Returns (o (S L, n_v
+    dv) bf16, the final states or None)."""
+    require_gpu(qk, v, g, beta, init, seq_state, out, name="gdn_recurrence")
+    M = S * L
+    if qk.shape != (M, 2 * n_k * dk) or v.shape != (M, n_v * dv) or g.shape != (M, n_v) or beta.shape != (M, n_v):
+        raise ValueError("gdn_recurrence: inputs do not match S, L and the head dims")
+    if g.dtype != torch.float32 or beta.dtype != torch.float32:
+        raise TypeError("gdn_recurrence: g and beta must be fp32")
+    qk, v, g, beta = qk.contiguous(), v.contiguous(), g.contiguous(), beta.contiguous()
+    n_states = 0
+    if init is not None:
+        if init.dtype != torch.float32 or init.dim() != 4 or init.shape[1:] != (n_v, dk, dv) or not init.is_contiguous():
+            raise ValueError("gdn_recurrence: init must be contiguous fp32 (n_states, n_v, dk, dv)")
+        n_states = init.shape[0]
+    if seq_state is not None:
+        if seq_state.dtype != torch.int32 or seq_state.numel() != S:
+            raise ValueError("gdn_recurrence: seq_state must be int32 (S,)")
+        seq_state = seq_state.contiguous()
+    fs = None
+    if final is True:
+        fs = torch.empty(S, n_v, dk, dv, dtype=torch.float32, device=qk.device)
+    elif isinstance(final, torch.Tensor):
+        fs = final
+        if fs.dtype != torch.float32 or fs.shape != (S, n_v, dk, dv) or not fs.is_contiguous():
+            raise ValueError("gdn_recurrence: final must be contiguous fp32 (S, n_v, dk, dv)")
+        if init is not None and fs.data_ptr() == init.data_ptr() and seq_state is not None:
+            raise ValueError("gdn_recurrence: an in-place state update needs seq_state None")
+    o = _check_out(out, (M, n_v * dv), qk.device, "gdn_recurrence")
+    check(lib().od_gdn_recurrence(ptr(qk), ptr(v), ptr(g), ptr(beta), ptr(init), ptr(seq_state), n_states, S, L, n_k,
+                                  n_v, dk, dv, ptr(o), ptr(fs), stream_of(qk)), "od_gdn_recurrence")
+    return o, fs
+
+
+def gdn_norm_quant(o: torch.Tensor, z: torch.Tensor, w: torch.Tensor, eps: float, n_v: int, dv: int, inv_s=None,
+                   xq=None, sx=None):
+    """od_gdn_norm_quant: the gated RMSNorm of o (M, n_v dv) bf16 with gate z (M, n_v dv) bf16 (a column slice of the
+    projection is fine) and weight w (dv,) bf16, then the out_proj input quantizer (inv_s (n_v dv,) bf16 or None).
+    Returns (xq int8 (M, n_v dv), sx fp32 (M,))."""
+    require_gpu(o, z, w, inv_s, xq, sx, name="gdn_norm_quant")
+    for t in (o, z, w):
+        _lib.bf16_bits(t)
+    M, V = o.shape
+    if V != n_v * dv or z.shape != (M, V):
+        raise ValueError("gdn_norm_quant: o and z must be (M, n_v dv)")
+    if o.stride(1) != 1:
+        o = o.contiguous()
+    if z.stride(1) != 1:
+        z = z.contiguous()
+    w = w.contiguous()
+    xq, sx = _quant_outputs(M, V, None, o.device, xq, sx)
+    inv_s = _vec(inv_s, V, "inv_s")
+    check(lib().od_gdn_norm_quant(ptr(o), o.stride(0) if M > 1 else V, ptr(z), z.stride(0) if M > 1 else V, ptr(w),
+                                  ptr(inv_s), eps, M, n_v, dv, ptr(xq), xq.stride(0), ptr(sx), stream_of(o)),
+          "od_gdn_norm_quant")
+    return xq, sx

@@ -1,0 +1,142 @@
+"""GPU parity of the Gated DeltaNet kernels against the oracle (oracle/gdn.py): od_gdn_prep and od_gdn_norm_quant
+bit-exact (every open-order sum is exact on both sides), od_gdn_recurrence against the float64 recurrence within
+one bf16 step per output (plus 2e-3 relative in norm) and its fp32 final state within 1e-5 relative."""
+import pytest
+import torch
+
+from oracle import gdn as og
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _bf(g, *shape, scale=1.0):
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _proj(g, M, n_k, n_v, dk, dv, pad=8):
+    C = 2 * n_k * dk + n_v * dv
+    P = C + n_v * dv + 2 * n_v
+    pad += (-(P + pad)) % 8  # rows of 16-byte multiples, as the kernel requires
+    p = _bf(g, M, P + pad)
+    p[:, C + n_v * dv:] = _bf(g, M, 2 * n_v + pad, scale=3.0)  # b and a over a wider range
+    return p
+
+
+@pytest.mark.parametrize("S,L,n_k,n_v,with_state", [(2, 5, 2, 4, False), (3, 33, 2, 4, True), (4, 1, 2, 4, True),
+                                                    (2, 2, 1, 2, True), (1, 70, 16, 32, False), (2, 24, 16, 32, True)])
+def test_gdn_prep_bit_exact(gpu_lib, S, L, n_k, n_v, with_state):
+    from opendecider_amd import kernels
+    dk = dv = 128
+    g = torch.Generator().manual_seed(S * 100 + L + n_k)
+    C = 2 * n_k * dk + n_v * dv
+    proj = _proj(g, S * L, n_k, n_v, dk, dv)
+    conv_w = _bf(g, C, 4, scale=0.3)
+    A_log = torch.log(torch.rand(n_v, generator=g) * 15.5 + 0.5).to(torch.bfloat16)
+    dt = (1 + 0.1 * torch.randn(n_v, generator=g)).to(torch.bfloat16)
+    n_states = 3
+    conv_in = _bf(g, n_states, 3, C) if with_state else None
+    seq = torch.randint(0, n_states, (S,), generator=g, dtype=torch.int32) if with_state else None
+    if with_state and S > 1:
+        seq[-1] = 7  # outside [0, n_states): reads zeros
+    print(f"gdn_prep S={S} L={L} n_k={n_k} n_v={n_v} state={with_state}", flush=True)
+    qk, v, gg, beta, co = kernels.gdn_prep(proj.to(DEV), conv_w.to(DEV), A_log.to(DEV), dt.to(DEV), S, L, n_k, n_v,
+                                           dk, dv, None if conv_in is None else conv_in.to(DEV),
+                                           None if seq is None else seq.to(DEV), conv_out=True)
+    qkv_r, z_r, b_r, a_r = og.split_proj(proj[:, :C + n_v * dv + 2 * n_v], og.GDNConfig(n_k_heads=n_k, n_v_heads=n_v))
+    cs = None
+    if with_state:
+        cs = torch.zeros(S, 3, C, dtype=torch.bfloat16)
+        for i in range(S):
+            if 0 <= int(seq[i]) < n_states:
+                cs[i] = conv_in[int(seq[i])]
+    y, new = og.conv_silu(qkv_r.reshape(S, L, C), conv_w, cs)
+    y = y.reshape(S * L, C)
+    kd = n_k * dk
+    q_r = og.l2norm_bf16(y[:, :kd].reshape(-1, n_k, dk)).reshape(-1, kd)
+    k_r = og.l2norm_bf16(y[:, kd:2 * kd].reshape(-1, n_k, dk)).reshape(-1, kd)
+    g_r, beta_r = og.gates(a_r, b_r, A_log, dt)
+    assert torch.equal(qk.cpu(), torch.cat([q_r, k_r], 1))
+    assert torch.equal(v.cpu(), y[:, 2 * kd:])
+    assert torch.equal(gg.cpu(), g_r) and torch.equal(beta.cpu(), beta_r)
+    assert torch.equal(co.cpu(), new)
+
+
+def _rec_inputs(g, S, L, n_k, n_v, dk=128, dv=128):
+    M = S * L
+    q = og.l2norm_bf16(_bf(g, M, n_k, dk))
+    k = og.l2norm_bf16(_bf(g, M, n_k, dk))
+    v = _bf(g, M, n_v, dv)
+    a, b = _bf(g, M, n_v, scale=2.0), _bf(g, M, n_v, scale=2.0)
+    A_log = torch.log(torch.rand(n_v, generator=g) * 15.5 + 0.5).to(torch.bfloat16)
+    dt = (1 + 0.1 * torch.randn(n_v, generator=g)).to(torch.bfloat16)
+    gg, beta = og.gates(a, b, A_log, dt)
+    return q, k, v, gg, beta
+
+
+@pytest.mark.parametrize("S,L,n_k,n_v,init", [(2, 1, 2, 4, False), (2, 16, 2, 4, True), (3, 70, 2, 4, True),
+                                              (1, 33, 16, 32, False), (4, 24, 16, 32, True)])
+def test_gdn_recurrence_matches_float64(gpu_lib, S, L, n_k, n_v, init):
+    from opendecider_amd import kernels
+    dk = dv = 128
+    g = torch.Generator().manual_seed(S * 1000 + L + n_v)
+    q, k, v, gg, beta = _rec_inputs(g, S, L, n_k, n_v)
+    n_states = 3
+    st0 = torch.randn(n_states, n_v, dk, dv, generator=g) * 0.5 if init else None
+    seq = torch.randint(0, n_states, (S,), generator=g, dtype=torch.int32) if init else None
+    print(f"gdn_recurrence S={S} L={L} n_k={n_k} n_v={n_v} init={init}", flush=True)
+    qk = torch.cat([q.reshape(S * L, -1), k.reshape(S * L, -1)], 1)
+    o, fs = kernels.gdn_recurrence(qk.to(DEV), v.reshape(S * L, -1).to(DEV), gg.to(DEV), beta.to(DEV), S, L, n_k,
+                                   n_v, dk, dv, None if st0 is None else st0.to(DEV),
+                                   None if seq is None else seq.to(DEV), final=True)
+    rep = n_v // n_k
+    init_r = None if st0 is None else st0[seq.long()]
+    o_r, st_r = og.recurrence(q.repeat_interleave(rep, 1).reshape(S, L, n_v, dk),
+                              k.repeat_interleave(rep, 1).reshape(S, L, n_v, dk), v.reshape(S, L, n_v, dv),
+                              gg.reshape(S, L, n_v), beta.reshape(S, L, n_v), init_r, torch.float64)
+    o_r = o_r.reshape(S * L, n_v * dv).float()
+    got = o.cpu().float()
+    d = (got - o_r).abs()
+    assert (d <= o_r.abs() * 2.0 ** -7 + 1e-6).all(), d.max().item()
+    assert (d.norm() / o_r.norm()).item() <= 2e-3
+    assert torch.allclose(fs.cpu(), st_r.float(), rtol=1e-5, atol=1e-5 * st_r.abs().max().item())
+
+
+def test_gdn_recurrence_in_place_state_and_continuation(gpu_lib):
+    """Running L1 tokens, then L2 more continuing the written state in place, equals one run over L1 + L2 tokens."""
+    from opendecider_amd import kernels
+    S, n_k, n_v, L1, L2 = 2, 2, 4, 9, 14
+    g = torch.Generator().manual_seed(5)
+    q, k, v, gg, beta = _rec_inputs(g, S, L1 + L2, n_k, n_v)
+
+    def part(lo, hi):
+        sel = lambda x: x.reshape(S, L1 + L2, *x.shape[1:])[:, lo:hi].reshape(S * (hi - lo), *x.shape[1:])
+        qk = torch.cat([sel(q).reshape(S * (hi - lo), -1), sel(k).reshape(S * (hi - lo), -1)], 1)
+        return qk.to(DEV), sel(v).reshape(S * (hi - lo), -1).to(DEV), sel(gg).to(DEV), sel(beta).to(DEV)
+
+    whole, fs_whole = kernels.gdn_recurrence(*part(0, L1 + L2), S, L1 + L2, n_k, n_v, 128, 128, final=True)
+    o1, st = kernels.gdn_recurrence(*part(0, L1), S, L1, n_k, n_v, 128, 128, final=True)
+    o2, st2 = kernels.gdn_recurrence(*part(L1, L1 + L2), S, L2, n_k, n_v, 128, 128, init=st, final=st)
+    assert st2.data_ptr() == st.data_ptr()
+    both = torch.cat([o1.reshape(S, L1, -1), o2.reshape(S, L2, -1)], 1).reshape(S * (L1 + L2), -1)
+    assert torch.equal(both, whole) and torch.equal(st2, fs_whole)
+
+
+@pytest.mark.parametrize("M,n_v,smooth", [(5, 4, False), (33, 4, True), (64, 32, True), (3, 2, False)])
+def test_gdn_norm_quant_bit_exact(gpu_lib, M, n_v, smooth):
+    from opendecider_amd import kernels
+    dv = 128
+    g = torch.Generator().manual_seed(M + n_v)
+    o = _bf(g, M, n_v * dv, scale=0.3)
+    if M > 2:
+        o[1] = 0                                               # a zero row: r = 1 / sqrt(eps)
+    zz = _bf(g, M, n_v * dv + 40, scale=2.0)[:, 24:24 + n_v * dv]   # a strided column slice, as from proj
+    w = (1 + 0.1 * torch.randn(dv, generator=g)).to(torch.bfloat16)
+    inv = (1.0 / (torch.rand(n_v * dv, generator=g) * 1.5 + 0.5)).to(torch.bfloat16) if smooth else None
+    print(f"gdn_norm_quant M={M} n_v={n_v} smooth={smooth}", flush=True)
+    zd = zz.to(DEV)
+    xq, sx = kernels.gdn_norm_quant(o.to(DEV), zd, w.to(DEV), 1e-6, n_v, dv, None if inv is None else inv.to(DEV))
+    y = og.gated_norm(o.reshape(M, n_v, dv), zz.reshape(M, n_v, dv), w, 1e-6).reshape(M, n_v * dv)
+    rq, rs = oq.act_quant(y, inv)
+    assert torch.equal(sx.cpu(), rs) and torch.equal(xq.cpu(), rq)
