@@ -21,7 +21,7 @@ from dataclasses import dataclass
 import torch
 
 from . import kernels
-from .kv_cache import Int8KVCache, StateKV
+from .kv_cache import GDNState, HybridState, Int8KVCache, StateKV
 
 
 @dataclass
@@ -36,10 +36,40 @@ class DecoderConfig:
     eps: float = 1e-6
     theta: float = 1e6
     gated: bool = False  # Qwen3.5's output gate: q_proj gives each head's q and gate (prefix_attn.py:84-85,130)
+    # The Qwen3.5 hybrid stack: with an interval n > 0, layer i is full attention when (i + 1) % n == 0 and a Gated
+    # DeltaNet (linear-attention) layer otherwise (the backbone's layer_types, src/opendecider/backbone.py:75,270);
+    # 0 keeps every layer full attention. The GDN dims are Qwen3.5's (16 key heads, 32 value heads, 128 / 128).
+    full_attention_interval: int = 0
+    lin_k_heads: int = 16
+    lin_v_heads: int = 32
+    lin_k_dim: int = 128
+    lin_v_dim: int = 128
+    conv_kernel: int = 4
 
     @property
     def qkv_out(self) -> int:
         return (self.n_heads * (2 if self.gated else 1) + 2 * self.n_kv_heads) * self.head_dim
+
+    def is_gdn(self, li: int) -> bool:
+        n = self.full_attention_interval
+        return n > 0 and (li + 1) % n != 0
+
+    @property
+    def lin_key(self) -> int:
+        return self.lin_k_heads * self.lin_k_dim
+
+    @property
+    def lin_value(self) -> int:
+        return self.lin_v_heads * self.lin_v_dim
+
+    @property
+    def lin_conv(self) -> int:
+        return 2 * self.lin_key + self.lin_value
+
+    @property
+    def lin_proj(self) -> int:
+        """The GDN input projection's rows: [qkv (lin_conv) | z (lin_value) | b (n_v) | a (n_v)]."""
+        return self.lin_conv + self.lin_value + 2 * self.lin_v_heads
 
 
 def rope_tables(cfg: DecoderConfig, n_pos: int):
@@ -86,6 +116,31 @@ def random_layer_weights(cfg: DecoderConfig, g: torch.Generator, device, smooth:
             "s_qkv": sm(H), "s_o": sm(cfg.n_heads * D), "s_gu": sm(H), "s_down": sm(F)}
 
 
+def random_gdn_layer_weights(cfg: DecoderConfig, g: torch.Generator, device, smooth: bool = True) -> dict:
+    """One Gated DeltaNet layer of random-init weights: the fused input projection [qkv | z | b | a] and out_proj
+    N(0, 0.02), conv N(0, 0.3), A = U(0.5, 16) (A_log = log A) and dt_bias ~ 1 + 0.1 N(0, 1) in bf16, the gated
+    norm's weight near 1, the MLP as in an attention layer, SmoothQuant factors U(0.5, 2) per linear input."""
+    bf = torch.bfloat16
+    H, F = cfg.hidden, cfg.ffn
+
+    def lin(n, k):
+        return (torch.randn(n, k, generator=g, device=device) * 0.02).to(bf)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
+
+    def sm(n):
+        return (torch.rand(n, generator=g, device=device) * 1.5 + 0.5) if smooth else None
+
+    A = torch.rand(cfg.lin_v_heads, generator=g, device=device) * 15.5 + 0.5
+    return {"ln1": norm(H), "ln2": norm(H), "win": lin(cfg.lin_proj, H),
+            "conv_w": (torch.randn(cfg.lin_conv, cfg.conv_kernel, generator=g, device=device) * 0.3).to(bf),
+            "A_log": torch.log(A).to(bf), "dt_bias": (1.0 + 0.1 * torch.randn(cfg.lin_v_heads, generator=g,
+                                                                            device=device)).to(bf),
+            "gnorm": norm(cfg.lin_v_dim), "wout": lin(H, cfg.lin_value), "wgu": lin(2 * F, H), "wdown": lin(H, F),
+            "s_in": sm(H), "s_out": sm(cfg.lin_value), "s_gu": sm(H), "s_down": sm(F)}
+
+
 def random_decoder(cfg: DecoderConfig, seed: int = 0, device="cuda", max_pos: int = 65536) -> "DenseDecoder":
     """A random-init decoder of `cfg` built layer by layer on the GPU (bf16 weights are quantized and dropped one
     layer at a time). The embedding is random bf16 (vocab x hidden)."""
@@ -95,8 +150,8 @@ def random_decoder(cfg: DecoderConfig, seed: int = 0, device="cuda", max_pos: in
             "head": torch.randn(H, generator=g, device=device) / H ** 0.5,
             "none_logit": torch.zeros((), device=device), "layers": []}
     dec = DenseDecoder(cfg, head, None, device, max_pos)
-    for _ in range(cfg.n_layers):
-        dec.add_layer(random_layer_weights(cfg, g, device))
+    for li in range(cfg.n_layers):
+        dec.add_layer((random_gdn_layer_weights if cfg.is_gdn(li) else random_layer_weights)(cfg, g, device))
     dec.embed = torch.randn(cfg.vocab, H, generator=g, device=device).to(torch.bfloat16)
     return dec
 
@@ -138,7 +193,11 @@ class DenseDecoder:
         return torch.cat([q_rows, kv_rows, g_rows])
 
     def add_layer(self, lw: dict) -> None:
+        if self.cfg.is_gdn(len(self.layers)):
+            self._add_gdn_layer(lw)
+            return
         L = {k: lw[k].to(self.dev) for k in ("ln1", "ln2", "q_norm", "k_norm")}
+        L["gdn"] = False
         rows = self.qkv_rows()
         wqkv = lw["wqkv"] if rows is None else lw["wqkv"][rows.to(lw["wqkv"].device)]
         L["qkv"] = QLinear(wqkv, lw.get("s_qkv"), self.dev)
@@ -148,6 +207,28 @@ class DenseDecoder:
         L["gu"] = QLinear(kernels.interleave_gate_up(lw["wgu"]), lw.get("s_gu"), self.dev)
         self.layers.append(L)
 
+    def _add_gdn_layer(self, lw: dict) -> None:
+        """A Gated DeltaNet layer: the fused input projection padded with zero rows to a multiple of 8 outputs (16-byte
+        rows for od_gdn_prep; a zero row quantizes to q = 0 and outputs 0), out_proj, the MLP."""
+        cfg = self.cfg
+        if cfg.conv_kernel != 4:
+            raise ValueError("GDN layers: the conv kernel must be 4 (Qwen3.5's)")
+        L = {k: lw[k].to(self.dev).contiguous() for k in ("ln1", "ln2", "conv_w", "A_log", "dt_bias", "gnorm")}
+        L["gdn"] = True
+        win = lw["win"]
+        pad = -win.shape[0] % 8
+        if pad:
+            win = torch.cat([win, torch.zeros(pad, win.shape[1], dtype=win.dtype, device=win.device)])
+        L["win"] = QLinear(win, lw.get("s_in"), self.dev)
+        L["wout"] = QLinear(lw["wout"], lw.get("s_out"), self.dev)
+        L["down"] = QLinear(lw["wdown"], lw.get("s_down"), self.dev)
+        L["gu"] = QLinear(kernels.interleave_gate_up(lw["wgu"]), lw.get("s_gu"), self.dev)
+        self.layers.append(L)
+
+    @property
+    def hybrid(self) -> bool:
+        return any(L["gdn"] for L in self.layers)
+
     # ---------------------------------------------------------------- buffers
     def workspace(self, M: int):
         """Activation buffers for M tokens (kept per M: a decision runs a state prefill and the option rows)."""
@@ -155,7 +236,7 @@ class DenseDecoder:
             return self._ws[M]
         cfg, d = self.cfg, self.dev
         bf = torch.bfloat16
-        kmax = max(cfg.hidden, cfg.ffn, cfg.n_heads * cfg.head_dim)
+        kmax = max(cfg.hidden, cfg.ffn, cfg.n_heads * cfg.head_dim, cfg.lin_value if self.hybrid else 0)
         self._ws[M] = {
             "M": M,
             "h": [torch.empty(M, cfg.hidden, dtype=bf, device=d) for _ in range(2)],
@@ -165,12 +246,42 @@ class DenseDecoder:
             "attn": torch.empty(M, cfg.n_heads * cfg.head_dim, dtype=bf, device=d),
             "hmlp": torch.empty(M, cfg.ffn, dtype=bf, device=d),
         }
+        if self.hybrid:  # the GDN layers' buffers: projection, conv outputs, gates, recurrence output
+            nv = cfg.lin_v_heads
+            self._ws[M].update({
+                "proj": torch.empty(M, self.layers[self._first_gdn()]["win"].out_features, dtype=bf, device=d),
+                "gqk": torch.empty(M, 2 * cfg.lin_key, dtype=bf, device=d),
+                "gv": torch.empty(M, cfg.lin_value, dtype=bf, device=d),
+                "gg": torch.empty(M, nv, dtype=torch.float32, device=d),
+                "gbeta": torch.empty(M, nv, dtype=torch.float32, device=d),
+                "go": torch.empty(M, cfg.lin_value, dtype=bf, device=d),
+            })
         return self._ws[M]
 
-    def new_state_caches(self, batch: int, capacity: int) -> StateKV:
-        """Empty per-layer (K, V) int8 caches for `batch` states of up to `capacity` tokens, in one allocation."""
+    def _first_gdn(self) -> int:
+        return next(i for i, L in enumerate(self.layers) if L["gdn"])
+
+    def new_state_caches(self, batch: int, capacity: int):
+        """Empty per-layer states for `batch` states of up to `capacity` tokens: the (K, V) int8 caches in one
+        allocation (StateKV), or for a hybrid stack a HybridState (K/V caches of the attention layers, conv and
+        recurrent states of the GDN layers)."""
         cfg = self.cfg
-        return StateKV(len(self.layers), batch, cfg.n_kv_heads, cfg.head_dim, capacity, self.dev)
+        if not self.hybrid:
+            return StateKV(len(self.layers), batch, cfg.n_kv_heads, cfg.head_dim, capacity, self.dev)
+        return HybridState([L["gdn"] for L in self.layers], batch, cfg.n_kv_heads, cfg.head_dim, capacity,
+                           cfg.lin_conv, cfg.lin_v_heads, cfg.lin_k_dim, cfg.lin_v_dim, self.dev)
+
+    @staticmethod
+    def state_length(states) -> int:
+        """Tokens held by the states (every layer holds the same number)."""
+        s0 = states[0]
+        return s0.length if isinstance(s0, GDNState) else s0[0].length
+
+    @staticmethod
+    def state_count(states) -> int:
+        """States held per layer."""
+        s0 = states[0]
+        return s0.batch if isinstance(s0, GDNState) else s0[0].q.shape[0]
 
     # ---------------------------------------------------------------- forward
     def _attn_in(self, li: int, h: torch.Tensor, ws: dict, pos: torch.Tensor, append=None) -> torch.Tensor:
@@ -210,11 +321,58 @@ class DenseDecoder:
         else:
             kernels.act_quant(ws["attn"], L["o"].inv_s, xq=xq[:, :hd], sx=sx)
         kernels.w8a8_gemm(xq[:, :hd], sx, L["o"].q, L["o"].scale, residual=h, out=h_out)
+        return self._mlp(li, h, h_out, ws)
+
+    def _mlp(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict) -> torch.Tensor:
+        """The MLP half of a layer on the mid residual h_out: RMSNorm + quantize, gate+up GEMM with SwiGLU in its
+        epilogue, quantize, down GEMM + residual (into h)."""
+        cfg, L = self.cfg, self.layers[li]
+        xq, sx = ws["xq"], ws["sx"]
         kernels.rmsnorm_quant(h_out, L["ln2"], cfg.eps, L["gu"].inv_s, xq[:, :cfg.hidden], sx)
         hm = kernels.w8a8_gemm_swiglu(xq[:, :cfg.hidden], sx, L["gu"].q, L["gu"].scale, out=ws["hmlp"])
         kernels.act_quant(hm, L["down"].inv_s, xq=xq[:, :cfg.ffn], sx=sx)
         kernels.w8a8_gemm(xq[:, :cfg.ffn], sx, L["down"].q, L["down"].scale, residual=h_out, out=h)
         return h
+
+    def gdn_layer(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict, st: GDNState, S: int, L: int,
+                  seq_state=None, prefill: bool = False, conv_tmp=None) -> torch.Tensor:
+        """One Gated DeltaNet layer over S sequences of L tokens (Qwen3_5GatedDeltaNet.forward's steps, the token
+        mixer of src/opendecider/backbone.py's linear_attention layers):
+            od_rmsnorm_quant -> od_w8a8_gemm (in_proj: [qkv | z | b | a]) -> od_gdn_prep (conv + SiLU, l2norm,
+            gates) -> od_gdn_recurrence -> od_gdn_norm_quant (gated RMSNorm + out_proj's quantizer)
+            -> od_w8a8_gemm (out_proj, + residual) -> the MLP.
+        Scoring (prefill False): sequence i is option row i and continues state seq_state[i] (int32 (S,) on the
+        GPU): its conv window starts from that state's last 3 inputs and its recurrence from that state's fp32 S0,
+        both read in place (no per-row copy of the state, docs/branched_shared_prefix_math.md:16-37); the rows are
+        terminal, nothing is written back. Prefill (prefill True, S = the states' batch): sequence i continues state
+        i (or starts from zeros when st.length is 0) and its new conv window and final recurrent state are written
+        back (the conv window through conv_tmp (S, 3, C) when continuing, since other tokens still read the old
+        one)."""
+        cfg, Ly = self.cfg, self.layers[li]
+        H, nk, nv, dk, dv = cfg.hidden, cfg.lin_k_heads, cfg.lin_v_heads, cfg.lin_k_dim, cfg.lin_v_dim
+        M = S * L
+        xq, sx = ws["xq"], ws["sx"]
+        kernels.rmsnorm_quant(h, Ly["ln1"], cfg.eps, Ly["win"].inv_s, xq[:, :H], sx)
+        proj = kernels.w8a8_gemm(xq[:, :H], sx, Ly["win"].q, Ly["win"].scale, out=ws["proj"])
+        bufs = (ws["gqk"], ws["gv"], ws["gg"], ws["gbeta"])
+        if prefill:
+            fresh = st.length == 0
+            conv_out = st.conv[:S] if fresh else conv_tmp
+            kernels.gdn_prep(proj, Ly["conv_w"], Ly["A_log"], Ly["dt_bias"], S, L, nk, nv, dk, dv,
+                             conv_in=None if fresh else st.conv, conv_out=conv_out, out=bufs)
+            kernels.gdn_recurrence(*bufs, S, L, nk, nv, dk, dv, init=None if fresh else st.rec[:S],
+                                   final=st.rec[:S], out=ws["go"])
+            if not fresh:
+                st.conv[:S].copy_(conv_tmp)
+        else:
+            kernels.gdn_prep(proj, Ly["conv_w"], Ly["A_log"], Ly["dt_bias"], S, L, nk, nv, dk, dv, conv_in=st.conv,
+                             seq_state=seq_state, out=bufs)
+            kernels.gdn_recurrence(*bufs, S, L, nk, nv, dk, dv, init=st.rec, seq_state=seq_state, out=ws["go"])
+        C, V = cfg.lin_conv, cfg.lin_value
+        kernels.gdn_norm_quant(ws["go"], proj[:, C:C + V], Ly["gnorm"], cfg.eps, nv, dv, Ly["wout"].inv_s,
+                               xq=xq[:, :V], sx=sx)
+        kernels.w8a8_gemm(xq[:, :V], sx, Ly["wout"].q, Ly["wout"].scale, residual=h, out=h_out)
+        return self._mlp(li, h, h_out, ws)
 
     def state_images(self, li: int, state_k: Int8KVCache, state_v: Int8KVCache):
         """Layer li's block images of the cached states (od_attn_stage), built once and reused by every scoring pass
@@ -272,25 +430,62 @@ class DenseDecoder:
         the same length n0). kvalid: (B, S) key mask of the new tokens (first prefill) or (B, n0) of the cached
         ones (an appended record). Returns the new tokens' final hidden states (B S, hidden)."""
         B, S = ids.shape
-        n0 = caches[0][0].length
+        n0 = self.state_length(caches)
         if n0 + S > self.cos.shape[0]:
             raise ValueError(f"positions up to {n0 + S} exceed the rotary tables ({self.cos.shape[0]})")
+        conv_tmp = None
+        if self.hybrid:
+            if kvalid is not None:
+                raise ValueError("prefill: key masks are not supported with GDN layers (every token enters the "
+                                 "recurrent state)")
+            if self.state_count(caches) != B:
+                raise ValueError(f"prefill: {B} sequences for {self.state_count(caches)} states")
+            if n0 > 0:
+                conv_tmp = self._conv_tmp(B)
         ws = self.workspace(B * S)
         h, mid = ws["h"]
         h.copy_(self.embed.index_select(0, ids.reshape(-1)))
         pos, row_start = self.prefill_layout(n0, B, S)
         for li in range(len(self.layers)):
-            self.prefill_layer(li, h, mid, ws, caches[li][0], caches[li][1], B, S, pos, kvalid, row_start)
+            if self.layers[li]["gdn"]:
+                self.gdn_layer(li, h, mid, ws, caches[li], B, S, prefill=True, conv_tmp=conv_tmp)
+            else:
+                self.prefill_layer(li, h, mid, ws, caches[li][0], caches[li][1], B, S, pos, kvalid, row_start)
+        for st in caches:
+            if isinstance(st, GDNState):
+                st.length = n0 + S
         return h
 
+    def _conv_tmp(self, B: int) -> torch.Tensor:
+        key = ("conv_tmp", B)
+        if key not in self._rows:
+            self._rows[key] = torch.empty(B, 3, self.cfg.lin_conv, dtype=torch.bfloat16, device=self.dev)
+        return self._rows[key]
+
+    def row_states(self, B: int, n_opt: int) -> torch.Tensor | None:
+        """Each option row's state index (int32 on the GPU, built once per shape) for the GDN layers; None for a
+        stack without them."""
+        if not self.hybrid:
+            return None
+        key = ("row_state", B, n_opt)
+        if key not in self._rows:
+            self._rows[key] = torch.arange(B, dtype=torch.int32).repeat_interleave(n_opt).to(self.dev)
+        return self._rows[key]
+
     def rows_forward(self, h0: torch.Tensor, states: list, R: int, t: int, pos: torch.Tensor, row_start, max_rows,
-                     kvalid=None) -> torch.Tensor:
-        """Option-row tokens h0 (M = R t, hidden) bf16 through every layer; states[l] = (K cache, V cache)."""
+                     kvalid=None, row_state=None) -> torch.Tensor:
+        """Option-row tokens h0 (M = R t, hidden) bf16 through every layer; states[l] = (K cache, V cache), or a
+        GDNState for a GDN layer (row_state: each row's state index, int32 (R,) on the GPU)."""
+        if self.hybrid and (row_state is None or kvalid is not None):
+            raise ValueError("rows_forward: GDN layers need row_state and take no key mask")
         ws = self.workspace(h0.shape[0])
         h, mid = ws["h"]
         h.copy_(h0)
         for li in range(len(self.layers)):
-            self.layer(li, h, mid, ws, states[li][0], states[li][1], R, t, pos, row_start, max_rows, kvalid)
+            if self.layers[li]["gdn"]:
+                self.gdn_layer(li, h, mid, ws, states[li], R, t, row_state)
+            else:
+                self.layer(li, h, mid, ws, states[li][0], states[li][1], R, t, pos, row_start, max_rows, kvalid)
         return h
 
     def question_pass(self, ids_q: torch.Tensor, qlen, states, group_state) -> "QuestionCache":
@@ -301,6 +496,8 @@ class DenseDecoder:
         into block images (od_attn_stage_bf16, keys past qlen[g] masked): the second prefix level the option rows
         read. Questions must be grouped by state (group_state non-decreasing)."""
         cfg = self.cfg
+        if self.hybrid:
+            raise NotImplementedError("question_pass: the question cache is built for full-attention stacks only")
         G, Lq = ids_q.shape
         gs = [int(s) for s in group_state]
         qlen = [int(n) for n in qlen]
@@ -341,6 +538,8 @@ class DenseDecoder:
         after its last real token (position T + qlen[g], v3.py:520) and attend [state group_state[g] ; question g's
         K/V] and their own tokens (od_branched_attn_staged2). Returns (G, n_opt + 1) log-probabilities."""
         cfg = self.cfg
+        if self.hybrid:
+            raise NotImplementedError("score_qcache: the question cache is built for full-attention stacks only")
         G, n_opt, t = ids_o.shape
         if G != len(qc.qlen):
             raise ValueError("score_qcache: one group of option rows per question")
@@ -397,10 +596,10 @@ class DenseDecoder:
         states. Returns (B, n_opt + 1) log-probabilities over the options and 'none'."""
         B, n_opt, t = ids.shape
         R = B * n_opt
-        T = states[0][0].length
+        T = self.state_length(states)
         h0 = self.embed.index_select(0, ids.reshape(-1))
         pos, row_start, max_rows = self.row_layout(T, B, n_opt, t)
-        h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
+        h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid, self.row_states(B, n_opt))
         return self.readout(h, B, n_opt, t, pool_last)
 
     def prefill_layout(self, n0: int, B: int, S: int):
@@ -422,17 +621,18 @@ class DenseDecoder:
         activation buffers: re-capture after the states change (append, restore)."""
         cfg = self.cfg
         R = B * n_opt
-        T = states[0][0].length
+        T = self.state_length(states)
         pos, row_start, max_rows = self.row_layout(T, B, n_opt, t)
+        row_state = self.row_states(B, n_opt)
         h0 = torch.zeros(R * t, cfg.hidden, dtype=torch.bfloat16, device=self.dev)
         side = torch.cuda.Stream(self.dev)  # warm-up off the capture: block images, module loads
         side.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(side):
-            self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
+            self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid, row_state)
         torch.cuda.current_stream(self.dev).wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid)
+            h = self.rows_forward(h0, states, R, t, pos, row_start, max_rows, kvalid, row_state)
 
         def run(ids: torch.Tensor) -> torch.Tensor:
             if tuple(ids.shape) != (B, n_opt, t):

@@ -679,11 +679,14 @@ def lm_head_logprob_q4(h: torch.Tensor, qs: torch.Tensor, d: torch.Tensor, tok: 
 
 # ------------------------------------------------------------------------------------------- Gated DeltaNet layers
 def gdn_prep(proj: torch.Tensor, conv_w: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor, S: int, L: int,
-             n_k: int, n_v: int, dk: int, dv: int, conv_in=None, seq_state=None, conv_out: bool = False):
+             n_k: int, n_v: int, dk: int, dv: int, conv_in=None, seq_state=None, conv_out: bool | torch.Tensor = False,
+             out=None):
     """od_gdn_prep: the conv + SiLU, l2norm and gates of a GDN layer. proj (S L, >= proj_out) bf16 with contiguous
     rows ([qkv | z | b | a]); conv_w (C, 4) bf16; A_log, dt_bias (n_v,) bf16; conv_in (n_states, 3, C) bf16 or
-    None; seq_state int32 (S,) or None. Returns (qk (S L, 2 n_k dk), v (S L, n_v dv), g, beta (S L, n_v) fp32,
-    new conv states (S, 3, C) or None)."""
+    None; seq_state int32 (S,) or None. conv_out: True for a new (S, 3, C) tensor of the new conv states, or a
+    contiguous tensor of that shape to write them into (not conv_in's memory: other tokens still read it). out:
+    preallocated (qk, v, g, beta). Returns (qk (S L, 2 n_k dk), v (S L, n_v dv), g, beta (S L, n_v) fp32, the new
+    conv states or None)."""
     require_gpu(proj, conv_w, A_log, dt_bias, conv_in, seq_state, name="gdn_prep")
     for t in (proj, conv_w, A_log, dt_bias):
         _lib.bf16_bits(t)
@@ -707,11 +710,29 @@ def gdn_prep(proj: torch.Tensor, conv_w: torch.Tensor, A_log: torch.Tensor, dt_b
             raise ValueError("gdn_prep: seq_state must be int32 (S,)")
         seq_state = seq_state.contiguous()
     dev = proj.device
-    qk = torch.empty(M, 2 * n_k * dk, dtype=torch.bfloat16, device=dev)
-    v = torch.empty(M, n_v * dv, dtype=torch.bfloat16, device=dev)
-    g = torch.empty(M, n_v, dtype=torch.float32, device=dev)
-    beta = torch.empty(M, n_v, dtype=torch.float32, device=dev)
-    co = torch.empty(S, 3, C, dtype=torch.bfloat16, device=dev) if conv_out else None
+    if out is None:
+        qk = torch.empty(M, 2 * n_k * dk, dtype=torch.bfloat16, device=dev)
+        v = torch.empty(M, n_v * dv, dtype=torch.bfloat16, device=dev)
+        g = torch.empty(M, n_v, dtype=torch.float32, device=dev)
+        beta = torch.empty(M, n_v, dtype=torch.float32, device=dev)
+    else:
+        qk, v, g, beta = out
+        require_gpu(qk, v, g, beta, name="gdn_prep")
+        for t, shape, dt in ((qk, (M, 2 * n_k * dk), torch.bfloat16), (v, (M, n_v * dv), torch.bfloat16),
+                             (g, (M, n_v), torch.float32), (beta, (M, n_v), torch.float32)):
+            if t.shape != shape or t.dtype != dt or not t.is_contiguous():
+                raise ValueError(f"gdn_prep: out tensors must be contiguous {shape} {dt}")
+    co = None
+    if isinstance(conv_out, torch.Tensor):
+        co = conv_out
+        require_gpu(co, name="gdn_prep")
+        if co.shape != (S, 3, C) or co.dtype != torch.bfloat16 or not co.is_contiguous():
+            raise ValueError(f"gdn_prep: conv_out must be contiguous bf16 ({S}, 3, {C})")
+        if conv_in is not None and co.data_ptr() < conv_in.data_ptr() + conv_in.numel() * 2 and \
+                conv_in.data_ptr() < co.data_ptr() + co.numel() * 2:
+            raise ValueError("gdn_prep: conv_out overlaps conv_in")
+    elif conv_out:
+        co = torch.empty(S, 3, C, dtype=torch.bfloat16, device=dev)
     check(lib().od_gdn_prep(ptr(proj), proj.stride(0) if M > 1 else proj.shape[1], ptr(conv_w), ptr(conv_in),
                             ptr(seq_state), n_states, ptr(A_log), ptr(dt_bias), S, L, n_k, n_v, dk, dv, ptr(qk),
                             ptr(v), ptr(g), ptr(beta), ptr(co), stream_of(proj)), "od_gdn_prep")

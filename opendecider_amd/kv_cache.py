@@ -112,3 +112,65 @@ class StateKV:
 
     def nbytes(self) -> int:
         return self.q.numel() + self.scale.numel() * 4
+
+
+class GDNState:
+    """A Gated DeltaNet layer's state of `batch` sequences, the counterpart of an attention layer's K/V cache (the
+    reference keeps it per row in the HF cache's conv_states / recurrent_states, src/opendecider/backbone.py:256-289,
+    529-571): conv (B, 3, C) bf16, the last 3 pre-conv inputs of the projection's qkv block, and rec (B, n_v, dk, dv)
+    fp32, the recurrent state. length counts the tokens absorbed. Option rows read these in place, one shared state
+    per request, never a per-row copy."""
+
+    def __init__(self, conv: torch.Tensor, rec: torch.Tensor):
+        self.conv, self.rec, self.length = conv, rec, 0
+
+    @property
+    def batch(self) -> int:
+        return self.conv.shape[0]
+
+
+class HybridState:
+    """Every layer's state of `batch` sequences for a hybrid stack: the attention layers' int8 K/V caches (one
+    StateKV) and the Gated DeltaNet layers' GDNState (two allocations: conv and rec of every GDN layer). Indexing by
+    layer gives a (K, V) Int8KVCache pair or a GDNState, so it stands wherever the decoder takes per-layer states."""
+
+    def __init__(self, gdn_layers: list, batch: int, n_kv_heads: int, head_dim: int, capacity: int, conv_dim: int,
+                 n_v: int, dk: int, dv: int, device):
+        n_gdn = sum(1 for g in gdn_layers if g)
+        n_attn = len(gdn_layers) - n_gdn
+        self.kv = StateKV(n_attn, batch, n_kv_heads, head_dim, capacity, device) if n_attn else None
+        self.conv = torch.zeros(n_gdn, batch, 3, conv_dim, dtype=torch.bfloat16, device=device)
+        self.rec = torch.zeros(n_gdn, batch, n_v, dk, dv, dtype=torch.float32, device=device)
+        self.items, ai, gi = [], 0, 0
+        for g in gdn_layers:
+            if g:
+                self.items.append(GDNState(self.conv[gi], self.rec[gi]))
+                gi += 1
+            else:
+                self.items.append(self.kv[ai])
+                ai += 1
+
+    def __len__(self) -> int:
+        return len(self.items)
+
+    def __getitem__(self, li):
+        return self.items[li]
+
+    def __iter__(self):
+        return iter(self.items)
+
+    @property
+    def capacity(self) -> int | None:
+        return None if self.kv is None else self.kv.capacity
+
+    @property
+    def length(self) -> int:
+        n = {it.length for it in self.items if isinstance(it, GDNState)}
+        if self.kv is not None:
+            n.add(self.kv.length)
+        if len(n) != 1:
+            raise RuntimeError(f"HybridState: layers hold different lengths {sorted(n)}")
+        return n.pop()
+
+    def nbytes(self) -> int:
+        return (0 if self.kv is None else self.kv.nbytes()) + self.conv.numel() * 2 + self.rec.numel() * 4

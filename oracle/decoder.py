@@ -32,10 +32,29 @@ class DecoderConfig:
     eps: float = 1e-6
     theta: float = 1e6
     gated: bool = False  # Qwen3.5's output gate: q_proj gives each head's q and gate (prefix_attn.py:84-85,130)
+    # Qwen3.5's hybrid stack (the backbone's layer_types, src/opendecider/backbone.py:75,270; transformers'
+    # Qwen3_5TextConfig): with an interval n > 0, layer i is full attention when (i + 1) % n == 0, a Gated DeltaNet
+    # layer otherwise (oracle/gdn.py); 0 keeps every layer full attention.
+    full_attention_interval: int = 0
+    lin_k_heads: int = 16
+    lin_v_heads: int = 32
+    lin_k_dim: int = 128
+    lin_v_dim: int = 128
+    conv_kernel: int = 4
 
     @property
     def qkv_out(self) -> int:
         return (self.n_heads * (2 if self.gated else 1) + 2 * self.n_kv_heads) * self.head_dim
+
+    def is_gdn(self, li: int) -> bool:
+        n = self.full_attention_interval
+        return n > 0 and (li + 1) % n != 0
+
+    @property
+    def gdn(self):
+        from .gdn import GDNConfig
+        return GDNConfig(hidden=self.hidden, n_k_heads=self.lin_k_heads, n_v_heads=self.lin_v_heads,
+                         dk=self.lin_k_dim, dv=self.lin_v_dim, conv=self.conv_kernel, eps=self.eps)
 
 
 def make_weights(cfg: DecoderConfig, seed: int = 0, device="cpu", layers: int | None = None, smooth: bool = True):
@@ -55,7 +74,14 @@ def make_weights(cfg: DecoderConfig, seed: int = 0, device="cpu", layers: int | 
         return (torch.rand(n, generator=g, device=device) * 1.5 + 0.5) if smooth else None
 
     out = {"layers": []}
-    for _ in range(cfg.n_layers if layers is None else layers):
+    for li in range(cfg.n_layers if layers is None else layers):
+        if cfg.is_gdn(li):  # a GDN token mixer (oracle/gdn.py) with the same norms and MLP
+            from .gdn import make_gdn_weights
+            lw = {"ln1": norm(H), "ln2": norm(H)}
+            lw.update(make_gdn_weights(cfg.gdn, g, device, smooth))
+            lw.update({"wgu": lin(2 * F, H), "wdown": lin(H, F), "s_gu": sm(H), "s_down": sm(F)})
+            out["layers"].append(lw)
+            continue
         out["layers"].append({
             "ln1": norm(H), "ln2": norm(H), "q_norm": norm(D), "k_norm": norm(D),
             "wqkv": lin(cfg.qkv_out, H), "wo": lin(H, cfg.n_heads * D), "wgu": lin(2 * F, H), "wdown": lin(H, F),
@@ -163,10 +189,10 @@ def swiglu(gu: torch.Tensor, F: int) -> torch.Tensor:
     return silu_bf16(gu[:, :F]) * gu[:, F:]
 
 
-def _layer_tail(h, attn, qlin, lw, cfg: DecoderConfig):
-    """O projection + residual, RMSNorm, gate+up, SwiGLU, down + residual (each linear W8A8 with its fused
-    activation quantizer)."""
-    q, sw, inv = qlin["wo"]
+def _layer_tail(h, attn, qlin, lw, cfg: DecoderConfig, o_proj: str = "wo"):
+    """O projection (o_proj: "wo", or a GDN layer's "wout") + residual, RMSNorm, gate+up, SwiGLU, down + residual
+    (each linear W8A8 with its fused activation quantizer)."""
+    q, sw, inv = qlin[o_proj]
     h, _, _, _ = oq.w8a8_linear(attn, q, sw, inv_s=inv, residual=h)
     x = rmsnorm(h, lw["ln2"], cfg.eps)
     q, sw, inv = qlin["wgu"]
@@ -213,14 +239,15 @@ def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: 
 
 
 def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: int = 0, kvalid=None,
-                    attn_hook=None, dequant: str = "bf16", attn_dtype=torch.float32):
+                    attn_hook=None, dequant: str = "bf16", attn_dtype=torch.float32, gdn_dtype=torch.float64):
     """State pass over S new tokens of each of B states (ids (B, S)) appended after n0 cached tokens.
     n0 = 0: causal attention among the new tokens on their bf16 K/V (exact softmax attention, the contract of the
     backbone's attention on the state, wide_attention.py:70-91). n0 > 0: the new tokens attend the cached int8 state
     (state_kv[l] = ((kq, ks), (vq, vs)) of length n0) and themselves causally, merged by LSE (one row per state,
     prefix_attn.py:43-76). Then only the new tokens' K/V are quantized per (token, head) and appended
-    (state_cache.py:79, quant.py:36-41). dequant / attn_dtype as layer_forward. Returns (h (B S, hidden) bf16, the
-    per-layer state K/V of length n0 + S)."""
+    (state_cache.py:79, quant.py:36-41). A GDN layer continues each state's conv and recurrent state (zeros at
+    n0 = 0) and returns the new ones in its slot. dequant / attn_dtype as layer_forward. Returns (h (B S, hidden)
+    bf16, the per-layer state K/V of length n0 + S, (conv, rec) for GDN layers)."""
     B, S = ids.shape
     D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     h = embed[ids.reshape(-1)]
@@ -229,6 +256,13 @@ def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: 
     out_kv = []
     for li, lw in enumerate(weights["layers"]):
         qlin = quantize_layer(lw)
+        if cfg.is_gdn(li):  # state i continues its own conv / recurrent state (or starts from zeros)
+            if kvalid is not None:
+                raise ValueError("prefill_forward: key masks are not defined for GDN layers")
+            conv, rec = (None, None) if n0 == 0 else state_kv[li]
+            h, conv, rec = gdn_layer_forward(h, lw, qlin, cfg, B, S, conv, rec, None, gdn_dtype)
+            out_kv.append((conv, rec))
+            continue
         x = rmsnorm(h, lw["ln1"], cfg.eps)
         q, sw, inv = qlin["wqkv"]
         qkv, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
@@ -259,7 +293,21 @@ def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: 
 
 
 def quantize_layer(lw):
-    return {k: quantize_linear(lw[k], lw["s_" + k[1:]]) for k in ("wqkv", "wo", "wgu", "wdown")}
+    names = ("win", "wout", "wgu", "wdown") if "win" in lw else ("wqkv", "wo", "wgu", "wdown")
+    return {k: quantize_linear(lw[k], lw["s_" + k[1:]]) for k in names}
+
+
+def gdn_layer_forward(h, lw, qlin, cfg: DecoderConfig, S: int, L: int, conv_state=None, rec_state=None,
+                      seq_state=None, dtype=torch.float64):
+    """One Gated DeltaNet layer over S sequences of L tokens (h (S L, hidden) bf16): RMSNorm, the GDN token mixer
+    (oracle/gdn.py's gdn_mixer: in_proj, conv + SiLU, l2norm, gates, gated delta rule, gated RMSNorm) continuing
+    the states conv_state / rec_state (seq_state: each sequence's state; None: sequence i continues state i; None
+    states: fresh sequences), out_proj + residual, then the MLP as in an attention layer. Returns (h, new conv states
+    (S, 3, C), new recurrent states (S, n_v, dk, dv) fp32)."""
+    from .gdn import gdn_mixer
+    x = rmsnorm(h, lw["ln1"], cfg.eps)
+    out, conv, rec = gdn_mixer(x, lw, qlin, cfg.gdn, S, L, conv_state, rec_state, seq_state, dtype)
+    return _layer_tail(h, out, qlin, lw, cfg, "wout"), conv, rec
 
 
 def readout(h, final_norm, head, none_logit, cfg: DecoderConfig, B: int, n_opt: int, t: int,
@@ -287,10 +335,12 @@ def nudge_bf16(x: torch.Tensor, frac: float, seed: int) -> torch.Tensor:
 
 def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, kvalid=None, attn_hook=None,
                      dequant: str = "bf16", attn_dtype=torch.float32, temperature: float | None = None,
-                     pool_last: int | None = None):
+                     pool_last: int | None = None, gdn_dtype=torch.float64):
     """Option-row scoring pass: ids (B, n_opt, t) token ids; state_kv[l] = ((kq, ks), (vq, vs)) per layer for the
-    B cached states of length T. dequant / attn_dtype as layer_forward, temperature as readout (None: the weights'
-    "temperature", 1 if absent). Returns (B, n_opt + 1) log-probabilities."""
+    B cached states of length T (for a GDN layer: (conv (B, 3, C) bf16, rec (B, n_v, dk, dv) fp32)). dequant /
+    attn_dtype as layer_forward, temperature as readout (None: the weights' "temperature", 1 if absent), gdn_dtype
+    the GDN recurrence's arithmetic (float64: the value an fp32 evaluation approximates). Returns (B, n_opt + 1)
+    log-probabilities."""
     if temperature is None:
         temperature = float(weights.get("temperature", 1.0))
     B, n_opt, t = ids.shape
@@ -300,6 +350,10 @@ def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, 
     cos, sin = rope_tables(cfg, T + t)
     row_state = torch.arange(B).repeat_interleave(n_opt)
     for li, lw in enumerate(weights["layers"]):
+        if cfg.is_gdn(li):  # state_kv[li] = (conv states, recurrent states); rows read their request's, in place
+            h, _, _ = gdn_layer_forward(h, lw, quantize_layer(lw), cfg, R, t, state_kv[li][0], state_kv[li][1],
+                                        row_state, gdn_dtype)
+            continue
         h = layer_forward(h, lw, quantize_layer(lw), cfg, state_kv[li][0], state_kv[li][1], R, t, pos, cos, sin,
                           row_state, kvalid, attn_hook, dequant, attn_dtype)
     return readout(h, weights["final_norm"], weights["head"], weights["none_logit"], cfg, B, n_opt, t, temperature,

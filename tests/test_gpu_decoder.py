@@ -186,6 +186,60 @@ def _setup(cfg_kw, B, n_opt, t, T):
     return cfg, w, emb, states, ids, dec, _gpu_states(states, T + 32)
 
 
+def attention_layer_stages(dec, cfg, w, li, ws, gs_li, states_li, R, t, pos, cos, sin, row_state, rs, mr):
+    """Runs attention layer li of dec on ws["h"] (in place) and checks every stage against the oracle fed the GPU's
+    own input to that stage (shared with the hybrid stack's tests)."""
+    from opendecider_amd import kernels
+    h, mid = ws["h"]
+    M = R * t
+    D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    lw, ql, L = w["layers"][li], od.quantize_layer(w["layers"][li]), dec.layers[li]
+    h_in_g = h.clone()
+    h_in = h_in_g.cpu()
+    dec.layer(li, h, mid, ws, gs_li[0], gs_li[1], R, t, pos.to(DEV, torch.int32), rs, mr)
+    qkv_g, attn_g, mid_g, hm_g, out_g = (ws["qkv"].cpu(), ws["attn"].cpu(), mid.cpu(), ws["hmlp"].cpu(), h.cpu())
+    # RMSNorm 1 + quantize, then QKV GEMM + q/k norm + RoPE from the GPU's bytes
+    xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["qkv"].inv_s)
+    _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps), ql["wqkv"][2]), f"layer {li}: ln1")
+    qkv_lin = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wqkv"][0]), sx.cpu(), ql["wqkv"][1])
+    qkv_lin, gate = od.split_qkv(qkv_lin, cfg)  # the reference's layout -> q | k | v and the gate
+    qkv = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
+    W = (Hq + 2 * Hk) * D
+    assert torch.equal(qkv_g[:, :W].view(torch.int16), qkv.view(torch.int16)), \
+        f"layer {li}: QKV GEMM + q/k norm + RoPE"
+    if cfg.gated:
+        assert torch.equal(qkv_g[:, W:].view(torch.int16), gate.view(torch.int16)), f"layer {li}: gate"
+    # attention
+    qh = qkv_g[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
+    kh = qkv_g[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
+    vh = qkv_g[:, (Hq + Hk) * D:(Hq + 2 * Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
+    (kq, ks), (vq, vs) = states_li
+    o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, None, row_state, dequant="bf16")
+    assert_close_rel(attn_g.float(), o.transpose(1, 2).reshape(M, Hq * D), what=f"layer {li}: attention")
+    # (output gate +) O projection + residual (the attention output's quantizer is bit-exact)
+    h_mid = oq.w8a8_linear(od.output_gate(attn_g, gate), *ql["wo"][:2], inv_s=ql["wo"][2], residual=h_in)[0]
+    assert torch.equal(mid_g, h_mid), f"layer {li}: O projection + residual"
+    # RMSNorm 2 + quantize, then the gate+up GEMM with SwiGLU from the GPU's bytes: the oracle's gate+up output
+    # is bit-exact to the GEMM epilogue, its SwiGLU uses the host exp (one step on bf16(silu(g)) can become two on
+    # h after the product with u), so h is held to two bf16 steps on <= 0.5%
+    xq, sx = kernels.rmsnorm_quant(mid.clone(), L["ln2"], cfg.eps, L["gu"].inv_s)
+    _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps), ql["wgu"][2]), f"layer {li}: ln2")
+    gu = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wgu"][0]), sx.cpu(), ql["wgu"][1])
+    hm = od.swiglu(gu, cfg.ffn)
+    assert torch.equal(hm_g.view(torch.int16), hm.view(torch.int16)), f"layer {li}: gate+up GEMM + SwiGLU"
+    # the same h through the unfused GPU path (gate+up GEMM in the original row order, then SwiGLU + quantize)
+    # gives the same bytes as quantizing the fused GEMM's h
+    gu_plain = kernels.w8a8_gemm(xq, sx, L["gu"].q.view(cfg.ffn, 2, -1).transpose(0, 1).reshape(2 * cfg.ffn, -1),
+                                 L["gu"].scale.view(cfg.ffn, 2).t().reshape(-1))
+    xq2, sx2 = kernels.silu_mul_quant(gu_plain, cfg.ffn, L["down"].inv_s)
+    xq, sx = kernels.act_quant(ws["hmlp"], L["down"].inv_s)
+    assert torch.equal(xq, xq2) and torch.equal(sx, sx2), f"layer {li}: fused SwiGLU vs unfused"
+    # quantize, down GEMM + residual from the GPU's bytes
+    _exact_quant(xq, sx, *oq.act_quant(hm_g, ql["wdown"][2]), f"layer {li}: SwiGLU output quantizer")
+    h_out = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wdown"][0]), sx.cpu(), ql["wdown"][1], residual=mid_g)
+    assert torch.equal(out_g, h_out), f"layer {li}: down GEMM + residual"
+
+
 @pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
 def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
     """Every stage of every layer against the oracle fed the GPU's own input to that stage: the quantizers, GEMMs
@@ -195,7 +249,6 @@ def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
     from opendecider_amd import kernels
     cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
     R, M = B * n_opt, B * n_opt * t
-    D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     pos = (T + torch.arange(t)).repeat(R)
     cos, sin = od.rope_tables(cfg, T + t + 8)
     row_state = torch.arange(B).repeat_interleave(n_opt)
@@ -204,51 +257,7 @@ def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
     h.copy_(emb[ids.reshape(-1)].to(DEV))
     rs, mr = kernels.row_start_of([n_opt] * B, DEV)
     for li in range(cfg.n_layers):
-        lw, ql, L = w["layers"][li], od.quantize_layer(w["layers"][li]), dec.layers[li]
-        h_in_g = h.clone()
-        h_in = h_in_g.cpu()
-        dec.layer(li, h, mid, ws, gs[li][0], gs[li][1], R, t, pos.to(DEV, torch.int32), rs, mr)
-        qkv_g, attn_g, mid_g, hm_g, out_g = (ws["qkv"].cpu(), ws["attn"].cpu(), mid.cpu(), ws["hmlp"].cpu(), h.cpu())
-        # RMSNorm 1 + quantize, then QKV GEMM + q/k norm + RoPE from the GPU's bytes
-        xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["qkv"].inv_s)
-        _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps), ql["wqkv"][2]), f"layer {li}: ln1")
-        qkv_lin = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wqkv"][0]), sx.cpu(), ql["wqkv"][1])
-        qkv_lin, gate = od.split_qkv(qkv_lin, cfg)  # the reference's layout -> q | k | v and the gate
-        qkv = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
-        W = (Hq + 2 * Hk) * D
-        assert torch.equal(qkv_g[:, :W].view(torch.int16), qkv.view(torch.int16)), \
-            f"layer {li}: QKV GEMM + q/k norm + RoPE"
-        if cfg.gated:
-            assert torch.equal(qkv_g[:, W:].view(torch.int16), gate.view(torch.int16)), f"layer {li}: gate"
-        # attention
-        qh = qkv_g[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
-        kh = qkv_g[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
-        vh = qkv_g[:, (Hq + Hk) * D:(Hq + 2 * Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
-        (kq, ks), (vq, vs) = states[li]
-        o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs, D ** -0.5, None, row_state, dequant="bf16")
-        assert_close_rel(attn_g.float(), o.transpose(1, 2).reshape(M, Hq * D), what=f"layer {li}: attention")
-        # (output gate +) O projection + residual (the attention output's quantizer is bit-exact)
-        h_mid = oq.w8a8_linear(od.output_gate(attn_g, gate), *ql["wo"][:2], inv_s=ql["wo"][2], residual=h_in)[0]
-        assert torch.equal(mid_g, h_mid), f"layer {li}: O projection + residual"
-        # RMSNorm 2 + quantize, then the gate+up GEMM with SwiGLU from the GPU's bytes: the oracle's gate+up output
-        # is bit-exact to the GEMM epilogue, its SwiGLU uses the host exp (one step on bf16(silu(g)) can become two on
-        # h after the product with u), so h is held to two bf16 steps on <= 0.5%
-        xq, sx = kernels.rmsnorm_quant(mid.clone(), L["ln2"], cfg.eps, L["gu"].inv_s)
-        _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps), ql["wgu"][2]), f"layer {li}: ln2")
-        gu = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wgu"][0]), sx.cpu(), ql["wgu"][1])
-        hm = od.swiglu(gu, cfg.ffn)
-        assert torch.equal(hm_g.view(torch.int16), hm.view(torch.int16)), f"layer {li}: gate+up GEMM + SwiGLU"
-        # the same h through the unfused GPU path (gate+up GEMM in the original row order, then SwiGLU + quantize)
-        # gives the same bytes as quantizing the fused GEMM's h
-        gu_plain = kernels.w8a8_gemm(xq, sx, L["gu"].q.view(cfg.ffn, 2, -1).transpose(0, 1).reshape(2 * cfg.ffn, -1),
-                                     L["gu"].scale.view(cfg.ffn, 2).t().reshape(-1))
-        xq2, sx2 = kernels.silu_mul_quant(gu_plain, cfg.ffn, L["down"].inv_s)
-        xq, sx = kernels.act_quant(ws["hmlp"], L["down"].inv_s)
-        assert torch.equal(xq, xq2) and torch.equal(sx, sx2), f"layer {li}: fused SwiGLU vs unfused"
-        # quantize, down GEMM + residual from the GPU's bytes
-        _exact_quant(xq, sx, *oq.act_quant(hm_g, ql["wdown"][2]), f"layer {li}: SwiGLU output quantizer")
-        h_out = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wdown"][0]), sx.cpu(), ql["wdown"][1], residual=mid_g)
-        assert torch.equal(out_g, h_out), f"layer {li}: down GEMM + residual"
+        attention_layer_stages(dec, cfg, w, li, ws, gs[li], states[li], R, t, pos, cos, sin, row_state, rs, mr)
     lp = dec.readout(h, B, n_opt, t)
     ref = od.readout(h.cpu(), w["final_norm"], w["head"], w["none_logit"], cfg, B, n_opt, t, T_E2E)
     assert (lp.cpu() - ref).abs().max().item() <= 1e-6, "readout"

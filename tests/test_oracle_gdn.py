@@ -138,3 +138,73 @@ def test_gated_norm_matches_qwen3_5_rmsnorm_gated():
     # the reference's fp32 rsqrt and silu are within a few ulps of the correctly rounded values the oracle uses
     d = (got.float() - ref.float()).abs()
     assert (d <= got.float().abs() * 2.0 ** -7 + 1e-30).all() and (got != ref).float().mean().item() < 0.01
+
+
+def _gdn_stack(n_layers=2, interval=0, **kw):
+    from oracle import decoder as od
+    base = dict(hidden=64, ffn=96, n_heads=2, n_kv_heads=1, head_dim=32, n_layers=n_layers, vocab=300,
+                lin_k_heads=2, lin_v_heads=4, lin_k_dim=16, lin_v_dim=8)
+    base.update(kw)
+    # interval > n_layers: every layer is a GDN layer
+    cfg = od.DecoderConfig(full_attention_interval=interval or n_layers + 1, **base)
+    return cfg, od.make_weights(cfg, seed=11), od.make_embedding(cfg, seed=11)
+
+
+def test_hybrid_layer_types_follow_qwen3_5():
+    from oracle import decoder as od
+    cfg = od.DecoderConfig(n_layers=32, full_attention_interval=4)
+    want = mq.Qwen3_5TextConfig().layer_types                    # transformers' own default stack
+    assert ["linear_attention" if cfg.is_gdn(i) else "full_attention" for i in range(32)] == want
+    assert not any(od.DecoderConfig(n_layers=8).is_gdn(i) for i in range(8))
+
+
+def test_gdn_stack_prefill_in_pieces_equals_one_prefill():
+    """A GDN-only stack: prefilling S1 tokens, then S2 more continuing the states, gives the same hidden states
+    and the same conv / recurrent states as one prefill of S1 + S2 tokens (fp32 recurrence: the same operations in
+    the same order, so bit for bit)."""
+    from oracle import decoder as od
+    cfg, w, emb = _gdn_stack()
+    g = torch.Generator().manual_seed(12)
+    ids = torch.randint(0, cfg.vocab, (2, 13), generator=g)
+    h_all, st_all = od.prefill_forward(ids, w, emb, cfg, gdn_dtype=torch.float32)
+    h1, st1 = od.prefill_forward(ids[:, :8], w, emb, cfg, gdn_dtype=torch.float32)
+    h2, st2 = od.prefill_forward(ids[:, 8:], w, emb, cfg, state_kv=st1, n0=8, gdn_dtype=torch.float32)
+    hw = h_all.reshape(2, 13, -1)
+    assert torch.equal(torch.cat([h1.reshape(2, 8, -1), h2.reshape(2, 5, -1)], 1), hw)
+    for (c, r), (ca, ra) in zip(st2, st_all):
+        assert torch.equal(c, ca) and torch.equal(r, ra)
+
+
+def test_gdn_stack_option_rows_equal_continuing_prefill():
+    """Option rows read their request's state in place: a GDN-only stack's decision forward equals the readout of
+    a prefill that continues each request's states with its option row (rows laid out one per state)."""
+    from oracle import decoder as od
+    cfg, w, emb = _gdn_stack()
+    g = torch.Generator().manual_seed(13)
+    B, n_opt, t, T = 2, 3, 5, 9
+    _, st = od.prefill_forward(torch.randint(0, cfg.vocab, (B, T), generator=g), w, emb, cfg)
+    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g)
+    lp = od.decision_forward(ids, w, emb, cfg, st, T)
+    rep = [(c.repeat_interleave(n_opt, 0), r.repeat_interleave(n_opt, 0)) for c, r in st]
+    h, _ = od.prefill_forward(ids.reshape(B * n_opt, t), w, emb, cfg, state_kv=rep, n0=T)
+    ref = od.readout(h, w["final_norm"], w["head"], w["none_logit"], cfg, B, n_opt, t)
+    assert torch.equal(lp, ref)
+
+
+def test_hybrid_option_rows_depend_on_their_own_state():
+    """In a hybrid stack (GDN, attention) each request's rows see only its own GDN state: perturbing request 1's
+    recurrent state moves request 1's probabilities and leaves request 0's bit for bit."""
+    from oracle import decoder as od
+    cfg, w, emb = _gdn_stack(interval=2)
+    assert cfg.is_gdn(0) and not cfg.is_gdn(1)
+    g = torch.Generator().manual_seed(14)
+    B, n_opt, t, T = 2, 3, 4, 7
+    _, st = od.prefill_forward(torch.randint(0, cfg.vocab, (B, T), generator=g), w, emb, cfg)
+    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g)
+    lp = od.decision_forward(ids, w, emb, cfg, st, T, temperature=1.0)
+    conv, rec = st[0]
+    rec2 = rec.clone()
+    rec2[1] += torch.randn(rec[1].shape, generator=g)   # (a uniform scale would cancel in the gated norm)
+    st2 = [(conv, rec2)] + st[1:]
+    lp2 = od.decision_forward(ids, w, emb, cfg, st2, T, temperature=1.0)
+    assert torch.equal(lp2[0], lp[0]) and not torch.equal(lp2[1], lp[1])
