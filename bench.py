@@ -79,7 +79,7 @@ def parse():
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--state", type=int, default=2048)
     ap.add_argument("--workload", choices=["scoring", "decision", "wide_choice", "gemm", "gemm_traffic",
-                                           "attention", "lm_logprob", "qcache_rows", "mfma_ceiling"],
+                                           "attention", "lm_logprob", "qcache_rows", "mfma_ceiling", "hybrid"],
                     default="scoring",
                     help="scoring (default): the metric's option-row scoring pass over cached 2048-token states; "
                          "decision: full decision forward from token ids (4 requests, 4096-token states prefilled, "
@@ -94,7 +94,8 @@ def parse():
                          "qcache_rows: decide latency with and without the question cache over the reference's "
                          "(questions, options) shapes (scripts/bench_qcache_rows.py); mfma_ceiling: what the "
                          "matrix cores sustain (int8 and bf16 MFMAs on constant, changing and LDS-fed operands, one "
-                         "8-wave workgroup per CU) with the core clock under that load")
+                         "8-wave workgroup per CU) with the core clock under that load; hybrid: the decision "
+                         "workload on the Qwen3.5 hybrid stack (32 layers, 24 Gated DeltaNet + 8 full attention)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--scoring-only", action="store_true",
                     help="the default line without its decision / wide_choice sub-objects")
@@ -179,6 +180,11 @@ class GemmTimers:
             tn, tms, ttot = t.summary()
             n, ms, tot = n + tn, ms + tms, [tot[0] + ttot[0], tot[1] + ttot[1]]
         return n, ms, tot
+
+    def reset(self):
+        self.shapes = []
+        for t in self.timers:
+            t.reset()
 
 
 def attn_work(*a):
@@ -423,6 +429,141 @@ def run_decision(args):
         "row_attention": {"kernel": ATTN_KERNELS, "tflops": fl_a / (ms_a * 1e-3) / 1e12 if n_a else 0,
                           "algorithmic_gbs": by_a / (ms_a * 1e-3) / 1e9 if n_a else 0, "launches": n_a},
         "time_share": {"gemm": ms_g / tot_ms, "state_attention": ms_w / tot_ms, "row_attention": ms_a / tot_ms},
+    }
+
+
+def gdn_prep_work(proj, ldp, conv_w, conv_in, seq_state, n_states, A_log, dt_bias, S, L, n_k, n_v, dk, dv, *rest):
+    # od_gdn_prep: the projection's qkv / b / a columns read once, q k v written bf16, g and beta fp32, the 3-row conv
+    # windows read per sequence (when continuing) and written (when asked); the taps' 4 rows hit the cache
+    M, C = S * L, 2 * n_k * dk + n_v * dv
+    conv_out = rest[4]
+    by = M * (C + 2 * n_v) * 2 + M * C * 2 + M * n_v * 8 + (S * 3 * C * 2 if conv_in else 0) + \
+        (S * 3 * C * 2 if conv_out else 0)
+    return (M * C * 9, by)
+
+
+def gdn_rec_work(qk, v, g, beta, init, seq_state, n_states, S, L, n_k, n_v, dk, dv, o, final_state, stream):
+    # od_gdn_recurrence, per token and value head: decay (dk dv), kv = S^T k (2 dk dv), the rank-1 update (2 dk dv),
+    # o = S^T q (2 dk dv); bytes: the token inputs and o once, the fp32 state read once per sequence that starts
+    # from one and written once per sequence that keeps one
+    M = S * L
+    st = n_v * dk * dv * 4
+    by = M * (2 * n_k * dk * 2 + n_v * dv * 2 + n_v * 8 + n_v * dv * 2) + (S * st if init else 0) + \
+        (S * st if final_state else 0)
+    return (7 * M * n_v * dk * dv, by)
+
+
+def gdn_norm_work(o, ldo, z, ldz, w, inv_s, eps, M, n_v, dv, *rest):
+    V = n_v * dv
+    return (M * V * 8, M * V * (2 + 2 + 1) + M * 4)
+
+
+FP32_PEAK_TFLOPS = 157.3     # MI355X fp32 (vector)
+
+
+def _rate(t, fl_peak=None):
+    n, ms, (fl, by) = t.summary()
+    out = {"launches": n, "avg_launch_us": ms / max(n, 1) * 1e3, "ms_total": ms}
+    if n:
+        out["algorithmic_gbs"] = by / (ms * 1e-3) / 1e9
+        out["frac_of_hbm"] = out["algorithmic_gbs"] / HBM_PEAK_GBS
+        if fl_peak:
+            out["tflops"] = fl / (ms * 1e-3) / 1e12
+            out["frac_of_fp32"] = out["tflops"] / fl_peak
+    return out
+
+
+def run_hybrid(args):
+    """The full decision forward on the Qwen3.5 hybrid stack: 32 layers (hidden 4096, FFN 12288), every 4th a
+    full-attention layer (32/8 heads x 128, output gate), the others Gated DeltaNet layers (16 key / 32 value heads
+    of 128, conv 4); 4 requests, each a 4096-token state of random ids prefilled (GDN layers: conv windows and
+    recurrent states; attention layers: int8 K/V), then 64 options x 24 tokens scored against it, the rows reading
+    their request's GDN states in place."""
+    import torch
+
+    from opendecider_amd import decoder as dmod
+    dev = "cuda:0"
+    cfg = dmod.DecoderConfig(n_layers=32, full_attention_interval=4, gated=True, vocab=248320)
+    B, S, n_opt, t = 4, 4096, 64, 24
+    dec = dmod.random_decoder(cfg, seed=0, device=dev, max_pos=S + t + 16)
+    g = torch.Generator(device=dev).manual_seed(3)
+    ids_state = torch.randint(0, cfg.vocab, (B, S), generator=g, device=dev)
+    ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g, device=dev)
+    st = dec.new_state_caches(B, S)
+    gemm_t = GemmTimers()
+    wide_t = AbiTimer("od_wide_attn", wide_work)
+    attn_t = AttnTimers()
+    prep_t = AbiTimer("od_gdn_prep", gdn_prep_work)
+    rec_t = AbiTimer("od_gdn_recurrence", gdn_rec_work)
+    norm_t = AbiTimer("od_gdn_norm_quant", gdn_norm_work)
+    timers = (gemm_t, wide_t, attn_t, prep_t, rec_t, norm_t)
+
+    def reset():
+        st.kv.set_length(0)
+        for it in st:
+            if isinstance(it, dmod.GDNState):
+                it.length = 0
+
+    def decide():
+        reset()
+        dec.prefill(ids_state, st)
+        return dec.score(ids, st)
+
+    for _ in range(args.warmup):
+        out = decide()
+    torch.cuda.synchronize()
+    # the scoring pass alone, over the prefilled states
+    for tm in timers:
+        tm.active = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = dec.score(ids, st)
+    torch.cuda.synchronize()
+    score_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    for tm in timers:
+        tm.active = False
+    score_rates = {"gemm": _gemm_roofline(gemm_t)[0], "row_attention": _rate(attn_t),
+                   "gdn_prep": _rate(prep_t), "gdn_recurrence": _rate(rec_t, FP32_PEAK_TFLOPS),
+                   "gdn_norm_quant": _rate(norm_t)}
+    for tm in timers:
+        tm.reset()
+    # the whole decision: prefill + scoring
+    for tm in timers:
+        tm.active = True
+    lat = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        out = decide()
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t0)
+    for tm in timers:
+        tm.active = False
+    assert torch.isfinite(out).all(), "non-finite log-probabilities"
+    lat_sorted = sorted(lat)
+    p50 = lat_sorted[len(lat) // 2]
+    roof, ms_g = _gemm_roofline(gemm_t)
+    tot_ms = sum(lat) * 1e3
+    parts = {"gemm": ms_g, "state_attention": wide_t.summary()[1], "row_attention": attn_t.summary()[1],
+             "gdn_prep": prep_t.summary()[1], "gdn_recurrence": rec_t.summary()[1],
+             "gdn_norm_quant": norm_t.summary()[1]}
+    return {
+        "metric": "decisions/sec (Qwen3.5 hybrid stack: 4096-token states prefilled from ids, 64 options x 24 "
+                  "tokens)",
+        "value": B / p50, "unit": "decisions/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": sum(lat) / len(lat) * 1e3, "p50_latency_ms": p50 * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": (f"full decision forward, hybrid stack: {B} requests, {S}-token states of random ids "
+                                f"prefilled through {cfg.n_layers} layers ({sum(cfg.is_gdn(i) for i in range(32))} "
+                                "Gated DeltaNet + 8 full attention), 64 options x 24 tokens scored, 'none' appended; "
+                                "hidden 4096, FFN 12288, random init"),
+                   "requests": B, "state_tokens": S, "options": n_opt, "tokens_per_option": t,
+                   "layers": cfg.n_layers, "full_attention_interval": 4},
+        "roofline": roof,
+        "gdn_prep": _rate(prep_t), "gdn_recurrence": _rate(rec_t, FP32_PEAK_TFLOPS),
+        "gdn_norm_quant": _rate(norm_t),
+        "state_attention": {"kernel": "od_wide_attn (causal)", **_rate(wide_t)},
+        "time_share": {k: v / tot_ms for k, v in parts.items()},
+        "scoring_pass": {"ms": score_ms, **score_rates},
     }
 
 
@@ -895,7 +1036,7 @@ def main():
         fn = {"decision": run_decision, "wide_choice": run_wide_choice, "gemm": run_gemm,
               "gemm_traffic": run_gemm_traffic, "attention": run_attention,
               "lm_logprob": run_lm_logprob, "qcache_rows": run_qcache_rows,
-              "mfma_ceiling": run_mfma_ceiling}[args.workload]
+              "mfma_ceiling": run_mfma_ceiling, "hybrid": run_hybrid}[args.workload]
         print(json.dumps(fn(args)))
         return
 

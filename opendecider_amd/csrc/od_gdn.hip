@@ -168,12 +168,22 @@ __global__ __launch_bounds__(1024) void gdn_prep_kernel(PrepArgs p) {
 // One workgroup of 4 waves per (sequence, value head, 32 columns of the state); wave w owns columns 8 w .. 8 w + 7
 // of those, lane l column l / 8 and rows 16 (l % 8) .. + 15 (dk = 128), 16 fp32 state values in registers. The
 // columns of S evolve independently (column j only needs k, q, v_j, g, beta), so the waves never exchange anything;
-// the 8 lanes of a column reduce their partial dot products with DPP. The token inputs go through LDS in chunks of
-// 32 tokens, the next chunk loaded into registers while the current one is computed.
+// the 8 lanes of a column reduce their partial dot products with DPP.
+//
+// Per token the decay multiplies the whole state by one scalar, so the state is held as S = c S' with a scalar c per
+// workgroup, and one pass over S' gives both dot products (e = e^g; c' = c e; kq = k . q~ with q~ = q / sqrt(dk)):
+//   A = S'^T k, B = S'^T q~ ; kv = c' A ; delta = (v - kv) beta ; o = c' B + kq delta ; S' += k (delta / c') ; c = c'
+// which is the reference's S <- S e^g ; kv = S^T k ; delta = (v - kv) beta ; S <- S + k delta^T ; o = S^T q~ with the
+// decay folded into c (o = (e S + k delta^T)^T q~ = e S^T q~ + (k . q~) delta): three fmas per state value and token
+// instead of a multiply and four fmas. When c' leaves [2^-64, 2^64] the state is renormalized (S' <- c' S', c' = 1),
+// so delta / c' stays finite (a zero decay factor empties the state, as e^g = 0 does). The token inputs go through LDS in
+// chunks of 16 tokens as fp32 (q pre-scaled, e^g and k . q~ computed once per token), the next chunk loaded into
+// registers while the current one is computed; the outputs of a chunk leave through LDS in 16-byte stores.
 constexpr int kRecThreads = 256;
 constexpr int kRecCols = 32;   // state columns per workgroup
-constexpr int kChunk = 32;     // tokens per staged chunk
+constexpr int kChunk = 16;     // tokens per staged chunk
 constexpr int kDk = 128;
+constexpr int kRowPad = 160;   // fp32 per staged k / q row: rows 16 g .. 16 g + 15 at 20 g (conflict-free b128 reads)
 
 struct RecArgs {
   const uint16_t* qk;
@@ -188,12 +198,11 @@ struct RecArgs {
   int n_k, n_v, dv;
 };
 
-struct RecSmem {
-  uint16_t q[kChunk][kDk];
-  uint16_t k[kChunk][kDk];
-  uint16_t v[kChunk][kRecCols];
-  float g[kChunk];
-  float beta[kChunk];
+struct RecStage {
+  float q[kChunk][kRowPad];
+  float k[kChunk][kRowPad];
+  float v[kChunk][kRecCols];
+  float4 tok[kChunk];  // (e^g, beta, k . q~, unused)
 };
 
 template <int CTRL>
@@ -206,9 +215,17 @@ __device__ __forceinline__ float sum8(float x) {
   x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]
   return dpp_add<0x141>(x);  // row_half_mirror: lane i of 8 adds lane 7 - i (the other quad's sum)
 }
+// sum over the 16 lanes of a DPP row
+__device__ __forceinline__ float sum16(float x) {
+  x = sum8(x);
+  return dpp_add<0x140>(x);  // row_mirror: lane i of 16 adds lane 15 - i (the other half-row's sum)
+}
+
+__device__ __forceinline__ int rec_pos(int r) { return 20 * (r >> 4) + (r & 15); }
 
 __global__ __launch_bounds__(kRecThreads) void gdn_recurrence_kernel(RecArgs p) {
-  __shared__ __attribute__((aligned(16))) RecSmem sm[2];
+  __shared__ __attribute__((aligned(16))) RecStage sm[2];
+  __shared__ __attribute__((aligned(16))) uint16_t ob[kChunk][kRecCols];
   const int nblk = p.dv / kRecCols;
   const int64_t bid = blockIdx.x;
   const int cb = (int)(bid % nblk);
@@ -221,8 +238,10 @@ __global__ __launch_bounds__(kRecThreads) void gdn_recurrence_kernel(RecArgs p) 
   const int col = cb * kRecCols + cl;             // column of the head's state
   const int64_t kd = (int64_t)p.n_k * kDk;
   const int64_t m0 = s * p.L;
+  const int64_t ldv = (int64_t)p.n_v * p.dv;
 
   float S[16];
+  float c = 1.0f;
   const int64_t st = p.seq_state ? (int64_t)p.seq_state[s] : s;
   if (p.init && st >= 0 && st < p.n_states) {
     const float* src = p.init + ((st * p.n_v + h) * kDk + 16 * rg) * p.dv + col;
@@ -234,47 +253,68 @@ __global__ __launch_bounds__(kRecThreads) void gdn_recurrence_kernel(RecArgs p) 
   }
   const float qscale = (float)0.08838834764831845;  // fp32(1 / sqrt(128)), as the reference scales the fp32 query
 
-  // chunk loads: thread i takes 16-byte pieces i, i + 256, ... of [q rows | k rows] (2 x 32 x 256 B), thread i < 128
-  // piece i of the v block (32 tokens x 64 B), threads 128..191 g and beta
-  uint4 rq[4];
-  uint4 rv;
-  float rgb;
+  // chunk loads: thread i takes the 8-row pieces (token i / 16, part i % 16) of q and of k; threads 0..63 the 16-byte
+  // pieces of the chunk's v block (16 tokens x 64 B), threads 64..79 g and 80..95 beta
+  uint4 rq, rk, rv;
+  float rgb = 0.0f;
+  const int ptok = tid >> 4, part = tid & 15;
   auto gload = [&](int64_t t0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int piece = tid + i * kRecThreads;   // 0 .. 1023
-      const int isk = piece >> 9, tok = (piece >> 4) & 31, part = piece & 15;
-      const int64_t tt = t0 + tok;
-      rq[i] = tt < p.L ? *reinterpret_cast<const uint4*>(p.qk + (m0 + tt) * 2 * kd + isk * kd + (int64_t)hk * kDk +
-                                                          part * 8)
-                       : make_uint4(0, 0, 0, 0);
-    }
-    if (tid < 128) {
-      const int tok = tid >> 2, part = tid & 3;
-      const int64_t tt = t0 + tok;
-      rv = tt < p.L ? *reinterpret_cast<const uint4*>(p.v + (m0 + tt) * (int64_t)p.n_v * p.dv + (int64_t)h * p.dv +
-                                                      cb * kRecCols + part * 8)
+    const int64_t tt = t0 + ptok;
+    const bool in = tt < p.L;
+    const uint16_t* src = p.qk + (m0 + tt) * 2 * kd + (int64_t)hk * kDk + part * 8;
+    rq = in ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+    rk = in ? *reinterpret_cast<const uint4*>(src + kd) : make_uint4(0, 0, 0, 0);
+    if (tid < 64) {
+      const int64_t tv = t0 + (tid >> 2);
+      rv = tv < p.L ? *reinterpret_cast<const uint4*>(p.v + (m0 + tv) * ldv + (int64_t)h * p.dv + cb * kRecCols +
+                                                      (tid & 3) * 8)
                     : make_uint4(0, 0, 0, 0);
-    } else if (tid < 192) {
-      const int tok = (tid - 128) & 31;
-      const int64_t tt = t0 + tok;
-      const float* src = tid < 160 ? p.g : p.beta;
-      rgb = tt < p.L ? src[(m0 + tt) * p.n_v + h] : 0.0f;
+    } else if (tid < 96) {
+      const int64_t tg = t0 + (tid & 15);
+      rgb = tg < p.L ? (tid < 80 ? p.g : p.beta)[(m0 + tg) * p.n_v + h] : 0.0f;
     }
   };
   auto swrite = [&](int buf) {
+    const uint32_t wq[4] = {rq.x, rq.y, rq.z, rq.w}, wk[4] = {rk.x, rk.y, rk.z, rk.w};
+    float qf[8], kf[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int piece = tid + i * kRecThreads;
-      const int isk = piece >> 9, tok = (piece >> 4) & 31, part = piece & 15;
-      uint16_t* dst = isk ? &sm[buf].k[tok][part * 8] : &sm[buf].q[tok][part * 8];
-      *reinterpret_cast<uint4*>(dst) = rq[i];
+      qf[2 * i] = __uint_as_float(wq[i] << 16) * qscale;
+      qf[2 * i + 1] = __uint_as_float(wq[i] & 0xffff0000u) * qscale;
+      kf[2 * i] = __uint_as_float(wk[i] << 16);
+      kf[2 * i + 1] = __uint_as_float(wk[i] & 0xffff0000u);
     }
-    if (tid < 128) {
-      *reinterpret_cast<uint4*>(&sm[buf].v[tid >> 2][(tid & 3) * 8]) = rv;
-    } else if (tid < 192) {
-      const int tok = (tid - 128) & 31;
-      (tid < 160 ? sm[buf].g : sm[buf].beta)[tok] = rgb;
+    float kq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kq = fmaf(kf[i], qf[i], kq);
+    kq = sum16(kq);  // the 16 parts of a token are the 16 lanes of one DPP row
+    const int pos = rec_pos(part * 8);
+    float4* dq = reinterpret_cast<float4*>(&sm[buf].q[ptok][pos]);
+    float4* dk = reinterpret_cast<float4*>(&sm[buf].k[ptok][pos]);
+    dq[0] = make_float4(qf[0], qf[1], qf[2], qf[3]);
+    dq[1] = make_float4(qf[4], qf[5], qf[6], qf[7]);
+    dk[0] = make_float4(kf[0], kf[1], kf[2], kf[3]);
+    dk[1] = make_float4(kf[4], kf[5], kf[6], kf[7]);
+    if (part == 0) sm[buf].tok[ptok].z = kq;   // every lane of the row holds the full sum
+    if (tid < 64) {
+      const uint32_t wv[4] = {rv.x, rv.y, rv.z, rv.w};
+      float4* dv = reinterpret_cast<float4*>(&sm[buf].v[tid >> 2][(tid & 3) * 8]);
+      dv[0] = make_float4(__uint_as_float(wv[0] << 16), __uint_as_float(wv[0] & 0xffff0000u),
+                          __uint_as_float(wv[1] << 16), __uint_as_float(wv[1] & 0xffff0000u));
+      dv[1] = make_float4(__uint_as_float(wv[2] << 16), __uint_as_float(wv[2] & 0xffff0000u),
+                          __uint_as_float(wv[3] << 16), __uint_as_float(wv[3] & 0xffff0000u));
+    } else if (tid < 80) {
+      sm[buf].tok[tid & 15].x = expf(rgb);
+    } else if (tid < 96) {
+      sm[buf].tok[tid & 15].y = rgb;
+    }
+  };
+  auto ostore = [&](int64_t t0) {
+    if (tid < 64) {
+      const int64_t tt = t0 + (tid >> 2);
+      if (tt < p.L)
+        *reinterpret_cast<uint4*>(p.o + (m0 + tt) * ldv + (int64_t)h * p.dv + cb * kRecCols + (tid & 3) * 8) =
+            *reinterpret_cast<const uint4*>(&ob[tid >> 2][(tid & 3) * 8]);
     }
   };
 
@@ -282,45 +322,71 @@ __global__ __launch_bounds__(kRecThreads) void gdn_recurrence_kernel(RecArgs p) 
   gload(0);
   swrite(0);
   __syncthreads();
-  for (int64_t c = 0; c < nchunk; ++c) {
-    const int buf = (int)(c & 1);
-    const int64_t t0 = c * kChunk;
-    if (c + 1 < nchunk) gload(t0 + kChunk);
+  for (int64_t ch = 0; ch < nchunk; ++ch) {
+    const int buf = (int)(ch & 1);
+    const int64_t t0 = ch * kChunk;
+    if (ch + 1 < nchunk) gload(t0 + kChunk);
     const int ntok = (int)min((int64_t)kChunk, p.L - t0);
-    for (int tt = 0; tt < ntok; ++tt) {
-      float kf[16], qf[16];
-      load16(&sm[buf].k[tt][16 * rg], kf);
-      load16(&sm[buf].q[tt][16 * rg], qf);
-      const float vv = od_bf16_to_f32(sm[buf].v[tt][cl]);
-      const float eg = expf(sm[buf].g[tt]);
-      const float bb = sm[buf].beta[tt];
-      float kv = 0.0f;
+    const RecStage& b = sm[buf];
+    // token tt's inputs are read from LDS during token tt - 1 (software pipelined)
+    float kf[16], qf[16], vv;
+    float4 ti;
+    auto lds_token = [&](int tt, float (&kd)[16], float (&qd)[16], float& vd, float4& td) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        S[r] = S[r] * eg;
-        kv = fmaf(S[r], kf[r], kv);
+      for (int i = 0; i < 4; ++i) {
+        const float4 a = *reinterpret_cast<const float4*>(&b.k[tt][20 * rg + 4 * i]);
+        const float4 e = *reinterpret_cast<const float4*>(&b.q[tt][20 * rg + 4 * i]);
+        kd[4 * i] = a.x, kd[4 * i + 1] = a.y, kd[4 * i + 2] = a.z, kd[4 * i + 3] = a.w;
+        qd[4 * i] = e.x, qd[4 * i + 1] = e.y, qd[4 * i + 2] = e.z, qd[4 * i + 3] = e.w;
       }
-      kv = sum8(kv);
-      const float delta = (vv - kv) * bb;
-      float os = 0.0f;
+      vd = b.v[tt][cl];
+      td = b.tok[tt];
+    };
+    auto step = [&](int tt, const float (&kd)[16], const float (&qd)[16], float vd, float4 td) {
+      float cn = c * td.x;
+      if (cn < 0x1p-64f || cn > 0x1p64f) {  // renormalize (c is the same in every lane: a uniform branch)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        S[r] = fmaf(kf[r], delta, S[r]);
-        os = fmaf(S[r], qf[r] * qscale, os);
+        for (int r = 0; r < 16; ++r) S[r] *= cn;
+        cn = 1.0f;
       }
-      os = sum8(os);
-      if (rg == 0) p.o[(m0 + t0 + tt) * (int64_t)p.n_v * p.dv + (int64_t)h * p.dv + col] = od_f32_to_bf16(os);
+      float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        a0 = fmaf(S[r], kd[r], a0);
+        b0 = fmaf(S[r], qd[r], b0);
+        a1 = fmaf(S[r + 1], kd[r + 1], a1);
+        b1 = fmaf(S[r + 1], qd[r + 1], b1);
+      }
+      const float A = sum8(a0 + a1), B = sum8(b0 + b1);
+      const float delta = (vd - cn * A) * td.y;
+      const float os = fmaf(cn, B, td.z * delta);
+      const float dd = delta * __builtin_amdgcn_rcpf(cn);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) S[r] = fmaf(kd[r], dd, S[r]);
+      c = cn;
+      if (rg == 0) ob[tt][cl] = od_f32_to_bf16(os);
+    };
+    // two register sets, alternating, so that no copy is needed between tokens
+    float kn[16], qn[16], vn = 0.0f;
+    float4 tn = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+    if (ntok > 0) lds_token(0, kf, qf, vv, ti);
+    for (int tt = 0; tt < ntok; tt += 2) {
+      if (tt + 1 < ntok) lds_token(tt + 1, kn, qn, vn, tn);
+      step(tt, kf, qf, vv, ti);
+      if (tt + 1 < ntok) {
+        if (tt + 2 < ntok) lds_token(tt + 2, kf, qf, vv, ti);
+        step(tt + 1, kn, qn, vn, tn);
+      }
     }
-    if (c + 1 < nchunk) {
-      __syncthreads();  // every wave is done with buffer buf ^ 1 (read in chunk c - 1)
-      swrite(buf ^ 1);
-      __syncthreads();
-    }
+    __syncthreads();  // every wave is done with buffer buf ^ 1 (read in chunk ch - 1) and has written its outputs
+    ostore(t0);
+    if (ch + 1 < nchunk) swrite(buf ^ 1);
+    __syncthreads();
   }
   if (p.final_state) {
     float* dst = p.final_state + ((s * p.n_v + h) * kDk + 16 * rg) * p.dv + col;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dst[(int64_t)r * p.dv] = S[r];
+    for (int r = 0; r < 16; ++r) dst[(int64_t)r * p.dv] = c * S[r];
   }
 }
 
@@ -437,7 +503,7 @@ extern "C" int od_gdn_recurrence(const uint16_t* qk, const uint16_t* v, const fl
   }
   if (!qk || !v || !g || !beta || !o) return OD_ERR_NULL;
   if (dk != kDk || dv % kRecCols || n_v % n_k) return OD_ERR_UNSUPPORTED;
-  if (!od_aligned16(qk) || !od_aligned16(v)) return OD_ERR_ALIGN;
+  if (!od_aligned16(qk) || !od_aligned16(v) || !od_aligned16(o)) return OD_ERR_ALIGN;
   const int64_t blocks = S * n_v * (dv / kRecCols);
   if (blocks > 0x7fffffffll) return OD_ERR_SHAPE;
   RecArgs p{qk, v, g, beta, init, seq_state, o, final_state, S, L, n_states, (int)n_k, (int)n_v, (int)dv};

@@ -104,7 +104,10 @@ def test_gdn_recurrence_matches_float64(gpu_lib, S, L, n_k, n_v, init):
 
 
 def test_gdn_recurrence_in_place_state_and_continuation(gpu_lib):
-    """Running L1 tokens, then L2 more continuing the written state in place, equals one run over L1 + L2 tokens."""
+    """Running L1 tokens, then L2 more continuing the written state in place, equals one run over L1 + L2 tokens up
+    to fp32 rounding: the kernel carries the decay as a scalar factor of the state, which the split run multiplies
+    into the state at the boundary (one more rounding), so the states agree to 1e-6 and the outputs to one bf16
+    step."""
     from opendecider_amd import kernels
     S, n_k, n_v, L1, L2 = 2, 2, 4, 9, 14
     g = torch.Generator().manual_seed(5)
@@ -119,8 +122,11 @@ def test_gdn_recurrence_in_place_state_and_continuation(gpu_lib):
     o1, st = kernels.gdn_recurrence(*part(0, L1), S, L1, n_k, n_v, 128, 128, final=True)
     o2, st2 = kernels.gdn_recurrence(*part(L1, L1 + L2), S, L2, n_k, n_v, 128, 128, init=st, final=st)
     assert st2.data_ptr() == st.data_ptr()
-    both = torch.cat([o1.reshape(S, L1, -1), o2.reshape(S, L2, -1)], 1).reshape(S * (L1 + L2), -1)
-    assert torch.equal(both, whole) and torch.equal(st2, fs_whole)
+    both = torch.cat([o1.reshape(S, L1, -1), o2.reshape(S, L2, -1)], 1).reshape(S * (L1 + L2), -1).float()
+    whole = whole.float()
+    assert ((both - whole).abs() <= whole.abs() * 2.0 ** -7 + 1e-6).all()
+    assert (both != whole).float().mean().item() < 0.01
+    assert torch.allclose(st2, fs_whole, rtol=1e-6, atol=1e-6 * fs_whole.abs().max().item())
 
 
 @pytest.mark.parametrize("M,n_v,smooth", [(5, 4, False), (33, 4, True), (64, 32, True), (3, 2, False)])
