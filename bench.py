@@ -442,9 +442,10 @@ def gdn_prep_work(proj, ldp, conv_w, conv_in, seq_state, n_states, A_log, dt_bia
     return (M * C * 9, by)
 
 
-def gdn_rec_work(qk, v, g, beta, init, seq_state, n_states, S, L, n_k, n_v, dk, dv, o, final_state, stream):
-    # od_gdn_recurrence, per token and value head: decay (dk dv), kv = S^T k (2 dk dv), the rank-1 update (2 dk dv),
-    # o = S^T q (2 dk dv); bytes: the token inputs and o once, the fp32 state read once per sequence that starts
+def gdn_rec_work(qk, v, g, beta, init, seq_state, n_states, S, L, n_k, n_v, dk, dv, o, final_state, *rest):
+    # od_gdn_recurrence(_chunked), counted as the token-by-token recurrence: per token and value head, decay (dk dv),
+    # kv = S^T k (2 dk dv), the rank-1 update (2 dk dv), o = S^T q (2 dk dv) (the chunked form does more arithmetic,
+    # on the matrix cores); bytes: the token inputs and o once, the fp32 state read once per sequence that starts
     # from one and written once per sequence that keeps one
     M = S * L
     st = n_v * dk * dv * 4
@@ -458,18 +459,14 @@ def gdn_norm_work(o, ldo, z, ldz, w, inv_s, eps, M, n_v, dv, *rest):
     return (M * V * 8, M * V * (2 + 2 + 1) + M * 4)
 
 
-FP32_PEAK_TFLOPS = 157.3     # MI355X fp32 (vector)
-
-
-def _rate(t, fl_peak=None):
+def _rate(t, flops_key=None):
     n, ms, (fl, by) = t.summary()
     out = {"launches": n, "avg_launch_us": ms / max(n, 1) * 1e3, "ms_total": ms}
     if n:
         out["algorithmic_gbs"] = by / (ms * 1e-3) / 1e9
         out["frac_of_hbm"] = out["algorithmic_gbs"] / HBM_PEAK_GBS
-        if fl_peak:
-            out["tflops"] = fl / (ms * 1e-3) / 1e12
-            out["frac_of_fp32"] = out["tflops"] / fl_peak
+        if flops_key:
+            out[flops_key] = fl / (ms * 1e-3) / 1e12
     return out
 
 
@@ -494,7 +491,7 @@ def run_hybrid(args):
     wide_t = AbiTimer("od_wide_attn", wide_work)
     attn_t = AttnTimers()
     prep_t = AbiTimer("od_gdn_prep", gdn_prep_work)
-    rec_t = AbiTimer("od_gdn_recurrence", gdn_rec_work)
+    rec_t = AbiTimer("od_gdn_recurrence_chunked", gdn_rec_work)
     norm_t = AbiTimer("od_gdn_norm_quant", gdn_norm_work)
     timers = (gemm_t, wide_t, attn_t, prep_t, rec_t, norm_t)
 
@@ -523,7 +520,7 @@ def run_hybrid(args):
     for tm in timers:
         tm.active = False
     score_rates = {"gemm": _gemm_roofline(gemm_t)[0], "row_attention": _rate(attn_t),
-                   "gdn_prep": _rate(prep_t), "gdn_recurrence": _rate(rec_t, FP32_PEAK_TFLOPS),
+                   "gdn_prep": _rate(prep_t), "gdn_recurrence": _rate(rec_t, "recurrent_equivalent_tflops"),
                    "gdn_norm_quant": _rate(norm_t)}
     for tm in timers:
         tm.reset()
@@ -559,7 +556,7 @@ def run_hybrid(args):
                    "requests": B, "state_tokens": S, "options": n_opt, "tokens_per_option": t,
                    "layers": cfg.n_layers, "full_attention_interval": 4},
         "roofline": roof,
-        "gdn_prep": _rate(prep_t), "gdn_recurrence": _rate(rec_t, FP32_PEAK_TFLOPS),
+        "gdn_prep": _rate(prep_t), "gdn_recurrence": _rate(rec_t, "recurrent_equivalent_tflops"),
         "gdn_norm_quant": _rate(norm_t),
         "state_attention": {"kernel": "od_wide_attn (causal)", **_rate(wide_t)},
         "time_share": {k: v / tot_ms for k, v in parts.items()},

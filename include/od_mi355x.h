@@ -420,6 +420,11 @@ int od_qk_norm_rope_kv_append(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, i
  * od_gdn_recurrence: qk, v, g, beta as od_gdn_prep writes them; init fp32 [n_states, n_v, dk, dv] or NULL (zeros),
  *   read through seq_state as above; writes o bf16 [M, n_v dv] and, if final_state is not NULL, fp32 [S, n_v, dk,
  *   dv] (final_state may alias init only when seq_state is NULL). dk == 128, dv % 32 == 0; L >= 1.
+ * od_gdn_recurrence_chunked: the same inputs, outputs and rules as od_gdn_recurrence, computed in chunks of 32 tokens
+ *   on bf16 MFMA (the WY form of the chunked delta rule, as torch_chunk_gated_delta_rule evaluates it; fp32 operands
+ *   split into bf16 hi + lo, fp32 accumulation): two launches, the first writing per-chunk matrices into the
+ *   caller's workspace ws (ws_floats >= what od_gdn_chunk_ws_size gives, 16-byte aligned), the second reading them
+ *   (the workspace must not be shared by calls that overlap). dv % 64 == 0.
  * od_gdn_norm_quant: o bf16 [M, ldo], z bf16 [M, ldz] (the z columns of proj), w bf16 [dv], inv_s bf16 [n_v dv] or
  *   NULL: y = bf16(bf16(w * bf16(o * r)) * silu(z)) per value head (r = 1 / sqrt(mean(o^2) + eps)), then
  *   od_act_quant's bytes and scale of y (times inv_s): xq int8 [M, ldq] (ldq % 16 == 0), sx fp32 [M].
@@ -431,6 +436,11 @@ int od_gdn_prep(const uint16_t* proj, int64_t ldp, const uint16_t* conv_w, const
 int od_gdn_recurrence(const uint16_t* qk, const uint16_t* v, const float* g, const float* beta, const float* init,
                       const int32_t* seq_state, int64_t n_states, int64_t S, int64_t L, int64_t n_k, int64_t n_v,
                       int64_t dk, int64_t dv, uint16_t* o, float* final_state, od_stream_t stream);
+int od_gdn_chunk_ws_size(int64_t S, int64_t L, int64_t n_v, int64_t* ws_floats);
+int od_gdn_recurrence_chunked(const uint16_t* qk, const uint16_t* v, const float* g, const float* beta,
+                              const float* init, const int32_t* seq_state, int64_t n_states, int64_t S, int64_t L,
+                              int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, uint16_t* o, float* final_state,
+                              float* ws, int64_t ws_floats, od_stream_t stream);
 int od_gdn_norm_quant(const uint16_t* o, int64_t ldo, const uint16_t* z, int64_t ldz, const uint16_t* w,
                       const uint16_t* inv_s, float eps, int64_t M, int64_t n_v, int64_t dv, int8_t* xq, int64_t ldq,
                       float* sx, od_stream_t stream);

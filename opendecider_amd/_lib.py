@@ -69,6 +69,9 @@ SIGNATURES = {
                           _c_ptr, _c_ptr, _c_ptr],
     "od_gdn_norm_quant": [_c_ptr, _i64, _c_ptr, _i64, _c_ptr, _c_ptr, ctypes.c_float, _i64, _i64, _i64, _c_ptr, _i64,
                           _c_ptr, _c_ptr],
+    "od_gdn_chunk_ws_size": [_i64, _i64, _i64, _c_ptr],
+    "od_gdn_recurrence_chunked": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64,
+                                  _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr],
     "od_lm_head_logprob_ws": [_i64, _i64, _c_ptr],
     "od_lm_head_logprob": [_c_ptr, _i64, _c_ptr, _i64, ctypes.c_int, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64,
                            _c_ptr, _c_ptr, _i64, _c_ptr],

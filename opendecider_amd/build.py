@@ -22,10 +22,14 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libod_mi355x.so")
-SOURCES = ["od_quant.hip", "od_gemm.hip", "od_attn.hip", "od_wide.hip", "od_layer.hip", "od_lmhead.hip", "od_gdn.hip"]
+SOURCES = ["od_quant.hip", "od_gemm.hip", "od_attn.hip", "od_wide.hip", "od_layer.hip", "od_lmhead.hip", "od_gdn.hip",
+           "od_gdn_chunk.hip"]
 # the matrix-core ceiling probe bench.py reports beside the rooflines, in a library of its own
 PROBE_SOURCE = "od_probe.hip"
 PROBE_LIB = os.path.join(PKG, "libod_probe.so")
+# per-source flags: the chunked GDN kernel feeds its MFMA accumulators to vector ALU work every step, so they are
+# kept in ordinary VGPRs (no accumulator-register copies)
+SOURCE_FLAGS = {"od_gdn_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-inline-asm"]
@@ -45,7 +49,8 @@ def build(verbose: bool = False) -> str:
     libod_mi355x.so."""
     os.makedirs(BUILD, exist_ok=True)
     objs = [os.path.join(BUILD, s.replace(".hip", ".o")) for s in SOURCES]
-    cmds = [[HIPCC, *FLAGS, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    cmds = [[HIPCC, *FLAGS, *SOURCE_FLAGS.get(s, []), "-c", os.path.join(CSRC, s), "-o", o]
+            for s, o in zip(SOURCES, objs)]
     probe_obj = os.path.join(BUILD, PROBE_SOURCE.replace(".hip", ".o"))
     cmds.append([HIPCC, *FLAGS, "-c", os.path.join(CSRC, PROBE_SOURCE), "-o", probe_obj])
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:

@@ -739,13 +739,28 @@ def gdn_prep(proj: torch.Tensor, conv_w: torch.Tensor, A_log: torch.Tensor, dt_b
     return qk, v, g, beta, co
 
 
+_GDN_WS: dict = {}
+
+
+def gdn_chunk_workspace_floats(S: int, L: int, n_v: int) -> int:
+    key = (S, L, n_v)
+    n = _GDN_WS.get(key)
+    if n is None:
+        v = ctypes.c_int64(0)
+        check(lib().od_gdn_chunk_ws_size(S, L, n_v, ctypes.byref(v)), "od_gdn_chunk_ws_size")
+        n = _GDN_WS[key] = v.value
+    return n
+
+
 def gdn_recurrence(qk: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor, S: int, L: int, n_k: int,
                    n_v: int, dk: int, dv: int, init=None, seq_state=None, final: bool | torch.Tensor = False,
-                   out=None):
-    """od_gdn_recurrence: the gated delta rule over S sequences of L tokens (inputs as gdn_prep returns them),
-    starting from init (n_states, n_v, dk, dv) fp32 through seq_state, or zeros. final: True for a new fp32 state
-    tensor (S, n_v, dk, dv), or a tensor to write it into (may be init when seq_state is None). Returns (o (S L, n_v
-    dv) bf16, the final states or None)."""
+                   out=None, chunked: bool = True):
+    """The gated delta rule over S sequences of L tokens (inputs as gdn_prep returns them), starting from init
+    (n_states, n_v, dk, dv) fp32 through seq_state, or zeros. final: True for a new fp32 state tensor (S, n_v, dk,
+    dv), or a tensor to write it into (may be init when seq_state is None). chunked: od_gdn_recurrence_chunked (the
+    chunked form on bf16 MFMA, dv a multiple of 64, with a workspace from the caching allocator) where it applies,
+    else od_gdn_recurrence (token by token on the vector ALUs). Returns (o (S L, n_v dv) bf16, the final states or
+    None)."""
     require_gpu(qk, v, g, beta, init, seq_state, out, name="gdn_recurrence")
     M = S * L
     if qk.shape != (M, 2 * n_k * dk) or v.shape != (M, n_v * dv) or g.shape != (M, n_v) or beta.shape != (M, n_v):
@@ -772,6 +787,12 @@ def gdn_recurrence(qk: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: tor
         if init is not None and fs.data_ptr() == init.data_ptr() and seq_state is not None:
             raise ValueError("gdn_recurrence: an in-place state update needs seq_state None")
     o = _check_out(out, (M, n_v * dv), qk.device, "gdn_recurrence")
+    if chunked and dk == 128 and dv % 64 == 0 and M > 0:
+        ws = torch.empty(gdn_chunk_workspace_floats(S, L, n_v), dtype=torch.float32, device=qk.device)
+        check(lib().od_gdn_recurrence_chunked(ptr(qk), ptr(v), ptr(g), ptr(beta), ptr(init), ptr(seq_state), n_states,
+                                              S, L, n_k, n_v, dk, dv, ptr(o), ptr(fs), ptr(ws), ws.numel(),
+                                              stream_of(qk)), "od_gdn_recurrence_chunked")
+        return o, fs
     check(lib().od_gdn_recurrence(ptr(qk), ptr(v), ptr(g), ptr(beta), ptr(init), ptr(seq_state), n_states, S, L, n_k,
                                   n_v, dk, dv, ptr(o), ptr(fs), stream_of(qk)), "od_gdn_recurrence")
     return o, fs

@@ -75,21 +75,27 @@ def _rec_inputs(g, S, L, n_k, n_v, dk=128, dv=128):
     return q, k, v, gg, beta
 
 
-@pytest.mark.parametrize("S,L,n_k,n_v,init", [(2, 1, 2, 4, False), (2, 16, 2, 4, True), (3, 70, 2, 4, True),
-                                              (1, 33, 16, 32, False), (4, 24, 16, 32, True)])
-def test_gdn_recurrence_matches_float64(gpu_lib, S, L, n_k, n_v, init):
+@pytest.mark.parametrize("chunked", [True, False])
+@pytest.mark.parametrize("S,L,n_k,n_v,init,gmul", [(2, 1, 2, 4, False, 1), (2, 16, 2, 4, True, 1),
+                                                   (3, 70, 2, 4, True, 1), (1, 33, 16, 32, False, 1),
+                                                   (4, 24, 16, 32, True, 1), (2, 300, 2, 4, True, 1),
+                                                   (2, 64, 2, 4, True, 40), (2, 96, 2, 4, True, 0.01)])
+def test_gdn_recurrence_matches_float64(gpu_lib, S, L, n_k, n_v, init, gmul, chunked):
+    """Both forms (the chunked one on bf16 MFMA, and token by token) against the float64 recurrence; gmul scales the
+    log-decays (x40: most of the state vanishes within a token; x0.01: almost no decay over the sequence)."""
     from opendecider_amd import kernels
     dk = dv = 128
     g = torch.Generator().manual_seed(S * 1000 + L + n_v)
     q, k, v, gg, beta = _rec_inputs(g, S, L, n_k, n_v)
+    gg = gg * gmul
     n_states = 3
     st0 = torch.randn(n_states, n_v, dk, dv, generator=g) * 0.5 if init else None
     seq = torch.randint(0, n_states, (S,), generator=g, dtype=torch.int32) if init else None
-    print(f"gdn_recurrence S={S} L={L} n_k={n_k} n_v={n_v} init={init}", flush=True)
+    print(f"gdn_recurrence S={S} L={L} n_k={n_k} n_v={n_v} init={init} gmul={gmul} chunked={chunked}", flush=True)
     qk = torch.cat([q.reshape(S * L, -1), k.reshape(S * L, -1)], 1)
     o, fs = kernels.gdn_recurrence(qk.to(DEV), v.reshape(S * L, -1).to(DEV), gg.to(DEV), beta.to(DEV), S, L, n_k,
                                    n_v, dk, dv, None if st0 is None else st0.to(DEV),
-                                   None if seq is None else seq.to(DEV), final=True)
+                                   None if seq is None else seq.to(DEV), final=True, chunked=chunked)
     rep = n_v // n_k
     init_r = None if st0 is None else st0[seq.long()]
     o_r, st_r = og.recurrence(q.repeat_interleave(rep, 1).reshape(S, L, n_v, dk),
@@ -103,13 +109,13 @@ def test_gdn_recurrence_matches_float64(gpu_lib, S, L, n_k, n_v, init):
     assert torch.allclose(fs.cpu(), st_r.float(), rtol=1e-5, atol=1e-5 * st_r.abs().max().item())
 
 
-def test_gdn_recurrence_in_place_state_and_continuation(gpu_lib):
+@pytest.mark.parametrize("chunked", [True, False])
+def test_gdn_recurrence_in_place_state_and_continuation(gpu_lib, chunked):
     """Running L1 tokens, then L2 more continuing the written state in place, equals one run over L1 + L2 tokens up
-    to fp32 rounding: the kernel carries the decay as a scalar factor of the state, which the split run multiplies
-    into the state at the boundary (one more rounding), so the states agree to 1e-6 and the outputs to one bf16
-    step."""
+    to rounding: the split moves the chunk boundaries (and the token-by-token form's scalar decay factor is
+    multiplied into the state there), so the states agree to 1e-5 and the outputs to one bf16 step."""
     from opendecider_amd import kernels
-    S, n_k, n_v, L1, L2 = 2, 2, 4, 9, 14
+    S, n_k, n_v, L1, L2 = 2, 2, 4, 45, 50
     g = torch.Generator().manual_seed(5)
     q, k, v, gg, beta = _rec_inputs(g, S, L1 + L2, n_k, n_v)
 
@@ -118,15 +124,17 @@ def test_gdn_recurrence_in_place_state_and_continuation(gpu_lib):
         qk = torch.cat([sel(q).reshape(S * (hi - lo), -1), sel(k).reshape(S * (hi - lo), -1)], 1)
         return qk.to(DEV), sel(v).reshape(S * (hi - lo), -1).to(DEV), sel(gg).to(DEV), sel(beta).to(DEV)
 
-    whole, fs_whole = kernels.gdn_recurrence(*part(0, L1 + L2), S, L1 + L2, n_k, n_v, 128, 128, final=True)
-    o1, st = kernels.gdn_recurrence(*part(0, L1), S, L1, n_k, n_v, 128, 128, final=True)
-    o2, st2 = kernels.gdn_recurrence(*part(L1, L1 + L2), S, L2, n_k, n_v, 128, 128, init=st, final=st)
+    whole, fs_whole = kernels.gdn_recurrence(*part(0, L1 + L2), S, L1 + L2, n_k, n_v, 128, 128, final=True,
+                                             chunked=chunked)
+    o1, st = kernels.gdn_recurrence(*part(0, L1), S, L1, n_k, n_v, 128, 128, final=True, chunked=chunked)
+    o2, st2 = kernels.gdn_recurrence(*part(L1, L1 + L2), S, L2, n_k, n_v, 128, 128, init=st, final=st,
+                                     chunked=chunked)
     assert st2.data_ptr() == st.data_ptr()
     both = torch.cat([o1.reshape(S, L1, -1), o2.reshape(S, L2, -1)], 1).reshape(S * (L1 + L2), -1).float()
     whole = whole.float()
     assert ((both - whole).abs() <= whole.abs() * 2.0 ** -7 + 1e-6).all()
     assert (both != whole).float().mean().item() < 0.01
-    assert torch.allclose(st2, fs_whole, rtol=1e-6, atol=1e-6 * fs_whole.abs().max().item())
+    assert torch.allclose(st2, fs_whole, rtol=1e-5, atol=1e-5 * fs_whole.abs().max().item())
 
 
 @pytest.mark.parametrize("M,n_v,smooth", [(5, 4, False), (33, 4, True), (64, 32, True), (3, 2, False)])
