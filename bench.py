@@ -9,14 +9,16 @@ W8A8 gate+up GEMM, SwiGLU+quantize, W8A8 down GEMM (+residual). The states' K/V 
 quantized by the append kernel) and resident in HBM before timing; so are the option token ids.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--scoring-only]
-                    [--workload scoring|decision|wide_choice|gemm|gemm_traffic|attention|lm_logprob]
+                    [--workload scoring|decision|wide_choice|gemm|gemm_traffic|attention|lm_logprob|
+                                qcache_rows|mfma_ceiling|hybrid]
 
 Prints ONE JSON line: metric / value (decisions/s) / timing, the roofline of the dominant kernel (the W8A8 GEMM,
 int8 MFMA), the branched attention's figures, and a CPU baseline (the oracle, on this host's cores, on a bounded
 sample of the same workload, scaled). The default line also carries the full decision forward from token ids
-("decision": 4096-token states prefilled, 64 options x 24 tokens) and the wide-choice growing state ("wide_choice":
-a 32768-token int8 state + 256-token records, 2 x 255 options x 12 tokens), each with its own CPU baseline
-(--scoring-only leaves them out).
+("decision": 4096-token states prefilled, 64 options x 24 tokens), the wide-choice growing state ("wide_choice":
+a 32768-token int8 state + 256-token records, 2 x 255 options x 12 tokens) and the decision on the Qwen3.5 hybrid
+stack ("hybrid": 24 Gated DeltaNet + 8 full-attention layers), each with its own CPU baseline (--scoring-only leaves
+them out).
 """
 from __future__ import annotations
 
@@ -358,6 +360,35 @@ def cpu_baseline_wide(args):
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": (f"1 record of {rec} tokens onto a {S0}-token int8 state x 1 of {args.layers} layers, one run, "
                        f"{per_layer:.2f} s per layer, scaled x{args.layers} layers")}
+
+
+def cpu_baseline_hybrid(args):
+    """The oracle on a bounded sample of the hybrid decision: ONE request (a 4096-token state of random ids prefilled,
+    then 64 options x 24 tokens scored) through ONE Gated DeltaNet layer (the gated delta rule in fp32, the
+    reference's own CPU arithmetic) and ONE gated full-attention layer, each timed once, scaled to the 24 + 8 layers
+    of the stack."""
+    import torch
+
+    from oracle import decoder as od
+    torch.set_num_threads(os.cpu_count() or 1)
+    emb = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(2)
+    S, n_opt, t = 4096, 64, 24
+    ids_s = torch.randint(0, 4096, (1, S), generator=g)
+    ids_o = torch.randint(0, 4096, (1, n_opt, t), generator=g)
+    per = {}
+    for kind, cfg in (("gdn", od.DecoderConfig(n_layers=1, full_attention_interval=4, gated=True)),
+                      ("attention", od.DecoderConfig(n_layers=1, gated=True))):
+        w = od.make_weights(cfg, seed=1)
+        t0 = time.perf_counter()
+        _, st = od.prefill_forward(ids_s, w, emb, cfg, gdn_dtype=torch.float32)
+        od.decision_forward(ids_o, w, emb, cfg, st, S, gdn_dtype=torch.float32)
+        per[kind] = time.perf_counter() - t0
+    per_request = 24 * per["gdn"] + 8 * per["attention"]
+    return {"value": 1.0 / per_request, "unit": "decisions/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"1 request ({S}-token state prefilled + {n_opt} options x {t} tokens) through 1 Gated DeltaNet "
+                       f"layer ({per['gdn']:.1f} s) and 1 gated attention layer ({per['attention']:.1f} s), one run "
+                       "each, scaled to 24 + 8 layers")}
 
 
 def _gemm_roofline(gemm_t):
@@ -1135,6 +1166,12 @@ def main():
                                   ("value", "unit", "config", "attention", "append_per_record", "scoring_ms"))
         if not args.no_cpu_baseline:
             res["wide_choice"]["cpu_baseline"] = cpu_baseline_wide(args)
+        torch.cuda.empty_cache()
+        res["hybrid"] = _sub(run_hybrid(_sub_args(args, steps=5, warmup=2)),
+                             ("value", "unit", "p50_latency_ms", "config", "roofline", "gdn_prep", "gdn_recurrence",
+                              "gdn_norm_quant", "time_share", "scoring_pass"))
+        if not args.no_cpu_baseline:
+            res["hybrid"]["cpu_baseline"] = cpu_baseline_hybrid(args)
     print(json.dumps(res))
 
 
