@@ -157,6 +157,39 @@ def recurrence(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tenso
     return out.float().to(torch.bfloat16), st
 
 
+def chunked_recurrence(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                       init: torch.Tensor | None, chunk: int = 32):
+    """The same gated delta rule in the chunked (WY) form that transformers' torch_chunk_gated_delta_rule evaluates
+    and od_gdn_recurrence_chunked implements, in float64: per chunk with gamma = cumsum(g) and S_0 the state at its
+    start, A_ij = beta_i e^{gamma_i - gamma_j} k_i.k_j (j < i), T = (I + A)^{-1} diag(beta),
+    delta = T V - T diag(e^gamma) K S_0, O = diag(e^gamma) Q~ S_0 + (Q~ K^T o D) delta (D_ij = e^{gamma_i - gamma_j},
+    j <= i), S_C = e^{gamma_C} S_0 + K^T diag(e^{gamma_C - gamma}) delta. Arguments as recurrence; returns (o bf16,
+    final state float64). Equal to the token-by-token recurrence up to float64 rounding (the algebra the kernel
+    relies on)."""
+    S_, L, Hv, dk = q.shape
+    dv = v.shape[-1]
+    qd = (q.float() * torch.tensor(1.0 / dk ** 0.5, dtype=torch.float32)).double()
+    kd, vd, gd, bd = k.double(), v.double(), g.double(), beta.double()
+    st = torch.zeros(S_, Hv, dk, dv, dtype=torch.float64) if init is None else init.double().clone()
+    out = torch.zeros(S_, L, Hv, dv, dtype=torch.float64)
+    for c0 in range(0, L, chunk):
+        sl = slice(c0, min(L, c0 + chunk))
+        K, Q, V = kd[:, sl].transpose(1, 2), qd[:, sl].transpose(1, 2), vd[:, sl].transpose(1, 2)  # (S, H, C, d)
+        gam = torch.cumsum(gd[:, sl].transpose(1, 2), -1)                                          # (S, H, C)
+        bb = bd[:, sl].transpose(1, 2)
+        n = K.shape[2]
+        D = torch.exp(gam[..., :, None] - gam[..., None, :])
+        A = torch.tril(bb[..., :, None] * D * (K @ K.transpose(-1, -2)), -1)
+        T = torch.linalg.solve_triangular(torch.eye(n, dtype=torch.float64) + A, torch.diag_embed(bb), upper=False,
+                                          unitriangular=True)
+        delta = T @ V - T @ (torch.exp(gam)[..., None] * (K @ st))
+        P = torch.tril((Q @ K.transpose(-1, -2)) * D)
+        out[:, sl] = (torch.exp(gam)[..., None] * (Q @ st) + P @ delta).transpose(1, 2)
+        dec = torch.exp(gam[..., -1:] - gam)
+        st = torch.exp(gam[..., -1])[..., None, None] * st + K.transpose(-1, -2) @ (dec[..., None] * delta)
+    return out.float().to(torch.bfloat16), st
+
+
 def silu_f32(z: torch.Tensor) -> torch.Tensor:
     """F.silu in fp32 on fp32 inputs, correctly rounded (float64, rounded once)."""
     zd = z.double()

@@ -92,6 +92,26 @@ def test_recurrence_matches_transformers_recurrent_and_chunked():
     assert torch.equal(o32, ref_o)                                          # fp32 mode: the reference's own ops
 
 
+@pytest.mark.parametrize("L,gmul", [(70, 1.0), (64, 30.0), (5, 0.01)])
+def test_chunked_form_equals_the_recurrence(L, gmul):
+    """The chunked (WY) form the MFMA kernel implements equals the token-by-token recurrence in float64 (state to
+    1e-10, outputs bit for bit after the bf16 rounding but for ties), including chunks whose decay empties the state
+    within a token (gmul 30) and a partial chunk."""
+    g = torch.Generator().manual_seed(7)
+    S, H, dk, dv = 2, 3, 16, 8
+    q = og.l2norm_bf16(_bf(g, S, L, H, dk))
+    k = og.l2norm_bf16(_bf(g, S, L, H, dk))
+    v = _bf(g, S, L, H, dv)
+    gg = -torch.rand(S, L, H, generator=g) * gmul
+    beta = torch.rand(S, L, H, generator=g)
+    init = torch.randn(S, H, dk, dv, generator=g)
+    o, st = og.recurrence(q, k, v, gg, beta, init, torch.float64)
+    oc, stc = og.chunked_recurrence(q, k, v, gg, beta, init, chunk=32)
+    assert torch.allclose(stc, st, rtol=1e-10, atol=1e-12)
+    assert (oc != o).float().mean().item() < 0.002
+    assert ((oc.float() - o.float()).abs() <= o.float().abs() * 2.0 ** -8 + 1e-30).all()
+
+
 def test_pure_decay_closed_form():
     """beta = 0 (no writes): S_t = exp(sum g) S_0 and o_t = exp(sum_{<=t} g) S_0^T q_t / sqrt(dk)."""
     g = torch.Generator().manual_seed(4)
