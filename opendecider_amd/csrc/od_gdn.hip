@@ -13,8 +13,9 @@
 //   od_gdn_norm_quant  bf16(bf16(w * bf16(o * rms(o))) * silu(z)) per value head (the gated RMSNorm), then the
 //                      out_proj input quantizer (optional SmoothQuant factors), per token
 // Every sum whose order torch leaves open (the conv taps, the squares of the l2norm and of the RMSNorm) is taken
-// exactly in float64 and rounded once, and the transcendental functions of the gates are evaluated in float64, so
-// od_gdn_prep and od_gdn_norm_quant give the oracle's bytes; the recurrence keeps fp32 with reductions in hardware
+// exactly in float64 and rounded once, the transcendental functions of the gates are evaluated in float64, and the
+// SiLUs are fp32 fast steps that fall back to float64 wherever their rounding could differ, so od_gdn_prep and
+// od_gdn_norm_quant give the oracle's bytes; the recurrence keeps fp32 with reductions in hardware
 // order.
 //
 // Layouts: proj bf16 [M, ldp] = [qkv (C = 2 n_k dk + n_v dv) | z (n_v dv) | b (n_v) | a (n_v)] with M = S L tokens,
@@ -65,102 +66,141 @@ __device__ __forceinline__ void store16(uint16_t* p, const float (&f)[kChan]) {
 
 __device__ __forceinline__ float bf(float x) { return od_bf16_to_f32(od_f32_to_bf16(x)); }
 
-// One workgroup per token; thread i handles channels 16 i .. 16 i + 15 (a q / k head is dk / 16 consecutive
-// threads, all in one wave).
-__global__ __launch_bounds__(1024) void gdn_prep_kernel(PrepArgs p) {
-  const int64_t m = blockIdx.x;
-  const int64_t s = m / p.L, t = m - s * p.L;
+// od_silu_bf16 with its float64 step out of line: the prep kernel calls it for 16 channels per token, and 16
+// inlined copies of the rare float64 path cost registers the common path needs
+__device__ __noinline__ float silu_bf16_slow(float g) {
+  const double gd = (double)g;
+  return od_bf16_to_f32(od_f32_to_bf16((float)(gd / (1.0 + exp(-gd)))));
+}
+// bf16(RN32(hw * RN32(silu(z)))), the gated norm's product (hw times silu of the fp32 gate, both fp32, then bf16).
+// Fast step for |z| < 16: the fp32 silu of od_silu_bf16 (within 11 ulps of silu(z)) times hw lands within 26 ulps of
+// RN32(hw * RN32(silu(z))), so its bf16 rounding is that of the reference value unless its low 16 bits lie within 48
+// ulps of the bf16 midpoint 0x8000; those (about 1 in 700), and |z| >= 16, take the float64 silu.
+__device__ __noinline__ float silu_mul_slow(float hw, float z) {
+  const double zd = (double)z;
+  const float sl = (float)(zd / (1.0 + exp(-zd)));
+  return od_bf16_to_f32(od_f32_to_bf16(hw * sl));
+}
+__device__ __forceinline__ float silu_mul_bf16(float hw, float z) {
+  const float sl = z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.44269504088896341f));
+  const float pr = hw * sl;
+  const uint32_t lo = __float_as_uint(pr) & 0xffffu;
+  if (__builtin_expect((lo - 0x7fd0u) <= 0x60u || !(fabsf(z) < 16.0f), 0)) return silu_mul_slow(hw, z);
+  return od_bf16_to_f32(od_f32_to_bf16(pr));
+}
+__device__ __forceinline__ float silu_bf16(float g) {
+  const float s = g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+  const uint32_t lo = __float_as_uint(s) & 0xffffu;
+  if (__builtin_expect((lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 16.0f), 0)) return silu_bf16_slow(g);
+  return od_bf16_to_f32(od_f32_to_bf16(s));
+}
+
+// One workgroup per (tile of kTok consecutive tokens of one sequence, block of 8192 channels); thread i handles
+// channels 16 i .. 16 i + 15 of the block (a q / k head is dk / 16 consecutive threads, all in one wave) and slides
+// the conv window (the previous 3 inputs of its channels) along the tile in registers, so each input row is read
+// once per tile instead of four times.
+constexpr int kTok = 8;
+constexpr int kPrepThreads = 512;
+
+__global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
+  const int64_t ntile = (p.L + kTok - 1) / kTok;
+  const int64_t s = blockIdx.x / ntile, t0 = (blockIdx.x % ntile) * kTok;
+  const int64_t m_s = s * p.L;  // first token of the sequence
   const int tid = threadIdx.x;
-  const int c0 = tid * kChan;
+  const int c0 = ((int)blockIdx.y * kPrepThreads + tid) * kChan;
   const bool on = c0 < p.C;
-  int64_t st = p.seq_state ? (int64_t)p.seq_state[s] : s;
+  const int64_t st = p.seq_state ? (int64_t)p.seq_state[s] : s;
   const bool st_ok = p.conv_in != nullptr && st >= 0 && st < p.n_states;
   const int kd = p.n_k * p.dk;
+  const int G = p.dk / kChan;  // lanes per head (a power of two <= 64)
+  const int tn = (int)min((int64_t)kTok, p.L - t0);
 
-  // conv inputs x[t - 3 + j] = full[t + j] over full = [state (3 rows) ; the sequence's tokens]
-  float y[kChan];
-  if (on) {
-    double acc[kChan];
+  // row r of full = [state (3 rows) ; the sequence's tokens]: full[r] = state row r (r < 3) or token r - 3
+  auto load_full = [&](int64_t r, float (&x)[kChan]) {
+    if (r >= kConvTaps - 1) {
+      load16(p.proj + (m_s + r - (kConvTaps - 1)) * p.ldp + c0, x);
+    } else if (st_ok) {
+      load16(p.conv_in + (st * (kConvTaps - 1) + r) * p.C + c0, x);
+    } else {
 #pragma unroll
-    for (int i = 0; i < kChan; ++i) acc[i] = 0.0;
-    uint16_t wt[kChan * kConvTaps];
+      for (int i = 0; i < kChan; ++i) x[i] = 0.0f;
+    }
+  };
+  uint32_t wr[kChan * kConvTaps / 2];  // the conv taps of this thread's channels, bf16 pairs (channel i: 2 words)
+  float win[kConvTaps - 1][kChan];     // full rows t0 .. t0 + 2 (the inputs before token t0)
+  if (on) {
 #pragma unroll
     for (int i = 0; i < kChan * kConvTaps / 8; ++i)
-      *reinterpret_cast<uint4*>(&wt[8 * i]) = *reinterpret_cast<const uint4*>(p.conv_w + (int64_t)c0 * kConvTaps + 8 * i);
+      *reinterpret_cast<uint4*>(&wr[4 * i]) = *reinterpret_cast<const uint4*>(p.conv_w + (int64_t)c0 * kConvTaps + 8 * i);
 #pragma unroll
-    for (int j = 0; j < kConvTaps; ++j) {
-      const int64_t r = t + j;  // row of full
+    for (int j = 0; j < kConvTaps - 1; ++j) load_full(t0 + j, win[j]);
+  }
+
+  for (int tt = 0; tt < tn; ++tt) {
+    const int64_t t = t0 + tt, m = m_s + t;
+    float y[kChan];
+    if (on) {
       float x[kChan];
-      if (r >= kConvTaps - 1) {
-        load16(p.proj + (s * p.L + r - (kConvTaps - 1)) * p.ldp + c0, x);
-      } else if (st_ok) {
-        load16(p.conv_in + (st * (kConvTaps - 1) + r) * p.C + c0, x);
-      } else {
+      load_full(t + kConvTaps - 1, x);
 #pragma unroll
-        for (int i = 0; i < kChan; ++i) x[i] = 0.0f;
+      for (int i = 0; i < kChan; ++i) {
+        const uint32_t w01 = wr[2 * i], w23 = wr[2 * i + 1];
+        double acc = (double)__uint_as_float(w01 << 16) * (double)win[0][i];
+        acc += (double)__uint_as_float(w01 & 0xffff0000u) * (double)win[1][i];
+        acc += (double)__uint_as_float(w23 << 16) * (double)win[2][i];
+        acc += (double)__uint_as_float(w23 & 0xffff0000u) * (double)x[i];
+        y[i] = silu_bf16(bf((float)acc));
       }
 #pragma unroll
-      for (int i = 0; i < kChan; ++i) acc[i] += (double)od_bf16_to_f32(wt[i * kConvTaps + j]) * (double)x[i];
+      for (int i = 0; i < kChan; ++i) {
+        win[0][i] = win[1][i];
+        win[1][i] = win[2][i];
+        win[2][i] = x[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kChan; ++i) y[i] = 0.0f;
     }
+    // l2norm of the q and k heads: squares rounded to bf16, their exact sum rounded to bf16, + eps, rsqrt and the
+    // product each rounded to bf16 (torch's bf16 arithmetic, with a correctly rounded rsqrt)
+    const bool qk_chan = on && c0 < 2 * kd;
+    double ss = 0.0;
+    if (qk_chan) {
 #pragma unroll
-    for (int i = 0; i < kChan; ++i) y[i] = od_silu_bf16(bf((float)acc[i]));
-  } else {
+      for (int i = 0; i < kChan; ++i) ss += (double)bf(y[i] * y[i]);
+    }
+    for (int o = G / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, OD_WAVE);
+    if (qk_chan) {
+      const float sb = bf((float)ss);
+      const float den = bf(sb + 1e-6f);
+      const float inv = bf((float)(1.0 / sqrt((double)den)));
 #pragma unroll
-    for (int i = 0; i < kChan; ++i) y[i] = 0.0f;
+      for (int i = 0; i < kChan; ++i) y[i] = bf(y[i] * inv);
+      store16(p.qk + m * (int64_t)(2 * kd) + c0, y);
+    } else if (on) {
+      store16(p.v + m * (int64_t)(p.n_v * p.dv) + (c0 - 2 * kd), y);
+    }
   }
 
-  // l2norm of the q and k heads: squares rounded to bf16, their exact sum rounded to bf16, + eps, rsqrt and the
-  // product each rounded to bf16 (torch's bf16 arithmetic, with a correctly rounded rsqrt)
-  const bool qk_chan = on && c0 < 2 * kd;
-  double ss = 0.0;
-  if (qk_chan) {
-#pragma unroll
-    for (int i = 0; i < kChan; ++i) ss += (double)bf(y[i] * y[i]);
-  }
-  const int G = p.dk / kChan;  // lanes per head (a power of two <= 64)
-  for (int o = G / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, OD_WAVE);
-  if (qk_chan) {
-    const float sb = bf((float)ss);
-    const float den = bf(sb + 1e-6f);
-    const float inv = bf((float)(1.0 / sqrt((double)den)));
-#pragma unroll
-    for (int i = 0; i < kChan; ++i) y[i] = bf(y[i] * inv);
-    store16(p.qk + m * (int64_t)(2 * kd) + c0, y);
-  } else if (on) {
-    store16(p.v + m * (int64_t)(p.n_v * p.dv) + (c0 - 2 * kd), y);
-  }
-
-  // gates of the value heads
-  if (tid < p.n_v) {
+  // gates of the tile's tokens (first channel block): thread i takes (token i / n_v, value head i % n_v)
+  for (int i = blockIdx.y == 0 ? tid : tn * p.n_v; i < tn * p.n_v; i += blockDim.x) {
+    const int64_t m = m_s + t0 + i / p.n_v;
+    const int hh = i % p.n_v;
     const uint16_t* row = p.proj + m * p.ldp + p.C + (int64_t)p.n_v * p.dv;
-    const float b = od_bf16_to_f32(row[tid]), a = od_bf16_to_f32(row[p.n_v + tid]);
-    p.beta[m * p.n_v + tid] = od_sigmoid_bf16(b);
-    const float e = (float)exp((double)od_bf16_to_f32(p.A_log[tid]));
-    const float x = (float)((double)a + (double)od_bf16_to_f32(p.dt_bias[tid]));
+    const float b = od_bf16_to_f32(row[hh]), a = od_bf16_to_f32(row[p.n_v + hh]);
+    p.beta[m * p.n_v + hh] = od_sigmoid_bf16(b);
+    const float e = (float)exp((double)od_bf16_to_f32(p.A_log[hh]));
+    const float x = (float)((double)a + (double)od_bf16_to_f32(p.dt_bias[hh]));
     const float sp = x > 20.0f ? x : (float)log1p(exp((double)x));
-    p.g[m * p.n_v + tid] = (float)(-((double)e * (double)sp));
+    p.g[m * p.n_v + hh] = (float)(-((double)e * (double)sp));
   }
 
-  // the new conv state: the last 3 rows of [state ; tokens]
-  if (p.conv_out && on) {
+  // the new conv state: the last 3 rows of [state ; tokens], written by the tile holding the last token
+  if (p.conv_out && on && t0 + tn == p.L) {
     const int64_t keep = kConvTaps - 1;
-    if (t >= p.L - keep) {
-      float x[kChan];
-      load16(p.proj + m * p.ldp + c0, x);
-      store16(p.conv_out + (s * keep + (t - (p.L - keep))) * p.C + c0, x);
-    }
-    if (t == 0) {
-      for (int64_t j = p.L; j < keep; ++j) {  // sequences shorter than 3 keep part of the old state
-        float x[kChan];
-        if (st_ok) {
-          load16(p.conv_in + (st * keep + j) * p.C + c0, x);
-        } else {
+    // win holds full rows L, L + 1, L + 2 = the last 3 rows of full (full has L + 3 rows)
 #pragma unroll
-          for (int i = 0; i < kChan; ++i) x[i] = 0.0f;
-        }
-        store16(p.conv_out + (s * keep + (j - p.L)) * p.C + c0, x);
-      }
-    }
+    for (int j = 0; j < kConvTaps - 1; ++j) store16(p.conv_out + (s * keep + j) * p.C + c0, win[j]);
   }
 }
 
@@ -433,9 +473,7 @@ __global__ __launch_bounds__(1024) void gdn_norm_quant_kernel(NormArgs p) {
     const int c = c0 + i;
     const float hn = bf(o[i] * r);
     const float hw = bf(od_bf16_to_f32(p.w[c % p.dv]) * hn);
-    const double zd = (double)z[i];
-    const float sl = (float)(zd / (1.0 + exp(-zd)));
-    float v = bf(hw * sl);
+    float v = silu_mul_bf16(hw, z[i]);
     if (p.inv_s) v = bf(v * od_bf16_to_f32(p.inv_s[c]));
     y[i] = on ? v : 0.0f;
     const uint32_t a = (__float_as_uint(y[i]) >> 16) & 0x7fffu;  // |bf16| bits: NaN patterns exceed every number
@@ -485,7 +523,10 @@ extern "C" int od_gdn_prep(const uint16_t* proj, int64_t ldp, const uint16_t* co
   if (S * L > 0x7fffffffll) return OD_ERR_SHAPE;
   PrepArgs p{proj, conv_w, conv_in, seq_state, A_log, dt_bias, qk, v, g, beta, conv_out, ldp, S, L, n_states,
              (int)n_k, (int)n_v, (int)dk, (int)dv, (int)C};
-  gdn_prep_kernel<<<dim3((unsigned)(S * L)), dim3(threads_for(C)), 0, (hipStream_t)stream>>>(p);
+  const int64_t tiles = S * ((L + kTok - 1) / kTok);
+  const int64_t cblocks = (C / kChan + kPrepThreads - 1) / kPrepThreads;
+  gdn_prep_kernel<<<dim3((unsigned)tiles, (unsigned)cblocks), dim3(min(threads_for(C), kPrepThreads)), 0,
+                    (hipStream_t)stream>>>(p);
   return od_launch_status();
 }
 

@@ -137,7 +137,29 @@ def test_gdn_recurrence_in_place_state_and_continuation(gpu_lib, chunked):
     assert torch.allclose(st2, fs_whole, rtol=1e-5, atol=1e-5 * fs_whole.abs().max().item())
 
 
-@pytest.mark.parametrize("M,n_v,smooth", [(5, 4, False), (33, 4, True), (64, 32, True), (3, 2, False)])
+def test_gdn_norm_quant_every_gate_value(gpu_lib):
+    """The gate z takes every finite bf16 value (the fast fp32 SiLU product and its float64 fallback both run) under
+    random o and weights: bytes and scales equal the oracle's."""
+    from opendecider_amd import kernels
+    M, n_v, dv = 16, 32, 128
+    g = torch.Generator().manual_seed(17)
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    zv = bits.view(torch.bfloat16)
+    zv = zv[torch.isfinite(zv.float())]
+    z = torch.cat([zv, zv[: M * n_v * dv - zv.numel()]]).reshape(M, n_v * dv)
+    o = _bf(g, M, n_v * dv, scale=0.3)
+    w = (1 + 0.1 * torch.randn(dv, generator=g)).to(torch.bfloat16)
+    inv = (1.0 / (torch.rand(n_v * dv, generator=g) * 1.5 + 0.5)).to(torch.bfloat16)
+    for smooth in (None, inv):
+        xq, sx = kernels.gdn_norm_quant(o.to(DEV), z.to(DEV), w.to(DEV), 1e-6, n_v, dv,
+                                        None if smooth is None else smooth.to(DEV))
+        y = og.gated_norm(o.reshape(M, n_v, dv), z.reshape(M, n_v, dv), w, 1e-6).reshape(M, n_v * dv)
+        rq, rs = oq.act_quant(y, smooth)
+        assert torch.equal(sx.cpu(), rs) and torch.equal(xq.cpu(), rq)
+
+
+@pytest.mark.parametrize("M,n_v,smooth", [(5, 4, False), (33, 4, True), (64, 32, True), (3, 2, False),
+                                          (512, 32, True)])
 def test_gdn_norm_quant_bit_exact(gpu_lib, M, n_v, smooth):
     from opendecider_amd import kernels
     dv = 128
