@@ -30,6 +30,11 @@ __device__ __forceinline__ uint32_t od_bfr2(float& a, float& b) {
   return p;
 }
 
+// Rounds two fp32 values to bf16 (nearest even) and packs them, a in the low half: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t od_pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((od_f32x2){a, b}, od_bf16x2));
+}
+
 // Running max of |bf16| over packed pairs, on the bit patterns (monotonic in the magnitude; a NaN dominates, as
 // in a float amax that propagates NaN): one v_pk_max_u16 per pair.
 __device__ __forceinline__ uint32_t od_absmax_bf16x2(uint32_t acc, uint32_t p) {
@@ -52,13 +57,21 @@ __device__ __forceinline__ float od_absmax_bf16x2_value(uint32_t acc) {
 // its low 16 bits lie within 16 ulps of the bf16 midpoint 0x8000. Those values (about 1 in 2000), and |g| >= 16, are
 // recomputed in float64 and rounded once to fp32. Every SwiGLU kernel uses this one function, so fused and unfused
 // paths agree bit for bit, and g has 65536 values, so it is checked against the oracle exhaustively.
-__device__ __forceinline__ float od_silu_bf16(float g) {
-  float s = g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+// The three steps are also callable one by one (a kernel can check several fast values before one branch).
+__device__ __forceinline__ float od_silu_fast32(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+}
+__device__ __forceinline__ bool od_silu_needs_slow(float g, float s) {
   const uint32_t lo = __float_as_uint(s) & 0xffffu;
-  if (__builtin_expect((lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 16.0f), 0)) {
-    const double gd = (double)g;
-    s = (float)(gd / (1.0 + exp(-gd)));
-  }
+  return (lo - 0x7ff0u) <= 0x20u || !(fabsf(g) < 16.0f);
+}
+__device__ __forceinline__ float od_silu_slow32(float g) {
+  const double gd = (double)g;
+  return (float)(gd / (1.0 + exp(-gd)));
+}
+__device__ __forceinline__ float od_silu_bf16(float g) {
+  float s = od_silu_fast32(g);
+  if (__builtin_expect(od_silu_needs_slow(g, s), 0)) s = od_silu_slow32(g);
   return od_bf16_to_f32(od_f32_to_bf16(s));
 }
 

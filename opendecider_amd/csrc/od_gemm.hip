@@ -52,6 +52,7 @@ constexpr int kMaxBM = 256;
 constexpr int BK = 128;      // bytes of K per stage
 constexpr int kCpr = BK / 16;  // 16-byte chunks per row per stage
 constexpr int kGroupM = 4;
+constexpr int kScaleRows = 256;  // the WIDE variant's LDS scale slot: kScaleRows row scales, then 256 column scales
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any range: the load returns zeros
 
 struct GemmArgs {
@@ -234,11 +235,23 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const v16i (&acc)[TM
   }
 }
 
-// The epilogue with 8 columns per lane in the row pass (16-byte band reads, residual loads and output stores; 8-byte
-// stores for SwiGLU): N % 8 == 0, 16-byte aligned out / bias / residual rows (8-byte out for SwiGLU).
+// The epilogue of the WIDE variant: N % 8 == 0, 16-byte aligned out / bias / residual rows (8-byte out rows for
+// SwiGLU), 16-byte aligned scale vectors, row strides below 2^22 elements. Same arithmetic as `epilogue`, with fewer
+// instructions and waits:
+//  * the tile's row and column scales come from LDS (`sc`: kScaleRows row scales, then the column scales), where the
+//    stage that loaded the tile's first operands put them, instead of global loads between the epilogue's stores;
+//  * the row pass takes 8 columns per lane (16-byte band reads, residual loads and stores; 8-byte stores for
+//    SwiGLU);
+//  * output and residual go through buffer descriptors over the tile's valid rows with 32-bit offsets: rows past M
+//    are dropped by the range check (stores) or read as zeros (loads), so there is no per-row bounds arithmetic;
+//  * the residual of the next 16-row band-half is loaded before the current band-half's stores are issued, so that
+//    waiting for it does not wait for them (vector-memory operations complete in issue order);
+//  * SwiGLU: g and u are rounded to bf16 by one conversion, the fast SiLU values of a lane's four outputs are
+//    checked together for the rare float64 recomputation, and each pair of products is rounded and packed by one
+//    conversion.
 template <int BM, int BN, bool SWIGLU, int TM, int TN>
-__device__ __forceinline__ void epilogue8(const GemmArgs& p, const v16i (&acc)[TM][TN], int8_t* stage_buf, int tm,
-                                          int tn, int wm, int wn, int wave, int lane) {
+__device__ __forceinline__ void epilogue8(const GemmArgs& p, const v16i (&acc)[TM][TN], int8_t* stage_buf,
+                                          const float* sc, int tm, int tn, int wm, int wn, int wave, int lane) {
   constexpr int kWM = WaveGrid<BM>::kWM, kWN = WaveGrid<BM>::kWN;
   constexpr int kRowsW = BM / kWM;
   constexpr int kCols = BN / kWN;
@@ -249,18 +262,25 @@ __device__ __forceinline__ void epilogue8(const GemmArgs& p, const v16i (&acc)[T
   static_assert(kPasses <= 4, "one group of residual loads per band");
   constexpr int kBand = kHalf * kCols * 4;
   uint32_t* band = reinterpret_cast<uint32_t*>(stage_buf + wave * kBand);
-  const int64_t m_w = (int64_t)tm * BM + wm * kRowsW;
-  const int64_t n_w = (int64_t)tn * BN + wn * kCols;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int rows_valid = (int)min((int64_t)BM, p.M - m0);
   const int col = lane & 31, h = lane >> 5;
+  const float* ssa = sc + wm * kRowsW;
+  const float* ssw = sc + kScaleRows + wn * kCols;
   float swv[TN];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) swv[j] = p.sw[min(n_w + j * 32 + col, p.N - 1)];
+  for (int j = 0; j < TN; ++j) swv[j] = ssw[j * 32 + col];
   const int c8 = lane % kC8, rr = lane / kC8;
-  const int64_t n = n_w + 8 * c8;
-  const bool lane_on = rr < kRowsPass && n < p.N;
+  const int nl = wn * kCols + 8 * c8;  // the lane's first column inside the tile
+  const bool lane_on = rr < kRowsPass && n0 + nl < p.N;
+  const int ldo = (int)p.ldo, ldr = (int)p.ldr;
+  const __amdgpu_buffer_rsrc_t rout = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.out + m0 * p.ldo + (SWIGLU ? n0 / 2 : n0)), (short)0, rows_valid * ldo * 2, 0x00020000);
+  const int row0 = wm * kRowsW + rr;  // the lane's row in band-half 0, pass 0
+  const int ovo = (row0 * ldo + (SWIGLU ? nl / 2 : nl)) * 2;
   float bias8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (!SWIGLU && p.bias && lane_on) {
-    const uint4 b = *reinterpret_cast<const uint4*>(p.bias + n);
+    const uint4 b = *reinterpret_cast<const uint4*>(p.bias + n0 + nl);
     const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -268,12 +288,31 @@ __device__ __forceinline__ void epilogue8(const GemmArgs& p, const v16i (&acc)[T
       bias8[2 * e + 1] = __uint_as_float(bw[e] & 0xffff0000u);
     }
   }
+  const bool has_res = !SWIGLU && p.residual && lane_on;
+  const __amdgpu_buffer_rsrc_t rres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(has_res ? p.residual + m0 * p.ldr + n0 : p.residual), (short)0, has_res ? rows_valid * ldr * 2 : 0,
+      0x00020000);
+  const int rvo = (row0 * ldr + nl) * 2;
+  // residual rows of band-half bq (rows 16 bq .. 16 bq + 15 of the wave's sub-tile)
+  auto load_res = [&](int bq, uint4 (&r)[kPasses]) {
+#pragma unroll
+    for (int u = 0; u < kPasses; ++u)
+      r[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rres, rvo, (16 * bq + kRowsPass * u) * ldr * 2, 0));
+  };
+  uint4 res[kPasses], resn[kPasses];
+  if (has_res) load_res(0, res);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int64_t m_band = m_w + i * 32;
     float sav[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sav[r] = p.sa[min(m_band + 8 * (r >> 2) + 4 * h + (r & 3), p.M - 1)];
+    for (int k = 0; k < 4; ++k) {
+      const float4 s4 = *reinterpret_cast<const float4*>(ssa + i * 32 + 8 * k + 4 * h);
+      sav[4 * k] = s4.x;
+      sav[4 * k + 1] = s4.y;
+      sav[4 * k + 2] = s4.z;
+      sav[4 * k + 3] = s4.w;
+    }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       __builtin_amdgcn_sched_barrier(0);
@@ -288,42 +327,56 @@ __device__ __forceinline__ void epilogue8(const GemmArgs& p, const v16i (&acc)[T
         }
       }
       if (!lane_on) continue;
-      const int64_t m_half = m_band + 16 * q;
-      uint4 res[kPasses];
-      if (!SWIGLU && p.residual) {
-#pragma unroll
-        for (int u = 0; u < kPasses; ++u)
-          res[u] = *reinterpret_cast<const uint4*>(p.residual + min(m_half + kRowsPass * u + rr, p.M - 1) * p.ldr + n);
-      }
+      const int bq = 2 * i + q;
+      if (has_res && bq + 1 < 2 * TM) load_res(bq + 1, resn);
 #pragma unroll
       for (int u = 0; u < kPasses; ++u) {
         const int row = kRowsPass * u + rr;
-        const int64_t m = m_half + row;
-        if (row >= kHalf || m >= p.M) continue;
+        if (kRowsPass * kPasses > kHalf && row >= kHalf) continue;
+        const int soff = (16 * bq + kRowsPass * u) * ldo * 2;
         const uint4 va = *reinterpret_cast<const uint4*>(band + row * kCols + 8 * c8);
         const uint4 vb = *reinterpret_cast<const uint4*>(band + row * kCols + 8 * c8 + 4);
         const uint32_t vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
         if constexpr (SWIGLU) {
-          uint32_t hh[4];
+          // columns 2e, 2e + 1 of the group are (gate, up) of output column nl / 2 + e
+          float g[4], uu[4], s[4];
+          bool slow = false;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float g = bfr(__uint_as_float(vv[2 * e])), uu = bfr(__uint_as_float(vv[2 * e + 1]));
-            hh[e] = od_f32_to_bf16(od_silu_bf16(g) * uu);
+            g[e] = __uint_as_float(vv[2 * e]);
+            uu[e] = __uint_as_float(vv[2 * e + 1]);
+            od_bfr2(g[e], uu[e]);
+            s[e] = od_silu_fast32(g[e]);
+            slow |= od_silu_needs_slow(g[e], s[e]);
           }
-          *reinterpret_cast<uint2*>(p.out + m * p.ldo + n / 2) = make_uint2(hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16));
+          if (__builtin_expect(slow, 0)) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (od_silu_needs_slow(g[e], s[e])) s[e] = od_silu_slow32(g[e]);
+          }
+          od_bfr2(s[0], s[1]);
+          od_bfr2(s[2], s[3]);
+          typedef unsigned v2u __attribute__((ext_vector_type(2)));
+          const v2u w = {od_pack_bf16x2(s[0] * uu[0], s[1] * uu[1]), od_pack_bf16x2(s[2] * uu[2], s[3] * uu[3])};
+          __builtin_amdgcn_raw_buffer_store_b64(w, rout, ovo, soff, 0);
         } else {
           const uint32_t rw4[4] = {res[u].x, res[u].y, res[u].z, res[u].w};
-          uint32_t o[8];
+          float y[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            float y = __uint_as_float(vv[e]);
-            if (p.bias) y = y + bias8[e];
-            if (p.residual) y = y + __uint_as_float(e & 1 ? (rw4[e >> 1] & 0xffff0000u) : (rw4[e >> 1] << 16));
-            o[e] = od_f32_to_bf16(y);
+            y[e] = __uint_as_float(vv[e]);
+            if (p.bias) y[e] = y[e] + bias8[e];
+            if (has_res) y[e] = y[e] + __uint_as_float(e & 1 ? (rw4[e >> 1] & 0xffff0000u) : (rw4[e >> 1] << 16));
           }
-          *reinterpret_cast<uint4*>(p.out + m * p.ldo + n) =
-              make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+          typedef unsigned v4u __attribute__((ext_vector_type(4)));
+          const v4u w = {od_pack_bf16x2(y[0], y[1]), od_pack_bf16x2(y[2], y[3]), od_pack_bf16x2(y[4], y[5]),
+                         od_pack_bf16x2(y[6], y[7])};
+          __builtin_amdgcn_raw_buffer_store_b128(w, rout, ovo, soff, 0);
         }
+      }
+      if (has_res) {
+#pragma unroll
+        for (int u = 0; u < kPasses; ++u) res[u] = resn[u];
       }
     }
   }
@@ -371,6 +424,10 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   constexpr int kSlabA = BM * BK, kSlabB = BN * BK, kStage = kSlabA + kSlabB;
   constexpr int kOpsA = BM / 64, kOpsB = BN / 64;  // DMA loads per wave per stage (8 waves x 8 rows each)
   __shared__ __attribute__((aligned(16))) int8_t smem[2 * kStage];
+  // WIDE: the row and column scales of a tile, two slots by tile parity, each loaded by the stage that loads the
+  // tile's first operands (one 1 KB LDS-DMA load each; rows / columns past M / N read as zeros)
+  constexpr int kSlot = 2 * kScaleRows;
+  __shared__ __attribute__((aligned(16))) float sscale[WIDE ? 2 * kSlot : 4];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -384,6 +441,25 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   if constexpr (ACC_ONLY) p.acc += blockIdx.y * p.split_stride;
   const int lda_step = (int)(p.lda * 64), ldw_step = (int)(p.ldw * 64);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)(smem);
+  auto dma_scales = [&](int v, int slot) {
+    if constexpr (WIDE) {
+      if (v >= ntiles || wave > 1) return;
+      int tm, tn;
+      tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
+      const uint32_t lds_sc = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)(sscale + slot * kSlot);
+      if (wave == 0) {
+        const int64_t m0 = (int64_t)tm * BM;
+        dma16(__builtin_amdgcn_make_buffer_rsrc((void*)(p.sa + m0), (short)0, (int)(min((int64_t)BM, p.M - m0) * 4),
+                                                0x00020000),
+              lane * 16, 0, lds_sc);
+      } else {
+        const int64_t n0 = (int64_t)tn * BN;
+        dma16(__builtin_amdgcn_make_buffer_rsrc((void*)(p.sw + n0), (short)0, (int)(min((int64_t)BN, p.N - n0) * 4),
+                                                0x00020000),
+              lane * 16, 0, lds_sc + kScaleRows * 4);
+      }
+    }
+  };
 
   // DMA load o of a stage: wave w moves slab rows 8 (w + 8 o') .. +7 (o' = o, or o - kOpsA for the W slab); lane
   // l takes row l / 8 of those and physical chunk l % 8 of the row, which holds logical chunk (l % 8) ^ ((row >> 1)
@@ -461,16 +537,18 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   Panels cur = panels_of<BM, BN>(p, v, ntiles);
 #pragma unroll
   for (int o = 0; o < kOps0; ++o) dma(0, cur, kb, o);
+  dma_scales(v, 0);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   frags(0, 0, f0a, f0b);
   zero_acc();
 
-  auto stage = [&](int CUR, const Panels& src, int kt_src) {
+  auto stage = [&](int CUR, const Panels& src, int kt_src, int scale_tile, int slot) {
     const int NXT = 1 - CUR;
     frags(CUR, 1, f1a, f1b);
     __builtin_amdgcn_sched_barrier(0);
     auto fill0 = [&](int o) { dma(NXT, src, kt_src, o); };
     mma(f0a, f0b, fill0, std::integral_constant<int, kOps0>{});
+    if (scale_tile >= 0) dma_scales(scale_tile, slot);
     frags(CUR, 2, f0a, f0b);
     __builtin_amdgcn_sched_barrier(0);
     mma(f1a, f1b, nofill, Zero{});
@@ -483,21 +561,22 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
     mma(f1a, f1b, nofill, Zero{});
   };
 
-  int buf = 0;
+  int buf = 0, parity = 0;
   // (the stage buffer is a run-time value: unrolling two stages with compile-time buffer indices lengthens the
   // live ranges)
   for (; v < ntiles; v += gridDim.x) {
     const Panels nxt = panels_of<BM, BN>(p, v + (int)gridDim.x, ntiles);
     for (int kt = kb; kt + 1 < ke; ++kt) {
-      stage(buf, cur, kt + 1);
+      stage(buf, cur, kt + 1, -1, 0);
       buf ^= 1;
     }
-    stage(buf, nxt, kb);
+    stage(buf, nxt, kb, v + (int)gridDim.x, parity ^ 1);
     buf ^= 1;
     int tm, tn;
     tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
     if constexpr (WIDE)
-      epilogue8<BM, BN, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, tm, tn, wm, wn, wave, lane);
+      epilogue8<BM, BN, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, sscale + parity * kSlot, tm, tn, wm, wn,
+                                        wave, lane);
     else
       epilogue<BM, BN, ACC_ONLY, GENERAL, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, tm, tn, wm, wn, wave,
                                                           lane);
@@ -505,6 +584,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     zero_acc();
     cur = nxt;
+    parity ^= 1;
   }
 }
 
@@ -704,10 +784,10 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
   const bool fast_out = fast_k && (swiglu ? (p.ldo % 2 == 0 && al(p.out, 4))
                                           : (p.ldo % 4 == 0 && al(p.out, 8) && al(p.bias, 8) && p.ldr % 4 == 0 &&
                                              al(p.residual, 8)));
-  const bool wide_out = fast_out && N % 8 == 0 &&
+  const bool wide_out = fast_out && N % 8 == 0 && al(p.sa, 16) && al(p.sw, 16) && p.ldo < (1 << 22) &&
                         (swiglu ? (p.ldo % 4 == 0 && al(p.out, 8))
                                 : (p.ldo % 8 == 0 && al(p.out, 16) && al(p.bias, 16) && p.ldr % 8 == 0 &&
-                                   al(p.residual, 16)));
+                                   p.ldr < (1 << 22) && al(p.residual, 16)));
   const int out_variant = wide_out ? kWide : (fast_out ? kFast : kGeneral);
   const bool fast_acc = fast_k && p.ldacc % 4 == 0 && al(p.acc, 16);
   if (p.acc) {
