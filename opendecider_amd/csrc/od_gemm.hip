@@ -339,17 +339,21 @@ __device__ __forceinline__ void epilogue8(const GemmArgs& p, const v16i (&acc)[T
         const uint32_t vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
         if constexpr (SWIGLU) {
           // columns 2e, 2e + 1 of the group are (gate, up) of output column nl / 2 + e
+          // the slow-path test of od_silu_needs_slow for the four at once: the least (low 16 bits - 0x7ff0) and
+          // any |g| >= 16 (or NaN)
           float g[4], uu[4], s[4];
-          bool slow = false;
+          uint32_t dmin = 0xffffffffu;
+          bool big = false;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             g[e] = __uint_as_float(vv[2 * e]);
             uu[e] = __uint_as_float(vv[2 * e + 1]);
             od_bfr2(g[e], uu[e]);
             s[e] = od_silu_fast32(g[e]);
-            slow |= od_silu_needs_slow(g[e], s[e]);
+            dmin = min(dmin, (__float_as_uint(s[e]) & 0xffffu) - 0x7ff0u);
+            big |= !(fabsf(g[e]) < 16.0f);
           }
-          if (__builtin_expect(slow, 0)) {
+          if (__builtin_expect(dmin <= 0x20u || big, 0)) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               if (od_silu_needs_slow(g[e], s[e])) s[e] = od_silu_slow32(g[e]);

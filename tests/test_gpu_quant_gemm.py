@@ -119,6 +119,31 @@ def test_gemm_bias_residual_epilogue(gpu_lib):
     assert torch.equal(out.cpu(), oq.w8a8_epilogue(oq.int_gemm(a, w), sa, sw, bias, res))
 
 
+def test_gemm_wide_epilogue_equals_narrow_epilogue(gpu_lib):
+    """The wide epilogue (N % 8 == 0, 16-byte aligned scale vectors and rows: the tile's scales staged in LDS, stores
+    through a buffer descriptor whose range drops rows past M) against the same GEMM with scale vectors 4 bytes off
+    16-byte alignment, which takes the 4-column epilogue: the same bytes, and the oracle's on a sample of rows.
+    M = 1100 and N = 16384 make 320 tiles, so some workgroups run two (the scale slots alternate), and the last tile
+    row is ragged (76 of 256 rows)."""
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(11)
+    M, N, K = 1100, 16384, 128
+    a, w, sa, sw = _gemm_case(g, M, N, K)
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    A, W, R = a.to(DEV), w.to(DEV), res.to(DEV)
+    out_w = kernels.w8a8_gemm(A, sa.to(DEV), W, sw.to(DEV), residual=R)
+    sab = torch.zeros(M + 1, device=DEV)
+    swb = torch.zeros(N + 1, device=DEV)
+    sab[1:] = sa.to(DEV)
+    swb[1:] = sw.to(DEV)
+    assert sab[1:].data_ptr() % 16 != 0 and swb[1:].data_ptr() % 16 != 0
+    out_n = kernels.w8a8_gemm(A, sab[1:], W, swb[1:], residual=R)
+    assert torch.equal(out_w, out_n)
+    rows = torch.tensor([0, 1, 255, 256, 511, 1023, 1024, 1099])
+    ref = oq.w8a8_epilogue(oq.int_gemm(a[rows], w), sa[rows], sw, None, res[rows])
+    assert torch.equal(out_w.cpu()[rows], ref)
+
+
 def test_config0_single_w8a8_linear(gpu_lib):
     """X bf16 [256,4096] N(0,1) with 1% outlier channels x20, per-token int8; W int8 [4096,4096] uniform in
     [-127,127]; per-channel fp32 scales U(0.5e-3, 2e-3); int32 accumulators compared exactly."""
@@ -195,7 +220,7 @@ def test_int8_tensor_quantize_matches_reference_formula(gpu_lib):
     assert err <= x.float().abs().amax() / 127 + 1e-2
 
 
-@pytest.mark.parametrize("M,K,F", [(4096, 4096, 12288), (300, 272, 520), (77, 4096, 98)])
+@pytest.mark.parametrize("M,K,F", [(4096, 4096, 12288), (300, 272, 520), (77, 4096, 98), (333, 512, 1024)])
 def test_w8a8_gemm_swiglu_equals_gemm_then_swiglu(gpu_lib, M, K, F):
     """The SwiGLU epilogue gives the bytes of the plain GEMM followed by the SwiGLU kernel (shared device silu):
     quantizing its h equals od_silu_mul_quant on the plain GEMM's [gate | up] output, bit for bit; and h differs
