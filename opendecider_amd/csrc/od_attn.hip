@@ -411,7 +411,9 @@ __device__ __forceinline__ uint32_t lds_addr(T* p) {
 }
 
 // Copies NBYTES (a multiple of 16) of a staged image into LDS, 16 bytes per lane and no registers: round i moves
-// bytes [4096 i, 4096 (i + 1)), wave w the 1 KiB at 1024 w of it, and lanes of the first wave take the tail.
+// bytes [4096 i, 4096 (i + 1)), wave w the 1 KiB at 1024 w of it; the tail round has every wave copy the last
+// 1 KiB (bytes already copied are written again with the same values), so that no round branches on the lane or
+// the wave and a caller's code around the copies stays one basic block (one scheduling region).
 // Completion is a vmcnt wait by every thread that issued a part, then a barrier.
 template <int NBYTES>
 struct CopyShape {
@@ -419,7 +421,7 @@ struct CopyShape {
   static constexpr int kFull = NBYTES / kRound;
   static constexpr int kTailLanes = (NBYTES - kFull * kRound) / 16;
   static constexpr int kRounds = kFull + (kTailLanes > 0 ? 1 : 0);
-  static_assert(NBYTES % 16 == 0 && kTailLanes <= 64, "copy shape");
+  static_assert(NBYTES % 16 == 0 && NBYTES >= 1024 && kTailLanes <= 64, "copy shape");
 };
 
 // Round i of such a copy (so that a caller can spread the rounds over its work).
@@ -430,10 +432,11 @@ __device__ __forceinline__ void copy_round(const void* src, void* dst, int i) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const char* s = reinterpret_cast<const char*>(src);
   const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(dst));
+  const int lane = tid & 63;
   if (i < C::kFull)
     dma16(s + i * C::kRound + tid * 16, d + i * C::kRound + wave * 1024);
-  else if (tid < C::kTailLanes)
-    dma16(s + C::kFull * C::kRound + tid * 16, d + C::kFull * C::kRound);
+  else
+    dma16(s + NBYTES - 1024 + lane * 16, d + NBYTES - 1024);
 }
 
 template <int NBYTES>
@@ -930,11 +933,13 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
         auto dma = [&](int ks) {
 #pragma unroll
           for (int r = ks * kNR / (D / 16); r < (ks + 1) * kNR / (D / 16); ++r) {
-            if (r < kKR) {
-              if (b + 2 < b_hi) copy_round<kKeyBytes>(blk(b + 2), cur.k, r);
-            } else if (b + 1 < b_hi) {
-              copy_round<kRestBytes>(rest(blk(b + 1)), reinterpret_cast<char*>(&nxt) + kKeyBytes, r - kKR);
-            }
+            // past the last block the copies repeat the last block into buffers no later step reads, so that
+            // the step has no branch: its score MFMAs and softmax groups stay one scheduling region
+            if (r < kKR)
+              copy_round<kKeyBytes>(blk(min(b + 2, b_hi - 1)), cur.k, r);
+            else
+              copy_round<kRestBytes>(rest(blk(min(b + 1, b_hi - 1))), reinterpret_cast<char*>(&nxt) + kKeyBytes,
+                                     r - kKR);
           }
         };
         // the last block's step scores its own keys again (in place of a next block), and the result is not used
