@@ -273,7 +273,8 @@ GEMM_TRAFFIC_M4096 = {(6144, 4096): 218.5e6, (4096, 4096): 168.0e6, ("swiglu", 2
 
 def cpu_baseline(args):
     """The oracle (CPU torch restatement of the path) on a bounded sample: ONE request (32 options x 16 tokens, its
-    2048-token int8 state) through ONE 9B-dims layer, timed and scaled x36 layers x8 requests."""
+    2048-token int8 state) through ONE 9B-dims layer, timed and scaled x36 layers. A decision is one request, so
+    the CPU's decisions/s is 1 / (36 x the layer time) whatever the batch (8 requests take 8 times as long)."""
     import torch
 
     from oracle import decoder as od
