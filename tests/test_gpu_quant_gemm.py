@@ -119,28 +119,30 @@ def test_gemm_bias_residual_epilogue(gpu_lib):
     assert torch.equal(out.cpu(), oq.w8a8_epilogue(oq.int_gemm(a, w), sa, sw, bias, res))
 
 
-def test_gemm_wide_epilogue_equals_narrow_epilogue(gpu_lib):
+@pytest.mark.parametrize("M,N,K,with_bias", [(1100, 16384, 128, False), (300, 712, 128, True)])
+def test_gemm_wide_epilogue_equals_narrow_epilogue(gpu_lib, M, N, K, with_bias):
     """The wide epilogue (N % 8 == 0, 16-byte aligned scale vectors and rows: the tile's scales staged in LDS, stores
     through a buffer descriptor whose range drops rows past M) against the same GEMM with scale vectors 4 bytes off
     16-byte alignment, which takes the 4-column epilogue: the same bytes, and the oracle's on a sample of rows.
     M = 1100 and N = 16384 make 320 tiles, so some workgroups run two (the scale slots alternate), and the last tile
-    row is ragged (76 of 256 rows)."""
+    row is ragged (76 of 256 rows); N = 712 leaves the last tile column ragged (200 of 256 columns), with a bias."""
     from opendecider_amd import kernels
-    g = torch.Generator().manual_seed(11)
-    M, N, K = 1100, 16384, 128
+    g = torch.Generator().manual_seed(11 + M)
     a, w, sa, sw = _gemm_case(g, M, N, K)
     res = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16) if with_bias else None
     A, W, R = a.to(DEV), w.to(DEV), res.to(DEV)
-    out_w = kernels.w8a8_gemm(A, sa.to(DEV), W, sw.to(DEV), residual=R)
+    Bd = None if bias is None else bias.to(DEV)
+    out_w = kernels.w8a8_gemm(A, sa.to(DEV), W, sw.to(DEV), bias=Bd, residual=R)
     sab = torch.zeros(M + 1, device=DEV)
     swb = torch.zeros(N + 1, device=DEV)
     sab[1:] = sa.to(DEV)
     swb[1:] = sw.to(DEV)
     assert sab[1:].data_ptr() % 16 != 0 and swb[1:].data_ptr() % 16 != 0
-    out_n = kernels.w8a8_gemm(A, sab[1:], W, swb[1:], residual=R)
+    out_n = kernels.w8a8_gemm(A, sab[1:], W, swb[1:], bias=Bd, residual=R)
     assert torch.equal(out_w, out_n)
-    rows = torch.tensor([0, 1, 255, 256, 511, 1023, 1024, 1099])
-    ref = oq.w8a8_epilogue(oq.int_gemm(a[rows], w), sa[rows], sw, None, res[rows])
+    rows = torch.tensor(sorted({0, 1, 255, 256, 511, 1023, 1024, M - 1} & set(range(M))))
+    ref = oq.w8a8_epilogue(oq.int_gemm(a[rows], w), sa[rows], sw, bias, res[rows])
     assert torch.equal(out_w.cpu()[rows], ref)
 
 
