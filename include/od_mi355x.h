@@ -69,6 +69,16 @@ int od_gate_act_quant(const uint16_t* x, int64_t ldx, const uint16_t* gate, int6
                       int8_t* xq, int64_t ldq, float* sx, int64_t M, int64_t K, od_stream_t stream);
 
 /*
+ * od_act_quant_f32 — the od_act_quant formula over fp32 rows.
+ * Replaces: Int8Tensor.quantize (src/opendecider/quant.py:36-41) of float32 input, and of float16 / float64 input,
+ * which the reference also quantizes from xf = x.float() (quant.py:38): the caller passes x.float().
+ *   x   fp32 [M, K], row stride ldx;  xq int8 [M, K], row stride ldq (out);  sx fp32 [M] (out).
+ * Same scale and bytes as the torch formula, NaN and inf rows included. Any M >= 0, K >= 1.
+ */
+int od_act_quant_f32(const float* x, int64_t ldx, int8_t* xq, int64_t ldq, float* sx, int64_t M, int64_t K,
+                     od_stream_t stream);
+
+/*
  * od_w8a8_gemm — int8 x int8 -> int32 GEMM on CDNA4 int8 MFMA with a bf16 dequant epilogue.
  * Replaces: the GEMM of GemLite A8W8_int8_dynamic behind gemlite_a8w8_ / smooth_a8w8_
  * (src/opendecider/quant.py:302-314, :332-350), and Int8Linear.forward's dequantize + F.linear

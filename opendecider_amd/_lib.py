@@ -22,6 +22,7 @@ SIGNATURES = {
     "od_abi_version": [],
     "od_act_quant": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr],
     "od_gate_act_quant": [_c_ptr, _i64, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr],
+    "od_act_quant_f32": [_c_ptr, _i64, _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr],
     "od_w8a8_gemm": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _c_ptr, _i64,
                      _i64, _i64, _i64, _c_ptr],
     "od_kv_quant_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _i64, _i64, _c_ptr],

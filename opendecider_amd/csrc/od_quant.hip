@@ -274,6 +274,42 @@ extern "C" int od_gate_act_quant(const uint16_t* x, int64_t ldx, const uint16_t*
   return launch_quant<kGate>(m, inv_s, M, K, vec_ok, (hipStream_t)stream);
 }
 
+namespace {
+
+// fp32 rows: Int8Tensor.quantize of float32 input, and of float16 / float64 input through x.float() (the reference
+// quantizes xf = x.float() whatever the dtype, quant.py:38). One wave per row, 4 rows per workgroup; the max runs on
+// |x| bit patterns (a NaN has the largest pattern, so it reaches the scale as in the bf16 rows); the same per-element
+// quantizer as the bf16 rows. Not a hot path: the decoder's activations and caches are bf16.
+__global__ __launch_bounds__(kThreads) void quant_rows_f32_kernel(const float* __restrict__ x, int64_t ldx,
+                                                                  int8_t* __restrict__ q, int64_t ldq,
+                                                                  float* __restrict__ s, int64_t n_rows, int64_t K) {
+  const int lane = threadIdx.x % OD_WAVE;
+  const int64_t r = (int64_t)blockIdx.x * (kThreads / OD_WAVE) + threadIdx.x / OD_WAVE;
+  if (r >= n_rows) return;  // a whole wave leaves; no barrier in this kernel
+  const float* xin = x + r * ldx;
+  uint32_t am = 0;
+  for (int64_t k = lane; k < K; k += OD_WAVE) am = umax(am, __float_as_uint(fabsf(xin[k])));
+  const float amax = __uint_as_float(od_wave_umax_dpp(am));
+  const float scale = od_q8_scale(amax), inv = 1.0f / scale;
+  int8_t* qout = q + r * ldq;
+  for (int64_t k = lane; k < K; k += OD_WAVE) qout[k] = od_q8_one(xin[k], scale, inv);
+  if (lane == 0) s[r] = scale;
+}
+
+}  // namespace
+
+extern "C" int od_act_quant_f32(const float* x, int64_t ldx, int8_t* xq, int64_t ldq, float* sx, int64_t M,
+                                int64_t K, od_stream_t stream) {
+  if (M < 0 || K < 1 || ldx < K || ldq < K) return OD_ERR_SHAPE;
+  if (M == 0) return OD_OK;
+  if (!x || !xq || !sx) return OD_ERR_NULL;
+  constexpr int64_t kRows = kThreads / OD_WAVE;
+  const int64_t blocks = (M + kRows - 1) / kRows;
+  if (blocks > 0x7fffffff) return OD_ERR_SHAPE;
+  quant_rows_f32_kernel<<<dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream>>>(x, ldx, xq, ldq, sx, M, K);
+  return od_launch_status();
+}
+
 extern "C" int od_kv_quant_append(const uint16_t* x, int64_t B, int64_t H, int64_t n_new, int64_t D, int64_t sxb,
                                   int64_t sxh, int64_t sxt, int8_t* q, float* s, int64_t cap, int64_t n0,
                                   od_stream_t stream) {

@@ -74,6 +74,24 @@ def act_quant(x: torch.Tensor, inv_s: torch.Tensor | None = None, ld: int | None
     return xq, sx
 
 
+def act_quant_float(x: torch.Tensor):
+    """Per-row int8 quantization of a float32 / float16 / float64 x (..., K): the formula of act_quant over
+    x.float(), as the reference quantizes any dtype (quant.py:38; the conversion is exact for float16, and for
+    float64 it is the reference's own first step). Returns (xq int8 (rows, K), sx fp32 (rows,))."""
+    require_gpu(x, name="act_quant_float")
+    if x.dtype not in (torch.float32, torch.float16, torch.float64):
+        raise TypeError(f"act_quant_float: expected float32, float16 or float64, got {x.dtype}")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).float()
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    xq, sx = _quant_outputs(M, K, None, x.device, None, None)
+    check(lib().od_act_quant_f32(ptr(x2), x2.stride(0) if M > 1 else K, ptr(xq), xq.stride(0), ptr(sx), M, K,
+                                 stream_of(x)), "od_act_quant_f32")
+    return xq, sx
+
+
 def gate_act_quant(x: torch.Tensor, gate: torch.Tensor, inv_s: torch.Tensor | None = None, xq=None, sx=None):
     """Per-row int8 quantization of bf16(x * bf16(sigmoid(gate))) (the attention output times the output gate,
     prefix_attn.py:130), with the optional SmoothQuant input scale inv_s applied after the gate. x, gate (M, K) bf16

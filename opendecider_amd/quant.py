@@ -33,9 +33,12 @@ class Int8Tensor:
     def quantize(cls, x: torch.Tensor, scale_dtype: torch.dtype | None = None) -> "Int8Tensor":
         """quant.py:36-41 on the GPU. The scale is stored like the reference (x.dtype, fp32 for fp32 input) unless
         scale_dtype is given; the KV caches of this package keep it in fp32 (the value that produced q)."""
-        if x.dtype != torch.bfloat16:
-            raise TypeError("Int8Tensor.quantize: the MI355X quantizer takes bfloat16 input")
-        q, s = kernels.act_quant(x)
+        if x.dtype == torch.bfloat16:
+            q, s = kernels.act_quant(x)
+        elif x.dtype in (torch.float32, torch.float16, torch.float64):
+            q, s = kernels.act_quant_float(x)
+        else:
+            raise TypeError(f"Int8Tensor.quantize: floating-point input expected, got {x.dtype}")
         q = q.view(x.shape)
         s = s.view(*x.shape[:-1], 1)
         sd = scale_dtype or (x.dtype if x.dtype != torch.float32 else torch.float32)

@@ -24,6 +24,11 @@ def test_act_quant_and_kv_append_checks(L):
     assert L.od_act_quant(P, 8, None, P, 16, P, 4, 16, None) == SHAPE       # ldx < K
     assert L.od_act_quant(None, 16, None, P, 16, P, 4, 16, None) == NULL
     assert L.od_act_quant(None, 16, None, None, 16, None, 0, 16, None) == OK  # M = 0: nothing to do, no launch
+    assert L.od_act_quant_f32(P, 16, P, 16, P, 4, 0, None) == SHAPE             # K = 0
+    assert L.od_act_quant_f32(P, 16, P, 8, P, 4, 16, None) == SHAPE             # ldq < K
+    assert L.od_act_quant_f32(P, 16, P, 16, P, -1, 16, None) == SHAPE           # M < 0
+    assert L.od_act_quant_f32(P, 16, P, 16, None, 4, 16, None) == NULL
+    assert L.od_act_quant_f32(None, 16, None, 16, None, 0, 16, None) == OK
     # n0 + n_new past the capacity
     assert L.od_kv_quant_append(P, 1, 2, 5, 128, 1280, 640, 128, P, P, 8, 4, None) == SHAPE
     assert L.od_kv_quant_append(P, 1, 2, 5, 128, -1, 640, 128, P, P, 16, 4, None) == SHAPE  # negative stride

@@ -222,6 +222,46 @@ def test_int8_tensor_quantize_matches_reference_formula(gpu_lib):
     assert err <= x.float().abs().amax() / 127 + 1e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.float64])
+@pytest.mark.parametrize("K", [4096, 200, 1])
+def test_int8_tensor_quantize_float_inputs(gpu_lib, dtype, K):
+    """Int8Tensor.quantize of float32 / float16 / float64 input (the reference quantizes x.float() for any dtype,
+    quant.py:36-41; od_act_quant_f32): bytes and scales equal the oracle's, the scale stored in x.dtype (fp32 for
+    fp32); rows whose values sit on and next to half-integer quotients (fp32 neighbours of (n + 1/2) * scale, which
+    the fast reciprocal path alone would round wrongly on some), and NaN / inf rows as torch's rule."""
+    import numpy as np
+    from opendecider_amd.quant import Int8Tensor
+    g = torch.Generator().manual_seed(K + 17)
+    x = (torch.randn(9, K, generator=g, dtype=torch.float64) * 3).to(dtype)
+    if K >= 200:
+        amax = np.float32(x[0].float().abs().max().item())
+        scale = np.float32(amax / np.float32(127))
+        n = np.arange(-60, 60, dtype=np.float32)
+        ties = ((n + np.float32(0.5)) * scale).astype(np.float32)
+        near = np.concatenate([ties, np.nextafter(ties, np.float32(np.inf)), np.nextafter(ties, np.float32(-np.inf))])
+        near = near[: K - 1]
+        if dtype != torch.float16:
+            x[0, 1:1 + near.size] = torch.from_numpy(near).to(dtype)
+        x[2, 7] = float("nan")
+        x[3, K - 1] = float("inf")
+        x[4, 0] = float("-inf")
+    print(f"Int8Tensor.quantize {dtype} rows of K={K}", flush=True)
+    t = Int8Tensor.quantize(x.to(DEV))
+    rq, rs = oq.quantize_rows(x)
+    assert torch.equal(t.q.cpu(), rq)
+    assert t.scale.dtype == dtype and t.scale.shape == (9, 1)
+    fin = torch.isfinite(rs[:, 0])
+    assert torch.equal(t.scale.cpu()[fin], rs[fin].to(dtype))
+    if K >= 200:
+        assert torch.isnan(t.scale.cpu()[2]).all() and torch.isinf(t.scale.cpu()[[3, 4]]).all()
+    t32 = Int8Tensor.quantize(x.to(DEV), scale_dtype=torch.float32)
+    assert torch.equal(t32.scale.cpu()[fin].view(torch.int32), rs[fin].view(torch.int32))
+    empty = Int8Tensor.quantize(torch.zeros(0, K, dtype=dtype, device=DEV))
+    assert empty.q.shape == (0, K) and empty.scale.shape == (0, 1)
+    with pytest.raises(TypeError):
+        Int8Tensor.quantize(torch.zeros(2, K, dtype=torch.int32, device=DEV))
+
+
 @pytest.mark.parametrize("M,K,F", [(4096, 4096, 12288), (300, 272, 520), (77, 4096, 98), (333, 512, 1024)])
 def test_w8a8_gemm_swiglu_equals_gemm_then_swiglu(gpu_lib, M, K, F):
     """The SwiGLU epilogue gives the bytes of the plain GEMM followed by the SwiGLU kernel (shared device silu):
