@@ -158,8 +158,9 @@ def qk_norm_rope(qkv: torch.Tensor, n_heads_q: int, n_heads_k: int, D: int, q_w,
         raise ValueError("qk_norm_rope: cos/sin tables must be contiguous [positions, D/2]")
     if pos.dtype != torch.int32 or pos.numel() != M:
         raise ValueError("qk_norm_rope: pos must be int32 (M,)")
+    pos = pos.contiguous()  # held across the call
     check(lib().od_qk_norm_rope(ptr(qkv), qkv.stride(0), M, n_heads_q, n_heads_k, D, ptr(q_w), ptr(k_w),
-                                ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos.contiguous()), float(eps),
+                                ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos), float(eps),
                                 stream_of(qkv)),
           "od_qk_norm_rope")
 
@@ -178,6 +179,7 @@ def qk_norm_rope_kv_append(qkv: torch.Tensor, B: int, S: int, n_heads_q: int, n_
         raise ValueError("qk_norm_rope_kv_append: cos/sin tables must be contiguous [positions, D/2]")
     if pos.dtype != torch.int32 or pos.numel() != B * S:
         raise ValueError("qk_norm_rope_kv_append: pos must be int32 (B S,)")
+    pos = pos.contiguous()  # held across the call
     n0 = k_cache.length
     if v_cache.length != n0 or k_cache.q.shape != (B, n_heads_k, k_cache.capacity, D) or \
             v_cache.q.shape != k_cache.q.shape:
@@ -185,7 +187,7 @@ def qk_norm_rope_kv_append(qkv: torch.Tensor, B: int, S: int, n_heads_q: int, n_
     if n0 + S > k_cache.capacity:
         raise ValueError(f"qk_norm_rope_kv_append: {n0} + {S} tokens exceed the capacity {k_cache.capacity}")
     check(lib().od_qk_norm_rope_kv_append(ptr(qkv), qkv.stride(0), B, S, n_heads_q, n_heads_k, D, ptr(q_w), ptr(k_w),
-                                          ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos.contiguous()), float(eps),
+                                          ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos), float(eps),
                                           ptr(k_cache.q), ptr(k_cache.scale), ptr(v_cache.q), ptr(v_cache.scale),
                                           k_cache.capacity, n0, stream_of(qkv)),
           "od_qk_norm_rope_kv_append")
