@@ -709,6 +709,14 @@ __device__ __forceinline__ void staged_step(const BlockImg<D>& cur, const uint16
   for (int ks = 0; ks < KA; ++ks) kread(ks);
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
+    // this k-step's key multipliers are read ahead of the next k-step's K fragments, so that waiting for them
+    // leaves those fragments in flight
+    float4 g4s[kPerStep];
+#pragma unroll
+    for (int c = 0; c < kPerStep; ++c) {
+      const int grp = ks * kPerStep + c, kt = grp / 4, r4 = grp % 4;
+      g4s[c] = *reinterpret_cast<const float4*>(&cur.gk[kt * 32 + 8 * r4 + 4 * h]);
+    }
     if (ks + KA < KS) kread(ks + KA);
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
@@ -717,7 +725,7 @@ __device__ __forceinline__ void staged_step(const BlockImg<D>& cur, const uint16
 #pragma unroll
     for (int c = 0; c < kPerStep; ++c) {
       const int grp = ks * kPerStep + c, kt = grp / 4, r4 = grp % 4;
-      const float4 g4 = *reinterpret_cast<const float4*>(&cur.gk[kt * 32 + 8 * r4 + 4 * h]);
+      const float4 g4 = g4s[c];
       const float gg[4] = {g4.x, g4.y, g4.z, g4.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
