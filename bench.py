@@ -210,18 +210,20 @@ def stage_work(*a):
     return (0, 0)
 
 
-ATTN_KERNELS = "od_attn_stage + od_branched_attn_staged (or od_branched_attn / od_branched_attn_split)"
+ATTN_KERNELS = ("od_attn_stage + od_branched_attn_staged (or od_branched_attn / od_branched_attn_split / "
+                "od_branched_attn_stream)")
 
 
 class AttnTimers:
     """The branched attention's entry points timed together: od_branched_attn and od_branched_attn_split (direct
-    path), od_attn_stage and od_branched_attn_staged (staged path)."""
+    path), od_attn_stage and od_branched_attn_staged (staged path), od_branched_attn_stream (few slots)."""
 
     def __init__(self, every=1):
         # one stage and one attention call per layer: the same `every` times both on the same layers
         self.timers = [AbiTimer("od_branched_attn", attn_work, every), AbiTimer("od_attn_stage", stage_work, every),
                        AbiTimer("od_branched_attn_staged", staged_work, every),
-                       AbiTimer("od_branched_attn_split", attn_work, every)]  # same leading arguments
+                       AbiTimer("od_branched_attn_split", attn_work, every),  # same leading arguments
+                       AbiTimer("od_branched_attn_stream", attn_work, every)]
 
     @property
     def active(self):
@@ -933,7 +935,8 @@ def run_attention(args):
     g = torch.Generator(device=dev).manual_seed(5)
     Hq, Hkv, t, D = 32, 8, 16, 128
     res = {}
-    for name, Ns, rows, T in (("config1", 8, 32, 2048), ("kv_probe", 8, 2, 32768)):
+    for name, Ns, rows, T, t in (("config1", 8, 32, 2048, 16), ("kv_probe", 8, 2, 32768, 16),
+                                 ("kv_stream", 8, 2, 32768, 2)):
         R = Ns * rows
         q = torch.randn(R, Hq, t, D, device=dev, generator=g).to(torch.bfloat16)
         k = torch.randn(R, Hkv, t, D, device=dev, generator=g).to(torch.bfloat16)
@@ -965,7 +968,8 @@ def run_attention(args):
                      "kv_gbs": kv_bytes / (ms / n * 1e-3) / 1e9,
                      "kv_frac_of_hbm": kv_bytes / (ms / n * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "algorithmic_gbs": by / (ms * 1e-3) / 1e9, "launches": n,
-                     "path": "staged" if kernels.uses_staging(rows, t, Hq, Hkv) else "direct"}
+                     "path": ("stream" if rows * t * (Hq // Hkv) <= kernels.STREAM_MAX_SLOTS else
+                              "staged" if kernels.uses_staging(rows, t, Hq, Hkv) else "direct")}
     out = {"metric": "branched attention: KV GB/s on the KV-bound probe (TFLOP/s on the config-1 shape beside it)",
            "value": res["kv_probe"]["kv_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": res["kv_probe"]["avg_launch_us"] / 1e3, "higher_is_better": True,

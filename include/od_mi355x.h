@@ -238,6 +238,29 @@ int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t 
                            od_stream_t stream);
 
 /*
+ * od_branched_attn_stream — od_branched_attn_split for the few-slot case: every (state, KV head) carries at most 32
+ * query slots (max_rows * t * Hq / Hkv <= 32, e.g. a yes/no decision of 2 options x 2 tokens over a long state), and
+ * the attention is bound by reading the int8 state. One wave holds all slots of its (state, head) and streams the
+ * int8 K/V from memory into registers 32 keys at a time, dequantized there as `dequant` says (no block images, no
+ * LDS staging); P enters the P.V product as two bf16 parts (hi + lo). Each slot's result depends on its own scores
+ * only (option order cannot change it); results agree with od_branched_attn to the attention bar, not bit for bit.
+ * Replaces: the same reference code as od_branched_attn (prefix_attn.py:43-76 with Kp/Vp materialized at :145-149).
+ *   D          128 only (else OD_ERR_UNSUPPORTED); more than 32 slots per (state, head): OD_ERR_UNSUPPORTED
+ *   ks, vs     16-byte aligned when T > 0
+ *   nsplit, ws as od_branched_attn_split (the keys of a (state, head) split over nsplit workgroups of 4 waves)
+ * Other arguments and the result as od_branched_attn_split. One launch, plus the merge when nsplit > 1.
+ */
+int od_branched_attn_stream(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                            const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                            const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                            const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
+                            const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
+                            uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
+                            int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T,
+                            int64_t cap, float scale, int dequant, int64_t nsplit, float* ws, int64_t ws_floats,
+                            od_stream_t stream);
+
+/*
  * od_branched_attn_split_noalloc — od_branched_attn_split without a workspace argument and without any allocation:
  * the per-split partials go to a static device array inside the library (OD_SPLIT_SCRATCH_FLOATS floats = 64 MiB per
  * GPU, held from the first call until the process ends). No counterpart in the reference: it is for callers that

@@ -33,6 +33,10 @@ SIGNATURES = {
                                _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64,
                                _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _i64,
                                _c_ptr, _i64, _c_ptr],
+    "od_branched_attn_stream": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
+                                _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64,
+                                _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int,
+                                _i64, _c_ptr, _i64, _c_ptr],
     "od_branched_attn_split_noalloc": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64,
                                        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64,
                                        _i64, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -1446,3 +1446,413 @@ extern "C" int od_branched_attn_staged2(const uint16_t* q, int64_t sqr, int64_t 
                          nullptr, nullptr, T > 0 ? img : nullptr, row_start, max_rows, out, sor, soh, sot, lse, R,
                          Hq, Hkv, t, D, n_groups, T, T, scale, OD_DEQUANT_BF16, nsplit, ws, ws_floats, stream, &l2);
 }
+
+// ================================================================================================ KV streaming
+// od_branched_attn_stream: the few-slot case. When every (state, KV head) carries at most 32 query slots (a few
+// short option rows, e.g. a yes/no decision over a long state), the attention does 32 x 4 FLOP per state key and
+// dimension against 2 bytes of int8 K/V, so it is bound by reading the state from HBM, and the block-image paths
+// (LDS images, 128-slot tiles) leave most of their MFMA columns and conversion work idle. Here one wave takes all
+// slots of its (state, head) and streams the state's int8 K/V straight from HBM into registers, 32 keys per tile,
+// one tile ahead, converting there (no LDS until the end); a workgroup's 4 waves take interleaved tiles of one
+// key range, the key range of each (state, head) is split over workgroups (nsplit), and partials are merged by
+// log-sum-exp (combine_kernel).
+//
+// Per tile (keys kb .. kb + 31), lane l = 32 h + c of a wave:
+//  * scores S^T = K' Q^T on V_MFMA_F32_32X32X16_BF16, 8 k-steps; k-step ks takes dims 64 h + 8 ks .. +7 of both
+//    operands (a permutation of the reduction index, applied to both sides). The lane loads 64 contiguous bytes of
+//    key kb + c (its A row) and converts them: K' = bf16(q bf16(ks_j)) (OD_DEQUANT_BF16) or the exact integer q
+//    (OD_DEQUANT_FP32, the key's fp32 multiplier then goes on the score). In the result lane l holds slot c and
+//    keys 8 r + 4 h + j (register 4 r + j), so the online softmax is lane-local plus one exchange with lane l ^ 32;
+//  * values O^T += V'^T P^T: k-step m (keys 16 m .. 16 m + 15) takes P registers 8 m .. 8 m + 7 as its B operand,
+//    so the A operand of lane (c, h) holds value d of the keys 8 r + 4 h + j in that order. Output row c of d
+//    block db is d = 4 c + db: the lane reads dword 4 c .. 4 c + 3 of each of its 16 keys (lanes 0..31 read one
+//    key's 128 bytes, lanes 32..63 another), and byte db of each is element db's value. V' = bf16(q bf16(vs_j))
+//    (exact bf16) or, OD_DEQUANT_FP32, the integer q with vs_j folded into the probability;
+//  * P goes to the P.V product as two bf16 parts, hi = bf16(p) and lo = bf16(p - hi) (16 significant bits, two
+//    MFMAs per k-step): V' is exactly the reference's bf16 value and P keeps fp16-level precision. The row sum is
+//    taken on the unrounded fp32 p.
+// The row's own keys (at most 32: rows x t <= slots) are one extra masked tile of bf16 K/V, taken by wave 0 of the
+// last split. Each slot's arithmetic depends only on its own scores, so option order cannot change a result.
+namespace {
+
+constexpr int kStrWaves = 4;
+constexpr int kStrKeys = 32;
+constexpr int kStrD = 128;
+
+struct StrTile {
+  uint4 k[4];      // lane (key c, half h): int8 bytes 64 h + 16 i .. +16 of key kb + c
+  uint32_t v[16];  // lane (c, h): V bytes 4 c .. 4 c + 3 of key kb + 8 (i / 4) + 4 h + i % 4
+  float vs, ks;    // V and K scales of key kb + c
+  int valid;       // key kb + c exists (and is not masked by kvalid)
+};
+
+// The per-wave LDS of the streaming kernel: a tile's per-key factors, written by the lane that loaded key c and
+// read back in the score layout (keys 8 r + 4 h + 0..3 as one float4 per r).
+struct StrKeyLds {
+  float4 f[2][8];  // [0]: V factor (bf16(vs) or vs), [1]: score multiplier (OD_DEQUANT_FP32: ks scale log2(e))
+};
+
+template <int DQ>
+__device__ __forceinline__ void str_load(const PrefixSrc& src, int kb, int T, int h, int c, StrTile& tl) {
+  const int sk = kb * kStrD;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    tl.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.k, c * kStrD + 64 * h + 16 * i, sk, 0));
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    tl.v[i] = __builtin_amdgcn_raw_buffer_load_b32(src.v, 4 * c + 512 * h + (8 * (i >> 2) + (i & 3)) * kStrD, sk, 0);
+  tl.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.vs, c * 4, kb * 4, 0));
+  tl.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.ks, c * 4, kb * 4, 0));
+  tl.valid = kb + c < T;
+  if (src.has_valid) tl.valid = tl.valid && __builtin_amdgcn_raw_buffer_load_b8(src.valid, c, kb, 0) != 0;
+}
+
+__device__ __forceinline__ float f4_at(const float4& v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
+
+// int8 byte b of w, times an fp32 factor
+__device__ __forceinline__ float byte_times(uint32_t w, int b, float f) { return (float)(int8_t)((w >> (8 * b)) & 0xffu) * f; }
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((od_f32x2){a, b}, od_bf16x2));
+}
+
+// The queries of the wave's 32 slots in LDS, read per k-step (lane (c, h) of k-step ks: slot c, dims
+// 64 h + 8 ks .. +7); the row stride of 272 bytes puts 16 consecutive slots on 16 distinct bank quads.
+constexpr int kStrQRow = kStrD + 8;
+
+// One tile's online-softmax update and P.V product. y: the lane's 16 scores in log2 units (-inf: masked); pw: a
+// factor on p for the P.V product only (the fp32 path's V scales); vf(m, db): the V'^T A operand of k-step m and d
+// block db.
+template <bool PW, class VF>
+__device__ __forceinline__ void str_update(float (&y)[16], const float (&pw)[16], float& m_run, float& l_run,
+                                           v16f (&o)[4], VF&& vf) {
+  float mx = y[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) mx = fmaxf(mx, y[i]);
+  mx = od_xor32_max(mx);
+  const bool move = mx > m_run + kSlack;  // lazy: p = exp2(y - m) <= 2^kSlack otherwise
+  if (__builtin_amdgcn_ballot_w64(move) != 0) {
+    const float a = move ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;  // m_run = -inf: 0
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][i] *= a;
+    l_run *= a;
+    if (move) m_run = mx;
+  }
+  const float msub = m_run == -INFINITY ? 0.0f : m_run;
+  float p[16];
+  float ls = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    p[i] = __builtin_amdgcn_exp2f(y[i] - msub);
+    ls += p[i];
+  }
+  l_run += ls;
+  bf16x8 bh[2], bl[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = PW ? p[8 * m + 2 * e] * pw[8 * m + 2 * e] : p[8 * m + 2 * e];
+      const float b = PW ? p[8 * m + 2 * e + 1] * pw[8 * m + 2 * e + 1] : p[8 * m + 2 * e + 1];
+      hw[e] = pk_bf16(a, b);
+      lw[e] = pk_bf16(a - __uint_as_float(hw[e] << 16), b - __uint_as_float(hw[e] & 0xffff0000u));
+    }
+    bh[m] = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+    bl[m] = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const bf16x8 a = vf(m, db);
+      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bh[m], o[db], 0, 0, 0);
+      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bl[m], o[db], 0, 0, 0);
+    }
+}
+
+__device__ __forceinline__ bf16x8 str_q(const uint16_t* qs, int c, int h, int ks) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qs + c * kStrQRow + 64 * h + 8 * ks));
+}
+
+template <int DQ>
+__device__ __forceinline__ void str_state_tile(const StrTile& tl, const uint16_t* qs, StrKeyLds& kl, float c2, int h,
+                                               int c, float& m_run, float& l_run, v16f (&o)[4]) {
+  // the tile's per-key factors through LDS into the score layout (in-order LDS access within the wave)
+  if (h == 0) {
+    reinterpret_cast<float*>(kl.f[0])[c] = DQ == OD_DEQUANT_BF16 ? bf16_round(tl.vs) : tl.vs;
+    if constexpr (DQ == OD_DEQUANT_FP32) reinterpret_cast<float*>(kl.f[1])[c] = tl.ks * c2;
+  }
+  v16f s = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  const float sk = DQ == OD_DEQUANT_BF16 ? bf16_round(tl.ks) : 0.0f;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const uint32_t w0 = (ks & 1) ? tl.k[ks >> 1].z : tl.k[ks >> 1].x;
+    const uint32_t w1 = (ks & 1) ? tl.k[ks >> 1].w : tl.k[ks >> 1].y;
+    uint4 a;
+    if constexpr (DQ == OD_DEQUANT_BF16) {
+      i8x4_times_bf16(w0, sk, a.x, a.y);
+      i8x4_times_bf16(w1, sk, a.z, a.w);
+    } else {
+      i8x4_to_bf16(w0, a.x, a.y);
+      i8x4_to_bf16(w1, a.z, a.w);
+    }
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), str_q(qs, c, h, ks), s, 0, 0, 0);
+  }
+  // masked keys (past the state's length or masked by kvalid): bit k of the ballot is key kb + k
+  const uint32_t vm = (uint32_t)__builtin_amdgcn_ballot_w64(tl.valid != 0);
+  float y[16], f[16];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float4 fv = kl.f[0][2 * r + h];
+    float4 gk = make_float4(c2, c2, c2, c2);
+    if constexpr (DQ == OD_DEQUANT_FP32) gk = kl.f[1][2 * r + h];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      y[4 * r + j] = s[4 * r + j] * f4_at(gk, j);
+      f[4 * r + j] = f4_at(fv, j);
+    }
+  }
+  if (vm != 0xffffffffu) {
+    const uint32_t bits = vm >> (4 * h);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (!((bits >> (8 * (i >> 2) + (i & 3))) & 1u)) y[i] = -INFINITY;
+  }
+  auto vf = [&](int m, int db) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i0 = 8 * m + 2 * e, i1 = i0 + 1;
+      if constexpr (DQ == OD_DEQUANT_BF16)
+        w[e] = pk_bf16(byte_times(tl.v[i0], db, f[i0]), byte_times(tl.v[i1], db, f[i1]));
+      else
+        w[e] = pk_bf16(byte_times(tl.v[i0], db, 1.0f), byte_times(tl.v[i1], db, 1.0f));
+    }
+    return __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+  };
+  str_update<DQ == OD_DEQUANT_FP32>(y, f, m_run, l_run, o, vf);
+}
+
+template <int DQ>
+__global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
+  constexpr int D = kStrD;
+  // the queries (while the tiles run), then the waves' accumulators for the merge
+  __shared__ __attribute__((aligned(16))) union {
+    uint16_t q[32 * kStrQRow];
+    float o[kStrWaves][32][D + 4];
+  } sm;
+  __shared__ float sml[kStrWaves][2][32];
+  __shared__ StrKeyLds skl[kStrWaves];
+  const int sp = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+  const int row0 = p.row_start ? p.row_start[s] : 0;
+  const int nrows = p.row_start ? p.row_start[s + 1] - row0 : p.R;
+  const int per_row = p.t * p.rep;
+  const int nslots = nrows * per_row;
+  if (nslots <= 0) return;  // uniform over the workgroup
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, c = lane & 31;
+  const bool slot_ok = c < nslots;
+  int rl = 0, tok = 0;
+  if (slot_ok) {
+    rl = c / per_row;
+    tok = (c - rl * per_row) / p.rep;
+  }
+  {
+    // thread: slot z = tid / 8, dims 16 (tid % 8) .. +15
+    const int z = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 16;
+    uint4 a = make_uint4(0, 0, 0, 0), b = a;
+    if (z < nslots) {
+      const int zr = z / per_row, zrem = z - zr * per_row;
+      const uint16_t* qp = p.q + (int64_t)(row0 + zr) * p.sqr + (int64_t)(g * p.rep + zrem % p.rep) * p.sqh +
+                           (int64_t)(zrem / p.rep) * p.sqt + d0;
+      a = *reinterpret_cast<const uint4*>(qp);
+      b = *reinterpret_cast<const uint4*>(qp + 8);
+    }
+    *reinterpret_cast<uint4*>(sm.q + z * kStrQRow + d0) = a;
+    *reinterpret_cast<uint4*>(sm.q + z * kStrQRow + d0 + 8) = b;
+  }
+  __syncthreads();
+  float m_run = -INFINITY, l_run = 0.0f;
+  v16f o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+  // ---- the state's tiles of this split: [t_lo, t_hi), wave w takes t_lo + w, t_lo + w + 4, ...
+  const int n_tiles = (p.T + kStrKeys - 1) / kStrKeys;
+  const int tps = (n_tiles + p.nsplit - 1) / p.nsplit;
+  const int t_lo = min(n_tiles, sp * tps), t_hi = min(n_tiles, t_lo + tps);
+  const PrefixSrc src = prefix_src<D>(p.kq, p.ks, p.vq, p.vs, p.kvalid, p.Hkv, p.T, p.cap, s, g);
+  int tt = t_lo + wave;
+  if (tt < t_hi) {
+    StrTile ta, tb;
+    str_load<DQ>(src, tt * kStrKeys, p.T, h, c, ta);
+    // two tiles per trip, so that the loads of the next tile go into the other register set without copies
+    for (;; tt += 2 * kStrWaves) {
+      const bool more1 = tt + kStrWaves < t_hi;
+      if (more1) str_load<DQ>(src, (tt + kStrWaves) * kStrKeys, p.T, h, c, tb);
+      str_state_tile<DQ>(ta, sm.q, skl[wave], p.scale_log2, h, c, m_run, l_run, o);
+      if (!more1) break;
+      const bool more2 = tt + 2 * kStrWaves < t_hi;
+      if (more2) str_load<DQ>(src, (tt + 2 * kStrWaves) * kStrKeys, p.T, h, c, ta);
+      str_state_tile<DQ>(tb, sm.q, skl[wave], p.scale_log2, h, c, m_run, l_run, o);
+      if (!more2) break;
+    }
+  }
+
+  // ---- the rows' own keys: one masked tile of bf16 K/V (key k = row k / t, token k % t), wave 0 of the last split
+  if (sp == p.nsplit - 1 && wave == 0) {
+    const int n_own = nrows * p.t;
+    v16f sc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    {
+      const bool kok = c < n_own;
+      const int kr = kok ? c / p.t : 0, kj = kok ? c % p.t : 0;
+      const uint16_t* kp = p.k_own + (int64_t)(row0 + kr) * p.skr + (int64_t)g * p.skh + (int64_t)kj * p.skt + 64 * h;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, kok ? *reinterpret_cast<const uint4*>(kp + 8 * ks) : make_uint4(0, 0, 0, 0)),
+            str_q(sm.q, c, h, ks), sc, 0, 0, 0);
+    }
+    uint2 vo[16];
+    float y[16], one[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kk = 8 * (i >> 2) + 4 * h + (i & 3);  // own key of score register i
+      const bool vis = slot_ok && kk < n_own && kk >= rl * p.t && kk <= rl * p.t + tok;
+      y[i] = vis ? sc[i] * p.scale_log2 : -INFINITY;
+      one[i] = 1.0f;
+      vo[i] = make_uint2(0, 0);
+      if (kk < n_own) {
+        const int kr = kk / p.t, kj = kk % p.t;
+        vo[i] = *reinterpret_cast<const uint2*>(p.v_own + (int64_t)(row0 + kr) * p.svr + (int64_t)g * p.svh +
+                                                (int64_t)kj * p.svt + 4 * c);
+      }
+    }
+    auto vf = [&](int m, int db) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint2 a = vo[8 * m + 2 * e], b = vo[8 * m + 2 * e + 1];
+        const uint32_t xa = db < 2 ? a.x : a.y, xb = db < 2 ? b.x : b.y;
+        w[e] = (db & 1) ? ((xa >> 16) | (xb & 0xffff0000u)) : ((xa & 0xffffu) | (xb << 16));
+      }
+      return __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+    };
+    str_update<false>(y, one, m_run, l_run, o, vf);
+  }
+
+  // ---- merge the 4 waves (LDS), then this split's normalized partial + LSE, or the output
+  const float l_tot = od_xor32_sum(l_run);
+  __syncthreads();  // every wave is done with the queries: their LDS now takes the accumulators
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<float4*>(&sm.o[wave][c][32 * r + 16 * h + 4 * j]) =
+          make_float4(o[0][4 * r + j], o[1][4 * r + j], o[2][4 * r + j], o[3][4 * r + j]);
+  if (h == 0) {
+    sml[wave][0][c] = m_run;
+    sml[wave][1][c] = l_tot;
+  }
+  __syncthreads();
+  const int z = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 16;
+  if (z >= nslots) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kStrWaves; ++w) M = fmaxf(M, sml[w][0][z]);
+  float L = 0.0f, acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int w = 0; w < kStrWaves; ++w) {
+      const float mw = sml[w][0][z];
+      if (mw == -INFINITY) continue;
+      const float a = __builtin_amdgcn_exp2f(mw - M);
+      L += a * sml[w][1][z];
+#pragma unroll
+      for (int e = 0; e < 16; e += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&sm.o[w][z][d0 + e]);
+        acc[e] += a * v.x; acc[e + 1] += a * v.y; acc[e + 2] += a * v.z; acc[e + 3] += a * v.w;
+      }
+    }
+  }
+  const int zr = z / per_row, zrem = z - zr * per_row;
+  const int64_t slot_idx = ((int64_t)(row0 + zr) * p.Hq + g * p.rep + zrem % p.rep) * p.t + zrem / p.rep;
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  const float lse_v = L > 0.0f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+  if (p.nsplit > 1) {
+    const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
+    float* po = p.part + ((int64_t)sp * nsl + slot_idx) * D + d0;
+#pragma unroll
+    for (int e = 0; e < 16; e += 4)
+      *reinterpret_cast<float4*>(po + e) = make_float4(acc[e] * inv, acc[e + 1] * inv, acc[e + 2] * inv, acc[e + 3] * inv);
+    if (d0 == 0) p.part[(int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx] = lse_v;
+    return;
+  }
+  uint16_t* op = p.out + (int64_t)(row0 + zr) * p.sor + (int64_t)(g * p.rep + zrem % p.rep) * p.soh +
+                 (int64_t)(zrem / p.rep) * p.sot + d0;
+#pragma unroll
+  for (int e = 0; e < 16; e += 4)
+    *reinterpret_cast<uint2*>(op + e) = make_uint2(pk_bf16(acc[e] * inv, acc[e + 1] * inv),
+                                                   pk_bf16(acc[e + 2] * inv, acc[e + 3] * inv));
+  if (p.lse && d0 == 0) p.lse[slot_idx] = lse_v;
+}
+
+}  // namespace
+
+extern "C" int od_branched_attn_stream(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
+                                       const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
+                                       const uint16_t* v_own, int64_t svr, int64_t svh, int64_t svt,
+                                       const int8_t* kq, const float* ks, const int8_t* vq, const float* vs,
+                                       const uint8_t* kvalid, const int32_t* row_start, int64_t max_rows,
+                                       uint16_t* out, int64_t sor, int64_t soh, int64_t sot, float* lse,
+                                       int64_t R, int64_t Hq, int64_t Hkv, int64_t t, int64_t D, int64_t Ns,
+                                       int64_t T, int64_t cap, float scale, int dequant, int64_t nsplit, float* ws,
+                                       int64_t ws_floats, od_stream_t stream) {
+  if (dequant != OD_DEQUANT_BF16 && dequant != OD_DEQUANT_FP32) return OD_ERR_UNSUPPORTED;
+  if (R < 0 || Hq < 1 || Hkv < 1 || t < 1 || Ns < 1 || T < 0 || cap < T || max_rows < 0) return OD_ERR_SHAPE;
+  if (Hq % Hkv || D != kStrD) return OD_ERR_UNSUPPORTED;
+  if (!row_start && Ns != 1) return OD_ERR_SHAPE;
+  if (nsplit < 1 || nsplit > 256) return OD_ERR_SHAPE;
+  if (!row_start) max_rows = R;
+  const int64_t rep = Hq / Hkv;
+  if (max_rows * t * rep > 32) return OD_ERR_UNSUPPORTED;  // one wave holds all slots of a (state, head)
+  if (R == 0 || max_rows == 0) return OD_OK;
+  if (!q || !k_own || !v_own || !out) return OD_ERR_NULL;
+  if (T > 0 && (!kq || !ks || !vq || !vs)) return OD_ERR_NULL;
+  if (nsplit > 1) {
+    if (!ws) return OD_ERR_NULL;
+    if (ws_floats < nsplit * R * Hq * t * (D + 1)) return OD_ERR_SHAPE;
+    if (!od_aligned16(ws)) return OD_ERR_ALIGN;
+  }
+  const int64_t strides[] = {sqr, sqh, sqt, skr, skh, skt, svr, svh, svt};
+  for (int64_t st : strides)
+    if (st < 0 || st % 8) return OD_ERR_ALIGN;
+  if (sor < 0 || soh < 0 || sot < 0 || sor % 4 || soh % 4 || sot % 4) return OD_ERR_ALIGN;
+  if (!od_aligned16(q) || !od_aligned16(k_own) || !od_aligned16(v_own) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
+  if (T > 0 && (!od_aligned16(kq) || !od_aligned16(vq) || !od_aligned16(ks) || !od_aligned16(vs))) return OD_ERR_ALIGN;
+  if (Hkv > 65535 || Ns > 65535 || R * t * rep > 0x7fffffff || cap * Hkv * Ns * D > (1ll << 40) ||
+      nsplit * R * Hq * t * (D + 1) > (1ll << 40) || T * D >= (1ll << 31))
+    return OD_ERR_SHAPE;
+  AttnArgs a{q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, lse, sqr, sqh, sqt, skr, skh, skt, svr, svh,
+             svt, sor, soh, sot, (int)R, (int)Hq, (int)Hkv, (int)t, (int)Ns, (int)T, (int)cap, (int)rep,
+             scale * 1.4426950408889634f, dequant, (int)nsplit, nsplit > 1 ? ws : nullptr, nullptr, nullptr,
+             nullptr, 0, (int)Ns};
+  dim3 grid((unsigned)nsplit, (unsigned)Hkv, (unsigned)Ns), block(kStrWaves * 64);
+  hipStream_t st = (hipStream_t)stream;
+  if (dequant == OD_DEQUANT_BF16)
+    stream_kernel<OD_DEQUANT_BF16><<<grid, block, 0, st>>>(a);
+  else
+    stream_kernel<OD_DEQUANT_FP32><<<grid, block, 0, st>>>(a);
+  if (nsplit > 1) {
+    const int rc = od_launch_status();
+    if (rc != OD_OK) return rc;
+    const int64_t threads = R * Hq * t * (D / 8);
+    combine_kernel<128><<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(a);
+  }
+  return od_launch_status();
+}

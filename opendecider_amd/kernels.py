@@ -363,6 +363,18 @@ def split_count(slot_tiles: int, T: int, target_workgroups: int = 1024, min_bloc
     return max(1, min(-(-target_workgroups // max(slot_tiles, 1)), blocks // min_blocks, 256))
 
 
+# The KV-streaming kernel (od_branched_attn_stream): one wave holds every query slot of a (state, head).
+STREAM_D = 128
+STREAM_MAX_SLOTS = 32
+
+
+def stream_split_count(Ns: int, Hkv: int, T: int, target_workgroups: int = 512, min_tiles: int = 8) -> int:
+    """Key-range splits for od_branched_attn_stream: about two 4-wave workgroups per CU over all (state, head)
+    pairs, keeping at least `min_tiles` 32-key tiles (two per wave) in each split."""
+    tiles = (T + 31) // 32
+    return max(1, min(-(-target_workgroups // max(Ns * Hkv, 1)), tiles // min_tiles, 256))
+
+
 # The staged path writes each state block's image (twice the int8 bytes) once and lets every slot tile copy it
 # instead of converting it; it pays off when several tiles read each (state, head).
 STAGE_MIN_TILES = 4
@@ -501,7 +513,8 @@ def uses_staging(max_rows: int, t: int, n_heads_q: int, n_heads_k: int) -> bool:
 
 def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, row_counts=None, length=None,
                   out=None, return_lse: bool = False, row_start=None, max_rows=None, n_split=None, staged=None,
-                  stage_buf=None, dequant: str = "bf16", images=None, static_workspace: bool = False):
+                  stage_buf=None, dequant: str = "bf16", images=None, static_workspace: bool = False,
+                  stream=None):
     """Branched option-row attention over int8 states. q (R, Hq, t, D) bf16; k_own/v_own (R, Hkv, t, D) bf16;
     kq/vq (Ns, Hkv, cap, D) int8 of which the first T tokens are used (T = `length`, else kvalid.shape[1], else
     cap); ks/vs (Ns, Hkv, cap) fp32; kvalid (Ns, T) bool/uint8 or None.
@@ -515,7 +528,10 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
     caller keeps them valid). dequant: "bf16", the reference's materialize bf16(q * bf16(s)) (quant.py:45,
     prefix_attn.py:145-149), or "fp32", the exact q * s. static_workspace: the direct path's split partials go to
     the library's static scratch (od_branched_attn_split_noalloc: nothing is allocated for them; calls on one GPU
-    must not overlap). Returns out (R, Hq, t, D) bf16 [, lse (R, Hq, t) fp32]."""
+    must not overlap). stream: the KV-streaming kernel for at most 32 query slots per (state, head)
+    (od_branched_attn_stream, head_dim 128); None takes it when the caller chose no other path (staged, images and
+    static_workspace left at their defaults) and the shape allows it. Returns out (R, Hq, t, D) bf16
+    [, lse (R, Hq, t) fp32]."""
     require_gpu(q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, name="branched_attn")
     for x in (q, k_own, v_own):
         _lib.bf16_bits(x)
@@ -554,7 +570,23 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
     q, k_own, v_own = _rows_aligned(q), _rows_aligned(k_own), _rows_aligned(v_own)
     out = _check_out(out, (R, Hq, t, D), q.device, "branched_attn")
     lse = torch.empty(R, Hq, t, dtype=torch.float32, device=q.device) if return_lse else None
-    tiles = -(-(int(max_rows) * t * (Hq // Hkv)) // 128)  # slot tiles per (state, head)
+    slots = int(max_rows) * t * (Hq // Hkv)  # query slots per (state, head)
+    if stream is None:
+        stream = (staged is None and images is None and not static_workspace and D == STREAM_D
+                  and slots <= STREAM_MAX_SLOTS and T > 0)
+    if stream:
+        if D != STREAM_D or slots > STREAM_MAX_SLOTS:
+            raise ValueError(f"branched_attn: the streaming kernel takes head_dim {STREAM_D} and at most "
+                             f"{STREAM_MAX_SLOTS} slots per (state, head), not D={D} with {slots}")
+        nsp = stream_split_count(Ns, Hkv, T) if n_split is None else int(n_split)
+        ws = torch.empty(nsp * R * Hq * t * (D + 1), dtype=torch.float32, device=q.device) if nsp > 1 else None
+        check(lib().od_branched_attn_stream(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
+                                            *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
+                                            ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R,
+                                            Hq, Hkv, t, D, Ns, T, cap, float(scale), dq, nsp, ptr(ws),
+                                            0 if ws is None else ws.numel(), stream_of(q)), "od_branched_attn_stream")
+        return (out, lse) if return_lse else out
+    tiles = -(-slots // 128)  # slot tiles per (state, head)
     if n_split is None:
         n_split = split_count(tiles * Hkv * Ns, T)
     if staged is None:

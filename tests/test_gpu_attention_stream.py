@@ -1,0 +1,113 @@
+"""GPU parity of the KV-streaming branched attention (od_branched_attn_stream: at most 32 query slots per (state,
+KV head), the int8 state streamed from memory into registers) against the oracle.
+
+Bar, as for the block-image paths: outputs within 2e-3 relative of the oracle (the three forms in tests/helpers.py)
+in both dequantization modes (the reference's bf16 materialize, quant.py:45 / prefix_attn.py:145-149, and the exact
+fp32 q * s), natural-log LSE within 1e-4 absolute, option-row order invariance bitwise. Cases cover lengths that are
+not a multiple of the 32-key tile, capacity past the length (garbage that must not be read), masked keys, states
+without rows, a state of length 0 (own keys only), GQA 1..8, V scales over 17 binades, key-range splits from 1 to
+more splits than tiles, and the few-slot probe shape at its full 32768-key length.
+"""
+import pytest
+import torch
+
+from helpers import assert_close_rel
+from test_gpu_attention import make_case, run_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+CASES = {
+    # yes/no: 2 options x 2 tokens, 4 query heads per KV head: 16 slots per (state, head)
+    "yes_no_T5000": dict(seed=21, Ns=4, row_counts=[2, 2, 2, 2], Hq=32, Hkv=8, t=2, D=128, T=5000),
+    "one_row_8tok_holes": dict(seed=22, Ns=2, row_counts=[1, 1], Hq=32, Hkv=8, t=8, D=128, T=3000, holes=True),
+    "ragged_rows_cap": dict(seed=23, Ns=3, row_counts=[3, 0, 1], Hq=8, Hkv=2, t=2, D=128, T=777, cap=900),
+    "gqa1_t6": dict(seed=24, Ns=1, row_counts=[5], Hq=4, Hkv=4, t=6, D=128, T=100),
+    "own_only_T0": dict(seed=25, Ns=1, row_counts=[2], Hq=8, Hkv=2, t=3, D=128, T=0),
+    "v_frames_spread": dict(seed=26, Ns=2, row_counts=[2, 1], Hq=8, Hkv=2, t=4, D=128, T=1500, vspread=True),
+    "t1_single_token": dict(seed=27, Ns=2, row_counts=[4, 3], Hq=8, Hkv=8, t=1, D=128, T=257),
+    "short_state_T31": dict(seed=28, Ns=1, row_counts=[2], Hq=32, Hkv=8, t=4, D=128, T=31),
+}
+
+
+def run_stream(c, n_split=None, dequant="bf16", q=None, perm=None):
+    from opendecider_amd import kernels
+    Ns = c["kq"].shape[0]
+    take = (lambda x: x) if perm is None else (lambda x: x[perm])
+    return kernels.branched_attn(
+        take(c["q"]).to(DEV) if q is None else q, take(c["k"]).to(DEV), take(c["v"]).to(DEV), c["kq"].to(DEV),
+        c["ks"].to(DEV), c["vq"].to(DEV), c["vs"].to(DEV), c["scale"],
+        kvalid=None if c["kvalid"] is None else c["kvalid"].to(DEV),
+        row_counts=c["row_counts"] if Ns > 1 else None, length=c["T"], return_lse=True, n_split=n_split,
+        stream=True, dequant=dequant)
+
+
+@pytest.mark.parametrize("dequant", ["bf16", "fp32"])
+@pytest.mark.parametrize("n_split", [1, 3, None])
+@pytest.mark.parametrize("name", list(CASES))
+def test_stream_matches_oracle(gpu_lib, name, n_split, dequant):
+    c = make_case(**CASES[name])
+    print(f"stream {name} n_split={n_split} {dequant}", flush=True)
+    out, lse = run_stream(c, n_split=n_split, dequant=dequant)
+    ref, ref_lse = run_oracle(c, dequant=dequant)
+    assert_close_rel(out.float().cpu(), ref, what=f"stream {name} split {n_split} {dequant}")
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+
+
+def test_stream_more_splits_than_tiles(gpu_lib):
+    """Splits past the last tile get no keys (an empty partial, LSE -inf) and the merge ignores them."""
+    c = make_case(**CASES["gqa1_t6"])
+    out, lse = run_stream(c, n_split=9)  # 4 tiles of 32 keys
+    ref, ref_lse = run_oracle(c)
+    assert_close_rel(out.float().cpu(), ref, what="stream 9 splits over 4 tiles")
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+
+
+def test_stream_option_order_invariance_bitwise(gpu_lib):
+    """Shuffling the option rows of each state permutes the outputs and LSEs and changes nothing else, bit for bit."""
+    c = make_case(seed=29, Ns=3, row_counts=[4, 2, 3], Hq=32, Hkv=8, t=2, D=128, T=2100, holes=True)
+    perm = torch.tensor([2, 0, 3, 1, 5, 4, 8, 6, 7])
+    for n_split in (1, 5):
+        out, lse = run_stream(c, n_split=n_split)
+        out_p, lse_p = run_stream(c, n_split=n_split, perm=perm)
+        assert torch.equal(out_p.view(torch.int16), out[perm.to(DEV)].view(torch.int16)), n_split
+        assert torch.equal(lse_p, lse[perm.to(DEV)]), n_split
+
+
+def test_stream_is_the_default_for_few_slots(gpu_lib):
+    """With no path chosen, a few-slot shape takes the streaming kernel: the default call equals stream=True bit for
+    bit (and differs in path from the direct kernel, which is held to the same bar)."""
+    from opendecider_amd import kernels
+    c = make_case(**CASES["yes_no_T5000"])
+    args = (c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV), c["kq"].to(DEV), c["ks"].to(DEV), c["vq"].to(DEV),
+            c["vs"].to(DEV), c["scale"])
+    kw = dict(row_counts=c["row_counts"], length=c["T"], return_lse=True)
+    out_a, lse_a = kernels.branched_attn(*args, **kw)
+    out_s, lse_s = kernels.branched_attn(*args, stream=True, **kw)
+    out_d, _ = kernels.branched_attn(*args, staged=False, **kw)
+    assert torch.equal(out_a.view(torch.int16), out_s.view(torch.int16)) and torch.equal(lse_a, lse_s)
+    ref, _ = run_oracle(c)
+    assert_close_rel(out_d.float().cpu(), ref, what="direct path, same shape")
+
+
+def test_stream_probe_full_length(gpu_lib):
+    """The few-slot probe at full length: 32768-key int8 states, 2 options x 2 tokens, 32/8 heads (2 of the 8
+    probe states, so that the oracle stays quick)."""
+    c = make_case(seed=30, Ns=2, row_counts=[2, 2], Hq=32, Hkv=8, t=2, D=128, T=32768)
+    out, lse = run_stream(c)
+    ref, ref_lse = run_oracle(c)
+    st = assert_close_rel(out.float().cpu(), ref, what="stream probe 32768")
+    print(f"stream probe: {st}", flush=True)
+    assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+
+
+def test_stream_refuses_what_it_cannot_run(gpu_lib):
+    """More than 32 slots per (state, head), or head_dim 64: refused before any launch."""
+    from opendecider_amd import kernels
+    c = make_case(seed=31, Ns=1, row_counts=[3], Hq=32, Hkv=8, t=4, D=128, T=64)  # 48 slots
+    with pytest.raises(ValueError):
+        run_stream(c)
+    c = make_case(seed=32, Ns=1, row_counts=[1], Hq=8, Hkv=8, t=2, D=64, T=64)
+    with pytest.raises(ValueError):
+        run_stream(c)
+    assert kernels.stream_split_count(8, 8, 32768) == 8
