@@ -923,11 +923,16 @@ def run_gemm_traffic(args):
     return {"workload": "gemm_traffic", "copy_bytes": 256 << 20, "layers": 2, "passes": 2, "tokens_per_layer": 4096}
 
 
-def run_attention(args):
-    """The branched attention alone on the two shapes its roofline is quoted on: the config-1 shape (8 states of
-    2048 int8 K/V tokens, 32 options x 16 tokens each, 32/8 heads, head_dim 128: bf16-MFMA-bound) and the KV-bound
-    probe (the same dims with 32768-token states and 2 options x 16 tokens each: about 250 FLOP per K/V byte). K/V
-    int8 uniform in [-127, 127] with fp32 scales, queries and own K/V bf16 N(0, 1); HIP events around every call."""
+ATTN_SHAPES = (("config1", 8, 32, 2048, 16), ("kv_probe", 8, 2, 32768, 16), ("kv_stream", 8, 2, 32768, 2))
+
+
+def run_attention(args, only=None):
+    """The branched attention alone on the shapes its rooflines are quoted on: the config-1 shape (8 states of
+    2048 int8 K/V tokens, 32 options x 16 tokens each, 32/8 heads, head_dim 128: bf16-MFMA-bound), the ridge probe
+    (the same dims with 32768-token states and 2 options x 16 tokens each: about 250 FLOP per K/V byte, at the
+    MFMA/HBM ridge) and the KV-bound few-slot probe (32768-token states, 2 options x 2 tokens each: 16 query slots
+    per KV head, about 31 FLOP per K/V byte, od_branched_attn_stream). K/V int8 uniform in [-127, 127] with fp32
+    scales, queries and own K/V bf16 N(0, 1); HIP events around every call. only: a subset of the shape names."""
     import torch
 
     from opendecider_amd import kernels
@@ -935,8 +940,9 @@ def run_attention(args):
     g = torch.Generator(device=dev).manual_seed(5)
     Hq, Hkv, t, D = 32, 8, 16, 128
     res = {}
-    for name, Ns, rows, T, t in (("config1", 8, 32, 2048, 16), ("kv_probe", 8, 2, 32768, 16),
-                                 ("kv_stream", 8, 2, 32768, 2)):
+    for name, Ns, rows, T, t in ATTN_SHAPES:
+        if only is not None and name not in only:
+            continue
         R = Ns * rows
         q = torch.randn(R, Hq, t, D, device=dev, generator=g).to(torch.bfloat16)
         k = torch.randn(R, Hkv, t, D, device=dev, generator=g).to(torch.bfloat16)
@@ -970,11 +976,15 @@ def run_attention(args):
                      "algorithmic_gbs": by / (ms * 1e-3) / 1e9, "launches": n,
                      "path": ("stream" if rows * t * (Hq // Hkv) <= kernels.STREAM_MAX_SLOTS else
                               "staged" if kernels.uses_staging(rows, t, Hq, Hkv) else "direct")}
-    out = {"metric": "branched attention: KV GB/s on the KV-bound probe (TFLOP/s on the config-1 shape beside it)",
-           "value": res["kv_probe"]["kv_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-           "warmup": args.warmup, "ms_per_step": res["kv_probe"]["avg_launch_us"] / 1e3, "higher_is_better": True,
+    if only is not None:
+        return {"shapes": res}
+    out = {"metric": "branched attention: KV GB/s on the KV-bound few-slot probe (TFLOP/s on the config-1 shape "
+                     "and the ridge probe beside it)",
+           "value": res["kv_stream"]["kv_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": res["kv_stream"]["avg_launch_us"] / 1e3, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "int8 K/V, bf16 MFMA", "data": "synthetic",
-           "config": {"workload": "branched attention alone: config-1 shape and KV-bound probe"}, "shapes": res}
+           "config": {"workload": "branched attention alone: config-1 shape, ridge probe, KV-bound few-slot probe"},
+           "shapes": res}
     if not args.no_cpu_baseline:
         # the reference's CPU branch of _split_attention (prefix_attn.py:58-76) on K/V materialized in bf16, as the
         # oracle restates it, for 1 of the 8 config-1 states (32 options x 16 tokens over 2048 keys), scaled x8
@@ -1185,6 +1195,16 @@ def main():
         res["cpu_baseline"] = cpu_baseline(args)
     if not args.scoring_only:
         del states, dec
+        torch.cuda.empty_cache()
+        # the int8-KV option-row attention where it is HBM-bound: the few-slot probe (od_branched_attn_stream)
+        kvb = run_attention(_sub_args(args, steps=20, warmup=3), only=("kv_stream",))["shapes"]["kv_stream"]
+        res["attention_kv_bound"] = {
+            "kernel": "od_branched_attn_stream (+ split merge)", "bound": "hbm", "achieved": kvb["kv_gbs"],
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": kvb["kv_frac_of_hbm"],
+            "avg_launch_us": kvb["avg_launch_us"], "launches": kvb["launches"],
+            "config": {"workload": "8 states x 32768 int8 K/V tokens (fp32 per-token scales), 2 options x 2 tokens "
+                                   "per state, 32/8 heads, head_dim 128", "slots_per_kv_head": 16},
+            "note": "K/V bytes (int8 + fp32 scales) per call over the call's duration (HIP events)"}
         torch.cuda.empty_cache()
         res["decision"] = _sub(run_decision(_sub_args(args, steps=10, warmup=2)),
                                ("value", "unit", "p50_latency_ms", "p90_latency_ms", "config", "roofline",

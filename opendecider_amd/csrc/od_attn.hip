@@ -1483,7 +1483,7 @@ struct StrTile {
   uint4 k[4];      // lane (key c, half h): int8 bytes 64 h + 16 i .. +16 of key kb + c
   uint32_t v[16];  // lane (c, h): V bytes 4 c .. 4 c + 3 of key kb + 8 (i / 4) + 4 h + i % 4
   float vs, ks;    // V and K scales of key kb + c
-  int valid;       // key kb + c exists (and is not masked by kvalid)
+  int valid;       // the kvalid byte of key kb + c (0 without a mask)
 };
 
 // The per-wave LDS of the streaming kernel: a tile's per-key factors, written by the lane that loaded key c and
@@ -1492,19 +1492,39 @@ struct StrKeyLds {
   float4 f[2][8];  // [0]: V factor (bf16(vs) or vs), [1]: score multiplier (OD_DEQUANT_FP32: ks scale log2(e))
 };
 
+// One (state, KV head)'s int8 state as the streaming kernel reads it.
+struct StrSrc {
+  const int8_t* k;
+  const int8_t* v;
+  const float* ks;
+  const float* vs;
+  const uint8_t* valid;  // null: no mask
+  int T;
+};
+
+// The tile's loads, all unconditional (a conditional load makes the compiler wait for every load in flight). Each
+// load goes through a descriptor made for the tile (base at key kb, length T - kb keys: keys past the length read
+// as zeros), so the per-lane offsets are loop-invariant and no address register is rewritten while loads are in
+// flight.
 template <int DQ>
-__device__ __forceinline__ void str_load(const PrefixSrc& src, int kb, int T, int h, int c, StrTile& tl) {
-  const int sk = kb * kStrD;
+__device__ __forceinline__ void str_load(const StrSrc& src, int kb, int h, int c, StrTile& tl) {
+  const int n = max(src.T - kb, 0);  // keys left from kb (wave-uniform)
+  constexpr int kF = 0x00020000;
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(src.k + (int64_t)kb * kStrD), (short)0, n * kStrD, kF);
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)(src.v + (int64_t)kb * kStrD), (short)0, n * kStrD, kF);
+  const auto rks = __builtin_amdgcn_make_buffer_rsrc((void*)(src.ks + kb), (short)0, n * 4, kF);
+  const auto rvs = __builtin_amdgcn_make_buffer_rsrc((void*)(src.vs + kb), (short)0, n * 4, kF);
+  const auto rva = __builtin_amdgcn_make_buffer_rsrc((void*)(src.valid ? src.valid + kb : nullptr), (short)0,
+                                                     src.valid ? n : 0, kF);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    tl.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.k, c * kStrD + 64 * h + 16 * i, sk, 0));
+    tl.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, c * kStrD + 64 * h + 16 * i, 0, 0));
 #pragma unroll
   for (int i = 0; i < 16; ++i)
-    tl.v[i] = __builtin_amdgcn_raw_buffer_load_b32(src.v, 4 * c + 512 * h + (8 * (i >> 2) + (i & 3)) * kStrD, sk, 0);
-  tl.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.vs, c * 4, kb * 4, 0));
-  tl.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.ks, c * 4, kb * 4, 0));
-  tl.valid = kb + c < T;
-  if (src.has_valid) tl.valid = tl.valid && __builtin_amdgcn_raw_buffer_load_b8(src.valid, c, kb, 0) != 0;
+    tl.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, 4 * c + 512 * h + (8 * (i >> 2) + (i & 3)) * kStrD, 0, 0);
+  tl.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, c * 4, 0, 0));
+  tl.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, c * 4, 0, 0));
+  tl.valid = __builtin_amdgcn_raw_buffer_load_b8(rva, c, 0, 0);  // 0 past the mask (or without one)
 }
 
 __device__ __forceinline__ float f4_at(const float4& v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
@@ -1579,12 +1599,11 @@ __device__ __forceinline__ bf16x8 str_q(const uint16_t* qs, int c, int h, int ks
 
 template <int DQ>
 __device__ __forceinline__ void str_state_tile(const StrTile& tl, const uint16_t* qs, StrKeyLds& kl, float c2, int h,
-                                               int c, float& m_run, float& l_run, v16f (&o)[4]) {
-  // the tile's per-key factors through LDS into the score layout (in-order LDS access within the wave)
-  if (h == 0) {
-    reinterpret_cast<float*>(kl.f[0])[c] = DQ == OD_DEQUANT_BF16 ? bf16_round(tl.vs) : tl.vs;
-    if constexpr (DQ == OD_DEQUANT_FP32) reinterpret_cast<float*>(kl.f[1])[c] = tl.ks * c2;
-  }
+                                               int c, bool key_ok, float& m_run, float& l_run, v16f (&o)[4]) {
+  // the tile's per-key factors through LDS into the score layout (in-order LDS access within the wave; lanes c and
+  // c + 32 write the same value)
+  reinterpret_cast<float*>(kl.f[0])[c] = DQ == OD_DEQUANT_BF16 ? bf16_round(tl.vs) : tl.vs;
+  if constexpr (DQ == OD_DEQUANT_FP32) reinterpret_cast<float*>(kl.f[1])[c] = tl.ks * c2;
   v16f s = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   const float sk = DQ == OD_DEQUANT_BF16 ? bf16_round(tl.ks) : 0.0f;
 #pragma unroll
@@ -1602,7 +1621,7 @@ __device__ __forceinline__ void str_state_tile(const StrTile& tl, const uint16_t
     s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), str_q(qs, c, h, ks), s, 0, 0, 0);
   }
   // masked keys (past the state's length or masked by kvalid): bit k of the ballot is key kb + k
-  const uint32_t vm = (uint32_t)__builtin_amdgcn_ballot_w64(tl.valid != 0);
+  const uint32_t vm = (uint32_t)__builtin_amdgcn_ballot_w64(key_ok);
   float y[16], f[16];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -1652,7 +1671,8 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
   const int per_row = p.t * p.rep;
   const int nslots = nrows * per_row;
   if (nslots <= 0) return;  // uniform over the workgroup
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index made visibly uniform: the tile offsets derived from it are scalar buffer offsets
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5, c = lane & 31;
   const bool slot_ok = c < nslots;
   int rl = 0, tok = 0;
@@ -1684,20 +1704,28 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
   const int n_tiles = (p.T + kStrKeys - 1) / kStrKeys;
   const int tps = (n_tiles + p.nsplit - 1) / p.nsplit;
   const int t_lo = min(n_tiles, sp * tps), t_hi = min(n_tiles, t_lo + tps);
-  const PrefixSrc src = prefix_src<D>(p.kq, p.ks, p.vq, p.vs, p.kvalid, p.Hkv, p.T, p.cap, s, g);
+  const int64_t head_base = ((int64_t)s * p.Hkv + g) * p.cap;
+  const StrSrc src{p.kq + head_base * D, p.vq + head_base * D, p.ks + head_base, p.vs + head_base,
+                   p.kvalid ? p.kvalid + (int64_t)s * p.T : nullptr, p.T};
   int tt = t_lo + wave;
   if (tt < t_hi) {
+    const bool has_valid = p.kvalid != nullptr;
+    auto ok = [&](const StrTile& tl, int t0) { return t0 * kStrKeys + c < p.T && (!has_valid || tl.valid != 0); };
+    // two register sets, loads one tile ahead (two tiles per trip, so the sets alternate without copies); past the
+    // wave's last tile the "next" loads repeat the current tile (cached), so that no load is conditional. A third
+    // set (loads two tiles ahead) measured no faster.
     StrTile ta, tb;
-    str_load<DQ>(src, tt * kStrKeys, p.T, h, c, ta);
-    // two tiles per trip, so that the loads of the next tile go into the other register set without copies
+    str_load<DQ>(src, tt * kStrKeys, h, c, ta);
     for (;; tt += 2 * kStrWaves) {
       const bool more1 = tt + kStrWaves < t_hi;
-      if (more1) str_load<DQ>(src, (tt + kStrWaves) * kStrKeys, p.T, h, c, tb);
-      str_state_tile<DQ>(ta, sm.q, skl[wave], p.scale_log2, h, c, m_run, l_run, o);
+      str_load<DQ>(src, (more1 ? tt + kStrWaves : tt) * kStrKeys, h, c, tb);
+      __builtin_amdgcn_sched_barrier(0);  // the next tile's loads go out before this tile's first use of its data
+      str_state_tile<DQ>(ta, sm.q, skl[wave], p.scale_log2, h, c, ok(ta, tt), m_run, l_run, o);
       if (!more1) break;
       const bool more2 = tt + 2 * kStrWaves < t_hi;
-      if (more2) str_load<DQ>(src, (tt + 2 * kStrWaves) * kStrKeys, p.T, h, c, ta);
-      str_state_tile<DQ>(tb, sm.q, skl[wave], p.scale_log2, h, c, m_run, l_run, o);
+      str_load<DQ>(src, (more2 ? tt + 2 * kStrWaves : tt + kStrWaves) * kStrKeys, h, c, ta);
+      __builtin_amdgcn_sched_barrier(0);
+      str_state_tile<DQ>(tb, sm.q, skl[wave], p.scale_log2, h, c, ok(tb, tt + kStrWaves), m_run, l_run, o);
       if (!more2) break;
     }
   }
