@@ -246,7 +246,6 @@ int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t 
  * only (option order cannot change it); results agree with od_branched_attn to the attention bar, not bit for bit.
  * Replaces: the same reference code as od_branched_attn (prefix_attn.py:43-76 with Kp/Vp materialized at :145-149).
  *   D          128 only (else OD_ERR_UNSUPPORTED); more than 32 slots per (state, head): OD_ERR_UNSUPPORTED
- *   ks, vs     16-byte aligned when T > 0
  *   nsplit, ws as od_branched_attn_split (the keys of a (state, head) split over nsplit workgroups of 4 waves)
  * Other arguments and the result as od_branched_attn_split. One launch, plus the merge when nsplit > 1.
  */

@@ -1862,7 +1862,7 @@ extern "C" int od_branched_attn_stream(const uint16_t* q, int64_t sqr, int64_t s
     if (st < 0 || st % 8) return OD_ERR_ALIGN;
   if (sor < 0 || soh < 0 || sot < 0 || sor % 4 || soh % 4 || sot % 4) return OD_ERR_ALIGN;
   if (!od_aligned16(q) || !od_aligned16(k_own) || !od_aligned16(v_own) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
-  if (T > 0 && (!od_aligned16(kq) || !od_aligned16(vq) || !od_aligned16(ks) || !od_aligned16(vs))) return OD_ERR_ALIGN;
+  if (T > 0 && (!od_aligned16(kq) || !od_aligned16(vq) || (((uintptr_t)ks | (uintptr_t)vs) & 3u))) return OD_ERR_ALIGN;
   if (Hkv > 65535 || Ns > 65535 || R * t * rep > 0x7fffffff || cap * Hkv * Ns * D > (1ll << 40) ||
       nsplit * R * Hq * t * (D + 1) > (1ll << 40) || T * D >= (1ll << 31))
     return OD_ERR_SHAPE;

@@ -111,3 +111,26 @@ def test_stream_refuses_what_it_cannot_run(gpu_lib):
     with pytest.raises(ValueError):
         run_stream(c)
     assert kernels.stream_split_count(8, 8, 32768) == 8
+
+
+def test_split_attention_int8_few_rows_streams(gpu_lib):
+    """The drop-in `_split_attention` with the reference caller's arguments (prefix_attn.py:127: q (n, Hq, t, D), own
+    k/v (n, Hkv, t, D), the state Kp/Vp (Hkv, T, D) as Int8Tensor, a key mask pm (T,)) on a yes/no shape takes the
+    streaming kernel and meets the bar against the oracle on the same int8 state."""
+    from opendecider_amd.prefix_attn import _split_attention
+    from opendecider_amd.quant import Int8Tensor
+    g = torch.Generator().manual_seed(33)
+    n, Hq, Hkv, t, D, T = 2, 32, 8, 2, 128, 4000
+    src = torch.randn(2, Hkv, T, D, generator=g).to(torch.bfloat16)
+    Kp, Vp = Int8Tensor.quantize(src[0].to(DEV)), Int8Tensor.quantize(src[1].to(DEV))
+    pm = torch.ones(T, dtype=torch.bool)
+    pm[:37] = False  # leading pads
+    q = torch.randn(n, Hq, t, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(n, Hkv, t, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, Hkv, t, D, generator=g).to(torch.bfloat16)
+    out = _split_attention(q.to(DEV), k.to(DEV), v.to(DEV), Kp, Vp, pm.to(DEV), D ** -0.5)
+    c = dict(q=q, k=k, v=v, kq=Kp.q.cpu()[None], ks=Kp.scale.float().cpu().reshape(1, Hkv, T),
+             vq=Vp.q.cpu()[None], vs=Vp.scale.float().cpu().reshape(1, Hkv, T), kvalid=pm[None],
+             row_state=torch.zeros(n, dtype=torch.long), T=T, scale=D ** -0.5)
+    ref, _ = run_oracle(c)
+    assert_close_rel(out.float().cpu(), ref, what="_split_attention few rows (stream)")
