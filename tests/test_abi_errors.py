@@ -75,6 +75,25 @@ def test_attention_checks(L):
     assert L.od_attn_stage_bf16(P, *bf, P, *bf, None, 1, 1, 64, 128, 0.1, P, 100, None) == SHAPE  # image too small
 
 
+def test_stream_attention_checks(L):
+    """od_branched_attn_stream: head_dim 128 only, at most 32 query slots per (state, KV head), the split workspace
+    and alignment rules of od_branched_attn_split."""
+    s = (1024, 128, 128) * 3
+    def stream(D=128, Hq=8, Hkv=2, t=4, max_rows=2, dq=0, nsplit=1, ws=None, ws_floats=0, ks=P, kq=P):
+        return L.od_branched_attn_stream(P, *s[:3], P, *s[3:6], P, *s[6:], kq, ks, P, P, None, None, max_rows, P,
+                                         1024, 128, 128, None, 2, Hq, Hkv, t, D, 1, 64, 64, 0.1, dq, nsplit, ws,
+                                         ws_floats, None)
+    assert stream(D=64) == UNSUP
+    assert stream(t=5, max_rows=2) == UNSUP       # 2 rows x 5 tokens x 4 heads = 40 slots
+    assert stream(Hq=6, Hkv=4) == UNSUP
+    assert stream(dq=2) == UNSUP
+    assert stream(nsplit=0) == SHAPE
+    assert stream(nsplit=3, ws=P, ws_floats=100) == SHAPE   # workspace too small
+    assert stream(nsplit=3) == NULL                          # no workspace
+    assert stream(ks=P + 2) == ALIGN                         # scales must be 4-byte aligned
+    assert stream(kq=P + 8) == ALIGN                         # int8 K must be 16-byte aligned
+
+
 def test_row_kernel_checks(L):
     assert L.od_rmsnorm_quant(P, 8, P, None, 1e-6, P, 16, P, 4, 16, None) == SHAPE  # ldx < K
     assert L.od_silu_mul_quant(P, 16, 16, None, P, 16, P, 4, None) == SHAPE  # ldg < 2F
