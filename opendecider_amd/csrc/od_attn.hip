@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(kThreads) void stage_bf16_kernel(StageBf16Args p) {
 
 // LSE merge of the key-range splits (prefix_attn.py:74-76 generalised to n parts): M = max_s lse_s,
 // w_s = exp(lse_s - M), out = sum_s w_s o_s / sum_s w_s (bf16), lse = M + log(sum_s w_s); no visible key in any
-// split -> 0 and -inf. One thread per (slot, 8 values of d).
+// split -> 0 and -inf. One thread per (slot, 8 values of d); M is taken as a running max in the same pass.
 template <int D>
 __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
   const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
@@ -1159,25 +1159,28 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
   const int d0 = (int)(gid % (D / 8)) * 8;
   if (slot >= nsl) return;
   const float* lse_p = p.part + (int64_t)p.nsplit * nsl * D;
-  // the loops are unrolled so that the loads of several splits are in flight together (a rolled loop waits for
-  // one split's partial at a time)
+  // one pass with a running max (the sum rescaled when the max moves), so that no load waits for another: the loop
+  // is unrolled and every split's LSE and partial are in flight together
   float M = -INFINITY;
-#pragma unroll 8
-  for (int sp = 0; sp < p.nsplit; ++sp) M = fmaxf(M, lse_p[sp * nsl + slot]);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   float wsum = 0.0f;
-  if (M != -INFINITY) {
 #pragma unroll 8
-    for (int sp = 0; sp < p.nsplit; ++sp) {
-      const float l = lse_p[sp * nsl + slot];
-      if (l == -INFINITY) continue;
-      const float w = __expf(l - M);
-      wsum += w;
-      const float4* po = reinterpret_cast<const float4*>(p.part + (sp * nsl + slot) * D + d0);
-      const float4 a = po[0], b = po[1];
-      acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
-      acc[4] += w * b.x; acc[5] += w * b.y; acc[6] += w * b.z; acc[7] += w * b.w;
+  for (int sp = 0; sp < p.nsplit; ++sp) {
+    const float l = lse_p[sp * nsl + slot];
+    const float4* po = reinterpret_cast<const float4*>(p.part + (sp * nsl + slot) * D + d0);
+    const float4 a = po[0], b = po[1];
+    if (l == -INFINITY) continue;  // a split with no visible key
+    if (l > M) {
+      const float r = __expf(M - l);  // M = -inf: 0 (nothing accumulated yet)
+      wsum *= r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= r;
+      M = l;
     }
+    const float w = __expf(l - M);
+    wsum += w;
+    acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
+    acc[4] += w * b.x; acc[5] += w * b.y; acc[6] += w * b.z; acc[7] += w * b.w;
   }
   const int row = (int)(slot / ((int64_t)p.Hq * p.t)), rem = (int)(slot % ((int64_t)p.Hq * p.t));
   const int head = rem / p.t, tok = rem % p.t;
