@@ -376,7 +376,8 @@ class DenseDecoder:
 
     def state_images(self, li: int, state_k: Int8KVCache, state_v: Int8KVCache):
         """Layer li's block images of the cached states (od_attn_stage), built once and reused by every scoring pass
-        until the caches change (their generation counters or length move). Only for an unmasked state."""
+        until the caches change (their generations or length move; generations are unique across caches, so a new
+        state never hits the images of a freed one). Only for an unmasked state."""
         cfg = self.cfg
         key = (id(state_k), id(state_v), state_k.generation, state_v.generation, state_k.length)
         hit = self._images.get(li)

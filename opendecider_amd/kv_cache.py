@@ -12,10 +12,16 @@ kernel streams one (state, head) as a single contiguous slab.
 """
 from __future__ import annotations
 
+import itertools
+
 import torch
 
 from . import kernels
 from .quant import Int8Tensor
+
+# Cache versions come from one process-wide counter: every new cache and every write takes a value no other cache
+# has held, so a (generation) key can never match a different cache, even one that reuses a freed cache's id().
+_GENERATIONS = itertools.count(1)
 
 
 class Int8KVCache:
@@ -24,7 +30,9 @@ class Int8KVCache:
         self.scale = torch.zeros(batch, n_heads, capacity, dtype=torch.float32, device=device)
         self.length = 0
         self.dtype = dtype
-        self.generation = 0  # bumped by every write through this package (derived data, e.g. block images, keys on it)
+        # a fresh value on every write through this package (derived data, e.g. block images, keys on it); unique
+        # across caches, so a new cache never looks like an old one
+        self.generation = next(_GENERATIONS)
 
     @classmethod
     def from_tensors(cls, q: torch.Tensor, scale: torch.Tensor, dtype=torch.bfloat16) -> "Int8KVCache":
@@ -34,12 +42,12 @@ class Int8KVCache:
         if not (q.is_contiguous() and scale.is_contiguous()):
             raise ValueError("Int8KVCache.from_tensors: buffers must be contiguous")
         c = cls.__new__(cls)
-        c.q, c.scale, c.length, c.dtype, c.generation = q, scale, 0, dtype, 0
+        c.q, c.scale, c.length, c.dtype, c.generation = q, scale, 0, dtype, next(_GENERATIONS)
         return c
 
     def touch(self) -> None:
         """Mark the bytes as changed (call after writing q / scale directly)."""
-        self.generation += 1
+        self.generation = next(_GENERATIONS)
 
     @property
     def capacity(self) -> int:

@@ -399,3 +399,32 @@ def test_question_cache_end_to_end(gpu_lib, name, cfg_kw, B, T, gs, Lq, qlen, n_
         dp = (lp_rows.exp() - lp[full].exp()).abs().max().item()
         print(f"{name}: question cache vs rows carrying the question: max |dp| {dp:.2e}")
         assert dp <= PROB_ABS
+
+
+def test_new_state_of_same_length_gets_its_own_images(gpu_lib):
+    """State images are cached per layer by cache version: score state A (staged path, images built), free A, build
+    state B of the same length (new caches that may reuse A's ids), score B with the same decoder. The result equals
+    B scored by a fresh decoder (which has never seen A) bit for bit, and differs from A's."""
+    import gc
+    from opendecider_amd import kernels
+    from opendecider_amd.decoder import DecoderConfig, DenseDecoder
+    name, cfg_kw, B, n_opt, t, T = CASES[1]
+    cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
+    assert kernels.uses_staging(n_opt, t, cfg.n_heads, cfg.n_kv_heads)
+    print(f"{name}: image cache across states B={B} options={n_opt} t={t} T={T}", flush=True)
+    lp_a = dec.score(ids.to(DEV), gs).cpu()
+    del gs
+    gc.collect()
+    g = torch.Generator().manual_seed(40)
+    states_b = []
+    for _ in range(cfg.n_layers):
+        kv = torch.randn(2, B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).to(torch.bfloat16)
+        kq, ks = oq.quantize_rows(kv[0])
+        vq, vs = oq.quantize_rows(kv[1])
+        states_b.append(((kq, ks[..., 0]), (vq, vs[..., 0])))
+    gs_b = _gpu_states(states_b, T + 32)
+    lp_b = dec.score(ids.to(DEV), gs_b).cpu()
+    fresh = DenseDecoder(DecoderConfig(**cfg_kw), w, emb, DEV, max_pos=T + t + 8)
+    lp_b_fresh = fresh.score(ids.to(DEV), gs_b).cpu()
+    assert torch.equal(lp_b, lp_b_fresh)
+    assert not torch.equal(lp_b, lp_a)
