@@ -206,7 +206,8 @@ int od_lm_head_logprob_q4(const uint16_t* hb, int64_t ldh, const void* hn, int64
  *   dequant   OD_DEQUANT_BF16 or OD_DEQUANT_FP32 (else OD_ERR_UNSUPPORTED)
  * Query head h reads KV head h / (Hq / Hkv). Every query sees every valid prefix key and its own row's keys
  * 0..i (causal). A query with no visible key would return 0 (never happens: its own key is visible).
- * Supports D in {64, 128}, Hq % Hkv == 0, 1 <= t <= 256, T <= cap.
+ * Supports D in {64, 128, 256} (the reference's dispatch set, prefix_attn.py:50; D = 256 runs one workgroup per CU),
+ * Hq % Hkv == 0, t >= 1 (R * t * Hq / Hkv below 2^31), T <= cap.
  */
 int od_branched_attn(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
                      const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,
@@ -246,6 +247,8 @@ int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t 
  * only (option order cannot change it); results agree with od_branched_attn to the attention bar, not bit for bit.
  * Replaces: the same reference code as od_branched_attn (prefix_attn.py:43-76 with Kp/Vp materialized at :145-149).
  *   D          128 only (else OD_ERR_UNSUPPORTED); more than 32 slots per (state, head): OD_ERR_UNSUPPORTED
+ *   max_rows   as od_branched_attn (an upper bound); a state whose row_start span holds more rows than max_rows
+ *              (more than 32 slots) gets NaN outputs and LSEs instead of an attention result
  *   nsplit, ws as od_branched_attn_split (the keys of a (state, head) split over nsplit workgroups of 4 waves)
  * Other arguments and the result as od_branched_attn_split. One launch, plus the merge when nsplit > 1.
  */
@@ -318,7 +321,7 @@ int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq, const flo
  *   scale     the softmax scale of the attention calls that will read the images
  *   img       device buffer of at least od_attn_stage_size bytes, 16-byte aligned (out)
  * Keys are used as they are; values become fp16(v 2^-eb) with 2^eb above the block's largest |v| (exact down to
- * 2^(eb - 14)). D in {64, 128}. One launch on `stream`.
+ * 2^(eb - 14)). D in {64, 128, 256}. One launch on `stream`.
  */
 int od_attn_stage_bf16(const uint16_t* k, int64_t skb, int64_t skh, int64_t skt, const uint16_t* v, int64_t svb,
                        int64_t svh, int64_t svt, const uint8_t* kvalid, int64_t Ns, int64_t Hkv, int64_t T, int64_t D,

@@ -113,8 +113,15 @@ struct alignas(16) BlockImg {
   alignas(16) float kb[kBlockKeys];         // 0, or -inf for a masked key
   alignas(16) int info[4];                  // the block constants: 0, eb, masked, 0
 };
+static_assert(sizeof(BlockImg<256>) == 4 * kBlockKeys * 256 + 8 * kBlockKeys + 16, "block image layout");
 static_assert(sizeof(BlockImg<128>) == 4 * kBlockKeys * 128 + 8 * kBlockKeys + 16, "block image layout");
 static_assert(sizeof(BlockImg<64>) == 4 * kBlockKeys * 64 + 8 * kBlockKeys + 16, "block image layout");
+
+// Head dims of the block-image kernels. D = 256 (Qwen3.5's full-attention heads) holds twice the accumulators and
+// query fragments of D = 128 and two 66 KB images: one workgroup per CU, one wave per SIMD with its 512 registers.
+constexpr bool block_d_ok(int64_t D) { return D == 64 || D == 128 || D == 256; }
+template <int D>
+constexpr int kWgPerCu = D == 256 ? 1 : 2;
 
 template <int D>
 struct alignas(16) Smem {  // double-buffered block images
@@ -134,13 +141,16 @@ struct BlockInfo {
 // ds_write_b64). A fragment read has lanes 16g .. 16g+15 take 16 consecutive rows (keys of K, d of V^T) at one
 // logical 16-byte chunk, so the chunk is XORed with a function of the row that gives those 16 rows 16 distinct
 // bank quads:
-//  * K, rows of 2D bytes (D/8 chunks): 128/D rows share a 256-byte period, XOR with (key / (128/D)) mod D/8;
+//  * K, rows of 2D bytes (D/8 chunks): D = 64, two rows share a 256-byte period, XOR with (key / 2) mod 8; D >= 128,
+//    a row spans whole periods, XOR with key mod 16;
 //  * V^T, rows of 128 bytes (8 chunks), two rows per period: XOR with ((d >> 1) ^ (d >> 3)) & 7, which is a
 //    bijection on any 8 consecutive even (or odd) d and also on {8 dg + e : dg = 8 consecutive values} for a
 //    fixed e, which the transposing store needs (see vmap).
 template <int D>
 __device__ __forceinline__ int k_off(int key, int chunk) {
-  return key * D + ((chunk ^ ((key / (128 / D)) & (D / 8 - 1))) << 3);
+  constexpr int kRowsPerPeriod = D >= 128 ? 1 : 128 / D;
+  constexpr int kMask = D >= 128 ? 15 : D / 8 - 1;
+  return key * D + ((chunk ^ ((key / kRowsPerPeriod) & kMask)) << 3);
 }
 __device__ __forceinline__ int vt_off(int d, int chunk) {
   return d * kBlockKeys + ((chunk ^ (((d >> 1) ^ (d >> 3)) & 7)) << 3);
@@ -151,10 +161,16 @@ __device__ __forceinline__ int vt_off(int d, int chunk) {
 // 0..2 of the lane pick 8 consecutive dg (8 distinct chunks after the V^T swizzle) and bit 3 flips bit 1 of kg,
 // which is the half of the 16-byte chunk the 4 keys occupy, so the 16 lanes write 16 distinct 8-byte slots.
 // D = 128: 16 dg x 16 kg = 256 threads; D = 64: 8 dg x 16 kg = threads 0..127. kg < 8 <=> thread < D.
+// D = 256: 32 dg x 8 kg = 256 threads, and a 64-key block takes two passes (pass 1: kg + 8).
 template <int D>
-__device__ __forceinline__ void vmap(int tid, int& dg, int& kg) {
+constexpr int kVPasses = D == 256 ? 2 : 1;
+template <int D>
+__device__ __forceinline__ void vmap(int tid, int pass, int& dg, int& kg) {
   const int lo = tid & 7, t3 = (tid >> 3) & 1, hi = tid >> 4;
-  if constexpr (D == 128) {
+  if constexpr (D == 256) {
+    dg = lo | ((hi & 3) << 3);
+    kg = (t3 << 1) | ((hi >> 2) & 1) | ((hi >> 3) << 2) | (pass << 3);
+  } else if constexpr (D == 128) {
     dg = lo | ((hi & 1) << 3);
     kg = (t3 << 1) | ((hi >> 1) & 1) | ((hi >> 2) << 2);
   } else {
@@ -162,6 +178,9 @@ __device__ __forceinline__ void vmap(int tid, int& dg, int& kg) {
     kg = (t3 << 1) | (hi & 1) | ((hi >> 1) << 2);
   }
 }
+// whether thread tid takes part in a 64-key block's transposing V store (16 kg x D / 8 dg per pass)
+template <int D>
+__device__ __forceinline__ bool v_active(int tid) { return D == 256 || tid < 2 * D; }
 // position of key j (0..63) inside its V^T row: bits 2 and 3 swapped
 __device__ __forceinline__ int jj_of(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
 
@@ -253,7 +272,7 @@ __device__ __forceinline__ PrefixSrc prefix_src(const int8_t* kq, const float* k
 template <int D>
 struct PrefixRegs {
   uint4 k[(kBlockKeys * D / 16 + kThreads - 1) / kThreads];
-  uint2 v[4];
+  uint2 v[4 * kVPasses<D>];  // pass p: v[4 p + a]
   float ks, vs;  // lane l of every wave: the K and V scale of key j0 + l (0 past the state's length)
   int in_range;  // lane l: key j0 + l exists
   int valid;     // lane l: its kvalid byte (1 without a mask); only read when converting, so the load is not waited
@@ -270,13 +289,17 @@ __device__ __forceinline__ void prefix_load(const PrefixSrc& src, int T, int j0,
     if (cid < kChunks)
       r.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.k, cid * 16, j0 * D, 0));
   }
-  int dg, kg;
-  vmap<D>(tid, dg, kg);
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    r.v[a] = make_uint2(0, 0);
-    if (tid < 2 * D)
-      r.v[a] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.v, (4 * kg + a) * D + 8 * dg, j0 * D, 0));
+  for (int ps = 0; ps < kVPasses<D>; ++ps) {
+    int dg, kg;
+    vmap<D>(tid, ps, dg, kg);
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      r.v[4 * ps + a] = make_uint2(0, 0);
+      if (v_active<D>(tid))
+        r.v[4 * ps + a] = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_raw_buffer_load_b64(src.v, (4 * kg + a) * D + 8 * dg, j0 * D, 0));
+    }
   }
   const int l = tid & 63;
   r.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.ks, l * 4, j0 * 4, 0));
@@ -340,15 +363,18 @@ __device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, Block
       *reinterpret_cast<uint4*>(&dst.k[k_off<D>(key, 2 * c + 1 - flip)]) = h1;
     }
   }
+#pragma unroll
+  for (int ps = 0; ps < kVPasses<D>; ++ps) {
   int dg, kg;
-  vmap<D>(tid, dg, kg);
-  if (tid < 2 * D) {
+  vmap<D>(tid, ps, dg, kg);
+  if (v_active<D>(tid)) {
     // 4 keys x 8 bytes -> for each of the 8 d: the 4 keys' bytes (a 4x4 byte transpose per dword half)
+    const uint2* rv = &r.v[4 * ps];
     uint32_t cols[8];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const uint32_t L0 = half ? r.v[0].y : r.v[0].x, L1 = half ? r.v[1].y : r.v[1].x;
-      const uint32_t L2 = half ? r.v[2].y : r.v[2].x, L3 = half ? r.v[3].y : r.v[3].x;
+      const uint32_t L0 = half ? rv[0].y : rv[0].x, L1 = half ? rv[1].y : rv[1].x;
+      const uint32_t L2 = half ? rv[2].y : rv[2].x, L3 = half ? rv[3].y : rv[3].x;
       const uint32_t t0 = __builtin_amdgcn_perm(L1, L0, 0x05010400u);  // L0b0 L1b0 L0b1 L1b1
       const uint32_t t1 = __builtin_amdgcn_perm(L3, L2, 0x05010400u);  // L2b0 L3b0 L2b1 L3b1
       const uint32_t t2 = __builtin_amdgcn_perm(L1, L0, 0x07030602u);  // L0b2 L1b2 L0b3 L1b3
@@ -376,6 +402,7 @@ __device__ __forceinline__ BlockInfo convert_block(const PrefixRegs<D>& r, Block
       }
       *reinterpret_cast<uint2*>(&dst.vt[vt_off(d, jj0 >> 3) + (jj0 & 7)]) = hv;
     }
+  }
   }
   if (tid < kBlockKeys) {
     dst.gk[tid] = ok ? (mat ? scale_log2 : r.ks * scale_log2) : 1.0f;
@@ -681,9 +708,11 @@ __device__ __forceinline__ void staged_step(const BlockImg<D>& cur, const uint16
                                             v16f (&s)[2], v16f (&sn)[2], float& m_run, float& l_run, int& e_run,
                                             v16f (&o)[D / 32], Dma&& dma) {
   constexpr int KT = 2, KA = 1, KS = D / 16;
-  constexpr int kGroups = KT * 4;          // groups of 4 scores: (key tile kt, register quad r4)
-  constexpr int kPerStep = kGroups / KS;   // D = 128: one group per k-step; D = 64: two
-  static_assert(kGroups % KS == 0, "score groups per k-step");
+  constexpr int kGroups = KT * 4;  // groups of 4 scores: (key tile kt, register quad r4)
+  // D = 128: one group per k-step; D = 64: two; D = 256: one on every second k-step
+  constexpr int kPerStep = kGroups >= KS ? kGroups / KS : 1;
+  constexpr int kStride = KS > kGroups ? KS / kGroups : 1;
+  static_assert(kPerStep * KS == kGroups * kStride, "score groups per k-step");
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
   const BlockInfo ci = read_info(cur.info);
@@ -711,11 +740,15 @@ __device__ __forceinline__ void staged_step(const BlockImg<D>& cur, const uint16
   for (int ks = 0; ks < KS; ++ks) {
     // this k-step's key multipliers are read ahead of the next k-step's K fragments, so that waiting for them
     // leaves those fragments in flight
+    const bool gstep = ks % kStride == kStride - 1;  // this k-step carries score groups (a constant once unrolled)
+    const int g0 = (ks / kStride) * kPerStep;
     float4 g4s[kPerStep];
+    if (gstep) {
 #pragma unroll
-    for (int c = 0; c < kPerStep; ++c) {
-      const int grp = ks * kPerStep + c, kt = grp / 4, r4 = grp % 4;
-      g4s[c] = *reinterpret_cast<const float4*>(&cur.gk[kt * 32 + 8 * r4 + 4 * h]);
+      for (int c = 0; c < kPerStep; ++c) {
+        const int grp = g0 + c, kt = grp / 4, r4 = grp % 4;
+        g4s[c] = *reinterpret_cast<const float4*>(&cur.gk[kt * 32 + 8 * r4 + 4 * h]);
+      }
     }
     if (ks + KA < KS) kread(ks + KA);
 #pragma unroll
@@ -723,8 +756,8 @@ __device__ __forceinline__ void staged_step(const BlockImg<D>& cur, const uint16
       sn[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % (KA + 1)][kt], qf[ks], sn[kt], 0, 0, 0);
     dma(ks);
 #pragma unroll
-    for (int c = 0; c < kPerStep; ++c) {
-      const int grp = ks * kPerStep + c, kt = grp / 4, r4 = grp % 4;
+    for (int c = 0; c < (gstep ? kPerStep : 0); ++c) {
+      const int grp = g0 + c, kt = grp / 4, r4 = grp % 4;
       const float4 g4 = g4s[c];
       const float gg[4] = {g4.x, g4.y, g4.z, g4.w};
 #pragma unroll
@@ -812,7 +845,7 @@ __device__ __forceinline__ void own_stage(const AttnArgs& p, float (&red)[2][kWa
   }
   // V: a thread takes 4 keys x 8 d (kOwnKeys / 4 key groups x D / 8 d groups, threads 0 .. D - 1)
   int dg, kg;
-  vmap<D>(tid, dg, kg);
+  vmap<D>(tid, 0, dg, kg);
   const bool vact = tid < D;
   uint4 vr[4];
   float va = 0.0f, unused = 0.0f;
@@ -986,7 +1019,10 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
   const int last = min(slot_base + kSlotsPerTile, nslots) - 1;
   const int r_lo = row0 + slot_base / per_row, r_hi = sp == p.nsplit - 1 ? row0 + last / per_row : r_lo - 1;
   for (int row = r_lo; row <= r_hi; ++row) {
-    for (int j0 = 0; j0 < p.t; j0 += kOwnKeys) {
+    // only the own blocks that some slot of the tile can see: keys up to the largest token of this row in the tile
+    const int rl = row - row0;
+    const int tok_hi = (min(last, (rl + 1) * per_row - 1) - rl * per_row) / p.rep;
+    for (int j0 = 0; j0 <= tok_hi; j0 += kOwnKeys) {
       __syncthreads();  // LDS image 0 free
       BlockInfo bi;
       own_stage<D>(p, sm.red, sm.b[0].k, sm.b[0].vt, row, g, j0, bi);
@@ -1033,16 +1069,16 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
   if (p.lse && h == 0) p.lse[slot_idx] = lse_v;
 }
 
-// The int8 path: two workgroups per CU (two waves per SIMD hide each other's phases).
+// The int8 path: two workgroups per CU (two waves per SIMD hide each other's phases; one at D = 256).
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void branched_attn_kernel(AttnArgs p) {
+__global__ __launch_bounds__(kThreads, kWgPerCu<D>) void branched_attn_kernel(AttnArgs p) {
   __shared__ Smem<D> sm;
   branched_attn_body<D, false>(p, sm);
 }
 
 // The staged path: the same, each workgroup copying block images into LDS.
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void branched_staged_kernel(AttnArgs p) {
+__global__ __launch_bounds__(kThreads, kWgPerCu<D>) void branched_staged_kernel(AttnArgs p) {
   __shared__ Smem<D> sm;
   branched_attn_body<D, true>(p, sm);
 }
@@ -1104,19 +1140,24 @@ __global__ __launch_bounds__(kThreads) void stage_bf16_kernel(StageBf16Args p) {
     if (valid(key)) val = *reinterpret_cast<const uint4*>(kbase + (int64_t)(j0 + key) * p.skt + 8 * c);
     *reinterpret_cast<uint4*>(&dst.k[k_off<D>(key, c)]) = val;
   }
-  int dg, kg;
-  vmap<D>(tid, dg, kg);
-  uint4 vv[4];
+  constexpr int kP = kVPasses<D>;
+  uint4 vv[4 * kP];  // pass ps: vv[4 ps + a]
   float vmax = 0.0f;
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    vv[a] = make_uint4(0, 0, 0, 0);
-    if (tid < 2 * D && valid(4 * kg + a))
-      vv[a] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(j0 + 4 * kg + a) * p.svt + 8 * dg);
-    const uint32_t w[4] = {vv[a].x, vv[a].y, vv[a].z, vv[a].w};
+  for (int ps = 0; ps < kP; ++ps) {
+    int dg, kg;
+    vmap<D>(tid, ps, dg, kg);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      vmax = fmaxf(vmax, fmaxf(fabsf(__uint_as_float(w[e] << 16)), fabsf(__uint_as_float(w[e] & 0xffff0000u))));
+    for (int a = 0; a < 4; ++a) {
+      uint4& x = vv[4 * ps + a];
+      x = make_uint4(0, 0, 0, 0);
+      if (v_active<D>(tid) && valid(4 * kg + a))
+        x = *reinterpret_cast<const uint4*>(vbase + (int64_t)(j0 + 4 * kg + a) * p.svt + 8 * dg);
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        vmax = fmaxf(vmax, fmaxf(fabsf(__uint_as_float(w[e] << 16)), fabsf(__uint_as_float(w[e] & 0xffff0000u))));
+    }
   }
   vmax = od_wave_max_dpp(vmax);
   if ((tid & 63) == 0) red[tid >> 6] = vmax;
@@ -1126,19 +1167,25 @@ __global__ __launch_bounds__(kThreads) void stage_bf16_kernel(StageBf16Args p) {
   const bool any = __builtin_amdgcn_ballot_w64(ok) != 0;
   const int masked = __builtin_amdgcn_ballot_w64(!ok) != 0;  // taken with the whole wave active
   const int eb = any ? exp_above(vmax) : kNoFrame;
-  if (tid < 2 * D) {
-    const float f = any ? ldexpf(1.0f, -eb) : 0.0f;
-    const int jj0 = jj_of(4 * kg);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {  // d = 8 dg + e: the 4 keys' values
-      float x[4];
+  for (int ps = 0; ps < kP; ++ps) {
+    int dg, kg;
+    vmap<D>(tid, ps, dg, kg);
+    if (v_active<D>(tid)) {
+      const float f = any ? ldexpf(1.0f, -eb) : 0.0f;
+      const int jj0 = jj_of(4 * kg);
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const uint32_t w = e < 2 ? vv[a].x : e < 4 ? vv[a].y : e < 6 ? vv[a].z : vv[a].w;
-        x[a] = __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16)) * f;
+      for (int e = 0; e < 8; ++e) {  // d = 8 dg + e: the 4 keys' values
+        float x[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const uint4& y = vv[4 * ps + a];
+          const uint32_t w = e < 2 ? y.x : e < 4 ? y.y : e < 6 ? y.z : y.w;
+          x[a] = __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16)) * f;
+        }
+        const uint2 hv = make_uint2(pack_h2(x[0], x[1]), pack_h2(x[2], x[3]));
+        *reinterpret_cast<uint2*>(&dst.vt[vt_off(8 * dg + e, jj0 >> 3) + (jj0 & 7)]) = hv;
       }
-      const uint2 hv = make_uint2(pack_h2(x[0], x[1]), pack_h2(x[2], x[3]));
-      *reinterpret_cast<uint2*>(&dst.vt[vt_off(8 * dg + e, jj0 >> 3) + (jj0 & 7)]) = hv;
     }
   }
   if (tid < kBlockKeys) {
@@ -1184,7 +1231,8 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
   }
   const int row = (int)(slot / ((int64_t)p.Hq * p.t)), rem = (int)(slot % ((int64_t)p.Hq * p.t));
   const int head = rem / p.t, tok = rem % p.t;
-  const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+  // wsum 0: no visible key (0 and -inf); NaN (a NaN partial) propagates to the output and the LSE
+  const float inv = wsum > 0.0f ? 1.0f / wsum : wsum == 0.0f ? 0.0f : wsum;
   uint32_t w4[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
@@ -1192,7 +1240,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
   uint16_t* op = p.out + (int64_t)row * p.sor + (int64_t)head * p.soh + (int64_t)tok * p.sot + d0;
   *reinterpret_cast<uint2*>(op) = make_uint2(w4[0], w4[1]);
   *reinterpret_cast<uint2*>(op + 4) = make_uint2(w4[2], w4[3]);
-  if (p.lse && d0 == 0) p.lse[slot] = wsum > 0.0f ? M + __logf(wsum) : -INFINITY;
+  if (p.lse && d0 == 0) p.lse[slot] = wsum > 0.0f ? M + __logf(wsum) : wsum == 0.0f ? -INFINITY : wsum;
 }
 
 }  // namespace
@@ -1200,7 +1248,9 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs p) {
 namespace {
 
 int64_t stage_blocks(int64_t Ns, int64_t Hkv, int64_t T) { return Ns * Hkv * ((T + kBlockKeys - 1) / kBlockKeys); }
-int64_t stage_block_bytes(int64_t D) { return D == 128 ? (int64_t)sizeof(BlockImg<128>) : (int64_t)sizeof(BlockImg<64>); }
+int64_t stage_block_bytes(int64_t D) {
+  return D == 256 ? (int64_t)sizeof(BlockImg<256>) : D == 128 ? (int64_t)sizeof(BlockImg<128>) : (int64_t)sizeof(BlockImg<64>);
+}
 
 // The second prefix level of od_branched_attn_staged2 (absent for the other entry points).
 struct Level2 {
@@ -1221,8 +1271,7 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
   if (dq != OD_DEQUANT_BF16 && dq != OD_DEQUANT_FP32) return OD_ERR_UNSUPPORTED;
   if (R < 0 || Hq < 1 || Hkv < 1 || t < 1 || Ns < 1 || T < 0 || cap < T || max_rows < 0) return OD_ERR_SHAPE;
   if (Hq % Hkv) return OD_ERR_UNSUPPORTED;
-  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
-  if (t > 256) return OD_ERR_UNSUPPORTED;
+  if (!block_d_ok(D)) return OD_ERR_UNSUPPORTED;
   if (!row_start && Ns != 1) return OD_ERR_SHAPE;
   if (nsplit < 1 || nsplit > 256) return OD_ERR_SHAPE;
   if (!row_start) max_rows = R;
@@ -1261,7 +1310,9 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
              l2 ? (int)l2->T2 : 0, l2 ? (int)l2->n_states : (int)Ns};
   dim3 grid((unsigned)tiles, (unsigned)Hkv, (unsigned)(Ns * nsplit)), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
-  if (D == 128) {
+  if (D == 256) {
+    staged ? branched_staged_kernel<256><<<grid, block, 0, st>>>(a) : branched_attn_kernel<256><<<grid, block, 0, st>>>(a);
+  } else if (D == 128) {
     staged ? branched_staged_kernel<128><<<grid, block, 0, st>>>(a) : branched_attn_kernel<128><<<grid, block, 0, st>>>(a);
   } else {
     staged ? branched_staged_kernel<64><<<grid, block, 0, st>>>(a) : branched_attn_kernel<64><<<grid, block, 0, st>>>(a);
@@ -1271,7 +1322,9 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
     if (rc != OD_OK) return rc;
     const int64_t threads = R * Hq * t * (D / 8);
     const unsigned blocks = (unsigned)((threads + 255) / 256);
-    if (D == 128) {
+    if (D == 256) {
+      combine_kernel<256><<<blocks, 256, 0, st>>>(a);
+    } else if (D == 128) {
       combine_kernel<128><<<blocks, 256, 0, st>>>(a);
     } else {
       combine_kernel<64><<<blocks, 256, 0, st>>>(a);
@@ -1310,7 +1363,7 @@ extern "C" int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sq
 
 extern "C" int od_attn_stage_size(int64_t Ns, int64_t Hkv, int64_t T, int64_t D, int64_t* img_bytes) {
   if (Ns < 1 || Hkv < 1 || T < 0) return OD_ERR_SHAPE;
-  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (!block_d_ok(D)) return OD_ERR_UNSUPPORTED;
   if (!img_bytes) return OD_ERR_NULL;
   *img_bytes = stage_blocks(Ns, Hkv, T) * stage_block_bytes(D);
   return OD_OK;
@@ -1321,7 +1374,7 @@ extern "C" int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq
                              float scale, int dequant, void* img, int64_t img_bytes, od_stream_t stream) {
   if (Ns < 1 || Hkv < 1 || T < 0 || cap < T) return OD_ERR_SHAPE;
   if (dequant != OD_DEQUANT_BF16 && dequant != OD_DEQUANT_FP32) return OD_ERR_UNSUPPORTED;
-  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (!block_d_ok(D)) return OD_ERR_UNSUPPORTED;
   if (T == 0) return OD_OK;
   if (!kq || !ks || !vq || !vs || !img) return OD_ERR_NULL;
   if (!od_aligned16(kq) || !od_aligned16(vq) || !od_aligned16(img)) return OD_ERR_ALIGN;
@@ -1333,7 +1386,9 @@ extern "C" int od_attn_stage(const int8_t* kq, const float* ks, const int8_t* vq
               scale * 1.4426950408889634f, dequant};
   dim3 grid((unsigned)nb, (unsigned)Hkv, (unsigned)Ns), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
-  if (D == 128) {
+  if (D == 256) {
+    stage_kernel<256><<<grid, block, 0, st>>>(a);
+  } else if (D == 128) {
     stage_kernel<128><<<grid, block, 0, st>>>(a);
   } else {
     stage_kernel<64><<<grid, block, 0, st>>>(a);
@@ -1349,7 +1404,7 @@ extern "C" int od_branched_attn_staged(const uint16_t* q, int64_t sqr, int64_t s
                                        int64_t Hkv, int64_t t, int64_t D, int64_t Ns, int64_t T, float scale,
                                        int64_t nsplit, float* ws, int64_t ws_floats, od_stream_t stream) {
   if (T > 0 && !img) return OD_ERR_NULL;
-  if ((D == 64 || D == 128) && Ns >= 1 && Hkv >= 1 && T > 0 && img_bytes < stage_blocks(Ns, Hkv, T) * stage_block_bytes(D))
+  if (block_d_ok(D) && Ns >= 1 && Hkv >= 1 && T > 0 && img_bytes < stage_blocks(Ns, Hkv, T) * stage_block_bytes(D))
     return OD_ERR_SHAPE;
   return branched_launch(q, sqr, sqh, sqt, k_own, skr, skh, skt, v_own, svr, svh, svt, nullptr, nullptr, nullptr,
                          nullptr, nullptr, T > 0 ? img : nullptr, row_start, max_rows, out, sor, soh, sot, lse, R, Hq,
@@ -1362,7 +1417,7 @@ extern "C" int od_attn_stage_bf16(const uint16_t* k, int64_t skb, int64_t skh, i
                                   int64_t Hkv, int64_t T, int64_t D, float scale, void* img, int64_t img_bytes,
                                   od_stream_t stream) {
   if (Ns < 1 || Hkv < 1 || T < 0) return OD_ERR_SHAPE;
-  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (!block_d_ok(D)) return OD_ERR_UNSUPPORTED;
   if (T == 0) return OD_OK;
   if (!k || !v || !img) return OD_ERR_NULL;
   const int64_t strides[] = {skb, skh, skt, svb, svh, svt};
@@ -1376,7 +1431,9 @@ extern "C" int od_attn_stage_bf16(const uint16_t* k, int64_t skb, int64_t skh, i
                   scale * 1.4426950408889634f};
   dim3 grid((unsigned)nb, (unsigned)Hkv, (unsigned)Ns), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
-  if (D == 128) {
+  if (D == 256) {
+    stage_bf16_kernel<256><<<grid, block, 0, st>>>(a);
+  } else if (D == 128) {
     stage_bf16_kernel<128><<<grid, block, 0, st>>>(a);
   } else {
     stage_bf16_kernel<64><<<grid, block, 0, st>>>(a);
@@ -1441,7 +1498,7 @@ extern "C" int od_branched_attn_staged2(const uint16_t* q, int64_t sqr, int64_t 
   if (n_groups < 1 || n_states < 1 || T < 0) return OD_ERR_SHAPE;
   if (T > 0 && !img) return OD_ERR_NULL;
   if (!group_state && n_groups > n_states) return OD_ERR_SHAPE;
-  if ((D == 64 || D == 128) && T > 0 && img_bytes < stage_blocks(n_states, Hkv, T) * stage_block_bytes(D))
+  if (block_d_ok(D) && T > 0 && img_bytes < stage_blocks(n_states, Hkv, T) * stage_block_bytes(D))
     return OD_ERR_SHAPE;
   const Level2 l2{img2, img2_bytes, group_state, T2, n_states};
   // with T = 0 the level-1 images may be absent: the staged path then reads only the second level
@@ -1674,6 +1731,31 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
   const int per_row = p.t * p.rep;
   const int nslots = nrows * per_row;
   if (nslots <= 0) return;  // uniform over the workgroup
+  if (nslots > 32) {
+    // the caller's max_rows understated this state's rows (one wave holds at most 32 slots): its outputs become NaN,
+    // a visible error instead of unwritten memory. With splits every split poisons its own partials and LSEs, so the
+    // merge gives NaN as well.
+    const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
+    for (int i = threadIdx.x; i < nslots * (D / 8); i += blockDim.x) {
+      const int z = i / (D / 8), d0 = (i % (D / 8)) * 8;
+      const int zr = z / per_row, zrem = z - zr * per_row;
+      const int row = row0 + zr, head = g * p.rep + zrem % p.rep, tk = zrem / p.rep;
+      if (row >= p.R) break;
+      const int64_t slot_idx = ((int64_t)row * p.Hq + head) * p.t + tk;
+      if (p.nsplit > 1) {
+        float* po = p.part + ((int64_t)sp * nsl + slot_idx) * D + d0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) po[e] = __builtin_nanf("");
+        if (d0 == 0) p.part[(int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx] = __builtin_nanf("");
+      } else {
+        uint16_t* op = p.out + (int64_t)row * p.sor + (int64_t)head * p.soh + (int64_t)tk * p.sot + d0;
+        *reinterpret_cast<uint2*>(op) = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
+        *reinterpret_cast<uint2*>(op + 4) = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
+        if (p.lse && d0 == 0) p.lse[slot_idx] = __builtin_nanf("");
+      }
+    }
+    return;
+  }
   // the wave index made visibly uniform: the tile offsets derived from it are scalar buffer offsets
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5, c = lane & 31;

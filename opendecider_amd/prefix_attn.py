@@ -49,16 +49,56 @@ def _split_attention(q, k, v, Kp, Vp, pm, scale, dequant: str = "bf16"):
 split_attention = _split_attention
 
 
+def group_rows(row_state: torch.Tensor, n_states: int, max_rows: int | None = None):
+    """Rows in any state order -> the grouped layout the one-launch kernels take. row_state (R,) integer device
+    tensor, row i reads state row_state[i] (the reference's `rows`, prefix_attn.py:103-117,152-154). Returns
+    (order, row_start, max_rows): order (R,) int64 lists the rows grouped by state, stably (rows of one state keep
+    their relative order); row_start int32 (n_states + 1,) the groups' offsets in `order`; max_rows the largest
+    group. All on the device with no host sync when max_rows is given (a caller that captures a graph knows it);
+    otherwise one host read, which also checks that every state index lies in [0, n_states)."""
+    rs = row_state.reshape(-1).to(torch.int64)
+    order = torch.argsort(rs, stable=True)
+    # row_start[s] = number of rows whose state is below s (searchsorted on the sorted states)
+    bounds = torch.arange(n_states + 1, dtype=torch.int64, device=rs.device)
+    row_start = torch.searchsorted(rs.index_select(0, order), bounds).to(torch.int32)
+    if max_rows is None:
+        counts = row_start[1:] - row_start[:-1]
+        lo, hi, mr = torch.stack([rs.min(), rs.max(), counts.max().to(torch.int64)]).tolist() if rs.numel() else (0, 0, 0)
+        if lo < 0 or hi >= n_states:
+            raise ValueError(f"row_state values must lie in [0, {n_states}), got [{lo}, {hi}]")
+        max_rows = int(mr)
+    return order, row_start, int(max_rows)
+
+
 def split_attention_int8(q, k, v, Kq, Ks, Vq, Vs, pm, scale, row_counts=None, return_lse: bool = False,
-                         dequant: str = "bf16"):
+                         dequant: str = "bf16", row_state=None, max_rows: int | None = None):
     """The batched form: rows of several states in one launch. q (R, Hq, t, D); k/v (R, Hkv, t, D); Kq/Vq int8
-    (Ns, Hkv, T, D) or (Hkv, T, D); Ks/Vs fp32 (Ns, Hkv, T[, 1]); pm (Ns, T) bool or None; row_counts: how many
-    consecutive rows belong to each state (rows grouped by state; None for one state); dequant as
-    _split_attention."""
+    (Ns, Hkv, T, D) or (Hkv, T, D); Ks/Vs fp32 (Ns, Hkv, T[, 1]); pm (Ns, T) bool or None; dequant as
+    _split_attention. Which rows read which state, one of:
+      * row_counts: how many consecutive rows belong to each state (rows grouped by state);
+      * row_state: (R,) integer device tensor, row i reads state row_state[i], rows in any order (the reference's
+        `rows`, prefix_attn.py:152-154); the rows are grouped on the device (group_rows), attended in one launch and
+        returned in the caller's order. max_rows: the largest number of rows of one state, when the caller knows it
+        (no host sync; the state indices are then trusted to lie in [0, Ns));
+      * neither: one state."""
     if Kq.dim() == 3:
         Kq, Vq, Ks, Vs = Kq[None], Vq[None], Ks[None], Vs[None]
     Ks = Ks.float().reshape(Kq.shape[:3]).contiguous()
     Vs = Vs.float().reshape(Vq.shape[:3]).contiguous()
-    return kernels.branched_attn(q, k, v, Kq.contiguous(), Ks, Vq.contiguous(), Vs, scale, kvalid=pm,
-                                 row_counts=row_counts, length=Kq.shape[2] if pm is None else None,
-                                 return_lse=return_lse, dequant=dequant)
+    length = Kq.shape[2] if pm is None else None
+    if row_state is None:
+        return kernels.branched_attn(q, k, v, Kq.contiguous(), Ks, Vq.contiguous(), Vs, scale, kvalid=pm,
+                                     row_counts=row_counts, length=length, return_lse=return_lse, dequant=dequant)
+    if row_counts is not None:
+        raise ValueError("split_attention_int8: give row_counts or row_state, not both")
+    if row_state.numel() != q.shape[0]:
+        raise ValueError("split_attention_int8: row_state must have one entry per row")
+    order, row_start, max_rows = group_rows(row_state.to(q.device), Kq.shape[0], max_rows)
+    res = kernels.branched_attn(q.index_select(0, order), k.index_select(0, order), v.index_select(0, order),
+                                Kq.contiguous(), Ks, Vq.contiguous(), Vs, scale, kvalid=pm, length=length,
+                                row_start=row_start, max_rows=max_rows, return_lse=return_lse, dequant=dequant)
+    out_g, lse_g = res if return_lse else (res, None)
+    out = torch.empty_like(out_g).index_copy_(0, order, out_g)
+    if not return_lse:
+        return out
+    return out, torch.empty_like(lse_g).index_copy_(0, order, lse_g)

@@ -1,6 +1,7 @@
 """The C ABI's argument checks, driven on the CPU: every call below is refused by the host-side validation with its
 OD_ERR_* code before any HIP call (no GPU work is launched; a call whose arguments pass validation is never made
 here). Also the reference's own CPU test of the fused-kernel installer (tests/test_int8_gemm.py:8-16) restated."""
+import ctypes
 import os
 
 import pytest
@@ -50,8 +51,9 @@ def test_attention_checks(L):
         return L.od_branched_attn(q, *s[:3], P, *s[3:6], P, *s[6:], P, P, P, P, None, None, 2, P, 1024, 128, 128,
                                   None, 2, Hq, Hkv, t, D, 1, 64, 64, 0.1, dq, None)
     assert branched(D=96) == UNSUP
+    assert branched(D=512) == UNSUP  # D in {64, 128, 256}, the reference's dispatch set
     assert branched(Hq=6, Hkv=4) == UNSUP
-    assert branched(t=300) == UNSUP
+    assert branched(t=0) == SHAPE
     assert branched(dq=5) == UNSUP
     assert branched(q=None) == NULL
     rc = L.od_branched_attn_split(P, *s[:3], P, *s[3:6], P, *s[6:], P, P, P, P, None, None, 2, P, 1024, 128, 128,
@@ -66,6 +68,11 @@ def test_attention_checks(L):
     assert L.od_attn_stage(P, P, P, P, None, 1, 1, 64, 32, 128, 0.1, 0, P, 1 << 20, None) == SHAPE  # cap < T
     assert L.od_attn_stage(P, P, P, P, None, 1, 1, 64, 64, 128, 0.1, 3, P, 1 << 20, None) == UNSUP  # dequant
     assert L.od_attn_stage(P, P, P, P, None, 1, 1, 64, 64, 128, 0.1, 0, P, 100, None) == SHAPE  # image too small
+    assert L.od_attn_stage(P, P, P, P, None, 1, 1, 64, 64, 256, 0.1, 0, P, 66063, None) == SHAPE  # D = 256 image
+    n = ctypes.c_int64(0)
+    for D in (64, 128, 256):  # a 64-key image holds 4 * 64 * D bytes of K and V plus 528 of per-key data
+        assert L.od_attn_stage_size(2, 3, 65, D, ctypes.byref(n)) == OK and n.value == 2 * 3 * 2 * (256 * D + 528)
+    assert L.od_attn_stage_size(1, 1, 64, 96, ctypes.byref(n)) == UNSUP
     w = (1024, 128, 128)
     assert L.od_wide_attn(P, *w, P, *w, P, *w, None, 0, P, *w, None, 1, 2, 2, 4, 4, 128, 96, 1, 0.1, None) == UNSUP
     assert L.od_wide_attn(P, *w, P, *w, P, *w, None, 0, P, *w, None, 1, 3, 2, 4, 4, 128, 128, 1, 0.1, None) == SHAPE

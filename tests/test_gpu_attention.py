@@ -76,6 +76,12 @@ CASES = {
     # V scales over 17 binades: the accumulator's power-of-two frame moves up and down across the state blocks and
     # many blocks enter with their probabilities scaled by 2^-1..2^-3
     "v_frames_spread": dict(seed=8, Ns=2, row_counts=[3, 4], Hq=8, Hkv=2, t=6, D=128, T=700, vspread=True),
+    # head_dim 256, Qwen3.5's full-attention heads (16 query / 4 KV heads), with key holes; and 8 / 2 heads with
+    # rows longer than one 32-key own block
+    "qwen35_d256_holes": dict(seed=13, Ns=2, row_counts=[3, 4], Hq=16, Hkv=4, t=6, D=256, T=300, holes=True),
+    "d256_gqa4_own_two_chunks": dict(seed=14, Ns=1, row_counts=[5], Hq=8, Hkv=2, t=40, D=256, T=129),
+    # rows of 300 tokens (10 own blocks, one slot tile spans a fraction of a row)
+    "long_rows_t300": dict(seed=15, Ns=2, row_counts=[2, 1], Hq=8, Hkv=2, t=300, D=128, T=100),
 }
 
 
@@ -149,7 +155,7 @@ def test_config1_branched_attention_full_shape(gpu_lib):
 
 SPLIT_CASES = [("two_states_holes", 2), ("two_states_holes", 7), ("own_two_chunks_d64", 3), ("own_only_T0", 4),
                ("empty_state_group", 3), ("t1_single_token_rows", 5), ("config4_like_t12", 64),
-               ("v_frames_spread", 5)]
+               ("v_frames_spread", 5), ("qwen35_d256_holes", 4), ("long_rows_t300", 2)]
 
 
 @pytest.mark.parametrize("name,n_split", SPLIT_CASES)
@@ -221,7 +227,8 @@ def test_stage_size_and_errors(gpu_lib):
 # ---- the reference caller's own arguments: dense bf16 Kp/Vp (prefix_attn.py:127, fed from :145-149)
 
 @pytest.mark.parametrize("n,Hq,Hkv,t,D,T,mask", [(5, 8, 2, 6, 128, 300, True), (3, 4, 4, 17, 64, 129, False),
-                                                 (32, 32, 8, 16, 128, 2048, False)])
+                                                 (32, 32, 8, 16, 128, 2048, False), (6, 16, 4, 9, 256, 300, True),
+                                                 (4, 8, 2, 33, 256, 140, True)])
 def test_split_attention_dense_prefix(gpu_lib, n, Hq, Hkv, t, D, T, mask):
     """_split_attention called exactly as the reference's _forward calls it: the state K/V materialized to dense bf16
     (q.to(bf16) * s.to(bf16)), a key mask pm (T,), own k/v, the softmax scale; against the oracle's
@@ -252,6 +259,7 @@ TWO_LEVEL = [
     dict(seed=62, Ns=1, counts=[4, 3], Hq=32, Hkv=8, t=16, D=128, T=2048, T2=130),
     dict(seed=63, Ns=3, counts=[1, 2, 1, 3], Hq=4, Hkv=4, t=9, D=64, T=0, T2=40),
     dict(seed=64, Ns=2, counts=[3, 5], Hq=16, Hkv=4, t=12, D=128, T=300, T2=256),
+    dict(seed=65, Ns=2, counts=[3, 2], Hq=16, Hkv=4, t=7, D=256, T=200, T2=90),
 ]
 
 
