@@ -592,6 +592,155 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------ small M
+// The small-M kernel (M up to a few hundred rows and few tiles: config 0's single linear, the question and record
+// passes): the 256-row tiles above leave most CUs idle there, and splitting K across workgroups costs int32 partial
+// planes in memory (2 x splits x M x N x 4 bytes) and a second launch. Here one workgroup of 4 waves owns a
+// 64 x BN tile and splits K inside itself: wave w sums the 128-byte k-chunks w, w + 4, w + 8, ... of the tile. Each
+// wave has two LDS buffers of its own (a chunk's 64 A rows and BN W rows, 128 bytes each, in the swizzled layout of
+// the 256-row kernel) and moves its next chunk in by LDS DMA (8 lanes per 128-byte line; rows past M / N and bytes
+// past K read as zeros) while it computes the current one, so the waves never wait for each other until the end.
+// The four partial tiles are then added through LDS (integer sums: exact, in any order) and the epilogue runs on
+// the sum. (Tried: operands loaded straight into the MFMA registers, 32 rows per load instruction, 1.8x slower;
+// three chunks in flight per wave staged through registers and copied to LDS, 1.3x slower.)
+constexpr int kSmWaves = 4;
+constexpr int kSmBM = 64;
+
+template <int BN>
+__device__ __forceinline__ void small_tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  // XCD-aware: workgroup b runs on XCD b % 8; each XCD takes a contiguous range of tiles, M fastest, so the tiles
+  // that read one W panel share an XCD's L2
+  const int ntiles = tiles_m * tiles_n;
+  const int xcd = bid & 7, local = bid >> 3;
+  const int per = ntiles >> 3, rem = ntiles & 7;
+  const int id = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  tm = id % tiles_m;
+  tn = id / tiles_m;
+}
+
+template <int BN, bool SWIGLU>
+__global__ __launch_bounds__(kSmWaves * 64, 1) void w8a8_gemm_small_kernel(GemmArgs p) {
+  constexpr int TM = kSmBM / 32, TN = BN / 32;
+  constexpr int kRows = kSmBM + BN;        // rows of one chunk: A rows, then W rows
+  constexpr int kChunk = kRows * BK;       // bytes of one chunk buffer
+  constexpr int kLoads = kRows / 8;        // LDS DMA loads of a chunk (8 rows of 128 bytes each)
+  constexpr int kLoadsA = kSmBM / 8;
+  static_assert(kLoads <= 63, "the vmcnt wait counts one chunk's loads");
+  // [wave][buffer][chunk bytes]; after the main loop the first 64 x BN x 4 x 4 bytes hold the partial tiles
+  __shared__ __attribute__((aligned(16))) int8_t smem[kSmWaves * 2 * kChunk];
+  static_assert(kSmWaves * TM * TN * 4 * 64 * 16 <= kSmWaves * 2 * kChunk, "partial tiles fit the chunk buffers");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5, c = lane & 31;
+  int tm, tn;
+  small_tile_of<BN>(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * kSmBM, n0 = (int64_t)tn * BN;
+  const int rows_a = (int)min((int64_t)kSmBM, p.M - m0), rows_w = (int)min((int64_t)BN, p.N - n0);
+  const int K = (int)p.K;
+  const auto ra = __builtin_amdgcn_make_buffer_rsrc((void*)(p.a + m0 * p.lda), (short)0,
+                                                    (int)((rows_a - 1) * p.lda + K), 0x00020000);
+  const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)(p.w + n0 * p.ldw), (short)0,
+                                                    (int)((rows_w - 1) * p.ldw + K), 0x00020000);
+  // DMA load o moves chunk rows 8 o .. 8 o + 7: lane l takes row 8 o + l / 8 and physical 16-byte chunk l % 8 of it,
+  // which holds logical chunk (l % 8) ^ ((row >> 1) & 7) = (l % 8) ^ ((4 (o & 1) + l / 16) & 7)
+  const int dc0 = (lane & 7) ^ ((lane >> 4) & 7), dc1 = (lane & 7) ^ ((4 + (lane >> 4)) & 7);
+  const int va0 = (int)((lane >> 3) * p.lda) + dc0 * 16, va1 = (int)((lane >> 3) * p.lda) + dc1 * 16;
+  const int vw0 = (int)((lane >> 3) * p.ldw) + dc0 * 16, vw1 = (int)((lane >> 3) * p.ldw) + dc1 * 16;
+  const uint32_t lds_w = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)(smem) + wave * 2 * kChunk;
+  auto dma_chunk = [&](int b, int kc) {
+    const int kb = __builtin_amdgcn_readfirstlane(kc * BK);  // wave-uniform (the scalar offset of the loads)
+    b = __builtin_amdgcn_readfirstlane(b);
+#pragma unroll
+    for (int o = 0; o < kLoads; ++o) {
+      const bool is_a = o < kLoadsA;
+      const int oo = is_a ? o : o - kLoadsA;
+      const int dc = (o & 1) ? dc1 : dc0;
+      const int soff = kb + oo * 8 * (int)(is_a ? p.lda : p.ldw);
+      int vo = is_a ? ((o & 1) ? va1 : va0) : ((o & 1) ? vw1 : vw0);
+      if (kb + dc * 16 >= K) vo = kOOB - soff;  // a K tail, or a chunk past the last: zeros
+      dma16(is_a ? ra : rw, vo, soff, lds_w + b * kChunk + o * 1024);
+    }
+  };
+  v16i acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  const int nk = (K + BK - 1) / BK;
+  int kc = wave, b = 0;
+  dma_chunk(0, kc);
+  while (kc < nk) {
+    dma_chunk(b ^ 1, kc + kSmWaves);  // always issued (past the last chunk it reads zeros), so the count is fixed
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads) : "memory");  // this chunk's loads are in LDS
+    const int8_t* lb = smem + (wave * 2 + b) * kChunk;
+#pragma unroll
+    for (int s = 0; s < BK / 32; ++s) {
+      const int chunk = s * 2 + h;
+      v4i fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = *reinterpret_cast<const v4i*>(lb + swz(32 * i + c, chunk));
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = *reinterpret_cast<const v4i*>(lb + swz(kSmBM + 32 * j + c, chunk));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    // every fragment read of this buffer is done before the next iteration's DMA overwrites it
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    b ^= 1;
+    kc += kSmWaves;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) chunk's loads, before the LDS is reused
+  __syncthreads();
+  // the partial tiles in the MFMA result layout: [wave][tile][quad of registers][lane] as int4
+  v4i* part = reinterpret_cast<v4i*>(smem);
+  auto pidx = [](int w, int x, int r4, int l) { return ((w * TM * TN + x) * 4 + r4) * 64 + l; };
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        part[pidx(wave, i * TN + j, r4, lane)] = v4i{acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2],
+                                                     acc[i][j][4 * r4 + 3]};
+  __syncthreads();
+  // thread (r4 = wave, lane) of tile x holds rows 32 i + 8 r4 + 4 h + 0..3 of column 32 j + c; the epilogue is the
+  // fp32 arithmetic of the 256-row kernel in its order: t = (float(acc) sa[m]) sw[n], then + bias, + residual, one
+  // bf16 rounding; SwiGLU pairs columns (gate 2f, up 2f + 1) across neighbouring lanes
+#pragma unroll
+  for (int x = 0; x < TM * TN; ++x) {
+    const int i = x / TN, j = x % TN;
+    v4i s4 = part[pidx(0, x, wave, lane)];
+#pragma unroll
+    for (int w = 1; w < kSmWaves; ++w) s4 = s4 + part[pidx(w, x, wave, lane)];
+    const int64_t n = n0 + 32 * j + c;
+    const bool n_ok = n < p.N;
+    const float swn = n_ok ? p.sw[n] : 0.0f;
+    const float bn = (!SWIGLU && n_ok && p.bias) ? od_bf16_to_f32(p.bias[n]) : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t m = m0 + 32 * i + 8 * wave + 4 * h + e;
+      const bool m_ok = m < p.M;
+      const float sam = m_ok ? p.sa[m] : 0.0f;
+      const float t = ((float)s4[e] * sam) * swn;
+      if constexpr (SWIGLU) {
+        const float u = __shfl_xor(t, 1, 64);  // the up value of the pair, from lane c ^ 1
+        if (m_ok && n_ok && (c & 1) == 0)
+          p.out[m * p.ldo + n / 2] = (uint16_t)od_f32_to_bf16(od_silu_bf16(bfr(t)) * bfr(u));
+      } else {
+        if (m_ok && n_ok) {
+          float y = t;
+          if (p.bias) y = y + bn;
+          if (p.residual) y = y + od_bf16_to_f32(p.residual[m * p.ldr + n]);
+          p.out[m * p.ldo + n] = (uint16_t)od_f32_to_bf16(y);
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 namespace {
@@ -646,9 +795,23 @@ struct SplitPlan {
   int64_t ldws, ws_ints;
 };
 
+// Shapes for the small-M kernel (w8a8_gemm_small_kernel): up to 512 rows and at most two of its 64 x 64 tiles per
+// CU (it runs one workgroup per CU and pays each tile's first-chunk latency in full; M = 512 x N = 6144 is faster on
+// the 128 x 256 tiles with split-K). Its tile width: 64 columns when that gives every CU a tile, else 32 (twice the
+// tiles, each reading A again).
+constexpr int64_t kSmallMaxM = 512;
+bool small_m(int64_t M, int64_t N) {
+  return M <= kSmallMaxM && ((M + kSmBM - 1) / kSmBM) * ((N + 63) / 64) <= 2 * (int64_t)cu_count();
+}
+int small_bn(int64_t M, int64_t N) {
+  const int64_t tiles64 = ((M + kSmBM - 1) / kSmBM) * ((N + 63) / 64);
+  return tiles64 >= cu_count() ? 64 : 32;
+}
+
 SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
   const int nk = (int)((K + BK - 1) / BK);
   const SplitPlan none{1, nk, 0, 0};
+  if (small_m(M, N)) return none;  // the small-M kernel splits K inside its workgroups
   const Tiling t = tiling_of(M, N);
   const int64_t ntiles = t.tiles_m * t.tiles_n, cus = cu_count();
   if (ntiles * 2 > cus || nk < 4) return none;
@@ -719,6 +882,22 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
                 int32_t* ws = nullptr) {
   GemmArgs p = p0;
   const int64_t M = p.M, N = p.N, K = p.K;
+  if (!p.acc && small_m(M, N)) {
+    const int bn = small_bn(M, N);
+    const int64_t tiles_m = (M + kSmBM - 1) / kSmBM, tiles_n = (N + bn - 1) / bn;
+    if (tiles_m * tiles_n > 0x7fffffff) return OD_ERR_SHAPE;
+    p.tiles_m = (int)tiles_m;
+    p.tiles_n = (int)tiles_n;
+    const dim3 grid((unsigned)(tiles_m * tiles_n)), block(kSmWaves * 64);
+    if (bn == 64) {
+      swiglu ? w8a8_gemm_small_kernel<64, true><<<grid, block, 0, st>>>(p)
+             : w8a8_gemm_small_kernel<64, false><<<grid, block, 0, st>>>(p);
+    } else {
+      swiglu ? w8a8_gemm_small_kernel<32, true><<<grid, block, 0, st>>>(p)
+             : w8a8_gemm_small_kernel<32, false><<<grid, block, 0, st>>>(p);
+    }
+    return od_launch_status();
+  }
   const Tiling t = tiling_of(M, N);
   const int64_t tiles_m = t.tiles_m, tiles_n = t.tiles_n;
   if (tiles_m * tiles_n > 0x7fffffff) return OD_ERR_SHAPE;

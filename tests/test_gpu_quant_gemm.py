@@ -92,7 +92,10 @@ def test_gemm_int32_accumulators_bit_exact(gpu_lib, M, N, K):
     out, acc = kernels.w8a8_gemm(a.to(DEV), sa.to(DEV), w.to(DEV), sw.to(DEV), want_acc=True)
     ref_acc = oq.int_gemm(a, w)
     assert torch.equal(acc.cpu(), ref_acc)
-    assert torch.equal(out.cpu(), oq.w8a8_epilogue(ref_acc, sa, sw))
+    ref_out = oq.w8a8_epilogue(ref_acc, sa, sw)
+    assert torch.equal(out.cpu(), ref_out)
+    # without the accumulator output small M (<= 512 rows) takes the small-M kernel: the same bits
+    assert torch.equal(kernels.w8a8_gemm(a.to(DEV), sa.to(DEV), w.to(DEV), sw.to(DEV)).cpu(), ref_out)
 
 
 def test_gemm_extreme_accumulators(gpu_lib):
@@ -160,6 +163,8 @@ def test_config0_single_w8a8_linear(gpu_lib):
     assert torch.equal(xq.cpu(), rxq) and torch.equal(sx.cpu(), rsx)
     assert torch.equal(acc.cpu(), racc)
     assert torch.equal(out.cpu(), rout)
+    # the path the linear takes (no accumulator output: the small-M kernel at M = 256)
+    assert torch.equal(kernels.w8a8_gemm(xq, sx, w.to(DEV), sw.to(DEV)).cpu(), rout)
 
 
 def test_w8a8_linear_module_smoothquant(gpu_lib):
@@ -392,7 +397,8 @@ def test_gate_sigmoid_on_all_bf16_inputs(gpu_lib, K):
 
 
 def _one_pass(a, sa, w, sw, bias, res, swiglu):
-    """The GEMM without split-K: od_w8a8_gemm / od_w8a8_gemm_swiglu called directly."""
+    """The GEMM without split-K, by the 256-row tile kernel: od_w8a8_gemm / od_w8a8_gemm_swiglu called directly (a
+    plain GEMM also asks for the int32 accumulators, which only that kernel writes, so small M takes it too)."""
     from opendecider_amd import _lib
     from opendecider_amd._lib import ptr, stream_of
     M, K = a.shape
@@ -403,19 +409,45 @@ def _one_pass(a, sa, w, sw, bias, res, swiglu):
         rc = L.od_w8a8_gemm_swiglu(ptr(a), K, ptr(sa), ptr(w), K, ptr(sw), ptr(out), out.stride(0), M, N, K,
                                    stream_of(a))
     else:
+        acc = torch.empty(M, N, dtype=torch.int32, device=DEV)
         rc = L.od_w8a8_gemm(ptr(a), K, ptr(sa), ptr(w), K, ptr(sw), ptr(bias), ptr(res), N if res is not None else 0,
-                            ptr(out), N, None, 0, M, N, K, stream_of(a))
+                            ptr(out), N, ptr(acc), N, M, N, K, stream_of(a))
     assert rc == 0
     return out
 
 
 @pytest.mark.parametrize("M,N,K,epi", [(64, 6144, 2048, "plain"), (1, 2048, 6144, "bias_res"), (7, 3000, 4000, "res"),
-                                       (64, 2048, 2048, "bias"), (64, 24576, 4096, "swiglu"), (5, 1030, 6144, "swiglu"),
-                                       (33, 20, 2064, "bias_res"), (64, 4096, 12288, "res"), (200, 2048, 6144, "plain")])
+                                       (64, 2048, 2048, "bias"), (33, 20, 2064, "bias_res"), (64, 4096, 12288, "res"),
+                                       (200, 2048, 6144, "plain"), (256, 4096, 4096, "bias_res"),
+                                       (512, 2048, 6144, "res"), (129, 4104, 1040, "bias")])
+def test_small_m_kernel_bit_identical_to_256_row_kernel(gpu_lib, M, N, K, epi):
+    """Up to 512 rows the GEMM takes the small-M kernel (64-row tiles, K split over the workgroup's waves, the
+    partial tiles summed exactly through LDS): the same bits as one pass of the 256-row kernel, and on the smaller
+    cases as the oracle's. K tails (K % 128 != 0) and ragged N included."""
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(M + N + K)
+    a, w, sa, sw = _gemm_case(g, M, N, K)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16).to(DEV) if "bias" in epi else None
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV) if "res" in epi else None
+    ad, wd, sad, swd = a.to(DEV), w.to(DEV), sa.to(DEV), sw.to(DEV)
+    print(f"small-M M={M} N={N} K={K} {epi}", flush=True)
+    assert kernels.splitk_workspace(M, N, K, DEV) is None
+    got = kernels.w8a8_gemm(ad, sad, wd, swd, bias, res)
+    ref = _one_pass(ad, sad, wd, swd, bias, res, False)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    if M * N * K <= 64 * 6144 * 2048:
+        refo = oq.w8a8_epilogue(oq.int_gemm(a, w), sa, sw, None if bias is None else bias.cpu(),
+                                None if res is None else res.cpu())
+        assert torch.equal(got.cpu(), refo)
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(1024, 2048, 6144, "plain"), (600, 1030, 6144, "swiglu"),
+                                       (1024, 4096, 12288, "res"), (700, 2048, 6144, "bias_res"),
+                                       (1000, 20, 2064, "bias_res")])
 def test_splitk_bit_identical_to_one_pass(gpu_lib, M, N, K, epi):
-    """Small-M shapes take split-K (int32 partial planes in a workspace, summed exactly, then the same epilogue):
-    the output equals the one-pass GEMM's bit for bit, also when the workspace is one element short (the call then
-    runs one pass), and on the small cases the oracle's."""
+    """Mid-size M with few tiles takes split-K (int32 partial planes in a workspace, summed exactly, then the same
+    epilogue): the output equals the one-pass GEMM's bit for bit, also when the workspace is one element short (the
+    call then runs one pass), and on the small cases the oracle's."""
     from opendecider_amd import _lib, kernels
     from opendecider_amd._lib import ptr, stream_of
     g = torch.Generator().manual_seed(M + N + K)
@@ -426,8 +458,7 @@ def test_splitk_bit_identical_to_one_pass(gpu_lib, M, N, K, epi):
     swiglu = epi == "swiglu"
     print(f"splitk M={M} N={N} K={K} {epi}", flush=True)
     ws = kernels.splitk_workspace(M, N, K, DEV)
-    if (M, N, K) in ((1, 2048, 6144), (64, 4096, 12288), (64, 2048, 2048), (5, 1030, 6144), (200, 2048, 6144)):
-        assert ws is not None, "the plan should split this shape"
+    assert ws is not None, "the plan should split this shape"
     if swiglu:
         got = kernels.w8a8_gemm_swiglu(ad, sad, wd, swd)
     else:
