@@ -18,6 +18,7 @@ Conventions followed (reference file:line):
 """
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
@@ -107,6 +108,28 @@ def wide_attention_blocked(q, k, v, scale: float, kvalid=None, causal: bool = Tr
     if with_bound:
         return out, lse, 2.0 ** -7 * acc_abs / den
     return out, lse
+
+
+@contextlib.contextmanager
+def reference_gpu_arithmetic():
+    """Within this context every softmax attention of the oracle (split_attention's prefix and own parts, hence
+    branched_attention, two_level_attention and the prefill's causal attention) runs as the reference's CUDA path
+    computes it: _split_attention's two wide_attention calls (prefix_attn.py:50-57), i.e. the flash kernel's blocked
+    online softmax with P rounded to bf16 before P.V (wide_attention.py:54-62, restated by wide_attention_blocked),
+    instead of its CPU branch's one-shot fp32 softmax (prefix_attn.py:58-73). How far the two disagree end to end is
+    the spread between the reference's own GPU and CPU paths."""
+    global attention
+    cpu = attention
+
+    def blocked(q, k, v, scale: float, kvalid=None, causal: bool = True, dtype=torch.float32, chunk: int = 1 << 24):
+        o, lse = wide_attention_blocked(q, k, v, scale, kvalid, causal)
+        return o.to(dtype), lse.to(dtype)
+
+    attention = blocked
+    try:
+        yield
+    finally:
+        attention = cpu
 
 
 def lse_merge(o_p, l_p, o_o, l_o):

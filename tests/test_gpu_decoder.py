@@ -263,16 +263,29 @@ def test_decoder_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
     assert (lp.cpu() - ref).abs().max().item() <= 1e-6, "readout"
 
 
-def _assert_e2e(lp, ref, what):
-    """The path's end-to-end bar: probabilities within 1e-4 absolute, log-probabilities within 2e-3 relative; the
-    T = 1 difference (log-probs at T = 1 are log_softmax(T_E2E * lp), the same logits) is printed."""
+T1_MULTIPLE = 2.0
+
+
+def _assert_e2e(lp, ref, what, ref_gpu, t1_bar: bool = True):
+    """The path's end-to-end bars. At T_E2E: probabilities within 1e-4 absolute, log-probabilities within 2e-3
+    relative. At T = 1 (log-probs at T = 1 are log_softmax(T_E2E * lp), the same logits): the probabilities within
+    T1_MULTIPLE times the spread between the reference's own two attention arithmetics on this case, ref (its CPU
+    branch, prefix_attn.py:58-73) against ref_gpu (its CUDA path, the blocked flash kernel with P rounded to bf16,
+    oa.reference_gpu_arithmetic): no implementation can be held closer to one of them than the reference's own
+    paths are to each other (measured spreads 3e-4 .. 1.6e-3; planted kernel mistakes that this cannot see are
+    caught by the stage-by-stage test, tests/test_oracle_decoder.py). t1_bar False prints the T = 1 figures only
+    (a stack whose reference GPU arithmetic the oracle does not restate in full)."""
     lp = lp.cpu()
     dp = (lp.exp() - ref.exp()).abs().max().item()
     dl = ((lp - ref).abs() / ref.abs()).max().item()
     one = lambda x: torch.log_softmax(x * T_E2E, -1).exp()
     dp1 = (one(lp) - one(ref)).abs().max().item()
-    print(f"{what}: T={T_E2E:g}: max |dp| {dp:.2e}, max log-prob rel {dl:.2e}; at T=1 (diagnostic) max |dp| {dp1:.2e}")
+    spread1 = (one(ref_gpu) - one(ref)).abs().max().item()
+    print(f"{what}: T={T_E2E:g}: max |dp| {dp:.2e}, max log-prob rel {dl:.2e}; T=1: max |dp| {dp1:.2e}, the "
+          f"reference's GPU-vs-CPU spread {spread1:.2e} (ratio {dp1 / max(spread1, 1e-30):.2f})")
     assert dp <= PROB_ABS and dl <= REL, (dp, dl)
+    if t1_bar:
+        assert dp1 <= T1_MULTIPLE * spread1, (dp1, spread1)
 
 
 @pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
@@ -282,8 +295,10 @@ def test_decision_forward_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, T):
     cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
     print(f"{name}: e2e B={B} options={n_opt} t={t} T={T}", flush=True)
     ref = od.decision_forward(ids, w, emb, cfg, states, T)
+    with oa.reference_gpu_arithmetic():
+        ref_gpu = od.decision_forward(ids, w, emb, cfg, states, T)
     lp = dec.score(ids.to(DEV), gs)
-    _assert_e2e(lp, ref, name)
+    _assert_e2e(lp, ref, name, ref_gpu)
     perm = torch.randperm(n_opt, generator=torch.Generator().manual_seed(6))
     lp_p = dec.score(ids[:, perm].to(DEV), gs)
     assert (lp_p[:, :n_opt].exp() - lp[:, perm.to(DEV)].exp()).abs().max().item() <= 1e-6
@@ -325,6 +340,8 @@ def test_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, S, rec
     dec.prefill(ids_state.to(DEV), caches)
     torch.cuda.synchronize()
     _, kv_ref = od.prefill_forward(ids_state, w, emb, cfg)
+    with oa.reference_gpu_arithmetic():
+        _, kv_gpu = od.prefill_forward(ids_state, w, emb, cfg)
     for (kc, vc), ((kq, ks), (vq, vs)) in zip(caches[:1], kv_ref[:1]):
         _exact_quant(kc.q[:, :, :S].reshape(-1, cfg.head_dim), kc.scale[:, :, :S].reshape(-1),
                      kq.reshape(-1, cfg.head_dim), ks.reshape(-1), "layer 0 K cache")
@@ -334,12 +351,16 @@ def test_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, S, rec
     for r in recs:
         dec.prefill(r.to(DEV), caches)
         _, kv_ref = od.prefill_forward(r, w, emb, cfg, state_kv=kv_ref, n0=n0)
+        with oa.reference_gpu_arithmetic():
+            _, kv_gpu = od.prefill_forward(r, w, emb, cfg, state_kv=kv_gpu, n0=n0)
         n0 += r.shape[1]
     assert all(kc.length == n0 and vc.length == n0 for kc, vc in caches)
     lp = dec.score(ids.to(DEV), caches)
     ref = od.decision_forward(ids, w, emb, cfg, kv_ref, n0)
+    with oa.reference_gpu_arithmetic():
+        ref_gpu = od.decision_forward(ids, w, emb, cfg, kv_gpu, n0)
 
-    _assert_e2e(lp, ref, f"{name} (prefilled)")
+    _assert_e2e(lp, ref, f"{name} (prefilled)", ref_gpu)
 
 
 @pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
@@ -391,7 +412,10 @@ def test_question_cache_end_to_end(gpu_lib, name, cfg_kw, B, T, gs, Lq, qlen, n_
     lp = dec.score_qcache(ids_o.to(DEV), qc, gstates)
     q_kv = od.question_forward(ids_q, w, emb, cfg, states, T, gs)
     ref = od.qcache_decision_forward(ids_o, w, emb, cfg, states, T, q_kv, qlen, gs)
-    _assert_e2e(lp, ref, f"{name} (question cache)")
+    with oa.reference_gpu_arithmetic():
+        q_kv_gpu = od.question_forward(ids_q, w, emb, cfg, states, T, gs)
+        ref_gpu = od.qcache_decision_forward(ids_o, w, emb, cfg, states, T, q_kv_gpu, qlen, gs)
+    _assert_e2e(lp, ref, f"{name} (question cache)", ref_gpu)
     full = [i for i, n in enumerate(qlen) if n == Lq and gs.count(gs[i]) == 1]
     if len(full) == B:  # one unpadded question per state: rows that carry the question, scored by `score`
         rows = torch.cat([ids_q[full][:, None, :].expand(B, n_opt, Lq), ids_o[full]], 2)

@@ -7,16 +7,19 @@ out_proj quantizer, out_proj + residual and the MLP are bit-exact; the recurrenc
 order) is within one bf16 step of the float64 recurrence. Option rows
 read their request's conv window and recurrent state in place (seq_state), never a per-row copy. End to end: the
 path's bar at the harness's decision temperature T_E2E (probabilities 1e-4, log-probabilities 2e-3), option-order
-invariance <= 1e-6, a prefilled and record-appended state, and the captured scoring pass equal to eager."""
+invariance <= 1e-6, a prefilled and record-appended state, and the captured scoring pass equal to eager. The T = 1
+figures are printed, not held to the all-attention stacks' T = 1 bar: the reference runs the Gated DeltaNet layers
+through the fla Triton kernels (a dependency absent here, its bf16 chunked arithmetic not restated by the oracle), so
+the spread between the reference's own GPU and CPU arithmetic is known for the attention layers only."""
 import pytest
 import torch
 
-from helpers import PROB_ABS, REL
+from oracle import attention as oa
 from oracle import decoder as od
 from oracle import gdn as og
 from oracle import quant as oq
 
-from test_gpu_decoder import attention_layer_stages
+from test_gpu_decoder import _assert_e2e, attention_layer_stages
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -169,14 +172,6 @@ def test_hybrid_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
             _exact(gs[li].rec, states[li][1], f"layer {li}: recurrent state untouched")
 
 
-def _assert_e2e(lp, ref, what):
-    lp = lp.cpu()
-    dp = (lp.exp() - ref.exp()).abs().max().item()
-    dl = ((lp - ref).abs() / ref.abs()).max().item()
-    one = lambda x: torch.log_softmax(x * T_E2E, -1).exp()
-    dp1 = (one(lp) - one(ref)).abs().max().item()
-    print(f"{what}: T={T_E2E:g}: max |dp| {dp:.2e}, max log-prob rel {dl:.2e}; at T=1 (diagnostic) max |dp| {dp1:.2e}")
-    assert dp <= PROB_ABS and dl <= REL, (dp, dl)
 
 
 @pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)
@@ -184,8 +179,12 @@ def test_hybrid_decision_forward_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, 
     cfg, w, emb, states, ids, dec, gs = _setup(cfg_kw, B, n_opt, t, T)
     print(f"{name}: e2e B={B} options={n_opt} t={t} T={T}", flush=True)
     ref = od.decision_forward(ids, w, emb, cfg, states, T)
+    # the reference's own GPU arithmetic: the blocked flash attention and the recurrence in fp32 (the oracle's
+    # reference value uses float64)
+    with oa.reference_gpu_arithmetic():
+        ref_gpu = od.decision_forward(ids, w, emb, cfg, states, T, gdn_dtype=torch.float32)
     lp = dec.score(ids.to(DEV), gs)
-    _assert_e2e(lp, ref, name)
+    _assert_e2e(lp, ref, name, ref_gpu, t1_bar=False)
     perm = torch.randperm(n_opt, generator=torch.Generator().manual_seed(6))
     lp_p = dec.score(ids[:, perm].to(DEV), gs)
     assert (lp_p[:, :n_opt].exp() - lp[:, perm.to(DEV)].exp()).abs().max().item() <= 1e-6
@@ -215,6 +214,8 @@ def test_hybrid_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t,
     dec.prefill(ids_state.to(DEV), st)
     torch.cuda.synchronize()
     _, ref_st = od.prefill_forward(ids_state, w, emb, cfg)
+    with oa.reference_gpu_arithmetic():
+        _, gpu_st = od.prefill_forward(ids_state, w, emb, cfg, gdn_dtype=torch.float32)
     assert cfg.is_gdn(0)
     _exact(st[0].conv, ref_st[0][0], "layer 0 conv window")
     r0 = ref_st[0][1]
@@ -223,13 +224,17 @@ def test_hybrid_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t,
     for r in recs:
         dec.prefill(r.to(DEV), st)
         _, ref_st = od.prefill_forward(r, w, emb, cfg, state_kv=ref_st, n0=n0)
+        with oa.reference_gpu_arithmetic():
+            _, gpu_st = od.prefill_forward(r, w, emb, cfg, state_kv=gpu_st, n0=n0, gdn_dtype=torch.float32)
         n0 += r.shape[1]
     assert st.length == n0
     torch.cuda.synchronize()
     _exact(st[0].conv, ref_st[0][0], "layer 0 conv window after the records")
     lp = dec.score(ids.to(DEV), st)
     ref = od.decision_forward(ids, w, emb, cfg, ref_st, n0)
-    _assert_e2e(lp, ref, f"{name} (prefilled)")
+    with oa.reference_gpu_arithmetic():
+        ref_gpu = od.decision_forward(ids, w, emb, cfg, gpu_st, n0, gdn_dtype=torch.float32)
+    _assert_e2e(lp, ref, f"{name} (prefilled)", ref_gpu, t1_bar=False)
 
 
 @pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,T", CASES)

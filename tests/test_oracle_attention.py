@@ -211,3 +211,32 @@ def test_wide_blocked_empty_rows():
     kv = torch.zeros(1, 5, dtype=torch.bool)
     ob, lb = oa.wide_attention_blocked(q, k, v, 0.3, kv, causal=False)
     assert torch.count_nonzero(ob).item() == 0 and torch.isneginf(lb).all()
+
+
+def test_reference_gpu_arithmetic_composes_the_blocked_kernel():
+    """Inside oa.reference_gpu_arithmetic(), split_attention is the reference's CUDA composition (prefix_attn.py:
+    50-57): the blocked flash kernel on the prefix (non-causal, key mask) and on the row's own keys (causal), merged
+    by LSE; it stays within the blocked kernel's bf16-P flip bound of the exact fp32 result; and the CPU arithmetic
+    is back afterwards."""
+    g = torch.Generator().manual_seed(21)
+    n, Hq, Hkv, t, D, T = 3, 8, 2, 5, 64, 150
+    q = torch.randn(n, Hq, t, D, generator=g).bfloat16()
+    k = torch.randn(n, Hkv, t, D, generator=g).bfloat16()
+    v = torch.randn(n, Hkv, t, D, generator=g).bfloat16()
+    Kp = torch.randn(Hkv, T, D, generator=g).bfloat16().float()
+    Vp = torch.randn(Hkv, T, D, generator=g).bfloat16().float()
+    pm = torch.rand(T, generator=g) > 0.2
+    exact, lse_exact = oa.split_attention(q, k, v, Kp, Vp, pm, 0.125)
+    with oa.reference_gpu_arithmetic():
+        got, lse = oa.split_attention(q, k, v, Kp, Vp, pm, 0.125)
+    assert oa.attention.__name__ == "attention"
+    qs = q.transpose(0, 1).reshape(1, Hq, n * t, D)
+    o_p, l_p, b_p = oa.wide_attention_blocked(qs, Kp[None], Vp[None], 0.125, pm[None], causal=False, with_bound=True)
+    o_p, l_p = o_p.reshape(Hq, n, t, D).transpose(0, 1), l_p.reshape(Hq, n, t).transpose(0, 1)
+    o_o, l_o, b_o = oa.wide_attention_blocked(q, k, v, 0.125, None, causal=True, with_bound=True)
+    want, lse_want = oa.lse_merge(o_p, l_p, o_o, l_o)
+    assert torch.equal(got, want) and torch.equal(lse, lse_want)
+    bound = b_p.reshape(Hq, n, t, D).transpose(0, 1) + b_o
+    assert ((got - exact).abs() <= bound + 1e-5).all()
+    assert (lse - lse_exact).abs().max().item() <= 1e-5
+    assert (got - exact).abs().max().item() > 0  # the bf16 rounding of P is there

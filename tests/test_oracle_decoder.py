@@ -3,6 +3,7 @@ closed form, RoPE as a complex rotation (norm preservation, relative-position pr
 normalisation, and option-order invariance of the whole forward."""
 import math
 
+import pytest
 import torch
 
 from oracle import decoder as od
@@ -321,3 +322,68 @@ def test_question_cache_equals_rows_that_carry_the_question():
     rows = torch.cat([ids_q[:, None, :].expand(2, n_opt, Lq), ids_o], 2)  # (2, n_opt, Lq + t)
     lp_rows = od.decision_forward(rows, w, emb, cfg, states, 70, attn_dtype=torch.float64, pool_last=t)
     assert (lp_qc - lp_rows).abs().max().item() <= 1e-6
+
+
+def _layer0_attention_inputs():
+    """Layer 0's attention inputs at the GPU end-to-end test's 9B scoring configuration, computed by the oracle's
+    stage functions exactly as tests/test_gpu_decoder.py's stage-by-stage test does: (qkv before RoPE, cfg, layer
+    weights, positions, rope tables, the (R, t) layout, the int8 state, row states)."""
+    from helpers import decoder_case
+    from oracle import quant as oq
+    cfg_kw, B, n_opt, t, T = E2E_SCORING
+    cfg, w, emb, states, ids = decoder_case(cfg_kw, B, n_opt, t, T, T_E2E)
+    R = B * n_opt
+    lw, ql = w["layers"][0], od.quantize_layer(w["layers"][0])
+    h = emb[ids.reshape(-1)]
+    xq, sx = oq.act_quant(od.rmsnorm(h, lw["ln1"], cfg.eps), ql["wqkv"][2])
+    qkv_lin, _ = od.split_qkv(oq.w8a8_epilogue(oq.int_gemm(xq, ql["wqkv"][0]), sx, ql["wqkv"][1]), cfg)
+    pos = (T + torch.arange(t)).repeat(R)
+    cos, sin = od.rope_tables(cfg, T + t)
+    return qkv_lin, cfg, lw, pos, cos, sin, R, t, states[0], torch.arange(B).repeat_interleave(n_opt)
+
+
+def _heads(qkv, cfg, R, t):
+    D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    qh = qkv[:, :Hq * D].reshape(R, t, Hq, D).transpose(1, 2)
+    kh = qkv[:, Hq * D:(Hq + Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
+    vh = qkv[:, (Hq + Hk) * D:(Hq + 2 * Hk) * D].reshape(R, t, Hk, D).transpose(1, 2)
+    return qh, kh, vh
+
+
+def test_stage_checks_catch_the_mistakes_the_end_to_end_bar_cannot_see():
+    """Three kernel mistakes that move the end-to-end probabilities by less than the bar (0.7-1.1e-4 at T = 24, and
+    at T = 1 less than the reference's own GPU-vs-CPU spread): RoPE one position off, a non-causal own block, each
+    key's V dequantized with the neighbouring token's scale. The GPU stage-by-stage test compares each stage with the
+    oracle fed the GPU's input to that stage; here each mistake is planted in a copy of the oracle's stage and the
+    same comparison (bit-exact for q/k norm + RoPE, the 2e-3 bar of tests/helpers.py for the attention) rejects it,
+    while the unplanted stage passes it."""
+    from helpers import assert_close_rel
+    from oracle import attention as oa
+    qkv_lin, cfg, lw, pos, cos, sin, R, t, ((kq, ks), (vq, vs)), row_state = _layer0_attention_inputs()
+    D, Hq = cfg.head_dim, cfg.n_heads
+    M = R * t
+    # RoPE: the GPU test asserts torch.equal on the bits of the fused QKV + q/k norm + RoPE output
+    qkv = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
+    qkv_again = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
+    qkv_off = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos - 1)
+    assert torch.equal(qkv_again.view(torch.int16), qkv.view(torch.int16))
+    assert not torch.equal(qkv_off.view(torch.int16), qkv.view(torch.int16))
+    # attention: the GPU test asserts assert_close_rel(GPU output, oracle on the GPU's q/k/v)
+    qh, kh, vh = _heads(qkv, cfg, R, t)
+
+    def run(vs_=vs):
+        o, _ = oa.branched_attention_int8(qh, kh, vh, kq, ks, vq, vs_, D ** -0.5, None, row_state, dequant="bf16")
+        return o.to(torch.bfloat16).float().transpose(1, 2).reshape(M, Hq * D)
+
+    ref = run()
+    assert_close_rel(ref, ref, what="the unplanted stage")
+    orig = oa.attention
+    oa.attention = lambda q, k, v, scale, kvalid=None, causal=True, **kw: orig(q, k, v, scale, kvalid, False, **kw)
+    try:
+        noncausal = run()
+    finally:
+        oa.attention = orig
+    neighbour = run(vs.roll(-1, dims=2))
+    for what, got in (("non-causal own block", noncausal), ("neighbouring V scale", neighbour)):
+        with pytest.raises(AssertionError):
+            assert_close_rel(got, ref, what=what)
