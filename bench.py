@@ -17,8 +17,13 @@ int8 MFMA), the branched attention's figures, and a CPU baseline (the oracle, on
 sample of the same workload, scaled). The default line also carries the full decision forward from token ids
 ("decision": 4096-token states prefilled, 64 options x 24 tokens), the wide-choice growing state ("wide_choice":
 a 32768-token int8 state + 256-token records, 2 x 255 options x 12 tokens) and the decision on the Qwen3.5 hybrid
-stack ("hybrid": 24 Gated DeltaNet + 8 full-attention layers), each with its own CPU baseline (--scoring-only leaves
-them out).
+stack ("hybrid": 24 Gated DeltaNet + 8 full-attention layers), each with its own CPU baseline, and the kernel-level
+figures: the few-slot KV-bound attention ("attention_kv_bound", 16 query slots per KV head) beside the KV-bound probe
+as the survey defines it ("attention_kv_probe": 32768-token states, 2 options x 16 tokens, 128 slots per KV head),
+the single W8A8 linear of config 0 with the reference's CPU linear path ("config0_linear"), the reference's
+scripts/bench_gemm.py sweep beside the vendor int8 GEMM ("gemm_sweep") and scripts/bench_qcache_rows.py's question
+cache shapes with a CPU baseline ("qcache_rows"). --scoring-only leaves all sub-objects out. Every CPU baseline is
+the median of --cpu-sample-repeats timed runs after one warm-up and names the host CPU model.
 """
 from __future__ import annotations
 
@@ -101,7 +106,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--scoring-only", action="store_true",
                     help="the default line without its decision / wide_choice sub-objects")
-    ap.add_argument("--cpu-sample-repeats", type=int, default=3)
+    ap.add_argument("--cpu-sample-repeats", type=int, default=5)
     return ap.parse_args()
 
 
@@ -273,6 +278,35 @@ GEMM_TRAFFIC_M4096 = {(6144, 4096): 218.5e6, (4096, 4096): 168.0e6, ("swiglu", 2
                       (4096, 12288): 369.3e6}
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo, what lscpu prints as 'Model name')."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_timed(fn, repeats: int):
+    """One warm-up call, then `repeats` timed calls (time.perf_counter); returns (median seconds, all times)."""
+    fn()
+    ts = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2], ts
+
+
+def cpu_fields(torch, repeats: int) -> dict:
+    """The host description every CPU baseline carries."""
+    return {"cores": torch.get_num_threads(), "host_cpus": os.cpu_count(), "cpu_model": cpu_model(),
+            "repeats": repeats, "statistic": f"median of {repeats} after one warm-up"}
+
+
 def cpu_baseline(args):
     """The oracle (CPU torch restatement of the path) on a bounded sample: ONE request (32 options x 16 tokens, its
     2048-token int8 state) through ONE 9B-dims layer, timed and scaled x36 layers. A decision is one request, so
@@ -298,16 +332,10 @@ def cpu_baseline(args):
     def run():
         return od.layer_forward(h, lw, ql, cfg, (kq, ks[..., 0]), (vq, vs[..., 0]), n_opt, t, pos, cos, sin)
 
-    run()
-    ts = []
-    for _ in range(args.cpu_sample_repeats):
-        t0 = time.perf_counter()
-        run()
-        ts.append(time.perf_counter() - t0)
-    ts.sort()
-    per_layer = ts[len(ts) // 2]
+    per_layer, _ = cpu_timed(run, args.cpu_sample_repeats)
     decision_s = per_layer * args.layers  # one request's scoring pass
-    return {"value": 1.0 / decision_s, "unit": "decisions/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": 1.0 / decision_s, "unit": "decisions/s", **cpu_fields(torch, args.cpu_sample_repeats),
+            "kind": "port",
             "sample": (f"1 request (32 options x 16 tokens, {T}-token int8 state) x 1 of {args.layers} layers, "
                        f"median of {args.cpu_sample_repeats} after a warm-up, {per_layer * 1e3:.0f} ms per layer, "
                        f"scaled x{args.layers} layers")}
@@ -315,7 +343,8 @@ def cpu_baseline(args):
 
 def cpu_baseline_decision(args):
     """The oracle on a bounded sample of the decision forward: ONE request (a 4096-token state of random ids
-    prefilled, then 64 options x 24 tokens scored) through ONE 9B-dims layer, timed once, scaled x36 layers."""
+    prefilled, then 64 options x 24 tokens scored) through ONE 9B-dims layer, the median of the timed runs after a
+    warm-up, scaled x36 layers."""
     import torch
 
     from oracle import decoder as od
@@ -327,20 +356,23 @@ def cpu_baseline_decision(args):
     S, n_opt, t = 4096, 64, 24
     ids_s = torch.randint(0, 4096, (1, S), generator=g)
     ids_o = torch.randint(0, 4096, (1, n_opt, t), generator=g)
-    t0 = time.perf_counter()
-    _, kv = od.prefill_forward(ids_s, w, emb, cfg)
-    od.decision_forward(ids_o, w, emb, cfg, kv, S)
-    per_layer = time.perf_counter() - t0
+    def run():
+        _, kv = od.prefill_forward(ids_s, w, emb, cfg)
+        od.decision_forward(ids_o, w, emb, cfg, kv, S)
+
+    n = args.cpu_sample_repeats
+    per_layer, _ = cpu_timed(run, n)
     per_request = per_layer * args.layers
-    return {"value": 1.0 / per_request, "unit": "decisions/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": 1.0 / per_request, "unit": "decisions/s", **cpu_fields(torch, n), "kind": "port",
             "sample": (f"1 request ({S}-token state prefilled + {n_opt} options x {t} tokens) x 1 of {args.layers} "
-                       f"layers, one run, {per_layer:.1f} s per layer, scaled x{args.layers} layers")}
+                       f"layers, median of {n} after a warm-up, {per_layer:.2f} s per layer, scaled x{args.layers} "
+                       "layers")}
 
 
 def cpu_baseline_wide(args):
     """The oracle on a bounded sample of the wide-choice workload: ONE 256-token record appended to a 32768-token
     int8 state through ONE 9B-dims layer (attention over the cached state + itself, only the new K/V quantized),
-    timed once, scaled x36 layers: the full-record append cost."""
+    the median of the timed runs after a warm-up, scaled x36 layers: the full-record append cost."""
     import torch
 
     from oracle import decoder as od
@@ -356,20 +388,19 @@ def cpu_baseline_wide(args):
     vq, vs = oq.quantize_rows(kv[1])
     state = [((kq, ks[..., 0]), (vq, vs[..., 0]))]
     ids = torch.randint(0, 4096, (1, rec), generator=g)
-    t0 = time.perf_counter()
-    od.prefill_forward(ids, w, emb, cfg, state_kv=state, n0=S0)
-    per_layer = time.perf_counter() - t0
+    n = args.cpu_sample_repeats
+    per_layer, _ = cpu_timed(lambda: od.prefill_forward(ids, w, emb, cfg, state_kv=state, n0=S0), n)
     return {"value": per_layer * args.layers * 1e3, "unit": "ms per appended record (full prefill)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": (f"1 record of {rec} tokens onto a {S0}-token int8 state x 1 of {args.layers} layers, one run, "
-                       f"{per_layer:.2f} s per layer, scaled x{args.layers} layers")}
+            **cpu_fields(torch, n), "kind": "port",
+            "sample": (f"1 record of {rec} tokens onto a {S0}-token int8 state x 1 of {args.layers} layers, median "
+                       f"of {n} after a warm-up, {per_layer:.2f} s per layer, scaled x{args.layers} layers")}
 
 
 def cpu_baseline_hybrid(args):
     """The oracle on a bounded sample of the hybrid decision: ONE request (a 4096-token state of random ids prefilled,
     then 64 options x 24 tokens scored) through ONE Gated DeltaNet layer (the gated delta rule in fp32, the
-    reference's own CPU arithmetic) and ONE gated full-attention layer, each timed once, scaled to the 24 + 8 layers
-    of the stack."""
+    reference's own CPU arithmetic) and ONE gated full-attention layer, each the median of the timed runs after a
+    warm-up, scaled to the 24 + 8 layers of the stack."""
     import torch
 
     from oracle import decoder as od
@@ -380,18 +411,58 @@ def cpu_baseline_hybrid(args):
     ids_s = torch.randint(0, 4096, (1, S), generator=g)
     ids_o = torch.randint(0, 4096, (1, n_opt, t), generator=g)
     per = {}
+    n = args.cpu_sample_repeats
     for kind, cfg in (("gdn", od.DecoderConfig(n_layers=1, full_attention_interval=4, gated=True)),
                       ("attention", od.DecoderConfig(n_layers=1, gated=True))):
         w = od.make_weights(cfg, seed=1)
-        t0 = time.perf_counter()
-        _, st = od.prefill_forward(ids_s, w, emb, cfg, gdn_dtype=torch.float32)
-        od.decision_forward(ids_o, w, emb, cfg, st, S, gdn_dtype=torch.float32)
-        per[kind] = time.perf_counter() - t0
+
+        def run():
+            _, st = od.prefill_forward(ids_s, w, emb, cfg, gdn_dtype=torch.float32)
+            od.decision_forward(ids_o, w, emb, cfg, st, S, gdn_dtype=torch.float32)
+
+        per[kind], _ = cpu_timed(run, n)
     per_request = 24 * per["gdn"] + 8 * per["attention"]
-    return {"value": 1.0 / per_request, "unit": "decisions/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": 1.0 / per_request, "unit": "decisions/s", **cpu_fields(torch, n), "kind": "port",
             "sample": (f"1 request ({S}-token state prefilled + {n_opt} options x {t} tokens) through 1 Gated DeltaNet "
-                       f"layer ({per['gdn']:.1f} s) and 1 gated attention layer ({per['attention']:.1f} s), one run "
-                       "each, scaled to 24 + 8 layers")}
+                       f"layer ({per['gdn']:.2f} s) and 1 gated attention layer ({per['attention']:.2f} s), median of "
+                       f"{n} after a warm-up each, scaled to 24 + 8 layers")}
+
+
+def cpu_baseline_qcache(args, n_q: int = 2, k: int = 16):
+    """The oracle on a bounded sample of the question-cache decide (scripts/bench_qcache_rows.py's measurement):
+    one decide of n_q questions x k options over one 900-token int8 state, with the cache (question pass, then the
+    option rows over [state ; question]), through ONE 9B-dims layer, the median of the timed runs after a warm-up,
+    scaled x36 layers."""
+    import torch
+
+    from oracle import decoder as od
+    from oracle import quant as oq
+    torch.set_num_threads(os.cpu_count() or 1)
+    cfg = od.DecoderConfig(n_layers=1, vocab=4096)
+    w = od.make_weights(cfg, seed=1)
+    emb = od.make_embedding(cfg, seed=3)
+    g = torch.Generator().manual_seed(7)
+    S, t = 900, 6
+    Lq = min(256 - t, 24 + 4 * k)
+    kv = torch.randn(2, 1, cfg.n_kv_heads, S, cfg.head_dim, generator=g).to(torch.bfloat16)
+    kq, ks = oq.quantize_rows(kv[0])
+    vq, vs = oq.quantize_rows(kv[1])
+    state = [((kq, ks[..., 0]), (vq, vs[..., 0]))]
+    ids_q = torch.randint(0, cfg.vocab, (n_q, Lq), generator=g)
+    ids_o = torch.randint(0, cfg.vocab, (n_q, k, t), generator=g)
+    gs = [0] * n_q
+
+    def run():
+        q_kv = od.question_forward(ids_q, w, emb, cfg, state, S, gs)
+        od.qcache_decision_forward(ids_o, w, emb, cfg, state, S, q_kv, [Lq] * n_q, gs)
+
+    n = args.cpu_sample_repeats
+    per_layer, _ = cpu_timed(run, n)
+    return {"value": per_layer * args.layers * 1e3, "unit": f"ms per decide ({n_q} questions x {k} options)",
+            **cpu_fields(torch, n), "kind": "port",
+            "sample": (f"1 decide with the question cache ({n_q} questions of {Lq} tokens, {k} options x {t} tokens "
+                       f"each, {S}-token int8 state) x 1 of {args.layers} layers, median of {n} after a warm-up, "
+                       f"{per_layer * 1e3:.0f} ms per layer, scaled x{args.layers} layers")}
 
 
 def _gemm_roofline(gemm_t):
@@ -795,22 +866,16 @@ def run_gemm(args):
         wq = _t.randint(-127, 128, (N, K), generator=cg, dtype=_t.int8)
         sw = _t.rand(N, generator=cg) * 1.5e-3 + 0.5e-3
         ops = 2 * M * N * K
-        tims = {}
-        for label, fn in (("dequant + F.linear (Int8Linear.forward)", lambda: oq.int8_linear_dequant(x, wq, sw)),
-                          ("W8A8 port (act-quant, int32 GEMM, epilogue)", lambda: oq.w8a8_linear(x, wq, sw))):
-            fn()
-            ts = []
-            for _ in range(5):
-                t0 = time.perf_counter()
-                fn()
-                ts.append(time.perf_counter() - t0)
-            tims[label] = sorted(ts)[2]
-        ref = tims["dequant + F.linear (Int8Linear.forward)"]
-        res["cpu_baseline"] = {"value": ops / ref / 1e12, "unit": "TOPS", "cores": _t.get_num_threads(),
-                               "kind": "port",
-                               "sample": (f"config 0 (M={M}, K={K}, N={N}), median of 5: the reference's CPU linear "
-                                          f"path {ref * 1e3:.1f} ms; the W8A8 oracle "
-                                          f"{tims['W8A8 port (act-quant, int32 GEMM, epilogue)'] * 1e3:.1f} ms")}
+        n = args.cpu_sample_repeats
+        ref, _ = cpu_timed(lambda: oq.int8_linear_dequant(x, wq, sw), n)
+        port, _ = cpu_timed(lambda: oq.w8a8_linear(x, wq, sw), n)
+        res["cpu_baseline"] = {"value": ops / ref / 1e12, "unit": "TOPS", **cpu_fields(_t, n), "kind": "port",
+                               "reference_linear_ms": ref * 1e3, "w8a8_port_ms": port * 1e3,
+                               "w8a8_port_tops": ops / port / 1e12,
+                               "sample": (f"config 0 (M={M}, K={K}, N={N}), median of {n} after a warm-up: the "
+                                          f"reference's CPU linear path (Int8Linear.forward: dequantize + F.linear, "
+                                          f"quant.py:156-157) {ref * 1e3:.1f} ms; the W8A8 oracle (act-quant, int32 "
+                                          f"GEMM, epilogue) {port * 1e3:.1f} ms")}
     return res
 
 
@@ -1001,19 +1066,13 @@ def run_attention(args, only=None):
         kq = torch.randint(-127, 128, (1, Hkv, T, D), generator=cg, dtype=torch.int8)
         vq = torch.randint(-127, 128, (1, Hkv, T, D), generator=cg, dtype=torch.int8)
         ks, vs = torch.rand(1, Hkv, T, generator=cg) * 0.02, torch.rand(1, Hkv, T, generator=cg) * 0.02
-        fn = lambda: oa.branched_attention_int8(q, k, v, kq, ks, vq, vs, D ** -0.5)
-        fn()
-        ts = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        per_state = sorted(ts)[1]
-        out["cpu_baseline"] = {"value": 1e3 * per_state * 8, "unit": "ms per config-1 call", "cores": torch.get_num_threads(),
+        n = args.cpu_sample_repeats
+        per_state, _ = cpu_timed(lambda: oa.branched_attention_int8(q, k, v, kq, ks, vq, vs, D ** -0.5), n)
+        out["cpu_baseline"] = {"value": 1e3 * per_state * 8, "unit": "ms per config-1 call", **cpu_fields(torch, n),
                                "kind": "port",
                                "sample": (f"1 of the 8 states (32 options x 16 tokens over 2048 int8 keys, K/V "
-                                          f"materialized in bf16), median of 3 after a warm-up: {per_state * 1e3:.0f} ms, "
-                                          f"scaled x8"),
+                                          f"materialized in bf16), median of {n} after a warm-up: "
+                                          f"{per_state * 1e3:.0f} ms, scaled x8"),
                                "gpu_speedup": per_state * 8 / (res["config1"]["avg_launch_us"] * 1e-6)}
     return out
 
@@ -1203,12 +1262,48 @@ def main():
         # it runs after the CPU baseline has left the GPU idle: 300 untimed calls (~35 ms) bring the clocks back up
         kvb = run_attention(_sub_args(args, steps=20, warmup=300), only=("kv_stream",))["shapes"]["kv_stream"]
         res["attention_kv_bound"] = {
-            "kernel": "od_branched_attn_stream (+ split merge)", "bound": "hbm", "achieved": kvb["kv_gbs"],
+            "kernel": "od_branched_attn_stream (split merge fused in the kernel)", "bound": "hbm", "achieved": kvb["kv_gbs"],
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": kvb["kv_frac_of_hbm"],
             "avg_launch_us": kvb["avg_launch_us"], "launches": kvb["launches"],
             "config": {"workload": "8 states x 32768 int8 K/V tokens (fp32 per-token scales), 2 options x 2 tokens "
                                    "per state, 32/8 heads, head_dim 128", "slots_per_kv_head": 16},
             "note": "K/V bytes (int8 + fp32 scales) per call over the call's duration (HIP events)"}
+        # the KV-bound probe as the survey defines it: the same states with 2 options x 16 tokens per state (128
+        # query slots per KV head, ~250 FLOP per K/V byte: at the bf16-MFMA / HBM ridge, so both fractions apply)
+        kvp = run_attention(_sub_args(args, steps=20, warmup=50), only=("kv_probe",))["shapes"]["kv_probe"]
+        res["attention_kv_probe"] = {
+            "kernel": f"branched attention, {kvp['path']} path", "bound": "hbm and bf16 mfma (ridge)",
+            "achieved": kvp["kv_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": kvp["kv_frac_of_hbm"],
+            "tflops": kvp["tflops"], "frac_of_bf16_mfma": kvp["frac_of_bf16_mfma"],
+            "avg_launch_us": kvp["avg_launch_us"], "launches": kvp["launches"],
+            "config": {"workload": "8 states x 32768 int8 K/V tokens (fp32 per-token scales), 2 options x 16 tokens "
+                                   "per state, 32/8 heads, head_dim 128", "slots_per_kv_head": 128,
+                       "definition": "the KV-bound probe as the survey defines it (S=32768, 2 rows x 16 tokens)"},
+            "note": "K/V bytes (int8 + fp32 scales) per call over the call's duration (HIP events)"}
+        torch.cuda.empty_cache()
+        # config 0 (the single W8A8 linear) and the reference's scripts/bench_gemm.py sweep, with the vendor int8
+        # GEMM (torch._int_mm, hipBLASLt) beside each shape and config 0's CPU baselines
+        gm = run_gemm(args)
+        c0 = next(r for r in gm["shapes"] if r["shape"] == "config0")
+        res["config0_linear"] = {
+            "config": {"workload": "single W8A8 linear: X bf16 [256, 4096] (1% outlier channels x20), W int8 "
+                                   "[4096, 4096] per-channel, per-token dynamic activation quantizer"},
+            "act_quant_us": c0["act_quant_us"], "gemm_us": c0["gemm_us"], "linear_us": c0["act_quant_us"] + c0["gemm_us"],
+            "gemm_tops": c0["gemm_tops"], "frac": c0["frac"], "linear_tops": c0["linear_tops"],
+            "gemm_us_cold": c0["gemm_us_cold"], "vendor_int_mm_us": c0["vendor_int_mm_us"],
+            "note": "HIP-graph replays of 20 calls (warm caches); gemm_us_cold: after a 512 MB cache flush"}
+        if "cpu_baseline" in gm:
+            res["config0_linear"]["cpu_baseline"] = gm["cpu_baseline"]
+        keep = ("shape", "M", "K", "N", "gemm_us", "gemm_tops", "frac", "gemm_us_cold", "vendor_int_mm_us",
+                "swiglu_gemm_us", "swiglu_gemm_tops")
+        res["gemm_sweep"] = {
+            "kernel": "od_w8a8_gemm (gate+up also od_w8a8_gemm_swiglu)",
+            "config": {"workload": "scripts/bench_gemm.py (K, N) x M sweep and the 9B layer GEMMs at M = 4096"},
+            "nine_b_tops": gm["value"], "nine_b_frac": gm["roofline"]["frac"], "cold": gm["cold"],
+            "sustained": gm["roofline"]["sustained"],
+            "shapes": [{k: r[k] for k in keep if k in r} | {"vendor_tops": 2 * r["M"] * r["N"] * r["K"] /
+                                                           r["vendor_int_mm_us"] / 1e6} for r in gm["shapes"]]}
+        del gm
         torch.cuda.empty_cache()
         res["decision"] = _sub(run_decision(_sub_args(args, steps=10, warmup=2)),
                                ("value", "unit", "p50_latency_ms", "p90_latency_ms", "config", "roofline",
@@ -1226,6 +1321,15 @@ def main():
                               "gdn_norm_quant", "time_share", "scoring_pass"))
         if not args.no_cpu_baseline:
             res["hybrid"]["cpu_baseline"] = cpu_baseline_hybrid(args)
+        torch.cuda.empty_cache()
+        qc = run_qcache_rows(args)
+        res["qcache_rows"] = {"value": qc["value"], "unit": qc["unit"], "metric": qc["metric"], "config": qc["config"],
+                              "shapes": qc["shapes"]}
+        if not args.no_cpu_baseline:
+            cb = cpu_baseline_qcache(args)
+            gpu_ms = next(r["with_qcache_ms"] for r in qc["shapes"] if (r["questions"], r["options"]) == (2, 16))
+            res["qcache_rows"]["cpu_baseline"] = cb | {"gpu_with_qcache_ms": gpu_ms,
+                                                       "gpu_speedup": cb["value"] / gpu_ms}
     print(json.dumps(res))
 
 

@@ -249,8 +249,13 @@ int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t 
  *   D          128 only (else OD_ERR_UNSUPPORTED); more than 32 slots per (state, head): OD_ERR_UNSUPPORTED
  *   max_rows   as od_branched_attn (an upper bound); a state whose row_start span holds more rows than max_rows
  *              (more than 32 slots) gets NaN outputs and LSEs instead of an attention result
- *   nsplit, ws as od_branched_attn_split (the keys of a (state, head) split over nsplit workgroups of 4 waves)
- * Other arguments and the result as od_branched_attn_split. One launch, plus the merge when nsplit > 1.
+ *   nsplit     1 .. 256: the keys of a (state, head) split over nsplit workgroups of 4 waves
+ *   ws         nsplit > 1: fp32 workspace of ws_floats >= nsplit * R * Hq * t * (D + 1) + Ns * Hkv floats, 16-byte
+ *              aligned: the splits' normalized partials and LSEs, then one int32 merge counter per (state, KV head).
+ *              The counters must be zero when the call starts and are zero again when it ends (the last split of a
+ *              (state, head) to finish merges the partials and resets its counter), so a workspace zeroed once serves
+ *              every later call; calls that share a workspace must not overlap
+ * Other arguments and the result as od_branched_attn_split. One launch (the split merge is fused into it).
  */
 int od_branched_attn_stream(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt,
                             const uint16_t* k_own, int64_t skr, int64_t skh, int64_t skt,

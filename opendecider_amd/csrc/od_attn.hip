@@ -61,6 +61,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
@@ -100,6 +101,7 @@ struct AttnArgs {
   const uint8_t* img2;
   const int32_t* group_state;
   int T2, n_states;
+  int* ctr;  // od_branched_attn_stream with splits: one merge counter per (state, KV head), zero between calls
 };
 
 // One block of 64 state keys as the attention reads it from LDS (and as od_attn_stage stores it, byte for byte).
@@ -1715,6 +1717,81 @@ __device__ __forceinline__ void str_state_tile(const StrTile& tl, const uint16_t
   str_update<DQ == OD_DEQUANT_FP32>(y, f, m_run, l_run, o, vf);
 }
 
+// The splits of one (state, KV head) after their partials are written: each publishes its partial and counts itself
+// on the (state, head)'s counter (device-scope atomic, after a device-scope release fence); the workgroup that
+// arrives last acquires every split's partial and merges them for all slots of the (state, head) with
+// combine_kernel's arithmetic (the same operations in the same order, so the result equals the separate merge launch
+// bit for bit), then sets the counter back to zero for the next call.
+// Device-scope coherent store / load of one float (agent-scope relaxed atomics: the access goes to the level all
+// XCDs share instead of this XCD's L2), for the split partials the merging workgroup reads. Device-scope fences
+// would do the same by writing back and invalidating the whole L2 of every XCD in every workgroup, which measured
+// twice as slow on the K/V streams.
+__device__ __forceinline__ void str_put(float* a, float v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float str_get(const float* a) {
+  return __hip_atomic_load(const_cast<float*>(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes at float offset `off` of the partials, with the device-scope coherence policy (sc1) of the stores and loads
+// above; the partials of a call are below 2 GiB (checked by the host), so a 32-bit offset reaches them all
+constexpr int kCoherent = 16;  // the sc1 bit of the buffer instructions' cache policy
+__device__ __forceinline__ void str_put4(float* part, int off, float4 v) {
+  const auto r = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off * 4, 0, kCoherent);
+}
+__device__ __forceinline__ float4 str_get4(const float* part, int off) {
+  const auto r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part), (short)0, 0x7fffffff, 0x00020000);
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, kCoherent));
+}
+
+__device__ __forceinline__ void str_merge_last(const AttnArgs& p, int* counters, int s, int g, int row0, int nslots,
+                                               int per_row) {
+  __shared__ int last;
+  // every thread's coherent partial stores have completed before the workgroup is counted
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  int* ctr = counters + (int64_t)s * p.Hkv + g;
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.nsplit - 1;
+  __syncthreads();
+  if (!last) return;
+  constexpr int D = kStrD;
+  const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
+  const float* lse_p = p.part + (int64_t)p.nsplit * nsl * D;
+  // item (slot z, f): the 4 dims 4 f .. 4 f + 3; consecutive threads take consecutive float4 of a slot
+  for (int i = threadIdx.x; i < nslots * (D / 4); i += blockDim.x) {
+    const int z = i / (D / 4), d0 = (i % (D / 4)) * 4;
+    const int zr = z / per_row, zrem = z - zr * per_row;
+    const int row = row0 + zr, head = g * p.rep + zrem % p.rep, tok = zrem / p.rep;
+    const int64_t slot = ((int64_t)row * p.Hq + head) * p.t + tok;
+    float M = -INFINITY;
+    float acc[4] = {0, 0, 0, 0};
+    float wsum = 0.0f;
+    // unrolled, so that every split's LSE and partial are in flight together (one round trip, not one per split)
+#pragma unroll 8
+    for (int sp = 0; sp < p.nsplit; ++sp) {
+      const float l = str_get(lse_p + sp * nsl + slot);
+      const float4 a = str_get4(p.part, (int)((sp * nsl + slot) * D + d0));
+      if (l == -INFINITY) continue;
+      if (l > M) {
+        const float r = __expf(M - l);
+        wsum *= r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] *= r;
+        M = l;
+      }
+      const float w = __expf(l - M);
+      wsum += w;
+      acc[0] += w * a.x; acc[1] += w * a.y; acc[2] += w * a.z; acc[3] += w * a.w;
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : wsum == 0.0f ? 0.0f : wsum;
+    uint16_t* op = p.out + (int64_t)row * p.sor + (int64_t)head * p.soh + (int64_t)tok * p.sot + d0;
+    *reinterpret_cast<uint2*>(op) = make_uint2(pk_bf16(acc[0] * inv, acc[1] * inv), pk_bf16(acc[2] * inv, acc[3] * inv));
+    if (p.lse && d0 == 0) p.lse[slot] = wsum > 0.0f ? M + __logf(wsum) : wsum == 0.0f ? -INFINITY : wsum;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+}
+
 template <int DQ>
 __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
   constexpr int D = kStrD;
@@ -1733,26 +1810,19 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
   if (nslots <= 0) return;  // uniform over the workgroup
   if (nslots > 32) {
     // the caller's max_rows understated this state's rows (one wave holds at most 32 slots): its outputs become NaN,
-    // a visible error instead of unwritten memory. With splits every split poisons its own partials and LSEs, so the
-    // merge gives NaN as well.
-    const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
+    // a visible error instead of unwritten memory (written by split 0; no split publishes a partial, so the merge
+    // counter of this (state, head) is not touched)
+    if (sp != 0) return;
     for (int i = threadIdx.x; i < nslots * (D / 8); i += blockDim.x) {
       const int z = i / (D / 8), d0 = (i % (D / 8)) * 8;
       const int zr = z / per_row, zrem = z - zr * per_row;
       const int row = row0 + zr, head = g * p.rep + zrem % p.rep, tk = zrem / p.rep;
       if (row >= p.R) break;
       const int64_t slot_idx = ((int64_t)row * p.Hq + head) * p.t + tk;
-      if (p.nsplit > 1) {
-        float* po = p.part + ((int64_t)sp * nsl + slot_idx) * D + d0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) po[e] = __builtin_nanf("");
-        if (d0 == 0) p.part[(int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx] = __builtin_nanf("");
-      } else {
-        uint16_t* op = p.out + (int64_t)row * p.sor + (int64_t)head * p.soh + (int64_t)tk * p.sot + d0;
-        *reinterpret_cast<uint2*>(op) = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
-        *reinterpret_cast<uint2*>(op + 4) = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
-        if (p.lse && d0 == 0) p.lse[slot_idx] = __builtin_nanf("");
-      }
+      uint16_t* op = p.out + (int64_t)row * p.sor + (int64_t)head * p.soh + (int64_t)tk * p.sot + d0;
+      *reinterpret_cast<uint2*>(op) = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
+      *reinterpret_cast<uint2*>(op + 4) = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
+      if (p.lse && d0 == 0) p.lse[slot_idx] = __builtin_nanf("");
     }
     return;
   }
@@ -1871,49 +1941,60 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
     sml[wave][1][c] = l_tot;
   }
   __syncthreads();
-  const int z = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 16;
-  if (z >= nslots) return;
-  float M = -INFINITY;
+  // thread (slot z, j): the four float4 of dims 4 j + 32 e .. +3 (e = 0..3), so that the 8 threads of a slot write
+  // whole 128-byte lines of its partial per instruction
+  const int z = threadIdx.x >> 3, j8 = threadIdx.x & 7;
+  if (z < nslots) {
+    float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kStrWaves; ++w) M = fmaxf(M, sml[w][0][z]);
-  float L = 0.0f, acc[16];
+    for (int w = 0; w < kStrWaves; ++w) M = fmaxf(M, sml[w][0][z]);
+    float L = 0.0f;
+    float4 acc[4];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-  if (M != -INFINITY) {
+    for (int e = 0; e < 4; ++e) acc[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (M != -INFINITY) {
 #pragma unroll
-    for (int w = 0; w < kStrWaves; ++w) {
-      const float mw = sml[w][0][z];
-      if (mw == -INFINITY) continue;
-      const float a = __builtin_amdgcn_exp2f(mw - M);
-      L += a * sml[w][1][z];
+      for (int w = 0; w < kStrWaves; ++w) {
+        const float mw = sml[w][0][z];
+        if (mw == -INFINITY) continue;
+        const float a = __builtin_amdgcn_exp2f(mw - M);
+        L += a * sml[w][1][z];
 #pragma unroll
-      for (int e = 0; e < 16; e += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(&sm.o[w][z][d0 + e]);
-        acc[e] += a * v.x; acc[e + 1] += a * v.y; acc[e + 2] += a * v.z; acc[e + 3] += a * v.w;
+        for (int e = 0; e < 4; ++e) {
+          const float4 v = *reinterpret_cast<const float4*>(&sm.o[w][z][4 * j8 + 32 * e]);
+          acc[e].x += a * v.x; acc[e].y += a * v.y; acc[e].z += a * v.z; acc[e].w += a * v.w;
+        }
       }
     }
-  }
-  const int zr = z / per_row, zrem = z - zr * per_row;
-  const int64_t slot_idx = ((int64_t)(row0 + zr) * p.Hq + g * p.rep + zrem % p.rep) * p.t + zrem / p.rep;
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  const float lse_v = L > 0.0f ? (M + __log2f(L)) * kLn2 : -INFINITY;
-  if (p.nsplit > 1) {
-    const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
-    float* po = p.part + ((int64_t)sp * nsl + slot_idx) * D + d0;
+    const int zr = z / per_row, zrem = z - zr * per_row;
+    const int64_t slot_idx = ((int64_t)(row0 + zr) * p.Hq + g * p.rep + zrem % p.rep) * p.t + zrem / p.rep;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const float lse_v = L > 0.0f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+    if (p.nsplit == 1) {
+      uint16_t* op = p.out + (int64_t)(row0 + zr) * p.sor + (int64_t)(g * p.rep + zrem % p.rep) * p.soh +
+                     (int64_t)(zrem / p.rep) * p.sot;
 #pragma unroll
-    for (int e = 0; e < 16; e += 4)
-      *reinterpret_cast<float4*>(po + e) = make_float4(acc[e] * inv, acc[e + 1] * inv, acc[e + 2] * inv, acc[e + 3] * inv);
-    if (d0 == 0) p.part[(int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx] = lse_v;
-    return;
-  }
-  uint16_t* op = p.out + (int64_t)(row0 + zr) * p.sor + (int64_t)(g * p.rep + zrem % p.rep) * p.soh +
-                 (int64_t)(zrem / p.rep) * p.sot + d0;
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<uint2*>(op + 4 * j8 + 32 * e) = make_uint2(pk_bf16(acc[e].x * inv, acc[e].y * inv),
+                                                                     pk_bf16(acc[e].z * inv, acc[e].w * inv));
+      if (p.lse && j8 == 0) p.lse[slot_idx] = lse_v;
+    } else {
+      // this split's normalized partial and its LSE, stored coherently at device scope (the merging workgroup may
+      // run on another XCD, whose L2 does not see this one's)
+      const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
+      const int base = (int)(((int64_t)sp * nsl + slot_idx) * D);
 #pragma unroll
-  for (int e = 0; e < 16; e += 4)
-    *reinterpret_cast<uint2*>(op + e) = make_uint2(pk_bf16(acc[e] * inv, acc[e + 1] * inv),
-                                                   pk_bf16(acc[e + 2] * inv, acc[e + 3] * inv));
-  if (p.lse && d0 == 0) p.lse[slot_idx] = lse_v;
+      for (int e = 0; e < 4; ++e)
+        str_put4(p.part, base + 4 * j8 + 32 * e,
+                 make_float4(acc[e].x * inv, acc[e].y * inv, acc[e].z * inv, acc[e].w * inv));
+      if (j8 == 0) str_put(p.part + (int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx, lse_v);
+    }
+  }
+  // with splits, the last of this (state, head)'s workgroups to finish merges them (every thread takes part)
+  if (p.nsplit > 1) str_merge_last(p, p.ctr, s, g, row0, nslots, per_row);
 }
+
+
 
 }  // namespace
 
@@ -1939,7 +2020,7 @@ extern "C" int od_branched_attn_stream(const uint16_t* q, int64_t sqr, int64_t s
   if (T > 0 && (!kq || !ks || !vq || !vs)) return OD_ERR_NULL;
   if (nsplit > 1) {
     if (!ws) return OD_ERR_NULL;
-    if (ws_floats < nsplit * R * Hq * t * (D + 1)) return OD_ERR_SHAPE;
+    if (ws_floats < nsplit * R * Hq * t * (D + 1) + Ns * Hkv) return OD_ERR_SHAPE;
     if (!od_aligned16(ws)) return OD_ERR_ALIGN;
   }
   const int64_t strides[] = {sqr, sqh, sqt, skr, skh, skt, svr, svh, svt};
@@ -1949,23 +2030,18 @@ extern "C" int od_branched_attn_stream(const uint16_t* q, int64_t sqr, int64_t s
   if (!od_aligned16(q) || !od_aligned16(k_own) || !od_aligned16(v_own) || (((uintptr_t)out) & 7u)) return OD_ERR_ALIGN;
   if (T > 0 && (!od_aligned16(kq) || !od_aligned16(vq) || (((uintptr_t)ks | (uintptr_t)vs) & 3u))) return OD_ERR_ALIGN;
   if (Hkv > 65535 || Ns > 65535 || R * t * rep > 0x7fffffff || cap * Hkv * Ns * D > (1ll << 40) ||
-      nsplit * R * Hq * t * (D + 1) > (1ll << 40) || T * D >= (1ll << 31))
+      nsplit * R * Hq * t * (D + 1) * 4 >= (1ll << 31) || T * D >= (1ll << 31))  // partials: 32-bit byte offsets
     return OD_ERR_SHAPE;
   AttnArgs a{q, k_own, v_own, kq, ks, vq, vs, kvalid, row_start, out, lse, sqr, sqh, sqt, skr, skh, skt, svr, svh,
              svt, sor, soh, sot, (int)R, (int)Hq, (int)Hkv, (int)t, (int)Ns, (int)T, (int)cap, (int)rep,
              scale * 1.4426950408889634f, dequant, (int)nsplit, nsplit > 1 ? ws : nullptr, nullptr, nullptr,
-             nullptr, 0, (int)Ns};
+             nullptr, 0, (int)Ns,
+             nsplit > 1 ? reinterpret_cast<int*>(ws + nsplit * R * Hq * t * (D + 1)) : nullptr};
   dim3 grid((unsigned)nsplit, (unsigned)Hkv, (unsigned)Ns), block(kStrWaves * 64);
   hipStream_t st = (hipStream_t)stream;
   if (dequant == OD_DEQUANT_BF16)
     stream_kernel<OD_DEQUANT_BF16><<<grid, block, 0, st>>>(a);
   else
     stream_kernel<OD_DEQUANT_FP32><<<grid, block, 0, st>>>(a);
-  if (nsplit > 1) {
-    const int rc = od_launch_status();
-    if (rc != OD_OK) return rc;
-    const int64_t threads = R * Hq * t * (D / 8);
-    combine_kernel<128><<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(a);
-  }
   return od_launch_status();
 }

@@ -368,6 +368,22 @@ STREAM_D = 128
 STREAM_MAX_SLOTS = 32
 
 
+# Workspaces of the streaming kernel's key-range splits, per (device, stream, size): the split partials and LSEs, then
+# one merge counter per (state, KV head) that must be zero when a call starts; the kernel sets every counter back to
+# zero, so a workspace zeroed once serves every later call made on its stream.
+_STREAM_WS: dict = {}
+
+
+def stream_workspace(nsplit: int, R: int, Hq: int, t: int, D: int, Ns: int, Hkv: int, device) -> torch.Tensor:
+    n = nsplit * R * Hq * t * (D + 1) + Ns * Hkv
+    device = torch.device(device)
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream, n)
+    ws = _STREAM_WS.get(key)
+    if ws is None:
+        ws = _STREAM_WS[key] = torch.zeros(n, dtype=torch.float32, device=device)
+    return ws
+
+
 def stream_split_count(Ns: int, Hkv: int, T: int, target_workgroups: int = 512, min_tiles: int = 8) -> int:
     """Key-range splits for od_branched_attn_stream: about two 4-wave workgroups per CU over all (state, head)
     pairs, keeping at least `min_tiles` 32-key tiles (two per wave) in each split."""
@@ -579,7 +595,7 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
             raise ValueError(f"branched_attn: the streaming kernel takes head_dim {STREAM_D} and at most "
                              f"{STREAM_MAX_SLOTS} slots per (state, head), not D={D} with {slots}")
         nsp = stream_split_count(Ns, Hkv, T) if n_split is None else int(n_split)
-        ws = torch.empty(nsp * R * Hq * t * (D + 1), dtype=torch.float32, device=q.device) if nsp > 1 else None
+        ws = stream_workspace(nsp, R, Hq, t, D, Ns, Hkv, q.device) if nsp > 1 else None
         check(lib().od_branched_attn_stream(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
                                             *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),
                                             ptr(row_start), int(max_rows), ptr(out), *out.stride()[:3], ptr(lse), R,

@@ -96,6 +96,8 @@ def test_stream_attention_checks(L):
     assert stream(dq=2) == UNSUP
     assert stream(nsplit=0) == SHAPE
     assert stream(nsplit=3, ws=P, ws_floats=100) == SHAPE   # workspace too small
+    # R = 2 rows, Hq = 8, t = 4, D = 128: 3 splits take 3 x 2 x 8 x 4 x 129 floats, plus Ns x Hkv = 2 merge counters
+    assert stream(nsplit=3, ws=P, ws_floats=3 * 2 * 8 * 4 * 129 + 1) == SHAPE
     assert stream(nsplit=3) == NULL                          # no workspace
     assert stream(ks=P + 2) == ALIGN                         # scales must be 4-byte aligned
     assert stream(kq=P + 8) == ALIGN                         # int8 K must be 16-byte aligned

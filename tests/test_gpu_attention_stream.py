@@ -134,3 +134,46 @@ def test_split_attention_int8_few_rows_streams(gpu_lib):
              row_state=torch.zeros(n, dtype=torch.long), T=T, scale=D ** -0.5)
     ref, _ = run_oracle(c)
     assert_close_rel(out.float().cpu(), ref, what="_split_attention few rows (stream)")
+
+
+def test_stream_fused_merge_repeats_and_replays(gpu_lib):
+    """The split merge runs inside the kernel (the last split of a (state, head) to finish merges, then resets its
+    counter): ten calls in a row on one workspace give the same bits (the counters return to zero every call), the
+    workspace's counters are zero afterwards, a HIP graph of the call replays bit for bit with eager calls on other
+    queries between the replays, and the result equals the oracle at the bar."""
+    from opendecider_amd import kernels
+    c = make_case(seed=33, Ns=4, row_counts=[2, 1, 2, 2], Hq=32, Hkv=8, t=2, D=128, T=4000, holes=True)
+    ref, ref_lse = run_oracle(c)
+    first, first_lse = run_stream(c, n_split=7)
+    assert_close_rel(first.float().cpu(), ref, what="fused merge, 7 splits")
+    assert (first_lse.cpu() - ref_lse).abs().max().item() <= 1e-4
+    for _ in range(10):
+        o, l = run_stream(c, n_split=7)
+        assert torch.equal(o.view(torch.int16), first.view(torch.int16)) and torch.equal(l, first_lse)
+    torch.cuda.synchronize()
+    ws = kernels.stream_workspace(7, 7, 32, 2, 128, 4, 8, DEV)
+    assert torch.count_nonzero(ws[-4 * 8:]).item() == 0
+    # graph capture: the call recorded once, replayed with eager calls on other queries in between
+    q = c["q"].to(DEV)
+    args = (c["k"].to(DEV), c["v"].to(DEV), c["kq"].to(DEV), c["ks"].to(DEV), c["vq"].to(DEV), c["vs"].to(DEV),
+            c["scale"])
+    rs, mr = kernels.row_start_of(c["row_counts"], DEV)
+    kw = dict(kvalid=c["kvalid"].to(DEV), row_start=rs, max_rows=mr, length=c["T"], n_split=7, stream=True)
+    out = torch.empty_like(q)
+    s_ = torch.cuda.Stream()
+    with torch.cuda.stream(s_):
+        kernels.branched_attn(q, *args, out=out, **kw)  # warm-up: the stream's workspace exists before the capture
+        s_.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s_):
+            kernels.branched_attn(q, *args, out=out, **kw)
+    q2 = torch.randn(q.shape, device=DEV).to(torch.bfloat16)
+    other = kernels.branched_attn(q2, *args, **kw)
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), first.view(torch.int16)), f"replay {i}"
+        again = kernels.branched_attn(q2, *args, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), other.view(torch.int16)), f"eager call after replay {i}"
