@@ -69,6 +69,25 @@ def mfma_ceiling(modes=(0, 1, 2, 3, 4), iters=100000):
     return out
 
 
+def hbm_ceiling(gib: int = 2, reps: int = 10):
+    """HBM read rate the chip sustains (od_probe_hbm_read in libod_probe.so): a buffer of `gib` GiB (well past the
+    256 MB Infinity Cache) streamed by a plain grid-stride read kernel with 16-byte loads, the best of 4, 8 and 16
+    workgroups per CU; GB/s."""
+    import ctypes
+
+    from opendecider_amd import build as _b
+    L = ctypes.CDLL(_b.PROBE_LIB)
+    L.od_probe_hbm_read.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    L.od_probe_hbm_read.restype = ctypes.c_int
+    gbs = ctypes.c_double()
+    rc = L.od_probe_hbm_read(gib << 30, reps, ctypes.byref(gbs))
+    if rc != 0:
+        raise RuntimeError(f"od_probe_hbm_read failed: {rc}")
+    return {"value": gbs.value, "unit": "GB/s", "frac_of_peak": gbs.value / HBM_PEAK_GBS,
+            "probe": f"od_probe_hbm_read: {gib} GiB read by a grid-stride kernel, 16-byte loads, 8 in flight per "
+                     "thread, best of 4/8/16 workgroups per CU"}
+
+
 def _sustained(ceil, mode):
     c = ceil[f"mode{mode}"]
     return {"value": c["value"], "clock_mhz": c["clock_mhz"], "frac_of_peak": c["frac_of_peak"],
@@ -885,6 +904,7 @@ def run_mfma_ceiling(args):
     per wave, with the core clock under that load. `value` is the int8 LDS-fed rate, the ceiling the W8A8 GEMM's
     inner loop has without any global traffic."""
     ceil = mfma_ceiling()
+    ceil["hbm_read"] = hbm_ceiling()
     return {"metric": "int8 MFMA sustained TOPS (LDS-fed operands)", "value": ceil["mode2"]["value"], "unit": "TOPS",
             "n_gpus": 1, "steps": 1, "warmup": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "int8", "data": "synthetic",
@@ -1268,6 +1288,9 @@ def main():
             "config": {"workload": "8 states x 32768 int8 K/V tokens (fp32 per-token scales), 2 options x 2 tokens "
                                    "per state, 32/8 heads, head_dim 128", "slots_per_kv_head": 16},
             "note": "K/V bytes (int8 + fp32 scales) per call over the call's duration (HIP events)"}
+        hbm = hbm_ceiling()
+        res["attention_kv_bound"]["sustained"] = hbm
+        res["attention_kv_bound"]["frac_of_sustained"] = kvb["kv_gbs"] / hbm["value"]
         # the KV-bound probe as the survey defines it: the same states with 2 options x 16 tokens per state (128
         # query slots per KV head, ~250 FLOP per K/V byte: at the bf16-MFMA / HBM ridge, so both fractions apply)
         kvp = run_attention(_sub_args(args, steps=20, warmup=50), only=("kv_probe",))["shapes"]["kv_probe"]
@@ -1279,6 +1302,7 @@ def main():
             "config": {"workload": "8 states x 32768 int8 K/V tokens (fp32 per-token scales), 2 options x 16 tokens "
                                    "per state, 32/8 heads, head_dim 128", "slots_per_kv_head": 128,
                        "definition": "the KV-bound probe as the survey defines it (S=32768, 2 rows x 16 tokens)"},
+            "frac_of_sustained_hbm": kvp["kv_gbs"] / hbm["value"],
             "note": "K/V bytes (int8 + fp32 scales) per call over the call's duration (HIP events)"}
         torch.cuda.empty_cache()
         # config 0 (the single W8A8 linear) and the reference's scripts/bench_gemm.py sweep, with the vendor int8

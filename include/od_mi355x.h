@@ -7,7 +7,9 @@
  *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream). Work is enqueued on it and
  *     the call returns without synchronizing.
  *   - Nothing allocates device or host memory and nothing synchronizes, so every call may be captured in a
- *     HIP graph. Calls are reentrant (no mutable global state).
+ *     HIP graph. Calls on different streams may run concurrently when they share no output or workspace, with two
+ *     exceptions that hold device-side state: od_branched_attn_split_noalloc (one static scratch array per GPU) and
+ *     od_branched_attn_stream with splits (merge counters in its workspace); each says so below.
  *   - Return value: OD_OK (0) or a negative OD_ERR_* code; no exception crosses the ABI. od_strerror() gives
  *     the text. (The reference's own C ABI uses the same int-rc convention: deploy/llamacpp/od_llama.cpp:13-22,
  *     mapped to RuntimeError by src/opendecider/llamacpp.py:57-58.)
@@ -270,7 +272,9 @@ int od_branched_attn_stream(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t
 /*
  * od_branched_attn_split_noalloc — od_branched_attn_split without a workspace argument and without any allocation:
  * the per-split partials go to a static device array inside the library (OD_SPLIT_SCRATCH_FLOATS floats = 64 MiB per
- * GPU, held from the first call until the process ends). No counterpart in the reference: it is for callers that
+ * GPU). The array is part of the library's code object, so every GPU the library is loaded on holds it from then
+ * until the process ends, whether or not this entry point is ever called. No counterpart in the reference: it is
+ * for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  *   arguments, result and launches as od_branched_attn_split (without ws / ws_floats)
  *   nsplit * R * Hq * t * (D + 1) must not exceed OD_SPLIT_SCRATCH_FLOATS (else OD_ERR_SCRATCH, nothing launched);

@@ -1,6 +1,6 @@
-// Matrix-core ceiling probe for MI355X (gfx950), used by bench.py to put the GEMM and attention rooflines next to
-// what the chip sustains, not only next to the published peak. Built into its own library (libod_probe.so); no part
-// of the scoring path calls it.
+// Matrix-core and HBM ceiling probes for MI355X (gfx950), used by bench.py to put the GEMM and attention rooflines
+// next to what the chip sustains, not only next to the published peaks. Built into their own library
+// (libod_probe.so); no part of the scoring path calls them.
 //
 // One workgroup of 8 waves per CU (two per SIMD, as the W8A8 GEMM runs); each wave issues `iters` rounds of 8
 // independent MFMAs into 8 accumulator tiles. Modes:
@@ -153,7 +153,74 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_probe_kernel(int iters, long
   }
 }
 
+// HBM read-bandwidth probe: every thread streams 16-byte pieces of a buffer far larger than the caches (grid-stride,
+// 8 loads in flight per thread) and folds them into one word it stores, so that no load can be dropped.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void hbm_read_kernel(const v4u* __restrict__ src, int64_t n16, int* sink) {
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x, stride = (int64_t)gridDim.x * 256;
+  uint32_t acc = 0;
+  int64_t i = tid;
+  for (; i + 7 * stride < n16; i += 8 * stride) {
+    v4u v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < n16; i += stride) {
+    const v4u v = src[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  sink[tid] = (int)acc;
+}
+
 }  // namespace
+
+// Reads a `bytes`-byte device buffer (filled first) with hbm_read_kernel at 4, 8 and 16 workgroups of 4 waves per
+// CU, `reps` timed launches each after a warm-up launch, on the current device; synchronous. Writes the best read
+// rate in GB/s. Returns 0, or -1 (bad argument) / -2 (HIP error).
+extern "C" int od_probe_hbm_read(int64_t bytes, int reps, double* gbs) {
+  if (bytes < (1 << 24) || bytes % 16 || reps < 1 || !gbs) return -1;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -2;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) return -2;
+  v4u* buf = nullptr;
+  int* sink = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = 0;
+  double best = 0.0;
+  const int64_t n16 = bytes / 16;
+  if (hipMalloc(&buf, bytes) != hipSuccess || hipMalloc(&sink, sizeof(int) * 256 * 16 * (size_t)cus) != hipSuccess ||
+      hipMemset(buf, 0x5a, bytes) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+      hipEventCreate(&e1) != hipSuccess) {
+    rc = -2;
+  }
+  for (int per_cu : {4, 8, 16}) {
+    if (rc != 0) break;
+    const int grid = per_cu * cus;
+    float ms = 0.0f;
+    hbm_read_kernel<<<grid, 256>>>(buf, n16, sink);
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess || hipEventRecord(e0, 0) != hipSuccess) {
+      rc = -2;
+      break;
+    }
+    for (int r = 0; r < reps; ++r) hbm_read_kernel<<<grid, 256>>>(buf, n16, sink);
+    if (hipGetLastError() != hipSuccess || hipEventRecord(e1, 0) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms <= 0.0f) {
+      rc = -2;
+      break;
+    }
+    const double rate = (double)bytes * reps / (ms * 1e-3) / 1e9;
+    if (rate > best) best = rate;
+  }
+  if (rc == 0) *gbs = best;
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (buf) (void)hipFree(buf);
+  if (sink) (void)hipFree(sink);
+  return rc;
+}
 
 // Runs mode `mode` (0..4) with one workgroup per CU for `iters` rounds per wave, after one warm-up launch, on the
 // current device; synchronous. Writes the throughput (dense TOPS / TFLOP/s) and the mean core clock in MHz.
