@@ -243,15 +243,18 @@ int od_branched_attn_split(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t 
 /*
  * od_branched_attn_stream — od_branched_attn_split for the few-slot case: every (state, KV head) carries at most 32
  * query slots (max_rows * t * Hq / Hkv <= 32, e.g. a yes/no decision of 2 options x 2 tokens over a long state), and
- * the attention is bound by reading the int8 state. One wave holds all slots of its (state, head) and streams the
- * int8 K/V from memory into registers 32 keys at a time, dequantized there as `dequant` says (no block images, no
- * LDS staging); P enters the P.V product as two bf16 parts (hi + lo). Each slot's result depends on its own scores
- * only (option order cannot change it); results agree with od_branched_attn to the attention bar, not bit for bit.
+ * the attention is bound by reading the int8 state. One wave holds all slots of its (state, head) as one or two
+ * 16-slot MFMA column tiles (one when max_rows * t * Hq / Hkv <= 16) and streams the int8 K/V from memory into
+ * registers 32 keys at a time with non-temporal loads, dequantized there as `dequant` says (no block images, no LDS
+ * staging); P enters the P.V product as two bf16 parts (hi + lo). Each slot's result depends on its own scores only
+ * (option order cannot change it); results agree with od_branched_attn to the attention bar, not bit for bit.
  * Replaces: the same reference code as od_branched_attn (prefix_attn.py:43-76 with Kp/Vp materialized at :145-149).
  *   D          128 only (else OD_ERR_UNSUPPORTED); more than 32 slots per (state, head): OD_ERR_UNSUPPORTED
- *   max_rows   as od_branched_attn (an upper bound); a state whose row_start span holds more rows than max_rows
- *              (more than 32 slots) gets NaN outputs and LSEs instead of an attention result
- *   nsplit     1 .. 256: the keys of a (state, head) split over nsplit workgroups of 4 waves
+ *   max_rows   as od_branched_attn (an upper bound); a state whose row_start span holds more slots than the column
+ *              tiles max_rows sized (16 or 32) gets NaN outputs and LSEs instead of an attention result
+ *   nsplit     1 .. 256: the keys of a (state, head) split over nsplit workgroups of 8 waves. A CU runs one such
+ *              workgroup at a time: Ns * Hkv * nsplit at (or just below) a multiple of the CU count fills the GPU
+ *              without a partial last round (4 splits for 64 (state, head) pairs on MI355X's 256 CUs)
  *   ws         nsplit > 1: fp32 workspace of ws_floats >= nsplit * R * Hq * t * (D + 1) + Ns * Hkv floats, 16-byte
  *              aligned: the splits' normalized partials and LSEs, then one int32 merge counter per (state, KV head).
  *              The counters must be zero when the call starts and are zero again when it ends (the last split of a

@@ -62,6 +62,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
@@ -1511,45 +1512,42 @@ extern "C" int od_branched_attn_staged2(const uint16_t* q, int64_t sqr, int64_t 
 
 // ================================================================================================ KV streaming
 // od_branched_attn_stream: the few-slot case. When every (state, KV head) carries at most 32 query slots (a few
-// short option rows, e.g. a yes/no decision over a long state), the attention does 32 x 4 FLOP per state key and
-// dimension against 2 bytes of int8 K/V, so it is bound by reading the state from HBM, and the block-image paths
+// short option rows, e.g. a yes/no decision over a long state), the attention does at most 32 x 4 FLOP per state key
+// and dimension against 2 bytes of int8 K/V, so it is bound by reading the state from HBM, and the block-image paths
 // (LDS images, 128-slot tiles) leave most of their MFMA columns and conversion work idle. Here one wave takes all
-// slots of its (state, head) and streams the state's int8 K/V straight from HBM into registers, 32 keys per tile,
-// one tile ahead, converting there (no LDS until the end); a workgroup's 4 waves take interleaved tiles of one
-// key range, the key range of each (state, head) is split over workgroups (nsplit), and partials are merged by
-// log-sum-exp (combine_kernel).
+// slots of its (state, head) as NC column tiles of 16 (NC = 1 for up to 16 slots, 2 for up to 32) and streams the
+// state's int8 K/V straight from HBM into registers, 32 keys per tile, one tile ahead, converting there; a
+// workgroup's 8 waves take interleaved tiles of one key range, the key range of each (state, head) is split over
+// workgroups (nsplit, chosen by the caller so that the workgroups fill the CUs once), and the last workgroup of a
+// (state, head) merges the splits' partials by log-sum-exp. The K/V loads are non-temporal: each byte is read once,
+// and keeping it out of the caches measured 12% faster on 32768-key states.
 //
-// Per tile (keys kb .. kb + 31), lane l = 32 h + c of a wave:
-//  * scores S^T = K' Q^T on V_MFMA_F32_32X32X16_BF16, 8 k-steps; k-step ks takes dims 64 h + 8 ks .. +7 of both
-//    operands (a permutation of the reduction index, applied to both sides). The lane loads 64 contiguous bytes of
-//    key kb + c (its A row) and converts them: K' = bf16(q bf16(ks_j)) (OD_DEQUANT_BF16) or the exact integer q
-//    (OD_DEQUANT_FP32, the key's fp32 multiplier then goes on the score). In the result lane l holds slot c and
-//    keys 8 r + 4 h + j (register 4 r + j), so the online softmax is lane-local plus one exchange with lane l ^ 32;
-//  * values O^T += V'^T P^T: k-step m (keys 16 m .. 16 m + 15) takes P registers 8 m .. 8 m + 7 as its B operand,
-//    so the A operand of lane (c, h) holds value d of the keys 8 r + 4 h + j in that order. Output row c of d
-//    block db is d = 4 c + db: the lane reads dword 4 c .. 4 c + 3 of each of its 16 keys (lanes 0..31 read one
-//    key's 128 bytes, lanes 32..63 another), and byte db of each is element db's value. V' = bf16(q bf16(vs_j))
-//    (exact bf16) or, OD_DEQUANT_FP32, the integer q with vs_j folded into the probability;
+// On V_MFMA_F32_16X16X32_BF16 (lane l: column l % 16; result rows 4 (l / 16) + i), per tile (keys kb .. kb + 31 as
+// two 16-key row tiles kr), lane l = (j, g) = (l % 16, l / 16):
+//  * scores S^T[kr] = K'[kr] Q^T: k-step ks takes dims 32 g + 8 ks .. +7 of both operands (a permutation of the
+//    reduction index, applied to both sides); the lane loads 32 contiguous bytes of each of its keys kb + j and
+//    kb + 16 + j and converts them: K' = bf16(q bf16(ks_j)) (OD_DEQUANT_BF16) or the exact integer q
+//    (OD_DEQUANT_FP32, the key's fp32 multiplier then goes on the score). The result gives lane (j, g) slot
+//    16 nc + j and keys 16 kr + 4 g + i, so a slot's online softmax is lane-local plus two exchanges (l ^ 16, l ^ 32);
+//  * values O^T[dt] += V'^T[dt] P^T, output row r of d-tile dt being d = 8 r + dt, with the keys in the order
+//    kappa(g, i) = (4 g + i, i < 4; 12 + 4 g + i, i >= 4): the B operand is then exactly the lane's own 8
+//    probabilities, and the A operand of lane (r, g) is byte dt of the 8 bytes d = 8 r .. 8 r + 7 it loaded for each
+//    of its keys kappa(g, 0..7) (16 lanes read a key's whole 128-byte row). V' = bf16(q bf16(vs_j)) (exact bf16) or,
+//    OD_DEQUANT_FP32, the integer q with vs_j folded into the probability;
 //  * P goes to the P.V product as two bf16 parts, hi = bf16(p) and lo = bf16(p - hi) (16 significant bits, two
-//    MFMAs per k-step): V' is exactly the reference's bf16 value and P keeps fp16-level precision. The row sum is
+//    MFMAs per d-tile): V' is exactly the reference's bf16 value and P keeps fp16-level precision. The row sum is
 //    taken on the unrounded fp32 p.
-// The row's own keys (at most 32: rows x t <= slots) are one extra masked tile of bf16 K/V, taken by wave 0 of the
-// last split. Each slot's arithmetic depends only on its own scores, so option order cannot change a result.
+// Lane (j, g) ends with slot 16 nc + j's dims 32 g .. 32 g + 31. The rows' own keys (at most 32: rows x t <= slots)
+// are one extra masked tile of bf16 K/V, taken by wave 0 of the last split. Each slot's arithmetic depends only on
+// its own scores, so option order cannot change a result.
 namespace {
 
-constexpr int kStrWaves = 4;
+constexpr int kStrWaves = 8;
 constexpr int kStrKeys = 32;
 constexpr int kStrD = 128;
 
-struct StrTile {
-  uint4 k[4];      // lane (key c, half h): int8 bytes 64 h + 16 i .. +16 of key kb + c
-  uint32_t v[16];  // lane (c, h): V bytes 4 c .. 4 c + 3 of key kb + 8 (i / 4) + 4 h + i % 4
-  float vs, ks;    // V and K scales of key kb + c
-  int valid;       // the kvalid byte of key kb + c (0 without a mask)
-};
-
-// The per-wave LDS of the streaming kernel: a tile's per-key factors, written by the lane that loaded key c and
-// read back in the score layout (keys 8 r + 4 h + 0..3 as one float4 per r).
+// The per-wave LDS of the streaming kernel: a tile's per-key factors, written by lane l for key l % 32 and read
+// back in the score layout (keys 16 kr + 4 g + 0..3 as one float4).
 struct StrKeyLds {
   float4 f[2][8];  // [0]: V factor (bf16(vs) or vs), [1]: score multiplier (OD_DEQUANT_FP32: ks scale log2(e))
 };
@@ -1564,31 +1562,6 @@ struct StrSrc {
   int T;
 };
 
-// The tile's loads, all unconditional (a conditional load makes the compiler wait for every load in flight). Each
-// load goes through a descriptor made for the tile (base at key kb, length T - kb keys: keys past the length read
-// as zeros), so the per-lane offsets are loop-invariant and no address register is rewritten while loads are in
-// flight.
-template <int DQ>
-__device__ __forceinline__ void str_load(const StrSrc& src, int kb, int h, int c, StrTile& tl) {
-  const int n = max(src.T - kb, 0);  // keys left from kb (wave-uniform)
-  constexpr int kF = 0x00020000;
-  const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(src.k + (int64_t)kb * kStrD), (short)0, n * kStrD, kF);
-  const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)(src.v + (int64_t)kb * kStrD), (short)0, n * kStrD, kF);
-  const auto rks = __builtin_amdgcn_make_buffer_rsrc((void*)(src.ks + kb), (short)0, n * 4, kF);
-  const auto rvs = __builtin_amdgcn_make_buffer_rsrc((void*)(src.vs + kb), (short)0, n * 4, kF);
-  const auto rva = __builtin_amdgcn_make_buffer_rsrc((void*)(src.valid ? src.valid + kb : nullptr), (short)0,
-                                                     src.valid ? n : 0, kF);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    tl.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, c * kStrD + 64 * h + 16 * i, 0, 0));
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    tl.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, 4 * c + 512 * h + (8 * (i >> 2) + (i & 3)) * kStrD, 0, 0);
-  tl.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, c * 4, 0, 0));
-  tl.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, c * 4, 0, 0));
-  tl.valid = __builtin_amdgcn_raw_buffer_load_b8(rva, c, 0, 0);  // 0 past the mask (or without one)
-}
-
 __device__ __forceinline__ float f4_at(const float4& v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; }
 
 // int8 byte b of w, times an fp32 factor
@@ -1598,130 +1571,195 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((od_f32x2){a, b}, od_bf16x2));
 }
 
-// The queries of the wave's 32 slots in LDS, read per k-step (lane (c, h) of k-step ks: slot c, dims
-// 64 h + 8 ks .. +7); the row stride of 272 bytes puts 16 consecutive slots on 16 distinct bank quads.
+// The queries of the workgroup's (at most 32) slots in LDS, read per k-step (lane (j, g) of k-step ks: slot
+// 16 nc + j, dims 32 g + 8 ks .. +7); the row stride of 272 bytes puts 16 consecutive slots on 16 distinct bank quads.
 constexpr int kStrQRow = kStrD + 8;
 
-// One tile's online-softmax update and P.V product. y: the lane's 16 scores in log2 units (-inf: masked); pw: a
-// factor on p for the P.V product only (the fp32 path's V scales); vf(m, db): the V'^T A operand of k-step m and d
-// block db.
-template <bool PW, class VF>
-__device__ __forceinline__ void str_update(float (&y)[16], const float (&pw)[16], float& m_run, float& l_run,
-                                           v16f (&o)[4], VF&& vf) {
-  float mx = y[0];
+__device__ __forceinline__ v4f_t mfma16(bf16x8 a, bf16x8 b, v4f_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ int s16_kappa(int g, int i) { return i < 4 ? 4 * g + i : 12 + 4 * g + i; }
+
+// One tile of the stream in registers.
+struct S16Tile {
+  uint4 k[4];     // lane (j, g): int8 bytes 32 g .. 32 g + 15 and + 16 .. + 31 of key kb + j (k[0], k[1]), kb + 16 + j
+  uint2 v[8];     // lane (r, g): V bytes 8 r .. 8 r + 7 of key kb + kappa(g, i)
+  float vs, ks;   // lane l: the V and K scales of key kb + (l & 31)
+  int valid;      // lane l: the kvalid byte of key kb + (l & 31) (0 without a mask)
+};
+
+// The cache policy of the stream's loads: non-temporal (nt), for data read exactly once.
+constexpr int kStreamOnce = 2;
+
+// The tile's loads, all unconditional (a conditional load makes the compiler wait for every load in flight). Each
+// load goes through a descriptor made for the tile (base at key kb, length T - kb keys: keys past the length read
+// as zeros), so the per-lane offsets are loop-invariant and no address register is rewritten while loads are in
+// flight.
+__device__ __forceinline__ void s16_load(const StrSrc& src, int kb, int lane, S16Tile& tl) {
+  const int n = max(src.T - kb, 0);
+  constexpr int kF = 0x00020000;
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(src.k + (int64_t)kb * kStrD), (short)0, n * kStrD, kF);
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)(src.v + (int64_t)kb * kStrD), (short)0, n * kStrD, kF);
+  const auto rks = __builtin_amdgcn_make_buffer_rsrc((void*)(src.ks + kb), (short)0, n * 4, kF);
+  const auto rvs = __builtin_amdgcn_make_buffer_rsrc((void*)(src.vs + kb), (short)0, n * 4, kF);
+  const auto rva = __builtin_amdgcn_make_buffer_rsrc((void*)(src.valid ? src.valid + kb : nullptr), (short)0,
+                                                     src.valid ? n : 0, kF);
+  const int j = lane & 15, g = lane >> 4, c = lane & 31;
 #pragma unroll
-  for (int i = 1; i < 16; ++i) mx = fmaxf(mx, y[i]);
-  mx = od_xor32_max(mx);
-  const bool move = mx > m_run + kSlack;  // lazy: p = exp2(y - m) <= 2^kSlack otherwise
-  if (__builtin_amdgcn_ballot_w64(move) != 0) {
-    const float a = move ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;  // m_run = -inf: 0
+  for (int i = 0; i < 4; ++i)
+    tl.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rk, ((i >> 1) * 16 + j) * kStrD + 32 * g + 16 * (i & 1), 0, kStreamOnce));
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+  for (int i = 0; i < 8; ++i)
+    tl.v[i] = __builtin_bit_cast(
+        uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, s16_kappa(g, i) * kStrD + 8 * j, 0, kStreamOnce));
+  tl.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, c * 4, 0, kStreamOnce));
+  tl.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, c * 4, 0, kStreamOnce));
+  tl.valid = __builtin_amdgcn_raw_buffer_load_b8(rva, c, 0, kStreamOnce);  // 0 past the mask (or without one)
+}
+
+// The queries' B operand of k-step ks for column tile nc: slot 16 nc + j, dims 32 g + 8 ks .. +7.
+__device__ __forceinline__ bf16x8 s16_q(const uint16_t* qs, int slot, int g, int ks) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qs + slot * kStrQRow + 32 * g + 8 * ks));
+}
+
+// One tile's online-softmax update and P.V product on the 16 x 16 layout. y[nc]: the lane's 8 scores of column tile
+// nc (log2 units, -inf masked), in the key order kappa; pw: a factor on p for the P.V product only (the fp32 path's
+// V scales); vf(dt): the V'^T A operand of d-tile dt (shared by the column tiles). The max over a slot's keys runs
+// over the lane's 8 scores and the 4 lane groups g that hold the same column.
+template <int NC, bool PW, class VF>
+__device__ __forceinline__ void s16_update(float (&y)[NC][8], const float (&pw)[8], float (&m_run)[NC],
+                                           float (&l_run)[NC], v4f_t (&o)[NC][8], VF&& vf) {
+  bf16x8 bh[NC], bl[NC];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] *= a;
-    l_run *= a;
-    if (move) m_run = mx;
-  }
-  const float msub = m_run == -INFINITY ? 0.0f : m_run;
-  float p[16];
-  float ls = 0.0f;
+  for (int nc = 0; nc < NC; ++nc) {
+    float mx = y[nc][0];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    p[i] = __builtin_amdgcn_exp2f(y[i] - msub);
-    ls += p[i];
-  }
-  l_run += ls;
-  bf16x8 bh[2], bl[2];
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, y[nc][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const bool move = mx > m_run[nc] + kSlack;  // lazy: p = exp2(y - m) <= 2^kSlack otherwise
+    if (__builtin_amdgcn_ballot_w64(move) != 0) {
+      const float a = move ? __builtin_amdgcn_exp2f(m_run[nc] - mx) : 1.0f;  // m_run = -inf: 0
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[nc][dt][i] *= a;
+      l_run[nc] *= a;
+      if (move) m_run[nc] = mx;
+    }
+    const float msub = m_run[nc] == -INFINITY ? 0.0f : m_run[nc];
+    float pr[8];
+    float ls = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pr[i] = __builtin_amdgcn_exp2f(y[nc][i] - msub);
+      ls += pr[i];
+    }
+    l_run[nc] += ls;
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float a = PW ? p[8 * m + 2 * e] * pw[8 * m + 2 * e] : p[8 * m + 2 * e];
-      const float b = PW ? p[8 * m + 2 * e + 1] * pw[8 * m + 2 * e + 1] : p[8 * m + 2 * e + 1];
+      const float a = PW ? pr[2 * e] * pw[2 * e] : pr[2 * e];
+      const float b = PW ? pr[2 * e + 1] * pw[2 * e + 1] : pr[2 * e + 1];
       hw[e] = pk_bf16(a, b);
       lw[e] = pk_bf16(a - __uint_as_float(hw[e] << 16), b - __uint_as_float(hw[e] & 0xffff0000u));
     }
-    bh[m] = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
-    bl[m] = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+    bh[nc] = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+    bl[nc] = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
   }
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+  for (int dt = 0; dt < 8; ++dt) {
+    const bf16x8 a = vf(dt);
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const bf16x8 a = vf(m, db);
-      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bh[m], o[db], 0, 0, 0);
-      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bl[m], o[db], 0, 0, 0);
+    for (int nc = 0; nc < NC; ++nc) {
+      o[nc][dt] = mfma16(a, bh[nc], o[nc][dt]);
+      o[nc][dt] = mfma16(a, bl[nc], o[nc][dt]);
     }
+  }
 }
 
-__device__ __forceinline__ bf16x8 str_q(const uint16_t* qs, int c, int h, int ks) {
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qs + c * kStrQRow + 64 * h + 8 * ks));
-}
-
-template <int DQ>
-__device__ __forceinline__ void str_state_tile(const StrTile& tl, const uint16_t* qs, StrKeyLds& kl, float c2, int h,
-                                               int c, bool key_ok, float& m_run, float& l_run, v16f (&o)[4]) {
-  // the tile's per-key factors through LDS into the score layout (in-order LDS access within the wave; lanes c and
-  // c + 32 write the same value)
+// One state tile (32 keys) of the 16 x 16 stream.
+template <int DQ, int NC>
+__device__ __forceinline__ void s16_state_tile(const S16Tile& tl, const uint16_t* qs, StrKeyLds& kl, float c2,
+                                               int lane, bool key_ok, float (&m_run)[NC], float (&l_run)[NC],
+                                               v4f_t (&o)[NC][8]) {
+  const int j = lane & 15, g = lane >> 4, c = lane & 31;
+  // the tile's per-key factors through LDS into the layouts that read them (in-order LDS access within the wave;
+  // lanes c and c + 32 write the same value)
   reinterpret_cast<float*>(kl.f[0])[c] = DQ == OD_DEQUANT_BF16 ? bf16_round(tl.vs) : tl.vs;
   if constexpr (DQ == OD_DEQUANT_FP32) reinterpret_cast<float*>(kl.f[1])[c] = tl.ks * c2;
-  v16f s = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  const float sk = DQ == OD_DEQUANT_BF16 ? bf16_round(tl.ks) : 0.0f;
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    const uint32_t w0 = (ks & 1) ? tl.k[ks >> 1].z : tl.k[ks >> 1].x;
-    const uint32_t w1 = (ks & 1) ? tl.k[ks >> 1].w : tl.k[ks >> 1].y;
-    uint4 a;
-    if constexpr (DQ == OD_DEQUANT_BF16) {
-      i8x4_times_bf16(w0, sk, a.x, a.y);
-      i8x4_times_bf16(w1, sk, a.z, a.w);
-    } else {
-      i8x4_to_bf16(w0, a.x, a.y);
-      i8x4_to_bf16(w1, a.z, a.w);
-    }
-    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), str_q(qs, c, h, ks), s, 0, 0, 0);
+  float sk[2] = {0.0f, 0.0f};  // the bf16 K scales of the lane's keys kb + j and kb + 16 + j
+  if constexpr (DQ == OD_DEQUANT_BF16) {
+    sk[0] = bf16_round(__shfl(tl.ks, j, 64));
+    sk[1] = bf16_round(__shfl(tl.ks, 16 + j, 64));
   }
-  // masked keys (past the state's length or masked by kvalid): bit k of the ballot is key kb + k
+  v4f_t s[NC][2];
+#pragma unroll
+  for (int nc = 0; nc < NC; ++nc) s[nc][0] = s[nc][1] = v4f_t{0, 0, 0, 0};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+    for (int kr = 0; kr < 2; ++kr) {
+      const uint4 w = tl.k[2 * kr + (ks >> 1)];
+      const uint32_t w0 = (ks & 1) ? w.z : w.x, w1 = (ks & 1) ? w.w : w.y;
+      uint4 a;
+      if constexpr (DQ == OD_DEQUANT_BF16) {
+        i8x4_times_bf16(w0, sk[kr], a.x, a.y);
+        i8x4_times_bf16(w1, sk[kr], a.z, a.w);
+      } else {
+        i8x4_to_bf16(w0, a.x, a.y);
+        i8x4_to_bf16(w1, a.z, a.w);
+      }
+#pragma unroll
+      for (int nc = 0; nc < NC; ++nc)
+        s[nc][kr] = mfma16(__builtin_bit_cast(bf16x8, a), s16_q(qs, 16 * nc + j, g, ks), s[nc][kr]);
+    }
+  }
+  // keys 16 kr + 4 g + i: masked keys (past the state's length or by kvalid) from one ballot (bit k: key kb + k)
   const uint32_t vm = (uint32_t)__builtin_amdgcn_ballot_w64(key_ok);
-  float y[16], f[16];
+  const float4 fv[2] = {kl.f[0][g], kl.f[0][4 + g]};
+  float4 gk[2] = {make_float4(c2, c2, c2, c2), make_float4(c2, c2, c2, c2)};
+  if constexpr (DQ == OD_DEQUANT_FP32) {
+    gk[0] = kl.f[1][g];
+    gk[1] = kl.f[1][4 + g];
+  }
+  float y[NC][8], f[8];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float4 fv = kl.f[0][2 * r + h];
-    float4 gk = make_float4(c2, c2, c2, c2);
-    if constexpr (DQ == OD_DEQUANT_FP32) gk = kl.f[1][2 * r + h];
+  for (int kr = 0; kr < 2; ++kr)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      y[4 * r + j] = s[4 * r + j] * f4_at(gk, j);
-      f[4 * r + j] = f4_at(fv, j);
+    for (int i = 0; i < 4; ++i) {
+      f[4 * kr + i] = f4_at(fv[kr], i);
+#pragma unroll
+      for (int nc = 0; nc < NC; ++nc) y[nc][4 * kr + i] = s[nc][kr][i] * f4_at(gk[kr], i);
+    }
+  if (vm != 0xffffffffu) {
+#pragma unroll
+    for (int kr = 0; kr < 2; ++kr) {
+      const uint32_t bits = vm >> (16 * kr + 4 * g);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (!((bits >> i) & 1u))
+#pragma unroll
+          for (int nc = 0; nc < NC; ++nc) y[nc][4 * kr + i] = -INFINITY;
     }
   }
-  if (vm != 0xffffffffu) {
-    const uint32_t bits = vm >> (4 * h);
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (!((bits >> (8 * (i >> 2) + (i & 3))) & 1u)) y[i] = -INFINITY;
-  }
-  auto vf = [&](int m, int db) {
+  auto vf = [&](int dt) {
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int i0 = 8 * m + 2 * e, i1 = i0 + 1;
+      const int i0 = 2 * e, i1 = 2 * e + 1;
+      const uint32_t x0 = dt < 4 ? tl.v[i0].x : tl.v[i0].y, x1 = dt < 4 ? tl.v[i1].x : tl.v[i1].y;
       if constexpr (DQ == OD_DEQUANT_BF16)
-        w[e] = pk_bf16(byte_times(tl.v[i0], db, f[i0]), byte_times(tl.v[i1], db, f[i1]));
+        w[e] = pk_bf16(byte_times(x0, dt & 3, f[i0]), byte_times(x1, dt & 3, f[i1]));
       else
-        w[e] = pk_bf16(byte_times(tl.v[i0], db, 1.0f), byte_times(tl.v[i1], db, 1.0f));
+        w[e] = pk_bf16(byte_times(x0, dt & 3, 1.0f), byte_times(x1, dt & 3, 1.0f));
     }
     return __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
   };
-  str_update<DQ == OD_DEQUANT_FP32>(y, f, m_run, l_run, o, vf);
+  s16_update<NC, DQ == OD_DEQUANT_FP32>(y, f, m_run, l_run, o, vf);
 }
 
-// The splits of one (state, KV head) after their partials are written: each publishes its partial and counts itself
-// on the (state, head)'s counter (device-scope atomic, after a device-scope release fence); the workgroup that
-// arrives last acquires every split's partial and merges them for all slots of the (state, head) with
-// combine_kernel's arithmetic (the same operations in the same order, so the result equals the separate merge launch
-// bit for bit), then sets the counter back to zero for the next call.
 // Device-scope coherent store / load of one float (agent-scope relaxed atomics: the access goes to the level all
 // XCDs share instead of this XCD's L2), for the split partials the merging workgroup reads. Device-scope fences
 // would do the same by writing back and invalidating the whole L2 of every XCD in every workgroup, which measured
@@ -1744,6 +1782,11 @@ __device__ __forceinline__ float4 str_get4(const float* part, int off) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4, 0, kCoherent));
 }
 
+// The splits of one (state, KV head) after their partials are written: each has stored its partial with the coherent
+// policy above, waits until those stores have completed, and counts itself on the (state, head)'s counter
+// (device-scope atomic); the workgroup that arrives last reads every split's partial with coherent loads and merges
+// them for all slots of the (state, head) with combine_kernel's arithmetic (the same operations in the same order, so
+// the result equals the separate merge launch bit for bit), then sets the counter back to zero for the next call.
 __device__ __forceinline__ void str_merge_last(const AttnArgs& p, int* counters, int s, int g, int row0, int nslots,
                                                int per_row) {
   __shared__ int last;
@@ -1792,31 +1835,32 @@ __device__ __forceinline__ void str_merge_last(const AttnArgs& p, int* counters,
   if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
 }
 
-template <int DQ>
-__global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
+// The stream: workgroup (split sp, KV head hk, state s) with 8 waves; wave w takes tiles t_lo + w, t_lo + w + 8, ...
+// of the split's key range, two register sets with loads one tile ahead (a third set measured no faster).
+template <int DQ, int NC>
+__global__ __launch_bounds__(kStrWaves * 64, NC == 1 ? 2 : 1) void stream_kernel(AttnArgs p) {
   constexpr int D = kStrD;
-  // the queries (while the tiles run), then the waves' accumulators for the merge
+  constexpr int kSlots = 16 * NC;
   __shared__ __attribute__((aligned(16))) union {
     uint16_t q[32 * kStrQRow];
-    float o[kStrWaves][32][D + 4];
+    float o[kStrWaves][kSlots][D + 4];
   } sm;
-  __shared__ float sml[kStrWaves][2][32];
+  __shared__ float sml[kStrWaves][2][kSlots];
   __shared__ StrKeyLds skl[kStrWaves];
-  const int sp = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+  const int sp = blockIdx.x, hk = blockIdx.y, s = blockIdx.z;
   const int row0 = p.row_start ? p.row_start[s] : 0;
   const int nrows = p.row_start ? p.row_start[s + 1] - row0 : p.R;
   const int per_row = p.t * p.rep;
   const int nslots = nrows * per_row;
   if (nslots <= 0) return;  // uniform over the workgroup
-  if (nslots > 32) {
-    // the caller's max_rows understated this state's rows (one wave holds at most 32 slots): its outputs become NaN,
-    // a visible error instead of unwritten memory (written by split 0; no split publishes a partial, so the merge
-    // counter of this (state, head) is not touched)
+  if (nslots > kSlots) {
+    // more slots than the wave's column tiles hold (the caller's max_rows understated this state's rows): NaN
+    // outputs, written by split 0 (no split publishes a partial or counts itself)
     if (sp != 0) return;
     for (int i = threadIdx.x; i < nslots * (D / 8); i += blockDim.x) {
       const int z = i / (D / 8), d0 = (i % (D / 8)) * 8;
       const int zr = z / per_row, zrem = z - zr * per_row;
-      const int row = row0 + zr, head = g * p.rep + zrem % p.rep, tk = zrem / p.rep;
+      const int row = row0 + zr, head = hk * p.rep + zrem % p.rep, tk = zrem / p.rep;
       if (row >= p.R) break;
       const int64_t slot_idx = ((int64_t)row * p.Hq + head) * p.t + tk;
       uint16_t* op = p.out + (int64_t)row * p.sor + (int64_t)head * p.soh + (int64_t)tk * p.sot + d0;
@@ -1826,61 +1870,58 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
     }
     return;
   }
-  // the wave index made visibly uniform: the tile offsets derived from it are scalar buffer offsets
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int h = lane >> 5, c = lane & 31;
-  const bool slot_ok = c < nslots;
-  int rl = 0, tok = 0;
-  if (slot_ok) {
-    rl = c / per_row;
-    tok = (c - rl * per_row) / p.rep;
-  }
+  const int j = lane & 15, qd = lane >> 4, c = lane & 31;
   {
-    // thread: slot z = tid / 8, dims 16 (tid % 8) .. +15
+    // thread: slot z = tid / 8, dims 16 (tid % 8) .. +15 (rows past the slots are zeros)
     const int z = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 16;
-    uint4 a = make_uint4(0, 0, 0, 0), b = a;
-    if (z < nslots) {
-      const int zr = z / per_row, zrem = z - zr * per_row;
-      const uint16_t* qp = p.q + (int64_t)(row0 + zr) * p.sqr + (int64_t)(g * p.rep + zrem % p.rep) * p.sqh +
-                           (int64_t)(zrem / p.rep) * p.sqt + d0;
-      a = *reinterpret_cast<const uint4*>(qp);
-      b = *reinterpret_cast<const uint4*>(qp + 8);
+    if (z < 32) {
+      uint4 a = make_uint4(0, 0, 0, 0), b = a;
+      if (z < nslots) {
+        const int zr = z / per_row, zrem = z - zr * per_row;
+        const uint16_t* qp = p.q + (int64_t)(row0 + zr) * p.sqr + (int64_t)(hk * p.rep + zrem % p.rep) * p.sqh +
+                             (int64_t)(zrem / p.rep) * p.sqt + d0;
+        a = *reinterpret_cast<const uint4*>(qp);
+        b = *reinterpret_cast<const uint4*>(qp + 8);
+      }
+      *reinterpret_cast<uint4*>(sm.q + z * kStrQRow + d0) = a;
+      *reinterpret_cast<uint4*>(sm.q + z * kStrQRow + d0 + 8) = b;
     }
-    *reinterpret_cast<uint4*>(sm.q + z * kStrQRow + d0) = a;
-    *reinterpret_cast<uint4*>(sm.q + z * kStrQRow + d0 + 8) = b;
   }
   __syncthreads();
-  float m_run = -INFINITY, l_run = 0.0f;
-  v16f o[4];
+  float m_run[NC], l_run[NC];
+  v4f_t o[NC][8];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) o[db] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int nc = 0; nc < NC; ++nc) {
+    m_run[nc] = -INFINITY;
+    l_run[nc] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[nc][dt] = v4f_t{0, 0, 0, 0};
+  }
 
-  // ---- the state's tiles of this split: [t_lo, t_hi), wave w takes t_lo + w, t_lo + w + 4, ...
+  // ---- the state's tiles of this split: [t_lo, t_hi)
   const int n_tiles = (p.T + kStrKeys - 1) / kStrKeys;
   const int tps = (n_tiles + p.nsplit - 1) / p.nsplit;
   const int t_lo = min(n_tiles, sp * tps), t_hi = min(n_tiles, t_lo + tps);
-  const int64_t head_base = ((int64_t)s * p.Hkv + g) * p.cap;
+  const int64_t head_base = ((int64_t)s * p.Hkv + hk) * p.cap;
   const StrSrc src{p.kq + head_base * D, p.vq + head_base * D, p.ks + head_base, p.vs + head_base,
                    p.kvalid ? p.kvalid + (int64_t)s * p.T : nullptr, p.T};
   int tt = t_lo + wave;
   if (tt < t_hi) {
     const bool has_valid = p.kvalid != nullptr;
-    auto ok = [&](const StrTile& tl, int t0) { return t0 * kStrKeys + c < p.T && (!has_valid || tl.valid != 0); };
-    // two register sets, loads one tile ahead (two tiles per trip, so the sets alternate without copies); past the
-    // wave's last tile the "next" loads repeat the current tile (cached), so that no load is conditional. A third
-    // set (loads two tiles ahead) measured no faster.
-    StrTile ta, tb;
-    str_load<DQ>(src, tt * kStrKeys, h, c, ta);
+    auto ok = [&](const S16Tile& tl, int t0) { return t0 * kStrKeys + c < p.T && (!has_valid || tl.valid != 0); };
+    S16Tile ta, tb;
+    s16_load(src, tt * kStrKeys, lane, ta);
     for (;; tt += 2 * kStrWaves) {
       const bool more1 = tt + kStrWaves < t_hi;
-      str_load<DQ>(src, (more1 ? tt + kStrWaves : tt) * kStrKeys, h, c, tb);
-      __builtin_amdgcn_sched_barrier(0);  // the next tile's loads go out before this tile's first use of its data
-      str_state_tile<DQ>(ta, sm.q, skl[wave], p.scale_log2, h, c, ok(ta, tt), m_run, l_run, o);
+      s16_load(src, (more1 ? tt + kStrWaves : tt) * kStrKeys, lane, tb);
+      __builtin_amdgcn_sched_barrier(0);
+      s16_state_tile<DQ, NC>(ta, sm.q, skl[wave], p.scale_log2, lane, ok(ta, tt), m_run, l_run, o);
       if (!more1) break;
       const bool more2 = tt + 2 * kStrWaves < t_hi;
-      str_load<DQ>(src, (more2 ? tt + 2 * kStrWaves : tt + kStrWaves) * kStrKeys, h, c, ta);
+      s16_load(src, (more2 ? tt + 2 * kStrWaves : tt + kStrWaves) * kStrKeys, lane, ta);
       __builtin_amdgcn_sched_barrier(0);
-      str_state_tile<DQ>(tb, sm.q, skl[wave], p.scale_log2, h, c, ok(tb, tt + kStrWaves), m_run, l_run, o);
+      s16_state_tile<DQ, NC>(tb, sm.q, skl[wave], p.scale_log2, lane, ok(tb, tt + kStrWaves), m_run, l_run, o);
       if (!more2) break;
     }
   }
@@ -1888,60 +1929,88 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
   // ---- the rows' own keys: one masked tile of bf16 K/V (key k = row k / t, token k % t), wave 0 of the last split
   if (sp == p.nsplit - 1 && wave == 0) {
     const int n_own = nrows * p.t;
-    v16f sc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    {
-      const bool kok = c < n_own;
-      const int kr = kok ? c / p.t : 0, kj = kok ? c % p.t : 0;
-      const uint16_t* kp = p.k_own + (int64_t)(row0 + kr) * p.skr + (int64_t)g * p.skh + (int64_t)kj * p.skt + 64 * h;
+    v4f_t sc[NC][2];
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8, kok ? *reinterpret_cast<const uint4*>(kp + 8 * ks) : make_uint4(0, 0, 0, 0)),
-            str_q(sm.q, c, h, ks), sc, 0, 0, 0);
-    }
-    uint2 vo[16];
-    float y[16], one[16];
+    for (int nc = 0; nc < NC; ++nc) sc[nc][0] = sc[nc][1] = v4f_t{0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kk = 8 * (i >> 2) + 4 * h + (i & 3);  // own key of score register i
-      const bool vis = slot_ok && kk < n_own && kk >= rl * p.t && kk <= rl * p.t + tok;
-      y[i] = vis ? sc[i] * p.scale_log2 : -INFINITY;
-      one[i] = 1.0f;
-      vo[i] = make_uint2(0, 0);
-      if (kk < n_own) {
-        const int kr = kk / p.t, kj = kk % p.t;
-        vo[i] = *reinterpret_cast<const uint2*>(p.v_own + (int64_t)(row0 + kr) * p.svr + (int64_t)g * p.svh +
-                                                (int64_t)kj * p.svt + 4 * c);
+    for (int kr = 0; kr < 2; ++kr) {
+      const int kk = 16 * kr + j;
+      const bool kok = kk < n_own;
+      const int orow = kok ? kk / p.t : 0, oj = kok ? kk % p.t : 0;
+      const uint16_t* kp =
+          p.k_own + (int64_t)(row0 + orow) * p.skr + (int64_t)hk * p.skh + (int64_t)oj * p.skt + 32 * qd;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 a =
+            __builtin_bit_cast(bf16x8, kok ? *reinterpret_cast<const uint4*>(kp + 8 * ks) : make_uint4(0, 0, 0, 0));
+#pragma unroll
+        for (int nc = 0; nc < NC; ++nc) sc[nc][kr] = mfma16(a, s16_q(sm.q, 16 * nc + j, qd, ks), sc[nc][kr]);
       }
     }
-    auto vf = [&](int m, int db) {
+    float y[NC][8], one[8];
+#pragma unroll
+    for (int nc = 0; nc < NC; ++nc) {
+      const int z = 16 * nc + j;
+      const bool zok = z < nslots;
+      const int rl = zok ? z / per_row : 0, tok = zok ? (z - rl * per_row) / p.rep : 0;
+#pragma unroll
+      for (int kr = 0; kr < 2; ++kr)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kk = 16 * kr + 4 * qd + i;
+          const bool vis = zok && kk < n_own && kk >= rl * p.t && kk <= rl * p.t + tok;
+          y[nc][4 * kr + i] = vis ? sc[nc][kr][i] * p.scale_log2 : -INFINITY;
+        }
+    }
+    uint4 vo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      one[i] = 1.0f;
+      const int kk = s16_kappa(qd, i);
+      vo[i] = make_uint4(0, 0, 0, 0);
+      if (kk < n_own) {
+        const int orow = kk / p.t, oj = kk % p.t;
+        vo[i] = *reinterpret_cast<const uint4*>(p.v_own + (int64_t)(row0 + orow) * p.svr + (int64_t)hk * p.svh +
+                                                (int64_t)oj * p.svt + 8 * j);
+      }
+    }
+    auto word = [](const uint4& v, int w) { return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w; };
+    auto vf = [&](int dt) {
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint2 a = vo[8 * m + 2 * e], b = vo[8 * m + 2 * e + 1];
-        const uint32_t xa = db < 2 ? a.x : a.y, xb = db < 2 ? b.x : b.y;
-        w[e] = (db & 1) ? ((xa >> 16) | (xb & 0xffff0000u)) : ((xa & 0xffffu) | (xb << 16));
+        const uint32_t xa = word(vo[2 * e], dt >> 1), xb = word(vo[2 * e + 1], dt >> 1);
+        w[e] = (dt & 1) ? ((xa >> 16) | (xb & 0xffff0000u)) : ((xa & 0xffffu) | (xb << 16));
       }
       return __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
     };
-    str_update<false>(y, one, m_run, l_run, o, vf);
+    s16_update<NC, false>(y, one, m_run, l_run, o, vf);
   }
 
-  // ---- merge the 4 waves (LDS), then this split's normalized partial + LSE, or the output
-  const float l_tot = od_xor32_sum(l_run);
+  // ---- merge the waves (LDS), then this split's normalized partial + LSE, or the output
+  float l_tot[NC];
+#pragma unroll
+  for (int nc = 0; nc < NC; ++nc) {
+    l_tot[nc] = l_run[nc] + __shfl_xor(l_run[nc], 16, 64);
+    l_tot[nc] += __shfl_xor(l_tot[nc], 32, 64);
+  }
   __syncthreads();  // every wave is done with the queries: their LDS now takes the accumulators
+  // lane (j, qd) of column tile nc: slot 16 nc + j, dims 32 qd + 8 i + dt in o[nc][dt][i]
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int nc = 0; nc < NC; ++nc) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<float4*>(&sm.o[wave][c][32 * r + 16 * h + 4 * j]) =
-          make_float4(o[0][4 * r + j], o[1][4 * r + j], o[2][4 * r + j], o[3][4 * r + j]);
-  if (h == 0) {
-    sml[wave][0][c] = m_run;
-    sml[wave][1][c] = l_tot;
+    for (int i = 0; i < 4; ++i) {
+      float* dst = &sm.o[wave][16 * nc + j][32 * qd + 8 * i];
+      *reinterpret_cast<float4*>(dst) = make_float4(o[nc][0][i], o[nc][1][i], o[nc][2][i], o[nc][3][i]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[nc][4][i], o[nc][5][i], o[nc][6][i], o[nc][7][i]);
+    }
+    if (qd == 0) {
+      sml[wave][0][16 * nc + j] = m_run[nc];
+      sml[wave][1][16 * nc + j] = l_tot[nc];
+    }
   }
   __syncthreads();
-  // thread (slot z, j): the four float4 of dims 4 j + 32 e .. +3 (e = 0..3), so that the 8 threads of a slot write
+  // thread (slot z, j8): the four float4 of dims 4 j8 + 32 e .. +3 (e = 0..3), so that the 8 threads of a slot write
   // whole 128-byte lines of its partial per instruction
   const int z = threadIdx.x >> 3, j8 = threadIdx.x & 7;
   if (z < nslots) {
@@ -1967,11 +2036,11 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
       }
     }
     const int zr = z / per_row, zrem = z - zr * per_row;
-    const int64_t slot_idx = ((int64_t)(row0 + zr) * p.Hq + g * p.rep + zrem % p.rep) * p.t + zrem / p.rep;
+    const int64_t slot_idx = ((int64_t)(row0 + zr) * p.Hq + hk * p.rep + zrem % p.rep) * p.t + zrem / p.rep;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     const float lse_v = L > 0.0f ? (M + __log2f(L)) * kLn2 : -INFINITY;
     if (p.nsplit == 1) {
-      uint16_t* op = p.out + (int64_t)(row0 + zr) * p.sor + (int64_t)(g * p.rep + zrem % p.rep) * p.soh +
+      uint16_t* op = p.out + (int64_t)(row0 + zr) * p.sor + (int64_t)(hk * p.rep + zrem % p.rep) * p.soh +
                      (int64_t)(zrem / p.rep) * p.sot;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -1979,8 +2048,6 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
                                                                      pk_bf16(acc[e].z * inv, acc[e].w * inv));
       if (p.lse && j8 == 0) p.lse[slot_idx] = lse_v;
     } else {
-      // this split's normalized partial and its LSE, stored coherently at device scope (the merging workgroup may
-      // run on another XCD, whose L2 does not see this one's)
       const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
       const int base = (int)(((int64_t)sp * nsl + slot_idx) * D);
 #pragma unroll
@@ -1990,10 +2057,8 @@ __global__ __launch_bounds__(kStrWaves * 64, 2) void stream_kernel(AttnArgs p) {
       if (j8 == 0) str_put(p.part + (int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx, lse_v);
     }
   }
-  // with splits, the last of this (state, head)'s workgroups to finish merges them (every thread takes part)
-  if (p.nsplit > 1) str_merge_last(p, p.ctr, s, g, row0, nslots, per_row);
+  if (p.nsplit > 1) str_merge_last(p, p.ctr, s, hk, row0, nslots, per_row);
 }
-
 
 
 }  // namespace
@@ -2039,9 +2104,17 @@ extern "C" int od_branched_attn_stream(const uint16_t* q, int64_t sqr, int64_t s
              nsplit > 1 ? reinterpret_cast<int*>(ws + nsplit * R * Hq * t * (D + 1)) : nullptr};
   dim3 grid((unsigned)nsplit, (unsigned)Hkv, (unsigned)Ns), block(kStrWaves * 64);
   hipStream_t st = (hipStream_t)stream;
-  if (dequant == OD_DEQUANT_BF16)
-    stream_kernel<OD_DEQUANT_BF16><<<grid, block, 0, st>>>(a);
-  else
-    stream_kernel<OD_DEQUANT_FP32><<<grid, block, 0, st>>>(a);
+  const bool one_tile = max_rows * t * rep <= 16;  // every (state, head)'s slots fit one 16-column tile
+  if (dequant == OD_DEQUANT_BF16) {
+    if (one_tile)
+      stream_kernel<OD_DEQUANT_BF16, 1><<<grid, block, 0, st>>>(a);
+    else
+      stream_kernel<OD_DEQUANT_BF16, 2><<<grid, block, 0, st>>>(a);
+  } else {
+    if (one_tile)
+      stream_kernel<OD_DEQUANT_FP32, 1><<<grid, block, 0, st>>>(a);
+    else
+      stream_kernel<OD_DEQUANT_FP32, 2><<<grid, block, 0, st>>>(a);
+  }
   return od_launch_status();
 }

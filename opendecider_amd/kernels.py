@@ -384,11 +384,35 @@ def stream_workspace(nsplit: int, R: int, Hq: int, t: int, D: int, Ns: int, Hkv:
     return ws
 
 
-def stream_split_count(Ns: int, Hkv: int, T: int, target_workgroups: int = 512, min_tiles: int = 8) -> int:
-    """Key-range splits for od_branched_attn_stream: about two 4-wave workgroups per CU over all (state, head)
-    pairs, keeping at least `min_tiles` 32-key tiles (two per wave) in each split."""
+def stream_split_count(Ns: int, Hkv: int, T: int, n_cu: int = 256, min_tiles: int = 16) -> int:
+    """Key-range splits for od_branched_attn_stream. Its 8-wave workgroups take half of every SIMD's registers, so a
+    CU runs one at a time, and n splits of Ns x Hkv (state, head) pairs take ceil(pairs n / n_cu) rounds of
+    ceil(tiles / n) 32-key tiles plus a workgroup's fixed work (about two tiles per wave: the queries, the wave
+    merge, the partials): the n of least cost (the smallest on ties), keeping at least `min_tiles` tiles per split.
+    With fewer, larger splits the state is read by fewer concurrent streams, which measured faster than filling the
+    CUs twice over."""
+    pairs = max(Ns * Hkv, 1)
     tiles = (T + 31) // 32
-    return max(1, min(-(-target_workgroups // max(Ns * Hkv, 1)), tiles // min_tiles, 256))
+    n_max = max(1, min(tiles // min_tiles, 256))
+    best, best_cost = 1, None
+    for n in range(1, n_max + 1):
+        cost = -(-pairs * n // n_cu) * (-(-tiles // n) + 16)
+        if best_cost is None or cost < best_cost:
+            best, best_cost = n, cost
+    return best
+
+
+_CU_COUNT: dict = {}
+
+
+def cu_count(device) -> int:
+    """Compute units of a GPU (cached per device index)."""
+    device = torch.device(device)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _CU_COUNT.get(idx)
+    if n is None:
+        n = _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return n
 
 
 # The staged path writes each state block's image (twice the int8 bytes) once and lets every slot tile copy it
@@ -594,7 +618,7 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
         if D != STREAM_D or slots > STREAM_MAX_SLOTS:
             raise ValueError(f"branched_attn: the streaming kernel takes head_dim {STREAM_D} and at most "
                              f"{STREAM_MAX_SLOTS} slots per (state, head), not D={D} with {slots}")
-        nsp = stream_split_count(Ns, Hkv, T) if n_split is None else int(n_split)
+        nsp = stream_split_count(Ns, Hkv, T, cu_count(q.device)) if n_split is None else int(n_split)
         ws = stream_workspace(nsp, R, Hq, t, D, Ns, Hkv, q.device) if nsp > 1 else None
         check(lib().od_branched_attn_stream(ptr(q), *q.stride()[:3], ptr(k_own), *k_own.stride()[:3], ptr(v_own),
                                             *v_own.stride()[:3], ptr(kq), ptr(ks), ptr(vq), ptr(vs), ptr(kvalid),

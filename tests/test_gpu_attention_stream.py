@@ -110,7 +110,11 @@ def test_stream_refuses_what_it_cannot_run(gpu_lib):
     c = make_case(seed=32, Ns=1, row_counts=[1], Hq=8, Hkv=8, t=2, D=64, T=64)
     with pytest.raises(ValueError):
         run_stream(c)
-    assert kernels.stream_split_count(8, 8, 32768) == 8
+    # 64 (state, head) pairs of 32768 keys on 256 CUs: 4 splits fill the CUs once; 48 pairs: 5 splits (240
+    # workgroups), not 6 (288, a second round on 32 CUs); a short state keeps 16 tiles per split
+    assert kernels.stream_split_count(8, 8, 32768) == 4
+    assert kernels.stream_split_count(6, 8, 32768) == 5
+    assert kernels.stream_split_count(1, 1, 1024) == 2
 
 
 def test_split_attention_int8_few_rows_streams(gpu_lib):
