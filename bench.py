@@ -71,8 +71,8 @@ def mfma_ceiling(modes=(0, 1, 2, 3, 4), iters=100000):
 
 def hbm_ceiling(gib: int = 2, reps: int = 10):
     """HBM read rate the chip sustains (od_probe_hbm_read in libod_probe.so): a buffer of `gib` GiB (well past the
-    256 MB Infinity Cache) streamed by a plain grid-stride read kernel with 16-byte loads, the best of 4, 8 and 16
-    workgroups per CU; GB/s."""
+    256 MB Infinity Cache) read with 16-byte non-temporal loads, by a grid-stride kernel at 4, 8 and 16 workgroups
+    per CU and as contiguous per-workgroup chunks at 1 and 2 workgroups of 8 waves per CU; the best, in GB/s."""
     import ctypes
 
     from opendecider_amd import build as _b
@@ -84,8 +84,8 @@ def hbm_ceiling(gib: int = 2, reps: int = 10):
     if rc != 0:
         raise RuntimeError(f"od_probe_hbm_read failed: {rc}")
     return {"value": gbs.value, "unit": "GB/s", "frac_of_peak": gbs.value / HBM_PEAK_GBS,
-            "probe": f"od_probe_hbm_read: {gib} GiB read by a grid-stride kernel, 16-byte loads, 8 in flight per "
-                     "thread, best of 4/8/16 workgroups per CU"}
+            "probe": f"od_probe_hbm_read: {gib} GiB read with 16-byte non-temporal loads, best of a grid-stride "
+                     "kernel (4/8/16 workgroups per CU) and contiguous chunks (1/2 workgroups of 8 waves per CU)"}
 
 
 def _sustained(ceil, mode):

@@ -175,11 +175,35 @@ __global__ __launch_bounds__(256) void hbm_read_kernel(const v4u* __restrict__ s
   sink[tid] = (int)acc;
 }
 
+// The same read as contiguous chunks: workgroup b (8 waves) reads bytes [b chunk, (b + 1) chunk) of the buffer in
+// 4 KB pieces, wave w taking pieces w, w + 8, ... with four pieces (16 loads of 16 bytes per lane) in flight, through a
+// buffer descriptor bounded to the chunk (the pieces past its end read as zeros, none past the buffer), with the
+// non-temporal cache policy; the access pattern of a key-range stream over an int8 state.
+__global__ __launch_bounds__(512) void hbm_chunk_kernel(const uint8_t* __restrict__ src, int64_t chunk, int* sink) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const auto r = __builtin_amdgcn_make_buffer_rsrc((void*)(src + (int64_t)blockIdx.x * chunk), (short)0, (int)chunk,
+                                                   0x00020000);
+  const int pieces = (int)(chunk >> 12);
+  uint32_t acc = 0;
+  for (int pc = wave; pc < pieces; pc += 32) {
+    v4u v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        v[4 * k + u] = __builtin_amdgcn_raw_buffer_load_b128(r, ((pc + 8 * k) << 12) + 1024 * u + 16 * lane, 0, 2);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  sink[blockIdx.x * 512 + threadIdx.x] = (int)acc;
+}
+
 }  // namespace
 
 // Reads a `bytes`-byte device buffer (filled first) with hbm_read_kernel at 4, 8 and 16 workgroups of 4 waves per
-// CU, `reps` timed launches each after a warm-up launch, on the current device; synchronous. Writes the best read
-// rate in GB/s. Returns 0, or -1 (bad argument) / -2 (HIP error).
+// CU and with hbm_chunk_kernel at 1 and 2 workgroups of 8 waves per CU, `reps` timed launches each after a warm-up
+// launch, on the current device; synchronous. Writes the best read rate in GB/s (of the bytes each launch reads).
+// Returns 0, or -1 (bad argument) / -2 (HIP error).
 extern "C" int od_probe_hbm_read(int64_t bytes, int reps, double* gbs) {
   if (bytes < (1 << 24) || bytes % 16 || reps < 1 || !gbs) return -1;
   int dev = 0, cus = 0;
@@ -196,22 +220,31 @@ extern "C" int od_probe_hbm_read(int64_t bytes, int reps, double* gbs) {
       hipEventCreate(&e1) != hipSuccess) {
     rc = -2;
   }
-  for (int per_cu : {4, 8, 16}) {
-    if (rc != 0) break;
-    const int grid = per_cu * cus;
+  // variants 0..2: grid-stride at 4, 8, 16 workgroups per CU; 3, 4: chunks at 1, 2 workgroups per CU
+  for (int var = 0; var < 5 && rc == 0; ++var) {
+    const int grid = var < 3 ? (4 << var) * cus : (var - 2) * cus;
+    const int64_t chunk = (bytes / grid) & ~(int64_t)4095;  // whole 4 KB pieces
+    if (var >= 3 && (chunk < 4096 || chunk >= (1ll << 30))) continue;  // 32-bit piece offsets, 24 pieces past the end
+    const double read = var < 3 ? (double)bytes : (double)chunk * grid;
+    auto launch = [&]() {
+      if (var < 3)
+        hbm_read_kernel<<<grid, 256>>>(buf, n16, sink);
+      else
+        hbm_chunk_kernel<<<grid, 512>>>(reinterpret_cast<const uint8_t*>(buf), chunk, sink);
+    };
     float ms = 0.0f;
-    hbm_read_kernel<<<grid, 256>>>(buf, n16, sink);
+    launch();
     if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess || hipEventRecord(e0, 0) != hipSuccess) {
       rc = -2;
       break;
     }
-    for (int r = 0; r < reps; ++r) hbm_read_kernel<<<grid, 256>>>(buf, n16, sink);
+    for (int r = 0; r < reps; ++r) launch();
     if (hipGetLastError() != hipSuccess || hipEventRecord(e1, 0) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms <= 0.0f) {
       rc = -2;
       break;
     }
-    const double rate = (double)bytes * reps / (ms * 1e-3) / 1e9;
+    const double rate = read * reps / (ms * 1e-3) / 1e9;
     if (rate > best) best = rate;
   }
   if (rc == 0) *gbs = best;
