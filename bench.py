@@ -415,6 +415,11 @@ def cpu_baseline_wide(args):
                        f"of {n} after a warm-up, {per_layer:.2f} s per layer, scaled x{args.layers} layers")}
 
 
+# Qwen3.5's full-attention layer geometry (transformers' Qwen3_5TextConfig): 16 / 4 heads of 256, rotary on the
+# first 64 dims (partial_rotary_factor 0.25), zero-centred RMSNorms, the output gate
+QWEN35_ATTENTION = dict(n_heads=16, n_kv_heads=4, head_dim=256, rot_dim=64, norm_offset=True, gated=True)
+
+
 def cpu_baseline_hybrid(args):
     """The oracle on a bounded sample of the hybrid decision: ONE request (a 4096-token state of random ids prefilled,
     then 64 options x 24 tokens scored) through ONE Gated DeltaNet layer (the gated delta rule in fp32, the
@@ -431,8 +436,8 @@ def cpu_baseline_hybrid(args):
     ids_o = torch.randint(0, 4096, (1, n_opt, t), generator=g)
     per = {}
     n = args.cpu_sample_repeats
-    for kind, cfg in (("gdn", od.DecoderConfig(n_layers=1, full_attention_interval=4, gated=True)),
-                      ("attention", od.DecoderConfig(n_layers=1, gated=True))):
+    for kind, cfg in (("gdn", od.DecoderConfig(n_layers=1, full_attention_interval=4, **QWEN35_ATTENTION)),
+                      ("attention", od.DecoderConfig(n_layers=1, **QWEN35_ATTENTION))):
         w = od.make_weights(cfg, seed=1)
 
         def run():
@@ -596,15 +601,16 @@ def _rate(t, flops_key=None):
 
 def run_hybrid(args):
     """The full decision forward on the Qwen3.5 hybrid stack: 32 layers (hidden 4096, FFN 12288), every 4th a
-    full-attention layer (32/8 heads x 128, output gate), the others Gated DeltaNet layers (16 key / 32 value heads
-    of 128, conv 4); 4 requests, each a 4096-token state of random ids prefilled (GDN layers: conv windows and
-    recurrent states; attention layers: int8 K/V), then 64 options x 24 tokens scored against it, the rows reading
-    their request's GDN states in place."""
+    full-attention layer in Qwen3.5's geometry (16 / 4 heads of 256, rotary on the first 64 dims, zero-centred
+    RMSNorms, output gate), the others Gated DeltaNet layers (16 key / 32 value heads of 128, conv 4); 4 requests,
+    each a 4096-token state of random ids prefilled (GDN layers: conv windows and recurrent states; attention layers:
+    int8 K/V), then 64 options x 24 tokens scored against it, the rows reading their request's GDN states in
+    place."""
     import torch
 
     from opendecider_amd import decoder as dmod
     dev = "cuda:0"
-    cfg = dmod.DecoderConfig(n_layers=32, full_attention_interval=4, gated=True, vocab=248320)
+    cfg = dmod.DecoderConfig(n_layers=32, full_attention_interval=4, vocab=248320, **QWEN35_ATTENTION)
     B, S, n_opt, t = 4, 4096, 64, 24
     dec = dmod.random_decoder(cfg, seed=0, device=dev, max_pos=S + t + 16)
     g = torch.Generator(device=dev).manual_seed(3)
@@ -676,9 +682,11 @@ def run_hybrid(args):
         "config": {"workload": (f"full decision forward, hybrid stack: {B} requests, {S}-token states of random ids "
                                 f"prefilled through {cfg.n_layers} layers ({sum(cfg.is_gdn(i) for i in range(32))} "
                                 "Gated DeltaNet + 8 full attention), 64 options x 24 tokens scored, 'none' appended; "
-                                "hidden 4096, FFN 12288, random init"),
+                                "hidden 4096, FFN 12288, attention 16 / 4 heads of 256 with rotary on 64 dims and "
+                                "zero-centred norms, random init"),
                    "requests": B, "state_tokens": S, "options": n_opt, "tokens_per_option": t,
-                   "layers": cfg.n_layers, "full_attention_interval": 4},
+                   "layers": cfg.n_layers, "full_attention_interval": 4, "attention_heads": "16/4 x 256",
+                   "rotary_dims": cfg.rotary_dims},
         "roofline": roof,
         "gdn_prep": _rate(prep_t), "gdn_recurrence": _rate(rec_t, "recurrent_equivalent_tflops"),
         "gdn_norm_quant": _rate(norm_t),

@@ -411,6 +411,16 @@ int od_rmsnorm_quant(const uint16_t* x, int64_t ldx, const uint16_t* w, const ui
                      int64_t ldq, float* sx, int64_t M, int64_t K, od_stream_t stream);
 
 /*
+ * od_rmsnorm_quant_ex: od_rmsnorm_quant with the weight convention chosen by weight_offset: 0 is the one above;
+ *   1 is Qwen3.5's zero-centred norm (transformers' Qwen3_5RMSNorm, the input / post-attention / final norms of the
+ *   reference's default backbone, configs/backbone.yaml:1-4): y = bf16((x * r) * (1 + w)), products and the sum
+ *   1 + w in fp32, one rounding. Any other weight_offset returns OD_ERR_UNSUPPORTED.
+ */
+int od_rmsnorm_quant_ex(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* inv_s, float eps,
+                        int weight_offset, int8_t* xq, int64_t ldq, float* sx, int64_t M, int64_t K,
+                        od_stream_t stream);
+
+/*
  * od_silu_mul_quant: y = bf16(bf16(silu(g)) * u) with g = gu[:, :F], u = gu[:, F:2F] (fused gate+up GEMM output,
  *   row stride ldg), optionally y = bf16(y * inv_s), then the od_act_quant formula per row -> aq int8 [M, ldq],
  *   sa fp32 [M].
@@ -430,6 +440,20 @@ int od_qk_norm_rope(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int
                     int64_t n_pos, const int32_t* pos, float eps, od_stream_t stream);
 
 /*
+ * od_qk_norm_rope_ex: od_qk_norm_rope for Qwen3.5's full-attention heads as well: D in {64, 128, 256}; rot_dim = D
+ *   (full rotary) or D / 4 (partial rotary, Qwen3.5's partial_rotary_factor 0.25: rotate_half acts on dims
+ *   0 .. rot_dim - 1, pairs (d, d + rot_dim / 2), and dims rot_dim .. D - 1 keep their normalized values, as
+ *   transformers' apply_rotary_pos_emb does for a cos/sin table narrower than the head); the tables are
+ *   [n_pos, rot_dim / 2]. weight_offset as od_rmsnorm_quant_ex (1: the q/k norms are Qwen3_5RMSNorm,
+ *   n = bf16((x * r) * (1 + w))). Needs ld % 4 == 0 and 8-byte aligned qkv / weights / tables (else OD_ERR_ALIGN)
+ *   except for the D in {64, 128}, full-rotary, weight_offset 0 case, which od_qk_norm_rope also serves unaligned.
+ */
+int od_qk_norm_rope_ex(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int64_t n_heads_k, int64_t D,
+                       int64_t rot_dim, int weight_offset, const uint16_t* q_w, const uint16_t* k_w,
+                       const uint16_t* cos_t, const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps,
+                       od_stream_t stream);
+
+/*
  * od_qk_norm_rope_kv_append: od_qk_norm_rope plus the int8 K/V append of the same tokens, in one pass over the QKV
  *   GEMM output. Replaces, for a state prefill: the q/k norm + RoPE of the attention layer (prefix_attn.py:81-90)
  *   followed by the quantization of the new tokens' K/V slice that PrefixCache._take (state_cache.py:79) and
@@ -445,6 +469,16 @@ int od_qk_norm_rope_kv_append(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, i
                               int64_t D, const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
                               const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps, int8_t* kq,
                               float* ks, int8_t* vq, float* vs, int64_t cap, int64_t n0, od_stream_t stream);
+
+/*
+ * od_qk_norm_rope_kv_append_ex: od_qk_norm_rope_kv_append with od_qk_norm_rope_ex's head dims (64, 128, 256),
+ *   rot_dim (D or D / 4) and weight_offset (0 or 1); the same alignment requirements.
+ */
+int od_qk_norm_rope_kv_append_ex(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, int64_t n_heads_q,
+                                 int64_t n_heads_k, int64_t D, int64_t rot_dim, int weight_offset,
+                                 const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
+                                 const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps, int8_t* kq,
+                                 float* ks, int8_t* vq, float* vs, int64_t cap, int64_t n0, od_stream_t stream);
 
 /*
  * Gated DeltaNet (linear-attention) layers of the Qwen3.5 hybrid backbone: the passes between the layer's input

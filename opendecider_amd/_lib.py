@@ -55,9 +55,13 @@ SIGNATURES = {
                      _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int,
                      ctypes.c_float, _c_ptr],
     "od_rmsnorm_quant": [_c_ptr, _i64, _c_ptr, _c_ptr, ctypes.c_float, _c_ptr, _i64, _c_ptr, _i64, _i64, _c_ptr],
+    "od_rmsnorm_quant_ex": [_c_ptr, _i64, _c_ptr, _c_ptr, ctypes.c_float, ctypes.c_int, _c_ptr, _i64, _c_ptr, _i64,
+                            _i64, _c_ptr],
     "od_silu_mul_quant": [_c_ptr, _i64, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _c_ptr],
     "od_qk_norm_rope": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr,
                         ctypes.c_float, _c_ptr],
+    "od_qk_norm_rope_ex": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                           _i64, _c_ptr, ctypes.c_float, _c_ptr],
     "od_w8a8_gemm_swiglu": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _c_ptr],
     "od_w8a8_gemm_ws_size": [_i64, _i64, _i64, _c_ptr],
     "od_w8a8_gemm_ws": [_c_ptr, _i64, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _i64, _i64, _i64,
@@ -66,6 +70,9 @@ SIGNATURES = {
                         _i64, _c_ptr],
     "od_qk_norm_rope_kv_append": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64,
                                   _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _c_ptr],
+    "od_qk_norm_rope_kv_append_ex": [_c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _c_ptr, _c_ptr,
+                                     _c_ptr, _c_ptr, _i64, _c_ptr, ctypes.c_float, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                     _i64, _i64, _c_ptr],
     "od_attn_stage_bf16": [_c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _c_ptr, _i64, _i64, _i64, _i64,
                            ctypes.c_float, _c_ptr, _i64, _c_ptr],
     "od_gdn_prep": [_c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64,

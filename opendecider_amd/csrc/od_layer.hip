@@ -51,11 +51,13 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 // ---------------------------------------------------------------------------- RMSNorm + quantize
-// y_k = bf16(w_k * bf16(x_k * r)), r = 1 / sqrt(mean(x^2) + eps) (od_rms_factor); then optionally
-// y_k = bf16(y_k * inv_s_k);
+// y_k = bf16(w_k * bf16(x_k * r)), r = 1 / sqrt(mean(x^2) + eps) (od_rms_factor), or with zc (Qwen3.5's norm, one
+// rounding) y_k = bf16((x_k * r) * (1 + w_k)) in fp32; then optionally y_k = bf16(y_k * inv_s_k);
 // then the per-row int8 quantizer. One workgroup per row; the row is read three times (L1/L2 after the first).
-__device__ __forceinline__ float rms_val(const uint16_t* xr, const uint16_t* w, const uint16_t* inv_s, int k, float r) {
-  float y = bfr(od_bf16_to_f32(w[k]) * bfr(od_bf16_to_f32(xr[k]) * r));
+__device__ __forceinline__ float rms_val(const uint16_t* xr, const uint16_t* w, const uint16_t* inv_s, int k, float r,
+                                         bool zc) {
+  const float x = od_bf16_to_f32(xr[k]), wk = od_bf16_to_f32(w[k]);
+  float y = zc ? bfr((x * r) * (1.0f + wk)) : bfr(wk * bfr(x * r));
   if (inv_s) y = bfr(y * od_bf16_to_f32(inv_s[k]));
   return y;
 }
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_kernel(const uint16_t*
                                                                  const uint16_t* __restrict__ w,
                                                                  const uint16_t* __restrict__ inv_s, float eps,
                                                                  int8_t* __restrict__ xq, int64_t ldq,
-                                                                 float* __restrict__ sx, int K) {
+                                                                 float* __restrict__ sx, int K, int zc) {
   __shared__ float red[kThreads / OD_WAVE];
   __shared__ double red64[kThreads / OD_WAVE];
   const int64_t row = blockIdx.x;
@@ -77,11 +79,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_kernel(const uint16_t*
   ss = block_sum_f64(ss, red64);
   const float r = od_rms_factor(ss, K, eps);
   float amax = 0.0f;
-  for (int k = threadIdx.x; k < K; k += kThreads) amax = fmaxf(amax, fabsf(rms_val(xr, w, inv_s, k, r)));
+  for (int k = threadIdx.x; k < K; k += kThreads) amax = fmaxf(amax, fabsf(rms_val(xr, w, inv_s, k, r, zc)));
   amax = block_max(amax, red);
   const float scale = od_q8_scale(amax), inv = 1.0f / scale;
   int8_t* qr = xq + row * ldq;
-  for (int k = threadIdx.x; k < K; k += kThreads) qr[k] = od_q8_one(rms_val(xr, w, inv_s, k, r), scale, inv);
+  for (int k = threadIdx.x; k < K; k += kThreads) qr[k] = od_q8_one(rms_val(xr, w, inv_s, k, r, zc), scale, inv);
   if (threadIdx.x == 0) sx[row] = scale;
 }
 
@@ -167,7 +169,7 @@ __device__ __forceinline__ void store_q8(int8_t* dst, const float (&y)[8], float
   *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
 }
 
-template <int NV, bool INV>
+template <int NV, bool INV, bool ZC>
 __global__ __launch_bounds__(kThreads) void rmsnorm_quant_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                      const uint16_t* __restrict__ w,
                                                                      const uint16_t* __restrict__ inv_s, float eps,
@@ -203,10 +205,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_quant_vec_kernel(const uint1
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float a = y[v][2 * j] * r, b = y[v][2 * j + 1] * r, wa, wb;
-      od_bfr2(a, b);
+      if (!ZC) od_bfr2(a, b);
       unpack2(word(wv[v], j), wa, wb);
-      a *= wa;
-      b *= wb;
+      if (ZC) {
+        a *= 1.0f + wa;
+        b *= 1.0f + wb;
+      } else {
+        a *= wa;
+        b *= wb;
+      }
       uint32_t p = od_bfr2(a, b);
       if (INV) {
         float ia, ib;
@@ -300,11 +307,11 @@ __device__ __forceinline__ uint2 pack4(const uint16_t (&h)[4]) {
   return make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
 }
 
-// Quantizes a head's D bf16 values held 8 per lane (oa: d = 4j.., ob: D/2 + 4j..) over the G lanes of its group and
-// writes the int8 row and its scale.
+// Quantizes a head's D bf16 values held 8 per lane (oa: d = da .. da + 3, ob: d = db .. db + 3) over the G lanes of
+// its group and writes the int8 row and its scale.
 template <int D>
-__device__ __forceinline__ void quant_head(const uint16_t (&oa)[4], const uint16_t (&ob)[4], int j, int8_t* qrow,
-                                           float* srow) {
+__device__ __forceinline__ void quant_head(const uint16_t (&oa)[4], const uint16_t (&ob)[4], int j, int da, int db,
+                                           int8_t* qrow, float* srow) {
   constexpr int G = D / 8;
   float y[8];
   uint32_t bits = 0;
@@ -320,12 +327,16 @@ __device__ __forceinline__ void quant_head(const uint16_t (&oa)[4], const uint16
   const float scale = od_q8_scale(__uint_as_float(bits << 16)), inv = 1.0f / scale;
   uint32_t w[2];
   od_q8_words<8>(y, scale, inv, w);
-  *reinterpret_cast<uint32_t*>(qrow + 4 * j) = w[0];
-  *reinterpret_cast<uint32_t*>(qrow + D / 2 + 4 * j) = w[1];
+  *reinterpret_cast<uint32_t*>(qrow + da) = w[0];
+  *reinterpret_cast<uint32_t*>(qrow + db) = w[1];
   if (j == 0) *srow = scale;
 }
 
-template <int D, bool APPEND>
+// Partial rotary (RD < D, Qwen3.5's 64 of 256): rotate_half acts on the first RD dims only (pairs d, d + RD/2) and the
+// other D - RD pass through the norm unrotated; lane j < RD/8 holds the pairs 4j .. 4j + 3 and RD/2 + 4j .., a lane
+// j >= RD/8 the 8 dims RD + 8 (j - RD/8) .. +7. The tables are [n_pos, RD/2]. ZC: the Qwen3.5 norm, one rounding:
+// n_d = bf16((x_d * r) * (1 + w_d)) (fp32 products), instead of bf16(w_d * bf16(x_d * r)).
+template <int D, int RD, bool ZC, bool APPEND>
 __global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restrict__ qkv, int64_t ld, int64_t M,
                                                                int n_heads_q, int n_heads_k,
                                                                const uint16_t* __restrict__ qw,
@@ -334,15 +345,18 @@ __global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restr
                                                                const uint16_t* __restrict__ sin_t, int64_t n_pos,
                                                                const int32_t* __restrict__ pos, float eps,
                                                                KvAppend kv) {
-  constexpr int G = D / 8, L = D / 2;
+  constexpr int G = D / 8, RL = RD / 8, RH = RD / 2;
+  static_assert(RD % 16 == 0 && RD <= D, "rotary dims");
   const int heads = n_heads_q + n_heads_k * (APPEND ? 2 : 1);
   const int64_t gh = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
   if (gh >= M * heads) return;  // whole G-lane groups exit together
   const int64_t row = gh / heads;
   const int head = (int)(gh % heads);
   const int j = threadIdx.x % G;
+  const bool rot = j < RL;  // this lane holds rotary pairs
+  const int da = rot ? 4 * j : RD + 8 * (j - RL), db = rot ? RH + 4 * j : da + 4;
   uint16_t* hp = qkv + row * ld + (int64_t)head * D;
-  const uint2 ra = *reinterpret_cast<const uint2*>(hp + 4 * j), rb = *reinterpret_cast<const uint2*>(hp + L + 4 * j);
+  const uint2 ra = *reinterpret_cast<const uint2*>(hp + da), rb = *reinterpret_cast<const uint2*>(hp + db);
   int64_t crow = 0;
   if (APPEND) {
     const int64_t b = row / kv.S, i = row % kv.S;
@@ -351,49 +365,69 @@ __global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restr
   if (APPEND && head >= n_heads_q + n_heads_k) {  // a value head: quantize only
     const uint16_t va[4] = {(uint16_t)ra.x, (uint16_t)(ra.x >> 16), (uint16_t)ra.y, (uint16_t)(ra.y >> 16)};
     const uint16_t vb[4] = {(uint16_t)rb.x, (uint16_t)(rb.x >> 16), (uint16_t)rb.y, (uint16_t)(rb.y >> 16)};
-    quant_head<D>(va, vb, j, kv.vq + crow * D, kv.vs + crow);
+    quant_head<D>(va, vb, j, da, db, kv.vq + crow * D, kv.vs + crow);
     return;
   }
   const uint16_t* w = head < n_heads_q ? qw : kw;
   float a[4], b[4], fa[4], fb[4];
   unpack4(ra, a);
   unpack4(rb, b);
-  unpack4(*reinterpret_cast<const uint2*>(w + 4 * j), fa);
-  unpack4(*reinterpret_cast<const uint2*>(w + L + 4 * j), fb);
+  unpack4(*reinterpret_cast<const uint2*>(w + da), fa);
+  unpack4(*reinterpret_cast<const uint2*>(w + db), fb);
   double ss = 0.0;
 #pragma unroll
   for (int e = 0; e < 4; ++e) ss = fma((double)b[e], (double)b[e], fma((double)a[e], (double)a[e], ss));
   ss = od_group_sum_f64<G>(ss);
   const float r = od_rms_factor(ss, D, eps);
-  const int64_t p = pos[row];
-  const bool in_table = p >= 0 && p < n_pos;  // a position past the tables yields NaN, never an out-of-bounds read
-  float c[4], sn[4];
-  if (in_table) {
-    unpack4(*reinterpret_cast<const uint2*>(cos_t + p * L + 4 * j), c);
-    unpack4(*reinterpret_cast<const uint2*>(sin_t + p * L + 4 * j), sn);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) c[e] = sn[e] = __builtin_nanf("");
-  }
-  uint16_t oa[4], ob[4];
+  float na[4], nb[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float na = bfr(fa[e] * bfr(a[e] * r)), nb = bfr(fb[e] * bfr(b[e] * r));
-    oa[e] = od_f32_to_bf16(bfr(na * c[e]) + bfr(-nb * sn[e]));
-    ob[e] = od_f32_to_bf16(bfr(nb * c[e]) + bfr(na * sn[e]));
+    if constexpr (ZC) {
+      na[e] = bfr((a[e] * r) * (1.0f + fa[e]));
+      nb[e] = bfr((b[e] * r) * (1.0f + fb[e]));
+    } else {
+      na[e] = bfr(fa[e] * bfr(a[e] * r));
+      nb[e] = bfr(fb[e] * bfr(b[e] * r));
+    }
   }
-  *reinterpret_cast<uint2*>(hp + 4 * j) = pack4(oa);
-  *reinterpret_cast<uint2*>(hp + L + 4 * j) = pack4(ob);
-  if (APPEND && head >= n_heads_q) quant_head<D>(oa, ob, j, kv.kq + crow * D, kv.ks + crow);
+  uint16_t oa[4], ob[4];
+  if (rot) {
+    const int64_t p = pos[row];
+    const bool in_table = p >= 0 && p < n_pos;  // a position past the tables yields NaN, never an out-of-bounds read
+    float c[4], sn[4];
+    if (in_table) {
+      unpack4(*reinterpret_cast<const uint2*>(cos_t + p * RH + 4 * j), c);
+      unpack4(*reinterpret_cast<const uint2*>(sin_t + p * RH + 4 * j), sn);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c[e] = sn[e] = __builtin_nanf("");
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      oa[e] = od_f32_to_bf16(bfr(na[e] * c[e]) + bfr(-nb[e] * sn[e]));
+      ob[e] = od_f32_to_bf16(bfr(nb[e] * c[e]) + bfr(na[e] * sn[e]));
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      oa[e] = od_f32_to_bf16(na[e]);
+      ob[e] = od_f32_to_bf16(nb[e]);
+    }
+  }
+  *reinterpret_cast<uint2*>(hp + da) = pack4(oa);
+  *reinterpret_cast<uint2*>(hp + db) = pack4(ob);
+  if (APPEND && head >= n_heads_q) quant_head<D>(oa, ob, j, da, db, kv.kq + crow * D, kv.ks + crow);
 }
 
 template <int NV>
 void launch_rmsnorm_vec(dim3 grid, hipStream_t st, const uint16_t* x, int64_t ldx, const uint16_t* w,
-                        const uint16_t* inv_s, float eps, int8_t* xq, int64_t ldq, float* sx) {
-  if (inv_s) {
-    rmsnorm_quant_vec_kernel<NV, true><<<grid, dim3(kThreads), 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+                        const uint16_t* inv_s, float eps, int8_t* xq, int64_t ldq, float* sx, bool zc) {
+  if (zc) {
+    if (inv_s) rmsnorm_quant_vec_kernel<NV, true, true><<<grid, dim3(kThreads), 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+    else rmsnorm_quant_vec_kernel<NV, false, true><<<grid, dim3(kThreads), 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
   } else {
-    rmsnorm_quant_vec_kernel<NV, false><<<grid, dim3(kThreads), 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+    if (inv_s) rmsnorm_quant_vec_kernel<NV, true, false><<<grid, dim3(kThreads), 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
+    else rmsnorm_quant_vec_kernel<NV, false, false><<<grid, dim3(kThreads), 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx);
   }
 }
 
@@ -409,26 +443,34 @@ void launch_silu_vec(dim3 grid, hipStream_t st, const uint16_t* gu, int64_t ldg,
 
 }  // namespace
 
-extern "C" int od_rmsnorm_quant(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* inv_s, float eps,
-                                int8_t* xq, int64_t ldq, float* sx, int64_t M, int64_t K, od_stream_t stream) {
+extern "C" int od_rmsnorm_quant_ex(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* inv_s,
+                                   float eps, int weight_offset, int8_t* xq, int64_t ldq, float* sx, int64_t M,
+                                   int64_t K, od_stream_t stream) {
   if (M < 0 || K < 1 || K > (1 << 30) || ldx < K || ldq < K) return OD_ERR_SHAPE;
+  if (weight_offset != 0 && weight_offset != 1) return OD_ERR_UNSUPPORTED;
   if (M == 0) return OD_OK;
   if (!x || !w || !xq || !sx) return OD_ERR_NULL;
   if (M > 0x7fffffff) return OD_ERR_SHAPE;
   hipStream_t st = (hipStream_t)stream;
+  const bool zc = weight_offset != 0;
   const bool vec = (ldx % 8 == 0) && (ldq % 8 == 0) && od_aligned16(x) && od_aligned16(w) &&
                    (!inv_s || od_aligned16(inv_s)) && ((((uintptr_t)xq) & 7u) == 0);
   const dim3 grid((unsigned)M), block(kThreads);
   if (vec && K == 2048) {
-    launch_rmsnorm_vec<1>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx);
+    launch_rmsnorm_vec<1>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx, zc);
   } else if (vec && K == 4096) {
-    launch_rmsnorm_vec<2>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx);
+    launch_rmsnorm_vec<2>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx, zc);
   } else if (vec && K == 8192) {
-    launch_rmsnorm_vec<4>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx);
+    launch_rmsnorm_vec<4>(grid, st, x, ldx, w, inv_s, eps, xq, ldq, sx, zc);
   } else {
-    rmsnorm_quant_kernel<<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx, (int)K);
+    rmsnorm_quant_kernel<<<grid, block, 0, st>>>(x, ldx, w, inv_s, eps, xq, ldq, sx, (int)K, zc ? 1 : 0);
   }
   return od_launch_status();
+}
+
+extern "C" int od_rmsnorm_quant(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* inv_s, float eps,
+                                int8_t* xq, int64_t ldq, float* sx, int64_t M, int64_t K, od_stream_t stream) {
+  return od_rmsnorm_quant_ex(x, ldx, w, inv_s, eps, 0, xq, ldq, sx, M, K, stream);
 }
 
 extern "C" int od_silu_mul_quant(const uint16_t* gu, int64_t ldg, int64_t F, const uint16_t* inv_s, int8_t* aq,
@@ -457,62 +499,99 @@ namespace {
 
 bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; }
 
+template <int D, int RD, bool ZC, bool APPEND>
+void launch_rope_vec_t(dim3 grid, hipStream_t st, uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q,
+                       int64_t n_heads_k, const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
+                       const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps, const KvAppend& kv) {
+  qk_rope_vec_kernel<D, RD, ZC, APPEND><<<grid, dim3(kThreads), 0, st>>>(
+      qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+}
+
+// The (D, rotary dims) pairs the vector kernel is built for: full rotary at D = 64, 128, 256 and a quarter of the
+// head (Qwen3.5's partial_rotary_factor 0.25).
+bool rope_shape_ok(int64_t D, int64_t rot_dim) {
+  return (D == 64 || D == 128 || D == 256) && (rot_dim == D || rot_dim == D / 4);
+}
+
 template <bool APPEND>
 int launch_rope_vec(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int64_t n_heads_k, int64_t D,
-                    const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t, const uint16_t* sin_t,
-                    int64_t n_pos, const int32_t* pos, float eps, const KvAppend& kv, hipStream_t st) {
+                    int64_t rot_dim, bool zc, const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
+                    const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps, const KvAppend& kv,
+                    hipStream_t st) {
   const int64_t heads = n_heads_q + n_heads_k * (APPEND ? 2 : 1);
   const int64_t per_block = kThreads / (D / 8);
   const int64_t blocks = (M * heads + per_block - 1) / per_block;
   if (blocks > 0x7fffffff || heads > 0x7fffffff) return OD_ERR_SHAPE;
-  if (D == 128) {
-    qk_rope_vec_kernel<128, APPEND><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
-        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
-  } else {
-    qk_rope_vec_kernel<64, APPEND><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
-        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
-  }
+  if (!rope_shape_ok(D, rot_dim)) return OD_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)blocks);
+  auto go = [&](auto DC) {
+    constexpr int DD = decltype(DC)::value;
+    const bool full = rot_dim == DD;
+    if (zc) {
+      if (full) launch_rope_vec_t<DD, DD, true, APPEND>(grid, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+      else launch_rope_vec_t<DD, DD / 4, true, APPEND>(grid, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+    } else {
+      if (full) launch_rope_vec_t<DD, DD, false, APPEND>(grid, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+      else launch_rope_vec_t<DD, DD / 4, false, APPEND>(grid, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+    }
+  };
+  if (D == 256) go(std::integral_constant<int, 256>{});
+  else if (D == 128) go(std::integral_constant<int, 128>{});
+  else go(std::integral_constant<int, 64>{});
   return od_launch_status();
 }
 
 }  // namespace
 
+extern "C" int od_qk_norm_rope_ex(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int64_t n_heads_k,
+                                  int64_t D, int64_t rot_dim, int weight_offset, const uint16_t* q_w,
+                                  const uint16_t* k_w, const uint16_t* cos_t, const uint16_t* sin_t, int64_t n_pos,
+                                  const int32_t* pos, float eps, od_stream_t stream) {
+  if (M < 0 || n_heads_q < 0 || n_heads_k < 0 || ld < (n_heads_q + n_heads_k) * D) return OD_ERR_SHAPE;
+  if (weight_offset != 0 && weight_offset != 1) return OD_ERR_UNSUPPORTED;
+  if (!rope_shape_ok(D, rot_dim)) return OD_ERR_UNSUPPORTED;
+  const int64_t heads = n_heads_q + n_heads_k;
+  if (M == 0 || heads == 0) return OD_OK;
+  if (!qkv || !q_w || !k_w || !cos_t || !sin_t || !pos) return OD_ERR_NULL;
+  const bool vec = (ld % 4 == 0) && aligned8(qkv) && aligned8(q_w) && aligned8(k_w) && aligned8(cos_t) &&
+                   aligned8(sin_t);
+  hipStream_t st = (hipStream_t)stream;
+  if (vec)
+    return launch_rope_vec<false>(qkv, ld, M, n_heads_q, n_heads_k, D, rot_dim, weight_offset != 0, q_w, k_w, cos_t,
+                                  sin_t, n_pos, pos, eps, KvAppend{}, st);
+  // unaligned rows: the scalar kernel, for the full-rotary Llama-style norm at D = 64 or 128 only
+  if (rot_dim != D || weight_offset != 0 || D == 256) return OD_ERR_ALIGN;
+  const int64_t per_block = kThreads / (D / 2);
+  const int64_t blocks = (M * heads + per_block - 1) / per_block;
+  if (blocks > 0x7fffffff || heads > 0x7fffffff) return OD_ERR_SHAPE;
+  if (D == 128)
+    qk_norm_rope_kernel<128><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
+        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
+  else
+    qk_norm_rope_kernel<64><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
+        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
+  return od_launch_status();
+}
+
 extern "C" int od_qk_norm_rope(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int64_t n_heads_k,
                                int64_t D, const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
                                const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps,
                                od_stream_t stream) {
-  if (M < 0 || n_heads_q < 0 || n_heads_k < 0 || ld < (n_heads_q + n_heads_k) * D) return OD_ERR_SHAPE;
   if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
-  const int64_t heads = n_heads_q + n_heads_k;
-  if (M == 0 || heads == 0) return OD_OK;
-  if (!qkv || !q_w || !k_w || !cos_t || !sin_t || !pos) return OD_ERR_NULL;
-  const int64_t per_block = kThreads / (D / 2);
-  const int64_t blocks = (M * heads + per_block - 1) / per_block;
-  if (blocks > 0x7fffffff || heads > 0x7fffffff) return OD_ERR_SHAPE;
-  hipStream_t st = (hipStream_t)stream;
-  const bool vec = (ld % 4 == 0) && aligned8(qkv) && aligned8(q_w) && aligned8(k_w) && aligned8(cos_t) &&
-                   aligned8(sin_t);
-  if (vec) {
-    return launch_rope_vec<false>(qkv, ld, M, n_heads_q, n_heads_k, D, q_w, k_w, cos_t, sin_t, n_pos, pos, eps,
-                                  KvAppend{}, st);
-  } else if (D == 128) {
-    qk_norm_rope_kernel<128><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
-        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
-  } else {
-    qk_norm_rope_kernel<64><<<dim3((unsigned)blocks), dim3(kThreads), 0, st>>>(
-        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps);
-  }
-  return od_launch_status();
+  return od_qk_norm_rope_ex(qkv, ld, M, n_heads_q, n_heads_k, D, D, 0, q_w, k_w, cos_t, sin_t, n_pos, pos, eps,
+                            stream);
 }
 
-extern "C" int od_qk_norm_rope_kv_append(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, int64_t n_heads_q,
-                                         int64_t n_heads_k, int64_t D, const uint16_t* q_w, const uint16_t* k_w,
-                                         const uint16_t* cos_t, const uint16_t* sin_t, int64_t n_pos,
-                                         const int32_t* pos, float eps, int8_t* kq, float* ks, int8_t* vq, float* vs,
-                                         int64_t cap, int64_t n0, od_stream_t stream) {
+extern "C" int od_qk_norm_rope_kv_append_ex(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, int64_t n_heads_q,
+                                            int64_t n_heads_k, int64_t D, int64_t rot_dim, int weight_offset,
+                                            const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
+                                            const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps,
+                                            int8_t* kq, float* ks, int8_t* vq, float* vs, int64_t cap, int64_t n0,
+                                            od_stream_t stream) {
   if (B < 0 || S < 0 || n_heads_q < 0 || n_heads_k < 0 || ld < (n_heads_q + 2 * n_heads_k) * D) return OD_ERR_SHAPE;
   if (n0 < 0 || cap < 0 || n0 + S > cap) return OD_ERR_SHAPE;
-  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  if (weight_offset != 0 && weight_offset != 1) return OD_ERR_UNSUPPORTED;
+  if (!rope_shape_ok(D, rot_dim)) return OD_ERR_UNSUPPORTED;
   const int64_t M = B * S;
   if (M == 0 || n_heads_q + n_heads_k == 0) return OD_OK;
   if (!qkv || !q_w || !k_w || !cos_t || !sin_t || !pos) return OD_ERR_NULL;
@@ -522,6 +601,16 @@ extern "C" int od_qk_norm_rope_kv_append(uint16_t* qkv, int64_t ld, int64_t B, i
       (((uintptr_t)kq) & 3u) || (((uintptr_t)vq) & 3u))
     return OD_ERR_ALIGN;
   KvAppend kv{kq, ks, vq, vs, S, cap, n0};
-  return launch_rope_vec<true>(qkv, ld, M, n_heads_q, n_heads_k, D, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv,
-                               (hipStream_t)stream);
+  return launch_rope_vec<true>(qkv, ld, M, n_heads_q, n_heads_k, D, rot_dim, weight_offset != 0, q_w, k_w, cos_t,
+                               sin_t, n_pos, pos, eps, kv, (hipStream_t)stream);
+}
+
+extern "C" int od_qk_norm_rope_kv_append(uint16_t* qkv, int64_t ld, int64_t B, int64_t S, int64_t n_heads_q,
+                                         int64_t n_heads_k, int64_t D, const uint16_t* q_w, const uint16_t* k_w,
+                                         const uint16_t* cos_t, const uint16_t* sin_t, int64_t n_pos,
+                                         const int32_t* pos, float eps, int8_t* kq, float* ks, int8_t* vq, float* vs,
+                                         int64_t cap, int64_t n0, od_stream_t stream) {
+  if (D != 64 && D != 128) return OD_ERR_UNSUPPORTED;
+  return od_qk_norm_rope_kv_append_ex(qkv, ld, B, S, n_heads_q, n_heads_k, D, D, 0, q_w, k_w, cos_t, sin_t, n_pos,
+                                      pos, eps, kq, ks, vq, vs, cap, n0, stream);
 }

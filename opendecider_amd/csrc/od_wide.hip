@@ -37,6 +37,7 @@ struct WideArgs {
   int64_t sqb, sqh, sqt, skb, skg, sks, svb, svg, svs, sob, soh, sot, smb;
   int H, G, T, S, DK, rep, causal;
   float scale_log2;
+  int dv_half;  // value columns blockIdx.z * dv_half .. +dv_half of a wider head (0: one launch covers DV)
 };
 
 template <int DKP, int DV, int NBUF>
@@ -308,6 +309,13 @@ __device__ __forceinline__ void wide_block(const WSmem<DKP, DV, NBUF>& sm, int b
 template <int DKP, int DV, int NBUF, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void wide_attn_kernel(WideArgs p) {
   __shared__ WSmem<DKP, DV, NBUF> sm;
+  // a head of 2 DV value columns in two halves (blockIdx.z): each half recomputes the same scores and softmax and
+  // accumulates its own columns, so both halves' outputs are those of one pass over all columns; half 0 writes LSE
+  if (p.dv_half) {
+    p.v += blockIdx.z * p.dv_half;
+    p.out += blockIdx.z * p.dv_half;
+    if (blockIdx.z) p.lse = nullptr;
+  }
   // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs (flat id f runs on XCD f % 8); work item
   // w = bg * tiles + tile goes to XCD (w's range), so the slot tiles of one (batch, KV group) share an L2 for the
   // K/V they all stream. A bijection of [0, tiles * B G). Causal with the queries' own triangle at least half of
@@ -406,6 +414,16 @@ void launch_wide(const WideArgs& a, dim3 grid, hipStream_t st) {
   wide_attn_kernel<DKP, DV, NBUF, OCC><<<grid, dim3(kThreads), 0, st>>>(a);
 }
 
+// DV = 256 with DK > 128 runs as two DV = 128 halves (grid.z = 2): the 256-column accumulators next to the
+// 256-dim query fragments and the block staging registers spill (121 VGPRs, ~100 scratch accesses per 64-key block,
+// 4x slower), the halves do not; each half repeats the score MFMAs, 1.5x the FLOPs of one pass.
+template <int DKP>
+void launch_wide_halves(WideArgs a, dim3 grid, hipStream_t st) {
+  a.dv_half = 128;
+  grid.z = 2;
+  launch_wide<DKP, 128>(a, grid, st);
+}
+
 }  // namespace
 
 extern "C" int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* k, int64_t skb,
@@ -429,7 +447,7 @@ extern "C" int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t
   const int64_t tiles = (T * rep + kSlotsPerTile - 1) / kSlotsPerTile;
   if (tiles > 0x7fffffff || B * G > 65535 || T * rep > 0x7fffffff || S > 0x7fffffff - kBK) return OD_ERR_SHAPE;
   WideArgs a{q, k, v, kvalid, out, lse, sqb, sqh, sqt, skb, skg, sks, svb, svg, svs, sob, soh, sot, smb,
-             (int)H, (int)G, (int)T, (int)S, (int)DK, (int)rep, causal ? 1 : 0, scale * 1.4426950408889634f};
+             (int)H, (int)G, (int)T, (int)S, (int)DK, (int)rep, causal ? 1 : 0, scale * 1.4426950408889634f, 0};
   dim3 grid((unsigned)tiles, (unsigned)(B * G));
   hipStream_t st = (hipStream_t)stream;
   const int dkp = DK <= 64 ? 64 : DK <= 128 ? 128 : DK <= 256 ? 256 : 512;
@@ -437,6 +455,7 @@ extern "C" int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t
     constexpr int DKP = decltype(DKc)::value;
     if (DV == 64) launch_wide<DKP, 64>(a, grid, st);
     else if (DV == 128) launch_wide<DKP, 128>(a, grid, st);
+    else if (DKP > 128) launch_wide_halves<DKP>(a, grid, st);
     else launch_wide<DKP, 256>(a, grid, st);
   };
   if (dkp == 64) by_dv(std::integral_constant<int, 64>{});

@@ -45,6 +45,15 @@ class DecoderConfig:
     lin_k_dim: int = 128
     lin_v_dim: int = 128
     conv_kernel: int = 4
+    # Qwen3.5's attention geometry (transformers' Qwen3_5TextConfig / Qwen3_5Attention): rotary embedding on the first
+    # rot_dim dims of each head (partial_rotary_factor 0.25 of head_dim 256; 0 = the whole head), and every RMSNorm of
+    # the decoder (input / post-attention / q / k / final) zero-centred: Qwen3_5RMSNorm's (x * r) * (1 + w).
+    rot_dim: int = 0
+    norm_offset: bool = False
+
+    @property
+    def rotary_dims(self) -> int:
+        return self.rot_dim or self.head_dim
 
     @property
     def qkv_out(self) -> int:
@@ -73,9 +82,9 @@ class DecoderConfig:
 
 
 def rope_tables(cfg: DecoderConfig, n_pos: int):
-    """cos/sin bf16 tables [n_pos, D/2]: inv_freq = 1 / theta^(2i/D), angle = pos * inv_freq in fp32 (computed on
-    the host, as the rotary-embedding module of the backbone does)."""
-    D = cfg.head_dim
+    """cos/sin bf16 tables [n_pos, R/2] over the R = cfg.rotary_dims rotated dims: inv_freq = 1 / theta^(2i/R),
+    angle = pos * inv_freq in fp32 (computed on the host, as the rotary-embedding module of the backbone does)."""
+    D = cfg.rotary_dims
     inv_freq = 1.0 / (cfg.theta ** (torch.arange(0, D, 2, dtype=torch.int64).float() / D))
     ang = torch.arange(n_pos, dtype=torch.float32)[:, None] * inv_freq[None, :]
     return ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
@@ -105,8 +114,8 @@ def random_layer_weights(cfg: DecoderConfig, g: torch.Generator, device, smooth:
     def lin(n, k):
         return (torch.randn(n, k, generator=g, device=device) * 0.02).to(bf)
 
-    def norm(n):
-        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
+    def norm(n):  # near 1 as applied: 1 + w with the zero-centred weights
+        return ((0.0 if cfg.norm_offset else 1.0) + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
 
     def sm(n):
         return (torch.rand(n, generator=g, device=device) * 1.5 + 0.5) if smooth else None
@@ -126,8 +135,8 @@ def random_gdn_layer_weights(cfg: DecoderConfig, g: torch.Generator, device, smo
     def lin(n, k):
         return (torch.randn(n, k, generator=g, device=device) * 0.02).to(bf)
 
-    def norm(n):
-        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
+    def norm(n):  # near 1 as applied: 1 + w with the zero-centred weights
+        return ((0.0 if cfg.norm_offset else 1.0) + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
 
     def sm(n):
         return (torch.rand(n, generator=g, device=device) * 1.5 + 0.5) if smooth else None
@@ -146,7 +155,8 @@ def random_decoder(cfg: DecoderConfig, seed: int = 0, device="cuda", max_pos: in
     layer at a time). The embedding is random bf16 (vocab x hidden)."""
     g = torch.Generator(device=device).manual_seed(seed)
     H = cfg.hidden
-    head = {"final_norm": (1.0 + 0.1 * torch.randn(H, generator=g, device=device)).to(torch.bfloat16),
+    head = {"final_norm": ((0.0 if cfg.norm_offset else 1.0) + 0.1 * torch.randn(H, generator=g, device=device)
+                           ).to(torch.bfloat16),
             "head": torch.randn(H, generator=g, device=device) / H ** 0.5,
             "none_logit": torch.zeros((), device=device), "layers": []}
     dec = DenseDecoder(cfg, head, None, device, max_pos)
@@ -288,15 +298,17 @@ class DenseDecoder:
         """RMSNorm + quantize, W8A8 QKV GEMM, q/k norm + RoPE (in place): the layer's qkv (M, qkv_out) bf16.
         append = (B, S, K cache, V cache): the same pass also appends the tokens' int8 K/V to the caches."""
         cfg, L = self.cfg, self.layers[li]
-        kernels.rmsnorm_quant(h, L["ln1"], cfg.eps, L["qkv"].inv_s, ws["xq"][:, :cfg.hidden], ws["sx"])
+        kernels.rmsnorm_quant(h, L["ln1"], cfg.eps, L["qkv"].inv_s, ws["xq"][:, :cfg.hidden], ws["sx"],
+                              offset=cfg.norm_offset)
         qkv = kernels.w8a8_gemm(ws["xq"][:, :cfg.hidden], ws["sx"], L["qkv"].q, L["qkv"].scale, out=ws["qkv"])
         if append is None:
             kernels.qk_norm_rope(qkv, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, L["q_norm"], L["k_norm"], self.cos,
-                                 self.sin, pos, cfg.eps)
+                                 self.sin, pos, cfg.eps, cfg.rotary_dims, cfg.norm_offset)
         else:
             B, S, cache_k, cache_v = append
             kernels.qk_norm_rope_kv_append(qkv, B, S, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, L["q_norm"],
-                                           L["k_norm"], self.cos, self.sin, pos, cfg.eps, cache_k, cache_v)
+                                           L["k_norm"], self.cos, self.sin, pos, cfg.eps, cache_k, cache_v,
+                                           cfg.rotary_dims, cfg.norm_offset)
         return qkv
 
     def _heads(self, qkv: torch.Tensor, ws: dict, R: int, t: int):
@@ -328,7 +340,7 @@ class DenseDecoder:
         epilogue, quantize, down GEMM + residual (into h)."""
         cfg, L = self.cfg, self.layers[li]
         xq, sx = ws["xq"], ws["sx"]
-        kernels.rmsnorm_quant(h_out, L["ln2"], cfg.eps, L["gu"].inv_s, xq[:, :cfg.hidden], sx)
+        kernels.rmsnorm_quant(h_out, L["ln2"], cfg.eps, L["gu"].inv_s, xq[:, :cfg.hidden], sx, offset=cfg.norm_offset)
         hm = kernels.w8a8_gemm_swiglu(xq[:, :cfg.hidden], sx, L["gu"].q, L["gu"].scale, out=ws["hmlp"])
         kernels.act_quant(hm, L["down"].inv_s, xq=xq[:, :cfg.ffn], sx=sx)
         kernels.w8a8_gemm(xq[:, :cfg.ffn], sx, L["down"].q, L["down"].scale, residual=h_out, out=h)
@@ -352,7 +364,7 @@ class DenseDecoder:
         H, nk, nv, dk, dv = cfg.hidden, cfg.lin_k_heads, cfg.lin_v_heads, cfg.lin_k_dim, cfg.lin_v_dim
         M = S * L
         xq, sx = ws["xq"], ws["sx"]
-        kernels.rmsnorm_quant(h, Ly["ln1"], cfg.eps, Ly["win"].inv_s, xq[:, :H], sx)
+        kernels.rmsnorm_quant(h, Ly["ln1"], cfg.eps, Ly["win"].inv_s, xq[:, :H], sx, offset=cfg.norm_offset)
         proj = kernels.w8a8_gemm(xq[:, :H], sx, Ly["win"].q, Ly["win"].scale, out=ws["proj"])
         bufs = (ws["gqk"], ws["gv"], ws["gg"], ws["gbeta"])
         if prefill:
@@ -577,11 +589,14 @@ class DenseDecoder:
         appended,
         divided by the decision temperature (softmax(logits / T), decider.py:255-257), log-softmax per request:
         (B, n_opt + 1) fp32. The RMSNorm factor is the correctly rounded one (a float64 mean of squares, as
-        od_rmsnorm_quant computes it)."""
+        od_rmsnorm_quant computes it); with cfg.norm_offset the zero-centred norm bf16((h * r) * (1 + w))."""
         hf = h.float()
         hd = hf.double()
         r = (1.0 / torch.sqrt((hd * hd).sum(-1, keepdim=True) / hd.shape[-1] + self._eps32)).float()
-        hn = (self.final_norm * (hf * r).to(torch.bfloat16)).float()
+        if self.cfg.norm_offset:
+            hn = ((hf * r) * (1.0 + self.final_norm.float())).to(torch.bfloat16).float()
+        else:
+            hn = (self.final_norm * (hf * r).to(torch.bfloat16)).float()
         hn = hn.view(B, n_opt, t, -1)
         pooled = (hn if pool_last is None else hn[:, :, t - pool_last:]).mean(2)
         logits = torch.cat([pooled @ self.head, self.none_logit.expand(B, 1)], 1)

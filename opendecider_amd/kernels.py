@@ -114,9 +114,10 @@ def gate_act_quant(x: torch.Tensor, gate: torch.Tensor, inv_s: torch.Tensor | No
     return xq, sx
 
 
-def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float, inv_s=None, xq=None, sx=None):
-    """RMSNorm (bf16(w * bf16(x * rsqrt(mean x^2 + eps)))) -> optional SmoothQuant scale -> per-row int8.
-    x (M, K) bf16 with contiguous rows. Returns (xq, sx)."""
+def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float, inv_s=None, xq=None, sx=None, offset: bool = False):
+    """RMSNorm (bf16(w * bf16(x * rsqrt(mean x^2 + eps))), or with offset Qwen3.5's zero-centred
+    bf16((x * r) * (1 + w))) -> optional SmoothQuant scale -> per-row int8. x (M, K) bf16 with contiguous rows.
+    Returns (xq, sx)."""
     require_gpu(x, w, inv_s, xq, sx, name="rmsnorm_quant")
     _lib.bf16_bits(x)
     M, K = x.shape
@@ -124,8 +125,8 @@ def rmsnorm_quant(x: torch.Tensor, w: torch.Tensor, eps: float, inv_s=None, xq=N
         x = x.contiguous()
     xq, sx = _quant_outputs(M, K, None, x.device, xq, sx)
     w, inv_s = _vec(w, K, "w"), _vec(inv_s, K, "inv_s")
-    check(lib().od_rmsnorm_quant(ptr(x), x.stride(0), ptr(w), ptr(inv_s), float(eps), ptr(xq), xq.stride(0), ptr(sx),
-                                 M, K, stream_of(x)), "od_rmsnorm_quant")
+    check(lib().od_rmsnorm_quant_ex(ptr(x), x.stride(0), ptr(w), ptr(inv_s), float(eps), int(bool(offset)), ptr(xq),
+                                    xq.stride(0), ptr(sx), M, K, stream_of(x)), "od_rmsnorm_quant_ex")
     return xq, sx
 
 
@@ -144,29 +145,39 @@ def silu_mul_quant(gu: torch.Tensor, F: int, inv_s=None, xq=None, sx=None):
     return xq, sx
 
 
+def _rope_tables_ok(cos_t, sin_t, D: int, rot_dim: int, name: str) -> None:
+    if rot_dim not in (D, D // 4):
+        raise ValueError(f"{name}: rot_dim must be the head dim ({D}) or a quarter of it, got {rot_dim}")
+    if cos_t.shape != sin_t.shape or cos_t.shape[1] != rot_dim // 2 or not (cos_t.is_contiguous() and
+                                                                            sin_t.is_contiguous()):
+        raise ValueError(f"{name}: cos/sin tables must be contiguous [positions, rot_dim/2]")
+
+
 def qk_norm_rope(qkv: torch.Tensor, n_heads_q: int, n_heads_k: int, D: int, q_w, k_w, cos_t, sin_t, pos,
-                 eps: float) -> None:
-    """In place on qkv (M, >= (Hq + Hk) D): per-head RMSNorm of the q and k heads, then rotary embedding with the
-    bf16 cos/sin tables [positions, D/2] at positions pos (M,) int32."""
+                 eps: float, rot_dim: int | None = None, offset: bool = False) -> None:
+    """In place on qkv (M, >= (Hq + Hk) D): per-head RMSNorm of the q and k heads (offset: Qwen3.5's zero-centred
+    weights), then rotary embedding on the first rot_dim dims (default D; D / 4 is Qwen3.5's partial rotary) with
+    the bf16 cos/sin tables [positions, rot_dim/2] at positions pos (M,) int32."""
     require_gpu(qkv, q_w, k_w, cos_t, sin_t, pos, name="qk_norm_rope")
     _lib.bf16_bits(qkv)
     M = qkv.shape[0]
+    rot_dim = D if rot_dim is None else rot_dim
     if qkv.stride(1) != 1:
         raise ValueError("qk_norm_rope: qkv must have contiguous rows")
     q_w, k_w = _vec(q_w, D, "q_w"), _vec(k_w, D, "k_w")
-    if cos_t.shape != sin_t.shape or cos_t.shape[1] != D // 2 or not (cos_t.is_contiguous() and sin_t.is_contiguous()):
-        raise ValueError("qk_norm_rope: cos/sin tables must be contiguous [positions, D/2]")
+    _rope_tables_ok(cos_t, sin_t, D, rot_dim, "qk_norm_rope")
     if pos.dtype != torch.int32 or pos.numel() != M:
         raise ValueError("qk_norm_rope: pos must be int32 (M,)")
     pos = pos.contiguous()  # held across the call
-    check(lib().od_qk_norm_rope(ptr(qkv), qkv.stride(0), M, n_heads_q, n_heads_k, D, ptr(q_w), ptr(k_w),
-                                ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos), float(eps),
-                                stream_of(qkv)),
-          "od_qk_norm_rope")
+    check(lib().od_qk_norm_rope_ex(ptr(qkv), qkv.stride(0), M, n_heads_q, n_heads_k, D, rot_dim, int(bool(offset)),
+                                   ptr(q_w), ptr(k_w), ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos), float(eps),
+                                   stream_of(qkv)),
+          "od_qk_norm_rope_ex")
 
 
 def qk_norm_rope_kv_append(qkv: torch.Tensor, B: int, S: int, n_heads_q: int, n_heads_k: int, D: int, q_w, k_w,
-                           cos_t, sin_t, pos, eps: float, k_cache, v_cache) -> None:
+                           cos_t, sin_t, pos, eps: float, k_cache, v_cache, rot_dim: int | None = None,
+                           offset: bool = False) -> None:
     """qk_norm_rope on qkv (B S, >= (Hq + 2 Hk) D), then the new tokens' key heads (after RoPE) and value heads
     quantized per (token, head) and written at positions length .. length + S - 1 of the Int8KVCache pair, in one
     pass (the bytes kv_quant_append writes for the same bf16 K/V). The caches' lengths are advanced."""
@@ -175,8 +186,8 @@ def qk_norm_rope_kv_append(qkv: torch.Tensor, B: int, S: int, n_heads_q: int, n_
     if qkv.stride(1) != 1 or qkv.shape[0] != B * S:
         raise ValueError("qk_norm_rope_kv_append: qkv must be (B S, ...) with contiguous rows")
     q_w, k_w = _vec(q_w, D, "q_w"), _vec(k_w, D, "k_w")
-    if cos_t.shape != sin_t.shape or cos_t.shape[1] != D // 2 or not (cos_t.is_contiguous() and sin_t.is_contiguous()):
-        raise ValueError("qk_norm_rope_kv_append: cos/sin tables must be contiguous [positions, D/2]")
+    rot_dim = D if rot_dim is None else rot_dim
+    _rope_tables_ok(cos_t, sin_t, D, rot_dim, "qk_norm_rope_kv_append")
     if pos.dtype != torch.int32 or pos.numel() != B * S:
         raise ValueError("qk_norm_rope_kv_append: pos must be int32 (B S,)")
     pos = pos.contiguous()  # held across the call
@@ -186,11 +197,11 @@ def qk_norm_rope_kv_append(qkv: torch.Tensor, B: int, S: int, n_heads_q: int, n_
         raise ValueError("qk_norm_rope_kv_append: K/V caches must match (B, Hkv, cap, D) at the same length")
     if n0 + S > k_cache.capacity:
         raise ValueError(f"qk_norm_rope_kv_append: {n0} + {S} tokens exceed the capacity {k_cache.capacity}")
-    check(lib().od_qk_norm_rope_kv_append(ptr(qkv), qkv.stride(0), B, S, n_heads_q, n_heads_k, D, ptr(q_w), ptr(k_w),
-                                          ptr(cos_t), ptr(sin_t), cos_t.shape[0], ptr(pos), float(eps),
-                                          ptr(k_cache.q), ptr(k_cache.scale), ptr(v_cache.q), ptr(v_cache.scale),
-                                          k_cache.capacity, n0, stream_of(qkv)),
-          "od_qk_norm_rope_kv_append")
+    check(lib().od_qk_norm_rope_kv_append_ex(ptr(qkv), qkv.stride(0), B, S, n_heads_q, n_heads_k, D, rot_dim,
+                                             int(bool(offset)), ptr(q_w), ptr(k_w), ptr(cos_t), ptr(sin_t),
+                                             cos_t.shape[0], ptr(pos), float(eps), ptr(k_cache.q), ptr(k_cache.scale),
+                                             ptr(v_cache.q), ptr(v_cache.scale), k_cache.capacity, n0, stream_of(qkv)),
+          "od_qk_norm_rope_kv_append_ex")
     k_cache.length += S
     v_cache.length += S
     for c in (k_cache, v_cache):

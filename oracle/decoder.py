@@ -41,6 +41,16 @@ class DecoderConfig:
     lin_k_dim: int = 128
     lin_v_dim: int = 128
     conv_kernel: int = 4
+    # Qwen3.5's attention geometry (transformers' Qwen3_5TextConfig / Qwen3_5Attention): rotary embedding on the first
+    # rot_dim dims of each head only (partial_rotary_factor 0.25 of head_dim 256; 0 = the whole head), and every
+    # RMSNorm of the decoder (input / post-attention / q / k / final) zero-centred, Qwen3_5RMSNorm's
+    # (x * r) * (1 + w), instead of w * bf16(x * r).
+    rot_dim: int = 0
+    norm_offset: bool = False
+
+    @property
+    def rotary_dims(self) -> int:
+        return self.rot_dim or self.head_dim
 
     @property
     def qkv_out(self) -> int:
@@ -67,8 +77,8 @@ def make_weights(cfg: DecoderConfig, seed: int = 0, device="cpu", layers: int | 
     def lin(n, k):
         return (torch.randn(n, k, generator=g, device=device) * 0.02).to(bf)
 
-    def norm(n):
-        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
+    def norm(n):  # near 1 as applied: 1 + w with the zero-centred weights
+        return ((0.0 if cfg.norm_offset else 1.0) + 0.1 * torch.randn(n, generator=g, device=device)).to(bf)
 
     def sm(n):
         return (torch.rand(n, generator=g, device=device) * 1.5 + 0.5) if smooth else None
@@ -107,8 +117,9 @@ def quantize_linear(w: torch.Tensor, s: torch.Tensor | None):
 
 
 def rope_tables(cfg: DecoderConfig, n_pos: int):
-    """cos/sin bf16 tables [n_pos, D/2]: inv_freq = 1 / theta^(2i/D), angle = pos * inv_freq in fp32."""
-    D = cfg.head_dim
+    """cos/sin bf16 tables [n_pos, R/2] over the R = cfg.rotary_dims rotated dims: inv_freq = 1 / theta^(2i/R), angle
+    = pos * inv_freq in fp32 (transformers' default rope parameters take dim = head_dim * partial_rotary_factor)."""
+    D = cfg.rotary_dims
     inv_freq = 1.0 / (cfg.theta ** (torch.arange(0, D, 2, dtype=torch.int64).float() / D))
     ang = torch.arange(n_pos, dtype=torch.float32)[:, None] * inv_freq[None, :]
     return ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
@@ -126,26 +137,35 @@ def rms_factor(x: torch.Tensor, eps: float) -> torch.Tensor:
     return (1.0 / torch.sqrt(ms + eps32)).float()
 
 
-def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, offset: bool = False) -> torch.Tensor:
     """w * bf16(x * r) in bf16 (the HF RMSNorm arithmetic: x * r in fp32, rounded to bf16, times the bf16 weight,
-    rounded again), r = rms_factor(x)."""
+    rounded again), r = rms_factor(x). offset: Qwen3.5's zero-centred norm (transformers' Qwen3_5RMSNorm.forward:
+    output = norm(x.float()) * (1.0 + weight.float()), then .type_as(x)): (x * r) * (1 + w) with the sum and both
+    products in fp32, rounded once to bf16."""
     xf = x.float()
+    if offset:
+        return ((xf * rms_factor(xf, eps)) * (1.0 + w.float())).to(torch.bfloat16)
     return w * (xf * rms_factor(xf, eps)).to(torch.bfloat16)
 
 
 def qk_norm_rope(qkv: torch.Tensor, cfg: DecoderConfig, q_w, k_w, cos, sin, pos) -> torch.Tensor:
-    """Per-head RMSNorm of the q and k heads of qkv (M, qkv_out), then rotate_half RoPE; v untouched."""
+    """Per-head RMSNorm of the q and k heads of qkv (M, qkv_out) (zero-centred with cfg.norm_offset), then
+    rotate_half RoPE on the first R = cfg.rotary_dims dims of each head, the other D - R passing through (transformers'
+    apply_rotary_pos_emb for a table narrower than the head: q_embed = cat((q_rot * cos) + (rotate_half(q_rot) *
+    sin), q_pass)); v untouched."""
     M = qkv.shape[0]
     D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
-    L = D // 2
+    R = cfg.rotary_dims
+    L = R // 2
     out = qkv.clone()
-    c = cos[pos].repeat(1, 2)[:, None, :]            # (M, 1, D), halves shared
+    c = cos[pos].repeat(1, 2)[:, None, :]            # (M, 1, R), halves shared
     s = sin[pos].repeat(1, 2)[:, None, :]
     for lo, nh, w in ((0, Hq, q_w), (Hq * D, Hk, k_w)):
         x = qkv[:, lo:lo + nh * D].reshape(M, nh, D)
-        n = rmsnorm(x, w, cfg.eps)
-        rot = torch.cat([-n[..., L:], n[..., :L]], -1)
-        out[:, lo:lo + nh * D] = ((n * c) + (rot * s)).reshape(M, nh * D)
+        n = rmsnorm(x, w, cfg.eps, cfg.norm_offset)
+        nr = n[..., :R]
+        rot = torch.cat([-nr[..., L:], nr[..., :L]], -1)
+        out[:, lo:lo + nh * D] = torch.cat([(nr * c) + (rot * s), n[..., R:]], -1).reshape(M, nh * D)
     return out
 
 
@@ -194,7 +214,7 @@ def _layer_tail(h, attn, qlin, lw, cfg: DecoderConfig, o_proj: str = "wo"):
     (each linear W8A8 with its fused activation quantizer)."""
     q, sw, inv = qlin[o_proj]
     h, _, _, _ = oq.w8a8_linear(attn, q, sw, inv_s=inv, residual=h)
-    x = rmsnorm(h, lw["ln2"], cfg.eps)
+    x = rmsnorm(h, lw["ln2"], cfg.eps, cfg.norm_offset)
     q, sw, inv = qlin["wgu"]
     gu, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
     a = swiglu(gu, cfg.ffn)
@@ -215,7 +235,7 @@ def layer_forward(h, lw, qlin, cfg: DecoderConfig, state_k, state_v, R: int, t: 
     bf16 after q/k norm + RoPE (the question pass's capture, prefix_attn.py:92-93). two_level: (Kq2, Vq2, qmask,
     row_group, group_state) to attend the two-level prefix instead (prefix_attn.py:94-99). Returns the new h."""
     D, Hq, Hk = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
-    x = rmsnorm(h, lw["ln1"], cfg.eps)
+    x = rmsnorm(h, lw["ln1"], cfg.eps, cfg.norm_offset)
     q, sw, inv = qlin["wqkv"]
     qkv, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
     qkv, gate = split_qkv(qkv, cfg)
@@ -263,7 +283,7 @@ def prefill_forward(ids, weights, embed, cfg: DecoderConfig, state_kv=None, n0: 
             h, conv, rec = gdn_layer_forward(h, lw, qlin, cfg, B, S, conv, rec, None, gdn_dtype)
             out_kv.append((conv, rec))
             continue
-        x = rmsnorm(h, lw["ln1"], cfg.eps)
+        x = rmsnorm(h, lw["ln1"], cfg.eps, cfg.norm_offset)
         q, sw, inv = qlin["wqkv"]
         qkv, _, _, _ = oq.w8a8_linear(x, q, sw, inv_s=inv)
         qkv, gate = split_qkv(qkv, cfg)
@@ -305,7 +325,7 @@ def gdn_layer_forward(h, lw, qlin, cfg: DecoderConfig, S: int, L: int, conv_stat
     states: fresh sequences), out_proj + residual, then the MLP as in an attention layer. Returns (h, new conv states
     (S, 3, C), new recurrent states (S, n_v, dk, dv) fp32)."""
     from .gdn import gdn_mixer
-    x = rmsnorm(h, lw["ln1"], cfg.eps)
+    x = rmsnorm(h, lw["ln1"], cfg.eps, cfg.norm_offset)
     out, conv, rec = gdn_mixer(x, lw, qlin, cfg.gdn, S, L, conv_state, rec_state, seq_state, dtype)
     return _layer_tail(h, out, qlin, lw, cfg, "wout"), conv, rec
 
@@ -316,7 +336,7 @@ def readout(h, final_norm, head, none_logit, cfg: DecoderConfig, B: int, n_opt: 
     own tokens of a row that also carries its question), one logit per row (pooled . head), append the 'none' logit,
     divide by the decision temperature (the reference's softmax(logits / T), decider.py:255-257) and log-softmax per
     request. Returns (B, n_opt + 1) fp32 log-probabilities."""
-    hf = rmsnorm(h, final_norm, cfg.eps).float().reshape(B, n_opt, t, -1)
+    hf = rmsnorm(h, final_norm, cfg.eps, cfg.norm_offset).float().reshape(B, n_opt, t, -1)
     hf = (hf if pool_last is None else hf[:, :, t - pool_last:]).mean(2)
     logits = hf @ head.float()
     logits = torch.cat([logits, none_logit.float().expand(B, 1)], 1)

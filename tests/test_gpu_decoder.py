@@ -35,15 +35,19 @@ def _exact_quant(xq, sx, rq, rs, what=""):
     assert d.max().item() == 0, (what, d.max().item(), (d > 0).float().mean().item())
 
 
-@pytest.mark.parametrize("M,K,smooth", [(7, 4096, False), (33, 4096, True), (5, 200, True)])
-def test_rmsnorm_quant(gpu_lib, M, K, smooth):
+@pytest.mark.parametrize("M,K,smooth,offset", [(7, 4096, False, False), (33, 4096, True, False), (5, 200, True, False),
+                                              (7, 4096, False, True), (33, 4096, True, True), (5, 200, True, True),
+                                              (9, 2048, True, True), (3, 8192, False, True)])
+def test_rmsnorm_quant(gpu_lib, M, K, smooth, offset):
+    """Both weight conventions (offset: Qwen3.5's zero-centred (x * r) * (1 + w)), the vector kernels (K = 2048,
+    4096, 8192) and the general one (K = 200)."""
     from opendecider_amd import kernels
     g = torch.Generator().manual_seed(M + K)
     x = (torch.randn(M, K, generator=g) * 2).to(torch.bfloat16)
-    w = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    w = ((0.0 if offset else 1.0) + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
     inv = (1 / (torch.rand(K, generator=g) * 1.5 + 0.5)).to(torch.bfloat16) if smooth else None
-    xq, sx = kernels.rmsnorm_quant(x.to(DEV), w.to(DEV), 1e-6, None if inv is None else inv.to(DEV))
-    rq, rs = oq.act_quant(od.rmsnorm(x, w, 1e-6), inv)
+    xq, sx = kernels.rmsnorm_quant(x.to(DEV), w.to(DEV), 1e-6, None if inv is None else inv.to(DEV), offset=offset)
+    rq, rs = oq.act_quant(od.rmsnorm(x, w, 1e-6, offset), inv)
     _exact_quant(xq, sx, rq, rs, "rmsnorm_quant")
 
 
@@ -85,27 +89,34 @@ def test_silu_all_bf16_inputs(gpu_lib):
     assert not bad.any(), (gv[bad][:8], got[bad][:8], ref[bad][:8])
 
 
-@pytest.mark.parametrize("D", [128, 64])
-def test_qk_norm_rope(gpu_lib, D):
+@pytest.mark.parametrize("D,rot,offset", [(128, 128, False), (64, 64, False), (256, 256, False), (256, 64, True),
+                                          (256, 64, False), (128, 32, True), (64, 64, True)])
+def test_qk_norm_rope(gpu_lib, D, rot, offset):
+    """Head dims 64 / 128 / 256, full and partial rotary (rot = D / 4: Qwen3.5's 64 of 256), both norm weight
+    conventions: bit-exact, v untouched."""
     from opendecider_amd import kernels
-    cfg = od.DecoderConfig(hidden=8 * D, n_heads=8, n_kv_heads=2, head_dim=D)
-    g = torch.Generator().manual_seed(D)
+    cfg = od.DecoderConfig(hidden=8 * D, n_heads=8, n_kv_heads=2, head_dim=D, rot_dim=rot, norm_offset=offset)
+    g = torch.Generator().manual_seed(D + rot)
     M = 37
     qkv = (torch.randn(M, cfg.qkv_out, generator=g) * 2).to(torch.bfloat16)
-    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
-    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    qw = ((0.0 if offset else 1.0) + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kw = ((0.0 if offset else 1.0) + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
     pos = torch.randint(0, 40000, (M,), generator=g)
     cos, sin = od.rope_tables(cfg, 40000)
+    assert cos.shape == (40000, rot // 2)
     ref = od.qk_norm_rope(qkv, cfg, qw, kw, cos, sin, pos)
     x = qkv.to(DEV)
+    print(f"qk_norm_rope D={D} rot={rot} offset={offset}", flush=True)
     kernels.qk_norm_rope(x, 8, 2, D, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV), pos.to(DEV, torch.int32),
-                         cfg.eps)
+                         cfg.eps, rot, offset)
     assert torch.equal(x.cpu().view(torch.int16), ref.view(torch.int16))
     assert torch.equal(x.cpu()[:, 10 * D:], qkv[:, 10 * D:])
 
 
-@pytest.mark.parametrize("D,B,S,n0", [(128, 2, 37, 0), (128, 3, 16, 21), (64, 2, 9, 5)])
-def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0):
+@pytest.mark.parametrize("D,B,S,n0,rot,offset", [(128, 2, 37, 0, 128, False), (128, 3, 16, 21, 128, False),
+                                                 (64, 2, 9, 5, 64, False), (256, 2, 19, 7, 64, True),
+                                                 (256, 2, 8, 0, 256, False)])
+def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0, rot, offset):
     """The fused q/k norm + RoPE + int8 K/V append writes exactly what qk_norm_rope followed by two kv_quant_append
     calls write: the same qkv bits, cache bytes and scales, and leaves the cache rows before n0 and after n0 + S
     alone. Then the fused result against the oracle: RoPE within one bf16 step, K/V bytes = the oracle's
@@ -113,11 +124,11 @@ def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0):
     from opendecider_amd import kernels
     from opendecider_amd.kv_cache import Int8KVCache
     Hq, Hk, cap = 8, 2, n0 + S + 7
-    cfg = od.DecoderConfig(hidden=Hq * D, n_heads=Hq, n_kv_heads=Hk, head_dim=D)
+    cfg = od.DecoderConfig(hidden=Hq * D, n_heads=Hq, n_kv_heads=Hk, head_dim=D, rot_dim=rot, norm_offset=offset)
     g = torch.Generator().manual_seed(D + S + n0)
     qkv = (torch.randn(B * S, cfg.qkv_out, generator=g) * 2).to(torch.bfloat16)
-    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
-    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    qw = ((0.0 if offset else 1.0) + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    kw = ((0.0 if offset else 1.0) + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
     pos = (n0 + torch.arange(S, dtype=torch.int32)).repeat(B).to(DEV)
     cos, sin = (t.to(DEV) for t in od.rope_tables(cfg, n0 + S + 8))
     caches = []
@@ -129,9 +140,9 @@ def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0):
             c.length = n0
         caches.append(pair)
     x1, x2 = qkv.to(DEV), qkv.to(DEV)
-    print(f"fused rope+append D={D} B={B} S={S} n0={n0}", flush=True)
-    kernels.qk_norm_rope_kv_append(x1, B, S, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, *caches[0])
-    kernels.qk_norm_rope(x2, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps)
+    print(f"fused rope+append D={D} B={B} S={S} n0={n0} rot={rot} offset={offset}", flush=True)
+    kernels.qk_norm_rope_kv_append(x1, B, S, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, *caches[0], rot, offset)
+    kernels.qk_norm_rope(x2, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, rot, offset)
     k = x2[:, Hq * D:(Hq + Hk) * D].view(B, S, Hk, D).transpose(1, 2)
     v = x2[:, (Hq + Hk) * D:].view(B, S, Hk, D).transpose(1, 2)
     caches[1][0].append(k)
@@ -150,7 +161,7 @@ def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0):
         assert torch.equal(c.q[:, :, n0:n0 + S].cpu().reshape(-1, D), rq)
         assert torch.equal(c.scale[:, :, n0:n0 + S].cpu().reshape(-1), rs.reshape(-1))
     with pytest.raises(ValueError):                      # past the capacity: refused before any write
-        kernels.qk_norm_rope_kv_append(x1, B, S, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, *caches[0])
+        kernels.qk_norm_rope_kv_append(x1, B, S, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, *caches[0], rot, offset)
 
 
 def _gpu_states(states, cap):
@@ -176,6 +187,9 @@ CASES = [
     ("tiny_d64_gated", dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=2, vocab=500,
                             gated=True), 2, 5, 4, 70),
     ("9b_dims_2_layers_gated", dict(n_layers=2, vocab=1000, gated=True), 2, 32, 16, 256),
+    # Qwen3.5's attention geometry: 16 / 4 heads of 256, rotary on 64 dims, zero-centred norms, output gate
+    ("qwen35_attention_2_layers", dict(n_layers=2, vocab=1000, gated=True, n_heads=16, n_kv_heads=4, head_dim=256,
+                                       rot_dim=64, norm_offset=True), 2, 32, 16, 256),
 ]
 
 
@@ -199,8 +213,9 @@ def attention_layer_stages(dec, cfg, w, li, ws, gs_li, states_li, R, t, pos, cos
     dec.layer(li, h, mid, ws, gs_li[0], gs_li[1], R, t, pos.to(DEV, torch.int32), rs, mr)
     qkv_g, attn_g, mid_g, hm_g, out_g = (ws["qkv"].cpu(), ws["attn"].cpu(), mid.cpu(), ws["hmlp"].cpu(), h.cpu())
     # RMSNorm 1 + quantize, then QKV GEMM + q/k norm + RoPE from the GPU's bytes
-    xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["qkv"].inv_s)
-    _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps), ql["wqkv"][2]), f"layer {li}: ln1")
+    xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["qkv"].inv_s, offset=cfg.norm_offset)
+    _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps, cfg.norm_offset), ql["wqkv"][2]),
+                 f"layer {li}: ln1")
     qkv_lin = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wqkv"][0]), sx.cpu(), ql["wqkv"][1])
     qkv_lin, gate = od.split_qkv(qkv_lin, cfg)  # the reference's layout -> q | k | v and the gate
     qkv = od.qk_norm_rope(qkv_lin, cfg, lw["q_norm"], lw["k_norm"], cos, sin, pos)
@@ -222,8 +237,9 @@ def attention_layer_stages(dec, cfg, w, li, ws, gs_li, states_li, R, t, pos, cos
     # RMSNorm 2 + quantize, then the gate+up GEMM with SwiGLU from the GPU's bytes: the oracle's gate+up output
     # is bit-exact to the GEMM epilogue, its SwiGLU uses the host exp (one step on bf16(silu(g)) can become two on
     # h after the product with u), so h is held to two bf16 steps on <= 0.5%
-    xq, sx = kernels.rmsnorm_quant(mid.clone(), L["ln2"], cfg.eps, L["gu"].inv_s)
-    _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps), ql["wgu"][2]), f"layer {li}: ln2")
+    xq, sx = kernels.rmsnorm_quant(mid.clone(), L["ln2"], cfg.eps, L["gu"].inv_s, offset=cfg.norm_offset)
+    _exact_quant(xq, sx, *oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps, cfg.norm_offset), ql["wgu"][2]),
+                 f"layer {li}: ln2")
     gu = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["wgu"][0]), sx.cpu(), ql["wgu"][1])
     hm = od.swiglu(gu, cfg.ffn)
     assert torch.equal(hm_g.view(torch.int16), hm.view(torch.int16)), f"layer {li}: gate+up GEMM + SwiGLU"

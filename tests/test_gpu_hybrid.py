@@ -28,7 +28,13 @@ T_E2E = 24.0
 TINY = dict(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=4, vocab=500,
             full_attention_interval=2, lin_k_heads=2, lin_v_heads=4, gated=True)
 NINE_B = dict(n_layers=4, vocab=1000, full_attention_interval=4, gated=True)   # 3 GDN layers + 1 attention layer
-CASES = [("tiny_hybrid", TINY, 2, 5, 4, 40), ("9b_dims_hybrid_4_layers", NINE_B, 2, 32, 16, 256)]
+# Qwen3.5's own attention geometry (transformers' Qwen3_5TextConfig): 16 / 4 heads of 256, rotary on the first 64
+# dims, zero-centred RMSNorms
+QWEN35 = dict(NINE_B, n_heads=16, n_kv_heads=4, head_dim=256, rot_dim=64, norm_offset=True)
+TINY_QWEN35 = dict(TINY, rot_dim=16, norm_offset=True)
+CASES = [("tiny_hybrid", TINY, 2, 5, 4, 40), ("9b_dims_hybrid_4_layers", NINE_B, 2, 32, 16, 256),
+         ("tiny_hybrid_qwen35_geometry", TINY_QWEN35, 2, 5, 4, 40),
+         ("qwen35_hybrid_4_layers", QWEN35, 2, 32, 16, 256)]
 
 
 def _exact(a, b, what):
@@ -118,8 +124,8 @@ def test_hybrid_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
         proj_g, qk_g, v_g, g_g, b_g, o_g = (ws[k].cpu() for k in ("proj", "gqk", "gv", "gg", "gbeta", "go"))
         mid_g, hm_g, out_g = mid.cpu(), ws["hmlp"].cpu(), h.cpu()
         # ln1 + quantize, in_proj GEMM (the padding rows stay zero)
-        xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["win"].inv_s)
-        rq, rsx = oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps), ql["win"][2])
+        xq, sx = kernels.rmsnorm_quant(h_in_g, L["ln1"], cfg.eps, L["win"].inv_s, offset=cfg.norm_offset)
+        rq, rsx = oq.act_quant(od.rmsnorm(h_in, lw["ln1"], cfg.eps, cfg.norm_offset), ql["win"][2])
         _exact(xq, rq, f"layer {li}: ln1 bytes")
         _exact(sx, rsx.reshape(sx.shape), f"layer {li}: ln1 scales")
         proj = oq.w8a8_epilogue(oq.int_gemm(xq.cpu(), ql["win"][0]), sx.cpu(), ql["win"][1])
@@ -154,8 +160,8 @@ def test_hybrid_layers_stage_by_stage(gpu_lib, name, cfg_kw, B, n_opt, t, T):
         h_mid = oq.w8a8_epilogue(oq.int_gemm(rq, ql["wout"][0]), rsx, ql["wout"][1], residual=h_in)
         _exact(mid_g, h_mid, f"layer {li}: out_proj + residual")
         # the MLP
-        xq, sx = kernels.rmsnorm_quant(mid.clone(), L["ln2"], cfg.eps, L["gu"].inv_s)
-        rq, rsx = oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps), ql["wgu"][2])
+        xq, sx = kernels.rmsnorm_quant(mid.clone(), L["ln2"], cfg.eps, L["gu"].inv_s, offset=cfg.norm_offset)
+        rq, rsx = oq.act_quant(od.rmsnorm(mid_g, lw["ln2"], cfg.eps, cfg.norm_offset), ql["wgu"][2])
         _exact(xq, rq, f"layer {li}: ln2")
         gu = oq.w8a8_epilogue(oq.int_gemm(rq, ql["wgu"][0]), rsx, ql["wgu"][1])
         _exact(hm_g, od.swiglu(gu, cfg.ffn), f"layer {li}: gate+up + SwiGLU")
@@ -192,7 +198,10 @@ def test_hybrid_decision_forward_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, 
 
 @pytest.mark.parametrize("name,cfg_kw,B,n_opt,t,S,records", [("tiny_hybrid", TINY, 2, 5, 4, 37, [24, 2]),
                                                              ("9b_dims_hybrid_4_layers", NINE_B, 2, 32, 16, 256,
-                                                              [64])])
+                                                              [64]),
+                                                             ("tiny_hybrid_qwen35_geometry", TINY_QWEN35, 2, 5, 4, 37,
+                                                              [24, 2]),
+                                                             ("qwen35_hybrid_4_layers", QWEN35, 2, 32, 16, 256, [64])])
 def test_hybrid_prefill_and_score_end_to_end(gpu_lib, name, cfg_kw, B, n_opt, t, S, records):
     """States prefilled from token ids (GDN layers: conv windows and recurrent states written back; attention layers:
     int8 K/V), records appended (GDN layers continue their states), then the option rows scored. Layer 0 (a GDN

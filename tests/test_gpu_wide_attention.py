@@ -10,7 +10,8 @@ output by at most 2^-7 sum_j p_j |v_j| / l. Its natural-log LSE to 1e-4 absolute
 (the LSE sums unrounded p), and to the reference test's own bar (max |out - exact| < 2e-2,
 tests/test_wide_attention.py:38,62) against the exact one. Shapes: the reference test's four (Dk 448/200) with and
 without padding (:19-20), its non-causal LSE case (:47-62), plus the decoder's head width 128 (causal prefill, a
-causal offset S - T, GQA 4) and 64.
+causal offset S - T, GQA 4), 64, and Qwen3.5's 256 (Dk = Dv = 256, which runs as two 128-column halves, as the
+reference's Dv = 256 shapes do).
 """
 import pytest
 import torch
@@ -23,7 +24,9 @@ DEV = "cuda"
 
 SHAPES = [(1, 16, 4, 100, 100, 448, 256), (2, 16, 4, 37, 300, 448, 256), (1, 16, 4, 1, 77, 448, 256),
           (2, 8, 2, 129, 129, 200, 128), (2, 32, 8, 256, 256, 128, 128), (1, 32, 8, 70, 1000, 128, 128),
-          (2, 8, 8, 33, 70, 64, 64), (1, 8, 2, 130, 130, 128, 64), (1, 4, 4, 20, 90, 64, 256)]
+          (2, 8, 8, 33, 70, 64, 64), (1, 8, 2, 130, 130, 128, 64), (1, 4, 4, 20, 90, 64, 256),
+          # Qwen3.5's full-attention heads (16 / 4 x 256): a causal prefill and queries at the end of the keys
+          (2, 16, 4, 300, 300, 256, 256), (1, 16, 4, 64, 500, 256, 256)]
 
 
 def make(seed, B, H, G, T, S, DK, DV, padded):

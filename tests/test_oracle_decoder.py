@@ -23,6 +23,68 @@ def test_rmsnorm_matches_float64_within_bf16_rounding():
     assert torch.equal(od.rmsnorm(c, w, 0.0), (-w.float()).to(torch.bfloat16)[None])
 
 
+def _qwen35_modules():
+    return pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+
+
+def test_zero_centred_rmsnorm_matches_transformers_qwen3_5_rmsnorm():
+    """The offset convention against transformers' Qwen3_5RMSNorm (the norm of the reference's default backbone):
+    with the module's normalisation given the oracle's r, the module's own (1 + w) product and cast give the oracle's
+    bits; with its own fp32 mean / rsqrt it lands within one bf16 step on a few elements. The Llama-style product
+    with 1 + w folded into the weight (w' * bf16(x * r), two roundings) is shown to differ, so the check can tell
+    the conventions apart."""
+    mq = _qwen35_modules()
+    g = torch.Generator().manual_seed(11)
+    K = 256
+    x = (torch.randn(64, K, generator=g) * 3).to(torch.bfloat16)
+    w = (0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    m = mq.Qwen3_5RMSNorm(K, eps=1e-6).to(torch.bfloat16)
+    with torch.no_grad():
+        m.weight.copy_(w)
+    ours = od.rmsnorm(x, w, 1e-6, offset=True)
+    own = m(x)
+    d = (own.view(torch.int16).int() - ours.view(torch.int16).int()).abs()
+    assert d.max().item() <= 1 and (d > 0).float().mean().item() < 0.02
+    m._norm = lambda t: t * od.rms_factor(t, m.eps)     # the module's arithmetic around the oracle's r
+    assert torch.equal(m(x).view(torch.int16), ours.view(torch.int16))
+    folded = od.rmsnorm(x, (1.0 + w.float()).to(torch.bfloat16), 1e-6)
+    assert not torch.equal(folded.view(torch.int16), ours.view(torch.int16))
+
+
+def test_partial_rotary_matches_transformers_qwen3_5():
+    """Qwen3.5's partial rotary (64 of 256 dims) against transformers: the oracle's cos/sin tables equal
+    Qwen3_5TextRotaryEmbedding's (bf16, halves repeated) and qk_norm_rope equals apply_rotary_pos_emb applied to
+    the oracle's zero-centred q/k norms, bit for bit; the 192 unrotated dims keep the normed values."""
+    mq = _qwen35_modules()
+    cfg = od.DecoderConfig(hidden=1024, n_heads=4, n_kv_heads=2, head_dim=256, rot_dim=64, norm_offset=True)
+    tcfg = mq.Qwen3_5TextConfig(head_dim=256, num_attention_heads=4, num_key_value_heads=2, hidden_size=1024,
+                                rope_parameters={"rope_type": "default", "rope_theta": cfg.theta,
+                                                 "partial_rotary_factor": 0.25})
+    pos = torch.tensor([0, 1, 2, 7, 300, 4095, 20000, 32767])
+    M = pos.numel()
+    cos_t, sin_t = mq.Qwen3_5TextRotaryEmbedding(tcfg)(torch.zeros(1, dtype=torch.bfloat16), pos[None])
+    cos, sin = od.rope_tables(cfg, 32768)
+    assert cos.shape == (32768, 32)
+    assert torch.equal(cos_t[0], cos[pos].repeat(1, 2)) and torch.equal(sin_t[0], sin[pos].repeat(1, 2))
+    g = torch.Generator().manual_seed(12)
+    qkv = (torch.randn(M, cfg.qkv_out, generator=g) * 2).to(torch.bfloat16)
+    qw, kw = ((0.1 * torch.randn(256, generator=g)).to(torch.bfloat16) for _ in range(2))
+    out = od.qk_norm_rope(qkv, cfg, qw, kw, cos, sin, pos)
+    D = 256
+    qn = od.rmsnorm(qkv[:, :4 * D].reshape(M, 4, D), qw, cfg.eps, True)
+    kn = od.rmsnorm(qkv[:, 4 * D:6 * D].reshape(M, 2, D), kw, cfg.eps, True)
+    qe, ke = mq.apply_rotary_pos_emb(qn.transpose(0, 1)[None], kn.transpose(0, 1)[None], cos_t, sin_t)
+    assert torch.equal(out[:, :4 * D].view(torch.int16), qe[0].transpose(0, 1).reshape(M, 4 * D).view(torch.int16))
+    assert torch.equal(out[:, 4 * D:6 * D].view(torch.int16),
+                       ke[0].transpose(0, 1).reshape(M, 2 * D).view(torch.int16))
+    assert torch.equal(out[:, :4 * D].reshape(M, 4, D)[..., 64:], qn[..., 64:])
+    assert torch.equal(out[:, 6 * D:], qkv[:, 6 * D:])
+    # a full-head rotation (the dense configs' convention) is a different function on these heads
+    full = od.qk_norm_rope(qkv, od.DecoderConfig(**{**cfg.__dict__, "rot_dim": 0}), qw, kw,
+                           *od.rope_tables(od.DecoderConfig(head_dim=256), 32768), pos)
+    assert not torch.equal(full.view(torch.int16), out.view(torch.int16))
+
+
 def _rope64(x, pos, cfg):
     """Independent float64 RoPE: pairs (x_i, x_{i+D/2}) rotated by pos * theta^(-2i/D) as complex numbers."""
     D = x.shape[-1]
