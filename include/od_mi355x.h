@@ -514,6 +514,18 @@ int od_gdn_prep(const uint16_t* proj, int64_t ldp, const uint16_t* conv_w, const
                 const int32_t* seq_state, int64_t n_states, const uint16_t* A_log, const uint16_t* dt_bias, int64_t S,
                 int64_t L, int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, uint16_t* qk, uint16_t* v, float* g,
                 float* beta, uint16_t* conv_out, od_stream_t stream);
+/*
+ * od_gdn_prep_ex: od_gdn_prep for right-padded sequences, the reference's Backbone.padded_continuation
+ *   (src/opendecider/backbone.py:256-289, used by the batched question pass, v3.py:446-497): seq_len int32 [S] holds
+ *   each sequence's real tokens (NULL: all L; values are clamped into [0, L]). A pad token gets beta = 0 and g = -0,
+ *   what the reference's b = a = -inf give, so the recurrence carries the state through it unchanged; conv_out takes
+ *   the 3 pre-conv inputs of [state ; sequence] that end at the last real token (the state's own window when
+ *   seq_len is 0). Outputs at pad positions are computed from the pad tokens and carry no meaning.
+ */
+int od_gdn_prep_ex(const uint16_t* proj, int64_t ldp, const uint16_t* conv_w, const uint16_t* conv_in,
+                   const int32_t* seq_state, int64_t n_states, const int32_t* seq_len, const uint16_t* A_log,
+                   const uint16_t* dt_bias, int64_t S, int64_t L, int64_t n_k, int64_t n_v, int64_t dk, int64_t dv,
+                   uint16_t* qk, uint16_t* v, float* g, float* beta, uint16_t* conv_out, od_stream_t stream);
 int od_gdn_recurrence(const uint16_t* qk, const uint16_t* v, const float* g, const float* beta, const float* init,
                       const int32_t* seq_state, int64_t n_states, int64_t S, int64_t L, int64_t n_k, int64_t n_v,
                       int64_t dk, int64_t dv, uint16_t* o, float* final_state, od_stream_t stream);

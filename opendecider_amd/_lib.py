@@ -77,6 +77,8 @@ SIGNATURES = {
                            ctypes.c_float, _c_ptr, _i64, _c_ptr],
     "od_gdn_prep": [_c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64,
                     _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
+    "od_gdn_prep_ex": [_c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64,
+                       _i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr],
     "od_gdn_recurrence": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                           _c_ptr, _c_ptr, _c_ptr],
     "od_gdn_norm_quant": [_c_ptr, _i64, _c_ptr, _i64, _c_ptr, _c_ptr, ctypes.c_float, _i64, _i64, _i64, _c_ptr, _i64,

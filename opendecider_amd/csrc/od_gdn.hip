@@ -41,6 +41,7 @@ struct PrepArgs {
   float* g;
   float* beta;
   uint16_t* conv_out;
+  const int32_t* seq_len;  // real tokens of each sequence (NULL: L); the rest are right pads
   int64_t ldp, S, L, n_states;
   int n_k, n_v, dk, dv, C;
 };
@@ -114,6 +115,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
   const int kd = p.n_k * p.dk;
   const int G = p.dk / kChan;  // lanes per head (a power of two <= 64)
   const int tn = (int)min((int64_t)kTok, p.L - t0);
+  // real tokens of the sequence (clamped into [0, L]); tokens at or past it are right pads
+  const int64_t len = p.seq_len ? min(max((int64_t)p.seq_len[s], (int64_t)0), p.L) : p.L;
 
   // row r of full = [state (3 rows) ; the sequence's tokens]: full[r] = state row r (r < 3) or token r - 3
   auto load_full = [&](int64_t r, float (&x)[kChan]) {
@@ -134,6 +137,12 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
       *reinterpret_cast<uint4*>(&wr[4 * i]) = *reinterpret_cast<const uint4*>(p.conv_w + (int64_t)c0 * kConvTaps + 8 * i);
 #pragma unroll
     for (int j = 0; j < kConvTaps - 1; ++j) load_full(t0 + j, win[j]);
+  }
+  // the new conv state is the 3 rows of [state ; tokens] that end at the last real token (rows len .. len + 2):
+  // the window after that token, or, for a sequence with no real token, the state's own window
+  if (p.conv_out && on && len == 0 && t0 == 0) {
+#pragma unroll
+    for (int j = 0; j < kConvTaps - 1; ++j) store16(p.conv_out + (s * (kConvTaps - 1) + j) * p.C + c0, win[j]);
   }
 
   for (int tt = 0; tt < tn; ++tt) {
@@ -156,6 +165,10 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
         win[0][i] = win[1][i];
         win[1][i] = win[2][i];
         win[2][i] = x[i];
+      }
+      if (p.conv_out && t == len - 1) {
+#pragma unroll
+        for (int j = 0; j < kConvTaps - 1; ++j) store16(p.conv_out + (s * (kConvTaps - 1) + j) * p.C + c0, win[j]);
       }
     } else {
 #pragma unroll
@@ -182,10 +195,17 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
     }
   }
 
-  // gates of the tile's tokens (first channel block): thread i takes (token i / n_v, value head i % n_v)
+  // gates of the tile's tokens (first channel block): thread i takes (token i / n_v, value head i % n_v). A right pad
+  // gets beta = 0 and g = -0, what b = a = -inf give (sigmoid(-inf) = 0, softplus(-inf) = 0): the state passes
+  // through it unchanged (e^g = 1, no write)
   for (int i = blockIdx.y == 0 ? tid : tn * p.n_v; i < tn * p.n_v; i += blockDim.x) {
     const int64_t m = m_s + t0 + i / p.n_v;
     const int hh = i % p.n_v;
+    if (t0 + i / p.n_v >= len) {
+      p.beta[m * p.n_v + hh] = 0.0f;
+      p.g[m * p.n_v + hh] = -0.0f;
+      continue;
+    }
     const uint16_t* row = p.proj + m * p.ldp + p.C + (int64_t)p.n_v * p.dv;
     const float b = od_bf16_to_f32(row[hh]), a = od_bf16_to_f32(row[p.n_v + hh]);
     p.beta[m * p.n_v + hh] = od_sigmoid_bf16(b);
@@ -195,13 +215,6 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
     p.g[m * p.n_v + hh] = (float)(-((double)e * (double)sp));
   }
 
-  // the new conv state: the last 3 rows of [state ; tokens], written by the tile holding the last token
-  if (p.conv_out && on && t0 + tn == p.L) {
-    const int64_t keep = kConvTaps - 1;
-    // win holds full rows L, L + 1, L + 2 = the last 3 rows of full (full has L + 3 rows)
-#pragma unroll
-    for (int j = 0; j < kConvTaps - 1; ++j) store16(p.conv_out + (s * keep + j) * p.C + c0, win[j]);
-  }
 }
 
 // ------------------------------------------------------------------------------------------------ recurrence
@@ -505,10 +518,11 @@ bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
 }  // namespace
 
-extern "C" int od_gdn_prep(const uint16_t* proj, int64_t ldp, const uint16_t* conv_w, const uint16_t* conv_in,
-                           const int32_t* seq_state, int64_t n_states, const uint16_t* A_log, const uint16_t* dt_bias,
-                           int64_t S, int64_t L, int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, uint16_t* qk,
-                           uint16_t* v, float* g, float* beta, uint16_t* conv_out, od_stream_t stream) {
+extern "C" int od_gdn_prep_ex(const uint16_t* proj, int64_t ldp, const uint16_t* conv_w, const uint16_t* conv_in,
+                              const int32_t* seq_state, int64_t n_states, const int32_t* seq_len,
+                              const uint16_t* A_log, const uint16_t* dt_bias, int64_t S, int64_t L, int64_t n_k,
+                              int64_t n_v, int64_t dk, int64_t dv, uint16_t* qk, uint16_t* v, float* g, float* beta,
+                              uint16_t* conv_out, od_stream_t stream) {
   if (S < 0 || L < 0 || n_k < 1 || n_v < 1 || dk < 1 || dv < 1 || n_states < 0) return OD_ERR_SHAPE;
   if (S == 0 || L == 0) return OD_OK;
   if (!proj || !conv_w || !A_log || !dt_bias || !qk || !v || !g || !beta) return OD_ERR_NULL;
@@ -521,13 +535,21 @@ extern "C" int od_gdn_prep(const uint16_t* proj, int64_t ldp, const uint16_t* co
       !od_aligned16(qk) || !od_aligned16(v) || (conv_out && !od_aligned16(conv_out)))
     return OD_ERR_ALIGN;
   if (S * L > 0x7fffffffll) return OD_ERR_SHAPE;
-  PrepArgs p{proj, conv_w, conv_in, seq_state, A_log, dt_bias, qk, v, g, beta, conv_out, ldp, S, L, n_states,
-             (int)n_k, (int)n_v, (int)dk, (int)dv, (int)C};
+  PrepArgs p{proj, conv_w, conv_in, seq_state, A_log, dt_bias, qk, v, g, beta, conv_out, seq_len, ldp, S, L,
+             n_states, (int)n_k, (int)n_v, (int)dk, (int)dv, (int)C};
   const int64_t tiles = S * ((L + kTok - 1) / kTok);
   const int64_t cblocks = (C / kChan + kPrepThreads - 1) / kPrepThreads;
   gdn_prep_kernel<<<dim3((unsigned)tiles, (unsigned)cblocks), dim3(min(threads_for(C), kPrepThreads)), 0,
                     (hipStream_t)stream>>>(p);
   return od_launch_status();
+}
+
+extern "C" int od_gdn_prep(const uint16_t* proj, int64_t ldp, const uint16_t* conv_w, const uint16_t* conv_in,
+                           const int32_t* seq_state, int64_t n_states, const uint16_t* A_log, const uint16_t* dt_bias,
+                           int64_t S, int64_t L, int64_t n_k, int64_t n_v, int64_t dk, int64_t dv, uint16_t* qk,
+                           uint16_t* v, float* g, float* beta, uint16_t* conv_out, od_stream_t stream) {
+  return od_gdn_prep_ex(proj, ldp, conv_w, conv_in, seq_state, n_states, nullptr, A_log, dt_bias, S, L, n_k, n_v, dk,
+                        dv, qk, v, g, beta, conv_out, stream);
 }
 
 extern "C" int od_gdn_recurrence(const uint16_t* qk, const uint16_t* v, const float* g, const float* beta,

@@ -16,7 +16,7 @@ forward can be captured in one HIP graph.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -347,7 +347,7 @@ class DenseDecoder:
         return h
 
     def gdn_layer(self, li: int, h: torch.Tensor, h_out: torch.Tensor, ws: dict, st: GDNState, S: int, L: int,
-                  seq_state=None, prefill: bool = False, conv_tmp=None) -> torch.Tensor:
+                  seq_state=None, prefill: bool = False, conv_tmp=None, continue_into=None) -> torch.Tensor:
         """One Gated DeltaNet layer over S sequences of L tokens (Qwen3_5GatedDeltaNet.forward's steps, the token
         mixer of src/opendecider/backbone.py's linear_attention layers):
             od_rmsnorm_quant -> od_w8a8_gemm (in_proj: [qkv | z | b | a]) -> od_gdn_prep (conv + SiLU, l2norm,
@@ -359,7 +359,9 @@ class DenseDecoder:
         terminal, nothing is written back. Prefill (prefill True, S = the states' batch): sequence i continues state
         i (or starts from zeros when st.length is 0) and its new conv window and final recurrent state are written
         back (the conv window through conv_tmp (S, 3, C) when continuing, since other tokens still read the old
-        one)."""
+        one). continue_into = (GDNState of S sequences, seq_len int32 (S,)): the question pass; sequence i continues
+        state seq_state[i] over its seq_len[i] real tokens (right pads leave the state unchanged, the reference's
+        padded continuation, backbone.py:256-289) and its conv window and final state go to that GDNState."""
         cfg, Ly = self.cfg, self.layers[li]
         H, nk, nv, dk, dv = cfg.hidden, cfg.lin_k_heads, cfg.lin_v_heads, cfg.lin_k_dim, cfg.lin_v_dim
         M = S * L
@@ -367,7 +369,13 @@ class DenseDecoder:
         kernels.rmsnorm_quant(h, Ly["ln1"], cfg.eps, Ly["win"].inv_s, xq[:, :H], sx, offset=cfg.norm_offset)
         proj = kernels.w8a8_gemm(xq[:, :H], sx, Ly["win"].q, Ly["win"].scale, out=ws["proj"])
         bufs = (ws["gqk"], ws["gv"], ws["gg"], ws["gbeta"])
-        if prefill:
+        if continue_into is not None:
+            qst, seq_len = continue_into
+            kernels.gdn_prep(proj, Ly["conv_w"], Ly["A_log"], Ly["dt_bias"], S, L, nk, nv, dk, dv, conv_in=st.conv,
+                             seq_state=seq_state, conv_out=qst.conv, out=bufs, seq_len=seq_len)
+            kernels.gdn_recurrence(*bufs, S, L, nk, nv, dk, dv, init=st.rec, seq_state=seq_state, final=qst.rec,
+                                   out=ws["go"])
+        elif prefill:
             fresh = st.length == 0
             conv_out = st.conv[:S] if fresh else conv_tmp
             kernels.gdn_prep(proj, Ly["conv_w"], Ly["A_log"], Ly["dt_bias"], S, L, nk, nv, dk, dv,
@@ -507,10 +515,11 @@ class DenseDecoder:
         state's int8 K/V and themselves causally through every layer (the branched kernel, one row per question), and
         each layer's question K/V (bf16, after q/k norm + RoPE; prefix_attn.py:92-93's capture) are written straight
         into block images (od_attn_stage_bf16, keys past qlen[g] masked): the second prefix level the option rows
-        read. Questions must be grouped by state (group_state non-decreasing)."""
+        read. Questions must be grouped by state (group_state non-decreasing). On a hybrid stack each Gated DeltaNet
+        layer continues question g's state over its qlen[g] real tokens as the reference's batched question pass does
+        (Backbone.padded_continuation, v3.py:494-497: pads leave the recurrent state unchanged, the conv window ends
+        at the last real token) into a per-question state that the option rows then continue."""
         cfg = self.cfg
-        if self.hybrid:
-            raise NotImplementedError("question_pass: the question cache is built for full-attention stacks only")
         G, Lq = ids_q.shape
         gs = [int(s) for s in group_state]
         qlen = [int(n) for n in qlen]
@@ -518,8 +527,8 @@ class DenseDecoder:
             raise ValueError("question_pass: one state per question, questions grouped by state")
         if any(not 1 <= n <= Lq for n in qlen) or Lq > 256:
             raise ValueError("question_pass: 1 <= qlen <= Lq <= 256")
-        T = states[0][0].length
-        Ns = states[0][0].q.shape[0]
+        T = self.state_length(states)
+        Ns = self.state_count(states)
         if T + Lq > self.cos.shape[0]:
             raise ValueError(f"question_pass: positions up to {T + Lq} exceed the rotary tables ({self.cos.shape[0]})")
         if min(gs) < 0 or max(gs) >= Ns:
@@ -531,8 +540,19 @@ class DenseDecoder:
         row_start, max_rows = kernels.row_start_of([gs.count(s) for s in range(Ns)], self.dev)
         qmask = (torch.arange(Lq)[None, :] < torch.tensor(qlen)[:, None]).to(torch.uint8).to(self.dev)
         D = cfg.head_dim
-        images = []
+        images, gdn = [], {}
+        gs_dev = torch.tensor(gs, dtype=torch.int32).to(self.dev)
+        qlen_dev = torch.tensor(qlen, dtype=torch.int32).to(self.dev)
         for li in range(len(self.layers)):
+            if self.layers[li]["gdn"]:
+                src = states[li]
+                qst = GDNState(torch.empty(G, *src.conv.shape[1:], dtype=src.conv.dtype, device=self.dev),
+                               torch.empty(G, *src.rec.shape[1:], dtype=src.rec.dtype, device=self.dev))
+                qst.length = T + Lq
+                self.gdn_layer(li, h, mid, ws, src, G, Lq, seq_state=gs_dev, continue_into=(qst, qlen_dev))
+                images.append(None)
+                gdn[li] = qst
+                continue
             state_k, state_v = states[li]
             qkv = self._attn_in(li, h, ws, pos)
             q, k, v, attn = self._heads(qkv, ws, G, Lq)
@@ -544,19 +564,18 @@ class DenseDecoder:
                                   images=img)
             images.append(kernels.stage_state_bf16(k, v, Lq, D ** -0.5, qmask))
             self._attn_out_mlp(li, h, mid, ws)
-        return QuestionCache(images, Lq, qlen, gs, torch.tensor(gs, dtype=torch.int32).to(self.dev), T)
+        return QuestionCache(images, Lq, qlen, gs, gs_dev, T, gdn)
 
     def score_qcache(self, ids_o: torch.Tensor, qc: "QuestionCache", states) -> torch.Tensor:
         """Option rows over the question cache: ids_o (G, n_opt, t) on the GPU; the rows of question g start right
         after its last real token (position T + qlen[g], v3.py:520) and attend [state group_state[g] ; question g's
-        K/V] and their own tokens (od_branched_attn_staged2). Returns (G, n_opt + 1) log-probabilities."""
+        K/V] and their own tokens (od_branched_attn_staged2); in a Gated DeltaNet layer they continue their
+        question's state from the question pass, read in place. Returns (G, n_opt + 1) log-probabilities."""
         cfg = self.cfg
-        if self.hybrid:
-            raise NotImplementedError("score_qcache: the question cache is built for full-attention stacks only")
         G, n_opt, t = ids_o.shape
         if G != len(qc.qlen):
             raise ValueError("score_qcache: one group of option rows per question")
-        T = states[0][0].length
+        T = self.state_length(states)
         if T != qc.T:
             raise ValueError("score_qcache: the states changed since the question pass")
         R = G * n_opt
@@ -565,14 +584,18 @@ class DenseDecoder:
         key = ("qcache", T, tuple(qc.qlen), n_opt, t)
         if key not in self._rows:
             pos = torch.cat([T + n + torch.arange(t, dtype=torch.int32) for n in qc.qlen for _ in range(n_opt)])
-            self._rows[key] = (pos.to(self.dev), *kernels.row_start_of([n_opt] * G, self.dev))
-        pos, row_start, max_rows = self._rows[key]
+            row_q = torch.arange(G, dtype=torch.int32).repeat_interleave(n_opt)
+            self._rows[key] = (pos.to(self.dev), *kernels.row_start_of([n_opt] * G, self.dev), row_q.to(self.dev))
+        pos, row_start, max_rows, row_q = self._rows[key]
         ws = self.workspace(R * t)
         h, mid = ws["h"]
         h.copy_(self.embed.index_select(0, ids_o.reshape(-1)))
-        Ns = states[0][0].q.shape[0]
+        Ns = self.state_count(states)
         D = cfg.head_dim
         for li in range(len(self.layers)):
+            if self.layers[li]["gdn"]:  # row r continues question r // n_opt's state
+                self.gdn_layer(li, h, mid, ws, qc.gdn[li], R, t, seq_state=row_q)
+                continue
             state_k, state_v = states[li]
             qkv = self._attn_in(li, h, ws, pos)
             q, k, v, attn = self._heads(qkv, ws, R, t)
@@ -681,3 +704,4 @@ class QuestionCache:
     gs: list
     group_state: torch.Tensor
     T: int
+    gdn: dict = field(default_factory=dict)  # a hybrid stack's per-question GDNState of each Gated DeltaNet layer

@@ -792,14 +792,15 @@ def lm_head_logprob_q4(h: torch.Tensor, qs: torch.Tensor, d: torch.Tensor, tok: 
 # ------------------------------------------------------------------------------------------- Gated DeltaNet layers
 def gdn_prep(proj: torch.Tensor, conv_w: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor, S: int, L: int,
              n_k: int, n_v: int, dk: int, dv: int, conv_in=None, seq_state=None, conv_out: bool | torch.Tensor = False,
-             out=None):
+             out=None, seq_len=None):
     """od_gdn_prep: the conv + SiLU, l2norm and gates of a GDN layer. proj (S L, >= proj_out) bf16 with contiguous
     rows ([qkv | z | b | a]); conv_w (C, 4) bf16; A_log, dt_bias (n_v,) bf16; conv_in (n_states, 3, C) bf16 or
     None; seq_state int32 (S,) or None. conv_out: True for a new (S, 3, C) tensor of the new conv states, or a
     contiguous tensor of that shape to write them into (not conv_in's memory: other tokens still read it). out:
     preallocated (qk, v, g, beta). Returns (qk (S L, 2 n_k dk), v (S L, n_v dv), g, beta (S L, n_v) fp32, the new
-    conv states or None)."""
-    require_gpu(proj, conv_w, A_log, dt_bias, conv_in, seq_state, name="gdn_prep")
+    conv states or None). seq_len: int32 (S,) real tokens of right-padded sequences (the reference's padded
+    continuation: pads leave the recurrent state unchanged and the new conv state ends at the last real token)."""
+    require_gpu(proj, conv_w, A_log, dt_bias, conv_in, seq_state, seq_len, name="gdn_prep")
     for t in (proj, conv_w, A_log, dt_bias):
         _lib.bf16_bits(t)
     C = 2 * n_k * dk + n_v * dv
@@ -821,6 +822,10 @@ def gdn_prep(proj: torch.Tensor, conv_w: torch.Tensor, A_log: torch.Tensor, dt_b
         if seq_state.dtype != torch.int32 or seq_state.numel() != S:
             raise ValueError("gdn_prep: seq_state must be int32 (S,)")
         seq_state = seq_state.contiguous()
+    if seq_len is not None:
+        if seq_len.dtype != torch.int32 or seq_len.numel() != S:
+            raise ValueError("gdn_prep: seq_len must be int32 (S,)")
+        seq_len = seq_len.contiguous()
     dev = proj.device
     if out is None:
         qk = torch.empty(M, 2 * n_k * dk, dtype=torch.bfloat16, device=dev)
@@ -845,9 +850,9 @@ def gdn_prep(proj: torch.Tensor, conv_w: torch.Tensor, A_log: torch.Tensor, dt_b
             raise ValueError("gdn_prep: conv_out overlaps conv_in")
     elif conv_out:
         co = torch.empty(S, 3, C, dtype=torch.bfloat16, device=dev)
-    check(lib().od_gdn_prep(ptr(proj), proj.stride(0) if M > 1 else proj.shape[1], ptr(conv_w), ptr(conv_in),
-                            ptr(seq_state), n_states, ptr(A_log), ptr(dt_bias), S, L, n_k, n_v, dk, dv, ptr(qk),
-                            ptr(v), ptr(g), ptr(beta), ptr(co), stream_of(proj)), "od_gdn_prep")
+    check(lib().od_gdn_prep_ex(ptr(proj), proj.stride(0) if M > 1 else proj.shape[1], ptr(conv_w), ptr(conv_in),
+                               ptr(seq_state), n_states, ptr(seq_len), ptr(A_log), ptr(dt_bias), S, L, n_k, n_v, dk,
+                               dv, ptr(qk), ptr(v), ptr(g), ptr(beta), ptr(co), stream_of(proj)), "od_gdn_prep_ex")
     return qk, v, g, beta, co
 
 

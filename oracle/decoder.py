@@ -318,7 +318,7 @@ def quantize_layer(lw):
 
 
 def gdn_layer_forward(h, lw, qlin, cfg: DecoderConfig, S: int, L: int, conv_state=None, rec_state=None,
-                      seq_state=None, dtype=torch.float64):
+                      seq_state=None, dtype=torch.float64, seq_len=None):
     """One Gated DeltaNet layer over S sequences of L tokens (h (S L, hidden) bf16): RMSNorm, the GDN token mixer
     (oracle/gdn.py's gdn_mixer: in_proj, conv + SiLU, l2norm, gates, gated delta rule, gated RMSNorm) continuing
     the states conv_state / rec_state (seq_state: each sequence's state; None: sequence i continues state i; None
@@ -326,7 +326,7 @@ def gdn_layer_forward(h, lw, qlin, cfg: DecoderConfig, S: int, L: int, conv_stat
     (S, 3, C), new recurrent states (S, n_v, dk, dv) fp32)."""
     from .gdn import gdn_mixer
     x = rmsnorm(h, lw["ln1"], cfg.eps, cfg.norm_offset)
-    out, conv, rec = gdn_mixer(x, lw, qlin, cfg.gdn, S, L, conv_state, rec_state, seq_state, dtype)
+    out, conv, rec = gdn_mixer(x, lw, qlin, cfg.gdn, S, L, conv_state, rec_state, seq_state, dtype, seq_len)
     return _layer_tail(h, out, qlin, lw, cfg, "wout"), conv, rec
 
 
@@ -380,11 +380,16 @@ def decision_forward(ids, weights, embed, cfg: DecoderConfig, state_kv, T: int, 
                    pool_last)
 
 
-def question_forward(ids_q, weights, embed, cfg: DecoderConfig, state_kv, T: int, group_state, attn_dtype=torch.float32):
+def question_forward(ids_q, weights, embed, cfg: DecoderConfig, state_kv, T: int, group_state, attn_dtype=torch.float32,
+                     qlen=None, gdn_dtype=torch.float64):
     """The question pass of the question cache (v3.py:446-534, the capture of prefix_attn.py:92-93): question g's
     Lq tokens (ids_q (G, Lq), right-padded), at positions T .. T + Lq - 1 after its state group_state[g], attend that
     state's int8 K/V and themselves causally through every layer. Pads come after the real tokens, so no real token
-    sees them; they are masked as keys by the rows. Returns [(K, V) (G, Hkv, Lq, D) bf16] per layer."""
+    sees them; they are masked as keys by the rows. A Gated DeltaNet layer continues the question's state
+    (state_kv[l] = (conv, rec) of the states) over its real tokens qlen[g] as the reference's batched question pass
+    does (Backbone.padded_continuation, v3.py:494-497): pads leave the recurrent state unchanged and the new conv
+    state ends at the last real token. Returns per layer [(K, V) (G, Hkv, Lq, D) bf16] or, for a GDN layer, the
+    questions' (conv (G, 3, C), rec (G, Hv, dk, dv)) states."""
     G, Lq = ids_q.shape
     h = embed[ids_q.reshape(-1)]
     pos = (T + torch.arange(Lq)).repeat(G)
@@ -392,23 +397,31 @@ def question_forward(ids_q, weights, embed, cfg: DecoderConfig, state_kv, T: int
     gs = torch.as_tensor(group_state).long()
     out = []
     for li, lw in enumerate(weights["layers"]):
+        if cfg.is_gdn(li):
+            if qlen is None:
+                raise ValueError("question_forward: a GDN layer needs the questions' real lengths (qlen)")
+            h, conv, rec = gdn_layer_forward(h, lw, quantize_layer(lw), cfg, G, Lq, state_kv[li][0], state_kv[li][1],
+                                             gs, gdn_dtype, seq_len=qlen)
+            out.append((conv, rec))
+            continue
         h = layer_forward(h, lw, quantize_layer(lw), cfg, state_kv[li][0], state_kv[li][1], G, Lq, pos, cos, sin,
                           gs, attn_dtype=attn_dtype, capture=out)
     return out
 
 
 def qcache_decision_forward(ids_o, weights, embed, cfg: DecoderConfig, state_kv, T: int, q_kv, qlen, group_state,
-                            attn_dtype=torch.float32, temperature: float | None = None):
+                            attn_dtype=torch.float32, temperature: float | None = None, gdn_dtype=torch.float64):
     """Option rows over the question cache: ids_o (G, n_opt, t); the rows of question g start right after their
     question's last real token (position T + qlen[g], v3.py:520) and attend [state group_state[g] ; question g's K/V
-    from question_forward, keys past qlen[g] masked] + their own tokens causally (prefix_attn.py:94-99). Returns
-    (G, n_opt + 1) log-probabilities."""
+    from question_forward, keys past qlen[g] masked] + their own tokens causally (prefix_attn.py:94-99); in a GDN
+    layer they continue their question's (conv, rec) state from question_forward. Returns (G, n_opt + 1)
+    log-probabilities."""
     if temperature is None:
         temperature = float(weights.get("temperature", 1.0))
     G, n_opt, t = ids_o.shape
     R = G * n_opt
     qlen = torch.as_tensor(qlen).long()
-    Lq = q_kv[0][0].shape[2]
+    Lq = next(kv[0].shape[2] for li, kv in enumerate(q_kv) if not cfg.is_gdn(li))
     row_group = torch.arange(G).repeat_interleave(n_opt)
     pos = (T + qlen[row_group][:, None] + torch.arange(t)[None, :]).reshape(-1)
     qmask = torch.arange(Lq)[None, :] < qlen[:, None]
@@ -416,6 +429,10 @@ def qcache_decision_forward(ids_o, weights, embed, cfg: DecoderConfig, state_kv,
     gs = torch.as_tensor(group_state).long()
     h = embed[ids_o.reshape(-1)]
     for li, lw in enumerate(weights["layers"]):
+        if cfg.is_gdn(li):
+            h, _, _ = gdn_layer_forward(h, lw, quantize_layer(lw), cfg, R, t, q_kv[li][0], q_kv[li][1], row_group,
+                                        gdn_dtype)
+            continue
         Kq2, Vq2 = q_kv[li]
         h = layer_forward(h, lw, quantize_layer(lw), cfg, state_kv[li][0], state_kv[li][1], R, t, pos, cos, sin,
                           attn_dtype=attn_dtype, two_level=(Kq2, Vq2, qmask, row_group, gs))

@@ -82,12 +82,14 @@ def split_proj(proj: torch.Tensor, cfg: GDNConfig):
     return proj[:, :c], proj[:, c:c + v], proj[:, c + v:c + v + cfg.n_v_heads], proj[:, c + v + cfg.n_v_heads:]
 
 
-def conv_silu(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor | None):
+def conv_silu(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor | None, lens=None):
     """Causal depthwise conv over the sequence axis + SiLU (causal_conv1d_fn / causal_conv1d_update with SiLU).
     x (S, L, C) bf16 pre-conv inputs of S sequences; w (C, K) bf16; state (S, K-1, C) bf16: the previous K-1 inputs
     of each sequence (None: zeros, a fresh sequence). y[t, c] = sum_j w[c, j] full[t + j, c] over full = [state ; x],
     taken exactly (float64) and rounded once to bf16 (torch's bf16 conv accumulates in fp32 and rounds), then
-    bf16(silu(y)). Returns (y (S, L, C) bf16, the new state: the last K-1 inputs of [state ; x])."""
+    bf16(silu(y)). Returns (y (S, L, C) bf16, the new state: the last K-1 inputs of [state ; x]; with lens (S,), the
+    real lengths of right-padded sequences, the K-1 inputs ending at each sequence's last real token, the gather of
+    Backbone.padded_continuation, src/opendecider/backbone.py:284-289)."""
     S, L, C = x.shape
     K = w.shape[1]
     if state is None:
@@ -99,7 +101,10 @@ def conv_silu(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor | None):
         y += full[:, j:j + L, :] * wd[:, j]
     y = y.float().to(torch.bfloat16)
     from .decoder import silu_bf16
-    return silu_bf16(y), full[:, L:, :].to(x.dtype)
+    if lens is None:
+        return silu_bf16(y), full[:, L:, :].to(x.dtype)
+    idx = torch.as_tensor(lens).long()[:, None] + torch.arange(K - 1)[None, :]
+    return silu_bf16(y), torch.stack([full[s, idx[s]] for s in range(S)]).to(x.dtype)
 
 
 def l2norm_bf16(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
@@ -208,19 +213,27 @@ def gated_norm(o: torch.Tensor, z: torch.Tensor, w: torch.Tensor, eps: float) ->
 
 
 def gdn_mixer(x: torch.Tensor, lw: dict, qlin: dict, cfg: GDNConfig, S: int, L: int, conv_state=None,
-              rec_state=None, seq_state=None, dtype=torch.float64):
+              rec_state=None, seq_state=None, dtype=torch.float64, seq_len=None):
     """The GDN token mixer over S sequences of L tokens each (x (S L, hidden) bf16, the ln1-normed input):
     projection, conv + SiLU, l2norm, gates, recurrence, gated norm. conv_state (Ns, K-1, conv_dim) bf16 and
     rec_state (Ns, Hv, dk, dv) fp32 are the states the sequences continue (seq_state (S,): each sequence's state
-    index; None: sequence i continues state i; conv_state / rec_state None: fresh sequences). Returns (the gated-norm
-    output (S L, value_dim) bf16, new conv states (S, K-1, conv_dim), new recurrent states (S, Hv, dk, dv))."""
+    index; None: sequence i continues state i; conv_state / rec_state None: fresh sequences). seq_len (S,): real
+    lengths of right-padded sequences, the reference's Backbone.padded_continuation (backbone.py:256-289): the
+    in_proj outputs a and b are set to -inf at the pads (so g = -exp(A) softplus(-inf) = -0 and beta = sigmoid(-inf)
+    = 0 and the recurrent state passes through), and the new conv state is re-gathered at each real end. Returns (the
+    gated-norm output (S L, value_dim) bf16, new conv states (S, K-1, conv_dim), new recurrent states (S, Hv, dk,
+    dv))."""
     M = S * L
     q8, sw, inv = qlin["win"]
     proj, _, _, _ = oq.w8a8_linear(x, q8, sw, inv_s=inv)
     qkv, z, b, a = split_proj(proj, cfg)
+    if seq_len is not None:
+        keep = (torch.arange(L)[None, :] < torch.as_tensor(seq_len).long()[:, None]).reshape(M, 1)
+        ninf = torch.full((), -float("inf"), dtype=a.dtype)
+        a, b = torch.where(keep, a, ninf), torch.where(keep, b, ninf)
     idx = torch.arange(S) if seq_state is None else torch.as_tensor(seq_state).long()
     cs = None if conv_state is None else conv_state[idx]
-    y, new_conv = conv_silu(qkv.reshape(S, L, cfg.conv_dim), lw["conv_w"], cs)
+    y, new_conv = conv_silu(qkv.reshape(S, L, cfg.conv_dim), lw["conv_w"], cs, seq_len)
     y = y.reshape(M, cfg.conv_dim)
     kd = cfg.key_dim
     q = l2norm_bf16(y[:, :kd].reshape(M, cfg.n_k_heads, cfg.dk), cfg.eps)

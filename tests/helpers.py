@@ -70,3 +70,22 @@ def decoder_case(cfg_kw: dict, B: int, n_opt: int, t: int, T: int, temperature: 
         states.append(((kq, ks[..., 0]), (vq, vs[..., 0])))
     ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=torch.Generator().manual_seed(5))
     return cfg, w, emb, states, ids
+
+
+def hybrid_states(cfg, B: int, T: int, seed: int = 4):
+    """Per-layer states of B requests for a hybrid stack: int8 K/V of T tokens (bf16 N(0, 1) source) for the attention
+    layers; a conv window (bf16 N(0, 1)) and a recurrent state (fp32 0.05 N(0, 1)) for the GDN layers."""
+    from oracle import quant as oq
+    g = torch.Generator().manual_seed(seed)
+    gc = cfg.gdn
+    out = []
+    for li in range(cfg.n_layers):
+        if cfg.is_gdn(li):
+            out.append((torch.randn(B, 3, gc.conv_dim, generator=g).to(torch.bfloat16),
+                        torch.randn(B, gc.n_v_heads, gc.dk, gc.dv, generator=g) * 0.05))
+        else:
+            kv = torch.randn(2, B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).to(torch.bfloat16)
+            kq, ks = oq.quantize_rows(kv[0])
+            vq, vs = oq.quantize_rows(kv[1])
+            out.append(((kq, ks[..., 0]), (vq, vs[..., 0])))
+    return out

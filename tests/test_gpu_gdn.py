@@ -63,6 +63,76 @@ def test_gdn_prep_bit_exact(gpu_lib, S, L, n_k, n_v, with_state):
     assert torch.equal(co.cpu(), new)
 
 
+@pytest.mark.parametrize("S,L,n_k,n_v,lens", [(4, 11, 2, 4, [11, 6, 2, 0]), (3, 40, 16, 32, [40, 17, 1]),
+                                               (2, 9, 2, 4, [3, 8])])
+def test_gdn_prep_padded_sequences_bit_exact(gpu_lib, S, L, n_k, n_v, lens):
+    """od_gdn_prep_ex with right-padded sequences (the reference's padded continuation): gates beta = 0, g = -0 at
+    every pad (what b = a = -inf give), the conv window ending at each sequence's last real token (the state's own
+    window for an empty one), everything at real positions as without padding; bit-exact against the oracle."""
+    from opendecider_amd import kernels
+    dk = dv = 128
+    g = torch.Generator().manual_seed(S * 31 + L)
+    C = 2 * n_k * dk + n_v * dv
+    proj = _proj(g, S * L, n_k, n_v, dk, dv)
+    conv_w = _bf(g, C, 4, scale=0.3)
+    A_log = torch.log(torch.rand(n_v, generator=g) * 15.5 + 0.5).to(torch.bfloat16)
+    dt = (1 + 0.1 * torch.randn(n_v, generator=g)).to(torch.bfloat16)
+    conv_in = _bf(g, S, 3, C)
+    seq_len = torch.tensor(lens, dtype=torch.int32)
+    print(f"gdn_prep padded S={S} L={L} lens={lens}", flush=True)
+    qk, v, gg, beta, co = kernels.gdn_prep(proj.to(DEV), conv_w.to(DEV), A_log.to(DEV), dt.to(DEV), S, L, n_k, n_v,
+                                           dk, dv, conv_in.to(DEV), conv_out=True, seq_len=seq_len.to(DEV))
+    cfg = og.GDNConfig(n_k_heads=n_k, n_v_heads=n_v)
+    qkv_r, z_r, b_r, a_r = og.split_proj(proj[:, :C + n_v * dv + 2 * n_v], cfg)
+    keep = (torch.arange(L)[None, :] < seq_len[:, None].long()).reshape(-1, 1)
+    ninf = torch.full((), -float("inf"), dtype=torch.bfloat16)
+    g_r, beta_r = og.gates(torch.where(keep, a_r, ninf), torch.where(keep, b_r, ninf), A_log, dt)
+    y, new = og.conv_silu(qkv_r.reshape(S, L, C), conv_w, conv_in, lens)
+    y = y.reshape(S * L, C)
+    kd = n_k * dk
+    real = keep[:, 0]
+    q_r = og.l2norm_bf16(y[:, :kd].reshape(-1, n_k, dk)).reshape(-1, kd)
+    k_r = og.l2norm_bf16(y[:, kd:2 * kd].reshape(-1, n_k, dk)).reshape(-1, kd)
+    assert torch.equal(qk.cpu()[real], torch.cat([q_r, k_r], 1)[real])
+    assert torch.equal(v.cpu()[real], y[real, 2 * kd:])
+    assert torch.equal(gg.cpu().view(torch.int32), g_r.view(torch.int32))
+    assert torch.equal(beta.cpu(), beta_r)
+    assert (beta.cpu()[~real] == 0).all() and (gg.cpu()[~real] == 0).all()
+    assert torch.equal(co.cpu(), new)
+
+
+@pytest.mark.parametrize("chunked", [True, False])
+def test_gdn_padded_continuation_keeps_each_state(gpu_lib, chunked):
+    """The recurrence over right-padded sequences (gates from od_gdn_prep_ex) leaves each sequence's final state equal
+    to that of its unpadded pass at its real length, and a sequence with no real token its initial state bit for
+    bit."""
+    from opendecider_amd import kernels
+    dk = dv = 128
+    n_k, n_v, S, L = 2, 4, 3, 37
+    lens = [37, 12, 0]
+    g = torch.Generator().manual_seed(77)
+    C = 2 * n_k * dk + n_v * dv
+    proj = _proj(g, S * L, n_k, n_v, dk, dv).to(DEV)
+    conv_w = _bf(g, C, 4, scale=0.3).to(DEV)
+    A_log = torch.log(torch.rand(n_v, generator=g) * 15.5 + 0.5).to(torch.bfloat16).to(DEV)
+    dt = (1 + 0.1 * torch.randn(n_v, generator=g)).to(torch.bfloat16).to(DEV)
+    conv_in = _bf(g, S, 3, C).to(DEV)
+    init = (torch.randn(S, n_v, dk, dv, generator=g) * 0.05).to(DEV)
+    print(f"gdn padded continuation chunked={chunked}", flush=True)
+    qk, v, gg, beta, _ = kernels.gdn_prep(proj, conv_w, A_log, dt, S, L, n_k, n_v, dk, dv, conv_in,
+                                          seq_len=torch.tensor(lens, dtype=torch.int32, device=DEV))
+    _, fin = kernels.gdn_recurrence(qk, v, gg, beta, S, L, n_k, n_v, dk, dv, init=init, final=True, chunked=chunked)
+    assert torch.equal(fin[2], init[2])
+    for s_, n in enumerate(lens[:2]):
+        rows = slice(s_ * L, s_ * L + n)
+        qk1, v1, g1, b1, _ = kernels.gdn_prep(proj[rows].contiguous(), conv_w, A_log, dt, 1, n, n_k, n_v, dk, dv,
+                                              conv_in[s_:s_ + 1])
+        _, fin1 = kernels.gdn_recurrence(qk1, v1, g1, b1, 1, n, n_k, n_v, dk, dv, init=init[s_:s_ + 1].contiguous(),
+                                         final=True, chunked=chunked)
+        d = (fin[s_] - fin1[0]).abs().max().item()
+        assert d <= 1e-5 * fin1.abs().max().item() + 1e-7, (s_, d)
+
+
 def _rec_inputs(g, S, L, n_k, n_v, dk=128, dv=128):
     M = S * L
     q = og.l2norm_bf16(_bf(g, M, n_k, dk))

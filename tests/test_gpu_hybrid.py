@@ -19,6 +19,7 @@ from oracle import decoder as od
 from oracle import gdn as og
 from oracle import quant as oq
 
+from helpers import hybrid_states
 from test_gpu_decoder import _assert_e2e, attention_layer_stages
 
 pytestmark = pytest.mark.gpu
@@ -49,21 +50,7 @@ def _exact(a, b, what):
 
 
 def _random_states(cfg, B, T, seed=4):
-    """Per-layer states of B requests: int8 K/V of T tokens (bf16 N(0, 1) source) for the attention layers; a conv
-    window (bf16 N(0, 1)) and a recurrent state (fp32 0.05 N(0, 1)) for the GDN layers."""
-    g = torch.Generator().manual_seed(seed)
-    gc = cfg.gdn
-    out = []
-    for li in range(cfg.n_layers):
-        if cfg.is_gdn(li):
-            out.append((torch.randn(B, 3, gc.conv_dim, generator=g).to(torch.bfloat16),
-                        torch.randn(B, gc.n_v_heads, gc.dk, gc.dv, generator=g) * 0.05))
-        else:
-            kv = torch.randn(2, B, cfg.n_kv_heads, T, cfg.head_dim, generator=g).to(torch.bfloat16)
-            kq, ks = oq.quantize_rows(kv[0])
-            vq, vs = oq.quantize_rows(kv[1])
-            out.append(((kq, ks[..., 0]), (vq, vs[..., 0])))
-    return out
+    return hybrid_states(cfg, B, T, seed)
 
 
 def _load_states(dec, cfg, states, B, T, cap):
@@ -265,9 +252,43 @@ def test_hybrid_scoring_graph_replays_equal_eager(gpu_lib, name, cfg_kw, B, n_op
             _exact(gs[li].rec, states[li][1], f"layer {li}: recurrent state untouched")
 
 
+QCACHE_CASES = [("tiny_hybrid_qwen35_geometry", TINY_QWEN35, 2, 40, [0, 0, 1], 12, [12, 7, 3], 4, 5),
+                ("qwen35_hybrid_4_layers", QWEN35, 2, 256, [0, 1], 48, [48, 29], 32, 8)]
+
+
+@pytest.mark.parametrize("name,cfg_kw,B,T,gs,Lq,qlen,n_opt,t", QCACHE_CASES)
+def test_hybrid_question_cache_end_to_end(gpu_lib, name, cfg_kw, B, T, gs, Lq, qlen, n_opt, t):
+    """The question cache on the hybrid stack (v3.py:446-534 with the batched, right-padded question pass of
+    Backbone.padded_continuation): each question continues its state's GDN layers over its real tokens into a
+    per-question state and keeps its K/V for the attention layers; the option rows continue that state and attend
+    [state ; question]. Against the oracle's question_forward + qcache_decision_forward at the end-to-end bar; the
+    request states are left as they were."""
+    cfg, w, emb, states, _, dec, gstates = _setup(cfg_kw, B, 1, Lq + t, T)  # rotary tables past T + Lq + t
+    g = torch.Generator().manual_seed(11)
+    ids_q = torch.randint(0, cfg.vocab, (len(gs), Lq), generator=g)
+    ids_o = torch.randint(0, cfg.vocab, (len(gs), n_opt, t), generator=g)
+    print(f"{name}: hybrid question cache questions={len(gs)} Lq={Lq} qlen={qlen} options={n_opt} t={t}", flush=True)
+    qc = dec.question_pass(ids_q.to(DEV), qlen, gstates, gs)
+    lp = dec.score_qcache(ids_o.to(DEV), qc, gstates)
+    q_kv = od.question_forward(ids_q, w, emb, cfg, states, T, gs, qlen=qlen)
+    ref = od.qcache_decision_forward(ids_o, w, emb, cfg, states, T, q_kv, qlen, gs)
+    with oa.reference_gpu_arithmetic():
+        q_kv_gpu = od.question_forward(ids_q, w, emb, cfg, states, T, gs, qlen=qlen, gdn_dtype=torch.float32)
+        ref_gpu = od.qcache_decision_forward(ids_o, w, emb, cfg, states, T, q_kv_gpu, qlen, gs,
+                                             gdn_dtype=torch.float32)
+    _assert_e2e(lp, ref, f"{name} (hybrid question cache)", ref_gpu, t1_bar=False)
+    for li in range(cfg.n_layers):
+        if cfg.is_gdn(li):
+            _exact(gstates[li].rec, states[li][1], f"layer {li}: request state untouched")
+            _exact(gstates[li].conv, states[li][0], f"layer {li}: request conv window untouched")
+    # layer 0 is fed the embeddings on both sides: the questions' conv windows (gathered at each real end) are exact
+    assert cfg.is_gdn(0)
+    _exact(qc.gdn[0].conv, q_kv[0][0], "layer 0: question conv windows")
+
+
 def test_hybrid_rejects_what_it_does_not_define(gpu_lib):
-    """Key masks (every token enters a recurrent state), a prefill batch that is not the states' and the question
-    cache are refused before any launch."""
+    """Key masks (every token enters a recurrent state) and a prefill batch that is not the states' are refused
+    before any launch."""
     from opendecider_amd.decoder import DecoderConfig, DenseDecoder
     cfg = od.DecoderConfig(**TINY)
     w = od.make_weights(cfg, seed=3)
@@ -278,6 +299,4 @@ def test_hybrid_rejects_what_it_does_not_define(gpu_lib):
         dec.prefill(ids, st, kvalid=torch.ones(2, 8, dtype=torch.uint8, device=DEV))
     with pytest.raises(ValueError):
         dec.prefill(ids[:1], st)
-    with pytest.raises(NotImplementedError):
-        dec.question_pass(ids, [8, 8], st, [0, 1])
     assert st.length == 0

@@ -228,3 +228,64 @@ def test_hybrid_option_rows_depend_on_their_own_state():
     st2 = [(conv, rec2)] + st[1:]
     lp2 = od.decision_forward(ids, w, emb, cfg, st2, T, temperature=1.0)
     assert torch.equal(lp2[0], lp[0]) and not torch.equal(lp2[1], lp[1])
+
+
+def test_padded_continuation_equals_one_unpadded_pass_per_sequence():
+    """The reference's claim for Backbone.padded_continuation (backbone.py:257-263: features equal one unpadded pass
+    per row): right-padded sequences continuing their states, with a and b set to -inf at the pads, give at every
+    real position the outputs of each sequence run alone at its real length, and leave exactly that pass's conv and
+    recurrent state (bit for bit: at a pad e^g = 1 and beta = 0, so the state is carried unchanged); a sequence with no
+    real token leaves its state as it was."""
+    from oracle import decoder as od
+    cfg = og.GDNConfig(hidden=128, n_k_heads=2, n_v_heads=4, dk=128, dv=32)
+    g = torch.Generator().manual_seed(21)
+    lw = og.make_gdn_weights(cfg, g)
+    qlin = og.quantize_gdn(lw)
+    S, L = 4, 11
+    lens = [11, 6, 2, 0]
+    x = _bf(g, S * L, cfg.hidden)
+    conv0 = _bf(g, S, 3, cfg.conv_dim)
+    rec0 = torch.randn(S, cfg.n_v_heads, cfg.dk, cfg.dv, generator=g) * 0.05
+    out, conv, rec = og.gdn_mixer(x, lw, qlin, cfg, S, L, conv0, rec0, seq_len=lens)
+    out = out.reshape(S, L, -1)
+    for s_, n in enumerate(lens):
+        if n == 0:
+            assert torch.equal(conv[s_], conv0[s_]) and torch.equal(rec[s_], rec0[s_])
+            continue
+        o1, c1, r1 = og.gdn_mixer(x.reshape(S, L, -1)[s_, :n], lw, qlin, cfg, 1, n, conv0[s_:s_ + 1],
+                                  rec0[s_:s_ + 1])
+        assert torch.equal(out[s_, :n].view(torch.int16), o1.view(torch.int16)), s_
+        assert torch.equal(conv[s_], c1[0]) and torch.equal(rec[s_], r1[0]), s_
+    # without the masking the pads would move the states
+    _, conv_np, rec_np = og.gdn_mixer(x, lw, qlin, cfg, S, L, conv0, rec0)
+    assert not torch.equal(rec_np[1], rec[1]) and not torch.equal(conv_np[1], conv[1])
+
+
+def test_hybrid_question_cache_equals_rows_that_carry_the_question():
+    """The question cache on the hybrid stack (a batched, right-padded question pass, v3.py:446-497): question g's
+    real tokens continue every layer's state (GDN: the padded continuation above; attention: the captured K/V, pads
+    masked), and option rows over that cache give the log-probabilities of rows that carry [question g's real tokens
+    ; option] over state g, pooled over the option tokens (float64 attention and recurrence)."""
+    from helpers import hybrid_states
+    from oracle import decoder as od
+    cfg = od.DecoderConfig(hidden=256, ffn=512, n_heads=4, n_kv_heads=2, head_dim=64, n_layers=4, vocab=500,
+                           full_attention_interval=2, lin_k_heads=2, lin_v_heads=4, gated=True, rot_dim=16,
+                           norm_offset=True)
+    w = od.make_weights(cfg, seed=3)
+    w["temperature"] = 24.0
+    emb = od.make_embedding(cfg, seed=3)
+    T = 40
+    states = hybrid_states(cfg, 2, T)
+    g = torch.Generator().manual_seed(22)
+    qlen, Lq, n_opt, t = [9, 5], 9, 3, 4
+    ids_q = torch.randint(0, 500, (2, Lq), generator=g)
+    ids_o = torch.randint(0, 500, (2, n_opt, t), generator=g)
+    q_kv = od.question_forward(ids_q, w, emb, cfg, states, T, [0, 1], attn_dtype=torch.float64, qlen=qlen)
+    lp_qc = od.qcache_decision_forward(ids_o, w, emb, cfg, states, T, q_kv, qlen, [0, 1], attn_dtype=torch.float64)
+    for q in range(2):
+        # state q alone: ((kq, ks), (vq, vs)) of an attention layer, (conv, rec) of a GDN layer
+        st_q = [tuple(tuple(x[q:q + 1] for x in e) for e in st) if isinstance(st[0], tuple) else
+                tuple(x[q:q + 1] for x in st) for st in states]
+        rows = torch.cat([ids_q[q, :qlen[q]][None, None, :].expand(1, n_opt, qlen[q]), ids_o[q:q + 1]], 2)
+        lp_rows = od.decision_forward(rows, w, emb, cfg, st_q, T, attn_dtype=torch.float64, pool_last=t)
+        assert (lp_qc[q] - lp_rows[0]).abs().max().item() <= 1e-6, q
