@@ -284,7 +284,7 @@ def append_work(x, B, H, n, D, *rest):
 
 
 def rope_append_work(qkv, ld, B, S, Hq, Hk, D, *rest):
-    # od_qk_norm_rope_kv_append: q/k/v heads read, q/k heads written back, int8 K/V + scales written
+    # od_qk_norm_rope_kv_append(_ex): q/k/v heads read, q/k heads written back, int8 K/V + scales written
     tok = B * S
     return (tok * (Hq + 2 * Hk) * D, tok * ((Hq + 2 * Hk) * D * 2 + (Hq + Hk) * D * 2 + 2 * Hk * (D + 4)))
 
@@ -561,9 +561,10 @@ def run_decision(args):
     }
 
 
-def gdn_prep_work(proj, ldp, conv_w, conv_in, seq_state, n_states, A_log, dt_bias, S, L, n_k, n_v, dk, dv, *rest):
-    # od_gdn_prep: the projection's qkv / b / a columns read once, q k v written bf16, g and beta fp32, the 3-row conv
-    # windows read per sequence (when continuing) and written (when asked); the taps' 4 rows hit the cache
+def gdn_prep_work(proj, ldp, conv_w, conv_in, seq_state, n_states, seq_len, A_log, dt_bias, S, L, n_k, n_v, dk, dv,
+                  *rest):
+    # od_gdn_prep_ex: the projection's qkv / b / a columns read once, q k v written bf16, g and beta fp32, the 3-row
+    # conv windows read per sequence (when continuing) and written (when asked); the taps' 4 rows hit the cache
     M, C = S * L, 2 * n_k * dk + n_v * dv
     conv_out = rest[4]
     by = M * (C + 2 * n_v) * 2 + M * C * 2 + M * n_v * 8 + (S * 3 * C * 2 if conv_in else 0) + \
@@ -620,7 +621,7 @@ def run_hybrid(args):
     gemm_t = GemmTimers()
     wide_t = AbiTimer("od_wide_attn", wide_work)
     attn_t = AttnTimers()
-    prep_t = AbiTimer("od_gdn_prep", gdn_prep_work)
+    prep_t = AbiTimer("od_gdn_prep_ex", gdn_prep_work)
     rec_t = AbiTimer("od_gdn_recurrence_chunked", gdn_rec_work)
     norm_t = AbiTimer("od_gdn_norm_quant", gdn_norm_work)
     timers = (gemm_t, wide_t, attn_t, prep_t, rec_t, norm_t)
@@ -718,7 +719,7 @@ def run_wide_choice(args):
                          .to(torch.bfloat16))
     records = [torch.randint(0, cfg.vocab, (1, rec), generator=g, device=dev) for _ in range(n_rec + args.warmup)]
     ids = torch.randint(0, cfg.vocab, (1, n_req * n_opt, t), generator=g, device=dev)
-    app_t = AbiTimer("od_qk_norm_rope_kv_append", rope_append_work)
+    app_t = AbiTimer("od_qk_norm_rope_kv_append_ex", rope_append_work)
     attn_t = AttnTimers()
     # warm-up: one record + one scoring pass, then rewind the caches
     for i in range(args.warmup):
