@@ -675,10 +675,10 @@ __device__ __forceinline__ int frame_for(int e_blk, int e_run) {
 
 // The three pieces in sequence. `mid` runs between the softmax and the P V product (the int8 path issues the next
 // block's global loads there, so that their registers are not held through the score and softmax phases).
-template <int D, int KT, bool OWN, typename Mid>
+template <int D, int DV, int KT, bool OWN, typename Mid>
 __device__ __forceinline__ void attend_block(const uint16_t* kimg, const _Float16* vtimg, const float* gk,
                                              const float* kb, const bf16x8 (&qf)[D / 16], float c, int eb,
-                                             bool masked, float& m_run, float& l_run, int& e_run, v16f (&o)[D / 32],
+                                             bool masked, float& m_run, float& l_run, int& e_run, v16f (&o)[DV / 32],
                                              int own_row, int own_j0, int slot_row, int slot_tok, Mid&& mid) {
   constexpr int KA = 2;
   v16f s[KT];
@@ -693,9 +693,9 @@ __device__ __forceinline__ void attend_block(const uint16_t* kimg, const _Float1
   const bool grow = softmax_block<D, KT, OWN>(gk, s, c, e_blk - e_new, m_run, l_run, alpha, pb, own_row, own_j0,
                                               slot_row, slot_tok, [] {});
   mid();
-  if (grow || e_new != e_run) rescale<D>(o, alpha, e_new, e_run);
+  if (grow || e_new != e_run) rescale<DV>(o, alpha, e_new, e_run);
   __builtin_amdgcn_s_setprio(1);
-  pv_block<D, KT, 1>(vtimg, pb, o);
+  pv_block<DV, KT, 1>(vtimg, pb, o);
   __builtin_amdgcn_s_setprio(0);
 }
 
@@ -706,10 +706,10 @@ __device__ __forceinline__ void attend_block(const uint16_t* kimg, const _Float1
 // k-steps, so the wave issues VALU work while its MFMAs run; dma(ks) issues the k-step's share of the copies of
 // later blocks. The arithmetic per block is that of attend_block (the same operations on the same values in the
 // same order), so both paths give the same bits.
-template <int D, typename Dma>
+template <int D, int DV, typename Dma>
 __device__ __forceinline__ void staged_step(const BlockImg<D>& cur, const uint16_t* knext, const bf16x8 (&qf)[D / 16],
                                             v16f (&s)[2], v16f (&sn)[2], float& m_run, float& l_run, int& e_run,
-                                            v16f (&o)[D / 32], Dma&& dma) {
+                                            v16f (&o)[DV / 32], int vh, Dma&& dma) {
   constexpr int KT = 2, KA = 1, KS = D / 16;
   constexpr int kGroups = KT * 4;  // groups of 4 scores: (key tile kt, register quad r4)
   // D = 128: one group per k-step; D = 64: two; D = 256: one on every second k-step
@@ -798,9 +798,9 @@ __device__ __forceinline__ void staged_step(const BlockImg<D>& cur, const uint16
       }
   }
   l_run = fmaf(l_run, alpha, ldexpf(od_xor32_sum(psum), -dlt));
-  if (any_grow || e_new != e_run) rescale<D>(o, alpha, e_new, e_run);
+  if (any_grow || e_new != e_run) rescale<DV>(o, alpha, e_new, e_run);
   __builtin_amdgcn_s_setprio(1);
-  pv_block<D, KT, 1>(cur.vt, pb, o);
+  pv_block<DV, KT, 1>(cur.vt + vh * DV * kBlockKeys, pb, o);
   __builtin_amdgcn_s_setprio(0);
 }
 
@@ -884,17 +884,22 @@ __device__ __forceinline__ void own_stage(const AttnArgs& p, float (&red)[2][kWa
   bi.masked = 0;  // the causal mask is applied per score
 }
 
-template <int D, bool STAGED>
+// DV: the value columns one workgroup accumulates (D, or D / 2 at D = 256: the two halves of a slot tile are two
+// workgroups, each recomputing the same scores and softmax; see branched_launch).
+template <int D, int DV, bool STAGED>
 __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& sm) {
+  constexpr int kHalves = D / DV;
+  static_assert(kHalves == 1 || kHalves == 2, "value halves");
   // XCD-aware work order: workgroups are dealt round-robin over the 8 XCDs, so flat id f runs on XCD f % 8. Work item
   // w = (state split, KV head, slot tile) with the tile fastest is given to XCD (w's range), so that the tiles of
   // one (state, head) share one XCD's L2 for the state blocks they all stream.
-  const int tiles = gridDim.x;
-  const int n_items = tiles * gridDim.y * gridDim.z;
-  const int f = blockIdx.x + tiles * (blockIdx.y + gridDim.y * blockIdx.z);
+  // (the value halves of a slot tile, blockIdx.x = 2 tile + half, are adjacent work items and share the XCD too)
+  const int nx = gridDim.x;
+  const int n_items = nx * gridDim.y * gridDim.z;
+  const int f = blockIdx.x + nx * (blockIdx.y + gridDim.y * blockIdx.z);
   const int xcd = f & 7, local = f >> 3, per = n_items >> 3, rem = n_items & 7;
   const int w = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-  const int tile = w % tiles, zy = w / tiles;
+  const int tile = (w % nx) / kHalves, vh = (w % nx) % kHalves, zy = w / nx;
   const int g = zy % gridDim.y, zz = zy / gridDim.y;
   const int s = zz / p.nsplit, sp = zz % p.nsplit;
   const int row0 = p.row_start ? p.row_start[s] : 0;
@@ -948,9 +953,10 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
 
   float m_run = -INFINITY, l_run = 0.0f;
   int e_run = kNoFrame;  // the power-of-two frame the accumulator is in (follows the blocks' V exponents)
-  v16f o[D / 32];
+  v16f o[DV / 32];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) o[dt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int dt = 0; dt < DV / 32; ++dt) o[dt] = v16f{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  const int vcol = vh * DV * kBlockKeys;  // this workgroup's value rows in a block image's V^T
 
   if (b_hi > b_lo) {
     if constexpr (STAGED) {
@@ -987,7 +993,7 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
           }
         };
         // the last block's step scores its own keys again (in place of a next block), and the result is not used
-        staged_step<D>(cur, b + 1 < b_hi ? nxt.k : cur.k, qf, sc, sn, m_run, l_run, e_run, o, dma);
+        staged_step<D, DV>(cur, b + 1 < b_hi ? nxt.k : cur.k, qf, sc, sn, m_run, l_run, e_run, o, vh, dma);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
       };
@@ -1006,7 +1012,8 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
       for (int b = b_lo; b < b_hi; ++b) {
         const int buf = (b - b_lo) & 1;
         const BlockImg<D>& bk = sm.b[buf];
-        attend_block<D, 2, false>(bk.k, bk.vt, bk.gk, bk.kb, qf, 0.0f, cur.eb, cur.masked != 0, m_run, l_run, e_run, o,
+        attend_block<D, DV, 2, false>(bk.k, bk.vt + vcol, bk.gk, bk.kb, qf, 0.0f, cur.eb, cur.masked != 0, m_run,
+                                      l_run, e_run, o,
                                   0, 0, slot_row, slot_tok, [&] {
                                     if (b + 1 < b_hi) prefix_load<D>(src, p.T, (b + 1) * kBlockKeys, pr);
                                   });
@@ -1032,8 +1039,8 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
       __syncthreads();
       // a wave with no slot in this row skips its block (all its scores would be masked)
       if (__builtin_amdgcn_ballot_w64(slot_row == row) != 0)
-        attend_block<D, 1, true>(sm.b[0].k, sm.b[0].vt, nullptr, nullptr, qf, p.scale_log2, bi.eb, false, m_run,
-                                 l_run, e_run, o, row, j0, slot_row, slot_tok, [] {});
+        attend_block<D, DV, 1, true>(sm.b[0].k, sm.b[0].vt + vcol, nullptr, nullptr, qf, p.scale_log2, bi.eb, false,
+                                     m_run, l_run, e_run, o, row, j0, slot_row, slot_tok, [] {});
     }
   }
 
@@ -1043,22 +1050,22 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
   const float lse_v = l_run > 0.0f ? (m_run + __log2f(l_run)) * kLn2 : -INFINITY;
   const int64_t slot_idx = ((int64_t)slot_row * p.Hq + slot_head) * p.t + slot_tok;
   if (p.nsplit > 1) {
-    // this split's normalized fp32 partial and its LSE, merged by combine_kernel
+    // this split's normalized fp32 partial (this half's columns) and its LSE, merged by combine_kernel
     const int64_t nsl = (int64_t)p.R * p.Hq * p.t;
-    float* po = p.part + ((int64_t)sp * nsl + slot_idx) * D;
+    float* po = p.part + ((int64_t)sp * nsl + slot_idx) * D + vh * DV;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+    for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4)
         *reinterpret_cast<float4*>(po + dt * 32 + 8 * r4 + 4 * h) =
             make_float4(o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
                         o[dt][4 * r4 + 3] * inv);
-    if (h == 0) p.part[(int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx] = lse_v;
+    if (h == 0 && vh == 0) p.part[(int64_t)p.nsplit * nsl * D + (int64_t)sp * nsl + slot_idx] = lse_v;
     return;
   }
-  uint16_t* op = p.out + (int64_t)slot_row * p.sor + (int64_t)slot_head * p.soh + (int64_t)slot_tok * p.sot;
+  uint16_t* op = p.out + (int64_t)slot_row * p.sor + (int64_t)slot_head * p.soh + (int64_t)slot_tok * p.sot + vh * DV;
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) {
+  for (int dt = 0; dt < DV / 32; ++dt) {
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
       const int d0 = dt * 32 + 8 * r4 + 4 * h;
@@ -1069,21 +1076,21 @@ __device__ __forceinline__ void branched_attn_body(const AttnArgs& p, Smem<D>& s
       *reinterpret_cast<uint2*>(op + d0) = make_uint2(lo, hi);
     }
   }
-  if (p.lse && h == 0) p.lse[slot_idx] = lse_v;
+  if (p.lse && h == 0 && vh == 0) p.lse[slot_idx] = lse_v;
 }
 
 // The int8 path: two workgroups per CU (two waves per SIMD hide each other's phases; one at D = 256).
-template <int D>
+template <int D, int DV>
 __global__ __launch_bounds__(kThreads, kWgPerCu<D>) void branched_attn_kernel(AttnArgs p) {
   __shared__ Smem<D> sm;
-  branched_attn_body<D, false>(p, sm);
+  branched_attn_body<D, DV, false>(p, sm);
 }
 
 // The staged path: the same, each workgroup copying block images into LDS.
-template <int D>
+template <int D, int DV>
 __global__ __launch_bounds__(kThreads, kWgPerCu<D>) void branched_staged_kernel(AttnArgs p) {
   __shared__ Smem<D> sm;
-  branched_attn_body<D, true>(p, sm);
+  branched_attn_body<D, DV, true>(p, sm);
 }
 
 // od_attn_stage: one workgroup per (block, KV head, state) converts an int8 block into its image.
@@ -1311,14 +1318,25 @@ int branched_launch(const uint16_t* q, int64_t sqr, int64_t sqh, int64_t sqt, co
              static_cast<const uint8_t*>(img),
              l2 && l2->T2 > 0 ? static_cast<const uint8_t*>(l2->img2) : nullptr, l2 ? l2->group_state : nullptr,
              l2 ? (int)l2->T2 : 0, l2 ? (int)l2->n_states : (int)Ns};
-  dim3 grid((unsigned)tiles, (unsigned)Hkv, (unsigned)(Ns * nsplit)), block(kThreads);
+  // D = 256 on the staged path runs as two workgroups per slot tile, each accumulating 128 of the value columns
+  // (blockIdx.x = 2 tile + half): one pass over all 256 columns holds 256-column accumulators beside 256-dim query
+  // fragments, which spilled (136 bytes per lane) and moved accumulators between register files every block; each
+  // half recomputes the scores and softmax, so its outputs are those of one pass (bit for bit), and the pass takes
+  // 0.63x the time (4 states x 4096 keys, 64 rows x 24 tokens, 16 / 4 heads: 1088 -> 683 us). The int8 path keeps
+  // one workgroup per tile: its halves would each convert the whole block, and its few-row shapes measured slower.
+  const int64_t halves = D == 256 && staged ? 2 : 1;
+  if (tiles * halves > 0x7fffffff) return OD_ERR_SHAPE;
+  dim3 grid((unsigned)(tiles * halves), (unsigned)Hkv, (unsigned)(Ns * nsplit)), block(kThreads);
   hipStream_t st = (hipStream_t)stream;
   if (D == 256) {
-    staged ? branched_staged_kernel<256><<<grid, block, 0, st>>>(a) : branched_attn_kernel<256><<<grid, block, 0, st>>>(a);
+    staged ? branched_staged_kernel<256, 128><<<grid, block, 0, st>>>(a)
+           : branched_attn_kernel<256, 256><<<grid, block, 0, st>>>(a);
   } else if (D == 128) {
-    staged ? branched_staged_kernel<128><<<grid, block, 0, st>>>(a) : branched_attn_kernel<128><<<grid, block, 0, st>>>(a);
+    staged ? branched_staged_kernel<128, 128><<<grid, block, 0, st>>>(a)
+           : branched_attn_kernel<128, 128><<<grid, block, 0, st>>>(a);
   } else {
-    staged ? branched_staged_kernel<64><<<grid, block, 0, st>>>(a) : branched_attn_kernel<64><<<grid, block, 0, st>>>(a);
+    staged ? branched_staged_kernel<64, 64><<<grid, block, 0, st>>>(a)
+           : branched_attn_kernel<64, 64><<<grid, block, 0, st>>>(a);
   }
   if (nsplit > 1) {
     const int rc = od_launch_status();
