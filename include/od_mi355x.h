@@ -392,7 +392,8 @@ int od_branched_attn_staged2(const uint16_t* q, int64_t sqr, int64_t sqh, int64_
  * Query head h reads KV group h / (H / G); queries are the last T of the S key positions (query t sits at t + S - T
  * and, with causal != 0, sees keys 0 .. t + S - T). A query with no visible key returns 0. P is rounded to bf16
  * before the P.V product, as in the reference. Supports H % G == 0, DK <= 512 with DK % 8 == 0, DV in
- * {64, 128, 256}; element strides multiples of 8 (q, k, v) and 4 (out); q, k, v 16-byte aligned, out 8-byte.
+ * {64, 128, 256}; element strides multiples of 8 (q, k, v) and 4 (out); q, k, v 16-byte aligned, out 8-byte; a
+ * positive finite scale (else OD_ERR_UNSUPPORTED: the block max is taken on the unscaled scores).
  */
 int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* k, int64_t skb,
                  int64_t skg, int64_t sks, const uint16_t* v, int64_t svb, int64_t svg, int64_t svs,

@@ -690,8 +690,8 @@ def branched_attn(q, k_own, v_own, kq, ks, vq, vs, scale: float, kvalid=None, ro
 
 def wide_attn(q, k, v, scale: float, kvalid=None, causal: bool = True, return_lse: bool = False, out=None):
     """Flash attention over bf16 K/V (od_wide_attn). q (B, H, T, DK), k (B, G, S, DK), v (B, G, S, DV) bf16 with
-    DK % 8 == 0 and DK <= 512, DV in {64, 128, 256}; kvalid (B, S) bool/uint8 or None. Queries are the last T of the
-    S positions. Returns out (B, H, T, DV) bf16 [, lse (B, H, T) fp32]."""
+    DK % 8 == 0 and DK <= 512, DV in {64, 128, 256}; kvalid (B, S) bool/uint8 or None; scale > 0 and finite.
+    Queries are the last T of the S positions. Returns out (B, H, T, DV) bf16 [, lse (B, H, T) fp32]."""
     require_gpu(q, k, v, kvalid, out, name="wide_attn")
     for x in (q, k, v):
         _lib.bf16_bits(x)

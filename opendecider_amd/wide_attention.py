@@ -18,7 +18,9 @@ def wide_attention(q, k, v, scale: float, kvalid=None, causal: bool = True, retu
                    BN: int = 64, BD: int = 32, num_warps: int = 4, num_stages: int = 2):
     """causal=False: every query sees every (valid) key. return_lse: also the (B, H, T) fp32 log-sum-exp of the
     scaled scores (natural log), to merge with attention over other keys. bf16 inputs; Dv in {64, 128, 256};
-    Dk up to 512 (a Dk that is not a multiple of 8 is zero-padded, which leaves every score unchanged)."""
+    Dk up to 512 (a Dk that is not a multiple of 8 is zero-padded, which leaves every score unchanged). The scale
+    must be positive and finite (the kernel takes each block's max on the unscaled scores); the softmax scale
+    Dk^-0.5 the reference passes always is."""
     B, H, T, DK = q.shape
     G, S, DV = k.shape[1], k.shape[2], v.shape[-1]
     rep = H // G
@@ -27,6 +29,8 @@ def wide_attention(q, k, v, scale: float, kvalid=None, causal: bool = True, retu
         raise TypeError("wide_attention: q, k and v must be bf16")
     if DK > 512:
         raise ValueError(f"wide_attention: head width {DK} above 512 is not supported")
+    if not 0.0 < float(scale) < float("inf"):
+        raise ValueError(f"wide_attention: the scale must be positive and finite, got {scale}")
     if DK % 8:
         pad = 8 - DK % 8
         q, k = F.pad(q, (0, pad)), F.pad(k, (0, pad))

@@ -76,6 +76,9 @@ def test_attention_checks(L):
     w = (1024, 128, 128)
     assert L.od_wide_attn(P, *w, P, *w, P, *w, None, 0, P, *w, None, 1, 2, 2, 4, 4, 128, 96, 1, 0.1, None) == UNSUP
     assert L.od_wide_attn(P, *w, P, *w, P, *w, None, 0, P, *w, None, 1, 3, 2, 4, 4, 128, 128, 1, 0.1, None) == SHAPE
+    for bad_scale in (0.0, -0.1, float("inf"), float("nan")):  # the block max is taken on unscaled scores
+        assert L.od_wide_attn(P, *w, P, *w, P, *w, None, 0, P, *w, None, 1, 2, 2, 4, 4, 128, 128, 1, bad_scale,
+                              None) == UNSUP
     bf = (1024, 128, 128)
     assert L.od_attn_stage_bf16(P, *bf, P, *bf, None, 1, 1, 64, 96, 0.1, P, 1 << 20, None) == UNSUP  # D = 96
     assert L.od_attn_stage_bf16(P, 1028, 128, 128, P, *bf, None, 1, 1, 64, 128, 0.1, P, 1 << 20, None) == ALIGN
