@@ -103,7 +103,7 @@ __device__ __forceinline__ float silu_bf16(float g) {
 constexpr int kTok = 8;
 constexpr int kPrepThreads = 512;
 
-__global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
+__global__ __launch_bounds__(kPrepThreads, 4) void gdn_prep_kernel(PrepArgs p) {
   const int64_t ntile = (p.L + kTok - 1) / kTok;
   const int64_t s = blockIdx.x / ntile, t0 = (blockIdx.x % ntile) * kTok;
   const int64_t m_s = s * p.L;  // first token of the sequence
@@ -118,19 +118,30 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
   // real tokens of the sequence (clamped into [0, L]); tokens at or past it are right pads
   const int64_t len = p.seq_len ? min(max((int64_t)p.seq_len[s], (int64_t)0), p.L) : p.L;
 
-  // row r of full = [state (3 rows) ; the sequence's tokens]: full[r] = state row r (r < 3) or token r - 3
-  auto load_full = [&](int64_t r, float (&x)[kChan]) {
-    if (r >= kConvTaps - 1) {
-      load16(p.proj + (m_s + r - (kConvTaps - 1)) * p.ldp + c0, x);
-    } else if (st_ok) {
-      load16(p.conv_in + (st * (kConvTaps - 1) + r) * p.C + c0, x);
+  // row r of full = [state (3 rows) ; the sequence's tokens]: full[r] = state row r (r < 3) or token r - 3, as 8
+  // words of bf16 pairs (the window and the next row stay in this raw form: half the registers of fp32)
+  auto load_full = [&](int64_t r, uint32_t (&x)[kChan / 2]) {
+    const uint16_t* src = nullptr;
+    if (r >= kConvTaps - 1) src = p.proj + (m_s + r - (kConvTaps - 1)) * p.ldp + c0;
+    else if (st_ok) src = p.conv_in + (st * (kConvTaps - 1) + r) * p.C + c0;
+    if (src) {
+      const uint4 lo = *reinterpret_cast<const uint4*>(src), hi = *reinterpret_cast<const uint4*>(src + 8);
+      x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w; x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
     } else {
 #pragma unroll
-      for (int i = 0; i < kChan; ++i) x[i] = 0.0f;
+      for (int i = 0; i < kChan / 2; ++i) x[i] = 0u;
     }
   };
+  auto store_raw = [&](uint16_t* dst, const uint32_t (&x)[kChan / 2]) {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<uint4*>(dst + 8) = make_uint4(x[4], x[5], x[6], x[7]);
+  };
+  // channel i of a raw row, as fp32
+  auto chan = [](const uint32_t (&x)[kChan / 2], int i) {
+    return __uint_as_float((i & 1) ? (x[i >> 1] & 0xffff0000u) : (x[i >> 1] << 16));
+  };
   uint32_t wr[kChan * kConvTaps / 2];  // the conv taps of this thread's channels, bf16 pairs (channel i: 2 words)
-  float win[kConvTaps - 1][kChan];     // full rows t0 .. t0 + 2 (the inputs before token t0)
+  uint32_t win[kConvTaps - 1][kChan / 2];  // full rows t0 .. t0 + 2 (the inputs before token t0)
   if (on) {
 #pragma unroll
     for (int i = 0; i < kChan * kConvTaps / 8; ++i)
@@ -142,33 +153,40 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_prep_kernel(PrepArgs p) {
   // the window after that token, or, for a sequence with no real token, the state's own window
   if (p.conv_out && on && len == 0 && t0 == 0) {
 #pragma unroll
-    for (int j = 0; j < kConvTaps - 1; ++j) store16(p.conv_out + (s * (kConvTaps - 1) + j) * p.C + c0, win[j]);
+    for (int j = 0; j < kConvTaps - 1; ++j) store_raw(p.conv_out + (s * (kConvTaps - 1) + j) * p.C + c0, win[j]);
   }
 
+  // the next token's input row is loaded one token ahead, so its latency overlaps this token's work
+  uint32_t xn[kChan / 2];
+  if (on && tn > 0) load_full(t0 + kConvTaps - 1, xn);
   for (int tt = 0; tt < tn; ++tt) {
     const int64_t t = t0 + tt, m = m_s + t;
     float y[kChan];
     if (on) {
-      float x[kChan];
-      load_full(t + kConvTaps - 1, x);
+      uint32_t x[kChan / 2];
+#pragma unroll
+      for (int i = 0; i < kChan / 2; ++i) x[i] = xn[i];
+      if (tt + 1 < tn) load_full(t + kConvTaps, xn);
 #pragma unroll
       for (int i = 0; i < kChan; ++i) {
-        const uint32_t w01 = wr[2 * i], w23 = wr[2 * i + 1];
-        double acc = (double)__uint_as_float(w01 << 16) * (double)win[0][i];
-        acc += (double)__uint_as_float(w01 & 0xffff0000u) * (double)win[1][i];
-        acc += (double)__uint_as_float(w23 << 16) * (double)win[2][i];
-        acc += (double)__uint_as_float(w23 & 0xffff0000u) * (double)x[i];
+        uint32_t w01 = wr[2 * i], w23 = wr[2 * i + 1];
+        // keeps the float64 taps out of the registers between tokens (hoisted, 64 doubles would take 128 VGPRs)
+        asm volatile("" : "+v"(w01), "+v"(w23));
+        double acc = (double)__uint_as_float(w01 << 16) * (double)chan(win[0], i);
+        acc += (double)__uint_as_float(w01 & 0xffff0000u) * (double)chan(win[1], i);
+        acc += (double)__uint_as_float(w23 << 16) * (double)chan(win[2], i);
+        acc += (double)__uint_as_float(w23 & 0xffff0000u) * (double)chan(x, i);
         y[i] = silu_bf16(bf((float)acc));
       }
 #pragma unroll
-      for (int i = 0; i < kChan; ++i) {
+      for (int i = 0; i < kChan / 2; ++i) {
         win[0][i] = win[1][i];
         win[1][i] = win[2][i];
         win[2][i] = x[i];
       }
       if (p.conv_out && t == len - 1) {
 #pragma unroll
-        for (int j = 0; j < kConvTaps - 1; ++j) store16(p.conv_out + (s * (kConvTaps - 1) + j) * p.C + c0, win[j]);
+        for (int j = 0; j < kConvTaps - 1; ++j) store_raw(p.conv_out + (s * (kConvTaps - 1) + j) * p.C + c0, win[j]);
       }
     } else {
 #pragma unroll
@@ -454,6 +472,7 @@ struct NormArgs {
   int64_t ldo, ldz, ldq;
   int n_v, dv;
   float eps;
+  int vec_w;  // w and inv_s 16-byte aligned: a thread's 16 weights and scales come in two 16-byte loads each
 };
 
 // One workgroup per token; thread i handles values 16 i .. 16 i + 15 of the n_v dv outputs (a head is dv / 16
@@ -465,13 +484,24 @@ __global__ __launch_bounds__(1024) void gdn_norm_quant_kernel(NormArgs p) {
   const int V = p.n_v * p.dv;
   const int c0 = tid * kChan;
   const bool on = c0 < V;
-  float o[kChan], z[kChan];
+  float o[kChan], z[kChan], wv[kChan], sv[kChan];
   if (on) {
     load16(p.o + m * p.ldo + c0, o);
     load16(p.z + m * p.ldz + c0, z);
+    // the thread's 16 channels lie in one head (dv % 16 == 0): weights c0 % dv .. +15, scales c0 .. c0 + 15
+    if (p.vec_w) {
+      load16(p.w + c0 % p.dv, wv);
+      if (p.inv_s) load16(p.inv_s + c0, sv);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kChan; ++i) {
+        wv[i] = od_bf16_to_f32(p.w[(c0 + i) % p.dv]);
+        if (p.inv_s) sv[i] = od_bf16_to_f32(p.inv_s[c0 + i]);
+      }
+    }
   } else {
 #pragma unroll
-    for (int i = 0; i < kChan; ++i) o[i] = z[i] = 0.0f;
+    for (int i = 0; i < kChan; ++i) o[i] = z[i] = wv[i] = sv[i] = 0.0f;
   }
   double ss = 0.0;
 #pragma unroll
@@ -483,11 +513,10 @@ __global__ __launch_bounds__(1024) void gdn_norm_quant_kernel(NormArgs p) {
   uint32_t amax = 0;
 #pragma unroll
   for (int i = 0; i < kChan; ++i) {
-    const int c = c0 + i;
     const float hn = bf(o[i] * r);
-    const float hw = bf(od_bf16_to_f32(p.w[c % p.dv]) * hn);
+    const float hw = bf(wv[i] * hn);
     float v = silu_mul_bf16(hw, z[i]);
-    if (p.inv_s) v = bf(v * od_bf16_to_f32(p.inv_s[c]));
+    if (p.inv_s) v = bf(v * sv[i]);
     y[i] = on ? v : 0.0f;
     const uint32_t a = (__float_as_uint(y[i]) >> 16) & 0x7fffu;  // |bf16| bits: NaN patterns exceed every number
     amax = a > amax ? a : amax;
@@ -585,7 +614,8 @@ extern "C" int od_gdn_norm_quant(const uint16_t* o, int64_t ldo, const uint16_t*
   if (ldo < V || ldz < V || ldq < V) return OD_ERR_SHAPE;
   if (ldo % 8 || ldz % 8 || ldq % 16 || !od_aligned16(o) || !od_aligned16(z) || !od_aligned16(xq)) return OD_ERR_ALIGN;
   if (M > 0x7fffffffll) return OD_ERR_SHAPE;
-  NormArgs p{o, z, w, inv_s, xq, sx, ldo, ldz, ldq, (int)n_v, (int)dv, eps};
+  NormArgs p{o, z, w, inv_s, xq, sx, ldo, ldz, ldq, (int)n_v, (int)dv, eps,
+             od_aligned16(w) && (!inv_s || od_aligned16(inv_s)) ? 1 : 0};
   gdn_norm_quant_kernel<<<dim3((unsigned)M), dim3(threads_for(V)), 0, (hipStream_t)stream>>>(p);
   return od_launch_status();
 }
