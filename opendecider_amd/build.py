@@ -31,10 +31,11 @@ PROBE_LIB = os.path.join(PKG, "libod_probe.so")
 # kept in ordinary VGPRs (no accumulator-register copies); so do the attention kernels (softmax and rescale on the
 # score and output accumulators): at head_dim 256 (one wave per SIMD, 512 registers) the accumulator-register form
 # moved them between register files every block and spilled to scratch, the VGPR form does neither (the staged
-# path 0.92x and the int8 path 0.79x the time, bit-identical); at head_dims 64 / 128 no accumulator register is used
-# either way
+# path 0.92x and the int8 path 0.79x the time, bit-identical; the wide attention's LDS-DMA kernel at head_dim 256
+# fits 220 VGPRs and two workgroups per CU with it); at head_dims 64 / 128 no accumulator register is used either way
 SOURCE_FLAGS = {"od_gdn_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-                "od_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+                "od_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                "od_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-inline-asm"]

@@ -473,23 +473,26 @@ __global__ __launch_bounds__(kThreads, OCC) void wide_attn_kernel(WideArgs p) {
   wide_epilogue<DV>(p, t, o, m_run, l_run);
 }
 
-// ---- LDS-DMA path: DK = DKP in {64, 128}, DV = 128 ----
+// ---- LDS-DMA path: DK = DKP in {64, 128, 256}, 128 value columns per pass (DV = 128, or DV = 256 in two halves) ----
 //
 // Each block's K and V rows go from HBM straight into LDS (buffer_load ... lds, 16 bytes per lane, rows past S read
-// as zeros through the buffer range) with no staging registers, issued one whole block ahead. V stays row-major
+// as zeros through the buffer range) with no staging registers. One LDS buffer per workgroup (48 / 32 / 24 KB at
+// DKP = 256 / 128 / 64), so two workgroups share a CU and one's copy overlaps the other's compute: at DKP = 256 a
+// double-buffered workgroup (96 KB) ran alone on its CU and took 1.72x as long (4 x 16 / 4 heads of 256, 4096 causal
+// tokens); at DKP = 128 both forms measured within 3%. V stays row-major
 // ([key][d]) in LDS; the A operand of O^T += V^T P^T is gathered with ds_read_b64_tr_b16, which hands lane l of
 // each 16-lane group element e of the 4 elements at the address of lane 4 e + l / 4 of the group, column l % 4
 // (measured): with lane 4 e + c pointing at V[k + e][d + 4 c], lane l receives V[k .. k + 3][d + l]. Two such reads
 // (keys k and k + 8) make one operand. Outputs are bit-identical to the register-staged path (same products, same
-// order). No spills (192 VGPRs at DKP = 128, against 256 and 10 spilled for the register-staged kernel).
+// order). No spills (176 VGPRs at DKP = 128, against 256 and 10 spilled for the register-staged kernel).
 constexpr int kDvT = 128;
 
 template <int DKP>
 struct alignas(16) WDSmem {
-  alignas(16) uint16_t k[2][kBK * DKP];   // [key][d], 16-byte chunks swizzled (wk_off)
-  alignas(16) uint16_t v[2][kBK * kDvT];  // [key][d], 16-byte chunk c of key j at chunk c ^ 4 (j & 3)
-  alignas(16) float kb[2][kBK];
-  int mk[2];
+  alignas(16) uint16_t k[kBK * DKP];   // [key][d], 16-byte chunks swizzled (wk_off)
+  alignas(16) uint16_t v[kBK * kDvT];  // [key][d], 16-byte chunk c of key j at chunk c ^ 4 (j & 3)
+  alignas(16) float kb[kBK];
+  int mk;
 };
 
 // The transposing read's 16 lanes touch 4 consecutive keys (j & 3 = 0..3) x 2 chunks of 8 d: XOR-ing the chunk's
@@ -567,10 +570,10 @@ __global__ __launch_bounds__(kThreads, OCC) void wide_dma_kernel(WideArgs p) {
 
   const uint16_t* kg0 = p.k + (int64_t)t.b * p.skb + (int64_t)t.g * p.skg;
   const uint16_t* vg0 = p.v + (int64_t)t.b * p.svb + (int64_t)t.g * p.svg;
-  auto issue = [&](int buf, int j0) {
+  auto issue = [&](int j0) {
     const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kg0 + (int64_t)j0 * p.sks, p.sks, p.S - j0);
     const __amdgpu_buffer_rsrc_t rv = rows_rsrc(vg0 + (int64_t)j0 * p.svs, p.svs, p.S - j0);
-    const uint32_t kl = wlds_addr(&sm.k[buf][0]) + 1024 * wave_u, vl = wlds_addr(&sm.v[buf][0]) + 1024 * wave_u;
+    const uint32_t kl = wlds_addr(&sm.k[0]) + 1024 * wave_u, vl = wlds_addr(&sm.v[0]) + 1024 * wave_u;
 #pragma unroll
     for (int i = 0; i < KI; ++i) wdma16(rk, kvo[i], kl + 4096 * i);
 #pragma unroll
@@ -585,43 +588,49 @@ __global__ __launch_bounds__(kThreads, OCC) void wide_dma_kernel(WideArgs p) {
     }
     return ok;
   };
-  auto put_bias = [&](int buf, int ok) {
+  auto put_bias = [&](int ok) {
     if (tid < kBK) {
-      sm.kb[buf][tid] = ok ? 0.0f : -INFINITY;
+      sm.kb[tid] = ok ? 0.0f : -INFINITY;
       const bool all_ok = __builtin_amdgcn_ballot_w64(ok != 0) == ~0ull;  // wave 0 holds the block's 64 keys
-      if (tid == 0) sm.mk[buf] = all_ok ? 0 : 1;
+      if (tid == 0) sm.mk = all_ok ? 0 : 1;
     }
   };
 
   const int nb = t.nb;
   if (nb > 0) {
-    issue(0, 0);
-    put_bias(0, key_ok(0));
+    issue(0);
+    put_bias(key_ok(0));
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     for (int blk = 0; blk < nb; ++blk) {
-      const int cur = blk & 1, j0 = blk * kBK;
+      const int j0 = blk * kBK;
       const bool more = blk + 1 < nb;
-      // the other buffer was last read in the previous block, which every wave has finished (barrier)
-      if (more) issue(cur ^ 1, j0 + kBK);
       const int ok_next = more ? key_ok(j0 + kBK) : 0;
-      const uint16_t* vblk = sm.v[cur];
+      const uint16_t* vblk = sm.v;
       wide_block<DKP, DV, 2>(
-          sm.k[cur], sm.kb[cur], sm.mk[cur], [&](int dt, int kk) { return wv_frag(vblk, vb[dt], kk); }, qf,
-          p.scale_log2, m_run, l_run, o, p.causal && j0 + kBK - 1 > t.free_until, j0, t.qpos, [] {});
-      if (more) put_bias(cur ^ 1, ok_next);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
+          sm.k, sm.kb, sm.mk, [&](int dt, int kk) { return wv_frag(vblk, vb[dt], kk); }, qf, p.scale_log2, m_run,
+          l_run, o, p.causal && j0 + kBK - 1 > t.free_until, j0, t.qpos, [] {});
+      if (more) {
+        __syncthreads();  // every wave is done with the buffer
+        issue(j0 + kBK);
+        put_bias(ok_next);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      }
     }
   }
   wide_epilogue<DV>(p, t, o, m_run, l_run);
 }
 
-// DKP 64 / 128 (LDS 2 x (64 DKP + 8192) bf16 = 48 / 64 KB, two workgroups per CU). A 256-wide head stays on the
-// register-staged path: there this kernel holds its accumulators in AGPRs and ran 1.17x slower (4 x 16 / 4 heads,
-// 4096 keys, causal).
+// Two workgroups per CU (two waves per SIMD; the accumulators in VGPRs: this file is built with the VGPR-only MFMA
+// form, which keeps DKP = 256 at 220 VGPRs with no AGPR copies). DV = 256 runs as two 128-column halves (grid.z = 2),
+// as on the register-staged path.
 template <int DKP>
-void launch_wide_dma(const WideArgs& a, dim3 grid, hipStream_t st) {
+void launch_wide_dma(WideArgs a, dim3 grid, bool halves, hipStream_t st) {
+  if (halves) {
+    a.dv_half = kDvT;
+    grid.z = 2;
+  }
   wide_dma_kernel<DKP, 2><<<grid, dim3(kThreads), 0, st>>>(a);
 }
 
@@ -674,10 +683,12 @@ extern "C" int od_wide_attn(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t
   const int dkp = DK <= 64 ? 64 : DK <= 128 ? 128 : DK <= 256 ? 256 : 512;
   // LDS-DMA path: K rows of exactly DKP (no zero padding to insert), 128 value columns per pass, rows that do not
   // overlap (the buffer range ends at the last row's end) and 64-row block offsets that fit the 32-bit offsets
-  const bool dma = DK == dkp && dkp <= 128 && DV == 128 && sks >= DK && svs >= DV && sks < (1 << 24) && svs < (1 << 24);
+  const bool dma = DK == dkp && dkp <= 256 && (DV == 128 || (DV == 256 && dkp == 256)) && sks >= DK && svs >= DV &&
+                   sks < (1 << 24) && svs < (1 << 24);
   if (dma) {
-    if (dkp == 64) launch_wide_dma<64>(a, grid, st);
-    else launch_wide_dma<128>(a, grid, st);
+    if (dkp == 64) launch_wide_dma<64>(a, grid, false, st);
+    else if (dkp == 128) launch_wide_dma<128>(a, grid, false, st);
+    else launch_wide_dma<256>(a, grid, DV == 256, st);
     return od_launch_status();
   }
   auto by_dv = [&](auto DKc) {
