@@ -126,22 +126,26 @@ def test_strided_inputs():
     assert torch.equal(out, ref)
 
 
-@pytest.mark.parametrize("B,H,G,T,S,causal,padded", [(2, 16, 4, 200, 333, True, True), (1, 32, 8, 64, 700, False, False),
-                                                     (1, 8, 2, 130, 130, True, False)])
-def test_dma_path_matches_staged_path(B, H, G, T, S, causal, padded):
-    """Head width 128 runs on the LDS-DMA path (rows copied straight into LDS, V^T gathered with transposing LDS
-    reads); head width 120 on the register-staged path, which pads it to 128 with zeros. With the last 8 dims of q
-    and k zero both see the same scores and must agree bit for bit: the two paths share the arithmetic."""
+@pytest.mark.parametrize("B,H,G,T,S,D,DV,causal,padded", [
+    (2, 16, 4, 200, 333, 128, 128, True, True), (1, 32, 8, 64, 700, 128, 128, False, False),
+    (1, 8, 2, 130, 130, 128, 128, True, False), (2, 8, 2, 150, 300, 64, 128, True, True),
+    (1, 16, 4, 100, 260, 256, 256, True, True), (1, 8, 2, 40, 200, 256, 128, False, False)])
+def test_dma_path_matches_staged_path(B, H, G, T, S, D, DV, causal, padded):
+    """Head widths 64, 128 and 256 with 128 value columns per pass (Dv = 256 in two halves) run on the LDS-DMA path
+    (rows copied straight into LDS, V^T gathered with transposing LDS reads); head width D - 8 on the
+    register-staged path, which pads it to D with zeros. With the last 8 dims of q and k zero both see the same
+    scores and must agree bit for bit: the two paths share the arithmetic."""
     from opendecider_amd import wide_attention
-    q, k, v, kv = make(11, B, H, G, T, S, 128, 128, padded)
-    q[..., 120:] = 0
-    k[..., 120:] = 0
+    q, k, v, kv = make(11, B, H, G, T, S, D, DV, padded)
+    q[..., D - 8:] = 0
+    k[..., D - 8:] = 0
     q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
     kv = None if kv is None else kv.to(DEV)
-    print(f"wide_attention DMA vs staged B={B} H={H} G={G} T={T} S={S} causal={causal} padded={padded}", flush=True)
+    print(f"wide_attention DMA vs staged B={B} H={H} G={G} T={T} S={S} D={D} DV={DV} causal={causal} "
+          f"padded={padded}", flush=True)
     out_dma, lse_dma = wide_attention(q, k, v, 0.125, kv, causal=causal, return_lse=True)
-    out_st, lse_st = wide_attention(q[..., :120].contiguous(), k[..., :120].contiguous(), v, 0.125, kv, causal=causal,
-                                    return_lse=True)
+    out_st, lse_st = wide_attention(q[..., :D - 8].contiguous(), k[..., :D - 8].contiguous(), v, 0.125, kv,
+                                    causal=causal, return_lse=True)
     assert torch.equal(out_dma.view(torch.int16), out_st.view(torch.int16))
     assert torch.equal(lse_dma, lse_st)
 
