@@ -19,8 +19,9 @@ sample of the same workload, scaled). The default line also carries the full dec
 a 32768-token int8 state + 256-token records, 2 x 255 options x 12 tokens) and the decision on the Qwen3.5 hybrid
 stack ("hybrid": 24 Gated DeltaNet + 8 full-attention layers), each with its own CPU baseline, and the kernel-level
 figures: the few-slot KV-bound attention ("attention_kv_bound", 16 query slots per KV head) beside the KV-bound probe
-as the survey defines it ("attention_kv_probe": 32768-token states, 2 options x 16 tokens, 128 slots per KV head),
-the single W8A8 linear of config 0 with the reference's CPU linear path ("config0_linear"), the reference's
+("attention_kv_probe": the same 32768-token states with 2 options x 16 tokens, 128 slots per KV head, near the
+HBM / bf16 ridge),
+the single 256 x 4096 x 4096 W8A8 linear with the reference's CPU linear path ("config0_linear"), the reference's
 scripts/bench_gemm.py sweep beside the vendor int8 GEMM ("gemm_sweep") and scripts/bench_qcache_rows.py's question
 cache shapes with a CPU baseline ("qcache_rows"). --scoring-only leaves all sub-objects out. Every CPU baseline is
 the median of --cpu-sample-repeats timed runs after one warm-up and names the host CPU model.
@@ -113,7 +114,7 @@ def parse():
                          "records, 2 requests x 255 options x 12 tokens scored after each record; gemm_traffic: "
                          "the run the GEMM traffic counters are read on (a 256 MiB device copy to calibrate them, "
                          "then two scoring passes through 2 layers, i.e. each M = 4096 GEMM shape twice); "
-                         "attention: the branched attention alone on the config-1 shape and on the KV-bound probe "
+                         "attention: the branched attention alone on the 8-state option-row shape and on the KV-bound probe "
                          "(32768-token states, 2 options x 16 tokens per state); lm_logprob: the LM head's token "
                          "log-prob of 1024 rows over a 151936 x 4096 int8 table; gemm: the W8A8 linear alone over "
                          "the reference's (K, N) x M sweep (scripts/bench_gemm.py) and the 9B layer shapes at M = 4096; "
@@ -541,7 +542,7 @@ def run_decision(args):
     n_a, ms_a, (fl_a, by_a) = attn_t.summary()
     tot_ms = sum(lat) * 1e3
     return {
-        "metric": "decisions/sec (config 3: 4096-token states prefilled from ids, 64 options x 24 tokens, 9B dims)",
+        "metric": "decisions/sec (4 requests, 4096-token states prefilled from ids, 64 options x 24 tokens, 9B dims)",
         "value": B / p50, "unit": "decisions/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": sum(lat) / len(lat) * 1e3, "p50_latency_ms": p50 * 1e3,
         "p90_latency_ms": lat_sorted[min(len(lat) - 1, int(0.9 * len(lat)))] * 1e3,
@@ -752,7 +753,7 @@ def run_wide_choice(args):
     # 2 x 255 x 12 x 4 = 24,480 query slots per KV head read each state key: ~1,500 FLOP per K/V byte, so the row
     # attention is bf16-MFMA-bound and its rate is quoted in TFLOP/s (the HBM figure stays beside it)
     return {
-        "metric": "row-attention TFLOP/s and append cost per record (config 4: 32k int8 state + 8 x 256-token "
+        "metric": "row-attention TFLOP/s and append cost per record (32k int8 state + 8 x 256-token "
                   "records, 2 x 255 options x 12 tokens)",
         "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": n_rec, "warmup": args.warmup,
         "ms_per_step": sum(rec_ms) / n_rec + sum(score_ms) / n_rec, "higher_is_better": True, "scaling": "weak",
@@ -776,14 +777,14 @@ def run_gemm(args):
     """The W8A8 linear alone: od_act_quant + od_w8a8_gemm on the reference's sweep (scripts/bench_gemm.py:22-23:
     (K, N) in {(2048, 6144), (6144, 2048), (2048, 2048)} x M in {64, 512, 2048, 8192}) and on the 9B layer shapes at
     M = 4096 (QKV 4096 -> 6144, O 4096 -> 4096, gate+up 4096 -> 24576 also with SwiGLU in the epilogue, down
-    12288 -> 4096), and the single 256 x 4096 x 4096 linear of config 0. Inputs as config 2: X bf16 N(0, 1) with 1% outlier channels x20, W N(0, 0.02) with SmoothQuant
+    12288 -> 4096), and the single 256 x 4096 x 4096 linear. Inputs as the layer shapes: X bf16 N(0, 1) with 1% outlier channels x20, W N(0, 0.02) with SmoothQuant
     factors U(0.5, 2) folded in, per-channel int8; 1/s fused into the activation quantizer. HIP events over 20 calls
     of each kernel after 3 warm-up calls; the vendor int8 GEMM (torch._int_mm, hipBLASLt, int32 output, no
     epilogue) beside it. Each timing is a replay of a HIP graph of the 20 calls (GPU time, no host launch gaps): warm
     caches, the weights of the smaller shapes staying in the Infinity Cache between calls. gemm_us_cold: the median
     of 5 single calls, each after a 512 MB buffer has been read and written (no operand in L2 or the Infinity
     Cache; the 36-layer passes see the weights this way, 36 layers of them being far larger than the cache).
-    CPU baselines on config 0 (M = 256, 4096 x 4096): the reference's CPU linear path
+    CPU baselines on the single linear (M = 256, 4096 x 4096): the reference's CPU linear path
     (Int8Linear.forward: dequantize + F.linear in bf16, quant.py:156-157) and the W8A8 oracle."""
     import torch
 
@@ -900,7 +901,7 @@ def run_gemm(args):
         res["cpu_baseline"] = {"value": ops / ref / 1e12, "unit": "TOPS", **cpu_fields(_t, n), "kind": "port",
                                "reference_linear_ms": ref * 1e3, "w8a8_port_ms": port * 1e3,
                                "w8a8_port_tops": ops / port / 1e12,
-                               "sample": (f"config 0 (M={M}, K={K}, N={N}), median of {n} after a warm-up: the "
+                               "sample": (f"the single linear (M={M}, K={K}, N={N}), median of {n} after a warm-up: the "
                                           f"reference's CPU linear path (Int8Linear.forward: dequantize + F.linear, "
                                           f"quant.py:156-157) {ref * 1e3:.1f} ms; the W8A8 oracle (act-quant, int32 "
                                           f"GEMM, epilogue) {port * 1e3:.1f} ms")}
@@ -1024,7 +1025,7 @@ ATTN_SHAPES = (("config1", 8, 32, 2048, 16), ("kv_probe", 8, 2, 32768, 16), ("kv
 
 
 def run_attention(args, only=None):
-    """The branched attention alone on the shapes its rooflines are quoted on: the config-1 shape (8 states of
+    """The branched attention alone on the shapes its rooflines are quoted on: the 8-state option-row shape (8 states of
     2048 int8 K/V tokens, 32 options x 16 tokens each, 32/8 heads, head_dim 128: bf16-MFMA-bound), the ridge probe
     (the same dims with 32768-token states and 2 options x 16 tokens each: about 250 FLOP per K/V byte, at the
     MFMA/HBM ridge) and the KV-bound few-slot probe (32768-token states, 2 options x 2 tokens each: 16 query slots
@@ -1075,16 +1076,16 @@ def run_attention(args, only=None):
                               "staged" if kernels.uses_staging(rows, t, Hq, Hkv) else "direct")}
     if only is not None:
         return {"shapes": res}
-    out = {"metric": "branched attention: KV GB/s on the KV-bound few-slot probe (TFLOP/s on the config-1 shape "
+    out = {"metric": "branched attention: KV GB/s on the KV-bound few-slot probe (TFLOP/s on the 8-state option-row shape "
                      "and the ridge probe beside it)",
            "value": res["kv_stream"]["kv_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": res["kv_stream"]["avg_launch_us"] / 1e3, "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "int8 K/V, bf16 MFMA", "data": "synthetic",
-           "config": {"workload": "branched attention alone: config-1 shape, ridge probe, KV-bound few-slot probe"},
+           "config": {"workload": "branched attention alone: 8-state option-row shape, ridge probe, KV-bound few-slot probe"},
            "shapes": res}
     if not args.no_cpu_baseline:
         # the reference's CPU branch of _split_attention (prefix_attn.py:58-76) on K/V materialized in bf16, as the
-        # oracle restates it, for 1 of the 8 config-1 states (32 options x 16 tokens over 2048 keys), scaled x8
+        # oracle restates it, for 1 of the 8 states (32 options x 16 tokens over 2048 keys), scaled x8
         from oracle import attention as oa
         torch.set_num_threads(os.cpu_count() or 1)
         cg = torch.Generator().manual_seed(5)
@@ -1097,7 +1098,7 @@ def run_attention(args, only=None):
         ks, vs = torch.rand(1, Hkv, T, generator=cg) * 0.02, torch.rand(1, Hkv, T, generator=cg) * 0.02
         n = args.cpu_sample_repeats
         per_state, _ = cpu_timed(lambda: oa.branched_attention_int8(q, k, v, kq, ks, vq, vs, D ** -0.5), n)
-        out["cpu_baseline"] = {"value": 1e3 * per_state * 8, "unit": "ms per config-1 call", **cpu_fields(torch, n),
+        out["cpu_baseline"] = {"value": 1e3 * per_state * 8, "unit": "ms per 8-state option-row call", **cpu_fields(torch, n),
                                "kind": "port",
                                "sample": (f"1 of the 8 states (32 options x 16 tokens over 2048 int8 keys, K/V "
                                           f"materialized in bf16), median of {n} after a warm-up: "
@@ -1300,7 +1301,7 @@ def main():
         hbm = hbm_ceiling()
         res["attention_kv_bound"]["sustained"] = hbm
         res["attention_kv_bound"]["frac_of_sustained"] = kvb["kv_gbs"] / hbm["value"]
-        # the KV-bound probe as the survey defines it: the same states with 2 options x 16 tokens per state (128
+        # the KV-bound probe near the HBM / bf16 ridge: the same states with 2 options x 16 tokens per state (128
         # query slots per KV head, ~250 FLOP per K/V byte: at the bf16-MFMA / HBM ridge, so both fractions apply)
         kvp = run_attention(_sub_args(args, steps=20, warmup=50), only=("kv_probe",))["shapes"]["kv_probe"]
         res["attention_kv_probe"] = {
@@ -1310,12 +1311,12 @@ def main():
             "avg_launch_us": kvp["avg_launch_us"], "launches": kvp["launches"],
             "config": {"workload": "8 states x 32768 int8 K/V tokens (fp32 per-token scales), 2 options x 16 tokens "
                                    "per state, 32/8 heads, head_dim 128", "slots_per_kv_head": 128,
-                       "definition": "the KV-bound probe as the survey defines it (S=32768, 2 rows x 16 tokens)"},
+                       "definition": "the KV-bound ridge probe (S=32768, 2 rows x 16 tokens, 128 slots per KV head)"},
             "frac_of_sustained_hbm": kvp["kv_gbs"] / hbm["value"],
             "note": "K/V bytes (int8 + fp32 scales) per call over the call's duration (HIP events)"}
         torch.cuda.empty_cache()
-        # config 0 (the single W8A8 linear) and the reference's scripts/bench_gemm.py sweep, with the vendor int8
-        # GEMM (torch._int_mm, hipBLASLt) beside each shape and config 0's CPU baselines
+        # the single 256 x 4096 x 4096 W8A8 linear and the reference's scripts/bench_gemm.py sweep, with the vendor int8
+        # GEMM (torch._int_mm, hipBLASLt) beside each shape and the single linear's CPU baselines
         gm = run_gemm(args)
         c0 = next(r for r in gm["shapes"] if r["shape"] == "config0")
         res["config0_linear"] = {

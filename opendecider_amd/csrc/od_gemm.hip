@@ -593,7 +593,7 @@ __global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
 }
 
 // ------------------------------------------------------------------------------------------------ small M
-// The small-M kernel (M up to a few hundred rows and few tiles: config 0's single linear, the question and record
+// The small-M kernel (M up to a few hundred rows and few tiles: a single 256-row linear, the question and record
 // passes): the 256-row tiles above leave most CUs idle there, and splitting K across workgroups costs int32 partial
 // planes in memory (2 x splits x M x N x 4 bytes) and a second launch. Here one workgroup of 4 waves owns a
 // 64 x BN tile and splits K inside itself: wave w sums the 128-byte k-chunks w, w + 4, w + 8, ... of the tile. Each

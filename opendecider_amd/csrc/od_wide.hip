@@ -19,9 +19,10 @@
 // with the keys in the score layout's order (bits 2 and 3 of the key index swapped inside each 16-key group). Q is
 // held in registers (the reduction dimension DK is padded with zeros to DKP).
 //
-// Two paths: the LDS-DMA path (DK = 64 or 128, DV = 128: the decoder's prefill) copies K and V rows straight into
-// LDS and reads V^T out of the row-major block with transposing LDS reads; the register-staged path (any other
-// shape) passes each block through registers and stores V transposed.
+// Two paths: the LDS-DMA path (DK = 64, 128 or 256 with 128 value columns per pass: the decoder's prefill, 256-wide
+// heads in two halves) copies K and V rows straight into LDS and reads V^T out of the row-major block with
+// transposing LDS reads; the register-staged path (any other shape) passes each block through registers and stores
+// V transposed.
 #include "od_common.h"
 
 namespace {
@@ -365,7 +366,7 @@ __device__ __forceinline__ bool wide_tile(WideArgs& p, WideTile& t) {
   // w = bg * tiles + tile goes to XCD (w's range), so the slot tiles of one (batch, KV group) share an L2 for the
   // K/V they all stream. A bijection of [0, tiles * B G). Causal with the queries' own triangle at least half of
   // the keys (a prefill): a tile's work grows with its index, so each (batch, group) deals its tiles last first and
-  // the light tiles fill the end instead of the heaviest ones (config 3's state pass: 761 -> 703 us).
+  // the light tiles fill the end instead of the heaviest ones (4 x 4096-token causal prefill, 32 / 8 heads of 128: 761 -> 703 us).
   const int tiles = gridDim.x, total = gridDim.x * gridDim.y;
   const int f = blockIdx.x + blockIdx.y * tiles;
   const int per = total >> 3, rem = total & 7, xcd = f & 7, local = f >> 3;

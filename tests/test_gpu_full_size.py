@@ -2,7 +2,8 @@
 the attention kernels against the oracle on those shapes (every output, or sampled rows where the oracle would take
 minutes), and the 36-layer passes through properties that do not depend on size.
 
-* Config 3 (4 requests, 4096-token states prefilled from ids, 64 options x 24 tokens, 36 layers of 9B dims):
+* The decision from ids (4 requests, 4096-token states prefilled from ids, 64 options x 24 tokens, 36 layers of 9B
+  dims):
   - the causal state attention (od_wide_attn, B 4 x 32 heads x 4096 x 4096) against the blocked oracle on the first
     and the last 128 query positions of every (request, head);
   - the option-row attention over the 4096-token int8 states, every output against the oracle;
@@ -11,7 +12,7 @@ minutes), and the 36-layer passes through properties that do not depend on size.
     (those tokens see the same keys, and every kernel of the pass is row-independent), and the same layer-0 bytes
     for all 4096 tokens (layer 0's K/V depend on no attention); two scoring passes give the same bits; options
     permuted give the permuted probabilities (<= 1e-6); the probabilities over options and 'none' sum to 1.
-* Config 4 (one 32768-token shared state grown by 256-token records, 2 x 255 options x 12 tokens):
+* The wide-choice state (one 32768-token shared state grown by 256-token records, 2 x 255 options x 12 tokens):
   - the option-row attention over 33280 int8 keys, sampled rows against the oracle;
   - the pass: two 128-token records appended one at a time give the same layer-0 cache bytes as the two appended
     as one 256-token record; scoring is deterministic and option-order invariant (<= 1e-6).
@@ -46,7 +47,7 @@ def test_config3_state_attention_full_shape(gpu_lib):
         _, le = oa.attention(qs, ks, vs, D ** -0.5, None, causal=True)
         assert (lse[:, :, rows] - le).abs().max().item() < 1e-4, what
         check_vs_blocked(out[:, :, rows].reshape(B * H, n, D), ob.reshape(B * H, n, D), bound.reshape(B * H, n, D),
-                         f"config 3 state attention, {what} {n} positions")
+                         f"4 x 4096-token state attention, {what} {n} positions")
 
 
 def test_config3_row_attention_full_shape(gpu_lib):
@@ -54,7 +55,7 @@ def test_config3_row_attention_full_shape(gpu_lib):
     print("branched attention: 4 states x 4096 keys, 4 x 64 rows x 24 tokens", flush=True)
     out, lse = run_gpu(c)
     ref, ref_lse = run_oracle(c)
-    st = assert_close_rel(out.float().cpu(), ref, what="config 3 row attention")
+    st = assert_close_rel(out.float().cpu(), ref, what="4096-token-state row attention")
     print(st)
     assert (lse.cpu() - ref_lse).abs().max().item() <= 1e-4
 
@@ -68,7 +69,7 @@ def test_config4_row_attention_full_shape_sampled_rows(gpu_lib):
     sub = dict(c, q=c["q"][rows], k=c["k"][rows], v=c["v"][rows], row_counts=[len(rows)],
                row_state=torch.zeros(len(rows), dtype=torch.long))
     ref, ref_lse = run_oracle(sub)
-    st = assert_close_rel(out.float().cpu()[rows], ref, what="config 4 row attention (sampled rows)")
+    st = assert_close_rel(out.float().cpu()[rows], ref, what="32768-token-state row attention (sampled rows)")
     print(st)
     assert (lse.cpu()[rows] - ref_lse).abs().max().item() <= 1e-4
 
@@ -82,7 +83,7 @@ def test_config3_decision_full_size_properties(gpu_lib):
     g = torch.Generator(device=DEV).manual_seed(3)
     ids_state = torch.randint(0, cfg.vocab, (B, S), generator=g, device=DEV)
     ids = torch.randint(0, cfg.vocab, (B, n_opt, t), generator=g, device=DEV)
-    print(f"config 3 full size: {cfg.n_layers} layers, {B} x {S} prefill, {n_opt} x {t} options", flush=True)
+    print(f"decision full size: {cfg.n_layers} layers, {B} x {S} prefill, {n_opt} x {t} options", flush=True)
     one = dec.new_state_caches(B, S)
     dec.prefill(ids_state, one)
     two = dec.new_state_caches(B, S)
@@ -125,7 +126,7 @@ def test_config4_wide_choice_full_size_properties(gpu_lib):
     r1 = torch.randint(0, cfg.vocab, (1, rec), generator=g, device=DEV)
     r2 = torch.randint(0, cfg.vocab, (1, rec), generator=g, device=DEV)
     ids = torch.randint(0, cfg.vocab, (1, n_opt, t), generator=g, device=DEV)
-    print(f"config 4 full size: {S0}-token state + 2 x {rec}-token records (and as one), {n_opt} x {t} options",
+    print(f"wide-choice full size: {S0}-token state + 2 x {rec}-token records (and as one), {n_opt} x {t} options",
           flush=True)
     dec.prefill(r1, a)
     dec.prefill(r2, a)
