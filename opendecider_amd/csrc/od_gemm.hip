@@ -419,7 +419,7 @@ __device__ __forceinline__ Panels panels_of(const GemmArgs& p, int v, int ntiles
 }
 
 template <int BM, int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU, bool WIDE>
-__global__ __launch_bounds__(kThreads, 1) void w8a8_gemm_kernel(GemmArgs p) {
+__global__ __launch_bounds__(kThreads, BM == 128 && BN == 128 ? 4 : 1) void w8a8_gemm_kernel(GemmArgs p) {
   constexpr int kWM = WaveGrid<BM>::kWM, kWN = WaveGrid<BM>::kWN;
   constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile: 64 x BN/kWN
   constexpr int TM = kRowsW / 32;    // 2
@@ -769,14 +769,24 @@ struct Tiling {
 // persistent workgroup runs times the time of one tile. Measured per-tile times relative to 256 x 256 (K = 4096 and
 // 12288, N = 4096 to 24576, M = 512 to 16384): 0.79-0.88 for 256 x 192, 0.61-0.69 for 128 x 256 (a smaller tile
 // reads more LDS fragments per MFMA); 0.84 and 0.68 pick the fastest of the three at every measured shape.
-Tiling tiling_of(int64_t M, int64_t N) {
-  const struct { int bm, bn; double cost; } cand[3] = {{256, 256, 1.0}, {256, 192, 0.84}, {128, 256, 0.68}};
+// With `small` (a bf16 output through the wide epilogue, no accumulator output) 128 x 128 is a fourth candidate,
+// for mid-size M x N that leave most CUs without a larger tile. Its workgroup needs 68 KB of LDS and at most 128
+// VGPRs per lane, so two run on a CU (the persistent grid is twice the CUs): measured on the sweep's and the 9B
+// shapes at M = 512 to 8192, one such tile per CU takes 0.53 of a 256 x 256 tile's time (its main loop waits on
+// its one stage of loads in flight) and two together 0.60.
+constexpr double kRel128x128 = 0.53, kRel128x128Pair = 0.60;
+Tiling tiling_of(int64_t M, int64_t N, bool small) {
+  const struct { int bm, bn; double cost; } cand[4] = {
+      {256, 256, 1.0}, {256, 192, 0.84}, {128, 256, 0.68}, {128, 128, kRel128x128}};
   const int64_t cus = cu_count();
   Tiling best{256, 256, 0, 0, 1.0};
   double best_cost = 0.0;
   for (const auto& c : cand) {
+    const bool t128 = c.bn == 128;
+    if (t128 && !small) continue;
     const int64_t tm = (M + c.bm - 1) / c.bm, tn = (N + c.bn - 1) / c.bn;
-    const double cost = (double)((tm * tn + cus - 1) / cus) * c.cost;
+    const double cost = t128 ? (tm * tn <= cus ? kRel128x128 : (double)((tm * tn + 2 * cus - 1) / (2 * cus)) * kRel128x128Pair)
+                             : (double)((tm * tn + cus - 1) / cus) * c.cost;
     if (best.tiles_m == 0 || cost < best_cost) {
       best = {c.bm, c.bn, tm, tn, c.cost};
       best_cost = cost;
@@ -812,7 +822,7 @@ SplitPlan split_plan(int64_t M, int64_t N, int64_t K) {
   const int nk = (int)((K + BK - 1) / BK);
   const SplitPlan none{1, nk, 0, 0};
   if (small_m(M, N)) return none;  // the small-M kernel splits K inside its workgroups
-  const Tiling t = tiling_of(M, N);
+  const Tiling t = tiling_of(M, N, false);
   const int64_t ntiles = t.tiles_m * t.tiles_n, cus = cu_count();
   if (ntiles * 2 > cus || nk < 4) return none;
   const double t_stage = 1.2 * t.rel;  // us per k-tile stage of one tile
@@ -898,23 +908,33 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
     }
     return od_launch_status();
   }
-  const Tiling t = tiling_of(M, N);
-  const int64_t tiles_m = t.tiles_m, tiles_n = t.tiles_n;
-  if (tiles_m * tiles_n > 0x7fffffff) return OD_ERR_SHAPE;
-  p.tiles_m = (int)tiles_m;
-  p.tiles_n = (int)tiles_n;
-  p.kt_per = (int)((K + BK - 1) / BK);
-  p.split_stride = 0;
-  // persistent workgroups: one per CU (the kernel's LDS admits one), each looping over tiles bid + i * grid
-  const int64_t ntiles = tiles_m * tiles_n;
-  const int64_t cus = cu_count();
-  dim3 grid((unsigned)(ntiles <= cus ? ntiles : cus)), block(kThreads);
   // The fast variant needs whole k-tiles and 4-column output groups that are 8-byte (bf16) / 16-byte (int32)
   // aligned (with SwiGLU, 2-column output groups 4-byte aligned); anything else takes the GENERAL variant. The wide
   // variant (the epilogue's row pass on 8-column groups: 16-byte loads and stores) needs N % 8 == 0 and 16-byte
   // aligned bf16 rows (8-byte with SwiGLU).
   auto al = [](const void* q, unsigned a) { return (((uintptr_t)q) & (a - 1)) == 0; };
   const bool fast_k = K % BK == 0 && N % 4 == 0;
+  const bool fast_out = fast_k && (swiglu ? (p.ldo % 2 == 0 && al(p.out, 4))
+                                          : (p.ldo % 4 == 0 && al(p.out, 8) && al(p.bias, 8) && p.ldr % 4 == 0 &&
+                                             al(p.residual, 8)));
+  const bool wide_out = fast_out && N % 8 == 0 && al(p.sa, 16) && al(p.sw, 16) && p.ldo < (1 << 22) &&
+                        (swiglu ? (p.ldo % 4 == 0 && al(p.out, 8))
+                                : (p.ldo % 8 == 0 && al(p.out, 16) && al(p.bias, 16) && p.ldr % 8 == 0 &&
+                                   p.ldr < (1 << 22) && al(p.residual, 16)));
+  const bool split = sp && sp->splits > 1;
+  // 128 x 128 tiles only for a bf16 output through the wide epilogue (one launch, no accumulator output)
+  const Tiling t = tiling_of(M, N, wide_out && !split && !p.acc);
+  const int64_t tiles_m = t.tiles_m, tiles_n = t.tiles_n;
+  if (tiles_m * tiles_n > 0x7fffffff) return OD_ERR_SHAPE;
+  p.tiles_m = (int)tiles_m;
+  p.tiles_n = (int)tiles_n;
+  p.kt_per = (int)((K + BK - 1) / BK);
+  p.split_stride = 0;
+  // persistent workgroups: one per CU (the kernel's LDS admits one; two of the 128 x 128 tile's), each looping over
+  // tiles bid + i * grid
+  const int64_t ntiles = tiles_m * tiles_n;
+  const int64_t gmax = (t.bm == 128 && t.bn == 128 ? 2 : 1) * cu_count();
+  dim3 grid((unsigned)(ntiles <= gmax ? ntiles : gmax)), block(kThreads);
   enum { kFast, kGeneral, kWide };
   auto launch = [&](auto BMc, auto BNc, auto ACCc, auto GENc, auto SWc, auto WIc) {
     w8a8_gemm_kernel<decltype(BMc)::value, decltype(BNc)::value, decltype(ACCc)::value, decltype(GENc)::value,
@@ -934,15 +954,20 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
   };
   auto launch2 = [&](auto ACCc, auto SWc, int variant) {
     using I = std::integral_constant<int, 256>;
-    if (t.bm == 128) {
-      launch1(std::integral_constant<int, 128>{}, I{}, ACCc, SWc, variant);
+    using H = std::integral_constant<int, 128>;
+    if (t.bm == 128 && t.bn == 128) {
+      // chosen only for the wide variant without accumulators (the 4-column epilogue needs 64-column sub-tiles)
+      if constexpr (!decltype(ACCc)::value)
+        if (variant == kWide) launch(H{}, H{}, ACCc, std::false_type{}, SWc, std::true_type{});
+    } else if (t.bm == 128) {
+      launch1(H{}, I{}, ACCc, SWc, variant);
     } else if (t.bn == 192) {
       launch1(I{}, std::integral_constant<int, 192>{}, ACCc, SWc, variant);
     } else {
       launch1(I{}, I{}, ACCc, SWc, variant);
     }
   };
-  if (sp && sp->splits > 1) {
+  if (split) {
     // partial planes into the workspace, then the finalize pass writes out
     GemmArgs q = p;
     p.out = nullptr;
@@ -964,13 +989,6 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
     }
     return od_launch_status();
   }
-  const bool fast_out = fast_k && (swiglu ? (p.ldo % 2 == 0 && al(p.out, 4))
-                                          : (p.ldo % 4 == 0 && al(p.out, 8) && al(p.bias, 8) && p.ldr % 4 == 0 &&
-                                             al(p.residual, 8)));
-  const bool wide_out = fast_out && N % 8 == 0 && al(p.sa, 16) && al(p.sw, 16) && p.ldo < (1 << 22) &&
-                        (swiglu ? (p.ldo % 4 == 0 && al(p.out, 8))
-                                : (p.ldo % 8 == 0 && al(p.out, 16) && al(p.bias, 16) && p.ldr % 8 == 0 &&
-                                   p.ldr < (1 << 22) && al(p.residual, 16)));
   const int out_variant = wide_out ? kWide : (fast_out ? kFast : kGeneral);
   const bool fast_acc = fast_k && p.ldacc % 4 == 0 && al(p.acc, 16);
   if (p.acc) {

@@ -149,6 +149,47 @@ def test_gemm_wide_epilogue_equals_narrow_epilogue(gpu_lib, M, N, K, with_bias):
     assert torch.equal(out_w.cpu()[rows], ref)
 
 
+@pytest.mark.parametrize("M,N,K,epi", [(2048, 2048, 2048, "res"), (2000, 2040, 1024, "bias_res"),
+                                       (2100, 7424, 256, "plain"), (1536, 4096, 2048, "swiglu"),
+                                       (512, 6144, 2048, "res")])
+def test_gemm_128x128_tiles_equal_larger_tiles(gpu_lib, M, N, K, epi):
+    """Mid-size M x N with a bf16 output through the wide epilogue take 128 x 128 tiles (two workgroups per CU):
+    2048 x 2048 makes one tile per CU; 2000 x 2040 leaves the last tile row (80 of 128 rows) and column (120 of 128
+    columns) ragged; 2100 x 7424 makes 986 tiles for 512 persistent workgroups, so most run two (the scale slots
+    alternate); SwiGLU at F = 2048. The same GEMM with scale vectors 4 bytes off 16-byte alignment takes the
+    4-column epilogue on the larger tiles: the same bytes, and the oracle's on a sample of rows."""
+    from opendecider_amd import kernels
+    g = torch.Generator().manual_seed(M + N + K)
+    a, w, sa, sw = _gemm_case(g, M, N, K)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16) if "bias" in epi else None
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16) if "res" in epi else None
+    A, W = a.to(DEV), w.to(DEV)
+    Bd = None if bias is None else bias.to(DEV)
+    R = None if res is None else res.to(DEV)
+    sab = torch.zeros(M + 1, device=DEV)
+    swb = torch.zeros(N + 1, device=DEV)
+    sab[1:] = sa.to(DEV)
+    swb[1:] = sw.to(DEV)
+    assert sab[1:].data_ptr() % 16 != 0 and swb[1:].data_ptr() % 16 != 0
+    print(f"128x128 tiles M={M} N={N} K={K} {epi}", flush=True)
+    if epi == "swiglu":
+        assert kernels.splitk_workspace(M, N, K, DEV) is None
+        out_w = kernels.w8a8_gemm_swiglu(A, sa.to(DEV), W, sw.to(DEV))
+        out_n = kernels.w8a8_gemm_swiglu(A, sab[1:], W, swb[1:])
+        assert torch.equal(out_w.view(torch.int16), out_n.view(torch.int16))
+        gu = oq.w8a8_epilogue(oq.int_gemm(a[:64], w), sa[:64], sw)
+        ref = od.swiglu(gu[:, torch.cat([torch.arange(0, N, 2), torch.arange(1, N, 2)])], N // 2).float()
+        d = (out_w[:64].cpu().float() - ref).abs()
+        assert (d <= ref.abs() * 2.0 ** -6 + 2.0 ** -120).all() and (d > 0).float().mean().item() <= 5e-3
+        return
+    out_w = kernels.w8a8_gemm(A, sa.to(DEV), W, sw.to(DEV), bias=Bd, residual=R)
+    out_n = kernels.w8a8_gemm(A, sab[1:], W, swb[1:], bias=Bd, residual=R)
+    assert torch.equal(out_w.view(torch.int16), out_n.view(torch.int16))
+    rows = torch.tensor(sorted({0, 1, 127, 128, 1023, 1024, 1920, M - 1} & set(range(M))))
+    ref = oq.w8a8_epilogue(oq.int_gemm(a[rows], w), sa[rows], sw, bias, None if res is None else res[rows])
+    assert torch.equal(out_w.cpu()[rows], ref)
+
+
 def test_config0_single_w8a8_linear(gpu_lib):
     """X bf16 [256,4096] N(0,1) with 1% outlier channels x20, per-token int8; W int8 [4096,4096] uniform in
     [-127,127]; per-channel fp32 scales U(0.5e-3, 2e-3); int32 accumulators compared exactly."""
