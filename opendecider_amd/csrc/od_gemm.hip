@@ -418,8 +418,10 @@ __device__ __forceinline__ Panels panels_of(const GemmArgs& p, int v, int ntiles
                                             (int)((rows_w - 1) * p.ldw + p.K), 0x00020000)};
 }
 
-template <int BM, int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU, bool WIDE>
-__global__ __launch_bounds__(kThreads, BM == 128 && BN == 128 ? 4 : 1) void w8a8_gemm_kernel(GemmArgs p) {
+// NS: LDS stage buffers. 2: the pipeline below. 4 (128 x 128 tiles, one workgroup per CU): a ring with three
+// stages of loads in flight, for tiles whose main loop would otherwise wait on a single stage's loads.
+template <int BM, int BN, bool ACC_ONLY, bool GENERAL, bool SWIGLU, bool WIDE, int NS = 2>
+__global__ __launch_bounds__(kThreads, BM == 128 && BN == 128 && NS == 2 ? 4 : 1) void w8a8_gemm_kernel(GemmArgs p) {
   constexpr int kWM = WaveGrid<BM>::kWM, kWN = WaveGrid<BM>::kWN;
   constexpr int kRowsW = BM / kWM, kColsW = BN / kWN;  // a wave's sub-tile: 64 x BN/kWN
   constexpr int TM = kRowsW / 32;    // 2
@@ -427,11 +429,13 @@ __global__ __launch_bounds__(kThreads, BM == 128 && BN == 128 ? 4 : 1) void w8a8
   static_assert(kColsW % 32 == 0, "a wave's columns are whole 32-column MFMA tiles");
   constexpr int kSlabA = BM * BK, kSlabB = BN * BK, kStage = kSlabA + kSlabB;
   constexpr int kOpsA = BM / 64, kOpsB = BN / 64;  // DMA loads per wave per stage (8 waves x 8 rows each)
-  __shared__ __attribute__((aligned(16))) int8_t smem[2 * kStage];
-  // WIDE: the row and column scales of a tile, two slots by tile parity, each loaded by the stage that loads the
-  // tile's first operands (one 1 KB LDS-DMA load each; rows / columns past M / N read as zeros)
+  static_assert(NS == 2 || (NS == 4 && BM == 128 && BN == 128 && WIDE && !ACC_ONLY && !GENERAL), "stage ring");
+  __shared__ __attribute__((aligned(16))) int8_t smem[NS * kStage];
+  // WIDE: the row and column scales of a tile, NS slots by the tile's index among the workgroup's tiles (mod NS), each
+  // loaded by the stage that loads the tile's first operands (one 1 KB LDS-DMA load each; rows / columns past M / N
+  // read as zeros)
   constexpr int kSlot = 2 * kScaleRows;
-  __shared__ __attribute__((aligned(16))) float sscale[WIDE ? 2 * kSlot : 4];
+  __shared__ __attribute__((aligned(16))) float sscale[WIDE ? NS * kSlot : 4];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -533,8 +537,78 @@ __global__ __launch_bounds__(kThreads, BM == 128 && BN == 128 ? 4 : 1) void w8a8
   //   k-step 3: vmcnt + lgkmcnt wait and barrier (the next stage is in LDS for every wave, every wave is done
   //             reading CUR), read k-step 0 of the next stage, MFMAs of k-step 3
   // After a tile's last stage its accumulators go out through the epilogue, which stages them in buffer CUR of
-  // that stage (read by no one any more) while NXT already holds the next tile's first stage; the epilogue's
-  // global stores drain while the next tile computes.
+  // that stage (read by no one any more) while NXT already holds the next tile's first stage. (The next tile's first
+  // stage waits for the epilogue's stores: the compiler counts the epilogue's conditional loads as outstanding there
+  // and waits for every memory operation.)
+  if constexpr (NS > 2) {
+    // The ring: stage j of the workgroup's sequence of (tile, k-tile) stages computes from buffer j % NS, and its
+    // loads go out during stage j - (NS - 1), into the buffer stage j - NS read (free since the barrier that ended
+    // that stage). A stage ends by waiting for the next stage's loads, leaving the NS - 2 later stages' loads in flight
+    // (vector memory operations complete in issue order; a scale load or an epilogue's loads and stores issued after
+    // them only make the wait stricter).
+    v4i f0a[TM], f0b[TN], f1a[TM], f1b[TN];
+    constexpr int kOps0 = kOpsA + kOpsB;
+    static_assert(2 * kOps0 == 8, "the ring's wait count: two stages of loads in flight");
+    int v = blockIdx.x;
+    const int G = (int)gridDim.x;
+    const int nks = ke - kb;  // stages per tile
+    Panels cur = panels_of<BM, BN>(p, v, ntiles);
+    Panels nxt = panels_of<BM, BN>(p, v + G, ntiles);
+    // the panels of the tile d tiles after the current one
+    auto src_of = [&](int d) { return d == 0 ? cur : d == 1 ? nxt : panels_of<BM, BN>(p, v + d * G, ntiles); };
+    // stages 0 .. NS - 2 (stage j in buffer j), then wait for stage 0 only
+    for (int q = 0; q < NS - 1; ++q) {
+      const int d = q / nks, ktt = kb + q - d * nks;
+      const Panels src = src_of(d);
+#pragma unroll
+      for (int o = 0; o < kOps0; ++o) dma(q, src, ktt, o);
+      if (ktt == kb) dma_scales(v + d * G, d % NS);
+    }
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    frags(0, 0, f0a, f0b);
+    zero_acc();
+    int cb = 0;  // the current stage's buffer
+    for (int i = 0; v < ntiles; v += G, ++i) {
+      for (int kr = 0; kr < nks; ++kr) {
+        const int tgt = kr + NS - 1;  // the stage whose loads go out now, counted from this tile's first
+        const int d = tgt < nks ? 0 : tgt / nks;
+        const int ktt = kb + tgt - d * nks;
+        const int nb = cb == NS - 1 ? 0 : cb + 1, lb = cb == 0 ? NS - 1 : cb - 1;
+        const Panels src = src_of(d);
+        frags(cb, 1, f1a, f1b);
+        __builtin_amdgcn_sched_barrier(0);
+        auto fill0 = [&](int o) { dma(lb, src, ktt, o); };
+        mma(f0a, f0b, fill0, std::integral_constant<int, kOps0>{});
+        if (d > 0 && ktt == kb) dma_scales(v + d * G, (i + d) % NS);
+        frags(cb, 2, f0a, f0b);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f1a, f1b, nofill, Zero{});
+        frags(cb, 3, f1a, f1b);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f0a, f0b, nofill, Zero{});
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        frags(nb, 0, f0a, f0b);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f1a, f1b, nofill, Zero{});
+        cb = nb;
+      }
+      int tm, tn;
+      tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
+      epilogue8<BM, BN, SWIGLU, TM, TN>(p, acc, smem + (cb == 0 ? NS - 1 : cb - 1) * kStage,
+                                        sscale + (i % NS) * kSlot, tm, tn, wm, wn, wave, lane);
+      // A wait the compiler sees. It cannot relate the epilogue's loads' conditions to those of their uses and
+      // would otherwise count them outstanding into the next tile's stages, waiting for every memory operation (the
+      // ring's loads included) at the top of each stage. Here it costs one drain per tile.
+      __builtin_amdgcn_s_waitcnt(0);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      zero_acc();
+      cur = nxt;
+      nxt = panels_of<BM, BN>(p, v + 2 * G, ntiles);
+    }
+    // the loads of the stages past the last tile (zeros from empty ranges) land before the workgroup's LDS is freed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
   v4i f0a[TM], f0b[TN], f1a[TM], f1b[TN];
   constexpr int kOps0 = kOpsA + kOpsB;
   int v = blockIdx.x;
@@ -956,9 +1030,18 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
     using I = std::integral_constant<int, 256>;
     using H = std::integral_constant<int, 128>;
     if (t.bm == 128 && t.bn == 128) {
-      // chosen only for the wide variant without accumulators (the 4-column epilogue needs 64-column sub-tiles)
-      if constexpr (!decltype(ACCc)::value)
-        if (variant == kWide) launch(H{}, H{}, ACCc, std::false_type{}, SWc, std::true_type{});
+      // chosen only for the wide variant without accumulators (the 4-column epilogue needs 64-column sub-tiles);
+      // at most one tile per CU and K >= 3072: one workgroup per CU on the 4-stage ring (2048 x 2048 x 6144: 41.7 ->
+      // 33.3 us; at K = 2048 it measured 3% slower, its three stages of prologue loads a larger share of the tile),
+      // else two workgroups per CU on 2 stages each
+      if constexpr (!decltype(ACCc)::value) {
+        if (variant == kWide) {
+          if (ntiles <= cu_count() && p.kt_per >= 24)
+            w8a8_gemm_kernel<128, 128, false, false, decltype(SWc)::value, true, 4><<<grid, block, 0, st>>>(p);
+          else
+            launch(H{}, H{}, ACCc, std::false_type{}, SWc, std::true_type{});
+        }
+      }
     } else if (t.bm == 128) {
       launch1(H{}, I{}, ACCc, SWc, variant);
     } else if (t.bn == 192) {
