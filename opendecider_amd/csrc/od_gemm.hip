@@ -5,12 +5,14 @@
 // Tiling (MFMA-bound at the 9B shapes; one workgroup of 8 waves per CU, two per SIMD so that one wave's MFMAs
 // cover the other's LDS latency and barrier waits):
 //   * workgroup tile BM x BN = 256 x 256, 256 x 192 or 128 x 256 (chosen per shape: 128-row tiles when M is too
-//     small to fill the chip with 256-row ones); K advances 128 bytes per stage, so every row segment a stage
-//     loads is one whole 128-byte line (64-byte segments measured at about 60% of the L2 -> CU rate).
+//     small to fill the chip with 256-row ones), or 128 x 128 for mid-size M x N with a bf16 output through the
+//     wide epilogue (two workgroups per CU, or one on a 4-stage LDS ring when every tile has a CU and K >= 3072);
+//     K advances 128 bytes per stage, so every row segment a stage loads is one whole 128-byte line (64-byte
+//     segments measured at about 60% of the L2 -> CU rate).
 //   * persistent workgroups, one per CU: workgroup b computes tiles b, b + G, b + 2G, ... (G = grid size), as one
 //     pipeline over its (tile, k-tile) stages, so the next tile's first stage loads during the last stage of the
-//     current one and the epilogue's stores drain while the next tile computes (launched one tile per workgroup,
-//     every CU stalled on its epilogue at the same time: about 10-15 us per wave of tiles).
+//     current one (launched one tile per workgroup, every CU stalled on its epilogue at the same time: about
+//     10-15 us per wave of tiles).
 //   * global -> LDS by LDS DMA (buffer_load_dwordx4 ... lds): no register staging and no LDS write instructions;
 //     the LDS holds two stages (2 x (256 + BN) x 128 B <= 128 KB) and the loads of the next stage are issued at
 //     the start of the current one. Rows past M/N and bytes past K read as zeros (buffer range check).
