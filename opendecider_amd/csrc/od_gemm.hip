@@ -848,8 +848,9 @@ struct Tiling {
 // With `small` (a bf16 output through the wide epilogue, no accumulator output) 128 x 128 is a fourth candidate,
 // for mid-size M x N that leave most CUs without a larger tile. Its workgroup needs 68 KB of LDS and at most 128
 // VGPRs per lane, so two run on a CU (the persistent grid is twice the CUs): measured on the sweep's and the 9B
-// shapes at M = 512 to 8192, one such tile per CU takes 0.53 of a 256 x 256 tile's time (its main loop waits on
-// its one stage of loads in flight) and two together 0.60.
+// shapes at M = 512 to 2048, one such tile per CU takes 0.53 of a 256 x 256 tile's time (its main loop waits on
+// its one stage of loads in flight) and two together 0.60. It is a candidate only up to two tiles per CU: with more,
+// each pair of tiles measured 0.71-0.73 (M = 6144: O and down projections 2-8% slower than on 128 x 256 tiles).
 constexpr double kRel128x128 = 0.53, kRel128x128Pair = 0.60;
 Tiling tiling_of(int64_t M, int64_t N, bool small) {
   const struct { int bm, bn; double cost; } cand[4] = {
@@ -861,7 +862,8 @@ Tiling tiling_of(int64_t M, int64_t N, bool small) {
     const bool t128 = c.bn == 128;
     if (t128 && !small) continue;
     const int64_t tm = (M + c.bm - 1) / c.bm, tn = (N + c.bn - 1) / c.bn;
-    const double cost = t128 ? (tm * tn <= cus ? kRel128x128 : (double)((tm * tn + 2 * cus - 1) / (2 * cus)) * kRel128x128Pair)
+    if (t128 && tm * tn > 2 * cus) continue;
+    const double cost = t128 ? (tm * tn <= cus ? kRel128x128 : kRel128x128Pair)
                              : (double)((tm * tn + cus - 1) / cus) * c.cost;
     if (best.tiles_m == 0 || cost < best_cost) {
       best = {c.bm, c.bn, tm, tn, c.cost};

@@ -151,16 +151,15 @@ def test_gemm_wide_epilogue_equals_narrow_epilogue(gpu_lib, M, N, K, with_bias):
 
 @pytest.mark.parametrize("M,N,K,epi", [(2048, 2048, 3072, "res"), (2000, 2040, 4096, "bias_res"),
                                        (1024, 4096, 4096, "swiglu"), (512, 6144, 2048, "res"),
-                                       (1024, 2048, 128, "bias_res"), (2100, 7424, 256, "plain"),
+                                       (1024, 2048, 128, "bias_res"), (1536, 4096, 1024, "res"),
                                        (1536, 4096, 2048, "swiglu")])
 def test_gemm_128x128_tiles_equal_larger_tiles(gpu_lib, M, N, K, epi):
-    """Mid-size M x N with a bf16 output through the wide epilogue take 128 x 128 tiles. Up to one tile per CU and
-    K >= 3072 they run on the 4-stage ring (one workgroup per CU): 2048 x 2048; 2000 x 2040 with the last tile row
-    (80 of 128 rows) and column (120 of 128 columns) ragged; SwiGLU at F = 2048. Otherwise on 2 stages, two
-    workgroups per CU: one tile per workgroup at K = 2048 and 128; 2100 x 7424 makes 986 tiles for 512 persistent
-    workgroups, so most run two (the scale slots alternate); SwiGLU at 1536 x 2048. The same GEMM with scale vectors
-    4 bytes off 16-byte alignment takes the 4-column epilogue on the larger tiles: the same bytes, and the oracle's on
-    a sample of rows."""
+    """Mid-size M x N with a bf16 output through the wide epilogue take 128 x 128 tiles (up to two per CU). Up to one
+    tile per CU and K >= 3072 they run on the 4-stage ring (one workgroup per CU): 2048 x 2048; 2000 x 2040 with the
+    last tile row (80 of 128 rows) and column (120 of 128 columns) ragged; SwiGLU at F = 2048. Otherwise on 2
+    stages: one tile per CU at K = 2048 and 128; 384 tiles, two workgroups on most CUs, at 1536 x 4096 and SwiGLU at
+    1536 x 2048. The same GEMM with scale vectors 4 bytes off 16-byte alignment takes the 4-column epilogue on the
+    larger tiles: the same bytes, and the oracle's on a sample of rows."""
     from opendecider_amd import kernels
     g = torch.Generator().manual_seed(M + N + K)
     a, w, sa, sw = _gemm_case(g, M, N, K)
