@@ -56,6 +56,9 @@ constexpr int kCpr = BK / 16;  // 16-byte chunks per row per stage
 constexpr int kGroupM = 4;
 constexpr int kScaleRows = 256;  // the WIDE variant's LDS scale slot: kScaleRows row scales, then 256 column scales
 constexpr int kOOB = 0x7ffffff0;  // a buffer offset past any range: the load returns zeros
+// The SwiGLU epilogue's LDS table of bf16(silu(g)) (od_silu_bf16) for 2^-8 <= |g| < 16: bf16 patterns
+// kSiluLo .. kSiluHi - 1 of each sign, positive ones first (2 x 1536 entries, 6 KB)
+constexpr uint32_t kSiluLo = 0x3b80u, kSiluHi = 0x4180u, kSiluHalf = kSiluHi - kSiluLo;
 
 struct GemmArgs {
   const int8_t* a;
@@ -253,7 +256,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, const v16i (&acc)[TM
 //    conversion.
 template <int BM, int BN, bool SWIGLU, int TM, int TN>
 __device__ __forceinline__ void epilogue8(const GemmArgs& p, const v16i (&acc)[TM][TN], int8_t* stage_buf,
-                                          const float* sc, int tm, int tn, int wm, int wn, int wave, int lane) {
+                                          const float* sc, const uint16_t* stab, int tm, int tn, int wm, int wn,
+                                          int wave, int lane) {
   constexpr int kWM = WaveGrid<BM>::kWM, kWN = WaveGrid<BM>::kWN;
   constexpr int kRowsW = BM / kWM;
   constexpr int kCols = BN / kWN;
@@ -341,27 +345,29 @@ __device__ __forceinline__ void epilogue8(const GemmArgs& p, const v16i (&acc)[T
         const uint32_t vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
         if constexpr (SWIGLU) {
           // columns 2e, 2e + 1 of the group are (gate, up) of output column nl / 2 + e
-          // the slow-path test of od_silu_needs_slow for the four at once: the least (low 16 bits - 0x7ff0) and
-          // any |g| >= 16 (or NaN)
+          // bf16(silu(g)) = od_silu_bf16(g) of the bf16 gate g: for 2^-125 <= |g| < 2^-8 it is bf16(g / 2) (checked
+          // on every bf16 g), the bf16 pattern with the exponent one lower; for 2^-8 <= |g| < 16 the LDS table;
+          // the function itself for the rest (zero, tiny and |g| >= 16 or NaN: rare)
           float g[4], uu[4], s[4];
-          uint32_t dmin = 0xffffffffu;
-          bool big = false;
+          bool rare = false;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             g[e] = __uint_as_float(vv[2 * e]);
             uu[e] = __uint_as_float(vv[2 * e + 1]);
             od_bfr2(g[e], uu[e]);
-            s[e] = od_silu_fast32(g[e]);
-            dmin = min(dmin, (__float_as_uint(s[e]) & 0xffffu) - 0x7ff0u);
-            big |= !(fabsf(g[e]) < 16.0f);
+            const uint32_t gb = __float_as_uint(g[e]) >> 16, a = gb & 0x7fffu;
+            const uint32_t idx = min(max(a, kSiluLo), kSiluHi - 1u) - kSiluLo + (gb >> 15) * kSiluHalf;
+            const uint32_t tv = stab[idx];
+            s[e] = __uint_as_float((a < kSiluLo ? gb - 0x80u : tv) << 16);
+            rare |= a >= kSiluHi || a < 0x0100u;
           }
-          if (__builtin_expect(dmin <= 0x20u || big, 0)) {
+          if (__builtin_expect(rare, 0)) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (od_silu_needs_slow(g[e], s[e])) s[e] = od_silu_slow32(g[e]);
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t a = (__float_as_uint(g[e]) >> 16) & 0x7fffu;
+              if (a >= kSiluHi || a < 0x0100u) s[e] = od_silu_bf16(g[e]);
+            }
           }
-          od_bfr2(s[0], s[1]);
-          od_bfr2(s[2], s[3]);
           typedef unsigned v2u __attribute__((ext_vector_type(2)));
           const v2u w = {od_pack_bf16x2(s[0] * uu[0], s[1] * uu[1]), od_pack_bf16x2(s[2] * uu[2], s[3] * uu[3])};
           __builtin_amdgcn_raw_buffer_store_b64(w, rout, ovo, soff, 0);
@@ -438,6 +444,15 @@ __global__ __launch_bounds__(kThreads, BM == 128 && BN == 128 && NS == 2 ? 4 : 1
   // read as zeros)
   constexpr int kSlot = 2 * kScaleRows;
   __shared__ __attribute__((aligned(16))) float sscale[WIDE ? NS * kSlot : 4];
+  // the wide SwiGLU epilogue's silu table, filled here (its first stage's barrier orders the fill before any read)
+  __shared__ uint16_t stab[SWIGLU && WIDE ? 2 * kSiluHalf : 2];
+  if constexpr (SWIGLU && WIDE) {
+    for (int i = threadIdx.x; i < (int)(2 * kSiluHalf); i += kThreads) {
+      const uint32_t h = (uint32_t)i >= kSiluHalf;
+      const uint32_t bits = (h << 15) | (kSiluLo + (uint32_t)i - h * kSiluHalf);
+      stab[i] = od_f32_to_bf16(od_silu_bf16(__uint_as_float(bits << 16)));
+    }
+  }
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -597,7 +612,7 @@ __global__ __launch_bounds__(kThreads, BM == 128 && BN == 128 && NS == 2 ? 4 : 1
       int tm, tn;
       tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
       epilogue8<BM, BN, SWIGLU, TM, TN>(p, acc, smem + (cb == 0 ? NS - 1 : cb - 1) * kStage,
-                                        sscale + (i % NS) * kSlot, tm, tn, wm, wn, wave, lane);
+                                        sscale + (i % NS) * kSlot, stab, tm, tn, wm, wn, wave, lane);
       // A wait the compiler sees. It cannot relate the epilogue's loads' conditions to those of their uses and
       // would otherwise count them outstanding into the next tile's stages, waiting for every memory operation (the
       // ring's loads included) at the top of each stage. Here it costs one drain per tile.
@@ -655,8 +670,8 @@ __global__ __launch_bounds__(kThreads, BM == 128 && BN == 128 && NS == 2 ? 4 : 1
     int tm, tn;
     tile_of(v, p.tiles_m, p.tiles_n, tm, tn);
     if constexpr (WIDE)
-      epilogue8<BM, BN, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, sscale + parity * kSlot, tm, tn, wm, wn,
-                                        wave, lane);
+      epilogue8<BM, BN, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, sscale + parity * kSlot, stab, tm, tn,
+                                        wm, wn, wave, lane);
     else
       epilogue<BM, BN, ACC_ONLY, GENERAL, SWIGLU, TM, TN>(p, acc, smem + (buf ^ 1) * kStage, tm, tn, wm, wn, wave,
                                                           lane);

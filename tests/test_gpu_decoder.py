@@ -62,11 +62,14 @@ def test_silu_mul_quant(gpu_lib, M, F, smooth):
     _exact_quant(xq, sx, rq, rs, "silu_mul_quant")
 
 
-def test_silu_all_bf16_inputs(gpu_lib):
+@pytest.mark.parametrize("M", [1, 520])
+def test_silu_all_bf16_inputs(gpu_lib, M):
     """bf16(silu(g)) of the SwiGLU GEMM epilogue on every bf16 bit pattern of g (normal numbers, zeros, infinities,
     NaNs; the 2 x 127 x 128 subnormal patterns are left out: the epilogue forms g from an fp32 product, where the
-    device may flush them) against the oracle's correctly rounded table. One row, K = 16: a = e_0, gate row 2f =
-    e_0 with scale g_f, up row 2f + 1 = e_0 with scale 1, so g = g_f and u = 1 exactly."""
+    device may flush them) against the oracle's correctly rounded table. K = 16: every row a = e_0, gate row 2f =
+    e_0 with scale g_f, up row 2f + 1 = e_0 with scale 1, so g = g_f and u = 1 exactly. M = 1 takes the small-M
+    kernel's epilogue; M = 520 the 256-row kernel's wide epilogue (bf16(g / 2) below 2^-8, its LDS table up to 16,
+    the function beyond), checked on its first and last rows."""
     from opendecider_amd import kernels
     bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
     gv = bits.view(torch.bfloat16)
@@ -74,19 +77,21 @@ def test_silu_all_bf16_inputs(gpu_lib):
     keep = (expo != 0) | ((bits.int() & 0x7F) == 0)
     gv = gv[keep]
     F = gv.numel()
-    a = torch.zeros(1, 16, dtype=torch.int8)
-    a[0, 0] = 1
+    a = torch.zeros(M, 16, dtype=torch.int8)
+    a[:, 0] = 1
     w = torch.zeros(2 * F, 16, dtype=torch.int8)
     w[:, 0] = 1
     sw = torch.ones(2 * F)
     sw[0::2] = gv.float()
-    out = kernels.w8a8_gemm_swiglu(a.to(DEV), torch.ones(1, device=DEV), w.to(DEV), sw.to(DEV))
-    got = out.cpu()[0]
+    print(f"silu all bf16 M={M}", flush=True)
+    out = kernels.w8a8_gemm_swiglu(a.to(DEV), torch.ones(M, device=DEV), w.to(DEV), sw.to(DEV))
     ref = od.silu_bf16(gv)
     nan = torch.isnan(ref)
-    assert torch.equal(torch.isnan(got), nan)
-    bad = (got.view(torch.int16) != ref.view(torch.int16)) & ~nan
-    assert not bad.any(), (gv[bad][:8], got[bad][:8], ref[bad][:8])
+    for r in sorted({0, M - 1}):
+        got = out[r].cpu()
+        assert torch.equal(torch.isnan(got), nan)
+        bad = (got.view(torch.int16) != ref.view(torch.int16)) & ~nan
+        assert not bad.any(), (r, gv[bad][:8], got[bad][:8], ref[bad][:8])
 
 
 @pytest.mark.parametrize("D,rot,offset", [(128, 128, False), (64, 64, False), (256, 256, False), (256, 64, True),
