@@ -865,7 +865,7 @@ struct Tiling {
 // VGPRs per lane, so two run on a CU (the persistent grid is twice the CUs): measured on the sweep's and the 9B
 // shapes at M = 512 to 2048, one such tile per CU takes 0.53 of a 256 x 256 tile's time (its main loop waits on
 // its one stage of loads in flight) and two together 0.60. It is a candidate only up to two tiles per CU: with more,
-// each pair of tiles measured 0.71-0.73 (M = 6144: O and down projections 2-8% slower than on 128 x 256 tiles).
+// each pair of tiles measured 0.71-0.73 (M = 6144: O and down projections 2-8% slower than on 256 x 256 tiles).
 constexpr double kRel128x128 = 0.53, kRel128x128Pair = 0.60;
 Tiling tiling_of(int64_t M, int64_t N, bool small) {
   const struct { int bm, bn; double cost; } cand[4] = {
@@ -1050,8 +1050,8 @@ int gemm_launch(const GemmArgs& p0, bool swiglu, hipStream_t st, const SplitPlan
     using H = std::integral_constant<int, 128>;
     if (t.bm == 128 && t.bn == 128) {
       // chosen only for the wide variant without accumulators (the 4-column epilogue needs 64-column sub-tiles);
-      // at most one tile per CU and K >= 3072: one workgroup per CU on the 4-stage ring (2048 x 2048 x 6144: 41.7 ->
-      // 33.3 us; at K = 2048 it measured 3% slower, its three stages of prologue loads a larger share of the tile),
+      // at most one tile per CU and K >= 3072: one workgroup per CU on the 4-stage ring (M = N = 2048, K = 6144: 41.7
+      // -> 33.3 us; at K = 2048 it measured 3% slower, its three stages of prologue loads a larger share of the tile),
       // else two workgroups per CU on 2 stages each
       if constexpr (!decltype(ACCc)::value) {
         if (variant == kWide) {
