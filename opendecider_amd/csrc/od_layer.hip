@@ -7,6 +7,8 @@
 // tensors is rounded to bf16 once). The two values that a plain fp32 evaluation would leave dependent on the device
 // (the order of a sum, the last bit of exp / rsqrt) are correctly rounded instead: the RMSNorm factor comes from a
 // float64 sum of squares (od_rms_factor) and silu from od_silu_bf16, so the outputs equal the oracle's bit for bit.
+#include <type_traits>
+
 #include "od_common.h"
 
 namespace {
@@ -283,8 +285,9 @@ __global__ __launch_bounds__(kThreads) void silu_mul_quant_vec_kernel(const uint
   if (threadIdx.x == 0) sa[row] = scale;
 }
 
-// q/k RMSNorm + RoPE with G = D / 8 lanes per head: lane j holds d = 4j..4j+3 and the rotary partners
-// D/2 + 4j..D/2 + 4j + 3, so every load and store is 8 bytes and no lane exchange is needed for the rotation.
+// q/k RMSNorm + RoPE with G = D / 8 lanes per head (lane j holds d = 4j..4j+3 and the rotary partners
+// D/2 + 4j..D/2 + 4j + 3: 8-byte loads and stores) or, for 16-byte aligned rows, G = D / 16 (8 + 8 values per lane,
+// 16-byte accesses); no lane exchange is needed for the rotation.
 // APPEND: the launch also covers the n_heads_k value heads of every row, and the key heads (after RoPE) and value
 // heads are quantized per (token, head) into int8 caches, with the bytes od_kv_quant_append writes for the same
 // bf16 values (row m = b * S + i of qkv goes to cache row (b * n_heads_k + h) * cap + n0 + i).
@@ -296,47 +299,66 @@ struct KvAppend {
   int64_t S, cap, n0;
 };
 
-__device__ __forceinline__ void unpack4(uint2 u, float (&f)[4]) {
-  f[0] = __uint_as_float(u.x << 16);
-  f[1] = __uint_as_float(u.x & 0xffff0000u);
-  f[2] = __uint_as_float(u.y << 16);
-  f[3] = __uint_as_float(u.y & 0xffff0000u);
+// H = 4 bf16 values (8 bytes) or H = 8 (16 bytes) of one vector load
+template <int H>
+using VecH = std::conditional_t<H == 4, uint2, uint4>;
+
+template <int H>
+__device__ __forceinline__ void unpackh(const VecH<H>& u, float (&f)[H]) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(&u);
+#pragma unroll
+  for (int k = 0; k < H / 2; ++k) {
+    f[2 * k] = __uint_as_float(w[k] << 16);
+    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
 }
 
-__device__ __forceinline__ uint2 pack4(const uint16_t (&h)[4]) {
-  return make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+template <int H>
+__device__ __forceinline__ VecH<H> packh(const uint16_t (&h)[H]) {
+  VecH<H> v;
+  uint32_t* w = reinterpret_cast<uint32_t*>(&v);
+#pragma unroll
+  for (int k = 0; k < H / 2; ++k) w[k] = (uint32_t)h[2 * k] | ((uint32_t)h[2 * k + 1] << 16);
+  return v;
 }
 
-// Quantizes a head's D bf16 values held 8 per lane (oa: d = da .. da + 3, ob: d = db .. db + 3) over the G lanes of
-// its group and writes the int8 row and its scale.
-template <int D>
-__device__ __forceinline__ void quant_head(const uint16_t (&oa)[4], const uint16_t (&ob)[4], int j, int da, int db,
+// Quantizes a head's D bf16 values held 2H per lane (oa: d = da .. da + H - 1, ob: d = db .. db + H - 1) over the G
+// lanes of its group and writes the int8 row and its scale.
+template <int D, int H>
+__device__ __forceinline__ void quant_head(const uint16_t (&oa)[H], const uint16_t (&ob)[H], int j, int da, int db,
                                            int8_t* qrow, float* srow) {
-  constexpr int G = D / 8;
-  float y[8];
+  constexpr int G = D / (2 * H);
+  float y[2 * H];
   uint32_t bits = 0;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < H; ++e) {
     y[e] = od_bf16_to_f32(oa[e]);
-    y[4 + e] = od_bf16_to_f32(ob[e]);
+    y[H + e] = od_bf16_to_f32(ob[e]);
     bits = max(bits, (uint32_t)(oa[e] & 0x7fffu));
     bits = max(bits, (uint32_t)(ob[e] & 0x7fffu));
   }
 #pragma unroll
   for (int o = G / 2; o > 0; o >>= 1) bits = max(bits, (uint32_t)__shfl_xor((int)bits, o, OD_WAVE));
   const float scale = od_q8_scale(__uint_as_float(bits << 16)), inv = 1.0f / scale;
-  uint32_t w[2];
-  od_q8_words<8>(y, scale, inv, w);
-  *reinterpret_cast<uint32_t*>(qrow + da) = w[0];
-  *reinterpret_cast<uint32_t*>(qrow + db) = w[1];
+  uint32_t w[2 * H / 4];
+  od_q8_words<2 * H>(y, scale, inv, w);
+  if constexpr (H == 4) {
+    *reinterpret_cast<uint32_t*>(qrow + da) = w[0];
+    *reinterpret_cast<uint32_t*>(qrow + db) = w[1];
+  } else {
+    *reinterpret_cast<uint2*>(qrow + da) = make_uint2(w[0], w[1]);
+    *reinterpret_cast<uint2*>(qrow + db) = make_uint2(w[2], w[3]);
+  }
   if (j == 0) *srow = scale;
 }
 
 // Partial rotary (RD < D, Qwen3.5's 64 of 256): rotate_half acts on the first RD dims only (pairs d, d + RD/2) and the
-// other D - RD pass through the norm unrotated; lane j < RD/8 holds the pairs 4j .. 4j + 3 and RD/2 + 4j .., a lane
-// j >= RD/8 the 8 dims RD + 8 (j - RD/8) .. +7. The tables are [n_pos, RD/2]. ZC: the Qwen3.5 norm, one rounding:
+// other D - RD pass through the norm unrotated. A group of G = D / (2H) lanes owns a head: lane j < RD / (2H) holds
+// the pairs Hj .. Hj + H - 1 and RD/2 + Hj .., a lane j >= RD / (2H) the 2H dims RD + 2H (j - RD / (2H)) .. +2H - 1, so
+// no lane exchange is needed for the rotation. H = 4: 8-byte loads and stores; H = 8: 16-byte ones (rows and tables
+// 16-byte aligned), half the lanes per head. The tables are [n_pos, RD/2]. ZC: the Qwen3.5 norm, one rounding:
 // n_d = bf16((x_d * r) * (1 + w_d)) (fp32 products), instead of bf16(w_d * bf16(x_d * r)).
-template <int D, int RD, bool ZC, bool APPEND>
+template <int D, int RD, bool ZC, bool APPEND, int H>
 __global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restrict__ qkv, int64_t ld, int64_t M,
                                                                int n_heads_q, int n_heads_k,
                                                                const uint16_t* __restrict__ qw,
@@ -345,8 +367,9 @@ __global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restr
                                                                const uint16_t* __restrict__ sin_t, int64_t n_pos,
                                                                const int32_t* __restrict__ pos, float eps,
                                                                KvAppend kv) {
-  constexpr int G = D / 8, RL = RD / 8, RH = RD / 2;
-  static_assert(RD % 16 == 0 && RD <= D, "rotary dims");
+  constexpr int G = D / (2 * H), RL = RD / (2 * H), RH = RD / 2;
+  static_assert(RD % (2 * H) == 0 && RD <= D, "rotary dims");
+  using V = VecH<H>;
   const int heads = n_heads_q + n_heads_k * (APPEND ? 2 : 1);
   const int64_t gh = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
   if (gh >= M * heads) return;  // whole G-lane groups exit together
@@ -354,34 +377,42 @@ __global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restr
   const int head = (int)(gh % heads);
   const int j = threadIdx.x % G;
   const bool rot = j < RL;  // this lane holds rotary pairs
-  const int da = rot ? 4 * j : RD + 8 * (j - RL), db = rot ? RH + 4 * j : da + 4;
+  const int da = rot ? H * j : RD + 2 * H * (j - RL), db = rot ? RH + H * j : da + H;
   uint16_t* hp = qkv + row * ld + (int64_t)head * D;
-  const uint2 ra = *reinterpret_cast<const uint2*>(hp + da), rb = *reinterpret_cast<const uint2*>(hp + db);
+  const V ra = *reinterpret_cast<const V*>(hp + da), rb = *reinterpret_cast<const V*>(hp + db);
   int64_t crow = 0;
   if (APPEND) {
     const int64_t b = row / kv.S, i = row % kv.S;
     crow = (b * n_heads_k + (head - n_heads_q) % n_heads_k) * kv.cap + kv.n0 + i;
   }
   if (APPEND && head >= n_heads_q + n_heads_k) {  // a value head: quantize only
-    const uint16_t va[4] = {(uint16_t)ra.x, (uint16_t)(ra.x >> 16), (uint16_t)ra.y, (uint16_t)(ra.y >> 16)};
-    const uint16_t vb[4] = {(uint16_t)rb.x, (uint16_t)(rb.x >> 16), (uint16_t)rb.y, (uint16_t)(rb.y >> 16)};
-    quant_head<D>(va, vb, j, da, db, kv.vq + crow * D, kv.vs + crow);
+    const uint32_t* wa = reinterpret_cast<const uint32_t*>(&ra);
+    const uint32_t* wb = reinterpret_cast<const uint32_t*>(&rb);
+    uint16_t va[H], vb[H];
+#pragma unroll
+    for (int k = 0; k < H / 2; ++k) {
+      va[2 * k] = (uint16_t)wa[k];
+      va[2 * k + 1] = (uint16_t)(wa[k] >> 16);
+      vb[2 * k] = (uint16_t)wb[k];
+      vb[2 * k + 1] = (uint16_t)(wb[k] >> 16);
+    }
+    quant_head<D, H>(va, vb, j, da, db, kv.vq + crow * D, kv.vs + crow);
     return;
   }
   const uint16_t* w = head < n_heads_q ? qw : kw;
-  float a[4], b[4], fa[4], fb[4];
-  unpack4(ra, a);
-  unpack4(rb, b);
-  unpack4(*reinterpret_cast<const uint2*>(w + da), fa);
-  unpack4(*reinterpret_cast<const uint2*>(w + db), fb);
+  float a[H], b[H], fa[H], fb[H];
+  unpackh<H>(ra, a);
+  unpackh<H>(rb, b);
+  unpackh<H>(*reinterpret_cast<const V*>(w + da), fa);
+  unpackh<H>(*reinterpret_cast<const V*>(w + db), fb);
   double ss = 0.0;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) ss = fma((double)b[e], (double)b[e], fma((double)a[e], (double)a[e], ss));
+  for (int e = 0; e < H; ++e) ss = fma((double)b[e], (double)b[e], fma((double)a[e], (double)a[e], ss));
   ss = od_group_sum_f64<G>(ss);
   const float r = od_rms_factor(ss, D, eps);
-  float na[4], nb[4];
+  float na[H], nb[H];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < H; ++e) {
     if constexpr (ZC) {
       na[e] = bfr((a[e] * r) * (1.0f + fa[e]));
       nb[e] = bfr((b[e] * r) * (1.0f + fb[e]));
@@ -390,33 +421,33 @@ __global__ __launch_bounds__(kThreads) void qk_rope_vec_kernel(uint16_t* __restr
       nb[e] = bfr(fb[e] * bfr(b[e] * r));
     }
   }
-  uint16_t oa[4], ob[4];
+  uint16_t oa[H], ob[H];
   if (rot) {
     const int64_t p = pos[row];
     const bool in_table = p >= 0 && p < n_pos;  // a position past the tables yields NaN, never an out-of-bounds read
-    float c[4], sn[4];
+    float c[H], sn[H];
     if (in_table) {
-      unpack4(*reinterpret_cast<const uint2*>(cos_t + p * RH + 4 * j), c);
-      unpack4(*reinterpret_cast<const uint2*>(sin_t + p * RH + 4 * j), sn);
+      unpackh<H>(*reinterpret_cast<const V*>(cos_t + p * RH + H * j), c);
+      unpackh<H>(*reinterpret_cast<const V*>(sin_t + p * RH + H * j), sn);
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) c[e] = sn[e] = __builtin_nanf("");
+      for (int e = 0; e < H; ++e) c[e] = sn[e] = __builtin_nanf("");
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < H; ++e) {
       oa[e] = od_f32_to_bf16(bfr(na[e] * c[e]) + bfr(-nb[e] * sn[e]));
       ob[e] = od_f32_to_bf16(bfr(nb[e] * c[e]) + bfr(na[e] * sn[e]));
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < H; ++e) {
       oa[e] = od_f32_to_bf16(na[e]);
       ob[e] = od_f32_to_bf16(nb[e]);
     }
   }
-  *reinterpret_cast<uint2*>(hp + da) = pack4(oa);
-  *reinterpret_cast<uint2*>(hp + db) = pack4(ob);
-  if (APPEND && head >= n_heads_q) quant_head<D>(oa, ob, j, da, db, kv.kq + crow * D, kv.ks + crow);
+  *reinterpret_cast<V*>(hp + da) = packh<H>(oa);
+  *reinterpret_cast<V*>(hp + db) = packh<H>(ob);
+  if (APPEND && head >= n_heads_q) quant_head<D, H>(oa, ob, j, da, db, kv.kq + crow * D, kv.ks + crow);
 }
 
 template <int NV>
@@ -500,11 +531,20 @@ namespace {
 bool aligned8(const void* p) { return (((uintptr_t)p) & 7u) == 0; }
 
 template <int D, int RD, bool ZC, bool APPEND>
-void launch_rope_vec_t(dim3 grid, hipStream_t st, uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q,
-                       int64_t n_heads_k, const uint16_t* q_w, const uint16_t* k_w, const uint16_t* cos_t,
-                       const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps, const KvAppend& kv) {
-  qk_rope_vec_kernel<D, RD, ZC, APPEND><<<grid, dim3(kThreads), 0, st>>>(
-      qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+void launch_rope_vec_t(bool wide, int64_t items, hipStream_t st, uint16_t* qkv, int64_t ld, int64_t M,
+                       int64_t n_heads_q, int64_t n_heads_k, const uint16_t* q_w, const uint16_t* k_w,
+                       const uint16_t* cos_t, const uint16_t* sin_t, int64_t n_pos, const int32_t* pos, float eps,
+                       const KvAppend& kv) {
+  // items: (row, head) pairs; a workgroup takes kThreads / G of them, G = D / 16 lanes (wide) or D / 8
+  if (wide) {
+    const dim3 grid((unsigned)((items + kThreads / (D / 16) - 1) / (kThreads / (D / 16))));
+    qk_rope_vec_kernel<D, RD, ZC, APPEND, 8><<<grid, dim3(kThreads), 0, st>>>(
+        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+  } else {
+    const dim3 grid((unsigned)((items + kThreads / (D / 8) - 1) / (kThreads / (D / 8))));
+    qk_rope_vec_kernel<D, RD, ZC, APPEND, 4><<<grid, dim3(kThreads), 0, st>>>(
+        qkv, ld, M, (int)n_heads_q, (int)n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+  }
 }
 
 // The (D, rotary dims) pairs the vector kernel is built for: full rotary at D = 64, 128, 256 and a quarter of the
@@ -523,16 +563,20 @@ int launch_rope_vec(uint16_t* qkv, int64_t ld, int64_t M, int64_t n_heads_q, int
   const int64_t blocks = (M * heads + per_block - 1) / per_block;
   if (blocks > 0x7fffffff || heads > 0x7fffffff) return OD_ERR_SHAPE;
   if (!rope_shape_ok(D, rot_dim)) return OD_ERR_UNSUPPORTED;
-  const dim3 grid((unsigned)blocks);
+  // 16-byte rows, weights and tables (and 8-byte cache rows): 16 values per lane, 16-byte loads and stores
+  auto al16 = [](const void* q) { return (((uintptr_t)q) & 15u) == 0; };
+  const bool wide = ld % 8 == 0 && al16(qkv) && al16(q_w) && al16(k_w) && al16(cos_t) && al16(sin_t) &&
+                    (!APPEND || (aligned8(kv.kq) && aligned8(kv.vq)));
+  const int64_t items = M * heads;
   auto go = [&](auto DC) {
     constexpr int DD = decltype(DC)::value;
     const bool full = rot_dim == DD;
     if (zc) {
-      if (full) launch_rope_vec_t<DD, DD, true, APPEND>(grid, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
-      else launch_rope_vec_t<DD, DD / 4, true, APPEND>(grid, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+      if (full) launch_rope_vec_t<DD, DD, true, APPEND>(wide, items, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+      else launch_rope_vec_t<DD, DD / 4, true, APPEND>(wide, items, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
     } else {
-      if (full) launch_rope_vec_t<DD, DD, false, APPEND>(grid, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
-      else launch_rope_vec_t<DD, DD / 4, false, APPEND>(grid, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+      if (full) launch_rope_vec_t<DD, DD, false, APPEND>(wide, items, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
+      else launch_rope_vec_t<DD, DD / 4, false, APPEND>(wide, items, st, qkv, ld, M, n_heads_q, n_heads_k, q_w, k_w, cos_t, sin_t, n_pos, pos, eps, kv);
     }
   };
   if (D == 256) go(std::integral_constant<int, 256>{});

@@ -94,11 +94,27 @@ def test_silu_all_bf16_inputs(gpu_lib, M):
         assert not bad.any(), (r, gv[bad][:8], got[bad][:8], ref[bad][:8])
 
 
-@pytest.mark.parametrize("D,rot,offset", [(128, 128, False), (64, 64, False), (256, 256, False), (256, 64, True),
-                                          (256, 64, False), (128, 32, True), (64, 64, True)])
-def test_qk_norm_rope(gpu_lib, D, rot, offset):
+def _rows_on_gpu(t: torch.Tensor, rows8: bool) -> torch.Tensor:
+    """t on the GPU with contiguous rows: 16-byte aligned (the rope kernels' 16-value lanes), or with rows8 a view
+    whose rows start 8 bytes off 16-byte alignment (the 8-value lanes)."""
+    if not rows8:
+        return t.to(DEV)
+    big = torch.zeros(t.shape[0], t.shape[1] + 4, dtype=t.dtype, device=DEV)
+    big[:, 4:] = t.to(DEV)
+    v = big[:, 4:]
+    assert v.data_ptr() % 16 == 8 and v.stride(0) % 8 == 4
+    return v
+
+
+@pytest.mark.parametrize("D,rot,offset,rows8", [(128, 128, False, False), (128, 128, False, True),
+                                                (64, 64, False, False), (256, 256, False, False),
+                                                (256, 64, True, False), (256, 64, True, True), (256, 64, False, False),
+                                                (128, 32, True, False), (128, 32, True, True), (64, 64, True, False),
+                                                (64, 16, True, False), (64, 16, False, True)])
+def test_qk_norm_rope(gpu_lib, D, rot, offset, rows8):
     """Head dims 64 / 128 / 256, full and partial rotary (rot = D / 4: Qwen3.5's 64 of 256), both norm weight
-    conventions: bit-exact, v untouched."""
+    conventions, 16-byte aligned rows (16 values per lane) and rows 8 bytes off (8 per lane): bit-exact, v
+    untouched."""
     from opendecider_amd import kernels
     cfg = od.DecoderConfig(hidden=8 * D, n_heads=8, n_kv_heads=2, head_dim=D, rot_dim=rot, norm_offset=offset)
     g = torch.Generator().manual_seed(D + rot)
@@ -110,22 +126,27 @@ def test_qk_norm_rope(gpu_lib, D, rot, offset):
     cos, sin = od.rope_tables(cfg, 40000)
     assert cos.shape == (40000, rot // 2)
     ref = od.qk_norm_rope(qkv, cfg, qw, kw, cos, sin, pos)
-    x = qkv.to(DEV)
-    print(f"qk_norm_rope D={D} rot={rot} offset={offset}", flush=True)
+    x = _rows_on_gpu(qkv, rows8)
+    print(f"qk_norm_rope D={D} rot={rot} offset={offset} rows8={rows8}", flush=True)
     kernels.qk_norm_rope(x, 8, 2, D, qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV), pos.to(DEV, torch.int32),
                          cfg.eps, rot, offset)
     assert torch.equal(x.cpu().view(torch.int16), ref.view(torch.int16))
     assert torch.equal(x.cpu()[:, 10 * D:], qkv[:, 10 * D:])
 
 
-@pytest.mark.parametrize("D,B,S,n0,rot,offset", [(128, 2, 37, 0, 128, False), (128, 3, 16, 21, 128, False),
-                                                 (64, 2, 9, 5, 64, False), (256, 2, 19, 7, 64, True),
-                                                 (256, 2, 8, 0, 256, False)])
-def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0, rot, offset):
+@pytest.mark.parametrize("D,B,S,n0,rot,offset,rows8", [(128, 2, 37, 0, 128, False, False),
+                                                       (128, 2, 37, 0, 128, False, True),
+                                                       (128, 3, 16, 21, 128, False, False),
+                                                       (64, 2, 9, 5, 64, False, False), (64, 2, 9, 5, 64, False, True),
+                                                       (256, 2, 19, 7, 64, True, False),
+                                                       (256, 2, 19, 7, 64, True, True),
+                                                       (256, 2, 8, 0, 256, False, False)])
+def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0, rot, offset, rows8):
     """The fused q/k norm + RoPE + int8 K/V append writes exactly what qk_norm_rope followed by two kv_quant_append
     calls write: the same qkv bits, cache bytes and scales, and leaves the cache rows before n0 and after n0 + S
-    alone. Then the fused result against the oracle: RoPE within one bf16 step, K/V bytes = the oracle's
-    quantizer applied to the GPU's rotated K and to V."""
+    alone; with 16-byte aligned rows (16 values per lane) and rows 8 bytes off (8 per lane). Then the fused result
+    against the oracle: RoPE within one bf16 step, K/V bytes = the oracle's quantizer applied to the GPU's rotated
+    K and to V."""
     from opendecider_amd import kernels
     from opendecider_amd.kv_cache import Int8KVCache
     Hq, Hk, cap = 8, 2, n0 + S + 7
@@ -144,8 +165,8 @@ def test_qk_norm_rope_kv_append_equals_separate_kernels(gpu_lib, D, B, S, n0, ro
             c.scale.fill_(-1.0)
             c.length = n0
         caches.append(pair)
-    x1, x2 = qkv.to(DEV), qkv.to(DEV)
-    print(f"fused rope+append D={D} B={B} S={S} n0={n0} rot={rot} offset={offset}", flush=True)
+    x1, x2 = _rows_on_gpu(qkv, rows8), _rows_on_gpu(qkv, rows8)
+    print(f"fused rope+append D={D} B={B} S={S} n0={n0} rot={rot} offset={offset} rows8={rows8}", flush=True)
     kernels.qk_norm_rope_kv_append(x1, B, S, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, *caches[0], rot, offset)
     kernels.qk_norm_rope(x2, Hq, Hk, D, qw, kw, cos, sin, pos, cfg.eps, rot, offset)
     k = x2[:, Hq * D:(Hq + Hk) * D].view(B, S, Hk, D).transpose(1, 2)
